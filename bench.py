@@ -1,0 +1,272 @@
+"""Benchmark of the gfx950 SharedDictionaryAttention forward path.
+
+One step = one ``SharedDictionaryAttention`` forward (dictionary
+normalization, Q/K/V projection, fused route, flash attention with the map
+mix, output projection) on one synthetic batch already resident in HBM, the
+same unit of work as the reference's ``benchmarks/benchmark_attention.py``
+forward mode.  The default workload is the north-star configuration: preset
+a1, x = [8, 512, 512] bf16.
+
+Prints ONE JSON line (rank 0).  Besides the module throughput it reports the
+per-kernel average durations measured with HIP events on the launch stream,
+the roofline of the dominant kernel and the fp32 CPU oracle timed on the
+host's cores for a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "double-attention_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "routed rows/s + attention tokens/s on 1 MI355X; % MFMA/HBM roofline"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+WORKLOADS = {
+    # name: (preset, batch, length, overrides, description)
+    "c1": ("a1", 8, 512, {}, "C1 preset a1 SharedDictionaryAttention forward x=[8,512,512]"),
+    "c2": ("qk4-s4", 8, 1024, {}, "C2 preset qk4-s4 SharedDictionaryAttention forward x=[8,1024,512]"),
+    "c3": ("a1-r512-d1536", 4, 2048, {}, "C3 preset a1-r512-d1536 SharedDictionaryAttention forward x=[4,2048,512]"),
+    "c5": ("a1", 1, 8192, {}, "C5 preset a1 long-context SharedDictionaryAttention forward x=[1,8192,512]"),
+}
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="c1")
+    p.add_argument("--dtype", choices=("bf16", "fp16"), default="bf16")
+    p.add_argument("--kernel-reps", type=int, default=200, help="launches per per-kernel timing loop")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
+    return p.parse_args()
+
+
+def cpu_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        counts = [info.get("num_threads", 1) for info in threadpool_info() if info.get("user_api") == "blas"]
+        if counts:
+            return int(max(counts))
+    except Exception:  # noqa: BLE001 - informational only
+        pass
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> None:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only: this build has no multi-GPU path "
+            f"(requested --gpus {args.gpus}); run with --gpus 1",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import double_attention as da
+    from double_attention import _lib
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a ROCm GPU")
+    lib = _lib.get()
+    device = torch.device("cuda:0")
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    code = _lib.DA_BF16 if dtype == torch.bfloat16 else _lib.DA_F16
+    preset, batch, length, overrides, description = WORKLOADS[args.workload]
+    config = da.experiment_config(preset, backend="hip", **overrides)
+    torch.manual_seed(0)
+    module = da.SharedDictionaryAttention(config).to(device=device, dtype=dtype).eval()
+    x = torch.randn(batch, length, config.model_dim, generator=torch.Generator().manual_seed(1)).to(device, dtype)
+
+    # ---- whole forward (the step) ----------------------------------------
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            module(x)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(args.steps):
+            out = module(x)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+    ms_per_step = elapsed * 1e3 / args.steps
+    tokens = batch * length
+    H, S, R, M, d = config.qk_branches, config.outer_maps, config.routing_dim, config.dictionary_size, config.model_dim
+    W = H * R
+    rows = 2 * batch * H * length
+    group = H // S if H > S else 1
+    rp = group * R
+
+    # ---- per-kernel timing on the launch stream ---------------------------
+    stream = torch.cuda.current_stream(device)
+    handle = stream.cuda_stream
+    with torch.inference_mode():
+        key, value = module.bank.normalized_hip(config.eps, dtype)
+        layout = key._da_route_layout
+        qk = torch.empty(tokens, 2 * W, device=device, dtype=dtype)
+        tp = lib.da_padded_length(length)
+        vt = torch.zeros(batch, d, tp, device=device, dtype=dtype)
+        routed = torch.empty_like(qk)
+        mixed = torch.empty(tokens, d, device=device, dtype=dtype)
+        final = torch.empty(tokens, d, device=device, dtype=dtype)
+        p = {k: v.contiguous() for k, v in module.state_dict().items()}
+        pdt = da.hip_ops.dtype_code(p["log_beta"].dtype)
+        raw_key = module.bank.raw_key.detach()
+        raw_value = module.bank.raw_value.detach() if module.bank.raw_value is not None else None
+
+        launches = {
+            "dict_normalize": lambda: lib.da_dictionary_normalize(
+                raw_key.data_ptr(), None if raw_value is None else raw_value.data_ptr(),
+                da.hip_ops.dtype_code(raw_key.dtype), R, M, config.eps,
+                layout.key_t.data_ptr(), layout.value.data_ptr(), code, handle),
+            "qkv_projection": lambda: lib.da_qkv_projection(
+                x.data_ptr(), tokens, d, length, p["query.weight"].data_ptr(), p["key.weight"].data_ptr(), W,
+                p["value.weight"].data_ptr(), p["value.bias"].data_ptr(), d, pdt, code,
+                qk.data_ptr(), vt.data_ptr(), vt.stride(0), vt.stride(1), handle),
+            "route": lambda: lib.da_dictionary_route(
+                qk.data_ptr(), rows, R, R, layout.key_t.data_ptr(), layout.value.data_ptr(), M,
+                p["log_beta"].data_ptr(), pdt, 0.0, config.eps,
+                _lib.DA_ROUTE_NORMALIZE_INPUT | _lib.DA_ROUTE_NORMALIZE_OUTPUT | _lib.DA_ROUTE_BETA_IS_LOG,
+                code, routed.data_ptr(), R, handle),
+            "attention": lambda: lib.da_routed_attention(
+                routed.data_ptr(), routed.data_ptr() + W * routed.element_size(), length * 2 * W, 2 * W,
+                rp if H > S else R, S // H if S > H else 1, rp, vt.data_ptr(), vt.stride(0), vt.stride(1),
+                batch, S, length, d, p["log_score_scales"].data_ptr(), pdt,
+                float(group ** -0.5), None if S == 1 else p["map_mix_logits"].data_ptr(), pdt,
+                _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX, code,
+                mixed.data_ptr(), length * d, d, 0, handle),
+            "output_projection": lambda: lib.da_linear(
+                mixed.data_ptr(), tokens, d, p["output.weight"].data_ptr(), d, None, pdt, code,
+                final.data_ptr(), handle),
+        }
+        kernel_us = {}
+        for name, launch in launches.items():
+            for _ in range(5):
+                _lib.check(launch(), name)
+            torch.cuda.synchronize()
+            begin = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            begin.record(stream)
+            for _ in range(args.kernel_reps):
+                launch()
+            end.record(stream)
+            end.synchronize()
+            kernel_us[name] = begin.elapsed_time(end) * 1e3 / args.kernel_reps
+
+    flops = {
+        "route": 4.0 * R * M * rows,
+        "attention": 2.0 * (rp + d) * length * (length + 1) / 2 * batch * S,
+        "qkv_projection": 2.0 * tokens * d * (2 * W + d),
+        "output_projection": 2.0 * tokens * d * d,
+    }
+    elem = 2
+    n_dict = 1 if raw_value is None else 2
+    in_elem = raw_key.element_size()
+    bytes_moved = {
+        "dict_normalize": n_dict * R * M * in_elem + 2 * R * M * elem,
+        "qkv_projection": (tokens * d + (2 * W + d) * d + tokens * (2 * W + d)) * elem,
+        "output_projection": (2 * tokens * d + d * d) * elem,
+    }
+    dominant = max(("route", "attention", "qkv_projection", "output_projection"), key=lambda k: kernel_us[k])
+    achieved = flops[dominant] / (kernel_us[dominant] * 1e-6) / 1e12
+    roofline = {
+        "kernel": dominant,
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+        "traffic": None,
+        "avg_launch_us": round(kernel_us[dominant], 3),
+    }
+    kernels = {}
+    for name, us in kernel_us.items():
+        entry = {"avg_us": round(us, 3)}
+        if name in flops:
+            tf = flops[name] / (us * 1e-6) / 1e12
+            entry.update(tflops=round(tf, 2), mfma_frac=round(tf / PEAK_BF16_TFLOPS, 4))
+        if name in bytes_moved:
+            gbs = bytes_moved[name] / (us * 1e-6) / 1e9
+            entry.update(gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
+        kernels[name] = entry
+
+    # ---- CPU baseline: the fp32 NumPy oracle on the host cores -------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+
+        params = {k: v.float().cpu().numpy() for k, v in module.state_dict().items()}
+        xn = x.float().cpu().numpy()
+        reps = 0
+        started = time.perf_counter()
+        while True:
+            oracle.shared_dictionary_attention(params, config, xn)
+            reps += 1
+            spent = time.perf_counter() - started
+            if spent >= args.cpu_seconds or spent / reps * (reps + 1) > 30.0:
+                break
+        cpu = {
+            "value": round(tokens * reps / spent, 1),
+            "unit": "tokens/s",
+            "cores": cpu_threads(),
+            "kind": "port",
+            "sample": f"{reps} full {args.workload} forwards of the fp32 NumPy oracle ({tokens} tokens each) in {spent:.1f} s on {cpu_model()}",
+        }
+        del np
+
+    line = {
+        "metric": METRIC,
+        "value": round(tokens / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic: x ~ N(0,1) seeded, default-init weights seeded",
+        "config": {
+            "workload": description,
+            "preset": preset,
+            "global_batch": batch,
+            "seq_len": length,
+            "routed_rows": rows,
+            "parallelism": "single GPU",
+        },
+        "routed_rows_per_s": round(rows / (kernel_us["route"] * 1e-6), 1),
+        "attention_tokens_per_s": round(tokens / (kernel_us["attention"] * 1e-6), 1),
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    del out
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,332 @@
+// C ABI entry points (declared in include/double_attention_hip.h).
+//
+// Each entry point validates its arguments on the host, then enqueues the
+// kernels on the caller's stream.  Nothing is allocated, freed or
+// synchronized here.  Validation failures return before any launch so the
+// stream is untouched; launch failures are reported from hipGetLastError.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/double_attention_hip.h"
+#include "da_launch.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+bool pow2_width(int64_t v) { return v == 64 || v == 128 || v == 256 || v == 512; }
+bool half_dtype(int d) { return d == DA_F16 || d == DA_BF16; }
+bool any_dtype(int d) { return d == DA_F32 || d == DA_F16 || d == DA_BF16; }
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DA_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  g_error.clear();
+  return DA_OK;
+}
+
+constexpr int64_t kAlign = 256;
+int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+int validate_route(const void* x, int64_t rows, int64_t R, int64_t xs, const void* kt,
+                   const void* v, int64_t atoms, const void* beta, int beta_dtype, int dtype,
+                   const void* out, int64_t os) {
+  if (!half_dtype(dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "route: dtype must be DA_F16 or DA_BF16");
+  if (!pow2_width(R)) return fail(DA_ERR_UNSUPPORTED, "route: routing_dim %lld not in {64,128,256,512}", (long long)R);
+  if (rows < 0 || atoms < 1 || atoms > (1 << 24)) return fail(DA_ERR_INVALID_ARGUMENT, "route: bad rows/atoms");
+  if (!x || !kt || !v || !out) return fail(DA_ERR_INVALID_ARGUMENT, "route: null pointer");
+  if (beta && !any_dtype(beta_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "route: bad beta dtype");
+  if (!aligned(x, 16) || !aligned(kt, 16) || !aligned(v, 16) || !aligned(out, 16))
+    return fail(DA_ERR_ALIGNMENT, "route: tensors must be 16-byte aligned");
+  if (xs < R || xs % 8 || os < R || os % 8)
+    return fail(DA_ERR_ALIGNMENT, "route: row strides must be >= routing_dim and multiples of 8");
+  if ((rows + 63) / 64 > 0x7fffffffLL) return fail(DA_ERR_UNSUPPORTED, "route: too many rows");
+  return DA_OK;
+}
+
+int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int64_t ms, int64_t rep,
+                       int64_t RP, const void* vt, int64_t vsb, int64_t vsd, int64_t B, int64_t S,
+                       int64_t T, int64_t D, const void* scales, int scales_dtype,
+                       const void* mix, int mix_dtype, int dtype, const void* out, int64_t ob,
+                       int64_t ot, int64_t os) {
+  if (!half_dtype(dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "attention: dtype must be DA_F16 or DA_BF16");
+  if (!pow2_width(RP)) return fail(DA_ERR_UNSUPPORTED, "attention: score_dim %lld not in {64,128,256,512}", (long long)RP);
+  if (!pow2_width(D)) return fail(DA_ERR_UNSUPPORTED, "attention: value_dim %lld not in {64,128,256,512}", (long long)D);
+  if (B < 0 || T < 0 || S < 1 || rep < 1 || B > 65535 || T > (1LL << 30))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention: bad batch/maps/length/map_repeat");
+  if (!q || !k || !vt || !scales || !out) return fail(DA_ERR_INVALID_ARGUMENT, "attention: null pointer");
+  if (!any_dtype(scales_dtype) || (mix && !any_dtype(mix_dtype)))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention: bad scalar dtype");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(vt, 16) || !aligned(out, 8))
+    return fail(DA_ERR_ALIGNMENT, "attention: q/k/value_t must be 16-byte and out 8-byte aligned");
+  if (sb % 8 || st % 8 || ms % 8 || st < RP)
+    return fail(DA_ERR_ALIGNMENT, "attention: q/k strides must be multiples of 8 and stride_t >= score_dim");
+  if (vsd % 8 || vsb % 8 || vsd < da::round_up(T, da::kKeyPad) || (B > 1 && vsb < D * vsd))
+    return fail(DA_ERR_ALIGNMENT, "attention: value_t pitches must be multiples of 8, vt_stride_d >= padded length");
+  if (ob % 4 || ot % 4 || os % 4) return fail(DA_ERR_ALIGNMENT, "attention: out strides must be multiples of 4");
+  return DA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int da_abi_version(void) { return 1; }
+
+const char* da_last_error(void) { return g_error.c_str(); }
+
+int64_t da_padded_atoms(int64_t atoms) { return da::round_up(atoms, da::kAtomPad); }
+
+int64_t da_padded_length(int64_t length) { return da::round_up(length, da::kKeyPad); }
+
+int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_dtype,
+                            int64_t routing_dim, int64_t atoms, float eps, void* key_t,
+                            void* value, int out_dtype, da_stream_t stream) {
+  if (!any_dtype(raw_dtype) || !half_dtype(out_dtype))
+    return fail(DA_ERR_INVALID_ARGUMENT, "normalize: bad dtype");
+  if (!pow2_width(routing_dim))
+    return fail(DA_ERR_UNSUPPORTED, "normalize: routing_dim %lld not in {64,128,256,512}", (long long)routing_dim);
+  if (atoms < 1 || atoms > (1 << 24)) return fail(DA_ERR_INVALID_ARGUMENT, "normalize: bad atom count");
+  if (!raw_key || !key_t || !value) return fail(DA_ERR_INVALID_ARGUMENT, "normalize: null pointer");
+  if (!aligned(key_t, 16) || !aligned(value, 16)) return fail(DA_ERR_ALIGNMENT, "normalize: outputs must be 16-byte aligned");
+  da::launch_dictionary_normalize(raw_key, raw_value, raw_dtype, static_cast<int>(routing_dim),
+                                  static_cast<int>(atoms), eps, key_t, value, out_dtype,
+                                  reinterpret_cast<hipStream_t>(stream));
+  return check_launch("normalize");
+}
+
+int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_t x_row_stride,
+                        const void* key_t, const void* value, int64_t atoms, const void* beta,
+                        int beta_dtype, float beta_value, float eps, int flags, int dtype,
+                        void* out, int64_t out_row_stride, da_stream_t stream) {
+  int rc = validate_route(x, rows, routing_dim, x_row_stride, key_t, value, atoms, beta, beta_dtype,
+                          dtype, out, out_row_stride);
+  if (rc) return rc;
+  da::RouteArgs a{x, rows, x_row_stride, static_cast<int>(routing_dim), key_t, value,
+                  static_cast<int>(atoms), beta, beta_dtype, beta_value, eps, flags, dtype, out,
+                  out_row_stride};
+  da::launch_dictionary_route(a, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("route");
+}
+
+int da_routed_attention(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
+                        int64_t map_stride, int64_t map_repeat, int64_t score_dim,
+                        const void* value_t, int64_t vt_stride_b, int64_t vt_stride_d,
+                        int64_t batch, int64_t maps, int64_t length, int64_t value_dim,
+                        const void* scales, int scales_dtype, float scale_mult,
+                        const void* mix_logits, int mix_dtype, int flags, int dtype, void* out,
+                        int64_t out_stride_b, int64_t out_stride_t, int64_t out_stride_s,
+                        da_stream_t stream) {
+  int rc = validate_attention(query, key, stride_b, stride_t, map_stride, map_repeat, score_dim,
+                              value_t, vt_stride_b, vt_stride_d, batch, maps, length, value_dim,
+                              scales, scales_dtype, mix_logits, mix_dtype, dtype, out,
+                              out_stride_b, out_stride_t, out_stride_s);
+  if (rc) return rc;
+  da::AttentionArgs a;
+  a.q = query;
+  a.k = key;
+  a.qk_stride_b = stride_b;
+  a.qk_stride_t = stride_t;
+  a.map_stride = map_stride;
+  a.map_repeat = static_cast<int>(map_repeat);
+  a.RP = static_cast<int>(score_dim);
+  a.vt = value_t;
+  a.vt_stride_b = vt_stride_b;
+  a.vt_stride_d = vt_stride_d;
+  a.B = static_cast<int>(batch);
+  a.S = static_cast<int>(maps);
+  a.T = static_cast<int>(length);
+  a.D = static_cast<int>(value_dim);
+  a.scales = scales;
+  a.scales_dtype = scales_dtype;
+  a.scale_mult = scale_mult;
+  a.mix_logits = mix_logits;
+  a.mix_dtype = mix_dtype;
+  a.flags = flags;
+  a.dtype = dtype;
+  a.out = out;
+  a.out_stride_b = out_stride_b;
+  a.out_stride_t = out_stride_t;
+  a.out_stride_s = out_stride_s;
+  da::launch_routed_attention(a, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("attention");
+}
+
+static int validate_gemm_common(const char* what, const void* x, int64_t rows, int64_t K, int dtype) {
+  if (!half_dtype(dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "%s: dtype must be DA_F16 or DA_BF16", what);
+  if (rows < 0 || K < 32 || K % 32) return fail(DA_ERR_UNSUPPORTED, "%s: in_features must be a positive multiple of 32", what);
+  if (!x || !aligned(x, 16)) return fail(DA_ERR_ALIGNMENT, "%s: input must be non-null and 16-byte aligned", what);
+  return DA_OK;
+}
+
+int da_qkv_projection(const void* x, int64_t tokens, int64_t model_dim, int64_t length,
+                      const void* wq, const void* wk, int64_t qk_width, const void* wv,
+                      const void* bv, int64_t value_dim, int bias_dtype, int dtype, void* qk_out,
+                      void* value_t, int64_t vt_stride_b, int64_t vt_pitch, da_stream_t stream) {
+  int rc = validate_gemm_common("projection", x, tokens, model_dim, dtype);
+  if (rc) return rc;
+  if (length < 1 || tokens % length) return fail(DA_ERR_INVALID_ARGUMENT, "projection: tokens must be a multiple of length");
+  if (qk_width < 8 || qk_width % 8 || value_dim < 4 || value_dim % 4)
+    return fail(DA_ERR_UNSUPPORTED, "projection: qk_width must be a multiple of 8 and value_dim of 4");
+  if (!wq || !wk || !wv || !qk_out || !value_t) return fail(DA_ERR_INVALID_ARGUMENT, "projection: null pointer");
+  if (!aligned(wq, 16) || !aligned(wk, 16) || !aligned(wv, 16) || !aligned(qk_out, 16) || !aligned(value_t, 16))
+    return fail(DA_ERR_ALIGNMENT, "projection: tensors must be 16-byte aligned");
+  if (bv && !any_dtype(bias_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "projection: bad bias dtype");
+  if (vt_pitch < length || vt_pitch % 8 || vt_stride_b < value_dim * vt_pitch)
+    return fail(DA_ERR_ALIGNMENT, "projection: bad value_t pitches");
+  da::GemmSegment segs[2];
+  segs[0] = da::GemmSegment{wq, wk, qk_width, x, 2 * qk_width, tokens, model_dim, nullptr, 0, 0,
+                            qk_out, 2 * qk_width, 0, 0, 0};
+  segs[1] = da::GemmSegment{x, nullptr, 0, wv, tokens, value_dim, model_dim, bv, bias_dtype, 1,
+                            value_t, 0, length, vt_pitch, vt_stride_b};
+  da::launch_gemm(segs, 2, dtype, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("projection");
+}
+
+int da_linear(const void* x, int64_t rows, int64_t in_features, const void* weight,
+              int64_t out_features, const void* bias, int bias_dtype, int dtype, void* out,
+              da_stream_t stream) {
+  int rc = validate_gemm_common("linear", x, rows, in_features, dtype);
+  if (rc) return rc;
+  if (out_features < 4 || out_features % 4) return fail(DA_ERR_UNSUPPORTED, "linear: out_features must be a multiple of 4");
+  if (!weight || !out || !aligned(weight, 16) || !aligned(out, 8))
+    return fail(DA_ERR_ALIGNMENT, "linear: weight/out must be non-null and aligned");
+  if (bias && !any_dtype(bias_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "linear: bad bias dtype");
+  da::GemmSegment seg{weight, nullptr, 0, x, out_features, rows, in_features, bias, bias_dtype, 0,
+                      out, out_features, 0, 0, 0};
+  da::launch_gemm(&seg, 1, dtype, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("linear");
+}
+
+int64_t da_sda_workspace_offset(int64_t batch, int64_t length, int64_t model_dim, int64_t qk_width,
+                                int which) {
+  const int64_t tokens = batch * length;
+  const int64_t routed = align_up(tokens * 2 * qk_width * 2);
+  const int64_t vt = align_up(batch * model_dim * da::round_up(length, da::kKeyPad) * 2);
+  if (which <= 0) return 0;
+  if (which == 1) return routed;
+  return routed + vt;
+}
+
+int64_t da_sda_workspace_bytes(int64_t batch, int64_t length, int64_t model_dim, int64_t qk_width,
+                               int64_t outer_maps, int concat, int has_output_projection) {
+  const int64_t tokens = batch * length;
+  const int64_t mixed =
+      has_output_projection ? align_up(tokens * (concat ? outer_maps : 1) * model_dim * 2) : 0;
+  return da_sda_workspace_offset(batch, length, model_dim, qk_width, 2) + mixed;
+}
+
+int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stream_t stream) {
+  if (!a) return fail(DA_ERR_INVALID_ARGUMENT, "forward: null args");
+  const int64_t B = a->batch, T = a->length, d = a->model_dim;
+  const int64_t H = a->qk_branches, S = a->outer_maps, R = a->routing_dim;
+  if (B < 1 || T < 1 || d < 1 || H < 1 || S < 1 || R < 1 || a->atoms < 1)
+    return fail(DA_ERR_INVALID_ARGUMENT, "forward: sizes must be positive");
+  if ((H > S ? H % S : S % H) != 0) return fail(DA_ERR_INVALID_ARGUMENT, "forward: branches and maps must divide one another");
+  if (!half_dtype(a->dtype) || !any_dtype(a->param_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "forward: bad dtype");
+  if (!a->x || !a->wq || !a->wk || !a->wv || !a->key_t || !a->value || !a->log_beta ||
+      !a->log_score_scales || !a->out || !a->workspace)
+    return fail(DA_ERR_INVALID_ARGUMENT, "forward: null pointer");
+  const bool concat = a->flags & DA_SDA_CONCAT;
+  if (concat && !a->wo) return fail(DA_ERR_INVALID_ARGUMENT, "forward: concat combine needs an output projection");
+  if (!aligned(a->workspace, 256)) return fail(DA_ERR_ALIGNMENT, "forward: workspace must be 256-byte aligned");
+  const int64_t need = da_sda_workspace_bytes(B, T, d, H * R, S, concat, a->wo != nullptr);
+  if (a->workspace_bytes < need)
+    return fail(DA_ERR_WORKSPACE, "forward: workspace of %lld bytes < %lld required",
+                (long long)a->workspace_bytes, (long long)need);
+  const int64_t W = H * R;
+  const int64_t group = H > S ? H / S : 1;
+  const int64_t RP = group * R;
+  const int64_t Tp = da::round_up(T, da::kKeyPad);
+  char* ws = static_cast<char*>(a->workspace);
+  void* routed = ws;
+  void* vt = ws + da_sda_workspace_offset(B, T, d, W, 1);
+  void* mixed = a->wo ? ws + da_sda_workspace_offset(B, T, d, W, 2) : a->out;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  // Validate every stage before enqueueing the first one.
+  int rc = validate_gemm_common("forward/projection", a->x, B * T, d, a->dtype);
+  if (rc) return rc;
+  if (W % 8) return fail(DA_ERR_UNSUPPORTED, "forward: qk width must be a multiple of 8");
+  rc = validate_route(routed, B * T * 2 * H, R, R, a->key_t, a->value, a->atoms, a->log_beta,
+                      a->param_dtype, a->dtype, routed, R);
+  if (rc) return rc;
+  const int64_t ot = concat ? S * d : d;
+  rc = validate_attention(routed, static_cast<char*>(routed) + W * 2, T * 2 * W, 2 * W,
+                          H > S ? RP : R, 1, RP, vt, d * Tp, Tp, B, S, T, d, a->log_score_scales,
+                          a->param_dtype, a->map_mix_logits, a->param_dtype, a->dtype, mixed,
+                          T * ot, ot, concat ? d : 0);
+  if (rc) return rc;
+  if (a->wo) {
+    rc = validate_gemm_common("forward/output", mixed, B * T, ot, a->dtype);
+    if (rc) return rc;
+    if (d % 4) return fail(DA_ERR_UNSUPPORTED, "forward: model_dim must be a multiple of 4");
+  }
+  if (!aligned(a->wq, 16) || !aligned(a->wk, 16) || !aligned(a->wv, 16) || (a->wo && !aligned(a->wo, 16)) ||
+      !aligned(a->out, 16))
+    return fail(DA_ERR_ALIGNMENT, "forward: weights and output must be 16-byte aligned");
+
+  // 1. Q/K projections (route rows) and V^T with bias.
+  da::GemmSegment proj[2];
+  proj[0] = da::GemmSegment{a->wq, a->wk, W, a->x, 2 * W, B * T, d, nullptr, 0, 0, routed, 2 * W, 0, 0, 0};
+  proj[1] = da::GemmSegment{a->x, nullptr, 0, a->wv, B * T, d, d, a->bv, a->param_dtype, 1, vt, 0, T, Tp, d * Tp};
+  da::launch_gemm(proj, 2, a->dtype, s);
+  // 2. Route all Q and K rows in place: [tokens, 2, H, R] is [tokens*2H, R].
+  int rflags = da::kRouteBetaIsLog;
+  if (a->flags & DA_SDA_NORMALIZE_INPUT) rflags |= da::kRouteNormalizeInput;
+  if (a->flags & DA_SDA_NORMALIZE_OUTPUT) rflags |= da::kRouteNormalizeOutput;
+  da::RouteArgs ra{routed, B * T * 2 * H, R, static_cast<int>(R), a->key_t, a->value,
+                   static_cast<int>(a->atoms), a->log_beta, a->param_dtype, 0.f, a->eps, rflags,
+                   a->dtype, routed, R};
+  da::launch_dictionary_route(ra, s);
+  // 3. Outer attention over the S maps, mixed (or concatenated).
+  da::AttentionArgs at;
+  at.q = routed;
+  at.k = static_cast<char*>(routed) + W * 2;
+  at.qk_stride_b = T * 2 * W;
+  at.qk_stride_t = 2 * W;
+  at.map_stride = H > S ? RP : R;
+  at.map_repeat = static_cast<int>(S > H ? S / H : 1);
+  at.RP = static_cast<int>(RP);
+  at.vt = vt;
+  at.vt_stride_b = d * Tp;
+  at.vt_stride_d = Tp;
+  at.B = static_cast<int>(B);
+  at.S = static_cast<int>(S);
+  at.T = static_cast<int>(T);
+  at.D = static_cast<int>(d);
+  at.scales = a->log_score_scales;
+  at.scales_dtype = a->param_dtype;
+  at.scale_mult = group > 1 ? static_cast<float>(1.0 / std::sqrt(static_cast<double>(group))) : 1.f;
+  at.mix_logits = a->map_mix_logits;
+  at.mix_dtype = a->param_dtype;
+  at.flags = da::kAttnScalesAreLog | ((a->flags & DA_SDA_CAUSAL) ? da::kAttnCausal : 0) |
+             (concat ? 0 : da::kAttnMix);
+  at.dtype = a->dtype;
+  at.out = mixed;
+  at.out_stride_b = T * ot;
+  at.out_stride_t = ot;
+  at.out_stride_s = concat ? d : 0;
+  da::launch_routed_attention(at, s);
+  // 4. Output projection.
+  if (a->wo) {
+    da::GemmSegment o{a->wo, nullptr, 0, mixed, d, B * T, ot, nullptr, 0, 0, a->out, d, 0, 0, 0};
+    da::launch_gemm(&o, 1, a->dtype, s);
+  }
+  return check_launch("forward");
+}
+
+}  // extern "C"

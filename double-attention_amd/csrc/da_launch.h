@@ -1,0 +1,97 @@
+// Host-side launch interfaces between the C ABI (capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+namespace da {
+
+constexpr int kAtomPad = 64;   // dictionary atoms are padded to a multiple of this
+constexpr int kKeyPad = 64;    // V^T rows are padded to a multiple of this many tokens
+
+// Clamp bounds of the reference's temperatures (modules.py:130-132, ops.py:160-161).
+constexpr float kLogBetaMin = -2.995732273553991f;   // ln 0.05
+constexpr float kLogBetaMax = 4.1588830833596715f;   // ln 64
+constexpr float kLogScaleMin = -1.3862943611198906f; // ln 0.25
+constexpr float kLogScaleMax = 6.931471805599453f;   // ln 1024
+
+// Route flags (mirrored in include/double_attention_hip.h).
+enum : int {
+  kRouteNormalizeInput = 1,
+  kRouteNormalizeOutput = 2,
+  kRouteBetaIsLog = 4,
+};
+
+// Attention flags.
+enum : int {
+  kAttnCausal = 1,
+  kAttnScalesAreLog = 2,
+  kAttnMix = 4,   // weighted sum over maps into one output; else one output per map
+};
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+struct RouteArgs {
+  const void* x;
+  int64_t rows;
+  int64_t x_stride;
+  int R;
+  const void* key_t;
+  const void* value;
+  int M;
+  const void* beta_ptr;
+  int beta_dtype;
+  float beta_value;
+  float eps;
+  int flags;
+  int dtype;
+  void* out;
+  int64_t out_stride;
+};
+
+struct AttentionArgs {
+  const void* q;
+  const void* k;
+  int64_t qk_stride_b, qk_stride_t;   // element strides of a routed row
+  int64_t map_stride;                 // elements between the first branches of consecutive maps
+  int map_repeat;                     // maps sharing one branch (S > H repeat)
+  int RP;                             // score width R' of one map
+  const void* vt;                     // V^T [B, D, Tv] (token-contiguous)
+  int64_t vt_stride_b, vt_stride_d;
+  int B, S, T, D;
+  const void* scales;
+  int scales_dtype;
+  float scale_mult;                   // extra factor on every score scale (RMS-sum groups)
+  const void* mix_logits;             // [S] map-mix logits or nullptr (uniform)
+  int mix_dtype;
+  int flags;
+  int dtype;
+  void* out;
+  int64_t out_stride_b, out_stride_t, out_stride_s;
+};
+
+struct GemmSegment {
+  // D[i, j] = sum_k P[i, k] Q[j, k]; P rows may come from two stacked matrices
+  // (rows [0, split) from p0, rows [split, I) from p1).
+  const void* p0;
+  const void* p1;
+  int64_t p_split;
+  const void* q;
+  int64_t I, J, K;
+  const void* bias;       // nullptr or [I] (mode rows) / [J] (mode vt)
+  int bias_dtype;
+  int mode;               // 0: out[j, i] (row-major by j), 1: V^T layout
+  void* out;
+  int64_t ldo;            // mode 0: row pitch of out (elements)
+  int64_t T, Tp, vt_stride_b;   // mode 1: token t of sequence b goes to out[b*vt_stride_b + i_feat*Tp + t]
+};
+
+void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int in_dtype, int R,
+                                 int M, float eps, void* key_t, void* value, int out_dtype,
+                                 hipStream_t stream);
+void launch_dictionary_route(const RouteArgs& a, hipStream_t stream);
+void launch_routed_attention(const AttentionArgs& a, hipStream_t stream);
+void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream);
+
+}  // namespace da

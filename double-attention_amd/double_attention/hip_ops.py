@@ -1,0 +1,559 @@
+"""PyTorch-facing wrappers of the gfx950 kernels.
+
+Operator-level entry points mirror the reference's Triton functions so that
+code and tests written against those read the same:
+
+* ``dictionary_route_hip``   <- ``dictionary_route_triton`` (reference
+  ``src/double_attention/triton_kernels.py:1984-2019``)
+* ``routed_attention_hip``   <- ``routed_attention_triton`` (``triton_kernels.py:2290-2305``)
+* ``dictionary_normalize_hip`` <- ``SharedDictionaryBank.normalized`` (``modules.py:45-48``)
+
+``shared_dictionary_attention_hip`` runs a whole ``SharedDictionaryAttention``
+forward (``modules.py:190-291``) in one C call: projection GEMM, route, flash
+attention with the fused map mix, output GEMM.
+
+PyTorch only supplies device memory and the current stream.  Every buffer,
+including the workspace, is allocated here with the caching allocator and
+handed to the library as a raw pointer; kernels run on
+``torch.cuda.current_stream()``.  Nothing here falls back to another
+implementation: an unsupported shape or variant raises.
+
+Autograd: the kernels are forward-only.  When gradients are required the
+forward still runs on the HIP path and the backward recomputes the
+PyTorch reference composition (``ops.py``) on the same device, the pattern
+the reference itself used before it had native backward kernels.
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from .ops import dictionary_route_reference, routed_attention_reference
+
+_DTYPE_CODES = {torch.float32: _lib.DA_F32, torch.float16: _lib.DA_F16, torch.bfloat16: _lib.DA_BF16}
+SUPPORTED_WIDTHS = (64, 128, 256, 512)
+ATOM_PAD = 64
+TOKEN_PAD = 64
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError as exc:
+        raise ValueError(f"unsupported dtype {dtype}") from exc
+
+
+def _half_code(dtype: torch.dtype) -> int:
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"HIP kernels require fp16 or bf16 tensors, got {dtype}")
+    return _DTYPE_CODES[dtype]
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(*tensors: Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError("HIP kernels require tensors on a ROCm device")
+
+
+def _round_up(v: int, m: int) -> int:
+    return (v + m - 1) // m * m
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# --------------------------------------------------------------------------
+# Dictionary normalization and route layouts
+# --------------------------------------------------------------------------
+
+
+class RouteDictionary(NamedTuple):
+    """A normalized bank in the layouts the route kernel reads.
+
+    ``key_t`` is ``[Mp, R]`` (atom-major), ``value`` is ``[R, Mp]``; atoms past
+    ``atoms`` are zero.  ``Mp`` is ``atoms`` rounded up to a multiple of 64.
+    """
+
+    key_t: Tensor
+    value: Tensor
+    atoms: int
+
+
+def _tag(key: Tensor, value: Tensor, layout: RouteDictionary) -> tuple[Tensor, Tensor]:
+    key._da_route_layout = layout  # type: ignore[attr-defined]
+    value._da_route_layout = layout  # type: ignore[attr-defined]
+    return key, value
+
+
+def dictionary_normalize_hip(
+    raw_key: Tensor,
+    raw_value: Tensor | None,
+    eps: float = 1e-6,
+    dtype: torch.dtype | None = None,
+) -> tuple[Tensor, Tensor]:
+    """Column-normalize a bank in one launch; returns ``(key, value)`` as ``[R, M]``.
+
+    The returned tensors are views of the route layouts (so handing them back
+    to the route costs no copy); for a tied bank both views read the same
+    normalized atoms.  Matches ``F.normalize(raw, dim=0, eps=eps)``.
+    """
+
+    if raw_key.ndim != 2:
+        raise ValueError("raw_key must be [routing_dim, atoms]")
+    if raw_value is not None and raw_value.shape != raw_key.shape:
+        raise ValueError("raw_value must match raw_key")
+    _require_cuda(raw_key, *(() if raw_value is None else (raw_value,)))
+    dtype = dtype or raw_key.dtype
+    routing_dim, atoms = raw_key.shape
+    if routing_dim not in SUPPORTED_WIDTHS:
+        raise NotImplementedError(f"HIP route supports routing_dim in {SUPPORTED_WIDTHS}, got {routing_dim}")
+    padded = _round_up(atoms, ATOM_PAD)
+    key_t = torch.empty(padded, routing_dim, dtype=dtype, device=raw_key.device)
+    value = torch.empty(routing_dim, padded, dtype=dtype, device=raw_key.device)
+    raw_key_c = raw_key.detach().contiguous()
+    raw_value_c = None if raw_value is None else raw_value.detach().to(raw_key.dtype).contiguous()
+    lib = _lib.get()
+    _lib.check(
+        lib.da_dictionary_normalize(
+            raw_key_c.data_ptr(),
+            _ptr(raw_value_c),
+            dtype_code(raw_key_c.dtype),
+            routing_dim,
+            atoms,
+            float(eps),
+            key_t.data_ptr(),
+            value.data_ptr(),
+            _half_code(dtype),
+            _stream(raw_key.device),
+        ),
+        "dictionary_normalize_hip",
+    )
+    layout = RouteDictionary(key_t, value, atoms)
+    return _tag(key_t[:atoms].t(), value[:, :atoms], layout)
+
+
+def route_layout(dictionary_key: Tensor, dictionary_value: Tensor, dtype: torch.dtype) -> RouteDictionary:
+    """Route layouts for a normalized ``[R, M]`` key/value pair (copy-free when tagged)."""
+
+    layout = getattr(dictionary_key, "_da_route_layout", None)
+    if (
+        layout is not None
+        and getattr(dictionary_value, "_da_route_layout", None) is layout
+        and layout.key_t.dtype == dtype
+    ):
+        return layout
+    if dictionary_key.ndim != 2 or dictionary_value.shape != dictionary_key.shape:
+        raise ValueError("dictionary key and value must both be [routing_dim, atoms]")
+    routing_dim, atoms = dictionary_key.shape
+    padded = _round_up(atoms, ATOM_PAD)
+    key_t = torch.zeros(padded, routing_dim, dtype=dtype, device=dictionary_key.device)
+    value = torch.zeros(routing_dim, padded, dtype=dtype, device=dictionary_key.device)
+    key_t[:atoms].copy_(dictionary_key.detach().t())
+    value[:, :atoms].copy_(dictionary_value.detach())
+    return RouteDictionary(key_t, value, atoms)
+
+
+# --------------------------------------------------------------------------
+# Route
+# --------------------------------------------------------------------------
+
+
+def _check_route_variant(
+    silu_logits: bool, direct_silu: bool, standardize_logits: bool
+) -> None:
+    if silu_logits or direct_silu or standardize_logits:
+        raise NotImplementedError(
+            "the HIP route kernel implements the identity activation with softmax "
+            "assignment; SiLU logits, standardized logits and direct SiLU assignment "
+            "are not implemented on this backend"
+        )
+
+
+def _route_forward(
+    x: Tensor,
+    layout: RouteDictionary,
+    beta: Tensor | float,
+    eps: float,
+    normalize_input: bool,
+    normalize_output: bool,
+) -> Tensor:
+    routing_dim = x.shape[-1]
+    if routing_dim != layout.key_t.shape[1]:
+        raise ValueError("input width does not match the dictionary routing_dim")
+    if routing_dim not in SUPPORTED_WIDTHS:
+        raise NotImplementedError(f"HIP route supports routing_dim in {SUPPORTED_WIDTHS}, got {routing_dim}")
+    if x.dtype != layout.key_t.dtype:
+        raise ValueError("input and dictionary must have one matching dtype")
+    rows_view = x.reshape(-1, routing_dim)
+    if rows_view.stride(-1) != 1 or rows_view.stride(0) % 8 or rows_view.data_ptr() % 16:
+        rows_view = rows_view.contiguous()
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    flags = (_lib.DA_ROUTE_NORMALIZE_INPUT if normalize_input else 0) | (
+        _lib.DA_ROUTE_NORMALIZE_OUTPUT if normalize_output else 0
+    )
+    if isinstance(beta, Tensor):
+        if beta.numel() != 1:
+            raise ValueError("beta must be a scalar")
+        _require_cuda(beta)
+        beta_c = beta.detach().contiguous()
+        beta_ptr, beta_code, beta_value = beta_c.data_ptr(), dtype_code(beta_c.dtype), 0.0
+    else:
+        beta_c = None
+        beta_ptr, beta_code, beta_value = None, _lib.DA_F32, float(beta)
+    lib = _lib.get()
+    _lib.check(
+        lib.da_dictionary_route(
+            rows_view.data_ptr(),
+            rows_view.shape[0],
+            routing_dim,
+            rows_view.stride(0),
+            layout.key_t.data_ptr(),
+            layout.value.data_ptr(),
+            layout.atoms,
+            beta_ptr,
+            beta_code,
+            beta_value,
+            float(eps),
+            flags,
+            _half_code(x.dtype),
+            out.data_ptr(),
+            routing_dim,
+            _stream(x.device),
+        ),
+        "dictionary_route_hip",
+    )
+    del beta_c
+    return out
+
+
+class _RouteFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output):  # type: ignore[override]
+        layout = route_layout(dictionary_key, dictionary_value, x.dtype)
+        ctx.save_for_backward(x, dictionary_key, dictionary_value, *(beta,) if isinstance(beta, Tensor) else ())
+        ctx.beta_is_tensor = isinstance(beta, Tensor)
+        ctx.beta = None if ctx.beta_is_tensor else beta
+        ctx.eps = eps
+        ctx.flags = (normalize_input, normalize_output)
+        return _route_forward(x, layout, beta, eps, normalize_input, normalize_output)
+
+    @staticmethod
+    def backward(ctx, grad):  # type: ignore[override]
+        saved = ctx.saved_tensors
+        x, dk, dv = saved[:3]
+        beta = saved[3] if ctx.beta_is_tensor else ctx.beta
+        with torch.enable_grad():
+            inputs = [t.detach().requires_grad_(t.requires_grad) for t in (x, dk, dv)]
+            beta_in = beta.detach().requires_grad_(beta.requires_grad) if ctx.beta_is_tensor else beta
+            out = dictionary_route_reference(
+                inputs[0], inputs[1], inputs[2], beta_in, ctx.eps,
+                normalize_input=ctx.flags[0], normalize_output=ctx.flags[1],
+            )
+            wrt = [t for t in inputs if t.requires_grad]
+            if ctx.beta_is_tensor and beta_in.requires_grad:
+                wrt.append(beta_in)
+            grads = torch.autograd.grad(out, wrt, grad) if wrt else ()
+        it = iter(grads)
+        result = [next(it) if t.requires_grad else None for t in inputs]
+        beta_grad = next(it) if ctx.beta_is_tensor and beta_in.requires_grad else None
+        return (*result, beta_grad, None, None, None)
+
+
+def dictionary_route_hip(
+    input: Tensor,
+    dictionary_key: Tensor,
+    dictionary_value: Tensor,
+    beta: Tensor | float,
+    eps: float = 1e-6,
+    silu_logits: bool = False,
+    direct_silu: bool = False,
+    silu_gain: float = 1.0,
+    standardize_logits: bool = False,
+    standardized_logit_scale: float | None = None,
+    normalize_input: bool = True,
+    normalize_output: bool = True,
+) -> Tensor:
+    """Fused dictionary route on gfx950; same arguments as ``dictionary_route_triton``.
+
+    ``input`` is ``[..., R]`` (any number of rows), ``dictionary_key`` and
+    ``dictionary_value`` are normalized ``[R, M]`` banks in the input dtype.
+    """
+
+    del silu_gain, standardized_logit_scale
+    _check_route_variant(silu_logits, direct_silu, standardize_logits)
+    _require_cuda(input, dictionary_key, dictionary_value)
+    if dictionary_key.dtype != input.dtype or dictionary_value.dtype != input.dtype:
+        raise ValueError("input and dictionaries must have one matching dtype")
+    needs_grad = torch.is_grad_enabled() and any(
+        t.requires_grad for t in (input, dictionary_key, dictionary_value, *((beta,) if isinstance(beta, Tensor) else ()))
+    )
+    if needs_grad:
+        return _RouteFunction.apply(input, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output)
+    layout = route_layout(dictionary_key, dictionary_value, input.dtype)
+    return _route_forward(input, layout, beta, eps, normalize_input, normalize_output)
+
+
+# --------------------------------------------------------------------------
+# Outer attention
+# --------------------------------------------------------------------------
+
+
+def _next_width(width: int) -> int:
+    for w in SUPPORTED_WIDTHS:
+        if width <= w:
+            return w
+    raise NotImplementedError(f"HIP attention supports widths up to {SUPPORTED_WIDTHS[-1]}, got {width}")
+
+
+def value_transposed(value: Tensor, width: int | None = None) -> Tensor:
+    """``[B, T, D]`` -> zero-padded V^T ``[B, width, round_up(T, 64)]``."""
+
+    batch, length, model_dim = value.shape
+    width = width or model_dim
+    vt = torch.zeros(batch, width, _round_up(max(length, 1), TOKEN_PAD), dtype=value.dtype, device=value.device)
+    vt[:, :model_dim, :length].copy_(value.detach().transpose(1, 2))
+    return vt
+
+
+def _attention_forward(query: Tensor, key: Tensor, value: Tensor, scales: Tensor, causal: bool) -> Tensor:
+    batch, maps, length, score_dim = query.shape
+    model_dim = value.shape[-1]
+    score_width = _next_width(score_dim)
+    value_width = _next_width(model_dim)
+    q = query.detach()
+    k = key.detach()
+    if score_width != score_dim:
+        pad = (0, score_width - score_dim)
+        q = torch.nn.functional.pad(q, pad)
+        k = torch.nn.functional.pad(k, pad)
+    q = q.contiguous()
+    k = k.contiguous()
+    vt = value_transposed(value, value_width)
+    out = torch.empty(batch, maps, length, value_width, dtype=value.dtype, device=value.device)
+    scales_c = scales.detach().contiguous()
+    lib = _lib.get()
+    _lib.check(
+        lib.da_routed_attention(
+            q.data_ptr(), k.data_ptr(),
+            maps * length * score_width, score_width, length * score_width, 1, score_width,
+            vt.data_ptr(), vt.stride(0), vt.stride(1),
+            batch, maps, length, value_width,
+            scales_c.data_ptr(), dtype_code(scales_c.dtype), 1.0, None, _lib.DA_F32,
+            _lib.DA_ATTN_CAUSAL if causal else 0,
+            _half_code(value.dtype),
+            out.data_ptr(), out.stride(0), out.stride(2), out.stride(1),
+            _stream(value.device),
+        ),
+        "routed_attention_hip",
+    )
+    return out if value_width == model_dim else out[..., :model_dim]
+
+
+class _AttentionFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, query, key, value, scales, causal):  # type: ignore[override]
+        ctx.save_for_backward(query, key, value, scales)
+        ctx.causal = causal
+        return _attention_forward(query, key, value, scales, causal)
+
+    @staticmethod
+    def backward(ctx, grad):  # type: ignore[override]
+        saved = ctx.saved_tensors
+        with torch.enable_grad():
+            inputs = [t.detach().requires_grad_(t.requires_grad) for t in saved]
+            out = routed_attention_reference(*inputs, ctx.causal)
+            wrt = [t for t in inputs if t.requires_grad]
+            grads = torch.autograd.grad(out, wrt, grad) if wrt else ()
+        it = iter(grads)
+        return (*[next(it) if t.requires_grad else None for t in inputs], None)
+
+
+def routed_attention_hip(
+    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, causal: bool = True
+) -> Tensor:
+    """Flash outer attention on gfx950; same contract as ``routed_attention_triton``.
+
+    ``query``/``key`` ``[B, S, T, R]``, ``value`` ``[B, T, D]`` (shared by every
+    map), ``scales`` ``[S]``; returns ``[B, S, T, D]``.
+    """
+
+    if query.ndim != 4 or key.shape != query.shape:
+        raise ValueError("query and key must have matching [B, S, T, R] shapes")
+    if value.ndim != 3 or value.shape[:2] != (query.shape[0], query.shape[2]):
+        raise ValueError("value must have shape [B, T, D] matching query")
+    if scales.shape != (query.shape[1],):
+        raise ValueError(f"scales must have shape [{query.shape[1]}]")
+    _require_cuda(query, key, value, scales)
+    if query.dtype != key.dtype or query.dtype != value.dtype:
+        raise ValueError("query, key, and value must have one matching dtype")
+    _half_code(query.dtype)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value, scales)):
+        return _AttentionFunction.apply(query, key, value, scales, causal)
+    return _attention_forward(query, key, value, scales, causal)
+
+
+# --------------------------------------------------------------------------
+# Linear layers (exposed for tests and the LM path)
+# --------------------------------------------------------------------------
+
+
+def linear_hip(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    """``x @ weight.T (+ bias)`` with the library's MFMA GEMM."""
+
+    _require_cuda(x, weight)
+    code = _half_code(x.dtype)
+    if weight.dtype != x.dtype:
+        raise ValueError("x and weight must share a dtype")
+    rows = x.reshape(-1, x.shape[-1]).contiguous()
+    w = weight.contiguous()
+    out = torch.empty(*x.shape[:-1], weight.shape[0], dtype=x.dtype, device=x.device)
+    b = None if bias is None else bias.detach().contiguous()
+    lib = _lib.get()
+    _lib.check(
+        lib.da_linear(
+            rows.data_ptr(), rows.shape[0], rows.shape[1], w.data_ptr(), w.shape[0],
+            _ptr(b), dtype_code(b.dtype) if b is not None else _lib.DA_F32, code,
+            out.data_ptr(), _stream(x.device),
+        ),
+        "linear_hip",
+    )
+    return out
+
+
+def qkv_projection_hip(
+    x: Tensor, query_weight: Tensor, key_weight: Tensor, value_weight: Tensor, value_bias: Tensor | None
+) -> tuple[Tensor, Tensor]:
+    """Q/K projections ``[B, T, 2W]`` and padded V^T ``[B, D, Tp]`` in one launch."""
+
+    batch, length, model_dim = x.shape
+    width = query_weight.shape[0]
+    code = _half_code(x.dtype)
+    xc = x.contiguous()
+    qk = torch.empty(batch, length, 2 * width, dtype=x.dtype, device=x.device)
+    vt = torch.zeros(batch, value_weight.shape[0], _round_up(length, TOKEN_PAD), dtype=x.dtype, device=x.device)
+    b = None if value_bias is None else value_bias.detach().contiguous()
+    lib = _lib.get()
+    _lib.check(
+        lib.da_qkv_projection(
+            xc.data_ptr(), batch * length, model_dim, length,
+            query_weight.contiguous().data_ptr(), key_weight.contiguous().data_ptr(), width,
+            value_weight.contiguous().data_ptr(), _ptr(b), value_weight.shape[0],
+            dtype_code(b.dtype) if b is not None else _lib.DA_F32, code,
+            qk.data_ptr(), vt.data_ptr(), vt.stride(0), vt.stride(1), _stream(x.device),
+        ),
+        "qkv_projection_hip",
+    )
+    return qk, vt
+
+
+# --------------------------------------------------------------------------
+# Whole-module forward
+# --------------------------------------------------------------------------
+
+
+class HipForwardResult(NamedTuple):
+    output: Tensor
+    routed: Tensor   # [B, T, 2, H, R]: routed query branches, then key branches
+
+
+def check_module_supported(config) -> None:
+    """Raise ``NotImplementedError`` for variants the HIP kernels do not cover."""
+
+    if config.dictionary_activation != "identity" or config.dictionary_assignment != "softmax":
+        raise NotImplementedError(
+            "backend='hip' implements identity dictionary activation with softmax "
+            f"assignment; got activation={config.dictionary_activation!r}, "
+            f"assignment={config.dictionary_assignment!r}"
+        )
+    if config.standardize_dictionary_logits:
+        raise NotImplementedError("backend='hip' does not implement standardized dictionary logits")
+    if config.routing_dim not in SUPPORTED_WIDTHS:
+        raise NotImplementedError(f"backend='hip' supports routing_dim in {SUPPORTED_WIDTHS}")
+    group = config.qk_branches // config.outer_maps if config.qk_branches > config.outer_maps else 1
+    if group * config.routing_dim not in SUPPORTED_WIDTHS:
+        raise NotImplementedError("backend='hip' supports grouped score widths up to 512")
+    if config.model_dim not in SUPPORTED_WIDTHS:
+        raise NotImplementedError(f"backend='hip' supports model_dim in {SUPPORTED_WIDTHS}")
+
+
+def shared_dictionary_attention_hip(
+    module,
+    x: Tensor,
+    layout: RouteDictionary,
+    dtype: torch.dtype,
+) -> HipForwardResult:
+    """One ``SharedDictionaryAttention`` forward through the fused C entry point."""
+
+    config = module.config
+    batch, length, model_dim = x.shape
+    code = _half_code(dtype)
+
+    def cast(t: Tensor | None) -> Tensor | None:
+        if t is None:
+            return None
+        t = t.detach()
+        if t.dtype != dtype:
+            t = t.to(dtype)
+        return t.contiguous()
+
+    xc = cast(x)
+    wq = cast(module.query.weight)
+    wk = cast(module.key.weight)
+    wv = cast(module.value.weight)
+    wo = cast(module.output.weight) if isinstance(module.output, torch.nn.Linear) else None
+    # Scalars and the value bias share one dtype code.
+    scalar_dtype = module.log_score_scales.dtype
+    bv = module.value.bias
+    bv = None if bv is None else bv.detach().to(scalar_dtype).contiguous()
+    log_beta = module.log_beta.detach().to(scalar_dtype).contiguous()
+    log_scales = module.log_score_scales.detach().contiguous()
+    mix = module.map_mix_logits
+    mix = None if mix is None else mix.detach().to(scalar_dtype).contiguous()
+
+    concat = config.map_combine == "concat"
+    width = config.total_qk_width
+    lib = _lib.get()
+    ws_bytes = lib.da_sda_workspace_bytes(batch, length, model_dim, width, config.outer_maps, int(concat), int(wo is not None))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    out = torch.empty(batch, length, model_dim, dtype=dtype, device=x.device)
+    flags = (
+        (_lib.DA_SDA_NORMALIZE_INPUT if config.normalize_routing_input else 0)
+        | (_lib.DA_SDA_NORMALIZE_OUTPUT if config.normalize_routing_output else 0)
+        | (_lib.DA_SDA_CAUSAL if config.causal else 0)
+        | (_lib.DA_SDA_CONCAT if concat else 0)
+    )
+    args = _lib.SdaForwardArgs(
+        xc.data_ptr(), batch, length, model_dim,
+        config.qk_branches, config.outer_maps, config.routing_dim, layout.atoms,
+        wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), _ptr(bv), _ptr(wo),
+        layout.key_t.data_ptr(), layout.value.data_ptr(),
+        log_beta.data_ptr(), log_scales.data_ptr(), _ptr(mix),
+        dtype_code(scalar_dtype), code, float(config.eps), flags,
+        workspace.data_ptr(), ws_bytes, out.data_ptr(),
+    )
+    _lib.check(lib.da_shared_dictionary_attention_forward(args, _stream(x.device)), "shared_dictionary_attention_hip")
+    routed_bytes = batch * length * 2 * width * xc.element_size()
+    routed = workspace[:routed_bytes].view(dtype).view(batch, length, 2, config.qk_branches, config.routing_dim)
+    return HipForwardResult(out, routed)
+
+
+__all__ = [
+    "RouteDictionary",
+    "dictionary_normalize_hip",
+    "dictionary_route_hip",
+    "linear_hip",
+    "qkv_projection_hip",
+    "route_layout",
+    "routed_attention_hip",
+    "shared_dictionary_attention_hip",
+    "value_transposed",
+]

@@ -1,0 +1,536 @@
+"""Shared-dictionary attention modules with a gfx950 ``backend="hip"`` forward.
+
+The module tree, parameter names, buffer names and construction order follow
+the reference (``src/double_attention/modules.py:25-460``): checkpoints load
+unchanged, and a seeded construction consumes the RNG in the same order, so
+default-initialized weights are identical.  The HIP forward
+(``SharedDictionaryAttention._hip_forward``) replaces the projection,
+route, outer attention and map combine with one C call into the gfx950
+library; LayerNorm, FFN, embeddings and the LM head stay PyTorch ops.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import NamedTuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch import Tensor
+
+from .config import DoubleAttentionConfig
+from .ops import (
+    assemble_score_maps,
+    dictionary_route_reference,
+    resolve_backend,
+    routed_attention_reference,
+    score_scale_from_log,
+)
+
+# Reference switch (modules.py:22): one GEMM over cat(Wq, Wk) instead of two.
+FUSED_QUERY_KEY_PROJECTION = True
+
+
+class SharedDictionaryBank(nn.Module):
+    """Routing dictionary shared by several attention layers (``modules.py:25-54``).
+
+    ``raw_key`` (and ``raw_value`` when untied) are ``[routing_dim, atoms]``
+    and drawn ``N(0, 1/routing_dim)``.  A tied bank registers ``raw_value`` as
+    ``None`` and reconstructs with the key atoms.
+    """
+
+    def __init__(self, routing_dim: int, dictionary_size: int, *, untied: bool = True) -> None:
+        super().__init__()
+        self.routing_dim = routing_dim
+        self.dictionary_size = dictionary_size
+        self.untied = untied
+        std = routing_dim ** -0.5
+        self.raw_key = nn.Parameter(torch.randn(routing_dim, dictionary_size) * std)
+        if untied:
+            self.raw_value = nn.Parameter(torch.randn(routing_dim, dictionary_size) * std)
+        else:
+            self.register_parameter("raw_value", None)
+
+    def normalized(self, eps: float = 1e-6) -> tuple[Tensor, Tensor]:
+        """Unit-norm atoms ``(key, value)``; a tied bank returns one tensor twice."""
+
+        key = F.normalize(self.raw_key, dim=0, eps=eps)
+        value = key if self.raw_value is None else F.normalize(self.raw_value, dim=0, eps=eps)
+        return key, value
+
+    def normalized_hip(self, eps: float = 1e-6, dtype: torch.dtype | None = None) -> tuple[Tensor, Tensor]:
+        """``normalized`` computed by the gfx950 kernel, in the route layouts.
+
+        One launch covers both banks of an untied dictionary.  The returned
+        ``[R, M]`` tensors are views that the HIP route reads without a copy.
+        """
+
+        from .hip_ops import dictionary_normalize_hip
+
+        return dictionary_normalize_hip(self.raw_key, self.raw_value, eps, dtype)
+
+    def extra_repr(self) -> str:
+        return (
+            f"routing_dim={self.routing_dim}, dictionary_size={self.dictionary_size}, "
+            f"untied={self.untied}"
+        )
+
+
+@dataclass
+class DoubleAttentionAux:
+    """Intermediate tensors of one forward (``modules.py:57-65``)."""
+
+    routing_query: Tensor
+    routing_key: Tensor
+    score_query: Tensor
+    score_key: Tensor
+    score_scales: Tensor
+    map_weights: Tensor
+    backend: str
+
+
+class _Spec(NamedTuple):
+    is_cuda: bool
+    dtype: torch.dtype
+
+
+def _compute_dtype(x: Tensor, weight: Tensor) -> torch.dtype:
+    if x.is_cuda and torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return weight.dtype if x.dtype == weight.dtype else torch.promote_types(x.dtype, weight.dtype)
+
+
+class SharedDictionaryAttention(nn.Module):
+    """Routing/content-decoupled attention (``modules.py:68-291``)."""
+
+    def __init__(
+        self,
+        config: DoubleAttentionConfig,
+        *,
+        bank: SharedDictionaryBank | None = None,
+        create_bank: bool = True,
+    ) -> None:
+        super().__init__()
+        self.config = config
+        width = config.qk_branches * config.routing_dim
+        # Registration order matters: it fixes the default-init RNG stream.
+        self.query = nn.Linear(config.model_dim, width, bias=False)
+        self.key = nn.Linear(config.model_dim, width, bias=False)
+        self.value = nn.Linear(config.model_dim, config.model_dim, bias=config.value_bias)
+        if bank is None and create_bank:
+            bank = SharedDictionaryBank(
+                config.routing_dim, config.dictionary_size, untied=config.untied_dictionary
+            )
+        self.bank = bank
+
+        log_scale = math.log(config.initial_score_scale)
+        if config.outer_maps == 1:
+            scales = torch.tensor([log_scale])
+        else:
+            # A small deterministic spread breaks the symmetry between maps
+            # that share one Q/K branch (modules.py:101-105).
+            scales = log_scale + torch.linspace(-0.05, 0.05, config.outer_maps)
+        self.log_score_scales = nn.Parameter(scales)
+        log_beta = torch.tensor(math.log(config.beta))
+        if config.learnable_beta:
+            self.log_beta = nn.Parameter(log_beta)
+        else:
+            self.register_buffer("log_beta", log_beta, persistent=True)
+
+        if config.map_combine == "weighted_sum":
+            if config.outer_maps > 1:
+                self.map_mix_logits = nn.Parameter(torch.zeros(config.outer_maps))
+            else:
+                self.register_parameter("map_mix_logits", None)
+            self.output = (
+                nn.Linear(config.model_dim, config.model_dim, bias=False)
+                if config.output_projection
+                else nn.Identity()
+            )
+        else:
+            self.register_parameter("map_mix_logits", None)
+            self.output = nn.Linear(config.outer_maps * config.model_dim, config.model_dim, bias=False)
+
+    @property
+    def beta(self) -> Tensor:
+        return self.log_beta.clamp(math.log(0.05), math.log(64.0)).exp()
+
+    # ---- PyTorch path -----------------------------------------------------
+
+    def _project_branches(self, projection: nn.Linear, x: Tensor) -> Tensor:
+        batch, length, _ = x.shape
+        return self._reshape_branches(projection(x), batch, length)
+
+    def _reshape_branches(self, result: Tensor, batch: int, length: int) -> Tensor:
+        shaped = result.view(batch, length, self.config.qk_branches, self.config.routing_dim)
+        return shaped.permute(0, 2, 1, 3).contiguous()
+
+    def _project_query_key(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        if not FUSED_QUERY_KEY_PROJECTION:
+            return self._project_branches(self.query, x), self._project_branches(self.key, x)
+        batch, length, _ = x.shape
+        fused = F.linear(x, torch.cat((self.query.weight, self.key.weight), dim=0))
+        query, key = fused.split(self.config.total_qk_width, dim=-1)
+        return self._reshape_branches(query, batch, length), self._reshape_branches(key, batch, length)
+
+    def _route(self, x: Tensor, dictionary_key: Tensor, dictionary_value: Tensor, backend: str) -> Tensor:
+        cfg = self.config
+        if backend == "hip":
+            from .hip_ops import dictionary_route_hip
+
+            return dictionary_route_hip(
+                x, dictionary_key, dictionary_value, self.beta, cfg.eps,
+                cfg.dictionary_activation == "silu", cfg.dictionary_assignment == "silu",
+                cfg.dictionary_silu_gain, cfg.standardize_dictionary_logits,
+                cfg.standardized_logit_scale, cfg.normalize_routing_input,
+                cfg.normalize_routing_output,
+            )
+        return dictionary_route_reference(
+            x, dictionary_key, dictionary_value, self.beta, cfg.eps,
+            cfg.dictionary_activation, cfg.dictionary_assignment, cfg.dictionary_silu_gain,
+            cfg.standardize_dictionary_logits, cfg.standardized_logit_scale,
+            cfg.normalize_routing_input, cfg.normalize_routing_output,
+        )
+
+    def _combine(self, x: Tensor, map_output: Tensor) -> tuple[Tensor, Tensor]:
+        if self.config.map_combine == "weighted_sum":
+            if self.map_mix_logits is None:
+                return self.output(map_output[:, 0]), x.new_ones(1)
+            weights = torch.softmax(self.map_mix_logits, dim=0).to(map_output.dtype)
+            combined = torch.einsum("s,bstd->btd", weights, map_output)
+            return self.output(combined), weights
+        weights = x.new_full((self.config.outer_maps,), 1.0 / self.config.outer_maps)
+        return self.output(map_output.permute(0, 2, 1, 3).flatten(2)), weights
+
+    def _torch_forward(
+        self, x: Tensor, dictionary_key: Tensor, dictionary_value: Tensor, return_aux: bool
+    ) -> Tensor | tuple[Tensor, DoubleAttentionAux]:
+        query, key = self._project_query_key(x)
+        dense_value = self.value(x)
+        # Under AMP the masters stay fp32 while projections are fp16/bf16;
+        # route in the projection dtype (modules.py:226-231).
+        if dictionary_key.dtype != query.dtype:
+            dictionary_key = dictionary_key.to(query.dtype)
+            dictionary_value = dictionary_value.to(query.dtype)
+        # Q and K tokens route together, as one batch of rows (modules.py:236-241).
+        pair = torch.cat((query, key), dim=2)
+        routed = self._route(pair, dictionary_key, dictionary_value, "torch")
+        routed_query, routed_key = routed.split(x.shape[1], dim=2)
+        score_query, score_key = assemble_score_maps(routed_query, routed_key, self.config.outer_maps)
+        scales = score_scale_from_log(self.log_score_scales)
+        map_output = routed_attention_reference(score_query, score_key, dense_value, scales, self.config.causal)
+        output, weights = self._combine(x, map_output)
+        if not return_aux:
+            return output
+        return output, DoubleAttentionAux(
+            routing_query=routed_query,
+            routing_key=routed_key,
+            score_query=score_query,
+            score_key=score_key,
+            score_scales=scales,
+            map_weights=weights,
+            backend="torch",
+        )
+
+    # ---- HIP path ---------------------------------------------------------
+
+    def _hip_forward(
+        self,
+        x: Tensor,
+        bank: SharedDictionaryBank,
+        normalized_dictionary: tuple[Tensor, Tensor] | None,
+        dtype: torch.dtype,
+        return_aux: bool,
+    ) -> Tensor | tuple[Tensor, DoubleAttentionAux]:
+        from . import hip_ops
+
+        hip_ops.check_module_supported(self.config)
+        eps = self.config.eps
+        needs_grad = torch.is_grad_enabled() and (
+            x.requires_grad or any(p.requires_grad for p in self.parameters())
+            or (normalized_dictionary is not None and any(t.requires_grad for t in normalized_dictionary))
+            or any(p.requires_grad for p in bank.parameters())
+        )
+        if needs_grad:
+            return _HipModuleFunction.run(self, x, bank, normalized_dictionary, dtype, return_aux)
+        if normalized_dictionary is None:
+            layout = hip_ops.route_layout(*bank.normalized_hip(eps, dtype), dtype)
+        else:
+            layout = hip_ops.route_layout(*normalized_dictionary, dtype)
+        result = hip_ops.shared_dictionary_attention_hip(self, x, layout, dtype)
+        if not return_aux:
+            return result.output
+        return result.output, self._hip_aux(result.routed)
+
+    def _hip_aux(self, routed: Tensor) -> DoubleAttentionAux:
+        # routed: [B, T, 2, H, R] -> [B, H, T, R] views for queries and keys.
+        routed_query = routed[:, :, 0].permute(0, 2, 1, 3)
+        routed_key = routed[:, :, 1].permute(0, 2, 1, 3)
+        score_query, score_key = assemble_score_maps(routed_query, routed_key, self.config.outer_maps)
+        scales = score_scale_from_log(self.log_score_scales)
+        if self.config.map_combine == "weighted_sum":
+            weights = (
+                routed.new_ones(1)
+                if self.map_mix_logits is None
+                else torch.softmax(self.map_mix_logits, dim=0).to(routed.dtype)
+            )
+        else:
+            weights = routed.new_full((self.config.outer_maps,), 1.0 / self.config.outer_maps)
+        return DoubleAttentionAux(
+            routing_query=routed_query,
+            routing_key=routed_key,
+            score_query=score_query,
+            score_key=score_key,
+            score_scales=scales,
+            map_weights=weights,
+            backend="hip",
+        )
+
+    # ---- entry point -------------------------------------------------------
+
+    def forward(
+        self,
+        x: Tensor,
+        *,
+        bank: SharedDictionaryBank | None = None,
+        normalized_dictionary: tuple[Tensor, Tensor] | None = None,
+        return_aux: bool = False,
+    ) -> Tensor | tuple[Tensor, DoubleAttentionAux]:
+        cfg = self.config
+        if x.ndim != 3 or x.shape[-1] != cfg.model_dim:
+            raise ValueError(f"expected x with shape [B, T, {cfg.model_dim}], got {tuple(x.shape)}")
+        active = bank if bank is not None else self.bank
+        if active is None:
+            raise ValueError("no dictionary bank supplied")
+        if active.routing_dim != cfg.routing_dim or active.dictionary_size != cfg.dictionary_size:
+            raise ValueError("dictionary bank dimensions do not match the attention config")
+        if normalized_dictionary is not None:
+            expected = (cfg.routing_dim, cfg.dictionary_size)
+            if normalized_dictionary[0].shape != expected or normalized_dictionary[1].shape != expected:
+                raise ValueError("normalized dictionary dimensions do not match attention config")
+
+        if cfg.backend != "torch":
+            dtype = _compute_dtype(x, self.query.weight)
+            spec = _Spec(x.is_cuda, dtype)
+            if resolve_backend(cfg.backend, (spec,)) == "hip":  # type: ignore[arg-type]
+                return self._hip_forward(x, active, normalized_dictionary, dtype, return_aux)
+
+        if normalized_dictionary is None:
+            dictionary_key, dictionary_value = active.normalized(cfg.eps)
+        else:
+            dictionary_key, dictionary_value = normalized_dictionary
+        return self._torch_forward(x, dictionary_key, dictionary_value, return_aux)
+
+
+class _HipModuleFunction(torch.autograd.Function):
+    """HIP forward with a backward that recomputes the PyTorch composition.
+
+    Inputs are ``x``, the normalized dictionary (or the raw bank parameters)
+    and every module parameter, so autograd routes gradients to all of them.
+    """
+
+    @staticmethod
+    def run(module, x, bank, normalized_dictionary, dtype, return_aux):
+        params = [p for p in module.parameters()]
+        if normalized_dictionary is None:
+            dictionary = bank.normalized(module.config.eps)
+            if dictionary[0] is dictionary[1]:
+                dictionary = (dictionary[0], dictionary[0].view_as(dictionary[0]))
+        else:
+            dictionary = normalized_dictionary
+        out = _HipModuleFunction.apply(module, dtype, x, dictionary[0], dictionary[1], *params)
+        if not return_aux:
+            return out
+        with torch.no_grad():
+            from . import hip_ops
+
+            layout = hip_ops.route_layout(dictionary[0], dictionary[1], dtype)
+            routed = hip_ops.shared_dictionary_attention_hip(module, x, layout, dtype).routed
+        return out, module._hip_aux(routed)
+
+    @staticmethod
+    def forward(ctx, module, dtype, x, dictionary_key, dictionary_value, *params):  # type: ignore[override]
+        from . import hip_ops
+
+        ctx.module = module
+        ctx.dtype = dtype
+        ctx.autocast = x.is_cuda and torch.is_autocast_enabled("cuda")
+        ctx.save_for_backward(x, dictionary_key, dictionary_value, *params)
+        layout = hip_ops.route_layout(dictionary_key, dictionary_value, dtype)
+        return hip_ops.shared_dictionary_attention_hip(module, x, layout, dtype).output
+
+    @staticmethod
+    def backward(ctx, grad):  # type: ignore[override]
+        module = ctx.module
+        saved = ctx.saved_tensors
+        x, dk, dv = saved[:3]
+        params = list(module.parameters())
+        with torch.enable_grad(), torch.autocast("cuda", dtype=ctx.dtype, enabled=ctx.autocast):
+            xs = x.detach().requires_grad_(x.requires_grad)
+            dks = dk.detach().requires_grad_(dk.requires_grad)
+            dvs = dv.detach().requires_grad_(dv.requires_grad)
+            out = module._torch_forward(xs, dks, dvs, False)
+            wrt = [t for t in (xs, dks, dvs) if t.requires_grad] + [p for p in params if p.requires_grad]
+            grads = torch.autograd.grad(out, wrt, grad.to(out.dtype), allow_unused=True) if wrt else ()
+        it = iter(grads)
+        head = [next(it) if t.requires_grad else None for t in (xs, dks, dvs)]
+        tail = [next(it) if p.requires_grad else None for p in params]
+        return (None, None, *head, *tail)
+
+
+class DoubleAttentionBlock(nn.Module):
+    """Pre-norm transformer block around ``SharedDictionaryAttention`` (``modules.py:294-356``)."""
+
+    def __init__(
+        self,
+        config: DoubleAttentionConfig,
+        *,
+        feedforward_dim: int | None = None,
+        dropout: float = 0.0,
+    ) -> None:
+        super().__init__()
+        feedforward_dim = feedforward_dim or 3 * config.model_dim
+        if config.q_dictionary_feedforward:
+            if config.qk_branches != 1:
+                raise ValueError("Q-dictionary FFN requires exactly one Q branch")
+            if feedforward_dim != config.dictionary_size:
+                raise ValueError("Q-dictionary FFN requires feedforward_dim == dictionary_size")
+        self.attention_norm = nn.LayerNorm(config.model_dim)
+        self.attention = SharedDictionaryAttention(config, create_bank=False)
+        self.feedforward_norm = nn.LayerNorm(config.model_dim)
+        # The Q-dictionary FFN keeps the standard FFN's module indices; only
+        # feedforward[0] (the expansion) is replaced by Dk^T Q (modules.py:314-323).
+        first = nn.Identity() if config.q_dictionary_feedforward else nn.Linear(config.model_dim, feedforward_dim)
+        self.feedforward = nn.Sequential(
+            first,
+            nn.GELU(),
+            nn.Linear(feedforward_dim, config.model_dim),
+            nn.Dropout(dropout),
+        )
+
+    def forward(
+        self,
+        x: Tensor,
+        bank: SharedDictionaryBank,
+        *,
+        normalized_dictionary: tuple[Tensor, Tensor] | None = None,
+    ) -> Tensor:
+        x = x + self.attention(
+            self.attention_norm(x), bank=bank, normalized_dictionary=normalized_dictionary
+        )
+        normalized_x = self.feedforward_norm(x)
+        if not self.attention.config.q_dictionary_feedforward:
+            return x + self.feedforward(normalized_x)
+        if normalized_dictionary is None:
+            dictionary_key, _ = bank.normalized(self.attention.config.eps)
+        else:
+            dictionary_key, _ = normalized_dictionary
+        query = self.attention.query(normalized_x)
+        if dictionary_key.dtype != query.dtype:
+            dictionary_key = dictionary_key.to(query.dtype)
+        hidden = F.linear(query, dictionary_key.transpose(0, 1).contiguous())
+        return x + self.feedforward(hidden)
+
+
+class DoubleAttentionStack(nn.Module):
+    """Blocks sharing global or stage-wise banks (``modules.py:359-412``)."""
+
+    def __init__(
+        self,
+        config: DoubleAttentionConfig,
+        num_layers: int,
+        *,
+        dictionary_group_size: int | None = None,
+        feedforward_dim: int | None = None,
+        dropout: float = 0.0,
+    ) -> None:
+        super().__init__()
+        if num_layers <= 0:
+            raise ValueError("num_layers must be positive")
+        group_size = dictionary_group_size or num_layers
+        if group_size <= 0:
+            raise ValueError("dictionary_group_size must be positive")
+        self.config = config
+        self.num_layers = num_layers
+        self.dictionary_group_size = group_size
+        self.banks = nn.ModuleList(
+            SharedDictionaryBank(config.routing_dim, config.dictionary_size, untied=config.untied_dictionary)
+            for _ in range(math.ceil(num_layers / group_size))
+        )
+        self.blocks = nn.ModuleList(
+            DoubleAttentionBlock(config, feedforward_dim=feedforward_dim, dropout=dropout)
+            for _ in range(num_layers)
+        )
+
+    def _normalize_banks(self, x: Tensor) -> tuple[tuple[Tensor, Tensor], ...]:
+        # Each bank is normalized once per forward and reused by every block
+        # of its group (modules.py:398-404).  On the HIP path that is one
+        # kernel launch per bank, already in the route layouts.
+        cfg = self.config
+        if cfg.backend != "torch" and not torch.is_grad_enabled():
+            attention = self.blocks[0].attention
+            dtype = _compute_dtype(x, attention.query.weight)
+            if resolve_backend(cfg.backend, (_Spec(x.is_cuda, dtype),)) == "hip":  # type: ignore[arg-type]
+                from . import hip_ops
+
+                hip_ops.check_module_supported(cfg)
+                return tuple(bank.normalized_hip(cfg.eps, dtype) for bank in self.banks)
+        return tuple(bank.normalized(cfg.eps) for bank in self.banks)
+
+    def forward(self, x: Tensor) -> Tensor:
+        dictionaries = self._normalize_banks(x)
+        for index, block in enumerate(self.blocks):
+            bank_index = min(index // self.dictionary_group_size, len(self.banks) - 1)
+            x = block(x, self.banks[bank_index], normalized_dictionary=dictionaries[bank_index])
+        return x
+
+
+class DoubleAttentionLM(nn.Module):
+    """Causal LM over a ``DoubleAttentionStack`` (``modules.py:415-460``)."""
+
+    def __init__(
+        self,
+        vocab_size: int,
+        max_sequence_length: int,
+        config: DoubleAttentionConfig,
+        num_layers: int,
+        *,
+        dictionary_group_size: int | None = None,
+        feedforward_dim: int | None = None,
+        dropout: float = 0.0,
+    ) -> None:
+        super().__init__()
+        self.max_sequence_length = max_sequence_length
+        self.token_embedding = nn.Embedding(vocab_size, config.model_dim)
+        self.position_embedding = nn.Embedding(max_sequence_length, config.model_dim)
+        self.stack = DoubleAttentionStack(
+            config,
+            num_layers,
+            dictionary_group_size=dictionary_group_size,
+            feedforward_dim=feedforward_dim,
+            dropout=dropout,
+        )
+        self.final_norm = nn.LayerNorm(config.model_dim)
+        # Built (consuming its init draws) and then tied to the embedding.
+        self.lm_head = nn.Linear(config.model_dim, vocab_size, bias=False)
+        self.lm_head.weight = self.token_embedding.weight
+
+    def forward(self, token_ids: Tensor, targets: Tensor | None = None) -> tuple[Tensor, Tensor | None]:
+        if token_ids.ndim != 2:
+            raise ValueError("token_ids must have shape [B, T]")
+        length = token_ids.shape[1]
+        if length > self.max_sequence_length:
+            raise ValueError(
+                f"sequence length {length} exceeds configured maximum {self.max_sequence_length}"
+            )
+        positions = torch.arange(length, device=token_ids.device)
+        hidden = self.token_embedding(token_ids) + self.position_embedding(positions)[None]
+        logits = self.lm_head(self.final_norm(self.stack(hidden)))
+        loss = None
+        if targets is not None:
+            if targets.shape != token_ids.shape:
+                raise ValueError("targets must match token_ids shape")
+            loss = F.cross_entropy(logits.flatten(0, 1), targets.flatten())
+        return logits, loss

@@ -1,0 +1,190 @@
+/*
+ * C ABI of the MI355X (gfx950) shared-dictionary attention forward path.
+ *
+ * Every entry point takes plain device pointers, element counts and strides,
+ * a dtype code and the HIP stream to enqueue on.  Nothing here allocates,
+ * frees or synchronizes: the caller owns every buffer (including the
+ * workspace of da_shared_dictionary_attention_forward) and the stream order.
+ * Scalars that the reference keeps as device tensors (beta, the score scales,
+ * the map-mix logits) are passed as device pointers and read on the device,
+ * so no entry point needs a host round trip.
+ *
+ * Return value: 0 on success, a negative DA_ERR_* code otherwise; the
+ * message of the last failure on the calling thread is da_last_error().
+ * Argument checks run before anything is enqueued, so a failed call leaves
+ * the stream untouched.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository
+ * Ahnd6474/double-attention):
+ *   da_dictionary_normalize   SharedDictionaryBank.normalized        src/double_attention/modules.py:45-48
+ *   da_dictionary_route       dictionary_route_triton / _reference   src/double_attention/triton_kernels.py:1984-2019, ops.py:16-62
+ *   da_routed_attention       routed_attention_triton / _reference   src/double_attention/triton_kernels.py:2290-2305, ops.py:65-93
+ *                             + map combine                          src/double_attention/modules.py:265-272
+ *   da_qkv_projection         _project_query_key + self.value        src/double_attention/modules.py:143-157, 212
+ *   da_linear                 self.output                            src/double_attention/modules.py:117-121, 272
+ *   da_shared_dictionary_attention_forward
+ *                             SharedDictionaryAttention.forward      src/double_attention/modules.py:190-291
+ */
+#ifndef DOUBLE_ATTENTION_HIP_H
+#define DOUBLE_ATTENTION_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* da_stream_t; /* hipStream_t; NULL = default stream */
+
+/* dtype codes */
+#define DA_F32 0
+#define DA_F16 1
+#define DA_BF16 2
+
+/* error codes */
+#define DA_OK 0
+#define DA_ERR_INVALID_ARGUMENT (-1)
+#define DA_ERR_UNSUPPORTED (-2)
+#define DA_ERR_ALIGNMENT (-3)
+#define DA_ERR_LAUNCH (-4)
+#define DA_ERR_WORKSPACE (-5)
+
+/* da_dictionary_route flags */
+#define DA_ROUTE_NORMALIZE_INPUT 1  /* u = x / max(||x||, eps) before the assignment   */
+#define DA_ROUTE_NORMALIZE_OUTPUT 2 /* z = r / max(||r||, eps) after the reconstruction */
+#define DA_ROUTE_BETA_IS_LOG 4      /* *beta is log_beta: use exp(clamp(., ln .05, ln 64)) */
+
+/* da_routed_attention flags */
+#define DA_ATTN_CAUSAL 1
+#define DA_ATTN_SCALES_ARE_LOG 2    /* scales are log_score_scales: exp(clamp(., ln .25, ln 1024)) */
+#define DA_ATTN_MIX 4               /* alpha-weighted sum of the maps into one output */
+
+/* da_shared_dictionary_attention_forward flags */
+#define DA_SDA_NORMALIZE_INPUT 1
+#define DA_SDA_NORMALIZE_OUTPUT 2
+#define DA_SDA_CAUSAL 4
+#define DA_SDA_CONCAT 8             /* map_combine == "concat" */
+
+/* ABI version of this header (bumped on any signature change). */
+int da_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* da_last_error(void);
+
+/* Atoms after padding: the route layouts hold round_up(atoms, 64) atoms. */
+int64_t da_padded_atoms(int64_t atoms);
+
+/* Tokens after padding: V^T rows hold round_up(length, 64) tokens. */
+int64_t da_padded_length(int64_t length);
+
+/*
+ * Column-normalize one dictionary bank (modules.py:45-48).
+ *   raw_key, raw_value: [routing_dim, atoms] row-major, dtype raw_dtype
+ *                       (raw_value NULL = tied bank: key atoms serve both roles)
+ *   key_t:  out [da_padded_atoms(atoms), routing_dim]   atom-major
+ *   value:  out [routing_dim, da_padded_atoms(atoms)]   coordinate-major
+ * Atom j becomes raw[:, j] / max(||raw[:, j]||, eps); padding atoms are zero.
+ * routing_dim must be 64, 128, 256 or 512; out_dtype DA_F16 or DA_BF16.
+ */
+int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_dtype,
+                            int64_t routing_dim, int64_t atoms, float eps, void* key_t,
+                            void* value, int out_dtype, da_stream_t stream);
+
+/*
+ * Fused dictionary route (ops.py:16-62 with identity activation and softmax
+ * assignment), for any number of rows:
+ *   z = N_out( sum_j softmax_j(beta <N_in(x), Dk_j>) Dv_j )
+ *   x:   rows x routing_dim, row pitch x_row_stride (elements)
+ *   key_t, value: the layouts written by da_dictionary_normalize
+ *   beta: device scalar of beta_dtype, or NULL to use beta_value
+ *   out: rows x routing_dim, row pitch out_row_stride (may alias x when the
+ *        pitches match: each row is read completely before it is written)
+ */
+int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_t x_row_stride,
+                        const void* key_t, const void* value, int64_t atoms, const void* beta,
+                        int beta_dtype, float beta_value, float eps, int flags, int dtype,
+                        void* out, int64_t out_row_stride, da_stream_t stream);
+
+/*
+ * Flash outer attention over `maps` score maps (ops.py:65-93) with the map
+ * combine of modules.py:265-272 fused in.
+ *   query/key row of (batch b, token t, map s) starts at
+ *       base + b*stride_b + t*stride_t + (s / map_repeat) * map_stride
+ *     and holds score_dim elements.
+ *   value_t: V^T, element (b, d, t) at value_t[b*vt_stride_b + d*vt_stride_d + t];
+ *     vt_stride_d >= da_padded_length(length).
+ *   scales: [maps] device tensor (gamma_s, or log gamma_s with
+ *     DA_ATTN_SCALES_ARE_LOG); every gamma is multiplied by scale_mult.
+ *   DA_ATTN_MIX: out(b, t) = sum_s alpha_s O_s(b, t), alpha = softmax(mix_logits)
+ *     (uniform 1/maps if mix_logits is NULL); else O_s(b, t) goes to
+ *     out + b*out_stride_b + t*out_stride_t + s*out_stride_s.
+ * score_dim and value_dim must be 64, 128, 256 or 512.
+ */
+int da_routed_attention(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
+                        int64_t map_stride, int64_t map_repeat, int64_t score_dim,
+                        const void* value_t, int64_t vt_stride_b, int64_t vt_stride_d,
+                        int64_t batch, int64_t maps, int64_t length, int64_t value_dim,
+                        const void* scales, int scales_dtype, float scale_mult,
+                        const void* mix_logits, int mix_dtype, int flags, int dtype, void* out,
+                        int64_t out_stride_b, int64_t out_stride_t, int64_t out_stride_s,
+                        da_stream_t stream);
+
+/*
+ * Q/K and V projections in one launch (modules.py:143-157 and 212):
+ *   qk_out [tokens, 2*qk_width] = x @ [wq; wk]^T   (row n: query features, then key features)
+ *   value_t[b, f, t]            = (x @ wv^T + bv)[b*length + t, f]
+ *   x: [tokens, model_dim] with tokens = batch*length; wq, wk: [qk_width, model_dim];
+ *   wv: [value_dim, model_dim]; bv: [value_dim] of bias_dtype or NULL.
+ *   value_t pitch: vt_stride_b per sequence, vt_pitch per feature row.
+ */
+int da_qkv_projection(const void* x, int64_t tokens, int64_t model_dim, int64_t length,
+                      const void* wq, const void* wk, int64_t qk_width, const void* wv,
+                      const void* bv, int64_t value_dim, int bias_dtype, int dtype, void* qk_out,
+                      void* value_t, int64_t vt_stride_b, int64_t vt_pitch, da_stream_t stream);
+
+/* out [rows, out_features] = x [rows, in_features] @ weight^T (+ bias) */
+int da_linear(const void* x, int64_t rows, int64_t in_features, const void* weight,
+              int64_t out_features, const void* bias, int bias_dtype, int dtype, void* out,
+              da_stream_t stream);
+
+/* Whole SharedDictionaryAttention forward (modules.py:190-291). */
+typedef struct da_sda_forward_args {
+  const void* x;            /* [batch, length, model_dim] */
+  int64_t batch, length, model_dim;
+  int64_t qk_branches, outer_maps, routing_dim, atoms;
+  const void* wq;           /* query.weight [qk_branches*routing_dim, model_dim] */
+  const void* wk;           /* key.weight */
+  const void* wv;           /* value.weight [model_dim, model_dim] */
+  const void* bv;           /* value.bias [model_dim] or NULL */
+  const void* wo;           /* output.weight [model_dim, model_dim or maps*model_dim] or NULL (identity) */
+  const void* key_t;        /* normalized bank, da_dictionary_normalize layouts */
+  const void* value;
+  const void* log_beta;     /* scalar */
+  const void* log_score_scales; /* [outer_maps] */
+  const void* map_mix_logits;   /* [outer_maps] or NULL */
+  int param_dtype;          /* dtype of bias and of the three scalar tensors */
+  int dtype;                /* activation / weight dtype: DA_F16 or DA_BF16 */
+  float eps;
+  int flags;                /* DA_SDA_* */
+  void* workspace;          /* da_sda_workspace_bytes(...) bytes, 256-byte aligned */
+  int64_t workspace_bytes;
+  void* out;                /* [batch, length, model_dim] */
+} da_sda_forward_args;
+
+/* Workspace layout (byte offsets, each 256-aligned):
+ *   routed [tokens, 2*qk_width]   Q/K projections, routed in place
+ *   value_t [batch, model_dim, da_padded_length(length)]
+ *   mixed  [tokens, model_dim or maps*model_dim] (only with an output projection) */
+int64_t da_sda_workspace_bytes(int64_t batch, int64_t length, int64_t model_dim,
+                               int64_t qk_width, int64_t outer_maps, int concat,
+                               int has_output_projection);
+int64_t da_sda_workspace_offset(int64_t batch, int64_t length, int64_t model_dim,
+                                int64_t qk_width, int which /* 0 routed, 1 value_t, 2 mixed */);
+
+int da_shared_dictionary_attention_forward(const da_sda_forward_args* args, da_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DOUBLE_ATTENTION_HIP_H */

@@ -1,0 +1,259 @@
+"""NumPy restatement of the reference forward math (test infrastructure only).
+
+Every function cites the reference lines it restates (paths relative to the
+reference repository).  Arithmetic runs in the dtype of the inputs: float64
+for the tight CPU checks, float32 for the parity tests and the CPU baseline.
+Parameters are passed as a ``{state_dict name: ndarray}`` mapping so the
+oracle consumes exactly the tensors the module under test holds.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Mapping
+from typing import Any
+
+import numpy as np
+from scipy.special import erf
+
+LOG_BETA_MIN, LOG_BETA_MAX = math.log(0.05), math.log(64.0)     # modules.py:130-132
+LOG_SCALE_MIN, LOG_SCALE_MAX = math.log(0.25), math.log(1024.0)  # ops.py:160-161
+
+
+def _cfg(cfg: Any, name: str) -> Any:
+    return cfg[name] if isinstance(cfg, Mapping) else getattr(cfg, name)
+
+
+def l2_normalize(x: np.ndarray, axis: int, eps: float) -> np.ndarray:
+    """``x / max(||x||_2, eps)`` along ``axis`` -- the semantics of ``F.normalize``."""
+
+    norm = np.sqrt(np.sum(x * x, axis=axis, keepdims=True))
+    return x / np.maximum(norm, eps)
+
+
+def _softmax(x: np.ndarray, axis: int) -> np.ndarray:
+    shifted = x - np.max(x, axis=axis, keepdims=True)
+    e = np.exp(shifted)
+    return e / np.sum(e, axis=axis, keepdims=True)
+
+
+def _silu(x: np.ndarray) -> np.ndarray:
+    return x / (1.0 + np.exp(-x))
+
+
+def beta_from_log(log_beta: np.ndarray | float) -> np.ndarray:
+    """``exp(clamp(log_beta, ln 0.05, ln 64))`` (modules.py:130-132)."""
+
+    return np.exp(np.clip(np.asarray(log_beta), LOG_BETA_MIN, LOG_BETA_MAX))
+
+
+def score_scale_from_log(log_scale: np.ndarray) -> np.ndarray:
+    """``exp(clamp(log_scale, ln 0.25, ln 1024))`` (ops.py:160-161)."""
+
+    return np.exp(np.clip(np.asarray(log_scale), LOG_SCALE_MIN, LOG_SCALE_MAX))
+
+
+def bank_normalized(raw_key: np.ndarray, raw_value: np.ndarray | None, eps: float = 1e-6):
+    """Unit-norm atoms (columns) of a bank; tied banks reuse the key (modules.py:45-48)."""
+
+    key = l2_normalize(raw_key, 0, eps)
+    value = key if raw_value is None else l2_normalize(raw_value, 0, eps)
+    return key, value
+
+
+def dictionary_route(
+    x: np.ndarray,
+    dictionary_key: np.ndarray,
+    dictionary_value: np.ndarray,
+    beta: float | np.ndarray,
+    eps: float = 1e-6,
+    activation: str = "identity",
+    assignment: str = "softmax",
+    silu_gain: float = 1.0,
+    standardize_logits: bool = False,
+    standardized_logit_scale: float | None = None,
+    normalize_input: bool = True,
+    normalize_output: bool = True,
+) -> np.ndarray:
+    """Dictionary feature map of ``x [..., R]`` (ops.py:16-62)."""
+
+    dt = x.dtype
+    u = l2_normalize(x, -1, eps) if normalize_input else x
+    logits = u @ dictionary_key.astype(dt)
+    if activation == "silu":
+        logits = 2.0 * _silu(logits)
+    elif activation != "identity":
+        raise ValueError(activation)
+    if standardize_logits:
+        centered = logits - logits.mean(axis=-1, keepdims=True)
+        inv_std = 1.0 / np.sqrt(np.mean(centered * centered, axis=-1, keepdims=True) + eps)
+        scale = x.shape[-1] ** -0.5 if standardized_logit_scale is None else standardized_logit_scale
+        logits = centered * inv_std * scale
+    if assignment == "softmax":
+        weights = _softmax(logits * np.asarray(beta, dtype=dt), -1)
+    elif assignment == "silu":
+        weights = (2.0 / silu_gain) * _silu(silu_gain * logits)
+    else:
+        raise ValueError(assignment)
+    recon = weights @ dictionary_value.astype(dt).T
+    return l2_normalize(recon, -1, eps) if normalize_output else recon
+
+
+def routed_attention(
+    query: np.ndarray, key: np.ndarray, value: np.ndarray, scales: np.ndarray, causal: bool = True
+) -> np.ndarray:
+    """``softmax(scale_s q k^T, causal) V`` for every map (ops.py:65-93).
+
+    ``query``/``key`` ``[B, S, T, R]``, ``value`` ``[B, T, D]`` shared by all
+    maps; returns ``[B, S, T, D]``.  Future positions get ``-inf``.
+    """
+
+    dt = query.dtype
+    scores = np.matmul(query, np.swapaxes(key, -1, -2)) * np.asarray(scales, dtype=dt)[None, :, None, None]
+    if causal:
+        length = query.shape[-2]
+        future = np.triu(np.ones((length, length), dtype=bool), 1)
+        scores = np.where(future, -np.inf, scores)
+    probs = _softmax(scores, -1)
+    return np.matmul(probs, value.astype(dt)[:, None])
+
+
+def assemble_score_maps(query: np.ndarray, key: np.ndarray, outer_maps: int):
+    """Branch-to-map assembly (ops.py:96-139): identity, RMS-sum groups or repeats."""
+
+    branches = query.shape[1]
+    if branches == outer_maps:
+        return query, key
+    if branches > outer_maps:
+        group = branches // outer_maps
+        factor = group ** -0.25
+
+        def grouped(t: np.ndarray) -> np.ndarray:
+            b, _, length, width = t.shape
+            parts = t.reshape(b, outer_maps, group, length, width).transpose(0, 1, 3, 2, 4)
+            return parts.reshape(b, outer_maps, length, group * width) * factor
+
+        return grouped(query), grouped(key)
+    repeats = outer_maps // branches
+    return np.repeat(query, repeats, axis=1), np.repeat(key, repeats, axis=1)
+
+
+def shared_dictionary_attention(
+    params: Mapping[str, np.ndarray],
+    cfg: Any,
+    x: np.ndarray,
+    normalized_dictionary: tuple[np.ndarray, np.ndarray] | None = None,
+    prefix: str = "",
+    return_routed: bool = False,
+):
+    """``SharedDictionaryAttention.forward`` (modules.py:190-291) on NumPy arrays.
+
+    ``params`` holds the module's state-dict entries under ``prefix``; the
+    bank comes from ``prefix + 'bank.'`` unless ``normalized_dictionary`` is
+    given.
+    """
+
+    dt = x.dtype
+
+    def p(name: str) -> np.ndarray | None:
+        v = params.get(prefix + name)
+        return None if v is None else np.asarray(v, dtype=dt)
+
+    batch, length, _ = x.shape
+    branches = _cfg(cfg, "qk_branches")
+    routing = _cfg(cfg, "routing_dim")
+    maps = _cfg(cfg, "outer_maps")
+    eps = _cfg(cfg, "eps")
+
+    def project(weight: np.ndarray) -> np.ndarray:
+        return (x @ weight.T).reshape(batch, length, branches, routing).transpose(0, 2, 1, 3)
+
+    query = project(p("query.weight"))
+    key = project(p("key.weight"))
+    value = x @ p("value.weight").T
+    if p("value.bias") is not None:
+        value = value + p("value.bias")
+    if normalized_dictionary is None:
+        dk, dv = bank_normalized(p("bank.raw_key"), p("bank.raw_value"), eps)
+    else:
+        dk, dv = (np.asarray(t, dtype=dt) for t in normalized_dictionary)
+    beta = beta_from_log(p("log_beta"))
+    routed = dictionary_route(
+        np.concatenate([query, key], axis=2), dk, dv, beta, eps,
+        _cfg(cfg, "dictionary_activation"), _cfg(cfg, "dictionary_assignment"),
+        _cfg(cfg, "dictionary_silu_gain"), _cfg(cfg, "standardize_dictionary_logits"),
+        _cfg(cfg, "standardized_logit_scale"), _cfg(cfg, "normalize_routing_input"),
+        _cfg(cfg, "normalize_routing_output"),
+    )
+    routed_query, routed_key = routed[:, :, :length], routed[:, :, length:]
+    score_query, score_key = assemble_score_maps(routed_query, routed_key, maps)
+    scales = score_scale_from_log(p("log_score_scales"))
+    map_output = routed_attention(score_query, score_key, value, scales, _cfg(cfg, "causal"))
+    if _cfg(cfg, "map_combine") == "weighted_sum":
+        if maps == 1:
+            combined = map_output[:, 0]
+        else:
+            alpha = _softmax(p("map_mix_logits"), 0)
+            combined = np.einsum("s,bstd->btd", alpha, map_output)
+    else:
+        combined = map_output.transpose(0, 2, 1, 3).reshape(batch, length, -1)
+    out = combined @ p("output.weight").T if p("output.weight") is not None else combined
+    if return_routed:
+        return out, routed_query, routed_key
+    return out
+
+
+def layer_norm(x: np.ndarray, weight: np.ndarray, bias: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """``nn.LayerNorm`` over the last axis (biased variance)."""
+
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    return (x - mean) / np.sqrt(var + eps) * weight + bias
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    """Exact (erf) GELU, ``nn.GELU()``'s default."""
+
+    return 0.5 * x * (1.0 + erf(x / math.sqrt(2.0)))
+
+
+def double_attention_lm(
+    params: Mapping[str, np.ndarray],
+    cfg: Any,
+    token_ids: np.ndarray,
+    num_layers: int,
+    dictionary_group_size: int | None = None,
+    dtype: np.dtype = np.float64,
+) -> np.ndarray:
+    """``DoubleAttentionLM.forward`` logits (modules.py:332-356, 398-412, 444-460)."""
+
+    def p(name: str) -> np.ndarray:
+        return np.asarray(params[name], dtype=dtype)
+
+    length = token_ids.shape[1]
+    hidden = p("token_embedding.weight")[token_ids] + p("position_embedding.weight")[:length][None]
+    group = dictionary_group_size or num_layers
+    bank_count = math.ceil(num_layers / group)
+    eps = _cfg(cfg, "eps")
+    banks = []
+    for i in range(bank_count):
+        raw_value = params.get(f"stack.banks.{i}.raw_value")
+        banks.append(
+            bank_normalized(p(f"stack.banks.{i}.raw_key"), None if raw_value is None else np.asarray(raw_value, dtype), eps)
+        )
+    qffn = _cfg(cfg, "q_dictionary_feedforward")
+    for layer in range(num_layers):
+        pre = f"stack.blocks.{layer}."
+        dictionary = banks[min(layer // group, bank_count - 1)]
+        normed = layer_norm(hidden, p(pre + "attention_norm.weight"), p(pre + "attention_norm.bias"))
+        hidden = hidden + shared_dictionary_attention(
+            params, cfg, normed, normalized_dictionary=dictionary, prefix=pre + "attention."
+        )
+        normed = layer_norm(hidden, p(pre + "feedforward_norm.weight"), p(pre + "feedforward_norm.bias"))
+        if qffn:
+            expanded = (normed @ p(pre + "attention.query.weight").T) @ dictionary[0]
+        else:
+            expanded = normed @ p(pre + "feedforward.0.weight").T + p(pre + "feedforward.0.bias")
+        hidden = hidden + gelu(expanded) @ p(pre + "feedforward.2.weight").T + p(pre + "feedforward.2.bias")
+    hidden = layer_norm(hidden, p("final_norm.weight"), p("final_norm.bias"))
+    return hidden @ p("token_embedding.weight").T

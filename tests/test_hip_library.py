@@ -1,0 +1,103 @@
+"""CPU checks of the C-ABI library: it loads, exports every declared symbol,
+and rejects bad arguments on the host before anything is launched."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import double_attention._lib as lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "double_attention_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(da_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    handle = lib.get()
+    names = declared_functions()
+    assert len(names) == 12
+    for name in names:
+        assert hasattr(handle, name), name
+        assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(lib.SIGNATURES) == set(names)
+
+
+def test_abi_version_and_helpers() -> None:
+    h = lib.get()
+    assert h.da_abi_version() == lib.ABI_VERSION
+    assert h.da_padded_atoms(512) == 512 and h.da_padded_atoms(513) == 576 and h.da_padded_atoms(2855) == 2880
+    assert h.da_padded_length(65) == 128 and h.da_padded_length(8192) == 8192
+    # C1 workspace: routed [4096, 512] + V^T [8, 512, 512] + mixed [4096, 512], bf16.
+    assert h.da_sda_workspace_bytes(8, 512, 512, 256, 1, 0, 1) == 3 * 4096 * 512 * 2
+    assert h.da_sda_workspace_bytes(8, 512, 512, 256, 1, 0, 0) == 2 * 4096 * 512 * 2
+    assert h.da_sda_workspace_offset(8, 512, 512, 256, 1) == 4096 * 512 * 2
+
+
+def _fake(addr: int = 1 << 20) -> int:
+    # A 256-aligned non-null address: only reaches host-side validation.
+    return addr
+
+
+@pytest.mark.parametrize(
+    ("kwargs", "code", "pattern"),
+    [
+        ({"routing_dim": 96}, -2, "routing_dim 96"),
+        ({"dtype": lib.DA_F32}, -1, "dtype"),
+        ({"x_row_stride": 100}, -3, "row strides"),
+        ({"x": 0}, -1, "null pointer"),
+        ({"x": (1 << 20) + 2}, -3, "16-byte aligned"),
+        ({"atoms": 0}, -1, "rows/atoms"),
+    ],
+)
+def test_route_rejects_bad_arguments_before_launch(kwargs, code, pattern) -> None:
+    h = lib.get()
+    args = dict(
+        x=_fake(), rows=16, routing_dim=128, x_row_stride=128, key_t=_fake(), value=_fake(),
+        atoms=512, beta=None, beta_dtype=lib.DA_F32, beta_value=4.0, eps=1e-6, flags=3,
+        dtype=lib.DA_BF16, out=_fake(), out_row_stride=128, stream=None,
+    )
+    args.update(kwargs)
+    rc = h.da_dictionary_route(*args.values())
+    assert rc == code
+    assert re.search(pattern, h.da_last_error().decode())
+
+
+def test_attention_rejects_bad_arguments_before_launch() -> None:
+    h = lib.get()
+    base = [
+        _fake(), _fake(), 512 * 256, 256, 512 * 256, 1, 256,  # q, k, strides, map stride/repeat, score dim
+        _fake(), 512 * 512, 512,  # value_t pitches
+        1, 1, 512, 512,  # batch, maps, length, value dim
+        _fake(), lib.DA_F32, 1.0, None, lib.DA_F32,
+        lib.DA_ATTN_CAUSAL, lib.DA_BF16, _fake(), 512 * 512, 512, 0, None,
+    ]
+    bad_dim = list(base)
+    bad_dim[6] = 384
+    assert h.da_routed_attention(*bad_dim) == -2
+    short_pitch = list(base)
+    short_pitch[9] = 448   # vt_stride_d below the padded length 512
+    assert h.da_routed_attention(*short_pitch) == -3
+    assert "padded length" in h.da_last_error().decode()
+    no_scales = list(base)
+    no_scales[14] = None
+    assert h.da_routed_attention(*no_scales) == -1
+
+
+def test_forward_rejects_small_workspace() -> None:
+    h = lib.get()
+    f = _fake()
+    args = lib.SdaForwardArgs(
+        f, 8, 512, 512, 1, 1, 256, 512, f, f, f, f, f, f, f, f, f, None,
+        lib.DA_F32, lib.DA_BF16, 1e-6, 7, f, 1024, f,
+    )
+    assert h.da_shared_dictionary_attention_forward(ctypes.byref(args), None) == -5
+    assert "workspace" in h.da_last_error().decode()
+    with pytest.raises(ValueError, match="workspace too small"):
+        lib.check(-5, "forward")

@@ -1,0 +1,352 @@
+"""GPU parity of the gfx950 kernels against the fp32 NumPy oracle.
+
+Protocol (same for every case): seeded inputs and weights are cast to the
+GPU dtype; the oracle receives exactly those (bf16/fp16-valued) numbers
+upcast to fp32, so the comparison measures the kernels and not the input
+rounding.  The bar is the one the north star states for the attention
+output: relative L2 error <= 5e-3 and max abs error <= 2e-2 against fp32.
+Shapes are deliberately odd (17/65/257 rows or tokens, atom counts that are
+not tile multiples) as in the reference's own parity tests
+(reference ``tests/test_triton_parity.py``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import double_attention as da
+import oracle
+from conftest import Golden
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 5e-3
+MAX_ABS = 2e-2
+DTYPES = [torch.bfloat16, torch.float16]
+
+
+def _device() -> torch.device:
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    if not da.HIP_AVAILABLE:
+        raise RuntimeError("HIP library not built; run python double-attention_amd/build.py")
+    return torch.device("cuda")
+
+
+def np32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def assert_parity(actual: torch.Tensor, expected: np.ndarray, rel_l2: float = REL_L2, max_abs: float = MAX_ABS, label: str = "") -> None:
+    a = np32(actual).astype(np.float64)
+    e = expected.astype(np.float64)
+    assert a.shape == e.shape, (a.shape, e.shape)
+    assert np.isfinite(a).all(), f"{label}: non-finite output"
+    rel = np.linalg.norm(a - e) / max(np.linalg.norm(e), 1e-30)
+    mx = np.abs(a - e).max()
+    print(f"[parity] {label} rel_l2={rel:.3e} max_abs={mx:.3e}", flush=True)
+    assert rel <= rel_l2, f"{label}: rel-L2 {rel:.3e} > {rel_l2}"
+    assert mx <= max_abs, f"{label}: max-abs {mx:.3e} > {max_abs}"
+
+
+def unit_rows(shape, dtype, device, seed):
+    g = torch.Generator().manual_seed(seed)
+    t = torch.randn(*shape, generator=g)
+    return torch.nn.functional.normalize(t, dim=-1).to(device=device, dtype=dtype)
+
+
+def unit_columns(r, m, dtype, device, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.nn.functional.normalize(torch.randn(r, m, generator=g), dim=0).to(device=device, dtype=dtype)
+
+
+# ---------------------------------------------------------------- dictionary normalization
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("routing_dim", "atoms", "tied"), [(64, 100, False), (256, 512, True), (512, 1536, False)])
+def test_dictionary_normalize(dtype, routing_dim, atoms, tied) -> None:
+    device = _device()
+    g = torch.Generator().manual_seed(routing_dim + atoms)
+    raw_key = (torch.randn(routing_dim, atoms, generator=g) * 0.1).to(device)
+    raw_value = None if tied else (torch.randn(routing_dim, atoms, generator=g) * 3).to(device)
+    key, value = da.dictionary_normalize_hip(raw_key, raw_value, 1e-6, dtype)
+    torch.cuda.synchronize()
+    ek, ev = oracle.bank_normalized(np32(raw_key), None if tied else np32(raw_value))
+    assert_parity(key, ek, 4e-3, 4e-3, "norm key")
+    assert_parity(value, ev, 4e-3, 4e-3, "norm value")
+    layout = key._da_route_layout
+    padded = layout.key_t.shape[0]
+    assert padded % 64 == 0 and padded >= atoms
+    assert torch.count_nonzero(layout.key_t[atoms:]) == 0
+    assert torch.count_nonzero(layout.value[:, atoms:]) == 0
+
+
+# ---------------------------------------------------------------- GEMMs
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("rows", "k", "n", "bias"), [(33, 64, 96, False), (300, 512, 512, True), (4096, 512, 512, False)])
+def test_linear(dtype, rows, k, n, bias) -> None:
+    device = _device()
+    g = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, k, generator=g).to(device, dtype)
+    w = (torch.randn(n, k, generator=g) * k ** -0.5).to(device, dtype)
+    b = torch.randn(n, generator=g).to(device, dtype) if bias else None
+    out = da.hip_ops.linear_hip(x, w, b)
+    expected = np32(x) @ np32(w).T + (np32(b) if bias else 0)
+    assert_parity(out, expected, label=f"linear {rows}x{k}->{n}")
+
+
+@pytest.mark.parametrize(("batch", "length", "width"), [(2, 17, 64), (8, 512, 256), (1, 65, 512)])
+def test_qkv_projection(batch, length, width) -> None:
+    device = _device()
+    dtype = torch.bfloat16
+    d = 512 if width >= 256 else 64
+    g = torch.Generator().manual_seed(length)
+    x = torch.randn(batch, length, d, generator=g).to(device, dtype)
+    wq, wk = ((torch.randn(width, d, generator=g) * d ** -0.5).to(device, dtype) for _ in range(2))
+    wv = (torch.randn(d, d, generator=g) * d ** -0.5).to(device, dtype)
+    bv = torch.randn(d, generator=g).to(device, dtype)
+    qk, vt = da.hip_ops.qkv_projection_hip(x, wq, wk, wv, bv)
+    xn = np32(x)
+    assert_parity(qk[..., :width], xn @ np32(wq).T, label="proj q")
+    assert_parity(qk[..., width:], xn @ np32(wk).T, label="proj k")
+    v = xn @ np32(wv).T + np32(bv)
+    assert_parity(vt[:, :, :length], v.transpose(0, 2, 1), label="proj v^T")
+
+
+# ---------------------------------------------------------------- dictionary route
+
+
+ROUTE_FLAGS = [(True, True), (False, True), (True, False), (False, False)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("normalize_input", "normalize_output"), ROUTE_FLAGS)
+def test_route_flags_odd_rows(dtype, normalize_input, normalize_output) -> None:
+    device = _device()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 3, 17, 64, generator=g).to(device, dtype)
+    dk = unit_columns(64, 128, dtype, device, 1)
+    dv = unit_columns(64, 128, dtype, device, 2)
+    beta = torch.tensor(4.0, device=device)
+    out = da.dictionary_route_hip(x, dk, dv, beta, normalize_input=normalize_input, normalize_output=normalize_output)
+    expected = oracle.dictionary_route(np32(x), np32(dk), np32(dv), 4.0,
+                                       normalize_input=normalize_input, normalize_output=normalize_output)
+    assert_parity(out, expected, label=f"route flags {normalize_input}/{normalize_output} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("routing_dim", "atoms", "rows", "beta"), [
+    (128, 512, 1000, 4.0),
+    (256, 512, 8192, 4.0),          # C1 route: 8192 rows
+    (512, 1536, 16384, 4.0 * 2 ** 0.5),  # C3 route, past the reference's 4096-row cutoff
+    (256, 100, 77, 4.0),            # atom count that is not a tile multiple
+    (512, 2855, 333, 5.0),
+])
+def test_route_shapes(dtype, routing_dim, atoms, rows, beta) -> None:
+    device = _device()
+    g = torch.Generator().manual_seed(routing_dim * 7 + atoms)
+    x = torch.randn(rows, routing_dim, generator=g).to(device, dtype)
+    dk = unit_columns(routing_dim, atoms, dtype, device, 3)
+    dv = unit_columns(routing_dim, atoms, dtype, device, 4)
+    out = da.dictionary_route_hip(x, dk, dv, beta)
+    expected = oracle.dictionary_route(np32(x), np32(dk), np32(dv), beta)
+    assert_parity(out, expected, label=f"route R{routing_dim} M{atoms} rows{rows} {dtype}")
+    # Size-independent property: every routed row is a unit vector.
+    norms = out.float().norm(dim=-1)
+    torch.testing.assert_close(norms, torch.ones_like(norms), atol=1e-2, rtol=0)
+
+
+def test_route_zero_rows_and_empty() -> None:
+    device = _device()
+    dk = unit_columns(128, 64, torch.bfloat16, device, 5)
+    x = torch.zeros(5, 128, device=device, dtype=torch.bfloat16)
+    out = da.dictionary_route_hip(x, dk, dk, 4.0)
+    mean_atom = np32(dk).mean(axis=1)
+    assert_parity(out, np.broadcast_to(mean_atom / np.linalg.norm(mean_atom), (5, 128)), label="route zero rows")
+    empty = da.dictionary_route_hip(torch.zeros(0, 128, device=device, dtype=torch.bfloat16), dk, dk, 4.0)
+    assert empty.shape == (0, 128)
+
+
+# ---------------------------------------------------------------- outer attention
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize(("batch", "maps", "length", "score_dim", "value_dim", "scales"), [
+    (2, 2, 65, 64, 96, (12.0, 17.0)),
+    (1, 4, 64, 128, 512, (12.0, 12.0, 12.0, 12.0)),
+    (1, 2, 257, 64, 80, (11.0, 15.0)),
+    (1, 2, 64, 256, 128, (10.0, 14.0)),
+    (1, 1, 1, 64, 64, (16.0,)),
+])
+def test_routed_attention(dtype, causal, batch, maps, length, score_dim, value_dim, scales) -> None:
+    device = _device()
+    q = unit_rows((batch, maps, length, score_dim), dtype, device, 10)
+    k = unit_rows((batch, maps, length, score_dim), dtype, device, 11)
+    g = torch.Generator().manual_seed(12)
+    v = torch.randn(batch, length, value_dim, generator=g).to(device, dtype)
+    s = torch.tensor(scales, device=device)
+    out = da.routed_attention_hip(q, k, v, s, causal)
+    expected = oracle.routed_attention(np32(q), np32(k), np32(v), np.array(scales, np.float32), causal)
+    assert_parity(out, expected, label=f"attention b{batch} s{maps} t{length} r{score_dim} d{value_dim} causal={causal} {dtype}")
+
+
+def test_attention_long_context_properties() -> None:
+    # C5-sized attention (T = 8192): rows of P sum to one and the first
+    # causal row returns V[0] exactly up to rounding.
+    device = _device()
+    length = 8192
+    q = unit_rows((1, 1, length, 256), torch.bfloat16, device, 13)
+    k = unit_rows((1, 1, length, 256), torch.bfloat16, device, 14)
+    ones = torch.ones(1, length, 512, device=device, dtype=torch.bfloat16)
+    out = da.routed_attention_hip(q, k, ones, torch.tensor([16.0], device=device), True)
+    torch.testing.assert_close(out.float(), torch.ones_like(out, dtype=torch.float32), atol=1e-2, rtol=0)
+    g = torch.Generator().manual_seed(15)
+    v = torch.randn(1, length, 512, generator=g).to(device, torch.bfloat16)
+    out = da.routed_attention_hip(q, k, v, torch.tensor([16.0], device=device), True)
+    torch.testing.assert_close(out[0, 0, 0].float(), v[0, 0].float(), atol=2e-2, rtol=0)
+
+
+# ---------------------------------------------------------------- whole module
+
+
+def oracle_params(module: torch.nn.Module) -> dict[str, np.ndarray]:
+    return {k: np32(v) for k, v in module.state_dict().items()}
+
+
+def build_module(preset: str, dtype: torch.dtype, seed: int, **overrides):
+    device = _device()
+    config = da.experiment_config(preset, backend="hip", **overrides)
+    torch.manual_seed(seed)
+    module = da.SharedDictionaryAttention(config).to(device=device, dtype=dtype).eval()
+    return module
+
+
+def run_module_case(preset, shape, dtype=torch.bfloat16, seed=0, **overrides):
+    module = build_module(preset, dtype, seed, **overrides)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(*shape, generator=g).to("cuda", dtype)
+    with torch.inference_mode():
+        out, aux = module(x, return_aux=True)
+    assert aux.backend == "hip"
+    params = oracle_params(module)
+    expected, rq, rk = oracle.shared_dictionary_attention(params, module.config, np32(x), return_routed=True)
+    label = f"{preset} {tuple(shape)} {dtype} {overrides}"
+    assert_parity(out, expected, label=label)
+    assert_parity(aux.routing_query, rq, label=label + " routed q")
+    assert_parity(aux.routing_key, rk, label=label + " routed k")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_module_c1_a1(dtype) -> None:
+    run_module_case("a1", (8, 512, 512), dtype)
+
+
+def test_module_c2_qk4_s4() -> None:
+    run_module_case("qk4-s4", (8, 1024, 512))
+
+
+def test_module_c3_r512_d1536() -> None:
+    run_module_case("a1-r512-d1536", (4, 2048, 512))
+
+
+def test_module_c5_long_context() -> None:
+    run_module_case("a1", (1, 8192, 512))
+
+
+@pytest.mark.parametrize(("preset", "overrides"), [
+    ("a1", {"untied_dictionary": False}),
+    ("a1-no-qnorm", {}),
+    ("a1-no-dpnorm", {}),
+    ("a1-no-norm", {}),
+    ("qk2-s1", {}),
+    ("qk1-s2", {}),
+    ("qk2-s2", {}),
+    ("qk2-s2", {"map_combine": "concat"}),
+    ("a1", {"output_projection": False, "value_bias": False}),
+    ("a1", {"causal": False}),
+    ("a1-r512-d512", {}),
+])
+def test_module_variants_odd_shapes(preset, overrides) -> None:
+    run_module_case(preset, (2, 33, 512), seed=3, **overrides)
+    run_module_case(preset, (1, 1, 512), seed=4, **overrides)
+
+
+@pytest.mark.parametrize("name", ["a1_hip", "qk2_s2_hip"])
+def test_module_matches_reference_golden_vectors(name) -> None:
+    device = _device()
+    g = Golden(name)
+    config = da.DoubleAttentionConfig(**{**g.config, "backend": "hip"})
+    module = da.SharedDictionaryAttention(config)
+    module.load_state_dict({k: torch.from_numpy(v) for k, v in g.params.items()})
+    module = module.to(device=device, dtype=torch.bfloat16).eval()
+    x = torch.from_numpy(g["x"]).to(device, torch.bfloat16)
+    with torch.inference_mode():
+        out = module(x)
+    # The golden is the reference module in float64 on the unrounded inputs,
+    # so this bound also absorbs the bf16 rounding of weights and input.
+    assert_parity(out, g["out"], rel_l2=2e-2, max_abs=5e-2, label=f"golden {name}")
+
+
+def test_lm_c4_qk2_s2_tied() -> None:
+    device = _device()
+    config = da.experiment_config("qk2-s2", untied_dictionary=False, backend="hip")
+    torch.manual_seed(0)
+    model = da.DoubleAttentionLM(2048, 64, config, 6, dictionary_group_size=6, feedforward_dim=1536)
+    model = model.to(device=device, dtype=torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, 2048, (64, 64), generator=g)
+    with torch.inference_mode():
+        logits, _ = model(ids.to(device))
+    expected = oracle.double_attention_lm(oracle_params(model), config, ids.numpy(), 6, 6, dtype=np.float32)
+    # LayerNorm/FFN/LM head run as PyTorch bf16 ops between the HIP layers.
+    assert_parity(logits, expected, rel_l2=2e-2, max_abs=0.25, label="lm c4")
+
+
+def test_stack_normalizes_each_bank_once_on_hip(monkeypatch) -> None:
+    device = _device()
+    config = da.experiment_config("a1", backend="hip")
+    stack = da.DoubleAttentionStack(config, 6, dictionary_group_size=3, feedforward_dim=512).to(device, torch.bfloat16)
+    calls = []
+    original = da.SharedDictionaryBank.normalized_hip
+
+    def counted(bank, eps=1e-6, dtype=None):
+        calls.append(bank)
+        return original(bank, eps, dtype)
+
+    monkeypatch.setattr(da.SharedDictionaryBank, "normalized_hip", counted)
+    with torch.inference_mode():
+        stack(torch.randn(2, 16, 512, device=device, dtype=torch.bfloat16))
+    assert len(calls) == 2
+
+
+def test_hip_backward_matches_torch_path() -> None:
+    device = _device()
+    torch.manual_seed(5)
+    config = da.experiment_config("qk2-s2", backend="hip")
+    module = da.SharedDictionaryAttention(config).to(device)
+    reference = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(device)
+    reference.load_state_dict(module.state_dict())
+    x = torch.randn(1, 40, 512, device=device, requires_grad=True)
+    x_ref = x.detach().clone().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = module(x)
+        out_ref = reference(x_ref)
+    out.float().square().mean().backward()
+    out_ref.float().square().mean().backward()
+    torch.testing.assert_close(x.grad, x_ref.grad, atol=1e-3, rtol=5e-2)
+    for (name, p), p_ref in zip(module.named_parameters(), reference.parameters()):
+        assert p.grad is not None, name
+        torch.testing.assert_close(p.grad, p_ref.grad, atol=1e-3, rtol=5e-2, msg=name)
+
+
+def test_unsupported_variant_raises_on_gpu() -> None:
+    device = _device()
+    module = da.SharedDictionaryAttention(da.experiment_config("a1-silu", backend="hip")).to(device, torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        module(torch.randn(1, 8, 512, device=device, dtype=torch.bfloat16))

@@ -1,0 +1,223 @@
+"""CPU tests of the package's PyTorch path, API surface and backend dispatch.
+
+Mirrors the reference's CPU test strategy (reference ``tests/test_modules.py``):
+golden outputs written by the reference itself, the default-init RNG stream,
+state-dict names, normalize-once behaviour, config validation and clean
+errors for unavailable backends.
+"""
+
+from __future__ import annotations
+
+import copy
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import double_attention as da
+import double_attention._lib as lib
+import double_attention.modules as modules
+from conftest import Golden, golden_names
+
+
+def _assert_scaled(actual: torch.Tensor, expected: np.ndarray, tol: float = 1e-6) -> None:
+    err = np.abs(actual.detach().numpy() - expected).max() / np.abs(expected).max()
+    assert err <= tol, err
+
+
+def _config(g: Golden) -> da.DoubleAttentionConfig:
+    return da.DoubleAttentionConfig(**g.config)
+
+
+# ---------------------------------------------------------------- goldens
+
+
+@pytest.mark.parametrize("name", golden_names("attention"))
+def test_default_init_and_forward_match_reference(name: str) -> None:
+    g = Golden(name)
+    torch.manual_seed(int(g["seed"]))
+    module = da.SharedDictionaryAttention(_config(g))
+    state = module.state_dict()
+    # Same names in the same order, and bit-identical seeded default init.
+    assert list(state) == list(g.params)
+    for key, value in g.params.items():
+        np.testing.assert_array_equal(state[key].numpy(), value, err_msg=key)
+    module64 = copy.deepcopy(module).double().eval()
+    with torch.no_grad():
+        out, aux = module64(torch.from_numpy(g["x"]), return_aux=True)
+    _assert_scaled(out, g["out"])
+    np.testing.assert_allclose(aux.routing_query.numpy(), g["routing_query"], rtol=1e-10, atol=1e-12)
+    assert aux.backend == "torch"
+
+
+@pytest.mark.parametrize("name", golden_names("lm"))
+def test_lm_default_init_and_logits_match_reference(name: str) -> None:
+    g = Golden(name)
+    torch.manual_seed(int(g["seed"]))
+    model = da.DoubleAttentionLM(
+        vocab_size=int(g["vocab"]),
+        max_sequence_length=int(g["max_len"]),
+        config=_config(g),
+        num_layers=int(g["layers"]),
+        dictionary_group_size=int(g["group"]),
+        feedforward_dim=int(g["ffn"]),
+    )
+    state = model.state_dict()
+    assert list(state) == list(g.params)
+    for key, value in g.params.items():
+        np.testing.assert_array_equal(state[key].numpy(), value, err_msg=key)
+    with torch.no_grad():
+        logits, loss = copy.deepcopy(model).double()(torch.from_numpy(g["ids"]))
+    assert loss is None
+    _assert_scaled(logits, g["logits"])
+
+
+# Parameter counts recorded in the reference's run reports for the 6-layer,
+# d=512, vocab 2048, sequence 64 models (runs/tied/RESULTS.md:11,
+# runs/screen/RESULTS.md:13, runs/a1_multicorpus_8k/python_docs/
+# a1-r512-d1536_tied_s0_steps8000_sched12000.json).
+@pytest.mark.parametrize(
+    ("preset", "untied", "count"),
+    [("qk2-s2", False, 16_969_752), ("a1", True, 15_527_942), ("a1-r512-d1536", False, 17_625_094)],
+)
+def test_parameter_counts_match_reference_runs(preset: str, untied: bool, count: int) -> None:
+    config = da.experiment_config(preset, model_dim=512, untied_dictionary=untied, backend="torch")
+    with torch.device("meta"):
+        model = da.DoubleAttentionLM(2048, 64, config, 6, dictionary_group_size=6, feedforward_dim=1536)
+    assert sum(p.numel() for p in model.parameters()) == count
+
+
+# ---------------------------------------------------------------- module behaviour
+
+
+def small_config(name: str, **overrides: object) -> da.DoubleAttentionConfig:
+    values: dict[str, object] = {"model_dim": 32, "routing_dim": 8, "dictionary_size": 16, "backend": "torch"}
+    values.update(overrides)
+    return da.experiment_config(name, **values)
+
+
+@pytest.mark.parametrize("name", da.experiment_names())
+def test_all_presets_forward_and_backward(name: str) -> None:
+    torch.manual_seed(7)
+    module = da.SharedDictionaryAttention(small_config(name))
+    x = torch.randn(2, 7, 32, requires_grad=True)
+    out, aux = module(x, return_aux=True)
+    assert out.shape == x.shape
+    assert aux.routing_query.shape[:3] == (2, module.config.qk_branches, 7)
+    assert aux.score_query.shape[:3] == (2, module.config.outer_maps, 7)
+    assert aux.map_weights.shape == (module.config.outer_maps,)
+    out.square().mean().backward()
+    assert x.grad is not None and torch.isfinite(x.grad).all()
+    assert module.bank.raw_key.grad is not None
+
+
+def test_fused_and_separate_projection_agree(monkeypatch: pytest.MonkeyPatch) -> None:
+    torch.manual_seed(8)
+    module = da.SharedDictionaryAttention(small_config("qk2-s2"))
+    assert not any("fused" in k for k in module.state_dict())
+    x = torch.randn(2, 7, 32)
+    monkeypatch.setattr(modules, "FUSED_QUERY_KEY_PROJECTION", False)
+    separate = module(x)
+    monkeypatch.setattr(modules, "FUSED_QUERY_KEY_PROJECTION", True)
+    torch.testing.assert_close(module(x), separate, atol=1e-6, rtol=1e-5)
+
+
+def test_stack_normalizes_each_bank_once(monkeypatch: pytest.MonkeyPatch) -> None:
+    stack = da.DoubleAttentionStack(small_config("a1"), num_layers=6, dictionary_group_size=3, feedforward_dim=48)
+    calls = 0
+    original = modules.SharedDictionaryBank.normalized
+
+    def counted(bank, eps=1e-6):
+        nonlocal calls
+        calls += 1
+        return original(bank, eps)
+
+    monkeypatch.setattr(modules.SharedDictionaryBank, "normalized", counted)
+    stack(torch.randn(2, 6, 32)).square().mean().backward()
+    assert calls == len(stack.banks) == 2
+
+
+def test_tied_bank_shares_storage() -> None:
+    module = da.SharedDictionaryAttention(small_config("a1", untied_dictionary=False))
+    assert module.bank.raw_value is None
+    key, value = module.bank.normalized()
+    assert key.data_ptr() == value.data_ptr()
+
+
+def test_causal_prefix_independent_of_future() -> None:
+    torch.manual_seed(11)
+    module = da.SharedDictionaryAttention(
+        da.DoubleAttentionConfig(model_dim=16, routing_dim=8, dictionary_size=16, output_projection=False, backend="torch")
+    ).eval()
+    a = torch.randn(1, 8, 16)
+    b = a.clone()
+    b[:, 4:] = torch.randn_like(b[:, 4:]) * 10
+    with torch.no_grad():
+        torch.testing.assert_close(module(a)[:, :4], module(b)[:, :4], atol=1e-6, rtol=1e-5)
+
+
+def test_config_validation_and_presets() -> None:
+    with pytest.raises(ValueError, match="divide one another"):
+        da.DoubleAttentionConfig(qk_branches=3, outer_maps=2)
+    with pytest.raises(ValueError, match="unsupported backend"):
+        da.DoubleAttentionConfig(backend="cuda")  # type: ignore[arg-type]
+    assert da.DoubleAttentionConfig(backend="hip").backend == "hip"
+    c = da.experiment_config("a1-r512-d1536")
+    assert (c.routing_dim, c.dictionary_size) == (512, 1536)
+    assert c.beta == pytest.approx(4 * math.sqrt(2)) and c.initial_score_scale == pytest.approx(math.sqrt(512))
+    assert da.experiment_config("QK4_S4").qk_branches == 4
+    with pytest.raises(ValueError, match="unknown experiment"):
+        da.experiment_config("nope")
+    assert len(da.experiment_names()) == 21
+
+
+# ---------------------------------------------------------------- backend dispatch
+
+
+def test_auto_backend_uses_torch_on_cpu() -> None:
+    module = da.SharedDictionaryAttention(small_config("a1", backend="auto"))
+    _, aux = module(torch.randn(1, 4, 32), return_aux=True)
+    assert aux.backend == "torch"
+
+
+def test_explicit_hip_backend_fails_cleanly_on_cpu() -> None:
+    module = da.SharedDictionaryAttention(
+        da.DoubleAttentionConfig(model_dim=64, routing_dim=64, dictionary_size=64, backend="hip")
+    )
+    with pytest.raises(RuntimeError, match="HIP backend requested"):
+        module(torch.randn(1, 4, 64))
+
+
+def test_triton_backend_fails_cleanly() -> None:
+    module = da.SharedDictionaryAttention(small_config("a1", backend="triton"))
+    with pytest.raises(RuntimeError, match="Triton backend requested"):
+        module(torch.randn(1, 4, 32))
+    assert da.TRITON_AVAILABLE is False
+
+
+def test_missing_library_is_reported(monkeypatch: pytest.MonkeyPatch, tmp_path) -> None:
+    monkeypatch.setenv("DOUBLE_ATTENTION_HIP_LIBRARY", str(tmp_path / "missing.so"))
+    lib.reset()
+    try:
+        assert not lib.available()
+        with pytest.raises(RuntimeError, match="HIP backend requested but unavailable.*missing.so"):
+            da.ops.resolve_backend("hip", [torch.empty(1)])
+        # auto on CPU tensors never needs the library
+        assert da.ops.resolve_backend("auto", [torch.empty(1)]) == "torch"
+    finally:
+        monkeypatch.delenv("DOUBLE_ATTENTION_HIP_LIBRARY")
+        lib.reset()
+
+
+def test_unsupported_hip_variants_are_rejected() -> None:
+    from double_attention.hip_ops import check_module_supported
+
+    check_module_supported(da.experiment_config("a1"))
+    check_module_supported(da.experiment_config("qk4-s4"))
+    check_module_supported(da.experiment_config("a1-r512-d1536"))
+    for name in ("a1-silu", "a1-silu-logitnorm", "a1-no-softmax"):
+        with pytest.raises(NotImplementedError):
+            check_module_supported(da.experiment_config(name))
+    with pytest.raises(NotImplementedError):
+        check_module_supported(da.experiment_config("a1", routing_dim=96))
