@@ -124,12 +124,14 @@ def main() -> None:
     stream = torch.cuda.current_stream(device)
     handle = stream.cuda_stream
     with torch.inference_mode():
-        key, value = module.bank.normalized_hip(config.eps, dtype)
+        key_dtype = da.hip_ops.route_key_dtype(config.normalize_routing_input, dtype)
+        key_code = da.hip_ops.dtype_code(key_dtype)
+        key, value = module.bank.normalized_hip(config.eps, key_dtype)
         layout = key._da_route_layout
         qk = torch.empty(tokens, 2 * W, device=device, dtype=dtype)
         tp = lib.da_padded_length(length)
         vt = torch.zeros(batch, d, tp, device=device, dtype=dtype)
-        routed = torch.empty_like(qk)
+        routed = torch.empty(tokens, 2 * W, device=device, dtype=torch.float16)
         mixed = torch.empty(tokens, d, device=device, dtype=dtype)
         final = torch.empty(tokens, d, device=device, dtype=dtype)
         p = {k: v.contiguous() for k, v in module.state_dict().items()}
@@ -141,22 +143,22 @@ def main() -> None:
             "dict_normalize": lambda: lib.da_dictionary_normalize(
                 raw_key.data_ptr(), None if raw_value is None else raw_value.data_ptr(),
                 da.hip_ops.dtype_code(raw_key.dtype), R, M, config.eps,
-                layout.key_t.data_ptr(), layout.value.data_ptr(), code, handle),
+                layout.key_t.data_ptr(), key_code, layout.value.data_ptr(), handle),
             "qkv_projection": lambda: lib.da_qkv_projection(
                 x.data_ptr(), tokens, d, length, p["query.weight"].data_ptr(), p["key.weight"].data_ptr(), W,
                 p["value.weight"].data_ptr(), p["value.bias"].data_ptr(), d, pdt, code,
                 qk.data_ptr(), vt.data_ptr(), vt.stride(0), vt.stride(1), handle),
             "route": lambda: lib.da_dictionary_route(
-                qk.data_ptr(), rows, R, R, layout.key_t.data_ptr(), layout.value.data_ptr(), M,
+                qk.data_ptr(), rows, R, R, code, layout.key_t.data_ptr(), key_code, layout.value.data_ptr(), M,
                 p["log_beta"].data_ptr(), pdt, 0.0, config.eps,
                 _lib.DA_ROUTE_NORMALIZE_INPUT | _lib.DA_ROUTE_NORMALIZE_OUTPUT | _lib.DA_ROUTE_BETA_IS_LOG,
-                code, routed.data_ptr(), R, handle),
+                routed.data_ptr(), R, _lib.DA_F16, handle),
             "attention": lambda: lib.da_routed_attention(
                 routed.data_ptr(), routed.data_ptr() + W * routed.element_size(), length * 2 * W, 2 * W,
                 rp if H > S else R, S // H if S > H else 1, rp, vt.data_ptr(), vt.stride(0), vt.stride(1),
                 batch, S, length, d, p["log_score_scales"].data_ptr(), pdt,
                 float(group ** -0.5), None if S == 1 else p["map_mix_logits"].data_ptr(), pdt,
-                _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX, code,
+                _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX, _lib.DA_F16, code,
                 mixed.data_ptr(), length * d, d, 0, handle),
             "output_projection": lambda: lib.da_linear(
                 mixed.data_ptr(), tokens, d, p["output.weight"].data_ptr(), d, None, pdt, code,

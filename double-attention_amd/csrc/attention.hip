@@ -8,25 +8,27 @@
 // or every O_s written to its own slot (per-map mode, used by the concat
 // combine and by the operator-level API).
 //
-// One workgroup owns NW*16 query rows of one sequence and loops over the maps
-// and over 64-key tiles up to the causal bound.  As in the route kernel, work
-// happens in the transposed domain:
+// One workgroup (4 waves) owns 64 query rows of one sequence and walks the
+// (map, 32-key tile) sequence up to the causal bound.  Work happens in the
+// transposed domain:
 //   S^T[key, q] = sum_r K[key, r] Q^T[r, q]      (A = key rows from LDS, B = queries in VGPRs)
 //   O^T[d, q]  += sum_key V^T[d, key] P^T[key, q] (A = V^T from LDS, B = P in VGPRs)
-// so P never leaves registers and the score tile is computed exactly once per
-// (query tile, key tile) for the full value width D -- there is no per-D-block
-// recomputation.  V arrives token-contiguous (V^T, [B, D, Tv]) straight from
-// the projection GEMM's epilogue.  The temperatures gamma_s = exp(clamp(log
-// scale)) and the mix weights are computed on the device from the parameter
-// tensors, so a forward never synchronizes with the host.
+// so P never leaves registers and each score tile is computed once for the
+// full value width D.  Key and V^T tiles are double-buffered in LDS and
+// filled by global->LDS DMA while the previous tile is multiplied.  V comes
+// token-contiguous (V^T, [B, D, Tv]) from the projection GEMM's epilogue.
+// gamma_s = exp(clamp(log scale)) and the mix weights are computed on the
+// device, so a forward never synchronizes with the host.
+//
+// Element types: TQ for the routed queries/keys (fp16 on the module path: they
+// are unit vectors), TV for V and the probabilities (the model dtype).
 #include "da_common.h"
 #include "da_launch.h"
+#include "da_tile.h"
 
 namespace da {
 
-constexpr int kKeyTile = 64;
-constexpr int kAttnKeyPad = 8;
-constexpr int kAttnValPad = 8;
+constexpr int kKeyTile = 32;
 
 struct AttnParams {
   const void* q;
@@ -76,180 +78,226 @@ __device__ __forceinline__ void store_rows(const AttnParams& p, int b, int s, in
   }
 }
 
-template <typename T, int RP, int D, int NW, bool MULTI>
-__global__ __launch_bounds__(NW * 64) void attention_kernel(AttnParams p) {
-  typedef typename Elem<T>::v8 v8;
+template <typename TQ, typename TV, int RP, int D>
+struct AttnTile {
+  static constexpr int NCK = RP / 8;                  // 16B chunks per key row
+  static constexpr int KCH = kKeyTile * NCK;          // chunks in the key tile
+  static constexpr int VCK = kKeyTile / 8;            // chunks per V^T row (4)
+  static constexpr int VCH = D * VCK;                 // chunks in the V^T tile
+  static constexpr int BYTES = (KCH + VCH) * 16;
+  static_assert(KCH % 256 == 0 && VCH % 256 == 0, "tile must split evenly over 256 lanes");
+
+  // Issue the DMA of key tile [k0, k0+32) of map offset `off` into `buf`.
+  static __device__ __forceinline__ void issue(char* buf, const TQ* kbase, const TV* vtb,
+                                               const AttnParams& p, int64_t off, int k0, int wave,
+                                               int lane) {
+#pragma unroll
+    for (int i = 0; i < KCH / 256; ++i) {
+      const int j = i * 4 + wave;
+      int row, ck;
+      chunk_of<NCK, true>(j * 64 + lane, row, ck);
+      // Rows past the sequence end are masked to -inf; any valid row will do.
+      const int key = min(k0 + row, p.T - 1);
+      dma16(kbase + static_cast<int64_t>(key) * p.qk_stride_t + off + ck * 8, buf + j * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < VCH / 256; ++i) {
+      const int j = i * 4 + wave;
+      int d, ck;
+      chunk_of<VCK, false>(j * 64 + lane, d, ck);
+      int key = k0 + ck * 8;
+      // Chunks wholly past the end read token 0 (their P is zero); a chunk
+      // that straddles the end reads the V^T row padding, which the producer
+      // keeps finite.
+      if (key >= p.T) key = 0;
+      dma16(vtb + d * p.vt_stride_d + key, buf + KCH * 16 + j * 1024);
+    }
+  }
+};
+
+template <typename TQ, typename TV, int RP, int D, bool MULTI>
+__global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
+  typedef AttnTile<TQ, TV, RP, D> Tile;
+  typedef typename Elem<TQ>::v8 q8;
   constexpr int KS = RP / 32;
-  constexpr int KROW = RP + kAttnKeyPad;
-  constexpr int VROW = kKeyTile + kAttnValPad;
-  constexpr int QT = NW * 16;   // queries per workgroup
-  __shared__ __attribute__((aligned(16))) T ks[kKeyTile * KROW];
-  __shared__ __attribute__((aligned(16))) T vs[D * VROW];
+  constexpr int QT = 64;   // queries per workgroup
+  __shared__ __attribute__((aligned(1024))) char lds0[Tile::BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds1[Tile::BYTES];
 
   const int lane = lane_id();
   const int c = lane & 15;
   const int g = lane >> 4;
+  const int wave = uniform_wave();
   const int n_qt = (p.T + QT - 1) / QT;
   const int qt = n_qt - 1 - static_cast<int>(blockIdx.x);   // heaviest causal tiles first
   const int b = blockIdx.y;
   const int q0 = qt * QT;
-  const int tq = q0 + wave_id() * 16 + c;                  // this lane's query token
+  const int tq = q0 + wave * 16 + c;                       // this lane's query token
   const bool q_ok = tq < p.T;
   const bool causal = p.flags & kAttnCausal;
   const int q_last = min(q0 + QT, p.T) - 1;
   const int n_kt = causal ? q_last / kKeyTile + 1 : (p.T + kKeyTile - 1) / kKeyTile;
+  const int total = p.S * n_kt;
 
-  const T* qbase = static_cast<const T*>(p.q) + b * p.qk_stride_b;
-  const T* kbase = static_cast<const T*>(p.k) + b * p.qk_stride_b;
-  const T* vtb = static_cast<const T*>(p.vt) + b * p.vt_stride_b;
+  const TQ* qbase = static_cast<const TQ*>(p.q) + b * p.qk_stride_b;
+  const TQ* kbase = static_cast<const TQ*>(p.k) + b * p.qk_stride_b;
+  const TV* vtb = static_cast<const TV*>(p.vt) + b * p.vt_stride_b;
 
   f32x4 yacc[MULTI ? D / 16 : 1];
   if constexpr (MULTI) {
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) yacc[i] = zero4();
   }
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) acc[i] = zero4();
+  float m_run = -INFINITY;
+  float l_part = 0.f;
+  q8 qf[KS];
+  float sc = 0.f;
 
-  for (int s = 0; s < p.S; ++s) {
-    const int64_t off = static_cast<int64_t>(s / p.map_repeat) * p.map_stride;
-    const float sc = map_gamma(p, s) * kLog2e;
-    v8 qf[KS];
+  auto map_offset = [&](int s) -> int64_t { return static_cast<int64_t>(s / p.map_repeat) * p.map_stride; };
+  auto load_map = [&](int s) {
+    const int64_t off = map_offset(s);
+    sc = map_gamma(p, s) * kLog2e;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk)
       qf[kk] = q_ok ? load8(qbase + static_cast<int64_t>(tq) * p.qk_stride_t + off + kk * 32 + 8 * g)
-                    : zero8<T>();
+                    : zero8<TQ>();
+  };
 
-    f32x4 acc[D / 16];
-#pragma unroll
-    for (int i = 0; i < D / 16; ++i) acc[i] = zero4();
-    float m_run = -INFINITY;
-    float l_part = 0.f;
+  // One pipeline step: tile u is resident in `cur`; prefetch u+1 into `nxt`.
+  auto step = [&](int u, char* cur, char* nxt) {
+    wait_vmem();
+    __syncthreads();
+    if (u + 1 < total) {
+      const int s1 = (u + 1) / n_kt;
+      Tile::issue(nxt, kbase, vtb, p, map_offset(s1), ((u + 1) - s1 * n_kt) * kKeyTile, wave, lane);
+    }
+    const int s = u / n_kt;
+    const int kt = u - s * n_kt;
+    const int k0 = kt * kKeyTile;
 
-    for (int kt = 0; kt < n_kt; ++kt) {
-      const int k0 = kt * kKeyTile;
-      __syncthreads();
-      for (int ch = threadIdx.x; ch < kKeyTile * (RP / 8); ch += NW * 64) {
-        const int a = ch / (RP / 8);
-        const int k8 = ch % (RP / 8);
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (k0 + a < p.T) v = load16B(kbase + static_cast<int64_t>(k0 + a) * p.qk_stride_t + off + k8 * 8);
-        store16B(&ks[a * KROW + k8 * 8], v);
-      }
-      for (int ch = threadIdx.x; ch < D * (kKeyTile / 8); ch += NW * 64) {
-        const int d = ch / (kKeyTile / 8);
-        const int a8 = ch % (kKeyTile / 8);
-        const int key = k0 + a8 * 8;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (key < p.T) {
-          v = load16B(vtb + d * p.vt_stride_d + key);
-          if (key + 8 > p.T) {
-            // Zero the tokens past the sequence end: P is zero there, but the
-            // padding of V^T is never written and must not inject NaN/Inf.
-            // Word w holds tokens key+2w (low half) and key+2w+1 (high half).
+    // Scores: two independent accumulator chains (the two 16-key blocks),
+    // fragments read from LDS in batches ahead of their MFMAs.
+    f32x4 st[2] = {zero4(), zero4()};
+    {
+      const int row0 = blocked_row(0, c);
+      const int row1 = blocked_row(1, c);
+      constexpr int KB = KS < 4 ? KS : 4;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              const uint32_t lo = key + 2 * w < p.T ? 0x0000ffffu : 0u;
-              const uint32_t hi = key + 2 * w + 1 < p.T ? 0xffff0000u : 0u;
-              v[w] &= (lo | hi);
-            }
-          }
+      for (int kk0 = 0; kk0 < KS; kk0 += KB) {
+        u32x4 a0[KB], a1[KB];
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+          a0[i] = lds_chunk<Tile::NCK, true>(cur, row0, (kk0 + i) * 4 + g);
+          a1[i] = lds_chunk<Tile::NCK, true>(cur, row1, (kk0 + i) * 4 + g);
         }
-        store16B(&vs[d * VROW + a8 * 8], v);
-      }
-      __syncthreads();
-
-      f32x4 st[4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        f32x4 t = zero4();
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk)
-          t = Elem<T>::mma(load8(&ks[(kb * 16 + c) * KROW + kk * 32 + 8 * g]), qf[kk], t);
-        st[kb] = t;
-      }
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = k0 + kb * 16 + 4 * g + i;
-          const bool ok = key < p.T && (!causal || key <= tq);
-          const float v = ok ? st[kb][i] * sc : -INFINITY;
-          st[kb][i] = v;
-          tmax = fmaxf(tmax, v);
+        for (int i = 0; i < KB; ++i) {
+          st[0] = Elem<TQ>::mma(as_v8<TQ>(a0[i]), qf[kk0 + i], st[0]);
+          st[1] = Elem<TQ>::mma(as_v8<TQ>(a1[i]), qf[kk0 + i], st[1]);
         }
-      }
-      const float m_new = fmaxf(m_run, group_max(tmax));
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;   // fully masked so far
-      const float alpha = exp2f(m_run - m_use);
-      float psum = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pr = exp2f(st[kb][i] - m_use);
-          st[kb][i] = pr;
-          psum += pr;
-        }
-      }
-      l_part = l_part * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int i = 0; i < D / 16; ++i) acc[i] *= alpha;
-
-      const v8 p0 = pack_blocked<T>(st[0], st[1]);
-      const v8 p1 = pack_blocked<T>(st[2], st[3]);
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db) {
-        const T* vrow = &vs[(db * 16 + c) * VROW];
-        acc[db] = Elem<T>::mma(load_blocked<T>(vrow, g), p0, acc[db]);
-        acc[db] = Elem<T>::mma(load_blocked<T>(vrow + 32, g), p1, acc[db]);
       }
     }
-
-    const float l = group_sum(l_part);
-    const float w = map_weight(p, s) / (l > 0.f ? l : 1.f);
-    if constexpr (MULTI) {
+    // Lane (c, g) now holds keys k0 + 8g + 4kb + i of query tq.
+    float tmax = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < D / 16; ++i) yacc[i] += acc[i] * w;
-    } else {
-      if (q_ok) store_rows<T, D>(p, b, (p.flags & kAttnMix) ? 0 : s, tq, g, acc, w);
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = k0 + 8 * g + 4 * kb + i;
+        const bool ok = key < p.T && (!causal || key <= tq);
+        const float v = ok ? st[kb][i] * sc : -INFINITY;
+        st[kb][i] = v;
+        tmax = fmaxf(tmax, v);
+      }
     }
+    lazy_rescale<D / 16>(group_max(tmax), m_run, l_part, acc);
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;   // fully masked so far
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pr = exp2f(st[kb][i] - m_use);
+        st[kb][i] = pr;
+        psum += pr;
+      }
+    }
+    l_part += psum;
+    const typename Elem<TV>::v8 pb = pack_blocked<TV>(st[0], st[1]);   // keys k0 + 8g + e
+    const char* vtile = cur + Tile::KCH * 16;
+    constexpr int DB = D / 16 < 8 ? D / 16 : 8;
+#pragma unroll
+    for (int db0 = 0; db0 < D / 16; db0 += DB) {
+      u32x4 a[DB];
+#pragma unroll
+      for (int i = 0; i < DB; ++i) a[i] = lds_chunk<Tile::VCK, false>(vtile, (db0 + i) * 16 + c, g);
+#pragma unroll
+      for (int i = 0; i < DB; ++i) acc[db0 + i] = Elem<TV>::mma(as_v8<TV>(a[i]), pb, acc[db0 + i]);
+    }
+
+    if (kt == n_kt - 1) {   // map s complete
+      const float l = group_sum(l_part);
+      const float w = map_weight(p, s) / (l > 0.f ? l : 1.f);
+      if constexpr (MULTI) {
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) yacc[i] += acc[i] * w;
+      } else {
+        if (q_ok) store_rows<TV, D>(p, b, (p.flags & kAttnMix) ? 0 : s, tq, g, acc, w);
+      }
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) acc[i] = zero4();
+      m_run = -INFINITY;
+      l_part = 0.f;
+      if (s + 1 < p.S) load_map(s + 1);
+    }
+  };
+
+  load_map(0);
+  Tile::issue(lds0, kbase, vtb, p, map_offset(0), 0, wave, lane);
+  int u = 0;
+  for (; u + 1 < total; u += 2) {
+    step(u, lds0, lds1);
+    step(u + 1, lds1, lds0);
   }
+  if (u < total) step(u, lds0, lds1);
+
   if constexpr (MULTI) {
-    if (q_ok) store_rows<T, D>(p, b, 0, tq, g, yacc, 1.f);
+    if (q_ok) store_rows<TV, D>(p, b, 0, tq, g, yacc, 1.f);
   }
 }
 
-template <typename T, int RP, int D, bool MULTI>
+template <typename TQ, typename TV, int RP, int D, bool MULTI>
 static void launch_attn_3(const AttentionArgs& a, const AttnParams& p, hipStream_t s) {
-  constexpr int NW = 4;
-  const int n_qt = (a.T + NW * 16 - 1) / (NW * 16);
-  hipLaunchKernelGGL((attention_kernel<T, RP, D, NW, MULTI>), dim3(n_qt, a.B), dim3(NW * 64), 0, s, p);
+  const int n_qt = (a.T + 63) / 64;
+  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, D, MULTI>), dim3(n_qt, a.B), dim3(256), 0, s, p);
 }
 
-template <typename T, int RP, int D>
+template <typename TQ, typename TV, int RP, int D>
 static void launch_attn_2(const AttentionArgs& a, const AttnParams& p, hipStream_t s) {
-  if ((a.flags & kAttnMix) && a.S > 1) launch_attn_3<T, RP, D, true>(a, p, s);
-  else launch_attn_3<T, RP, D, false>(a, p, s);
+  if ((a.flags & kAttnMix) && a.S > 1) launch_attn_3<TQ, TV, RP, D, true>(a, p, s);
+  else launch_attn_3<TQ, TV, RP, D, false>(a, p, s);
 }
 
-template <typename T, int RP>
+template <typename TQ, typename TV, int RP>
 static void launch_attn_1(const AttentionArgs& a, const AttnParams& p, hipStream_t s) {
   switch (a.D) {
-    case 64: launch_attn_2<T, RP, 64>(a, p, s); break;
-    case 128: launch_attn_2<T, RP, 128>(a, p, s); break;
-    case 256: launch_attn_2<T, RP, 256>(a, p, s); break;
-    default: launch_attn_2<T, RP, 512>(a, p, s); break;
+    case 64: launch_attn_2<TQ, TV, RP, 64>(a, p, s); break;
+    case 128: launch_attn_2<TQ, TV, RP, 128>(a, p, s); break;
+    case 256: launch_attn_2<TQ, TV, RP, 256>(a, p, s); break;
+    default: launch_attn_2<TQ, TV, RP, 512>(a, p, s); break;
   }
 }
 
-template <typename T>
+template <typename TQ, typename TV>
 static void launch_attn_0(const AttentionArgs& a, const AttnParams& p, hipStream_t s) {
   switch (a.RP) {
-    case 64: launch_attn_1<T, 64>(a, p, s); break;
-    case 128: launch_attn_1<T, 128>(a, p, s); break;
-    case 256: launch_attn_1<T, 256>(a, p, s); break;
-    default: launch_attn_1<T, 512>(a, p, s); break;
+    case 64: launch_attn_1<TQ, TV, 64>(a, p, s); break;
+    case 128: launch_attn_1<TQ, TV, 128>(a, p, s); break;
+    case 256: launch_attn_1<TQ, TV, 256>(a, p, s); break;
+    default: launch_attn_1<TQ, TV, 512>(a, p, s); break;
   }
 }
 
@@ -277,8 +325,9 @@ void launch_routed_attention(const AttentionArgs& a, hipStream_t stream) {
   p.out_stride_b = a.out_stride_b;
   p.out_stride_t = a.out_stride_t;
   p.out_stride_s = a.out_stride_s;
-  if (a.dtype == kF16) launch_attn_0<_Float16>(a, p, stream);
-  else launch_attn_0<__bf16>(a, p, stream);
+  if (a.qk_dtype == kF16 && a.v_dtype == kBF16) launch_attn_0<_Float16, __bf16>(a, p, stream);
+  else if (a.qk_dtype == kF16) launch_attn_0<_Float16, _Float16>(a, p, stream);
+  else launch_attn_0<__bf16, __bf16>(a, p, stream);
 }
 
 }  // namespace da

@@ -31,6 +31,11 @@ bool pow2_width(int64_t v) { return v == 64 || v == 128 || v == 256 || v == 512;
 bool half_dtype(int d) { return d == DA_F16 || d == DA_BF16; }
 bool any_dtype(int d) { return d == DA_F32 || d == DA_F16 || d == DA_BF16; }
 
+int ok() {
+  g_error.clear();
+  return DA_OK;
+}
+
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DA_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
@@ -41,12 +46,20 @@ int check_launch(const char* what) {
 constexpr int64_t kAlign = 256;
 int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-int validate_route(const void* x, int64_t rows, int64_t R, int64_t xs, const void* kt,
-                   const void* v, int64_t atoms, const void* beta, int beta_dtype, int dtype,
-                   const void* out, int64_t os) {
-  if (!half_dtype(dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "route: dtype must be DA_F16 or DA_BF16");
+int validate_route(const void* x, int64_t rows, int64_t R, int64_t xs, int x_dtype, const void* kt,
+                   int key_dtype, const void* v, int64_t atoms, const void* beta, int beta_dtype,
+                   int flags, const void* out, int64_t os, int out_dtype) {
+  if (!half_dtype(x_dtype) || !half_dtype(key_dtype) || !half_dtype(out_dtype))
+    return fail(DA_ERR_INVALID_ARGUMENT, "route: element types must be DA_F16 or DA_BF16");
+  if (key_dtype != DA_F16 && key_dtype != x_dtype)
+    return fail(DA_ERR_UNSUPPORTED, "route: key_dtype must be DA_F16 or x_dtype");
+  if (!(flags & DA_ROUTE_NORMALIZE_INPUT) && key_dtype != x_dtype)
+    return fail(DA_ERR_UNSUPPORTED, "route: without input normalization key_dtype must equal x_dtype");
+  if (out_dtype != DA_F16 && out_dtype != x_dtype)
+    return fail(DA_ERR_UNSUPPORTED, "route: out_dtype must be DA_F16 or x_dtype");
   if (!pow2_width(R)) return fail(DA_ERR_UNSUPPORTED, "route: routing_dim %lld not in {64,128,256,512}", (long long)R);
   if (rows < 0 || atoms < 1 || atoms > (1 << 24)) return fail(DA_ERR_INVALID_ARGUMENT, "route: bad rows/atoms");
+  if (rows == 0) return DA_OK;
   if (!x || !kt || !v || !out) return fail(DA_ERR_INVALID_ARGUMENT, "route: null pointer");
   if (beta && !any_dtype(beta_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "route: bad beta dtype");
   if (!aligned(x, 16) || !aligned(kt, 16) || !aligned(v, 16) || !aligned(out, 16))
@@ -60,13 +73,17 @@ int validate_route(const void* x, int64_t rows, int64_t R, int64_t xs, const voi
 int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int64_t ms, int64_t rep,
                        int64_t RP, const void* vt, int64_t vsb, int64_t vsd, int64_t B, int64_t S,
                        int64_t T, int64_t D, const void* scales, int scales_dtype,
-                       const void* mix, int mix_dtype, int dtype, const void* out, int64_t ob,
-                       int64_t ot, int64_t os) {
-  if (!half_dtype(dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "attention: dtype must be DA_F16 or DA_BF16");
+                       const void* mix, int mix_dtype, int qk_dtype, int v_dtype, const void* out,
+                       int64_t ob, int64_t ot, int64_t os) {
+  const bool types_ok = (qk_dtype == DA_F16 && (v_dtype == DA_BF16 || v_dtype == DA_F16)) ||
+                        (qk_dtype == DA_BF16 && v_dtype == DA_BF16);
+  if (!types_ok)
+    return fail(DA_ERR_UNSUPPORTED, "attention: (qk_dtype, v_dtype) must be (F16,BF16), (F16,F16) or (BF16,BF16)");
   if (!pow2_width(RP)) return fail(DA_ERR_UNSUPPORTED, "attention: score_dim %lld not in {64,128,256,512}", (long long)RP);
   if (!pow2_width(D)) return fail(DA_ERR_UNSUPPORTED, "attention: value_dim %lld not in {64,128,256,512}", (long long)D);
   if (B < 0 || T < 0 || S < 1 || rep < 1 || B > 65535 || T > (1LL << 30))
     return fail(DA_ERR_INVALID_ARGUMENT, "attention: bad batch/maps/length/map_repeat");
+  if (B == 0 || T == 0) return DA_OK;
   if (!q || !k || !vt || !scales || !out) return fail(DA_ERR_INVALID_ARGUMENT, "attention: null pointer");
   if (!any_dtype(scales_dtype) || (mix && !any_dtype(mix_dtype)))
     return fail(DA_ERR_INVALID_ARGUMENT, "attention: bad scalar dtype");
@@ -84,7 +101,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 1; }
+int da_abi_version(void) { return 2; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -94,8 +111,8 @@ int64_t da_padded_length(int64_t length) { return da::round_up(length, da::kKeyP
 
 int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_dtype,
                             int64_t routing_dim, int64_t atoms, float eps, void* key_t,
-                            void* value, int out_dtype, da_stream_t stream) {
-  if (!any_dtype(raw_dtype) || !half_dtype(out_dtype))
+                            int key_dtype, void* value, da_stream_t stream) {
+  if (!any_dtype(raw_dtype) || !half_dtype(key_dtype))
     return fail(DA_ERR_INVALID_ARGUMENT, "normalize: bad dtype");
   if (!pow2_width(routing_dim))
     return fail(DA_ERR_UNSUPPORTED, "normalize: routing_dim %lld not in {64,128,256,512}", (long long)routing_dim);
@@ -103,21 +120,23 @@ int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_
   if (!raw_key || !key_t || !value) return fail(DA_ERR_INVALID_ARGUMENT, "normalize: null pointer");
   if (!aligned(key_t, 16) || !aligned(value, 16)) return fail(DA_ERR_ALIGNMENT, "normalize: outputs must be 16-byte aligned");
   da::launch_dictionary_normalize(raw_key, raw_value, raw_dtype, static_cast<int>(routing_dim),
-                                  static_cast<int>(atoms), eps, key_t, value, out_dtype,
+                                  static_cast<int>(atoms), eps, key_t, key_dtype, value,
                                   reinterpret_cast<hipStream_t>(stream));
   return check_launch("normalize");
 }
 
 int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_t x_row_stride,
-                        const void* key_t, const void* value, int64_t atoms, const void* beta,
-                        int beta_dtype, float beta_value, float eps, int flags, int dtype,
-                        void* out, int64_t out_row_stride, da_stream_t stream) {
-  int rc = validate_route(x, rows, routing_dim, x_row_stride, key_t, value, atoms, beta, beta_dtype,
-                          dtype, out, out_row_stride);
+                        int x_dtype, const void* key_t, int key_dtype, const void* value,
+                        int64_t atoms, const void* beta, int beta_dtype, float beta_value,
+                        float eps, int flags, void* out, int64_t out_row_stride, int out_dtype,
+                        da_stream_t stream) {
+  int rc = validate_route(x, rows, routing_dim, x_row_stride, x_dtype, key_t, key_dtype, value, atoms,
+                          beta, beta_dtype, flags, out, out_row_stride, out_dtype);
   if (rc) return rc;
-  da::RouteArgs a{x, rows, x_row_stride, static_cast<int>(routing_dim), key_t, value,
-                  static_cast<int>(atoms), beta, beta_dtype, beta_value, eps, flags, dtype, out,
-                  out_row_stride};
+  if (rows == 0) return ok();
+  da::RouteArgs a{x, rows, x_row_stride, x_dtype, static_cast<int>(routing_dim), key_t, key_dtype,
+                  value, static_cast<int>(atoms), beta, beta_dtype, beta_value, eps, flags, out,
+                  out_row_stride, out_dtype};
   da::launch_dictionary_route(a, reinterpret_cast<hipStream_t>(stream));
   return check_launch("route");
 }
@@ -127,14 +146,15 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
                         const void* value_t, int64_t vt_stride_b, int64_t vt_stride_d,
                         int64_t batch, int64_t maps, int64_t length, int64_t value_dim,
                         const void* scales, int scales_dtype, float scale_mult,
-                        const void* mix_logits, int mix_dtype, int flags, int dtype, void* out,
-                        int64_t out_stride_b, int64_t out_stride_t, int64_t out_stride_s,
-                        da_stream_t stream) {
+                        const void* mix_logits, int mix_dtype, int flags, int qk_dtype,
+                        int v_dtype, void* out, int64_t out_stride_b, int64_t out_stride_t,
+                        int64_t out_stride_s, da_stream_t stream) {
   int rc = validate_attention(query, key, stride_b, stride_t, map_stride, map_repeat, score_dim,
                               value_t, vt_stride_b, vt_stride_d, batch, maps, length, value_dim,
-                              scales, scales_dtype, mix_logits, mix_dtype, dtype, out,
+                              scales, scales_dtype, mix_logits, mix_dtype, qk_dtype, v_dtype, out,
                               out_stride_b, out_stride_t, out_stride_s);
   if (rc) return rc;
+  if (batch == 0 || length == 0) return ok();
   da::AttentionArgs a;
   a.q = query;
   a.k = key;
@@ -156,7 +176,8 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
   a.mix_logits = mix_logits;
   a.mix_dtype = mix_dtype;
   a.flags = flags;
-  a.dtype = dtype;
+  a.qk_dtype = qk_dtype;
+  a.v_dtype = v_dtype;
   a.out = out;
   a.out_stride_b = out_stride_b;
   a.out_stride_t = out_stride_t;
@@ -185,8 +206,8 @@ int da_qkv_projection(const void* x, int64_t tokens, int64_t model_dim, int64_t 
   if (!aligned(wq, 16) || !aligned(wk, 16) || !aligned(wv, 16) || !aligned(qk_out, 16) || !aligned(value_t, 16))
     return fail(DA_ERR_ALIGNMENT, "projection: tensors must be 16-byte aligned");
   if (bv && !any_dtype(bias_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "projection: bad bias dtype");
-  if (vt_pitch < length || vt_pitch % 8 || vt_stride_b < value_dim * vt_pitch)
-    return fail(DA_ERR_ALIGNMENT, "projection: bad value_t pitches");
+  if (vt_pitch < length || vt_pitch % da::kKeyPad || vt_stride_b < value_dim * vt_pitch || vt_stride_b % 8)
+    return fail(DA_ERR_ALIGNMENT, "projection: vt_pitch must be a multiple of 64 and >= length");
   da::GemmSegment segs[2];
   segs[0] = da::GemmSegment{wq, wk, qk_width, x, 2 * qk_width, tokens, model_dim, nullptr, 0, 0,
                             qk_out, 2 * qk_width, 0, 0, 0};
@@ -261,14 +282,19 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   int rc = validate_gemm_common("forward/projection", a->x, B * T, d, a->dtype);
   if (rc) return rc;
   if (W % 8) return fail(DA_ERR_UNSUPPORTED, "forward: qk width must be a multiple of 8");
-  rc = validate_route(routed, B * T * 2 * H, R, R, a->key_t, a->value, a->atoms, a->log_beta,
-                      a->param_dtype, a->dtype, routed, R);
+  const bool norm_in = a->flags & DA_SDA_NORMALIZE_INPUT;
+  const int key_dtype = norm_in ? DA_F16 : a->dtype;
+  int rflags = da::kRouteBetaIsLog;
+  if (norm_in) rflags |= da::kRouteNormalizeInput;
+  if (a->flags & DA_SDA_NORMALIZE_OUTPUT) rflags |= da::kRouteNormalizeOutput;
+  rc = validate_route(routed, B * T * 2 * H, R, R, a->dtype, a->key_t, key_dtype, a->value, a->atoms,
+                      a->log_beta, a->param_dtype, rflags, routed, R, DA_F16);
   if (rc) return rc;
   const int64_t ot = concat ? S * d : d;
   rc = validate_attention(routed, static_cast<char*>(routed) + W * 2, T * 2 * W, 2 * W,
                           H > S ? RP : R, 1, RP, vt, d * Tp, Tp, B, S, T, d, a->log_score_scales,
-                          a->param_dtype, a->map_mix_logits, a->param_dtype, a->dtype, mixed,
-                          T * ot, ot, concat ? d : 0);
+                          a->param_dtype, a->map_mix_logits, a->param_dtype, DA_F16, a->dtype,
+                          mixed, T * ot, ot, concat ? d : 0);
   if (rc) return rc;
   if (a->wo) {
     rc = validate_gemm_common("forward/output", mixed, B * T, ot, a->dtype);
@@ -285,12 +311,11 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   proj[1] = da::GemmSegment{a->x, nullptr, 0, a->wv, B * T, d, d, a->bv, a->param_dtype, 1, vt, 0, T, Tp, d * Tp};
   da::launch_gemm(proj, 2, a->dtype, s);
   // 2. Route all Q and K rows in place: [tokens, 2, H, R] is [tokens*2H, R].
-  int rflags = da::kRouteBetaIsLog;
-  if (a->flags & DA_SDA_NORMALIZE_INPUT) rflags |= da::kRouteNormalizeInput;
-  if (a->flags & DA_SDA_NORMALIZE_OUTPUT) rflags |= da::kRouteNormalizeOutput;
-  da::RouteArgs ra{routed, B * T * 2 * H, R, static_cast<int>(R), a->key_t, a->value,
-                   static_cast<int>(a->atoms), a->log_beta, a->param_dtype, 0.f, a->eps, rflags,
-                   a->dtype, routed, R};
+  //    The routed rows are written as fp16 (unit vectors, or convex
+  //    combinations of unit atoms without output normalization).
+  da::RouteArgs ra{routed, B * T * 2 * H, R, a->dtype, static_cast<int>(R), a->key_t, key_dtype,
+                   a->value, static_cast<int>(a->atoms), a->log_beta, a->param_dtype, 0.f, a->eps,
+                   rflags, routed, R, DA_F16};
   da::launch_dictionary_route(ra, s);
   // 3. Outer attention over the S maps, mixed (or concatenated).
   da::AttentionArgs at;
@@ -315,7 +340,8 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   at.mix_dtype = a->param_dtype;
   at.flags = da::kAttnScalesAreLog | ((a->flags & DA_SDA_CAUSAL) ? da::kAttnCausal : 0) |
              (concat ? 0 : da::kAttnMix);
-  at.dtype = a->dtype;
+  at.qk_dtype = DA_F16;
+  at.v_dtype = a->dtype;
   at.out = mixed;
   at.out_stride_b = T * ot;
   at.out_stride_t = ot;

@@ -77,6 +77,28 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Online-softmax bookkeeping with lazy rescaling.  `tile_max` is this tile's
+// row maximum (log2 domain, already reduced over the lane groups).  The
+// running reference max only moves -- and the accumulators are rescaled --
+// when a row maximum exceeds it by more than kRescaleSlack, so exponentials
+// stay <= 2^kRescaleSlack (exact in fp16/bf16 operands) and most tiles skip
+// the rescale.  The branch is taken by the whole wave if any row needs it;
+// rows that do not need it use factor 1.  The common factor 2^-m cancels in
+// the final division by the row sum.
+constexpr float kRescaleSlack = 8.f;
+
+template <int N>
+__device__ __forceinline__ void lazy_rescale(float tile_max, float& m_run, float& l_part, f32x4* acc) {
+  const bool need = tile_max > m_run + kRescaleSlack;
+  if (__ballot(need)) {
+    const float alpha = need ? exp2f(m_run - tile_max) : 1.f;
+    if (need) m_run = tile_max;
+    l_part *= alpha;
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc[i] *= alpha;
+  }
+}
+
 // Build a B operand (8 values of T) from two stacked 16x16 fp32 accumulator
 // blocks using the "blocked" k assignment described above.
 template <typename T>

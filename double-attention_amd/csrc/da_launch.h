@@ -36,18 +36,20 @@ struct RouteArgs {
   const void* x;
   int64_t rows;
   int64_t x_stride;
+  int x_dtype;
   int R;
   const void* key_t;
-  const void* value;
+  int key_dtype;
+  const void* value;    // fp16
   int M;
   const void* beta_ptr;
   int beta_dtype;
   float beta_value;
   float eps;
   int flags;
-  int dtype;
   void* out;
   int64_t out_stride;
+  int out_dtype;
 };
 
 struct AttentionArgs {
@@ -66,7 +68,8 @@ struct AttentionArgs {
   const void* mix_logits;             // [S] map-mix logits or nullptr (uniform)
   int mix_dtype;
   int flags;
-  int dtype;
+  int qk_dtype;                       // routed queries/keys
+  int v_dtype;                        // V, probabilities and the output
   void* out;
   int64_t out_stride_b, out_stride_t, out_stride_s;
 };
@@ -84,11 +87,13 @@ struct GemmSegment {
   int mode;               // 0: out[j, i] (row-major by j), 1: V^T layout
   void* out;
   int64_t ldo;            // mode 0: row pitch of out (elements)
-  int64_t T, Tp, vt_stride_b;   // mode 1: token t of sequence b goes to out[b*vt_stride_b + i_feat*Tp + t]
+  // mode 1: I counts the B*T real tokens; token t of sequence b goes to
+  // out[b*vt_stride_b + j_feat*Tp + t], and tokens T..Tp-1 are filled too.
+  int64_t T, Tp, vt_stride_b;
 };
 
 void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int in_dtype, int R,
-                                 int M, float eps, void* key_t, void* value, int out_dtype,
+                                 int M, float eps, void* key_t, int key_dtype, void* value,
                                  hipStream_t stream);
 void launch_dictionary_route(const RouteArgs& a, hipStream_t stream);
 void launch_routed_attention(const AttentionArgs& a, hipStream_t stream);

@@ -8,9 +8,12 @@
 //
 // Output layouts are the ones the fused route kernel reads, padded to
 // Mp = round_up(M, 64) atoms with zero atoms in the padding:
-//   key_t  [Mp, R]  atom-major (row j = normalized key atom j)
-//   value  [R, Mp]  routing-dim-major (row r = coordinate r of every value atom)
-// The sums of squares are accumulated in fp32; each output is rounded once.
+//   key_t  [Mp, R]  atom-major, element type TK
+//   value  [R, Mp]  coordinate-major, fp16 (normalized atoms are bounded by 1)
+// A workgroup owns 32 atoms: it reads each column once into registers (fp32),
+// reduces the sums of squares through LDS, writes the value layout directly
+// and the atom-major key layout through an LDS transpose, so every global
+// store is a full 16-byte chunk or a coalesced row segment.
 #include "da_common.h"
 #include "da_launch.h"
 
@@ -19,10 +22,11 @@ namespace da {
 constexpr int kNormCols = 32;     // atoms per workgroup
 constexpr int kNormGroups = 8;    // row groups per workgroup (256 threads)
 
-template <typename Tin, typename Tout>
+template <typename Tin, typename TK, int R>
 __global__ __launch_bounds__(256) void dict_normalize_kernel(
-    const Tin* __restrict__ raw_key, const Tin* __restrict__ raw_value, int R, int M, int Mp,
-    float eps, Tout* __restrict__ key_t, Tout* __restrict__ value) {
+    const Tin* __restrict__ raw_key, const Tin* __restrict__ raw_value, int M, int Mp, float eps,
+    TK* __restrict__ key_t, _Float16* __restrict__ value) {
+  constexpr int PER = R / kNormGroups;
   const int which = blockIdx.y;  // 0: key bank, 1: value bank (untied only)
   const Tin* src = which == 0 ? raw_key : raw_value;
   const bool write_key = which == 0;
@@ -30,18 +34,21 @@ __global__ __launch_bounds__(256) void dict_normalize_kernel(
 
   const int jj = threadIdx.x % kNormCols;
   const int rg = threadIdx.x / kNormCols;
-  const int j = blockIdx.x * kNormCols + jj;
+  const int j0 = blockIdx.x * kNormCols;
+  const int j = j0 + jj;
   const bool valid = j < M;
 
   __shared__ float partial[kNormGroups][kNormCols];
   __shared__ float scale_s[kNormCols];
+  __shared__ __attribute__((aligned(16))) TK tile[kNormCols][R + 8];
 
+  float v[PER];
   float ss = 0.f;
-  if (valid) {
-    for (int r = rg; r < R; r += kNormGroups) {
-      const float v = static_cast<float>(src[static_cast<int64_t>(r) * M + j]);
-      ss += v * v;
-    }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int r = rg + i * kNormGroups;
+    v[i] = valid ? static_cast<float>(src[static_cast<int64_t>(r) * M + j]) : 0.f;
+    ss += v[i] * v[i];
   }
   partial[rg][jj] = ss;
   __syncthreads();
@@ -54,56 +61,62 @@ __global__ __launch_bounds__(256) void dict_normalize_kernel(
   __syncthreads();
   const float scale = scale_s[jj];
 
-  if (write_value && j < Mp) {
-    for (int r = rg; r < R; r += kNormGroups) {
-      const float v = valid ? static_cast<float>(src[static_cast<int64_t>(r) * M + j]) : 0.f;
-      value[static_cast<int64_t>(r) * Mp + j] = static_cast<Tout>(v * scale);
-    }
-  }
-  if (write_key && j < Mp) {
-    // Thread (jj, rg) writes a contiguous run of R / kNormGroups coordinates
-    // of atom j, eight at a time (R is a multiple of 64, so runs are 16B
-    // aligned and whole).
-    const int run = R / kNormGroups;
-    Tout* dst = key_t + static_cast<int64_t>(j) * R + rg * run;
-    for (int r0 = 0; r0 < run; r0 += 8) {
-      Tout buf[8];
+  if (write_value) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int r = rg * run + r0 + e;
-        const float v = valid ? static_cast<float>(src[static_cast<int64_t>(r) * M + j]) : 0.f;
-        buf[e] = static_cast<Tout>(v * scale);
-      }
-      store16B(dst + r0, *reinterpret_cast<const u32x4*>(buf));
+    for (int i = 0; i < PER; ++i) {
+      const int r = rg + i * kNormGroups;
+      value[static_cast<int64_t>(r) * Mp + j] = static_cast<_Float16>(v[i] * scale);
+    }
+  }
+  if (write_key) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) tile[jj][rg + i * kNormGroups] = static_cast<TK>(v[i] * scale);
+    __syncthreads();
+    // 32 atoms x R coordinates = 32 * R / 8 chunks of 16 bytes.
+    for (int ch = threadIdx.x; ch < kNormCols * (R / 8); ch += 256) {
+      const int a = ch / (R / 8);
+      const int r8 = (ch % (R / 8)) * 8;
+      store16B(key_t + static_cast<int64_t>(j0 + a) * R + r8, *reinterpret_cast<const u32x4*>(&tile[a][r8]));
     }
   }
 }
 
-template <typename Tin, typename Tout>
-static void launch_norm(const void* rk, const void* rv, int R, int M, int Mp, float eps, void* kt,
-                        void* v, hipStream_t s) {
+template <typename Tin, typename TK, int R>
+static void launch_norm(const void* rk, const void* rv, int M, int Mp, float eps, void* kt, void* v,
+                        hipStream_t s) {
   dim3 grid(Mp / kNormCols, rv ? 2 : 1);
-  hipLaunchKernelGGL((dict_normalize_kernel<Tin, Tout>), grid, dim3(256), 0, s,
-                     static_cast<const Tin*>(rk), static_cast<const Tin*>(rv), R, M, Mp, eps,
-                     static_cast<Tout*>(kt), static_cast<Tout*>(v));
+  hipLaunchKernelGGL((dict_normalize_kernel<Tin, TK, R>), grid, dim3(256), 0, s,
+                     static_cast<const Tin*>(rk), static_cast<const Tin*>(rv), M, Mp, eps,
+                     static_cast<TK*>(kt), static_cast<_Float16*>(v));
 }
 
-template <typename Tout>
-static void dispatch_in(int in_dtype, const void* rk, const void* rv, int R, int M, int Mp, float eps,
+template <typename Tin, typename TK>
+static void dispatch_r(int R, const void* rk, const void* rv, int M, int Mp, float eps, void* kt,
+                       void* v, hipStream_t s) {
+  switch (R) {
+    case 64: launch_norm<Tin, TK, 64>(rk, rv, M, Mp, eps, kt, v, s); break;
+    case 128: launch_norm<Tin, TK, 128>(rk, rv, M, Mp, eps, kt, v, s); break;
+    case 256: launch_norm<Tin, TK, 256>(rk, rv, M, Mp, eps, kt, v, s); break;
+    default: launch_norm<Tin, TK, 512>(rk, rv, M, Mp, eps, kt, v, s); break;
+  }
+}
+
+template <typename TK>
+static void dispatch_in(int in_dtype, int R, const void* rk, const void* rv, int M, int Mp, float eps,
                         void* kt, void* v, hipStream_t s) {
-  if (in_dtype == kF32) launch_norm<float, Tout>(rk, rv, R, M, Mp, eps, kt, v, s);
-  else if (in_dtype == kF16) launch_norm<_Float16, Tout>(rk, rv, R, M, Mp, eps, kt, v, s);
-  else launch_norm<__bf16, Tout>(rk, rv, R, M, Mp, eps, kt, v, s);
+  if (in_dtype == kF32) dispatch_r<float, TK>(R, rk, rv, M, Mp, eps, kt, v, s);
+  else if (in_dtype == kF16) dispatch_r<_Float16, TK>(R, rk, rv, M, Mp, eps, kt, v, s);
+  else dispatch_r<__bf16, TK>(R, rk, rv, M, Mp, eps, kt, v, s);
 }
 
 void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int in_dtype, int R,
-                                 int M, float eps, void* key_t, void* value, int out_dtype,
+                                 int M, float eps, void* key_t, int key_dtype, void* value,
                                  hipStream_t stream) {
-  const int Mp = round_up(M, kAtomPad);
-  if (out_dtype == kF16)
-    dispatch_in<_Float16>(in_dtype, raw_key, raw_value, R, M, Mp, eps, key_t, value, stream);
+  const int Mp = static_cast<int>(round_up(M, kAtomPad));
+  if (key_dtype == kF16)
+    dispatch_in<_Float16>(in_dtype, R, raw_key, raw_value, M, Mp, eps, key_t, value, stream);
   else
-    dispatch_in<__bf16>(in_dtype, raw_key, raw_value, R, M, Mp, eps, key_t, value, stream);
+    dispatch_in<__bf16>(in_dtype, R, raw_key, raw_value, M, Mp, eps, key_t, value, stream);
 }
 
 }  // namespace da

@@ -8,20 +8,27 @@
 // (+ bias), with both operands K-contiguous, as PyTorch stores x [N, d] and
 // Linear weights [out, in].  The query and key weights are read as two stacked
 // operands, so no concatenated weight is ever materialized.  Epilogues:
-//   mode 0: out[j, i]                      -- Q/K features (i) of token j, or the output projection
-//   mode 1: out[b, i_feature, t] (V^T)     -- value features in the token-contiguous
-//                                             layout the attention kernel streams
-// Tiles: 128 x 128 per workgroup, 64-wide K stages staged through LDS; each
-// of the four waves owns a 64 x 64 quadrant (4 x 4 MFMA 16x16x32 blocks).
+//   mode 0: out[j, i]                 -- features i of token j (Q/K projection,
+//                                        output projection)
+//   mode 1: out[b, j_feature, t] (V^T) -- value features in the token-contiguous
+//                                        layout the attention kernel streams.
+//           Rows i run over B * Tp "virtual" tokens (t < Tp, the padded
+//           length); tokens past T reuse the last real row, so the padding of
+//           V^T is always finite.
+// Tiles: 128 x 128 per workgroup, 64-wide K stages double-buffered in LDS and
+// filled by global->LDS DMA; each of the four waves owns a 64 x 64 quadrant
+// (4 x 4 MFMA 16x16x32 blocks).
 #include "da_common.h"
 #include "da_launch.h"
+#include "da_tile.h"
 
 namespace da {
 
 constexpr int kBI = 128;
 constexpr int kBJ = 128;
 constexpr int kBK = 64;
-constexpr int kGemmPad = 8;
+constexpr int kGemmNck = kBK / 8;                        // chunks per tile row
+constexpr int kGemmTileBytes = kBI * kBK * 2;            // one operand tile
 
 struct GemmSeg {
   const void* p0;
@@ -35,7 +42,7 @@ struct GemmSeg {
   void* out;
   int64_t ldo;
   int64_t T, Tp, vt_stride_b;
-  int tiles_i, tiles;   // tiles along i, total tiles of this segment
+  int tiles_i, tiles;
 };
 
 struct GemmParams {
@@ -44,30 +51,39 @@ struct GemmParams {
 };
 
 template <typename T>
-__device__ __forceinline__ void stage_operand(T* lds, const T* p0, const T* p1, int64_t split,
-                                              int64_t rows, int64_t K, int64_t r0, int k0) {
-  // 128 rows x 64 k = 1024 chunks of 8 elements; 4 per thread.
+__device__ __forceinline__ const T* p_row(const GemmSeg& sg, int64_t i) {
+  const T* p0 = static_cast<const T*>(sg.p0);
+  i = min(i, sg.I - 1);   // rows of a partial last tile are computed but never stored
+  if (sg.mode == 1) {   // virtual token i = b * Tp + t of the value segment
+    const int64_t b = i / sg.Tp;
+    const int64_t t = min(i % sg.Tp, sg.T - 1);
+    return p0 + (b * sg.T + t) * sg.K;
+  }
+  return i < sg.p_split ? p0 + i * sg.K : static_cast<const T*>(sg.p1) + (i - sg.p_split) * sg.K;
+}
+
+template <typename T>
+__device__ __forceinline__ void issue_stage(char* buf, const GemmSeg& sg, int64_t i0, int64_t j0, int k0,
+                                            int wave, int lane) {
+  const T* qq = static_cast<const T*>(sg.q);
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
-    const int ch = threadIdx.x + it * 256;
-    const int r = ch >> 3;
-    const int k8 = (ch & 7) * 8;
-    const int64_t gr = r0 + r;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (gr < rows && k0 + k8 < K) {
-      const T* src = gr < split ? p0 + gr * K : p1 + (gr - split) * K;
-      v = load16B(src + k0 + k8);
-    }
-    store16B(lds + r * (kBK + kGemmPad) + k8, v);
+    const int j = it * 4 + wave;
+    int r, ck;
+    chunk_of<kGemmNck, false>(j * 64 + lane, r, ck);
+    // Columns past K only occur in a final half stage that is never read.
+    const int kc = min(k0 + ck * 8, static_cast<int>(sg.K) - 8);
+    dma16(p_row<T>(sg, i0 + r) + kc, buf + j * 1024);
+    const int64_t jr = min(j0 + r, sg.J - 1);
+    dma16(qq + jr * sg.K + kc, buf + kGemmTileBytes + j * 1024);
   }
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   typedef typename Elem<T>::v8 v8;
-  constexpr int ROW = kBK + kGemmPad;
-  __shared__ __attribute__((aligned(16))) T as[kBI * ROW];
-  __shared__ __attribute__((aligned(16))) T bs[kBJ * ROW];
+  __shared__ __attribute__((aligned(1024))) char lds0[2 * kGemmTileBytes];
+  __shared__ __attribute__((aligned(1024))) char lds1[2 * kGemmTileBytes];
 
   int tile = blockIdx.x;
   const int si = (prm.nseg > 1 && tile >= prm.seg[0].tiles) ? 1 : 0;
@@ -79,8 +95,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   const int lane = lane_id();
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int wi = wave_id() & 1;
-  const int wj = wave_id() >> 1;
+  const int wave = uniform_wave();
+  const int wi = wave & 1;
+  const int wj = wave >> 1;
+  const int K = static_cast<int>(sg.K);
+  const int n_stages = (K + kBK - 1) / kBK;
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -88,28 +107,33 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = zero4();
 
-  const T* p0 = static_cast<const T*>(sg.p0);
-  const T* p1 = static_cast<const T*>(sg.p1 ? sg.p1 : sg.p0);
-  const T* qq = static_cast<const T*>(sg.q);
-
-  for (int k0 = 0; k0 < sg.K; k0 += kBK) {
+  auto step = [&](int st, char* cur, char* nxt) {
+    wait_vmem();
     __syncthreads();
-    stage_operand<T>(as, p0, p1, sg.p_split, sg.I, sg.K, i0, k0);
-    stage_operand<T>(bs, qq, qq, sg.J, sg.J, sg.K, j0, k0);
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < kBK / 32; ++kk) {
+    if (st + 1 < n_stages) issue_stage<T>(nxt, sg, i0, j0, (st + 1) * kBK, wave, lane);
+    const int ksteps = min(kBK, K - st * kBK) / 32;
+    for (int kk = 0; kk < ksteps; ++kk) {
       v8 af[4], bf[4];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) af[a] = load8(&as[(wi * 64 + a * 16 + c) * ROW + kk * 32 + 8 * g]);
+      for (int a = 0; a < 4; ++a)
+        af[a] = as_v8<T>(lds_chunk<kGemmNck, false>(cur, wi * 64 + a * 16 + c, kk * 4 + g));
 #pragma unroll
-      for (int b = 0; b < 4; ++b) bf[b] = load8(&bs[(wj * 64 + b * 16 + c) * ROW + kk * 32 + 8 * g]);
+      for (int b = 0; b < 4; ++b)
+        bf[b] = as_v8<T>(lds_chunk<kGemmNck, false>(cur + kGemmTileBytes, wj * 64 + b * 16 + c, kk * 4 + g));
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = Elem<T>::mma(af[a], bf[b], acc[a][b]);
     }
+  };
+
+  issue_stage<T>(lds0, sg, i0, j0, 0, wave, lane);
+  int st = 0;
+  for (; st + 1 < n_stages; st += 2) {
+    step(st, lds0, lds1);
+    step(st + 1, lds1, lds0);
   }
+  if (st < n_stages) step(st, lds0, lds1);
 
   // Epilogue: lane holds D[i0 + wi*64 + a*16 + 4g + r][j0 + wj*64 + b*16 + c], r = 0..3.
   T* out = static_cast<T*>(sg.out);
@@ -122,39 +146,25 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     for (int a = 0; a < 4; ++a) {
       const int64_t i = i0 + wi * 64 + a * 16 + 4 * g;
       if (i >= sg.I) continue;
-      float v[4];
+      typename Elem<T>::v4 o;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float bi = 0.f;
         if (sg.mode == 0 && sg.bias && i + r < sg.I) bi = load_scalar(sg.bias, sg.bias_dtype, i + r);
-        v[r] = acc[a][b][r] + bi + bj;
+        o[r] = static_cast<T>(acc[a][b][r] + bi + bj);
       }
       if (sg.mode == 0) {
         T* dst = out + j * sg.ldo + i;
         if (i + 4 <= sg.I) {
-          typename Elem<T>::v4 o;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = static_cast<T>(v[r]);
           *reinterpret_cast<typename Elem<T>::v4*>(dst) = o;
         } else {
-          for (int r = 0; r < 4 && i + r < sg.I; ++r) dst[r] = static_cast<T>(v[r]);
+          for (int r = 0; r < 4 && i + r < sg.I; ++r) dst[r] = o[r];
         }
       } else {
-        // i indexes tokens n = b*T + t, j indexes value features.
-        const int64_t bb = i / sg.T;
-        const int64_t t = i % sg.T;
-        T* dst = out + bb * sg.vt_stride_b + j * sg.Tp + t;
-        if (i + 4 <= sg.I && t + 4 <= sg.T && (sg.T % 4) == 0) {
-          typename Elem<T>::v4 o;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = static_cast<T>(v[r]);
-          *reinterpret_cast<typename Elem<T>::v4*>(dst) = o;
-        } else {
-          for (int r = 0; r < 4 && i + r < sg.I; ++r) {
-            const int64_t n = i + r;
-            out[(n / sg.T) * sg.vt_stride_b + j * sg.Tp + (n % sg.T)] = static_cast<T>(v[r]);
-          }
-        }
+        // Four consecutive virtual tokens of one sequence (Tp % 64 == 0).
+        const int64_t bb = i / sg.Tp;
+        const int64_t t = i % sg.Tp;
+        *reinterpret_cast<typename Elem<T>::v4*>(out + bb * sg.vt_stride_b + j * sg.Tp + t) = o;
       }
     }
   }
@@ -168,21 +178,22 @@ void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t strea
     GemmSeg& d = prm.seg[s];
     const GemmSegment& a = segs[s];
     d.p0 = a.p0;
-    d.p1 = a.p1;
+    d.p1 = a.p1 ? a.p1 : a.p0;
     d.p_split = a.p1 ? a.p_split : a.I;
     d.q = a.q;
-    d.I = a.I;
+    d.mode = a.mode;
+    d.T = a.T > 0 ? a.T : 1;
+    d.Tp = a.Tp > 0 ? a.Tp : 1;
+    // The value segment runs over B * Tp virtual tokens (a.I = B * T real ones).
+    d.I = a.mode == 1 ? (a.I / d.T) * d.Tp : a.I;
     d.J = a.J;
     d.K = a.K;
     d.bias = a.bias;
     d.bias_dtype = a.bias_dtype;
-    d.mode = a.mode;
     d.out = a.out;
     d.ldo = a.ldo;
-    d.T = a.T > 0 ? a.T : 1;
-    d.Tp = a.Tp;
     d.vt_stride_b = a.vt_stride_b;
-    d.tiles_i = static_cast<int>((a.I + kBI - 1) / kBI);
+    d.tiles_i = static_cast<int>((d.I + kBI - 1) / kBI);
     d.tiles = d.tiles_i * static_cast<int>((a.J + kBJ - 1) / kBJ);
     total += d.tiles;
   }

@@ -38,7 +38,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -84,10 +84,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_last_error": (ctypes.c_char_p, []),
     "da_padded_atoms": (_i64, [_i64]),
     "da_padded_length": (_i64, [_i64]),
-    "da_dictionary_normalize": (_i32, [_vp, _vp, _i32, _i64, _i64, _f32, _vp, _vp, _i32, _vp]),
+    "da_dictionary_normalize": (_i32, [_vp, _vp, _i32, _i64, _i64, _f32, _vp, _i32, _vp, _vp]),
     "da_dictionary_route": (
         _i32,
-        [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _f32, _f32, _i32, _i32, _vp, _i64, _vp],
+        [
+            _vp, _i64, _i64, _i64, _i32,  # x, rows, routing_dim, row pitch, x dtype
+            _vp, _i32, _vp, _i64,  # key_t, key dtype, value, atoms
+            _vp, _i32, _f32, _f32, _i32,  # beta, beta dtype, beta value, eps, flags
+            _vp, _i64, _i32, _vp,  # out, out pitch, out dtype, stream
+        ],
     ),
     "da_routed_attention": (
         _i32,
@@ -96,7 +101,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i64, _i64,  # value_t and pitches
             _i64, _i64, _i64, _i64,  # batch, maps, length, value_dim
             _vp, _i32, _f32, _vp, _i32,  # scales, mix logits
-            _i32, _i32, _vp, _i64, _i64, _i64, _vp,  # flags, dtype, out + strides, stream
+            _i32, _i32, _i32, _vp, _i64, _i64, _i64, _vp,  # flags, qk/v dtypes, out + strides, stream
         ],
     ),
     "da_qkv_projection": (

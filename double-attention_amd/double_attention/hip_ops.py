@@ -79,8 +79,10 @@ def _ptr(t: Tensor | None) -> int | None:
 class RouteDictionary(NamedTuple):
     """A normalized bank in the layouts the route kernel reads.
 
-    ``key_t`` is ``[Mp, R]`` (atom-major), ``value`` is ``[R, Mp]``; atoms past
-    ``atoms`` are zero.  ``Mp`` is ``atoms`` rounded up to a multiple of 64.
+    ``key_t`` is ``[Mp, R]`` (atom-major) in the key dtype, ``value`` is
+    ``[R, Mp]`` in fp16; atoms past ``atoms`` are zero.  ``Mp`` is ``atoms``
+    rounded up to a multiple of 64.  Normalized atoms are bounded by one, so
+    fp16 holds them with eight times finer rounding than bf16.
     """
 
     key_t: Tensor
@@ -94,17 +96,24 @@ def _tag(key: Tensor, value: Tensor, layout: RouteDictionary) -> tuple[Tensor, T
     return key, value
 
 
+def route_key_dtype(normalize_input: bool, dtype: torch.dtype) -> torch.dtype:
+    """Key-atom dtype the route uses: fp16 for unit (normalized) inputs, else the input dtype."""
+
+    return torch.float16 if normalize_input else dtype
+
+
 def dictionary_normalize_hip(
     raw_key: Tensor,
     raw_value: Tensor | None,
     eps: float = 1e-6,
-    dtype: torch.dtype | None = None,
+    key_dtype: torch.dtype = torch.float16,
 ) -> tuple[Tensor, Tensor]:
     """Column-normalize a bank in one launch; returns ``(key, value)`` as ``[R, M]``.
 
-    The returned tensors are views of the route layouts (so handing them back
-    to the route costs no copy); for a tied bank both views read the same
-    normalized atoms.  Matches ``F.normalize(raw, dim=0, eps=eps)``.
+    Matches ``F.normalize(raw, dim=0, eps=eps)``.  The returned tensors are
+    views of the route layouts -- ``key`` in ``key_dtype``, ``value`` in fp16
+    -- so handing them back to the route costs no copy; for a tied bank both
+    views hold the same normalized atoms.
     """
 
     if raw_key.ndim != 2:
@@ -112,13 +121,12 @@ def dictionary_normalize_hip(
     if raw_value is not None and raw_value.shape != raw_key.shape:
         raise ValueError("raw_value must match raw_key")
     _require_cuda(raw_key, *(() if raw_value is None else (raw_value,)))
-    dtype = dtype or raw_key.dtype
     routing_dim, atoms = raw_key.shape
     if routing_dim not in SUPPORTED_WIDTHS:
         raise NotImplementedError(f"HIP route supports routing_dim in {SUPPORTED_WIDTHS}, got {routing_dim}")
     padded = _round_up(atoms, ATOM_PAD)
-    key_t = torch.empty(padded, routing_dim, dtype=dtype, device=raw_key.device)
-    value = torch.empty(routing_dim, padded, dtype=dtype, device=raw_key.device)
+    key_t = torch.empty(padded, routing_dim, dtype=key_dtype, device=raw_key.device)
+    value = torch.empty(routing_dim, padded, dtype=torch.float16, device=raw_key.device)
     raw_key_c = raw_key.detach().contiguous()
     raw_value_c = None if raw_value is None else raw_value.detach().to(raw_key.dtype).contiguous()
     lib = _lib.get()
@@ -131,8 +139,8 @@ def dictionary_normalize_hip(
             atoms,
             float(eps),
             key_t.data_ptr(),
+            _half_code(key_dtype),
             value.data_ptr(),
-            _half_code(dtype),
             _stream(raw_key.device),
         ),
         "dictionary_normalize_hip",
@@ -141,22 +149,22 @@ def dictionary_normalize_hip(
     return _tag(key_t[:atoms].t(), value[:, :atoms], layout)
 
 
-def route_layout(dictionary_key: Tensor, dictionary_value: Tensor, dtype: torch.dtype) -> RouteDictionary:
+def route_layout(dictionary_key: Tensor, dictionary_value: Tensor, key_dtype: torch.dtype) -> RouteDictionary:
     """Route layouts for a normalized ``[R, M]`` key/value pair (copy-free when tagged)."""
 
     layout = getattr(dictionary_key, "_da_route_layout", None)
     if (
         layout is not None
         and getattr(dictionary_value, "_da_route_layout", None) is layout
-        and layout.key_t.dtype == dtype
+        and layout.key_t.dtype == key_dtype
     ):
         return layout
     if dictionary_key.ndim != 2 or dictionary_value.shape != dictionary_key.shape:
         raise ValueError("dictionary key and value must both be [routing_dim, atoms]")
     routing_dim, atoms = dictionary_key.shape
     padded = _round_up(atoms, ATOM_PAD)
-    key_t = torch.zeros(padded, routing_dim, dtype=dtype, device=dictionary_key.device)
-    value = torch.zeros(routing_dim, padded, dtype=dtype, device=dictionary_key.device)
+    key_t = torch.zeros(padded, routing_dim, dtype=key_dtype, device=dictionary_key.device)
+    value = torch.zeros(routing_dim, padded, dtype=torch.float16, device=dictionary_key.device)
     key_t[:atoms].copy_(dictionary_key.detach().t())
     value[:, :atoms].copy_(dictionary_value.detach())
     return RouteDictionary(key_t, value, atoms)
@@ -191,9 +199,9 @@ def _route_forward(
         raise ValueError("input width does not match the dictionary routing_dim")
     if routing_dim not in SUPPORTED_WIDTHS:
         raise NotImplementedError(f"HIP route supports routing_dim in {SUPPORTED_WIDTHS}, got {routing_dim}")
-    if x.dtype != layout.key_t.dtype:
-        raise ValueError("input and dictionary must have one matching dtype")
     rows_view = x.reshape(-1, routing_dim)
+    if rows_view.shape[0] == 0:
+        return torch.empty(x.shape, dtype=x.dtype, device=x.device)
     if rows_view.stride(-1) != 1 or rows_view.stride(0) % 8 or rows_view.data_ptr() % 16:
         rows_view = rows_view.contiguous()
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
@@ -216,7 +224,9 @@ def _route_forward(
             rows_view.shape[0],
             routing_dim,
             rows_view.stride(0),
+            _half_code(x.dtype),
             layout.key_t.data_ptr(),
+            _half_code(layout.key_t.dtype),
             layout.value.data_ptr(),
             layout.atoms,
             beta_ptr,
@@ -224,9 +234,9 @@ def _route_forward(
             beta_value,
             float(eps),
             flags,
-            _half_code(x.dtype),
             out.data_ptr(),
             routing_dim,
+            _half_code(x.dtype),
             _stream(x.device),
         ),
         "dictionary_route_hip",
@@ -238,7 +248,7 @@ def _route_forward(
 class _RouteFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output):  # type: ignore[override]
-        layout = route_layout(dictionary_key, dictionary_value, x.dtype)
+        layout = route_layout(dictionary_key, dictionary_value, route_key_dtype(normalize_input, x.dtype))
         ctx.save_for_backward(x, dictionary_key, dictionary_value, *(beta,) if isinstance(beta, Tensor) else ())
         ctx.beta_is_tensor = isinstance(beta, Tensor)
         ctx.beta = None if ctx.beta_is_tensor else beta
@@ -291,14 +301,16 @@ def dictionary_route_hip(
     del silu_gain, standardized_logit_scale
     _check_route_variant(silu_logits, direct_silu, standardize_logits)
     _require_cuda(input, dictionary_key, dictionary_value)
-    if dictionary_key.dtype != input.dtype or dictionary_value.dtype != input.dtype:
+    _half_code(input.dtype)
+    tagged = getattr(dictionary_key, "_da_route_layout", None) is not None
+    if not tagged and (dictionary_key.dtype != input.dtype or dictionary_value.dtype != input.dtype):
         raise ValueError("input and dictionaries must have one matching dtype")
     needs_grad = torch.is_grad_enabled() and any(
         t.requires_grad for t in (input, dictionary_key, dictionary_value, *((beta,) if isinstance(beta, Tensor) else ()))
     )
     if needs_grad:
         return _RouteFunction.apply(input, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output)
-    layout = route_layout(dictionary_key, dictionary_value, input.dtype)
+    layout = route_layout(dictionary_key, dictionary_value, route_key_dtype(normalize_input, input.dtype))
     return _route_forward(input, layout, beta, eps, normalize_input, normalize_output)
 
 
@@ -349,7 +361,7 @@ def _attention_forward(query: Tensor, key: Tensor, value: Tensor, scales: Tensor
             batch, maps, length, value_width,
             scales_c.data_ptr(), dtype_code(scales_c.dtype), 1.0, None, _lib.DA_F32,
             _lib.DA_ATTN_CAUSAL if causal else 0,
-            _half_code(value.dtype),
+            _half_code(q.dtype), _half_code(value.dtype),
             out.data_ptr(), out.stride(0), out.stride(2), out.stride(1),
             _stream(value.device),
         ),
@@ -393,9 +405,10 @@ def routed_attention_hip(
     if scales.shape != (query.shape[1],):
         raise ValueError(f"scales must have shape [{query.shape[1]}]")
     _require_cuda(query, key, value, scales)
-    if query.dtype != key.dtype or query.dtype != value.dtype:
-        raise ValueError("query, key, and value must have one matching dtype")
+    if query.dtype != key.dtype or query.dtype not in (value.dtype, torch.float16):
+        raise ValueError("query, key, and value must have one matching dtype (or fp16 query/key)")
     _half_code(query.dtype)
+    _half_code(value.dtype)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value, scales)):
         return _AttentionFunction.apply(query, key, value, scales, causal)
     return _attention_forward(query, key, value, scales, causal)
@@ -462,7 +475,7 @@ def qkv_projection_hip(
 
 class HipForwardResult(NamedTuple):
     output: Tensor
-    routed: Tensor   # [B, T, 2, H, R]: routed query branches, then key branches
+    routed: Tensor   # [B, T, 2, H, R] fp16: routed query branches, then key branches
 
 
 def check_module_supported(config) -> None:
@@ -496,6 +509,8 @@ def shared_dictionary_attention_hip(
     config = module.config
     batch, length, model_dim = x.shape
     code = _half_code(dtype)
+    if layout.key_t.dtype != route_key_dtype(config.normalize_routing_input, dtype):
+        raise ValueError("route dictionary key dtype does not match the configuration")
 
     def cast(t: Tensor | None) -> Tensor | None:
         if t is None:
@@ -541,8 +556,10 @@ def shared_dictionary_attention_hip(
         workspace.data_ptr(), ws_bytes, out.data_ptr(),
     )
     _lib.check(lib.da_shared_dictionary_attention_forward(args, _stream(x.device)), "shared_dictionary_attention_hip")
-    routed_bytes = batch * length * 2 * width * xc.element_size()
-    routed = workspace[:routed_bytes].view(dtype).view(batch, length, 2, config.qk_branches, config.routing_dim)
+    routed_bytes = batch * length * 2 * width * 2
+    routed = workspace[:routed_bytes].view(torch.float16).view(
+        batch, length, 2, config.qk_branches, config.routing_dim
+    )
     return HipForwardResult(out, routed)
 
 
@@ -552,6 +569,7 @@ __all__ = [
     "dictionary_route_hip",
     "linear_hip",
     "qkv_projection_hip",
+    "route_key_dtype",
     "route_layout",
     "routed_attention_hip",
     "shared_dictionary_attention_hip",

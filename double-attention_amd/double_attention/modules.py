@@ -60,16 +60,17 @@ class SharedDictionaryBank(nn.Module):
         value = key if self.raw_value is None else F.normalize(self.raw_value, dim=0, eps=eps)
         return key, value
 
-    def normalized_hip(self, eps: float = 1e-6, dtype: torch.dtype | None = None) -> tuple[Tensor, Tensor]:
+    def normalized_hip(self, eps: float = 1e-6, key_dtype: torch.dtype = torch.float16) -> tuple[Tensor, Tensor]:
         """``normalized`` computed by the gfx950 kernel, in the route layouts.
 
         One launch covers both banks of an untied dictionary.  The returned
-        ``[R, M]`` tensors are views that the HIP route reads without a copy.
+        ``[R, M]`` tensors are views that the HIP route reads without a copy
+        (key atoms in ``key_dtype``, value atoms in fp16).
         """
 
         from .hip_ops import dictionary_normalize_hip
 
-        return dictionary_normalize_hip(self.raw_key, self.raw_value, eps, dtype)
+        return dictionary_normalize_hip(self.raw_key, self.raw_value, eps, key_dtype)
 
     def extra_repr(self) -> str:
         return (
@@ -255,17 +256,20 @@ class SharedDictionaryAttention(nn.Module):
         )
         if needs_grad:
             return _HipModuleFunction.run(self, x, bank, normalized_dictionary, dtype, return_aux)
+        key_dtype = hip_ops.route_key_dtype(self.config.normalize_routing_input, dtype)
         if normalized_dictionary is None:
-            layout = hip_ops.route_layout(*bank.normalized_hip(eps, dtype), dtype)
+            layout = hip_ops.route_layout(*bank.normalized_hip(eps, key_dtype), key_dtype)
         else:
-            layout = hip_ops.route_layout(*normalized_dictionary, dtype)
+            layout = hip_ops.route_layout(*normalized_dictionary, key_dtype)
         result = hip_ops.shared_dictionary_attention_hip(self, x, layout, dtype)
         if not return_aux:
             return result.output
-        return result.output, self._hip_aux(result.routed)
+        return result.output, self._hip_aux(result.routed, dtype)
 
-    def _hip_aux(self, routed: Tensor) -> DoubleAttentionAux:
-        # routed: [B, T, 2, H, R] -> [B, H, T, R] views for queries and keys.
+    def _hip_aux(self, routed: Tensor, dtype: torch.dtype) -> DoubleAttentionAux:
+        # routed: [B, T, 2, H, R] (fp16) -> [B, H, T, R] for queries and keys,
+        # in the activation dtype like the PyTorch path's aux tensors.
+        routed = routed.to(dtype)
         routed_query = routed[:, :, 0].permute(0, 2, 1, 3)
         routed_key = routed[:, :, 1].permute(0, 2, 1, 3)
         score_query, score_key = assemble_score_maps(routed_query, routed_key, self.config.outer_maps)
@@ -346,9 +350,10 @@ class _HipModuleFunction(torch.autograd.Function):
         with torch.no_grad():
             from . import hip_ops
 
-            layout = hip_ops.route_layout(dictionary[0], dictionary[1], dtype)
+            key_dtype = hip_ops.route_key_dtype(module.config.normalize_routing_input, dtype)
+            layout = hip_ops.route_layout(dictionary[0], dictionary[1], key_dtype)
             routed = hip_ops.shared_dictionary_attention_hip(module, x, layout, dtype).routed
-        return out, module._hip_aux(routed)
+        return out, module._hip_aux(routed, dtype)
 
     @staticmethod
     def forward(ctx, module, dtype, x, dictionary_key, dictionary_value, *params):  # type: ignore[override]
@@ -358,7 +363,8 @@ class _HipModuleFunction(torch.autograd.Function):
         ctx.dtype = dtype
         ctx.autocast = x.is_cuda and torch.is_autocast_enabled("cuda")
         ctx.save_for_backward(x, dictionary_key, dictionary_value, *params)
-        layout = hip_ops.route_layout(dictionary_key, dictionary_value, dtype)
+        key_dtype = hip_ops.route_key_dtype(module.config.normalize_routing_input, dtype)
+        layout = hip_ops.route_layout(dictionary_key, dictionary_value, key_dtype)
         return hip_ops.shared_dictionary_attention_hip(module, x, layout, dtype).output
 
     @staticmethod
@@ -476,7 +482,8 @@ class DoubleAttentionStack(nn.Module):
                 from . import hip_ops
 
                 hip_ops.check_module_supported(cfg)
-                return tuple(bank.normalized_hip(cfg.eps, dtype) for bank in self.banks)
+                key_dtype = hip_ops.route_key_dtype(cfg.normalize_routing_input, dtype)
+                return tuple(bank.normalized_hip(cfg.eps, key_dtype) for bank in self.banks)
         return tuple(bank.normalized(cfg.eps) for bank in self.banks)
 
     def forward(self, x: Tensor) -> Tensor:

@@ -81,29 +81,33 @@ int64_t da_padded_length(int64_t length);
  * Column-normalize one dictionary bank (modules.py:45-48).
  *   raw_key, raw_value: [routing_dim, atoms] row-major, dtype raw_dtype
  *                       (raw_value NULL = tied bank: key atoms serve both roles)
- *   key_t:  out [da_padded_atoms(atoms), routing_dim]   atom-major
- *   value:  out [routing_dim, da_padded_atoms(atoms)]   coordinate-major
+ *   key_t:  out [da_padded_atoms(atoms), routing_dim]   atom-major, key_dtype
+ *   value:  out [routing_dim, da_padded_atoms(atoms)]   coordinate-major, fp16
  * Atom j becomes raw[:, j] / max(||raw[:, j]||, eps); padding atoms are zero.
- * routing_dim must be 64, 128, 256 or 512; out_dtype DA_F16 or DA_BF16.
+ * routing_dim must be 64, 128, 256 or 512; key_dtype DA_F16 or DA_BF16.
  */
 int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_dtype,
                             int64_t routing_dim, int64_t atoms, float eps, void* key_t,
-                            void* value, int out_dtype, da_stream_t stream);
+                            int key_dtype, void* value, da_stream_t stream);
 
 /*
  * Fused dictionary route (ops.py:16-62 with identity activation and softmax
  * assignment), for any number of rows:
  *   z = N_out( sum_j softmax_j(beta <N_in(x), Dk_j>) Dv_j )
- *   x:   rows x routing_dim, row pitch x_row_stride (elements)
- *   key_t, value: the layouts written by da_dictionary_normalize
+ *   x:   rows x routing_dim, row pitch x_row_stride (elements), x_dtype
+ *   key_t (key_dtype), value (fp16): the layouts of da_dictionary_normalize.
+ *        key_dtype is DA_F16, or x_dtype; without DA_ROUTE_NORMALIZE_INPUT it
+ *        must equal x_dtype (raw rows are not range-limited).
  *   beta: device scalar of beta_dtype, or NULL to use beta_value
- *   out: rows x routing_dim, row pitch out_row_stride (may alias x when the
- *        pitches match: each row is read completely before it is written)
+ *   out: rows x routing_dim, row pitch out_row_stride, out_dtype (DA_F16 or
+ *        x_dtype); may alias x when the pitches match (each row is read
+ *        completely before it is written).  A DA_F16 x needs DA_F16 keys and out.
  */
 int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_t x_row_stride,
-                        const void* key_t, const void* value, int64_t atoms, const void* beta,
-                        int beta_dtype, float beta_value, float eps, int flags, int dtype,
-                        void* out, int64_t out_row_stride, da_stream_t stream);
+                        int x_dtype, const void* key_t, int key_dtype, const void* value,
+                        int64_t atoms, const void* beta, int beta_dtype, float beta_value,
+                        float eps, int flags, void* out, int64_t out_row_stride, int out_dtype,
+                        da_stream_t stream);
 
 /*
  * Flash outer attention over `maps` score maps (ops.py:65-93) with the map
@@ -118,16 +122,19 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  *   DA_ATTN_MIX: out(b, t) = sum_s alpha_s O_s(b, t), alpha = softmax(mix_logits)
  *     (uniform 1/maps if mix_logits is NULL); else O_s(b, t) goes to
  *     out + b*out_stride_b + t*out_stride_t + s*out_stride_s.
- * score_dim and value_dim must be 64, 128, 256 or 512.
+ * score_dim and value_dim must be 64, 128, 256 or 512.  Element types:
+ *   (qk_dtype, v_dtype) in {(F16, BF16), (F16, F16), (BF16, BF16)}; the output
+ *   has v_dtype.  V^T padding columns (tokens length..vt_stride_d-1) must hold
+ *   finite values.
  */
 int da_routed_attention(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
                         int64_t map_stride, int64_t map_repeat, int64_t score_dim,
                         const void* value_t, int64_t vt_stride_b, int64_t vt_stride_d,
                         int64_t batch, int64_t maps, int64_t length, int64_t value_dim,
                         const void* scales, int scales_dtype, float scale_mult,
-                        const void* mix_logits, int mix_dtype, int flags, int dtype, void* out,
-                        int64_t out_stride_b, int64_t out_stride_t, int64_t out_stride_s,
-                        da_stream_t stream);
+                        const void* mix_logits, int mix_dtype, int flags, int qk_dtype,
+                        int v_dtype, void* out, int64_t out_stride_b, int64_t out_stride_t,
+                        int64_t out_stride_s, da_stream_t stream);
 
 /*
  * Q/K and V projections in one launch (modules.py:143-157 and 212):
@@ -135,7 +142,8 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
  *   value_t[b, f, t]            = (x @ wv^T + bv)[b*length + t, f]
  *   x: [tokens, model_dim] with tokens = batch*length; wq, wk: [qk_width, model_dim];
  *   wv: [value_dim, model_dim]; bv: [value_dim] of bias_dtype or NULL.
- *   value_t pitch: vt_stride_b per sequence, vt_pitch per feature row.
+ *   value_t pitch: vt_stride_b per sequence, vt_pitch = da_padded_length(length)
+ *   per feature row; the padding tokens are filled with finite values.
  */
 int da_qkv_projection(const void* x, int64_t tokens, int64_t model_dim, int64_t length,
                       const void* wq, const void* wk, int64_t qk_width, const void* wv,
@@ -172,7 +180,7 @@ typedef struct da_sda_forward_args {
 } da_sda_forward_args;
 
 /* Workspace layout (byte offsets, each 256-aligned):
- *   routed [tokens, 2*qk_width]   Q/K projections, routed in place
+ *   routed [tokens, 2*qk_width]   Q/K projections, routed in place (fp16 out)
  *   value_t [batch, model_dim, da_padded_length(length)]
  *   mixed  [tokens, model_dim or maps*model_dim] (only with an output projection) */
 int64_t da_sda_workspace_bytes(int64_t batch, int64_t length, int64_t model_dim,

@@ -49,7 +49,10 @@ def _fake(addr: int = 1 << 20) -> int:
     ("kwargs", "code", "pattern"),
     [
         ({"routing_dim": 96}, -2, "routing_dim 96"),
-        ({"dtype": lib.DA_F32}, -1, "dtype"),
+        ({"x_dtype": lib.DA_F32}, -1, "element types"),
+        ({"flags": 2, "key_dtype": lib.DA_F16}, -2, "without input normalization"),
+        ({"x_dtype": lib.DA_F16, "out_dtype": lib.DA_BF16}, -2, "out_dtype"),
+        ({"x": 0, "rows": 0}, 0, "^$"),
         ({"x_row_stride": 100}, -3, "row strides"),
         ({"x": 0}, -1, "null pointer"),
         ({"x": (1 << 20) + 2}, -3, "16-byte aligned"),
@@ -59,9 +62,10 @@ def _fake(addr: int = 1 << 20) -> int:
 def test_route_rejects_bad_arguments_before_launch(kwargs, code, pattern) -> None:
     h = lib.get()
     args = dict(
-        x=_fake(), rows=16, routing_dim=128, x_row_stride=128, key_t=_fake(), value=_fake(),
-        atoms=512, beta=None, beta_dtype=lib.DA_F32, beta_value=4.0, eps=1e-6, flags=3,
-        dtype=lib.DA_BF16, out=_fake(), out_row_stride=128, stream=None,
+        x=_fake(), rows=16, routing_dim=128, x_row_stride=128, x_dtype=lib.DA_BF16,
+        key_t=_fake(), key_dtype=lib.DA_F16, value=_fake(), atoms=512,
+        beta=None, beta_dtype=lib.DA_F32, beta_value=4.0, eps=1e-6, flags=3,
+        out=_fake(), out_row_stride=128, out_dtype=lib.DA_F16, stream=None,
     )
     args.update(kwargs)
     rc = h.da_dictionary_route(*args.values())
@@ -76,8 +80,11 @@ def test_attention_rejects_bad_arguments_before_launch() -> None:
         _fake(), 512 * 512, 512,  # value_t pitches
         1, 1, 512, 512,  # batch, maps, length, value dim
         _fake(), lib.DA_F32, 1.0, None, lib.DA_F32,
-        lib.DA_ATTN_CAUSAL, lib.DA_BF16, _fake(), 512 * 512, 512, 0, None,
+        lib.DA_ATTN_CAUSAL, lib.DA_F16, lib.DA_BF16, _fake(), 512 * 512, 512, 0, None,
     ]
+    bad_types = list(base)
+    bad_types[20], bad_types[21] = lib.DA_BF16, lib.DA_F16
+    assert h.da_routed_attention(*bad_types) == -2
     bad_dim = list(base)
     bad_dim[6] = 384
     assert h.da_routed_attention(*bad_dim) == -2

@@ -65,14 +65,16 @@ def unit_columns(r, m, dtype, device, seed):
 # ---------------------------------------------------------------- dictionary normalization
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("key_dtype", DTYPES)
+@pytest.mark.parametrize("raw_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize(("routing_dim", "atoms", "tied"), [(64, 100, False), (256, 512, True), (512, 1536, False)])
-def test_dictionary_normalize(dtype, routing_dim, atoms, tied) -> None:
+def test_dictionary_normalize(key_dtype, raw_dtype, routing_dim, atoms, tied) -> None:
     device = _device()
     g = torch.Generator().manual_seed(routing_dim + atoms)
-    raw_key = (torch.randn(routing_dim, atoms, generator=g) * 0.1).to(device)
-    raw_value = None if tied else (torch.randn(routing_dim, atoms, generator=g) * 3).to(device)
-    key, value = da.dictionary_normalize_hip(raw_key, raw_value, 1e-6, dtype)
+    raw_key = (torch.randn(routing_dim, atoms, generator=g) * 0.1).to(device, raw_dtype)
+    raw_value = None if tied else (torch.randn(routing_dim, atoms, generator=g) * 3).to(device, raw_dtype)
+    key, value = da.dictionary_normalize_hip(raw_key, raw_value, 1e-6, key_dtype)
+    assert key.dtype == key_dtype and value.dtype == torch.float16
     torch.cuda.synchronize()
     ek, ev = oracle.bank_normalized(np32(raw_key), None if tied else np32(raw_value))
     assert_parity(key, ek, 4e-3, 4e-3, "norm key")
@@ -227,7 +229,16 @@ def build_module(preset: str, dtype: torch.dtype, seed: int, **overrides):
     return module
 
 
-def run_module_case(preset, shape, dtype=torch.bfloat16, seed=0, **overrides):
+def run_module_case(preset, shape, dtype=torch.bfloat16, seed=0, relative_to_torch=False, **overrides):
+    """HIP module forward vs the fp32 oracle.
+
+    With ``relative_to_torch`` the bar is also met if the HIP path is no
+    further from fp32 than the same bf16/fp16 module on the PyTorch path
+    (the reference's own low-precision numerics).  That is the bar for the
+    ablation presets that skip the input normalization: there the routing
+    logits are |q| (about 9) times larger, so the 16-bit rounding of the
+    projections that both paths share is amplified past 5e-3.
+    """
     module = build_module(preset, dtype, seed, **overrides)
     g = torch.Generator().manual_seed(seed + 1)
     x = torch.randn(*shape, generator=g).to("cuda", dtype)
@@ -237,9 +248,21 @@ def run_module_case(preset, shape, dtype=torch.bfloat16, seed=0, **overrides):
     params = oracle_params(module)
     expected, rq, rk = oracle.shared_dictionary_attention(params, module.config, np32(x), return_routed=True)
     label = f"{preset} {tuple(shape)} {dtype} {overrides}"
-    assert_parity(out, expected, label=label)
-    assert_parity(aux.routing_query, rq, label=label + " routed q")
-    assert_parity(aux.routing_key, rk, label=label + " routed k")
+    bars = {}
+    if relative_to_torch:
+        reference = da.SharedDictionaryAttention(module.config.with_updates(backend="torch")).to("cuda", dtype).eval()
+        reference.load_state_dict(module.state_dict())
+        with torch.inference_mode():
+            ref_out, ref_aux = reference(x, return_aux=True)
+        for name, got, exp in (("out", ref_out, expected), ("q", ref_aux.routing_query, rq), ("k", ref_aux.routing_key, rk)):
+            e = exp.astype(np.float64)
+            rel = np.linalg.norm(np32(got) - e) / np.linalg.norm(e)
+            mx = np.abs(np32(got) - e).max()
+            print(f"[parity] {label} torch path {name} rel_l2={rel:.3e} max_abs={mx:.3e}", flush=True)
+            bars[name] = (max(REL_L2, 1.1 * rel), max(MAX_ABS, 1.1 * mx))
+    assert_parity(out, expected, *bars.get("out", (REL_L2, MAX_ABS)), label=label)
+    assert_parity(aux.routing_query, rq, *bars.get("q", (REL_L2, MAX_ABS)), label=label + " routed q")
+    assert_parity(aux.routing_key, rk, *bars.get("k", (REL_L2, MAX_ABS)), label=label + " routed k")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -273,8 +296,9 @@ def test_module_c5_long_context() -> None:
     ("a1-r512-d512", {}),
 ])
 def test_module_variants_odd_shapes(preset, overrides) -> None:
-    run_module_case(preset, (2, 33, 512), seed=3, **overrides)
-    run_module_case(preset, (1, 1, 512), seed=4, **overrides)
+    relative = preset in ("a1-no-qnorm", "a1-no-norm")
+    run_module_case(preset, (2, 33, 512), seed=3, relative_to_torch=relative, **overrides)
+    run_module_case(preset, (1, 1, 512), seed=4, relative_to_torch=relative, **overrides)
 
 
 @pytest.mark.parametrize("name", ["a1_hip", "qk2_s2_hip"])
@@ -303,9 +327,21 @@ def test_lm_c4_qk2_s2_tied() -> None:
     ids = torch.randint(0, 2048, (64, 64), generator=g)
     with torch.inference_mode():
         logits, _ = model(ids.to(device))
+        # The same bf16 model on the PyTorch path: the reference's own bf16 numerics.
+        torch_model = da.DoubleAttentionLM(
+            2048, 64, config.with_updates(backend="torch"), 6, dictionary_group_size=6, feedforward_dim=1536
+        ).to(device=device, dtype=torch.bfloat16).eval()
+        torch_model.load_state_dict(model.state_dict())
+        torch_logits, _ = torch_model(ids.to(device))
     expected = oracle.double_attention_lm(oracle_params(model), config, ids.numpy(), 6, 6, dtype=np.float32)
-    # LayerNorm/FFN/LM head run as PyTorch bf16 ops between the HIP layers.
-    assert_parity(logits, expected, rel_l2=2e-2, max_abs=0.25, label="lm c4")
+    # LayerNorm, FFN and the LM head run as PyTorch bf16 ops between the HIP
+    # layers, so the logits carry bf16 rounding of activations of size ~30.
+    # Bar: the HIP LM is no further from fp32 than the bf16 PyTorch path is.
+    e = expected.astype(np.float64)
+    torch_rel = np.linalg.norm(np32(torch_logits) - e) / np.linalg.norm(e)
+    torch_max = np.abs(np32(torch_logits) - e).max()
+    print(f"[parity] lm c4 bf16 torch path rel_l2={torch_rel:.3e} max_abs={torch_max:.3e}", flush=True)
+    assert_parity(logits, expected, rel_l2=max(5e-3, 1.1 * torch_rel), max_abs=max(2e-2, 1.1 * torch_max), label="lm c4")
 
 
 def test_stack_normalizes_each_bank_once_on_hip(monkeypatch) -> None:
@@ -315,9 +351,9 @@ def test_stack_normalizes_each_bank_once_on_hip(monkeypatch) -> None:
     calls = []
     original = da.SharedDictionaryBank.normalized_hip
 
-    def counted(bank, eps=1e-6, dtype=None):
+    def counted(bank, eps=1e-6, key_dtype=torch.float16):
         calls.append(bank)
-        return original(bank, eps, dtype)
+        return original(bank, eps, key_dtype)
 
     monkeypatch.setattr(da.SharedDictionaryBank, "normalized_hip", counted)
     with torch.inference_mode():
