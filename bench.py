@@ -130,7 +130,7 @@ def main() -> None:
         layout = key._da_route_layout
         qk = torch.empty(tokens, 2 * W, device=device, dtype=dtype)
         tp = lib.da_padded_length(length)
-        vt = torch.zeros(batch, d, tp, device=device, dtype=dtype)
+        vt = torch.zeros(batch, tp // 32, d, 32, device=device, dtype=dtype)
         routed = torch.empty(tokens, 2 * W, device=device, dtype=torch.float16)
         mixed = torch.empty(tokens, d, device=device, dtype=dtype)
         final = torch.empty(tokens, d, device=device, dtype=dtype)
@@ -147,7 +147,7 @@ def main() -> None:
             "qkv_projection": lambda: lib.da_qkv_projection(
                 x.data_ptr(), tokens, d, length, p["query.weight"].data_ptr(), p["key.weight"].data_ptr(), W,
                 p["value.weight"].data_ptr(), p["value.bias"].data_ptr(), d, pdt, code,
-                qk.data_ptr(), vt.data_ptr(), vt.stride(0), vt.stride(1), handle),
+                qk.data_ptr(), vt.data_ptr(), vt.stride(0), tp, handle),
             "route": lambda: lib.da_dictionary_route(
                 qk.data_ptr(), rows, R, R, code, layout.key_t.data_ptr(), key_code, layout.value.data_ptr(), M,
                 p["log_beta"].data_ptr(), pdt, 0.0, config.eps,
@@ -155,7 +155,7 @@ def main() -> None:
                 routed.data_ptr(), R, _lib.DA_F16, handle),
             "attention": lambda: lib.da_routed_attention(
                 routed.data_ptr(), routed.data_ptr() + W * routed.element_size(), length * 2 * W, 2 * W,
-                rp if H > S else R, S // H if S > H else 1, rp, vt.data_ptr(), vt.stride(0), vt.stride(1),
+                rp if H > S else R, S // H if S > H else 1, rp, vt.data_ptr(), vt.stride(0),
                 batch, S, length, d, p["log_score_scales"].data_ptr(), pdt,
                 float(group ** -0.5), None if S == 1 else p["map_mix_logits"].data_ptr(), pdt,
                 _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX, _lib.DA_F16, code,

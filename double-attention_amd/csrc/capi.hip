@@ -71,7 +71,7 @@ int validate_route(const void* x, int64_t rows, int64_t R, int64_t xs, int x_dty
 }
 
 int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int64_t ms, int64_t rep,
-                       int64_t RP, const void* vt, int64_t vsb, int64_t vsd, int64_t B, int64_t S,
+                       int64_t RP, const void* vt, int64_t vsb, int64_t B, int64_t S,
                        int64_t T, int64_t D, const void* scales, int scales_dtype,
                        const void* mix, int mix_dtype, int qk_dtype, int v_dtype, const void* out,
                        int64_t ob, int64_t ot, int64_t os) {
@@ -91,8 +91,8 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
     return fail(DA_ERR_ALIGNMENT, "attention: q/k/value_t must be 16-byte and out 8-byte aligned");
   if (sb % 8 || st % 8 || ms % 8 || st < RP)
     return fail(DA_ERR_ALIGNMENT, "attention: q/k strides must be multiples of 8 and stride_t >= score_dim");
-  if (vsd % 8 || vsb % 8 || vsd < da::round_up(T, da::kKeyPad) || (B > 1 && vsb < D * vsd))
-    return fail(DA_ERR_ALIGNMENT, "attention: value_t pitches must be multiples of 8, vt_stride_d >= padded length");
+  if (vsb % 8 || (B > 1 && vsb < D * da::round_up(T, da::kKeyPad)))
+    return fail(DA_ERR_ALIGNMENT, "attention: vt_stride_b must be a multiple of 8 and >= value_dim * padded length");
   if (ob % 4 || ot % 4 || os % 4) return fail(DA_ERR_ALIGNMENT, "attention: out strides must be multiples of 4");
   return DA_OK;
 }
@@ -101,7 +101,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 2; }
+int da_abi_version(void) { return 3; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -143,14 +143,14 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
 
 int da_routed_attention(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
                         int64_t map_stride, int64_t map_repeat, int64_t score_dim,
-                        const void* value_t, int64_t vt_stride_b, int64_t vt_stride_d,
+                        const void* value_t, int64_t vt_stride_b,
                         int64_t batch, int64_t maps, int64_t length, int64_t value_dim,
                         const void* scales, int scales_dtype, float scale_mult,
                         const void* mix_logits, int mix_dtype, int flags, int qk_dtype,
                         int v_dtype, void* out, int64_t out_stride_b, int64_t out_stride_t,
                         int64_t out_stride_s, da_stream_t stream) {
   int rc = validate_attention(query, key, stride_b, stride_t, map_stride, map_repeat, score_dim,
-                              value_t, vt_stride_b, vt_stride_d, batch, maps, length, value_dim,
+                              value_t, vt_stride_b, batch, maps, length, value_dim,
                               scales, scales_dtype, mix_logits, mix_dtype, qk_dtype, v_dtype, out,
                               out_stride_b, out_stride_t, out_stride_s);
   if (rc) return rc;
@@ -165,7 +165,6 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
   a.RP = static_cast<int>(score_dim);
   a.vt = value_t;
   a.vt_stride_b = vt_stride_b;
-  a.vt_stride_d = vt_stride_d;
   a.B = static_cast<int>(batch);
   a.S = static_cast<int>(maps);
   a.T = static_cast<int>(length);
@@ -292,7 +291,7 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   if (rc) return rc;
   const int64_t ot = concat ? S * d : d;
   rc = validate_attention(routed, static_cast<char*>(routed) + W * 2, T * 2 * W, 2 * W,
-                          H > S ? RP : R, 1, RP, vt, d * Tp, Tp, B, S, T, d, a->log_score_scales,
+                          H > S ? RP : R, 1, RP, vt, d * Tp, B, S, T, d, a->log_score_scales,
                           a->param_dtype, a->map_mix_logits, a->param_dtype, DA_F16, a->dtype,
                           mixed, T * ot, ot, concat ? d : 0);
   if (rc) return rc;
@@ -328,7 +327,6 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   at.RP = static_cast<int>(RP);
   at.vt = vt;
   at.vt_stride_b = d * Tp;
-  at.vt_stride_d = Tp;
   at.B = static_cast<int>(B);
   at.S = static_cast<int>(S);
   at.T = static_cast<int>(T);

@@ -59,8 +59,8 @@ struct AttentionArgs {
   int64_t map_stride;                 // elements between the first branches of consecutive maps
   int map_repeat;                     // maps sharing one branch (S > H repeat)
   int RP;                             // score width R' of one map
-  const void* vt;                     // V^T [B, D, Tv] (token-contiguous)
-  int64_t vt_stride_b, vt_stride_d;
+  const void* vt;                     // V^T in 32-token tiles: (b, d, t) at b*vt_stride_b + (t/32)*32*D + 32*d + t%32
+  int64_t vt_stride_b;
   int B, S, T, D;
   const void* scales;
   int scales_dtype;
@@ -87,8 +87,9 @@ struct GemmSegment {
   int mode;               // 0: out[j, i] (row-major by j), 1: V^T layout
   void* out;
   int64_t ldo;            // mode 0: row pitch of out (elements)
-  // mode 1: I counts the B*T real tokens; token t of sequence b goes to
-  // out[b*vt_stride_b + j_feat*Tp + t], and tokens T..Tp-1 are filled too.
+  // mode 1: I counts the B*T real tokens; token t of sequence b, feature j
+  // goes to out[b*vt_stride_b + (t/32)*32*J + 32*j + t%32] (32-token tiles),
+  // and tokens T..Tp-1 are filled too.
   int64_t T, Tp, vt_stride_b;
 };
 

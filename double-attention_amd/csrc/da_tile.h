@@ -1,18 +1,24 @@
-// LDS tile staging for gfx950: direct global->LDS DMA and swizzled layouts.
+// LDS tile staging for gfx950: direct global->LDS DMA into padded tiles.
 //
 // Tiles are staged with global_load_lds_dwordx4: every lane names its own
-// 16-byte global chunk and the wave writes 64 consecutive 16-byte LDS slots
+// 16-byte global chunk and a wave writes 64 consecutive 16-byte LDS slots
 // (slot = M0 base + 16 * lane).  Data never passes through VGPRs, so the next
 // tile's loads run while the current tile is being multiplied.
 //
-// A tile is a row-major array of 16-byte chunks, `nck` chunks per row (nck a
-// power of two).  Chunk (row, ck) lives in LDS slot row*nck + (ck ^ swz(row)).
-// The swizzle makes each 16-lane group of a ds_read_b128 hit 16 distinct
-// 16-byte bank groups, for the two row orders the kernels read in:
-//   linear rows:  lanes c = 0..15 read rows base + c
-//   blocked rows: lanes c = 0..15 read rows base + 8*(c/4) + (c%4)
-// (the blocked order is the key/atom order that makes a score accumulator
-// directly usable as the next MFMA's B operand; see da_common.h).
+// A tile is ROWS rows of NCK 16-byte chunks.  In LDS each row occupies
+// NCK + 1 slots (one pad slot), so the 16 lanes of a ds_read_b128 that read
+// 16 consecutive rows at one chunk position hit 16 distinct bank groups, and
+// a lane's address for chunk k of row r is base + 16 * (r * (NCK + 1) + k):
+// every fragment read of a kernel's inner loop is a per-lane base plus an
+// immediate offset.  Pad slots are filled with a duplicate chunk and never
+// read.
+//
+// "Blocked" tiles store their rows permuted inside each 32-row window:
+// logical row 8a + 4h + i (a, i in 0..3, h in 0..1) sits at physical row
+// 16h + 4a + i.  MFMA block kb = 2w + h of the window then reads physical rows
+// 16 kb + c, c = 0..15 -- linear -- while its 16x16 accumulator holds logical
+// rows 32w + 8g + 4h + i in lane group g: exactly the k order in which two
+// stacked accumulator blocks form the next MFMA's B operand (da_common.h).
 #pragma once
 
 #include "da_common.h"
@@ -28,49 +34,42 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_slot_base) {
 // s_waitcnt vmcnt(0) only (gfx9 encoding: expcnt and lgkmcnt left at max).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-template <int NCK>
-__device__ __forceinline__ int swz_linear(int row) {
-  if constexpr (NCK >= 16) return row & 15;
-  else return (row / (16 / NCK)) & (NCK - 1);
-}
-
-template <int NCK>
-__device__ __forceinline__ int swz_blocked(int row) {
-  if constexpr (NCK >= 16) return ((row >> 1) & 12) | (row & 3);
-  else if constexpr (NCK == 8) return (((row >> 3) & 3) << 1) | ((row >> 1) & 1);
-  else return swz_linear<NCK>(row);
-}
-
-template <int NCK, bool BLOCKED>
-__device__ __forceinline__ int slot_of(int row, int ck) {
-  return row * NCK + (ck ^ (BLOCKED ? swz_blocked<NCK>(row) : swz_linear<NCK>(row)));
-}
-
-// Inverse of slot_of: which (row, ck) a given LDS slot holds.
-template <int NCK, bool BLOCKED>
-__device__ __forceinline__ void chunk_of(int slot, int& row, int& ck) {
-  row = slot / NCK;
-  ck = (slot % NCK) ^ (BLOCKED ? swz_blocked<NCK>(row) : swz_linear<NCK>(row));
-}
-
-// 16-byte read of chunk (row, ck) from a tile starting at `tile`.
-template <int NCK, bool BLOCKED>
-__device__ __forceinline__ u32x4 lds_chunk(const char* tile, int row, int ck) {
-  return *reinterpret_cast<const u32x4*>(tile + slot_of<NCK, BLOCKED>(row, ck) * 16);
-}
-
-template <typename T>
-__device__ __forceinline__ typename Elem<T>::v8 as_v8(u32x4 v) {
-  return __builtin_bit_cast(typename Elem<T>::v8, v);
-}
-
-// Row of the blocked order: MFMA block `kb` of a 32-row window, lane row c.
-__device__ __forceinline__ int blocked_row(int kb, int c) {
-  return 32 * (kb >> 1) + 8 * (c >> 2) + 4 * (kb & 1) + (c & 3);
-}
-
 __device__ __forceinline__ int uniform_wave() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
+template <int ROWS, int NCK, bool BLOCKED>
+struct PaddedTile {
+  static_assert(!BLOCKED || ROWS % 32 == 0, "blocked tiles are made of 32-row windows");
+  static constexpr int PITCH = NCK + 1;                 // slots per row
+  static constexpr int SLOTS = ROWS * PITCH;
+  static constexpr int LOADS = (SLOTS + 63) / 64;       // wave loads that fill the tile
+  static constexpr int BYTES = LOADS * 1024;
+
+  // Logical row held by physical row p.
+  static __device__ __forceinline__ int logical_row(int p) {
+    if constexpr (BLOCKED) return (p & ~31) + 8 * ((p >> 2) & 3) + 4 * ((p >> 4) & 1) + (p & 3);
+    else return p;
+  }
+
+  // What slot `slot` holds: logical row and chunk; false for pad slots and the
+  // tail of the last wave load (which then load a duplicate of chunk 0 of row 0).
+  static __device__ __forceinline__ bool slot_chunk(int slot, int& row, int& ck) {
+    const int p = slot / PITCH;
+    ck = slot - p * PITCH;
+    const bool real = ck < NCK && p < ROWS;
+    row = real ? logical_row(p) : 0;
+    if (!real) ck = 0;
+    return real;
+  }
+
+  // Byte offset of (physical row, chunk).
+  static __device__ __forceinline__ constexpr int offset(int prow, int ck) { return (prow * PITCH + ck) * 16; }
+};
+
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::v8 lds_v8(const char* p) {
+  return *reinterpret_cast<const typename Elem<T>::v8*>(p);
 }
 
 }  // namespace da

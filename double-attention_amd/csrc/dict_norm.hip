@@ -9,7 +9,8 @@
 // Output layouts are the ones the fused route kernel reads, padded to
 // Mp = round_up(M, 64) atoms with zero atoms in the padding:
 //   key_t  [Mp, R]  atom-major, element type TK
-//   value  [R, Mp]  coordinate-major, fp16 (normalized atoms are bounded by 1)
+//   value  32-atom tiles, fp16 (normalized atoms are bounded by 1): coordinate
+//          r of atom j at value[(j/32)*32*R + 32*r + j%32]
 // A workgroup owns 32 atoms: it reads each column once into registers (fp32),
 // reduces the sums of squares through LDS, writes the value layout directly
 // and the atom-major key layout through an LDS transpose, so every global
@@ -62,10 +63,12 @@ __global__ __launch_bounds__(256) void dict_normalize_kernel(
   const float scale = scale_s[jj];
 
   if (write_value) {
+    // The workgroup's 32 atoms are exactly one value tile.
+    _Float16* vtile = value + static_cast<int64_t>(j0) * R;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int r = rg + i * kNormGroups;
-      value[static_cast<int64_t>(r) * Mp + j] = static_cast<_Float16>(v[i] * scale);
+      vtile[r * kNormCols + jj] = static_cast<_Float16>(v[i] * scale);
     }
   }
   if (write_key) {

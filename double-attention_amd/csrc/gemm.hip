@@ -10,14 +10,14 @@
 // operands, so no concatenated weight is ever materialized.  Epilogues:
 //   mode 0: out[j, i]                 -- features i of token j (Q/K projection,
 //                                        output projection)
-//   mode 1: out[b, j_feature, t] (V^T) -- value features in the token-contiguous
-//                                        layout the attention kernel streams.
-//           Rows i run over B * Tp "virtual" tokens (t < Tp, the padded
-//           length); tokens past T reuse the last real row, so the padding of
-//           V^T is always finite.
-// Tiles: 128 x 128 per workgroup, 64-wide K stages double-buffered in LDS and
-// filled by global->LDS DMA; each of the four waves owns a 64 x 64 quadrant
-// (4 x 4 MFMA 16x16x32 blocks).
+//   mode 1: V^T in 32-token tiles -- feature j of token t of sequence b at
+//           out[b*vt_stride_b + (t/32)*32*J + 32*j + t%32], the layout the
+//           attention kernel streams one contiguous tile at a time.  Rows i
+//           run over B * Tp "virtual" tokens (t < Tp, the padded length);
+//           tokens past T reuse the last real row, so the padding is finite.
+// Tiles: 128 x 128 per workgroup, 64-wide K stages double-buffered in padded
+// LDS tiles (da_tile.h) and filled by global->LDS DMA; each of the four waves
+// owns a 64 x 64 quadrant (4 x 4 MFMA 16x16x32 blocks).
 #include "da_common.h"
 #include "da_launch.h"
 #include "da_tile.h"
@@ -27,8 +27,9 @@ namespace da {
 constexpr int kBI = 128;
 constexpr int kBJ = 128;
 constexpr int kBK = 64;
-constexpr int kGemmNck = kBK / 8;                        // chunks per tile row
-constexpr int kGemmTileBytes = kBI * kBK * 2;            // one operand tile
+typedef PaddedTile<128, kBK / 8, false> GemmTile;       // one operand tile: 128 rows x 64 k
+constexpr int kGemmPerWave = 2 * GemmTile::LOADS / 4;    // wave loads per wave per stage
+static_assert((2 * GemmTile::LOADS) % 4 == 0, "stage must split evenly over four waves");
 
 struct GemmSeg {
   const void* p0;
@@ -54,7 +55,7 @@ template <typename T>
 __device__ __forceinline__ const T* p_row(const GemmSeg& sg, int64_t i) {
   const T* p0 = static_cast<const T*>(sg.p0);
   i = min(i, sg.I - 1);   // rows of a partial last tile are computed but never stored
-  if (sg.mode == 1) {   // virtual token i = b * Tp + t of the value segment
+  if (sg.mode == 1) {     // virtual token i = b * Tp + t of the value segment
     const int64_t b = i / sg.Tp;
     const int64_t t = min(i % sg.Tp, sg.T - 1);
     return p0 + (b * sg.T + t) * sg.K;
@@ -63,27 +64,11 @@ __device__ __forceinline__ const T* p_row(const GemmSeg& sg, int64_t i) {
 }
 
 template <typename T>
-__device__ __forceinline__ void issue_stage(char* buf, const GemmSeg& sg, int64_t i0, int64_t j0, int k0,
-                                            int wave, int lane) {
-  const T* qq = static_cast<const T*>(sg.q);
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int j = it * 4 + wave;
-    int r, ck;
-    chunk_of<kGemmNck, false>(j * 64 + lane, r, ck);
-    // Columns past K only occur in a final half stage that is never read.
-    const int kc = min(k0 + ck * 8, static_cast<int>(sg.K) - 8);
-    dma16(p_row<T>(sg, i0 + r) + kc, buf + j * 1024);
-    const int64_t jr = min(j0 + r, sg.J - 1);
-    dma16(qq + jr * sg.K + kc, buf + kGemmTileBytes + j * 1024);
-  }
-}
-
-template <typename T>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   typedef typename Elem<T>::v8 v8;
-  __shared__ __attribute__((aligned(1024))) char lds0[2 * kGemmTileBytes];
-  __shared__ __attribute__((aligned(1024))) char lds1[2 * kGemmTileBytes];
+  constexpr int STAGE = 2 * GemmTile::BYTES;   // P tile, then Q tile
+  __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
 
   int tile = blockIdx.x;
   const int si = (prm.nseg > 1 && tile >= prm.seg[0].tiles) ? 1 : 0;
@@ -101,25 +86,51 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   const int K = static_cast<int>(sg.K);
   const int n_stages = (K + kBK - 1) / kBK;
 
+  // This wave's DMA sources for stage k0 = 0: wave load j < LOADS fills the
+  // P tile, the rest the Q tile; only the k offset moves between stages.
+  const T* src[kGemmPerWave];
+  int kchunk[kGemmPerWave];
+#pragma unroll
+  for (int n = 0; n < kGemmPerWave; ++n) {
+    const int j = n * 4 + wave;
+    const int jj = j < GemmTile::LOADS ? j : j - GemmTile::LOADS;
+    int r, ck;
+    GemmTile::slot_chunk(jj * 64 + lane, r, ck);
+    kchunk[n] = ck * 8;
+    src[n] = j < GemmTile::LOADS ? p_row<T>(sg, i0 + r)
+                                 : static_cast<const T*>(sg.q) + min(j0 + r, sg.J - 1) * sg.K;
+  }
+  auto issue = [&](char* buf, int k0) {
+    // Columns past K only occur in a final half stage that is never read.
+    const bool tail = k0 + kBK > K;
+#pragma unroll
+    for (int n = 0; n < kGemmPerWave; ++n) {
+      const int j = n * 4 + wave;
+      const int kc = tail ? min(k0 + kchunk[n], K - 8) : k0 + kchunk[n];
+      dma16(src[n] + kc, buf + j * 1024);
+    }
+  };
+
   f32x4 acc[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = zero4();
 
+  const int afrag = GemmTile::offset(wi * 64 + c, g);
+  const int bfrag = GemmTile::BYTES + GemmTile::offset(wj * 64 + c, g);
+
   auto step = [&](int st, char* cur, char* nxt) {
     wait_vmem();
     __syncthreads();
-    if (st + 1 < n_stages) issue_stage<T>(nxt, sg, i0, j0, (st + 1) * kBK, wave, lane);
+    if (st + 1 < n_stages) issue(nxt, (st + 1) * kBK);
     const int ksteps = min(kBK, K - st * kBK) / 32;
     for (int kk = 0; kk < ksteps; ++kk) {
       v8 af[4], bf[4];
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
-        af[a] = as_v8<T>(lds_chunk<kGemmNck, false>(cur, wi * 64 + a * 16 + c, kk * 4 + g));
+      for (int a = 0; a < 4; ++a) af[a] = lds_v8<T>(cur + afrag + GemmTile::offset(a * 16, kk * 4));
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-        bf[b] = as_v8<T>(lds_chunk<kGemmNck, false>(cur + kGemmTileBytes, wj * 64 + b * 16 + c, kk * 4 + g));
+      for (int b = 0; b < 4; ++b) bf[b] = lds_v8<T>(cur + bfrag + GemmTile::offset(b * 16, kk * 4));
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -127,7 +138,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     }
   };
 
-  issue_stage<T>(lds0, sg, i0, j0, 0, wave, lane);
+  issue(lds0, 0);
   int st = 0;
   for (; st + 1 < n_stages; st += 2) {
     step(st, lds0, lds1);
@@ -161,10 +172,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
           for (int r = 0; r < 4 && i + r < sg.I; ++r) dst[r] = o[r];
         }
       } else {
-        // Four consecutive virtual tokens of one sequence (Tp % 64 == 0).
+        // Four consecutive virtual tokens of one sequence and one 32-token
+        // tile (Tp % 64 == 0, i % 4 == 0).
         const int64_t bb = i / sg.Tp;
         const int64_t t = i % sg.Tp;
-        *reinterpret_cast<typename Elem<T>::v4*>(out + bb * sg.vt_stride_b + j * sg.Tp + t) = o;
+        *reinterpret_cast<typename Elem<T>::v4*>(out + bb * sg.vt_stride_b + (t >> 5) * 32 * sg.J + 32 * j +
+                                                 (t & 31)) = o;
       }
     }
   }

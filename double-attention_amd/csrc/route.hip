@@ -15,166 +15,200 @@
 // first MFMA is directly the B operand of the second:
 //   S^T[j, c] = sum_r Dk^T[j, r] U^T[r, c]      (A = key atoms from LDS, B = rows in VGPRs)
 //   O^T[r, c] += sum_j Dv[r, j] P^T[j, c]       (A = value atoms from LDS, B = P in VGPRs)
-// One wave owns 16 rows; the four waves of a workgroup share each dictionary
-// tile, which is double-buffered in LDS and filled by global->LDS DMA while the
-// previous tile is multiplied.  The input scale beta/||x|| is applied before
-// the single rounding of the unit row.
+// A workgroup of four waves shares each dictionary tile, double-buffered in
+// padded LDS tiles (da_tile.h) and filled by global->LDS DMA while the previous
+// tile is multiplied.  Each wave owns QW rows (QW/16 MFMA column blocks), so
+// every dictionary fragment read from LDS feeds QW/16 MFMAs.  The input scale
+// beta/||x|| is applied before the single rounding of the unit row.
 //
 // Element types: TX = input rows, TK = key atoms and the normalized input (fp16
 // when the input is L2-normalized, since |u_i| <= 1; else TX), value atoms and
-// the softmax weights are fp16 (both bounded by 1), TO = output rows.
+// the softmax weights are fp16 (both bounded by 1), TO = output rows.  Value
+// atoms are stored in 32-atom tiles: coordinate r of atom j at
+// value[(j/32)*32*R + 32*r + j%32].
 #include "da_common.h"
 #include "da_launch.h"
 #include "da_tile.h"
 
 namespace da {
 
+constexpr int kRouteWaves = 4;
+
 template <int R>
-struct RouteTile {
+struct RouteCfg {
+  static constexpr int QW = R >= 512 ? 16 : 32;   // rows per wave
   static constexpr int AT = R >= 512 ? 32 : 64;   // atoms per tile
-  static constexpr int NCK = R / 8;              // chunks per key-atom row
-  static constexpr int KCH = AT * NCK;
-  static constexpr int VCK = AT / 8;             // chunks per value row
-  static constexpr int VCH = R * VCK;
-  static constexpr int BYTES = (KCH + VCH) * 16;
-  static_assert(KCH % 256 == 0 && VCH % 256 == 0, "tile must split evenly over 256 lanes");
+  typedef PaddedTile<AT, R / 8, true> KT;         // key atoms (blocked rows)
+  typedef PaddedTile<R, AT / 8, false> VT;        // value coordinates x atoms
+  static constexpr int LOADS = KT::LOADS + VT::LOADS;
+  static constexpr int PER_WAVE = (LOADS + kRouteWaves - 1) / kRouteWaves;
+  static constexpr int BYTES = LOADS * 1024;
+  static constexpr int ROWS = kRouteWaves * QW;   // rows per workgroup
 };
 
 template <typename TX, typename TK, typename TO, int R>
-__global__ __launch_bounds__(256) void route_kernel(
+__global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(
     const TX* x, int64_t rows, int64_t x_stride, const TK* __restrict__ key_t,
     const _Float16* __restrict__ value, int M, int Mp, const void* __restrict__ beta_ptr,
     int beta_dtype, float beta_value, float eps, int flags, TO* out, int64_t out_stride) {
   // x and out may alias (in-place routing): every row is read into VGPRs by
   // its own wave before that wave writes it.
-  typedef RouteTile<R> Tile;
+  typedef RouteCfg<R> Cfg;
+  typedef typename Cfg::KT KT;
+  typedef typename Cfg::VT VT;
   typedef typename Elem<TK>::v8 k8;
   constexpr int KS = R / 32;
-  constexpr int AT = Tile::AT;
-  __shared__ __attribute__((aligned(1024))) char lds0[Tile::BYTES];
-  __shared__ __attribute__((aligned(1024))) char lds1[Tile::BYTES];
+  constexpr int AT = Cfg::AT;
+  constexpr int CB = Cfg::QW / 16;   // column blocks per wave
+  constexpr int NB = AT / 16;        // atom blocks per tile
+  __shared__ __attribute__((aligned(1024))) char lds0[Cfg::BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds1[Cfg::BYTES];
 
   const int lane = lane_id();
   const int c = lane & 15;
   const int g = lane >> 4;
   const int wave = uniform_wave();
-  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * 16 + c;
-  const bool row_ok = row < rows;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kRouteWaves + wave) * Cfg::QW;
   const int n_tiles = Mp / AT;
 
-  auto issue = [&](char* buf, int j0) {
+  // Per-lane DMA sources relative to the tile's atom offset: key atoms are
+  // rows of key_t, value chunks live in 32-atom tiles.
+  int desc[Cfg::PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < Tile::KCH / 256; ++i) {
-      const int j = i * 4 + wave;
-      int a, ck;
-      chunk_of<Tile::NCK, true>(j * 64 + lane, a, ck);
-      dma16(key_t + static_cast<int64_t>(j0 + a) * R + ck * 8, buf + j * 1024);
+  for (int i = 0; i < Cfg::PER_WAVE; ++i) {
+    const int j = i * kRouteWaves + wave;
+    int row = 0, ck = 0;
+    if (j < KT::LOADS) {
+      KT::slot_chunk(j * 64 + lane, row, ck);
+      desc[i] = row * R + ck * 8;
+    } else if (j < Cfg::LOADS) {
+      VT::slot_chunk((j - KT::LOADS) * 64 + lane, row, ck);
+      desc[i] = (ck >> 2) * 32 * R + row * 32 + (ck & 3) * 8;
+    } else {
+      desc[i] = 0;
     }
+  }
+  auto issue = [&](char* buf, int t) {
+    const int j0 = t * AT;
+    const TK* ktile = key_t + static_cast<int64_t>(j0) * R;
+    const _Float16* vtile = value + static_cast<int64_t>(j0) * R;   // 32-atom tiles: j0/32 * 32R
 #pragma unroll
-    for (int i = 0; i < Tile::VCH / 256; ++i) {
-      const int j = i * 4 + wave;
-      int r, ck;
-      chunk_of<Tile::VCK, false>(j * 64 + lane, r, ck);
-      dma16(value + static_cast<int64_t>(r) * Mp + j0 + ck * 8, buf + Tile::KCH * 16 + j * 1024);
+    for (int i = 0; i < Cfg::PER_WAVE; ++i) {
+      const int j = i * kRouteWaves + wave;
+      if (j < KT::LOADS) dma16(ktile + desc[i], buf + j * 1024);
+      else if (j < Cfg::LOADS) dma16(vtile + desc[i], buf + j * 1024);
     }
   };
   issue(lds0, 0);
 
-  // Row fragment (B operand of the assignment contraction), kept in VGPRs.
-  typename Elem<TX>::v8 xr[KS];
-  float ss = 0.f;
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) {
-    xr[kk] = row_ok ? load8(x + row * x_stride + kk * 32 + 8 * g) : zero8<TX>();
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v = static_cast<float>(xr[kk][e]);
-      ss += v * v;
-    }
-  }
-  ss = group_sum(ss);
-  float beta = beta_ptr ? load_scalar(beta_ptr, beta_dtype, 0) : beta_value;
-  if (flags & kRouteBetaIsLog) beta = expf(fminf(fmaxf(beta, kLogBetaMin), kLogBetaMax));
-  const bool norm_in = flags & kRouteNormalizeInput;
-  const float inv_norm = norm_in ? 1.f / fmaxf(sqrtf(ss), eps) : 1.f;
-  // With input normalization the unit row is rounded once to TK; otherwise
-  // TK == TX and the raw row passes through unchanged.
-  k8 xf[KS];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xf[kk][e] = static_cast<TK>(static_cast<float>(xr[kk][e]) * inv_norm);
+  // Row fragments (B operands of the assignment contraction), kept in VGPRs.
+  const float beta_raw = beta_ptr ? load_scalar(beta_ptr, beta_dtype, 0) : beta_value;
+  const float beta = (flags & kRouteBetaIsLog) ? expf(fminf(fmaxf(beta_raw, kLogBetaMin), kLogBetaMax)) : beta_raw;
   const float scale = beta * kLog2e;   // logits -> log2-domain exponents
-
-  f32x4 acc[R / 16];
+  k8 xf[CB][KS];
 #pragma unroll
-  for (int i = 0; i < R / 16; ++i) acc[i] = zero4();
-  float m_run = -INFINITY;
-  float l_part = 0.f;   // this lane's share of the softmax denominator
+  for (int cb = 0; cb < CB; ++cb) {
+    const int64_t row = row0 + cb * 16 + c;
+    typename Elem<TX>::v8 xr[KS];
+    float ss = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      xr[kk] = row < rows ? load8(x + row * x_stride + kk * 32 + 8 * g) : zero8<TX>();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = static_cast<float>(xr[kk][e]);
+        ss += v * v;
+      }
+    }
+    ss = group_sum(ss);
+    // With input normalization the unit row is rounded once to TK; otherwise
+    // TK == TX and the raw row passes through unchanged.
+    const float inv_norm = (flags & kRouteNormalizeInput) ? 1.f / fmaxf(sqrtf(ss), eps) : 1.f;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xf[cb][kk][e] = static_cast<TK>(static_cast<float>(xr[kk][e]) * inv_norm);
+  }
+
+  f32x4 acc[CB][R / 16];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int i = 0; i < R / 16; ++i) acc[cb][i] = zero4();
+  float m_run[CB], l_part[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    m_run[cb] = -INFINITY;
+    l_part[cb] = 0.f;
+  }
+
+  const int kfrag = KT::offset(c, g);
+  const int vfrag = KT::BYTES + VT::offset(c, g);
 
   auto step = [&](int t, char* cur, char* nxt) {
     wait_vmem();
     __syncthreads();
-    if (t + 1 < n_tiles) issue(nxt, (t + 1) * AT);
+    if (t + 1 < n_tiles) issue(nxt, t + 1);
     const int j0 = t * AT;
-    // Logits: AT/16 independent accumulator chains, fragments read from LDS
-    // in batches ahead of their MFMAs.
-    constexpr int NB = AT / 16;
-    f32x4 s[NB];
+
+    // Logits: NB x CB independent accumulator chains; each key fragment
+    // feeds all CB column blocks.
+    f32x4 s[CB][NB];
 #pragma unroll
-    for (int kb = 0; kb < NB; ++kb) s[kb] = zero4();
-    {
-      constexpr int KB = NB == 4 ? 2 : 4;   // k-steps per batch (8 fragments in flight)
+    for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-      for (int kk0 = 0; kk0 < KS; kk0 += KB) {
-        u32x4 a[KB][NB];
+      for (int kb = 0; kb < NB; ++kb) s[cb][kb] = zero4();
+    const char* kf = cur + kfrag;
 #pragma unroll
-        for (int i = 0; i < KB; ++i)
+    for (int kk = 0; kk < KS; ++kk) {
+      k8 a[NB];
 #pragma unroll
-          for (int kb = 0; kb < NB; ++kb)
-            a[i][kb] = lds_chunk<Tile::NCK, true>(cur, blocked_row(kb, c), (kk0 + i) * 4 + g);
+      for (int kb = 0; kb < NB; ++kb) a[kb] = lds_v8<TK>(kf + KT::offset(16 * kb, kk * 4));
 #pragma unroll
-        for (int i = 0; i < KB; ++i)
+      for (int kb = 0; kb < NB; ++kb)
 #pragma unroll
-          for (int kb = 0; kb < NB; ++kb) s[kb] = Elem<TK>::mma(as_v8<TK>(a[i][kb]), xf[kk0 + i], s[kb]);
-      }
+        for (int cb = 0; cb < CB; ++cb) s[cb][kb] = Elem<TK>::mma(a[kb], xf[cb][kk], s[cb][kb]);
     }
     // Lane (c, g) holds atoms j0 + 32*(kb/2) + 8g + 4*(kb%2) + i of row c.
-    float tmax = -INFINITY;
+    const bool masked = j0 + AT > M;
+    f16x8 pb[CB][AT / 32];
 #pragma unroll
-    for (int kb = 0; kb < AT / 16; ++kb) {
+    for (int cb = 0; cb < CB; ++cb) {
+      float tmax = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int atom = j0 + 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + i;
-        const float v = atom < M ? s[kb][i] * scale : -INFINITY;
-        s[kb][i] = v;
-        tmax = fmaxf(tmax, v);
+      for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = s[cb][kb][i] * scale;
+          if (masked && j0 + 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + i >= M) v = -INFINITY;
+          s[cb][kb][i] = v;
+          tmax = fmaxf(tmax, v);
+        }
       }
-    }
-    lazy_rescale<R / 16>(group_max(tmax), m_run, l_part, acc);
-    float psum = 0.f;
+      lazy_rescale<R / 16>(group_max(tmax), m_run[cb], l_part[cb], acc[cb]);
+      float psum = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < AT / 16; ++kb) {
+      for (int kb = 0; kb < NB; ++kb) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pr = exp2f(s[kb][i] - m_run);
-        s[kb][i] = pr;
-        psum += pr;
+        for (int i = 0; i < 4; ++i) {
+          const float pr = __builtin_amdgcn_exp2f(s[cb][kb][i] - m_run[cb]);
+          s[cb][kb][i] = pr;
+          psum += pr;
+        }
       }
+      l_part[cb] += psum;
+#pragma unroll
+      for (int w = 0; w < AT / 32; ++w) pb[cb][w] = pack_blocked<_Float16>(s[cb][2 * w], s[cb][2 * w + 1]);
     }
-    l_part += psum;
-    const char* vtile = cur + Tile::KCH * 16;
-    constexpr int RB = R / 16 < 8 ? R / 16 : 8;
+
+    const char* vf = cur + vfrag;
 #pragma unroll
     for (int w = 0; w < AT / 32; ++w) {
-      const f16x8 pb = pack_blocked<_Float16>(s[2 * w], s[2 * w + 1]);   // atoms j0 + 32w + 8g + e
 #pragma unroll
-      for (int rb0 = 0; rb0 < R / 16; rb0 += RB) {
-        u32x4 a[RB];
+      for (int rb = 0; rb < R / 16; ++rb) {
+        const f16x8 a = lds_v8<_Float16>(vf + VT::offset(16 * rb, 4 * w));
 #pragma unroll
-        for (int i = 0; i < RB; ++i) a[i] = lds_chunk<Tile::VCK, false>(vtile, (rb0 + i) * 16 + c, 4 * w + g);
-#pragma unroll
-        for (int i = 0; i < RB; ++i) acc[rb0 + i] = Elem<_Float16>::mma(as_v8<_Float16>(a[i]), pb, acc[rb0 + i]);
+        for (int cb = 0; cb < CB; ++cb) acc[cb][rb] = Elem<_Float16>::mma(a, pb[cb][w], acc[cb][rb]);
       }
     }
   };
@@ -187,37 +221,42 @@ __global__ __launch_bounds__(256) void route_kernel(
   if (t < n_tiles) step(t, lds0, lds1);
 
   // r = O / l; z = r / max(||r||, eps).
-  const float inv_l = 1.f / group_sum(l_part);
-  float out_scale = inv_l;
-  if (flags & kRouteNormalizeOutput) {
-    float rs = 0.f;
 #pragma unroll
-    for (int rb = 0; rb < R / 16; ++rb)
+  for (int cb = 0; cb < CB; ++cb) {
+    const float inv_l = 1.f / group_sum(l_part[cb]);
+    float out_scale = inv_l;
+    if (flags & kRouteNormalizeOutput) {
+      float rs = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = acc[rb][i] * inv_l;
-        rs += v * v;
+      for (int rb = 0; rb < R / 16; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = acc[cb][rb][i] * inv_l;
+          rs += v * v;
+        }
+      rs = group_sum(rs);
+      out_scale = inv_l / fmaxf(sqrtf(rs), eps);
+    }
+    const int64_t row = row0 + cb * 16 + c;
+    if (row < rows) {
+      TO* orow = out + row * out_stride;
+#pragma unroll
+      for (int rb = 0; rb < R / 16; ++rb) {
+        typename Elem<TO>::v4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = static_cast<TO>(acc[cb][rb][i] * out_scale);
+        *reinterpret_cast<typename Elem<TO>::v4*>(orow + rb * 16 + 4 * g) = o;
       }
-    rs = group_sum(rs);
-    out_scale = inv_l / fmaxf(sqrtf(rs), eps);
-  }
-  if (row_ok) {
-    TO* orow = out + row * out_stride;
-#pragma unroll
-    for (int rb = 0; rb < R / 16; ++rb) {
-      typename Elem<TO>::v4 o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = static_cast<TO>(acc[rb][i] * out_scale);
-      *reinterpret_cast<typename Elem<TO>::v4*>(orow + rb * 16 + 4 * g) = o;
     }
   }
 }
 
 template <typename TX, typename TK, typename TO, int R>
 static void launch_route_r(const RouteArgs& a, hipStream_t s) {
-  const int64_t blocks = (a.rows + 63) / 64;
-  hipLaunchKernelGGL((route_kernel<TX, TK, TO, R>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,
-                     static_cast<const TX*>(a.x), a.rows, a.x_stride, static_cast<const TK*>(a.key_t),
+  constexpr int ROWS = RouteCfg<R>::ROWS;
+  const int64_t blocks = (a.rows + ROWS - 1) / ROWS;
+  hipLaunchKernelGGL((route_kernel<TX, TK, TO, R>), dim3(static_cast<unsigned>(blocks)), dim3(kRouteWaves * 64), 0,
+                     s, static_cast<const TX*>(a.x), a.rows, a.x_stride, static_cast<const TK*>(a.key_t),
                      static_cast<const _Float16*>(a.value), a.M, static_cast<int>(round_up(a.M, kAtomPad)),
                      a.beta_ptr, a.beta_dtype, a.beta_value, a.eps, a.flags, static_cast<TO*>(a.out),
                      a.out_stride);

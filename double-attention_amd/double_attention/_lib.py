@@ -38,7 +38,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -98,7 +98,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [
             _vp, _vp, _i64, _i64, _i64, _i64, _i64,  # q, k, strides, map stride/repeat, score dim
-            _vp, _i64, _i64,  # value_t and pitches
+            _vp, _i64,  # value_t, per-sequence pitch
             _i64, _i64, _i64, _i64,  # batch, maps, length, value_dim
             _vp, _i32, _f32, _vp, _i32,  # scales, mix logits
             _i32, _i32, _i32, _vp, _i64, _i64, _i64, _vp,  # flags, qk/v dtypes, out + strides, stream

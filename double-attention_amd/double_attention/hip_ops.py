@@ -79,10 +79,12 @@ def _ptr(t: Tensor | None) -> int | None:
 class RouteDictionary(NamedTuple):
     """A normalized bank in the layouts the route kernel reads.
 
-    ``key_t`` is ``[Mp, R]`` (atom-major) in the key dtype, ``value`` is
-    ``[R, Mp]`` in fp16; atoms past ``atoms`` are zero.  ``Mp`` is ``atoms``
-    rounded up to a multiple of 64.  Normalized atoms are bounded by one, so
-    fp16 holds them with eight times finer rounding than bf16.
+    ``key_t`` is ``[Mp, R]`` (atom-major) in the key dtype; ``value`` is
+    ``[Mp / 32, R, 32]`` in fp16, i.e. 32-atom tiles with coordinate ``r`` of
+    atom ``j`` at ``value[j // 32, r, j % 32]``.  Atoms past ``atoms`` are zero
+    and ``Mp`` is ``atoms`` rounded up to a multiple of 64.  Normalized atoms
+    are bounded by one, so fp16 holds them with eight times finer rounding than
+    bf16.
     """
 
     key_t: Tensor
@@ -110,10 +112,11 @@ def dictionary_normalize_hip(
 ) -> tuple[Tensor, Tensor]:
     """Column-normalize a bank in one launch; returns ``(key, value)`` as ``[R, M]``.
 
-    Matches ``F.normalize(raw, dim=0, eps=eps)``.  The returned tensors are
-    views of the route layouts -- ``key`` in ``key_dtype``, ``value`` in fp16
-    -- so handing them back to the route costs no copy; for a tied bank both
-    views hold the same normalized atoms.
+    Matches ``F.normalize(raw, dim=0, eps=eps)``.  ``key`` (in ``key_dtype``)
+    is a view of the route's atom-major key layout and ``value`` (fp16) a copy
+    of its tiled value layout; both carry the layouts, so handing them back to
+    the route re-lays nothing out.  For a tied bank both hold the same
+    normalized atoms.
     """
 
     if raw_key.ndim != 2:
@@ -126,7 +129,7 @@ def dictionary_normalize_hip(
         raise NotImplementedError(f"HIP route supports routing_dim in {SUPPORTED_WIDTHS}, got {routing_dim}")
     padded = _round_up(atoms, ATOM_PAD)
     key_t = torch.empty(padded, routing_dim, dtype=key_dtype, device=raw_key.device)
-    value = torch.empty(routing_dim, padded, dtype=torch.float16, device=raw_key.device)
+    value = torch.empty(padded // 32, routing_dim, 32, dtype=torch.float16, device=raw_key.device)
     raw_key_c = raw_key.detach().contiguous()
     raw_value_c = None if raw_value is None else raw_value.detach().to(raw_key.dtype).contiguous()
     lib = _lib.get()
@@ -146,7 +149,13 @@ def dictionary_normalize_hip(
         "dictionary_normalize_hip",
     )
     layout = RouteDictionary(key_t, value, atoms)
-    return _tag(key_t[:atoms].t(), value[:, :atoms], layout)
+    return _tag(key_t[:atoms].t(), _untile_value(value)[:, :atoms], layout)
+
+
+def _untile_value(value: Tensor) -> Tensor:
+    """``[Mp / 32, R, 32]`` value tiles -> ``[R, Mp]``."""
+
+    return value.permute(1, 0, 2).reshape(value.shape[1], -1)
 
 
 def route_layout(dictionary_key: Tensor, dictionary_value: Tensor, key_dtype: torch.dtype) -> RouteDictionary:
@@ -167,7 +176,8 @@ def route_layout(dictionary_key: Tensor, dictionary_value: Tensor, key_dtype: to
     value = torch.zeros(routing_dim, padded, dtype=torch.float16, device=dictionary_key.device)
     key_t[:atoms].copy_(dictionary_key.detach().t())
     value[:, :atoms].copy_(dictionary_value.detach())
-    return RouteDictionary(key_t, value, atoms)
+    tiles = value.view(routing_dim, padded // 32, 32).permute(1, 0, 2).contiguous()
+    return RouteDictionary(key_t, tiles, atoms)
 
 
 # --------------------------------------------------------------------------
@@ -327,12 +337,15 @@ def _next_width(width: int) -> int:
 
 
 def value_transposed(value: Tensor, width: int | None = None) -> Tensor:
-    """``[B, T, D]`` -> zero-padded V^T ``[B, width, round_up(T, 64)]``."""
+    """``[B, T, D]`` -> zero-padded V^T in 32-token tiles ``[B, Tp/32, width, 32]``."""
 
     batch, length, model_dim = value.shape
     width = width or model_dim
-    vt = torch.zeros(batch, width, _round_up(max(length, 1), TOKEN_PAD), dtype=value.dtype, device=value.device)
-    vt[:, :model_dim, :length].copy_(value.detach().transpose(1, 2))
+    padded = _round_up(max(length, 1), TOKEN_PAD)
+    vt = torch.zeros(batch, padded // 32, width, 32, dtype=value.dtype, device=value.device)
+    src = torch.zeros(batch, padded, width, dtype=value.dtype, device=value.device)
+    src[:, :length, :model_dim].copy_(value.detach())
+    vt.copy_(src.view(batch, padded // 32, 32, width).transpose(2, 3))
     return vt
 
 
@@ -357,7 +370,7 @@ def _attention_forward(query: Tensor, key: Tensor, value: Tensor, scales: Tensor
         lib.da_routed_attention(
             q.data_ptr(), k.data_ptr(),
             maps * length * score_width, score_width, length * score_width, 1, score_width,
-            vt.data_ptr(), vt.stride(0), vt.stride(1),
+            vt.data_ptr(), vt.stride(0),
             batch, maps, length, value_width,
             scales_c.data_ptr(), dtype_code(scales_c.dtype), 1.0, None, _lib.DA_F32,
             _lib.DA_ATTN_CAUSAL if causal else 0,
@@ -445,14 +458,15 @@ def linear_hip(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
 def qkv_projection_hip(
     x: Tensor, query_weight: Tensor, key_weight: Tensor, value_weight: Tensor, value_bias: Tensor | None
 ) -> tuple[Tensor, Tensor]:
-    """Q/K projections ``[B, T, 2W]`` and padded V^T ``[B, D, Tp]`` in one launch."""
+    """Q/K projections ``[B, T, 2W]`` and padded V^T ``[B, Tp/32, D, 32]`` in one launch."""
 
     batch, length, model_dim = x.shape
     width = query_weight.shape[0]
     code = _half_code(x.dtype)
     xc = x.contiguous()
     qk = torch.empty(batch, length, 2 * width, dtype=x.dtype, device=x.device)
-    vt = torch.zeros(batch, value_weight.shape[0], _round_up(length, TOKEN_PAD), dtype=x.dtype, device=x.device)
+    padded = _round_up(length, TOKEN_PAD)
+    vt = torch.empty(batch, padded // 32, value_weight.shape[0], 32, dtype=x.dtype, device=x.device)
     b = None if value_bias is None else value_bias.detach().contiguous()
     lib = _lib.get()
     _lib.check(
@@ -461,7 +475,7 @@ def qkv_projection_hip(
             query_weight.contiguous().data_ptr(), key_weight.contiguous().data_ptr(), width,
             value_weight.contiguous().data_ptr(), _ptr(b), value_weight.shape[0],
             dtype_code(b.dtype) if b is not None else _lib.DA_F32, code,
-            qk.data_ptr(), vt.data_ptr(), vt.stride(0), vt.stride(1), _stream(x.device),
+            qk.data_ptr(), vt.data_ptr(), vt.stride(0), padded, _stream(x.device),
         ),
         "qkv_projection_hip",
     )

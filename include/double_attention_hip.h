@@ -82,7 +82,9 @@ int64_t da_padded_length(int64_t length);
  *   raw_key, raw_value: [routing_dim, atoms] row-major, dtype raw_dtype
  *                       (raw_value NULL = tied bank: key atoms serve both roles)
  *   key_t:  out [da_padded_atoms(atoms), routing_dim]   atom-major, key_dtype
- *   value:  out [routing_dim, da_padded_atoms(atoms)]   coordinate-major, fp16
+ *   value:  out, fp16, 32-atom tiles: coordinate r of atom j at
+ *           value[(j/32)*32*routing_dim + 32*r + j%32]
+ *           (da_padded_atoms(atoms) * routing_dim elements)
  * Atom j becomes raw[:, j] / max(||raw[:, j]||, eps); padding atoms are zero.
  * routing_dim must be 64, 128, 256 or 512; key_dtype DA_F16 or DA_BF16.
  */
@@ -115,8 +117,9 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  *   query/key row of (batch b, token t, map s) starts at
  *       base + b*stride_b + t*stride_t + (s / map_repeat) * map_stride
  *     and holds score_dim elements.
- *   value_t: V^T, element (b, d, t) at value_t[b*vt_stride_b + d*vt_stride_d + t];
- *     vt_stride_d >= da_padded_length(length).
+ *   value_t: V^T in 32-token tiles, element (b, d, t) at
+ *     value_t[b*vt_stride_b + (t/32)*32*value_dim + 32*d + t%32];
+ *     vt_stride_b >= value_dim * da_padded_length(length).
  *   scales: [maps] device tensor (gamma_s, or log gamma_s with
  *     DA_ATTN_SCALES_ARE_LOG); every gamma is multiplied by scale_mult.
  *   DA_ATTN_MIX: out(b, t) = sum_s alpha_s O_s(b, t), alpha = softmax(mix_logits)
@@ -124,12 +127,12 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  *     out + b*out_stride_b + t*out_stride_t + s*out_stride_s.
  * score_dim and value_dim must be 64, 128, 256 or 512.  Element types:
  *   (qk_dtype, v_dtype) in {(F16, BF16), (F16, F16), (BF16, BF16)}; the output
- *   has v_dtype.  V^T padding columns (tokens length..vt_stride_d-1) must hold
+ *   has v_dtype.  V^T padding tokens (length .. padded length - 1) must hold
  *   finite values.
  */
 int da_routed_attention(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
                         int64_t map_stride, int64_t map_repeat, int64_t score_dim,
-                        const void* value_t, int64_t vt_stride_b, int64_t vt_stride_d,
+                        const void* value_t, int64_t vt_stride_b,
                         int64_t batch, int64_t maps, int64_t length, int64_t value_dim,
                         const void* scales, int scales_dtype, float scale_mult,
                         const void* mix_logits, int mix_dtype, int flags, int qk_dtype,
@@ -139,11 +142,13 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
 /*
  * Q/K and V projections in one launch (modules.py:143-157 and 212):
  *   qk_out [tokens, 2*qk_width] = x @ [wq; wk]^T   (row n: query features, then key features)
- *   value_t[b, f, t]            = (x @ wv^T + bv)[b*length + t, f]
+ *   value_t (b, f, t)           = (x @ wv^T + bv)[b*length + t, f], in the 32-token
+ *                                 tile layout of da_routed_attention
  *   x: [tokens, model_dim] with tokens = batch*length; wq, wk: [qk_width, model_dim];
  *   wv: [value_dim, model_dim]; bv: [value_dim] of bias_dtype or NULL.
- *   value_t pitch: vt_stride_b per sequence, vt_pitch = da_padded_length(length)
- *   per feature row; the padding tokens are filled with finite values.
+ *   vt_stride_b per sequence (>= value_dim * vt_pitch); vt_pitch (a multiple
+ *   of 64, >= length) tokens are written per sequence, the padding ones with
+ *   finite values.
  */
 int da_qkv_projection(const void* x, int64_t tokens, int64_t model_dim, int64_t length,
                       const void* wq, const void* wk, int64_t qk_width, const void* wv,
@@ -181,7 +186,7 @@ typedef struct da_sda_forward_args {
 
 /* Workspace layout (byte offsets, each 256-aligned):
  *   routed [tokens, 2*qk_width]   Q/K projections, routed in place (fp16 out)
- *   value_t [batch, model_dim, da_padded_length(length)]
+ *   value_t [batch, padded_length/32, model_dim, 32]  (32-token tiles)
  *   mixed  [tokens, model_dim or maps*model_dim] (only with an output projection) */
 int64_t da_sda_workspace_bytes(int64_t batch, int64_t length, int64_t model_dim,
                                int64_t qk_width, int64_t outer_maps, int concat,

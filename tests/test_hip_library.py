@@ -77,23 +77,23 @@ def test_attention_rejects_bad_arguments_before_launch() -> None:
     h = lib.get()
     base = [
         _fake(), _fake(), 512 * 256, 256, 512 * 256, 1, 256,  # q, k, strides, map stride/repeat, score dim
-        _fake(), 512 * 512, 512,  # value_t pitches
-        1, 1, 512, 512,  # batch, maps, length, value dim
+        _fake(), 512 * 512,  # value_t, per-sequence pitch
+        2, 1, 512, 512,  # batch, maps, length, value dim
         _fake(), lib.DA_F32, 1.0, None, lib.DA_F32,
         lib.DA_ATTN_CAUSAL, lib.DA_F16, lib.DA_BF16, _fake(), 512 * 512, 512, 0, None,
     ]
     bad_types = list(base)
-    bad_types[20], bad_types[21] = lib.DA_BF16, lib.DA_F16
+    bad_types[19], bad_types[20] = lib.DA_BF16, lib.DA_F16
     assert h.da_routed_attention(*bad_types) == -2
     bad_dim = list(base)
     bad_dim[6] = 384
     assert h.da_routed_attention(*bad_dim) == -2
     short_pitch = list(base)
-    short_pitch[9] = 448   # vt_stride_d below the padded length 512
+    short_pitch[8] = 512 * 448   # per-sequence pitch below value_dim * padded length
     assert h.da_routed_attention(*short_pitch) == -3
     assert "padded length" in h.da_last_error().decode()
     no_scales = list(base)
-    no_scales[14] = None
+    no_scales[13] = None
     assert h.da_routed_attention(*no_scales) == -1
 
 

@@ -83,7 +83,8 @@ def test_dictionary_normalize(key_dtype, raw_dtype, routing_dim, atoms, tied) ->
     padded = layout.key_t.shape[0]
     assert padded % 64 == 0 and padded >= atoms
     assert torch.count_nonzero(layout.key_t[atoms:]) == 0
-    assert torch.count_nonzero(layout.value[:, atoms:]) == 0
+    assert layout.value.shape == (padded // 32, routing_dim, 32)
+    assert torch.count_nonzero(da.hip_ops._untile_value(layout.value)[:, atoms:]) == 0
 
 
 # ---------------------------------------------------------------- GEMMs
@@ -117,7 +118,10 @@ def test_qkv_projection(batch, length, width) -> None:
     assert_parity(qk[..., :width], xn @ np32(wq).T, label="proj q")
     assert_parity(qk[..., width:], xn @ np32(wk).T, label="proj k")
     v = xn @ np32(wv).T + np32(bv)
-    assert_parity(vt[:, :, :length], v.transpose(0, 2, 1), label="proj v^T")
+    # V^T comes in 32-token tiles [B, Tp/32, D, 32]; untile to [B, Tp, D].
+    untiled = vt.transpose(2, 3).reshape(batch, -1, d)
+    assert_parity(untiled[:, :length], v, label="proj v^T")
+    assert torch.isfinite(untiled.float()).all()
 
 
 # ---------------------------------------------------------------- dictionary route
