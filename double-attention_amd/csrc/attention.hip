@@ -8,20 +8,23 @@
 // or every O_s written to its own slot (per-map mode, used by the concat
 // combine and by the operator-level API).
 //
-// A workgroup of four waves owns 64 query rows of one sequence: wave w takes
-// the 32 queries of group w%2 (two 16-column MFMA blocks) and half w/2 of the
-// value width.  It walks the (map, 32-key tile) sequence up to the causal
-// bound in the transposed domain:
+// A workgroup of NW waves (2 or 4) owns 32*NW query rows of one sequence and
+// a slice of DS value features; every wave owns 32 queries (two 16-column MFMA
+// blocks) and the whole slice, so no score tile is formed twice inside a
+// workgroup.  The value width is split over workgroups (DS <= 128) to keep a
+// wave's accumulators small enough for two waves per SIMD.  A wave walks the
+// (map, 32-key tile) sequence up to the causal bound in the transposed domain:
 //   S^T[key, q] = sum_r K[key, r] Q^T[r, q]      (A = key rows from LDS, B = queries in VGPRs)
 //   O^T[d, q]  += sum_key V^T[d, key] P^T[key, q] (A = V^T from LDS, B = P in VGPRs)
 // so P never leaves registers, and every A fragment read from LDS feeds two
 // MFMAs (the two query blocks).  Key and V^T tiles are double-buffered in
-// padded LDS tiles (da_tile.h) filled by global->LDS DMA while the previous
-// tile is multiplied.  V^T arrives from the projection GEMM in 32-token tiles
-// (element (b, d, t) at b*stride_b + (t/32)*32*D + 32*d + t%32), so each V tile
-// is one contiguous block.  gamma_s = exp(clamp(log scale)) and the mix
-// weights are computed on the device: a forward never synchronizes with the
-// host.
+// padded LDS tiles (da_tile.h) filled by global->LDS DMA; the loads of the next
+// tile are spread through the score loop, so no wave stalls on a full memory
+// queue in one burst.  V^T arrives from the projection GEMM in 32-token tiles
+// (element (b, d, t) at b*stride_b + (t/32)*32*D + 32*d + t%32), so each
+// slice of a V tile is one contiguous block.  gamma_s = exp(clamp(log scale))
+// and the mix weights are computed on the device: a forward never
+// synchronizes with the host.
 //
 // Element types: TQ for the routed queries/keys (fp16 on the module path: they
 // are unit vectors), TV for V, the probabilities and the output.
@@ -32,9 +35,7 @@
 namespace da {
 
 constexpr int kKeyTile = 32;
-constexpr int kAttnWaves = 4;   // 2 query groups x 2 value halves
 constexpr int kAttnQW = 32;     // queries per wave
-constexpr int kAttnQT = 64;     // queries per workgroup
 
 struct AttnParams {
   const void* q;
@@ -43,7 +44,8 @@ struct AttnParams {
   int map_repeat;
   const void* vt;
   int64_t vt_stride_b;
-  int S, T;
+  int S, T, D;
+  int n_qt, n_slices;
   const void* scales;
   int scales_dtype;
   float scale_mult;
@@ -85,24 +87,26 @@ __device__ __forceinline__ void store_rows(const AttnParams& p, int b, int s, in
   }
 }
 
-template <int RP, int D>
+template <int RP, int DS, int NW>
 struct AttnTile {
   typedef PaddedTile<kKeyTile, RP / 8, true> KT;    // keys (blocked rows)
-  typedef PaddedTile<D, kKeyTile / 8, false> VT;    // V^T rows: D features x 4 chunks
-  static constexpr int LOADS = KT::LOADS + VT::LOADS;
-  static constexpr int PER_WAVE = (LOADS + kAttnWaves - 1) / kAttnWaves;
-  static constexpr int BYTES = LOADS * 1024;        // K tile, then V^T tile
+  typedef PaddedTile<DS, kKeyTile / 8, false> VT;   // V^T rows: DS features x 4 chunks
+  static constexpr int KPW = (KT::LOADS + NW - 1) / NW;   // key loads per wave
+  static constexpr int VPW = (VT::LOADS + NW - 1) / NW;   // V^T loads per wave
+  static constexpr int BYTES = KT::BYTES + VT::BYTES;     // K tile, then V^T tile
 };
 
-template <typename TQ, typename TV, int RP, int D, bool MULTI>
-__global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnParams p) {
-  typedef AttnTile<RP, D> Tile;
+template <typename TQ, typename TV, int RP, int DS, int NW, bool MULTI>
+__global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
+  typedef AttnTile<RP, DS, NW> Tile;
   typedef typename Tile::KT KT;
   typedef typename Tile::VT VT;
   typedef typename Elem<TQ>::v8 q8;
+  typedef typename Elem<TV>::v8 v8;
   constexpr int KS = RP / 32;
-  constexpr int DC = D / 2;      // value columns per wave
-  constexpr int NB = DC / 16;    // accumulator blocks per query block
+  constexpr int NB = DS / 16;    // accumulator blocks per query block
+  constexpr int NL = Tile::KPW + Tile::VPW;
+  constexpr int QT = NW * kAttnQW;
   __shared__ __attribute__((aligned(1024))) char lds0[Tile::BYTES];
   __shared__ __attribute__((aligned(1024))) char lds1[Tile::BYTES];
 
@@ -110,55 +114,75 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnParams p
   const int c = lane & 15;
   const int g = lane >> 4;
   const int wave = uniform_wave();
-  const int qg = wave & 1;
-  const int d0 = (wave >> 1) * DC;
-  const int n_qt = (p.T + kAttnQT - 1) / kAttnQT;
-  const int qt = n_qt - 1 - static_cast<int>(blockIdx.x);   // heaviest causal tiles first
-  const int b = blockIdx.y;
-  const int q0 = qt * kAttnQT;
-  const int qw0 = q0 + qg * kAttnQW;                         // this wave's first query
+  // blockIdx.y ranks query tiles heaviest (causal) first; x = (sequence, slice).
+  const int qt = p.n_qt - 1 - static_cast<int>(blockIdx.y);
+  const int b = static_cast<int>(blockIdx.x) / p.n_slices;
+  const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;   // first feature of the slice
+  const int q0 = qt * QT;
+  const int qw0 = q0 + wave * kAttnQW;                       // this wave's first query
   const bool causal = p.flags & kAttnCausal;
-  const int q_last = min(q0 + kAttnQT, p.T) - 1;
+  const int q_last = min(q0 + QT, p.T) - 1;
   const int n_kt = causal ? q_last / kKeyTile + 1 : (p.T + kKeyTile - 1) / kKeyTile;
   const int total = p.S * n_kt;
 
   const TQ* qbase = static_cast<const TQ*>(p.q) + b * p.qk_stride_b;
-  const TQ* kbase = static_cast<const TQ*>(p.k) + b * p.qk_stride_b;
-  const TV* vtb = static_cast<const TV*>(p.vt) + b * p.vt_stride_b;
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const TQ*>(p.k) + b * p.qk_stride_b);
+  // Feature d of a 32-token V^T tile sits at 32*d, so the slice is one block.
+  const char* vbase = reinterpret_cast<const char*>(static_cast<const TV*>(p.vt) + b * p.vt_stride_b + 32 * ds0);
+  const int kstride = static_cast<int>(p.qk_stride_t) * static_cast<int>(sizeof(TQ));   // bytes per key row
 
-  // Per-lane DMA descriptors of this wave's share of a tile: key loads keep
-  // (row, chunk*8) packed, V^T loads their element offset inside the tile.
-  int desc[Tile::PER_WAVE];
+  // Per-lane DMA sources of this wave's loads, as byte offsets from the tile's
+  // base: key load i fills wave load i*NW + wave of the key tile (row in the
+  // top five bits, for clamping the last tile), V^T load i the same wave load
+  // of the V^T tile.  Out-of-range wave loads of a partial last round re-load
+  // slot data of load 0 into their own slots, which nothing reads.
+  uint32_t kdesc[Tile::KPW], vdesc[Tile::VPW];
 #pragma unroll
-  for (int i = 0; i < Tile::PER_WAVE; ++i) {
-    const int j = i * kAttnWaves + wave;
-    int row = 0, ck = 0;
-    if (j < KT::LOADS) {
-      KT::slot_chunk(j * 64 + lane, row, ck);
-      desc[i] = (row << 16) | (ck * 8);
-    } else if (j < Tile::LOADS) {
-      VT::slot_chunk((j - KT::LOADS) * 64 + lane, row, ck);
-      desc[i] = row * kKeyTile + ck * 8;
-    } else {
-      desc[i] = 0;
-    }
+  for (int i = 0; i < Tile::KPW; ++i) {
+    int row, ck;
+    const int j = i * NW + wave;
+    KT::slot_chunk((j < KT::LOADS ? j : 0) * 64 + lane, row, ck);
+    kdesc[i] = (static_cast<uint32_t>(row) << 27) | static_cast<uint32_t>(row * kstride + ck * 16);
   }
-  auto issue = [&](char* buf, int u) {
-    const int s = u / n_kt;
-    const int k0 = (u - s * n_kt) * kKeyTile;
-    const int64_t off = static_cast<int64_t>(s / p.map_repeat) * p.map_stride;
-    const TQ* ktile = kbase + static_cast<int64_t>(k0) * p.qk_stride_t + off;
-    const TV* vtile = vtb + static_cast<int64_t>(k0) * D;   // 32-token tile k0/32
-    const int last = p.T - 1 - k0;                           // keys past the end re-read the last one
 #pragma unroll
-    for (int i = 0; i < Tile::PER_WAVE; ++i) {
-      const int j = i * kAttnWaves + wave;
-      if (j < KT::LOADS) {
-        const int row = min(desc[i] >> 16, last);
-        dma16(ktile + static_cast<int64_t>(row) * p.qk_stride_t + (desc[i] & 0xffff), buf + j * 1024);
-      } else if (j < Tile::LOADS) {
-        dma16(vtile + desc[i], buf + j * 1024);
+  for (int i = 0; i < Tile::VPW; ++i) {
+    int row, ck;
+    const int j = i * NW + wave;
+    VT::slot_chunk((j < VT::LOADS ? j : 0) * 64 + lane, row, ck);
+    vdesc[i] = static_cast<uint32_t>((row * kKeyTile + ck * 8) * sizeof(TV));
+  }
+  // LDS slot of load n (K loads first); loads past a tile's end rewrite slot 0.
+  auto slot_of = [&](int n) {
+    if (n < Tile::KPW) {
+      const int j = n * NW + wave;
+      return j < KT::LOADS ? j * 1024 : 0;
+    }
+    const int j = (n - Tile::KPW) * NW + wave;
+    return KT::BYTES + (j < VT::LOADS ? j * 1024 : 0);
+  };
+  // Tile u = (map s, key tile kt): byte bases and the clamp row (keys past the
+  // end re-read the last one; only the final key tile has any).
+  struct Src {
+    const char* k;
+    const char* v;
+    int last;
+  };
+  auto source = [&](int s, int kt) {
+    const int k0 = kt * kKeyTile;
+    const int64_t off = static_cast<int64_t>(s / p.map_repeat) * p.map_stride * static_cast<int64_t>(sizeof(TQ));
+    return Src{kbase + static_cast<int64_t>(k0) * kstride + off,
+               vbase + static_cast<int64_t>(k0) * p.D * static_cast<int64_t>(sizeof(TV)), p.T - 1 - k0};
+  };
+  auto issue_one = [&](char* buf, const Src& src, int n) {
+    if (n < Tile::KPW) {
+      uint32_t off = kdesc[n] & 0x07FFFFFFu;
+      if (src.last < kKeyTile - 1) {
+        const int over = static_cast<int>(kdesc[n] >> 27) - src.last;
+        if (over > 0) off -= static_cast<uint32_t>(over * kstride);
       }
+      dma16(src.k + off, buf + slot_of(n));
+    } else {
+      dma16(src.v + vdesc[n - Tile::KPW], buf + slot_of(n));
     }
   };
 
@@ -178,85 +202,137 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnParams p
 
   auto load_map = [&](int s) {
     const int64_t off = static_cast<int64_t>(s / p.map_repeat) * p.map_stride;
-    sc = map_gamma(p, s) * kLog2e;
+    // The rescale test compares maxima of raw scores, so a negative score
+    // scale is folded into the queries instead (negation is exact).
+    const float gamma = map_gamma(p, s);
+    sc = fabsf(gamma) * kLog2e;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const int tq = qw0 + cb * 16 + c;
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk)
+      for (int kk = 0; kk < KS; ++kk) {
         qf[cb][kk] = tq < p.T ? load8(qbase + static_cast<int64_t>(tq) * p.qk_stride_t + off + kk * 32 + 8 * g)
                               : zero8<TQ>();
+        if (gamma < 0.f) qf[cb][kk] = -qf[cb][kk];
+      }
     }
   };
 
-  // Lane-relative LDS bases of the fragment reads.
+  // Lane-relative LDS offsets of the fragment reads.
   const int kfrag = KT::offset(c, g);
-  const int vfrag = KT::BYTES + VT::offset(d0 + c, g);
+  const int vfrag = KT::BYTES + VT::offset(c, g);
 
-  auto step = [&](int u, char* cur, char* nxt) {
-    wait_vmem();
-    __syncthreads();
-    if (u + 1 < total) issue(nxt, u + 1);
-    const int s = u / n_kt;
-    const int kt = u - s * n_kt;
+  load_map(0);
+  {
+    const Src src0 = source(0, 0);
+#pragma unroll
+    for (int n = 0; n < NL; ++n) issue_one(lds0, src0, n);
+  }
+
+  int s = 0, kt = 0;
+  for (int u = 0; u < total; ++u) {
+    char* cur = (u & 1) ? lds1 : lds0;
+    char* nxt = (u & 1) ? lds0 : lds1;
+    // Tile u + 1; the last step reloads its own tile into the idle buffer.
+    int s_n = s, kt_n = kt + 1;
+    if (kt_n == n_kt) {
+      kt_n = 0;
+      ++s_n;
+    }
+    if (s_n == p.S) {
+      s_n = s;
+      kt_n = kt;
+    }
+    const Src src = source(s_n, kt_n);
     const int k0 = kt * kKeyTile;
 
-    // Scores for 32 keys x 32 queries: four independent accumulator chains,
-    // each key fragment feeding both query blocks.
-    f32x4 st[2][2] = {{zero4(), zero4()}, {zero4(), zero4()}};
-    const char* kf = cur + kfrag;
+    wait_vmem();
+    __syncthreads();
+
+    if (!(causal && k0 > qw0 + kAttnQW - 1)) {   // else the tile lies above this wave's causal bound
+      // Scores for 32 keys x 32 queries: four independent accumulator chains,
+      // each key fragment feeding both query blocks; the next tile's loads are
+      // spread between the fragment reads.
+      f32x4 st[2][2] = {{zero4(), zero4()}, {zero4(), zero4()}};
+      const char* kf = cur + kfrag;
+      // Software pipeline: the fragments of step kk + 1 are read while the
+      // MFMAs of step kk run; scheduling barriers keep the compiler from
+      // hoisting every read (which would cost the second wave per SIMD).
+      q8 a0 = lds_v8<TQ>(kf + KT::offset(0, 0));
+      q8 a1 = lds_v8<TQ>(kf + KT::offset(16, 0));
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      const q8 a0 = lds_v8<TQ>(kf + KT::offset(0, kk * 4));
-      const q8 a1 = lds_v8<TQ>(kf + KT::offset(16, kk * 4));
+      for (int kk = 0; kk < KS; ++kk) {
+        q8 n0 = a0, n1 = a1;
+        if (kk + 1 < KS) {
+          n0 = lds_v8<TQ>(kf + KT::offset(0, (kk + 1) * 4));
+          n1 = lds_v8<TQ>(kf + KT::offset(16, (kk + 1) * 4));
+        }
+#pragma unroll
+        for (int n = 0; n < NL; ++n)
+          if (n * KS / NL == kk) issue_one(nxt, src, n);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          st[cb][0] = Elem<TQ>::mma(a0, qf[cb][kk], st[cb][0]);
+          st[cb][1] = Elem<TQ>::mma(a1, qf[cb][kk], st[cb][1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        a0 = n0;
+        a1 = n1;
+      }
+      // The first V^T fragments do not depend on the scores: read them before
+      // the softmax.
+      const char* vf = cur + vfrag;
+      v8 va = lds_v8<TV>(vf + VT::offset(0, 0));
+      v8 vb = lds_v8<TV>(vf + VT::offset(NB > 1 ? 16 : 0, 0));
+
+      // Lane (c, g) holds keys k0 + 8g + 4kb + i for query qw0 + 16cb + c.
+      // Only tiles on the causal diagonal or past the end carry masked keys.
+      if ((causal && k0 + kKeyTile - 1 > qw0) || k0 + kKeyTile > p.T) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const int tq = qw0 + cb * 16 + c;
+          const int kmax = min(causal ? tq : p.T - 1, p.T - 1);   // last key this query sees
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (k0 + 8 * g + 4 * kb + i > kmax) st[cb][kb][i] = -INFINITY;
+        }
+      }
+      v8 pb[2];
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
-        st[cb][0] = Elem<TQ>::mma(a0, qf[cb][kk], st[cb][0]);
-        st[cb][1] = Elem<TQ>::mma(a1, qf[cb][kk], st[cb][1]);
-      }
-    }
-    // Lane (c, g) holds keys k0 + 8g + 4kb + i for query qw0 + 16cb + c.
-    const bool masked = (causal && k0 + kKeyTile - 1 > qw0) || k0 + kKeyTile > p.T;
-    typename Elem<TV>::v8 pb[2];
+        const float lmax = fmaxf(fmaxf(fmaxf(st[cb][0][0], st[cb][0][1]), fmaxf(st[cb][0][2], st[cb][0][3])),
+                                 fmaxf(fmaxf(st[cb][1][0], st[cb][1][1]), fmaxf(st[cb][1][2], st[cb][1][3])));
+        lazy_rescale<NB>(lmax, sc, m_run[cb], l_part[cb], acc[cb]);
+        const float m_use = m_run[cb] == -INFINITY ? 0.f : m_run[cb];   // fully masked so far
+        float psum = 0.f;
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const int tq = qw0 + cb * 16 + c;
-      float tmax = -INFINITY;
+        for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = st[cb][kb][i] * sc;
-          if (masked) {
-            const int key = k0 + 8 * g + 4 * kb + i;
-            if (key >= p.T || (causal && key > tq)) v = -INFINITY;
+          for (int i = 0; i < 4; ++i) {
+            const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(st[cb][kb][i], sc, -m_use));
+            st[cb][kb][i] = pr;
+            psum += pr;
           }
-          st[cb][kb][i] = v;
-          tmax = fmaxf(tmax, v);
         }
+        l_part[cb] += psum;
+        pb[cb] = pack_blocked<TV>(st[cb][0], st[cb][1]);   // keys k0 + 8g + e
       }
-      lazy_rescale<NB>(group_max(tmax), m_run[cb], l_part[cb], acc[cb]);
-      const float m_use = m_run[cb] == -INFINITY ? 0.f : m_run[cb];   // fully masked so far
-      float psum = 0.f;
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pr = __builtin_amdgcn_exp2f(st[cb][kb][i] - m_use);
-          st[cb][kb][i] = pr;
-          psum += pr;
-        }
+      for (int db = 0; db < NB; ++db) {
+        v8 vn = vb;
+        if (db + 2 < NB) vn = lds_v8<TV>(vf + VT::offset((db + 2) * 16, 0));
+        acc[0][db] = Elem<TV>::mma(va, pb[0], acc[0][db]);
+        acc[1][db] = Elem<TV>::mma(va, pb[1], acc[1][db]);
+        __builtin_amdgcn_sched_barrier(0);
+        va = vb;
+        vb = vn;
       }
-      l_part[cb] += psum;
-      pb[cb] = pack_blocked<TV>(st[cb][0], st[cb][1]);   // keys k0 + 8g + e
-    }
-
-    const char* vf = cur + vfrag;
+    } else {
 #pragma unroll
-    for (int db = 0; db < NB; ++db) {
-      const typename Elem<TV>::v8 a = lds_v8<TV>(vf + VT::offset(db * 16, 0));
-      acc[0][db] = Elem<TV>::mma(a, pb[0], acc[0][db]);
-      acc[1][db] = Elem<TV>::mma(a, pb[1], acc[1][db]);
+      for (int n = 0; n < NL; ++n) issue_one(nxt, src, n);
     }
 
     if (kt == n_kt - 1) {   // map s complete
@@ -270,7 +346,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnParams p
 #pragma unroll
           for (int i = 0; i < NB; ++i) yacc[cb][i] += acc[cb][i] * w;
         } else {
-          if (tq < p.T) store_rows<TV, DC>(p, b, (p.flags & kAttnMix) ? 0 : s, tq, g, d0, acc[cb], w);
+          if (tq < p.T) store_rows<TV, DS>(p, b, (p.flags & kAttnMix) ? 0 : s, tq, g, ds0, acc[cb], w);
         }
 #pragma unroll
         for (int i = 0; i < NB; ++i) acc[cb][i] = zero4();
@@ -278,51 +354,54 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnParams p
         l_part[cb] = 0.f;
       }
       if (s + 1 < p.S) load_map(s + 1);
+      kt = 0;
+      ++s;
+    } else {
+      ++kt;
     }
-  };
-
-  load_map(0);
-  issue(lds0, 0);
-  int u = 0;
-  for (; u + 1 < total; u += 2) {
-    step(u, lds0, lds1);
-    step(u + 1, lds1, lds0);
   }
-  if (u < total) step(u, lds0, lds1);
 
   if constexpr (MULTI) {
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const int tq = qw0 + cb * 16 + c;
-      if (tq < p.T) store_rows<TV, DC>(p, b, 0, tq, g, d0, yacc[cb], 1.f);
+      if (tq < p.T) store_rows<TV, DS>(p, b, 0, tq, g, ds0, yacc[cb], 1.f);
     }
   }
 }
 
-template <typename TQ, typename TV, int RP, int D, bool MULTI>
-static void launch_attn_3(const AttentionArgs& a, const AttnParams& p, hipStream_t s) {
-  const int n_qt = (a.T + kAttnQT - 1) / kAttnQT;
-  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, D, MULTI>), dim3(n_qt, a.B), dim3(kAttnWaves * 64), 0, s, p);
+// Workgroups of four waves when there are enough of them to fill the chip
+// twice over, else of two waves (more, smaller workgroups).
+template <typename TQ, typename TV, int RP, int DS, bool MULTI>
+static void launch_attn_3(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
+  p.n_slices = a.D / DS;
+  const int64_t wg4 = static_cast<int64_t>(a.B) * p.n_slices * ((a.T + 127) / 128);
+  if (wg4 >= 512) {
+    p.n_qt = static_cast<int>((a.T + 127) / 128);
+    hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 4, MULTI>), dim3(a.B * p.n_slices, p.n_qt), dim3(256), 0,
+                       s, p);
+  } else {
+    p.n_qt = static_cast<int>((a.T + 63) / 64);
+    hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 2, MULTI>), dim3(a.B * p.n_slices, p.n_qt), dim3(128), 0,
+                       s, p);
+  }
 }
 
-template <typename TQ, typename TV, int RP, int D>
-static void launch_attn_2(const AttentionArgs& a, const AttnParams& p, hipStream_t s) {
-  if ((a.flags & kAttnMix) && a.S > 1) launch_attn_3<TQ, TV, RP, D, true>(a, p, s);
-  else launch_attn_3<TQ, TV, RP, D, false>(a, p, s);
-}
-
+// Value slice per workgroup: 128 features (64 when the value width is 64).
 template <typename TQ, typename TV, int RP>
-static void launch_attn_1(const AttentionArgs& a, const AttnParams& p, hipStream_t s) {
-  switch (a.D) {
-    case 64: launch_attn_2<TQ, TV, RP, 64>(a, p, s); break;
-    case 128: launch_attn_2<TQ, TV, RP, 128>(a, p, s); break;
-    case 256: launch_attn_2<TQ, TV, RP, 256>(a, p, s); break;
-    default: launch_attn_2<TQ, TV, RP, 512>(a, p, s); break;
+static void launch_attn_1(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
+  const bool multi = (a.flags & kAttnMix) && a.S > 1;
+  if (a.D == 64) {
+    if (multi) launch_attn_3<TQ, TV, RP, 64, true>(a, p, s);
+    else launch_attn_3<TQ, TV, RP, 64, false>(a, p, s);
+  } else {
+    if (multi) launch_attn_3<TQ, TV, RP, 128, true>(a, p, s);
+    else launch_attn_3<TQ, TV, RP, 128, false>(a, p, s);
   }
 }
 
 template <typename TQ, typename TV>
-static void launch_attn_0(const AttentionArgs& a, const AttnParams& p, hipStream_t s) {
+static void launch_attn_0(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
   switch (a.RP) {
     case 64: launch_attn_1<TQ, TV, 64>(a, p, s); break;
     case 128: launch_attn_1<TQ, TV, 128>(a, p, s); break;
@@ -344,6 +423,7 @@ void launch_routed_attention(const AttentionArgs& a, hipStream_t stream) {
   p.vt_stride_b = a.vt_stride_b;
   p.S = a.S;
   p.T = a.T;
+  p.D = static_cast<int>(a.D);
   p.scales = a.scales;
   p.scales_dtype = a.scales_dtype;
   p.scale_mult = a.scale_mult;

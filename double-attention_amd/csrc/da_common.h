@@ -59,17 +59,32 @@ __device__ __forceinline__ float load_scalar(const void* p, int dtype, int64_t i
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
-// Butterfly reductions across the four 16-lane groups (lanes c, c+16, c+32,
-// c+48 hold the same accumulator column).
+// Reductions across the four 16-lane rows (lanes c, c+16, c+32, c+48 hold the
+// same accumulator column), with gfx950's v_permlane32_swap / v_permlane16_swap:
+// swapping a value with itself leaves the two halves (rows) exchanged between
+// the pair of results, so one VALU op pairs lane l with lane l^32 (l^16) and no
+// LDS round trip is needed.
+__device__ __forceinline__ void lane_pair32(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void lane_pair16(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
 __device__ __forceinline__ float group_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  float a, b;
+  lane_pair32(v, a, b);
+  lane_pair16(fmaxf(a, b), a, b);
+  return fmaxf(a, b);
 }
 __device__ __forceinline__ float group_sum(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  float a, b;
+  lane_pair32(v, a, b);
+  lane_pair16(a + b, a, b);
+  return a + b;
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
@@ -77,20 +92,24 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// Online-softmax bookkeeping with lazy rescaling.  `tile_max` is this tile's
-// row maximum (log2 domain, already reduced over the lane groups).  The
-// running reference max only moves -- and the accumulators are rescaled --
-// when a row maximum exceeds it by more than kRescaleSlack, so exponentials
-// stay <= 2^kRescaleSlack (exact in fp16/bf16 operands) and most tiles skip
-// the rescale.  The branch is taken by the whole wave if any row needs it;
-// rows that do not need it use factor 1.  The common factor 2^-m cancels in
-// the final division by the row sum.
+// Online-softmax bookkeeping with lazy rescaling, in the log2 domain.  Each
+// lane holds raw scores of one accumulator column c; the exponent of a score s
+// is s * scale - m, where m (column-uniform) is a running reference maximum.
+// m only moves -- and the accumulators are rescaled -- when some score exceeds
+// it by more than kRescaleSlack, so exponentials stay <= 2^kRescaleSlack
+// (exact in fp16/bf16 operands) and most tiles skip both the rescale and the
+// cross-lane maximum: the test uses each lane's own maximum, and only when
+// the wave's ballot says some lane exceeded does it reduce the column maxima
+// across the lane rows.  Columns that do not need it keep factor 1; the common
+// factor 2^-m cancels in the final division by the row sum.
 constexpr float kRescaleSlack = 8.f;
 
 template <int N>
-__device__ __forceinline__ void lazy_rescale(float tile_max, float& m_run, float& l_part, f32x4* acc) {
-  const bool need = tile_max > m_run + kRescaleSlack;
-  if (__ballot(need)) {
+__device__ __forceinline__ void lazy_rescale(float lane_max, float scale, float& m_run, float& l_part,
+                                             f32x4* acc) {
+  if (__ballot(lane_max * scale > m_run + kRescaleSlack)) {
+    const float tile_max = group_max(lane_max) * scale;
+    const bool need = tile_max > m_run + kRescaleSlack;
     const float alpha = need ? exp2f(m_run - tile_max) : 1.f;
     if (need) m_run = tile_max;
     l_part *= alpha;

@@ -36,8 +36,8 @@ constexpr int kRouteWaves = 4;
 
 template <int R>
 struct RouteCfg {
-  static constexpr int QW = R >= 512 ? 16 : 32;   // rows per wave
-  static constexpr int AT = R >= 512 ? 32 : 64;   // atoms per tile
+  static constexpr int QW = 16;                   // rows per wave
+  static constexpr int AT = 32;                   // atoms per tile
   typedef PaddedTile<AT, R / 8, true> KT;         // key atoms (blocked rows)
   typedef PaddedTile<R, AT / 8, false> VT;        // value coordinates x atoms
   static constexpr int LOADS = KT::LOADS + VT::LOADS;
@@ -104,7 +104,10 @@ __global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(
   // Row fragments (B operands of the assignment contraction), kept in VGPRs.
   const float beta_raw = beta_ptr ? load_scalar(beta_ptr, beta_dtype, 0) : beta_value;
   const float beta = (flags & kRouteBetaIsLog) ? expf(fminf(fmaxf(beta_raw, kLogBetaMin), kLogBetaMax)) : beta_raw;
-  const float scale = beta * kLog2e;   // logits -> log2-domain exponents
+  // Logits -> log2-domain exponents.  The rescale test compares maxima of raw
+  // logits, so a negative beta is folded into the rows instead (exact).
+  const float scale = fabsf(beta) * kLog2e;
+  const float sign = beta < 0.f ? -1.f : 1.f;
   k8 xf[CB][KS];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
@@ -123,7 +126,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(
     ss = group_sum(ss);
     // With input normalization the unit row is rounded once to TK; otherwise
     // TK == TX and the raw row passes through unchanged.
-    const float inv_norm = (flags & kRouteNormalizeInput) ? 1.f / fmaxf(sqrtf(ss), eps) : 1.f;
+    const float inv_norm = sign * ((flags & kRouteNormalizeInput) ? 1.f / fmaxf(sqrtf(ss), eps) : 1.f);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
@@ -169,29 +172,31 @@ __global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) s[cb][kb] = Elem<TK>::mma(a[kb], xf[cb][kk], s[cb][kb]);
     }
-    // Lane (c, g) holds atoms j0 + 32*(kb/2) + 8g + 4*(kb%2) + i of row c.
-    const bool masked = j0 + AT > M;
+    // Lane (c, g) holds atoms j0 + 32*(kb/2) + 8g + 4*(kb%2) + i of row c;
+    // only the last tile can hold padding atoms.
+    if (j0 + AT > M) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (j0 + 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + i >= M) s[cb][kb][i] = -INFINITY;
+    }
     f16x8 pb[CB][AT / 32];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-      float tmax = -INFINITY;
+      float lmax = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < NB; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = s[cb][kb][i] * scale;
-          if (masked && j0 + 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + i >= M) v = -INFINITY;
-          s[cb][kb][i] = v;
-          tmax = fmaxf(tmax, v);
-        }
-      }
-      lazy_rescale<R / 16>(group_max(tmax), m_run[cb], l_part[cb], acc[cb]);
+      for (int kb = 0; kb < NB; ++kb)
+        lmax = fmaxf(lmax, fmaxf(fmaxf(s[cb][kb][0], s[cb][kb][1]), fmaxf(s[cb][kb][2], s[cb][kb][3])));
+      lazy_rescale<R / 16>(lmax, scale, m_run[cb], l_part[cb], acc[cb]);
       float psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < NB; ++kb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float pr = __builtin_amdgcn_exp2f(s[cb][kb][i] - m_run[cb]);
+          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[cb][kb][i], scale, -m_run[cb]));
           s[cb][kb][i] = pr;
           psum += pr;
         }
