@@ -49,6 +49,13 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--kernel-reps", type=int, default=200, help="launches per per-kernel timing loop")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
+    p.add_argument(
+        "--copy-mib",
+        type=int,
+        default=0,
+        help="after the measurement, copy a device buffer of this many MiB three times: a kernel of known "
+        "traffic that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters",
+    )
     return p.parse_args()
 
 
@@ -72,6 +79,21 @@ def cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def measured_traffic(workload: str, kernel: str) -> float | None:
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter runs.
+
+    ``profiles/traffic.json`` holds, per workload, FETCH_SIZE + WRITE_SIZE per
+    dispatch of each kernel, already divided by the factor the same counters
+    read for a device copy of known size (see the profile notes there).
+    """
+
+    try:
+        table = json.loads((REPO / "profiles" / "traffic.json").read_text())
+        return table[workload]["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def main() -> None:
@@ -201,7 +223,7 @@ def main() -> None:
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": None,
+        "traffic": measured_traffic(args.workload, dominant),
         "avg_launch_us": round(kernel_us[dominant], 3),
     }
     kernels = {}
@@ -268,6 +290,15 @@ def main() -> None:
     }
     print(json.dumps(line), flush=True)
     del out
+
+    if args.copy_mib > 0:
+        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
 
 if __name__ == "__main__":
