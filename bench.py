@@ -180,7 +180,8 @@ def main() -> None:
                 rp if H > S else R, S // H if S > H else 1, rp, vt.data_ptr(), vt.stride(0),
                 batch, S, length, d, p["log_score_scales"].data_ptr(), pdt,
                 float(group ** -0.5), None if S == 1 else p["map_mix_logits"].data_ptr(), pdt,
-                _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX, _lib.DA_F16, code,
+                _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX,
+                1.01 * group if config.normalize_routing_output else 0.0, _lib.DA_F16, code,
                 mixed.data_ptr(), length * d, d, 0, handle),
             "output_projection": lambda: lib.da_linear(
                 mixed.data_ptr(), tokens, d, p["output.weight"].data_ptr(), d, None, pdt, code,

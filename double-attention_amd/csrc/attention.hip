@@ -28,6 +28,8 @@
 //
 // Element types: TQ for the routed queries/keys (fp16 on the module path: they
 // are unit vectors), TV for V, the probabilities and the output.
+#include <type_traits>
+
 #include "da_common.h"
 #include "da_launch.h"
 #include "da_tile.h"
@@ -52,6 +54,7 @@ struct AttnParams {
   const void* mix_logits;
   int mix_dtype;
   int flags;
+  float score_bound;   // > 0: |q . k| <= score_bound for every raw score
   void* out;
   int64_t out_stride_b, out_stride_t, out_stride_s;
 };
@@ -93,9 +96,14 @@ struct AttnTile {
   typedef PaddedTile<DS, kKeyTile / 8, false> VT;   // V^T rows: DS features x 4 chunks
   static constexpr int KPW = (KT::LOADS + NW - 1) / NW;   // key loads per wave
   static constexpr int VPW = (VT::LOADS + NW - 1) / NW;   // V^T loads per wave
-  static constexpr int BYTES = KT::BYTES + VT::BYTES;     // K tile, then V^T tile
+  static constexpr int BYTES = KT::BYTES + VT::BYTES;     // one stage: a key tile, then a V^T tile
 };
 
+// The tile sequence u = 0 .. total-1 runs over (map s, key tile kt), u = s*n_kt + kt.
+// Stage buffer u%2 holds the keys of tile u+1 and the V^T of tile u, so step u
+// forms the scores of tile u+1 (MFMA) while it turns the scores of tile u into
+// probabilities (VALU) and accumulates P(u) V(u) (MFMA): the softmax of one
+// tile runs in the shadow of the next tile's score MFMAs.
 template <typename TQ, typename TV, int RP, int DS, int NW, bool MULTI>
 __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   typedef AttnTile<RP, DS, NW> Tile;
@@ -131,18 +139,18 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   const char* vbase = reinterpret_cast<const char*>(static_cast<const TV*>(p.vt) + b * p.vt_stride_b + 32 * ds0);
   const int kstride = static_cast<int>(p.qk_stride_t) * static_cast<int>(sizeof(TQ));   // bytes per key row
 
-  // Per-lane DMA sources of this wave's loads, as byte offsets from the tile's
-  // base: key load i fills wave load i*NW + wave of the key tile (row in the
-  // top five bits, for clamping the last tile), V^T load i the same wave load
-  // of the V^T tile.  Out-of-range wave loads of a partial last round re-load
-  // slot data of load 0 into their own slots, which nothing reads.
+  // Per-lane DMA sources of this wave's loads: key load i fills wave load
+  // i*NW + wave of the key tile ((row << 16) | byte offset of the chunk; rows
+  // are clamped to the last key when the tile is issued), V^T load i the same
+  // wave load of the V^T tile (byte offset inside the tile).  Wave loads past a tile's end re-load the data of wave
+  // load 0 into slot 0 of that tile.
   uint32_t kdesc[Tile::KPW], vdesc[Tile::VPW];
 #pragma unroll
   for (int i = 0; i < Tile::KPW; ++i) {
     int row, ck;
     const int j = i * NW + wave;
     KT::slot_chunk((j < KT::LOADS ? j : 0) * 64 + lane, row, ck);
-    kdesc[i] = (static_cast<uint32_t>(row) << 27) | static_cast<uint32_t>(row * kstride + ck * 16);
+    kdesc[i] = (static_cast<uint32_t>(row) << 16) | static_cast<uint32_t>(ck * 16);
   }
 #pragma unroll
   for (int i = 0; i < Tile::VPW; ++i) {
@@ -151,7 +159,6 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     VT::slot_chunk((j < VT::LOADS ? j : 0) * 64 + lane, row, ck);
     vdesc[i] = static_cast<uint32_t>((row * kKeyTile + ck * 8) * sizeof(TV));
   }
-  // LDS slot of load n (K loads first); loads past a tile's end rewrite slot 0.
   auto slot_of = [&](int n) {
     if (n < Tile::KPW) {
       const int j = n * NW + wave;
@@ -160,27 +167,25 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     const int j = (n - Tile::KPW) * NW + wave;
     return KT::BYTES + (j < VT::LOADS ? j * 1024 : 0);
   };
-  // Tile u = (map s, key tile kt): byte bases and the clamp row (keys past the
-  // end re-read the last one; only the final key tile has any).
+  // DMA sources of tile u: key rows (keys past the end re-read the last one)
+  // and the V^T tile.
   struct Src {
     const char* k;
     const char* v;
     int last;
   };
-  auto source = [&](int s, int kt) {
-    const int k0 = kt * kKeyTile;
-    const int64_t off = static_cast<int64_t>(s / p.map_repeat) * p.map_stride * static_cast<int64_t>(sizeof(TQ));
+  auto source = [&](int uk, int uv) {
+    const int sk = uk / n_kt;
+    const int k0 = (uk - sk * n_kt) * kKeyTile;
+    const int64_t off = static_cast<int64_t>(sk / p.map_repeat) * p.map_stride * static_cast<int64_t>(sizeof(TQ));
+    const int v0 = (uv - (uv / n_kt) * n_kt) * kKeyTile;
     return Src{kbase + static_cast<int64_t>(k0) * kstride + off,
-               vbase + static_cast<int64_t>(k0) * p.D * static_cast<int64_t>(sizeof(TV)), p.T - 1 - k0};
+               vbase + static_cast<int64_t>(v0) * p.D * static_cast<int64_t>(sizeof(TV)), p.T - 1 - k0};
   };
   auto issue_one = [&](char* buf, const Src& src, int n) {
     if (n < Tile::KPW) {
-      uint32_t off = kdesc[n] & 0x07FFFFFFu;
-      if (src.last < kKeyTile - 1) {
-        const int over = static_cast<int>(kdesc[n] >> 27) - src.last;
-        if (over > 0) off -= static_cast<uint32_t>(over * kstride);
-      }
-      dma16(src.k + off, buf + slot_of(n));
+      const int row = min(static_cast<int>(kdesc[n] >> 16), src.last);
+      dma16(src.k + static_cast<uint32_t>(row * kstride + static_cast<int>(kdesc[n] & 0xFFFFu)), buf + slot_of(n));
     } else {
       dma16(src.v + vdesc[n - Tile::KPW], buf + slot_of(n));
     }
@@ -198,14 +203,13 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_part[2] = {0.f, 0.f};
   q8 qf[2][KS];
-  float sc = 0.f;
 
+  // Query fragments of map s; returns the map's score multiplier (log2
+  // domain).  The rescale test compares maxima of raw scores, so a negative
+  // score scale is folded into the queries instead (negation is exact).
   auto load_map = [&](int s) {
     const int64_t off = static_cast<int64_t>(s / p.map_repeat) * p.map_stride;
-    // The rescale test compares maxima of raw scores, so a negative score
-    // scale is folded into the queries instead (negation is exact).
     const float gamma = map_gamma(p, s);
-    sc = fabsf(gamma) * kLog2e;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const int tq = qw0 + cb * 16 + c;
@@ -216,149 +220,173 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
         if (gamma < 0.f) qf[cb][kk] = -qf[cb][kk];
       }
     }
+    return fabsf(gamma) * kLog2e;
   };
 
-  // Lane-relative LDS offsets of the fragment reads.
   const int kfrag = KT::offset(c, g);
   const int vfrag = KT::BYTES + VT::offset(c, g);
 
-  load_map(0);
-  {
-    const Src src0 = source(0, 0);
+  // Scores of 32 keys x 32 queries from a key tile in LDS: four independent
+  // accumulator chains, each key fragment feeding both query blocks.  With
+  // DMA, the loads of the next stage are spread between the fragment reads.
+  auto scores = [&](const char* kt_lds, f32x4 (&st)[2][2], auto with_dma, char* nxt, const Src& src) {
 #pragma unroll
-    for (int n = 0; n < NL; ++n) issue_one(lds0, src0, n);
-  }
+    for (int cb = 0; cb < 2; ++cb) st[cb][0] = st[cb][1] = zero4();
+    const char* kf = kt_lds + kfrag;
+    // All key fragments of the tile are read up front (KS*2 reads in flight),
+    // then consumed; LDS latency is paid once per tile, not once per step.
+    q8 kfr[KS][2];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      kfr[kk][0] = lds_v8<TQ>(kf + KT::offset(0, kk * 4));
+      kfr[kk][1] = lds_v8<TQ>(kf + KT::offset(16, kk * 4));
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      if constexpr (decltype(with_dma)::value) {
+#pragma unroll
+        for (int n = 0; n < NL; ++n)
+          if (n * KS / NL == kk) issue_one(nxt, src, n);
+      }
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        st[cb][0] = Elem<TQ>::mma(kfr[kk][0], qf[cb][kk], st[cb][0]);
+        st[cb][1] = Elem<TQ>::mma(kfr[kk][1], qf[cb][kk], st[cb][1]);
+      }
+    }
+  };
 
-  int s = 0, kt = 0;
-  for (int u = 0; u < total; ++u) {
+  // Prologue: keys of tile 0 into stage 1's key slot, stage 0 = {K(1), V(0)}.
+  float sc = load_map(0);
+  float sc_next = sc;
+  {
+    const Src s0 = source(0, 0);
+#pragma unroll
+    for (int n = 0; n < Tile::KPW; ++n) issue_one(lds1, s0, n);
+    const Src s1 = source(min(1, total - 1), 0);
+#pragma unroll
+    for (int n = 0; n < NL; ++n) issue_one(lds0, s1, n);
+  }
+  wait_vmem();
+  __syncthreads();
+  f32x4 st_prev[2][2];
+  scores(lds1, st_prev, std::false_type{}, nullptr, Src{});
+
+  // One pipelined step u = s*n_kt + kt.  FIXED: every score is bounded by
+  // score_bound, so exponents use the fixed reference score_bound*sc (all
+  // probabilities <= 1) and the accumulators are never rescaled; otherwise the
+  // lazy online rescale runs.
+  auto step = [&](auto fixed, int u, int s, int kt) {
+    constexpr bool FIXED = decltype(fixed)::value;
     char* cur = (u & 1) ? lds1 : lds0;
     char* nxt = (u & 1) ? lds0 : lds1;
-    // Tile u + 1; the last step reloads its own tile into the idle buffer.
-    int s_n = s, kt_n = kt + 1;
-    if (kt_n == n_kt) {
-      kt_n = 0;
-      ++s_n;
-    }
-    if (s_n == p.S) {
-      s_n = s;
-      kt_n = kt;
-    }
-    const Src src = source(s_n, kt_n);
     const int k0 = kt * kKeyTile;
+    // Tile u + 1 opens map s + 1: its queries are needed by this step's scores.
+    if (kt == n_kt - 1 && s + 1 < p.S) sc_next = load_map(s + 1);
+    // Stage u + 1 = {K(u + 2), V(u + 1)}, clamped at the end of the sequence.
+    const Src src = source(min(u + 2, total - 1), min(u + 1, total - 1));
+
+    // What may branch comes before the barrier: the causal / end mask
+    // (diagonal and last tiles only) and the rescale test.  What follows it is
+    // one straight block, so the compiler can interleave the exponentials of
+    // tile u with the score MFMAs of tile u + 1.
+    if ((causal && k0 + kKeyTile - 1 > qw0) || k0 + kKeyTile > p.T) {
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        const int tq = qw0 + cb * 16 + c;
+        const int kmax = min(causal ? tq : p.T - 1, p.T - 1);   // last key this query sees
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (k0 + 8 * g + 4 * kb + i > kmax) st_prev[cb][kb][i] = -INFINITY;
+      }
+    }
+    float m_use[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      if constexpr (FIXED) {
+        m_use[cb] = -p.score_bound * sc;
+      } else {
+        const float lmax =
+            fmaxf(fmaxf(fmaxf(st_prev[cb][0][0], st_prev[cb][0][1]), fmaxf(st_prev[cb][0][2], st_prev[cb][0][3])),
+                  fmaxf(fmaxf(st_prev[cb][1][0], st_prev[cb][1][1]), fmaxf(st_prev[cb][1][2], st_prev[cb][1][3])));
+        lazy_rescale<NB>(lmax, sc, m_run[cb], l_part[cb], acc[cb]);
+        m_use[cb] = m_run[cb] == -INFINITY ? 0.f : -m_run[cb];   // negated; 0 while fully masked
+      }
+    }
 
     wait_vmem();
     __syncthreads();
 
-    if (!(causal && k0 > qw0 + kAttnQW - 1)) {   // else the tile lies above this wave's causal bound
-      // Scores for 32 keys x 32 queries: four independent accumulator chains,
-      // each key fragment feeding both query blocks; the next tile's loads are
-      // spread between the fragment reads.
-      f32x4 st[2][2] = {{zero4(), zero4()}, {zero4(), zero4()}};
-      const char* kf = cur + kfrag;
-      // Software pipeline: the fragments of step kk + 1 are read while the
-      // MFMAs of step kk run; scheduling barriers keep the compiler from
-      // hoisting every read (which would cost the second wave per SIMD).
-      q8 a0 = lds_v8<TQ>(kf + KT::offset(0, 0));
-      q8 a1 = lds_v8<TQ>(kf + KT::offset(16, 0));
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        q8 n0 = a0, n1 = a1;
-        if (kk + 1 < KS) {
-          n0 = lds_v8<TQ>(kf + KT::offset(0, (kk + 1) * 4));
-          n1 = lds_v8<TQ>(kf + KT::offset(16, (kk + 1) * 4));
-        }
-#pragma unroll
-        for (int n = 0; n < NL; ++n)
-          if (n * KS / NL == kk) issue_one(nxt, src, n);
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          st[cb][0] = Elem<TQ>::mma(a0, qf[cb][kk], st[cb][0]);
-          st[cb][1] = Elem<TQ>::mma(a1, qf[cb][kk], st[cb][1]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        a0 = n0;
-        a1 = n1;
-      }
-      // The first V^T fragments do not depend on the scores: read them before
-      // the softmax.
-      const char* vf = cur + vfrag;
-      v8 va = lds_v8<TV>(vf + VT::offset(0, 0));
-      v8 vb = lds_v8<TV>(vf + VT::offset(NB > 1 ? 16 : 0, 0));
+    f32x4 st_new[2][2];
+    scores(cur, st_new, std::true_type{}, nxt, src);
 
-      // Lane (c, g) holds keys k0 + 8g + 4kb + i for query qw0 + 16cb + c.
-      // Only tiles on the causal diagonal or past the end carry masked keys.
-      if ((causal && k0 + kKeyTile - 1 > qw0) || k0 + kKeyTile > p.T) {
+    // Probabilities of tile u: lane (c, g) holds keys k0 + 8g + 4kb + i for
+    // query qw0 + 16cb + c.
+    v8 pb[2];
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          const int tq = qw0 + cb * 16 + c;
-          const int kmax = min(causal ? tq : p.T - 1, p.T - 1);   // last key this query sees
+    for (int cb = 0; cb < 2; ++cb) {
+      float psum = 0.f;
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (k0 + 8 * g + 4 * kb + i > kmax) st[cb][kb][i] = -INFINITY;
+        for (int i = 0; i < 4; ++i) {
+          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(st_prev[cb][kb][i], sc, m_use[cb]));
+          st_prev[cb][kb][i] = pr;
+          psum += pr;
         }
       }
-      v8 pb[2];
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const float lmax = fmaxf(fmaxf(fmaxf(st[cb][0][0], st[cb][0][1]), fmaxf(st[cb][0][2], st[cb][0][3])),
-                                 fmaxf(fmaxf(st[cb][1][0], st[cb][1][1]), fmaxf(st[cb][1][2], st[cb][1][3])));
-        lazy_rescale<NB>(lmax, sc, m_run[cb], l_part[cb], acc[cb]);
-        const float m_use = m_run[cb] == -INFINITY ? 0.f : m_run[cb];   // fully masked so far
-        float psum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(st[cb][kb][i], sc, -m_use));
-            st[cb][kb][i] = pr;
-            psum += pr;
-          }
-        }
-        l_part[cb] += psum;
-        pb[cb] = pack_blocked<TV>(st[cb][0], st[cb][1]);   // keys k0 + 8g + e
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int db = 0; db < NB; ++db) {
-        v8 vn = vb;
-        if (db + 2 < NB) vn = lds_v8<TV>(vf + VT::offset((db + 2) * 16, 0));
-        acc[0][db] = Elem<TV>::mma(va, pb[0], acc[0][db]);
-        acc[1][db] = Elem<TV>::mma(va, pb[1], acc[1][db]);
-        __builtin_amdgcn_sched_barrier(0);
-        va = vb;
-        vb = vn;
-      }
-    } else {
-#pragma unroll
-      for (int n = 0; n < NL; ++n) issue_one(nxt, src, n);
+      l_part[cb] += psum;
+      pb[cb] = pack_blocked<TV>(st_prev[cb][0], st_prev[cb][1]);   // keys k0 + 8g + e
     }
 
-    if (kt == n_kt - 1) {   // map s complete
-      const float wmap = map_weight(p, s);
+    // O^T += V^T(u) P^T(u).
+    const char* vf = cur + vfrag;
+    v8 vfr[NB];
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const float l = group_sum(l_part[cb]);
-        const float w = wmap / (l > 0.f ? l : 1.f);
-        const int tq = qw0 + cb * 16 + c;
-        if constexpr (MULTI) {
+    for (int db = 0; db < NB; ++db) vfr[db] = lds_v8<TV>(vf + VT::offset(db * 16, 0));
 #pragma unroll
-          for (int i = 0; i < NB; ++i) yacc[cb][i] += acc[cb][i] * w;
-        } else {
-          if (tq < p.T) store_rows<TV, DS>(p, b, (p.flags & kAttnMix) ? 0 : s, tq, g, ds0, acc[cb], w);
-        }
-#pragma unroll
-        for (int i = 0; i < NB; ++i) acc[cb][i] = zero4();
-        m_run[cb] = -INFINITY;
-        l_part[cb] = 0.f;
-      }
-      if (s + 1 < p.S) load_map(s + 1);
-      kt = 0;
-      ++s;
-    } else {
-      ++kt;
+    for (int db = 0; db < NB; ++db) {
+      acc[0][db] = Elem<TV>::mma(vfr[db], pb[0], acc[0][db]);
+      acc[1][db] = Elem<TV>::mma(vfr[db], pb[1], acc[1][db]);
     }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      st_prev[cb][0] = st_new[cb][0];
+      st_prev[cb][1] = st_new[cb][1];
+    }
+  };
+
+  for (int s = 0; s < p.S; ++s) {
+    // The fixed reference keeps every probability within the range of the
+    // operand type: bf16 holds 2^-120 .. 1 exactly in exponent; fp16 does not.
+    const bool fixed = p.score_bound > 0.f && sizeof(TV) == 2 && !std::is_same<TV, _Float16>::value &&
+                       2.f * p.score_bound * sc <= 120.f;
+    const int u0 = s * n_kt;
+    if (fixed) {
+      for (int kt = 0; kt < n_kt; ++kt) step(std::true_type{}, u0 + kt, s, kt);
+    } else {
+      for (int kt = 0; kt < n_kt; ++kt) step(std::false_type{}, u0 + kt, s, kt);
+    }
+    const float wmap = map_weight(p, s);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const float l = group_sum(l_part[cb]);
+      const float w = wmap / (l > 0.f ? l : 1.f);
+      const int tq = qw0 + cb * 16 + c;
+      if constexpr (MULTI) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) yacc[cb][i] += acc[cb][i] * w;
+      } else {
+        if (tq < p.T) store_rows<TV, DS>(p, b, (p.flags & kAttnMix) ? 0 : s, tq, g, ds0, acc[cb], w);
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) acc[cb][i] = zero4();
+      m_run[cb] = -INFINITY;
+      l_part[cb] = 0.f;
+    }
+    sc = sc_next;
   }
 
   if constexpr (MULTI) {
@@ -368,35 +396,37 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       if (tq < p.T) store_rows<TV, DS>(p, b, 0, tq, g, ds0, yacc[cb], 1.f);
     }
   }
+  // The last step's (redundant) stage loads must land before the workgroup's
+  // LDS is released.
+  wait_vmem();
 }
 
-// Workgroups of four waves when there are enough of them to fill the chip
-// twice over, else of two waves (more, smaller workgroups).
 template <typename TQ, typename TV, int RP, int DS, bool MULTI>
 static void launch_attn_3(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
   p.n_slices = a.D / DS;
-  const int64_t wg4 = static_cast<int64_t>(a.B) * p.n_slices * ((a.T + 127) / 128);
-  if (wg4 >= 512) {
-    p.n_qt = static_cast<int>((a.T + 127) / 128);
-    hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 4, MULTI>), dim3(a.B * p.n_slices, p.n_qt), dim3(256), 0,
-                       s, p);
-  } else {
-    p.n_qt = static_cast<int>((a.T + 63) / 64);
-    hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 2, MULTI>), dim3(a.B * p.n_slices, p.n_qt), dim3(128), 0,
-                       s, p);
-  }
+  p.n_qt = static_cast<int>((a.T + 2 * kAttnQW - 1) / (2 * kAttnQW));
+  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 2, MULTI>), dim3(a.B * p.n_slices, p.n_qt), dim3(128), 0, s,
+                     p);
 }
 
-// Value slice per workgroup: 128 features (64 when the value width is 64).
+// Value slice per workgroup: as wide as possible (one score tile serves more
+// value columns, and the softmax is shared by more MFMAs) while the grid keeps
+// at least 256 workgroups.  The register budget caps it at 256 features, and
+// at 128 with the map mix (a second accumulator set) or 512-wide scores.
 template <typename TQ, typename TV, int RP>
 static void launch_attn_1(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
   const bool multi = (a.flags & kAttnMix) && a.S > 1;
-  if (a.D == 64) {
+  const int64_t tiles = static_cast<int64_t>(a.B) * ((a.T + 2 * kAttnQW - 1) / (2 * kAttnQW));
+  int ds = min(a.D, (multi || RP == 512) ? 128 : 256);
+  while (ds > 128 && tiles * (a.D / ds) < 256) ds /= 2;
+  if (ds == 64) {
     if (multi) launch_attn_3<TQ, TV, RP, 64, true>(a, p, s);
     else launch_attn_3<TQ, TV, RP, 64, false>(a, p, s);
-  } else {
+  } else if (ds == 128) {
     if (multi) launch_attn_3<TQ, TV, RP, 128, true>(a, p, s);
     else launch_attn_3<TQ, TV, RP, 128, false>(a, p, s);
+  } else {
+    if constexpr (RP < 512) launch_attn_3<TQ, TV, RP, 256, false>(a, p, s);
   }
 }
 
@@ -430,6 +460,7 @@ void launch_routed_attention(const AttentionArgs& a, hipStream_t stream) {
   p.mix_logits = a.mix_logits;
   p.mix_dtype = a.mix_dtype;
   p.flags = a.flags;
+  p.score_bound = a.score_bound;
   p.out = a.out;
   p.out_stride_b = a.out_stride_b;
   p.out_stride_t = a.out_stride_t;

@@ -101,7 +101,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 3; }
+int da_abi_version(void) { return 4; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -146,14 +146,16 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
                         const void* value_t, int64_t vt_stride_b,
                         int64_t batch, int64_t maps, int64_t length, int64_t value_dim,
                         const void* scales, int scales_dtype, float scale_mult,
-                        const void* mix_logits, int mix_dtype, int flags, int qk_dtype,
-                        int v_dtype, void* out, int64_t out_stride_b, int64_t out_stride_t,
-                        int64_t out_stride_s, da_stream_t stream) {
+                        const void* mix_logits, int mix_dtype, int flags, float score_bound,
+                        int qk_dtype, int v_dtype, void* out, int64_t out_stride_b,
+                        int64_t out_stride_t, int64_t out_stride_s, da_stream_t stream) {
   int rc = validate_attention(query, key, stride_b, stride_t, map_stride, map_repeat, score_dim,
                               value_t, vt_stride_b, batch, maps, length, value_dim,
                               scales, scales_dtype, mix_logits, mix_dtype, qk_dtype, v_dtype, out,
                               out_stride_b, out_stride_t, out_stride_s);
   if (rc) return rc;
+  if (!(score_bound >= 0.f) || std::isinf(score_bound))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention: score_bound must be finite and >= 0");
   if (batch == 0 || length == 0) return ok();
   da::AttentionArgs a;
   a.q = query;
@@ -175,6 +177,7 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
   a.mix_logits = mix_logits;
   a.mix_dtype = mix_dtype;
   a.flags = flags;
+  a.score_bound = score_bound;
   a.qk_dtype = qk_dtype;
   a.v_dtype = v_dtype;
   a.out = out;
@@ -338,6 +341,9 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   at.mix_dtype = a->param_dtype;
   at.flags = da::kAttnScalesAreLog | ((a->flags & DA_SDA_CAUSAL) ? da::kAttnCausal : 0) |
              (concat ? 0 : da::kAttnMix);
+  // Output-normalized routed rows are unit vectors (fp16 rounding aside), so a
+  // grouped score q'.k' = sum of `group` unit dot products is at most `group`.
+  at.score_bound = (a->flags & DA_SDA_NORMALIZE_OUTPUT) ? 1.01f * static_cast<float>(group) : 0.f;
   at.qk_dtype = DA_F16;
   at.v_dtype = a->dtype;
   at.out = mixed;

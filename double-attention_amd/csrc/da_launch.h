@@ -68,6 +68,7 @@ struct AttentionArgs {
   const void* mix_logits;             // [S] map-mix logits or nullptr (uniform)
   int mix_dtype;
   int flags;
+  float score_bound;                  // > 0: |q . k| <= score_bound for every raw score (e.g. unit rows)
   int qk_dtype;                       // routed queries/keys
   int v_dtype;                        // V, probabilities and the output
   void* out;

@@ -38,7 +38,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -101,7 +101,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i64,  # value_t, per-sequence pitch
             _i64, _i64, _i64, _i64,  # batch, maps, length, value_dim
             _vp, _i32, _f32, _vp, _i32,  # scales, mix logits
-            _i32, _i32, _i32, _vp, _i64, _i64, _i64, _vp,  # flags, qk/v dtypes, out + strides, stream
+            _i32, _f32,  # flags, score bound
+            _i32, _i32, _vp, _i64, _i64, _i64, _vp,  # qk/v dtypes, out + strides, stream
         ],
     ),
     "da_qkv_projection": (

@@ -26,6 +26,8 @@ the reference itself used before it had native backward kernels.
 
 from __future__ import annotations
 
+import math
+
 from typing import NamedTuple
 
 import torch
@@ -349,7 +351,9 @@ def value_transposed(value: Tensor, width: int | None = None) -> Tensor:
     return vt
 
 
-def _attention_forward(query: Tensor, key: Tensor, value: Tensor, scales: Tensor, causal: bool) -> Tensor:
+def _attention_forward(
+    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, causal: bool, score_bound: float = 0.0
+) -> Tensor:
     batch, maps, length, score_dim = query.shape
     model_dim = value.shape[-1]
     score_width = _next_width(score_dim)
@@ -373,7 +377,7 @@ def _attention_forward(query: Tensor, key: Tensor, value: Tensor, scales: Tensor
             vt.data_ptr(), vt.stride(0),
             batch, maps, length, value_width,
             scales_c.data_ptr(), dtype_code(scales_c.dtype), 1.0, None, _lib.DA_F32,
-            _lib.DA_ATTN_CAUSAL if causal else 0,
+            _lib.DA_ATTN_CAUSAL if causal else 0, float(score_bound),
             _half_code(q.dtype), _half_code(value.dtype),
             out.data_ptr(), out.stride(0), out.stride(2), out.stride(1),
             _stream(value.device),
@@ -403,13 +407,18 @@ class _AttentionFunction(torch.autograd.Function):
 
 
 def routed_attention_hip(
-    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, causal: bool = True
+    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, causal: bool = True, *, score_bound: float = 0.0
 ) -> Tensor:
     """Flash outer attention on gfx950; same contract as ``routed_attention_triton``.
 
     ``query``/``key`` ``[B, S, T, R]``, ``value`` ``[B, T, D]`` (shared by every
-    map), ``scales`` ``[S]``; returns ``[B, S, T, D]``.
+    map), ``scales`` ``[S]``; returns ``[B, S, T, D]``.  ``score_bound`` (an
+    extension; 0 = unknown) is an upper bound on ``|q . k|``, e.g. 1 for
+    L2-normalized rows: it lets the kernel skip online-softmax rescaling.
     """
+
+    if not score_bound >= 0.0 or math.isinf(score_bound):
+        raise ValueError("score_bound must be finite and >= 0")
 
     if query.ndim != 4 or key.shape != query.shape:
         raise ValueError("query and key must have matching [B, S, T, R] shapes")
@@ -424,7 +433,7 @@ def routed_attention_hip(
     _half_code(value.dtype)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value, scales)):
         return _AttentionFunction.apply(query, key, value, scales, causal)
-    return _attention_forward(query, key, value, scales, causal)
+    return _attention_forward(query, key, value, scales, causal, score_bound)
 
 
 # --------------------------------------------------------------------------

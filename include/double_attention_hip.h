@@ -125,6 +125,9 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  *   DA_ATTN_MIX: out(b, t) = sum_s alpha_s O_s(b, t), alpha = softmax(mix_logits)
  *     (uniform 1/maps if mix_logits is NULL); else O_s(b, t) goes to
  *     out + b*out_stride_b + t*out_stride_t + s*out_stride_s.
+ *   score_bound: 0, or an upper bound on |q . k| over all raw query/key rows
+ *     (1 for L2-normalized rows).  With a bound, maps whose scaled bound fits
+ *     the probability type skip the online-softmax rescaling (bf16 V only).
  * score_dim and value_dim must be 64, 128, 256 or 512.  Element types:
  *   (qk_dtype, v_dtype) in {(F16, BF16), (F16, F16), (BF16, BF16)}; the output
  *   has v_dtype.  V^T padding tokens (length .. padded length - 1) must hold
@@ -135,9 +138,9 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
                         const void* value_t, int64_t vt_stride_b,
                         int64_t batch, int64_t maps, int64_t length, int64_t value_dim,
                         const void* scales, int scales_dtype, float scale_mult,
-                        const void* mix_logits, int mix_dtype, int flags, int qk_dtype,
-                        int v_dtype, void* out, int64_t out_stride_b, int64_t out_stride_t,
-                        int64_t out_stride_s, da_stream_t stream);
+                        const void* mix_logits, int mix_dtype, int flags, float score_bound,
+                        int qk_dtype, int v_dtype, void* out, int64_t out_stride_b,
+                        int64_t out_stride_t, int64_t out_stride_s, da_stream_t stream);
 
 /*
  * Q/K and V projections in one launch (modules.py:143-157 and 212):

@@ -80,10 +80,10 @@ def test_attention_rejects_bad_arguments_before_launch() -> None:
         _fake(), 512 * 512,  # value_t, per-sequence pitch
         2, 1, 512, 512,  # batch, maps, length, value dim
         _fake(), lib.DA_F32, 1.0, None, lib.DA_F32,
-        lib.DA_ATTN_CAUSAL, lib.DA_F16, lib.DA_BF16, _fake(), 512 * 512, 512, 0, None,
+        lib.DA_ATTN_CAUSAL, 1.0, lib.DA_F16, lib.DA_BF16, _fake(), 512 * 512, 512, 0, None,
     ]
     bad_types = list(base)
-    bad_types[19], bad_types[20] = lib.DA_BF16, lib.DA_F16
+    bad_types[20], bad_types[21] = lib.DA_BF16, lib.DA_F16
     assert h.da_routed_attention(*bad_types) == -2
     bad_dim = list(base)
     bad_dim[6] = 384
@@ -95,6 +95,10 @@ def test_attention_rejects_bad_arguments_before_launch() -> None:
     no_scales = list(base)
     no_scales[13] = None
     assert h.da_routed_attention(*no_scales) == -1
+    bad_bound = list(base)
+    bad_bound[19] = -1.0
+    assert h.da_routed_attention(*bad_bound) == -1
+    assert "score_bound" in h.da_last_error().decode()
 
 
 def test_forward_rejects_small_workspace() -> None:

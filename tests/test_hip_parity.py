@@ -183,23 +183,30 @@ def test_route_zero_rows_and_empty() -> None:
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("score_bound", [0.0, 1.01])
 @pytest.mark.parametrize(("batch", "maps", "length", "score_dim", "value_dim", "scales"), [
     (2, 2, 65, 64, 96, (12.0, 17.0)),
     (1, 4, 64, 128, 512, (12.0, 12.0, 12.0, 12.0)),
     (1, 2, 257, 64, 80, (11.0, 15.0)),
     (1, 2, 64, 256, 128, (10.0, 14.0)),
     (1, 1, 1, 64, 64, (16.0,)),
+    (1, 2, 200, 128, 256, (90.0, 3.0)),   # with a bound: the first map exceeds the fixed range
 ])
-def test_routed_attention(dtype, causal, batch, maps, length, score_dim, value_dim, scales) -> None:
+def test_routed_attention(dtype, causal, score_bound, batch, maps, length, score_dim, value_dim, scales) -> None:
+    # Rows are unit vectors, so 1.01 bounds every score: bf16 maps whose scaled
+    # bound fits run without online rescaling, the others (and fp16) with it.
     device = _device()
     q = unit_rows((batch, maps, length, score_dim), dtype, device, 10)
     k = unit_rows((batch, maps, length, score_dim), dtype, device, 11)
     g = torch.Generator().manual_seed(12)
     v = torch.randn(batch, length, value_dim, generator=g).to(device, dtype)
     s = torch.tensor(scales, device=device)
-    out = da.routed_attention_hip(q, k, v, s, causal)
+    out = da.routed_attention_hip(q, k, v, s, causal, score_bound=score_bound)
     expected = oracle.routed_attention(np32(q), np32(k), np32(v), np.array(scales, np.float32), causal)
-    assert_parity(out, expected, label=f"attention b{batch} s{maps} t{length} r{score_dim} d{value_dim} causal={causal} {dtype}")
+    assert_parity(
+        out, expected,
+        label=f"attention b{batch} s{maps} t{length} r{score_dim} d{value_dim} causal={causal} bound={score_bound} {dtype}",
+    )
 
 
 def test_attention_long_context_properties() -> None:
@@ -210,12 +217,14 @@ def test_attention_long_context_properties() -> None:
     q = unit_rows((1, 1, length, 256), torch.bfloat16, device, 13)
     k = unit_rows((1, 1, length, 256), torch.bfloat16, device, 14)
     ones = torch.ones(1, length, 512, device=device, dtype=torch.bfloat16)
-    out = da.routed_attention_hip(q, k, ones, torch.tensor([16.0], device=device), True)
-    torch.testing.assert_close(out.float(), torch.ones_like(out, dtype=torch.float32), atol=1e-2, rtol=0)
+    for bound in (0.0, 1.01):
+        out = da.routed_attention_hip(q, k, ones, torch.tensor([16.0], device=device), True, score_bound=bound)
+        torch.testing.assert_close(out.float(), torch.ones_like(out, dtype=torch.float32), atol=1e-2, rtol=0)
     g = torch.Generator().manual_seed(15)
     v = torch.randn(1, length, 512, generator=g).to(device, torch.bfloat16)
-    out = da.routed_attention_hip(q, k, v, torch.tensor([16.0], device=device), True)
-    torch.testing.assert_close(out[0, 0, 0].float(), v[0, 0].float(), atol=2e-2, rtol=0)
+    for bound in (0.0, 1.01):
+        out = da.routed_attention_hip(q, k, v, torch.tensor([16.0], device=device), True, score_bound=bound)
+        torch.testing.assert_close(out[0, 0, 0].float(), v[0, 0].float(), atol=2e-2, rtol=0)
 
 
 # ---------------------------------------------------------------- whole module
