@@ -161,6 +161,9 @@ def main() -> None:
         raw_key = module.bank.raw_key.detach()
         raw_value = module.bank.raw_value.detach() if module.bank.raw_value is not None else None
 
+        attn_flags = _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX
+        attn_ws_bytes = lib.da_attention_workspace_bytes(batch, S, length, rp, d, attn_flags)
+        attn_ws = torch.empty(attn_ws_bytes, dtype=torch.uint8, device=device) if attn_ws_bytes else None
         launches = {
             "dict_normalize": lambda: lib.da_dictionary_normalize(
                 raw_key.data_ptr(), None if raw_value is None else raw_value.data_ptr(),
@@ -182,7 +185,8 @@ def main() -> None:
                 float(group ** -0.5), None if S == 1 else p["map_mix_logits"].data_ptr(), pdt,
                 _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX,
                 1.01 * group if config.normalize_routing_output else 0.0, _lib.DA_F16, code,
-                mixed.data_ptr(), length * d, d, 0, handle),
+                mixed.data_ptr(), length * d, d, 0,
+                attn_ws.data_ptr() if attn_ws is not None else None, attn_ws_bytes, handle),
             "output_projection": lambda: lib.da_linear(
                 mixed.data_ptr(), tokens, d, p["output.weight"].data_ptr(), d, None, pdt, code,
                 final.data_ptr(), handle),

@@ -28,6 +28,7 @@
 //
 // Element types: TQ for the routed queries/keys (fp16 on the module path: they
 // are unit vectors), TV for V, the probabilities and the output.
+#include <algorithm>
 #include <type_traits>
 
 #include "da_common.h"
@@ -48,6 +49,9 @@ struct AttnParams {
   int64_t vt_stride_b;
   int S, T, D;
   int n_qt, n_slices;
+  int chunk_tiles;     // > 0: split long causal key ranges into chunks of this many key tiles
+  int n_items;         // workgroups per (sequence, slice): sum over query tiles of their chunks
+  float* part;         // per item: [QT][DS] unnormalized outputs, then [QT] reference m, [QT] sums l
   const void* scales;
   int scales_dtype;
   float scale_mult;
@@ -90,6 +94,30 @@ __device__ __forceinline__ void store_rows(const AttnParams& p, int b, int s, in
   }
 }
 
+// Key tiles of query tile qt (QT queries) and the chunks they are split into.
+__device__ __forceinline__ int key_tiles_of(const AttnParams& p, int qt, int QT) {
+  if (!(p.flags & kAttnCausal)) return (p.T + kKeyTile - 1) / kKeyTile;
+  return (min(qt * QT + QT, p.T) - 1) / kKeyTile + 1;
+}
+__device__ __forceinline__ int chunks_of(const AttnParams& p, int qt, int QT) {
+  return p.chunk_tiles > 0 ? (key_tiles_of(p, qt, QT) + p.chunk_tiles - 1) / p.chunk_tiles : 1;
+}
+// Work item y of a (sequence, slice): items run heaviest query tile first,
+// then by chunk.  Returns the query tile; `chunk`, `n_chunks` and `first` (the
+// item index of the tile's chunk 0) describe its place.
+__device__ __forceinline__ int decode_item(const AttnParams& p, int y, int QT, int& chunk, int& n_chunks, int& first) {
+  int qt = p.n_qt - 1;
+  first = 0;
+  n_chunks = chunks_of(p, qt, QT);
+  while (qt > 0 && y >= first + n_chunks) {
+    first += n_chunks;
+    --qt;
+    n_chunks = chunks_of(p, qt, QT);
+  }
+  chunk = y - first;
+  return qt;
+}
+
 template <int RP, int DS, int NW>
 struct AttnTile {
   typedef PaddedTile<kKeyTile, RP / 8, true> KT;    // keys (blocked rows)
@@ -122,15 +150,19 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   const int c = lane & 15;
   const int g = lane >> 4;
   const int wave = uniform_wave();
-  // blockIdx.y ranks query tiles heaviest (causal) first; x = (sequence, slice).
-  const int qt = p.n_qt - 1 - static_cast<int>(blockIdx.y);
+  // blockIdx.y = work item (query tile and key chunk), heaviest first;
+  // x = (sequence, slice).
+  int chunk, n_chunks, first_item;
+  const int qt = decode_item(p, static_cast<int>(blockIdx.y), QT, chunk, n_chunks, first_item);
   const int b = static_cast<int>(blockIdx.x) / p.n_slices;
   const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;   // first feature of the slice
   const int q0 = qt * QT;
   const int qw0 = q0 + wave * kAttnQW;                       // this wave's first query
   const bool causal = p.flags & kAttnCausal;
-  const int q_last = min(q0 + QT, p.T) - 1;
-  const int n_kt = causal ? q_last / kKeyTile + 1 : (p.T + kKeyTile - 1) / kKeyTile;
+  // Key tiles [kt_begin, kt_begin + n_kt) of every map.
+  const int kt_all = key_tiles_of(p, qt, QT);
+  const int kt_begin = p.chunk_tiles > 0 ? chunk * p.chunk_tiles : 0;
+  const int n_kt = p.chunk_tiles > 0 ? min(p.chunk_tiles, kt_all - kt_begin) : kt_all;
   const int total = p.S * n_kt;
 
   const TQ* qbase = static_cast<const TQ*>(p.q) + b * p.qk_stride_b;
@@ -176,9 +208,9 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   };
   auto source = [&](int uk, int uv) {
     const int sk = uk / n_kt;
-    const int k0 = (uk - sk * n_kt) * kKeyTile;
+    const int k0 = (kt_begin + uk - sk * n_kt) * kKeyTile;
     const int64_t off = static_cast<int64_t>(sk / p.map_repeat) * p.map_stride * static_cast<int64_t>(sizeof(TQ));
-    const int v0 = (uv - (uv / n_kt) * n_kt) * kKeyTile;
+    const int v0 = (kt_begin + uv - (uv / n_kt) * n_kt) * kKeyTile;
     return Src{kbase + static_cast<int64_t>(k0) * kstride + off,
                vbase + static_cast<int64_t>(v0) * p.D * static_cast<int64_t>(sizeof(TV)), p.T - 1 - k0};
   };
@@ -233,25 +265,30 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) st[cb][0] = st[cb][1] = zero4();
     const char* kf = kt_lds + kfrag;
-    // All key fragments of the tile are read up front (KS*2 reads in flight),
-    // then consumed; LDS latency is paid once per tile, not once per step.
-    q8 kfr[KS][2];
+    // Key fragments are read in groups of KG steps (2*KG reads in flight),
+    // then consumed: LDS latency is paid once per group, and the group size
+    // bounds the registers the reads hold.
+    constexpr int KG = KS < 4 ? KS : 4;
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      kfr[kk][0] = lds_v8<TQ>(kf + KT::offset(0, kk * 4));
-      kfr[kk][1] = lds_v8<TQ>(kf + KT::offset(16, kk * 4));
-    }
+    for (int k0 = 0; k0 < KS; k0 += KG) {
+      q8 kfr[KG][2];
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      if constexpr (decltype(with_dma)::value) {
-#pragma unroll
-        for (int n = 0; n < NL; ++n)
-          if (n * KS / NL == kk) issue_one(nxt, src, n);
+      for (int kk = 0; kk < KG; ++kk) {
+        kfr[kk][0] = lds_v8<TQ>(kf + KT::offset(0, (k0 + kk) * 4));
+        kfr[kk][1] = lds_v8<TQ>(kf + KT::offset(16, (k0 + kk) * 4));
       }
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        st[cb][0] = Elem<TQ>::mma(kfr[kk][0], qf[cb][kk], st[cb][0]);
-        st[cb][1] = Elem<TQ>::mma(kfr[kk][1], qf[cb][kk], st[cb][1]);
+      for (int kk = 0; kk < KG; ++kk) {
+        if constexpr (decltype(with_dma)::value) {
+#pragma unroll
+          for (int n = 0; n < NL; ++n)
+            if (n * KS / NL == k0 + kk) issue_one(nxt, src, n);
+        }
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          st[cb][0] = Elem<TQ>::mma(kfr[kk][0], qf[cb][k0 + kk], st[cb][0]);
+          st[cb][1] = Elem<TQ>::mma(kfr[kk][1], qf[cb][k0 + kk], st[cb][1]);
+        }
       }
     }
   };
@@ -280,7 +317,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     constexpr bool FIXED = decltype(fixed)::value;
     char* cur = (u & 1) ? lds1 : lds0;
     char* nxt = (u & 1) ? lds0 : lds1;
-    const int k0 = kt * kKeyTile;
+    const int k0 = (kt_begin + kt) * kKeyTile;
     // Tile u + 1 opens map s + 1: its queries are needed by this step's scores.
     if (kt == n_kt - 1 && s + 1 < p.S) sc_next = load_map(s + 1);
     // Stage u + 1 = {K(u + 2), V(u + 1)}, clamped at the end of the sequence.
@@ -343,13 +380,17 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 
     // O^T += V^T(u) P^T(u).
     const char* vf = cur + vfrag;
-    v8 vfr[NB];
+    constexpr int VG = NB < 4 ? NB : 4;
 #pragma unroll
-    for (int db = 0; db < NB; ++db) vfr[db] = lds_v8<TV>(vf + VT::offset(db * 16, 0));
+    for (int d0 = 0; d0 < NB; d0 += VG) {
+      v8 vfr[VG];
 #pragma unroll
-    for (int db = 0; db < NB; ++db) {
-      acc[0][db] = Elem<TV>::mma(vfr[db], pb[0], acc[0][db]);
-      acc[1][db] = Elem<TV>::mma(vfr[db], pb[1], acc[1][db]);
+      for (int db = 0; db < VG; ++db) vfr[db] = lds_v8<TV>(vf + VT::offset((d0 + db) * 16, 0));
+#pragma unroll
+      for (int db = 0; db < VG; ++db) {
+        acc[0][d0 + db] = Elem<TV>::mma(vfr[db], pb[0], acc[0][d0 + db]);
+        acc[1][d0 + db] = Elem<TV>::mma(vfr[db], pb[1], acc[1][d0 + db]);
+      }
     }
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
@@ -370,16 +411,39 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       for (int kt = 0; kt < n_kt; ++kt) step(std::false_type{}, u0 + kt, s, kt);
     }
     const float wmap = map_weight(p, s);
+    // A chunk of a split key range (one map) stores its normalized outputs,
+    // reference and row sums in fp32 for the merge kernel; otherwise the map's
+    // output goes to its slot (or into the mix).
+    const bool partial = n_chunks > 1;
+    float* part = p.part + (static_cast<int64_t>(blockIdx.x) * p.n_items + blockIdx.y) * (QT * (DS + 2));
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const float l = group_sum(l_part[cb]);
-      const float w = wmap / (l > 0.f ? l : 1.f);
-      const int tq = qw0 + cb * 16 + c;
+      const float w = (partial ? 1.f : wmap) / (l > 0.f ? l : 1.f);
+      const int ql = wave * kAttnQW + cb * 16 + c;
+      const int tq = q0 + ql;
       if constexpr (MULTI) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) yacc[cb][i] += acc[cb][i] * w;
       } else {
-        if (tq < p.T) store_rows<TV, DS>(p, b, (p.flags & kAttnMix) ? 0 : s, tq, g, ds0, acc[cb], w);
+        TV* orow = static_cast<TV*>(p.out) + b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t +
+                   ((p.flags & kAttnMix) ? 0 : s) * p.out_stride_s + ds0;
+#pragma unroll
+        for (int db = 0; db < NB; ++db) {
+          const f32x4 v = acc[cb][db] * w;
+          if (partial) {
+            *reinterpret_cast<f32x4*>(part + ql * DS + db * 16 + 4 * g) = v;
+          } else if (tq < p.T) {
+            typename Elem<TV>::v4 o;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[r] = static_cast<TV>(v[r]);
+            *reinterpret_cast<typename Elem<TV>::v4*>(orow + db * 16 + 4 * g) = o;
+          }
+        }
+        if (partial && g == 0) {
+          part[QT * DS + ql] = fixed ? p.score_bound * sc : m_run[cb];
+          part[QT * DS + QT + ql] = l;
+        }
       }
 #pragma unroll
       for (int i = 0; i < NB; ++i) acc[cb][i] = zero4();
@@ -401,48 +465,132 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   wait_vmem();
 }
 
-template <typename TQ, typename TV, int RP, int DS, bool MULTI>
-static void launch_attn_3(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
-  p.n_slices = a.D / DS;
-  p.n_qt = static_cast<int>((a.T + 2 * kAttnQW - 1) / (2 * kAttnQW));
-  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 2, MULTI>), dim3(a.B * p.n_slices, p.n_qt), dim3(128), 0, s,
-                     p);
+// Merge of split key ranges: out = sum_c 2^(m_c - M) l_c o_c / sum_c 2^(m_c - M) l_c,
+// o_c = O_c / l_c the chunk's normalized output, M = max_c m_c, per query row
+// (one map, weight 1).
+template <typename TV, int DS>
+__global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
+  constexpr int QT = 2 * kAttnQW;
+  const int qt = p.n_qt - 1 - static_cast<int>(blockIdx.y);
+  const int n_ch = chunks_of(p, qt, QT);
+  if (n_ch <= 1) return;   // written directly by its only item
+  int first = 0;
+  for (int t = p.n_qt - 1; t > qt; --t) first += chunks_of(p, t, QT);
+  const int b = static_cast<int>(blockIdx.x) / p.n_slices;
+  const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;
+  constexpr int ITEM = QT * (DS + 2);
+  const float* part = p.part + (static_cast<int64_t>(blockIdx.x) * p.n_items + first) * ITEM;
+  for (int e = threadIdx.x; e < QT * DS / 4; e += 256) {
+    const int ql = e / (DS / 4);
+    const int d4 = (e - ql * (DS / 4)) * 4;
+    const int tq = qt * QT + ql;
+    if (tq >= p.T) continue;
+    float M = -INFINITY;
+    for (int c = 0; c < n_ch; ++c) M = fmaxf(M, part[c * ITEM + QT * DS + ql]);
+    float den = 0.f;
+    f32x4 o = zero4();
+    for (int c = 0; c < n_ch; ++c) {
+      const float m = part[c * ITEM + QT * DS + ql];
+      const float w = m == -INFINITY ? 0.f : exp2f(m - M);
+      const float wl = w * part[c * ITEM + QT * DS + QT + ql];   // stored outputs are O_c / l_c
+      den += wl;
+      o += wl * *reinterpret_cast<const f32x4*>(part + c * ITEM + ql * DS + d4);
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    typename Elem<TV>::v4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(o[i] * inv);
+    *reinterpret_cast<typename Elem<TV>::v4*>(static_cast<TV*>(p.out) + b * p.out_stride_b +
+                                              static_cast<int64_t>(tq) * p.out_stride_t + ds0 + d4) = v;
+  }
 }
 
-// Value slice per workgroup: as wide as possible (one score tile serves more
-// value columns, and the softmax is shared by more MFMAs) while the grid keeps
-// at least 256 workgroups.  The register budget caps it at 256 features, and
-// at 128 with the map mix (a second accumulator set) or 512-wide scores.
+template <typename TQ, typename TV, int RP, int DS, bool MULTI>
+static void launch_attn_3(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
+  p.n_slices = a.D / DS;
+  p.n_qt = plan.n_qt;
+  p.chunk_tiles = plan.chunk_tiles;
+  p.n_items = plan.n_items;
+  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 2, MULTI>), dim3(a.B * p.n_slices, plan.n_items), dim3(128),
+                     0, s, p);
+  if constexpr (!MULTI) {
+    if (plan.chunk_tiles > 0)
+      hipLaunchKernelGGL((attention_merge_kernel<TV, DS>), dim3(a.B * p.n_slices, plan.n_qt), dim3(256), 0, s, p);
+  }
+}
+
 template <typename TQ, typename TV, int RP>
-static void launch_attn_1(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
+static void launch_attn_1(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
   const bool multi = (a.flags & kAttnMix) && a.S > 1;
-  const int64_t tiles = static_cast<int64_t>(a.B) * ((a.T + 2 * kAttnQW - 1) / (2 * kAttnQW));
-  int ds = min(a.D, (multi || RP == 512) ? 128 : 256);
-  while (ds > 128 && tiles * (a.D / ds) < 256) ds /= 2;
-  if (ds == 64) {
-    if (multi) launch_attn_3<TQ, TV, RP, 64, true>(a, p, s);
-    else launch_attn_3<TQ, TV, RP, 64, false>(a, p, s);
-  } else if (ds == 128) {
-    if (multi) launch_attn_3<TQ, TV, RP, 128, true>(a, p, s);
-    else launch_attn_3<TQ, TV, RP, 128, false>(a, p, s);
+  if (plan.ds == 64) {
+    if (multi) launch_attn_3<TQ, TV, RP, 64, true>(a, plan, p, s);
+    else launch_attn_3<TQ, TV, RP, 64, false>(a, plan, p, s);
+  } else if (plan.ds == 128) {
+    if (multi) launch_attn_3<TQ, TV, RP, 128, true>(a, plan, p, s);
+    else launch_attn_3<TQ, TV, RP, 128, false>(a, plan, p, s);
   } else {
-    if constexpr (RP < 512) launch_attn_3<TQ, TV, RP, 256, false>(a, p, s);
+    if constexpr (RP < 512) launch_attn_3<TQ, TV, RP, 256, false>(a, plan, p, s);
   }
 }
 
 template <typename TQ, typename TV>
-static void launch_attn_0(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
+static void launch_attn_0(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
   switch (a.RP) {
-    case 64: launch_attn_1<TQ, TV, 64>(a, p, s); break;
-    case 128: launch_attn_1<TQ, TV, 128>(a, p, s); break;
-    case 256: launch_attn_1<TQ, TV, 256>(a, p, s); break;
-    default: launch_attn_1<TQ, TV, 512>(a, p, s); break;
+    case 64: launch_attn_1<TQ, TV, 64>(a, plan, p, s); break;
+    case 128: launch_attn_1<TQ, TV, 128>(a, plan, p, s); break;
+    case 256: launch_attn_1<TQ, TV, 256>(a, plan, p, s); break;
+    default: launch_attn_1<TQ, TV, 512>(a, plan, p, s); break;
   }
 }
 
-void launch_routed_attention(const AttentionArgs& a, hipStream_t stream) {
+// Key tiles of query tile qt of `length` tokens (host copy of key_tiles_of).
+static int64_t host_key_tiles(int64_t qt, int64_t qtile, int64_t length, bool causal) {
+  if (!causal) return (length + kKeyTile - 1) / kKeyTile;
+  return (std::min(qt * qtile + qtile, length) - 1) / kKeyTile + 1;
+}
+
+AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, bool multi, bool causal,
+                        bool allow_split) {
+  AttnPlan plan{};
+  const int64_t qtile = 2 * kAttnQW;
+  plan.n_qt = static_cast<int>((T + qtile - 1) / qtile);
+  // Value slice: as wide as possible (one score tile serves more value columns
+  // and the softmax is shared by more MFMAs) while the grid keeps at least 256
+  // workgroups.  The register budget caps it at 256 features, and at 128 with
+  // the map mix (a second accumulator set) or 512-wide scores.
+  const int64_t tiles = B * plan.n_qt;
+  int64_t ds = std::min<int64_t>(D, (multi || RP == 512) ? 128 : 256);
+  while (ds > 128 && tiles * (D / ds) < 256) ds /= 2;
+  plan.ds = static_cast<int>(ds);
+  const int64_t slices = D / ds;
+  plan.n_items = plan.n_qt;
+  plan.chunk_tiles = 0;
+  // Long key ranges (one map only) on a grid that cannot fill the chip twice:
+  // split them into chunks so that the grid holds enough workgroups for every
+  // SIMD and the causal staircase is cut into pieces of similar length.
+  // Chunks keep >= 32 key tiles: below that the partials' traffic and the
+  // merge cost more than the balance gains.
+  const int64_t most = host_key_tiles(plan.n_qt - 1, qtile, T, causal);
+  if (allow_split && S == 1 && B * slices * plan.n_qt < 512 && most >= 64) {
+    for (int64_t kc = 256; kc >= 32; kc /= 2) {
+      if (kc >= most) continue;
+      int64_t items = 0;
+      for (int64_t qt = 0; qt < plan.n_qt; ++qt) items += (host_key_tiles(qt, qtile, T, causal) + kc - 1) / kc;
+      plan.chunk_tiles = static_cast<int>(kc);
+      plan.n_items = static_cast<int>(items);
+      if (B * slices * items >= 512) break;
+    }
+  }
+  plan.part_bytes = plan.chunk_tiles > 0 ? B * slices * plan.n_items * qtile * (ds + 2) * 4 : 0;
+  return plan;
+}
+
+void launch_routed_attention(const AttentionArgs& a, void* partials, hipStream_t stream) {
   if (a.T == 0 || a.B == 0) return;
+  const AttnPlan plan = plan_attention(a.B, a.S, a.T, a.D, a.RP, (a.flags & kAttnMix) && a.S > 1,
+                                       a.flags & kAttnCausal, partials != nullptr);
   AttnParams p;
+  p.part = static_cast<float*>(partials);
   p.q = a.q;
   p.k = a.k;
   p.qk_stride_b = a.qk_stride_b;
@@ -465,9 +613,9 @@ void launch_routed_attention(const AttentionArgs& a, hipStream_t stream) {
   p.out_stride_b = a.out_stride_b;
   p.out_stride_t = a.out_stride_t;
   p.out_stride_s = a.out_stride_s;
-  if (a.qk_dtype == kF16 && a.v_dtype == kBF16) launch_attn_0<_Float16, __bf16>(a, p, stream);
-  else if (a.qk_dtype == kF16) launch_attn_0<_Float16, _Float16>(a, p, stream);
-  else launch_attn_0<__bf16, __bf16>(a, p, stream);
+  if (a.qk_dtype == kF16 && a.v_dtype == kBF16) launch_attn_0<_Float16, __bf16>(a, plan, p, stream);
+  else if (a.qk_dtype == kF16) launch_attn_0<_Float16, _Float16>(a, plan, p, stream);
+  else launch_attn_0<__bf16, __bf16>(a, plan, p, stream);
 }
 
 }  // namespace da

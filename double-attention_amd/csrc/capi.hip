@@ -4,6 +4,7 @@
 // kernels on the caller's stream.  Nothing is allocated, freed or
 // synchronized here.  Validation failures return before any launch so the
 // stream is untouched; launch failures are reported from hipGetLastError.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -101,7 +102,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 4; }
+int da_abi_version(void) { return 5; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -141,6 +142,14 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
   return check_launch("route");
 }
 
+int64_t da_attention_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t score_dim,
+                                     int64_t value_dim, int flags) {
+  if (batch < 1 || maps < 1 || length < 1 || value_dim < 1) return 0;
+  const bool multi = (flags & DA_ATTN_MIX) && maps > 1;
+  return align_up(da::plan_attention(batch, maps, length, value_dim, score_dim, multi, flags & DA_ATTN_CAUSAL, true)
+                      .part_bytes);
+}
+
 int da_routed_attention(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
                         int64_t map_stride, int64_t map_repeat, int64_t score_dim,
                         const void* value_t, int64_t vt_stride_b,
@@ -148,7 +157,8 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
                         const void* scales, int scales_dtype, float scale_mult,
                         const void* mix_logits, int mix_dtype, int flags, float score_bound,
                         int qk_dtype, int v_dtype, void* out, int64_t out_stride_b,
-                        int64_t out_stride_t, int64_t out_stride_s, da_stream_t stream) {
+                        int64_t out_stride_t, int64_t out_stride_s, void* workspace,
+                        int64_t workspace_bytes, da_stream_t stream) {
   int rc = validate_attention(query, key, stride_b, stride_t, map_stride, map_repeat, score_dim,
                               value_t, vt_stride_b, batch, maps, length, value_dim,
                               scales, scales_dtype, mix_logits, mix_dtype, qk_dtype, v_dtype, out,
@@ -156,6 +166,13 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
   if (rc) return rc;
   if (!(score_bound >= 0.f) || std::isinf(score_bound))
     return fail(DA_ERR_INVALID_ARGUMENT, "attention: score_bound must be finite and >= 0");
+  const int64_t need = da_attention_workspace_bytes(batch, maps, length, score_dim, value_dim, flags);
+  if (workspace && need > 0) {
+    if (!aligned(workspace, 256)) return fail(DA_ERR_ALIGNMENT, "attention: workspace must be 256-byte aligned");
+    if (workspace_bytes < need)
+      return fail(DA_ERR_WORKSPACE, "attention: workspace of %lld bytes < %lld required",
+                  (long long)workspace_bytes, (long long)need);
+  }
   if (batch == 0 || length == 0) return ok();
   da::AttentionArgs a;
   a.q = query;
@@ -184,7 +201,7 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
   a.out_stride_b = out_stride_b;
   a.out_stride_t = out_stride_t;
   a.out_stride_s = out_stride_s;
-  da::launch_routed_attention(a, reinterpret_cast<hipStream_t>(stream));
+  da::launch_routed_attention(a, need > 0 ? workspace : nullptr, reinterpret_cast<hipStream_t>(stream));
   return check_launch("attention");
 }
 
@@ -244,12 +261,23 @@ int64_t da_sda_workspace_offset(int64_t batch, int64_t length, int64_t model_dim
   return routed + vt;
 }
 
+// Split-key partials of the outer attention (one map only: then the score
+// width equals qk_width); the larger of the causal and non-causal plans.
+static int64_t attention_partial_bytes(int64_t batch, int64_t length, int64_t model_dim, int64_t qk_width,
+                                       int64_t outer_maps) {
+  if (outer_maps != 1) return 0;
+  const da::AttnPlan causal = da::plan_attention(batch, 1, length, model_dim, qk_width, false, true, true);
+  const da::AttnPlan full = da::plan_attention(batch, 1, length, model_dim, qk_width, false, false, true);
+  return align_up(std::max(causal.part_bytes, full.part_bytes));
+}
+
 int64_t da_sda_workspace_bytes(int64_t batch, int64_t length, int64_t model_dim, int64_t qk_width,
                                int64_t outer_maps, int concat, int has_output_projection) {
   const int64_t tokens = batch * length;
   const int64_t mixed =
       has_output_projection ? align_up(tokens * (concat ? outer_maps : 1) * model_dim * 2) : 0;
-  return da_sda_workspace_offset(batch, length, model_dim, qk_width, 2) + mixed;
+  return da_sda_workspace_offset(batch, length, model_dim, qk_width, 2) + mixed +
+         attention_partial_bytes(batch, length, model_dim, qk_width, outer_maps);
 }
 
 int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stream_t stream) {
@@ -278,6 +306,10 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   void* routed = ws;
   void* vt = ws + da_sda_workspace_offset(B, T, d, W, 1);
   void* mixed = a->wo ? ws + da_sda_workspace_offset(B, T, d, W, 2) : a->out;
+  const int64_t mixed_bytes = a->wo ? align_up(B * T * (concat ? S : 1) * d * 2) : 0;
+  void* partials = attention_partial_bytes(B, T, d, W, S) > 0
+                       ? ws + da_sda_workspace_offset(B, T, d, W, 2) + mixed_bytes
+                       : nullptr;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
   // Validate every stage before enqueueing the first one.
@@ -350,7 +382,7 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   at.out_stride_b = T * ot;
   at.out_stride_t = ot;
   at.out_stride_s = concat ? d : 0;
-  da::launch_routed_attention(at, s);
+  da::launch_routed_attention(at, partials, s);
   // 4. Output projection.
   if (a->wo) {
     da::GemmSegment o{a->wo, nullptr, 0, mixed, d, B * T, ot, nullptr, 0, 0, a->out, d, 0, 0, 0};

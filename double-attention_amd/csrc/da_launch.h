@@ -98,7 +98,20 @@ void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int
                                  int M, float eps, void* key_t, int key_dtype, void* value,
                                  hipStream_t stream);
 void launch_dictionary_route(const RouteArgs& a, hipStream_t stream);
-void launch_routed_attention(const AttentionArgs& a, hipStream_t stream);
+// Launch shape of the attention for a problem: value slice width, key-range
+// chunking (0 = none) and the bytes of split-key partials it needs.
+struct AttnPlan {
+  int ds;
+  int chunk_tiles;
+  int n_qt;
+  int n_items;
+  int64_t part_bytes;
+};
+AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, bool multi, bool causal,
+                        bool allow_split);
+// `partials`: plan.part_bytes of device scratch (plan with allow_split), or
+// nullptr to run without key-range splitting.
+void launch_routed_attention(const AttentionArgs& a, void* partials, hipStream_t stream);
 void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream);
 
 }  // namespace da

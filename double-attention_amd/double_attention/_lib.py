@@ -38,7 +38,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -94,6 +94,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i64, _i32, _vp,  # out, out pitch, out dtype, stream
         ],
     ),
+    "da_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32]),
     "da_routed_attention": (
         _i32,
         [
@@ -102,7 +103,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _i64, _i64, _i64, _i64,  # batch, maps, length, value_dim
             _vp, _i32, _f32, _vp, _i32,  # scales, mix logits
             _i32, _f32,  # flags, score bound
-            _i32, _i32, _vp, _i64, _i64, _i64, _vp,  # qk/v dtypes, out + strides, stream
+            _i32, _i32, _vp, _i64, _i64, _i64,  # qk/v dtypes, out + strides
+            _vp, _i64, _vp,  # workspace, its bytes, stream
         ],
     ),
     "da_qkv_projection": (

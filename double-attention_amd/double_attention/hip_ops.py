@@ -370,6 +370,9 @@ def _attention_forward(
     out = torch.empty(batch, maps, length, value_width, dtype=value.dtype, device=value.device)
     scales_c = scales.detach().contiguous()
     lib = _lib.get()
+    flags = _lib.DA_ATTN_CAUSAL if causal else 0
+    ws_bytes = lib.da_attention_workspace_bytes(batch, maps, length, score_width, value_width, flags)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=value.device) if ws_bytes > 0 else None
     _lib.check(
         lib.da_routed_attention(
             q.data_ptr(), k.data_ptr(),
@@ -377,9 +380,10 @@ def _attention_forward(
             vt.data_ptr(), vt.stride(0),
             batch, maps, length, value_width,
             scales_c.data_ptr(), dtype_code(scales_c.dtype), 1.0, None, _lib.DA_F32,
-            _lib.DA_ATTN_CAUSAL if causal else 0, float(score_bound),
+            flags, float(score_bound),
             _half_code(q.dtype), _half_code(value.dtype),
             out.data_ptr(), out.stride(0), out.stride(2), out.stride(1),
+            _ptr(workspace), ws_bytes,
             _stream(value.device),
         ),
         "routed_attention_hip",

@@ -125,6 +125,8 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  *   DA_ATTN_MIX: out(b, t) = sum_s alpha_s O_s(b, t), alpha = softmax(mix_logits)
  *     (uniform 1/maps if mix_logits is NULL); else O_s(b, t) goes to
  *     out + b*out_stride_b + t*out_stride_t + s*out_stride_s.
+ *   workspace: NULL, or >= da_attention_workspace_bytes(...) bytes, 256-byte
+ *     aligned (scratch for split key ranges; see below).
  *   score_bound: 0, or an upper bound on |q . k| over all raw query/key rows
  *     (1 for L2-normalized rows).  With a bound, maps whose scaled bound fits
  *     the probability type skip the online-softmax rescaling (bf16 V only).
@@ -140,7 +142,14 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
                         const void* scales, int scales_dtype, float scale_mult,
                         const void* mix_logits, int mix_dtype, int flags, float score_bound,
                         int qk_dtype, int v_dtype, void* out, int64_t out_stride_b,
-                        int64_t out_stride_t, int64_t out_stride_s, da_stream_t stream);
+                        int64_t out_stride_t, int64_t out_stride_s, void* workspace,
+                        int64_t workspace_bytes, da_stream_t stream);
+
+/* Scratch bytes da_routed_attention can use (0 if it needs none): fp32
+ * partials of long causal key ranges split over workgroups and merged by a
+ * second kernel.  Passing a NULL workspace is always allowed (no splitting). */
+int64_t da_attention_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t score_dim,
+                                     int64_t value_dim, int flags);
 
 /*
  * Q/K and V projections in one launch (modules.py:143-157 and 212):
@@ -190,7 +199,9 @@ typedef struct da_sda_forward_args {
 /* Workspace layout (byte offsets, each 256-aligned):
  *   routed [tokens, 2*qk_width]   Q/K projections, routed in place (fp16 out)
  *   value_t [batch, padded_length/32, model_dim, 32]  (32-token tiles)
- *   mixed  [tokens, model_dim or maps*model_dim] (only with an output projection) */
+ *   mixed  [tokens, model_dim or maps*model_dim] (only with an output projection)
+ *   then, with one outer map, fp32 partial results of the attention over
+ *   chunks of long causal key ranges (merged by a second kernel). */
 int64_t da_sda_workspace_bytes(int64_t batch, int64_t length, int64_t model_dim,
                                int64_t qk_width, int64_t outer_maps, int concat,
                                int has_output_projection);

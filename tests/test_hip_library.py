@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 12
+    assert len(names) == 13
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -37,6 +37,11 @@ def test_abi_version_and_helpers() -> None:
     # C1 workspace: routed [4096, 512] + V^T [8, 512, 512] + mixed [4096, 512], bf16.
     assert h.da_sda_workspace_bytes(8, 512, 512, 256, 1, 0, 1) == 3 * 4096 * 512 * 2
     assert h.da_sda_workspace_bytes(8, 512, 512, 256, 1, 0, 0) == 2 * 4096 * 512 * 2
+    # C5 (one long sequence) adds the fp32 partials of split causal key ranges.
+    base_c5 = 8192 * 512 * 2 * 3
+    partials = h.da_sda_workspace_bytes(1, 8192, 512, 256, 1, 0, 1) - base_c5
+    assert partials > 0 and partials % 256 == 0
+    assert h.da_sda_workspace_bytes(1, 8192, 512, 256, 4, 0, 1) == base_c5
     assert h.da_sda_workspace_offset(8, 512, 512, 256, 1) == 4096 * 512 * 2
 
 
@@ -80,7 +85,7 @@ def test_attention_rejects_bad_arguments_before_launch() -> None:
         _fake(), 512 * 512,  # value_t, per-sequence pitch
         2, 1, 512, 512,  # batch, maps, length, value dim
         _fake(), lib.DA_F32, 1.0, None, lib.DA_F32,
-        lib.DA_ATTN_CAUSAL, 1.0, lib.DA_F16, lib.DA_BF16, _fake(), 512 * 512, 512, 0, None,
+        lib.DA_ATTN_CAUSAL, 1.0, lib.DA_F16, lib.DA_BF16, _fake(), 512 * 512, 512, 0, None, 0, None,
     ]
     bad_types = list(base)
     bad_types[20], bad_types[21] = lib.DA_BF16, lib.DA_F16
@@ -99,6 +104,15 @@ def test_attention_rejects_bad_arguments_before_launch() -> None:
     bad_bound[19] = -1.0
     assert h.da_routed_attention(*bad_bound) == -1
     assert "score_bound" in h.da_last_error().decode()
+    # Split-key scratch: a C5-sized causal problem wants some, a short one none;
+    # a workspace that is given must be large enough.
+    need = h.da_attention_workspace_bytes(1, 1, 8192, 256, 512, lib.DA_ATTN_CAUSAL)
+    assert need > 0 and need % 256 == 0
+    assert h.da_attention_workspace_bytes(2, 1, 512, 256, 512, lib.DA_ATTN_CAUSAL) == 0
+    long_ctx = list(base)
+    long_ctx[9], long_ctx[11], long_ctx[26], long_ctx[27] = 1, 8192, _fake(), need - 256
+    long_ctx[8] = 8192 * 512
+    assert h.da_routed_attention(*long_ctx) == -5
 
 
 def test_forward_rejects_small_workspace() -> None:
