@@ -176,7 +176,8 @@ def main() -> None:
             "route": lambda: lib.da_dictionary_route(
                 qk.data_ptr(), rows, R, R, code, layout.key_t.data_ptr(), key_code, layout.value.data_ptr(), M,
                 p["log_beta"].data_ptr(), pdt, 0.0, config.eps,
-                _lib.DA_ROUTE_NORMALIZE_INPUT | _lib.DA_ROUTE_NORMALIZE_OUTPUT | _lib.DA_ROUTE_BETA_IS_LOG,
+                _lib.DA_ROUTE_NORMALIZE_INPUT | _lib.DA_ROUTE_NORMALIZE_OUTPUT | _lib.DA_ROUTE_BETA_IS_LOG
+                | _lib.DA_ROUTE_UNIT_KEYS,
                 routed.data_ptr(), R, _lib.DA_F16, handle),
             "attention": lambda: lib.da_routed_attention(
                 routed.data_ptr(), routed.data_ptr() + W * routed.element_size(), length * 2 * W, 2 * W,

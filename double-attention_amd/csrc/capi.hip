@@ -318,7 +318,7 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   if (W % 8) return fail(DA_ERR_UNSUPPORTED, "forward: qk width must be a multiple of 8");
   const bool norm_in = a->flags & DA_SDA_NORMALIZE_INPUT;
   const int key_dtype = norm_in ? DA_F16 : a->dtype;
-  int rflags = da::kRouteBetaIsLog;
+  int rflags = da::kRouteBetaIsLog | da::kRouteUnitKeys;   // the bank comes from da_dictionary_normalize
   if (norm_in) rflags |= da::kRouteNormalizeInput;
   if (a->flags & DA_SDA_NORMALIZE_OUTPUT) rflags |= da::kRouteNormalizeOutput;
   rc = validate_route(routed, B * T * 2 * H, R, R, a->dtype, a->key_t, key_dtype, a->value, a->atoms,

@@ -21,6 +21,7 @@ enum : int {
   kRouteNormalizeInput = 1,
   kRouteNormalizeOutput = 2,
   kRouteBetaIsLog = 4,
+  kRouteUnitKeys = 8,
 };
 
 // Attention flags.

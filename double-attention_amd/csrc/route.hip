@@ -26,6 +26,8 @@
 // the softmax weights are fp16 (both bounded by 1), TO = output rows.  Value
 // atoms are stored in 32-atom tiles: coordinate r of atom j at
 // value[(j/32)*32*R + 32*r + j%32].
+#include <type_traits>
+
 #include "da_common.h"
 #include "da_launch.h"
 #include "da_tile.h"
@@ -33,85 +35,103 @@
 namespace da {
 
 constexpr int kRouteWaves = 4;
+constexpr int kRouteQW = 16;    // rows per wave (one MFMA column block)
+constexpr int kRouteAT = 32;    // atoms per tile
+constexpr int kRouteRows = kRouteWaves * kRouteQW;
+// Fixed-reference mode keeps fp16 probabilities in [2^(kP16Lift - 2*beta*log2e), 2^kP16Lift].
+constexpr float kP16Lift = 14.f;
 
 template <int R>
-struct RouteCfg {
-  static constexpr int QW = 16;                   // rows per wave
-  static constexpr int AT = 32;                   // atoms per tile
-  typedef PaddedTile<AT, R / 8, true> KT;         // key atoms (blocked rows)
-  typedef PaddedTile<R, AT / 8, false> VT;        // value coordinates x atoms
-  static constexpr int LOADS = KT::LOADS + VT::LOADS;
-  static constexpr int PER_WAVE = (LOADS + kRouteWaves - 1) / kRouteWaves;
-  static constexpr int BYTES = LOADS * 1024;
-  static constexpr int ROWS = kRouteWaves * QW;   // rows per workgroup
+struct RouteTile {
+  typedef PaddedTile<kRouteAT, R / 8, true> KT;     // key atoms (blocked rows)
+  typedef PaddedTile<R, kRouteAT / 8, false> VT;    // value coordinates x atoms
+  static constexpr int KPW = (KT::LOADS + kRouteWaves - 1) / kRouteWaves;
+  static constexpr int VPW = (VT::LOADS + kRouteWaves - 1) / kRouteWaves;
+  static constexpr int BYTES = KT::BYTES + VT::BYTES;   // one stage: key atoms, then value atoms
 };
 
+// The atom tiles t = 0 .. n_tiles-1 are pipelined like the outer attention:
+// stage buffer t%2 holds the key atoms of tile t+1 and the value atoms of tile
+// t, so step t forms the logits of tile t+1 (MFMA) while it turns the logits
+// of tile t into weights (VALU) and accumulates their reconstruction (MFMA).
 template <typename TX, typename TK, typename TO, int R>
-__global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(
+__global__ __launch_bounds__(kRouteWaves * 64, R >= 512 ? 1 : 2) void route_kernel(
     const TX* x, int64_t rows, int64_t x_stride, const TK* __restrict__ key_t,
     const _Float16* __restrict__ value, int M, int Mp, const void* __restrict__ beta_ptr,
     int beta_dtype, float beta_value, float eps, int flags, TO* out, int64_t out_stride) {
   // x and out may alias (in-place routing): every row is read into VGPRs by
   // its own wave before that wave writes it.
-  typedef RouteCfg<R> Cfg;
-  typedef typename Cfg::KT KT;
-  typedef typename Cfg::VT VT;
+  typedef RouteTile<R> Tile;
+  typedef typename Tile::KT KT;
+  typedef typename Tile::VT VT;
   typedef typename Elem<TK>::v8 k8;
   constexpr int KS = R / 32;
-  constexpr int AT = Cfg::AT;
-  constexpr int CB = Cfg::QW / 16;   // column blocks per wave
-  constexpr int NB = AT / 16;        // atom blocks per tile
-  __shared__ __attribute__((aligned(1024))) char lds0[Cfg::BYTES];
-  __shared__ __attribute__((aligned(1024))) char lds1[Cfg::BYTES];
+  constexpr int RB = R / 16;           // output row blocks
+  constexpr int NL = Tile::KPW + Tile::VPW;
+  __shared__ __attribute__((aligned(1024))) char lds0[Tile::BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds1[Tile::BYTES];
 
   const int lane = lane_id();
   const int c = lane & 15;
   const int g = lane >> 4;
   const int wave = uniform_wave();
-  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kRouteWaves + wave) * Cfg::QW;
-  const int n_tiles = Mp / AT;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kRouteWaves + wave) * kRouteQW;
+  const int n_tiles = Mp / kRouteAT;
 
-  // Per-lane DMA sources relative to the tile's atom offset: key atoms are
-  // rows of key_t, value chunks live in 32-atom tiles.
-  int desc[Cfg::PER_WAVE];
+  // Per-lane DMA sources (byte offsets from the tile's first atom): key load i
+  // fills wave load i*4 + wave of the key tile (rows of key_t), value load i
+  // the same wave load of the value tile (32-atom tiles of the value bank).
+  // Wave loads past a tile's end re-load the data of wave load 0 into slot 0.
+  uint32_t kdesc[Tile::KPW], vdesc[Tile::VPW];
 #pragma unroll
-  for (int i = 0; i < Cfg::PER_WAVE; ++i) {
+  for (int i = 0; i < Tile::KPW; ++i) {
+    int row, ck;
     const int j = i * kRouteWaves + wave;
-    int row = 0, ck = 0;
-    if (j < KT::LOADS) {
-      KT::slot_chunk(j * 64 + lane, row, ck);
-      desc[i] = row * R + ck * 8;
-    } else if (j < Cfg::LOADS) {
-      VT::slot_chunk((j - KT::LOADS) * 64 + lane, row, ck);
-      desc[i] = (ck >> 2) * 32 * R + row * 32 + (ck & 3) * 8;
-    } else {
-      desc[i] = 0;
-    }
+    KT::slot_chunk((j < KT::LOADS ? j : 0) * 64 + lane, row, ck);
+    kdesc[i] = static_cast<uint32_t>((row * R + ck * 8) * sizeof(TK));
   }
-  auto issue = [&](char* buf, int t) {
-    const int j0 = t * AT;
-    const TK* ktile = key_t + static_cast<int64_t>(j0) * R;
-    const _Float16* vtile = value + static_cast<int64_t>(j0) * R;   // 32-atom tiles: j0/32 * 32R
 #pragma unroll
-    for (int i = 0; i < Cfg::PER_WAVE; ++i) {
-      const int j = i * kRouteWaves + wave;
-      if (j < KT::LOADS) dma16(ktile + desc[i], buf + j * 1024);
-      else if (j < Cfg::LOADS) dma16(vtile + desc[i], buf + j * 1024);
+  for (int i = 0; i < Tile::VPW; ++i) {
+    int row, ck;
+    const int j = i * kRouteWaves + wave;
+    VT::slot_chunk((j < VT::LOADS ? j : 0) * 64 + lane, row, ck);
+    vdesc[i] = static_cast<uint32_t>(((ck >> 2) * 32 * R + row * 32 + (ck & 3) * 8) * 2);
+  }
+  auto slot_of = [&](int n) {
+    if (n < Tile::KPW) {
+      const int j = n * kRouteWaves + wave;
+      return j < KT::LOADS ? j * 1024 : 0;
+    }
+    const int j = (n - Tile::KPW) * kRouteWaves + wave;
+    return KT::BYTES + (j < VT::LOADS ? j * 1024 : 0);
+  };
+  const char* kbytes = reinterpret_cast<const char*>(key_t);
+  const char* vbytes = reinterpret_cast<const char*>(value);
+  // Load n of this wave's share of stage {K(tk), V(tv)}.
+  auto issue_one = [&](char* buf, int tk, int tv, int n) {
+    if (n < Tile::KPW) {
+      dma16(kbytes + static_cast<int64_t>(tk) * kRouteAT * R * sizeof(TK) + kdesc[n], buf + slot_of(n));
+    } else {
+      dma16(vbytes + static_cast<int64_t>(tv) * kRouteAT * R * 2 + vdesc[n - Tile::KPW], buf + slot_of(n));
     }
   };
-  issue(lds0, 0);
+
+  // Prologue DMA: keys of tile 0 into stage 1's key slot, stage 0 = {K(1), V(0)}.
+#pragma unroll
+  for (int n = 0; n < Tile::KPW; ++n) issue_one(lds1, 0, 0, n);
+#pragma unroll
+  for (int n = 0; n < NL; ++n) issue_one(lds0, min(1, n_tiles - 1), 0, n);
 
   // Row fragments (B operands of the assignment contraction), kept in VGPRs.
   const float beta_raw = beta_ptr ? load_scalar(beta_ptr, beta_dtype, 0) : beta_value;
   const float beta = (flags & kRouteBetaIsLog) ? expf(fminf(fmaxf(beta_raw, kLogBetaMin), kLogBetaMax)) : beta_raw;
-  // Logits -> log2-domain exponents.  The rescale test compares maxima of raw
-  // logits, so a negative beta is folded into the rows instead (exact).
+  // Logits -> log2-domain exponents.  Maxima are taken of raw logits, so a
+  // negative beta is folded into the rows instead (exact).
   const float scale = fabsf(beta) * kLog2e;
   const float sign = beta < 0.f ? -1.f : 1.f;
-  k8 xf[CB][KS];
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb) {
-    const int64_t row = row0 + cb * 16 + c;
+  k8 xf[KS];
+  {
+    const int64_t row = row0 + c;
     typename Elem<TX>::v8 xr[KS];
     float ss = 0.f;
 #pragma unroll
@@ -130,136 +150,152 @@ __global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xf[cb][kk][e] = static_cast<TK>(static_cast<float>(xr[kk][e]) * inv_norm);
+      for (int e = 0; e < 8; ++e) xf[kk][e] = static_cast<TK>(static_cast<float>(xr[kk][e]) * inv_norm);
   }
 
-  f32x4 acc[CB][R / 16];
+  f32x4 acc[RB];
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-    for (int i = 0; i < R / 16; ++i) acc[cb][i] = zero4();
-  float m_run[CB], l_part[CB];
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb) {
-    m_run[cb] = -INFINITY;
-    l_part[cb] = 0.f;
-  }
+  for (int i = 0; i < RB; ++i) acc[i] = zero4();
+  float m_run = -INFINITY, l_part = 0.f;
 
   const int kfrag = KT::offset(c, g);
   const int vfrag = KT::BYTES + VT::offset(c, g);
 
-  auto step = [&](int t, char* cur, char* nxt) {
-    wait_vmem();
-    __syncthreads();
-    if (t + 1 < n_tiles) issue(nxt, t + 1);
-    const int j0 = t * AT;
-
-    // Logits: NB x CB independent accumulator chains; each key fragment
-    // feeds all CB column blocks.
-    f32x4 s[CB][NB];
+  // Logits of 32 atoms x 16 rows from a key tile in LDS: two accumulator
+  // chains; fragments are read in groups (latency paid once per group) and
+  // the next stage's loads are spread between them.
+  auto logits = [&](const char* kt_lds, f32x4 (&st)[2], auto with_dma, char* nxt, int tk, int tv) {
+    st[0] = st[1] = zero4();
+    const char* kf = kt_lds + kfrag;
+    constexpr int KG = KS < 4 ? KS : 4;
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb)
+    for (int k0 = 0; k0 < KS; k0 += KG) {
+      k8 kfr[KG][2];
 #pragma unroll
-      for (int kb = 0; kb < NB; ++kb) s[cb][kb] = zero4();
-    const char* kf = cur + kfrag;
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      k8 a[NB];
-#pragma unroll
-      for (int kb = 0; kb < NB; ++kb) a[kb] = lds_v8<TK>(kf + KT::offset(16 * kb, kk * 4));
-#pragma unroll
-      for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) s[cb][kb] = Elem<TK>::mma(a[kb], xf[cb][kk], s[cb][kb]);
-    }
-    // Lane (c, g) holds atoms j0 + 32*(kb/2) + 8g + 4*(kb%2) + i of row c;
-    // only the last tile can hold padding atoms.
-    if (j0 + AT > M) {
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-        for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (j0 + 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + i >= M) s[cb][kb][i] = -INFINITY;
-    }
-    f16x8 pb[CB][AT / 32];
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      float lmax = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < NB; ++kb)
-        lmax = fmaxf(lmax, fmaxf(fmaxf(s[cb][kb][0], s[cb][kb][1]), fmaxf(s[cb][kb][2], s[cb][kb][3])));
-      lazy_rescale<R / 16>(lmax, scale, m_run[cb], l_part[cb], acc[cb]);
-      float psum = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < NB; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[cb][kb][i], scale, -m_run[cb]));
-          s[cb][kb][i] = pr;
-          psum += pr;
-        }
+      for (int kk = 0; kk < KG; ++kk) {
+        kfr[kk][0] = lds_v8<TK>(kf + KT::offset(0, (k0 + kk) * 4));
+        kfr[kk][1] = lds_v8<TK>(kf + KT::offset(16, (k0 + kk) * 4));
       }
-      l_part[cb] += psum;
 #pragma unroll
-      for (int w = 0; w < AT / 32; ++w) pb[cb][w] = pack_blocked<_Float16>(s[cb][2 * w], s[cb][2 * w + 1]);
-    }
-
-    const char* vf = cur + vfrag;
+      for (int kk = 0; kk < KG; ++kk) {
+        if constexpr (decltype(with_dma)::value) {
 #pragma unroll
-    for (int w = 0; w < AT / 32; ++w) {
-#pragma unroll
-      for (int rb = 0; rb < R / 16; ++rb) {
-        const f16x8 a = lds_v8<_Float16>(vf + VT::offset(16 * rb, 4 * w));
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) acc[cb][rb] = Elem<_Float16>::mma(a, pb[cb][w], acc[cb][rb]);
+          for (int n = 0; n < NL; ++n)
+            if (n * KS / NL == k0 + kk) issue_one(nxt, tk, tv, n);
+        }
+        st[0] = Elem<TK>::mma(kfr[kk][0], xf[k0 + kk], st[0]);
+        st[1] = Elem<TK>::mma(kfr[kk][1], xf[k0 + kk], st[1]);
       }
     }
   };
 
-  int t = 0;
-  for (; t + 1 < n_tiles; t += 2) {
-    step(t, lds0, lds1);
-    step(t + 1, lds1, lds0);
+  wait_vmem();
+  __syncthreads();
+  f32x4 st_prev[2];
+  logits(lds1, st_prev, std::false_type{}, nullptr, 0, 0);
+
+  // FIXED: unit rows and unit key atoms bound every logit by |beta|, so the
+  // exponents use the fixed reference (|beta| - kP16Lift) log2e: weights stay
+  // in fp16's normal range and the accumulators are never rescaled.
+  // Otherwise the lazy online rescale runs.
+  auto step = [&](auto fixed, int t) {
+    constexpr bool FIXED = decltype(fixed)::value;
+    char* cur = (t & 1) ? lds1 : lds0;
+    char* nxt = (t & 1) ? lds0 : lds1;
+    const int j0 = t * kRouteAT;
+    // Lane (c, g) holds atoms j0 + 8g + 4kb + i of row c; only the last tile
+    // can hold padding atoms.
+    if (j0 + kRouteAT > M) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (j0 + 8 * g + 4 * kb + i >= M) st_prev[kb][i] = -INFINITY;
+    }
+    float m_use;
+    if constexpr (FIXED) {
+      m_use = kP16Lift - scale;
+    } else {
+      const float lmax = fmaxf(fmaxf(fmaxf(st_prev[0][0], st_prev[0][1]), fmaxf(st_prev[0][2], st_prev[0][3])),
+                               fmaxf(fmaxf(st_prev[1][0], st_prev[1][1]), fmaxf(st_prev[1][2], st_prev[1][3])));
+      lazy_rescale<RB>(lmax, scale, m_run, l_part, acc);
+      m_use = -m_run;
+    }
+
+    wait_vmem();
+    __syncthreads();
+
+    f32x4 st_new[2];
+    logits(cur, st_new, std::true_type{}, nxt, min(t + 2, n_tiles - 1), min(t + 1, n_tiles - 1));
+
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(st_prev[kb][i], scale, m_use));
+        st_prev[kb][i] = pr;
+        psum += pr;
+      }
+    l_part += psum;
+    const f16x8 pb = pack_blocked<_Float16>(st_prev[0], st_prev[1]);   // atoms j0 + 8g + e
+
+    // O^T += Dv(t) P^T(t).
+    const char* vf = cur + vfrag;
+    constexpr int VG = RB < 8 ? RB : 8;
+#pragma unroll
+    for (int r0 = 0; r0 < RB; r0 += VG) {
+      f16x8 vfr[VG];
+#pragma unroll
+      for (int rb = 0; rb < VG; ++rb) vfr[rb] = lds_v8<_Float16>(vf + VT::offset(16 * (r0 + rb), 0));
+#pragma unroll
+      for (int rb = 0; rb < VG; ++rb) acc[r0 + rb] = Elem<_Float16>::mma(vfr[rb], pb, acc[r0 + rb]);
+    }
+    st_prev[0] = st_new[0];
+    st_prev[1] = st_new[1];
+  };
+
+  const bool fixed = (flags & kRouteNormalizeInput) && (flags & kRouteUnitKeys) && 2.f * scale <= 2.f * kP16Lift;
+  if (fixed) {
+    for (int t = 0; t < n_tiles; ++t) step(std::true_type{}, t);
+  } else {
+    for (int t = 0; t < n_tiles; ++t) step(std::false_type{}, t);
   }
-  if (t < n_tiles) step(t, lds0, lds1);
 
   // r = O / l; z = r / max(||r||, eps).
+  const float inv_l = 1.f / group_sum(l_part);
+  float out_scale = inv_l;
+  if (flags & kRouteNormalizeOutput) {
+    float rs = 0.f;
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb) {
-    const float inv_l = 1.f / group_sum(l_part[cb]);
-    float out_scale = inv_l;
-    if (flags & kRouteNormalizeOutput) {
-      float rs = 0.f;
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int rb = 0; rb < R / 16; ++rb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = acc[cb][rb][i] * inv_l;
-          rs += v * v;
-        }
-      rs = group_sum(rs);
-      out_scale = inv_l / fmaxf(sqrtf(rs), eps);
-    }
-    const int64_t row = row0 + cb * 16 + c;
-    if (row < rows) {
-      TO* orow = out + row * out_stride;
-#pragma unroll
-      for (int rb = 0; rb < R / 16; ++rb) {
-        typename Elem<TO>::v4 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = static_cast<TO>(acc[cb][rb][i] * out_scale);
-        *reinterpret_cast<typename Elem<TO>::v4*>(orow + rb * 16 + 4 * g) = o;
+      for (int i = 0; i < 4; ++i) {
+        const float v = acc[rb][i] * inv_l;
+        rs += v * v;
       }
+    rs = group_sum(rs);
+    out_scale = inv_l / fmaxf(sqrtf(rs), eps);
+  }
+  const int64_t row = row0 + c;
+  if (row < rows) {
+    TO* orow = out + row * out_stride;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      typename Elem<TO>::v4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = static_cast<TO>(acc[rb][i] * out_scale);
+      *reinterpret_cast<typename Elem<TO>::v4*>(orow + rb * 16 + 4 * g) = o;
     }
   }
+  // The last step's (redundant) stage loads must land before the workgroup's
+  // LDS is released.
+  wait_vmem();
 }
 
 template <typename TX, typename TK, typename TO, int R>
 static void launch_route_r(const RouteArgs& a, hipStream_t s) {
-  constexpr int ROWS = RouteCfg<R>::ROWS;
-  const int64_t blocks = (a.rows + ROWS - 1) / ROWS;
+  const int64_t blocks = (a.rows + kRouteRows - 1) / kRouteRows;
   hipLaunchKernelGGL((route_kernel<TX, TK, TO, R>), dim3(static_cast<unsigned>(blocks)), dim3(kRouteWaves * 64), 0,
                      s, static_cast<const TX*>(a.x), a.rows, a.x_stride, static_cast<const TK*>(a.key_t),
                      static_cast<const _Float16*>(a.value), a.M, static_cast<int>(round_up(a.M, kAtomPad)),

@@ -20,6 +20,7 @@ DA_F32, DA_F16, DA_BF16 = 0, 1, 2
 DA_ROUTE_NORMALIZE_INPUT = 1
 DA_ROUTE_NORMALIZE_OUTPUT = 2
 DA_ROUTE_BETA_IS_LOG = 4
+DA_ROUTE_UNIT_KEYS = 8
 
 DA_ATTN_CAUSAL = 1
 DA_ATTN_SCALES_ARE_LOG = 2

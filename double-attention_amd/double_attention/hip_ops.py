@@ -92,6 +92,7 @@ class RouteDictionary(NamedTuple):
     key_t: Tensor
     value: Tensor
     atoms: int
+    unit: bool = False   # key atoms have L2 norm <= 1 (a normalized bank)
 
 
 def _tag(key: Tensor, value: Tensor, layout: RouteDictionary) -> tuple[Tensor, Tensor]:
@@ -150,7 +151,7 @@ def dictionary_normalize_hip(
         ),
         "dictionary_normalize_hip",
     )
-    layout = RouteDictionary(key_t, value, atoms)
+    layout = RouteDictionary(key_t, value, atoms, True)
     return _tag(key_t[:atoms].t(), _untile_value(value)[:, :atoms], layout)
 
 
@@ -217,8 +218,10 @@ def _route_forward(
     if rows_view.stride(-1) != 1 or rows_view.stride(0) % 8 or rows_view.data_ptr() % 16:
         rows_view = rows_view.contiguous()
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    flags = (_lib.DA_ROUTE_NORMALIZE_INPUT if normalize_input else 0) | (
-        _lib.DA_ROUTE_NORMALIZE_OUTPUT if normalize_output else 0
+    flags = (
+        (_lib.DA_ROUTE_NORMALIZE_INPUT if normalize_input else 0)
+        | (_lib.DA_ROUTE_NORMALIZE_OUTPUT if normalize_output else 0)
+        | (_lib.DA_ROUTE_UNIT_KEYS if layout.unit else 0)
     )
     if isinstance(beta, Tensor):
         if beta.numel() != 1:

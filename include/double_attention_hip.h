@@ -53,6 +53,9 @@ typedef struct ihipStream_t* da_stream_t; /* hipStream_t; NULL = default stream 
 #define DA_ROUTE_NORMALIZE_INPUT 1  /* u = x / max(||x||, eps) before the assignment   */
 #define DA_ROUTE_NORMALIZE_OUTPUT 2 /* z = r / max(||r||, eps) after the reconstruction */
 #define DA_ROUTE_BETA_IS_LOG 4      /* *beta is log_beta: use exp(clamp(., ln .05, ln 64)) */
+#define DA_ROUTE_UNIT_KEYS 8        /* key atoms have L2 norm <= 1 (a normalized bank): with
+                                       DA_ROUTE_NORMALIZE_INPUT every logit is bounded by |beta|,
+                                       which lets the kernel skip online-softmax rescaling */
 
 /* da_routed_attention flags */
 #define DA_ATTN_CAUSAL 1

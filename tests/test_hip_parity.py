@@ -146,19 +146,29 @@ def test_route_flags_odd_rows(dtype, normalize_input, normalize_output) -> None:
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("normalized_bank", [False, True])
 @pytest.mark.parametrize(("routing_dim", "atoms", "rows", "beta"), [
     (128, 512, 1000, 4.0),
     (256, 512, 8192, 4.0),          # C1 route: 8192 rows
     (512, 1536, 16384, 4.0 * 2 ** 0.5),  # C3 route, past the reference's 4096-row cutoff
     (256, 100, 77, 4.0),            # atom count that is not a tile multiple
     (512, 2855, 333, 5.0),
+    (128, 300, 500, 12.0),          # beta past the fixed-reference range: online rescaling
 ])
-def test_route_shapes(dtype, routing_dim, atoms, rows, beta) -> None:
+def test_route_shapes(dtype, normalized_bank, routing_dim, atoms, rows, beta) -> None:
+    # normalized_bank: the bank comes from dictionary_normalize_hip, whose unit
+    # atoms let the kernel use its fixed-reference softmax; plain tensors do not.
     device = _device()
     g = torch.Generator().manual_seed(routing_dim * 7 + atoms)
     x = torch.randn(rows, routing_dim, generator=g).to(device, dtype)
-    dk = unit_columns(routing_dim, atoms, dtype, device, 3)
-    dv = unit_columns(routing_dim, atoms, dtype, device, 4)
+    if normalized_bank:
+        raw_k = torch.randn(routing_dim, atoms, generator=g).to(device, torch.float32)
+        raw_v = torch.randn(routing_dim, atoms, generator=g).to(device, torch.float32)
+        dk, dv = da.dictionary_normalize_hip(raw_k, raw_v, 1e-6, da.hip_ops.route_key_dtype(True, dtype))
+        assert dk._da_route_layout.unit
+    else:
+        dk = unit_columns(routing_dim, atoms, dtype, device, 3)
+        dv = unit_columns(routing_dim, atoms, dtype, device, 4)
     out = da.dictionary_route_hip(x, dk, dv, beta)
     expected = oracle.dictionary_route(np32(x), np32(dk), np32(dv), beta)
     assert_parity(out, expected, label=f"route R{routing_dim} M{atoms} rows{rows} {dtype}")
