@@ -168,7 +168,7 @@ def main() -> None:
             "dict_normalize": lambda: lib.da_dictionary_normalize(
                 raw_key.data_ptr(), None if raw_value is None else raw_value.data_ptr(),
                 da.hip_ops.dtype_code(raw_key.dtype), R, M, config.eps,
-                layout.key_t.data_ptr(), key_code, layout.value.data_ptr(), handle),
+                layout.key_t.data_ptr(), key_code, layout.value.data_ptr(), None, handle),
             "qkv_projection": lambda: lib.da_qkv_projection(
                 x.data_ptr(), tokens, d, length, p["query.weight"].data_ptr(), p["key.weight"].data_ptr(), W,
                 p["value.weight"].data_ptr(), p["value.bias"].data_ptr(), d, pdt, code,

@@ -102,7 +102,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 5; }
+int da_abi_version(void) { return 6; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -112,16 +112,17 @@ int64_t da_padded_length(int64_t length) { return da::round_up(length, da::kKeyP
 
 int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_dtype,
                             int64_t routing_dim, int64_t atoms, float eps, void* key_t,
-                            int key_dtype, void* value, da_stream_t stream) {
+                            int key_dtype, void* value, void* value_rows, da_stream_t stream) {
   if (!any_dtype(raw_dtype) || !half_dtype(key_dtype))
     return fail(DA_ERR_INVALID_ARGUMENT, "normalize: bad dtype");
   if (!pow2_width(routing_dim))
     return fail(DA_ERR_UNSUPPORTED, "normalize: routing_dim %lld not in {64,128,256,512}", (long long)routing_dim);
   if (atoms < 1 || atoms > (1 << 24)) return fail(DA_ERR_INVALID_ARGUMENT, "normalize: bad atom count");
   if (!raw_key || !key_t || !value) return fail(DA_ERR_INVALID_ARGUMENT, "normalize: null pointer");
-  if (!aligned(key_t, 16) || !aligned(value, 16)) return fail(DA_ERR_ALIGNMENT, "normalize: outputs must be 16-byte aligned");
+  if (!aligned(key_t, 16) || !aligned(value, 16) || !aligned(value_rows, 16))
+    return fail(DA_ERR_ALIGNMENT, "normalize: outputs must be 16-byte aligned");
   da::launch_dictionary_normalize(raw_key, raw_value, raw_dtype, static_cast<int>(routing_dim),
-                                  static_cast<int>(atoms), eps, key_t, key_dtype, value,
+                                  static_cast<int>(atoms), eps, key_t, key_dtype, value, value_rows,
                                   reinterpret_cast<hipStream_t>(stream));
   return check_launch("normalize");
 }

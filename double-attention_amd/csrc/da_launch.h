@@ -97,7 +97,7 @@ struct GemmSegment {
 
 void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int in_dtype, int R,
                                  int M, float eps, void* key_t, int key_dtype, void* value,
-                                 hipStream_t stream);
+                                 void* value_rows, hipStream_t stream);
 void launch_dictionary_route(const RouteArgs& a, hipStream_t stream);
 // Launch shape of the attention for a problem: value slice width, key-range
 // chunking (0 = none) and the bytes of split-key partials it needs.

@@ -34,6 +34,14 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_slot_base) {
 // s_waitcnt vmcnt(0) only (gfx9 encoding: expcnt and lgkmcnt left at max).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// s_waitcnt vmcnt(N): vmcnt is split over bits [3:0] and [15:14]; expcnt
+// [6:4] and lgkmcnt [11:8] are left at their maxima (no wait).
+template <int N>
+__device__ __forceinline__ void wait_vmem_at_most() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
+
 __device__ __forceinline__ int uniform_wave() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }

@@ -11,6 +11,8 @@
 //   key_t  [Mp, R]  atom-major, element type TK
 //   value  32-atom tiles, fp16 (normalized atoms are bounded by 1): coordinate
 //          r of atom j at value[(j/32)*32*R + 32*r + j%32]
+//   value_rows (optional) [R, Mp] fp16, coordinate-major: the [R, M] bank of
+//          the module API, written by the same pass so no copy kernel is needed
 // A workgroup owns 32 atoms: it reads each column once into registers (fp32),
 // reduces the sums of squares through LDS, writes the value layout directly
 // and the atom-major key layout through an LDS transpose, so every global
@@ -26,7 +28,7 @@ constexpr int kNormGroups = 8;    // row groups per workgroup (256 threads)
 template <typename Tin, typename TK, int R>
 __global__ __launch_bounds__(256) void dict_normalize_kernel(
     const Tin* __restrict__ raw_key, const Tin* __restrict__ raw_value, int M, int Mp, float eps,
-    TK* __restrict__ key_t, _Float16* __restrict__ value) {
+    TK* __restrict__ key_t, _Float16* __restrict__ value, _Float16* __restrict__ value_rows) {
   constexpr int PER = R / kNormGroups;
   const int which = blockIdx.y;  // 0: key bank, 1: value bank (untied only)
   const Tin* src = which == 0 ? raw_key : raw_value;
@@ -68,7 +70,9 @@ __global__ __launch_bounds__(256) void dict_normalize_kernel(
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int r = rg + i * kNormGroups;
-      vtile[r * kNormCols + jj] = static_cast<_Float16>(v[i] * scale);
+      const _Float16 h = static_cast<_Float16>(v[i] * scale);
+      vtile[r * kNormCols + jj] = h;
+      if (value_rows) value_rows[static_cast<int64_t>(r) * Mp + j] = h;
     }
   }
   if (write_key) {
@@ -86,40 +90,40 @@ __global__ __launch_bounds__(256) void dict_normalize_kernel(
 
 template <typename Tin, typename TK, int R>
 static void launch_norm(const void* rk, const void* rv, int M, int Mp, float eps, void* kt, void* v,
-                        hipStream_t s) {
+                        void* vr, hipStream_t s) {
   dim3 grid(Mp / kNormCols, rv ? 2 : 1);
   hipLaunchKernelGGL((dict_normalize_kernel<Tin, TK, R>), grid, dim3(256), 0, s,
                      static_cast<const Tin*>(rk), static_cast<const Tin*>(rv), M, Mp, eps,
-                     static_cast<TK*>(kt), static_cast<_Float16*>(v));
+                     static_cast<TK*>(kt), static_cast<_Float16*>(v), static_cast<_Float16*>(vr));
 }
 
 template <typename Tin, typename TK>
 static void dispatch_r(int R, const void* rk, const void* rv, int M, int Mp, float eps, void* kt,
-                       void* v, hipStream_t s) {
+                       void* v, void* vr, hipStream_t s) {
   switch (R) {
-    case 64: launch_norm<Tin, TK, 64>(rk, rv, M, Mp, eps, kt, v, s); break;
-    case 128: launch_norm<Tin, TK, 128>(rk, rv, M, Mp, eps, kt, v, s); break;
-    case 256: launch_norm<Tin, TK, 256>(rk, rv, M, Mp, eps, kt, v, s); break;
-    default: launch_norm<Tin, TK, 512>(rk, rv, M, Mp, eps, kt, v, s); break;
+    case 64: launch_norm<Tin, TK, 64>(rk, rv, M, Mp, eps, kt, v, vr, s); break;
+    case 128: launch_norm<Tin, TK, 128>(rk, rv, M, Mp, eps, kt, v, vr, s); break;
+    case 256: launch_norm<Tin, TK, 256>(rk, rv, M, Mp, eps, kt, v, vr, s); break;
+    default: launch_norm<Tin, TK, 512>(rk, rv, M, Mp, eps, kt, v, vr, s); break;
   }
 }
 
 template <typename TK>
 static void dispatch_in(int in_dtype, int R, const void* rk, const void* rv, int M, int Mp, float eps,
-                        void* kt, void* v, hipStream_t s) {
-  if (in_dtype == kF32) dispatch_r<float, TK>(R, rk, rv, M, Mp, eps, kt, v, s);
-  else if (in_dtype == kF16) dispatch_r<_Float16, TK>(R, rk, rv, M, Mp, eps, kt, v, s);
-  else dispatch_r<__bf16, TK>(R, rk, rv, M, Mp, eps, kt, v, s);
+                        void* kt, void* v, void* vr, hipStream_t s) {
+  if (in_dtype == kF32) dispatch_r<float, TK>(R, rk, rv, M, Mp, eps, kt, v, vr, s);
+  else if (in_dtype == kF16) dispatch_r<_Float16, TK>(R, rk, rv, M, Mp, eps, kt, v, vr, s);
+  else dispatch_r<__bf16, TK>(R, rk, rv, M, Mp, eps, kt, v, vr, s);
 }
 
 void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int in_dtype, int R,
                                  int M, float eps, void* key_t, int key_dtype, void* value,
-                                 hipStream_t stream) {
+                                 void* value_rows, hipStream_t stream) {
   const int Mp = static_cast<int>(round_up(M, kAtomPad));
   if (key_dtype == kF16)
-    dispatch_in<_Float16>(in_dtype, R, raw_key, raw_value, M, Mp, eps, key_t, value, stream);
+    dispatch_in<_Float16>(in_dtype, R, raw_key, raw_value, M, Mp, eps, key_t, value, value_rows, stream);
   else
-    dispatch_in<__bf16>(in_dtype, R, raw_key, raw_value, M, Mp, eps, key_t, value, stream);
+    dispatch_in<__bf16>(in_dtype, R, raw_key, raw_value, M, Mp, eps, key_t, value, value_rows, stream);
 }
 
 }  // namespace da

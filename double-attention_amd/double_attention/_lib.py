@@ -39,7 +39,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -85,7 +85,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_last_error": (ctypes.c_char_p, []),
     "da_padded_atoms": (_i64, [_i64]),
     "da_padded_length": (_i64, [_i64]),
-    "da_dictionary_normalize": (_i32, [_vp, _vp, _i32, _i64, _i64, _f32, _vp, _i32, _vp, _vp]),
+    "da_dictionary_normalize": (_i32, [_vp, _vp, _i32, _i64, _i64, _f32, _vp, _i32, _vp, _vp, _vp]),
     "da_dictionary_route": (
         _i32,
         [

@@ -116,10 +116,10 @@ def dictionary_normalize_hip(
     """Column-normalize a bank in one launch; returns ``(key, value)`` as ``[R, M]``.
 
     Matches ``F.normalize(raw, dim=0, eps=eps)``.  ``key`` (in ``key_dtype``)
-    is a view of the route's atom-major key layout and ``value`` (fp16) a copy
-    of its tiled value layout; both carry the layouts, so handing them back to
-    the route re-lays nothing out.  For a tied bank both hold the same
-    normalized atoms.
+    is a view of the route's atom-major key layout and ``value`` (fp16) a view
+    of a coordinate-major copy the same kernel writes beside the route's tiled
+    value layout; both carry the layouts, so handing them back to the route
+    re-lays nothing out.  For a tied bank both hold the same normalized atoms.
     """
 
     if raw_key.ndim != 2:
@@ -133,6 +133,7 @@ def dictionary_normalize_hip(
     padded = _round_up(atoms, ATOM_PAD)
     key_t = torch.empty(padded, routing_dim, dtype=key_dtype, device=raw_key.device)
     value = torch.empty(padded // 32, routing_dim, 32, dtype=torch.float16, device=raw_key.device)
+    value_rows = torch.empty(routing_dim, padded, dtype=torch.float16, device=raw_key.device)
     raw_key_c = raw_key.detach().contiguous()
     raw_value_c = None if raw_value is None else raw_value.detach().to(raw_key.dtype).contiguous()
     lib = _lib.get()
@@ -147,12 +148,13 @@ def dictionary_normalize_hip(
             key_t.data_ptr(),
             _half_code(key_dtype),
             value.data_ptr(),
+            value_rows.data_ptr(),
             _stream(raw_key.device),
         ),
         "dictionary_normalize_hip",
     )
     layout = RouteDictionary(key_t, value, atoms, True)
-    return _tag(key_t[:atoms].t(), _untile_value(value)[:, :atoms], layout)
+    return _tag(key_t[:atoms].t(), value_rows[:, :atoms], layout)
 
 
 def _untile_value(value: Tensor) -> Tensor:

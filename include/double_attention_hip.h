@@ -88,12 +88,14 @@ int64_t da_padded_length(int64_t length);
  *   value:  out, fp16, 32-atom tiles: coordinate r of atom j at
  *           value[(j/32)*32*routing_dim + 32*r + j%32]
  *           (da_padded_atoms(atoms) * routing_dim elements)
+ *   value_rows: NULL, or out [routing_dim, da_padded_atoms(atoms)] fp16, the
+ *           same value atoms coordinate-major (written by the same pass)
  * Atom j becomes raw[:, j] / max(||raw[:, j]||, eps); padding atoms are zero.
  * routing_dim must be 64, 128, 256 or 512; key_dtype DA_F16 or DA_BF16.
  */
 int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_dtype,
                             int64_t routing_dim, int64_t atoms, float eps, void* key_t,
-                            int key_dtype, void* value, da_stream_t stream);
+                            int key_dtype, void* value, void* value_rows, da_stream_t stream);
 
 /*
  * Fused dictionary route (ops.py:16-62 with identity activation and softmax
