@@ -102,20 +102,37 @@ __device__ __forceinline__ int key_tiles_of(const AttnParams& p, int qt, int QT)
 __device__ __forceinline__ int chunks_of(const AttnParams& p, int qt, int QT) {
   return p.chunk_tiles > 0 ? (key_tiles_of(p, qt, QT) + p.chunk_tiles - 1) / p.chunk_tiles : 1;
 }
-// Work item y of a (sequence, slice): items run heaviest query tile first,
-// then by chunk.  Returns the query tile; `chunk`, `n_chunks` and `first` (the
-// item index of the tile's chunk 0) describe its place.
+// Items (query tile x key chunk) of query tiles qt .. n_qt-1, which come
+// first in the heaviest-first order.  With chunking the tiles are QT = 64
+// queries = 2 key tiles, so a full causal tile t has 2(t+1) key tiles and
+// ceil((t+1)/h) chunks (h = chunk_tiles/2), whose prefix sums have a closed
+// form: sum_{q=1..n} ceil(q/h) = h a(a+1)/2 + r(a+1), n = a h + r.
+__device__ __forceinline__ int ceil_sum(int n, int h) {
+  const int a = n / h;
+  const int r = n - a * h;
+  return h * a * (a + 1) / 2 + r * (a + 1);
+}
+__device__ __forceinline__ int items_from(const AttnParams& p, int qt, int QT) {
+  if (qt >= p.n_qt) return 0;
+  if (p.chunk_tiles == 0) return p.n_qt - qt;
+  if (!(p.flags & kAttnCausal)) return (p.n_qt - qt) * chunks_of(p, 0, QT);
+  const int last = p.n_qt - 1;   // the last tile may be partial
+  return ceil_sum(last, p.chunk_tiles / 2) - ceil_sum(qt, p.chunk_tiles / 2) + chunks_of(p, last, QT);
+}
+// Work item y of a (sequence, slice): returns its query tile; `chunk`,
+// `n_chunks` and `first` (the item index of the tile's chunk 0) describe its
+// place.  Binary search on the decreasing items_from.
 __device__ __forceinline__ int decode_item(const AttnParams& p, int y, int QT, int& chunk, int& n_chunks, int& first) {
-  int qt = p.n_qt - 1;
-  first = 0;
-  n_chunks = chunks_of(p, qt, QT);
-  while (qt > 0 && y >= first + n_chunks) {
-    first += n_chunks;
-    --qt;
-    n_chunks = chunks_of(p, qt, QT);
+  int lo = 0, hi = p.n_qt - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (items_from(p, mid, QT) > y) lo = mid;
+    else hi = mid - 1;
   }
+  first = items_from(p, lo + 1, QT);
+  n_chunks = chunks_of(p, lo, QT);
   chunk = y - first;
-  return qt;
+  return lo;
 }
 
 template <int RP, int DS, int NW>
@@ -467,41 +484,53 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 
 // Merge of split key ranges: out = sum_c 2^(m_c - M) l_c o_c / sum_c 2^(m_c - M) l_c,
 // o_c = O_c / l_c the chunk's normalized output, M = max_c m_c, per query row
-// (one map, weight 1).
+// (one map, weight 1).  Each wave takes one query row, its lanes covering
+// consecutive features, so every partial row is read by one coalesced sweep.
 template <typename TV, int DS>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   constexpr int QT = 2 * kAttnQW;
   const int qt = p.n_qt - 1 - static_cast<int>(blockIdx.y);
   const int n_ch = chunks_of(p, qt, QT);
   if (n_ch <= 1) return;   // written directly by its only item
-  int first = 0;
-  for (int t = p.n_qt - 1; t > qt; --t) first += chunks_of(p, t, QT);
+  const int first = items_from(p, qt + 1, QT);
   const int b = static_cast<int>(blockIdx.x) / p.n_slices;
   const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;
   constexpr int ITEM = QT * (DS + 2);
   const float* part = p.part + (static_cast<int64_t>(blockIdx.x) * p.n_items + first) * ITEM;
-  for (int e = threadIdx.x; e < QT * DS / 4; e += 256) {
-    const int ql = e / (DS / 4);
-    const int d4 = (e - ql * (DS / 4)) * 4;
+  const int lane = lane_id();
+  // blockIdx.z picks four query rows of the tile, one per wave.
+  {
+    const int ql = static_cast<int>(blockIdx.z) * 4 + (static_cast<int>(threadIdx.x) >> 6);
     const int tq = qt * QT + ql;
-    if (tq >= p.T) continue;
+    if (tq >= p.T) return;
     float M = -INFINITY;
     for (int c = 0; c < n_ch; ++c) M = fmaxf(M, part[c * ITEM + QT * DS + ql]);
+    f32x4 o[DS / 256 > 0 ? DS / 256 : 1];
+#pragma unroll
+    for (int k = 0; k < (DS / 256 > 0 ? DS / 256 : 1); ++k) o[k] = zero4();
     float den = 0.f;
-    f32x4 o = zero4();
     for (int c = 0; c < n_ch; ++c) {
       const float m = part[c * ITEM + QT * DS + ql];
-      const float w = m == -INFINITY ? 0.f : exp2f(m - M);
-      const float wl = w * part[c * ITEM + QT * DS + QT + ql];   // stored outputs are O_c / l_c
+      const float wl = (m == -INFINITY ? 0.f : exp2f(m - M)) * part[c * ITEM + QT * DS + QT + ql];
       den += wl;
-      o += wl * *reinterpret_cast<const f32x4*>(part + c * ITEM + ql * DS + d4);
+#pragma unroll
+      for (int k = 0; k < (DS / 256 > 0 ? DS / 256 : 1); ++k) {
+        const int d4 = (k * 64 + lane) * 4;
+        if (d4 < DS) o[k] += wl * *reinterpret_cast<const f32x4*>(part + c * ITEM + ql * DS + d4);
+      }
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
-    typename Elem<TV>::v4 v;
+    TV* orow = static_cast<TV*>(p.out) + b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t + ds0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(o[i] * inv);
-    *reinterpret_cast<typename Elem<TV>::v4*>(static_cast<TV*>(p.out) + b * p.out_stride_b +
-                                              static_cast<int64_t>(tq) * p.out_stride_t + ds0 + d4) = v;
+    for (int k = 0; k < (DS / 256 > 0 ? DS / 256 : 1); ++k) {
+      const int d4 = (k * 64 + lane) * 4;
+      if (d4 < DS) {
+        typename Elem<TV>::v4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(o[k][i] * inv);
+        *reinterpret_cast<typename Elem<TV>::v4*>(orow + d4) = v;
+      }
+    }
   }
 }
 
@@ -515,7 +544,8 @@ static void launch_attn_3(const AttentionArgs& a, const AttnPlan& plan, AttnPara
                      0, s, p);
   if constexpr (!MULTI) {
     if (plan.chunk_tiles > 0)
-      hipLaunchKernelGGL((attention_merge_kernel<TV, DS>), dim3(a.B * p.n_slices, plan.n_qt), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((attention_merge_kernel<TV, DS>), dim3(a.B * p.n_slices, plan.n_qt, 2 * kAttnQW / 4),
+                         dim3(256), 0, s, p);
   }
 }
 
