@@ -24,12 +24,20 @@
 
 namespace da {
 
-constexpr int kBI = 128;
 constexpr int kBJ = 128;
 constexpr int kBK = 64;
-typedef PaddedTile<128, kBK / 8, false> GemmTile;       // one operand tile: 128 rows x 64 k
-constexpr int kGemmPerWave = 2 * GemmTile::LOADS / 4;    // wave loads per wave per stage
-static_assert((2 * GemmTile::LOADS) % 4 == 0, "stage must split evenly over four waves");
+typedef PaddedTile<kBJ, kBK / 8, false> GemmTileQ;      // Q operand tile: 128 rows x 64 k
+
+// Row tile of BI (128 or 64) P rows; the four waves form a 2 x 2 grid of
+// (BI/2) x 64 output blocks.
+template <int BI>
+struct GemmCfg {
+  typedef PaddedTile<BI, kBK / 8, false> TileP;
+  static constexpr int LOADS = TileP::LOADS + GemmTileQ::LOADS;
+  static constexpr int PER_WAVE = (LOADS + 3) / 4;      // wave loads per wave per stage
+  static constexpr int NA = BI / 32;                    // 16-row MFMA blocks per wave
+  static constexpr int STAGE = TileP::BYTES + GemmTileQ::BYTES;
+};
 
 struct GemmSeg {
   const void* p0;
@@ -63,10 +71,13 @@ __device__ __forceinline__ const T* p_row(const GemmSeg& sg, int64_t i) {
   return i < sg.p_split ? p0 + i * sg.K : static_cast<const T*>(sg.p1) + (i - sg.p_split) * sg.K;
 }
 
-template <typename T>
+template <typename T, int BI>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   typedef typename Elem<T>::v8 v8;
-  constexpr int STAGE = 2 * GemmTile::BYTES;   // P tile, then Q tile
+  typedef GemmCfg<BI> Cfg;
+  typedef typename Cfg::TileP TileP;
+  constexpr int STAGE = Cfg::STAGE;            // P tile, then Q tile
+  constexpr int NA = Cfg::NA;
   __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
   __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
 
@@ -74,7 +85,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   const int si = (prm.nseg > 1 && tile >= prm.seg[0].tiles) ? 1 : 0;
   if (si) tile -= prm.seg[0].tiles;
   const GemmSeg& sg = prm.seg[si];
-  const int64_t i0 = static_cast<int64_t>(tile % sg.tiles_i) * kBI;
+  const int64_t i0 = static_cast<int64_t>(tile % sg.tiles_i) * BI;
   const int64_t j0 = static_cast<int64_t>(tile / sg.tiles_i) * kBJ;
 
   const int lane = lane_id();
@@ -86,39 +97,46 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   const int K = static_cast<int>(sg.K);
   const int n_stages = (K + kBK - 1) / kBK;
 
-  // This wave's DMA sources for stage k0 = 0: wave load j < LOADS fills the
-  // P tile, the rest the Q tile; only the k offset moves between stages.
-  const T* src[kGemmPerWave];
-  int kchunk[kGemmPerWave];
+  // This wave's DMA sources for stage k0 = 0: wave load j < TileP::LOADS
+  // fills the P tile, the rest the Q tile; only the k offset moves between
+  // stages.  A partial last round (j >= LOADS) re-loads wave load 0's data
+  // into slot 0.
+  const T* src[Cfg::PER_WAVE];
+  int kchunk[Cfg::PER_WAVE];
+  int slot[Cfg::PER_WAVE];
 #pragma unroll
-  for (int n = 0; n < kGemmPerWave; ++n) {
-    const int j = n * 4 + wave;
-    const int jj = j < GemmTile::LOADS ? j : j - GemmTile::LOADS;
+  for (int n = 0; n < Cfg::PER_WAVE; ++n) {
+    const int j0w = n * 4 + wave;
+    const int j = j0w < Cfg::LOADS ? j0w : 0;
+    slot[n] = j * 1024;
     int r, ck;
-    GemmTile::slot_chunk(jj * 64 + lane, r, ck);
+    if (j < TileP::LOADS) {
+      TileP::slot_chunk(j * 64 + lane, r, ck);
+      src[n] = p_row<T>(sg, i0 + r);
+    } else {
+      GemmTileQ::slot_chunk((j - TileP::LOADS) * 64 + lane, r, ck);
+      src[n] = static_cast<const T*>(sg.q) + min(j0 + r, sg.J - 1) * sg.K;
+    }
     kchunk[n] = ck * 8;
-    src[n] = j < GemmTile::LOADS ? p_row<T>(sg, i0 + r)
-                                 : static_cast<const T*>(sg.q) + min(j0 + r, sg.J - 1) * sg.K;
   }
   auto issue = [&](char* buf, int k0) {
     // Columns past K only occur in a final half stage that is never read.
     const bool tail = k0 + kBK > K;
 #pragma unroll
-    for (int n = 0; n < kGemmPerWave; ++n) {
-      const int j = n * 4 + wave;
+    for (int n = 0; n < Cfg::PER_WAVE; ++n) {
       const int kc = tail ? min(k0 + kchunk[n], K - 8) : k0 + kchunk[n];
-      dma16(src[n] + kc, buf + j * 1024);
+      dma16(src[n] + kc, buf + slot[n]);
     }
   };
 
-  f32x4 acc[4][4];
+  f32x4 acc[NA][4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < NA; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = zero4();
 
-  const int afrag = GemmTile::offset(wi * 64 + c, g);
-  const int bfrag = GemmTile::BYTES + GemmTile::offset(wj * 64 + c, g);
+  const int afrag = TileP::offset(wi * (BI / 2) + c, g);
+  const int bfrag = TileP::BYTES + GemmTileQ::offset(wj * 64 + c, g);
 
   auto step = [&](int st, char* cur, char* nxt) {
     wait_vmem();
@@ -126,13 +144,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     if (st + 1 < n_stages) issue(nxt, (st + 1) * kBK);
     const int ksteps = min(kBK, K - st * kBK) / 32;
     for (int kk = 0; kk < ksteps; ++kk) {
-      v8 af[4], bf[4];
+      v8 af[NA], bf[4];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) af[a] = lds_v8<T>(cur + afrag + GemmTile::offset(a * 16, kk * 4));
+      for (int a = 0; a < NA; ++a) af[a] = lds_v8<T>(cur + afrag + TileP::offset(a * 16, kk * 4));
 #pragma unroll
-      for (int b = 0; b < 4; ++b) bf[b] = lds_v8<T>(cur + bfrag + GemmTile::offset(b * 16, kk * 4));
+      for (int b = 0; b < 4; ++b) bf[b] = lds_v8<T>(cur + bfrag + GemmTileQ::offset(b * 16, kk * 4));
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+      for (int a = 0; a < NA; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = Elem<T>::mma(af[a], bf[b], acc[a][b]);
     }
@@ -146,7 +164,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   }
   if (st < n_stages) step(st, lds0, lds1);
 
-  // Epilogue: lane holds D[i0 + wi*64 + a*16 + 4g + r][j0 + wj*64 + b*16 + c], r = 0..3.
+  // Epilogue: lane holds D[i0 + wi*BI/2 + a*16 + 4g + r][j0 + wj*64 + b*16 + c], r = 0..3.
   T* out = static_cast<T*>(sg.out);
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
@@ -154,8 +172,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     if (j >= sg.J) continue;
     const float bj = (sg.mode == 1 && sg.bias) ? load_scalar(sg.bias, sg.bias_dtype, j) : 0.f;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int64_t i = i0 + wi * 64 + a * 16 + 4 * g;
+    for (int a = 0; a < NA; ++a) {
+      const int64_t i = i0 + wi * (BI / 2) + a * 16 + 4 * g;
       if (i >= sg.I) continue;
       typename Elem<T>::v4 o;
 #pragma unroll
@@ -183,8 +201,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   }
 }
 
-void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream) {
-  GemmParams prm;
+template <int BI>
+static int setup_gemm(const GemmSegment* segs, int nseg, GemmParams& prm) {
   prm.nseg = nseg;
   int total = 0;
   for (int s = 0; s < nseg; ++s) {
@@ -206,14 +224,28 @@ void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t strea
     d.out = a.out;
     d.ldo = a.ldo;
     d.vt_stride_b = a.vt_stride_b;
-    d.tiles_i = static_cast<int>((d.I + kBI - 1) / kBI);
+    d.tiles_i = static_cast<int>((d.I + BI - 1) / BI);
     d.tiles = d.tiles_i * static_cast<int>((a.J + kBJ - 1) / kBJ);
     total += d.tiles;
   }
   if (nseg == 1) prm.seg[1] = prm.seg[0];
+  return total;
+}
+
+// 128-row tiles when the grid holds two workgroups per CU, else 64-row tiles
+// (twice the workgroups, so two share every CU and hide each other's waits).
+void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream) {
+  GemmParams prm;
+  int total = setup_gemm<128>(segs, nseg, prm);
   if (total == 0) return;
-  if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16>), dim3(total), dim3(256), 0, stream, prm);
-  else hipLaunchKernelGGL((gemm_kernel<__bf16>), dim3(total), dim3(256), 0, stream, prm);
+  if (total >= 512) {
+    if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 128>), dim3(total), dim3(256), 0, stream, prm);
+    else hipLaunchKernelGGL((gemm_kernel<__bf16, 128>), dim3(total), dim3(256), 0, stream, prm);
+    return;
+  }
+  total = setup_gemm<64>(segs, nseg, prm);
+  if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 64>), dim3(total), dim3(256), 0, stream, prm);
+  else hipLaunchKernelGGL((gemm_kernel<__bf16, 64>), dim3(total), dim3(256), 0, stream, prm);
 }
 
 }  // namespace da
