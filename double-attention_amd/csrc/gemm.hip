@@ -59,15 +59,31 @@ struct GemmParams {
   int nseg;
 };
 
-template <typename T>
-__device__ __forceinline__ const T* p_row(const GemmSeg& sg, int64_t i) {
-  const T* p0 = static_cast<const T*>(sg.p0);
-  i = min(i, sg.I - 1);   // rows of a partial last tile are computed but never stored
-  if (sg.mode == 1) {     // virtual token i = b * Tp + t of the value segment
-    const int64_t b = i / sg.Tp;
-    const int64_t t = min(i % sg.Tp, sg.T - 1);
-    return p0 + (b * sg.T + t) * sg.K;
+// Virtual token i0 + off of the value segment as (sequence, token): the tile's
+// first row is split once per workgroup (b0, t0 = i0 = b0*Tp + t0), and a row
+// offset below 2*Tp (tiles are <= 128 rows, Tp >= 64) wraps at most twice.
+struct VToken {
+  int64_t b;
+  int64_t t;
+};
+__device__ __forceinline__ VToken vtoken(int64_t b0, int64_t t0, int64_t off, int64_t Tp) {
+  VToken v{b0, t0 + off};
+  while (v.t >= Tp) {
+    v.t -= Tp;
+    ++v.b;
   }
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ const T* p_row(const GemmSeg& sg, int64_t i0, int64_t b0, int64_t t0, int off) {
+  const T* p0 = static_cast<const T*>(sg.p0);
+  if (sg.mode == 1) {     // virtual token i = b * Tp + t of the value segment
+    VToken v = vtoken(b0, t0, off, sg.Tp);
+    if (i0 + off >= sg.I) v = VToken{sg.I / sg.Tp - 1, sg.Tp - 1};   // rows of a partial last tile
+    return p0 + (v.b * sg.T + min(v.t, sg.T - 1)) * sg.K;
+  }
+  const int64_t i = min(i0 + off, sg.I - 1);   // rows of a partial last tile are computed but never stored
   return i < sg.p_split ? p0 + i * sg.K : static_cast<const T*>(sg.p1) + (i - sg.p_split) * sg.K;
 }
 
@@ -87,6 +103,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   const GemmSeg& sg = prm.seg[si];
   const int64_t i0 = static_cast<int64_t>(tile % sg.tiles_i) * BI;
   const int64_t j0 = static_cast<int64_t>(tile / sg.tiles_i) * kBJ;
+  // Value segment: the tile's first virtual token, split once (uniform).
+  const int64_t b0 = sg.mode == 1 ? i0 / sg.Tp : 0;
+  const int64_t t0 = sg.mode == 1 ? i0 - b0 * sg.Tp : 0;
 
   const int lane = lane_id();
   const int c = lane & 15;
@@ -112,7 +131,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     int r, ck;
     if (j < TileP::LOADS) {
       TileP::slot_chunk(j * 64 + lane, r, ck);
-      src[n] = p_row<T>(sg, i0 + r);
+      src[n] = p_row<T>(sg, i0, b0, t0, r);
     } else {
       GemmTileQ::slot_chunk((j - TileP::LOADS) * 64 + lane, r, ck);
       src[n] = static_cast<const T*>(sg.q) + min(j0 + r, sg.J - 1) * sg.K;
@@ -192,10 +211,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
       } else {
         // Four consecutive virtual tokens of one sequence and one 32-token
         // tile (Tp % 64 == 0, i % 4 == 0).
-        const int64_t bb = i / sg.Tp;
-        const int64_t t = i % sg.Tp;
-        *reinterpret_cast<typename Elem<T>::v4*>(out + bb * sg.vt_stride_b + (t >> 5) * 32 * sg.J + 32 * j +
-                                                 (t & 31)) = o;
+        const VToken v = vtoken(b0, t0, i - i0, sg.Tp);
+        *reinterpret_cast<typename Elem<T>::v4*>(out + v.b * sg.vt_stride_b + (v.t >> 5) * 32 * sg.J + 32 * j +
+                                                 (v.t & 31)) = o;
       }
     }
   }
