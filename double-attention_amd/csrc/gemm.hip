@@ -183,38 +183,61 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   }
   if (st < n_stages) step(st, lds0, lds1);
 
-  // Epilogue: lane holds D[i0 + wi*BI/2 + a*16 + 4g + r][j0 + wj*64 + b*16 + c], r = 0..3.
-  T* out = static_cast<T*>(sg.out);
+  // Epilogue.  Lane (c, g) holds D[i0 + wi*BI/2 + a*16 + 4g + r][j0 + wj*64 + b*16 + c],
+  // r = 0..3: four consecutive i of one j.  Both output layouts run along i
+  // for a fixed j (mode 0: out[j*ldo + i]; mode 1: 32-token runs of V^T), so
+  // each wave stages its block in LDS as [j][i] rows and writes them back as
+  // 16-byte chunks, eight lanes per 128-byte row segment.
+  constexpr int WI = BI / 2;                 // i extent of a wave's block
+  constexpr int ROWB = WI * 2 + 16;          // bytes per staged j row (padded)
+  static_assert(64 * ROWB <= STAGE, "a wave's staging block must fit one stage buffer");
+  __syncthreads();                           // every wave is done reading the stage buffers
+  char* stage_w = (wave < 2 ? lds0 : lds1) + (wave & 1) * (STAGE / 2);
+  static_assert(2 * 64 * ROWB <= STAGE, "two waves share one stage buffer");
+  float bias_i[NA][4];
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t i = i0 + wi * WI + a * 16 + 4 * g + r;
+      bias_i[a][r] = (sg.mode == 0 && sg.bias && i < sg.I) ? load_scalar(sg.bias, sg.bias_dtype, i) : 0.f;
+    }
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const int64_t j = j0 + wj * 64 + b * 16 + c;
-    if (j >= sg.J) continue;
-    const float bj = (sg.mode == 1 && sg.bias) ? load_scalar(sg.bias, sg.bias_dtype, j) : 0.f;
+    const float bj = (sg.mode == 1 && sg.bias && j < sg.J) ? load_scalar(sg.bias, sg.bias_dtype, j) : 0.f;
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
-      const int64_t i = i0 + wi * (BI / 2) + a * 16 + 4 * g;
-      if (i >= sg.I) continue;
       typename Elem<T>::v4 o;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float bi = 0.f;
-        if (sg.mode == 0 && sg.bias && i + r < sg.I) bi = load_scalar(sg.bias, sg.bias_dtype, i + r);
-        o[r] = static_cast<T>(acc[a][b][r] + bi + bj);
+      for (int r = 0; r < 4; ++r) o[r] = static_cast<T>(acc[a][b][r] + bias_i[a][r] + bj);
+      *reinterpret_cast<typename Elem<T>::v4*>(stage_w + (b * 16 + c) * ROWB + (a * 16 + 4 * g) * 2) = o;
+    }
+  }
+  // Same-wave LDS round trip: the stores above complete before the loads below.
+  T* out = static_cast<T*>(sg.out);
+  constexpr int CHUNKS = WI / 8;             // 16-byte chunks per staged row
+  constexpr int ROWS_PER_PASS = 64 / CHUNKS;
+#pragma unroll
+  for (int pass = 0; pass < 64 / ROWS_PER_PASS; ++pass) {
+    const int jr = pass * ROWS_PER_PASS + lane / CHUNKS;   // staged row (j)
+    const int ic = (lane % CHUNKS) * 8;                     // first i of the chunk
+    const int64_t j = j0 + wj * 64 + jr;
+    const int64_t i = i0 + wi * WI + ic;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage_w + jr * ROWB + ic * 2);
+    if (j >= sg.J || i >= sg.I) continue;
+    if (sg.mode == 0) {
+      T* dst = out + j * sg.ldo + i;
+      if (i + 8 <= sg.I) {
+        store16B(dst, v);
+      } else {   // I % 4 == 0: a last half chunk
+        *reinterpret_cast<uint2*>(dst) = uint2{v[0], v[1]};
       }
-      if (sg.mode == 0) {
-        T* dst = out + j * sg.ldo + i;
-        if (i + 4 <= sg.I) {
-          *reinterpret_cast<typename Elem<T>::v4*>(dst) = o;
-        } else {
-          for (int r = 0; r < 4 && i + r < sg.I; ++r) dst[r] = o[r];
-        }
-      } else {
-        // Four consecutive virtual tokens of one sequence and one 32-token
-        // tile (Tp % 64 == 0, i % 4 == 0).
-        const VToken v = vtoken(b0, t0, i - i0, sg.Tp);
-        *reinterpret_cast<typename Elem<T>::v4*>(out + v.b * sg.vt_stride_b + (v.t >> 5) * 32 * sg.J + 32 * j +
-                                                 (v.t & 31)) = o;
-      }
+    } else {
+      // Eight consecutive virtual tokens of one sequence and one 32-token
+      // tile (Tp % 64 == 0, i % 8 == 0).
+      const VToken vt = vtoken(b0, t0, i - i0, sg.Tp);
+      store16B(out + vt.b * sg.vt_stride_b + (vt.t >> 5) * 32 * sg.J + 32 * j + (vt.t & 31), v);
     }
   }
 }
