@@ -39,6 +39,7 @@ namespace da {
 
 constexpr int kKeyTile = 32;
 constexpr int kAttnQW = 32;     // queries per wave
+constexpr int kAttnStages = 2; // stage buffers of the key/V^T ring
 
 struct AttnParams {
   const void* q;
@@ -49,9 +50,13 @@ struct AttnParams {
   int64_t vt_stride_b;
   int S, T, D;
   int n_qt, n_slices;
-  int chunk_tiles;     // > 0: split long causal key ranges into chunks of this many key tiles
-  int n_items;         // workgroups per (sequence, slice): sum over query tiles of their chunks
-  float* part;         // per item: [QT][DS] unnormalized outputs, then [QT] reference m, [QT] sums l
+  // Stream split (one map only): the key tiles of all query tiles of a
+  // (sequence, slice), query tile by query tile, form one stream that
+  // workgroup y covers from tile y*stream_len on, stream_len tiles.  0: one
+  // workgroup per query tile, every map.
+  int stream_len;
+  int n_seg;           // workgroups per (sequence, slice) in the stream split
+  float* part;         // per workgroup, two pieces: [QT][DS] normalized outputs, [QT] reference m, [QT] sums l
   const void* scales;
   int scales_dtype;
   float scale_mult;
@@ -94,45 +99,51 @@ __device__ __forceinline__ void store_rows(const AttnParams& p, int b, int s, in
   }
 }
 
-// Key tiles of query tile qt (QT queries) and the chunks they are split into.
+// Key tiles of query tile qt (QT queries).
 __device__ __forceinline__ int key_tiles_of(const AttnParams& p, int qt, int QT) {
   if (!(p.flags & kAttnCausal)) return (p.T + kKeyTile - 1) / kKeyTile;
   return (min(qt * QT + QT, p.T) - 1) / kKeyTile + 1;
 }
-__device__ __forceinline__ int chunks_of(const AttnParams& p, int qt, int QT) {
-  return p.chunk_tiles > 0 ? (key_tiles_of(p, qt, QT) + p.chunk_tiles - 1) / p.chunk_tiles : 1;
+// The stream split orders the query tiles of a (sequence, slice) in pairs
+// qt, n_qt-1-qt (0, n_qt-1, 1, n_qt-2, ...): a short causal tile next to a
+// long one, so every run of the stream holds few units (each unit switch
+// reloads the queries).  Stream unit i is query tile stream_qt(i).
+__device__ __forceinline__ int stream_qt(const AttnParams& p, int i) {
+  return (i & 1) ? p.n_qt - 1 - (i >> 1) : (i >> 1);
 }
-// Items (query tile x key chunk) of query tiles qt .. n_qt-1, which come
-// first in the heaviest-first order.  With chunking the tiles are QT = 64
-// queries = 2 key tiles, so a full causal tile t has 2(t+1) key tiles and
-// ceil((t+1)/h) chunks (h = chunk_tiles/2), whose prefix sums have a closed
-// form: sum_{q=1..n} ceil(q/h) = h a(a+1)/2 + r(a+1), n = a h + r.
-__device__ __forceinline__ int ceil_sum(int n, int h) {
-  const int a = n / h;
-  const int r = n - a * h;
-  return h * a * (a + 1) / 2 + r * (a + 1);
+__device__ __forceinline__ int stream_index(const AttnParams& p, int qt) {
+  return 2 * qt <= p.n_qt - 1 ? 2 * qt : 2 * (p.n_qt - 1 - qt) + 1;
 }
-__device__ __forceinline__ int items_from(const AttnParams& p, int qt, int QT) {
-  if (qt >= p.n_qt) return 0;
-  if (p.chunk_tiles == 0) return p.n_qt - qt;
-  if (!(p.flags & kAttnCausal)) return (p.n_qt - qt) * chunks_of(p, 0, QT);
-  const int last = p.n_qt - 1;   // the last tile may be partial
-  return ceil_sum(last, p.chunk_tiles / 2) - ceil_sum(qt, p.chunk_tiles / 2) + chunks_of(p, last, QT);
-}
-// Work item y of a (sequence, slice): returns its query tile; `chunk`,
-// `n_chunks` and `first` (the item index of the tile's chunk 0) describe its
-// place.  Binary search on the decreasing items_from.
-__device__ __forceinline__ int decode_item(const AttnParams& p, int y, int QT, int& chunk, int& n_chunks, int& first) {
-  int lo = 0, hi = p.n_qt - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (items_from(p, mid, QT) > y) lo = mid;
-    else hi = mid - 1;
+// Key tiles of every pair (PS) and the shortfall d of pair 0, whose second
+// tile is the last query tile (it may be partial): causal full tiles hold
+// QT/32 (qt+1) key tiles, so a pair holds (QT/32)(n_qt+1).
+__device__ __forceinline__ void stream_pairs(const AttnParams& p, int QT, int64_t& PS, int64_t& d) {
+  if (!(p.flags & kAttnCausal)) {
+    PS = 2 * static_cast<int64_t>(key_tiles_of(p, 0, QT));
+    d = 0;
+  } else {
+    PS = static_cast<int64_t>(QT / kKeyTile) * (p.n_qt + 1);
+    d = static_cast<int64_t>(QT / kKeyTile) * p.n_qt - key_tiles_of(p, p.n_qt - 1, QT);
   }
-  first = items_from(p, lo + 1, QT);
-  n_chunks = chunks_of(p, lo, QT);
-  chunk = y - first;
-  return lo;
+}
+// Stream position of unit i's first key tile.
+__device__ __forceinline__ int64_t tiles_before(const AttnParams& p, int i, int QT) {
+  int64_t PS, d;
+  stream_pairs(p, QT, PS, d);
+  const int j = i >> 1;
+  int64_t pos = static_cast<int64_t>(j) * PS - (j > 0 ? d : 0);
+  if (i & 1) pos += key_tiles_of(p, j, QT);
+  return pos;
+}
+// Stream unit holding stream tile gt.
+__device__ __forceinline__ int stream_unit(const AttnParams& p, int64_t gt, int QT) {
+  int64_t PS, d;
+  stream_pairs(p, QT, PS, d);
+  int64_t j = gt < PS - d ? 0 : 1 + (gt - (PS - d)) / PS;
+  j = min<int64_t>(j, (p.n_qt - 1) / 2);
+  int i = static_cast<int>(2 * j);
+  if (i + 1 < p.n_qt && gt >= tiles_before(p, i + 1, QT)) ++i;
+  return i;
 }
 
 template <int RP, int DS, int NW>
@@ -144,13 +155,16 @@ struct AttnTile {
   static constexpr int BYTES = KT::BYTES + VT::BYTES;     // one stage: a key tile, then a V^T tile
 };
 
-// The tile sequence u = 0 .. total-1 runs over (map s, key tile kt), u = s*n_kt + kt.
-// Stage buffer u%2 holds the keys of tile u+1 and the V^T of tile u, so step u
-// forms the scores of tile u+1 (MFMA) while it turns the scores of tile u into
-// probabilities (VALU) and accumulates P(u) V(u) (MFMA): the softmax of one
-// tile runs in the shadow of the next tile's score MFMAs.
-template <typename TQ, typename TV, int RP, int DS, int NW, bool MULTI>
+// A workgroup walks a run of key tiles u = 0 .. total-1 (the maps of one
+// query tile, or a stretch of the stream split).  A ring of NST stage buffers: stage u (buffer u % NST) holds the keys of tile
+// u+1 and the V^T of tile u, so step u forms the scores of tile u+1 (MFMA)
+// while it turns the scores of tile u into probabilities (VALU) and
+// accumulates P(u) V(u) (MFMA): the softmax of one tile runs in the shadow of
+// the next tile's score MFMAs.  Step u also issues stage u+NST-1 into the
+// buffer stage u-1 used, so every stage has NST-1 steps to land.
+template <typename TQ, typename TV, int RP, int DS, int NW, int NST, bool MULTI>
 __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
+  static_assert(NST == 2 || NST == 3, "two or three stage buffers");
   typedef AttnTile<RP, DS, NW> Tile;
   typedef typename Tile::KT KT;
   typedef typename Tile::VT VT;
@@ -160,27 +174,37 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   constexpr int NB = DS / 16;    // accumulator blocks per query block
   constexpr int NL = Tile::KPW + Tile::VPW;
   constexpr int QT = NW * kAttnQW;
-  __shared__ __attribute__((aligned(1024))) char lds0[Tile::BYTES];
-  __shared__ __attribute__((aligned(1024))) char lds1[Tile::BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds[NST * Tile::BYTES];
 
   const int lane = lane_id();
   const int c = lane & 15;
   const int g = lane >> 4;
   const int wave = uniform_wave();
-  // blockIdx.y = work item (query tile and key chunk), heaviest first;
-  // x = (sequence, slice).
-  int chunk, n_chunks, first_item;
-  const int qt = decode_item(p, static_cast<int>(blockIdx.y), QT, chunk, n_chunks, first_item);
   const int b = static_cast<int>(blockIdx.x) / p.n_slices;
   const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;   // first feature of the slice
-  const int q0 = qt * QT;
-  const int qw0 = q0 + wave * kAttnQW;                       // this wave's first query
   const bool causal = p.flags & kAttnCausal;
-  // Key tiles [kt_begin, kt_begin + n_kt) of every map.
-  const int kt_all = key_tiles_of(p, qt, QT);
-  const int kt_begin = p.chunk_tiles > 0 ? chunk * p.chunk_tiles : 0;
-  const int n_kt = p.chunk_tiles > 0 ? min(p.chunk_tiles, kt_all - kt_begin) : kt_all;
-  const int total = p.S * n_kt;
+  // The workgroup's work is a run of `total` key tiles over consecutive
+  // units: maps s of query tile n_qt-1-y (heaviest first), or in the stream
+  // split the query tiles of stream tiles [y*stream_len, ...).  The run starts
+  // at key tile kt_first of unit unit_first.
+  const bool stream = p.stream_len > 0;
+  const int qt_maps = p.n_qt - 1 - static_cast<int>(blockIdx.y);
+  const int n_kt_maps = key_tiles_of(p, qt_maps, QT);
+  int unit_first = 0, kt_first = 0, total;
+  if (stream) {
+    const int64_t g0 = static_cast<int64_t>(blockIdx.y) * p.stream_len;
+    const int last = p.n_qt - 1;
+    const int64_t all = tiles_before(p, last, QT) + key_tiles_of(p, stream_qt(p, last), QT);
+    unit_first = stream_unit(p, g0, QT);
+    kt_first = static_cast<int>(g0 - tiles_before(p, unit_first, QT));
+    total = static_cast<int>(min<int64_t>(p.stream_len, all - g0));
+  } else {
+    total = p.S * n_kt_maps;
+  }
+  // Units: key tiles, query tile and map.
+  auto unit_tiles = [&](int unit) { return stream ? key_tiles_of(p, stream_qt(p, unit), QT) : n_kt_maps; };
+  auto unit_qt = [&](int unit) { return stream ? stream_qt(p, unit) : qt_maps; };
+  auto unit_map = [&](int unit) { return stream ? 0 : unit; };
 
   const TQ* qbase = static_cast<const TQ*>(p.q) + b * p.qk_stride_b;
   const char* kbase = reinterpret_cast<const char*>(static_cast<const TQ*>(p.k) + b * p.qk_stride_b);
@@ -189,17 +213,19 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   const int kstride = static_cast<int>(p.qk_stride_t) * static_cast<int>(sizeof(TQ));   // bytes per key row
 
   // Per-lane DMA sources of this wave's loads: key load i fills wave load
-  // i*NW + wave of the key tile ((row << 16) | byte offset of the chunk; rows
-  // are clamped to the last key when the tile is issued), V^T load i the same
-  // wave load of the V^T tile (byte offset inside the tile).  Wave loads past a tile's end re-load the data of wave
-  // load 0 into slot 0 of that tile.
-  uint32_t kdesc[Tile::KPW], vdesc[Tile::VPW];
+  // i*NW + wave of the key tile (koff: byte offset of the lane's chunk from
+  // row 0; kchunk: the chunk's offset inside its row, so that rows past the
+  // last key clamp to it as min(koff, last*kstride + kchunk)), V^T load i the
+  // same wave load of the V^T tile (byte offset inside the tile).  Wave loads
+  // past a tile's end re-load the data of wave load 0 into slot 0 of that tile.
+  uint32_t koff[Tile::KPW], kchunk[Tile::KPW], vdesc[Tile::VPW];
 #pragma unroll
   for (int i = 0; i < Tile::KPW; ++i) {
     int row, ck;
     const int j = i * NW + wave;
     KT::slot_chunk((j < KT::LOADS ? j : 0) * 64 + lane, row, ck);
-    kdesc[i] = (static_cast<uint32_t>(row) << 16) | static_cast<uint32_t>(ck * 16);
+    kchunk[i] = static_cast<uint32_t>(ck * 16);
+    koff[i] = static_cast<uint32_t>(row * kstride) + kchunk[i];
   }
 #pragma unroll
   for (int i = 0; i < Tile::VPW; ++i) {
@@ -208,35 +234,83 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     VT::slot_chunk((j < VT::LOADS ? j : 0) * 64 + lane, row, ck);
     vdesc[i] = static_cast<uint32_t>((row * kKeyTile + ck * 8) * sizeof(TV));
   }
+  // LDS slot of this wave's load n inside a stage (key loads first): a
+  // constant plus wave*1024, except for the wave loads past a tile's end.
+  const int wave_slot = wave * 1024;
   auto slot_of = [&](int n) {
     if (n < Tile::KPW) {
-      const int j = n * NW + wave;
-      return j < KT::LOADS ? j * 1024 : 0;
+      if (n * NW + NW - 1 < KT::LOADS) return n * NW * 1024 + wave_slot;
+      return n * NW + wave < KT::LOADS ? n * NW * 1024 + wave_slot : 0;
     }
-    const int j = (n - Tile::KPW) * NW + wave;
-    return KT::BYTES + (j < VT::LOADS ? j * 1024 : 0);
+    const int i = n - Tile::KPW;
+    if (i * NW + NW - 1 < VT::LOADS) return KT::BYTES + i * NW * 1024 + wave_slot;
+    return KT::BYTES + (i * NW + wave < VT::LOADS ? i * NW * 1024 + wave_slot : 0);
   };
-  // DMA sources of tile u: key rows (keys past the end re-read the last one)
-  // and the V^T tile.
+  // DMA sources of one stage: row 0 of a key tile, the last key row it may
+  // read (rows past the end re-read it) and the V^T tile.
   struct Src {
     const char* k;
     const char* v;
     int last;
   };
-  auto source = [&](int uk, int uv) {
-    const int sk = uk / n_kt;
-    const int k0 = (kt_begin + uk - sk * n_kt) * kKeyTile;
-    const int64_t off = static_cast<int64_t>(sk / p.map_repeat) * p.map_stride * static_cast<int64_t>(sizeof(TQ));
-    const int v0 = (kt_begin + uv - (uv / n_kt) * n_kt) * kKeyTile;
-    return Src{kbase + static_cast<int64_t>(k0) * kstride + off,
-               vbase + static_cast<int64_t>(v0) * p.D * static_cast<int64_t>(sizeof(TV)), p.T - 1 - k0};
+  // Cursors over the key tiles and V^T tiles still to be loaded, in run
+  // order; each issue takes the next one, and past the end of the run the
+  // last tile is loaded again.  Key tiles follow the map's branch: maps s and
+  // s+1 share it while (s+1) % map_repeat != 0.
+  const int64_t ktile_bytes = static_cast<int64_t>(kKeyTile) * kstride;
+  const int64_t vtile_bytes = static_cast<int64_t>(kKeyTile) * p.D * static_cast<int64_t>(sizeof(TV));
+  const int64_t kmap_bytes = p.map_stride * static_cast<int64_t>(sizeof(TQ));
+  // Each cursor: unit, key tile, the unit's tile count, advances left, and
+  // the tile's address (keys: also the last row it may read).
+  struct Cursor {
+    int unit, kt, n, left;
+  };
+  Cursor kc{unit_first, kt_first, unit_tiles(unit_first), total - 1};
+  Cursor vc = kc;
+  const char* kmap = kbase;       // row 0 of the key cursor's map
+  const char* kptr = kbase + kt_first * ktile_bytes;
+  int klast = p.T - 1 - kt_first * kKeyTile;
+  int krep = 0;
+  const char* vptr = vbase + kt_first * vtile_bytes;
+  // Advances a cursor; true when it moved to the next unit (at key tile 0).
+  auto advance = [&](Cursor& cu) {
+    if (cu.left == 0) return false;
+    --cu.left;
+    if (++cu.kt == cu.n) {
+      cu.kt = 0;
+      cu.n = unit_tiles(++cu.unit);
+      return true;
+    }
+    return false;
+  };
+  auto next_key = [&]() {
+    const Src src{kptr, nullptr, klast};
+    if (kc.left > 0) {
+      if (advance(kc)) {
+        if (!stream && ++krep == p.map_repeat) {
+          krep = 0;
+          kmap += kmap_bytes;
+        }
+        kptr = kmap;
+        klast = p.T - 1;
+      } else {
+        kptr += ktile_bytes;
+        klast -= kKeyTile;
+      }
+    }
+    return src;
+  };
+  auto next_value = [&]() {
+    const char* v = vptr;
+    if (vc.left > 0) vptr = advance(vc) ? vbase : vptr + vtile_bytes;
+    return v;
   };
   auto issue_one = [&](char* buf, const Src& src, int n) {
     if (n < Tile::KPW) {
-      const int row = min(static_cast<int>(kdesc[n] >> 16), src.last);
-      dma16(src.k + static_cast<uint32_t>(row * kstride + static_cast<int>(kdesc[n] & 0xFFFFu)), buf + slot_of(n));
+      const uint32_t lim = static_cast<uint32_t>(src.last * kstride) + kchunk[n];
+      dma16(uniform_ptr(src.k) + min(koff[n], lim), buf + slot_of(n));
     } else {
-      dma16(src.v + vdesc[n - Tile::KPW], buf + slot_of(n));
+      dma16(uniform_ptr(src.v) + vdesc[n - Tile::KPW], buf + slot_of(n));
     }
   };
 
@@ -253,15 +327,16 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   float l_part[2] = {0.f, 0.f};
   q8 qf[2][KS];
 
-  // Query fragments of map s; returns the map's score multiplier (log2
-  // domain).  The rescale test compares maxima of raw scores, so a negative
-  // score scale is folded into the queries instead (negation is exact).
-  auto load_map = [&](int s) {
+  // Query fragments of map s for the wave's queries qw .. qw+31; returns the
+  // map's score multiplier (log2 domain).  The rescale test compares maxima
+  // of raw scores, so a negative score scale is folded into the queries
+  // instead (negation is exact).
+  auto load_queries = [&](int s, int qw) {
     const int64_t off = static_cast<int64_t>(s / p.map_repeat) * p.map_stride;
     const float gamma = map_gamma(p, s);
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const int tq = qw0 + cb * 16 + c;
+      const int tq = qw + cb * 16 + c;
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
         qf[cb][kk] = tq < p.T ? load8(qbase + static_cast<int64_t>(tq) * p.qk_stride_t + off + kk * 32 + 8 * g)
@@ -310,35 +385,46 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     }
   };
 
-  // Prologue: keys of tile 0 into stage 1's key slot, stage 0 = {K(1), V(0)}.
-  float sc = load_map(0);
-  float sc_next = sc;
+  // Prologue: keys of tile 0 into the last buffer's key slot, stages
+  // 0 .. NST-2 = {K(j+1), V(j)} into buffers 0 .. NST-2; the queries of map 0
+  // load meanwhile (one memory round trip for both).
   {
-    const Src s0 = source(0, 0);
+    const Src s0 = next_key();
 #pragma unroll
-    for (int n = 0; n < Tile::KPW; ++n) issue_one(lds1, s0, n);
-    const Src s1 = source(min(1, total - 1), 0);
+    for (int n = 0; n < Tile::KPW; ++n) issue_one(lds + (NST - 1) * Tile::BYTES, s0, n);
 #pragma unroll
-    for (int n = 0; n < NL; ++n) issue_one(lds0, s1, n);
+    for (int j = 0; j < NST - 1; ++j) {
+      Src sj = next_key();
+      sj.v = next_value();
+#pragma unroll
+      for (int n = 0; n < NL; ++n) issue_one(lds + j * Tile::BYTES, sj, n);
+    }
   }
+  int qw0 = unit_qt(unit_first) * QT + wave * kAttnQW;   // this wave's first query in the current unit
+  float sc = load_queries(unit_map(unit_first), qw0);
+  float sc_next = sc;
   wait_vmem();
   __syncthreads();
   f32x4 st_prev[2][2];
-  scores(lds1, st_prev, std::false_type{}, nullptr, Src{});
+  scores(lds + (NST - 1) * Tile::BYTES, st_prev, std::false_type{}, nullptr, Src{});
+  int cur_off = 0;                              // buffer of stage u
+  int nxt_off = (NST - 1) * Tile::BYTES;        // buffer of stage u-1: target of stage u+NST-1
 
-  // One pipelined step u = s*n_kt + kt.  FIXED: every score is bounded by
-  // score_bound, so exponents use the fixed reference score_bound*sc (all
-  // probabilities <= 1) and the accumulators are never rescaled; otherwise the
-  // lazy online rescale runs.
-  auto step = [&](auto fixed, int u, int s, int kt) {
+  // One pipelined step: tile u is key tile kt of the current unit.  FIXED:
+  // every score is bounded by score_bound, so exponents use the fixed
+  // reference score_bound*sc (all probabilities <= 1) and the accumulators
+  // are never rescaled; otherwise the lazy online rescale runs.  `opens`:
+  // tile u+1 is the first of unit `next`, whose queries this step's scores
+  // need.
+  auto step = [&](auto fixed, int kt, bool opens, int next) {
     constexpr bool FIXED = decltype(fixed)::value;
-    char* cur = (u & 1) ? lds1 : lds0;
-    char* nxt = (u & 1) ? lds0 : lds1;
-    const int k0 = (kt_begin + kt) * kKeyTile;
-    // Tile u + 1 opens map s + 1: its queries are needed by this step's scores.
-    if (kt == n_kt - 1 && s + 1 < p.S) sc_next = load_map(s + 1);
-    // Stage u + 1 = {K(u + 2), V(u + 1)}, clamped at the end of the sequence.
-    const Src src = source(min(u + 2, total - 1), min(u + 1, total - 1));
+    char* cur = lds + cur_off;
+    char* nxt = lds + nxt_off;
+    const int k0 = kt * kKeyTile;
+    if (opens) sc_next = load_queries(unit_map(next), unit_qt(next) * QT + wave * kAttnQW);
+    // Stage u + NST - 1 = {K(u + NST), V(u + NST - 1)}.
+    Src src = next_key();
+    src.v = next_value();
 
     // What may branch comes before the barrier: the causal / end mask
     // (diagonal and last tiles only) and the rescale test.  What follows it is
@@ -370,11 +456,53 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       }
     }
 
-    wait_vmem();
+    // Stage u has landed once at most the NST - 2 later stages are in flight.
+    wait_vmem_at_most<(NST - 2) * NL>();
     __syncthreads();
 
+    // Fragment reads come before the stage loads in program order where the
+    // registers allow: the loads write LDS, so the compiler keeps every later
+    // LDS read behind them.  Up to eight key steps and eight V^T blocks are
+    // read up front; 512-wide scores read their keys in groups of four steps,
+    // each two steps ahead of its first use, and their V^T blocks after the
+    // scores.  The loads are spread over the second half of the score MFMAs.
+    constexpr int KG = KS <= 8 ? KS : 4;
+    constexpr int KLEAD = 2;
+    constexpr int VA = KS <= 8 ? (NB < 8 ? NB : 8) : 0;
+    const char* kf = cur + kfrag;
+    const char* vf = cur + vfrag;
+    q8 kfr[KS][2];
+    v8 vfr[NB];
+    auto read_keys = [&](int kk) {
+      kfr[kk][0] = lds_v8<TQ>(kf + KT::offset(0, kk * 4));
+      kfr[kk][1] = lds_v8<TQ>(kf + KT::offset(16, kk * 4));
+    };
+#pragma unroll
+    for (int kk = 0; kk < KG; ++kk) read_keys(kk);
+#pragma unroll
+    for (int db = 0; db < VA; ++db) vfr[db] = lds_v8<TV>(vf + VT::offset(db * 16, 0));
+
     f32x4 st_new[2][2];
-    scores(cur, st_new, std::true_type{}, nxt, src);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) st_new[cb][0] = st_new[cb][1] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      if (KG < KS && kk + KLEAD >= KG && kk + KLEAD < KS && (kk + KLEAD) % KG == 0) {
+#pragma unroll
+        for (int k2 = kk + KLEAD; k2 < kk + KLEAD + KG; ++k2) read_keys(k2);
+      }
+      constexpr int D0 = KS / 2;
+#pragma unroll
+      for (int n = 0; n < NL; ++n)
+        if (kk >= D0 && D0 + n * (KS - D0) / NL == kk) issue_one(nxt, src, n);
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        st_new[cb][0] = Elem<TQ>::mma(kfr[kk][0], qf[cb][kk], st_new[cb][0]);
+        st_new[cb][1] = Elem<TQ>::mma(kfr[kk][1], qf[cb][kk], st_new[cb][1]);
+      }
+    }
+#pragma unroll
+    for (int db = VA; db < NB; ++db) vfr[db] = lds_v8<TV>(vf + VT::offset(db * 16, 0));
 
     // Probabilities of tile u: lane (c, g) holds keys k0 + 8g + 4kb + i for
     // query qw0 + 16cb + c.
@@ -396,43 +524,44 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     }
 
     // O^T += V^T(u) P^T(u).
-    const char* vf = cur + vfrag;
-    constexpr int VG = NB < 4 ? NB : 4;
 #pragma unroll
-    for (int d0 = 0; d0 < NB; d0 += VG) {
-      v8 vfr[VG];
-#pragma unroll
-      for (int db = 0; db < VG; ++db) vfr[db] = lds_v8<TV>(vf + VT::offset((d0 + db) * 16, 0));
-#pragma unroll
-      for (int db = 0; db < VG; ++db) {
-        acc[0][d0 + db] = Elem<TV>::mma(vfr[db], pb[0], acc[0][d0 + db]);
-        acc[1][d0 + db] = Elem<TV>::mma(vfr[db], pb[1], acc[1][d0 + db]);
-      }
+    for (int db = 0; db < NB; ++db) {
+      acc[0][db] = Elem<TV>::mma(vfr[db], pb[0], acc[0][db]);
+      acc[1][db] = Elem<TV>::mma(vfr[db], pb[1], acc[1][db]);
     }
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       st_prev[cb][0] = st_new[cb][0];
       st_prev[cb][1] = st_new[cb][1];
     }
+    nxt_off = cur_off;
+    cur_off = cur_off + Tile::BYTES == NST * Tile::BYTES ? 0 : cur_off + Tile::BYTES;
   };
 
-  for (int s = 0; s < p.S; ++s) {
+  int unit = unit_first, kt_start = kt_first, left = total;
+  while (left > 0) {
+    const int n_unit = unit_tiles(unit);
+    const int n_here = min(n_unit - kt_start, left);
+    const bool more = left > n_here;
+    const int s = unit_map(unit);
     // The fixed reference keeps every probability within the range of the
     // operand type: bf16 holds 2^-120 .. 1 exactly in exponent; fp16 does not.
     const bool fixed = p.score_bound > 0.f && sizeof(TV) == 2 && !std::is_same<TV, _Float16>::value &&
                        2.f * p.score_bound * sc <= 120.f;
-    const int u0 = s * n_kt;
     if (fixed) {
-      for (int kt = 0; kt < n_kt; ++kt) step(std::true_type{}, u0 + kt, s, kt);
+      for (int i = 0; i < n_here; ++i) step(std::true_type{}, kt_start + i, more && i == n_here - 1, unit + 1);
     } else {
-      for (int kt = 0; kt < n_kt; ++kt) step(std::false_type{}, u0 + kt, s, kt);
+      for (int i = 0; i < n_here; ++i) step(std::false_type{}, kt_start + i, more && i == n_here - 1, unit + 1);
     }
     const float wmap = map_weight(p, s);
-    // A chunk of a split key range (one map) stores its normalized outputs,
-    // reference and row sums in fp32 for the merge kernel; otherwise the map's
-    // output goes to its slot (or into the mix).
-    const bool partial = n_chunks > 1;
-    float* part = p.part + (static_cast<int64_t>(blockIdx.x) * p.n_items + blockIdx.y) * (QT * (DS + 2));
+    // A piece of a query tile's key range (stream split) stores its normalized
+    // outputs, reference and row sums in fp32 for the merge kernel: slot 0 if
+    // it is the run's first unit, else slot 1.  Otherwise the unit's output
+    // goes to its slot (or into the mix).
+    const bool partial = kt_start > 0 || n_here < n_unit;
+    float* part = p.part + ((static_cast<int64_t>(blockIdx.x) * p.n_seg + blockIdx.y) * 2 + (unit == unit_first ? 0 : 1)) *
+                               (QT * (DS + 2));
+    const int q0 = unit_qt(unit) * QT;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const float l = group_sum(l_part[cb]);
@@ -468,6 +597,10 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       l_part[cb] = 0.f;
     }
     sc = sc_next;
+    left -= n_here;
+    ++unit;
+    kt_start = 0;
+    qw0 = unit_qt(unit) * QT + wave * kAttnQW;
   }
 
   if constexpr (MULTI) {
@@ -482,70 +615,82 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   wait_vmem();
 }
 
-// Merge of split key ranges: out = sum_c 2^(m_c - M) l_c o_c / sum_c 2^(m_c - M) l_c,
-// o_c = O_c / l_c the chunk's normalized output, M = max_c m_c, per query row
-// (one map, weight 1).  Each wave takes one query row, its lanes covering
-// consecutive features, so every partial row is read by one coalesced sweep.
-template <typename TV, int DS>
+// Merge of a query tile split over stream workgroups: out = sum_c 2^(m_c - M)
+// l_c o_c / sum_c 2^(m_c - M) l_c over its pieces c, o_c the piece's
+// normalized output, M = max_c m_c, per query row (one map, weight 1).  The
+// tile's first stream tile is P; its pieces sit in workgroups y0 = P / L ..
+// y1 = (P + n - 1) / L, in slot 1 of y0 when the tile does not open y0's run,
+// else slot 0.  Each wave takes one query row, its lanes covering consecutive
+// features, so every partial row is read by one coalesced sweep.
+template <typename TV, int DS, int QT>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
-  constexpr int QT = 2 * kAttnQW;
-  const int qt = p.n_qt - 1 - static_cast<int>(blockIdx.y);
-  const int n_ch = chunks_of(p, qt, QT);
-  if (n_ch <= 1) return;   // written directly by its only item
-  const int first = items_from(p, qt + 1, QT);
+  const int qt = static_cast<int>(blockIdx.y);
+  const int64_t P = tiles_before(p, stream_index(p, qt), QT);
+  const int n = key_tiles_of(p, qt, QT);
+  const int y0 = static_cast<int>(P / p.stream_len);
+  const int y1 = static_cast<int>((P + n - 1) / p.stream_len);
+  if (y0 == y1) return;   // written directly by its workgroup
   const int b = static_cast<int>(blockIdx.x) / p.n_slices;
   const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;
   constexpr int ITEM = QT * (DS + 2);
-  const float* part = p.part + (static_cast<int64_t>(blockIdx.x) * p.n_items + first) * ITEM;
+  auto piece = [&](int y) {
+    const int slot = (y == y0 && P != static_cast<int64_t>(y0) * p.stream_len) ? 1 : 0;
+    return p.part + ((static_cast<int64_t>(blockIdx.x) * p.n_seg + y) * 2 + slot) * ITEM;
+  };
   const int lane = lane_id();
   // blockIdx.z picks four query rows of the tile, one per wave.
-  {
-    const int ql = static_cast<int>(blockIdx.z) * 4 + (static_cast<int>(threadIdx.x) >> 6);
-    const int tq = qt * QT + ql;
-    if (tq >= p.T) return;
-    float M = -INFINITY;
-    for (int c = 0; c < n_ch; ++c) M = fmaxf(M, part[c * ITEM + QT * DS + ql]);
-    f32x4 o[DS / 256 > 0 ? DS / 256 : 1];
+  const int ql = static_cast<int>(blockIdx.z) * 4 + (static_cast<int>(threadIdx.x) >> 6);
+  const int tq = qt * QT + ql;
+  if (tq >= p.T) return;
+  constexpr int NV = DS / 256 > 0 ? DS / 256 : 1;   // 4-feature vectors per lane
+  float M = -INFINITY;
+  for (int y = y0; y <= y1; ++y) M = fmaxf(M, piece(y)[QT * DS + ql]);
+  f32x4 o[NV];
 #pragma unroll
-    for (int k = 0; k < (DS / 256 > 0 ? DS / 256 : 1); ++k) o[k] = zero4();
-    float den = 0.f;
-    for (int c = 0; c < n_ch; ++c) {
-      const float m = part[c * ITEM + QT * DS + ql];
-      const float wl = (m == -INFINITY ? 0.f : exp2f(m - M)) * part[c * ITEM + QT * DS + QT + ql];
-      den += wl;
+  for (int k = 0; k < NV; ++k) o[k] = zero4();
+  float den = 0.f;
+  for (int y = y0; y <= y1; ++y) {
+    const float* pc = piece(y);
+    const float m = pc[QT * DS + ql];
+    const float wl = (m == -INFINITY ? 0.f : exp2f(m - M)) * pc[QT * DS + QT + ql];
+    den += wl;
 #pragma unroll
-      for (int k = 0; k < (DS / 256 > 0 ? DS / 256 : 1); ++k) {
-        const int d4 = (k * 64 + lane) * 4;
-        if (d4 < DS) o[k] += wl * *reinterpret_cast<const f32x4*>(part + c * ITEM + ql * DS + d4);
-      }
-    }
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    TV* orow = static_cast<TV*>(p.out) + b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t + ds0;
-#pragma unroll
-    for (int k = 0; k < (DS / 256 > 0 ? DS / 256 : 1); ++k) {
+    for (int k = 0; k < NV; ++k) {
       const int d4 = (k * 64 + lane) * 4;
-      if (d4 < DS) {
-        typename Elem<TV>::v4 v;
+      if (d4 < DS) o[k] += wl * *reinterpret_cast<const f32x4*>(pc + ql * DS + d4);
+    }
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  TV* orow = static_cast<TV*>(p.out) + b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t + ds0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(o[k][i] * inv);
-        *reinterpret_cast<typename Elem<TV>::v4*>(orow + d4) = v;
-      }
+  for (int k = 0; k < NV; ++k) {
+    const int d4 = (k * 64 + lane) * 4;
+    if (d4 < DS) {
+      typename Elem<TV>::v4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(o[k][i] * inv);
+      *reinterpret_cast<typename Elem<TV>::v4*>(orow + d4) = v;
     }
   }
 }
 
 template <typename TQ, typename TV, int RP, int DS, bool MULTI>
 static void launch_attn_3(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
+  // 512-wide scores take a whole CU's LDS per workgroup: four waves (128
+  // queries) share each key / V^T tile so every SIMD is busy.
+  constexpr int NW = RP == 512 ? 4 : 2;
+  constexpr int QT = NW * kAttnQW;
   p.n_slices = a.D / DS;
   p.n_qt = plan.n_qt;
-  p.chunk_tiles = plan.chunk_tiles;
-  p.n_items = plan.n_items;
-  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 2, MULTI>), dim3(a.B * p.n_slices, plan.n_items), dim3(128),
-                     0, s, p);
+  p.stream_len = plan.stream_len;
+  p.n_seg = plan.n_seg;
+  const int gy = plan.stream_len > 0 ? plan.n_seg : plan.n_qt;
+  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, NW, kAttnStages, MULTI>), dim3(a.B * p.n_slices, gy),
+                     dim3(NW * 64), 0, s, p);
   if constexpr (!MULTI) {
-    if (plan.chunk_tiles > 0)
-      hipLaunchKernelGGL((attention_merge_kernel<TV, DS>), dim3(a.B * p.n_slices, plan.n_qt, 2 * kAttnQW / 4),
-                         dim3(256), 0, s, p);
+    if (plan.stream_len > 0)
+      hipLaunchKernelGGL((attention_merge_kernel<TV, DS, QT>), dim3(a.B * p.n_slices, plan.n_qt, QT / 4), dim3(256), 0,
+                         s, p);
   }
 }
 
@@ -573,16 +718,27 @@ static void launch_attn_0(const AttentionArgs& a, const AttnPlan& plan, AttnPara
   }
 }
 
-// Key tiles of query tile qt of `length` tokens (host copy of key_tiles_of).
+// Host copy of key_tiles_of, and the key tiles of all query tiles.
 static int64_t host_key_tiles(int64_t qt, int64_t qtile, int64_t length, bool causal) {
   if (!causal) return (length + kKeyTile - 1) / kKeyTile;
   return (std::min(qt * qtile + qtile, length) - 1) / kKeyTile + 1;
 }
+static int64_t host_all_tiles(int64_t n_qt, int64_t qtile, int64_t length, bool causal) {
+  if (!causal) return n_qt * host_key_tiles(0, qtile, length, false);
+  return qtile / kKeyTile * (n_qt - 1) * n_qt / 2 + host_key_tiles(n_qt - 1, qtile, length, true);
+}
+
+// MI355X: 256 CUs of 160 KiB LDS; every attention variant holds more than 256
+// registers per lane, so a SIMD runs one wave.
+constexpr int64_t kCUs = 256;
+constexpr int64_t kLdsBytes = 160 * 1024;
 
 AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, bool multi, bool causal,
                         bool allow_split) {
   AttnPlan plan{};
-  const int64_t qtile = 2 * kAttnQW;
+  const int64_t nw = RP == 512 ? 4 : 2;
+  const int64_t qtile = nw * kAttnQW;
+  plan.nw = static_cast<int>(nw);
   plan.n_qt = static_cast<int>((T + qtile - 1) / qtile);
   // Value slice: as wide as possible (one score tile serves more value columns
   // and the softmax is shared by more MFMAs) while the grid keeps at least 256
@@ -593,25 +749,25 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
   while (ds > 128 && tiles * (D / ds) < 256) ds /= 2;
   plan.ds = static_cast<int>(ds);
   const int64_t slices = D / ds;
-  plan.n_items = plan.n_qt;
-  plan.chunk_tiles = 0;
-  // Long key ranges (one map only) on a grid that cannot fill the chip twice:
-  // split them into chunks so that the grid holds enough workgroups for every
-  // SIMD and the causal staircase is cut into pieces of similar length.
-  // Chunks keep >= 32 key tiles: below that the partials' traffic and the
-  // merge cost more than the balance gains.
-  const int64_t most = host_key_tiles(plan.n_qt - 1, qtile, T, causal);
-  if (allow_split && S == 1 && B * slices * plan.n_qt < 512 && most >= 64) {
-    for (int64_t kc = 256; kc >= 32; kc /= 2) {
-      if (kc >= most) continue;
-      int64_t items = 0;
-      for (int64_t qt = 0; qt < plan.n_qt; ++qt) items += (host_key_tiles(qt, qtile, T, causal) + kc - 1) / kc;
-      plan.chunk_tiles = static_cast<int>(kc);
-      plan.n_items = static_cast<int>(items);
-      if (B * slices * items >= 512) break;
-    }
+  // Stream split (one map only): when the longest query tile holds more key
+  // tiles than an even share of the whole problem over the workgroups that
+  // run at once, cut every (sequence, slice)'s stream of key tiles into runs
+  // of that share (at least 16 tiles, so the prologue and the partials stay
+  // small next to the run).
+  const int64_t stage = (RP / 8 + 1) * 32 * 16 + ds * 5 * 16;   // one key + V^T stage, padded
+  const int64_t stage_bytes = (stage + 1023) / 1024 * 1024;
+  const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4 / nw, kLdsBytes / (kAttnStages * stage_bytes)));
+  const int64_t last = plan.n_qt - 1;
+  const int64_t stream_all = host_all_tiles(plan.n_qt, qtile, T, causal);
+  const int64_t longest = host_key_tiles(last, qtile, T, causal);
+  const int64_t share = std::max<int64_t>(16, (B * slices * stream_all + kCUs * per_cu - 1) / (kCUs * per_cu));
+  plan.stream_len = 0;
+  plan.n_seg = 0;
+  if (allow_split && S == 1 && !multi && longest > share) {
+    plan.stream_len = static_cast<int>(share);
+    plan.n_seg = static_cast<int>((stream_all + share - 1) / share);
   }
-  plan.part_bytes = plan.chunk_tiles > 0 ? B * slices * plan.n_items * qtile * (ds + 2) * 4 : 0;
+  plan.part_bytes = plan.stream_len > 0 ? B * slices * plan.n_seg * 2 * qtile * (ds + 2) * 4 : 0;
   return plan;
 }
 

@@ -99,13 +99,15 @@ void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int
                                  int M, float eps, void* key_t, int key_dtype, void* value,
                                  void* value_rows, hipStream_t stream);
 void launch_dictionary_route(const RouteArgs& a, hipStream_t stream);
-// Launch shape of the attention for a problem: value slice width, key-range
-// chunking (0 = none) and the bytes of split-key partials it needs.
+// Launch shape of the attention for a problem: value slice width, waves per
+// workgroup, query tiles, the stream split of long key ranges (run length, 0
+// = none; runs per sequence and slice) and the bytes of partials it needs.
 struct AttnPlan {
   int ds;
-  int chunk_tiles;
+  int nw;
   int n_qt;
-  int n_items;
+  int stream_len;
+  int n_seg;
   int64_t part_bytes;
 };
 AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, bool multi, bool causal,

@@ -42,6 +42,16 @@ __device__ __forceinline__ void wait_vmem_at_most() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// A wave-uniform pointer moved to SGPRs, so that an address built from it
+// takes the scalar-base + 32-bit lane-offset form.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ int uniform_wave() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }

@@ -201,6 +201,9 @@ def test_route_zero_rows_and_empty() -> None:
     (1, 2, 64, 256, 128, (10.0, 14.0)),
     (1, 1, 1, 64, 64, (16.0,)),
     (1, 2, 200, 128, 256, (90.0, 3.0)),   # with a bound: the first map exceeds the fixed range
+    (1, 2, 300, 512, 128, (10.0, 13.0)),  # 512-wide scores: four-wave workgroups
+    (1, 1, 1024, 64, 128, (12.0,)),       # long key ranges: stream split and merge
+    (1, 1, 1000, 512, 128, (14.0,)),      # stream split with four-wave workgroups, ragged tail
 ])
 def test_routed_attention(dtype, causal, score_bound, batch, maps, length, score_dim, value_dim, scales) -> None:
     # Rows are unit vectors, so 1.01 bounds every score: bf16 maps whose scaled
