@@ -50,13 +50,16 @@ struct AttnParams {
   int64_t vt_stride_b;
   int S, T, D;
   int n_qt, n_slices;
-  // Stream split (one map only): the key tiles of all query tiles of a
-  // (sequence, slice), query tile by query tile, form one stream that
-  // workgroup y covers from tile y*stream_len on, stream_len tiles.  0: one
-  // workgroup per query tile, every map.
+  // Stream split (one map, or the map mix): the key tiles of every (query
+  // tile, map) unit of a (sequence, slice) form one stream that workgroup y
+  // covers from tile y*stream_len on, stream_len tiles.  0: one workgroup per
+  // query tile, every map.
   int stream_len;
   int n_seg;           // workgroups per (sequence, slice) in the stream split
-  float* part;         // per workgroup, two pieces: [QT][DS] normalized outputs, [QT] reference m, [QT] sums l
+  // Per workgroup of the stream split, slots of QT*(DS+2) floats: two unit
+  // pieces ([QT][DS] normalized outputs, [QT] reference m, [QT] sums l) and,
+  // with the map mix, two partial mixes ([QT][DS]).
+  float* part;
   const void* scales;
   int scales_dtype;
   float scale_mult;
@@ -135,7 +138,7 @@ __device__ __forceinline__ int64_t tiles_before(const AttnParams& p, int i, int 
   if (i & 1) pos += key_tiles_of(p, j, QT);
   return pos;
 }
-// Stream unit holding stream tile gt.
+// Query-tile stream index holding query-tile stream tile gt.
 __device__ __forceinline__ int stream_unit(const AttnParams& p, int64_t gt, int QT) {
   int64_t PS, d;
   stream_pairs(p, QT, PS, d);
@@ -144,6 +147,20 @@ __device__ __forceinline__ int stream_unit(const AttnParams& p, int64_t gt, int 
   int i = static_cast<int>(2 * j);
   if (i + 1 < p.n_qt && gt >= tiles_before(p, i + 1, QT)) ++i;
   return i;
+}
+
+// With S maps every query tile contributes S consecutive units (its maps in
+// order), so unit u = qi*S + s of query-tile stream index qi starts at
+// S * tiles_before(qi) + s * (key tiles of the query tile).
+__device__ __forceinline__ int64_t unit_start(const AttnParams& p, int u, int QT) {
+  const int qi = u / p.S;
+  const int s = u - qi * p.S;
+  return p.S * tiles_before(p, qi, QT) + static_cast<int64_t>(s) * key_tiles_of(p, stream_qt(p, qi), QT);
+}
+__device__ __forceinline__ int unit_of_tile(const AttnParams& p, int64_t gt, int QT) {
+  const int qi = stream_unit(p, gt / p.S, QT);
+  const int64_t a = p.S * tiles_before(p, qi, QT);
+  return qi * p.S + static_cast<int>((gt - a) / key_tiles_of(p, stream_qt(p, qi), QT));
 }
 
 template <int RP, int DS, int NW>
@@ -162,10 +179,20 @@ struct AttnTile {
 // accumulates P(u) V(u) (MFMA): the softmax of one tile runs in the shadow of
 // the next tile's score MFMAs.  Step u also issues stage u+NST-1 into the
 // buffer stage u-1 used, so every stage has NST-1 steps to land.
-template <typename TQ, typename TV, int RP, int DS, int NW, int NST, bool MULTI>
+//
+// SUB = 2 splits a workgroup's run between two sub-streams of NW/2 waves each
+// (the same queries): with one map the even and odd key tiles, with several
+// maps the even and odd maps.  Each sub-stream has its own key / V^T tiles in
+// every stage and the two step in lockstep (the shorter one pads with fully
+// masked tiles); at the end the odd sub-stream hands its accumulators over
+// LDS to the even one, which merges and stores.  A small grid so keeps every
+// SIMD of a CU busy, and long map mixes finish in half the steps.
+template <typename TQ, typename TV, int RP, int DS, int NW, int NST, bool MULTI, int SUB>
 __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   static_assert(NST == 2 || NST == 3, "two or three stage buffers");
-  typedef AttnTile<RP, DS, NW> Tile;
+  static_assert(SUB == 1 || SUB == 2, "one or two sub-streams");
+  constexpr int NQW = NW / SUB;   // waves of one sub-stream (its query waves)
+  typedef AttnTile<RP, DS, NQW> Tile;
   typedef typename Tile::KT KT;
   typedef typename Tile::VT VT;
   typedef typename Elem<TQ>::v8 q8;
@@ -173,13 +200,16 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   constexpr int KS = RP / 32;
   constexpr int NB = DS / 16;    // accumulator blocks per query block
   constexpr int NL = Tile::KPW + Tile::VPW;
-  constexpr int QT = NW * kAttnQW;
-  __shared__ __attribute__((aligned(1024))) char lds[NST * Tile::BYTES];
+  constexpr int QT = NQW * kAttnQW;
+  constexpr int SBYTES = SUB * Tile::BYTES;   // one stage: each sub-stream's key tile and V^T tile
+  __shared__ __attribute__((aligned(1024))) char lds[NST * SBYTES];
 
   const int lane = lane_id();
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int wave = uniform_wave();
+  const int sub = SUB == 1 ? 0 : uniform_wave() / NQW;
+  const int wave = uniform_wave() - sub * NQW;    // query wave inside the sub-stream
+  char* const lds_sub = lds + sub * Tile::BYTES;  // the sub-stream's share of stage 0
   const int b = static_cast<int>(blockIdx.x) / p.n_slices;
   const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;   // first feature of the slice
   const bool causal = p.flags & kAttnCausal;
@@ -187,24 +217,45 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   // units: maps s of query tile n_qt-1-y (heaviest first), or in the stream
   // split the query tiles of stream tiles [y*stream_len, ...).  The run starts
   // at key tile kt_first of unit unit_first.
-  const bool stream = p.stream_len > 0;
+  const bool stream = SUB == 1 && p.stream_len > 0;
   const int qt_maps = p.n_qt - 1 - static_cast<int>(blockIdx.y);
   const int n_kt_maps = key_tiles_of(p, qt_maps, QT);
-  int unit_first = 0, kt_first = 0, total;
-  if (stream) {
+  // Sub-streams of one map step over every second key tile (kt_stride 2).
+  const bool split_tiles = SUB == 2 && p.S == 1;
+  const int kt_stride = split_tiles ? 2 : 1;
+  int unit_first = 0, kt_first = 0, total, real;
+  if (SUB == 2) {
+    // Both sub-streams take `total` steps; the first `real` are theirs.  A
+    // sub-stream without a tile of its own points its loads at tile 0.
+    if (split_tiles) {
+      kt_first = min(sub, n_kt_maps - 1);
+      total = (n_kt_maps + 1) / 2;
+      real = (n_kt_maps - sub + 1) / 2;
+    } else {
+      total = (p.S + 1) / 2 * n_kt_maps;
+      real = (p.S - sub + 1) / 2 * n_kt_maps;
+    }
+  } else if (stream) {
     const int64_t g0 = static_cast<int64_t>(blockIdx.y) * p.stream_len;
     const int last = p.n_qt - 1;
-    const int64_t all = tiles_before(p, last, QT) + key_tiles_of(p, stream_qt(p, last), QT);
-    unit_first = stream_unit(p, g0, QT);
-    kt_first = static_cast<int>(g0 - tiles_before(p, unit_first, QT));
+    const int64_t all = p.S * (tiles_before(p, last, QT) + key_tiles_of(p, stream_qt(p, last), QT));
+    unit_first = unit_of_tile(p, g0, QT);
+    kt_first = static_cast<int>(g0 - unit_start(p, unit_first, QT));
     total = static_cast<int>(min<int64_t>(p.stream_len, all - g0));
+    real = total;
   } else {
     total = p.S * n_kt_maps;
+    real = total;
   }
-  // Units: key tiles, query tile and map.
-  auto unit_tiles = [&](int unit) { return stream ? key_tiles_of(p, stream_qt(p, unit), QT) : n_kt_maps; };
-  auto unit_qt = [&](int unit) { return stream ? stream_qt(p, unit) : qt_maps; };
-  auto unit_map = [&](int unit) { return stream ? 0 : unit; };
+  // Units: tiles (of this sub-stream), query tile and map.
+  auto unit_qt = [&](int unit) { return stream ? stream_qt(p, p.S == 1 ? unit : unit / p.S) : qt_maps; };
+  auto unit_tiles = [&](int unit) {
+    return stream ? key_tiles_of(p, unit_qt(unit), QT) : split_tiles ? real : n_kt_maps;
+  };
+  auto unit_map = [&](int unit) {
+    if (stream) return p.S == 1 ? 0 : unit % p.S;
+    return SUB == 2 ? min(sub + 2 * unit, p.S - 1) : unit;
+  };
 
   const TQ* qbase = static_cast<const TQ*>(p.q) + b * p.qk_stride_b;
   const char* kbase = reinterpret_cast<const char*>(static_cast<const TQ*>(p.k) + b * p.qk_stride_b);
@@ -213,7 +264,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   const int kstride = static_cast<int>(p.qk_stride_t) * static_cast<int>(sizeof(TQ));   // bytes per key row
 
   // Per-lane DMA sources of this wave's loads: key load i fills wave load
-  // i*NW + wave of the key tile (koff: byte offset of the lane's chunk from
+  // i*NQW + wave of the key tile (koff: byte offset of the lane's chunk from
   // row 0; kchunk: the chunk's offset inside its row, so that rows past the
   // last key clamp to it as min(koff, last*kstride + kchunk)), V^T load i the
   // same wave load of the V^T tile (byte offset inside the tile).  Wave loads
@@ -222,7 +273,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 #pragma unroll
   for (int i = 0; i < Tile::KPW; ++i) {
     int row, ck;
-    const int j = i * NW + wave;
+    const int j = i * NQW + wave;
     KT::slot_chunk((j < KT::LOADS ? j : 0) * 64 + lane, row, ck);
     kchunk[i] = static_cast<uint32_t>(ck * 16);
     koff[i] = static_cast<uint32_t>(row * kstride) + kchunk[i];
@@ -230,7 +281,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 #pragma unroll
   for (int i = 0; i < Tile::VPW; ++i) {
     int row, ck;
-    const int j = i * NW + wave;
+    const int j = i * NQW + wave;
     VT::slot_chunk((j < VT::LOADS ? j : 0) * 64 + lane, row, ck);
     vdesc[i] = static_cast<uint32_t>((row * kKeyTile + ck * 8) * sizeof(TV));
   }
@@ -239,12 +290,12 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   const int wave_slot = wave * 1024;
   auto slot_of = [&](int n) {
     if (n < Tile::KPW) {
-      if (n * NW + NW - 1 < KT::LOADS) return n * NW * 1024 + wave_slot;
-      return n * NW + wave < KT::LOADS ? n * NW * 1024 + wave_slot : 0;
+      if (n * NQW + NQW - 1 < KT::LOADS) return n * NQW * 1024 + wave_slot;
+      return n * NQW + wave < KT::LOADS ? n * NQW * 1024 + wave_slot : 0;
     }
     const int i = n - Tile::KPW;
-    if (i * NW + NW - 1 < VT::LOADS) return KT::BYTES + i * NW * 1024 + wave_slot;
-    return KT::BYTES + (i * NW + wave < VT::LOADS ? i * NW * 1024 + wave_slot : 0);
+    if (i * NQW + NQW - 1 < VT::LOADS) return KT::BYTES + i * NQW * 1024 + wave_slot;
+    return KT::BYTES + (i * NQW + wave < VT::LOADS ? i * NQW * 1024 + wave_slot : 0);
   };
   // DMA sources of one stage: row 0 of a key tile, the last key row it may
   // read (rows past the end re-read it) and the V^T tile.
@@ -260,50 +311,38 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   const int64_t ktile_bytes = static_cast<int64_t>(kKeyTile) * kstride;
   const int64_t vtile_bytes = static_cast<int64_t>(kKeyTile) * p.D * static_cast<int64_t>(sizeof(TV));
   const int64_t kmap_bytes = p.map_stride * static_cast<int64_t>(sizeof(TQ));
-  // Each cursor: unit, key tile, the unit's tile count, advances left, and
-  // the tile's address (keys: also the last row it may read).
-  struct Cursor {
-    int unit, kt, n, left;
-  };
-  Cursor kc{unit_first, kt_first, unit_tiles(unit_first), total - 1};
-  Cursor vc = kc;
-  const char* kmap = kbase;       // row 0 of the key cursor's map
-  const char* kptr = kbase + kt_first * ktile_bytes;
-  int klast = p.T - 1 - kt_first * kKeyTile;
-  int krep = 0;
+  // One cursor walks the run's tiles in order: unit, key tile, the unit's
+  // tile count, advances left (past the end of the run the last tile is
+  // loaded again), and the tile's key row 0, last readable key row and V^T
+  // tile.  A stage pairs the keys of one tile with the V^T of the tile before
+  // (vlag).
+  int cu_unit = unit_first, cu_kt = 0, cu_n = unit_tiles(unit_first), cu_left = real - 1;
+  if (!split_tiles) cu_kt = kt_first;
+  // Row 0 of a unit's key tiles: the map's branch (maps s and s+1 share it
+  // while (s+1) % map_repeat != 0).
+  auto key_row0 = [&](int unit) { return kbase + (unit_map(unit) / p.map_repeat) * kmap_bytes; };
+  const char* kptr = key_row0(unit_first) + kt_first * ktile_bytes;
   const char* vptr = vbase + kt_first * vtile_bytes;
-  // Advances a cursor; true when it moved to the next unit (at key tile 0).
-  auto advance = [&](Cursor& cu) {
-    if (cu.left == 0) return false;
-    --cu.left;
-    if (++cu.kt == cu.n) {
-      cu.kt = 0;
-      cu.n = unit_tiles(++cu.unit);
-      return true;
-    }
-    return false;
-  };
-  auto next_key = [&]() {
-    const Src src{kptr, nullptr, klast};
-    if (kc.left > 0) {
-      if (advance(kc)) {
-        if (!stream && ++krep == p.map_repeat) {
-          krep = 0;
-          kmap += kmap_bytes;
-        }
-        kptr = kmap;
-        klast = p.T - 1;
+  const char* vlag = vptr;
+  int klast = p.T - 1 - kt_first * kKeyTile;
+  auto take = [&]() {
+    const Src src{kptr, vlag, klast};
+    vlag = vptr;
+    if (cu_left > 0) {
+      --cu_left;
+      if (++cu_kt < cu_n) {
+        kptr += kt_stride * ktile_bytes;
+        vptr += kt_stride * vtile_bytes;
+        klast -= kt_stride * kKeyTile;
       } else {
-        kptr += ktile_bytes;
-        klast -= kKeyTile;
+        cu_kt = 0;
+        cu_n = unit_tiles(++cu_unit);
+        kptr = key_row0(cu_unit);
+        vptr = vbase;
+        klast = p.T - 1;
       }
     }
     return src;
-  };
-  auto next_value = [&]() {
-    const char* v = vptr;
-    if (vc.left > 0) vptr = advance(vc) ? vbase : vptr + vtile_bytes;
-    return v;
   };
   auto issue_one = [&](char* buf, const Src& src, int n) {
     if (n < Tile::KPW) {
@@ -389,15 +428,14 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   // 0 .. NST-2 = {K(j+1), V(j)} into buffers 0 .. NST-2; the queries of map 0
   // load meanwhile (one memory round trip for both).
   {
-    const Src s0 = next_key();
+    const Src s0 = take();
 #pragma unroll
-    for (int n = 0; n < Tile::KPW; ++n) issue_one(lds + (NST - 1) * Tile::BYTES, s0, n);
+    for (int n = 0; n < Tile::KPW; ++n) issue_one(lds_sub + (NST - 1) * SBYTES, s0, n);
 #pragma unroll
     for (int j = 0; j < NST - 1; ++j) {
-      Src sj = next_key();
-      sj.v = next_value();
+      const Src sj = take();
 #pragma unroll
-      for (int n = 0; n < NL; ++n) issue_one(lds + j * Tile::BYTES, sj, n);
+      for (int n = 0; n < NL; ++n) issue_one(lds_sub + j * SBYTES, sj, n);
     }
   }
   int qw0 = unit_qt(unit_first) * QT + wave * kAttnQW;   // this wave's first query in the current unit
@@ -406,9 +444,9 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   wait_vmem();
   __syncthreads();
   f32x4 st_prev[2][2];
-  scores(lds + (NST - 1) * Tile::BYTES, st_prev, std::false_type{}, nullptr, Src{});
+  scores(lds_sub + (NST - 1) * SBYTES, st_prev, std::false_type{}, nullptr, Src{});
   int cur_off = 0;                              // buffer of stage u
-  int nxt_off = (NST - 1) * Tile::BYTES;        // buffer of stage u-1: target of stage u+NST-1
+  int nxt_off = (NST - 1) * SBYTES;             // buffer of stage u-1: target of stage u+NST-1
 
   // One pipelined step: tile u is key tile kt of the current unit.  FIXED:
   // every score is bounded by score_bound, so exponents use the fixed
@@ -416,25 +454,25 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   // are never rescaled; otherwise the lazy online rescale runs.  `opens`:
   // tile u+1 is the first of unit `next`, whose queries this step's scores
   // need.
-  auto step = [&](auto fixed, int kt, bool opens, int next) {
+  auto step = [&](auto fixed, int kt, bool opens, int next, bool pad = false) {
     constexpr bool FIXED = decltype(fixed)::value;
-    char* cur = lds + cur_off;
-    char* nxt = lds + nxt_off;
+    char* cur = lds_sub + cur_off;
+    char* nxt = lds_sub + nxt_off;
     const int k0 = kt * kKeyTile;
     if (opens) sc_next = load_queries(unit_map(next), unit_qt(next) * QT + wave * kAttnQW);
     // Stage u + NST - 1 = {K(u + NST), V(u + NST - 1)}.
-    Src src = next_key();
-    src.v = next_value();
+    const Src src = take();
 
     // What may branch comes before the barrier: the causal / end mask
     // (diagonal and last tiles only) and the rescale test.  What follows it is
     // one straight block, so the compiler can interleave the exponentials of
     // tile u with the score MFMAs of tile u + 1.
-    if ((causal && k0 + kKeyTile - 1 > qw0) || k0 + kKeyTile > p.T) {
+    if ((causal && k0 + kKeyTile - 1 > qw0) || k0 + kKeyTile > p.T || pad) {
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
         const int tq = qw0 + cb * 16 + c;
-        const int kmax = min(causal ? tq : p.T - 1, p.T - 1);   // last key this query sees
+        // Last key this query sees; a padding step of a sub-stream sees none.
+        const int kmax = pad ? -1 : min(causal ? tq : p.T - 1, p.T - 1);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -535,66 +573,101 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       st_prev[cb][1] = st_new[cb][1];
     }
     nxt_off = cur_off;
-    cur_off = cur_off + Tile::BYTES == NST * Tile::BYTES ? 0 : cur_off + Tile::BYTES;
+    cur_off = cur_off + SBYTES == NST * SBYTES ? 0 : cur_off + SBYTES;
   };
 
-  int unit = unit_first, kt_start = kt_first, left = total;
+  // Slots of this workgroup's partial results (stream split).
+  constexpr int ITEM = QT * (DS + 2);
+  float* slots = p.part + static_cast<int64_t>(blockIdx.x * p.n_seg + blockIdx.y) * (MULTI ? 4 : 2) * ITEM;
+  // The fixed reference keeps every probability within the range of the
+  // operand type: bf16 holds 2^-120 .. 1 exactly in exponent; fp16 does not.
+  auto fixed_for = [&](float scale) {
+    return p.score_bound > 0.f && sizeof(TV) == 2 && !std::is_same<TV, _Float16>::value &&
+           2.f * p.score_bound * scale <= 120.f;
+  };
+  // Sub-streams of one map keep their accumulators for the final merge.
+  const bool keep = SUB == 2 && split_tiles;
+  int unit = unit_first, kt_start = split_tiles ? 0 : kt_first, left = real;
+  // The run holds the current query tile from its first map's first tile on.
+  bool qt_from_start = unit_map(unit_first) == 0 && kt_first == 0;
   while (left > 0) {
     const int n_unit = unit_tiles(unit);
     const int n_here = min(n_unit - kt_start, left);
     const bool more = left > n_here;
     const int s = unit_map(unit);
-    // The fixed reference keeps every probability within the range of the
-    // operand type: bf16 holds 2^-120 .. 1 exactly in exponent; fp16 does not.
-    const bool fixed = p.score_bound > 0.f && sizeof(TV) == 2 && !std::is_same<TV, _Float16>::value &&
-                       2.f * p.score_bound * sc <= 120.f;
+    const int qt = unit_qt(unit);
+    const bool fixed = fixed_for(sc);
     if (fixed) {
-      for (int i = 0; i < n_here; ++i) step(std::true_type{}, kt_start + i, more && i == n_here - 1, unit + 1);
+      for (int i = 0; i < n_here; ++i)
+        step(std::true_type{}, split_tiles ? sub + 2 * i : kt_start + i, more && i == n_here - 1, unit + 1);
     } else {
-      for (int i = 0; i < n_here; ++i) step(std::false_type{}, kt_start + i, more && i == n_here - 1, unit + 1);
+      for (int i = 0; i < n_here; ++i)
+        step(std::false_type{}, split_tiles ? sub + 2 * i : kt_start + i, more && i == n_here - 1, unit + 1);
     }
+    if (keep) break;
     const float wmap = map_weight(p, s);
-    // A piece of a query tile's key range (stream split) stores its normalized
+    // A piece of a unit's key range (stream split) stores its normalized
     // outputs, reference and row sums in fp32 for the merge kernel: slot 0 if
-    // it is the run's first unit, else slot 1.  Otherwise the unit's output
-    // goes to its slot (or into the mix).
-    const bool partial = kt_start > 0 || n_here < n_unit;
-    float* part = p.part + ((static_cast<int64_t>(blockIdx.x) * p.n_seg + blockIdx.y) * 2 + (unit == unit_first ? 0 : 1)) *
-                               (QT * (DS + 2));
-    const int q0 = unit_qt(unit) * QT;
+    // it is the run's first unit, else slot 1.  A whole unit goes to its
+    // output slot, or with the map mix into the query tile's mix.
+    const bool partial = stream && (kt_start > 0 || n_here < n_unit);
+    float* piece = slots + (unit == unit_first ? 0 : 1) * ITEM;
+    const int q0 = qt * QT;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const float l = group_sum(l_part[cb]);
       const float w = (partial ? 1.f : wmap) / (l > 0.f ? l : 1.f);
       const int ql = wave * kAttnQW + cb * 16 + c;
       const int tq = q0 + ql;
-      if constexpr (MULTI) {
+      if (partial) {
+#pragma unroll
+        for (int db = 0; db < NB; ++db)
+          *reinterpret_cast<f32x4*>(piece + ql * DS + db * 16 + 4 * g) = acc[cb][db] * w;
+        if (g == 0) {
+          piece[QT * DS + ql] = fixed ? p.score_bound * sc : m_run[cb];
+          piece[QT * DS + QT + ql] = l;
+        }
+      } else if constexpr (MULTI) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) yacc[cb][i] += acc[cb][i] * w;
-      } else {
+      } else if (tq < p.T) {
         TV* orow = static_cast<TV*>(p.out) + b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t +
                    ((p.flags & kAttnMix) ? 0 : s) * p.out_stride_s + ds0;
 #pragma unroll
         for (int db = 0; db < NB; ++db) {
           const f32x4 v = acc[cb][db] * w;
-          if (partial) {
-            *reinterpret_cast<f32x4*>(part + ql * DS + db * 16 + 4 * g) = v;
-          } else if (tq < p.T) {
-            typename Elem<TV>::v4 o;
+          typename Elem<TV>::v4 o;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[r] = static_cast<TV>(v[r]);
-            *reinterpret_cast<typename Elem<TV>::v4*>(orow + db * 16 + 4 * g) = o;
-          }
-        }
-        if (partial && g == 0) {
-          part[QT * DS + ql] = fixed ? p.score_bound * sc : m_run[cb];
-          part[QT * DS + QT + ql] = l;
+          for (int r = 0; r < 4; ++r) o[r] = static_cast<TV>(v[r]);
+          *reinterpret_cast<typename Elem<TV>::v4*>(orow + db * 16 + 4 * g) = o;
         }
       }
 #pragma unroll
       for (int i = 0; i < NB; ++i) acc[cb][i] = zero4();
       m_run[cb] = -INFINITY;
       l_part[cb] = 0.f;
+    }
+    if constexpr (MULTI && SUB == 1) {
+      // The query tile ends here (in this run): a tile the run holds whole is
+      // stored; otherwise its partial mix goes to mix slot 0 (the run's first
+      // query tile) or 1 for the merge kernel.
+      if (!more || unit_qt(unit + 1) != qt) {
+        const bool whole = qt_from_start && s == p.S - 1 && !partial;
+        float* mix = slots + (2 + (qt == unit_qt(unit_first) ? 0 : 1)) * ITEM;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const int ql = wave * kAttnQW + cb * 16 + c;
+          if (whole) {
+            if (q0 + ql < p.T) store_rows<TV, DS>(p, b, 0, q0 + ql, g, ds0, yacc[cb], 1.f);
+          } else {
+#pragma unroll
+            for (int db = 0; db < NB; ++db) *reinterpret_cast<f32x4*>(mix + ql * DS + db * 16 + 4 * g) = yacc[cb][db];
+          }
+#pragma unroll
+          for (int i = 0; i < NB; ++i) yacc[cb][i] = zero4();
+        }
+        qt_from_start = true;
+      }
     }
     sc = sc_next;
     left -= n_here;
@@ -603,11 +676,68 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     qw0 = unit_qt(unit) * QT + wave * kAttnQW;
   }
 
-  if constexpr (MULTI) {
+  if constexpr (SUB == 2) {
+    // Padding steps of the shorter sub-stream (every score masked).
+    const int n_pad = total - real;
+    if (fixed_for(sc)) {
+      for (int i = 0; i < n_pad; ++i) step(std::true_type{}, 0, false, 0, true);
+    } else {
+      for (int i = 0; i < n_pad; ++i) step(std::false_type{}, 0, false, 0, true);
+    }
+    if (keep || MULTI) {
+      // The odd sub-stream hands its accumulators (the map's unnormalized
+      // outputs with their references and row sums, or the mix) to the even
+      // one through LDS, in the lanes' own order.
+      wait_vmem();
+      __syncthreads();
+      constexpr int XW = 2 * NB * 256 + 256;   // floats per query wave
+      float* xch = reinterpret_cast<float*>(lds) + wave * XW;
+      if (sub == 1) {
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const int tq = qw0 + cb * 16 + c;
-      if (tq < p.T) store_rows<TV, DS>(p, b, 0, tq, g, ds0, yacc[cb], 1.f);
+        for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+          for (int db = 0; db < NB; ++db)
+            *reinterpret_cast<f32x4*>(xch + ((cb * NB + db) * 64 + lane) * 4) = MULTI ? yacc[cb][db] : acc[cb][db];
+          xch[2 * NB * 256 + lane * 4 + cb] = m_run[cb];
+          xch[2 * NB * 256 + lane * 4 + 2 + cb] = l_part[cb];
+        }
+      }
+      __syncthreads();
+      if (sub == 0) {
+        const bool fixed = fixed_for(sc);
+        const float wmap = map_weight(p, 0);
+        const int q0 = qt_maps * QT;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const int ql = wave * kAttnQW + cb * 16 + c;
+          if constexpr (MULTI) {
+#pragma unroll
+            for (int db = 0; db < NB; ++db)
+              yacc[cb][db] += *reinterpret_cast<const f32x4*>(xch + ((cb * NB + db) * 64 + lane) * 4);
+            if (q0 + ql < p.T) store_rows<TV, DS>(p, b, 0, q0 + ql, g, ds0, yacc[cb], 1.f);
+          } else {
+            // With the fixed reference both sub-streams share it; online,
+            // each scales to the larger running maximum.
+            const float m1 = xch[2 * NB * 256 + lane * 4 + cb];
+            const float l1 = xch[2 * NB * 256 + lane * 4 + 2 + cb];
+            float f0 = 1.f, f1 = 1.f;
+            if (!fixed) {
+              const float M = fmaxf(m_run[cb], m1);
+              f0 = m_run[cb] == -INFINITY ? 0.f : exp2f(m_run[cb] - M);
+              f1 = m1 == -INFINITY ? 0.f : exp2f(m1 - M);
+            }
+            const float l = group_sum(l_part[cb] * f0 + l1 * f1);
+            const float w = wmap / (l > 0.f ? l : 1.f);
+            if (q0 + ql < p.T) {
+              f32x4 o[NB];
+#pragma unroll
+              for (int db = 0; db < NB; ++db)
+                o[db] = acc[cb][db] * f0 + *reinterpret_cast<const f32x4*>(xch + ((cb * NB + db) * 64 + lane) * 4) * f1;
+              store_rows<TV, DS>(p, b, 0, q0 + ql, g, ds0, o, w);
+            }
+          }
+        }
+      }
     }
   }
   // The last step's (redundant) stage loads must land before the workgroup's
@@ -615,27 +745,32 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   wait_vmem();
 }
 
-// Merge of a query tile split over stream workgroups: out = sum_c 2^(m_c - M)
-// l_c o_c / sum_c 2^(m_c - M) l_c over its pieces c, o_c the piece's
-// normalized output, M = max_c m_c, per query row (one map, weight 1).  The
-// tile's first stream tile is P; its pieces sit in workgroups y0 = P / L ..
-// y1 = (P + n - 1) / L, in slot 1 of y0 when the tile does not open y0's run,
-// else slot 0.  Each wave takes one query row, its lanes covering consecutive
-// features, so every partial row is read by one coalesced sweep.
-template <typename TV, int DS, int QT>
+// Merge of a query tile split over stream workgroups.  The tile's S units
+// (maps) cover stream tiles [A, A + S n); a unit split over workgroups ya ..
+// yb merges as O = sum_c 2^(m_c - M) l_c o_c / sum_c 2^(m_c - M) l_c over its
+// pieces c (o_c normalized, M = max_c m_c), per query row.  Its piece sits in
+// slot 1 of ya when the unit does not open ya's run, else in slot 0.  With
+// the map mix the output is sum_s alpha_s O_s over the split units plus the
+// partial mixes of the whole units, one per workgroup ya .. yb of the tile
+// (slot rule as for pieces, offset by two slots).  Each wave takes one query
+// row, its lanes covering consecutive features, so every partial row is read
+// by one coalesced sweep.
+template <typename TV, int DS, int QT, bool MULTI>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   const int qt = static_cast<int>(blockIdx.y);
-  const int64_t P = tiles_before(p, stream_index(p, qt), QT);
+  const int64_t L = p.stream_len;
+  const int64_t A = p.S * tiles_before(p, stream_index(p, qt), QT);
   const int n = key_tiles_of(p, qt, QT);
-  const int y0 = static_cast<int>(P / p.stream_len);
-  const int y1 = static_cast<int>((P + n - 1) / p.stream_len);
+  const int y0 = static_cast<int>(A / L);
+  const int y1 = static_cast<int>((A + static_cast<int64_t>(p.S) * n - 1) / L);
   if (y0 == y1) return;   // written directly by its workgroup
   const int b = static_cast<int>(blockIdx.x) / p.n_slices;
   const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;
   constexpr int ITEM = QT * (DS + 2);
-  auto piece = [&](int y) {
-    const int slot = (y == y0 && P != static_cast<int64_t>(y0) * p.stream_len) ? 1 : 0;
-    return p.part + ((static_cast<int64_t>(blockIdx.x) * p.n_seg + y) * 2 + slot) * ITEM;
+  constexpr int NSLOT = MULTI ? 4 : 2;
+  auto slot = [&](int y, int64_t start, int k) {
+    const int first = (y == static_cast<int>(start / L) && start != (start / L) * L) ? 1 : 0;
+    return p.part + ((static_cast<int64_t>(blockIdx.x) * p.n_seg + y) * NSLOT + k + first) * ITEM;
   };
   const int lane = lane_id();
   // blockIdx.z picks four query rows of the tile, one per wave.
@@ -643,24 +778,45 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   const int tq = qt * QT + ql;
   if (tq >= p.T) return;
   constexpr int NV = DS / 256 > 0 ? DS / 256 : 1;   // 4-feature vectors per lane
-  float M = -INFINITY;
-  for (int y = y0; y <= y1; ++y) M = fmaxf(M, piece(y)[QT * DS + ql]);
-  f32x4 o[NV];
+  f32x4 out[NV];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) o[k] = zero4();
-  float den = 0.f;
-  for (int y = y0; y <= y1; ++y) {
-    const float* pc = piece(y);
-    const float m = pc[QT * DS + ql];
-    const float wl = (m == -INFINITY ? 0.f : exp2f(m - M)) * pc[QT * DS + QT + ql];
-    den += wl;
+  for (int k = 0; k < NV; ++k) out[k] = zero4();
+  if constexpr (MULTI) {
+    for (int y = y0; y <= y1; ++y) {
+      const float* mix = slot(y, A, 2);
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int d4 = (k * 64 + lane) * 4;
-      if (d4 < DS) o[k] += wl * *reinterpret_cast<const f32x4*>(pc + ql * DS + d4);
+      for (int k = 0; k < NV; ++k) {
+        const int d4 = (k * 64 + lane) * 4;
+        if (d4 < DS) out[k] += *reinterpret_cast<const f32x4*>(mix + ql * DS + d4);
+      }
     }
   }
-  const float inv = den > 0.f ? 1.f / den : 0.f;
+  for (int s = 0; s < p.S; ++s) {
+    const int64_t start = A + static_cast<int64_t>(s) * n;
+    const int ya = static_cast<int>(start / L);
+    const int yb = static_cast<int>((start + n - 1) / L);
+    if (ya == yb) continue;   // whole in one run: stored or in that run's mix
+    float M = -INFINITY;
+    for (int y = ya; y <= yb; ++y) M = fmaxf(M, slot(y, start, 0)[QT * DS + ql]);
+    f32x4 o[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) o[k] = zero4();
+    float den = 0.f;
+    for (int y = ya; y <= yb; ++y) {
+      const float* pc = slot(y, start, 0);
+      const float m = pc[QT * DS + ql];
+      const float wl = (m == -INFINITY ? 0.f : exp2f(m - M)) * pc[QT * DS + QT + ql];
+      den += wl;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int d4 = (k * 64 + lane) * 4;
+        if (d4 < DS) o[k] += wl * *reinterpret_cast<const f32x4*>(pc + ql * DS + d4);
+      }
+    }
+    const float w = (MULTI ? map_weight(p, s) : 1.f) * (den > 0.f ? 1.f / den : 0.f);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) out[k] += o[k] * w;
+  }
   TV* orow = static_cast<TV*>(p.out) + b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t + ds0;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -668,7 +824,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
     if (d4 < DS) {
       typename Elem<TV>::v4 v;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(o[k][i] * inv);
+      for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(out[k][i]);
       *reinterpret_cast<typename Elem<TV>::v4*>(orow + d4) = v;
     }
   }
@@ -677,7 +833,8 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
 template <typename TQ, typename TV, int RP, int DS, bool MULTI>
 static void launch_attn_3(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
   // 512-wide scores take a whole CU's LDS per workgroup: four waves (128
-  // queries) share each key / V^T tile so every SIMD is busy.
+  // queries) share each key / V^T tile so every SIMD is busy.  Narrower
+  // scores run two waves per query tile, or four as two sub-streams.
   constexpr int NW = RP == 512 ? 4 : 2;
   constexpr int QT = NW * kAttnQW;
   p.n_slices = a.D / DS;
@@ -685,13 +842,18 @@ static void launch_attn_3(const AttentionArgs& a, const AttnPlan& plan, AttnPara
   p.stream_len = plan.stream_len;
   p.n_seg = plan.n_seg;
   const int gy = plan.stream_len > 0 ? plan.n_seg : plan.n_qt;
-  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, NW, kAttnStages, MULTI>), dim3(a.B * p.n_slices, gy),
-                     dim3(NW * 64), 0, s, p);
-  if constexpr (!MULTI) {
-    if (plan.stream_len > 0)
-      hipLaunchKernelGGL((attention_merge_kernel<TV, DS, QT>), dim3(a.B * p.n_slices, plan.n_qt, QT / 4), dim3(256), 0,
-                         s, p);
+  if constexpr (RP < 512 && DS <= 128) {
+    if (plan.sub == 2) {
+      hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 2 * NW, kAttnStages, MULTI, 2>),
+                         dim3(a.B * p.n_slices, gy), dim3(2 * NW * 64), 0, s, p);
+      return;
+    }
   }
+  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, NW, kAttnStages, MULTI, 1>), dim3(a.B * p.n_slices, gy),
+                     dim3(NW * 64), 0, s, p);
+  if (plan.stream_len > 0)
+    hipLaunchKernelGGL((attention_merge_kernel<TV, DS, QT, MULTI>), dim3(a.B * p.n_slices, plan.n_qt, QT / 4),
+                       dim3(256), 0, s, p);
 }
 
 template <typename TQ, typename TV, int RP>
@@ -749,25 +911,52 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
   while (ds > 128 && tiles * (D / ds) < 256) ds /= 2;
   plan.ds = static_cast<int>(ds);
   const int64_t slices = D / ds;
-  // Stream split (one map only): when the longest query tile holds more key
-  // tiles than an even share of the whole problem over the workgroups that
-  // run at once, cut every (sequence, slice)'s stream of key tiles into runs
-  // of that share (at least 16 tiles, so the prologue and the partials stay
-  // small next to the run).
-  const int64_t stage = (RP / 8 + 1) * 32 * 16 + ds * 5 * 16;   // one key + V^T stage, padded
-  const int64_t stage_bytes = (stage + 1023) / 1024 * 1024;
-  const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4 / nw, kLdsBytes / (kAttnStages * stage_bytes)));
+  // Work shape, by the steps of the slowest workgroup slot: with G
+  // workgroups of at most h steps and W steps in all over C workgroups that
+  // run at once, about max(h, W / C).
+  //  - one workgroup per query tile (all maps);
+  //  - the same with two sub-streams (scores narrower than 512): half the
+  //    steps per workgroup, twice the LDS;
+  //  - the stream split (one map, or the map mix): runs of an even share of
+  //    all steps (at least 16, so the prologue and partials stay small next
+  //    to a run), plus the partials' round trip through memory.
+  auto concurrent = [&](int64_t waves, int64_t subs, int64_t width) {
+    const int64_t stage = subs * ((RP / 8 + 1) * 32 * 16 + width * 5 * 16);   // key + V^T tiles, padded
+    const int64_t stage_bytes = (stage + 1023) / 1024 * 1024;
+    return kCUs * std::max<int64_t>(1, std::min<int64_t>(4 / waves, kLdsBytes / (kAttnStages * stage_bytes)));
+  };
   const int64_t last = plan.n_qt - 1;
-  const int64_t stream_all = host_all_tiles(plan.n_qt, qtile, T, causal);
-  const int64_t longest = host_key_tiles(last, qtile, T, causal);
-  const int64_t share = std::max<int64_t>(16, (B * slices * stream_all + kCUs * per_cu - 1) / (kCUs * per_cu));
+  const int64_t n_last = host_key_tiles(last, qtile, T, causal);
+  const int64_t per_qt = S * n_last;   // the heaviest query tile
+  const int64_t stream_all = S * host_all_tiles(plan.n_qt, qtile, T, causal);
+  const int64_t work = B * slices * stream_all;
+  const int64_t c1 = concurrent(nw, 1, ds);
+  const int64_t span_maps = std::max(per_qt, (work + c1 - 1) / c1);
+  int64_t best = span_maps;
+  plan.sub = 1;
   plan.stream_len = 0;
   plan.n_seg = 0;
-  if (allow_split && S == 1 && !multi && longest > share) {
+  if (RP < 512) {
+    // Two sub-streams hold twice the accumulators: value slices of at most
+    // 128 features.
+    const int64_t ds2 = std::min<int64_t>(ds, 128);
+    const int64_t c2 = concurrent(2 * nw, 2, ds2);
+    const int64_t steps = S == 1 ? (n_last + 1) / 2 : (S + 1) / 2 * n_last;
+    const int64_t span_sub = std::max(steps, (B * (D / ds2) * stream_all / 2 + c2 - 1) / c2);
+    if (span_sub <= best) {
+      best = span_sub;
+      plan.sub = 2;
+      plan.ds = static_cast<int>(ds2);
+    }
+  }
+  const int64_t share = std::max<int64_t>(16, (work + c1 - 1) / c1);
+  if (allow_split && (S == 1 || multi) && per_qt > share && share * 5 / 4 < best) {
+    plan.sub = 1;
+    plan.ds = static_cast<int>(ds);
     plan.stream_len = static_cast<int>(share);
     plan.n_seg = static_cast<int>((stream_all + share - 1) / share);
   }
-  plan.part_bytes = plan.stream_len > 0 ? B * slices * plan.n_seg * 2 * qtile * (ds + 2) * 4 : 0;
+  plan.part_bytes = plan.stream_len > 0 ? B * slices * plan.n_seg * (multi ? 4 : 2) * qtile * (ds + 2) * 4 : 0;
   return plan;
 }
 

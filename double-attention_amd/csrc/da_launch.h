@@ -100,11 +100,12 @@ void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int
                                  void* value_rows, hipStream_t stream);
 void launch_dictionary_route(const RouteArgs& a, hipStream_t stream);
 // Launch shape of the attention for a problem: value slice width, waves per
-// workgroup, query tiles, the stream split of long key ranges (run length, 0
+// query tile, sub-streams, query tiles, the stream split of long key ranges (run length, 0
 // = none; runs per sequence and slice) and the bytes of partials it needs.
 struct AttnPlan {
   int ds;
   int nw;
+  int sub;          // sub-streams per workgroup (1 or 2)
   int n_qt;
   int stream_len;
   int n_seg;

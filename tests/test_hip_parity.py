@@ -327,6 +327,19 @@ def test_module_variants_odd_shapes(preset, overrides) -> None:
     run_module_case(preset, (1, 1, 512), seed=4, relative_to_torch=relative, **overrides)
 
 
+@pytest.mark.parametrize(("preset", "overrides"), [
+    ("a1", {}),
+    ("a1", {"causal": False}),
+    ("qk2-s2", {}),
+    ("qk4-s4", {}),
+    ("a1-r512-d512", {}),
+])
+def test_module_stream_split_ragged(preset, overrides) -> None:
+    # One ragged sequence long enough for the stream split of the key ranges
+    # (one map and the map mix), merged by the merge kernel.
+    run_module_case(preset, (1, 1000, 512), seed=5, **overrides)
+
+
 @pytest.mark.parametrize("name", ["a1_hip", "qk2_s2_hip"])
 def test_module_matches_reference_golden_vectors(name) -> None:
     device = _device()
