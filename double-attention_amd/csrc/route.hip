@@ -41,12 +41,12 @@ constexpr int kRouteRows = kRouteWaves * kRouteQW;
 // Fixed-reference mode keeps fp16 probabilities in [2^(kP16Lift - 2*beta*log2e), 2^kP16Lift].
 constexpr float kP16Lift = 14.f;
 
-template <int R>
+template <int R, int NW>
 struct RouteTile {
   typedef PaddedTile<kRouteAT, R / 8, true> KT;     // key atoms (blocked rows)
   typedef PaddedTile<R, kRouteAT / 8, false> VT;    // value coordinates x atoms
-  static constexpr int KPW = (KT::LOADS + kRouteWaves - 1) / kRouteWaves;
-  static constexpr int VPW = (VT::LOADS + kRouteWaves - 1) / kRouteWaves;
+  static constexpr int KPW = (KT::LOADS + NW - 1) / NW;   // loads per wave of NW sharing a tile
+  static constexpr int VPW = (VT::LOADS + NW - 1) / NW;
   static constexpr int BYTES = KT::BYTES + VT::BYTES;   // one stage: key atoms, then value atoms
 };
 
@@ -54,29 +54,41 @@ struct RouteTile {
 // stage buffer t%2 holds the key atoms of tile t+1 and the value atoms of tile
 // t, so step t forms the logits of tile t+1 (MFMA) while it turns the logits
 // of tile t into weights (VALU) and accumulates their reconstruction (MFMA).
-template <typename TX, typename TK, typename TO, int R>
-__global__ __launch_bounds__(kRouteWaves * 64, R >= 512 ? 1 : 2) void route_kernel(
+//
+// SUB = 2 runs two sub-streams of two waves over the same rows, the even and
+// the odd atom tiles (the padded atom count is even in tiles), each with its
+// own share of every stage; at the end the odd one hands its accumulators to
+// the even one through LDS.  Few rows then still spread over every CU.
+template <typename TX, typename TK, typename TO, int R, int SUB>
+__global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) void route_kernel(
     const TX* x, int64_t rows, int64_t x_stride, const TK* __restrict__ key_t,
     const _Float16* __restrict__ value, int M, int Mp, const void* __restrict__ beta_ptr,
     int beta_dtype, float beta_value, float eps, int flags, TO* out, int64_t out_stride) {
   // x and out may alias (in-place routing): every row is read into VGPRs by
   // its own wave before that wave writes it.
-  typedef RouteTile<R> Tile;
+  static_assert(SUB == 1 || SUB == 2, "one or two sub-streams");
+  constexpr int NQW = kRouteWaves / SUB;   // waves of one sub-stream (its row waves)
+  typedef RouteTile<R, NQW> Tile;
   typedef typename Tile::KT KT;
   typedef typename Tile::VT VT;
   typedef typename Elem<TK>::v8 k8;
   constexpr int KS = R / 32;
   constexpr int RB = R / 16;           // output row blocks
   constexpr int NL = Tile::KPW + Tile::VPW;
-  __shared__ __attribute__((aligned(1024))) char lds0[Tile::BYTES];
-  __shared__ __attribute__((aligned(1024))) char lds1[Tile::BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds_all[2 * SUB * Tile::BYTES];
 
   const int lane = lane_id();
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int wave = uniform_wave();
-  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kRouteWaves + wave) * kRouteQW;
-  const int n_tiles = Mp / kRouteAT;
+  const int sub = SUB == 1 ? 0 : uniform_wave() / NQW;
+  const int wave = uniform_wave() - sub * NQW;
+  // The sub-stream's share of the two stage buffers.
+  char* const lds0 = lds_all + sub * Tile::BYTES;
+  char* const lds1 = lds_all + (SUB + sub) * Tile::BYTES;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * NQW + wave) * kRouteQW;
+  // This sub-stream's atom tiles are tile_of(t) = SUB*t + sub, t < n_tiles.
+  const int n_tiles = Mp / kRouteAT / SUB;
+  auto tile_of = [&](int t) { return SUB * t + sub; };
 
   // Per-lane DMA sources (byte offsets from the tile's first atom): key load i
   // fills wave load i*4 + wave of the key tile (rows of key_t), value load i
@@ -86,33 +98,34 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 ? 1 : 2) void route_kern
 #pragma unroll
   for (int i = 0; i < Tile::KPW; ++i) {
     int row, ck;
-    const int j = i * kRouteWaves + wave;
+    const int j = i * NQW + wave;
     KT::slot_chunk((j < KT::LOADS ? j : 0) * 64 + lane, row, ck);
     kdesc[i] = static_cast<uint32_t>((row * R + ck * 8) * sizeof(TK));
   }
 #pragma unroll
   for (int i = 0; i < Tile::VPW; ++i) {
     int row, ck;
-    const int j = i * kRouteWaves + wave;
+    const int j = i * NQW + wave;
     VT::slot_chunk((j < VT::LOADS ? j : 0) * 64 + lane, row, ck);
     vdesc[i] = static_cast<uint32_t>(((ck >> 2) * 32 * R + row * 32 + (ck & 3) * 8) * 2);
   }
   auto slot_of = [&](int n) {
     if (n < Tile::KPW) {
-      const int j = n * kRouteWaves + wave;
+      const int j = n * NQW + wave;
       return j < KT::LOADS ? j * 1024 : 0;
     }
-    const int j = (n - Tile::KPW) * kRouteWaves + wave;
+    const int j = (n - Tile::KPW) * NQW + wave;
     return KT::BYTES + (j < VT::LOADS ? j * 1024 : 0);
   };
   const char* kbytes = reinterpret_cast<const char*>(key_t);
   const char* vbytes = reinterpret_cast<const char*>(value);
-  // Load n of this wave's share of stage {K(tk), V(tv)}.
+  // Load n of this wave's share of stage {K(tk), V(tv)} (the sub-stream's
+  // tiles tk, tv).
   auto issue_one = [&](char* buf, int tk, int tv, int n) {
     if (n < Tile::KPW) {
-      dma16(kbytes + static_cast<int64_t>(tk) * kRouteAT * R * sizeof(TK) + kdesc[n], buf + slot_of(n));
+      dma16(kbytes + static_cast<int64_t>(tile_of(tk)) * kRouteAT * R * sizeof(TK) + kdesc[n], buf + slot_of(n));
     } else {
-      dma16(vbytes + static_cast<int64_t>(tv) * kRouteAT * R * 2 + vdesc[n - Tile::KPW], buf + slot_of(n));
+      dma16(vbytes + static_cast<int64_t>(tile_of(tv)) * kRouteAT * R * 2 + vdesc[n - Tile::KPW], buf + slot_of(n));
     }
   };
 
@@ -202,7 +215,7 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 ? 1 : 2) void route_kern
     constexpr bool FIXED = decltype(fixed)::value;
     char* cur = (t & 1) ? lds1 : lds0;
     char* nxt = (t & 1) ? lds0 : lds1;
-    const int j0 = t * kRouteAT;
+    const int j0 = tile_of(t) * kRouteAT;
     // Lane (c, g) holds atoms j0 + 8g + 4kb + i of row c; only the last tile
     // can hold padding atoms.
     if (j0 + kRouteAT > M) {
@@ -262,6 +275,34 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 ? 1 : 2) void route_kern
     for (int t = 0; t < n_tiles; ++t) step(std::false_type{}, t);
   }
 
+  if constexpr (SUB == 2) {
+    // The odd sub-stream hands its accumulators (unnormalized outputs, their
+    // reference and row sums) to the even one through LDS, in the lanes' own
+    // order; with the fixed reference both share it, online each scales to
+    // the larger running maximum.
+    wait_vmem();
+    __syncthreads();
+    float* xch = reinterpret_cast<float*>(lds_all) + wave * (RB * 256 + 128);
+    if (sub == 1) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) *reinterpret_cast<f32x4*>(xch + (rb * 64 + lane) * 4) = acc[rb];
+      xch[RB * 256 + lane * 2] = m_run;
+      xch[RB * 256 + lane * 2 + 1] = l_part;
+    }
+    __syncthreads();
+    if (sub == 1) return;
+    const float m1 = xch[RB * 256 + lane * 2];
+    const float l1 = xch[RB * 256 + lane * 2 + 1];
+    float f0 = 1.f, f1 = 1.f;
+    if (!fixed) {
+      const float M = fmaxf(m_run, m1);
+      f0 = m_run == -INFINITY ? 0.f : exp2f(m_run - M);
+      f1 = m1 == -INFINITY ? 0.f : exp2f(m1 - M);
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = acc[rb] * f0 + *reinterpret_cast<const f32x4*>(xch + (rb * 64 + lane) * 4) * f1;
+    l_part = l_part * f0 + l1 * f1;
+  }
   // r = O / l; z = r / max(||r||, eps).
   const float inv_l = 1.f / group_sum(l_part);
   float out_scale = inv_l;
@@ -293,14 +334,31 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 ? 1 : 2) void route_kern
   wait_vmem();
 }
 
-template <typename TX, typename TK, typename TO, int R>
-static void launch_route_r(const RouteArgs& a, hipStream_t s) {
-  const int64_t blocks = (a.rows + kRouteRows - 1) / kRouteRows;
-  hipLaunchKernelGGL((route_kernel<TX, TK, TO, R>), dim3(static_cast<unsigned>(blocks)), dim3(kRouteWaves * 64), 0,
-                     s, static_cast<const TX*>(a.x), a.rows, a.x_stride, static_cast<const TK*>(a.key_t),
+template <typename TX, typename TK, typename TO, int R, int SUB>
+static void launch_route_s(const RouteArgs& a, hipStream_t s) {
+  constexpr int rows_per_block = kRouteRows / SUB;
+  const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((route_kernel<TX, TK, TO, R, SUB>), dim3(static_cast<unsigned>(blocks)), dim3(kRouteWaves * 64),
+                     0, s, static_cast<const TX*>(a.x), a.rows, a.x_stride, static_cast<const TK*>(a.key_t),
                      static_cast<const _Float16*>(a.value), a.M, static_cast<int>(round_up(a.M, kAtomPad)),
                      a.beta_ptr, a.beta_dtype, a.beta_value, a.eps, a.flags, static_cast<TO*>(a.out),
                      a.out_stride);
+}
+
+// Rows that do not give every CU (MI355X: 256) a workgroup of four row waves
+// run as two sub-streams (two row waves each) over the even and odd atom
+// tiles, up to 256-wide rows (the LDS holds four 512-wide stages only once).
+constexpr int64_t kRouteCUs = 256;
+
+template <typename TX, typename TK, typename TO, int R>
+static void launch_route_r(const RouteArgs& a, hipStream_t s) {
+  if constexpr (R <= 256) {
+    if ((a.rows + kRouteRows - 1) / kRouteRows < kRouteCUs) {
+      launch_route_s<TX, TK, TO, R, 2>(a, s);
+      return;
+    }
+  }
+  launch_route_s<TX, TK, TO, R, 1>(a, s);
 }
 
 template <typename TX, typename TK, typename TO>
