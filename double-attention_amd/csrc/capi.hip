@@ -12,6 +12,7 @@
 
 #include "../../include/double_attention_hip.h"
 #include "da_launch.h"
+#include "dict_norm.h"
 
 namespace {
 
@@ -102,7 +103,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 6; }
+int da_abi_version(void) { return 7; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -339,12 +340,24 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   if (!aligned(a->wq, 16) || !aligned(a->wk, 16) || !aligned(a->wv, 16) || (a->wo && !aligned(a->wo, 16)) ||
       !aligned(a->out, 16))
     return fail(DA_ERR_ALIGNMENT, "forward: weights and output must be 16-byte aligned");
+  // The bank's normalization, when asked for, rides in the projection launch.
+  da::NormJob norm{};
+  if (a->raw_key) {
+    if (!any_dtype(a->raw_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "forward: bad raw bank dtype");
+    if (!pow2_width(R)) return fail(DA_ERR_UNSUPPORTED, "forward: routing_dim %lld not in {64,128,256,512}", (long long)R);
+    if (a->atoms > (1 << 24)) return fail(DA_ERR_INVALID_ARGUMENT, "forward: bad atom count");
+    if (!aligned(a->key_t, 16) || !aligned(a->value, 16))
+      return fail(DA_ERR_ALIGNMENT, "forward: bank layouts must be 16-byte aligned");
+    norm = da::NormJob{a->raw_key, a->raw_value, a->raw_dtype, static_cast<int>(R), static_cast<int>(a->atoms),
+                       static_cast<int>(da::round_up(a->atoms, da::kAtomPad)), a->eps, const_cast<void*>(a->key_t),
+                       key_dtype, const_cast<void*>(a->value), nullptr};
+  }
 
   // 1. Q/K projections (route rows) and V^T with bias.
   da::GemmSegment proj[2];
   proj[0] = da::GemmSegment{a->wq, a->wk, W, a->x, 2 * W, B * T, d, nullptr, 0, 0, routed, 2 * W, 0, 0, 0};
   proj[1] = da::GemmSegment{a->x, nullptr, 0, a->wv, B * T, d, d, a->bv, a->param_dtype, 1, vt, 0, T, Tp, d * Tp};
-  da::launch_gemm(proj, 2, a->dtype, s);
+  da::launch_gemm(proj, 2, a->dtype, s, a->raw_key ? &norm : nullptr);
   // 2. Route all Q and K rows in place: [tokens, 2, H, R] is [tokens*2H, R].
   //    The routed rows are written as fp16 (unit vectors, or convex
   //    combinations of unit atoms without output normalization).

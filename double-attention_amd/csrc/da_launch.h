@@ -116,6 +116,9 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
 // `partials`: plan.part_bytes of device scratch (plan with allow_split), or
 // nullptr to run without key-range splitting.
 void launch_routed_attention(const AttentionArgs& a, void* partials, hipStream_t stream);
-void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream);
+struct NormJob;
+// `norm`: a dictionary normalization run by extra workgroups of the same
+// launch, or nullptr.
+void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream, const NormJob* norm = nullptr);
 
 }  // namespace da

@@ -18,9 +18,14 @@
 // Tiles: 128 x 128 per workgroup, 64-wide K stages double-buffered in padded
 // LDS tiles (da_tile.h) and filled by global->LDS DMA; each of the four waves
 // owns a 64 x 64 quadrant (4 x 4 MFMA 16x16x32 blocks).
+//
+// A launch may also carry a dictionary normalization (dict_norm.h): its
+// workgroups precede the GEMM tiles, so the module forward normalizes its bank
+// while the projections run, without a launch of its own.
 #include "da_common.h"
 #include "da_launch.h"
 #include "da_tile.h"
+#include "dict_norm.h"
 
 namespace da {
 
@@ -57,6 +62,8 @@ struct GemmSeg {
 struct GemmParams {
   GemmSeg seg[2];
   int nseg;
+  int gemm_blocks;     // workgroups of GEMM tiles, after those that run `norm`
+  NormJob norm;
 };
 
 // Virtual token i0 + off of the value segment as (sequence, token): the tile's
@@ -94,17 +101,26 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   typedef typename Cfg::TileP TileP;
   constexpr int STAGE = Cfg::STAGE;            // P tile, then Q tile
   constexpr int NA = Cfg::NA;
-  __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
-  __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
+  static_assert(2 * STAGE >= kNormLdsBytes, "a normalization workgroup reuses the stage buffers");
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  char* const lds0 = lds;
+  char* const lds1 = lds + STAGE;
 
-  int tile = blockIdx.x;
+  // The normalization's workgroups come first, so they start with the first
+  // wave of GEMM tiles instead of after them.
+  const int n_norm = static_cast<int>(gridDim.x) - prm.gemm_blocks;
+  if (static_cast<int>(blockIdx.x) < n_norm) {
+    normalize_block(prm.norm, static_cast<int>(blockIdx.x), lds);
+    return;
+  }
+  int tile = static_cast<int>(blockIdx.x) - n_norm;
   const int si = (prm.nseg > 1 && tile >= prm.seg[0].tiles) ? 1 : 0;
   if (si) tile -= prm.seg[0].tiles;
   const GemmSeg& sg = prm.seg[si];
   const int64_t i0 = static_cast<int64_t>(tile % sg.tiles_i) * BI;
   const int64_t j0 = static_cast<int64_t>(tile / sg.tiles_i) * kBJ;
   // Value segment: the tile's first virtual token, split once (uniform).
-  const int64_t b0 = sg.mode == 1 ? i0 / sg.Tp : 0;
+  const int64_t b0 = sg.mode == 1 ? static_cast<int>(i0) / static_cast<int>(sg.Tp) : 0;   // rows fit in int
   const int64_t t0 = sg.mode == 1 ? i0 - b0 * sg.Tp : 0;
 
   const int lane = lane_id();
@@ -157,21 +173,32 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   const int afrag = TileP::offset(wi * (BI / 2) + c, g);
   const int bfrag = TileP::BYTES + GemmTileQ::offset(wj * 64 + c, g);
 
+  // One K stage: every fragment of the stage is read first (LDS latency is
+  // paid once, and the reads precede the next stage's DMA in program order:
+  // the compiler keeps any LDS read behind a DMA that writes LDS), then the
+  // next stage is issued, then the MFMAs run.  A final half stage (K % 64 ==
+  // 32) takes one 32-deep step.
   auto step = [&](int st, char* cur, char* nxt) {
     wait_vmem();
     __syncthreads();
+    const bool full = K - st * kBK >= kBK;
+    v8 af[2][NA], bf[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      if (kk == 1 && !full) break;
+#pragma unroll
+      for (int a = 0; a < NA; ++a) af[kk][a] = lds_v8<T>(cur + afrag + TileP::offset(a * 16, kk * 4));
+#pragma unroll
+      for (int b = 0; b < 4; ++b) bf[kk][b] = lds_v8<T>(cur + bfrag + GemmTileQ::offset(b * 16, kk * 4));
+    }
     if (st + 1 < n_stages) issue(nxt, (st + 1) * kBK);
-    const int ksteps = min(kBK, K - st * kBK) / 32;
-    for (int kk = 0; kk < ksteps; ++kk) {
-      v8 af[NA], bf[4];
 #pragma unroll
-      for (int a = 0; a < NA; ++a) af[a] = lds_v8<T>(cur + afrag + TileP::offset(a * 16, kk * 4));
-#pragma unroll
-      for (int b = 0; b < 4; ++b) bf[b] = lds_v8<T>(cur + bfrag + GemmTileQ::offset(b * 16, kk * 4));
+    for (int kk = 0; kk < 2; ++kk) {
+      if (kk == 1 && !full) break;
 #pragma unroll
       for (int a = 0; a < NA; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = Elem<T>::mma(af[a], bf[b], acc[a][b]);
+        for (int b = 0; b < 4; ++b) acc[a][b] = Elem<T>::mma(af[kk][a], bf[kk][b], acc[a][b]);
     }
   };
 
@@ -275,18 +302,23 @@ static int setup_gemm(const GemmSegment* segs, int nseg, GemmParams& prm) {
 
 // 128-row tiles when the grid holds two workgroups per CU, else 64-row tiles
 // (twice the workgroups, so two share every CU and hide each other's waits).
-void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream) {
+// `norm` (or nullptr) adds a dictionary normalization's workgroups.
+void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream, const NormJob* norm) {
   GemmParams prm;
   int total = setup_gemm<128>(segs, nseg, prm);
-  if (total == 0) return;
+  prm.norm = norm ? *norm : NormJob{};
+  const int extra = norm_blocks(prm.norm);
+  if (total + extra == 0) return;
   if (total >= 512) {
-    if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 128>), dim3(total), dim3(256), 0, stream, prm);
-    else hipLaunchKernelGGL((gemm_kernel<__bf16, 128>), dim3(total), dim3(256), 0, stream, prm);
+    prm.gemm_blocks = total;
+    if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 128>), dim3(total + extra), dim3(256), 0, stream, prm);
+    else hipLaunchKernelGGL((gemm_kernel<__bf16, 128>), dim3(total + extra), dim3(256), 0, stream, prm);
     return;
   }
   total = setup_gemm<64>(segs, nseg, prm);
-  if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 64>), dim3(total), dim3(256), 0, stream, prm);
-  else hipLaunchKernelGGL((gemm_kernel<__bf16, 64>), dim3(total), dim3(256), 0, stream, prm);
+  prm.gemm_blocks = total;
+  if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 64>), dim3(total + extra), dim3(256), 0, stream, prm);
+  else hipLaunchKernelGGL((gemm_kernel<__bf16, 64>), dim3(total + extra), dim3(256), 0, stream, prm);
 }
 
 }  // namespace da

@@ -39,7 +39,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -76,6 +76,9 @@ class SdaForwardArgs(ctypes.Structure):
         ("workspace", _vp),
         ("workspace_bytes", _i64),
         ("out", _vp),
+        ("raw_key", _vp),
+        ("raw_value", _vp),
+        ("raw_dtype", _i32),
     ]
 
 

@@ -530,13 +530,30 @@ def check_module_supported(config) -> None:
         raise NotImplementedError(f"backend='hip' supports model_dim in {SUPPORTED_WIDTHS}")
 
 
+def own_bank_layout(bank, key_dtype: torch.dtype) -> RouteDictionary:
+    """Empty route layouts for a bank that the forward normalizes itself."""
+
+    routing_dim, atoms = bank.raw_key.shape
+    padded = _round_up(atoms, ATOM_PAD)
+    device = bank.raw_key.device
+    key_t = torch.empty(padded, routing_dim, dtype=key_dtype, device=device)
+    value = torch.empty(padded // 32, routing_dim, 32, dtype=torch.float16, device=device)
+    return RouteDictionary(key_t, value, atoms, True)
+
+
 def shared_dictionary_attention_hip(
     module,
     x: Tensor,
     layout: RouteDictionary,
     dtype: torch.dtype,
+    raw_bank: tuple[Tensor, Tensor | None] | None = None,
 ) -> HipForwardResult:
-    """One ``SharedDictionaryAttention`` forward through the fused C entry point."""
+    """One ``SharedDictionaryAttention`` forward through the fused C entry point.
+
+    With ``raw_bank`` (the bank's raw key / value atoms) the call first
+    normalizes them into ``layout`` (from ``own_bank_layout``), inside its
+    projection launch.
+    """
 
     config = module.config
     batch, length, model_dim = x.shape
@@ -587,6 +604,12 @@ def shared_dictionary_attention_hip(
         dtype_code(scalar_dtype), code, float(config.eps), flags,
         workspace.data_ptr(), ws_bytes, out.data_ptr(),
     )
+    if raw_bank is not None:
+        raw_key = raw_bank[0].detach().contiguous()
+        raw_value = None if raw_bank[1] is None else raw_bank[1].detach().to(raw_key.dtype).contiguous()
+        args.raw_key = raw_key.data_ptr()
+        args.raw_value = _ptr(raw_value)
+        args.raw_dtype = dtype_code(raw_key.dtype)
     _lib.check(lib.da_shared_dictionary_attention_forward(args, _stream(x.device)), "shared_dictionary_attention_hip")
     routed_bytes = batch * length * 2 * width * 2
     routed = workspace[:routed_bytes].view(torch.float16).view(

@@ -248,7 +248,6 @@ class SharedDictionaryAttention(nn.Module):
         from . import hip_ops
 
         hip_ops.check_module_supported(self.config)
-        eps = self.config.eps
         needs_grad = torch.is_grad_enabled() and (
             x.requires_grad or any(p.requires_grad for p in self.parameters())
             or (normalized_dictionary is not None and any(t.requires_grad for t in normalized_dictionary))
@@ -258,10 +257,14 @@ class SharedDictionaryAttention(nn.Module):
             return _HipModuleFunction.run(self, x, bank, normalized_dictionary, dtype, return_aux)
         key_dtype = hip_ops.route_key_dtype(self.config.normalize_routing_input, dtype)
         if normalized_dictionary is None:
-            layout = hip_ops.route_layout(*bank.normalized_hip(eps, key_dtype), key_dtype)
+            # The forward normalizes its own bank inside its projection launch.
+            layout = hip_ops.own_bank_layout(bank, key_dtype)
+            result = hip_ops.shared_dictionary_attention_hip(
+                self, x, layout, dtype, raw_bank=(bank.raw_key, bank.raw_value)
+            )
         else:
             layout = hip_ops.route_layout(*normalized_dictionary, key_dtype)
-        result = hip_ops.shared_dictionary_attention_hip(self, x, layout, dtype)
+            result = hip_ops.shared_dictionary_attention_hip(self, x, layout, dtype)
         if not return_aux:
             return result.output
         return result.output, self._hip_aux(result.routed, dtype)

@@ -187,7 +187,8 @@ typedef struct da_sda_forward_args {
   const void* wv;           /* value.weight [model_dim, model_dim] */
   const void* bv;           /* value.bias [model_dim] or NULL */
   const void* wo;           /* output.weight [model_dim, model_dim or maps*model_dim] or NULL (identity) */
-  const void* key_t;        /* normalized bank, da_dictionary_normalize layouts */
+  const void* key_t;        /* normalized bank, da_dictionary_normalize layouts (written by
+                               this call when raw_key is set) */
   const void* value;
   const void* log_beta;     /* scalar */
   const void* log_score_scales; /* [outer_maps] */
@@ -199,6 +200,12 @@ typedef struct da_sda_forward_args {
   void* workspace;          /* da_sda_workspace_bytes(...) bytes, 256-byte aligned */
   int64_t workspace_bytes;
   void* out;                /* [batch, length, model_dim] */
+  /* Optional: the raw bank (da_dictionary_normalize's raw_key / raw_value /
+   * raw_dtype).  When raw_key is non-NULL the call normalizes it into key_t
+   * and value first, inside its projection launch (no launch of its own). */
+  const void* raw_key;
+  const void* raw_value;
+  int raw_dtype;
 } da_sda_forward_args;
 
 /* Workspace layout (byte offsets, each 256-aligned):
