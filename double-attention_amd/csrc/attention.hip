@@ -166,7 +166,7 @@ __device__ __forceinline__ int unit_of_tile(const AttnParams& p, int64_t gt, int
 template <int RP, int DS, int NW>
 struct AttnTile {
   typedef PaddedTile<kKeyTile, RP / 8, true> KT;    // keys (blocked rows)
-  typedef PaddedTile<DS, kKeyTile / 8, false> VT;   // V^T rows: DS features x 4 chunks
+  typedef SwizzledTile4<DS> VT;                     // V^T rows: DS features x 4 chunks (32 tokens)
   static constexpr int KPW = (KT::LOADS + NW - 1) / NW;   // key loads per wave
   static constexpr int VPW = (VT::LOADS + NW - 1) / NW;   // V^T loads per wave
   static constexpr int BYTES = KT::BYTES + VT::BYTES;     // one stage: a key tile, then a V^T tile
@@ -691,6 +691,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       wait_vmem();
       __syncthreads();
       constexpr int XW = 2 * NB * 256 + 256;   // floats per query wave
+      static_assert(NQW * XW * 4 <= NST * SBYTES, "the hand-over fits the stage buffers");
       float* xch = reinterpret_cast<float*>(lds) + wave * XW;
       if (sub == 1) {
 #pragma unroll
@@ -921,7 +922,7 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
   //    all steps (at least 16, so the prologue and partials stay small next
   //    to a run), plus the partials' round trip through memory.
   auto concurrent = [&](int64_t waves, int64_t subs, int64_t width) {
-    const int64_t stage = subs * ((RP / 8 + 1) * 32 * 16 + width * 5 * 16);   // key + V^T tiles, padded
+    const int64_t stage = subs * ((RP / 8 + 1) * 32 * 16 + width * 4 * 16);   // key (padded) + V^T tiles
     const int64_t stage_bytes = (stage + 1023) / 1024 * 1024;
     return kCUs * std::max<int64_t>(1, std::min<int64_t>(4 / waves, kLdsBytes / (kAttnStages * stage_bytes)));
   };

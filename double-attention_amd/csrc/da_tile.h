@@ -85,6 +85,34 @@ struct PaddedTile {
   static __device__ __forceinline__ constexpr int offset(int prow, int ck) { return (prow * PITCH + ck) * 16; }
 };
 
+// A tile of ROWS rows of four 16-byte chunks with no pad slots: chunk c of
+// row r sits at slot 4r + (c ^ ((r >> 2) & 3)).  Sixteen lanes that read
+// sixteen consecutive rows at one chunk position cover 4 rows x 4 distinct
+// chunk slots of each 256-byte bank row, so they hit distinct bank groups,
+// and the DMA moves no padding.  For rows 16 apart the XOR term is equal, so
+// offset(r + 16 m, c) = offset(r, c) + 1024 m: fragment reads stay a per-lane
+// base plus an immediate offset.
+template <int ROWS>
+struct SwizzledTile4 {
+  static_assert(ROWS % 16 == 0, "whole wave loads");
+  static constexpr int NCK = 4;
+  static constexpr int SLOTS = ROWS * NCK;
+  static constexpr int LOADS = SLOTS / 64;
+  static constexpr int BYTES = LOADS * 1024;
+
+  // What slot `slot` holds (every slot is real).
+  static __device__ __forceinline__ bool slot_chunk(int slot, int& row, int& ck) {
+    row = slot >> 2;
+    ck = (slot & 3) ^ ((row >> 2) & 3);
+    return true;
+  }
+
+  // Byte offset of (row, chunk).
+  static __device__ __forceinline__ constexpr int offset(int row, int ck) {
+    return (row * NCK + (ck ^ ((row >> 2) & 3))) * 16;
+  }
+};
+
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::v8 lds_v8(const char* p) {
   return *reinterpret_cast<const typename Elem<T>::v8*>(p);

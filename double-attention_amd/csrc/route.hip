@@ -44,7 +44,7 @@ constexpr float kP16Lift = 14.f;
 template <int R, int NW>
 struct RouteTile {
   typedef PaddedTile<kRouteAT, R / 8, true> KT;     // key atoms (blocked rows)
-  typedef PaddedTile<R, kRouteAT / 8, false> VT;    // value coordinates x atoms
+  typedef SwizzledTile4<R> VT;                      // value coordinates x atoms (32 per row)
   static constexpr int KPW = (KT::LOADS + NW - 1) / NW;   // loads per wave of NW sharing a tile
   static constexpr int VPW = (VT::LOADS + NW - 1) / NW;
   static constexpr int BYTES = KT::BYTES + VT::BYTES;   // one stage: key atoms, then value atoms
@@ -282,6 +282,7 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
     // the larger running maximum.
     wait_vmem();
     __syncthreads();
+    static_assert(NQW * (RB * 256 + 128) * 4 <= 2 * SUB * Tile::BYTES, "the hand-over fits the stage buffers");
     float* xch = reinterpret_cast<float*>(lds_all) + wave * (RB * 256 + 128);
     if (sub == 1) {
 #pragma unroll
