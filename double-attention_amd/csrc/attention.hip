@@ -831,30 +831,41 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   }
 }
 
-template <typename TQ, typename TV, int RP, int DS, bool MULTI>
-static void launch_attn_3(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
-  // 512-wide scores take a whole CU's LDS per workgroup: four waves (128
-  // queries) share each key / V^T tile so every SIMD is busy.  Narrower
-  // scores run two waves per query tile, or four as two sub-streams.
-  constexpr int NW = RP == 512 ? 4 : 2;
+template <typename TQ, typename TV, int RP, int DS, bool MULTI, int NW>
+static void launch_attn_4(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
   constexpr int QT = NW * kAttnQW;
-  p.n_slices = a.D / DS;
-  p.n_qt = plan.n_qt;
-  p.stream_len = plan.stream_len;
-  p.n_seg = plan.n_seg;
   const int gy = plan.stream_len > 0 ? plan.n_seg : plan.n_qt;
-  if constexpr (RP < 512 && DS <= 128) {
-    if (plan.sub == 2) {
-      hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 2 * NW, kAttnStages, MULTI, 2>),
-                         dim3(a.B * p.n_slices, gy), dim3(2 * NW * 64), 0, s, p);
-      return;
-    }
-  }
   hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, NW, kAttnStages, MULTI, 1>), dim3(a.B * p.n_slices, gy),
                      dim3(NW * 64), 0, s, p);
   if (plan.stream_len > 0)
     hipLaunchKernelGGL((attention_merge_kernel<TV, DS, QT, MULTI>), dim3(a.B * p.n_slices, plan.n_qt, QT / 4),
                        dim3(256), 0, s, p);
+}
+
+template <typename TQ, typename TV, int RP, int DS, bool MULTI>
+static void launch_attn_3(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
+  // Two waves per query tile (64 queries), or four (128 queries) sharing each
+  // key / V^T tile: always for 512-wide scores, whose tiles take a whole CU's
+  // LDS, and for the stream split of long problems, where the tile fill per
+  // query halves.  Two sub-streams run four waves over 64 queries.
+  p.n_slices = a.D / DS;
+  p.n_qt = plan.n_qt;
+  p.stream_len = plan.stream_len;
+  p.n_seg = plan.n_seg;
+  if constexpr (RP < 512) {
+    if constexpr (DS <= 128) {
+      if (plan.sub == 2) {
+        hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, 4, kAttnStages, MULTI, 2>),
+                           dim3(a.B * p.n_slices, plan.n_qt), dim3(256), 0, s, p);
+        return;
+      }
+    }
+    if (plan.nw == 2) {
+      launch_attn_4<TQ, TV, RP, DS, MULTI, 2>(a, plan, p, s);
+      return;
+    }
+  }
+  launch_attn_4<TQ, TV, RP, DS, MULTI, 4>(a, plan, p, s);
 }
 
 template <typename TQ, typename TV, int RP>
@@ -951,13 +962,24 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
     }
   }
   const int64_t share = std::max<int64_t>(16, (work + c1 - 1) / c1);
+  int64_t part_qtile = qtile;
   if (allow_split && (S == 1 || multi) && per_qt > share && share * 5 / 4 < best) {
+    // The stream split runs four waves (128 queries) per workgroup: every key
+    // and V^T tile it fills serves twice the queries.
+    const int64_t q4 = 4 * kAttnQW;
+    const int64_t n_qt4 = (T + q4 - 1) / q4;
+    const int64_t all4 = S * host_all_tiles(n_qt4, q4, T, causal);
+    const int64_t c4 = concurrent(4, 1, ds);
+    const int64_t share4 = std::max<int64_t>(16, (B * slices * all4 + c4 - 1) / c4);
     plan.sub = 1;
+    plan.nw = 4;
     plan.ds = static_cast<int>(ds);
-    plan.stream_len = static_cast<int>(share);
-    plan.n_seg = static_cast<int>((stream_all + share - 1) / share);
+    plan.n_qt = static_cast<int>(n_qt4);
+    plan.stream_len = static_cast<int>(share4);
+    plan.n_seg = static_cast<int>((all4 + share4 - 1) / share4);
+    part_qtile = q4;
   }
-  plan.part_bytes = plan.stream_len > 0 ? B * slices * plan.n_seg * (multi ? 4 : 2) * qtile * (ds + 2) * 4 : 0;
+  plan.part_bytes = plan.stream_len > 0 ? B * slices * plan.n_seg * (multi ? 4 : 2) * part_qtile * (ds + 2) * 4 : 0;
   return plan;
 }
 

@@ -202,7 +202,7 @@ def test_route_zero_rows_and_empty() -> None:
     (1, 1, 1, 64, 64, (16.0,)),
     (1, 2, 200, 128, 256, (90.0, 3.0)),   # with a bound: the first map exceeds the fixed range
     (1, 2, 300, 512, 128, (10.0, 13.0)),  # 512-wide scores: four-wave workgroups
-    (1, 1, 1024, 64, 128, (12.0,)),       # long key ranges: stream split and merge
+    (1, 1, 2000, 64, 128, (12.0,)),       # long key ranges: stream split and merge, ragged tail
     (1, 1, 1000, 512, 128, (14.0,)),      # stream split with four-wave workgroups, ragged tail
 ])
 def test_routed_attention(dtype, causal, score_bound, batch, maps, length, score_dim, value_dim, scales) -> None:
@@ -337,7 +337,7 @@ def test_module_variants_odd_shapes(preset, overrides) -> None:
 def test_module_stream_split_ragged(preset, overrides) -> None:
     # One ragged sequence long enough for the stream split of the key ranges
     # (one map and the map mix), merged by the merge kernel.
-    run_module_case(preset, (1, 1000, 512), seed=5, **overrides)
+    run_module_case(preset, (1, 2000, 512), seed=5, **overrides)
 
 
 @pytest.mark.parametrize("name", ["a1_hip", "qk2_s2_hip"])
