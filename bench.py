@@ -5,7 +5,9 @@ normalization, Q/K/V projection, fused route, flash attention with the map
 mix, output projection) on one synthetic batch already resident in HBM, the
 same unit of work as the reference's ``benchmarks/benchmark_attention.py``
 forward mode.  The default workload is the north-star configuration: preset
-a1, x = [8, 512, 512] bf16.
+a1, x = [8, 512, 512] bf16.  ``--workload c4`` times the
+six-layer tied language model instead: a step is one ``DoubleAttentionLM``
+forward over [64, 64] token ids, and the per-kernel lines are one layer's.
 
 Prints ONE JSON line (rank 0).  Besides the module throughput it reports the
 per-kernel average durations measured with HIP events on the launch stream,
@@ -35,8 +37,15 @@ WORKLOADS = {
     "c1": ("a1", 8, 512, {}, "C1 preset a1 SharedDictionaryAttention forward x=[8,512,512]"),
     "c2": ("qk4-s4", 8, 1024, {}, "C2 preset qk4-s4 SharedDictionaryAttention forward x=[8,1024,512]"),
     "c3": ("a1-r512-d1536", 4, 2048, {}, "C3 preset a1-r512-d1536 SharedDictionaryAttention forward x=[4,2048,512]"),
+    "c4": ("qk2-s2", 64, 64, {"untied_dictionary": False},
+           "C4 DoubleAttentionLM qk2-s2 tied, 6 layers, vocab 2048, ffn 1536, tokens [64,64]"),
     "c5": ("a1", 1, 8192, {}, "C5 preset a1 long-context SharedDictionaryAttention forward x=[1,8192,512]"),
 }
+
+
+# C4 is the language model: a step is one whole LM forward (token ids to
+# logits); the per-kernel lines time one layer's attention launches.
+LM_VOCAB, LM_LAYERS, LM_FEEDFORWARD = 2048, 6, 1536
 
 
 def parse_args() -> argparse.Namespace:
@@ -121,17 +130,35 @@ def main() -> None:
     preset, batch, length, overrides, description = WORKLOADS[args.workload]
     config = da.experiment_config(preset, backend="hip", **overrides)
     torch.manual_seed(0)
-    module = da.SharedDictionaryAttention(config).to(device=device, dtype=dtype).eval()
+    lm = None
+    if args.workload == "c4":
+        lm = da.DoubleAttentionLM(
+            LM_VOCAB, length, config, LM_LAYERS, dictionary_group_size=LM_LAYERS, feedforward_dim=LM_FEEDFORWARD
+        ).to(device=device, dtype=dtype).eval()
+        ids = torch.randint(0, LM_VOCAB, (batch, length), generator=torch.Generator().manual_seed(1)).to(device)
+        module = lm.stack.blocks[0].attention
+        bank = lm.stack.banks[0]
+
+        def step():
+            return lm(ids)[0]
+    else:
+        module = da.SharedDictionaryAttention(config).to(device=device, dtype=dtype).eval()
+        bank = module.bank
+
+        def step():
+            return module(x)
+
+    # The attention input (for C4: one layer's, the LayerNorm output's shape).
     x = torch.randn(batch, length, config.model_dim, generator=torch.Generator().manual_seed(1)).to(device, dtype)
 
     # ---- whole forward (the step) ----------------------------------------
     with torch.inference_mode():
         for _ in range(args.warmup):
-            module(x)
+            step()
         torch.cuda.synchronize()
         start = time.perf_counter()
         for _ in range(args.steps):
-            out = module(x)
+            out = step()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
     ms_per_step = elapsed * 1e3 / args.steps
@@ -148,7 +175,7 @@ def main() -> None:
     with torch.inference_mode():
         key_dtype = da.hip_ops.route_key_dtype(config.normalize_routing_input, dtype)
         key_code = da.hip_ops.dtype_code(key_dtype)
-        key, value = module.bank.normalized_hip(config.eps, key_dtype)
+        key, value = bank.normalized_hip(config.eps, key_dtype)
         layout = key._da_route_layout
         qk = torch.empty(tokens, 2 * W, device=device, dtype=dtype)
         tp = lib.da_padded_length(length)
@@ -158,8 +185,8 @@ def main() -> None:
         final = torch.empty(tokens, d, device=device, dtype=dtype)
         p = {k: v.contiguous() for k, v in module.state_dict().items()}
         pdt = da.hip_ops.dtype_code(p["log_beta"].dtype)
-        raw_key = module.bank.raw_key.detach()
-        raw_value = module.bank.raw_value.detach() if module.bank.raw_value is not None else None
+        raw_key = bank.raw_key.detach()
+        raw_value = bank.raw_value.detach() if bank.raw_value is not None else None
 
         attn_flags = _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX
         attn_ws_bytes = lib.da_attention_workspace_bytes(batch, S, length, rp, d, attn_flags)
@@ -248,12 +275,22 @@ def main() -> None:
     if not args.no_cpu_baseline:
         import oracle
 
-        params = {k: v.float().cpu().numpy() for k, v in module.state_dict().items()}
-        xn = x.float().cpu().numpy()
+        if lm is not None:
+            params = {k: v.float().cpu().numpy() for k, v in lm.state_dict().items()}
+            idn = ids.cpu().numpy()
+
+            def cpu_step():
+                oracle.double_attention_lm(params, config, idn, LM_LAYERS, LM_LAYERS, dtype=np.float32)
+        else:
+            params = {k: v.float().cpu().numpy() for k, v in module.state_dict().items()}
+            xn = x.float().cpu().numpy()
+
+            def cpu_step():
+                oracle.shared_dictionary_attention(params, config, xn)
         reps = 0
         started = time.perf_counter()
         while True:
-            oracle.shared_dictionary_attention(params, config, xn)
+            cpu_step()
             reps += 1
             spent = time.perf_counter() - started
             if spent >= args.cpu_seconds or spent / reps * (reps + 1) > 30.0:
@@ -286,6 +323,7 @@ def main() -> None:
             "global_batch": batch,
             "seq_len": length,
             "routed_rows": rows,
+            **({"layers": LM_LAYERS, "vocab": LM_VOCAB, "feedforward_dim": LM_FEEDFORWARD} if lm is not None else {}),
             "parallelism": "single GPU",
         },
         "routed_rows_per_s": round(rows / (kernel_us["route"] * 1e-6), 1),

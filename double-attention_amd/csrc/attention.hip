@@ -71,12 +71,6 @@ struct AttnParams {
   int64_t out_stride_b, out_stride_t, out_stride_s;
 };
 
-__device__ __forceinline__ float map_gamma(const AttnParams& p, int s) {
-  float v = load_scalar(p.scales, p.scales_dtype, s);
-  if (p.flags & kAttnScalesAreLog) v = expf(fminf(fmaxf(v, kLogScaleMin), kLogScaleMax));
-  return v * p.scale_mult;
-}
-
 __device__ __forceinline__ float map_weight(const AttnParams& p, int s) {
   if (!(p.flags & kAttnMix)) return 1.f;
   if (p.mix_logits == nullptr) return 1.f / static_cast<float>(p.S);
@@ -207,6 +201,32 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   const int lane = lane_id();
   const int c = lane & 15;
   const int g = lane >> 4;
+  // Per-map constants, lane s holding map s (S <= 64; lanes past S repeat
+  // map S-1): the raw score scale and mix logit.  Issued first and without
+  // branches, so their round trip overlaps the set-up.
+  const int map_lane = min(lane, p.S - 1);
+  ScalarHalves scale_raw = fetch_scalar(p.scales, p.scales_dtype, map_lane);
+  const bool mix_logits = (p.flags & kAttnMix) && p.mix_logits != nullptr;
+  ScalarHalves mix_raw = fetch_scalar(mix_logits ? p.mix_logits : p.scales,
+                                      mix_logits ? p.mix_dtype : p.scales_dtype, map_lane);
+  auto lane_value = [](float v, int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i)); };
+  // Score scale gamma_s (clamped exp of the log scale, times scale_mult) and
+  // mix weight alpha_s (softmax of the logits, or 1/S) of map s.
+  auto gamma_of = [&](int s) {
+    float v = lane_value(scalar_value(scale_raw, p.scales_dtype), s);
+    if (p.flags & kAttnScalesAreLog) v = expf(fminf(fmaxf(v, kLogScaleMin), kLogScaleMax));
+    return v * p.scale_mult;
+  };
+  auto weight_of = [&](int s) {
+    if (!(p.flags & kAttnMix)) return 1.f;
+    if (!mix_logits) return 1.f / static_cast<float>(p.S);
+    const float logit = scalar_value(mix_raw, p.mix_dtype);
+    float mx = -INFINITY;
+    for (int i = 0; i < p.S; ++i) mx = fmaxf(mx, lane_value(logit, i));
+    float den = 0.f;
+    for (int i = 0; i < p.S; ++i) den += expf(lane_value(logit, i) - mx);
+    return expf(lane_value(logit, s) - mx) / den;
+  };
   const int sub = SUB == 1 ? 0 : uniform_wave() / NQW;
   const int wave = uniform_wave() - sub * NQW;    // query wave inside the sub-stream
   char* const lds_sub = lds + sub * Tile::BYTES;  // the sub-stream's share of stage 0
@@ -366,24 +386,35 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   float l_part[2] = {0.f, 0.f};
   q8 qf[2][KS];
 
-  // Query fragments of map s for the wave's queries qw .. qw+31; returns the
-  // map's score multiplier (log2 domain).  The rescale test compares maxima
-  // of raw scores, so a negative score scale is folded into the queries
-  // instead (negation is exact).
-  auto load_queries = [&](int s, int qw) {
+  // Query fragments of map s for the wave's queries qw .. qw+31 (fetch),
+  // then the map's score multiplier in the log2 domain (finish).  The
+  // rescale test compares maxima of raw scores, so a negative score scale is
+  // folded into the queries instead (negation is exact).
+  // Queries past the last token repeat its row: their outputs are never
+  // stored, and the loads need no branch.
+  auto fetch_queries = [&](int s, int qw) {
     const int64_t off = static_cast<int64_t>(s / p.map_repeat) * p.map_stride;
-    const float gamma = map_gamma(p, s);
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const int tq = qw + cb * 16 + c;
+      const int tq = min(qw + cb * 16 + c, p.T - 1);
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        qf[cb][kk] = tq < p.T ? load8(qbase + static_cast<int64_t>(tq) * p.qk_stride_t + off + kk * 32 + 8 * g)
-                              : zero8<TQ>();
-        if (gamma < 0.f) qf[cb][kk] = -qf[cb][kk];
-      }
+      for (int kk = 0; kk < KS; ++kk)
+        qf[cb][kk] = load8(qbase + static_cast<int64_t>(tq) * p.qk_stride_t + off + kk * 32 + 8 * g);
+    }
+  };
+  auto finish_queries = [&](int s) {
+    const float gamma = gamma_of(s);
+    if (gamma < 0.f) {
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) qf[cb][kk] = -qf[cb][kk];
     }
     return fabsf(gamma) * kLog2e;
+  };
+  auto load_queries = [&](int s, int qw) {
+    fetch_queries(s, qw);
+    return finish_queries(s);
   };
 
   const int kfrag = KT::offset(c, g);
@@ -424,9 +455,11 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     }
   };
 
-  // Prologue: keys of tile 0 into the last buffer's key slot, stages
-  // 0 .. NST-2 = {K(j+1), V(j)} into buffers 0 .. NST-2; the queries of map 0
-  // load meanwhile (one memory round trip for both).
+  // Prologue: the queries of the first unit, keys of tile 0 into the last
+  // buffer's key slot and stages 0 .. NST-2 = {K(j+1), V(j)} into buffers
+  // 0 .. NST-2, all in one memory round trip.
+  int qw0 = unit_qt(unit_first) * QT + wave * kAttnQW;   // this wave's first query in the current unit
+  fetch_queries(unit_map(unit_first), qw0);
   {
     const Src s0 = take();
 #pragma unroll
@@ -438,10 +471,12 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       for (int n = 0; n < NL; ++n) issue_one(lds_sub + j * SBYTES, sj, n);
     }
   }
-  int qw0 = unit_qt(unit_first) * QT + wave * kAttnQW;   // this wave's first query in the current unit
-  float sc = load_queries(unit_map(unit_first), qw0);
-  float sc_next = sc;
+  // Nothing that uses a loaded value moves above the loads' issue: with DMA
+  // in flight, an early use would wait for every load.
+  __builtin_amdgcn_sched_barrier(0);
   wait_vmem();
+  float sc = finish_queries(unit_map(unit_first));
+  float sc_next = sc;
   __syncthreads();
   f32x4 st_prev[2][2];
   scores(lds_sub + (NST - 1) * SBYTES, st_prev, std::false_type{}, nullptr, Src{});
@@ -605,7 +640,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
         step(std::false_type{}, split_tiles ? sub + 2 * i : kt_start + i, more && i == n_here - 1, unit + 1);
     }
     if (keep) break;
-    const float wmap = map_weight(p, s);
+    const float wmap = weight_of(s);
     // A piece of a unit's key range (stream split) stores its normalized
     // outputs, reference and row sums in fp32 for the merge kernel: slot 0 if
     // it is the run's first unit, else slot 1.  A whole unit goes to its
@@ -706,7 +741,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       __syncthreads();
       if (sub == 0) {
         const bool fixed = fixed_for(sc);
-        const float wmap = map_weight(p, 0);
+        const float wmap = weight_of(0);
         const int q0 = qt_maps * QT;
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {

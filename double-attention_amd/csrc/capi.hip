@@ -85,6 +85,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
   if (!pow2_width(D)) return fail(DA_ERR_UNSUPPORTED, "attention: value_dim %lld not in {64,128,256,512}", (long long)D);
   if (B < 0 || T < 0 || S < 1 || rep < 1 || B > 65535 || T > (1LL << 30))
     return fail(DA_ERR_INVALID_ARGUMENT, "attention: bad batch/maps/length/map_repeat");
+  if (S > 64) return fail(DA_ERR_UNSUPPORTED, "attention: at most 64 maps (got %lld)", (long long)S);
   if (B == 0 || T == 0) return DA_OK;
   if (!q || !k || !vt || !scales || !out) return fail(DA_ERR_INVALID_ARGUMENT, "attention: null pointer");
   if (!any_dtype(scales_dtype) || (mix && !any_dtype(mix_dtype)))
@@ -289,6 +290,7 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   if (B < 1 || T < 1 || d < 1 || H < 1 || S < 1 || R < 1 || a->atoms < 1)
     return fail(DA_ERR_INVALID_ARGUMENT, "forward: sizes must be positive");
   if ((H > S ? H % S : S % H) != 0) return fail(DA_ERR_INVALID_ARGUMENT, "forward: branches and maps must divide one another");
+  if (S > 64) return fail(DA_ERR_UNSUPPORTED, "forward: at most 64 maps (got %lld)", (long long)S);
   if (!half_dtype(a->dtype) || !any_dtype(a->param_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "forward: bad dtype");
   if (!a->x || !a->wq || !a->wk || !a->wv || !a->key_t || !a->value || !a->log_beta ||
       !a->log_score_scales || !a->out || !a->workspace)

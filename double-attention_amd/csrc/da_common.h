@@ -57,6 +57,25 @@ __device__ __forceinline__ float load_scalar(const void* p, int dtype, int64_t i
   return static_cast<float>(static_cast<const __bf16*>(p)[i]);
 }
 
+// Element i of a scalar array in two steps: fetch_scalar issues two 16-bit
+// loads without branching on the dtype (the second re-reads the first for
+// 16-bit types), so their wait falls at the first use; scalar_value
+// assembles and converts.
+struct ScalarHalves {
+  uint16_t lo, hi;
+};
+__device__ __forceinline__ ScalarHalves fetch_scalar(const void* p, int dtype, int64_t i) {
+  const bool wide = dtype == kF32;
+  const uint16_t* h = static_cast<const uint16_t*>(p) + (wide ? 2 * i : i);
+  return ScalarHalves{h[0], h[wide ? 1 : 0]};
+}
+__device__ __forceinline__ float scalar_value(ScalarHalves v, int dtype) {
+  const uint32_t lo = v.lo, hi = v.hi;
+  if (dtype == kF32) return __uint_as_float(hi << 16 | lo);
+  if (dtype == kF16) return static_cast<float>(__builtin_bit_cast(_Float16, v.lo));
+  return __uint_as_float(lo << 16);
+}
+
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
 // Reductions across the four 16-lane rows (lanes c, c+16, c+32, c+48 hold the

@@ -129,14 +129,28 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
     }
   };
 
-  // Prologue DMA: keys of tile 0 into stage 1's key slot, stage 0 = {K(1), V(0)}.
+  // Prologue: beta and the wave's rows, then the DMA of the keys of tile 0
+  // into stage 1's key slot and stage 0 = {K(1), V(0)}, all in one memory
+  // round trip.  Rows past the end repeat the last row (never stored).
+  const ScalarHalves beta_bits = fetch_scalar(beta_ptr ? beta_ptr : static_cast<const void*>(x),
+                                              beta_ptr ? beta_dtype : kF32, 0);
+  typename Elem<TX>::v8 xr[KS];
+  {
+    const int64_t row = min(row0 + c, rows - 1);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) xr[kk] = load8(x + row * x_stride + kk * 32 + 8 * g);
+  }
 #pragma unroll
   for (int n = 0; n < Tile::KPW; ++n) issue_one(lds1, 0, 0, n);
 #pragma unroll
   for (int n = 0; n < NL; ++n) issue_one(lds0, min(1, n_tiles - 1), 0, n);
+  // Nothing that uses a loaded value moves above the loads' issue: with DMA
+  // in flight, an early use would wait for every load.
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmem();
 
   // Row fragments (B operands of the assignment contraction), kept in VGPRs.
-  const float beta_raw = beta_ptr ? load_scalar(beta_ptr, beta_dtype, 0) : beta_value;
+  const float beta_raw = beta_ptr ? scalar_value(beta_bits, beta_dtype) : beta_value;
   const float beta = (flags & kRouteBetaIsLog) ? expf(fminf(fmaxf(beta_raw, kLogBetaMin), kLogBetaMax)) : beta_raw;
   // Logits -> log2-domain exponents.  Maxima are taken of raw logits, so a
   // negative beta is folded into the rows instead (exact).
@@ -144,12 +158,9 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
   const float sign = beta < 0.f ? -1.f : 1.f;
   k8 xf[KS];
   {
-    const int64_t row = row0 + c;
-    typename Elem<TX>::v8 xr[KS];
     float ss = 0.f;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      xr[kk] = row < rows ? load8(x + row * x_stride + kk * 32 + 8 * g) : zero8<TX>();
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float v = static_cast<float>(xr[kk][e]);
@@ -202,7 +213,6 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
     }
   };
 
-  wait_vmem();
   __syncthreads();
   f32x4 st_prev[2];
   logits(lds1, st_prev, std::false_type{}, nullptr, 0, 0);

@@ -528,6 +528,8 @@ def check_module_supported(config) -> None:
         raise NotImplementedError("backend='hip' supports grouped score widths up to 512")
     if config.model_dim not in SUPPORTED_WIDTHS:
         raise NotImplementedError(f"backend='hip' supports model_dim in {SUPPORTED_WIDTHS}")
+    if config.outer_maps > 64:
+        raise NotImplementedError("backend='hip' supports at most 64 outer maps")
 
 
 def own_bank_layout(bank, key_dtype: torch.dtype) -> RouteDictionary:

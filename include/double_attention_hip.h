@@ -135,7 +135,7 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  *   score_bound: 0, or an upper bound on |q . k| over all raw query/key rows
  *     (1 for L2-normalized rows).  With a bound, maps whose scaled bound fits
  *     the probability type skip the online-softmax rescaling (bf16 V only).
- * score_dim and value_dim must be 64, 128, 256 or 512.  Element types:
+ * maps <= 64.  score_dim and value_dim must be 64, 128, 256 or 512.  Element types:
  *   (qk_dtype, v_dtype) in {(F16, BF16), (F16, F16), (BF16, BF16)}; the output
  *   has v_dtype.  V^T padding tokens (length .. padded length - 1) must hold
  *   finite values.
