@@ -188,6 +188,12 @@ def main() -> None:
         raw_key = bank.raw_key.detach()
         raw_value = bank.raw_value.detach() if bank.raw_value is not None else None
 
+        variant = da.hip_ops.RouteVariant.of_config(config)
+        route_flags = (
+            _lib.DA_ROUTE_BETA_IS_LOG | _lib.DA_ROUTE_UNIT_KEYS | variant.flags()
+            | (_lib.DA_ROUTE_NORMALIZE_INPUT if config.normalize_routing_input else 0)
+            | (_lib.DA_ROUTE_NORMALIZE_OUTPUT if config.normalize_routing_output else 0)
+        )
         attn_flags = _lib.DA_ATTN_CAUSAL | _lib.DA_ATTN_SCALES_ARE_LOG | _lib.DA_ATTN_MIX
         attn_ws_bytes = lib.da_attention_workspace_bytes(batch, S, length, rp, d, attn_flags)
         attn_ws = torch.empty(attn_ws_bytes, dtype=torch.uint8, device=device) if attn_ws_bytes else None
@@ -202,10 +208,8 @@ def main() -> None:
                 qk.data_ptr(), vt.data_ptr(), vt.stride(0), tp, handle),
             "route": lambda: lib.da_dictionary_route(
                 qk.data_ptr(), rows, R, R, code, layout.key_t.data_ptr(), key_code, layout.value.data_ptr(), M,
-                p["log_beta"].data_ptr(), pdt, 0.0, config.eps,
-                _lib.DA_ROUTE_NORMALIZE_INPUT | _lib.DA_ROUTE_NORMALIZE_OUTPUT | _lib.DA_ROUTE_BETA_IS_LOG
-                | _lib.DA_ROUTE_UNIT_KEYS,
-                routed.data_ptr(), R, _lib.DA_F16, handle),
+                p["log_beta"].data_ptr(), pdt, 0.0, config.eps, route_flags, variant.silu_gain,
+                variant.logit_scale(R), routed.data_ptr(), R, _lib.DA_F16, handle),
             "attention": lambda: lib.da_routed_attention(
                 routed.data_ptr(), routed.data_ptr() + W * routed.element_size(), length * 2 * W, 2 * W,
                 rp if H > S else R, S // H if S > H else 1, rp, vt.data_ptr(), vt.stride(0),

@@ -48,9 +48,19 @@ int check_launch(const char* what) {
 constexpr int64_t kAlign = 256;
 int64_t align_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
+constexpr int kRouteFlagMask = DA_ROUTE_NORMALIZE_INPUT | DA_ROUTE_NORMALIZE_OUTPUT | DA_ROUTE_BETA_IS_LOG |
+                               DA_ROUTE_UNIT_KEYS | DA_ROUTE_SILU_LOGITS | DA_ROUTE_STANDARDIZE |
+                               DA_ROUTE_DIRECT_SILU;
+constexpr int kRouteVariantMask = DA_ROUTE_SILU_LOGITS | DA_ROUTE_STANDARDIZE | DA_ROUTE_DIRECT_SILU;
+
 int validate_route(const void* x, int64_t rows, int64_t R, int64_t xs, int x_dtype, const void* kt,
                    int key_dtype, const void* v, int64_t atoms, const void* beta, int beta_dtype,
-                   int flags, const void* out, int64_t os, int out_dtype) {
+                   int flags, float silu_gain, float logit_scale, const void* out, int64_t os, int out_dtype) {
+  if (flags & ~kRouteFlagMask) return fail(DA_ERR_INVALID_ARGUMENT, "route: unknown flag bits 0x%x", flags);
+  if ((flags & DA_ROUTE_DIRECT_SILU) && !(silu_gain > 0.f && std::isfinite(silu_gain)))
+    return fail(DA_ERR_INVALID_ARGUMENT, "route: silu_gain must be positive and finite");
+  if ((flags & DA_ROUTE_STANDARDIZE) && !(logit_scale > 0.f && std::isfinite(logit_scale)))
+    return fail(DA_ERR_INVALID_ARGUMENT, "route: logit_scale must be positive and finite");
   if (!half_dtype(x_dtype) || !half_dtype(key_dtype) || !half_dtype(out_dtype))
     return fail(DA_ERR_INVALID_ARGUMENT, "route: element types must be DA_F16 or DA_BF16");
   if (key_dtype != DA_F16 && key_dtype != x_dtype)
@@ -104,7 +114,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 7; }
+int da_abi_version(void) { return 8; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -132,15 +142,15 @@ int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_
 int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_t x_row_stride,
                         int x_dtype, const void* key_t, int key_dtype, const void* value,
                         int64_t atoms, const void* beta, int beta_dtype, float beta_value,
-                        float eps, int flags, void* out, int64_t out_row_stride, int out_dtype,
-                        da_stream_t stream) {
+                        float eps, int flags, float silu_gain, float logit_scale, void* out,
+                        int64_t out_row_stride, int out_dtype, da_stream_t stream) {
   int rc = validate_route(x, rows, routing_dim, x_row_stride, x_dtype, key_t, key_dtype, value, atoms,
-                          beta, beta_dtype, flags, out, out_row_stride, out_dtype);
+                          beta, beta_dtype, flags, silu_gain, logit_scale, out, out_row_stride, out_dtype);
   if (rc) return rc;
   if (rows == 0) return ok();
   da::RouteArgs a{x, rows, x_row_stride, x_dtype, static_cast<int>(routing_dim), key_t, key_dtype,
-                  value, static_cast<int>(atoms), beta, beta_dtype, beta_value, eps, flags, out,
-                  out_row_stride, out_dtype};
+                  value, static_cast<int>(atoms), beta, beta_dtype, beta_value, eps, flags, silu_gain,
+                  logit_scale, out, out_row_stride, out_dtype};
   da::launch_dictionary_route(a, reinterpret_cast<hipStream_t>(stream));
   return check_launch("route");
 }
@@ -325,8 +335,12 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   int rflags = da::kRouteBetaIsLog | da::kRouteUnitKeys;   // the bank comes from da_dictionary_normalize
   if (norm_in) rflags |= da::kRouteNormalizeInput;
   if (a->flags & DA_SDA_NORMALIZE_OUTPUT) rflags |= da::kRouteNormalizeOutput;
+  if (a->route_variant & ~kRouteVariantMask)
+    return fail(DA_ERR_INVALID_ARGUMENT, "forward: route_variant holds bits other than DA_ROUTE_SILU_LOGITS, "
+                "DA_ROUTE_STANDARDIZE and DA_ROUTE_DIRECT_SILU");
+  rflags |= a->route_variant;
   rc = validate_route(routed, B * T * 2 * H, R, R, a->dtype, a->key_t, key_dtype, a->value, a->atoms,
-                      a->log_beta, a->param_dtype, rflags, routed, R, DA_F16);
+                      a->log_beta, a->param_dtype, rflags, a->silu_gain, a->logit_scale, routed, R, DA_F16);
   if (rc) return rc;
   const int64_t ot = concat ? S * d : d;
   rc = validate_attention(routed, static_cast<char*>(routed) + W * 2, T * 2 * W, 2 * W,
@@ -365,7 +379,7 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   //    combinations of unit atoms without output normalization).
   da::RouteArgs ra{routed, B * T * 2 * H, R, a->dtype, static_cast<int>(R), a->key_t, key_dtype,
                    a->value, static_cast<int>(a->atoms), a->log_beta, a->param_dtype, 0.f, a->eps,
-                   rflags, routed, R, DA_F16};
+                   rflags, a->silu_gain, a->logit_scale, routed, R, DA_F16};
   da::launch_dictionary_route(ra, s);
   // 3. Outer attention over the S maps, mixed (or concatenated).
   da::AttentionArgs at;

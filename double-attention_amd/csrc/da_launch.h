@@ -22,6 +22,9 @@ enum : int {
   kRouteNormalizeOutput = 2,
   kRouteBetaIsLog = 4,
   kRouteUnitKeys = 8,
+  kRouteSiluLogits = 16,    // logits -> 2 SiLU(logits)                        (ops.py:41-44)
+  kRouteStandardize = 32,   // logits -> (logits - mean) / std * logit_scale   (ops.py:47-55)
+  kRouteDirectSilu = 64,    // weights = (2/g) SiLU(g logits), no softmax      (ops.py:58-59)
 };
 
 // Attention flags.
@@ -48,6 +51,8 @@ struct RouteArgs {
   float beta_value;
   float eps;
   int flags;
+  float silu_gain;      // g of kRouteDirectSilu
+  float logit_scale;    // scale of kRouteStandardize
   void* out;
   int64_t out_stride;
   int out_dtype;

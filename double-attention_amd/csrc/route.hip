@@ -59,11 +59,17 @@ struct RouteTile {
 // the odd atom tiles (the padded atom count is even in tiles), each with its
 // own share of every stage; at the end the odd one hands its accumulators to
 // the even one through LDS.  Few rows then still spread over every CU.
-template <typename TX, typename TK, typename TO, int R, int SUB>
+//
+// VAR builds the variants of ops.py:41-61 in: 2 SiLU logits, standardized
+// logits (a first pass over all atom tiles gathers each row's logit mean and
+// variance, then the pipeline runs again) and the direct-SiLU assignment,
+// whose weights need no softmax.
+template <typename TX, typename TK, typename TO, int R, int SUB, bool VAR>
 __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) void route_kernel(
     const TX* x, int64_t rows, int64_t x_stride, const TK* __restrict__ key_t,
     const _Float16* __restrict__ value, int M, int Mp, const void* __restrict__ beta_ptr,
-    int beta_dtype, float beta_value, float eps, int flags, TO* out, int64_t out_stride) {
+    int beta_dtype, float beta_value, float eps, int flags, float silu_gain, float logit_scale, TO* out,
+    int64_t out_stride) {
   // x and out may alias (in-place routing): every row is read into VGPRs by
   // its own wave before that wave writes it.
   static_assert(SUB == 1 || SUB == 2, "one or two sub-streams");
@@ -156,6 +162,14 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
   // negative beta is folded into the rows instead (exact).
   const float scale = fabsf(beta) * kLog2e;
   const float sign = beta < 0.f ? -1.f : 1.f;
+  // Variants: the sign of beta folds into the rows only where the logits stay
+  // linear in them; after a SiLU activation it multiplies the logits, and the
+  // direct-SiLU assignment does not use beta.
+  const bool silu_logits = VAR && (flags & kRouteSiluLogits);
+  const bool standardize = VAR && (flags & kRouteStandardize);
+  const bool direct = VAR && (flags & kRouteDirectSilu);
+  const float row_sign = silu_logits || direct ? 1.f : sign;
+  const float post_sign = silu_logits && !direct ? sign : 1.f;
   k8 xf[KS];
   {
     float ss = 0.f;
@@ -170,7 +184,7 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
     ss = group_sum(ss);
     // With input normalization the unit row is rounded once to TK; otherwise
     // TK == TX and the raw row passes through unchanged.
-    const float inv_norm = sign * ((flags & kRouteNormalizeInput) ? 1.f / fmaxf(sqrtf(ss), eps) : 1.f);
+    const float inv_norm = row_sign * ((flags & kRouteNormalizeInput) ? 1.f / fmaxf(sqrtf(ss), eps) : 1.f);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
@@ -217,28 +231,107 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
   f32x4 st_prev[2];
   logits(lds1, st_prev, std::false_type{}, nullptr, 0, 0);
 
-  // FIXED: unit rows and unit key atoms bound every logit by |beta|, so the
-  // exponents use the fixed reference (|beta| - kP16Lift) log2e: weights stay
-  // in fp16's normal range and the accumulators are never rescaled.
-  // Otherwise the lazy online rescale runs.
-  auto step = [&](auto fixed, int t) {
-    constexpr bool FIXED = decltype(fixed)::value;
+  // 2 SiLU(l) = 2 l / (1 + e^-l).
+  auto silu2 = [](float v) { return 2.f * v / (1.f + __builtin_amdgcn_exp2f(-kLog2e * v)); };
+  // Standardized logits: (l - mu) * cstd, cstd = logit_scale / sqrt(var + eps).
+  float mu = 0.f, cstd = 1.f;
+  if (standardize) {
+    // First pass: the same pipeline over every atom tile, gathering the sum
+    // and sum of squares of each row's (activated) logits over the M atoms.
+    float s1 = 0.f, s2 = 0.f;
+    for (int t = 0; t < n_tiles; ++t) {
+      char* cur = (t & 1) ? lds1 : lds0;
+      char* nxt = (t & 1) ? lds0 : lds1;
+      const int j0 = tile_of(t) * kRouteAT;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = silu_logits ? silu2(st_prev[kb][i]) : st_prev[kb][i];
+          if (j0 + 8 * g + 4 * kb + i < M) {
+            s1 += v;
+            s2 += v * v;
+          }
+        }
+      wait_vmem();
+      __syncthreads();
+      logits(cur, st_prev, std::true_type{}, nxt, min(t + 2, n_tiles - 1), min(t + 1, n_tiles - 1));
+    }
+    s1 = group_sum(s1);
+    s2 = group_sum(s2);
+    wait_vmem();
+    __syncthreads();
+    if constexpr (SUB == 2) {
+      // Each sub-stream saw half the atom tiles: exchange the partial sums.
+      float* xs = reinterpret_cast<float*>(lds_all) + (sub * NQW + wave) * 128;
+      xs[lane * 2] = s1;
+      xs[lane * 2 + 1] = s2;
+      __syncthreads();
+      const float* other = reinterpret_cast<const float*>(lds_all) + ((1 - sub) * NQW + wave) * 128;
+      s1 += other[lane * 2];
+      s2 += other[lane * 2 + 1];
+      __syncthreads();
+    }
+    mu = s1 / static_cast<float>(M);
+    const float var = fmaxf(s2 / static_cast<float>(M) - mu * mu, 0.f);
+    cstd = logit_scale / sqrtf(var + eps);
+    // Second pass: the pipeline restarts at tile 0.
+#pragma unroll
+    for (int n = 0; n < Tile::KPW; ++n) issue_one(lds1, 0, 0, n);
+#pragma unroll
+    for (int n = 0; n < NL; ++n) issue_one(lds0, min(1, n_tiles - 1), 0, n);
+    wait_vmem();
+    __syncthreads();
+    logits(lds1, st_prev, std::false_type{}, nullptr, 0, 0);
+  }
+
+  // Step modes.  kFixed: every logit is bounded by `bound` (unit rows and unit
+  // key atoms, or standardized logits), so the exponents use the fixed
+  // reference (bound |beta| - kP16Lift) log2e: weights stay in fp16's normal
+  // range and the accumulators are never rescaled.  kLazy: the lazy online
+  // rescale.  kDirect: direct-SiLU weights.
+  constexpr int kLazy = 0, kFixed = 1, kDirect = 2;
+  float bound = 1.f;
+  bool bounded = (flags & kRouteNormalizeInput) && (flags & kRouteUnitKeys);
+  if constexpr (VAR) {
+    if (silu_logits) bound = 1.4621172f;   // max |2 SiLU(l)| over |l| <= 1
+    if (standardize) {
+      // |l - mu| <= sqrt(M - 1) * std for every atom.
+      bound = sqrtf(static_cast<float>(M - 1)) * logit_scale;
+      bounded = true;
+    }
+  }
+  auto step = [&](auto mode, int t) {
+    constexpr int MODE = decltype(mode)::value;
     char* cur = (t & 1) ? lds1 : lds0;
     char* nxt = (t & 1) ? lds0 : lds1;
     const int j0 = tile_of(t) * kRouteAT;
+    if constexpr (VAR) {
+      if (silu_logits || standardize || post_sign != 1.f) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v = st_prev[kb][i];
+            if (silu_logits) v = silu2(v);
+            if (standardize) v = (v - mu) * cstd;
+            st_prev[kb][i] = v * post_sign;
+          }
+      }
+    }
     // Lane (c, g) holds atoms j0 + 8g + 4kb + i of row c; only the last tile
-    // can hold padding atoms.
+    // can hold padding atoms (weight zero).
     if (j0 + kRouteAT > M) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (j0 + 8 * g + 4 * kb + i >= M) st_prev[kb][i] = -INFINITY;
+          if (j0 + 8 * g + 4 * kb + i >= M) st_prev[kb][i] = MODE == kDirect ? 0.f : -INFINITY;
     }
-    float m_use;
-    if constexpr (FIXED) {
-      m_use = kP16Lift - scale;
-    } else {
+    float m_use = 0.f;
+    if constexpr (MODE == kFixed) {
+      m_use = kP16Lift - bound * scale;
+    } else if constexpr (MODE == kLazy) {
       const float lmax = fmaxf(fmaxf(fmaxf(st_prev[0][0], st_prev[0][1]), fmaxf(st_prev[0][2], st_prev[0][3])),
                                fmaxf(fmaxf(st_prev[1][0], st_prev[1][1]), fmaxf(st_prev[1][2], st_prev[1][3])));
       lazy_rescale<RB>(lmax, scale, m_run, l_part, acc);
@@ -251,16 +344,27 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
     f32x4 st_new[2];
     logits(cur, st_new, std::true_type{}, nxt, min(t + 2, n_tiles - 1), min(t + 1, n_tiles - 1));
 
-    float psum = 0.f;
+    if constexpr (MODE == kDirect) {
+      // (2/g) SiLU(g l) = 2 l / (1 + e^(-g l)).
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(st_prev[kb][i], scale, m_use));
-        st_prev[kb][i] = pr;
-        psum += pr;
-      }
-    l_part += psum;
+        for (int i = 0; i < 4; ++i) {
+          const float v = st_prev[kb][i];
+          st_prev[kb][i] = 2.f * v / (1.f + __builtin_amdgcn_exp2f(-kLog2e * silu_gain * v));
+        }
+    } else {
+      float psum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(st_prev[kb][i], scale, m_use));
+          st_prev[kb][i] = pr;
+          psum += pr;
+        }
+      l_part += psum;
+    }
     const f16x8 pb = pack_blocked<_Float16>(st_prev[0], st_prev[1]);   // atoms j0 + 8g + e
 
     // O^T += Dv(t) P^T(t).
@@ -278,11 +382,13 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
     st_prev[1] = st_new[1];
   };
 
-  const bool fixed = (flags & kRouteNormalizeInput) && (flags & kRouteUnitKeys) && 2.f * scale <= 2.f * kP16Lift;
-  if (fixed) {
-    for (int t = 0; t < n_tiles; ++t) step(std::true_type{}, t);
+  const bool fixed = !direct && bounded && 2.f * bound * scale <= 2.f * kP16Lift;
+  if (direct) {
+    for (int t = 0; t < n_tiles; ++t) step(std::integral_constant<int, kDirect>{}, t);
+  } else if (fixed) {
+    for (int t = 0; t < n_tiles; ++t) step(std::integral_constant<int, kFixed>{}, t);
   } else {
-    for (int t = 0; t < n_tiles; ++t) step(std::false_type{}, t);
+    for (int t = 0; t < n_tiles; ++t) step(std::integral_constant<int, kLazy>{}, t);
   }
 
   if constexpr (SUB == 2) {
@@ -305,7 +411,7 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
     const float m1 = xch[RB * 256 + lane * 2];
     const float l1 = xch[RB * 256 + lane * 2 + 1];
     float f0 = 1.f, f1 = 1.f;
-    if (!fixed) {
+    if (!fixed && !direct) {
       const float M = fmaxf(m_run, m1);
       f0 = m_run == -INFINITY ? 0.f : exp2f(m_run - M);
       f1 = m1 == -INFINITY ? 0.f : exp2f(m1 - M);
@@ -314,8 +420,8 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
     for (int rb = 0; rb < RB; ++rb) acc[rb] = acc[rb] * f0 + *reinterpret_cast<const f32x4*>(xch + (rb * 64 + lane) * 4) * f1;
     l_part = l_part * f0 + l1 * f1;
   }
-  // r = O / l; z = r / max(||r||, eps).
-  const float inv_l = 1.f / group_sum(l_part);
+  // r = O / l (direct-SiLU: r = O); z = r / max(||r||, eps).
+  const float inv_l = direct ? 1.f : 1.f / group_sum(l_part);
   float out_scale = inv_l;
   if (flags & kRouteNormalizeOutput) {
     float rs = 0.f;
@@ -345,15 +451,24 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
   wait_vmem();
 }
 
-template <typename TX, typename TK, typename TO, int R, int SUB>
-static void launch_route_s(const RouteArgs& a, hipStream_t s) {
+template <typename TX, typename TK, typename TO, int R, int SUB, bool VAR>
+static void launch_route_v(const RouteArgs& a, hipStream_t s) {
   constexpr int rows_per_block = kRouteRows / SUB;
   const int64_t blocks = (a.rows + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((route_kernel<TX, TK, TO, R, SUB>), dim3(static_cast<unsigned>(blocks)), dim3(kRouteWaves * 64),
-                     0, s, static_cast<const TX*>(a.x), a.rows, a.x_stride, static_cast<const TK*>(a.key_t),
-                     static_cast<const _Float16*>(a.value), a.M, static_cast<int>(round_up(a.M, kAtomPad)),
-                     a.beta_ptr, a.beta_dtype, a.beta_value, a.eps, a.flags, static_cast<TO*>(a.out),
-                     a.out_stride);
+  hipLaunchKernelGGL((route_kernel<TX, TK, TO, R, SUB, VAR>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kRouteWaves * 64), 0, s, static_cast<const TX*>(a.x), a.rows, a.x_stride,
+                     static_cast<const TK*>(a.key_t), static_cast<const _Float16*>(a.value), a.M,
+                     static_cast<int>(round_up(a.M, kAtomPad)), a.beta_ptr, a.beta_dtype, a.beta_value, a.eps,
+                     a.flags, a.silu_gain, a.logit_scale, static_cast<TO*>(a.out), a.out_stride);
+}
+
+template <typename TX, typename TK, typename TO, int R, int SUB>
+static void launch_route_s(const RouteArgs& a, hipStream_t s) {
+  if (a.flags & (kRouteSiluLogits | kRouteStandardize | kRouteDirectSilu)) {
+    launch_route_v<TX, TK, TO, R, SUB, true>(a, s);
+  } else {
+    launch_route_v<TX, TK, TO, R, SUB, false>(a, s);
+  }
 }
 
 // Rows that do not give every CU (MI355X: 256) a workgroup of four row waves

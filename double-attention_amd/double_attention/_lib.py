@@ -21,6 +21,9 @@ DA_ROUTE_NORMALIZE_INPUT = 1
 DA_ROUTE_NORMALIZE_OUTPUT = 2
 DA_ROUTE_BETA_IS_LOG = 4
 DA_ROUTE_UNIT_KEYS = 8
+DA_ROUTE_SILU_LOGITS = 16
+DA_ROUTE_STANDARDIZE = 32
+DA_ROUTE_DIRECT_SILU = 64
 
 DA_ATTN_CAUSAL = 1
 DA_ATTN_SCALES_ARE_LOG = 2
@@ -39,7 +42,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -79,6 +82,9 @@ class SdaForwardArgs(ctypes.Structure):
         ("raw_key", _vp),
         ("raw_value", _vp),
         ("raw_dtype", _i32),
+        ("route_variant", _i32),
+        ("silu_gain", _f32),
+        ("logit_scale", _f32),
     ]
 
 
@@ -95,6 +101,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i64, _i64, _i64, _i32,  # x, rows, routing_dim, row pitch, x dtype
             _vp, _i32, _vp, _i64,  # key_t, key dtype, value, atoms
             _vp, _i32, _f32, _f32, _i32,  # beta, beta dtype, beta value, eps, flags
+            _f32, _f32,  # silu gain, logit scale
             _vp, _i64, _i32, _vp,  # out, out pitch, out dtype, stream
         ],
     ),

@@ -190,14 +190,37 @@ def route_layout(dictionary_key: Tensor, dictionary_value: Tensor, key_dtype: to
 # --------------------------------------------------------------------------
 
 
-def _check_route_variant(
-    silu_logits: bool, direct_silu: bool, standardize_logits: bool
-) -> None:
-    if silu_logits or direct_silu or standardize_logits:
-        raise NotImplementedError(
-            "the HIP route kernel implements the identity activation with softmax "
-            "assignment; SiLU logits, standardized logits and direct SiLU assignment "
-            "are not implemented on this backend"
+class RouteVariant(NamedTuple):
+    """Activation, standardization and assignment of ``ops.py:41-59``."""
+
+    silu_logits: bool = False
+    direct_silu: bool = False
+    silu_gain: float = 1.0
+    standardize_logits: bool = False
+    standardized_logit_scale: float | None = None
+
+    def flags(self) -> int:
+        return (
+            (_lib.DA_ROUTE_SILU_LOGITS if self.silu_logits else 0)
+            | (_lib.DA_ROUTE_STANDARDIZE if self.standardize_logits else 0)
+            | (_lib.DA_ROUTE_DIRECT_SILU if self.direct_silu else 0)
+        )
+
+    def logit_scale(self, routing_dim: int) -> float:
+        """``standardized_logit_scale``, or ``routing_dim ** -0.5`` (ops.py:50-54)."""
+
+        if self.standardized_logit_scale is None:
+            return routing_dim ** -0.5
+        return float(self.standardized_logit_scale)
+
+    @classmethod
+    def of_config(cls, config) -> "RouteVariant":
+        return cls(
+            silu_logits=config.dictionary_activation == "silu",
+            direct_silu=config.dictionary_assignment == "silu",
+            silu_gain=float(config.dictionary_silu_gain),
+            standardize_logits=bool(config.standardize_dictionary_logits),
+            standardized_logit_scale=config.standardized_logit_scale,
         )
 
 
@@ -208,6 +231,7 @@ def _route_forward(
     eps: float,
     normalize_input: bool,
     normalize_output: bool,
+    variant: RouteVariant = RouteVariant(),
 ) -> Tensor:
     routing_dim = x.shape[-1]
     if routing_dim != layout.key_t.shape[1]:
@@ -224,6 +248,7 @@ def _route_forward(
         (_lib.DA_ROUTE_NORMALIZE_INPUT if normalize_input else 0)
         | (_lib.DA_ROUTE_NORMALIZE_OUTPUT if normalize_output else 0)
         | (_lib.DA_ROUTE_UNIT_KEYS if layout.unit else 0)
+        | variant.flags()
     )
     if isinstance(beta, Tensor):
         if beta.numel() != 1:
@@ -251,6 +276,8 @@ def _route_forward(
             beta_value,
             float(eps),
             flags,
+            float(variant.silu_gain),
+            float(variant.logit_scale(routing_dim)),
             out.data_ptr(),
             routing_dim,
             _half_code(x.dtype),
@@ -264,14 +291,15 @@ def _route_forward(
 
 class _RouteFunction(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output):  # type: ignore[override]
+    def forward(ctx, x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, variant):  # type: ignore[override]
         layout = route_layout(dictionary_key, dictionary_value, route_key_dtype(normalize_input, x.dtype))
         ctx.save_for_backward(x, dictionary_key, dictionary_value, *(beta,) if isinstance(beta, Tensor) else ())
         ctx.beta_is_tensor = isinstance(beta, Tensor)
         ctx.beta = None if ctx.beta_is_tensor else beta
         ctx.eps = eps
         ctx.flags = (normalize_input, normalize_output)
-        return _route_forward(x, layout, beta, eps, normalize_input, normalize_output)
+        ctx.variant = variant
+        return _route_forward(x, layout, beta, eps, normalize_input, normalize_output, variant)
 
     @staticmethod
     def backward(ctx, grad):  # type: ignore[override]
@@ -281,8 +309,14 @@ class _RouteFunction(torch.autograd.Function):
         with torch.enable_grad():
             inputs = [t.detach().requires_grad_(t.requires_grad) for t in (x, dk, dv)]
             beta_in = beta.detach().requires_grad_(beta.requires_grad) if ctx.beta_is_tensor else beta
+            v = ctx.variant
             out = dictionary_route_reference(
                 inputs[0], inputs[1], inputs[2], beta_in, ctx.eps,
+                activation="silu" if v.silu_logits else "identity",
+                assignment="silu" if v.direct_silu else "softmax",
+                silu_gain=v.silu_gain,
+                standardize_logits=v.standardize_logits,
+                standardized_logit_scale=v.standardized_logit_scale,
                 normalize_input=ctx.flags[0], normalize_output=ctx.flags[1],
             )
             wrt = [t for t in inputs if t.requires_grad]
@@ -292,7 +326,7 @@ class _RouteFunction(torch.autograd.Function):
         it = iter(grads)
         result = [next(it) if t.requires_grad else None for t in inputs]
         beta_grad = next(it) if ctx.beta_is_tensor and beta_in.requires_grad else None
-        return (*result, beta_grad, None, None, None)
+        return (*result, beta_grad, None, None, None, None)
 
 
 def dictionary_route_hip(
@@ -315,8 +349,11 @@ def dictionary_route_hip(
     ``dictionary_value`` are normalized ``[R, M]`` banks in the input dtype.
     """
 
-    del silu_gain, standardized_logit_scale
-    _check_route_variant(silu_logits, direct_silu, standardize_logits)
+    variant = RouteVariant(silu_logits, direct_silu, float(silu_gain), standardize_logits, standardized_logit_scale)
+    if direct_silu and not silu_gain > 0:
+        raise ValueError("silu_gain must be positive")
+    if standardize_logits and standardized_logit_scale is not None and not standardized_logit_scale > 0:
+        raise ValueError("standardized_logit_scale must be positive when provided")
     _require_cuda(input, dictionary_key, dictionary_value)
     _half_code(input.dtype)
     tagged = getattr(dictionary_key, "_da_route_layout", None) is not None
@@ -326,9 +363,11 @@ def dictionary_route_hip(
         t.requires_grad for t in (input, dictionary_key, dictionary_value, *((beta,) if isinstance(beta, Tensor) else ()))
     )
     if needs_grad:
-        return _RouteFunction.apply(input, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output)
+        return _RouteFunction.apply(
+            input, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, variant
+        )
     layout = route_layout(dictionary_key, dictionary_value, route_key_dtype(normalize_input, input.dtype))
-    return _route_forward(input, layout, beta, eps, normalize_input, normalize_output)
+    return _route_forward(input, layout, beta, eps, normalize_input, normalize_output, variant)
 
 
 # --------------------------------------------------------------------------
@@ -513,14 +552,14 @@ class HipForwardResult(NamedTuple):
 def check_module_supported(config) -> None:
     """Raise ``NotImplementedError`` for variants the HIP kernels do not cover."""
 
-    if config.dictionary_activation != "identity" or config.dictionary_assignment != "softmax":
+    if config.dictionary_activation not in ("identity", "silu") or config.dictionary_assignment not in (
+        "softmax",
+        "silu",
+    ):
         raise NotImplementedError(
-            "backend='hip' implements identity dictionary activation with softmax "
-            f"assignment; got activation={config.dictionary_activation!r}, "
+            f"backend='hip' has no kernel for activation={config.dictionary_activation!r}, "
             f"assignment={config.dictionary_assignment!r}"
         )
-    if config.standardize_dictionary_logits:
-        raise NotImplementedError("backend='hip' does not implement standardized dictionary logits")
     if config.routing_dim not in SUPPORTED_WIDTHS:
         raise NotImplementedError(f"backend='hip' supports routing_dim in {SUPPORTED_WIDTHS}")
     group = config.qk_branches // config.outer_maps if config.qk_branches > config.outer_maps else 1
@@ -606,6 +645,10 @@ def shared_dictionary_attention_hip(
         dtype_code(scalar_dtype), code, float(config.eps), flags,
         workspace.data_ptr(), ws_bytes, out.data_ptr(),
     )
+    variant = RouteVariant.of_config(config)
+    args.route_variant = variant.flags()
+    args.silu_gain = variant.silu_gain
+    args.logit_scale = variant.logit_scale(config.routing_dim)
     if raw_bank is not None:
         raw_key = raw_bank[0].detach().contiguous()
         raw_value = None if raw_bank[1] is None else raw_bank[1].detach().to(raw_key.dtype).contiguous()
@@ -622,6 +665,7 @@ def shared_dictionary_attention_hip(
 
 __all__ = [
     "RouteDictionary",
+    "RouteVariant",
     "dictionary_normalize_hip",
     "dictionary_route_hip",
     "linear_hip",

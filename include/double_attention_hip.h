@@ -56,6 +56,11 @@ typedef struct ihipStream_t* da_stream_t; /* hipStream_t; NULL = default stream 
 #define DA_ROUTE_UNIT_KEYS 8        /* key atoms have L2 norm <= 1 (a normalized bank): with
                                        DA_ROUTE_NORMALIZE_INPUT every logit is bounded by |beta|,
                                        which lets the kernel skip online-softmax rescaling */
+#define DA_ROUTE_SILU_LOGITS 16     /* logits -> 2 SiLU(logits)           (activation "silu", ops.py:41-44) */
+#define DA_ROUTE_STANDARDIZE 32     /* logits -> (logits - mean) / sqrt(var + eps) * logit_scale over the
+                                       atoms (standardize_logits, ops.py:47-55): two passes */
+#define DA_ROUTE_DIRECT_SILU 64     /* weights = (2/silu_gain) SiLU(silu_gain logits) instead of
+                                       softmax(beta logits) (assignment "silu", ops.py:56-59) */
 
 /* da_routed_attention flags */
 #define DA_ATTN_CAUSAL 1
@@ -98,14 +103,18 @@ int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_
                             int key_dtype, void* value, void* value_rows, da_stream_t stream);
 
 /*
- * Fused dictionary route (ops.py:16-62 with identity activation and softmax
- * assignment), for any number of rows:
- *   z = N_out( sum_j softmax_j(beta <N_in(x), Dk_j>) Dv_j )
+ * Fused dictionary route (ops.py:16-62), for any number of rows:
+ *   z = N_out( sum_j w_j Dv_j ),  w = softmax(beta l) or (2/g) SiLU(g l),
+ *   l_j = Std(Act(<N_in(x), Dk_j>)) with the optional 2 SiLU activation and
+ *   standardization over the atoms (the DA_ROUTE_* variant flags).
  *   x:   rows x routing_dim, row pitch x_row_stride (elements), x_dtype
  *   key_t (key_dtype), value (fp16): the layouts of da_dictionary_normalize.
  *        key_dtype is DA_F16, or x_dtype; without DA_ROUTE_NORMALIZE_INPUT it
  *        must equal x_dtype (raw rows are not range-limited).
- *   beta: device scalar of beta_dtype, or NULL to use beta_value
+ *   beta: device scalar of beta_dtype, or NULL to use beta_value (unused by
+ *        DA_ROUTE_DIRECT_SILU)
+ *   silu_gain: g of DA_ROUTE_DIRECT_SILU (> 0); logit_scale: the scale of
+ *        DA_ROUTE_STANDARDIZE (> 0; the reference's default is routing_dim^-1/2)
  *   out: rows x routing_dim, row pitch out_row_stride, out_dtype (DA_F16 or
  *        x_dtype); may alias x when the pitches match (each row is read
  *        completely before it is written).  A DA_F16 x needs DA_F16 keys and out.
@@ -113,8 +122,8 @@ int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_
 int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_t x_row_stride,
                         int x_dtype, const void* key_t, int key_dtype, const void* value,
                         int64_t atoms, const void* beta, int beta_dtype, float beta_value,
-                        float eps, int flags, void* out, int64_t out_row_stride, int out_dtype,
-                        da_stream_t stream);
+                        float eps, int flags, float silu_gain, float logit_scale, void* out,
+                        int64_t out_row_stride, int out_dtype, da_stream_t stream);
 
 /*
  * Flash outer attention over `maps` score maps (ops.py:65-93) with the map
@@ -206,6 +215,12 @@ typedef struct da_sda_forward_args {
   const void* raw_key;
   const void* raw_value;
   int raw_dtype;
+  /* Route variants: DA_ROUTE_SILU_LOGITS | DA_ROUTE_STANDARDIZE |
+   * DA_ROUTE_DIRECT_SILU bits (0 = identity activation, softmax assignment),
+   * with their silu_gain and logit_scale as for da_dictionary_route. */
+  int route_variant;
+  float silu_gain;
+  float logit_scale;
 } da_sda_forward_args;
 
 /* Workspace layout (byte offsets, each 256-aligned):

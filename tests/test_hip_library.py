@@ -62,6 +62,9 @@ def _fake(addr: int = 1 << 20) -> int:
         ({"x": 0}, -1, "null pointer"),
         ({"x": (1 << 20) + 2}, -3, "16-byte aligned"),
         ({"atoms": 0}, -1, "rows/atoms"),
+        ({"flags": 3 | 128}, -1, "unknown flag bits"),
+        ({"flags": 3 | lib.DA_ROUTE_DIRECT_SILU, "silu_gain": 0.0}, -1, "silu_gain"),
+        ({"flags": 3 | lib.DA_ROUTE_STANDARDIZE, "logit_scale": float("inf")}, -1, "logit_scale"),
     ],
 )
 def test_route_rejects_bad_arguments_before_launch(kwargs, code, pattern) -> None:
@@ -70,6 +73,7 @@ def test_route_rejects_bad_arguments_before_launch(kwargs, code, pattern) -> Non
         x=_fake(), rows=16, routing_dim=128, x_row_stride=128, x_dtype=lib.DA_BF16,
         key_t=_fake(), key_dtype=lib.DA_F16, value=_fake(), atoms=512,
         beta=None, beta_dtype=lib.DA_F32, beta_value=4.0, eps=1e-6, flags=3,
+        silu_gain=1.0, logit_scale=0.0625,
         out=_fake(), out_row_stride=128, out_dtype=lib.DA_F16, stream=None,
     )
     args.update(kwargs)

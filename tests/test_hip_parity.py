@@ -188,6 +188,62 @@ def test_route_zero_rows_and_empty() -> None:
     assert empty.shape == (0, 128)
 
 
+# Route variants of ops.py:41-59: (silu logits, standardize, logit scale,
+# direct-SiLU assignment, gain).  Row counts and widths cover both sub-stream
+# shapes (rows under 256 workgroups' worth and R <= 256: two sub-streams; R =
+# 512 or many rows: one), the fixed-reference softmax (unit rows and keys, or
+# standardized logits) and the online one (raw rows, or a wide logit range).
+ROUTE_VARIANTS = {
+    "silu": (True, False, None, False, 1.0),
+    "silu-std": (True, True, None, False, 1.0),
+    "silu-std-t1": (True, True, 0.25, False, 1.0),
+    "std": (False, True, None, False, 1.0),
+    "direct-g1": (False, False, None, True, 1.0),
+    "direct-g4": (False, False, None, True, 4.0),
+    "silu-std-direct": (True, True, 0.5, True, 2.0),
+}
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("variant", "normalize_input", "normalize_output", "routing_dim", "atoms", "rows", "beta"), [
+    ("silu", True, True, 256, 512, 1000, 4.0),
+    ("silu", False, True, 64, 100, 65, 4.0),
+    ("silu", True, False, 128, 300, 20000, -3.0),      # negative beta: sign after the activation
+    ("silu-std", False, True, 256, 512, 777, 4.0),
+    ("silu-std", False, True, 512, 1536, 999, 4.0 * 2 ** 0.5),
+    ("silu-std-t1", False, True, 256, 512, 4000, 4.0),
+    ("std", True, True, 128, 256, 20000, 4.0),
+    ("std", False, False, 64, 77, 33, -4.0),
+    ("direct-g1", True, True, 256, 512, 300, 4.0),
+    ("direct-g4", True, True, 128, 300, 20000, 4.0),
+    ("direct-g4", False, False, 512, 700, 129, 4.0),
+    ("silu-std-direct", True, True, 128, 256, 4000, 4.0),
+])
+def test_route_variants(dtype, variant, normalize_input, normalize_output, routing_dim, atoms, rows, beta) -> None:
+    device = _device()
+    silu, std, scale, direct, gain = ROUTE_VARIANTS[variant]
+    g = torch.Generator().manual_seed(routing_dim + atoms + rows)
+    x = torch.randn(rows, routing_dim, generator=g).to(device, dtype)
+    dk = unit_columns(routing_dim, atoms, dtype, device, 11)
+    dv = unit_columns(routing_dim, atoms, dtype, device, 12)
+    out = da.dictionary_route_hip(
+        x, dk, dv, torch.tensor(beta, device=device), 1e-6, silu_logits=silu, direct_silu=direct, silu_gain=gain,
+        standardize_logits=std, standardized_logit_scale=scale,
+        normalize_input=normalize_input, normalize_output=normalize_output,
+    )
+    expected = oracle.dictionary_route(
+        np32(x), np32(dk), np32(dv), beta, 1e-6, activation="silu" if silu else "identity",
+        assignment="silu" if direct else "softmax", silu_gain=gain, standardize_logits=std,
+        standardized_logit_scale=scale, normalize_input=normalize_input, normalize_output=normalize_output,
+    )
+    # Without the output normalization the rows keep their scale (direct-SiLU
+    # sums of up to M weighted atoms): the absolute bar scales with it.
+    scale_of = max(1.0, float(np.abs(expected).max()))
+    assert_parity(out, expected, REL_L2, MAX_ABS * scale_of,
+                  label=f"route {variant} in{int(normalize_input)} out{int(normalize_output)} R{routing_dim} "
+                        f"M{atoms} rows{rows} beta{beta} {dtype}")
+
+
 # ---------------------------------------------------------------- outer attention
 
 
@@ -327,6 +383,17 @@ def test_module_variants_odd_shapes(preset, overrides) -> None:
     run_module_case(preset, (1, 1, 512), seed=4, relative_to_torch=relative, **overrides)
 
 
+@pytest.mark.parametrize("preset", [
+    "a1-silu", "a1-silu-logitnorm", "a1-silu-logitnorm-t1", "a1-no-softmax", "a1-no-softmax-g4",
+])
+def test_module_route_variant_presets(preset) -> None:
+    # The presets whose route uses SiLU logits, standardized logits or the
+    # direct-SiLU assignment; the logit-norm ones route raw rows.
+    relative = not da.experiment_config(preset).normalize_routing_input
+    run_module_case(preset, (2, 33, 512), seed=6, relative_to_torch=relative)
+    run_module_case(preset, (8, 512, 512), seed=7, relative_to_torch=relative)
+
+
 @pytest.mark.parametrize(("preset", "overrides"), [
     ("a1", {}),
     ("a1", {"causal": False}),
@@ -420,8 +487,9 @@ def test_hip_backward_matches_torch_path() -> None:
         torch.testing.assert_close(p.grad, p_ref.grad, atol=1e-3, rtol=5e-2, msg=name)
 
 
-def test_unsupported_variant_raises_on_gpu() -> None:
+def test_unsupported_width_raises_on_gpu() -> None:
     device = _device()
-    module = da.SharedDictionaryAttention(da.experiment_config("a1-silu", backend="hip")).to(device, torch.bfloat16)
+    config = da.experiment_config("a1", routing_dim=96, backend="hip")
+    module = da.SharedDictionaryAttention(config).to(device, torch.bfloat16)
     with pytest.raises(NotImplementedError):
         module(torch.randn(1, 8, 512, device=device, dtype=torch.bfloat16))

@@ -210,14 +210,26 @@ def test_missing_library_is_reported(monkeypatch: pytest.MonkeyPatch, tmp_path) 
         lib.reset()
 
 
-def test_unsupported_hip_variants_are_rejected() -> None:
+def test_hip_supports_every_preset_and_rejects_other_widths() -> None:
     from double_attention.hip_ops import check_module_supported
 
-    check_module_supported(da.experiment_config("a1"))
-    check_module_supported(da.experiment_config("qk4-s4"))
-    check_module_supported(da.experiment_config("a1-r512-d1536"))
-    for name in ("a1-silu", "a1-silu-logitnorm", "a1-no-softmax"):
-        with pytest.raises(NotImplementedError):
-            check_module_supported(da.experiment_config(name))
+    for name in da.config._PRESETS:
+        check_module_supported(da.experiment_config(name))
     with pytest.raises(NotImplementedError):
         check_module_supported(da.experiment_config("a1", routing_dim=96))
+    with pytest.raises(NotImplementedError):
+        check_module_supported(da.experiment_config("a1", model_dim=384))
+
+
+def test_route_variant_flags_follow_the_config() -> None:
+    from double_attention import _lib
+    from double_attention.hip_ops import RouteVariant
+
+    assert RouteVariant.of_config(da.experiment_config("a1")).flags() == 0
+    v = RouteVariant.of_config(da.experiment_config("a1-silu-logitnorm-t1"))
+    assert v.flags() == _lib.DA_ROUTE_SILU_LOGITS | _lib.DA_ROUTE_STANDARDIZE
+    assert v.logit_scale(256) == 0.25
+    v = RouteVariant.of_config(da.experiment_config("a1-silu-logitnorm"))
+    assert v.logit_scale(256) == 256 ** -0.5   # ops.py:50-54 default
+    v = RouteVariant.of_config(da.experiment_config("a1-no-softmax-g4"))
+    assert v.flags() == _lib.DA_ROUTE_DIRECT_SILU and v.silu_gain == 4.0
