@@ -230,15 +230,27 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   const int sub = SUB == 1 ? 0 : uniform_wave() / NQW;
   const int wave = uniform_wave() - sub * NQW;    // query wave inside the sub-stream
   char* const lds_sub = lds + sub * Tile::BYTES;  // the sub-stream's share of stage 0
-  const int b = static_cast<int>(blockIdx.x) / p.n_slices;
-  const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;   // first feature of the slice
+  // XCD-aware placement: workgroups are dispatched x-fastest and dealt to
+  // the XCDs round-robin, so each XCD takes one contiguous range of the
+  // logical order (sequence, y, slice): the workgroups of a sequence share an
+  // XCD, whose L2 then fetches its key and V^T tiles once.  gx = b*n_slices +
+  // slice and gy take the roles of the grid's x and y.
+  const int n_wg = static_cast<int>(gridDim.x * gridDim.y);
+  const int wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
+  const int xcd = wg % kXcds, per_xcd = n_wg / kXcds, rem_xcd = n_wg % kXcds;
+  const int logical = xcd * per_xcd + min(xcd, rem_xcd) + wg / kXcds;
+  const int gy_b = logical / p.n_slices;
+  const int gy = gy_b % static_cast<int>(gridDim.y);
+  const int b = gy_b / static_cast<int>(gridDim.y);
+  const int gx = b * p.n_slices + (logical - gy_b * p.n_slices);
+  const int ds0 = (gx - b * p.n_slices) * DS;   // first feature of the slice
   const bool causal = p.flags & kAttnCausal;
   // The workgroup's work is a run of `total` key tiles over consecutive
   // units: maps s of query tile n_qt-1-y (heaviest first), or in the stream
   // split the query tiles of stream tiles [y*stream_len, ...).  The run starts
   // at key tile kt_first of unit unit_first.
   const bool stream = SUB == 1 && p.stream_len > 0;
-  const int qt_maps = p.n_qt - 1 - static_cast<int>(blockIdx.y);
+  const int qt_maps = p.n_qt - 1 - gy;
   const int n_kt_maps = key_tiles_of(p, qt_maps, QT);
   // Sub-streams of one map step over every second key tile (kt_stride 2).
   const bool split_tiles = SUB == 2 && p.S == 1;
@@ -256,7 +268,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       real = (p.S - sub + 1) / 2 * n_kt_maps;
     }
   } else if (stream) {
-    const int64_t g0 = static_cast<int64_t>(blockIdx.y) * p.stream_len;
+    const int64_t g0 = static_cast<int64_t>(gy) * p.stream_len;
     const int last = p.n_qt - 1;
     const int64_t all = p.S * (tiles_before(p, last, QT) + key_tiles_of(p, stream_qt(p, last), QT));
     unit_first = unit_of_tile(p, g0, QT);
@@ -613,7 +625,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 
   // Slots of this workgroup's partial results (stream split).
   constexpr int ITEM = QT * (DS + 2);
-  float* slots = p.part + static_cast<int64_t>(blockIdx.x * p.n_seg + blockIdx.y) * (MULTI ? 4 : 2) * ITEM;
+  float* slots = p.part + static_cast<int64_t>(gx * p.n_seg + gy) * (MULTI ? 4 : 2) * ITEM;
   // The fixed reference keeps every probability within the range of the
   // operand type: bf16 holds 2^-120 .. 1 exactly in exponent; fp16 does not.
   auto fixed_for = [&](float scale) {

@@ -76,6 +76,10 @@ __device__ __forceinline__ float scalar_value(ScalarHalves v, int dtype) {
   return __uint_as_float(lo << 16);
 }
 
+// MI355X: eight XCDs, each with its own L2; workgroups are dealt to them
+// round-robin in dispatch order.
+constexpr int kXcds = 8;
+
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
 // Reductions across the four 16-lane rows (lanes c, c+16, c+32, c+48 hold the

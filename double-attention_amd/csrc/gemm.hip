@@ -56,7 +56,7 @@ struct GemmSeg {
   void* out;
   int64_t ldo;
   int64_t T, Tp, vt_stride_b;
-  int tiles_i, tiles;
+  int tiles_i, tiles_j, tiles;
 };
 
 struct GemmParams {
@@ -107,18 +107,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   char* const lds1 = lds + STAGE;
 
   // The normalization's workgroups come first, so they start with the first
-  // wave of GEMM tiles instead of after them.
+  // wave of GEMM tiles instead of after them; their count is padded to a
+  // multiple of the XCD count.
   const int n_norm = static_cast<int>(gridDim.x) - prm.gemm_blocks;
   if (static_cast<int>(blockIdx.x) < n_norm) {
-    normalize_block(prm.norm, static_cast<int>(blockIdx.x), lds);
+    if (static_cast<int>(blockIdx.x) < norm_blocks(prm.norm)) normalize_block(prm.norm, static_cast<int>(blockIdx.x), lds);
     return;
   }
-  int tile = static_cast<int>(blockIdx.x) - n_norm;
+  // XCD-aware order: workgroup w runs on XCD w % kXcds (round-robin
+  // dispatch), so each XCD takes one contiguous range of tiles.  Inside a
+  // segment consecutive tiles share their block of the larger operand, which
+  // the XCD's L2 then fetches once.
+  const int w = static_cast<int>(blockIdx.x) - n_norm;
+  const int xcd = w % kXcds;
+  const int per = prm.gemm_blocks / kXcds, rem = prm.gemm_blocks % kXcds;
+  int tile = xcd * per + min(xcd, rem) + w / kXcds;
   const int si = (prm.nseg > 1 && tile >= prm.seg[0].tiles) ? 1 : 0;
   if (si) tile -= prm.seg[0].tiles;
   const GemmSeg& sg = prm.seg[si];
-  const int64_t i0 = static_cast<int64_t>(tile % sg.tiles_i) * BI;
-  const int64_t j0 = static_cast<int64_t>(tile / sg.tiles_i) * kBJ;
+  const bool i_fast = sg.tiles_i <= sg.tiles_j;
+  const int64_t i0 = static_cast<int64_t>(i_fast ? tile % sg.tiles_i : tile / sg.tiles_j) * BI;
+  const int64_t j0 = static_cast<int64_t>(i_fast ? tile / sg.tiles_i : tile % sg.tiles_j) * kBJ;
   // Value segment: the tile's first virtual token, split once (uniform).
   const int64_t b0 = sg.mode == 1 ? static_cast<int>(i0) / static_cast<int>(sg.Tp) : 0;   // rows fit in int
   const int64_t t0 = sg.mode == 1 ? i0 - b0 * sg.Tp : 0;
@@ -293,7 +302,8 @@ static int setup_gemm(const GemmSegment* segs, int nseg, GemmParams& prm) {
     d.ldo = a.ldo;
     d.vt_stride_b = a.vt_stride_b;
     d.tiles_i = static_cast<int>((d.I + BI - 1) / BI);
-    d.tiles = d.tiles_i * static_cast<int>((a.J + kBJ - 1) / kBJ);
+    d.tiles_j = static_cast<int>((a.J + kBJ - 1) / kBJ);
+    d.tiles = d.tiles_i * d.tiles_j;
     total += d.tiles;
   }
   if (nseg == 1) prm.seg[1] = prm.seg[0];
@@ -307,7 +317,7 @@ void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t strea
   GemmParams prm;
   int total = setup_gemm<128>(segs, nseg, prm);
   prm.norm = norm ? *norm : NormJob{};
-  const int extra = norm_blocks(prm.norm);
+  const int extra = static_cast<int>(round_up(norm_blocks(prm.norm), kXcds));
   if (total + extra == 0) return;
   if (total >= 512) {
     prm.gemm_blocks = total;
