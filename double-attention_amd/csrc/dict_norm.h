@@ -72,12 +72,19 @@ __device__ __forceinline__ void normalize_block_t(const NormJob& job, int block,
   float* scale_s = partial + kNormGroups * kNormCols;     // [32]
   uint16_t* tile = reinterpret_cast<uint16_t*>(scale_s + kNormCols);   // [32][R + 8]
 
+  // Every load is issued before any is used: padding atoms (j >= M) re-read
+  // atom M-1 and are zeroed afterwards, so the loads need no branch.
+  const int jc = min(j, job.M - 1);
   float v[PER];
-  float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int r = rg + i * kNormGroups;
-    v[i] = valid ? static_cast<float>(src[static_cast<int64_t>(r) * job.M + j]) : 0.f;
+    v[i] = static_cast<float>(src[static_cast<int64_t>(r) * job.M + jc]);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    v[i] = valid ? v[i] : 0.f;
     ss += v[i] * v[i];
   }
   partial[rg * kNormCols + jj] = ss;

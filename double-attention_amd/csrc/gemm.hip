@@ -106,19 +106,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   char* const lds0 = lds;
   char* const lds1 = lds + STAGE;
 
-  // The normalization's workgroups come first, so they start with the first
-  // wave of GEMM tiles instead of after them; their count is padded to a
-  // multiple of the XCD count.
-  const int n_norm = static_cast<int>(gridDim.x) - prm.gemm_blocks;
-  if (static_cast<int>(blockIdx.x) < n_norm) {
-    if (static_cast<int>(blockIdx.x) < norm_blocks(prm.norm)) normalize_block(prm.norm, static_cast<int>(blockIdx.x), lds);
+  // The normalization's workgroups follow the GEMM tiles: they take the
+  // CU slots that the first finished tiles free, instead of pushing tiles
+  // into a second round.
+  const int w = static_cast<int>(blockIdx.x);
+  if (w >= prm.gemm_blocks) {
+    normalize_block(prm.norm, w - prm.gemm_blocks, lds);
     return;
   }
   // XCD-aware order: workgroup w runs on XCD w % kXcds (round-robin
   // dispatch), so each XCD takes one contiguous range of tiles.  Inside a
   // segment consecutive tiles share their block of the larger operand, which
   // the XCD's L2 then fetches once.
-  const int w = static_cast<int>(blockIdx.x) - n_norm;
   const int xcd = w % kXcds;
   const int per = prm.gemm_blocks / kXcds, rem = prm.gemm_blocks % kXcds;
   int tile = xcd * per + min(xcd, rem) + w / kXcds;
@@ -173,6 +172,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     }
   };
 
+  // Bias of this lane's outputs (mode 0: along i, mode 1: along j), fetched
+  // ahead of the K loop without branches (clamped or dummy indices, valid
+  // addresses only), so the epilogue finds it landed.
+  constexpr int WI = BI / 2;                 // i extent of a wave's block
+  const bool has_bias = sg.bias != nullptr;
+  const void* bsrc = has_bias ? sg.bias : sg.q;
+  const int bdt = has_bias ? sg.bias_dtype : kF16;
+  ScalarHalves bias_raw[NA * 4 + 4];
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t i = min(i0 + wi * WI + a * 16 + 4 * g + r, sg.I - 1);
+      bias_raw[a * 4 + r] = fetch_scalar(bsrc, bdt, has_bias && sg.mode == 0 ? i : 0);
+    }
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int64_t j = min(j0 + wj * 64 + b * 16 + c, sg.J - 1);
+    bias_raw[NA * 4 + b] = fetch_scalar(bsrc, bdt, has_bias && sg.mode == 1 ? j : 0);
+  }
+
   f32x4 acc[NA][4];
 #pragma unroll
   for (int a = 0; a < NA; ++a)
@@ -224,7 +244,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   // for a fixed j (mode 0: out[j*ldo + i]; mode 1: 32-token runs of V^T), so
   // each wave stages its block in LDS as [j][i] rows and writes them back as
   // 16-byte chunks, eight lanes per 128-byte row segment.
-  constexpr int WI = BI / 2;                 // i extent of a wave's block
   constexpr int ROWB = WI * 2 + 16;          // bytes per staged j row (padded)
   static_assert(64 * ROWB <= STAGE, "a wave's staging block must fit one stage buffer");
   __syncthreads();                           // every wave is done reading the stage buffers
@@ -236,12 +255,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t i = i0 + wi * WI + a * 16 + 4 * g + r;
-      bias_i[a][r] = (sg.mode == 0 && sg.bias && i < sg.I) ? load_scalar(sg.bias, sg.bias_dtype, i) : 0.f;
+      bias_i[a][r] = (sg.mode == 0 && has_bias && i < sg.I) ? scalar_value(bias_raw[a * 4 + r], bdt) : 0.f;
     }
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const int64_t j = j0 + wj * 64 + b * 16 + c;
-    const float bj = (sg.mode == 1 && sg.bias && j < sg.J) ? load_scalar(sg.bias, sg.bias_dtype, j) : 0.f;
+    const float bj = (sg.mode == 1 && has_bias && j < sg.J) ? scalar_value(bias_raw[NA * 4 + b], bdt) : 0.f;
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
       typename Elem<T>::v4 o;
@@ -317,18 +336,20 @@ void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t strea
   GemmParams prm;
   int total = setup_gemm<128>(segs, nseg, prm);
   prm.norm = norm ? *norm : NormJob{};
-  const int extra = static_cast<int>(round_up(norm_blocks(prm.norm), kXcds));
-  if (total + extra == 0) return;
+  const int nb = norm_blocks(prm.norm);
+  if (total + nb == 0) return;
   if (total >= 512) {
     prm.gemm_blocks = total;
-    if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 128>), dim3(total + extra), dim3(256), 0, stream, prm);
-    else hipLaunchKernelGGL((gemm_kernel<__bf16, 128>), dim3(total + extra), dim3(256), 0, stream, prm);
+    const unsigned grid = static_cast<unsigned>(total + nb);
+    if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 128>), dim3(grid), dim3(256), 0, stream, prm);
+    else hipLaunchKernelGGL((gemm_kernel<__bf16, 128>), dim3(grid), dim3(256), 0, stream, prm);
     return;
   }
   total = setup_gemm<64>(segs, nseg, prm);
   prm.gemm_blocks = total;
-  if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 64>), dim3(total + extra), dim3(256), 0, stream, prm);
-  else hipLaunchKernelGGL((gemm_kernel<__bf16, 64>), dim3(total + extra), dim3(256), 0, stream, prm);
+  const unsigned grid = static_cast<unsigned>(total + nb);
+  if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 64>), dim3(grid), dim3(256), 0, stream, prm);
+  else hipLaunchKernelGGL((gemm_kernel<__bf16, 64>), dim3(grid), dim3(256), 0, stream, prm);
 }
 
 }  // namespace da
