@@ -162,6 +162,19 @@ def main() -> None:
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
     ms_per_step = elapsed * 1e3 / args.steps
+    graph_ms = None
+    if lm is not None:
+        # The same LM forward replayed as one HIP graph (no per-call host work).
+        graphed = da.GraphedForward(lm, ids)
+        for _ in range(args.warmup):
+            graphed(ids)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(args.steps):
+            graphed(ids)
+        torch.cuda.synchronize()
+        graph_ms = (time.perf_counter() - start) * 1e3 / args.steps
+        del graphed
     tokens = batch * length
     H, S, R, M, d = config.qk_branches, config.outer_maps, config.routing_dim, config.dictionary_size, config.model_dim
     W = H * R
@@ -332,6 +345,7 @@ def main() -> None:
         },
         "routed_rows_per_s": round(rows / (kernel_us["route"] * 1e-6), 1),
         "attention_tokens_per_s": round(tokens / (kernel_us["attention"] * 1e-6), 1),
+        **({"graph_ms_per_step": round(graph_ms, 4)} if graph_ms is not None else {}),
         "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -7,6 +7,7 @@ gfx950 operator functions ``dictionary_route_hip`` / ``routed_attention_hip``.
 """
 
 from . import _lib
+from .checkpoint import GraphedForward, load_model_from_checkpoint, load_training_checkpoint
 from .config import DoubleAttentionConfig, experiment_config, experiment_names
 from .hip_ops import dictionary_normalize_hip, dictionary_route_hip, routed_attention_hip
 from .modules import (
@@ -28,6 +29,7 @@ __all__ = [
     "DoubleAttentionConfig",
     "DoubleAttentionLM",
     "DoubleAttentionStack",
+    "GraphedForward",
     "HIP_AVAILABLE",
     "SharedDictionaryAttention",
     "SharedDictionaryBank",
@@ -38,6 +40,8 @@ __all__ = [
     "dictionary_route_reference",
     "experiment_config",
     "experiment_names",
+    "load_model_from_checkpoint",
+    "load_training_checkpoint",
     "routed_attention_hip",
     "routed_attention_reference",
 ]

@@ -450,6 +450,32 @@ def test_lm_c4_qk2_s2_tied() -> None:
     assert_parity(logits, expected, rel_l2=max(5e-3, 1.1 * torch_rel), max_abs=max(2e-2, 1.1 * torch_max), label="lm c4")
 
 
+@pytest.mark.parametrize("preset", ["a1-d1536-qffn", "a1-r512-d1536-qffn"])
+def test_lm_q_dictionary_feedforward(preset) -> None:
+    # The Q-dictionary FFN (modules.py:348-356) expands through the same
+    # normalized bank the HIP layers route with.
+    device = _device()
+    config = da.experiment_config(preset, backend="hip")
+    torch.manual_seed(0)
+    model = da.DoubleAttentionLM(512, 64, config, 2, dictionary_group_size=2,
+                                 feedforward_dim=config.dictionary_size)
+    model = model.to(device=device, dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, 512, (8, 64), generator=torch.Generator().manual_seed(2))
+    with torch.inference_mode():
+        logits, _ = model(ids.to(device))
+        torch_model = da.DoubleAttentionLM(512, 64, config.with_updates(backend="torch"), 2, dictionary_group_size=2,
+                                           feedforward_dim=config.dictionary_size).to(device=device, dtype=torch.bfloat16).eval()
+        torch_model.load_state_dict(model.state_dict())
+        torch_logits, _ = torch_model(ids.to(device))
+    expected = oracle.double_attention_lm(oracle_params(model), config, ids.numpy(), 2, 2, dtype=np.float32)
+    e = expected.astype(np.float64)
+    torch_rel = np.linalg.norm(np32(torch_logits) - e) / np.linalg.norm(e)
+    torch_max = np.abs(np32(torch_logits) - e).max()
+    print(f"[parity] lm {preset} bf16 torch path rel_l2={torch_rel:.3e} max_abs={torch_max:.3e}", flush=True)
+    assert_parity(logits, expected, rel_l2=max(5e-3, 1.1 * torch_rel), max_abs=max(2e-2, 1.1 * torch_max),
+                  label=f"lm {preset}")
+
+
 def test_stack_normalizes_each_bank_once_on_hip(monkeypatch) -> None:
     device = _device()
     config = da.experiment_config("a1", backend="hip")
