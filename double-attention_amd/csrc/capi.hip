@@ -114,7 +114,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 8; }
+int da_abi_version(void) { return 9; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -264,6 +264,40 @@ int da_linear(const void* x, int64_t rows, int64_t in_features, const void* weig
   return check_launch("linear");
 }
 
+int da_linear_ex(const void* x, int64_t rows, int64_t in_features, const void* weight, int64_t out_features,
+                 const void* bias, int bias_dtype, int dtype, int activation, const void* residual, void* out,
+                 da_stream_t stream) {
+  if (activation != DA_ACT_NONE && activation != DA_ACT_GELU)
+    return fail(DA_ERR_INVALID_ARGUMENT, "linear: unknown activation %d", activation);
+  if (residual && !aligned(residual, 8)) return fail(DA_ERR_ALIGNMENT, "linear: residual must be 8-byte aligned");
+  int rc = validate_gemm_common("linear", x, rows, in_features, dtype);
+  if (rc) return rc;
+  if (out_features < 4 || out_features % 4) return fail(DA_ERR_UNSUPPORTED, "linear: out_features must be a multiple of 4");
+  if (!weight || !out || !aligned(weight, 16) || !aligned(out, 8))
+    return fail(DA_ERR_ALIGNMENT, "linear: weight/out must be non-null and aligned");
+  if (bias && !any_dtype(bias_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "linear: bad bias dtype");
+  da::GemmSegment seg{weight, nullptr, 0, x, out_features, rows, in_features, bias, bias_dtype, 0,
+                      out, out_features, 0, 0, 0, activation == DA_ACT_GELU ? da::kGemmActGelu : da::kGemmActNone,
+                      residual};
+  da::launch_gemm(&seg, 1, dtype, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("linear");
+}
+
+int da_layer_norm(const void* x, int64_t rows, int64_t dim, const void* weight, const void* bias, int param_dtype,
+                  float eps, int dtype, void* out, da_stream_t stream) {
+  if (!half_dtype(dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "layer_norm: dtype must be DA_F16 or DA_BF16");
+  if ((weight || bias) && !any_dtype(param_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "layer_norm: bad parameter dtype");
+  if (rows < 0 || dim < 8 || dim % 8 || dim > 4096)
+    return fail(DA_ERR_UNSUPPORTED, "layer_norm: dim must be a multiple of 8 in [8, 4096]");
+  if (rows == 0) return ok();
+  if (!x || !out || !aligned(x, 16) || !aligned(out, 16) || !aligned(weight, 16) || !aligned(bias, 16))
+    return fail(DA_ERR_ALIGNMENT, "layer_norm: x, out, weight and bias must be 16-byte aligned");
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(DA_ERR_INVALID_ARGUMENT, "layer_norm: bad eps");
+  da::launch_layer_norm(x, rows, static_cast<int>(dim), weight, bias, param_dtype, eps, dtype, out,
+                        reinterpret_cast<hipStream_t>(stream));
+  return check_launch("layer_norm");
+}
+
 int64_t da_sda_workspace_offset(int64_t batch, int64_t length, int64_t model_dim, int64_t qk_width,
                                 int which) {
   const int64_t tokens = batch * length;
@@ -353,6 +387,8 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
     if (rc) return rc;
     if (d % 4) return fail(DA_ERR_UNSUPPORTED, "forward: model_dim must be a multiple of 4");
   }
+  if (a->residual && (!a->wo || !aligned(a->residual, 16)))
+    return fail(DA_ERR_UNSUPPORTED, "forward: a residual needs the output projection and 16-byte alignment");
   if (!aligned(a->wq, 16) || !aligned(a->wk, 16) || !aligned(a->wv, 16) || (a->wo && !aligned(a->wo, 16)) ||
       !aligned(a->out, 16))
     return fail(DA_ERR_ALIGNMENT, "forward: weights and output must be 16-byte aligned");
@@ -415,7 +451,8 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   da::launch_routed_attention(at, partials, s);
   // 4. Output projection.
   if (a->wo) {
-    da::GemmSegment o{a->wo, nullptr, 0, mixed, d, B * T, ot, nullptr, 0, 0, a->out, d, 0, 0, 0};
+    da::GemmSegment o{a->wo, nullptr, 0, mixed, d, B * T, ot, nullptr, 0, 0, a->out, d, 0, 0, 0, da::kGemmActNone,
+                      a->residual};
     da::launch_gemm(&o, 1, a->dtype, s);
   }
   return check_launch("forward");

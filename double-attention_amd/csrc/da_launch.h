@@ -98,12 +98,21 @@ struct GemmSegment {
   // goes to out[b*vt_stride_b + (t/32)*32*J + 32*j + t%32] (32-token tiles),
   // and tokens T..Tp-1 are filled too.
   int64_t T, Tp, vt_stride_b;
+  // mode 0 only: kGemmActGelu applies GELU (erf form) after the bias, and a
+  // non-null residual (same layout as out) is added to the rounded result.
+  int act;
+  const void* residual;
 };
+
+enum : int { kGemmActNone = 0, kGemmActGelu = 1 };
 
 void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int in_dtype, int R,
                                  int M, float eps, void* key_t, int key_dtype, void* value,
                                  void* value_rows, hipStream_t stream);
 void launch_dictionary_route(const RouteArgs& a, hipStream_t stream);
+// LayerNorm over the last dimension (dim a multiple of 8, at most 4096).
+void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight, const void* bias, int param_dtype,
+                       float eps, int dtype, void* out, hipStream_t stream);
 // Launch shape of the attention for a problem: value slice width, waves per
 // query tile, sub-streams, query tiles, the stream split of long key ranges (run length, 0
 // = none; runs per sequence and slice) and the bytes of partials it needs.

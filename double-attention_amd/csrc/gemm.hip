@@ -56,6 +56,8 @@ struct GemmSeg {
   void* out;
   int64_t ldo;
   int64_t T, Tp, vt_stride_b;
+  int act;               // mode 0: kGemmActGelu applies the exact GELU after the bias
+  const void* residual;  // mode 0: nullptr, or added to the output (same layout as out)
   int tiles_i, tiles_j, tiles;
 };
 
@@ -94,7 +96,11 @@ __device__ __forceinline__ const T* p_row(const GemmSeg& sg, int64_t i0, int64_t
   return i < sg.p_split ? p0 + i * sg.K : static_cast<const T*>(sg.p1) + (i - sg.p_split) * sg.K;
 }
 
-template <typename T, int BI>
+// EPI: kGemmActGelu applies GELU after the bias (mode 0); EPI_RES adds the
+// segment's residual (mode 0).  Launches without either compile neither.
+constexpr int kEpiResidual = 2;
+
+template <typename T, int BI, int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   typedef typename Elem<T>::v8 v8;
   typedef GemmCfg<BI> Cfg;
@@ -172,25 +178,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     }
   };
 
-  // Bias of this lane's outputs (mode 0: along i, mode 1: along j), fetched
-  // ahead of the K loop without branches (clamped or dummy indices, valid
-  // addresses only), so the epilogue finds it landed.
+  // Bias of this lane's outputs, fetched ahead of the K loop without
+  // branches (clamped or dummy indices, valid addresses only), so the
+  // epilogue finds it landed: slot a*4 + r holds i = ... + a*16 + 4g + r
+  // (mode 0), slot b the j = ... + b*16 + c (mode 1).
   constexpr int WI = BI / 2;                 // i extent of a wave's block
   const bool has_bias = sg.bias != nullptr;
   const void* bsrc = has_bias ? sg.bias : sg.q;
   const int bdt = has_bias ? sg.bias_dtype : kF16;
-  ScalarHalves bias_raw[NA * 4 + 4];
+  ScalarHalves bias_raw[NA * 4];
 #pragma unroll
-  for (int a = 0; a < NA; ++a)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t i = min(i0 + wi * WI + a * 16 + 4 * g + r, sg.I - 1);
-      bias_raw[a * 4 + r] = fetch_scalar(bsrc, bdt, has_bias && sg.mode == 0 ? i : 0);
-    }
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int64_t j = min(j0 + wj * 64 + b * 16 + c, sg.J - 1);
-    bias_raw[NA * 4 + b] = fetch_scalar(bsrc, bdt, has_bias && sg.mode == 1 ? j : 0);
+  for (int k = 0; k < NA * 4; ++k) {
+    const int64_t i = min(i0 + wi * WI + (k / 4) * 16 + 4 * g + k % 4, sg.I - 1);
+    const int64_t j = min(j0 + wj * 64 + (k % 4) * 16 + c, sg.J - 1);
+    const int64_t idx = !has_bias ? 0 : sg.mode == 0 ? i : k < 4 ? j : 0;
+    bias_raw[k] = fetch_scalar(bsrc, bdt, idx);
   }
 
   f32x4 acc[NA][4];
@@ -202,11 +204,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   const int afrag = TileP::offset(wi * (BI / 2) + c, g);
   const int bfrag = TileP::BYTES + GemmTileQ::offset(wj * 64 + c, g);
 
-  // One K stage: every fragment of the stage is read first (LDS latency is
-  // paid once, and the reads precede the next stage's DMA in program order:
-  // the compiler keeps any LDS read behind a DMA that writes LDS), then the
-  // next stage is issued, then the MFMAs run.  A final half stage (K % 64 ==
-  // 32) takes one 32-deep step.
+  // Two stage buffers: step st reads stage st and issues stage st + 1 into
+  // the other buffer.  Every fragment of the stage is read first (LDS latency
+  // is paid once, and the reads precede the next stage's DMA in program
+  // order: the compiler keeps any LDS read behind a DMA that writes LDS),
+  // then the next stage is issued, then the MFMAs run.  A final half stage
+  // (K % 64 == 32) takes one 32-deep step.  (A third stage, or a deeper ring
+  // at one workgroup per CU, ran slower at every projection and FFN shape
+  // measured: two co-resident workgroups hide more latency.)
   auto step = [&](int st, char* cur, char* nxt) {
     wait_vmem();
     __syncthreads();
@@ -260,12 +265,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const int64_t j = j0 + wj * 64 + b * 16 + c;
-    const float bj = (sg.mode == 1 && has_bias && j < sg.J) ? scalar_value(bias_raw[NA * 4 + b], bdt) : 0.f;
+    const float bj = (sg.mode == 1 && has_bias && j < sg.J) ? scalar_value(bias_raw[b], bdt) : 0.f;
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
       typename Elem<T>::v4 o;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = static_cast<T>(acc[a][b][r] + bias_i[a][r] + bj);
+      for (int r = 0; r < 4; ++r) {
+        float v = acc[a][b][r] + bias_i[a][r] + bj;
+        if constexpr ((EPI & kGemmActGelu) != 0) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+        o[r] = static_cast<T>(v);
+      }
       *reinterpret_cast<typename Elem<T>::v4*>(stage_w + (b * 16 + c) * ROWB + (a * 16 + 4 * g) * 2) = o;
     }
   }
@@ -283,10 +292,25 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     if (j >= sg.J || i >= sg.I) continue;
     if (sg.mode == 0) {
       T* dst = out + j * sg.ldo + i;
-      if (i + 8 <= sg.I) {
-        store16B(dst, v);
-      } else {   // I % 4 == 0: a last half chunk
-        *reinterpret_cast<uint2*>(dst) = uint2{v[0], v[1]};
+      const bool full = i + 8 <= sg.I;   // else I % 4 == 0: a last half chunk
+      u32x4 w = v;
+      if constexpr ((EPI & kEpiResidual) != 0) {
+        // out = residual + (rounded) result, rounded again: the order of the
+        // unfused `x + linear(...)` in the output dtype.
+        const T* res = static_cast<const T*>(sg.residual) + j * sg.ldo + i;
+        u32x4 rv = full ? *reinterpret_cast<const u32x4*>(res) : u32x4{reinterpret_cast<const uint2*>(res)->x,
+                                                                    reinterpret_cast<const uint2*>(res)->y, 0u, 0u};
+        const v8 a = __builtin_bit_cast(v8, v);
+        const v8 b = __builtin_bit_cast(v8, rv);
+        v8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = static_cast<T>(static_cast<float>(a[e]) + static_cast<float>(b[e]));
+        w = __builtin_bit_cast(u32x4, o);
+      }
+      if (full) {
+        store16B(dst, w);
+      } else {
+        *reinterpret_cast<uint2*>(dst) = uint2{w[0], w[1]};
       }
     } else {
       // Eight consecutive virtual tokens of one sequence and one 32-token
@@ -320,6 +344,8 @@ static int setup_gemm(const GemmSegment* segs, int nseg, GemmParams& prm) {
     d.out = a.out;
     d.ldo = a.ldo;
     d.vt_stride_b = a.vt_stride_b;
+    d.act = a.act;
+    d.residual = a.residual;
     d.tiles_i = static_cast<int>((d.I + BI - 1) / BI);
     d.tiles_j = static_cast<int>((a.J + kBJ - 1) / kBJ);
     d.tiles = d.tiles_i * d.tiles_j;
@@ -329,27 +355,40 @@ static int setup_gemm(const GemmSegment* segs, int nseg, GemmParams& prm) {
   return total;
 }
 
+template <typename T, int BI>
+static void launch_gemm_k(const GemmParams& prm, int total, int nb, hipStream_t stream) {
+  // Every segment of a launch shares its epilogue (only single-segment
+  // launches ask for GELU or a residual).
+  const int epi = (prm.seg[0].act == kGemmActGelu ? kGemmActGelu : 0) | (prm.seg[0].residual ? kEpiResidual : 0);
+  const dim3 grid(static_cast<unsigned>(total + nb));
+  switch (epi) {
+    case 0: hipLaunchKernelGGL((gemm_kernel<T, BI, 0>), grid, dim3(256), 0, stream, prm); break;
+    case kGemmActGelu: hipLaunchKernelGGL((gemm_kernel<T, BI, kGemmActGelu>), grid, dim3(256), 0, stream, prm); break;
+    case kEpiResidual: hipLaunchKernelGGL((gemm_kernel<T, BI, kEpiResidual>), grid, dim3(256), 0, stream, prm); break;
+    default:
+      hipLaunchKernelGGL((gemm_kernel<T, BI, kGemmActGelu | kEpiResidual>), grid, dim3(256), 0, stream, prm);
+      break;
+  }
+}
+
 // 128-row tiles when the grid holds two workgroups per CU, else 64-row tiles
 // (twice the workgroups, so two share every CU and hide each other's waits).
 // `norm` (or nullptr) adds a dictionary normalization's workgroups.
 void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream, const NormJob* norm) {
   GemmParams prm;
-  int total = setup_gemm<128>(segs, nseg, prm);
+  const int tiles128 = setup_gemm<128>(segs, nseg, prm);
   prm.norm = norm ? *norm : NormJob{};
   const int nb = norm_blocks(prm.norm);
-  if (total + nb == 0) return;
-  if (total >= 512) {
-    prm.gemm_blocks = total;
-    const unsigned grid = static_cast<unsigned>(total + nb);
-    if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 128>), dim3(grid), dim3(256), 0, stream, prm);
-    else hipLaunchKernelGGL((gemm_kernel<__bf16, 128>), dim3(grid), dim3(256), 0, stream, prm);
+  if (tiles128 + nb == 0) return;
+  const bool f16 = dtype == kF16;
+  if (tiles128 >= 512) {
+    prm.gemm_blocks = tiles128;
+    f16 ? launch_gemm_k<_Float16, 128>(prm, tiles128, nb, stream) : launch_gemm_k<__bf16, 128>(prm, tiles128, nb, stream);
     return;
   }
-  total = setup_gemm<64>(segs, nseg, prm);
+  const int total = setup_gemm<64>(segs, nseg, prm);
   prm.gemm_blocks = total;
-  const unsigned grid = static_cast<unsigned>(total + nb);
-  if (dtype == kF16) hipLaunchKernelGGL((gemm_kernel<_Float16, 64>), dim3(grid), dim3(256), 0, stream, prm);
-  else hipLaunchKernelGGL((gemm_kernel<__bf16, 64>), dim3(grid), dim3(256), 0, stream, prm);
+  f16 ? launch_gemm_k<_Float16, 64>(prm, total, nb, stream) : launch_gemm_k<__bf16, 64>(prm, total, nb, stream);
 }
 
 }  // namespace da

@@ -34,6 +34,9 @@ DA_SDA_NORMALIZE_OUTPUT = 2
 DA_SDA_CAUSAL = 4
 DA_SDA_CONCAT = 8
 
+DA_ACT_NONE = 0
+DA_ACT_GELU = 1
+
 ERROR_NAMES = {
     -1: "invalid argument",
     -2: "unsupported",
@@ -42,7 +45,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -85,6 +88,7 @@ class SdaForwardArgs(ctypes.Structure):
         ("route_variant", _i32),
         ("silu_gain", _f32),
         ("logit_scale", _f32),
+        ("residual", _vp),
     ]
 
 
@@ -123,6 +127,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _i64, _i64, _vp],
     ),
     "da_linear": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _vp, _vp]),
+    "da_linear_ex": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "da_layer_norm": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _f32, _i32, _vp, _vp]),
     "da_sda_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),
     "da_sda_workspace_offset": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "da_shared_dictionary_attention_forward": (_i32, [ctypes.POINTER(SdaForwardArgs), _vp]),

@@ -489,25 +489,74 @@ def routed_attention_hip(
 # --------------------------------------------------------------------------
 
 
-def linear_hip(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
-    """``x @ weight.T (+ bias)`` with the library's MFMA GEMM."""
+def linear_hip(
+    x: Tensor,
+    weight: Tensor,
+    bias: Tensor | None = None,
+    *,
+    activation: str | None = None,
+    residual: Tensor | None = None,
+) -> Tensor:
+    """``act(x @ weight.T (+ bias)) (+ residual)`` with the library's MFMA GEMM.
+
+    ``activation`` is None or ``"gelu"`` (exact, ``nn.GELU()``); ``residual``
+    has the output's shape and is added to the rounded result, as the
+    unfused ``residual + linear(x)`` does.
+    """
 
     _require_cuda(x, weight)
     code = _half_code(x.dtype)
     if weight.dtype != x.dtype:
         raise ValueError("x and weight must share a dtype")
+    if activation not in (None, "gelu"):
+        raise ValueError(f"unsupported activation {activation!r}")
     rows = x.reshape(-1, x.shape[-1]).contiguous()
-    w = weight.contiguous()
+    w = weight.detach().contiguous()
     out = torch.empty(*x.shape[:-1], weight.shape[0], dtype=x.dtype, device=x.device)
     b = None if bias is None else bias.detach().contiguous()
+    res = None
+    if residual is not None:
+        if residual.shape != out.shape or residual.dtype != x.dtype:
+            raise ValueError("residual must match the output's shape and dtype")
+        res = residual.detach().contiguous()
+    lib = _lib.get()
+    bias_code = dtype_code(b.dtype) if b is not None else _lib.DA_F32
+    if activation is None and res is None:
+        rc = lib.da_linear(
+            rows.data_ptr(), rows.shape[0], rows.shape[1], w.data_ptr(), w.shape[0],
+            _ptr(b), bias_code, code, out.data_ptr(), _stream(x.device),
+        )
+    else:
+        rc = lib.da_linear_ex(
+            rows.data_ptr(), rows.shape[0], rows.shape[1], w.data_ptr(), w.shape[0],
+            _ptr(b), bias_code, code, _lib.DA_ACT_GELU if activation == "gelu" else _lib.DA_ACT_NONE,
+            _ptr(res), out.data_ptr(), _stream(x.device),
+        )
+    _lib.check(rc, "linear_hip")
+    return out
+
+
+def layer_norm_hip(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: float = 1e-5) -> Tensor:
+    """``F.layer_norm`` over the last dimension (fp32 statistics, one rounding)."""
+
+    _require_cuda(x)
+    code = _half_code(x.dtype)
+    dim = x.shape[-1]
+    xc = x.contiguous()
+    params = [t.detach().contiguous() for t in (weight, bias) if t is not None]
+    if len({t.dtype for t in params}) > 1:
+        raise ValueError("LayerNorm weight and bias must share a dtype")
+    w = None if weight is None else params[0]
+    b = None if bias is None else params[-1]
+    out = torch.empty_like(xc)
     lib = _lib.get()
     _lib.check(
-        lib.da_linear(
-            rows.data_ptr(), rows.shape[0], rows.shape[1], w.data_ptr(), w.shape[0],
-            _ptr(b), dtype_code(b.dtype) if b is not None else _lib.DA_F32, code,
-            out.data_ptr(), _stream(x.device),
+        lib.da_layer_norm(
+            xc.data_ptr(), xc.numel() // dim if dim else 0, dim, _ptr(w), _ptr(b),
+            dtype_code(params[0].dtype) if params else _lib.DA_F32, float(eps), code, out.data_ptr(),
+            _stream(x.device),
         ),
-        "linear_hip",
+        "layer_norm_hip",
     )
     return out
 
@@ -588,12 +637,14 @@ def shared_dictionary_attention_hip(
     layout: RouteDictionary,
     dtype: torch.dtype,
     raw_bank: tuple[Tensor, Tensor | None] | None = None,
+    residual: Tensor | None = None,
 ) -> HipForwardResult:
     """One ``SharedDictionaryAttention`` forward through the fused C entry point.
 
     With ``raw_bank`` (the bank's raw key / value atoms) the call first
     normalizes them into ``layout`` (from ``own_bank_layout``), inside its
-    projection launch.
+    projection launch.  ``residual`` ([B, T, d] of the output dtype) is added
+    to the output projection's rounded result (the block's ``x + ...``).
     """
 
     config = module.config
@@ -645,6 +696,11 @@ def shared_dictionary_attention_hip(
         dtype_code(scalar_dtype), code, float(config.eps), flags,
         workspace.data_ptr(), ws_bytes, out.data_ptr(),
     )
+    if residual is not None:
+        if residual.shape != out.shape or residual.dtype != dtype:
+            raise ValueError("residual must match the output's shape and dtype")
+        residual = residual.detach().contiguous()
+        args.residual = residual.data_ptr()
     variant = RouteVariant.of_config(config)
     args.route_variant = variant.flags()
     args.silu_gain = variant.silu_gain
@@ -668,6 +724,7 @@ __all__ = [
     "RouteVariant",
     "dictionary_normalize_hip",
     "dictionary_route_hip",
+    "layer_norm_hip",
     "linear_hip",
     "qkv_projection_hip",
     "route_key_dtype",

@@ -255,19 +255,50 @@ class SharedDictionaryAttention(nn.Module):
         )
         if needs_grad:
             return _HipModuleFunction.run(self, x, bank, normalized_dictionary, dtype, return_aux)
+        result = self._hip_call(x, bank, normalized_dictionary, dtype)
+        if not return_aux:
+            return result.output
+        return result.output, self._hip_aux(result.routed, dtype)
+
+    def _hip_call(
+        self,
+        x: Tensor,
+        bank: SharedDictionaryBank,
+        normalized_dictionary: tuple[Tensor, Tensor] | None,
+        dtype: torch.dtype,
+        residual: Tensor | None = None,
+    ):
+        """The fused forward (no autograd); ``residual`` is added to its output."""
+
+        from . import hip_ops
+
         key_dtype = hip_ops.route_key_dtype(self.config.normalize_routing_input, dtype)
         if normalized_dictionary is None:
             # The forward normalizes its own bank inside its projection launch.
             layout = hip_ops.own_bank_layout(bank, key_dtype)
-            result = hip_ops.shared_dictionary_attention_hip(
-                self, x, layout, dtype, raw_bank=(bank.raw_key, bank.raw_value)
+            return hip_ops.shared_dictionary_attention_hip(
+                self, x, layout, dtype, raw_bank=(bank.raw_key, bank.raw_value), residual=residual
             )
-        else:
-            layout = hip_ops.route_layout(*normalized_dictionary, key_dtype)
-            result = hip_ops.shared_dictionary_attention_hip(self, x, layout, dtype)
-        if not return_aux:
-            return result.output
-        return result.output, self._hip_aux(result.routed, dtype)
+        layout = hip_ops.route_layout(*normalized_dictionary, key_dtype)
+        return hip_ops.shared_dictionary_attention_hip(self, x, layout, dtype, residual=residual)
+
+    def _hip_inference_dtype(self, x: Tensor, bank: SharedDictionaryBank) -> torch.dtype | None:
+        """The compute dtype when a forward of ``x`` would run the HIP kernels
+        without autograd (else None)."""
+
+        cfg = self.config
+        if cfg.backend == "torch" or x.ndim != 3 or x.shape[-1] != cfg.model_dim:
+            return None
+        dtype = _compute_dtype(x, self.query.weight)
+        if resolve_backend(cfg.backend, (_Spec(x.is_cuda, dtype),)) != "hip":  # type: ignore[arg-type]
+            return None
+        if torch.is_grad_enabled() and (
+            x.requires_grad
+            or any(p.requires_grad for p in self.parameters())
+            or any(p.requires_grad for p in bank.parameters())
+        ):
+            return None
+        return dtype
 
     def _hip_aux(self, routed: Tensor, dtype: torch.dtype) -> DoubleAttentionAux:
         # routed: [B, T, 2, H, R] (fp16) -> [B, H, T, R] for queries and keys,
@@ -419,19 +450,50 @@ class DoubleAttentionBlock(nn.Module):
             nn.Dropout(dropout),
         )
 
-    def forward(
+    def _hip_block(
         self,
         x: Tensor,
         bank: SharedDictionaryBank,
-        *,
-        normalized_dictionary: tuple[Tensor, Tensor] | None = None,
+        normalized_dictionary: tuple[Tensor, Tensor] | None,
+    ) -> Tensor | None:
+        """The block on the HIP kernels, without autograd, or None.
+
+        LayerNorms run as the library's LayerNorm kernel; the residual adds
+        ride in the epilogues of the attention's output projection and of the
+        FFN's second linear; the FFN's GELU rides in its first linear.  The
+        Q-dictionary FFN keeps its PyTorch expansion.
+        """
+
+        from . import hip_ops
+
+        attention = self.attention
+        dtype = attention._hip_inference_dtype(x, bank)
+        if dtype is None or x.dtype != dtype or not isinstance(attention.output, nn.Linear):
+            return None
+        if self.training and any(isinstance(m, nn.Dropout) and m.p > 0 for m in self.feedforward):
+            return None
+        if normalized_dictionary is not None and any(t.requires_grad for t in normalized_dictionary):
+            return None
+        hip_ops.check_module_supported(attention.config)
+        x = x.contiguous()
+        norm1 = self.attention_norm
+        hidden = hip_ops.layer_norm_hip(x, norm1.weight, norm1.bias, norm1.eps)
+        x = attention._hip_call(hidden, bank, normalized_dictionary, dtype, residual=x).output
+        norm2 = self.feedforward_norm
+        normalized_x = hip_ops.layer_norm_hip(x, norm2.weight, norm2.bias, norm2.eps)
+        if attention.config.q_dictionary_feedforward:
+            return self._q_dictionary_feedforward(x, normalized_x, bank, normalized_dictionary)
+        first, second = self.feedforward[0], self.feedforward[2]
+        expanded = hip_ops.linear_hip(normalized_x, first.weight, first.bias, activation="gelu")
+        return hip_ops.linear_hip(expanded, second.weight, second.bias, residual=x)
+
+    def _q_dictionary_feedforward(
+        self,
+        x: Tensor,
+        normalized_x: Tensor,
+        bank: SharedDictionaryBank,
+        normalized_dictionary: tuple[Tensor, Tensor] | None,
     ) -> Tensor:
-        x = x + self.attention(
-            self.attention_norm(x), bank=bank, normalized_dictionary=normalized_dictionary
-        )
-        normalized_x = self.feedforward_norm(x)
-        if not self.attention.config.q_dictionary_feedforward:
-            return x + self.feedforward(normalized_x)
         if normalized_dictionary is None:
             dictionary_key, _ = bank.normalized(self.attention.config.eps)
         else:
@@ -441,6 +503,24 @@ class DoubleAttentionBlock(nn.Module):
             dictionary_key = dictionary_key.to(query.dtype)
         hidden = F.linear(query, dictionary_key.transpose(0, 1).contiguous())
         return x + self.feedforward(hidden)
+
+    def forward(
+        self,
+        x: Tensor,
+        bank: SharedDictionaryBank,
+        *,
+        normalized_dictionary: tuple[Tensor, Tensor] | None = None,
+    ) -> Tensor:
+        fused = self._hip_block(x, bank, normalized_dictionary)
+        if fused is not None:
+            return fused
+        x = x + self.attention(
+            self.attention_norm(x), bank=bank, normalized_dictionary=normalized_dictionary
+        )
+        normalized_x = self.feedforward_norm(x)
+        if not self.attention.config.q_dictionary_feedforward:
+            return x + self.feedforward(normalized_x)
+        return self._q_dictionary_feedforward(x, normalized_x, bank, normalized_dictionary)
 
 
 class DoubleAttentionStack(nn.Module):
@@ -527,6 +607,16 @@ class DoubleAttentionLM(nn.Module):
         self.lm_head = nn.Linear(config.model_dim, vocab_size, bias=False)
         self.lm_head.weight = self.token_embedding.weight
 
+    def _final_norm(self, hidden: Tensor) -> Tensor:
+        # On the HIP path (inference) the final LayerNorm is the library's kernel.
+        attention = self.stack.blocks[0].attention
+        needs_grad = torch.is_grad_enabled() and any(p.requires_grad for p in self.final_norm.parameters())
+        if not needs_grad and attention._hip_inference_dtype(hidden, self.stack.banks[0]) == hidden.dtype:
+            from . import hip_ops
+
+            return hip_ops.layer_norm_hip(hidden, self.final_norm.weight, self.final_norm.bias, self.final_norm.eps)
+        return self.final_norm(hidden)
+
     def forward(self, token_ids: Tensor, targets: Tensor | None = None) -> tuple[Tensor, Tensor | None]:
         if token_ids.ndim != 2:
             raise ValueError("token_ids must have shape [B, T]")
@@ -537,7 +627,7 @@ class DoubleAttentionLM(nn.Module):
             )
         positions = torch.arange(length, device=token_ids.device)
         hidden = self.token_embedding(token_ids) + self.position_embedding(positions)[None]
-        logits = self.lm_head(self.final_norm(self.stack(hidden)))
+        logits = self.lm_head(self._final_norm(self.stack(hidden)))
         loss = None
         if targets is not None:
             if targets.shape != token_ids.shape:

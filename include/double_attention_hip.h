@@ -22,6 +22,10 @@
  *                             + map combine                          src/double_attention/modules.py:265-272
  *   da_qkv_projection         _project_query_key + self.value        src/double_attention/modules.py:143-157, 212
  *   da_linear                 self.output                            src/double_attention/modules.py:117-121, 272
+ *   da_linear_ex              DoubleAttentionBlock.feedforward       src/double_attention/modules.py:318-330, 343-346
+ *                             + the block's residual adds
+ *   da_layer_norm             attention_norm / feedforward_norm /    src/double_attention/modules.py:311, 313, 440
+ *                             final_norm (nn.LayerNorm)
  *   da_shared_dictionary_attention_forward
  *                             SharedDictionaryAttention.forward      src/double_attention/modules.py:190-291
  */
@@ -186,6 +190,31 @@ int da_linear(const void* x, int64_t rows, int64_t in_features, const void* weig
               int64_t out_features, const void* bias, int bias_dtype, int dtype, void* out,
               da_stream_t stream);
 
+/* Activations of da_linear_ex. */
+#define DA_ACT_NONE 0
+#define DA_ACT_GELU 1               /* exact (erf) GELU, nn.GELU()'s default */
+
+/*
+ * The block's feed-forward linears with their neighbours fused in
+ * (modules.py:318-330, 343-346: Linear -> GELU -> Linear, then x + ...):
+ *   out = act(x @ weight^T + bias), rounded to dtype, then + residual
+ *   (residual: NULL or [rows, out_features] like out, added to the rounded
+ *   result and rounded again, as the unfused `x + linear(...)` does).
+ */
+int da_linear_ex(const void* x, int64_t rows, int64_t in_features, const void* weight, int64_t out_features,
+                 const void* bias, int bias_dtype, int dtype, int activation, const void* residual, void* out,
+                 da_stream_t stream);
+
+/*
+ * LayerNorm over the last dimension (nn.LayerNorm of modules.py:311, 313, 440;
+ * applied at :340, :344, :454): out = (x - mean) / sqrt(var + eps) * weight +
+ * bias, biased variance, fp32 statistics.  x, out: [rows, dim] of dtype;
+ * weight, bias: [dim] of param_dtype, or NULL (1 and 0).  dim a multiple of 8,
+ * at most 4096; pointers 16-byte aligned.
+ */
+int da_layer_norm(const void* x, int64_t rows, int64_t dim, const void* weight, const void* bias, int param_dtype,
+                  float eps, int dtype, void* out, da_stream_t stream);
+
 /* Whole SharedDictionaryAttention forward (modules.py:190-291). */
 typedef struct da_sda_forward_args {
   const void* x;            /* [batch, length, model_dim] */
@@ -221,6 +250,10 @@ typedef struct da_sda_forward_args {
   int route_variant;
   float silu_gain;
   float logit_scale;
+  /* Optional: [batch, length, model_dim] added to the output projection's
+   * rounded result (the block's residual `x + attention(...)`, modules.py:
+   * 338-342); needs wo and 16-byte alignment.  NULL: none. */
+  const void* residual;
 } da_sda_forward_args;
 
 /* Workspace layout (byte offsets, each 256-aligned):

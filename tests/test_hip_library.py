@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 13
+    assert len(names) == 15
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -130,3 +130,23 @@ def test_forward_rejects_small_workspace() -> None:
     assert "workspace" in h.da_last_error().decode()
     with pytest.raises(ValueError, match="workspace too small"):
         lib.check(-5, "forward")
+
+
+def test_linear_ex_and_layer_norm_reject_bad_arguments() -> None:
+    h = lib.get()
+    good = [_fake(), 64, 512, _fake(), 512, None, lib.DA_F32, lib.DA_BF16, lib.DA_ACT_GELU, None, _fake(), None]
+    bad_act = list(good)
+    bad_act[8] = 7
+    assert h.da_linear_ex(*bad_act) == -1
+    assert "activation" in h.da_last_error().decode()
+    bad_res = list(good)
+    bad_res[9] = (1 << 20) + 2
+    assert h.da_linear_ex(*bad_res) == -3
+    ln = [_fake(), 64, 512, None, None, lib.DA_F32, 1e-5, lib.DA_BF16, _fake(), None]
+    bad_dim = list(ln)
+    bad_dim[2] = 100
+    assert h.da_layer_norm(*bad_dim) == -2
+    assert "multiple of 8" in h.da_last_error().decode()
+    empty = list(ln)
+    empty[1] = 0
+    assert h.da_layer_norm(*empty) == 0

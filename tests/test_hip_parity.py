@@ -103,6 +103,39 @@ def test_linear(dtype, rows, k, n, bias) -> None:
     assert_parity(out, expected, label=f"linear {rows}x{k}->{n}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("rows", "k", "n"), [(33, 512, 1536), (4096, 512, 1536), (4096, 1536, 512), (100, 64, 68)])
+def test_linear_gelu_and_residual(dtype, rows, k, n) -> None:
+    # The block's FFN: GELU(x W1^T + b1), then h + (. W2^T + b2), against fp32.
+    device = _device()
+    g = torch.Generator().manual_seed(rows + k + n)
+    x = torch.randn(rows, k, generator=g).to(device, dtype)
+    w = (torch.randn(n, k, generator=g) * k ** -0.5).to(device, dtype)
+    b = torch.randn(n, generator=g).to(device, dtype)
+    residual = torch.randn(rows, n, generator=g).to(device, dtype)
+    act = da.hip_ops.linear_hip(x, w, b, activation="gelu")
+    ref = torch.nn.functional.gelu(x.float() @ w.float().T + b.float())
+    assert_parity(act, np32(ref), 1e-2, 3e-2, label=f"linear gelu {rows}x{k}x{n} {dtype}")
+    summed = da.hip_ops.linear_hip(x, w, b, residual=residual)
+    ref = residual.float() + (x.float() @ w.float().T + b.float()).to(dtype).float()
+    assert_parity(summed, np32(ref), 1e-2, 8e-2, label=f"linear residual {rows}x{k}x{n} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("rows", "dim", "affine"), [(4096, 512, True), (33, 64, True), (7, 1000, False), (5, 4096, True)])
+def test_layer_norm(dtype, rows, dim, affine) -> None:
+    device = _device()
+    g = torch.Generator().manual_seed(rows + dim)
+    x = (torch.randn(rows, dim, generator=g) * 3 + 1).to(device, dtype)
+    w = torch.randn(dim, generator=g).to(device, dtype) if affine else None
+    b = torch.randn(dim, generator=g).to(device, dtype) if affine else None
+    out = da.hip_ops.layer_norm_hip(x, w, b, 1e-5)
+    ref = torch.nn.functional.layer_norm(x.float(), (dim,), None if w is None else w.float(),
+                                         None if b is None else b.float(), 1e-5)
+    # Outputs reach about 10 (weights ~ N(0, 1)): half a bf16 ulp there is 0.03.
+    assert_parity(out, np32(ref), 5e-3, 8e-2, label=f"layer norm {rows}x{dim} {dtype}")
+
+
 @pytest.mark.parametrize(("batch", "length", "width"), [(2, 17, 64), (8, 512, 256), (1, 65, 512)])
 def test_qkv_projection(batch, length, width) -> None:
     device = _device()
