@@ -844,22 +844,31 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
     const int ya = static_cast<int>(start / L);
     const int yb = static_cast<int>((start + n - 1) / L);
     if (ya == yb) continue;   // whole in one run: stored or in that run's mix
-    float M = -INFINITY;
-    for (int y = ya; y <= yb; ++y) M = fmaxf(M, slot(y, start, 0)[QT * DS + ql]);
+    // One pass with a running maximum: each piece's loads (reference, row
+    // sum, values) are issued together and do not wait on the previous
+    // piece's arithmetic.
+    float M = -INFINITY, den = 0.f;
     f32x4 o[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) o[k] = zero4();
-    float den = 0.f;
     for (int y = ya; y <= yb; ++y) {
       const float* pc = slot(y, start, 0);
       const float m = pc[QT * DS + ql];
-      const float wl = (m == -INFINITY ? 0.f : exp2f(m - M)) * pc[QT * DS + QT + ql];
-      den += wl;
+      const float l = pc[QT * DS + QT + ql];
+      f32x4 v[NV];
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
-        const int d4 = (k * 64 + lane) * 4;
-        if (d4 < DS) o[k] += wl * *reinterpret_cast<const f32x4*>(pc + ql * DS + d4);
+        const int d4 = min((k * 64 + lane) * 4, DS - 4);
+        v[k] = *reinterpret_cast<const f32x4*>(pc + ql * DS + d4);
       }
+      if (m == -INFINITY) continue;   // a piece with every key masked
+      const float Mn = fmaxf(M, m);
+      const float f_old = M == -INFINITY ? 0.f : exp2f(M - Mn);
+      const float wl = exp2f(m - Mn) * l;
+      den = den * f_old + wl;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) o[k] = o[k] * f_old + v[k] * wl;
+      M = Mn;
     }
     const float w = (MULTI ? map_weight(p, s) : 1.f) * (den > 0.f ? 1.f / den : 0.f);
 #pragma unroll
