@@ -65,6 +65,14 @@ def _require_cuda(*tensors: Tensor) -> None:
             raise ValueError("HIP kernels require tensors on a ROCm device")
 
 
+def _aligned(t: Tensor) -> Tensor:
+    """``t`` contiguous at a 16-byte aligned address (views at odd offsets
+    are copied): the kernels load and store 16-byte chunks."""
+
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _round_up(v: int, m: int) -> int:
     return (v + m - 1) // m * m
 
@@ -242,7 +250,7 @@ def _route_forward(
     if rows_view.shape[0] == 0:
         return torch.empty(x.shape, dtype=x.dtype, device=x.device)
     if rows_view.stride(-1) != 1 or rows_view.stride(0) % 8 or rows_view.data_ptr() % 16:
-        rows_view = rows_view.contiguous()
+        rows_view = _aligned(rows_view)
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     flags = (
         (_lib.DA_ROUTE_NORMALIZE_INPUT if normalize_input else 0)
@@ -408,8 +416,8 @@ def _attention_forward(
         pad = (0, score_width - score_dim)
         q = torch.nn.functional.pad(q, pad)
         k = torch.nn.functional.pad(k, pad)
-    q = q.contiguous()
-    k = k.contiguous()
+    q = _aligned(q)
+    k = _aligned(k)
     vt = value_transposed(value, value_width)
     out = torch.empty(batch, maps, length, value_width, dtype=value.dtype, device=value.device)
     scales_c = scales.detach().contiguous()
@@ -510,15 +518,15 @@ def linear_hip(
         raise ValueError("x and weight must share a dtype")
     if activation not in (None, "gelu"):
         raise ValueError(f"unsupported activation {activation!r}")
-    rows = x.reshape(-1, x.shape[-1]).contiguous()
-    w = weight.detach().contiguous()
+    rows = _aligned(x.reshape(-1, x.shape[-1]))
+    w = _aligned(weight.detach())
     out = torch.empty(*x.shape[:-1], weight.shape[0], dtype=x.dtype, device=x.device)
     b = None if bias is None else bias.detach().contiguous()
     res = None
     if residual is not None:
         if residual.shape != out.shape or residual.dtype != x.dtype:
             raise ValueError("residual must match the output's shape and dtype")
-        res = residual.detach().contiguous()
+        res = _aligned(residual.detach())
     lib = _lib.get()
     bias_code = dtype_code(b.dtype) if b is not None else _lib.DA_F32
     if activation is None and res is None:
@@ -542,8 +550,8 @@ def layer_norm_hip(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: f
     _require_cuda(x)
     code = _half_code(x.dtype)
     dim = x.shape[-1]
-    xc = x.contiguous()
-    params = [t.detach().contiguous() for t in (weight, bias) if t is not None]
+    xc = _aligned(x)
+    params = [_aligned(t.detach()) for t in (weight, bias) if t is not None]
     if len({t.dtype for t in params}) > 1:
         raise ValueError("LayerNorm weight and bias must share a dtype")
     w = None if weight is None else params[0]
@@ -569,17 +577,18 @@ def qkv_projection_hip(
     batch, length, model_dim = x.shape
     width = query_weight.shape[0]
     code = _half_code(x.dtype)
-    xc = x.contiguous()
+    xc = _aligned(x)
     qk = torch.empty(batch, length, 2 * width, dtype=x.dtype, device=x.device)
     padded = _round_up(length, TOKEN_PAD)
     vt = torch.empty(batch, padded // 32, value_weight.shape[0], 32, dtype=x.dtype, device=x.device)
     b = None if value_bias is None else value_bias.detach().contiguous()
+    wq, wk, wv = (_aligned(w.detach()) for w in (query_weight, key_weight, value_weight))
     lib = _lib.get()
     _lib.check(
         lib.da_qkv_projection(
             xc.data_ptr(), batch * length, model_dim, length,
-            query_weight.contiguous().data_ptr(), key_weight.contiguous().data_ptr(), width,
-            value_weight.contiguous().data_ptr(), _ptr(b), value_weight.shape[0],
+            wq.data_ptr(), wk.data_ptr(), width,
+            wv.data_ptr(), _ptr(b), value_weight.shape[0],
             dtype_code(b.dtype) if b is not None else _lib.DA_F32, code,
             qk.data_ptr(), vt.data_ptr(), vt.stride(0), padded, _stream(x.device),
         ),
@@ -659,7 +668,7 @@ def shared_dictionary_attention_hip(
         t = t.detach()
         if t.dtype != dtype:
             t = t.to(dtype)
-        return t.contiguous()
+        return _aligned(t)
 
     xc = cast(x)
     wq = cast(module.query.weight)
@@ -699,7 +708,7 @@ def shared_dictionary_attention_hip(
     if residual is not None:
         if residual.shape != out.shape or residual.dtype != dtype:
             raise ValueError("residual must match the output's shape and dtype")
-        residual = residual.detach().contiguous()
+        residual = _aligned(residual.detach())
         args.residual = residual.data_ptr()
     variant = RouteVariant.of_config(config)
     args.route_variant = variant.flags()

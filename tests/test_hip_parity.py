@@ -552,6 +552,25 @@ def test_hip_backward_matches_torch_path() -> None:
         torch.testing.assert_close(p.grad, p_ref.grad, atol=1e-3, rtol=5e-2, msg=name)
 
 
+def test_module_and_ops_accept_misaligned_views() -> None:
+    # A contiguous view two bytes into its storage: the wrappers copy it to
+    # an aligned buffer; results match the aligned input exactly.
+    device = _device()
+    module = build_module("a1", torch.bfloat16, 9)
+    x = torch.randn(2, 40, 512, generator=torch.Generator().manual_seed(9)).to(device, torch.bfloat16)
+    storage = torch.empty(x.numel() + 1, device=device, dtype=torch.bfloat16)
+    shifted = storage[1:].view_as(x)
+    shifted.copy_(x)
+    assert shifted.data_ptr() % 16 != 0
+    with torch.inference_mode():
+        torch.testing.assert_close(module(shifted), module(x), rtol=0, atol=0)
+        w = torch.randn(64, 512, generator=torch.Generator().manual_seed(10)).to(device, torch.bfloat16)
+        torch.testing.assert_close(da.hip_ops.linear_hip(shifted, w, activation="gelu"),
+                                   da.hip_ops.linear_hip(x, w, activation="gelu"), rtol=0, atol=0)
+        torch.testing.assert_close(da.hip_ops.layer_norm_hip(shifted, None, None),
+                                   da.hip_ops.layer_norm_hip(x, None, None), rtol=0, atol=0)
+
+
 def test_unsupported_width_raises_on_gpu() -> None:
     device = _device()
     config = da.experiment_config("a1", routing_dim=96, backend="hip")
