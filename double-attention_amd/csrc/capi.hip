@@ -114,7 +114,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 9; }
+int da_abi_version(void) { return 10; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -216,6 +216,62 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
   a.out_stride_s = out_stride_s;
   da::launch_routed_attention(a, need > 0 ? workspace : nullptr, reinterpret_cast<hipStream_t>(stream));
   return check_launch("attention");
+}
+
+int da_routed_attention_backward(const void* query, const void* key, const void* query_t, const void* key_t,
+                                 const void* value, const void* grad_out, const void* grad_out_t,
+                                 const float* out_rowsum, const float* scales, int64_t batch, int64_t maps,
+                                 int64_t length, int64_t score_dim, int64_t value_dim, int flags, int qk_dtype,
+                                 int v_dtype, float* lse_workspace, float* grad_query, float* grad_key,
+                                 float* grad_value, float* grad_scales, da_stream_t stream) {
+  const bool types_ok = (qk_dtype == DA_F16 && (v_dtype == DA_BF16 || v_dtype == DA_F16)) ||
+                        (qk_dtype == DA_BF16 && v_dtype == DA_BF16);
+  if (!types_ok)
+    return fail(DA_ERR_UNSUPPORTED,
+                "attention backward: (qk_dtype, v_dtype) must be (F16,BF16), (F16,F16) or (BF16,BF16)");
+  if (flags & ~DA_ATTN_CAUSAL) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: unknown flag bits 0x%x", flags);
+  if (score_dim != 64 && score_dim != 128 && score_dim != 256)
+    return fail(DA_ERR_UNSUPPORTED, "attention backward: score_dim %lld not in {64,128,256}", (long long)score_dim);
+  if (!pow2_width(value_dim))
+    return fail(DA_ERR_UNSUPPORTED, "attention backward: value_dim %lld not in {64,128,256,512}", (long long)value_dim);
+  if (batch < 0 || length < 0 || maps < 1 || maps > 64 || batch * maps > 65535 || length > (1LL << 30))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: bad batch/maps/length");
+  if (batch == 0 || length == 0) return ok();
+  const void* ptrs[] = {query, key, query_t, key_t, value, grad_out, grad_out_t, out_rowsum, scales,
+                        lse_workspace, grad_query, grad_key, grad_value, grad_scales};
+  for (const void* ptr : ptrs)
+    if (!ptr) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: null pointer");
+  const void* vec[] = {query, key, query_t, key_t, value, grad_out, grad_out_t};
+  for (const void* ptr : vec)
+    if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: half-precision tensors must be 16-byte aligned");
+  const void* f32[] = {out_rowsum, scales, lse_workspace, grad_query, grad_key, grad_value, grad_scales};
+  for (const void* ptr : f32)
+    if (!aligned(ptr, 4)) return fail(DA_ERR_ALIGNMENT, "attention backward: fp32 tensors must be 4-byte aligned");
+  da::AttentionBwdArgs a;
+  a.q = query;
+  a.k = key;
+  a.qt = query_t;
+  a.kt = key_t;
+  a.v = value;
+  a.dout = grad_out;
+  a.doutt = grad_out_t;
+  a.lse2 = lse_workspace;
+  a.dvec = out_rowsum;
+  a.gamma = scales;
+  a.dq = grad_query;
+  a.dk = grad_key;
+  a.dv = grad_value;
+  a.dgamma = grad_scales;
+  a.B = static_cast<int>(batch);
+  a.S = static_cast<int>(maps);
+  a.T = static_cast<int>(length);
+  a.RP = static_cast<int>(score_dim);
+  a.D = static_cast<int>(value_dim);
+  a.causal = (flags & DA_ATTN_CAUSAL) != 0;
+  a.qk_dtype = qk_dtype;
+  a.v_dtype = v_dtype;
+  da::launch_routed_attention_backward(a, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("attention backward");
 }
 
 static int validate_gemm_common(const char* what, const void* x, int64_t rows, int64_t K, int dtype) {

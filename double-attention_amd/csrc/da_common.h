@@ -97,6 +97,13 @@ __device__ __forceinline__ void lane_pair16(float v, float& a, float& b) {
   a = __uint_as_float(r[0]);
   b = __uint_as_float(r[1]);
 }
+// Sum over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
 __device__ __forceinline__ float group_max(float v) {
   float a, b;
   lane_pair32(v, a, b);

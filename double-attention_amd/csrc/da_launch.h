@@ -81,6 +81,28 @@ struct AttentionArgs {
   int64_t out_stride_b, out_stride_t, out_stride_s;
 };
 
+// Backward of the outer attention, per score map (see attention_bwd.hip).
+struct AttentionBwdArgs {
+  const void* q;         // [B*S][T][RP] routed queries, qk_dtype
+  const void* k;         // [B*S][T][RP] routed keys
+  const void* qt;        // [B*S][Tp/32][RP][32] Q^T in 32-token tiles (zero past T)
+  const void* kt;        // [B*S][Tp/32][RP][32] K^T tiles
+  const void* v;         // [B][T][D] values, v_dtype
+  const void* dout;      // [B*S][T][D] output gradient, v_dtype
+  const void* doutt;     // [B*S][Tp/32][D][32] its 32-token tiles
+  float* lse2;           // [B*S][T] workspace: log2-sum-exp of each query row
+  const float* dvec;     // [B*S][T] rowsum(dO . O)
+  const float* gamma;    // [S] score scales
+  float* dq;             // [B*S][T][RP] accumulated (zeroed by the caller)
+  float* dk;             // [B*S][T][RP] written
+  float* dv;             // [B][T][D] accumulated (zeroed by the caller)
+  float* dgamma;         // [S] accumulated (zeroed by the caller)
+  int B, S, T, RP, D;
+  bool causal;
+  int qk_dtype, v_dtype;
+};
+void launch_routed_attention_backward(const AttentionBwdArgs& a, hipStream_t stream);
+
 struct GemmSegment {
   // D[i, j] = sum_k P[i, k] Q[j, k]; P rows may come from two stacked matrices
   // (rows [0, split) from p0, rows [split, I) from p1).

@@ -11,12 +11,6 @@ namespace da {
 
 constexpr int kLnRowsPerBlock = 4;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-  return v;
-}
-
 // Eight parameters of a chunk as floats (weight / bias of param dtype pdt).
 __device__ __forceinline__ void load_params8(const void* p, int pdt, int64_t i0, float (&o)[8], float dflt) {
   if (p == nullptr) {

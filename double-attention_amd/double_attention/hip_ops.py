@@ -443,21 +443,92 @@ def _attention_forward(
     return out if value_width == model_dim else out[..., :model_dim]
 
 
+BACKWARD_SCORE_WIDTHS = (64, 128, 256)
+
+
+def _padded_rows(t: Tensor, width: int) -> Tensor:
+    """Contiguous, 16-byte-aligned copy of ``t`` zero-padded on its last dim to ``width``."""
+
+    if t.shape[-1] != width:
+        t = torch.nn.functional.pad(t, (0, width - t.shape[-1]))
+    return _aligned(t)
+
+
+def _attention_backward(
+    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, out: Tensor, grad: Tensor, causal: bool
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of ``routed_attention_reference`` on the library's backward kernels.
+
+    The flash-attention backward of ``triton_kernels.py:2093-2263``: a pass for
+    each query row's log-sum-exp, then one workgroup per (sequence, map, 32-key
+    tile) forming dV, dK, dQ and d(scale) from the saved forward output.
+    """
+
+    batch, maps, length, score_dim = query.shape
+    model_dim = value.shape[-1]
+    score_width = _next_width(score_dim)
+    value_width = _next_width(model_dim)
+    rows = batch * maps
+    device = value.device
+    q = _padded_rows(query.detach(), score_width).view(rows, length, score_width)
+    k = _padded_rows(key.detach(), score_width).view(rows, length, score_width)
+    v = _padded_rows(value.detach(), value_width)
+    go = _padded_rows(grad.detach().to(value.dtype), value_width).view(rows, length, value_width)
+    qt = value_transposed(q)
+    kt = value_transposed(k)
+    got = value_transposed(go)
+    rowsum = (grad.detach().float() * out.detach().float()).sum(-1).reshape(rows, length).contiguous()
+    gamma = scales.detach().float().contiguous()
+    lse = torch.empty(rows, length, dtype=torch.float32, device=device)
+    dq = torch.zeros(rows, length, score_width, dtype=torch.float32, device=device)
+    dk = torch.empty(rows, length, score_width, dtype=torch.float32, device=device)
+    dv = torch.zeros(batch, length, value_width, dtype=torch.float32, device=device)
+    dg = torch.zeros(maps, dtype=torch.float32, device=device)
+    lib = _lib.get()
+    _lib.check(
+        lib.da_routed_attention_backward(
+            q.data_ptr(), k.data_ptr(), qt.data_ptr(), kt.data_ptr(), v.data_ptr(), go.data_ptr(), got.data_ptr(),
+            rowsum.data_ptr(), gamma.data_ptr(), batch, maps, length, score_width, value_width,
+            _lib.DA_ATTN_CAUSAL if causal else 0, _half_code(q.dtype), _half_code(value.dtype),
+            lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), _stream(device),
+        ),
+        "routed_attention_hip backward",
+    )
+    shape = (batch, maps, length, score_width)
+    return (
+        dq.view(shape)[..., :score_dim].to(query.dtype),
+        dk.view(shape)[..., :score_dim].to(key.dtype),
+        dv[..., :model_dim].to(value.dtype),
+        dg.to(scales.dtype),
+    )
+
+
+def _native_backward_supported(query: Tensor, value: Tensor) -> bool:
+    batch, maps, _, score_dim = query.shape
+    return score_dim <= BACKWARD_SCORE_WIDTHS[-1] and batch * maps <= 65535 and value.shape[-1] <= SUPPORTED_WIDTHS[-1]
+
+
 class _AttentionFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, query, key, value, scales, causal):  # type: ignore[override]
-        ctx.save_for_backward(query, key, value, scales)
+        out = _attention_forward(query, key, value, scales, causal)
+        ctx.save_for_backward(query, key, value, scales, out)
         ctx.causal = causal
-        return _attention_forward(query, key, value, scales, causal)
+        return out
 
     @staticmethod
     def backward(ctx, grad):  # type: ignore[override]
-        saved = ctx.saved_tensors
+        query, key, value, scales, out = ctx.saved_tensors
+        needs = ctx.needs_input_grad[:4]
+        if _native_backward_supported(query, value) and query.numel() and value.numel():
+            grads = _attention_backward(query, key, value, scales, out, grad, ctx.causal)
+            return (*[g if need else None for g, need in zip(grads, needs)], None)
+        # Score widths above 256: recompute through the fp32-softmax reference.
         with torch.enable_grad():
-            inputs = [t.detach().requires_grad_(t.requires_grad) for t in saved]
-            out = routed_attention_reference(*inputs, ctx.causal)
+            inputs = [t.detach().requires_grad_(need) for t, need in zip((query, key, value, scales), needs)]
+            ref = routed_attention_reference(*inputs, ctx.causal)
             wrt = [t for t in inputs if t.requires_grad]
-            grads = torch.autograd.grad(out, wrt, grad) if wrt else ()
+            grads = torch.autograd.grad(ref, wrt, grad) if wrt else ()
         it = iter(grads)
         return (*[next(it) if t.requires_grad else None for t in inputs], None)
 

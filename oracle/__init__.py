@@ -19,6 +19,10 @@ Functions and what pins them (each check is in ``tests/test_oracle.py``):
 * ``routed_attention``        first causal row = V[0]; all-equal keys ->
                               causal running mean; probabilities sum to one;
                               causal prefix invariance; brute-force loop.
+* ``routed_attention_backward``
+                              central finite differences of a scalar loss in
+                              fp64 for every input; dV = P^T dO sums over maps;
+                              zero output gradient -> zero gradients.
 * ``assemble_score_maps``     RMS-sum identity q'.k' = sum_g q_g.k_g / sqrt(g);
                               repeat layout; shapes.
 * ``shared_dictionary_attention`` / ``double_attention_lm``
@@ -38,6 +42,7 @@ from .sda import (
     l2_normalize,
     layer_norm,
     routed_attention,
+    routed_attention_backward,
     score_scale_from_log,
     shared_dictionary_attention,
 )
@@ -52,6 +57,7 @@ __all__ = [
     "l2_normalize",
     "layer_norm",
     "routed_attention",
+    "routed_attention_backward",
     "score_scale_from_log",
     "shared_dictionary_attention",
 ]

@@ -118,6 +118,42 @@ def routed_attention(
     return np.matmul(probs, value.astype(dt)[:, None])
 
 
+def routed_attention_backward(
+    query: np.ndarray,
+    key: np.ndarray,
+    value: np.ndarray,
+    scales: np.ndarray,
+    grad_out: np.ndarray,
+    causal: bool = True,
+):
+    """Gradients of :func:`routed_attention` for an output gradient ``grad_out``.
+
+    With ``P = softmax(scale_s q k^T)``: ``dV = sum_s P^T dO``,
+    ``dP = dO V^T``, ``dS = P (dP - rowsum(dP P))``, ``dq = scale_s dS k``,
+    ``dk = scale_s dS^T q``, ``dscale_s = sum dS (q k^T)`` -- the gradients the
+    reference's autograd path returns for ops.py:65-93 (its Triton backward,
+    triton_kernels.py:2093-2263, computes the same products).  Returns
+    ``(dq, dk, dv, dscales)``.
+    """
+
+    dt = query.dtype
+    raw = np.matmul(query, np.swapaxes(key, -1, -2))
+    scores = raw * np.asarray(scales, dtype=dt)[None, :, None, None]
+    if causal:
+        length = query.shape[-2]
+        future = np.triu(np.ones((length, length), dtype=bool), 1)
+        scores = np.where(future, -np.inf, scores)
+    probs = _softmax(scores, -1)
+    dv = np.matmul(np.swapaxes(probs, -1, -2), grad_out).sum(axis=1)
+    dp = np.matmul(grad_out, value.astype(dt)[:, None].swapaxes(-1, -2))
+    ds = probs * (dp - (dp * probs).sum(-1, keepdims=True))
+    sc = np.asarray(scales, dtype=dt)[None, :, None, None]
+    dq = np.matmul(ds, key) * sc
+    dk = np.matmul(np.swapaxes(ds, -1, -2), query) * sc
+    dscales = (ds * np.where(np.isfinite(scores), raw, 0)).sum(axis=(0, 2, 3))
+    return dq, dk, dv.astype(dt), dscales
+
+
 def assemble_score_maps(query: np.ndarray, key: np.ndarray, outer_maps: int):
     """Branch-to-map assembly (ops.py:96-139): identity, RMS-sum groups or repeats."""
 

@@ -329,6 +329,73 @@ def test_attention_long_context_properties() -> None:
         torch.testing.assert_close(out[0, 0, 0].float(), v[0, 0].float(), atol=2e-2, rtol=0)
 
 
+# Gradients of the outer attention: the kernel rounds P and dS to the input
+# precision before the last products (as the reference's Triton backward
+# does), so the bound is rel-L2 <= 1e-2 per gradient (fp16: 5e-3) against
+# the fp32 oracle on the same rounded inputs; max-abs is taken relative to
+# each gradient's largest entry.  The scale gradient sums dS * (q . k) over
+# every (query, key) pair while each row of dS sums to zero, so the rounding
+# of the saved output O inside rowsum(dO . O) does not cancel: it is held to
+# rel-L2 <= 3e-2 (fp16: 1e-2).  The reference's own bf16 autograd path
+# (ops.py:65-93 under torch autograd) measures 1.3e-2 on the first case.
+BACKWARD_CASES = [
+    # (batch, maps, length, score_dim, value_dim, causal)
+    (2, 3, 77, 64, 64, True),
+    (1, 2, 130, 128, 256, False),
+    (2, 4, 200, 256, 512, True),
+    (1, 1, 33, 40, 96, True),
+    (3, 2, 64, 128, 128, False),
+    (1, 2, 1, 64, 64, True),
+]
+
+
+@pytest.mark.parametrize("dtypes", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                    (torch.float16, torch.bfloat16)], ids=["bf16", "fp16", "fp16qk-bf16v"])
+@pytest.mark.parametrize("case", BACKWARD_CASES, ids=lambda c: "b{}s{}t{}r{}d{}{}".format(*c[:5], "c" if c[5] else ""))
+def test_routed_attention_backward(case, dtypes) -> None:
+    device = _device()
+    batch, maps, length, score_dim, value_dim, causal = case
+    qk_dtype, v_dtype = dtypes
+    q = unit_rows((batch, maps, length, score_dim), qk_dtype, device, 20).requires_grad_()
+    k = unit_rows((batch, maps, length, score_dim), qk_dtype, device, 21).requires_grad_()
+    g = torch.Generator().manual_seed(22)
+    v = torch.randn(batch, length, value_dim, generator=g).to(device, v_dtype).requires_grad_()
+    s = torch.linspace(4.0, 16.0, maps, device=device).requires_grad_()
+    w = torch.randn(batch, maps, length, value_dim, generator=g).to(device, v_dtype)
+    out = da.routed_attention_hip(q, k, v, s, causal)
+    out.backward(w)
+    expected = oracle.routed_attention_backward(np32(q), np32(k), np32(v), np32(s), np32(w), causal)
+    rel = 5e-3 if qk_dtype == torch.float16 and v_dtype == torch.float16 else 1e-2
+    label = f"attention backward {case} {qk_dtype}/{v_dtype}"
+    for name, grad, exp in zip("qkvs", (q.grad, k.grad, v.grad, s.grad), expected):
+        assert grad is not None and grad.dtype == {"q": qk_dtype, "k": qk_dtype, "v": v_dtype, "s": torch.float32}[name]
+        scale = float(np.abs(exp).max())
+        if scale < 1e-6:
+            # One key per row (length 1): P = 1, so dS and with it dq, dk and
+            # dscale vanish; only the rounding of rowsum(dO . O) is left.
+            assert float(np32(grad).__abs__().max()) <= 1e-3, f"{label} d{name}"
+            continue
+        if name == "s":
+            assert_parity(grad, exp, 3 * rel, max(6e-2 * scale, 1e-6), f"{label} d{name}")
+        else:
+            assert_parity(grad, exp, rel, max(2e-2 * scale, 1e-6), f"{label} d{name}")
+
+
+def test_routed_attention_backward_wide_scores_fall_back() -> None:
+    # Score widths above 256 take the fp32 recompute path and still match.
+    device = _device()
+    q = unit_rows((1, 2, 50, 300), torch.bfloat16, device, 23).requires_grad_()
+    k = unit_rows((1, 2, 50, 300), torch.bfloat16, device, 24).requires_grad_()
+    v = torch.randn(1, 50, 64, generator=torch.Generator().manual_seed(25)).to(device, torch.bfloat16).requires_grad_()
+    s = torch.tensor([6.0, 10.0], device=device, requires_grad=True)
+    w = torch.randn(1, 2, 50, 64, generator=torch.Generator().manual_seed(26)).to(device, torch.bfloat16)
+    da.routed_attention_hip(q, k, v, s, True).backward(w)
+    expected = oracle.routed_attention_backward(np32(q), np32(k), np32(v), np32(s), np32(w), True)
+    for name, grad, exp in zip("qkvs", (q.grad, k.grad, v.grad, s.grad), expected):
+        bound = 3e-2 if name == "s" else 1e-2
+        assert_parity(grad, exp, bound, max(3 * bound * float(np.abs(exp).max()), 1e-6), f"fallback d{name}")
+
+
 # ---------------------------------------------------------------- whole module
 
 

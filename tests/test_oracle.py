@@ -170,10 +170,10 @@ def test_route_brute_force_loop() -> None:
 # ---------------------------------------------------------------- outer attention
 
 
-def _qkv(b=2, s=3, t=6, r=4, d=5):
-    q = RNG.standard_normal((b, s, t, r))
-    k = RNG.standard_normal((b, s, t, r))
-    v = RNG.standard_normal((b, t, d))
+def _qkv(b=2, s=3, t=6, r=4, d=5, rng=RNG):
+    q = rng.standard_normal((b, s, t, r))
+    k = rng.standard_normal((b, s, t, r))
+    v = rng.standard_normal((b, t, d))
     return q, k, v
 
 
@@ -222,6 +222,48 @@ def test_attention_matches_textbook_softmax_per_row() -> None:
         for t in range(5):
             w = scipy_softmax(scales[s] * (k[0, s, : t + 1] @ q[0, s, t]))
             np.testing.assert_allclose(out[0, s, t], w @ v[0, : t + 1], rtol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_backward_matches_finite_differences(causal: bool) -> None:
+    # Loss = sum(W * out) for a fixed random W, so d loss / d out = W; central
+    # differences in fp64 of every input element pin each gradient, including
+    # the scale gradient and the map sum of dV.
+    rng = np.random.default_rng(7)
+    q, k, v = _qkv(b=2, s=2, t=5, r=3, d=4, rng=rng)
+    scales = np.array([1.7, 0.6])
+    w = rng.standard_normal((2, 2, 5, 4))
+    dq, dk, dv, ds = oracle.routed_attention_backward(q, k, v, scales, w, causal)
+
+    def loss(q_, k_, v_, s_):
+        return float((oracle.routed_attention(q_, k_, v_, s_, causal) * w).sum())
+
+    h = 1e-6
+    for arr, grad, idx in ((q, dq, 0), (k, dk, 1), (v, dv, 2), (scales, ds, 3)):
+        numeric = np.zeros_like(arr)
+        for pos in np.ndindex(arr.shape):
+            args = [q, k, v, scales]
+            plus, minus = arr.copy(), arr.copy()
+            plus[pos] += h
+            minus[pos] -= h
+            args[idx] = plus
+            up = loss(*args)
+            args[idx] = minus
+            numeric[pos] = (up - loss(*args)) / (2 * h)
+        np.testing.assert_allclose(grad, numeric, rtol=1e-6, atol=1e-8)
+
+
+def test_attention_backward_zero_gradient_and_value_map_sum() -> None:
+    q, k, v = _qkv(b=1, s=3, t=6, r=4, d=5)
+    scales = np.array([1.0, 2.0, 3.0])
+    zero = oracle.routed_attention_backward(q, k, v, scales, np.zeros((1, 3, 6, 5)), True)
+    for g in zero:
+        assert not np.any(g)
+    w = RNG.standard_normal((1, 3, 6, 5))
+    _, _, dv, _ = oracle.routed_attention_backward(q, k, v, scales, w, True)
+    per_map = [oracle.routed_attention_backward(q[:, s:s + 1], k[:, s:s + 1], v, scales[s:s + 1], w[:, s:s + 1], True)[2]
+               for s in range(3)]
+    np.testing.assert_allclose(dv, sum(per_map), rtol=1e-12)
 
 
 # ---------------------------------------------------------------- score maps
