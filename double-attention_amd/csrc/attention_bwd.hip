@@ -1,22 +1,29 @@
 // Backward of the outer routed attention (ops.py:65-93), per score map:
-// given the forward's inputs, the per-row log-sum-exp and dO, it forms
-//   dV = P^T dO,  dP = dO V^T,  dS = P (dP - rowsum(dO . O)),
+// given the forward's inputs and output O and dO, it forms
+//   dV = sum_s P^T dO,  dP = dO V^T,  dS = P (dP - rowsum(dO . O)),
 //   dQ = gamma dS K,  dK = gamma dS^T Q,  dgamma = sum dS . (Q K^T),
 // the flash-attention backward (the reference's Triton kernels compute the
 // same products, triton_kernels.py:814-1278 and 2093-2263).
 //
-// attention_lse_kernel: per query row, LSE2 = m + log2(l) over its keys with
-// p = 2^(s gamma log2e - LSE2), one wave per 32 queries, key fragments read
-// straight from global memory.
+// Three launches:
+//   attention_bwd_prep_kernel  one workgroup per (sequence x map, 32-token
+//       tile): Q^T, K^T and dO^T in 32-token tiles (zero past the length),
+//       rowsum(dO . O), and zeroes of the accumulated gradients;
+//   attention_lse_kernel       one workgroup per 32-query tile; its four
+//       waves split the key tiles and merge (max, sum) through LDS into
+//       LSE2 = m + log2(l) with p = 2^(s gamma log2e - LSE2);
+//   attention_bwd_kernel       one workgroup per (64-key tile, run of query
+//       tiles); wave w owns keys 16w..16w+15 of the tile.
 //
-// attention_bwd_kernel: one workgroup per (sequence x map, 32-key tile), four
-// waves.  The key tile (and each wave's share of V and K^T) stays resident;
-// the workgroup walks the query tiles that see its keys, staging Q, Q^T, dO
-// and dO^T tiles in LDS.  Every wave forms the full 32 x 32 S^T and P^T; the
-// dP^T contraction over the value features is split over the waves and summed
-// through LDS; P^T, dS^T and dS go through LDS into the layouts the last three
-// products read.  dV (shared by the maps) and dQ (shared by the key tiles)
-// accumulate with fp32 atomics, dK is stored once.
+// In the main kernel S = Q K^T and dP = dO V^T come out of the MFMA with
+// lane (c, g) holding queries 4g..4g+3 and 16+4g..16+4g+3 of key c.  Those
+// eight values are exactly the eight contraction elements a lane supplies to
+// a 16x16x32 MFMA whose contraction runs over the 32 queries in that order,
+// so P and dS feed dV += P^T dO and dK += dS^T Q straight from registers; the
+// B operands read the matching two 8-byte pieces of the dO^T and Q^T tile
+// rows.  Only dQ = dS K needs dS with the query as the row, through LDS.
+// dQ accumulates over key tiles and dK, dV over query runs (and dV over the
+// maps) with fp32 atomics.
 #include "da_common.h"
 #include "da_launch.h"
 #include "da_tile.h"
@@ -25,46 +32,128 @@ namespace da {
 
 namespace {
 
-constexpr int kBwdTile = 32;   // keys per workgroup, queries per step
+constexpr int kQTile = 32;    // queries per step (and tokens per transposed tile)
+constexpr int kKTile = 64;    // keys per workgroup (16 per wave)
 
 struct BwdParams {
   const void* q;        // [BS][T][RP] routed queries (score dtype)
   const void* k;        // [BS][T][RP] routed keys
-  const void* qt;       // [BS][Tp/32][RP][32] Q^T tiles
-  const void* kt;       // [BS][Tp/32][RP][32] K^T tiles
   const void* v;        // [B][T][D] values
+  const void* out;      // [BS][T][D] forward output
   const void* dout;     // [BS][T][D] output gradient
-  const void* doutt;    // [BS][Tp/32][D][32] its transposed tiles
-  float* lse2;          // [BS][T] (written by the LSE pass)
-  const float* dvec;    // [BS][T] rowsum(dO . O)
+  void* qt;             // [BS][Tp/32][RP][32] Q^T tiles (workspace)
+  void* kt;             // [BS][Tp/32][RP][32] K^T tiles
+  void* doutt;          // [BS][Tp/32][D][32] dO^T tiles
+  float* lse2;          // [BS][T]
+  float* dvec;          // [BS][T] rowsum(dO . O)
   const float* gamma;   // [S] score scales
-  float* dq;            // [BS][T][RP] (accumulated)
+  float* dq;            // [BS][T][RP]
   float* dk;            // [BS][T][RP]
-  float* dv;            // [B][T][D] (accumulated)
-  float* dgamma;        // [S] (accumulated)
+  float* dv;            // [B][T][D]
+  float* dgamma;        // [S]
   int S, T, Tp, RP, D;
   int causal;
+  int qchunk;           // query tiles per workgroup of the main kernel
+  int n_chunks;         // query runs per key tile
 };
 
-// LDS tile pitches (bytes): row-major tiles get one 16-byte pad chunk per
-// row, transposed 32-token tiles a 16-byte pad on their 64-byte rows, so the
-// 16-byte fragment reads of 8 consecutive lanes hit distinct bank groups.
+// LDS pitches (bytes): row-major tiles get one 16-byte pad chunk per row,
+// transposed 32-token tiles a 16-byte pad on their 64-byte rows.
 __host__ __device__ constexpr int row_pitch(int width) { return width * 2 + 16; }
 constexpr int kTPitch = 80;
+constexpr int kDsPitch = kKTile * 2 + 16;
+
+// Rows [t0, t0+32) of a [len][W] tensor, transposed into a [W][32] tile at
+// `dst` (zero for tokens >= len).  Uses `lds` (32 * row_pitch(W) bytes).
+template <typename T, int W>
+__device__ __forceinline__ void transpose_tile(const T* src, int t0, int len, T* dst, char* lds) {
+  constexpr int P = row_pitch(W);
+  const int tid = static_cast<int>(threadIdx.x);
+  __syncthreads();   // the previous user of `lds` is done
+  for (int ch = tid; ch < kQTile * W / 8; ch += 256) {
+    const int r = ch / (W / 8), c8 = (ch % (W / 8)) * 8;
+    u32x4 v = load16B(src + static_cast<int64_t>(min(t0 + r, len - 1)) * W + c8);
+    if (t0 + r >= len) v = u32x4{0u, 0u, 0u, 0u};
+    store16B(lds + r * P + c8 * 2, v);
+  }
+  __syncthreads();
+  for (int ch = tid; ch < W * 4; ch += 256) {
+    const int f = ch / 4, t8 = (ch % 4) * 8;
+    uint16_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = *reinterpret_cast<const uint16_t*>(lds + (t8 + j) * P + f * 2);
+    u32x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = static_cast<uint32_t>(e[2 * j]) | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
+    store16B(dst + f * kQTile + t8, v);
+  }
+}
 
 }  // namespace
+
+template <typename TQ, typename TV, int RP, int D>
+__global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
+  constexpr int WMAX = RP > D ? RP : D;
+  __shared__ __attribute__((aligned(16))) char lds[kQTile * row_pitch(WMAX)];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = lane_id();
+  const int wave = uniform_wave();
+  const int bs = static_cast<int>(blockIdx.y);
+  const int b = bs / p.S, s = bs - b * p.S;
+  const int tile = static_cast<int>(blockIdx.x);
+  const int t0 = tile * kQTile;
+  const int64_t tiles = p.Tp / kQTile;
+  const int64_t rows = static_cast<int64_t>(bs) * p.T;
+
+  transpose_tile<TQ, RP>(static_cast<const TQ*>(p.q) + rows * RP, t0, p.T,
+                         static_cast<TQ*>(p.qt) + (bs * tiles + tile) * RP * kQTile, lds);
+  transpose_tile<TQ, RP>(static_cast<const TQ*>(p.k) + rows * RP, t0, p.T,
+                         static_cast<TQ*>(p.kt) + (bs * tiles + tile) * RP * kQTile, lds);
+  transpose_tile<TV, D>(static_cast<const TV*>(p.dout) + rows * D, t0, p.T,
+                        static_cast<TV*>(p.doutt) + (bs * tiles + tile) * D * kQTile, lds);
+  if (t0 >= p.T) return;   // padding tiles only need their zeroed transposes
+
+  // rowsum(dO . O): wave w takes rows w, w+4, ...
+  const TV* dob = static_cast<const TV*>(p.dout) + rows * D;
+  const TV* ob = static_cast<const TV*>(p.out) + rows * D;
+  for (int r = wave; r < kQTile; r += 4) {
+    const int t = t0 + r;
+    if (t >= p.T) break;
+    float acc = 0.f;
+    for (int d = lane * 8; d < D; d += 512) {
+      const typename Elem<TV>::v8 x = load8(dob + static_cast<int64_t>(t) * D + d);
+      const typename Elem<TV>::v8 y = load8(ob + static_cast<int64_t>(t) * D + d);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc += static_cast<float>(x[j]) * static_cast<float>(y[j]);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) p.dvec[rows + t] = acc;
+  }
+
+  // Zero the accumulated gradients of this tile's rows.
+  const int n_rows = min(kQTile, p.T - t0);
+  const f32x4 z = zero4();
+  for (int i = tid; i < n_rows * RP / 4; i += 256) {
+    reinterpret_cast<f32x4*>(p.dq + (rows + t0) * RP)[i] = z;
+    reinterpret_cast<f32x4*>(p.dk + (rows + t0) * RP)[i] = z;
+  }
+  if (s == 0)
+    for (int i = tid; i < n_rows * D / 4; i += 256)
+      reinterpret_cast<f32x4*>(p.dv + (static_cast<int64_t>(b) * p.T + t0) * D)[i] = z;
+  if (bs == 0 && tile == 0 && tid < p.S) p.dgamma[tid] = 0.f;
+}
 
 template <typename TQ, int RP>
 __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
   typedef typename Elem<TQ>::v8 q8;
   constexpr int KS = RP / 32;
+  __shared__ float part[4][2][kQTile];
   const int lane = lane_id();
   const int c = lane & 15, g = lane >> 4;
+  const int wave = uniform_wave();
   const int bs = static_cast<int>(blockIdx.y);
-  const int q0 = (static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x) / 64) * kBwdTile;
-  if (q0 >= p.T) return;   // whole waves
-  const int s = bs % p.S;
-  const float sc = p.gamma[s] * kLog2e;
+  const int q0 = static_cast<int>(blockIdx.x) * kQTile;
+  const float sc = p.gamma[bs % p.S] * kLog2e;
   const TQ* qb = static_cast<const TQ*>(p.q) + static_cast<int64_t>(bs) * p.T * RP;
   const TQ* kbase = static_cast<const TQ*>(p.k) + static_cast<int64_t>(bs) * p.T * RP;
   q8 qf[2][KS];
@@ -74,8 +163,8 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
     for (int kk = 0; kk < KS; ++kk)
       qf[cb][kk] = load8(qb + static_cast<int64_t>(min(q0 + cb * 16 + c, p.T - 1)) * RP + kk * 32 + 8 * g);
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  const int k_end = p.causal ? min(q0 + kBwdTile, p.T) : p.T;
-  for (int k0 = 0; k0 < k_end; k0 += kBwdTile) {
+  const int k_end = p.causal ? min(q0 + kQTile, p.T) : p.T;
+  for (int k0 = wave * kQTile; k0 < k_end; k0 += 4 * kQTile) {
     f32x4 st[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -118,9 +207,22 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
   if (g == 0) {
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const int q = q0 + cb * 16 + c;
-      if (q < p.T) p.lse2[static_cast<int64_t>(bs) * p.T + q] = m[cb] + log2f(l[cb]);
+      part[wave][0][cb * 16 + c] = m[cb];
+      part[wave][1][cb * 16 + c] = l[cb];
     }
+  }
+  __syncthreads();
+  const int tid = static_cast<int>(threadIdx.x);
+  if (tid < kQTile) {
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mm = fmaxf(mm, part[w][0][tid]);
+    float ll = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      if (part[w][0][tid] != -INFINITY) ll += part[w][1][tid] * exp2f(part[w][0][tid] - mm);
+    const int q = q0 + tid;
+    if (q < p.T) p.lse2[static_cast<int64_t>(bs) * p.T + q] = mm + log2f(ll);
   }
 }
 
@@ -128,26 +230,21 @@ template <typename TQ, typename TV, int RP, int D>
 __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   typedef typename Elem<TQ>::v8 q8;
   typedef typename Elem<TV>::v8 v8;
-  constexpr int KS = RP / 32;                  // 32-deep steps over the score width
-  constexpr int DC = D / 32;                   // 32-deep chunks of the value width
-  constexpr int MYDC = (DC + 3) / 4;           // chunks per wave (round robin)
-  constexpr int DB = D / 16 / 4;               // 16-wide dV column blocks per wave
-  constexpr int RB = RP / 16 / 4;              // 16-wide dK / dQ column blocks per wave
-  static_assert(D / 16 % 4 == 0 && RP / 16 % 4 == 0, "widths of at least 64");
-  constexpr int KP = row_pitch(RP), VP = row_pitch(D);
-  // LDS: key tile, Q tile, Q^T tile, dO tile, dO^T tile, P^T, dS^T, dS,
-  // the dP^T partials of the four waves, LSE2 and rowsum rows.
-  constexpr int OFF_K = 0;
-  constexpr int OFF_Q = OFF_K + kBwdTile * KP;
-  constexpr int OFF_QT = OFF_Q + kBwdTile * KP;
+  typedef typename Elem<TQ>::v4 q4;
+  typedef typename Elem<TV>::v4 v4;
+  constexpr int KS = RP / 32;       // 32-deep steps over the score width
+  constexpr int DC = D / 32;        // 32-deep steps over the value width
+  constexpr int NV = D / 16;        // 16-wide dV column blocks
+  constexpr int NK = RP / 16;       // 16-wide dK column blocks
+  constexpr int RB = RP / 64;       // dQ column blocks per wave
+  constexpr int QP = row_pitch(RP), VP = row_pitch(D);
+  constexpr int OFF_Q = 0;
+  constexpr int OFF_QT = OFF_Q + kQTile * QP;
   constexpr int OFF_DO = OFF_QT + RP * kTPitch;
-  constexpr int OFF_DOT = OFF_DO + kBwdTile * VP;
-  constexpr int OFF_PT = OFF_DOT + D * kTPitch;
-  constexpr int OFF_DST = OFF_PT + kBwdTile * kTPitch;
-  constexpr int OFF_DS = OFF_DST + kBwdTile * kTPitch;
-  constexpr int OFF_RED = OFF_DS + kBwdTile * kTPitch;
-  constexpr int OFF_ROW = OFF_RED + 4 * 64 * 16 * 4;
-  constexpr int LDS_BYTES = OFF_ROW + 2 * kBwdTile * 4;
+  constexpr int OFF_DOT = OFF_DO + kQTile * VP;
+  constexpr int OFF_DS = OFF_DOT + D * kTPitch;
+  constexpr int OFF_ROW = OFF_DS + kQTile * kDsPitch;
+  constexpr int LDS_BYTES = OFF_ROW + 2 * kQTile * 4;
   static_assert(LDS_BYTES <= 160 * 1024, "the tiles fit the LDS");
   __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
 
@@ -157,254 +254,208 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   const int tid = static_cast<int>(threadIdx.x);
   const int bs = static_cast<int>(blockIdx.y);
   const int b = bs / p.S, s = bs - b * p.S;
-  const int k0 = static_cast<int>(blockIdx.x) * kBwdTile;
+  const int kt = static_cast<int>(blockIdx.x) / p.n_chunks;
+  const int chunk = static_cast<int>(blockIdx.x) - kt * p.n_chunks;
+  const int k0 = kt * kKTile;
+  const int n_qt = (p.T + kQTile - 1) / kQTile;
+  const int qt_begin = (p.causal ? k0 / kQTile : 0) + chunk * p.qchunk;
+  if (qt_begin >= n_qt) return;   // whole workgroup, before any barrier
+  const int qt_end = min(n_qt, qt_begin + p.qchunk);
   const float gamma = p.gamma[s];
   const float sc = gamma * kLog2e;
+  const int64_t tiles = p.Tp / kQTile;
   const TQ* qb = static_cast<const TQ*>(p.q) + static_cast<int64_t>(bs) * p.T * RP;
   const TQ* kbase = static_cast<const TQ*>(p.k) + static_cast<int64_t>(bs) * p.T * RP;
-  const TQ* qtb = static_cast<const TQ*>(p.qt) + static_cast<int64_t>(bs) * p.Tp * RP;
-  const TQ* ktb = static_cast<const TQ*>(p.kt) + static_cast<int64_t>(bs) * p.Tp * RP;
+  const TQ* qtb = static_cast<const TQ*>(p.qt) + bs * tiles * RP * kQTile;
+  const TQ* ktb = static_cast<const TQ*>(p.kt) + bs * tiles * RP * kQTile;
   const TV* vb = static_cast<const TV*>(p.v) + static_cast<int64_t>(b) * p.T * D;
   const TV* dob = static_cast<const TV*>(p.dout) + static_cast<int64_t>(bs) * p.T * D;
-  const TV* dotb = static_cast<const TV*>(p.doutt) + static_cast<int64_t>(bs) * p.Tp * D;
+  const TV* dotb = static_cast<const TV*>(p.doutt) + bs * tiles * D * kQTile;
 
-  // Resident: the key tile (rows past T repeat row T-1; their P is masked to
-  // zero), this wave's V chunks (A operands of dP^T) and K^T blocks (B
-  // operands of dQ).
-  for (int ch = tid; ch < kBwdTile * RP / 8; ch += 256) {
-    const int r = ch / (RP / 8), c8 = (ch % (RP / 8)) * 8;
-    *reinterpret_cast<u32x4*>(lds + OFF_K + r * KP + c8 * 2) =
-        *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(min(k0 + r, p.T - 1)) * RP + c8);
-  }
-  v8 vf[MYDC][2];
+  // Resident per wave: its 16 keys as B operands of S (K rows) and dP
+  // (V rows), and K^T of all 64 keys for its dQ columns.
+  const int kw = k0 + wave * 16;
+  const int krow = min(kw + c, p.T - 1);
+  q8 kf[KS];
 #pragma unroll
-  for (int j = 0; j < MYDC; ++j) {
-    const int chunk = min(wave + 4 * j, DC - 1);   // waves past the last chunk repeat it (unused)
+  for (int kk = 0; kk < KS; ++kk) kf[kk] = load8(kbase + static_cast<int64_t>(krow) * RP + kk * 32 + 8 * g);
+  v8 vf[DC];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-      vf[j][kb] = load8(vb + static_cast<int64_t>(min(k0 + kb * 16 + c, p.T - 1)) * D + chunk * 32 + 8 * g);
-  }
-  q8 ktf[RB];
+  for (int j = 0; j < DC; ++j) vf[j] = load8(vb + static_cast<int64_t>(krow) * D + j * 32 + 8 * g);
+  q8 ktf[RB][2];
 #pragma unroll
-  for (int j = 0; j < RB; ++j) {
-    const int r = (wave + 4 * j) * 16 + c;
-    ktf[j] = load8(ktb + (static_cast<int64_t>(k0 / 32) * RP + r) * 32 + 8 * g);
-  }
+  for (int j = 0; j < RB; ++j)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      ktf[j][ks] = load8(ktb + ((k0 / kQTile + ks) * RP + (wave + 4 * j) * 16 + c) * static_cast<int64_t>(kQTile) + 8 * g);
 
-  f32x4 dv_acc[2][DB], dk_acc[2][RB];
+  f32x4 dv_acc[NV], dk_acc[NK];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int j = 0; j < NV; ++j) dv_acc[j] = zero4();
 #pragma unroll
-    for (int j = 0; j < DB; ++j) dv_acc[kb][j] = zero4();
-#pragma unroll
-    for (int j = 0; j < RB; ++j) dk_acc[kb][j] = zero4();
-  }
+  for (int j = 0; j < NK; ++j) dk_acc[j] = zero4();
   float dgamma = 0.f;
-  const int n_qt = (p.T + kBwdTile - 1) / kBwdTile;
-  const int qt_first = p.causal ? static_cast<int>(blockIdx.x) : 0;
-  float* red = reinterpret_cast<float*>(lds + OFF_RED);
-  float* rowv = reinterpret_cast<float*>(lds + OFF_ROW);
+  const float* rowv = reinterpret_cast<const float*>(lds + OFF_ROW);
+  const int key = kw + c;
 
-  for (int qt = qt_first; qt < n_qt; ++qt) {
-    const int q0 = qt * kBwdTile;
+  for (int qt = qt_begin; qt < qt_end; ++qt) {
+    const int q0 = qt * kQTile;
     __syncthreads();   // the previous step is done with every staged tile
-    for (int ch = tid; ch < kBwdTile * RP / 8; ch += 256) {
+    for (int ch = tid; ch < kQTile * RP / 8; ch += 256) {
       const int r = ch / (RP / 8), c8 = (ch % (RP / 8)) * 8;
-      *reinterpret_cast<u32x4*>(lds + OFF_Q + r * KP + c8 * 2) =
-          *reinterpret_cast<const u32x4*>(qb + static_cast<int64_t>(min(q0 + r, p.T - 1)) * RP + c8);
+      store16B(lds + OFF_Q + r * QP + c8 * 2, load16B(qb + static_cast<int64_t>(min(q0 + r, p.T - 1)) * RP + c8));
     }
-    for (int ch = tid; ch < RP * 4; ch += 256) {
-      const int r = ch / 4, c8 = (ch % 4) * 8;
-      *reinterpret_cast<u32x4*>(lds + OFF_QT + r * kTPitch + c8 * 2) =
-          *reinterpret_cast<const u32x4*>(qtb + (static_cast<int64_t>(qt) * RP + r) * 32 + c8);
-    }
-    for (int ch = tid; ch < kBwdTile * D / 8; ch += 256) {
+    for (int ch = tid; ch < RP * 4; ch += 256)
+      store16B(lds + OFF_QT + (ch / 4) * kTPitch + (ch % 4) * 16,
+               load16B(qtb + (static_cast<int64_t>(qt) * RP + ch / 4) * kQTile + (ch % 4) * 8));
+    for (int ch = tid; ch < kQTile * D / 8; ch += 256) {
       const int r = ch / (D / 8), c8 = (ch % (D / 8)) * 8;
-      *reinterpret_cast<u32x4*>(lds + OFF_DO + r * VP + c8 * 2) =
-          *reinterpret_cast<const u32x4*>(dob + static_cast<int64_t>(min(q0 + r, p.T - 1)) * D + c8);
+      store16B(lds + OFF_DO + r * VP + c8 * 2, load16B(dob + static_cast<int64_t>(min(q0 + r, p.T - 1)) * D + c8));
     }
-    for (int ch = tid; ch < D * 4; ch += 256) {
-      const int r = ch / 4, c8 = (ch % 4) * 8;
-      *reinterpret_cast<u32x4*>(lds + OFF_DOT + r * kTPitch + c8 * 2) =
-          *reinterpret_cast<const u32x4*>(dotb + (static_cast<int64_t>(qt) * D + r) * 32 + c8);
-    }
-    if (tid < 2 * kBwdTile) {
-      const int q = q0 + (tid & 31);
-      const float* src = tid < kBwdTile ? p.lse2 : p.dvec;
-      rowv[tid] = q < p.T ? src[static_cast<int64_t>(bs) * p.T + q] : 0.f;
+    for (int ch = tid; ch < D * 4; ch += 256)
+      store16B(lds + OFF_DOT + (ch / 4) * kTPitch + (ch % 4) * 16,
+               load16B(dotb + (static_cast<int64_t>(qt) * D + ch / 4) * kQTile + (ch % 4) * 8));
+    if (tid < 2 * kQTile) {
+      const int q = q0 + (tid & (kQTile - 1));
+      const float* src = tid < kQTile ? p.lse2 : p.dvec;
+      reinterpret_cast<float*>(lds + OFF_ROW)[tid] = q < p.T ? src[static_cast<int64_t>(bs) * p.T + q] : 0.f;
     }
     __syncthreads();
 
-    // S^T (keys x queries), every wave in full: A = key rows, B = query rows.
-    f32x4 st[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) st[kb][cb] = zero4();
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      q8 kf[2], qf[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        kf[h] = *reinterpret_cast<const q8*>(lds + OFF_K + (h * 16 + c) * KP + (kk * 32 + 8 * g) * 2);
-        qf[h] = *reinterpret_cast<const q8*>(lds + OFF_Q + (h * 16 + c) * KP + (kk * 32 + 8 * g) * 2);
-      }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) st[kb][cb] = Elem<TQ>::mma(kf[kb], qf[cb], st[kb][cb]);
-    }
-    // P^T: lane (c, g) element i is key k0 + 16kb + 4g + i, query q0 + 16cb + c.
-    f32x4 pt[2][2];
+    // S = Q K^T and dP = dO V^T for this wave's keys: lane (c, g) element i
+    // of block cb is query q0 + 16cb + 4g + i, key kw + c.
+    f32x4 sv[2], dp[2];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const int q = q0 + cb * 16 + c;
-      const float lse = rowv[cb * 16 + c];
+      sv[cb] = zero4();
+      dp[cb] = zero4();
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = k0 + kb * 16 + 4 * g + i;
-          const bool live = q < p.T && key < p.T && (!p.causal || key <= q);
-          pt[kb][cb][i] = live ? exp2f(st[kb][cb][i] * sc - lse) : 0.f;
-        }
-    }
-    // dP^T = V dO^T over this wave's value chunks, summed over the waves.
-    f32x4 dpt[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) dpt[kb][cb] = zero4();
-#pragma unroll
-    for (int j = 0; j < MYDC; ++j) {
-      const int chunk = wave + 4 * j;
-      if (chunk >= DC) break;
-      v8 df[2];
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb)
-        df[cb] = *reinterpret_cast<const v8*>(lds + OFF_DO + (cb * 16 + c) * VP + (chunk * 32 + 8 * g) * 2);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) dpt[kb][cb] = Elem<TV>::mma(vf[j][kb], df[cb], dpt[kb][cb]);
-    }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb)
-        *reinterpret_cast<f32x4*>(red + ((wave * 64 + lane) * 4 + kb * 2 + cb) * 4) = dpt[kb][cb];
-    __syncthreads();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        f32x4 sum = zero4();
-#pragma unroll
-        for (int w = 0; w < 4; ++w) sum += *reinterpret_cast<const f32x4*>(red + ((w * 64 + lane) * 4 + kb * 2 + cb) * 4);
-        dpt[kb][cb] = sum;
+      for (int kk = 0; kk < KS; ++kk) {
+        const q8 a = *reinterpret_cast<const q8*>(lds + OFF_Q + (cb * 16 + c) * QP + (kk * 32 + 8 * g) * 2);
+        sv[cb] = Elem<TQ>::mma(a, kf[kk], sv[cb]);
       }
-    // dS^T = P^T (dP^T - rowsum(dO . O)).
-    f32x4 dst[2][2];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const float dvq = rowv[kBwdTile + cb * 16 + c];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[kb][cb][i] = pt[kb][cb][i] * (dpt[kb][cb][i] - dvq);
-    }
-    // Wave w owns block (kb, cb) = (w >> 1, w & 1): it writes P^T and dS^T as
-    // [key][query] rows and dS as [query][key] rows, and adds dS . raw scores
-    // of that block to dgamma.
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        if (kb * 2 + cb != wave) continue;
-        TV* ptl = reinterpret_cast<TV*>(lds + OFF_PT);
-        TQ* dstl = reinterpret_cast<TQ*>(lds + OFF_DST);
-        typename Elem<TQ>::v4 dsq;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kb * 16 + 4 * g + i, q = cb * 16 + c;
-          ptl[key * (kTPitch / 2) + q] = static_cast<TV>(pt[kb][cb][i]);
-          dstl[key * (kTPitch / 2) + q] = static_cast<TQ>(dst[kb][cb][i]);
-          dsq[i] = static_cast<TQ>(dst[kb][cb][i]);
-          dgamma += dst[kb][cb][i] * st[kb][cb][i];
-        }
-        *reinterpret_cast<typename Elem<TQ>::v4*>(lds + OFF_DS + (cb * 16 + c) * kTPitch + (kb * 16 + 4 * g) * 2) = dsq;
+      for (int j = 0; j < DC; ++j) {
+        const v8 a = *reinterpret_cast<const v8*>(lds + OFF_DO + (cb * 16 + c) * VP + (j * 32 + 8 * g) * 2);
+        dp[cb] = Elem<TV>::mma(a, vf[j], dp[cb]);
       }
-    __syncthreads();
+    }
+    // P, dS = P (dP - rowsum(dO . O)); contraction element 4cb + i.
+    v8 pa;
+    q8 dsa;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ql = cb * 16 + 4 * g + i;
+        const int q = q0 + ql;
+        const bool live = q < p.T && key < p.T && (!p.causal || key <= q);
+        const float pr = live ? exp2f(sv[cb][i] * sc - rowv[ql]) : 0.f;
+        const float ds = pr * (dp[cb][i] - rowv[kQTile + ql]);
+        dgamma += ds * sv[cb][i];
+        pa[cb * 4 + i] = static_cast<TV>(pr);
+        dsa[cb * 4 + i] = static_cast<TQ>(ds);
+        *reinterpret_cast<TQ*>(lds + OFF_DS + ql * kDsPitch + (wave * 16 + c) * 2) = dsa[cb * 4 + i];
+      }
+    // dV += P^T dO and dK += dS^T Q; B rows read the same query order.
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const char* row = lds + OFF_DOT + (j * 16 + c) * kTPitch;
+      const v4 lo = *reinterpret_cast<const v4*>(row + 8 * g);
+      const v4 hi = *reinterpret_cast<const v4*>(row + 32 + 8 * g);
+      const v8 bf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      dv_acc[j] = Elem<TV>::mma(pa, bf, dv_acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < NK; ++j) {
+      const char* row = lds + OFF_QT + (j * 16 + c) * kTPitch;
+      const q4 lo = *reinterpret_cast<const q4*>(row + 8 * g);
+      const q4 hi = *reinterpret_cast<const q4*>(row + 32 + 8 * g);
+      const q8 bf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      dk_acc[j] = Elem<TQ>::mma(dsa, bf, dk_acc[j]);
+    }
+    __syncthreads();   // dS of all four waves is in LDS
 
-    // dV += P^T dO (B: dO^T rows), dK += dS^T Q (B: Q^T rows), dQ = dS K.
-    v8 pa[2];
-    q8 da[2], dsa[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      pa[h] = *reinterpret_cast<const v8*>(lds + OFF_PT + (h * 16 + c) * kTPitch + 8 * g * 2);
-      da[h] = *reinterpret_cast<const q8*>(lds + OFF_DST + (h * 16 + c) * kTPitch + 8 * g * 2);
-      dsa[h] = *reinterpret_cast<const q8*>(lds + OFF_DS + (h * 16 + c) * kTPitch + 8 * g * 2);
-    }
-#pragma unroll
-    for (int j = 0; j < DB; ++j) {
-      const int d = (wave + 4 * j) * 16 + c;
-      const v8 bf = *reinterpret_cast<const v8*>(lds + OFF_DOT + d * kTPitch + 8 * g * 2);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) dv_acc[kb][j] = Elem<TV>::mma(pa[kb], bf, dv_acc[kb][j]);
-    }
+    // dQ = dS K over the 64 keys, this wave's 16-column blocks.
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
       const int r = (wave + 4 * j) * 16 + c;
-      const q8 bf = *reinterpret_cast<const q8*>(lds + OFF_QT + r * kTPitch + 8 * g * 2);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) dk_acc[kb][j] = Elem<TQ>::mma(da[kb], bf, dk_acc[kb][j]);
-    }
-#pragma unroll
-    for (int j = 0; j < RB; ++j) {
-      const int r0 = (wave + 4 * j) * 16;
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
-        const f32x4 dqv = Elem<TQ>::mma(dsa[cb], ktf[j], zero4());
-        // Lane (c, g) element i: query q0 + 16cb + 4g + i, feature r0 + c.
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const q8 a = *reinterpret_cast<const q8*>(lds + OFF_DS + (cb * 16 + c) * kDsPitch + (ks * 32 + 8 * g) * 2);
+          acc = Elem<TQ>::mma(a, ktf[j][ks], acc);
+        }
+        // Lane (c, g) element i: query q0 + 16cb + 4g + i, feature r.
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int q = q0 + cb * 16 + 4 * g + i;
-          if (q < p.T)
-            unsafeAtomicAdd(p.dq + (static_cast<int64_t>(bs) * p.T + q) * RP + r0 + c, dqv[i] * gamma);
+          if (q < p.T) unsafeAtomicAdd(p.dq + (static_cast<int64_t>(bs) * p.T + q) * RP + r, acc[i] * gamma);
         }
       }
     }
   }
 
-  // dK rows of this tile; dV accumulates over the maps; dgamma over tiles.
+  // dK and dV rows of this wave's keys: lane (c, g) element i is key
+  // kw + 4g + i, column 16j + c.
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+  for (int i = 0; i < 4; ++i) {
+    const int kr = kw + 4 * g + i;
+    if (kr >= p.T) continue;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = k0 + kb * 16 + 4 * g + i;
-      if (key >= p.T) continue;
+    for (int j = 0; j < NK; ++j)
+      unsafeAtomicAdd(p.dk + (static_cast<int64_t>(bs) * p.T + kr) * RP + j * 16 + c, dk_acc[j][i] * gamma);
 #pragma unroll
-      for (int j = 0; j < RB; ++j)
-        p.dk[(static_cast<int64_t>(bs) * p.T + key) * RP + (wave + 4 * j) * 16 + c] = dk_acc[kb][j][i] * gamma;
-#pragma unroll
-      for (int j = 0; j < DB; ++j)
-        unsafeAtomicAdd(p.dv + (static_cast<int64_t>(b) * p.T + key) * D + (wave + 4 * j) * 16 + c, dv_acc[kb][j][i]);
-    }
+    for (int j = 0; j < NV; ++j)
+      unsafeAtomicAdd(p.dv + (static_cast<int64_t>(b) * p.T + kr) * D + j * 16 + c, dv_acc[j][i]);
+  }
   dgamma = wave_sum(dgamma);
   if (lane == 0) unsafeAtomicAdd(p.dgamma + s, dgamma);
 }
 
+namespace {
+
+// Query tiles per main-kernel workgroup: the longest run (at most 16 tiles)
+// that still gives at least 512 non-empty workgroups.
+int pick_qchunk(int B_S, int T, bool causal) {
+  const int n_qt = (T + kQTile - 1) / kQTile;
+  const int n_kt = (T + kKTile - 1) / kKTile;
+  for (int qc = 16; qc > 1; qc /= 2) {
+    int64_t wgs = 0;
+    for (int kt = 0; kt < n_kt; ++kt) {
+      const int steps = causal ? n_qt - kt * (kKTile / kQTile) : n_qt;
+      wgs += (steps + qc - 1) / qc;
+    }
+    if (wgs * B_S >= 512) return qc;
+  }
+  return 1;
+}
+
+}  // namespace
+
+template <typename TQ, typename TV, int RP, int D>
+static void launch_bwd_d(BwdParams p, int B, hipStream_t stream) {
+  const unsigned bs = static_cast<unsigned>(B * p.S);
+  hipLaunchKernelGGL((attention_bwd_prep_kernel<TQ, TV, RP, D>), dim3(static_cast<unsigned>(p.Tp / kQTile), bs),
+                     dim3(256), 0, stream, p);
+  const int n_qt = (p.T + kQTile - 1) / kQTile;
+  hipLaunchKernelGGL((attention_lse_kernel<TQ, RP>), dim3(static_cast<unsigned>(n_qt), bs), dim3(256), 0, stream, p);
+  p.qchunk = pick_qchunk(B * p.S, p.T, p.causal != 0);
+  p.n_chunks = (n_qt + p.qchunk - 1) / p.qchunk;
+  const int n_kt = (p.T + kKTile - 1) / kKTile;
+  hipLaunchKernelGGL((attention_bwd_kernel<TQ, TV, RP, D>), dim3(static_cast<unsigned>(n_kt * p.n_chunks), bs),
+                     dim3(256), 0, stream, p);
+}
+
 template <typename TQ, typename TV, int RP>
 static void launch_bwd_r(const BwdParams& p, int B, hipStream_t stream) {
-  const int n_kt = (p.T + kBwdTile - 1) / kBwdTile;
-  const dim3 lse_grid(static_cast<unsigned>((n_kt + 3) / 4), static_cast<unsigned>(B * p.S));
-  hipLaunchKernelGGL((attention_lse_kernel<TQ, RP>), lse_grid, dim3(256), 0, stream, p);
-  const dim3 grid(static_cast<unsigned>(n_kt), static_cast<unsigned>(B * p.S));
   switch (p.D) {
-    case 64: hipLaunchKernelGGL((attention_bwd_kernel<TQ, TV, RP, 64>), grid, dim3(256), 0, stream, p); break;
-    case 128: hipLaunchKernelGGL((attention_bwd_kernel<TQ, TV, RP, 128>), grid, dim3(256), 0, stream, p); break;
-    case 256: hipLaunchKernelGGL((attention_bwd_kernel<TQ, TV, RP, 256>), grid, dim3(256), 0, stream, p); break;
-    default: hipLaunchKernelGGL((attention_bwd_kernel<TQ, TV, RP, 512>), grid, dim3(256), 0, stream, p); break;
+    case 64: launch_bwd_d<TQ, TV, RP, 64>(p, B, stream); break;
+    case 128: launch_bwd_d<TQ, TV, RP, 128>(p, B, stream); break;
+    case 256: launch_bwd_d<TQ, TV, RP, 256>(p, B, stream); break;
+    default: launch_bwd_d<TQ, TV, RP, 512>(p, B, stream); break;
   }
 }
 
@@ -417,9 +468,26 @@ static void launch_bwd_t(const BwdParams& p, int B, hipStream_t stream) {
   }
 }
 
-void launch_routed_attention_backward(const AttentionBwdArgs& a, hipStream_t stream) {
-  BwdParams p{a.q, a.k, a.qt, a.kt, a.v, a.dout, a.doutt, a.lse2, a.dvec, a.gamma, a.dq, a.dk, a.dv, a.dgamma,
-              a.S, a.T, static_cast<int>(round_up(a.T, kKeyPad)), a.RP, a.D, a.causal ? 1 : 0};
+AttentionBwdLayout attention_bwd_layout(int64_t BS, int64_t T, int64_t RP, int64_t D) {
+  auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
+  const int64_t Tp = round_up(T, kKeyPad);
+  AttentionBwdLayout l;
+  l.qt = 0;
+  l.kt = l.qt + up(BS * Tp * RP * 2);
+  l.doutt = l.kt + up(BS * Tp * RP * 2);
+  l.lse2 = l.doutt + up(BS * Tp * D * 2);
+  l.dvec = l.lse2 + up(BS * T * 4);
+  l.bytes = l.dvec + up(BS * T * 4);
+  return l;
+}
+
+void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace, hipStream_t stream) {
+  const AttentionBwdLayout l = attention_bwd_layout(static_cast<int64_t>(a.B) * a.S, a.T, a.RP, a.D);
+  char* ws = static_cast<char*>(workspace);
+  BwdParams p{a.q, a.k, a.v, a.out, a.dout, ws + l.qt, ws + l.kt, ws + l.doutt,
+              reinterpret_cast<float*>(ws + l.lse2), reinterpret_cast<float*>(ws + l.dvec), a.gamma,
+              a.dq, a.dk, a.dv, a.dgamma,
+              a.S, a.T, static_cast<int>(round_up(a.T, kKeyPad)), a.RP, a.D, a.causal ? 1 : 0, 1, 1};
   if (a.qk_dtype == kF16) {
     if (a.v_dtype == kBF16) launch_bwd_t<_Float16, __bf16>(p, a.B, stream);
     else launch_bwd_t<_Float16, _Float16>(p, a.B, stream);

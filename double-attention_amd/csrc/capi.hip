@@ -218,12 +218,17 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
   return check_launch("attention");
 }
 
-int da_routed_attention_backward(const void* query, const void* key, const void* query_t, const void* key_t,
-                                 const void* value, const void* grad_out, const void* grad_out_t,
-                                 const float* out_rowsum, const float* scales, int64_t batch, int64_t maps,
+int64_t da_attention_backward_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t score_dim,
+                                              int64_t value_dim) {
+  if (batch < 1 || maps < 1 || length < 1 || score_dim < 1 || value_dim < 1) return 0;
+  return da::attention_bwd_layout(batch * maps, length, score_dim, value_dim).bytes;
+}
+
+int da_routed_attention_backward(const void* query, const void* key, const void* value, const void* out,
+                                 const void* grad_out, const float* scales, int64_t batch, int64_t maps,
                                  int64_t length, int64_t score_dim, int64_t value_dim, int flags, int qk_dtype,
-                                 int v_dtype, float* lse_workspace, float* grad_query, float* grad_key,
-                                 float* grad_value, float* grad_scales, da_stream_t stream) {
+                                 int v_dtype, void* workspace, int64_t workspace_bytes, float* grad_query,
+                                 float* grad_key, float* grad_value, float* grad_scales, da_stream_t stream) {
   const bool types_ok = (qk_dtype == DA_F16 && (v_dtype == DA_BF16 || v_dtype == DA_F16)) ||
                         (qk_dtype == DA_BF16 && v_dtype == DA_BF16);
   if (!types_ok)
@@ -234,29 +239,32 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
     return fail(DA_ERR_UNSUPPORTED, "attention backward: score_dim %lld not in {64,128,256}", (long long)score_dim);
   if (!pow2_width(value_dim))
     return fail(DA_ERR_UNSUPPORTED, "attention backward: value_dim %lld not in {64,128,256,512}", (long long)value_dim);
-  if (batch < 0 || length < 0 || maps < 1 || maps > 64 || batch * maps > 65535 || length > (1LL << 30))
+  if (batch < 0 || length < 0 || maps < 1 || maps > 64 || batch * maps > 65535 || length > (1LL << 24))
     return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: bad batch/maps/length");
   if (batch == 0 || length == 0) return ok();
-  const void* ptrs[] = {query, key, query_t, key_t, value, grad_out, grad_out_t, out_rowsum, scales,
-                        lse_workspace, grad_query, grad_key, grad_value, grad_scales};
+  const void* ptrs[] = {query, key, value, out, grad_out, scales, workspace, grad_query, grad_key, grad_value,
+                        grad_scales};
   for (const void* ptr : ptrs)
     if (!ptr) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: null pointer");
-  const void* vec[] = {query, key, query_t, key_t, value, grad_out, grad_out_t};
-  for (const void* ptr : vec)
+  const void* halves[] = {query, key, value, out, grad_out};
+  for (const void* ptr : halves)
     if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: half-precision tensors must be 16-byte aligned");
-  const void* f32[] = {out_rowsum, scales, lse_workspace, grad_query, grad_key, grad_value, grad_scales};
+  const void* f32[] = {grad_query, grad_key, grad_value};
   for (const void* ptr : f32)
-    if (!aligned(ptr, 4)) return fail(DA_ERR_ALIGNMENT, "attention backward: fp32 tensors must be 4-byte aligned");
+    if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: gradients must be 16-byte aligned");
+  if (!aligned(scales, 4) || !aligned(grad_scales, 4))
+    return fail(DA_ERR_ALIGNMENT, "attention backward: scales must be 4-byte aligned");
+  if (!aligned(workspace, 256)) return fail(DA_ERR_ALIGNMENT, "attention backward: workspace must be 256-byte aligned");
+  const int64_t need = da_attention_backward_workspace_bytes(batch, maps, length, score_dim, value_dim);
+  if (workspace_bytes < need)
+    return fail(DA_ERR_WORKSPACE, "attention backward: workspace of %lld bytes < %lld required",
+                (long long)workspace_bytes, (long long)need);
   da::AttentionBwdArgs a;
   a.q = query;
   a.k = key;
-  a.qt = query_t;
-  a.kt = key_t;
   a.v = value;
+  a.out = out;
   a.dout = grad_out;
-  a.doutt = grad_out_t;
-  a.lse2 = lse_workspace;
-  a.dvec = out_rowsum;
   a.gamma = scales;
   a.dq = grad_query;
   a.dk = grad_key;
@@ -270,7 +278,7 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
   a.causal = (flags & DA_ATTN_CAUSAL) != 0;
   a.qk_dtype = qk_dtype;
   a.v_dtype = v_dtype;
-  da::launch_routed_attention_backward(a, reinterpret_cast<hipStream_t>(stream));
+  da::launch_routed_attention_backward(a, workspace, reinterpret_cast<hipStream_t>(stream));
   return check_launch("attention backward");
 }
 

@@ -85,23 +85,24 @@ struct AttentionArgs {
 struct AttentionBwdArgs {
   const void* q;         // [B*S][T][RP] routed queries, qk_dtype
   const void* k;         // [B*S][T][RP] routed keys
-  const void* qt;        // [B*S][Tp/32][RP][32] Q^T in 32-token tiles (zero past T)
-  const void* kt;        // [B*S][Tp/32][RP][32] K^T tiles
   const void* v;         // [B][T][D] values, v_dtype
+  const void* out;       // [B*S][T][D] forward output, v_dtype
   const void* dout;      // [B*S][T][D] output gradient, v_dtype
-  const void* doutt;     // [B*S][Tp/32][D][32] its 32-token tiles
-  float* lse2;           // [B*S][T] workspace: log2-sum-exp of each query row
-  const float* dvec;     // [B*S][T] rowsum(dO . O)
   const float* gamma;    // [S] score scales
-  float* dq;             // [B*S][T][RP] accumulated (zeroed by the caller)
-  float* dk;             // [B*S][T][RP] written
-  float* dv;             // [B][T][D] accumulated (zeroed by the caller)
-  float* dgamma;         // [S] accumulated (zeroed by the caller)
+  float* dq;             // [B*S][T][RP]
+  float* dk;             // [B*S][T][RP]
+  float* dv;             // [B][T][D]
+  float* dgamma;         // [S]
   int B, S, T, RP, D;
   bool causal;
   int qk_dtype, v_dtype;
 };
-void launch_routed_attention_backward(const AttentionBwdArgs& a, hipStream_t stream);
+// Byte offsets of the backward's workspace pieces (256-byte aligned).
+struct AttentionBwdLayout {
+  int64_t qt, kt, doutt, lse2, dvec, bytes;
+};
+AttentionBwdLayout attention_bwd_layout(int64_t BS, int64_t T, int64_t RP, int64_t D);
+void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace, hipStream_t stream);
 
 struct GemmSegment {
   // D[i, j] = sum_k P[i, k] Q[j, k]; P rows may come from two stacked matrices

@@ -459,9 +459,10 @@ def _attention_backward(
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients of ``routed_attention_reference`` on the library's backward kernels.
 
-    The flash-attention backward of ``triton_kernels.py:2093-2263``: a pass for
-    each query row's log-sum-exp, then one workgroup per (sequence, map, 32-key
-    tile) forming dV, dK, dQ and d(scale) from the saved forward output.
+    The flash-attention backward of ``triton_kernels.py:2093-2263``: a prep
+    pass (transposed tiles, rowsum(dO . O), zeroed gradients), a pass for each
+    query row's log-sum-exp, then one workgroup per (sequence, map, 64-key
+    tile, run of query tiles) forming dV, dK, dQ and d(scale).
     """
 
     batch, maps, length, score_dim = query.shape
@@ -470,27 +471,26 @@ def _attention_backward(
     value_width = _next_width(model_dim)
     rows = batch * maps
     device = value.device
-    q = _padded_rows(query.detach(), score_width).view(rows, length, score_width)
-    k = _padded_rows(key.detach(), score_width).view(rows, length, score_width)
+    q = _padded_rows(query.detach(), score_width)
+    k = _padded_rows(key.detach(), score_width)
     v = _padded_rows(value.detach(), value_width)
-    go = _padded_rows(grad.detach().to(value.dtype), value_width).view(rows, length, value_width)
-    qt = value_transposed(q)
-    kt = value_transposed(k)
-    got = value_transposed(go)
-    rowsum = (grad.detach().float() * out.detach().float()).sum(-1).reshape(rows, length).contiguous()
+    o = _padded_rows(out.detach(), value_width)
+    go = _padded_rows(grad.detach().to(value.dtype), value_width)
     gamma = scales.detach().float().contiguous()
-    lse = torch.empty(rows, length, dtype=torch.float32, device=device)
-    dq = torch.zeros(rows, length, score_width, dtype=torch.float32, device=device)
-    dk = torch.empty(rows, length, score_width, dtype=torch.float32, device=device)
-    dv = torch.zeros(batch, length, value_width, dtype=torch.float32, device=device)
-    dg = torch.zeros(maps, dtype=torch.float32, device=device)
     lib = _lib.get()
+    ws_bytes = lib.da_attention_backward_workspace_bytes(batch, maps, length, score_width, value_width)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    dq = torch.empty(rows, length, score_width, dtype=torch.float32, device=device)
+    dk = torch.empty_like(dq)
+    dv = torch.empty(batch, length, value_width, dtype=torch.float32, device=device)
+    dg = torch.empty(maps, dtype=torch.float32, device=device)
     _lib.check(
         lib.da_routed_attention_backward(
-            q.data_ptr(), k.data_ptr(), qt.data_ptr(), kt.data_ptr(), v.data_ptr(), go.data_ptr(), got.data_ptr(),
-            rowsum.data_ptr(), gamma.data_ptr(), batch, maps, length, score_width, value_width,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), go.data_ptr(), gamma.data_ptr(),
+            batch, maps, length, score_width, value_width,
             _lib.DA_ATTN_CAUSAL if causal else 0, _half_code(q.dtype), _half_code(value.dtype),
-            lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), _stream(device),
+            workspace.data_ptr(), ws_bytes, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(),
+            _stream(device),
         ),
         "routed_attention_hip backward",
     )

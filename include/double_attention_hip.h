@@ -20,7 +20,7 @@
  *   da_dictionary_route       dictionary_route_triton / _reference   src/double_attention/triton_kernels.py:1984-2019, ops.py:16-62
  *   da_routed_attention       routed_attention_triton / _reference   src/double_attention/triton_kernels.py:2290-2305, ops.py:65-93
  *                             + map combine                          src/double_attention/modules.py:265-272
- *   da_routed_attention_backward
+ *   da_routed_attention_backward, da_attention_backward_workspace_bytes
  *                             backward of routed_attention_triton    src/double_attention/triton_kernels.py:2093-2263, 2290-2305
  *   da_qkv_projection         _project_query_key + self.value        src/double_attention/modules.py:143-157, 212
  *   da_linear                 self.output                            src/double_attention/modules.py:117-121, 272
@@ -174,32 +174,30 @@ int64_t da_attention_workspace_bytes(int64_t batch, int64_t maps, int64_t length
 /*
  * Backward of the per-map outer attention (no map mix): with
  *   P_s = softmax(scales[s] * q_s k_s^T, causal mask),  out_s = P_s v,
- * given dO_s = d loss / d out_s it accumulates the gradients of q, k, v and
+ * given dO_s = d loss / d out_s it writes the gradients of q, k, v and
  * scales (the products of triton_kernels.py:2093-2263 behind the autograd
  * function of triton_kernels.py:2290-2305; reference math ops.py:65-93).
  *   query, key:  [batch*maps, length, score_dim], qk_dtype
- *   query_t, key_t: [batch*maps, P/32, score_dim, 32] 32-token transposed tiles,
- *                zero for tokens >= length (P = da_padded_length(length))
  *   value:       [batch, length, value_dim], v_dtype
- *   grad_out:    [batch*maps, length, value_dim], v_dtype;
- *   grad_out_t:  [batch*maps, P/32, value_dim, 32] its tiles, zero past length
- *   out_rowsum:  [batch*maps, length] fp32, sum over features of grad_out * out
+ *   out:         [batch*maps, length, value_dim], v_dtype (the forward output)
+ *   grad_out:    [batch*maps, length, value_dim], v_dtype
  *   scales:      [maps] fp32 score scales (already exponentiated)
- *   lse_workspace: [batch*maps, length] fp32 scratch (overwritten)
- *   grad_query:  [batch*maps, length, score_dim] fp32, ACCUMULATED: zero it first
- *   grad_key:    [batch*maps, length, score_dim] fp32, written
- *   grad_value:  [batch, length, value_dim] fp32, ACCUMULATED: zero it first
- *   grad_scales: [maps] fp32, ACCUMULATED: zero it first
+ *   workspace:   >= da_attention_backward_workspace_bytes(...) bytes,
+ *                256-byte aligned (transposed tiles, row statistics)
+ *   grad_query, grad_key: [batch*maps, length, score_dim] fp32
+ *   grad_value:  [batch, length, value_dim] fp32 (summed over the maps)
+ *   grad_scales: [maps] fp32
  *   score_dim in {64, 128, 256}; value_dim in {64, 128, 256, 512}; flags:
- *   DA_ATTN_CAUSAL only.  Accumulation uses fp32 atomics, so the bits of
- *   grad_query, grad_value and grad_scales vary between runs.
+ *   DA_ATTN_CAUSAL only.  The gradients are zeroed and then accumulated with
+ *   fp32 atomics, so their last bits vary between runs.
  */
-int da_routed_attention_backward(const void* query, const void* key, const void* query_t, const void* key_t,
-                                 const void* value, const void* grad_out, const void* grad_out_t,
-                                 const float* out_rowsum, const float* scales, int64_t batch, int64_t maps,
+int64_t da_attention_backward_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t score_dim,
+                                              int64_t value_dim);
+int da_routed_attention_backward(const void* query, const void* key, const void* value, const void* out,
+                                 const void* grad_out, const float* scales, int64_t batch, int64_t maps,
                                  int64_t length, int64_t score_dim, int64_t value_dim, int flags, int qk_dtype,
-                                 int v_dtype, float* lse_workspace, float* grad_query, float* grad_key,
-                                 float* grad_value, float* grad_scales, da_stream_t stream);
+                                 int v_dtype, void* workspace, int64_t workspace_bytes, float* grad_query,
+                                 float* grad_key, float* grad_value, float* grad_scales, da_stream_t stream);
 
 /*
  * Q/K and V projections in one launch (modules.py:143-157 and 212):

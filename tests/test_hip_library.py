@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 16
+    assert len(names) == 17
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -155,17 +155,23 @@ def test_linear_ex_and_layer_norm_reject_bad_arguments() -> None:
 def test_attention_backward_rejects_bad_arguments() -> None:
     h = lib.get()
     f = _fake()
-    good = [f, f, f, f, f, f, f, f, f, 2, 3, 100, 128, 256, lib.DA_ATTN_CAUSAL, lib.DA_BF16, lib.DA_BF16,
-            f, f, f, f, f, None]
+    need = h.da_attention_backward_workspace_bytes(2, 3, 100, 128, 256)
+    # Q^T, K^T and dO^T tiles over 128 padded tokens, then two fp32 rows
+    # (6 * 100 * 4 = 2400 bytes, rounded up to 2560).
+    assert need == 2 * (6 * 128 * 128 * 2) + 6 * 128 * 256 * 2 + 2 * 2560
+    good = [f, f, f, f, f, f, 2, 3, 100, 128, 256, lib.DA_ATTN_CAUSAL, lib.DA_BF16, lib.DA_BF16,
+            f, need, f, f, f, f, None]
     cases = [
-        (12, 512, -2, "score_dim 512"),
-        (13, 96, -2, "value_dim 96"),
-        (14, 4, -1, "flag bits"),
-        (15, lib.DA_F32, -2, "qk_dtype"),
-        (10, 65, -1, "maps"),
+        (9, 512, -2, "score_dim 512"),
+        (10, 96, -2, "value_dim 96"),
+        (11, 4, -1, "flag bits"),
+        (12, lib.DA_F32, -2, "qk_dtype"),
+        (7, 65, -1, "maps"),
         (0, 0, -1, "null pointer"),
-        (5, (1 << 20) + 4, -3, "16-byte"),
-        (20, (1 << 20) + 2, -3, "4-byte"),
+        (3, (1 << 20) + 4, -3, "16-byte"),
+        (18, (1 << 20) + 4, -3, "gradients"),
+        (14, (1 << 20) + 16, -3, "workspace must be 256-byte"),
+        (15, need - 1, -5, "workspace of"),
     ]
     for index, value, code, pattern in cases:
         args = list(good)
@@ -173,5 +179,5 @@ def test_attention_backward_rejects_bad_arguments() -> None:
         assert h.da_routed_attention_backward(*args) == code, pattern
         assert pattern in h.da_last_error().decode(), h.da_last_error()
     empty = list(good)
-    empty[11] = 0
+    empty[8] = 0
     assert h.da_routed_attention_backward(*empty) == 0
