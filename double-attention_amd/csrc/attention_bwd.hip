@@ -236,13 +236,21 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   constexpr int DC = D / 32;        // 32-deep steps over the value width
   constexpr int NV = D / 16;        // 16-wide dV column blocks
   constexpr int NK = RP / 16;       // 16-wide dK column blocks
+  constexpr int GV = NV < 8 ? NV : 8, GK = NK < 8 ? NK : 8;   // B operands per read group
   constexpr int RB = RP / 64;       // dQ column blocks per wave
   constexpr int QP = row_pitch(RP), VP = row_pitch(D);
+  // Staged per step by LDS DMA: Q and dO rows, Q^T and dO^T tile rows, each
+  // row followed by one 16-byte pad slot (so QP, VP and kTPitch pitches).
+  typedef PaddedTile<kQTile, RP / 8, false> QRows;
+  typedef PaddedTile<RP, 4, false> QCols;
+  typedef PaddedTile<kQTile, D / 8, false> DRows;
+  typedef PaddedTile<D, 4, false> DCols;
+  static_assert(QRows::PITCH * 16 == QP && DRows::PITCH * 16 == VP && QCols::PITCH * 16 == kTPitch, "pitches");
   constexpr int OFF_Q = 0;
-  constexpr int OFF_QT = OFF_Q + kQTile * QP;
-  constexpr int OFF_DO = OFF_QT + RP * kTPitch;
-  constexpr int OFF_DOT = OFF_DO + kQTile * VP;
-  constexpr int OFF_DS = OFF_DOT + D * kTPitch;
+  constexpr int OFF_QT = OFF_Q + QRows::BYTES;
+  constexpr int OFF_DO = OFF_QT + QCols::BYTES;
+  constexpr int OFF_DOT = OFF_DO + DRows::BYTES;
+  constexpr int OFF_DS = OFF_DOT + DCols::BYTES;
   constexpr int OFF_ROW = OFF_DS + kQTile * kDsPitch;
   constexpr int LDS_BYTES = OFF_ROW + 2 * kQTile * 4;
   static_assert(LDS_BYTES <= 160 * 1024, "the tiles fit the LDS");
@@ -252,10 +260,19 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   const int c = lane & 15, g = lane >> 4;
   const int wave = uniform_wave();
   const int tid = static_cast<int>(threadIdx.x);
-  const int bs = static_cast<int>(blockIdx.y);
+  // Workgroups go round-robin over the XCDs; each XCD takes a contiguous run
+  // of the logical order (sequence, query run, key tile), so the workgroups
+  // that run together on one XCD stage nearly the same query tiles from its L2.
+  const int n_wg = static_cast<int>(gridDim.x * gridDim.y);
+  const int wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
+  const int xcd = wg % kXcds, per_xcd = n_wg / kXcds, rem_xcd = n_wg % kXcds;
+  const int logical = xcd * per_xcd + min(xcd, rem_xcd) + wg / kXcds;
+  const int n_kt = static_cast<int>(gridDim.x) / p.n_chunks;
+  const int bs = logical / static_cast<int>(gridDim.x);
+  const int rest = logical - bs * static_cast<int>(gridDim.x);
+  const int chunk = rest / n_kt;
+  const int kt = rest - chunk * n_kt;
   const int b = bs / p.S, s = bs - b * p.S;
-  const int kt = static_cast<int>(blockIdx.x) / p.n_chunks;
-  const int chunk = static_cast<int>(blockIdx.x) - kt * p.n_chunks;
   const int k0 = kt * kKTile;
   const int n_qt = (p.T + kQTile - 1) / kQTile;
   const int qt_begin = (p.causal ? k0 / kQTile : 0) + chunk * p.qchunk;
@@ -298,47 +315,81 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   const float* rowv = reinterpret_cast<const float*>(lds + OFF_ROW);
   const int key = kw + c;
 
+  // Step qt's tiles: the row statistics into a register (every thread loads
+  // one, at a clamped index), then the tile DMAs, wave w taking wave loads
+  // w, w+4, ...  The register load is older than the DMAs, so its use after
+  // the step's vmcnt(0) wait needs nothing more.
+  float row_stat = 0.f;
+  auto issue = [&](int qt) {
+    const int q0 = qt * kQTile;
+    const float* src = (tid & 63) < kQTile ? p.lse2 : p.dvec;
+    row_stat = src[static_cast<int64_t>(bs) * p.T + min(q0 + (tid & (kQTile - 1)), p.T - 1)];
+    for (int L = wave; L < QRows::LOADS; L += 4) {
+      int r, ck;
+      QRows::slot_chunk(L * 64 + lane, r, ck);
+      dma16(qb + static_cast<int64_t>(min(q0 + r, p.T - 1)) * RP + ck * 8, lds + OFF_Q + L * 1024);
+    }
+    for (int L = wave; L < QCols::LOADS; L += 4) {
+      int r, ck;
+      QCols::slot_chunk(L * 64 + lane, r, ck);
+      dma16(qtb + (static_cast<int64_t>(qt) * RP + r) * kQTile + ck * 8, lds + OFF_QT + L * 1024);
+    }
+    for (int L = wave; L < DRows::LOADS; L += 4) {
+      int r, ck;
+      DRows::slot_chunk(L * 64 + lane, r, ck);
+      dma16(dob + static_cast<int64_t>(min(q0 + r, p.T - 1)) * D + ck * 8, lds + OFF_DO + L * 1024);
+    }
+    for (int L = wave; L < DCols::LOADS; L += 4) {
+      int r, ck;
+      DCols::slot_chunk(L * 64 + lane, r, ck);
+      dma16(dotb + (static_cast<int64_t>(qt) * D + r) * kQTile + ck * 8, lds + OFF_DOT + L * 1024);
+    }
+  };
+  issue(qt_begin);
+
   for (int qt = qt_begin; qt < qt_end; ++qt) {
     const int q0 = qt * kQTile;
-    __syncthreads();   // the previous step is done with every staged tile
-    for (int ch = tid; ch < kQTile * RP / 8; ch += 256) {
-      const int r = ch / (RP / 8), c8 = (ch % (RP / 8)) * 8;
-      store16B(lds + OFF_Q + r * QP + c8 * 2, load16B(qb + static_cast<int64_t>(min(q0 + r, p.T - 1)) * RP + c8));
-    }
-    for (int ch = tid; ch < RP * 4; ch += 256)
-      store16B(lds + OFF_QT + (ch / 4) * kTPitch + (ch % 4) * 16,
-               load16B(qtb + (static_cast<int64_t>(qt) * RP + ch / 4) * kQTile + (ch % 4) * 8));
-    for (int ch = tid; ch < kQTile * D / 8; ch += 256) {
-      const int r = ch / (D / 8), c8 = (ch % (D / 8)) * 8;
-      store16B(lds + OFF_DO + r * VP + c8 * 2, load16B(dob + static_cast<int64_t>(min(q0 + r, p.T - 1)) * D + c8));
-    }
-    for (int ch = tid; ch < D * 4; ch += 256)
-      store16B(lds + OFF_DOT + (ch / 4) * kTPitch + (ch % 4) * 16,
-               load16B(dotb + (static_cast<int64_t>(qt) * D + ch / 4) * kQTile + (ch % 4) * 8));
-    if (tid < 2 * kQTile) {
-      const int q = q0 + (tid & (kQTile - 1));
-      const float* src = tid < kQTile ? p.lse2 : p.dvec;
-      reinterpret_cast<float*>(lds + OFF_ROW)[tid] = q < p.T ? src[static_cast<int64_t>(bs) * p.T + q] : 0.f;
-    }
+    wait_vmem();   // this step's DMAs (and the previous step's atomics)
+    if (tid < 2 * kQTile)
+      reinterpret_cast<float*>(lds + OFF_ROW)[tid] = q0 + (tid & (kQTile - 1)) < p.T ? row_stat : 0.f;
     __syncthreads();
 
     // S = Q K^T and dP = dO V^T for this wave's keys: lane (c, g) element i
     // of block cb is query q0 + 16cb + 4g + i, key kw + c.
-    f32x4 sv[2], dp[2];
+    f32x4 sv[2] = {zero4(), zero4()}, dp[2] = {zero4(), zero4()};
+    // Groups of four contraction steps: the eight A reads of both query
+    // blocks, then their eight MFMAs alternating between the two blocks.
+    constexpr int GS = KS < 4 ? KS : 4;
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      sv[cb] = zero4();
-      dp[cb] = zero4();
+    for (int k0 = 0; k0 < KS; k0 += GS) {
+      q8 a[GS][2];
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const q8 a = *reinterpret_cast<const q8*>(lds + OFF_Q + (cb * 16 + c) * QP + (kk * 32 + 8 * g) * 2);
-        sv[cb] = Elem<TQ>::mma(a, kf[kk], sv[cb]);
-      }
+      for (int kk = 0; kk < GS; ++kk)
 #pragma unroll
-      for (int j = 0; j < DC; ++j) {
-        const v8 a = *reinterpret_cast<const v8*>(lds + OFF_DO + (cb * 16 + c) * VP + (j * 32 + 8 * g) * 2);
-        dp[cb] = Elem<TV>::mma(a, vf[j], dp[cb]);
-      }
+        for (int cb = 0; cb < 2; ++cb)
+          a[kk][cb] = *reinterpret_cast<const q8*>(lds + OFF_Q + (cb * 16 + c) * QP + ((k0 + kk) * 32 + 8 * g) * 2);
+#pragma unroll
+      for (int kk = 0; kk < GS; ++kk)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) sv[cb] = Elem<TQ>::mma(a[kk][cb], kf[k0 + kk], sv[cb]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * GS, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * GS, 0);
+    }
+    constexpr int GD = DC < 4 ? DC : 4;
+#pragma unroll
+    for (int j0 = 0; j0 < DC; j0 += GD) {
+      v8 a[GD][2];
+#pragma unroll
+      for (int j = 0; j < GD; ++j)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+          a[j][cb] = *reinterpret_cast<const v8*>(lds + OFF_DO + (cb * 16 + c) * VP + ((j0 + j) * 32 + 8 * g) * 2);
+#pragma unroll
+      for (int j = 0; j < GD; ++j)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) dp[cb] = Elem<TV>::mma(a[j][cb], vf[j0 + j], dp[cb]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * GD, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * GD, 0);
     }
     // P, dS = P (dP - rowsum(dO . O)); contraction element 4cb + i.
     v8 pa;
@@ -355,28 +406,54 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
         dgamma += ds * sv[cb][i];
         pa[cb * 4 + i] = static_cast<TV>(pr);
         dsa[cb * 4 + i] = static_cast<TQ>(ds);
-        *reinterpret_cast<TQ*>(lds + OFF_DS + ql * kDsPitch + (wave * 16 + c) * 2) = dsa[cb * 4 + i];
       }
-    // dV += P^T dO and dK += dS^T Q; B rows read the same query order.
+    // dV += P^T dO and dK += dS^T Q; B rows read the same query order.  The
+    // B operands go in groups of eight: eight LDS reads, then eight MFMAs,
+    // so the reads of a group overlap instead of each waiting in turn.
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const char* row = lds + OFF_DOT + (j * 16 + c) * kTPitch;
-      const v4 lo = *reinterpret_cast<const v4*>(row + 8 * g);
-      const v4 hi = *reinterpret_cast<const v4*>(row + 32 + 8 * g);
-      const v8 bf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      dv_acc[j] = Elem<TV>::mma(pa, bf, dv_acc[j]);
+    for (int j0 = 0; j0 < NV; j0 += GV) {
+      v8 bf[GV];
+#pragma unroll
+      for (int j = 0; j < GV; ++j) {
+        const char* row = lds + OFF_DOT + ((j0 + j) * 16 + c) * kTPitch;
+        const v4 lo = *reinterpret_cast<const v4*>(row + 8 * g);
+        const v4 hi = *reinterpret_cast<const v4*>(row + 32 + 8 * g);
+        bf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int j = 0; j < GV; ++j) dv_acc[j0 + j] = Elem<TV>::mma(pa, bf[j], dv_acc[j0 + j]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * GV, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, GV, 0);
     }
 #pragma unroll
-    for (int j = 0; j < NK; ++j) {
-      const char* row = lds + OFF_QT + (j * 16 + c) * kTPitch;
-      const q4 lo = *reinterpret_cast<const q4*>(row + 8 * g);
-      const q4 hi = *reinterpret_cast<const q4*>(row + 32 + 8 * g);
-      const q8 bf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      dk_acc[j] = Elem<TQ>::mma(dsa, bf, dk_acc[j]);
+    for (int j0 = 0; j0 < NK; j0 += GK) {
+      q8 bf[GK];
+#pragma unroll
+      for (int j = 0; j < GK; ++j) {
+        const char* row = lds + OFF_QT + ((j0 + j) * 16 + c) * kTPitch;
+        const q4 lo = *reinterpret_cast<const q4*>(row + 8 * g);
+        const q4 hi = *reinterpret_cast<const q4*>(row + 32 + 8 * g);
+        bf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int j = 0; j < GK; ++j) dk_acc[j0 + j] = Elem<TQ>::mma(dsa, bf[j], dk_acc[j0 + j]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * GK, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, GK, 0);
     }
-    __syncthreads();   // dS of all four waves is in LDS
+    // dS with the query as the row, for dQ.
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      *reinterpret_cast<TQ*>(lds + OFF_DS + ((e >> 2) * 16 + 4 * g + (e & 3)) * kDsPitch + (wave * 16 + c) * 2) = dsa[e];
+    __syncthreads();   // dS of all four waves is in LDS; the staged tiles are free
+    if (qt + 1 < qt_end) issue(qt + 1);
 
     // dQ = dS K over the 64 keys, this wave's 16-column blocks.
+    q8 dsf[2][2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        dsf[cb][ks] = *reinterpret_cast<const q8*>(lds + OFF_DS + (cb * 16 + c) * kDsPitch + (ks * 32 + 8 * g) * 2);
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
       const int r = (wave + 4 * j) * 16 + c;
@@ -384,10 +461,7 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
       for (int cb = 0; cb < 2; ++cb) {
         f32x4 acc = zero4();
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const q8 a = *reinterpret_cast<const q8*>(lds + OFF_DS + (cb * 16 + c) * kDsPitch + (ks * 32 + 8 * g) * 2);
-          acc = Elem<TQ>::mma(a, ktf[j][ks], acc);
-        }
+        for (int ks = 0; ks < 2; ++ks) acc = Elem<TQ>::mma(dsf[cb][ks], ktf[j][ks], acc);
         // Lane (c, g) element i: query q0 + 16cb + 4g + i, feature r.
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -418,7 +492,9 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
 namespace {
 
 // Query tiles per main-kernel workgroup: the longest run (at most 16 tiles)
-// that still gives at least 512 non-empty workgroups.
+// that still gives at least 256 non-empty workgroups (one per CU).  Every
+// workgroup ends with 64 x (RP + D) atomic adds of its dK and dV rows, so
+// shorter runs than that cost more in atomics than they gain in balance.
 int pick_qchunk(int B_S, int T, bool causal) {
   const int n_qt = (T + kQTile - 1) / kQTile;
   const int n_kt = (T + kKTile - 1) / kKTile;
@@ -428,7 +504,7 @@ int pick_qchunk(int B_S, int T, bool causal) {
       const int steps = causal ? n_qt - kt * (kKTile / kQTile) : n_qt;
       wgs += (steps + qc - 1) / qc;
     }
-    if (wgs * B_S >= 512) return qc;
+    if (wgs * B_S >= 256) return qc;
   }
   return 1;
 }
