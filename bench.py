@@ -57,6 +57,12 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--dtype", choices=("bf16", "fp16"), default="bf16")
     p.add_argument("--kernel-reps", type=int, default=200, help="launches per per-kernel timing loop")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument(
+        "--backward",
+        action="store_true",
+        help="time the outer attention's native backward at the workload's attention shape instead "
+        "(a separate JSON line; not the headline metric)",
+    )
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
     p.add_argument(
         "--copy-mib",
@@ -105,8 +111,88 @@ def measured_traffic(workload: str, kernel: str) -> float | None:
         return None
 
 
+def backward_bench(args: argparse.Namespace) -> None:
+    """Outer-attention backward at the workload's attention shape.
+
+    One step = dQ, dK, dV and d(scale) of ``routed_attention_hip`` for one
+    output gradient (prep, LSE and key-tile kernels), timed with HIP events
+    on the launch stream; beside it the fp32-softmax recompute through torch
+    autograd that the backward replaces.  FLOPs count the five products
+    2 T^2 (3R + 2D) per map plus the LSE pass's 2 T^2 R, halved when causal.
+    """
+
+    import torch
+
+    import double_attention as da
+    from double_attention import hip_ops
+    from double_attention.ops import routed_attention_reference
+
+    device = torch.device("cuda:0")
+    preset, batch, length, overrides, description = WORKLOADS[args.workload]
+    config = da.experiment_config(preset, backend="hip", **overrides)
+    H, S, R = config.qk_branches, config.outer_maps, config.routing_dim
+    rp = (H // S if H > S else 1) * R
+    d = config.model_dim
+    g = torch.Generator().manual_seed(3)
+    q = torch.nn.functional.normalize(torch.randn(batch, S, length, rp, generator=g), dim=-1).to(device, torch.float16)
+    k = torch.nn.functional.normalize(torch.randn(batch, S, length, rp, generator=g), dim=-1).to(device, torch.float16)
+    v = torch.randn(batch, length, d, generator=g).to(device, torch.bfloat16)
+    scales = torch.full((S,), 8.0, device=device)
+    grad = torch.randn(batch, S, length, d, generator=g).to(device, torch.bfloat16)
+    causal = config.causal
+    out = hip_ops._attention_forward(q, k, v, scales, causal)
+
+    def native():
+        return hip_ops._attention_backward(q, k, v, scales, out, grad, causal)
+
+    def recompute():
+        with torch.enable_grad():
+            ins = [t.detach().requires_grad_() for t in (q, k, v, scales)]
+            ref = routed_attention_reference(*ins, causal)
+            return torch.autograd.grad(ref, ins, grad)
+
+    def timed(fn, reps):
+        for _ in range(max(args.warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    if not hip_ops._native_backward_supported(q, v):
+        print(json.dumps({
+            "metric": "outer-attention backward (dQ, dK, dV, dscale) on 1 MI355X",
+            "value": None, "unit": "TFLOP/s",
+            "note": f"score width {rp} has no native backward (widths up to 256); autograd recomputes in torch",
+            "config": {"workload": description, "score_dim": rp},
+        }), flush=True)
+        return
+    ms = timed(native, args.steps)
+    ref_ms = timed(recompute, max(1, min(args.steps, 20))) if length <= 4096 else None
+    flops = 2.0 * batch * S * length * length * (4 * rp + 2 * d) * (0.5 if causal else 1.0)
+    print(json.dumps({
+        "metric": "outer-attention backward (dQ, dK, dV, dscale) on 1 MI355X",
+        "value": round(flops / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 4),
+        "steps": args.steps,
+        "torch_recompute_ms": None if ref_ms is None else round(ref_ms, 4),
+        "speedup_vs_recompute": None if ref_ms is None else round(ref_ms / ms, 2),
+        "dtype": "fp16 q/k, bf16 v",
+        "config": {"workload": description, "batch": batch, "maps": S, "length": length, "score_dim": rp,
+                   "value_dim": d, "causal": causal},
+    }), flush=True)
+
+
 def main() -> None:
     args = parse_args()
+    if args.backward and args.gpus == 1:
+        backward_bench(args)
+        return
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU only: this build has no multi-GPU path "
