@@ -200,13 +200,20 @@ class SharedDictionaryAttention(nn.Module):
             if self.map_mix_logits is None:
                 return self.output(map_output[:, 0]), x.new_ones(1)
             weights = torch.softmax(self.map_mix_logits, dim=0).to(map_output.dtype)
-            combined = torch.einsum("s,bstd->btd", weights, map_output)
+            # The weighted map sum in fp32, rounded once (as einsum's fp32
+            # accumulation does), without einsum's internal transposed bmm.
+            combined = (map_output.float() * weights.float()[None, :, None, None]).sum(1).to(map_output.dtype)
             return self.output(combined), weights
         weights = x.new_full((self.config.outer_maps,), 1.0 / self.config.outer_maps)
         return self.output(map_output.permute(0, 2, 1, 3).flatten(2)), weights
 
     def _torch_forward(
-        self, x: Tensor, dictionary_key: Tensor, dictionary_value: Tensor, return_aux: bool
+        self,
+        x: Tensor,
+        dictionary_key: Tensor,
+        dictionary_value: Tensor,
+        return_aux: bool,
+        attention: str = "torch",
     ) -> Tensor | tuple[Tensor, DoubleAttentionAux]:
         query, key = self._project_query_key(x)
         dense_value = self.value(x)
@@ -221,7 +228,14 @@ class SharedDictionaryAttention(nn.Module):
         routed_query, routed_key = routed.split(x.shape[1], dim=2)
         score_query, score_key = assemble_score_maps(routed_query, routed_key, self.config.outer_maps)
         scales = score_scale_from_log(self.log_score_scales)
-        map_output = routed_attention_reference(score_query, score_key, dense_value, scales, self.config.causal)
+        if attention == "hip" and _hip_attention_backward_fits(score_query, dense_value):
+            # The HIP backward's recompute: the outer attention on the library's
+            # forward kernel, so its autograd runs the native backward kernels.
+            from . import hip_ops
+
+            map_output = hip_ops.routed_attention_hip(score_query, score_key, dense_value, scales, self.config.causal)
+        else:
+            map_output = routed_attention_reference(score_query, score_key, dense_value, scales, self.config.causal)
         output, weights = self._combine(x, map_output)
         if not return_aux:
             return output
@@ -411,13 +425,28 @@ class _HipModuleFunction(torch.autograd.Function):
             xs = x.detach().requires_grad_(x.requires_grad)
             dks = dk.detach().requires_grad_(dk.requires_grad)
             dvs = dv.detach().requires_grad_(dv.requires_grad)
-            out = module._torch_forward(xs, dks, dvs, False)
+            out = module._torch_forward(xs, dks, dvs, False, attention="hip")
             wrt = [t for t in (xs, dks, dvs) if t.requires_grad] + [p for p in params if p.requires_grad]
             grads = torch.autograd.grad(out, wrt, grad.to(out.dtype), allow_unused=True) if wrt else ()
         it = iter(grads)
         head = [next(it) if t.requires_grad else None for t in (xs, dks, dvs)]
         tail = [next(it) if p.requires_grad else None for p in params]
         return (None, None, *head, *tail)
+
+
+def _hip_attention_backward_fits(score_query: Tensor, value: Tensor) -> bool:
+    """Whether the native attention backward takes these score-map operands."""
+
+    from . import hip_ops
+
+    halves = (torch.float16, torch.bfloat16)
+    return (
+        score_query.is_cuda
+        and score_query.dtype in halves
+        and value.dtype in halves
+        and (score_query.dtype == value.dtype or score_query.dtype == torch.float16)
+        and hip_ops._native_backward_supported(score_query, value)
+    )
 
 
 class DoubleAttentionBlock(nn.Module):

@@ -86,7 +86,9 @@ def routed_attention_reference(
         raise ValueError("value must have shape [B, T, D] matching query")
     if scales.shape != (query.shape[1],):
         raise ValueError(f"scales must have shape [{query.shape[1]}]")
-    scores = torch.matmul(query, key.transpose(-2, -1)).float()
+    # A contiguous K^T: batched half-precision products with a transposed
+    # right operand have faulted ROCm GPUs; the values are unchanged.
+    scores = torch.matmul(query, key.transpose(-2, -1).contiguous()).float()
     scores = scores * scales.float()[None, :, None, None]
     if causal:
         length = query.shape[-2]
