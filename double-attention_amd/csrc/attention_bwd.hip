@@ -37,21 +37,22 @@ constexpr int kKTile = 64;    // keys per workgroup (16 per wave)
 
 struct BwdParams {
   const void* q;        // [BS][T][RP] routed queries (score dtype)
-  const void* k;        // [BS][T][RP] routed keys
-  const void* v;        // [B][T][D] values
+  const void* k;        // [BS][Tk][RP] routed keys
+  const void* v;        // [B][Tk][D] values
   const void* out;      // [BS][T][D] forward output
   const void* dout;     // [BS][T][D] output gradient
   void* qt;             // [BS][Tp/32][RP][32] Q^T tiles (workspace)
-  void* kt;             // [BS][Tp/32][RP][32] K^T tiles
+  void* kt;             // [BS][Tkp/32][RP][32] K^T tiles
   void* doutt;          // [BS][Tp/32][D][32] dO^T tiles
   float* lse2;          // [BS][T]
   float* dvec;          // [BS][T] rowsum(dO . O)
   const float* gamma;   // [S] score scales
   float* dq;            // [BS][T][RP]
-  float* dk;            // [BS][T][RP]
-  float* dv;            // [B][T][D]
+  float* dk;            // [BS][Tk][RP]
+  float* dv;            // [B][Tk][D]
   float* dgamma;        // [S]
   int S, T, Tp, RP, D;
+  int Tk, Tkp;          // keys (== T when causal) and their padded count
   int causal;
   int qchunk;           // query tiles per workgroup of the main kernel
   int n_chunks;         // query runs per key tile
@@ -102,16 +103,19 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
   const int b = bs / p.S, s = bs - b * p.S;
   const int tile = static_cast<int>(blockIdx.x);
   const int t0 = tile * kQTile;
-  const int64_t tiles = p.Tp / kQTile;
-  const int64_t rows = static_cast<int64_t>(bs) * p.T;
+  const int64_t tiles = p.Tp / kQTile, ktiles = p.Tkp / kQTile;
+  const int64_t rows = static_cast<int64_t>(bs) * p.T, krows = static_cast<int64_t>(bs) * p.Tk;
 
-  transpose_tile<TQ, RP>(static_cast<const TQ*>(p.q) + rows * RP, t0, p.T,
-                         static_cast<TQ*>(p.qt) + (bs * tiles + tile) * RP * kQTile, lds);
-  transpose_tile<TQ, RP>(static_cast<const TQ*>(p.k) + rows * RP, t0, p.T,
-                         static_cast<TQ*>(p.kt) + (bs * tiles + tile) * RP * kQTile, lds);
-  transpose_tile<TV, D>(static_cast<const TV*>(p.dout) + rows * D, t0, p.T,
-                        static_cast<TV*>(p.doutt) + (bs * tiles + tile) * D * kQTile, lds);
-  if (t0 >= p.T) return;   // padding tiles only need their zeroed transposes
+  // Tile conditions are uniform over the workgroup (transpose_tile syncs).
+  if (tile < tiles)
+    transpose_tile<TQ, RP>(static_cast<const TQ*>(p.q) + rows * RP, t0, p.T,
+                           static_cast<TQ*>(p.qt) + (bs * tiles + tile) * RP * kQTile, lds);
+  if (tile < ktiles)
+    transpose_tile<TQ, RP>(static_cast<const TQ*>(p.k) + krows * RP, t0, p.Tk,
+                           static_cast<TQ*>(p.kt) + (bs * ktiles + tile) * RP * kQTile, lds);
+  if (tile < tiles)
+    transpose_tile<TV, D>(static_cast<const TV*>(p.dout) + rows * D, t0, p.T,
+                          static_cast<TV*>(p.doutt) + (bs * tiles + tile) * D * kQTile, lds);
 
   // rowsum(dO . O): wave w takes rows w, w+4, ...
   const TV* dob = static_cast<const TV*>(p.dout) + rows * D;
@@ -130,16 +134,14 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
     if (lane == 0) p.dvec[rows + t] = acc;
   }
 
-  // Zero the accumulated gradients of this tile's rows.
-  const int n_rows = min(kQTile, p.T - t0);
+  // Zero the accumulated gradients of this tile's query and key rows.
   const f32x4 z = zero4();
-  for (int i = tid; i < n_rows * RP / 4; i += 256) {
-    reinterpret_cast<f32x4*>(p.dq + (rows + t0) * RP)[i] = z;
-    reinterpret_cast<f32x4*>(p.dk + (rows + t0) * RP)[i] = z;
-  }
+  const int q_rows = max(0, min(kQTile, p.T - t0)), k_rows = max(0, min(kQTile, p.Tk - t0));
+  for (int i = tid; i < q_rows * RP / 4; i += 256) reinterpret_cast<f32x4*>(p.dq + (rows + t0) * RP)[i] = z;
+  for (int i = tid; i < k_rows * RP / 4; i += 256) reinterpret_cast<f32x4*>(p.dk + (krows + t0) * RP)[i] = z;
   if (s == 0)
-    for (int i = tid; i < n_rows * D / 4; i += 256)
-      reinterpret_cast<f32x4*>(p.dv + (static_cast<int64_t>(b) * p.T + t0) * D)[i] = z;
+    for (int i = tid; i < k_rows * D / 4; i += 256)
+      reinterpret_cast<f32x4*>(p.dv + (static_cast<int64_t>(b) * p.Tk + t0) * D)[i] = z;
   if (bs == 0 && tile == 0 && tid < p.S) p.dgamma[tid] = 0.f;
 }
 
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
   const int q0 = static_cast<int>(blockIdx.x) * kQTile;
   const float sc = p.gamma[bs % p.S] * kLog2e;
   const TQ* qb = static_cast<const TQ*>(p.q) + static_cast<int64_t>(bs) * p.T * RP;
-  const TQ* kbase = static_cast<const TQ*>(p.k) + static_cast<int64_t>(bs) * p.T * RP;
+  const TQ* kbase = static_cast<const TQ*>(p.k) + static_cast<int64_t>(bs) * p.Tk * RP;
   q8 qf[2][KS];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb)
@@ -163,12 +165,12 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
     for (int kk = 0; kk < KS; ++kk)
       qf[cb][kk] = load8(qb + static_cast<int64_t>(min(q0 + cb * 16 + c, p.T - 1)) * RP + kk * 32 + 8 * g);
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  const int k_end = p.causal ? min(q0 + kQTile, p.T) : p.T;
+  const int k_end = p.causal ? min(q0 + kQTile, p.Tk) : p.Tk;
   for (int k0 = wave * kQTile; k0 < k_end; k0 += 4 * kQTile) {
     f32x4 st[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const TQ* krow = kbase + static_cast<int64_t>(min(k0 + kb * 16 + c, p.T - 1)) * RP + 8 * g;
+      const TQ* krow = kbase + static_cast<int64_t>(min(k0 + kb * 16 + c, p.Tk - 1)) * RP + 8 * g;
       q8 kf[KS];
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) kf[kk] = load8(krow + kk * 32);
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = k0 + kb * 16 + 4 * g + i;
-          const bool live = key < p.T && (!p.causal || key <= q);
+          const bool live = key < p.Tk && (!p.causal || key <= q);
           t[kb * 4 + i] = live ? st[kb][cb][i] * sc : -INFINITY;
           mx = fmaxf(mx, t[kb * 4 + i]);
         }
@@ -282,17 +284,17 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   const float sc = gamma * kLog2e;
   const int64_t tiles = p.Tp / kQTile;
   const TQ* qb = static_cast<const TQ*>(p.q) + static_cast<int64_t>(bs) * p.T * RP;
-  const TQ* kbase = static_cast<const TQ*>(p.k) + static_cast<int64_t>(bs) * p.T * RP;
+  const TQ* kbase = static_cast<const TQ*>(p.k) + static_cast<int64_t>(bs) * p.Tk * RP;
   const TQ* qtb = static_cast<const TQ*>(p.qt) + bs * tiles * RP * kQTile;
-  const TQ* ktb = static_cast<const TQ*>(p.kt) + bs * tiles * RP * kQTile;
-  const TV* vb = static_cast<const TV*>(p.v) + static_cast<int64_t>(b) * p.T * D;
+  const TQ* ktb = static_cast<const TQ*>(p.kt) + bs * static_cast<int64_t>(p.Tkp / kQTile) * RP * kQTile;
+  const TV* vb = static_cast<const TV*>(p.v) + static_cast<int64_t>(b) * p.Tk * D;
   const TV* dob = static_cast<const TV*>(p.dout) + static_cast<int64_t>(bs) * p.T * D;
   const TV* dotb = static_cast<const TV*>(p.doutt) + bs * tiles * D * kQTile;
 
   // Resident per wave: its 16 keys as B operands of S (K rows) and dP
   // (V rows), and K^T of all 64 keys for its dQ columns.
   const int kw = k0 + wave * 16;
-  const int krow = min(kw + c, p.T - 1);
+  const int krow = min(kw + c, p.Tk - 1);
   q8 kf[KS];
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) kf[kk] = load8(kbase + static_cast<int64_t>(krow) * RP + kk * 32 + 8 * g);
@@ -400,7 +402,7 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
       for (int i = 0; i < 4; ++i) {
         const int ql = cb * 16 + 4 * g + i;
         const int q = q0 + ql;
-        const bool live = q < p.T && key < p.T && (!p.causal || key <= q);
+        const bool live = q < p.T && key < p.Tk && (!p.causal || key <= q);
         const float pr = live ? exp2f(sv[cb][i] * sc - rowv[ql]) : 0.f;
         const float ds = pr * (dp[cb][i] - rowv[kQTile + ql]);
         dgamma += ds * sv[cb][i];
@@ -477,13 +479,13 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int kr = kw + 4 * g + i;
-    if (kr >= p.T) continue;
+    if (kr >= p.Tk) continue;
 #pragma unroll
     for (int j = 0; j < NK; ++j)
-      unsafeAtomicAdd(p.dk + (static_cast<int64_t>(bs) * p.T + kr) * RP + j * 16 + c, dk_acc[j][i] * gamma);
+      unsafeAtomicAdd(p.dk + (static_cast<int64_t>(bs) * p.Tk + kr) * RP + j * 16 + c, dk_acc[j][i] * gamma);
 #pragma unroll
     for (int j = 0; j < NV; ++j)
-      unsafeAtomicAdd(p.dv + (static_cast<int64_t>(b) * p.T + kr) * D + j * 16 + c, dv_acc[j][i]);
+      unsafeAtomicAdd(p.dv + (static_cast<int64_t>(b) * p.Tk + kr) * D + j * 16 + c, dv_acc[j][i]);
   }
   dgamma = wave_sum(dgamma);
   if (lane == 0) unsafeAtomicAdd(p.dgamma + s, dgamma);
@@ -495,9 +497,9 @@ namespace {
 // that still gives at least 256 non-empty workgroups (one per CU).  Every
 // workgroup ends with 64 x (RP + D) atomic adds of its dK and dV rows, so
 // shorter runs than that cost more in atomics than they gain in balance.
-int pick_qchunk(int B_S, int T, bool causal) {
+int pick_qchunk(int B_S, int T, int Tk, bool causal) {
   const int n_qt = (T + kQTile - 1) / kQTile;
-  const int n_kt = (T + kKTile - 1) / kKTile;
+  const int n_kt = (Tk + kKTile - 1) / kKTile;
   for (int qc = 16; qc > 1; qc /= 2) {
     int64_t wgs = 0;
     for (int kt = 0; kt < n_kt; ++kt) {
@@ -514,13 +516,13 @@ int pick_qchunk(int B_S, int T, bool causal) {
 template <typename TQ, typename TV, int RP, int D>
 static void launch_bwd_d(BwdParams p, int B, hipStream_t stream) {
   const unsigned bs = static_cast<unsigned>(B * p.S);
-  hipLaunchKernelGGL((attention_bwd_prep_kernel<TQ, TV, RP, D>), dim3(static_cast<unsigned>(p.Tp / kQTile), bs),
-                     dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((attention_bwd_prep_kernel<TQ, TV, RP, D>),
+                     dim3(static_cast<unsigned>(max(p.Tp, p.Tkp) / kQTile), bs), dim3(256), 0, stream, p);
   const int n_qt = (p.T + kQTile - 1) / kQTile;
   hipLaunchKernelGGL((attention_lse_kernel<TQ, RP>), dim3(static_cast<unsigned>(n_qt), bs), dim3(256), 0, stream, p);
-  p.qchunk = pick_qchunk(B * p.S, p.T, p.causal != 0);
+  p.qchunk = pick_qchunk(B * p.S, p.T, p.Tk, p.causal != 0);
   p.n_chunks = (n_qt + p.qchunk - 1) / p.qchunk;
-  const int n_kt = (p.T + kKTile - 1) / kKTile;
+  const int n_kt = (p.Tk + kKTile - 1) / kKTile;
   hipLaunchKernelGGL((attention_bwd_kernel<TQ, TV, RP, D>), dim3(static_cast<unsigned>(n_kt * p.n_chunks), bs),
                      dim3(256), 0, stream, p);
 }
@@ -544,13 +546,13 @@ static void launch_bwd_t(const BwdParams& p, int B, hipStream_t stream) {
   }
 }
 
-AttentionBwdLayout attention_bwd_layout(int64_t BS, int64_t T, int64_t RP, int64_t D) {
+AttentionBwdLayout attention_bwd_layout(int64_t BS, int64_t T, int64_t Tk, int64_t RP, int64_t D) {
   auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
-  const int64_t Tp = round_up(T, kKeyPad);
+  const int64_t Tp = round_up(T, kKeyPad), Tkp = round_up(Tk, kKeyPad);
   AttentionBwdLayout l;
   l.qt = 0;
   l.kt = l.qt + up(BS * Tp * RP * 2);
-  l.doutt = l.kt + up(BS * Tp * RP * 2);
+  l.doutt = l.kt + up(BS * Tkp * RP * 2);
   l.lse2 = l.doutt + up(BS * Tp * D * 2);
   l.dvec = l.lse2 + up(BS * T * 4);
   l.bytes = l.dvec + up(BS * T * 4);
@@ -558,12 +560,13 @@ AttentionBwdLayout attention_bwd_layout(int64_t BS, int64_t T, int64_t RP, int64
 }
 
 void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace, hipStream_t stream) {
-  const AttentionBwdLayout l = attention_bwd_layout(static_cast<int64_t>(a.B) * a.S, a.T, a.RP, a.D);
+  const AttentionBwdLayout l = attention_bwd_layout(static_cast<int64_t>(a.B) * a.S, a.T, a.Tk, a.RP, a.D);
   char* ws = static_cast<char*>(workspace);
   BwdParams p{a.q, a.k, a.v, a.out, a.dout, ws + l.qt, ws + l.kt, ws + l.doutt,
               reinterpret_cast<float*>(ws + l.lse2), reinterpret_cast<float*>(ws + l.dvec), a.gamma,
               a.dq, a.dk, a.dv, a.dgamma,
-              a.S, a.T, static_cast<int>(round_up(a.T, kKeyPad)), a.RP, a.D, a.causal ? 1 : 0, 1, 1};
+              a.S, a.T, static_cast<int>(round_up(a.T, kKeyPad)), a.RP, a.D,
+              a.Tk, static_cast<int>(round_up(a.Tk, kKeyPad)), a.causal ? 1 : 0, 1, 1};
   if (a.qk_dtype == kF16) {
     if (a.v_dtype == kBF16) launch_bwd_t<_Float16, __bf16>(p, a.B, stream);
     else launch_bwd_t<_Float16, _Float16>(p, a.B, stream);

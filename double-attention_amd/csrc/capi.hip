@@ -114,7 +114,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 10; }
+int da_abi_version(void) { return 11; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -218,17 +218,18 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
   return check_launch("attention");
 }
 
-int64_t da_attention_backward_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t score_dim,
-                                              int64_t value_dim) {
-  if (batch < 1 || maps < 1 || length < 1 || score_dim < 1 || value_dim < 1) return 0;
-  return da::attention_bwd_layout(batch * maps, length, score_dim, value_dim).bytes;
+int64_t da_attention_backward_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t key_length,
+                                              int64_t score_dim, int64_t value_dim) {
+  if (batch < 1 || maps < 1 || length < 1 || key_length < 1 || score_dim < 1 || value_dim < 1) return 0;
+  return da::attention_bwd_layout(batch * maps, length, key_length, score_dim, value_dim).bytes;
 }
 
 int da_routed_attention_backward(const void* query, const void* key, const void* value, const void* out,
                                  const void* grad_out, const float* scales, int64_t batch, int64_t maps,
-                                 int64_t length, int64_t score_dim, int64_t value_dim, int flags, int qk_dtype,
-                                 int v_dtype, void* workspace, int64_t workspace_bytes, float* grad_query,
-                                 float* grad_key, float* grad_value, float* grad_scales, da_stream_t stream) {
+                                 int64_t length, int64_t key_length, int64_t score_dim, int64_t value_dim,
+                                 int flags, int qk_dtype, int v_dtype, void* workspace, int64_t workspace_bytes,
+                                 float* grad_query, float* grad_key, float* grad_value, float* grad_scales,
+                                 da_stream_t stream) {
   const bool types_ok = (qk_dtype == DA_F16 && (v_dtype == DA_BF16 || v_dtype == DA_F16)) ||
                         (qk_dtype == DA_BF16 && v_dtype == DA_BF16);
   if (!types_ok)
@@ -239,9 +240,13 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
     return fail(DA_ERR_UNSUPPORTED, "attention backward: score_dim %lld not in {64,128,256}", (long long)score_dim);
   if (!pow2_width(value_dim))
     return fail(DA_ERR_UNSUPPORTED, "attention backward: value_dim %lld not in {64,128,256,512}", (long long)value_dim);
-  if (batch < 0 || length < 0 || maps < 1 || maps > 64 || batch * maps > 65535 || length > (1LL << 24))
-    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: bad batch/maps/length");
+  if (batch < 0 || length < 0 || key_length < 0 || maps < 1 || maps > 64 || batch * maps > 65535 ||
+      length > (1LL << 24) || key_length > (1LL << 24))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: bad batch/maps/length/key_length");
+  if ((flags & DA_ATTN_CAUSAL) && key_length != length)
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: a causal mask needs key_length == length");
   if (batch == 0 || length == 0) return ok();
+  if (key_length == 0) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: queries need at least one key");
   const void* ptrs[] = {query, key, value, out, grad_out, scales, workspace, grad_query, grad_key, grad_value,
                         grad_scales};
   for (const void* ptr : ptrs)
@@ -255,7 +260,7 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
   if (!aligned(scales, 4) || !aligned(grad_scales, 4))
     return fail(DA_ERR_ALIGNMENT, "attention backward: scales must be 4-byte aligned");
   if (!aligned(workspace, 256)) return fail(DA_ERR_ALIGNMENT, "attention backward: workspace must be 256-byte aligned");
-  const int64_t need = da_attention_backward_workspace_bytes(batch, maps, length, score_dim, value_dim);
+  const int64_t need = da_attention_backward_workspace_bytes(batch, maps, length, key_length, score_dim, value_dim);
   if (workspace_bytes < need)
     return fail(DA_ERR_WORKSPACE, "attention backward: workspace of %lld bytes < %lld required",
                 (long long)workspace_bytes, (long long)need);
@@ -273,6 +278,7 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
   a.B = static_cast<int>(batch);
   a.S = static_cast<int>(maps);
   a.T = static_cast<int>(length);
+  a.Tk = static_cast<int>(key_length);
   a.RP = static_cast<int>(score_dim);
   a.D = static_cast<int>(value_dim);
   a.causal = (flags & DA_ATTN_CAUSAL) != 0;

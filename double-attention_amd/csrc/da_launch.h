@@ -84,16 +84,17 @@ struct AttentionArgs {
 // Backward of the outer attention, per score map (see attention_bwd.hip).
 struct AttentionBwdArgs {
   const void* q;         // [B*S][T][RP] routed queries, qk_dtype
-  const void* k;         // [B*S][T][RP] routed keys
-  const void* v;         // [B][T][D] values, v_dtype
+  const void* k;         // [B*S][Tk][RP] routed keys
+  const void* v;         // [B][Tk][D] values, v_dtype
   const void* out;       // [B*S][T][D] forward output, v_dtype
   const void* dout;      // [B*S][T][D] output gradient, v_dtype
   const float* gamma;    // [S] score scales
   float* dq;             // [B*S][T][RP]
-  float* dk;             // [B*S][T][RP]
-  float* dv;             // [B][T][D]
+  float* dk;             // [B*S][Tk][RP]
+  float* dv;             // [B][Tk][D]
   float* dgamma;         // [S]
   int B, S, T, RP, D;
+  int Tk;                // keys per sequence (== T when causal)
   bool causal;
   int qk_dtype, v_dtype;
 };
@@ -101,7 +102,7 @@ struct AttentionBwdArgs {
 struct AttentionBwdLayout {
   int64_t qt, kt, doutt, lse2, dvec, bytes;
 };
-AttentionBwdLayout attention_bwd_layout(int64_t BS, int64_t T, int64_t RP, int64_t D);
+AttentionBwdLayout attention_bwd_layout(int64_t BS, int64_t T, int64_t Tk, int64_t RP, int64_t D);
 void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace, hipStream_t stream);
 
 struct GemmSegment {

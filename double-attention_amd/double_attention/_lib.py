@@ -45,7 +45,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -129,10 +129,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_linear": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _vp, _vp]),
     "da_linear_ex": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "da_layer_norm": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _f32, _i32, _vp, _vp]),
-    "da_attention_backward_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "da_attention_backward_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "da_routed_attention_backward": (
         _i32,
-        [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _i64,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _i64,
          _vp, _vp, _vp, _vp, _vp],
     ),
     "da_sda_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),

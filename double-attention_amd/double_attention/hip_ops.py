@@ -297,6 +297,92 @@ def _route_forward(
     return out
 
 
+def _route_backward_supported(x: Tensor, dictionary_key: Tensor, variant: RouteVariant) -> bool:
+    return (
+        variant.flags() == 0
+        and x.is_cuda
+        and x.dtype in (torch.float16, torch.bfloat16)
+        and x.shape[-1] in BACKWARD_SCORE_WIDTHS
+        and dictionary_key.shape[1] >= 1
+    )
+
+
+def _route_backward(
+    x: Tensor,
+    dictionary_key: Tensor,
+    dictionary_value: Tensor,
+    beta: Tensor | float,
+    eps: float,
+    normalize_input: bool,
+    normalize_output: bool,
+    grad: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of the softmax route (``ops.py:16-62``) on the attention backward kernels.
+
+    The route is one attention per row: the (normalized) row u is the query,
+    the key atoms the keys, the value atoms the values, beta the score scale
+    and r = softmax(beta u Dk) Dv^T the output, then z = r / max(|r|, eps).
+    The host forms u, r (one route launch without the output norm) and the
+    output-norm backward dr; ``da_routed_attention_backward`` with the atoms
+    as a key sequence of their own returns du, dDk, dDv and dbeta; the
+    input-norm backward gives dx.  Returns fp32-accumulated gradients in the
+    dtypes of ``x`` and the dictionary tensors.
+    """
+
+    routing_dim = x.shape[-1]
+    atoms = dictionary_key.shape[1]
+    device = x.device
+    rows = x.detach().reshape(-1, routing_dim).float()
+    n = rows.shape[0]
+    if normalize_input:
+        x_norm = rows.norm(dim=1, keepdim=True)
+        u = rows / x_norm.clamp_min(eps)
+    else:
+        u = rows
+    u16 = _aligned(u.to(torch.float16))
+    # r without the output norm, from the fp16 rows on fp16 keys.
+    layout16 = route_layout(dictionary_key.detach(), dictionary_value.detach(), torch.float16)
+    beta_t = beta.detach().float().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
+    r = _route_forward(u16, layout16, beta_t, eps, False, False, RouteVariant()).float()
+    g = grad.detach().reshape(-1, routing_dim).float()
+    if normalize_output:
+        r_norm = r.norm(dim=1, keepdim=True)
+        z = r / r_norm.clamp_min(eps)
+        dr = torch.where(r_norm > eps, (g - z * (z * g).sum(1, keepdim=True)) / r_norm.clamp_min(eps), g / eps)
+    else:
+        dr = g
+    keys = _aligned(dictionary_key.detach().t().to(torch.float16))
+    values = _aligned(dictionary_value.detach().t().to(torch.bfloat16))
+    out = _aligned(r.to(torch.bfloat16))
+    go = _aligned(dr.to(torch.bfloat16))
+    lib = _lib.get()
+    ws_bytes = lib.da_attention_backward_workspace_bytes(1, 1, n, atoms, routing_dim, routing_dim)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    du = torch.empty(n, routing_dim, dtype=torch.float32, device=device)
+    dkt = torch.empty(atoms, routing_dim, dtype=torch.float32, device=device)
+    dvt = torch.empty(atoms, routing_dim, dtype=torch.float32, device=device)
+    dbeta = torch.empty(1, dtype=torch.float32, device=device)
+    _lib.check(
+        lib.da_routed_attention_backward(
+            u16.data_ptr(), keys.data_ptr(), values.data_ptr(), out.data_ptr(), go.data_ptr(), beta_t.data_ptr(),
+            1, 1, n, atoms, routing_dim, routing_dim, 0, _lib.DA_F16, _lib.DA_BF16,
+            workspace.data_ptr(), ws_bytes, du.data_ptr(), dkt.data_ptr(), dvt.data_ptr(), dbeta.data_ptr(),
+            _stream(device),
+        ),
+        "dictionary_route_hip backward",
+    )
+    if normalize_input:
+        dx = torch.where(x_norm > eps, (du - u * (u * du).sum(1, keepdim=True)) / x_norm.clamp_min(eps), du / eps)
+    else:
+        dx = du
+    return (
+        dx.reshape(x.shape).to(x.dtype),
+        dkt.t().to(dictionary_key.dtype),
+        dvt.t().to(dictionary_value.dtype),
+        dbeta,
+    )
+
+
 class _RouteFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, variant):  # type: ignore[override]
@@ -314,6 +400,16 @@ class _RouteFunction(torch.autograd.Function):
         saved = ctx.saved_tensors
         x, dk, dv = saved[:3]
         beta = saved[3] if ctx.beta_is_tensor else ctx.beta
+        if _route_backward_supported(x, dk, ctx.variant):
+            dx, ddk, ddv, dbeta = _route_backward(x, dk, dv, beta, ctx.eps, *ctx.flags, grad)
+            return (
+                dx if ctx.needs_input_grad[0] else None,
+                ddk if ctx.needs_input_grad[1] else None,
+                ddv if ctx.needs_input_grad[2] else None,
+                dbeta.reshape(beta.shape).to(beta.dtype) if ctx.beta_is_tensor and ctx.needs_input_grad[3] else None,
+                None, None, None, None,
+            )
+        # Route variants and 512-wide rows: recompute through the torch route.
         with torch.enable_grad():
             inputs = [t.detach().requires_grad_(t.requires_grad) for t in (x, dk, dv)]
             beta_in = beta.detach().requires_grad_(beta.requires_grad) if ctx.beta_is_tensor else beta
@@ -478,7 +574,7 @@ def _attention_backward(
     go = _padded_rows(grad.detach().to(value.dtype), value_width)
     gamma = scales.detach().float().contiguous()
     lib = _lib.get()
-    ws_bytes = lib.da_attention_backward_workspace_bytes(batch, maps, length, score_width, value_width)
+    ws_bytes = lib.da_attention_backward_workspace_bytes(batch, maps, length, length, score_width, value_width)
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     dq = torch.empty(rows, length, score_width, dtype=torch.float32, device=device)
     dk = torch.empty_like(dq)
@@ -487,7 +583,7 @@ def _attention_backward(
     _lib.check(
         lib.da_routed_attention_backward(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), go.data_ptr(), gamma.data_ptr(),
-            batch, maps, length, score_width, value_width,
+            batch, maps, length, length, score_width, value_width,
             _lib.DA_ATTN_CAUSAL if causal else 0, _half_code(q.dtype), _half_code(value.dtype),
             workspace.data_ptr(), ws_bytes, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(),
             _stream(device),

@@ -176,6 +176,16 @@ class SharedDictionaryAttention(nn.Module):
         query, key = fused.split(self.config.total_qk_width, dim=-1)
         return self._reshape_branches(query, batch, length), self._reshape_branches(key, batch, length)
 
+    def _hip_route_backward_fits(self, rows: Tensor) -> bool:
+        from . import hip_ops
+
+        cfg = self.config
+        variant = hip_ops.RouteVariant(
+            cfg.dictionary_activation == "silu", cfg.dictionary_assignment == "silu", cfg.dictionary_silu_gain,
+            cfg.standardize_dictionary_logits, cfg.standardized_logit_scale,
+        )
+        return hip_ops._route_backward_supported(rows, rows.new_empty(rows.shape[-1], 1), variant)
+
     def _route(self, x: Tensor, dictionary_key: Tensor, dictionary_value: Tensor, backend: str) -> Tensor:
         cfg = self.config
         if backend == "hip":
@@ -224,7 +234,10 @@ class SharedDictionaryAttention(nn.Module):
             dictionary_value = dictionary_value.to(query.dtype)
         # Q and K tokens route together, as one batch of rows (modules.py:236-241).
         pair = torch.cat((query, key), dim=2)
-        routed = self._route(pair, dictionary_key, dictionary_value, "torch")
+        # The HIP backward's recompute routes on the library's kernel when the
+        # native route backward covers this configuration.
+        route_backend = "hip" if attention == "hip" and self._hip_route_backward_fits(pair) else "torch"
+        routed = self._route(pair, dictionary_key, dictionary_value, route_backend)
         routed_query, routed_key = routed.split(x.shape[1], dim=2)
         score_query, score_key = assemble_score_maps(routed_query, routed_key, self.config.outer_maps)
         scales = score_scale_from_log(self.log_score_scales)

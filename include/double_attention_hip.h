@@ -177,27 +177,32 @@ int64_t da_attention_workspace_bytes(int64_t batch, int64_t maps, int64_t length
  * given dO_s = d loss / d out_s it writes the gradients of q, k, v and
  * scales (the products of triton_kernels.py:2093-2263 behind the autograd
  * function of triton_kernels.py:2290-2305; reference math ops.py:65-93).
- *   query, key:  [batch*maps, length, score_dim], qk_dtype
- *   value:       [batch, length, value_dim], v_dtype
+ *   query:       [batch*maps, length, score_dim], qk_dtype
+ *   key:         [batch*maps, key_length, score_dim], qk_dtype (key_length == length
+ *                for causal; other lengths serve cross attention such as the
+ *                dictionary route, where the atoms are the keys and values)
+ *   value:       [batch, key_length, value_dim], v_dtype
  *   out:         [batch*maps, length, value_dim], v_dtype (the forward output)
  *   grad_out:    [batch*maps, length, value_dim], v_dtype
  *   scales:      [maps] fp32 score scales (already exponentiated)
  *   workspace:   >= da_attention_backward_workspace_bytes(...) bytes,
  *                256-byte aligned (transposed tiles, row statistics)
- *   grad_query, grad_key: [batch*maps, length, score_dim] fp32
- *   grad_value:  [batch, length, value_dim] fp32 (summed over the maps)
+ *   grad_query:  [batch*maps, length, score_dim] fp32
+ *   grad_key:    [batch*maps, key_length, score_dim] fp32
+ *   grad_value:  [batch, key_length, value_dim] fp32 (summed over the maps)
  *   grad_scales: [maps] fp32
  *   score_dim in {64, 128, 256}; value_dim in {64, 128, 256, 512}; flags:
  *   DA_ATTN_CAUSAL only.  The gradients are zeroed and then accumulated with
  *   fp32 atomics, so their last bits vary between runs.
  */
-int64_t da_attention_backward_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t score_dim,
-                                              int64_t value_dim);
+int64_t da_attention_backward_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t key_length,
+                                              int64_t score_dim, int64_t value_dim);
 int da_routed_attention_backward(const void* query, const void* key, const void* value, const void* out,
                                  const void* grad_out, const float* scales, int64_t batch, int64_t maps,
-                                 int64_t length, int64_t score_dim, int64_t value_dim, int flags, int qk_dtype,
-                                 int v_dtype, void* workspace, int64_t workspace_bytes, float* grad_query,
-                                 float* grad_key, float* grad_value, float* grad_scales, da_stream_t stream);
+                                 int64_t length, int64_t key_length, int64_t score_dim, int64_t value_dim,
+                                 int flags, int qk_dtype, int v_dtype, void* workspace, int64_t workspace_bytes,
+                                 float* grad_query, float* grad_key, float* grad_value, float* grad_scales,
+                                 da_stream_t stream);
 
 /*
  * Q/K and V projections in one launch (modules.py:143-157 and 212):

@@ -16,6 +16,10 @@ Functions and what pins them (each check is in ``tests/test_oracle.py``):
                               the argmax atom; one-atom bank; input-scale
                               invariance; atom-permutation invariance; scalar
                               fp64 loop brute force; golden module vectors.
+* ``dictionary_route_backward``
+                              central finite differences in fp64 of every
+                              input (x, both banks, beta) with both norms on
+                              and off.
 * ``routed_attention``        first causal row = V[0]; all-equal keys ->
                               causal running mean; probabilities sum to one;
                               causal prefix invariance; brute-force loop.
@@ -37,6 +41,7 @@ from .sda import (
     bank_normalized,
     beta_from_log,
     dictionary_route,
+    dictionary_route_backward,
     double_attention_lm,
     gelu,
     l2_normalize,
@@ -52,6 +57,7 @@ __all__ = [
     "bank_normalized",
     "beta_from_log",
     "dictionary_route",
+    "dictionary_route_backward",
     "double_attention_lm",
     "gelu",
     "l2_normalize",

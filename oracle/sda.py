@@ -99,6 +99,50 @@ def dictionary_route(
     return l2_normalize(recon, -1, eps) if normalize_output else recon
 
 
+def _normalize_backward(v: np.ndarray, grad: np.ndarray, eps: float) -> np.ndarray:
+    """Gradient through ``v / max(|v|, eps)`` along the last axis."""
+
+    norm = np.sqrt(np.sum(v * v, axis=-1, keepdims=True))
+    unit = v / np.maximum(norm, eps)
+    projected = (grad - unit * np.sum(unit * grad, axis=-1, keepdims=True)) / np.maximum(norm, eps)
+    return np.where(norm > eps, projected, grad / eps)
+
+
+def dictionary_route_backward(
+    x: np.ndarray,
+    dictionary_key: np.ndarray,
+    dictionary_value: np.ndarray,
+    beta: float,
+    grad_out: np.ndarray,
+    eps: float = 1e-6,
+    normalize_input: bool = True,
+    normalize_output: bool = True,
+):
+    """Gradients of the softmax route of :func:`dictionary_route` (ops.py:16-62).
+
+    ``z = N_out(softmax(beta u Dk) Dv^T)`` with ``u = N_in(x)``; returns
+    ``(dx, dDk, dDv, dbeta)`` for ``d loss / dz = grad_out`` -- what the
+    reference's autograd returns for ``dictionary_route_reference``.
+    """
+
+    dt = x.dtype
+    u = l2_normalize(x, -1, eps) if normalize_input else x
+    logits = u @ dictionary_key.astype(dt)
+    weights = _softmax(logits * beta, -1)
+    recon = weights @ dictionary_value.astype(dt).T
+    d_recon = _normalize_backward(recon, grad_out, eps) if normalize_output else grad_out
+    d_weights = d_recon @ dictionary_value.astype(dt)
+    d_scores = weights * (d_weights - np.sum(weights * d_weights, axis=-1, keepdims=True))
+    d_logits = beta * d_scores
+    d_u = d_logits @ dictionary_key.astype(dt).T
+    dx = _normalize_backward(x, d_u, eps) if normalize_input else d_u
+    rows_u = u.reshape(-1, u.shape[-1])
+    d_key = rows_u.T @ d_logits.reshape(-1, d_logits.shape[-1])
+    d_value = d_recon.reshape(-1, d_recon.shape[-1]).T @ weights.reshape(-1, weights.shape[-1])
+    d_beta = float(np.sum(d_scores * logits))
+    return dx, d_key, d_value, d_beta
+
+
 def routed_attention(
     query: np.ndarray, key: np.ndarray, value: np.ndarray, scales: np.ndarray, causal: bool = True
 ) -> np.ndarray:

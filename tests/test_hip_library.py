@@ -155,23 +155,27 @@ def test_linear_ex_and_layer_norm_reject_bad_arguments() -> None:
 def test_attention_backward_rejects_bad_arguments() -> None:
     h = lib.get()
     f = _fake()
-    need = h.da_attention_backward_workspace_bytes(2, 3, 100, 128, 256)
+    need = h.da_attention_backward_workspace_bytes(2, 3, 100, 100, 128, 256)
     # Q^T, K^T and dO^T tiles over 128 padded tokens, then two fp32 rows
     # (6 * 100 * 4 = 2400 bytes, rounded up to 2560).
     assert need == 2 * (6 * 128 * 128 * 2) + 6 * 128 * 256 * 2 + 2 * 2560
-    good = [f, f, f, f, f, f, 2, 3, 100, 128, 256, lib.DA_ATTN_CAUSAL, lib.DA_BF16, lib.DA_BF16,
+    # Cross attention: K^T tiles follow the key count (300 -> 320 padded).
+    cross = h.da_attention_backward_workspace_bytes(2, 3, 100, 300, 128, 256)
+    assert cross == 6 * 128 * 128 * 2 + 6 * 320 * 128 * 2 + 6 * 128 * 256 * 2 + 2 * 2560
+    good = [f, f, f, f, f, f, 2, 3, 100, 100, 128, 256, lib.DA_ATTN_CAUSAL, lib.DA_BF16, lib.DA_BF16,
             f, need, f, f, f, f, None]
     cases = [
-        (9, 512, -2, "score_dim 512"),
-        (10, 96, -2, "value_dim 96"),
-        (11, 4, -1, "flag bits"),
-        (12, lib.DA_F32, -2, "qk_dtype"),
+        (10, 512, -2, "score_dim 512"),
+        (11, 96, -2, "value_dim 96"),
+        (12, 4, -1, "flag bits"),
+        (13, lib.DA_F32, -2, "qk_dtype"),
         (7, 65, -1, "maps"),
+        (9, 300, -1, "key_length == length"),
         (0, 0, -1, "null pointer"),
         (3, (1 << 20) + 4, -3, "16-byte"),
-        (18, (1 << 20) + 4, -3, "gradients"),
-        (14, (1 << 20) + 16, -3, "workspace must be 256-byte"),
-        (15, need - 1, -5, "workspace of"),
+        (19, (1 << 20) + 4, -3, "gradients"),
+        (15, (1 << 20) + 16, -3, "workspace must be 256-byte"),
+        (16, need - 1, -5, "workspace of"),
     ]
     for index, value, code, pattern in cases:
         args = list(good)
@@ -179,5 +183,9 @@ def test_attention_backward_rejects_bad_arguments() -> None:
         assert h.da_routed_attention_backward(*args) == code, pattern
         assert pattern in h.da_last_error().decode(), h.da_last_error()
     empty = list(good)
-    empty[8] = 0
+    empty[8] = empty[9] = 0
     assert h.da_routed_attention_backward(*empty) == 0
+    no_keys = list(good)
+    no_keys[9] = 0
+    no_keys[12] = 0
+    assert h.da_routed_attention_backward(*no_keys) == -1

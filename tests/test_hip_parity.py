@@ -620,8 +620,8 @@ def test_hip_backward_matches_torch_path() -> None:
 
 
 def test_module_backward_runs_native_attention_backward(monkeypatch) -> None:
-    # The module's backward recomputes through torch except for the outer
-    # attention, whose gradients come from the native backward kernels.  Each
+    # The module's backward recomputes the projections through torch; the
+    # route and the outer attention take the native backward kernels.  Each
     # gradient of the bf16 HIP module is held to max(3e-2, 2x) the relative
     # error of the same module on the bf16 torch path, both against fp32.
     # The score-scale gradient sums dS (q . k) over rows whose dS sums to
@@ -642,6 +642,14 @@ def test_module_backward_runs_native_attention_backward(monkeypatch) -> None:
         return original(*args)
 
     monkeypatch.setattr(da.hip_ops, "_attention_backward", counted)
+    route_calls = []
+    original_route = da.hip_ops._route_backward
+
+    def counted_route(*args):
+        route_calls.append(args[0].shape)
+        return original_route(*args)
+
+    monkeypatch.setattr(da.hip_ops, "_route_backward", counted_route)
     g = torch.Generator().manual_seed(7)
     x = torch.randn(2, 70, 512, generator=g).to(device, torch.bfloat16)
     w = torch.randn(2, 70, 512, generator=g).to(device)
@@ -650,7 +658,7 @@ def test_module_backward_runs_native_attention_backward(monkeypatch) -> None:
         xi = x.detach().to(dtype).clone().requires_grad_()
         (m(xi).float() * w).sum().backward()
         grads.append([xi.grad] + [p.grad for p in m.parameters()])
-    assert len(calls) == 1
+    assert len(calls) == 1 and len(route_calls) == 1
     names = ["x"] + [n for n, _ in module.named_parameters()]
 
     def rel(a, b):
@@ -691,3 +699,59 @@ def test_unsupported_width_raises_on_gpu() -> None:
     module = da.SharedDictionaryAttention(config).to(device, torch.bfloat16)
     with pytest.raises(NotImplementedError):
         module(torch.randn(1, 8, 512, device=device, dtype=torch.bfloat16))
+
+
+# ---------------------------------------------------------------- route backward
+
+
+ROUTE_BACKWARD_CASES = [
+    # (rows, routing_dim, atoms, normalize_input, normalize_output)
+    (65, 64, 100, True, True),
+    (300, 128, 512, True, True),
+    (257, 256, 1000, True, True),
+    (130, 128, 77, False, True),
+    (96, 256, 512, True, False),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", ROUTE_BACKWARD_CASES, ids=lambda c: "n{}r{}m{}{}{}".format(*c[:3], "i" if c[3] else "", "o" if c[4] else ""))
+def test_route_backward(case, dtype) -> None:
+    # The softmax route's gradients come from the attention backward kernels
+    # (rows as queries, atoms as keys and values); against the fp32 oracle's
+    # gradients (pinned by finite differences) at rel-L2 <= 1e-2 for x and
+    # the banks, 3e-2 for beta (its sum cancels as the scale gradient does).
+    device = _device()
+    rows, routing_dim, atoms, normalize_input, normalize_output = case
+    g = torch.Generator().manual_seed(rows + atoms)
+    x = torch.randn(rows, routing_dim, generator=g).to(device, dtype)
+    if not normalize_input:
+        x = torch.nn.functional.normalize(x.float(), dim=-1).to(dtype)
+    x.requires_grad_()
+    dk = unit_columns(routing_dim, atoms, dtype, device, rows).requires_grad_()
+    dv = unit_columns(routing_dim, atoms, dtype, device, rows + 1).requires_grad_()
+    beta = torch.tensor(6.0, device=device, requires_grad=True)
+    w = torch.randn(rows, routing_dim, generator=g).to(device, dtype)
+    calls = []
+    original = da.hip_ops._route_backward
+
+    def counted(*args):
+        calls.append(1)
+        return original(*args)
+
+    da.hip_ops._route_backward = counted
+    try:
+        out = da.dictionary_route_hip(x, dk, dv, beta, 1e-6, normalize_input=normalize_input,
+                                      normalize_output=normalize_output)
+        out.backward(w)
+    finally:
+        da.hip_ops._route_backward = original
+    assert calls == [1]
+    expected = oracle.dictionary_route_backward(np32(x), np32(dk), np32(dv), 6.0, np32(w), 1e-6,
+                                                normalize_input, normalize_output)
+    label = f"route backward {case} {dtype}"
+    for name, grad, exp in zip(("x", "dk", "dv"), (x.grad, dk.grad, dv.grad), expected[:3]):
+        assert grad.dtype == dtype
+        assert_parity(grad, exp, 1e-2, 3e-2 * float(np.abs(exp).max()), f"{label} d{name}")
+    db = float(beta.grad)
+    assert abs(db - expected[3]) <= 3e-2 * max(abs(expected[3]), 1e-3) + 1e-3, (db, expected[3])

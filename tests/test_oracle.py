@@ -167,6 +167,36 @@ def test_route_brute_force_loop() -> None:
         np.testing.assert_allclose(z[i], [v / n for v in rec], rtol=1e-12)
 
 
+@pytest.mark.parametrize(("normalize_input", "normalize_output"), [(True, True), (False, True), (True, False)])
+def test_route_backward_matches_finite_differences(normalize_input: bool, normalize_output: bool) -> None:
+    rng = np.random.default_rng(11)
+    r, m = 4, 6
+    x = rng.standard_normal((2, 3, r))
+    dk, dv = _unit_columns(r, m, rng), _unit_columns(r, m, rng)
+    beta = 2.3
+    w = rng.standard_normal((2, 3, r))
+    dx, ddk, ddv, dbeta = oracle.dictionary_route_backward(x, dk, dv, beta, w, 1e-6, normalize_input, normalize_output)
+
+    def loss(x_, dk_, dv_, b_):
+        out = oracle.dictionary_route(x_, dk_, dv_, b_, 1e-6, normalize_input=normalize_input,
+                                      normalize_output=normalize_output)
+        return float((out * w).sum())
+
+    h = 1e-6
+    for idx, arr, grad in ((0, x, dx), (1, dk, ddk), (2, dv, ddv)):
+        numeric = np.zeros_like(arr)
+        for pos in np.ndindex(arr.shape):
+            plus, minus = arr.copy(), arr.copy()
+            plus[pos] += h
+            minus[pos] -= h
+            args_p, args_m = [x, dk, dv, beta], [x, dk, dv, beta]
+            args_p[idx], args_m[idx] = plus, minus
+            numeric[pos] = (loss(*args_p) - loss(*args_m)) / (2 * h)
+        np.testing.assert_allclose(grad, numeric, rtol=1e-6, atol=1e-8)
+    numeric_beta = (loss(x, dk, dv, beta + h) - loss(x, dk, dv, beta - h)) / (2 * h)
+    np.testing.assert_allclose(dbeta, numeric_beta, rtol=1e-6, atol=1e-8)
+
+
 # ---------------------------------------------------------------- outer attention
 
 
