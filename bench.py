@@ -117,7 +117,8 @@ def backward_bench(args: argparse.Namespace) -> None:
     One step = dQ, dK, dV and d(scale) of ``routed_attention_hip`` for one
     output gradient (prep, LSE and key-tile kernels), timed with HIP events
     on the launch stream; beside it the fp32-softmax recompute through torch
-    autograd that the backward replaces.  FLOPs count the five products
+    autograd that the backward replaces, and one module training step
+    (forward + backward) on the HIP and on the bf16 torch backend.  FLOPs count the five products
     2 T^2 (3R + 2D) per map plus the LSE pass's 2 T^2 R, halved when causal.
     """
 
@@ -163,11 +164,30 @@ def backward_bench(args: argparse.Namespace) -> None:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps
 
+    # One SharedDictionaryAttention training step (forward + backward) on the
+    # HIP backend beside the same module on the bf16 torch backend.
+    torch.manual_seed(0)
+    hip_module = da.SharedDictionaryAttention(config).to(device, torch.bfloat16)
+    torch_module = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(device, torch.bfloat16)
+    torch_module.load_state_dict(hip_module.state_dict())
+    x = torch.randn(batch, length, d, generator=g).to(device, torch.bfloat16).requires_grad_()
+    grad_x = torch.randn(batch, length, d, generator=g).to(device, torch.bfloat16)
+
+    def train_step(m):
+        def run():
+            m(x).backward(grad_x)
+        return run
+
+    module_ms = {name: round(timed(train_step(m), max(1, min(args.steps, 20))), 4)
+                 for name, m in (("hip", hip_module), ("torch_bf16", torch_module))}
+    del hip_module, torch_module
+
     if not hip_ops._native_backward_supported(q, v):
         print(json.dumps({
             "metric": "outer-attention backward (dQ, dK, dV, dscale) on 1 MI355X",
             "value": None, "unit": "TFLOP/s",
             "note": f"score width {rp} has no native backward (widths up to 256); autograd recomputes in torch",
+            "module_fwd_bwd_ms": module_ms,
             "config": {"workload": description, "score_dim": rp},
         }), flush=True)
         return
@@ -182,6 +202,7 @@ def backward_bench(args: argparse.Namespace) -> None:
         "steps": args.steps,
         "torch_recompute_ms": None if ref_ms is None else round(ref_ms, 4),
         "speedup_vs_recompute": None if ref_ms is None else round(ref_ms / ms, 2),
+        "module_fwd_bwd_ms": module_ms,
         "dtype": "fp16 q/k, bf16 v",
         "config": {"workload": description, "batch": batch, "maps": S, "length": length, "score_dim": rp,
                    "value_dim": d, "causal": causal},
