@@ -181,6 +181,27 @@ def backward_bench(args: argparse.Namespace) -> None:
     module_ms = {name: round(timed(train_step(m), max(1, min(args.steps, 20))), 4)
                  for name, m in (("hip", hip_module), ("torch_bf16", torch_module))}
     del hip_module, torch_module
+    lm_ms = None
+    if args.workload == "c4":
+        # The LM training step (token ids to loss, then backward) on both
+        # backends: the counterpart of the reference's LM fwd+bwd benchmark.
+        kwargs = dict(dictionary_group_size=LM_LAYERS, feedforward_dim=LM_FEEDFORWARD)
+        hip_lm = da.DoubleAttentionLM(LM_VOCAB, length, config, LM_LAYERS, **kwargs).to(device, torch.bfloat16)
+        torch_lm = da.DoubleAttentionLM(
+            LM_VOCAB, length, config.with_updates(backend="torch"), LM_LAYERS, **kwargs
+        ).to(device, torch.bfloat16)
+        torch_lm.load_state_dict(hip_lm.state_dict())
+        ids = torch.randint(0, LM_VOCAB, (batch, length), generator=g).to(device)
+        targets = torch.randint(0, LM_VOCAB, (batch, length), generator=g).to(device)
+
+        def lm_step(m):
+            def run():
+                m(ids, targets)[1].backward()
+            return run
+
+        lm_ms = {name: round(timed(lm_step(m), max(1, min(args.steps, 20))), 4)
+                 for name, m in (("hip", hip_lm), ("torch_bf16", torch_lm))}
+        del hip_lm, torch_lm
 
     if not hip_ops._native_backward_supported(q, v):
         print(json.dumps({
@@ -203,6 +224,7 @@ def backward_bench(args: argparse.Namespace) -> None:
         "torch_recompute_ms": None if ref_ms is None else round(ref_ms, 4),
         "speedup_vs_recompute": None if ref_ms is None else round(ref_ms / ms, 2),
         "module_fwd_bwd_ms": module_ms,
+        "lm_fwd_bwd_ms": lm_ms,
         "dtype": "fp16 q/k, bf16 v",
         "config": {"workload": description, "batch": batch, "maps": S, "length": length, "score_dim": rp,
                    "value_dim": d, "causal": causal},

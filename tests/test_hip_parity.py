@@ -556,6 +556,53 @@ def test_lm_c4_qk2_s2_tied(dtype) -> None:
                   label=f"lm c4 {dtype}")
 
 
+def test_lm_training_gradients(monkeypatch) -> None:
+    # One training step of a two-layer tied LM (the C4 preset) with the HIP
+    # backend: the attention layers' route and outer attention run the native
+    # backward kernels; every gradient is held to max(3e-2, 2x) the relative
+    # error of the same LM on the bf16 torch path, both against fp32.
+    device = _device()
+    config = da.experiment_config("qk2-s2", untied_dictionary=False, backend="hip")
+    torch.manual_seed(3)
+    kwargs = dict(dictionary_group_size=2, feedforward_dim=1536)
+    models = [
+        da.DoubleAttentionLM(512, 64, config, 2, **kwargs).to(device, torch.bfloat16),
+        da.DoubleAttentionLM(512, 64, config.with_updates(backend="torch"), 2, **kwargs).to(device, torch.bfloat16),
+        da.DoubleAttentionLM(512, 64, config.with_updates(backend="torch"), 2, **kwargs).to(device, torch.float32),
+    ]
+    models[1].load_state_dict(models[0].state_dict())
+    models[2].load_state_dict({k: v.float() for k, v in models[0].state_dict().items()})
+    calls = []
+    for fn in ("_attention_backward", "_route_backward"):
+        original = getattr(da.hip_ops, fn)
+
+        def counted(*args, _original=original, _name=fn):
+            calls.append(_name)
+            return _original(*args)
+
+        monkeypatch.setattr(da.hip_ops, fn, counted)
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, 512, (8, 64), generator=g).to(device)
+    targets = torch.randint(0, 512, (8, 64), generator=g).to(device)
+    for m in models:
+        _, loss = m(ids, targets)
+        loss.float().backward()
+    assert calls.count("_attention_backward") == 2 and calls.count("_route_backward") == 2
+
+    def rel(a, b):
+        return float((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-30))
+
+    worst = 0.0
+    for (name, p_hip), p_t16, p_ref in zip(models[0].named_parameters(), models[1].parameters(), models[2].parameters()):
+        if p_ref.grad is None:
+            continue
+        assert p_hip.grad is not None and torch.isfinite(p_hip.grad).all(), name
+        err, bound = rel(p_hip.grad, p_ref.grad), max(3e-2, 2 * rel(p_t16.grad, p_ref.grad))
+        worst = max(worst, err / bound)
+        assert err <= bound, f"d{name}: rel {err:.3e} > {bound:.3e}"
+    print(f"[parity] lm training gradients: worst error / bound = {worst:.2f}", flush=True)
+
+
 @pytest.mark.parametrize("preset", ["a1-d1536-qffn", "a1-r512-d1536-qffn"])
 def test_lm_q_dictionary_feedforward(preset) -> None:
     # The Q-dictionary FFN (modules.py:348-356) expands through the same
