@@ -228,7 +228,10 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
   }
 }
 
-template <typename TQ, typename TV, int RP, int D>
+// SPLIT = 2 (512-wide scores): two workgroups per (key tile, query run),
+// each forming S, P, dP and dS in full but accumulating half of the dV, dK
+// and dQ columns, so the accumulators fit the register file.
+template <typename TQ, typename TV, int RP, int D, int SPLIT>
 __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   typedef typename Elem<TQ>::v8 q8;
   typedef typename Elem<TV>::v8 v8;
@@ -236,17 +239,18 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   typedef typename Elem<TV>::v4 v4;
   constexpr int KS = RP / 32;       // 32-deep steps over the score width
   constexpr int DC = D / 32;        // 32-deep steps over the value width
-  constexpr int NV = D / 16;        // 16-wide dV column blocks
-  constexpr int NK = RP / 16;       // 16-wide dK column blocks
+  constexpr int NV = D / 16 / SPLIT;    // 16-wide dV column blocks of this workgroup
+  constexpr int NK = RP / 16 / SPLIT;   // 16-wide dK column blocks
   constexpr int GV = NV < 8 ? NV : 8, GK = NK < 8 ? NK : 8;   // B operands per read group
-  constexpr int RB = RP / 64;       // dQ column blocks per wave
+  constexpr int RB = RP / 64 / SPLIT;   // dQ column blocks per wave
+  static_assert(RB >= 1 && NV >= 1, "the split needs wide scores and values");
   constexpr int QP = row_pitch(RP), VP = row_pitch(D);
   // Staged per step by LDS DMA: Q and dO rows, Q^T and dO^T tile rows, each
   // row followed by one 16-byte pad slot (so QP, VP and kTPitch pitches).
   typedef PaddedTile<kQTile, RP / 8, false> QRows;
-  typedef PaddedTile<RP, 4, false> QCols;
+  typedef PaddedTile<RP / SPLIT, 4, false> QCols;   // Q^T rows of this workgroup's dK columns
   typedef PaddedTile<kQTile, D / 8, false> DRows;
-  typedef PaddedTile<D, 4, false> DCols;
+  typedef PaddedTile<D / SPLIT, 4, false> DCols;    // dO^T rows of its dV columns
   static_assert(QRows::PITCH * 16 == QP && DRows::PITCH * 16 == VP && QCols::PITCH * 16 == kTPitch, "pitches");
   constexpr int OFF_Q = 0;
   constexpr int OFF_QT = OFF_Q + QRows::BYTES;
@@ -269,9 +273,12 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   const int wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
   const int xcd = wg % kXcds, per_xcd = n_wg / kXcds, rem_xcd = n_wg % kXcds;
   const int logical = xcd * per_xcd + min(xcd, rem_xcd) + wg / kXcds;
-  const int n_kt = static_cast<int>(gridDim.x) / p.n_chunks;
+  const int n_kt = static_cast<int>(gridDim.x) / (p.n_chunks * SPLIT);
   const int bs = logical / static_cast<int>(gridDim.x);
-  const int rest = logical - bs * static_cast<int>(gridDim.x);
+  const int rest_h = logical - bs * static_cast<int>(gridDim.x);
+  const int half = rest_h % SPLIT;                  // which column half
+  const int rest = rest_h / SPLIT;
+  const int r_base = half * (RP / SPLIT), d_base = half * (D / SPLIT);
   const int chunk = rest / n_kt;
   const int kt = rest - chunk * n_kt;
   const int b = bs / p.S, s = bs - b * p.S;
@@ -306,7 +313,7 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   for (int j = 0; j < RB; ++j)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      ktf[j][ks] = load8(ktb + ((k0 / kQTile + ks) * RP + (wave + 4 * j) * 16 + c) * static_cast<int64_t>(kQTile) + 8 * g);
+      ktf[j][ks] = load8(ktb + ((k0 / kQTile + ks) * RP + r_base + (wave + 4 * j) * 16 + c) * static_cast<int64_t>(kQTile) + 8 * g);
 
   f32x4 dv_acc[NV], dk_acc[NK];
 #pragma unroll
@@ -334,7 +341,7 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
     for (int L = wave; L < QCols::LOADS; L += 4) {
       int r, ck;
       QCols::slot_chunk(L * 64 + lane, r, ck);
-      dma16(qtb + (static_cast<int64_t>(qt) * RP + r) * kQTile + ck * 8, lds + OFF_QT + L * 1024);
+      dma16(qtb + (static_cast<int64_t>(qt) * RP + r_base + r) * kQTile + ck * 8, lds + OFF_QT + L * 1024);
     }
     for (int L = wave; L < DRows::LOADS; L += 4) {
       int r, ck;
@@ -344,7 +351,7 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
     for (int L = wave; L < DCols::LOADS; L += 4) {
       int r, ck;
       DCols::slot_chunk(L * 64 + lane, r, ck);
-      dma16(dotb + (static_cast<int64_t>(qt) * D + r) * kQTile + ck * 8, lds + OFF_DOT + L * 1024);
+      dma16(dotb + (static_cast<int64_t>(qt) * D + d_base + r) * kQTile + ck * 8, lds + OFF_DOT + L * 1024);
     }
   };
   issue(qt_begin);
@@ -458,7 +465,7 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
         dsf[cb][ks] = *reinterpret_cast<const q8*>(lds + OFF_DS + (cb * 16 + c) * kDsPitch + (ks * 32 + 8 * g) * 2);
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
-      const int r = (wave + 4 * j) * 16 + c;
+      const int r = r_base + (wave + 4 * j) * 16 + c;
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
         f32x4 acc = zero4();
@@ -482,13 +489,13 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
     if (kr >= p.Tk) continue;
 #pragma unroll
     for (int j = 0; j < NK; ++j)
-      unsafeAtomicAdd(p.dk + (static_cast<int64_t>(bs) * p.Tk + kr) * RP + j * 16 + c, dk_acc[j][i] * gamma);
+      unsafeAtomicAdd(p.dk + (static_cast<int64_t>(bs) * p.Tk + kr) * RP + r_base + j * 16 + c, dk_acc[j][i] * gamma);
 #pragma unroll
     for (int j = 0; j < NV; ++j)
-      unsafeAtomicAdd(p.dv + (static_cast<int64_t>(b) * p.Tk + kr) * D + j * 16 + c, dv_acc[j][i]);
+      unsafeAtomicAdd(p.dv + (static_cast<int64_t>(b) * p.Tk + kr) * D + d_base + j * 16 + c, dv_acc[j][i]);
   }
   dgamma = wave_sum(dgamma);
-  if (lane == 0) unsafeAtomicAdd(p.dgamma + s, dgamma);
+  if (lane == 0 && half == 0) unsafeAtomicAdd(p.dgamma + s, dgamma);
 }
 
 namespace {
@@ -523,8 +530,11 @@ static void launch_bwd_d(BwdParams p, int B, hipStream_t stream) {
   p.qchunk = pick_qchunk(B * p.S, p.T, p.Tk, p.causal != 0);
   p.n_chunks = (n_qt + p.qchunk - 1) / p.qchunk;
   const int n_kt = (p.Tk + kKTile - 1) / kKTile;
-  hipLaunchKernelGGL((attention_bwd_kernel<TQ, TV, RP, D>), dim3(static_cast<unsigned>(n_kt * p.n_chunks), bs),
-                     dim3(256), 0, stream, p);
+  // 512-wide scores split their columns over two workgroups (the
+  // accumulators and resident K fragments would not fit one wave otherwise).
+  constexpr int SPLIT = RP == 512 ? 2 : 1;
+  hipLaunchKernelGGL((attention_bwd_kernel<TQ, TV, RP, D, SPLIT>),
+                     dim3(static_cast<unsigned>(n_kt * p.n_chunks * SPLIT), bs), dim3(256), 0, stream, p);
 }
 
 template <typename TQ, typename TV, int RP>
@@ -542,7 +552,8 @@ static void launch_bwd_t(const BwdParams& p, int B, hipStream_t stream) {
   switch (p.RP) {
     case 64: launch_bwd_r<TQ, TV, 64>(p, B, stream); break;
     case 128: launch_bwd_r<TQ, TV, 128>(p, B, stream); break;
-    default: launch_bwd_r<TQ, TV, 256>(p, B, stream); break;
+    case 256: launch_bwd_r<TQ, TV, 256>(p, B, stream); break;
+    default: launch_bwd_r<TQ, TV, 512>(p, B, stream); break;
   }
 }
 

@@ -236,8 +236,8 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
     return fail(DA_ERR_UNSUPPORTED,
                 "attention backward: (qk_dtype, v_dtype) must be (F16,BF16), (F16,F16) or (BF16,BF16)");
   if (flags & ~DA_ATTN_CAUSAL) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: unknown flag bits 0x%x", flags);
-  if (score_dim != 64 && score_dim != 128 && score_dim != 256)
-    return fail(DA_ERR_UNSUPPORTED, "attention backward: score_dim %lld not in {64,128,256}", (long long)score_dim);
+  if (!pow2_width(score_dim))
+    return fail(DA_ERR_UNSUPPORTED, "attention backward: score_dim %lld not in {64,128,256,512}", (long long)score_dim);
   if (!pow2_width(value_dim))
     return fail(DA_ERR_UNSUPPORTED, "attention backward: value_dim %lld not in {64,128,256,512}", (long long)value_dim);
   if (batch < 0 || length < 0 || key_length < 0 || maps < 1 || maps > 64 || batch * maps > 65535 ||

@@ -191,7 +191,7 @@ int64_t da_attention_workspace_bytes(int64_t batch, int64_t maps, int64_t length
  *   grad_key:    [batch*maps, key_length, score_dim] fp32
  *   grad_value:  [batch, key_length, value_dim] fp32 (summed over the maps)
  *   grad_scales: [maps] fp32
- *   score_dim in {64, 128, 256}; value_dim in {64, 128, 256, 512}; flags:
+ *   score_dim and value_dim in {64, 128, 256, 512}; flags:
  *   DA_ATTN_CAUSAL only.  The gradients are zeroed and then accumulated with
  *   fp32 atomics, so their last bits vary between runs.
  */

@@ -165,7 +165,7 @@ def test_attention_backward_rejects_bad_arguments() -> None:
     good = [f, f, f, f, f, f, 2, 3, 100, 100, 128, 256, lib.DA_ATTN_CAUSAL, lib.DA_BF16, lib.DA_BF16,
             f, need, f, f, f, f, None]
     cases = [
-        (10, 512, -2, "score_dim 512"),
+        (10, 96, -2, "score_dim 96"),
         (11, 96, -2, "value_dim 96"),
         (12, 4, -1, "flag bits"),
         (13, lib.DA_F32, -2, "qk_dtype"),
