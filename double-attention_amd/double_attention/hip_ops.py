@@ -298,9 +298,10 @@ def _route_forward(
 
 
 # Routing widths whose route backward runs on the attention backward kernels.
-# At 512-wide rows the two-workgroup split recomputes S and dP per half, and
-# the torch path's dense GEMMs are faster (C3: 3.1 against 2.2 ms per module
-# step), so 512 stays on the torch recompute.
+# Up to 256 it takes about the time of the torch recompute and keeps fp32
+# accumulation throughout; at 512-wide rows the two-workgroup split recomputes
+# S and dP per half and the torch path's dense GEMMs are faster (C3: 3.1
+# against 2.2 ms per module step), so 512 stays on the torch recompute.
 ROUTE_BACKWARD_WIDTHS = (64, 128, 256)
 
 
