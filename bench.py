@@ -5,7 +5,7 @@ normalization, Q/K/V projection, fused route, flash attention with the map
 mix, output projection) on one synthetic batch already resident in HBM, the
 same unit of work as the reference's ``benchmarks/benchmark_attention.py``
 forward mode.  The default workload is the north-star configuration: preset
-a1, x = [8, 512, 512] bf16 (BASELINE config 1).  ``--workload c4`` times the
+a1, x = [8, 512, 512] bf16.  ``--workload c4`` times the
 six-layer tied language model instead: a step is one ``DoubleAttentionLM``
 forward over [64, 64] token ids, and the per-kernel lines are one layer's.
 
