@@ -233,3 +233,22 @@ def test_route_variant_flags_follow_the_config() -> None:
     assert v.logit_scale(256) == 256 ** -0.5   # ops.py:50-54 default
     v = RouteVariant.of_config(da.experiment_config("a1-no-softmax-g4"))
     assert v.flags() == _lib.DA_ROUTE_DIRECT_SILU and v.silu_gain == 4.0
+
+
+def test_backward_dispatch_rules() -> None:
+    # Which shapes take the native backward kernels (host logic only).
+    from double_attention import hip_ops
+
+    q = torch.empty(2, 3, 10, 512)
+    assert hip_ops._native_backward_supported(q, torch.empty(2, 10, 512))
+    assert not hip_ops._native_backward_supported(torch.empty(1, 2, 10, 600), torch.empty(1, 10, 64))
+    assert not hip_ops._native_backward_supported(torch.empty(40000, 2, 4, 64), torch.empty(40000, 4, 64))
+    standard, silu = hip_ops.RouteVariant(), hip_ops.RouteVariant(silu_logits=True)
+    key = torch.empty(256, 100)
+    # CPU tensors never take the GPU path; on the GPU the width and variant decide.
+    assert not hip_ops._route_backward_supported(torch.empty(5, 256, dtype=torch.bfloat16), key, standard)
+    meta = torch.empty(5, 256, dtype=torch.bfloat16, device="meta")
+    assert not hip_ops._route_backward_supported(meta, key, standard)   # not a CUDA tensor
+    assert hip_ops.ROUTE_BACKWARD_WIDTHS == (64, 128, 256)
+    assert 512 in hip_ops.BACKWARD_SCORE_WIDTHS
+    assert silu.flags() != 0 and standard.flags() == 0
