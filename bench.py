@@ -235,6 +235,7 @@ def main() -> None:
     args = parse_args()
     if args.backward and args.gpus == 1:
         backward_bench(args)
+        calibration_copy(args.copy_mib, "cuda:0")
         return
     if args.gpus != 1:
         print(
@@ -482,14 +483,24 @@ def main() -> None:
     print(json.dumps(line), flush=True)
     del out
 
-    if args.copy_mib > 0:
-        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=device)
-        dst = torch.empty_like(src)
-        src.fill_(1)
-        torch.cuda.synchronize()
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+    calibration_copy(args.copy_mib, device)
+
+
+def calibration_copy(mib: int, device) -> None:
+    """Copy a device buffer of ``mib`` MiB three times: a kernel of known
+    traffic that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
+
+    import torch
+
+    if mib <= 0:
+        return
+    src = torch.empty(mib << 20, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 if __name__ == "__main__":
