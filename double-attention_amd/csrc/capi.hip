@@ -114,7 +114,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 11; }
+int da_abi_version(void) { return 12; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -436,7 +436,13 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
   if (W % 8) return fail(DA_ERR_UNSUPPORTED, "forward: qk width must be a multiple of 8");
   const bool norm_in = a->flags & DA_SDA_NORMALIZE_INPUT;
   const int key_dtype = norm_in ? DA_F16 : a->dtype;
-  int rflags = da::kRouteBetaIsLog | da::kRouteUnitKeys;   // the bank comes from da_dictionary_normalize
+  // Unit key atoms bound every logit by |beta| (fixed-reference softmax); that
+  // holds only for a bank this call normalizes or one the caller says came
+  // from da_dictionary_normalize.  Any other bank takes the online softmax.
+  if (a->flags & ~(DA_SDA_NORMALIZE_INPUT | DA_SDA_NORMALIZE_OUTPUT | DA_SDA_CAUSAL | DA_SDA_CONCAT | DA_SDA_UNIT_KEYS))
+    return fail(DA_ERR_INVALID_ARGUMENT, "forward: unknown flag bits 0x%x", a->flags);
+  int rflags = da::kRouteBetaIsLog;
+  if (a->raw_key || (a->flags & DA_SDA_UNIT_KEYS)) rflags |= da::kRouteUnitKeys;
   if (norm_in) rflags |= da::kRouteNormalizeInput;
   if (a->flags & DA_SDA_NORMALIZE_OUTPUT) rflags |= da::kRouteNormalizeOutput;
   if (a->route_variant & ~kRouteVariantMask)

@@ -33,6 +33,7 @@ DA_SDA_NORMALIZE_INPUT = 1
 DA_SDA_NORMALIZE_OUTPUT = 2
 DA_SDA_CAUSAL = 4
 DA_SDA_CONCAT = 8
+DA_SDA_UNIT_KEYS = 16
 
 DA_ACT_NONE = 0
 DA_ACT_GELU = 1
@@ -45,7 +46,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64

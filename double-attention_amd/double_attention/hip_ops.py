@@ -870,6 +870,7 @@ def shared_dictionary_attention_hip(
         | (_lib.DA_SDA_NORMALIZE_OUTPUT if config.normalize_routing_output else 0)
         | (_lib.DA_SDA_CAUSAL if config.causal else 0)
         | (_lib.DA_SDA_CONCAT if concat else 0)
+        | (_lib.DA_SDA_UNIT_KEYS if layout.unit or raw_bank is not None else 0)
     )
     args = _lib.SdaForwardArgs(
         xc.data_ptr(), batch, length, model_dim,

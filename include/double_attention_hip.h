@@ -78,6 +78,11 @@ typedef struct ihipStream_t* da_stream_t; /* hipStream_t; NULL = default stream 
 #define DA_SDA_NORMALIZE_OUTPUT 2
 #define DA_SDA_CAUSAL 4
 #define DA_SDA_CONCAT 8             /* map_combine == "concat" */
+#define DA_SDA_UNIT_KEYS 16         /* key_t holds atoms of L2 norm <= 1 (da_dictionary_normalize
+                                       output): the route may then bound its logits by |beta|
+                                       (DA_ROUTE_UNIT_KEYS).  Implied when raw_key is set (the call
+                                       normalizes the bank itself); never set it for a bank whose
+                                       atoms were not normalized. */
 
 /* ABI version of this header (bumped on any signature change). */
 int da_abi_version(void);

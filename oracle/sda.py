@@ -225,12 +225,16 @@ def shared_dictionary_attention(
     normalized_dictionary: tuple[np.ndarray, np.ndarray] | None = None,
     prefix: str = "",
     return_routed: bool = False,
+    routed: tuple[np.ndarray, np.ndarray] | None = None,
 ):
     """``SharedDictionaryAttention.forward`` (modules.py:190-291) on NumPy arrays.
 
     ``params`` holds the module's state-dict entries under ``prefix``; the
     bank comes from ``prefix + 'bank.'`` unless ``normalized_dictionary`` is
-    given.
+    given.  ``routed`` = (routed query, routed key), each ``[B, H, T, R]``,
+    replaces the route's output (modules.py:239-241) so that the stages after
+    it (score maps, outer attention, mix, output projection) can be checked
+    on given routed rows.
     """
 
     dt = x.dtype
@@ -258,14 +262,17 @@ def shared_dictionary_attention(
     else:
         dk, dv = (np.asarray(t, dtype=dt) for t in normalized_dictionary)
     beta = beta_from_log(p("log_beta"))
-    routed = dictionary_route(
-        np.concatenate([query, key], axis=2), dk, dv, beta, eps,
-        _cfg(cfg, "dictionary_activation"), _cfg(cfg, "dictionary_assignment"),
-        _cfg(cfg, "dictionary_silu_gain"), _cfg(cfg, "standardize_dictionary_logits"),
-        _cfg(cfg, "standardized_logit_scale"), _cfg(cfg, "normalize_routing_input"),
-        _cfg(cfg, "normalize_routing_output"),
-    )
-    routed_query, routed_key = routed[:, :, :length], routed[:, :, length:]
+    if routed is None:
+        pair = dictionary_route(
+            np.concatenate([query, key], axis=2), dk, dv, beta, eps,
+            _cfg(cfg, "dictionary_activation"), _cfg(cfg, "dictionary_assignment"),
+            _cfg(cfg, "dictionary_silu_gain"), _cfg(cfg, "standardize_dictionary_logits"),
+            _cfg(cfg, "standardized_logit_scale"), _cfg(cfg, "normalize_routing_input"),
+            _cfg(cfg, "normalize_routing_output"),
+        )
+        routed_query, routed_key = pair[:, :, :length], pair[:, :, length:]
+    else:
+        routed_query, routed_key = (np.asarray(t, dtype=dt) for t in routed)
     score_query, score_key = assemble_score_maps(routed_query, routed_key, maps)
     scales = score_scale_from_log(p("log_score_scales"))
     map_output = routed_attention(score_query, score_key, value, scales, _cfg(cfg, "causal"))
