@@ -205,14 +205,23 @@ class SharedDictionaryAttention(nn.Module):
             cfg.normalize_routing_input, cfg.normalize_routing_output,
         )
 
-    def _combine(self, x: Tensor, map_output: Tensor) -> tuple[Tensor, Tensor]:
+    def _combine(self, x: Tensor, map_output: Tensor, fp32_weight_grad: bool = False) -> tuple[Tensor, Tensor]:
         if self.config.map_combine == "weighted_sum":
             if self.map_mix_logits is None:
                 return self.output(map_output[:, 0]), x.new_ones(1)
             weights = torch.softmax(self.map_mix_logits, dim=0).to(map_output.dtype)
+            factors = weights.float()
+            if fp32_weight_grad:
+                # Same forward value (the weights rounded to the map dtype),
+                # but the gradient reaches the logits in fp32: the per-map
+                # gradients sum dY.O_s are large and nearly equal, and their
+                # softmax backward takes differences that a 16-bit rounding
+                # of each would swamp.
+                exact = torch.softmax(self.map_mix_logits.float(), dim=0)
+                factors = exact + (factors - exact).detach()
             # The weighted map sum in fp32, rounded once (as einsum's fp32
             # accumulation does), without einsum's internal transposed bmm.
-            combined = (map_output.float() * weights.float()[None, :, None, None]).sum(1).to(map_output.dtype)
+            combined = (map_output.float() * factors[None, :, None, None]).sum(1).to(map_output.dtype)
             return self.output(combined), weights
         weights = x.new_full((self.config.outer_maps,), 1.0 / self.config.outer_maps)
         return self.output(map_output.permute(0, 2, 1, 3).flatten(2)), weights
@@ -249,7 +258,7 @@ class SharedDictionaryAttention(nn.Module):
             map_output = hip_ops.routed_attention_hip(score_query, score_key, dense_value, scales, self.config.causal)
         else:
             map_output = routed_attention_reference(score_query, score_key, dense_value, scales, self.config.causal)
-        output, weights = self._combine(x, map_output)
+        output, weights = self._combine(x, map_output, fp32_weight_grad=attention == "hip")
         if not return_aux:
             return output
         return output, DoubleAttentionAux(
