@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/double_attention_hip.h"
@@ -114,7 +115,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 12; }
+int da_abi_version(void) { return 13; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -535,3 +536,57 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* a, da_stre
 }
 
 }  // extern "C"
+
+// Scratch of the allocation-free forward: one array per GPU, held until the
+// process ends.  Host code never passes `scratch` itself to a kernel (on the
+// host it names a shadow variable, not device memory): each device's address
+// comes from hipGetSymbolAddress, once per device, with that device current.
+static __device__ __align__(256) char scratch[DA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DA_ERR_LAUNCH, "noalloc forward: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(DA_ERR_UNSUPPORTED, "noalloc forward: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(DA_ERR_LAUNCH, "noalloc forward: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return DA_OK;
+}
+}  // namespace
+
+extern "C" int da_shared_dictionary_attention_forward_noalloc(const da_sda_forward_args* args, da_stream_t stream) {
+  if (!args) return fail(DA_ERR_INVALID_ARGUMENT, "noalloc forward: null args");
+  if (args->batch < 1 || args->length < 1 || args->model_dim < 1 || args->qk_branches < 1 || args->routing_dim < 1 ||
+      args->outer_maps < 1)
+    return fail(DA_ERR_INVALID_ARGUMENT, "noalloc forward: sizes must be positive");
+  const int64_t need = da_sda_workspace_bytes(args->batch, args->length, args->model_dim,
+                                              args->qk_branches * args->routing_dim, args->outer_maps,
+                                              (args->flags & DA_SDA_CONCAT) != 0, args->wo != nullptr);
+  if (need > DA_NOALLOC_SCRATCH_BYTES)
+    return fail(DA_ERR_WORKSPACE,
+                "noalloc forward: the problem needs %lld bytes of scratch, more than the %lld-byte per-GPU array "
+                "(use da_shared_dictionary_attention_forward with a workspace)",
+                (long long)need, (long long)DA_NOALLOC_SCRATCH_BYTES);
+  void* ptr = nullptr;
+  const int rc = scratch_of_current_device(&ptr);
+  if (rc) return rc;
+  // Nothing in the workspace needs to start at zero: every byte a kernel
+  // reads was written earlier in the same call.
+  da_sda_forward_args local = *args;
+  local.workspace = ptr;
+  local.workspace_bytes = DA_NOALLOC_SCRATCH_BYTES;
+  return da_shared_dictionary_attention_forward(&local, stream);
+}

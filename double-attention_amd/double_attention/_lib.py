@@ -46,7 +46,8 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 12
+ABI_VERSION = 13
+NOALLOC_SCRATCH_BYTES = 128 << 20
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -139,6 +140,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_sda_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),
     "da_sda_workspace_offset": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "da_shared_dictionary_attention_forward": (_i32, [ctypes.POINTER(SdaForwardArgs), _vp]),
+    "da_shared_dictionary_attention_forward_noalloc": (_i32, [ctypes.POINTER(SdaForwardArgs), _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

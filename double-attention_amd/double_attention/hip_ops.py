@@ -779,7 +779,7 @@ def qkv_projection_hip(
 
 class HipForwardResult(NamedTuple):
     output: Tensor
-    routed: Tensor   # [B, T, 2, H, R] fp16: routed query branches, then key branches
+    routed: Tensor | None   # [B, T, 2, H, R] fp16: routed query branches, then key branches
 
 
 def check_module_supported(config) -> None:
@@ -822,6 +822,7 @@ def shared_dictionary_attention_hip(
     dtype: torch.dtype,
     raw_bank: tuple[Tensor, Tensor | None] | None = None,
     residual: Tensor | None = None,
+    no_alloc: bool = False,
 ) -> HipForwardResult:
     """One ``SharedDictionaryAttention`` forward through the fused C entry point.
 
@@ -829,6 +830,9 @@ def shared_dictionary_attention_hip(
     normalizes them into ``layout`` (from ``own_bank_layout``), inside its
     projection launch.  ``residual`` ([B, T, d] of the output dtype) is added
     to the output projection's rounded result (the block's ``x + ...``).
+    ``no_alloc`` runs the allocation-free entry point, whose workspace is the
+    library's per-GPU scratch array: no workspace tensor is allocated, and
+    ``routed`` is None (the scratch belongs to the next call).
     """
 
     config = module.config
@@ -863,7 +867,7 @@ def shared_dictionary_attention_hip(
     width = config.total_qk_width
     lib = _lib.get()
     ws_bytes = lib.da_sda_workspace_bytes(batch, length, model_dim, width, config.outer_maps, int(concat), int(wo is not None))
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    workspace = None if no_alloc else torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
     out = torch.empty(batch, length, model_dim, dtype=dtype, device=x.device)
     flags = (
         (_lib.DA_SDA_NORMALIZE_INPUT if config.normalize_routing_input else 0)
@@ -879,7 +883,7 @@ def shared_dictionary_attention_hip(
         layout.key_t.data_ptr(), layout.value.data_ptr(),
         log_beta.data_ptr(), log_scales.data_ptr(), _ptr(mix),
         dtype_code(scalar_dtype), code, float(config.eps), flags,
-        workspace.data_ptr(), ws_bytes, out.data_ptr(),
+        _ptr(workspace), 0 if workspace is None else ws_bytes, out.data_ptr(),
     )
     if residual is not None:
         if residual.shape != out.shape or residual.dtype != dtype:
@@ -896,6 +900,10 @@ def shared_dictionary_attention_hip(
         args.raw_key = raw_key.data_ptr()
         args.raw_value = _ptr(raw_value)
         args.raw_dtype = dtype_code(raw_key.dtype)
+    if no_alloc:
+        _lib.check(lib.da_shared_dictionary_attention_forward_noalloc(args, _stream(x.device)),
+                   "shared_dictionary_attention_hip (no_alloc)")
+        return HipForwardResult(out, None)
     _lib.check(lib.da_shared_dictionary_attention_forward(args, _stream(x.device)), "shared_dictionary_attention_hip")
     routed_bytes = batch * length * 2 * width * 2
     routed = workspace[:routed_bytes].view(torch.float16).view(

@@ -310,6 +310,23 @@ int64_t da_sda_workspace_offset(int64_t batch, int64_t length, int64_t model_dim
 
 int da_shared_dictionary_attention_forward(const da_sda_forward_args* args, da_stream_t stream);
 
+/*
+ * Allocation-free variant of da_shared_dictionary_attention_forward.  It has
+ * no counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  args->workspace and args->workspace_bytes are
+ * ignored; the workspace is a library-owned device array of
+ * DA_NOALLOC_SCRATCH_BYTES per GPU (each GPU the library runs on holds it
+ * until the process ends), found once per device on its first call there.
+ * Problems whose da_sda_workspace_bytes exceed it fail with DA_ERR_WORKSPACE.
+ * The call itself allocates nothing.  Every call on one GPU shares that GPU's
+ * array, which keeps the last call's contents: calls that overlap on one GPU
+ * (other streams, other threads) race, so serialize them.  The caller still
+ * owns x, the weights, the bank layouts and out.
+ */
+#define DA_NOALLOC_SCRATCH_BYTES (128LL << 20)
+int da_shared_dictionary_attention_forward_noalloc(const da_sda_forward_args* args, da_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 17
+    assert len(names) == 18
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -189,3 +189,19 @@ def test_attention_backward_rejects_bad_arguments() -> None:
     no_keys[9] = 0
     no_keys[12] = 0
     assert h.da_routed_attention_backward(*no_keys) == -1
+
+
+def test_noalloc_forward_rejects_oversized_problems_on_the_host() -> None:
+    # The size check runs before anything touches a device: [8, 8192] tokens
+    # need more workspace than the library's per-GPU scratch array.
+    h = lib.get()
+    args = lib.SdaForwardArgs()
+    args.batch, args.length, args.model_dim = 8, 8192, 512
+    args.qk_branches, args.outer_maps, args.routing_dim, args.atoms = 1, 1, 256, 512
+    args.wo = _fake()
+    assert h.da_sda_workspace_bytes(8, 8192, 512, 256, 1, 0, 1) > lib.NOALLOC_SCRATCH_BYTES
+    rc = h.da_shared_dictionary_attention_forward_noalloc(ctypes.byref(args), None)
+    assert rc == -5
+    assert "scratch" in h.da_last_error().decode()
+    args.batch = 0
+    assert h.da_shared_dictionary_attention_forward_noalloc(ctypes.byref(args), None) == -1
