@@ -18,7 +18,7 @@
 //   O^T[d, q]  += sum_key V^T[d, key] P^T[key, q] (A = V^T from LDS, B = P in VGPRs)
 // so P never leaves registers, and every A fragment read from LDS feeds two
 // MFMAs (the two query blocks).  Key and V^T tiles are double-buffered in
-// padded LDS tiles (da_tile.h) filled by global->LDS DMA; the loads of the next
+// XOR-swizzled LDS tiles (da_tile.h) filled by global->LDS DMA; the loads of the next
 // tile are spread through the score loop, so no wave stalls on a full memory
 // queue in one burst.  V^T arrives from the projection GEMM in 32-token tiles
 // (element (b, d, t) at b*stride_b + (t/32)*32*D + 32*d + t%32), so each
@@ -159,8 +159,8 @@ __device__ __forceinline__ int unit_of_tile(const AttnParams& p, int64_t gt, int
 
 template <int RP, int DS, int NW>
 struct AttnTile {
-  typedef PaddedTile<kKeyTile, RP / 8, true> KT;    // keys (blocked rows)
-  typedef SwizzledTile4<DS> VT;                     // V^T rows: DS features x 4 chunks (32 tokens)
+  typedef XorTile<kKeyTile, RP / 8, true> KT;       // keys (blocked rows)
+  typedef XorTile<DS, 4, false> VT;                 // V^T rows: DS features x 4 chunks (32 tokens)
   static constexpr int KPW = (KT::LOADS + NW - 1) / NW;   // key loads per wave
   static constexpr int VPW = (VT::LOADS + NW - 1) / NW;   // V^T loads per wave
   static constexpr int BYTES = KT::BYTES + VT::BYTES;     // one stage: a key tile, then a V^T tile
@@ -429,7 +429,16 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     return finish_queries(s);
   };
 
-  const int kfrag = KT::offset(c, g);
+  // Key fragment of chunk group kk, row block kb: one of four per-lane bases
+  // plus an immediate (da_tile.h); V^T block db: a per-lane base plus 1 KiB
+  // per block.
+  constexpr int KB = KS < 4 ? KS : 4;
+  int kfrag[KB];
+#pragma unroll
+  for (int k = 0; k < KB; ++k) kfrag[k] = KT::base(c, g, k);
+  auto key_frag = [&](const char* tile, int kk, int kb) {
+    return lds_v8<TQ>(tile + kfrag[kk & 3] + 256 * (kk >> 2) + kb * KT::ROW_BLOCK);
+  };
   const int vfrag = KT::BYTES + VT::offset(c, g);
 
   // Scores of 32 keys x 32 queries from a key tile in LDS: four independent
@@ -438,7 +447,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   auto scores = [&](const char* kt_lds, f32x4 (&st)[2][2], auto with_dma, char* nxt, const Src& src) {
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) st[cb][0] = st[cb][1] = zero4();
-    const char* kf = kt_lds + kfrag;
+    const char* kf = kt_lds;
     // Key fragments are read in groups of KG steps (2*KG reads in flight),
     // then consumed: LDS latency is paid once per group, and the group size
     // bounds the registers the reads hold.
@@ -448,8 +457,8 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       q8 kfr[KG][2];
 #pragma unroll
       for (int kk = 0; kk < KG; ++kk) {
-        kfr[kk][0] = lds_v8<TQ>(kf + KT::offset(0, (k0 + kk) * 4));
-        kfr[kk][1] = lds_v8<TQ>(kf + KT::offset(16, (k0 + kk) * 4));
+        kfr[kk][0] = key_frag(kf, k0 + kk, 0);
+        kfr[kk][1] = key_frag(kf, k0 + kk, 1);
       }
 #pragma unroll
       for (int kk = 0; kk < KG; ++kk) {
@@ -554,18 +563,18 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     constexpr int KG = KS <= 8 ? KS : 4;
     constexpr int KLEAD = 2;
     constexpr int VA = KS <= 8 ? (NB < 8 ? NB : 8) : 0;
-    const char* kf = cur + kfrag;
+    const char* kf = cur;
     const char* vf = cur + vfrag;
     q8 kfr[KS][2];
     v8 vfr[NB];
     auto read_keys = [&](int kk) {
-      kfr[kk][0] = lds_v8<TQ>(kf + KT::offset(0, kk * 4));
-      kfr[kk][1] = lds_v8<TQ>(kf + KT::offset(16, kk * 4));
+      kfr[kk][0] = key_frag(kf, kk, 0);
+      kfr[kk][1] = key_frag(kf, kk, 1);
     };
 #pragma unroll
     for (int kk = 0; kk < KG; ++kk) read_keys(kk);
 #pragma unroll
-    for (int db = 0; db < VA; ++db) vfr[db] = lds_v8<TV>(vf + VT::offset(db * 16, 0));
+    for (int db = 0; db < VA; ++db) vfr[db] = lds_v8<TV>(vf + db * 1024);
 
     f32x4 st_new[2][2];
 #pragma unroll
@@ -587,7 +596,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       }
     }
 #pragma unroll
-    for (int db = VA; db < NB; ++db) vfr[db] = lds_v8<TV>(vf + VT::offset(db * 16, 0));
+    for (int db = VA; db < NB; ++db) vfr[db] = lds_v8<TV>(vf + db * 1024);
 
     // Probabilities of tile u: lane (c, g) holds keys k0 + 8g + 4kb + i for
     // query qw0 + 16cb + c.
@@ -989,7 +998,7 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
   //    all steps (at least 16, so the prologue and partials stay small next
   //    to a run), plus the partials' round trip through memory.
   auto concurrent = [&](int64_t waves, int64_t subs, int64_t width) {
-    const int64_t stage = subs * ((RP / 8 + 1) * 32 * 16 + width * 4 * 16);   // key (padded) + V^T tiles
+    const int64_t stage = subs * (RP / 8 * 32 * 16 + width * 4 * 16);   // key + V^T tiles
     const int64_t stage_bytes = (stage + 1023) / 1024 * 1024;
     return kCUs * std::max<int64_t>(1, std::min<int64_t>(4 / waves, kLdsBytes / (kAttnStages * stage_bytes)));
   };

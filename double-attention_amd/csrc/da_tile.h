@@ -113,6 +113,56 @@ struct SwizzledTile4 {
   }
 };
 
+// Chunk permutation of an XOR-swizzled tile row (NCK chunks of 16 bytes).
+template <int NCK>
+__host__ __device__ constexpr int xor_swizzle(int p) {
+  if constexpr (NCK >= 16) return p & 15;
+  else if constexpr (NCK == 8) return (p >> 1) & 7;
+  else return ((p >> 1) ^ (p >> 2)) & 3;   // NCK == 4
+}
+
+// A tile of ROWS rows of NCK 16-byte chunks with no padding: chunk ck of
+// physical row p sits at slot p*NCK + (ck ^ xor_swizzle(p)).  gfx950's LDS
+// serves a ds_read_b128 in four clocks (64 banks, 256 bytes per clock) when
+// the 64 lanes' chunks spread over the banks; the MFMA operand reads -- lane
+// (c, g) reading row c (or 16 + c) at chunk 4k + g -- then do: measured 205
+// bytes per clock per CU with four waves, against 120 for a padded pitch or a
+// row-XOR of fewer than 16 values, whose reads take four extra conflict
+// clocks.  Rows 16 apart share the permutation, so
+//   offset(p + 16m, ck) = offset(p, ck) + 256 m NCK,
+// and for NCK >= 16 the chunk group k adds 256 (k >> 2) to the lane's base
+// for k & 3: fragment reads are one of four per-lane bases plus an immediate.
+// The global->LDS DMA writes whole 1 KiB wave loads of consecutive slots.
+template <int ROWS, int NCK, bool BLOCKED>
+struct XorTile {
+  static_assert(NCK == 4 || NCK == 8 || NCK % 16 == 0, "4, 8 or a multiple of 16 chunks per row");
+  static_assert(!BLOCKED || ROWS % 32 == 0, "blocked tiles are made of 32-row windows");
+  static constexpr int SLOTS = ROWS * NCK;
+  static_assert(SLOTS % 64 == 0, "whole wave loads");
+  static constexpr int LOADS = SLOTS / 64;
+  static constexpr int BYTES = LOADS * 1024;
+  static constexpr int ROW_BLOCK = 16 * NCK * 16;   // bytes between rows p and p + 16
+
+  static __device__ __forceinline__ int logical_row(int p) {
+    if constexpr (BLOCKED) return (p & ~31) + 8 * ((p >> 2) & 3) + 4 * ((p >> 4) & 1) + (p & 3);
+    else return p;
+  }
+  // What slot `slot` holds (every slot is real).
+  static __device__ __forceinline__ bool slot_chunk(int slot, int& row, int& ck) {
+    const int p = slot / NCK;
+    ck = (slot - p * NCK) ^ xor_swizzle<NCK>(p);
+    row = logical_row(p);
+    return true;
+  }
+  // Byte offset of (physical row, chunk).
+  static __device__ __forceinline__ constexpr int offset(int prow, int ck) {
+    return (prow * NCK + (ck ^ xor_swizzle<NCK>(prow))) * 16;
+  }
+  // Lane (c, g)'s base for chunk group k (chunk 4k + g of row c): the read
+  // of group k is at base(c, g, k & 3) + 256 (k >> 2).
+  static __device__ __forceinline__ int base(int c, int g, int k) { return offset(c, 4 * k + g); }
+};
+
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::v8 lds_v8(const char* p) {
   return *reinterpret_cast<const typename Elem<T>::v8*>(p);

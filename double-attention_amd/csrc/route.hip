@@ -16,7 +16,7 @@
 //   S^T[j, c] = sum_r Dk^T[j, r] U^T[r, c]      (A = key atoms from LDS, B = rows in VGPRs)
 //   O^T[r, c] += sum_j Dv[r, j] P^T[j, c]       (A = value atoms from LDS, B = P in VGPRs)
 // A workgroup of four waves shares each dictionary tile, double-buffered in
-// padded LDS tiles (da_tile.h) and filled by global->LDS DMA while the previous
+// XOR-swizzled LDS tiles (da_tile.h) and filled by global->LDS DMA while the previous
 // tile is multiplied.  Each wave owns QW rows (QW/16 MFMA column blocks), so
 // every dictionary fragment read from LDS feeds QW/16 MFMAs.  The input scale
 // beta/||x|| is applied before the single rounding of the unit row.
@@ -43,8 +43,8 @@ constexpr float kP16Lift = 14.f;
 
 template <int R, int NW>
 struct RouteTile {
-  typedef PaddedTile<kRouteAT, R / 8, true> KT;     // key atoms (blocked rows)
-  typedef SwizzledTile4<R> VT;                      // value coordinates x atoms (32 per row)
+  typedef XorTile<kRouteAT, R / 8, true> KT;        // key atoms (blocked rows)
+  typedef XorTile<R, 4, false> VT;                  // value coordinates x atoms (32 per row)
   static constexpr int KPW = (KT::LOADS + NW - 1) / NW;   // loads per wave of NW sharing a tile
   static constexpr int VPW = (VT::LOADS + NW - 1) / NW;
   static constexpr int BYTES = KT::BYTES + VT::BYTES;   // one stage: key atoms, then value atoms
@@ -196,7 +196,16 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
   for (int i = 0; i < RB; ++i) acc[i] = zero4();
   float m_run = -INFINITY, l_part = 0.f;
 
-  const int kfrag = KT::offset(c, g);
+  // Key fragment of chunk group kk, row block kb: one of four per-lane bases
+  // plus an immediate (da_tile.h); value block rb: a per-lane base plus 1 KiB
+  // per block.
+  constexpr int KB = KS < 4 ? KS : 4;
+  int kfrag[KB];
+#pragma unroll
+  for (int k = 0; k < KB; ++k) kfrag[k] = KT::base(c, g, k);
+  auto key_frag = [&](const char* tile, int kk, int kb) {
+    return lds_v8<TK>(tile + kfrag[kk & 3] + 256 * (kk >> 2) + kb * KT::ROW_BLOCK);
+  };
   const int vfrag = KT::BYTES + VT::offset(c, g);
 
   // Logits of 32 atoms x 16 rows from a key tile in LDS: two accumulator
@@ -204,15 +213,15 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
   // the next stage's loads are spread between them.
   auto logits = [&](const char* kt_lds, f32x4 (&st)[2], auto with_dma, char* nxt, int tk, int tv) {
     st[0] = st[1] = zero4();
-    const char* kf = kt_lds + kfrag;
+    const char* kf = kt_lds;
     constexpr int KG = KS < 4 ? KS : 4;
 #pragma unroll
     for (int k0 = 0; k0 < KS; k0 += KG) {
       k8 kfr[KG][2];
 #pragma unroll
       for (int kk = 0; kk < KG; ++kk) {
-        kfr[kk][0] = lds_v8<TK>(kf + KT::offset(0, (k0 + kk) * 4));
-        kfr[kk][1] = lds_v8<TK>(kf + KT::offset(16, (k0 + kk) * 4));
+        kfr[kk][0] = key_frag(kf, k0 + kk, 0);
+        kfr[kk][1] = key_frag(kf, k0 + kk, 1);
       }
 #pragma unroll
       for (int kk = 0; kk < KG; ++kk) {
@@ -374,7 +383,7 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
     for (int r0 = 0; r0 < RB; r0 += VG) {
       f16x8 vfr[VG];
 #pragma unroll
-      for (int rb = 0; rb < VG; ++rb) vfr[rb] = lds_v8<_Float16>(vf + VT::offset(16 * (r0 + rb), 0));
+      for (int rb = 0; rb < VG; ++rb) vfr[rb] = lds_v8<_Float16>(vf + (r0 + rb) * 1024);
 #pragma unroll
       for (int rb = 0; rb < VG; ++rb) acc[r0 + rb] = Elem<_Float16>::mma(vfr[rb], pb, acc[r0 + rb]);
     }
