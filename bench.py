@@ -63,7 +63,6 @@ def parse_args() -> argparse.Namespace:
         help="time the outer attention's native backward at the workload's attention shape instead "
         "(a separate JSON line; not the headline metric)",
     )
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of the CPU sample")
     p.add_argument(
         "--copy-mib",
         type=int,
@@ -74,26 +73,23 @@ def parse_args() -> argparse.Namespace:
     return p.parse_args()
 
 
-def cpu_threads() -> int:
-    try:
-        from threadpoolctl import threadpool_info
+def cpu_info() -> dict:
+    """``lscpu``'s model name, physical cores and hardware threads of this host."""
 
-        counts = [info.get("num_threads", 1) for info in threadpool_info() if info.get("user_api") == "blas"]
-        if counts:
-            return int(max(counts))
+    info = {"model": "unknown", "physical_cores": None, "threads": os.cpu_count()}
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        fields = {k.strip(): v.strip() for k, v in fields.items()}
+        info["model"] = fields.get("Model name", "unknown")
+        cores = int(fields.get("Core(s) per socket", "0")) * int(fields.get("Socket(s)", "0"))
+        info["physical_cores"] = cores or None
+        info["threads"] = int(fields.get("CPU(s)", info["threads"] or 0)) or info["threads"]
     except Exception:  # noqa: BLE001 - informational only
         pass
-    return len(os.sched_getaffinity(0))
-
-
-def cpu_model() -> str:
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+    return info
 
 
 def measured_traffic(workload: str, kernel: str) -> float | None:
@@ -175,6 +171,10 @@ def backward_bench(args: argparse.Namespace) -> None:
 
     def train_step(m):
         def run():
+            # A fresh step each rep: no gradient accumulation into .grad.
+            x.grad = None
+            for param in m.parameters():
+                param.grad = None
             m(x).backward(grad_x)
         return run
 
@@ -196,6 +196,8 @@ def backward_bench(args: argparse.Namespace) -> None:
 
         def lm_step(m):
             def run():
+                for param in m.parameters():
+                    param.grad = None
                 m(ids, targets)[1].backward()
             return run
 
@@ -207,7 +209,7 @@ def backward_bench(args: argparse.Namespace) -> None:
         print(json.dumps({
             "metric": "outer-attention backward (dQ, dK, dV, dscale) on 1 MI355X",
             "value": None, "unit": "TFLOP/s",
-            "note": f"score width {rp} has no native backward (widths up to 256); autograd recomputes in torch",
+            "note": f"score width {rp} has no native backward (widths up to 512); autograd recomputes in torch",
             "module_fwd_bwd_ms": module_ms,
             "config": {"workload": description, "score_dim": rp},
         }), flush=True)
@@ -245,7 +247,6 @@ def main() -> None:
         )
         sys.exit(2)
 
-    import numpy as np
     import torch
 
     import double_attention as da
@@ -282,6 +283,7 @@ def main() -> None:
     x = torch.randn(batch, length, config.model_dim, generator=torch.Generator().manual_seed(1)).to(device, dtype)
 
     # ---- whole forward (the step) ----------------------------------------
+    torch.cuda.reset_peak_memory_stats(device)
     with torch.inference_mode():
         for _ in range(args.warmup):
             step()
@@ -292,6 +294,9 @@ def main() -> None:
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
     ms_per_step = elapsed * 1e3 / args.steps
+    # Peak device memory of the step loop (the reference's harness reports
+    # max_memory_allocated beside its timings): weights, input, workspace, outputs.
+    peak_mib = torch.cuda.max_memory_allocated(device) / 2**20
     graph_ms = None
     if lm is not None:
         # The same LM forward replayed as one HIP graph (no per-call host work).
@@ -379,6 +384,25 @@ def main() -> None:
             end.record(stream)
             end.synchronize()
             kernel_us[name] = begin.elapsed_time(end) * 1e3 / args.kernel_reps
+        # The memory-bound stages once more, each launch alone after a 512 MiB
+        # device write that evicts the 256 MB Infinity Cache and the L2s: the
+        # back-to-back loop above reads operands a previous launch left in
+        # cache.  Median of 20 launches.
+        flush = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+        flushed_us = {}
+        for name in ("dict_normalize", "qkv_projection", "output_projection"):
+            samples = []
+            for _ in range(20):
+                flush.fill_(1)
+                begin = torch.cuda.Event(enable_timing=True)
+                end = torch.cuda.Event(enable_timing=True)
+                begin.record(stream)
+                launches[name]()
+                end.record(stream)
+                end.synchronize()
+                samples.append(begin.elapsed_time(end) * 1e3)
+            flushed_us[name] = sorted(samples)[len(samples) // 2]
+        del flush
 
     flops = {
         "route": 4.0 * R * M * rows,
@@ -415,41 +439,65 @@ def main() -> None:
         if name in bytes_moved:
             gbs = bytes_moved[name] / (us * 1e-6) / 1e9
             entry.update(gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
+        if name in flushed_us:
+            fus = flushed_us[name]
+            fgbs = bytes_moved[name] / (fus * 1e-6) / 1e9
+            entry.update(flushed_us=round(fus, 3), flushed_gbs=round(fgbs, 1),
+                         flushed_hbm_frac=round(fgbs / PEAK_HBM_GBS, 4))
         kernels[name] = entry
 
-    # ---- CPU baseline: the fp32 NumPy oracle on the host cores -------------
+    # ---- CPU baseline: this package's backend="torch" fp32 path -----------
+    # The same seeded weights and input, on the host's cores: inference
+    # mode, two warmups, then the median of at least five forwards (three
+    # for the long-context C5, whose torch path materializes 8192^2 scores).
     cpu = None
     if not args.no_cpu_baseline:
-        import oracle
+        import statistics
 
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+        host = cpu_info()
+        cpu_config = config.with_updates(backend="torch")
         if lm is not None:
-            params = {k: v.float().cpu().numpy() for k, v in lm.state_dict().items()}
-            idn = ids.cpu().numpy()
+            cpu_model_ = da.DoubleAttentionLM(
+                LM_VOCAB, length, cpu_config, LM_LAYERS, dictionary_group_size=LM_LAYERS,
+                feedforward_dim=LM_FEEDFORWARD,
+            ).eval()
+            cpu_model_.load_state_dict({k: v.float().cpu() for k, v in lm.state_dict().items()})
+            cpu_in = ids.cpu()
 
             def cpu_step():
-                oracle.double_attention_lm(params, config, idn, LM_LAYERS, LM_LAYERS, dtype=np.float32)
+                return cpu_model_(cpu_in)[0]
         else:
-            params = {k: v.float().cpu().numpy() for k, v in module.state_dict().items()}
-            xn = x.float().cpu().numpy()
+            cpu_model_ = da.SharedDictionaryAttention(cpu_config).eval()
+            cpu_model_.load_state_dict({k: v.float().cpu() for k, v in module.state_dict().items()})
+            cpu_in = x.float().cpu()
 
             def cpu_step():
-                oracle.shared_dictionary_attention(params, config, xn)
-        reps = 0
-        started = time.perf_counter()
-        while True:
-            cpu_step()
-            reps += 1
-            spent = time.perf_counter() - started
-            if spent >= args.cpu_seconds or spent / reps * (reps + 1) > 30.0:
-                break
+                return cpu_model_(cpu_in)
+        reps = 3 if args.workload == "c5" else 5
+        times = []
+        with torch.inference_mode():
+            for _ in range(2):
+                cpu_step()
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                cpu_step()
+                times.append(time.perf_counter() - t0)
+        cpu_ms = statistics.median(times) * 1e3
         cpu = {
-            "value": round(tokens * reps / spent, 1),
+            "value": round(tokens / (cpu_ms * 1e-3), 1),
             "unit": "tokens/s",
-            "cores": cpu_threads(),
+            "ms_per_step": round(cpu_ms, 2),
+            "routed_rows_per_s": round(rows / (cpu_ms * 1e-3), 1),
+            "cores": threads,
             "kind": "port",
-            "sample": f"{reps} full {args.workload} forwards of the fp32 NumPy oracle ({tokens} tokens each) in {spent:.1f} s on {cpu_model()}",
+            "host": host,
+            "sample": f"median of {reps} {args.workload} forwards (after 2 warmups) of this package's backend='torch' "
+                      f"fp32 module on {threads} threads ({host['model']}, {host['physical_cores']} physical cores, "
+                      f"{host['threads']} threads), same weights and input",
         }
-        del np
+        del cpu_model_
 
     line = {
         "metric": METRIC,
@@ -476,6 +524,7 @@ def main() -> None:
         "routed_rows_per_s": round(rows / (kernel_us["route"] * 1e-6), 1),
         "attention_tokens_per_s": round(tokens / (kernel_us["attention"] * 1e-6), 1),
         **({"graph_ms_per_step": round(graph_ms, 4)} if graph_ms is not None else {}),
+        "peak_memory_mib": round(peak_mib, 1),
         "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,

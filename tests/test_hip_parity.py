@@ -784,8 +784,11 @@ def test_route_backward(case, dtype) -> None:
     expected = oracle.dictionary_route_backward(np32(x), np32(dk), np32(dv), 6.0, np32(w), 1e-6,
                                                 normalize_input, normalize_output)
     label = f"route backward {case} {dtype}"
+    # fp16 inputs keep r, dr and the value atoms in fp16 (8x finer than bf16).
+    rel, rel_beta = (5e-3, 1e-2) if dtype == torch.float16 else (1e-2, 3e-2)
     for name, grad, exp in zip(("x", "dk", "dv"), (x.grad, dk.grad, dv.grad), expected[:3]):
         assert grad.dtype == dtype
-        assert_parity(grad, exp, 1e-2, 3e-2 * float(np.abs(exp).max()), f"{label} d{name}")
+        assert_parity(grad, exp, rel, 3e-2 * float(np.abs(exp).max()), f"{label} d{name}")
     db = float(beta.grad)
-    assert abs(db - expected[3]) <= 3e-2 * max(abs(expected[3]), 1e-3) + 1e-3, (db, expected[3])
+    print(f"[parity] {label} dbeta {db:.5f} vs {float(expected[3]):.5f}", flush=True)
+    assert abs(db - expected[3]) <= rel_beta * max(abs(expected[3]), 1e-3) + 1e-3, (db, expected[3])
