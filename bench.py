@@ -70,6 +70,18 @@ def parse_args() -> argparse.Namespace:
         help="after the measurement, copy a device buffer of this many MiB three times: a kernel of known "
         "traffic that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters",
     )
+    p.add_argument(
+        "--kernels-only",
+        action="store_true",
+        help="run only the per-kernel timing loops (each kernel 5 + --kernel-reps launches, in a fixed order) "
+        "and the --copy-mib calibration copies: the child run that --collect-counters profiles",
+    )
+    p.add_argument(
+        "--collect-counters",
+        action="store_true",
+        help="profile a --kernels-only child run of the workload under rocprofv3 --pmc (MFMA, LDS and HBM "
+        "counters, one pass per group) and write profiles/counters_<workload>.json and .md",
+    )
     return p.parse_args()
 
 
@@ -92,19 +104,205 @@ def cpu_info() -> dict:
     return info
 
 
-def measured_traffic(workload: str, kernel: str) -> float | None:
-    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter runs.
+def kernel_source_hash() -> str:
+    """SHA-256 over the kernel library's sources (``csrc``): counter tables
+    measured on other sources are stale and are not reported."""
 
-    ``profiles/traffic.json`` holds, per workload, FETCH_SIZE + WRITE_SIZE per
-    dispatch of each kernel, already divided by the factor the same counters
-    read for a device copy of known size (see the profile notes there).
-    """
+    import hashlib
+
+    h = hashlib.sha256()
+    for path in sorted((REPO / "double-attention_amd" / "csrc").iterdir()):
+        if path.suffix in (".hip", ".h"):
+            h.update(path.name.encode())
+            h.update(path.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def measured_counters(workload: str) -> dict | None:
+    """Per-kernel rocprofv3 counter summary of ``workload`` written by
+    ``--collect-counters`` for the current kernel sources, else None."""
 
     try:
-        table = json.loads((REPO / "profiles" / "traffic.json").read_text())
-        return table[workload]["kernels"][kernel]["hbm_bytes_per_launch"]
-    except (OSError, KeyError, ValueError):
+        table = json.loads((REPO / "profiles" / f"counters_{workload}.json").read_text())
+    except (OSError, ValueError):
         return None
+    if table.get("source_hash") != kernel_source_hash():
+        return None
+    return table
+
+
+# rocprofv3 --pmc passes of --collect-counters: at most 8 SQ, 4 TCC (FETCH_SIZE
+# takes 3, WRITE_SIZE 2) and 2 GRBM counters per pass.
+COUNTER_PASSES = {
+    "mfma": ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+             "SQ_INSTS_VALU_MFMA_MOPS_F16"),
+    "lds": ("SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAIT_INST_LDS", "SQ_WAVE_CYCLES",
+            "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "SQ_WAIT_ANY"),
+    "fetch": ("FETCH_SIZE",),
+    "write": ("WRITE_SIZE",),
+}
+SIMDS = 1024          # MI355X: 256 CUs x 4 SIMDs
+COPY_MIB = 256        # calibration copy of the counter runs
+
+
+def _kernel_label(name: str) -> str:
+    for key, label in (("route_kernel", "route"), ("attention_kernel", "attention"), ("merge", "attention_merge"),
+                       ("dict_normalize", "dict_normalize"), ("gemm_kernel", "gemm"), ("copyBuffer", "copy")):
+        if key in name:
+            return label
+    return name.split("(")[0][-60:]
+
+
+def collect_counters(args: argparse.Namespace) -> None:
+    """Profile a ``--kernels-only`` child run under rocprofv3, one pass per
+    counter group, and write ``profiles/counters_<workload>.{json,md}``.
+
+    The child launches dict_normalize, qkv_projection, route, attention and
+    output_projection 5 + ``--kernel-reps`` times each, in that order, then
+    copies a 256 MiB buffer three times.  GEMM dispatches before the first
+    route dispatch are the QKV projection, later ones the output projection.
+    Derived figures per dispatch:
+
+    * MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x SIMDs),
+      rocprofv3's MfmaUtil (GRBM_GUI_ACTIVE is read per XCD and summed);
+    * MFMA flops executed = (MOPS_BF16 + MOPS_F16) x 512, beside the
+      kernel's algorithmic flops;
+    * LDS bank conflicts per access = SQ_LDS_BANK_CONFLICT /
+      (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT);
+    * HBM bytes = FETCH_SIZE / f + WRITE_SIZE / w, where f and w are what the
+      counters read per byte of the calibration copy.
+    """
+
+    import csv
+    import glob
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    child = [sys.executable, str(REPO / "bench.py"), "--workload", args.workload, "--dtype", args.dtype,
+             "--kernels-only", "--kernel-reps", str(min(args.kernel_reps, 20)), "--no-cpu-baseline",
+             "--copy-mib", str(COPY_MIB)]
+    env = dict(os.environ, TMPDIR="/tmp")
+    rows: dict[int, dict] = {}
+    commands = []
+    for pass_name, counters in COUNTER_PASSES.items():
+        out_dir = tempfile.mkdtemp(prefix=f"da_pmc_{pass_name}_", dir="/tmp")
+        cmd = ["rocprofv3", "--pmc", *counters, "--kernel-trace", "--output-format", "csv", "-d", out_dir,
+               "-o", "run", "--", *child]
+        commands.append(" ".join(cmd[:-len(child)] + ["python3", "bench.py", *child[2:]]).replace(out_dir, "<dir>"))
+        print(f"[counters] {args.workload} pass {pass_name}: {' '.join(counters)}", file=sys.stderr, flush=True)
+        proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                text=True, start_new_session=True)
+        try:
+            stdout, stderr = proc.communicate(timeout=240)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.communicate()
+            raise SystemExit(f"rocprofv3 pass {pass_name} timed out")
+        files = glob.glob(f"{out_dir}/**/*counter_collection.csv", recursive=True)
+        if not files:
+            print(stderr[-3000:], file=sys.stderr)
+            raise SystemExit(f"rocprofv3 pass {pass_name} (exit {proc.returncode}) wrote no counter file")
+        # A crash after the program's last line with complete results is the
+        # profiler's own exit; the counter file is what matters.
+        for path in files:
+            with open(path, newline="") as f:
+                for rec in csv.DictReader(f):
+                    d = int(rec["Dispatch_Id"])
+                    row = rows.setdefault(d, {"name": rec["Kernel_Name"], "grid": int(rec["Grid_Size"])})
+                    row[rec["Counter_Name"]] = row.get(rec["Counter_Name"], 0.0) + float(rec["Counter_Value"])
+        shutil.rmtree(out_dir, ignore_errors=True)
+
+    # Label every dispatch; dispatch ids follow launch order within the run.
+    first_route = min((d for d, r in rows.items() if _kernel_label(r["name"]) == "route"), default=None)
+    groups: dict[str, list[dict]] = {}
+    for d, r in sorted(rows.items()):
+        label = _kernel_label(r["name"])
+        if label == "gemm":
+            label = "qkv_projection" if first_route is not None and d < first_route else "output_projection"
+        groups.setdefault(label, []).append(r)
+    # The calibration copies are the run's last three copies (earlier ones
+    # stage the host inputs).
+    groups["copy"] = groups.get("copy", [])[-3:]
+
+    def mean(label: str, counter: str) -> float | None:
+        vals = [r[counter] for r in groups.get(label, []) if counter in r]
+        return sum(vals) / len(vals) if vals else None
+
+    copy_bytes = COPY_MIB << 20
+    f_fetch = (mean("copy", "FETCH_SIZE") or 0) * 1024 / copy_bytes
+    f_write = (mean("copy", "WRITE_SIZE") or 0) * 1024 / copy_bytes
+    xcds = 8
+    kernels = {}
+    for label, recs in groups.items():
+        if label not in ("dict_normalize", "qkv_projection", "route", "attention", "attention_merge",
+                         "output_projection"):
+            continue
+        e = {"dispatches": len(recs), "symbol": recs[0]["name"].split("(")[0][:120]}
+        busy, active = mean(label, "SQ_VALU_MFMA_BUSY_CYCLES"), mean(label, "GRBM_GUI_ACTIVE")
+        if busy is not None and active:
+            e["mfma_busy"] = round(busy / (active / xcds * SIMDS), 4)
+        mops = [mean(label, c) for c in ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F16")]
+        if all(m is not None for m in mops):
+            e["mfma_flops_executed"] = (mops[0] + mops[1]) * 512
+        conf, idx = mean(label, "SQ_LDS_BANK_CONFLICT"), mean(label, "SQ_LDS_IDX_ACTIVE")
+        if conf is not None and idx and idx > conf:
+            e["lds_bank_conflicts_per_access"] = round(conf / (idx - conf), 4)
+        wait_lds, wave = mean(label, "SQ_WAIT_INST_LDS"), mean(label, "SQ_WAVE_CYCLES")
+        if wait_lds is not None and wave:
+            e["lds_issue_wait_frac"] = round(wait_lds / wave, 4)
+        wait_any = mean(label, "SQ_WAIT_ANY")
+        if wait_any is not None and wave:
+            e["wait_any_frac"] = round(wait_any / wave, 4)
+        for c in ("SQ_INSTS_LDS", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "FETCH_SIZE", "WRITE_SIZE"):
+            v = mean(label, c)
+            if v is not None:
+                e[c] = round(v, 1)
+        fetch, write = mean(label, "FETCH_SIZE"), mean(label, "WRITE_SIZE")
+        if fetch is not None and write is not None and f_fetch > 0 and f_write > 0:
+            e["hbm_bytes_per_launch"] = round(fetch * 1024 / f_fetch + write * 1024 / f_write)
+        kernels[label] = e
+    table = {
+        "workload": args.workload,
+        "dtype": args.dtype,
+        "source_hash": kernel_source_hash(),
+        "commands": commands,
+        "calibration": {"copy_mib": COPY_MIB, "fetch_per_byte": round(f_fetch, 4), "write_per_byte": round(f_write, 4)},
+        "kernels": kernels,
+    }
+    out = REPO / "profiles" / f"counters_{args.workload}.json"
+    out.write_text(json.dumps(table, indent=1) + "\n")
+    lines = [
+        f"# rocprofv3 counters, workload {args.workload} ({WORKLOADS[args.workload][4]}, {args.dtype})",
+        "",
+        "Written by `python3 bench.py --workload " + args.workload + " --collect-counters` (run from the repository "
+        "root; it runs each pass below in /tmp with TMPDIR=/tmp).  Per-dispatch means over every dispatch of each "
+        "kernel in a `--kernels-only` child run.  Kernel sources: `" + table["source_hash"] + "` (SHA-256 prefix "
+        "of `double-attention_amd/csrc`).",
+        "",
+        "```",
+        *commands,
+        "```",
+        "",
+        f"Calibration: the child copies a {COPY_MIB} MiB buffer three times; per byte moved, FETCH_SIZE reads "
+        f"{f_fetch:.3f} and WRITE_SIZE {f_write:.3f} (KiB units), so HBM bytes = FETCH_SIZE*1024/{f_fetch:.3f} + "
+        f"WRITE_SIZE*1024/{f_write:.3f}.  MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x "
+        f"{SIMDS} SIMDs) (rocprofv3's MfmaUtil); MFMA flops executed = (SQ_INSTS_VALU_MFMA_MOPS_BF16 + _F16) x 512.",
+        "",
+        "| kernel | dispatches | MFMA busy | MFMA GFLOP executed | LDS conflicts / access | LDS issue wait / wave-cycles "
+        "| any wait / wave-cycles | HBM MiB / launch |",
+        "|---|---|---|---|---|---|---|---|",
+    ]
+    for label, e in kernels.items():
+        def fmt(key, scale=1.0, digits=3):
+            v = e.get(key)
+            return "-" if v is None else f"{v * scale:.{digits}f}"
+        lines.append(f"| {label} | {e['dispatches']} | {fmt('mfma_busy', 100, 1)}% | {fmt('mfma_flops_executed', 1e-9, 2)} "
+                     f"| {fmt('lds_bank_conflicts_per_access')} | {fmt('lds_issue_wait_frac')} | {fmt('wait_any_frac')} "
+                     f"| {fmt('hbm_bytes_per_launch', 2 ** -20, 1)} |")
+    (REPO / "profiles" / f"counters_{args.workload}.md").write_text("\n".join(lines) + "\n")
+    print(json.dumps({"workload": args.workload, "counters": str(out.relative_to(REPO))}), flush=True)
 
 
 def backward_bench(args: argparse.Namespace) -> None:
@@ -235,6 +433,9 @@ def backward_bench(args: argparse.Namespace) -> None:
 
 def main() -> None:
     args = parse_args()
+    if args.collect_counters:
+        collect_counters(args)
+        return
     if args.backward and args.gpus == 1:
         backward_bench(args)
         calibration_copy(args.copy_mib, "cuda:0")
@@ -284,21 +485,23 @@ def main() -> None:
 
     # ---- whole forward (the step) ----------------------------------------
     torch.cuda.reset_peak_memory_stats(device)
+    timed_steps = 0 if args.kernels_only else args.steps
     with torch.inference_mode():
-        for _ in range(args.warmup):
+        for _ in range(args.warmup if timed_steps else 0):
             step()
         torch.cuda.synchronize()
         start = time.perf_counter()
-        for _ in range(args.steps):
+        out = None
+        for _ in range(timed_steps):
             out = step()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
-    ms_per_step = elapsed * 1e3 / args.steps
+    ms_per_step = elapsed * 1e3 / max(timed_steps, 1)
     # Peak device memory of the step loop (the reference's harness reports
     # max_memory_allocated beside its timings): weights, input, workspace, outputs.
     peak_mib = torch.cuda.max_memory_allocated(device) / 2**20
     graph_ms = None
-    if lm is not None:
+    if lm is not None and timed_steps:
         # The same LM forward replayed as one HIP graph (no per-call host work).
         graphed = da.GraphedForward(lm, ids)
         for _ in range(args.warmup):
@@ -390,7 +593,7 @@ def main() -> None:
         # cache.  Median of 20 launches.
         flush = torch.empty(512 << 20, dtype=torch.uint8, device=device)
         flushed_us = {}
-        for name in ("dict_normalize", "qkv_projection", "output_projection"):
+        for name in () if args.kernels_only else ("dict_normalize", "qkv_projection", "output_projection"):
             samples = []
             for _ in range(20):
                 flush.fill_(1)
@@ -403,6 +606,10 @@ def main() -> None:
                 samples.append(begin.elapsed_time(end) * 1e3)
             flushed_us[name] = sorted(samples)[len(samples) // 2]
         del flush
+    if args.kernels_only:
+        print(json.dumps({"workload": args.workload, "kernel_order": list(launches), "kernel_us": kernel_us}), flush=True)
+        calibration_copy(args.copy_mib, device)
+        return
 
     flops = {
         "route": 4.0 * R * M * rows,
@@ -427,9 +634,21 @@ def main() -> None:
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": measured_traffic(args.workload, dominant),
+        "traffic": None,
         "avg_launch_us": round(kernel_us[dominant], 3),
     }
+    # Counter evidence for the same kernel sources (--collect-counters):
+    # rocprofv3's MFMA-busy fraction beside the algorithmic one, the MFMA
+    # flops the kernel executed, and HBM bytes per launch.
+    counters = measured_counters(args.workload)
+    if counters is not None and dominant in counters["kernels"]:
+        c = counters["kernels"][dominant]
+        roofline["traffic"] = c.get("hbm_bytes_per_launch")
+        roofline["counter_mfma_busy"] = c.get("mfma_busy")
+        if c.get("mfma_flops_executed"):
+            roofline["counter_mfma_flops_executed"] = c["mfma_flops_executed"]
+            roofline["algorithmic_flops"] = flops[dominant]
+        roofline["counters"] = f"profiles/counters_{args.workload}.json"
     kernels = {}
     for name, us in kernel_us.items():
         entry = {"avg_us": round(us, 3)}
@@ -439,6 +658,9 @@ def main() -> None:
         if name in bytes_moved:
             gbs = bytes_moved[name] / (us * 1e-6) / 1e9
             entry.update(gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
+        if counters is not None and name in counters["kernels"]:
+            c = counters["kernels"][name]
+            entry.update({k: c[k] for k in ("mfma_busy", "hbm_bytes_per_launch") if k in c})
         if name in flushed_us:
             fus = flushed_us[name]
             fgbs = bytes_moved[name] / (fus * 1e-6) / 1e9

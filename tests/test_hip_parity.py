@@ -12,6 +12,8 @@ not tile multiples) as in the reference's own parity tests
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -546,19 +548,15 @@ def test_lm_c4_qk2_s2_tied(dtype) -> None:
 def test_lm_training_gradients(monkeypatch) -> None:
     # One training step of a two-layer tied LM (the C4 preset) with the HIP
     # backend: the attention layers' route and outer attention run the native
-    # backward kernels; every gradient is held to max(3e-2, 2x) the relative
-    # error of the same LM on the bf16 torch path, both against fp32.
+    # backward kernels; every gradient's relative error against fp32, as a root
+    # mean square over three seeds, is held to max(3e-2, 2x) that of the same
+    # LM on the bf16 torch path.  One seed is not enough: the map-mix logits'
+    # gradient a_s (g_s - sum a g) differences two per-map sums g_s that agree
+    # to ~0.5%, so a 4e-4 error in g_s is a ~10% error in the gradient, and the
+    # bf16 torch path's error there ranges over 4%..80% from seed to seed.
     device = _device()
     config = da.experiment_config("qk2-s2", untied_dictionary=False, backend="hip")
-    torch.manual_seed(3)
     kwargs = dict(dictionary_group_size=2, feedforward_dim=1536)
-    models = [
-        da.DoubleAttentionLM(512, 64, config, 2, **kwargs).to(device, torch.bfloat16),
-        da.DoubleAttentionLM(512, 64, config.with_updates(backend="torch"), 2, **kwargs).to(device, torch.bfloat16),
-        da.DoubleAttentionLM(512, 64, config.with_updates(backend="torch"), 2, **kwargs).to(device, torch.float32),
-    ]
-    models[1].load_state_dict(models[0].state_dict())
-    models[2].load_state_dict({k: v.float() for k, v in models[0].state_dict().items()})
     calls = []
     for fn in ("_attention_backward", "_route_backward"):
         original = getattr(da.hip_ops, fn)
@@ -568,26 +566,48 @@ def test_lm_training_gradients(monkeypatch) -> None:
             return _original(*args)
 
         monkeypatch.setattr(da.hip_ops, fn, counted)
-    g = torch.Generator().manual_seed(4)
-    ids = torch.randint(0, 512, (8, 64), generator=g).to(device)
-    targets = torch.randint(0, 512, (8, 64), generator=g).to(device)
-    for m in models:
-        _, loss = m(ids, targets)
-        loss.float().backward()
-    assert calls.count("_attention_backward") == 2 and calls.count("_route_backward") == 2
 
     def rel(a, b):
         return float((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-30))
 
-    worst = 0.0
-    for (name, p_hip), p_t16, p_ref in zip(models[0].named_parameters(), models[1].parameters(), models[2].parameters()):
-        if p_ref.grad is None:
-            continue
-        assert p_hip.grad is not None and torch.isfinite(p_hip.grad).all(), name
-        err, bound = rel(p_hip.grad, p_ref.grad), max(3e-2, 2 * rel(p_t16.grad, p_ref.grad))
-        worst = max(worst, err / bound)
-        assert err <= bound, f"d{name}: rel {err:.3e} > {bound:.3e}"
-    print(f"[parity] lm training gradients: worst error / bound = {worst:.2f}", flush=True)
+    seeds = (3, 5, 7)
+    squares: dict[str, list[float]] = {}
+    for seed in seeds:
+        torch.manual_seed(seed)
+        models = [
+            da.DoubleAttentionLM(512, 64, config, 2, **kwargs).to(device, torch.bfloat16),
+            da.DoubleAttentionLM(512, 64, config.with_updates(backend="torch"), 2, **kwargs).to(device, torch.bfloat16),
+            da.DoubleAttentionLM(512, 64, config.with_updates(backend="torch"), 2, **kwargs).to(device, torch.float32),
+        ]
+        models[1].load_state_dict(models[0].state_dict())
+        models[2].load_state_dict({k: v.float() for k, v in models[0].state_dict().items()})
+        calls.clear()
+        g = torch.Generator().manual_seed(seed + 1)
+        ids = torch.randint(0, 512, (8, 64), generator=g).to(device)
+        targets = torch.randint(0, 512, (8, 64), generator=g).to(device)
+        for m in models:
+            _, loss = m(ids, targets)
+            loss.float().backward()
+        assert calls.count("_attention_backward") == 2 and calls.count("_route_backward") == 2
+        for (name, p_hip), p_t16, p_ref in zip(
+            models[0].named_parameters(), models[1].parameters(), models[2].parameters()
+        ):
+            if p_ref.grad is None:
+                continue
+            assert p_hip.grad is not None and torch.isfinite(p_hip.grad).all(), name
+            acc = squares.setdefault(name, [0.0, 0.0])
+            acc[0] += rel(p_hip.grad, p_ref.grad) ** 2
+            acc[1] += rel(p_t16.grad, p_ref.grad) ** 2
+    results = []
+    for name, (hip_sq, t16_sq) in squares.items():
+        err = math.sqrt(hip_sq / len(seeds))
+        bound = max(3e-2, 2 * math.sqrt(t16_sq / len(seeds)))
+        results.append((err / bound, name, err, bound))
+    results.sort(reverse=True)
+    for ratio, name, err, bound in results[:4]:
+        print(f"[parity] lm training d{name}: rms rel {err:.3e}, bound {bound:.3e} (ratio {ratio:.2f})", flush=True)
+    for ratio, name, err, bound in results:
+        assert err <= bound, f"d{name}: rms rel {err:.3e} > {bound:.3e}"
 
 
 @pytest.mark.parametrize("preset", ["a1-d1536-qffn", "a1-r512-d1536-qffn"])
