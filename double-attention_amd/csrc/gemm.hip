@@ -15,8 +15,8 @@
 //           attention kernel streams one contiguous tile at a time.  Rows i
 //           run over B * Tp "virtual" tokens (t < Tp, the padded length);
 //           tokens past T reuse the last real row, so the padding is finite.
-// Tiles: 128 x 128 per workgroup, 64-wide K stages double-buffered in padded
-// LDS tiles (da_tile.h) and filled by global->LDS DMA; each of the four waves
+// Tiles: 128 x 128 per workgroup, 64-wide K stages double-buffered in
+// XOR-swizzled LDS tiles (da_tile.h, conflict-free MFMA operand reads) and filled by global->LDS DMA; each of the four waves
 // owns a 64 x 64 quadrant (4 x 4 MFMA 16x16x32 blocks).
 //
 // A launch may also carry a dictionary normalization (dict_norm.h): its
@@ -31,13 +31,13 @@ namespace da {
 
 constexpr int kBJ = 128;
 constexpr int kBK = 64;
-typedef PaddedTile<kBJ, kBK / 8, false> GemmTileQ;      // Q operand tile: 128 rows x 64 k
+typedef XorTile<kBJ, kBK / 8, false> GemmTileQ;         // Q operand tile: 128 rows x 64 k
 
 // Row tile of BI (128 or 64) P rows; the four waves form a 2 x 2 grid of
 // (BI/2) x 64 output blocks.
 template <int BI>
 struct GemmCfg {
-  typedef PaddedTile<BI, kBK / 8, false> TileP;
+  typedef XorTile<BI, kBK / 8, false> TileP;
   static constexpr int LOADS = TileP::LOADS + GemmTileQ::LOADS;
   static constexpr int PER_WAVE = (LOADS + 3) / 4;      // wave loads per wave per stage
   static constexpr int NA = BI / 32;                    // 16-row MFMA blocks per wave
@@ -201,8 +201,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = zero4();
 
-  const int afrag = TileP::offset(wi * (BI / 2) + c, g);
-  const int bfrag = TileP::BYTES + GemmTileQ::offset(wj * 64 + c, g);
+  // Lane (c, g)'s fragment bases for chunk groups kk = 0, 1 (chunk 4kk + g of
+  // its row); 16-row blocks add XorTile::ROW_BLOCK.
+  const int afrag[2] = {TileP::base(wi * (BI / 2) + c, g, 0), TileP::base(wi * (BI / 2) + c, g, 1)};
+  const int bfrag[2] = {TileP::BYTES + GemmTileQ::base(wj * 64 + c, g, 0),
+                        TileP::BYTES + GemmTileQ::base(wj * 64 + c, g, 1)};
 
   // Two stage buffers: step st reads stage st and issues stage st + 1 into
   // the other buffer.  Every fragment of the stage is read first (LDS latency
@@ -221,9 +224,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     for (int kk = 0; kk < 2; ++kk) {
       if (kk == 1 && !full) break;
 #pragma unroll
-      for (int a = 0; a < NA; ++a) af[kk][a] = lds_v8<T>(cur + afrag + TileP::offset(a * 16, kk * 4));
+      for (int a = 0; a < NA; ++a) af[kk][a] = lds_v8<T>(cur + afrag[kk] + a * TileP::ROW_BLOCK);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) bf[kk][b] = lds_v8<T>(cur + bfrag + GemmTileQ::offset(b * 16, kk * 4));
+      for (int b = 0; b < 4; ++b) bf[kk][b] = lds_v8<T>(cur + bfrag[kk] + b * GemmTileQ::ROW_BLOCK);
     }
     if (st + 1 < n_stages) issue(nxt, (st + 1) * kBK);
 #pragma unroll
