@@ -115,7 +115,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 13; }
+int da_abi_version(void) { return 14; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -154,6 +154,35 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
                   logit_scale, out, out_row_stride, out_dtype};
   da::launch_dictionary_route(a, reinterpret_cast<hipStream_t>(stream));
   return check_launch("route");
+}
+
+int da_dictionary_route_backward_rows(const float* logits, const float* grad_weights, int64_t rows,
+                                      int64_t atoms, int64_t ld_in, const void* beta, int beta_dtype,
+                                      float beta_value, int flags, float silu_gain, float logit_scale, float eps,
+                                      void* grad_logits, void* weights, int64_t ld_out, int out_dtype,
+                                      float* dbeta_rows, da_stream_t stream) {
+  constexpr int kBwdRowsFlags = DA_ROUTE_BETA_IS_LOG | DA_ROUTE_SILU_LOGITS | DA_ROUTE_STANDARDIZE | DA_ROUTE_DIRECT_SILU;
+  if (flags & ~kBwdRowsFlags)
+    return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: unknown flag bits 0x%x", flags);
+  if ((flags & DA_ROUTE_DIRECT_SILU) && !(silu_gain > 0.f && std::isfinite(silu_gain)))
+    return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: silu_gain must be positive and finite");
+  if ((flags & DA_ROUTE_STANDARDIZE) && !(logit_scale > 0.f && std::isfinite(logit_scale)))
+    return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: logit_scale must be positive and finite");
+  if (!half_dtype(out_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: out_dtype must be DA_F16 or DA_BF16");
+  if (rows < 0 || atoms < 1) return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: bad rows/atoms");
+  if (atoms > da::kRouteBwdRowsMaxAtoms)
+    return fail(DA_ERR_UNSUPPORTED, "route backward rows: at most %d atoms (got %lld)", da::kRouteBwdRowsMaxAtoms,
+                (long long)atoms);
+  if (ld_in < atoms || ld_out < atoms) return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: row pitches < atoms");
+  if (rows == 0) return ok();
+  if (!logits || !grad_weights || !grad_logits || !weights)
+    return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: null pointer");
+  if (beta && !any_dtype(beta_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: bad beta dtype");
+  if ((rows + 3) / 4 > 0x7fffffffLL) return fail(DA_ERR_UNSUPPORTED, "route backward rows: too many rows");
+  da::RouteBwdRowsArgs a{logits, grad_weights, rows, static_cast<int>(atoms), ld_in, beta, beta_dtype, beta_value,
+                         flags, silu_gain, logit_scale, eps, grad_logits, weights, ld_out, out_dtype, dbeta_rows};
+  da::launch_route_backward_rows(a, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("route backward rows");
 }
 
 int64_t da_attention_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t score_dim,

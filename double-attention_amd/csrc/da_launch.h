@@ -134,6 +134,27 @@ void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int
                                  int M, float eps, void* key_t, int key_dtype, void* value,
                                  void* value_rows, hipStream_t stream);
 void launch_dictionary_route(const RouteArgs& a, hipStream_t stream);
+
+// Row-wise backward of the route's assignment (route_bwd.hip).
+struct RouteBwdRowsArgs {
+  const float* logits;        // [rows, ld_in] raw logits <u, Dk_j>
+  const float* grad_weights;  // [rows, ld_in] <dr, Dv_j>
+  int64_t rows;
+  int atoms;                  // M <= kRouteBwdRowsMaxAtoms
+  int64_t ld_in;
+  const void* beta_ptr;
+  int beta_dtype;
+  float beta_value;
+  int flags;                  // kRouteBetaIsLog and the variant bits
+  float silu_gain, logit_scale, eps;
+  void* grad_logits;          // [rows, ld_out] out_dtype
+  void* weights;              // [rows, ld_out] out_dtype
+  int64_t ld_out;
+  int out_dtype;
+  float* dbeta_rows;          // [rows] or nullptr
+};
+constexpr int kRouteBwdRowsMaxAtoms = 4096;
+void launch_route_backward_rows(const RouteBwdRowsArgs& a, hipStream_t stream);
 // LayerNorm over the last dimension (dim a multiple of 8, at most 4096).
 void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight, const void* bias, int param_dtype,
                        float eps, int dtype, void* out, hipStream_t stream);

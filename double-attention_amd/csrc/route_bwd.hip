@@ -1,0 +1,184 @@
+// Row-wise backward of the dictionary route's assignment, for every variant.
+//
+// Replaces the reference's _row_scaled_softmax_backward_kernel
+// (src/double_attention/triton_kernels.py:589-671, launched at :1480) and the
+// direct-SiLU branch of _DictionaryRouteFunction.backward (:1940-1948): the
+// step between the two GEMM pairs of the route backward.  Per row, from the
+// raw logits l_j = <u, Dk_j> and dW_j = <dr, Dv_j> (fp32, written by GEMMs),
+// it forms the forward weights of ops.py:41-61 again and returns the gradient
+// at the raw logits, the weights (for dDv = dr^T W) and the row's share of
+// d beta:
+//   a0 = l                   or 2 SiLU(l)                    (activation)
+//   a  = a0                  or s (a0 - mean a0) / sqrt(var a0 + eps)   (standardize)
+//   w  = softmax_j(beta a)   or (2/g) SiLU(g a)              (assignment)
+//   softmax: d(beta a_j) = w_j (dW_j - sum_k w_k dW_k); da = beta d(beta a);
+//            d beta = sum_j d(beta a_j) a_j
+//   direct:  da_j = dW_j 2 SiLU'(g a_j)
+//   standardize: with c = (a0 - mean) isd, dc = s da:
+//            da0 = isd (dc - mean dc - c mean(dc c))
+//   SiLU activation: dl = da0 2 SiLU'(l),  SiLU'(x) = sig(x) (1 + x (1 - sig(x)))
+// One wave per row, the row's atoms strided over the lanes and held in VGPRs
+// (NPL per lane, M <= 64 NPL), so every reduction is a wave reduction and the
+// two inputs are read once, coalesced.
+#include "da_common.h"
+#include "da_launch.h"
+#include "da_tile.h"
+
+namespace da {
+
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_max64(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
+
+template <typename TO, int NPL>
+__global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsArgs a) {
+  const int lane = lane_id();
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + uniform_wave();
+  if (row >= a.rows) return;   // whole waves
+  const int M = a.atoms;
+  const float* lrow = a.logits + row * a.ld_in;
+  const float* grow = a.grad_weights + row * a.ld_in;
+  const bool silu_logits = a.flags & kRouteSiluLogits;
+  const bool standardize = a.flags & kRouteStandardize;
+  const bool direct = a.flags & kRouteDirectSilu;
+
+  const ScalarHalves beta_bits = fetch_scalar(a.beta_ptr ? a.beta_ptr : static_cast<const void*>(a.logits),
+                                              a.beta_ptr ? a.beta_dtype : kF32, 0);
+  float l[NPL], g[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int j = lane + 64 * i;
+    l[i] = j < M ? lrow[j] : 0.f;
+    g[i] = j < M ? grow[j] : 0.f;
+  }
+  const float beta_raw = a.beta_ptr ? scalar_value(beta_bits, a.beta_dtype) : a.beta_value;
+  const float beta = (a.flags & kRouteBetaIsLog) ? expf(fminf(fmaxf(beta_raw, kLogBetaMin), kLogBetaMax)) : beta_raw;
+  const float inv_m = 1.f / static_cast<float>(M);
+
+  // Activation, then standardization: c holds the standardized value
+  // (before the scale s), a the assignment logits.
+  float c[NPL], w[NPL];
+  float isd = 1.f;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) c[i] = silu_logits ? 2.f * l[i] * sigmoidf(l[i]) : l[i];
+  if (standardize) {
+    float s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) s1 += lane + 64 * i < M ? c[i] : 0.f;
+    const float mean = wave_sum64(s1) * inv_m;
+    float s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      c[i] = lane + 64 * i < M ? c[i] - mean : 0.f;
+      s2 += c[i] * c[i];
+    }
+    isd = rsqrtf(wave_sum64(s2) * inv_m + a.eps);
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) c[i] *= isd;
+  }
+  const float s = standardize ? a.logit_scale : 1.f;
+
+  // Assignment weights and the gradient at the assignment logits (into g).
+  float dbeta = 0.f;
+  if (direct) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const float x = a.silu_gain * (c[i] * s);
+      const float sg = sigmoidf(x);
+      w[i] = (2.f / a.silu_gain) * x * sg;
+      g[i] *= 2.f * sg * (1.f + x * (1.f - sg));
+    }
+  } else {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i)
+      if (lane + 64 * i < M) mx = fmaxf(mx, beta * (c[i] * s));
+    mx = wave_max64(mx);
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      w[i] = lane + 64 * i < M ? __expf(beta * (c[i] * s) - mx) : 0.f;
+      z += w[i];
+    }
+    const float inv_z = 1.f / wave_sum64(z);
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      w[i] *= inv_z;
+      d += w[i] * g[i];
+    }
+    d = wave_sum64(d);
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const float dsc = w[i] * (g[i] - d);   // gradient at beta a_j
+      dbeta += dsc * (c[i] * s);
+      g[i] = beta * dsc;
+    }
+    dbeta = wave_sum64(dbeta);
+  }
+  if (standardize) {
+    float m1 = 0.f, m2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      g[i] *= s;
+      m1 += g[i];
+      m2 += g[i] * c[i];
+    }
+    m1 = wave_sum64(m1) * inv_m;
+    m2 = wave_sum64(m2) * inv_m;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) g[i] = isd * (g[i] - m1 - c[i] * m2);
+  }
+  if (silu_logits) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const float sg = sigmoidf(l[i]);
+      g[i] *= 2.f * sg * (1.f + l[i] * (1.f - sg));
+    }
+  }
+
+  TO* dl_row = static_cast<TO*>(a.grad_logits) + row * a.ld_out;
+  TO* w_row = static_cast<TO*>(a.weights) + row * a.ld_out;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int j = lane + 64 * i;
+    if (j < M) {
+      dl_row[j] = static_cast<TO>(g[i]);
+      w_row[j] = static_cast<TO>(w[i]);
+    }
+  }
+  if (a.dbeta_rows && lane == 0) a.dbeta_rows[row] = direct ? 0.f : dbeta;
+}
+
+template <typename TO>
+static void launch_route_bwd_rows_t(const RouteBwdRowsArgs& a, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
+  if (a.atoms <= 512) {
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 8>), grid, dim3(256), 0, s, a);
+  } else if (a.atoms <= 1024) {
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 16>), grid, dim3(256), 0, s, a);
+  } else if (a.atoms <= 2048) {
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 32>), grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 64>), grid, dim3(256), 0, s, a);
+  }
+}
+
+void launch_route_backward_rows(const RouteBwdRowsArgs& a, hipStream_t stream) {
+  if (a.rows == 0) return;
+  if (a.out_dtype == kBF16) {
+    launch_route_bwd_rows_t<__bf16>(a, stream);
+  } else {
+    launch_route_bwd_rows_t<_Float16>(a, stream);
+  }
+}
+
+}  // namespace da

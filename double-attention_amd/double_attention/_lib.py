@@ -46,7 +46,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 NOALLOC_SCRATCH_BYTES = 128 << 20
 
 _vp = ctypes.c_void_p
@@ -109,6 +109,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i32, _f32, _f32, _i32,  # beta, beta dtype, beta value, eps, flags
             _f32, _f32,  # silu gain, logit scale
             _vp, _i64, _i32, _vp,  # out, out pitch, out dtype, stream
+        ],
+    ),
+    "da_dictionary_route_backward_rows": (
+        _i32,
+        [
+            _vp, _vp, _i64, _i64, _i64,  # logits, grad_weights, rows, atoms, input pitch
+            _vp, _i32, _f32, _i32,  # beta, beta dtype, beta value, flags
+            _f32, _f32, _f32,  # silu gain, logit scale, eps
+            _vp, _vp, _i64, _i32, _vp, _vp,  # grad_logits, weights, output pitch, out dtype, dbeta rows, stream
         ],
     ),
     "da_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32]),

@@ -395,6 +395,116 @@ def _route_backward(
     )
 
 
+# The row kernel holds a row's atoms in VGPRs (at most 4096).
+ROUTE_BACKWARD_ROWS_MAX_ATOMS = 4096
+
+
+def _route_backward_rows_supported(x: Tensor, dictionary_key: Tensor) -> bool:
+    return (
+        x.is_cuda
+        and x.dtype in (torch.float16, torch.bfloat16)
+        and x.shape[-1] in SUPPORTED_WIDTHS
+        and 1 <= dictionary_key.shape[1] <= ROUTE_BACKWARD_ROWS_MAX_ATOMS
+    )
+
+
+def _mm_f32(a: Tensor, b: Tensor) -> Tensor:
+    """``a @ b`` of 16-bit operands with fp32 accumulation and an fp32 result
+    (a library GEMM; no 16-bit rounding of the product)."""
+
+    return torch.mm(a, b, out_dtype=torch.float32)
+
+
+def _route_backward_rows(
+    x: Tensor,
+    dictionary_key: Tensor,
+    dictionary_value: Tensor,
+    beta: Tensor | float,
+    eps: float,
+    normalize_input: bool,
+    normalize_output: bool,
+    grad: Tensor,
+    variant: RouteVariant,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of the route (``ops.py:16-62``) for every variant and width.
+
+    The structure of the reference's large-shape backward
+    (``triton_kernels.py:1929-1973``): two GEMMs give each row's raw logits
+    l = N_in(x) Dk and dW = dr Dv (fp32 results), ``da_dictionary_route_backward_rows``
+    turns them into the gradient at the logits and the assignment weights,
+    and three GEMMs give dN_in(x), dDk and dDv.  The logits use the forward
+    kernel's operands (unit rows rounded once to fp16 with fp16 keys; raw rows
+    in their own dtype); r, the reconstruction before the output norm, comes
+    from one route launch.  Returns gradients in the dtypes of ``x`` and the
+    dictionary tensors, and d beta as a 1-element fp32 tensor.
+    """
+
+    routing_dim = x.shape[-1]
+    atoms = dictionary_key.shape[1]
+    device = x.device
+    rows = x.detach().reshape(-1, routing_dim).float()
+    n = rows.shape[0]
+    if normalize_input:
+        x_norm = rows.norm(dim=1, keepdim=True)
+        u = rows / x_norm.clamp_min(eps)
+        key_type = torch.float16
+        u_h = _aligned(u.to(key_type))
+    else:
+        u = rows
+        key_type = x.dtype
+        u_h = _aligned(x.detach().reshape(-1, routing_dim))
+    layout = route_layout(dictionary_key.detach(), dictionary_value.detach(), key_type)
+    beta_t = beta.detach().float().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
+    r = _route_forward(u_h, layout, beta_t, eps, False, False, variant).float()
+    g = grad.detach().reshape(-1, routing_dim).float()
+    if normalize_output:
+        r_norm = r.norm(dim=1, keepdim=True)
+        z = r / r_norm.clamp_min(eps)
+        dr = torch.where(r_norm > eps, (g - z * (z * g).sum(1, keepdim=True)) / r_norm.clamp_min(eps), g / eps)
+    else:
+        dr = g
+    # 16-bit operands of the GEMMs: fp16 for fp16 inputs, bf16 for bf16 ones.
+    v_type = torch.float16 if x.dtype == torch.float16 else torch.bfloat16
+    keys_h = dictionary_key.detach().to(key_type)
+    logits = _mm_f32(u_h, keys_h)
+    dr_v = dr.to(v_type)
+    values_v = dictionary_value.detach().to(v_type)
+    # dW = dr Dv with dr split into two 16-bit terms (head + rounding
+    # residual): the softmax backward differences dW_j - sum_k w_k dW_k, so
+    # one 16-bit rounding of dr would reach every atom's gradient.
+    grad_weights = _mm_f32(dr_v, values_v)
+    grad_weights += _mm_f32((dr - dr_v.float()).to(v_type), values_v)
+    grad_logits = torch.empty(n, atoms, dtype=v_type, device=device)
+    weights = torch.empty(n, atoms, dtype=v_type, device=device)
+    dbeta_rows = torch.empty(n, dtype=torch.float32, device=device)
+    lib = _lib.get()
+    _lib.check(
+        lib.da_dictionary_route_backward_rows(
+            logits.data_ptr(), grad_weights.data_ptr(), n, atoms, atoms,
+            beta_t.data_ptr(), _lib.DA_F32, 0.0, variant.flags(),
+            float(variant.silu_gain), float(variant.logit_scale(routing_dim)), float(eps),
+            grad_logits.data_ptr(), weights.data_ptr(), atoms, _half_code(v_type), dbeta_rows.data_ptr(),
+            _stream(device),
+        ),
+        "dictionary_route_hip backward rows",
+    )
+    keys_v = dictionary_key.detach().to(v_type)
+    du = _mm_f32(grad_logits, keys_v.t())
+    d_key = _mm_f32(u.to(v_type).t(), grad_logits)
+    d_value = _mm_f32(dr_v.t(), weights)
+    dbeta = dbeta_rows.sum().reshape(1)
+    if normalize_input:
+        dx = torch.where(x_norm > eps, (du - u * (u * du).sum(1, keepdim=True)) / x_norm.clamp_min(eps), du / eps)
+    else:
+        dx = du
+    return (
+        dx.reshape(x.shape).to(x.dtype),
+        d_key.to(dictionary_key.dtype),
+        d_value.to(dictionary_value.dtype),
+        dbeta,
+    )
+
+
 class _RouteFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, variant):  # type: ignore[override]
@@ -412,8 +522,13 @@ class _RouteFunction(torch.autograd.Function):
         saved = ctx.saved_tensors
         x, dk, dv = saved[:3]
         beta = saved[3] if ctx.beta_is_tensor else ctx.beta
+        native = None
         if _route_backward_supported(x, dk, ctx.variant):
-            dx, ddk, ddv, dbeta = _route_backward(x, dk, dv, beta, ctx.eps, *ctx.flags, grad)
+            native = _route_backward(x, dk, dv, beta, ctx.eps, *ctx.flags, grad)
+        elif _route_backward_rows_supported(x, dk):
+            native = _route_backward_rows(x, dk, dv, beta, ctx.eps, *ctx.flags, grad, ctx.variant)
+        if native is not None:
+            dx, ddk, ddv, dbeta = native
             return (
                 dx if ctx.needs_input_grad[0] else None,
                 ddk if ctx.needs_input_grad[1] else None,
@@ -421,7 +536,7 @@ class _RouteFunction(torch.autograd.Function):
                 dbeta.reshape(beta.shape).to(beta.dtype) if ctx.beta_is_tensor and ctx.needs_input_grad[3] else None,
                 None, None, None, None,
             )
-        # Route variants and 512-wide rows: recompute through the torch route.
+        # More atoms than the row kernel holds: recompute through the torch route.
         with torch.enable_grad():
             inputs = [t.detach().requires_grad_(t.requires_grad) for t in (x, dk, dv)]
             beta_in = beta.detach().requires_grad_(beta.requires_grad) if ctx.beta_is_tensor else beta

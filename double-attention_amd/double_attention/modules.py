@@ -176,15 +176,14 @@ class SharedDictionaryAttention(nn.Module):
         query, key = fused.split(self.config.total_qk_width, dim=-1)
         return self._reshape_branches(query, batch, length), self._reshape_branches(key, batch, length)
 
-    def _hip_route_backward_fits(self, rows: Tensor) -> bool:
+    def _hip_route_backward_fits(self, rows: Tensor, atoms: int) -> bool:
+        """Whether a native route backward (either path) takes these rows and atoms."""
+
         from . import hip_ops
 
-        cfg = self.config
-        variant = hip_ops.RouteVariant(
-            cfg.dictionary_activation == "silu", cfg.dictionary_assignment == "silu", cfg.dictionary_silu_gain,
-            cfg.standardize_dictionary_logits, cfg.standardized_logit_scale,
-        )
-        return hip_ops._route_backward_supported(rows, rows.new_empty(rows.shape[-1], 1), variant)
+        variant = hip_ops.RouteVariant.of_config(self.config)
+        keys = torch.empty(rows.shape[-1], atoms, device="meta")
+        return hip_ops._route_backward_supported(rows, keys, variant) or hip_ops._route_backward_rows_supported(rows, keys)
 
     def _route(self, x: Tensor, dictionary_key: Tensor, dictionary_value: Tensor, backend: str) -> Tensor:
         cfg = self.config
@@ -245,7 +244,9 @@ class SharedDictionaryAttention(nn.Module):
         pair = torch.cat((query, key), dim=2)
         # The HIP backward's recompute routes on the library's kernel when the
         # native route backward covers this configuration.
-        route_backend = "hip" if attention == "hip" and self._hip_route_backward_fits(pair) else "torch"
+        route_backend = (
+            "hip" if attention == "hip" and self._hip_route_backward_fits(pair, dictionary_key.shape[1]) else "torch"
+        )
         routed = self._route(pair, dictionary_key, dictionary_value, route_backend)
         routed_query, routed_key = routed.split(x.shape[1], dim=2)
         score_query, score_key = assemble_score_maps(routed_query, routed_key, self.config.outer_maps)

@@ -18,6 +18,9 @@
  * Ahnd6474/double-attention):
  *   da_dictionary_normalize   SharedDictionaryBank.normalized        src/double_attention/modules.py:45-48
  *   da_dictionary_route       dictionary_route_triton / _reference   src/double_attention/triton_kernels.py:1984-2019, ops.py:16-62
+ *   da_dictionary_route_backward_rows
+ *                             _row_scaled_softmax_backward_kernel    src/double_attention/triton_kernels.py:589-671, 1480
+ *                             + direct-SiLU backward branch          src/double_attention/triton_kernels.py:1940-1948
  *   da_routed_attention       routed_attention_triton / _reference   src/double_attention/triton_kernels.py:2290-2305, ops.py:65-93
  *                             + map combine                          src/double_attention/modules.py:265-272
  *   da_routed_attention_backward, da_attention_backward_workspace_bytes
@@ -135,6 +138,29 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
                         int64_t atoms, const void* beta, int beta_dtype, float beta_value,
                         float eps, int flags, float silu_gain, float logit_scale, void* out,
                         int64_t out_row_stride, int out_dtype, da_stream_t stream);
+
+/*
+ * Row-wise backward of the route's assignment, every variant.  Replaces the
+ * reference's _row_scaled_softmax_backward_kernel (triton_kernels.py:589-671,
+ * launched at :1480) and the direct-SiLU branch of
+ * _DictionaryRouteFunction.backward (triton_kernels.py:1940-1948).
+ *   logits:       rows x atoms (row pitch ld_in, fp32), l_j = <N_in(x), Dk_j>
+ *   grad_weights: rows x atoms (pitch ld_in, fp32), <dr, Dv_j> for the
+ *                 gradient dr at the unnormalized reconstruction
+ *   beta, beta_dtype, beta_value, flags (DA_ROUTE_BETA_IS_LOG and the
+ *   variant bits), silu_gain, logit_scale, eps: as da_dictionary_route
+ * Writes, per row, the gradient at the raw logits (grad_logits) and the
+ * assignment weights (weights), rows x atoms with pitch ld_out in out_dtype
+ * (DA_F16 or DA_BF16), and the row's share of d beta to dbeta_rows[row]
+ * (fp32; 0 for DA_ROUTE_DIRECT_SILU; may be NULL).  atoms <= 4096.  The GEMMs
+ * around it (logits, grad_weights, then dN_in(x) = grad_logits Dk^T,
+ * dDk = N_in(x)^T grad_logits, dDv = dr^T weights) are plain library GEMMs.
+ */
+int da_dictionary_route_backward_rows(const float* logits, const float* grad_weights, int64_t rows,
+                                      int64_t atoms, int64_t ld_in, const void* beta, int beta_dtype,
+                                      float beta_value, int flags, float silu_gain, float logit_scale, float eps,
+                                      void* grad_logits, void* weights, int64_t ld_out, int out_dtype,
+                                      float* dbeta_rows, da_stream_t stream);
 
 /*
  * Flash outer attention over `maps` score maps (ops.py:65-93) with the map

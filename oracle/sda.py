@@ -117,29 +117,85 @@ def dictionary_route_backward(
     eps: float = 1e-6,
     normalize_input: bool = True,
     normalize_output: bool = True,
+    activation: str = "identity",
+    assignment: str = "softmax",
+    silu_gain: float = 1.0,
+    standardize_logits: bool = False,
+    standardized_logit_scale: float | None = None,
+    return_dbeta_rows: bool = False,
 ):
-    """Gradients of the softmax route of :func:`dictionary_route` (ops.py:16-62).
+    """Gradients of :func:`dictionary_route` (ops.py:16-62), every variant.
 
-    ``z = N_out(softmax(beta u Dk) Dv^T)`` with ``u = N_in(x)``; returns
-    ``(dx, dDk, dDv, dbeta)`` for ``d loss / dz = grad_out`` -- what the
-    reference's autograd returns for ``dictionary_route_reference``.
+    ``z = N_out(w Dv^T)`` with ``w = softmax(beta a)`` or ``(2/g) SiLU(g a)``,
+    ``a = Std(Act(u Dk))`` and ``u = N_in(x)``; returns ``(dx, dDk, dDv,
+    dbeta)`` for ``d loss / dz = grad_out`` -- what the reference's autograd
+    returns for ``dictionary_route_reference`` (dbeta is 0 for the SiLU
+    assignment, which does not use beta); with ``return_dbeta_rows`` also each
+    row's term of dbeta (the sum is often far smaller than its terms).  The chain rule, step by step:
+    the softmax backward ``d(beta a) = w (dw - sum w dw)``; the SiLU
+    assignment ``da = dw 2 SiLU'(g a)``; the standardization's backward
+    ``da0 = isd (dc - mean dc - c mean(dc c))`` with ``c`` the standardized
+    values and ``dc = s da``; the activation ``dl = da0 2 SiLU'(l)``, where
+    ``SiLU'(t) = sig(t) (1 + t (1 - sig(t)))``.
     """
 
     dt = x.dtype
     u = l2_normalize(x, -1, eps) if normalize_input else x
     logits = u @ dictionary_key.astype(dt)
-    weights = _softmax(logits * beta, -1)
+    if activation == "silu":
+        sig_l = 1.0 / (1.0 + np.exp(-logits))
+        act = 2.0 * logits * sig_l
+    elif activation == "identity":
+        act = logits
+    else:
+        raise ValueError(activation)
+    if standardize_logits:
+        centered = act - act.mean(axis=-1, keepdims=True)
+        inv_std = 1.0 / np.sqrt(np.mean(centered * centered, axis=-1, keepdims=True) + eps)
+        standardized = centered * inv_std
+        scale = x.shape[-1] ** -0.5 if standardized_logit_scale is None else standardized_logit_scale
+        assign = standardized * scale
+    else:
+        assign = act
+    if assignment == "softmax":
+        weights = _softmax(assign * beta, -1)
+    elif assignment == "silu":
+        sig_a = 1.0 / (1.0 + np.exp(-silu_gain * assign))
+        weights = (2.0 / silu_gain) * (silu_gain * assign) * sig_a
+    else:
+        raise ValueError(assignment)
     recon = weights @ dictionary_value.astype(dt).T
     d_recon = _normalize_backward(recon, grad_out, eps) if normalize_output else grad_out
     d_weights = d_recon @ dictionary_value.astype(dt)
-    d_scores = weights * (d_weights - np.sum(weights * d_weights, axis=-1, keepdims=True))
-    d_logits = beta * d_scores
+    if assignment == "softmax":
+        d_scores = weights * (d_weights - np.sum(weights * d_weights, axis=-1, keepdims=True))
+        d_assign = beta * d_scores
+        d_beta_rows = np.sum(d_scores * assign, axis=-1)
+    else:
+        t = silu_gain * assign
+        d_assign = d_weights * 2.0 * sig_a * (1.0 + t * (1.0 - sig_a))
+        d_beta_rows = np.zeros(assign.shape[:-1], dtype=dt)
+    d_beta = float(np.sum(d_beta_rows))
+    if standardize_logits:
+        d_std = d_assign * scale
+        d_act = inv_std * (
+            d_std
+            - d_std.mean(axis=-1, keepdims=True)
+            - standardized * np.mean(d_std * standardized, axis=-1, keepdims=True)
+        )
+    else:
+        d_act = d_assign
+    if activation == "silu":
+        d_logits = d_act * 2.0 * sig_l * (1.0 + logits * (1.0 - sig_l))
+    else:
+        d_logits = d_act
     d_u = d_logits @ dictionary_key.astype(dt).T
     dx = _normalize_backward(x, d_u, eps) if normalize_input else d_u
     rows_u = u.reshape(-1, u.shape[-1])
     d_key = rows_u.T @ d_logits.reshape(-1, d_logits.shape[-1])
     d_value = d_recon.reshape(-1, d_recon.shape[-1]).T @ weights.reshape(-1, weights.shape[-1])
-    d_beta = float(np.sum(d_scores * logits))
+    if return_dbeta_rows:
+        return dx, d_key, d_value, d_beta, d_beta_rows
     return dx, d_key, d_value, d_beta
 
 

@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 18
+    assert len(names) == 19
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -205,3 +205,27 @@ def test_noalloc_forward_rejects_oversized_problems_on_the_host() -> None:
     assert "scratch" in h.da_last_error().decode()
     args.batch = 0
     assert h.da_shared_dictionary_attention_forward_noalloc(ctypes.byref(args), None) == -1
+
+
+def test_route_backward_rows_rejects_bad_arguments() -> None:
+    # Host-side checks only: every call below fails before anything is launched.
+    h = lib.get()
+    buf = ctypes.c_void_p(16)   # never dereferenced
+
+    def call(**kw):
+        args = dict(logits=buf, grad_weights=buf, rows=10, atoms=100, ld_in=100, beta=None, beta_dtype=lib.DA_F32,
+                    beta_value=1.0, flags=0, silu_gain=1.0, logit_scale=1.0, eps=1e-6, grad_logits=buf, weights=buf,
+                    ld_out=100, out_dtype=lib.DA_BF16, dbeta_rows=None, stream=None)
+        args.update(kw)
+        return h.da_dictionary_route_backward_rows(*args.values())
+
+    assert call(atoms=5000) == -2                       # more atoms than the row kernel holds
+    assert call(flags=lib.DA_ROUTE_NORMALIZE_INPUT) == -1   # not a flag of this entry point
+    assert call(out_dtype=lib.DA_F32) == -1
+    assert call(ld_in=50) == -1
+    assert call(flags=lib.DA_ROUTE_DIRECT_SILU, silu_gain=0.0) == -1
+    assert call(flags=lib.DA_ROUTE_STANDARDIZE, logit_scale=-1.0) == -1
+    assert call(logits=None) == -1
+    assert b"atoms" in h.da_last_error() or b"null" in h.da_last_error()
+    assert call(rows=0, logits=None) == 0               # nothing to do
+

@@ -812,3 +812,92 @@ def test_route_backward(case, dtype) -> None:
     db = float(beta.grad)
     print(f"[parity] {label} dbeta {db:.5f} vs {float(expected[3]):.5f}", flush=True)
     assert abs(db - expected[3]) <= rel_beta * max(abs(expected[3]), 1e-3) + 1e-3, (db, expected[3])
+
+
+ROUTE_ROWS_CASES = [
+    # (rows, routing_dim, atoms, normalize_input, normalize_output, variant kwargs)
+    (300, 512, 1536, True, True, {}),
+    (130, 512, 77, False, True, {}),
+    (257, 256, 1000, True, True, {}),
+    (64, 64, 4096, True, True, {}),
+    (200, 128, 512, True, True, dict(silu_logits=True)),
+    (200, 256, 300, True, True, dict(standardize_logits=True)),
+    (96, 512, 1536, True, True, dict(standardize_logits=True, standardized_logit_scale=2.0)),
+    (150, 128, 512, True, True, dict(direct_silu=True)),
+    (150, 256, 700, False, False, dict(direct_silu=True, silu_gain=3.0)),
+    (120, 128, 512, True, True, dict(silu_logits=True, standardize_logits=True)),
+    (120, 256, 512, True, True, dict(silu_logits=True, standardize_logits=True, direct_silu=True, silu_gain=2.0)),
+]
+
+
+def _rows_case_id(c) -> str:
+    rows, r, m, ni, no, v = c
+    return f"n{rows}r{r}m{m}{'i' if ni else ''}{'o' if no else ''}" + "".join(f"-{k}={v[k]}" for k in v)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", ROUTE_ROWS_CASES, ids=_rows_case_id)
+def test_route_backward_rows(case, dtype) -> None:
+    # 512-wide rows, every variant and up to 4096 atoms: GEMMs around the row
+    # kernel (da_dictionary_route_backward_rows).  Against the fp32 oracle's
+    # gradients, pinned by finite differences for every variant; the same bar
+    # as the softmax route's other backward.  The plain softmax cases at
+    # widths up to 256 call the row path directly (the module takes the
+    # attention-kernel path there).
+    device = _device()
+    rows, routing_dim, atoms, normalize_input, normalize_output, kw = case
+    g = torch.Generator().manual_seed(rows + atoms + routing_dim)
+    x = torch.randn(rows, routing_dim, generator=g).to(device, dtype)
+    if not normalize_input:
+        x = torch.nn.functional.normalize(x.float(), dim=-1).to(dtype)
+    x.requires_grad_()
+    dk = unit_columns(routing_dim, atoms, dtype, device, rows).requires_grad_()
+    dv = unit_columns(routing_dim, atoms, dtype, device, rows + 1).requires_grad_()
+    beta = torch.tensor(6.0, device=device, requires_grad=True)
+    w = torch.randn(rows, routing_dim, generator=g).to(device, dtype)
+    variant = da.hip_ops.RouteVariant(
+        kw.get("silu_logits", False), kw.get("direct_silu", False), float(kw.get("silu_gain", 1.0)),
+        kw.get("standardize_logits", False), kw.get("standardized_logit_scale"),
+    )
+    direct_call = not kw and routing_dim in da.hip_ops.ROUTE_BACKWARD_WIDTHS
+    if direct_call:
+        dx, ddk, ddv, dbeta = da.hip_ops._route_backward_rows(
+            x, dk, dv, beta, 1e-6, normalize_input, normalize_output, w, variant)
+        grads = (dx, ddk, ddv)
+        db = float(dbeta)
+    else:
+        calls = []
+        original = da.hip_ops._route_backward_rows
+
+        def counted(*args):
+            calls.append(1)
+            return original(*args)
+
+        da.hip_ops._route_backward_rows = counted
+        try:
+            out = da.dictionary_route_hip(x, dk, dv, beta, 1e-6, normalize_input=normalize_input,
+                                          normalize_output=normalize_output, **kw)
+            out.backward(w)
+        finally:
+            da.hip_ops._route_backward_rows = original
+        assert calls == [1]
+        grads = (x.grad, dk.grad, dv.grad)
+        db = float(beta.grad) if beta.grad is not None else 0.0
+    expected = oracle.dictionary_route_backward(
+        np32(x), np32(dk), np32(dv), 6.0, np32(w), 1e-6, normalize_input, normalize_output,
+        activation="silu" if variant.silu_logits else "identity",
+        assignment="silu" if variant.direct_silu else "softmax",
+        silu_gain=variant.silu_gain, standardize_logits=variant.standardize_logits,
+        standardized_logit_scale=variant.logit_scale(routing_dim), return_dbeta_rows=True,
+    )
+    label = f"route backward rows {_rows_case_id(case)} {dtype}"
+    rel, rel_beta = (5e-3, 1e-2) if dtype == torch.float16 else (1e-2, 3e-2)
+    for name, grad, exp in zip(("x", "dk", "dv"), grads, expected[:3]):
+        assert grad.dtype == dtype
+        assert_parity(grad, exp, rel, 3e-2 * float(np.abs(exp).max()), f"{label} d{name}")
+    # d beta sums one term per row; rounding errors of the terms add in
+    # quadrature, so the bar scales with the terms' root sum of squares when
+    # they cancel (the standardized 512-wide case: terms ~1e-2, sum ~1e-3).
+    spread = float(np.sqrt(np.sum(np.square(expected[4], dtype=np.float64))))
+    print(f"[parity] {label} dbeta {db:.5f} vs {float(expected[3]):.5f} (row terms rss {spread:.4f})", flush=True)
+    assert abs(db - expected[3]) <= rel_beta * max(abs(expected[3]), spread, 1e-3) + 1e-3, (db, expected[3])

@@ -252,3 +252,6 @@ def test_backward_dispatch_rules() -> None:
     assert hip_ops.ROUTE_BACKWARD_WIDTHS == (64, 128, 256)
     assert 512 in hip_ops.BACKWARD_SCORE_WIDTHS
     assert silu.flags() != 0 and standard.flags() == 0
+    # The row-kernel path takes every width and variant up to 4096 atoms, on the GPU only.
+    assert not hip_ops._route_backward_rows_supported(meta, key)
+    assert hip_ops.ROUTE_BACKWARD_ROWS_MAX_ATOMS == 4096

@@ -197,6 +197,55 @@ def test_route_backward_matches_finite_differences(normalize_input: bool, normal
     np.testing.assert_allclose(dbeta, numeric_beta, rtol=1e-6, atol=1e-8)
 
 
+ROUTE_VARIANTS = [
+    dict(activation="silu"),
+    dict(standardize_logits=True),
+    dict(standardize_logits=True, standardized_logit_scale=1.7),
+    dict(assignment="silu", silu_gain=1.0),
+    dict(assignment="silu", silu_gain=3.0),
+    dict(activation="silu", standardize_logits=True),
+    dict(activation="silu", standardize_logits=True, assignment="silu", silu_gain=2.0),
+]
+
+
+@pytest.mark.parametrize("variant", ROUTE_VARIANTS, ids=lambda v: "-".join(f"{k}={v[k]}" for k in v))
+@pytest.mark.parametrize(("normalize_input", "normalize_output"), [(True, True), (False, False)])
+def test_route_variant_backward_matches_finite_differences(variant, normalize_input, normalize_output) -> None:
+    # The SiLU activation, standardized logits and the SiLU assignment
+    # (ops.py:41-59): every gradient of the oracle's chain rule against
+    # central differences of the oracle forward, in fp64.
+    rng = np.random.default_rng(12)
+    r, m = 4, 7
+    x = rng.standard_normal((2, 3, r))
+    dk, dv = _unit_columns(r, m, rng), _unit_columns(r, m, rng)
+    beta = 1.9
+    w = rng.standard_normal((2, 3, r))
+    dx, ddk, ddv, dbeta = oracle.dictionary_route_backward(
+        x, dk, dv, beta, w, 1e-6, normalize_input, normalize_output, **variant
+    )
+
+    def loss(x_, dk_, dv_, b_):
+        out = oracle.dictionary_route(x_, dk_, dv_, b_, 1e-6, normalize_input=normalize_input,
+                                      normalize_output=normalize_output, **variant)
+        return float((out * w).sum())
+
+    h = 1e-6
+    for idx, arr, grad in ((0, x, dx), (1, dk, ddk), (2, dv, ddv)):
+        numeric = np.zeros_like(arr)
+        for pos in np.ndindex(arr.shape):
+            plus, minus = arr.copy(), arr.copy()
+            plus[pos] += h
+            minus[pos] -= h
+            args_p, args_m = [x, dk, dv, beta], [x, dk, dv, beta]
+            args_p[idx], args_m[idx] = plus, minus
+            numeric[pos] = (loss(*args_p) - loss(*args_m)) / (2 * h)
+        np.testing.assert_allclose(grad, numeric, rtol=1e-5, atol=1e-8)
+    numeric_beta = (loss(x, dk, dv, beta + h) - loss(x, dk, dv, beta - h)) / (2 * h)
+    np.testing.assert_allclose(dbeta, numeric_beta, rtol=1e-5, atol=1e-8)
+    if variant.get("assignment") == "silu":
+        assert dbeta == 0.0
+
+
 # ---------------------------------------------------------------- outer attention
 
 
