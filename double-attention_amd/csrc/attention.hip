@@ -85,8 +85,14 @@ __device__ __forceinline__ float map_weight(const AttnParams& p, int s) {
 template <typename T, int DC>
 __device__ __forceinline__ void store_rows(const AttnParams& p, int b, int s, int t, int g, int d0,
                                            const f32x4* acc, float w) {
-  T* orow = static_cast<T*>(p.out) + b * p.out_stride_b + static_cast<int64_t>(t) * p.out_stride_t +
-            s * p.out_stride_s + d0;
+  const int64_t at = b * p.out_stride_b + static_cast<int64_t>(t) * p.out_stride_t + s * p.out_stride_s + d0;
+  if (p.flags & kAttnOutF32) {
+    float* orow = static_cast<float*>(p.out) + at;
+#pragma unroll
+    for (int db = 0; db < DC / 16; ++db) *reinterpret_cast<f32x4*>(orow + db * 16 + 4 * g) = acc[db] * w;
+    return;
+  }
+  T* orow = static_cast<T*>(p.out) + at;
 #pragma unroll
   for (int db = 0; db < DC / 16; ++db) {
     typename Elem<T>::v4 o;
@@ -687,16 +693,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) yacc[cb][i] += acc[cb][i] * w;
       } else if (tq < p.T) {
-        TV* orow = static_cast<TV*>(p.out) + b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t +
-                   ((p.flags & kAttnMix) ? 0 : s) * p.out_stride_s + ds0;
-#pragma unroll
-        for (int db = 0; db < NB; ++db) {
-          const f32x4 v = acc[cb][db] * w;
-          typename Elem<TV>::v4 o;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = static_cast<TV>(v[r]);
-          *reinterpret_cast<typename Elem<TV>::v4*>(orow + db * 16 + 4 * g) = o;
-        }
+        store_rows<TV, DS>(p, b, (p.flags & kAttnMix) ? 0 : s, tq, g, ds0, acc[cb], w);
       }
 #pragma unroll
       for (int i = 0; i < NB; ++i) acc[cb][i] = zero4();
@@ -883,15 +880,19 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) out[k] += o[k] * w;
   }
-  TV* orow = static_cast<TV*>(p.out) + b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t + ds0;
+  const int64_t at = b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t + ds0;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int d4 = (k * 64 + lane) * 4;
     if (d4 < DS) {
-      typename Elem<TV>::v4 v;
+      if (p.flags & kAttnOutF32) {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + at + d4) = out[k];
+      } else {
+        typename Elem<TV>::v4 v;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(out[k][i]);
-      *reinterpret_cast<typename Elem<TV>::v4*>(orow + d4) = v;
+        for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(out[k][i]);
+        *reinterpret_cast<typename Elem<TV>::v4*>(static_cast<TV*>(p.out) + at + d4) = v;
+      }
     }
   }
 }

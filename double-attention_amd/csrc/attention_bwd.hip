@@ -54,6 +54,7 @@ struct BwdParams {
   int S, T, Tp, RP, D;
   int Tk, Tkp;          // keys (== T when causal) and their padded count
   int causal;
+  int out_f32;          // out holds fp32 values
   int qchunk;           // query tiles per workgroup of the main kernel
   int n_chunks;         // query runs per key tile
 };
@@ -117,18 +118,33 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
     transpose_tile<TV, D>(static_cast<const TV*>(p.dout) + rows * D, t0, p.T,
                           static_cast<TV*>(p.doutt) + (bs * tiles + tile) * D * kQTile, lds);
 
-  // rowsum(dO . O): wave w takes rows w, w+4, ...
+  // rowsum(dO . O): wave w takes rows w, w+4, ...  O in fp32 (out_f32) keeps
+  // this sum free of O's 16-bit rounding, which would otherwise reach every
+  // dS = P (dP - rowsum) of the row (and the scale gradient's sum over them).
   const TV* dob = static_cast<const TV*>(p.dout) + rows * D;
-  const TV* ob = static_cast<const TV*>(p.out) + rows * D;
   for (int r = wave; r < kQTile; r += 4) {
     const int t = t0 + r;
     if (t >= p.T) break;
     float acc = 0.f;
     for (int d = lane * 8; d < D; d += 512) {
       const typename Elem<TV>::v8 x = load8(dob + static_cast<int64_t>(t) * D + d);
-      const typename Elem<TV>::v8 y = load8(ob + static_cast<int64_t>(t) * D + d);
+      float y[8];
+      if (p.out_f32) {
+        const float* of = static_cast<const float*>(p.out) + (rows + t) * D + d;
+        const f32x4 y0 = *reinterpret_cast<const f32x4*>(of);
+        const f32x4 y1 = *reinterpret_cast<const f32x4*>(of + 4);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc += static_cast<float>(x[j]) * static_cast<float>(y[j]);
+        for (int j = 0; j < 4; ++j) {
+          y[j] = y0[j];
+          y[4 + j] = y1[j];
+        }
+      } else {
+        const typename Elem<TV>::v8 yh = load8(static_cast<const TV*>(p.out) + (rows + t) * D + d);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = static_cast<float>(yh[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc += static_cast<float>(x[j]) * y[j];
     }
     acc = wave_sum(acc);
     if (lane == 0) p.dvec[rows + t] = acc;
@@ -577,7 +593,7 @@ void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace
               reinterpret_cast<float*>(ws + l.lse2), reinterpret_cast<float*>(ws + l.dvec), a.gamma,
               a.dq, a.dk, a.dv, a.dgamma,
               a.S, a.T, static_cast<int>(round_up(a.T, kKeyPad)), a.RP, a.D,
-              a.Tk, static_cast<int>(round_up(a.Tk, kKeyPad)), a.causal ? 1 : 0, 1, 1};
+              a.Tk, static_cast<int>(round_up(a.Tk, kKeyPad)), a.causal ? 1 : 0, a.out_f32 ? 1 : 0, 1, 1};
   if (a.qk_dtype == kF16) {
     if (a.v_dtype == kBF16) launch_bwd_t<_Float16, __bf16>(p, a.B, stream);
     else launch_bwd_t<_Float16, _Float16>(p, a.B, stream);

@@ -209,6 +209,8 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
   if (rc) return rc;
   if (!(score_bound >= 0.f) || std::isinf(score_bound))
     return fail(DA_ERR_INVALID_ARGUMENT, "attention: score_bound must be finite and >= 0");
+  if (flags & ~(DA_ATTN_CAUSAL | DA_ATTN_SCALES_ARE_LOG | DA_ATTN_MIX | DA_ATTN_OUT_F32))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention: unknown flag bits 0x%x", flags);
   const int64_t need = da_attention_workspace_bytes(batch, maps, length, score_dim, value_dim, flags);
   if (workspace && need > 0) {
     if (!aligned(workspace, 256)) return fail(DA_ERR_ALIGNMENT, "attention: workspace must be 256-byte aligned");
@@ -265,7 +267,8 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
   if (!types_ok)
     return fail(DA_ERR_UNSUPPORTED,
                 "attention backward: (qk_dtype, v_dtype) must be (F16,BF16), (F16,F16) or (BF16,BF16)");
-  if (flags & ~DA_ATTN_CAUSAL) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: unknown flag bits 0x%x", flags);
+  if (flags & ~(DA_ATTN_CAUSAL | DA_ATTN_OUT_F32))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: unknown flag bits 0x%x", flags);
   if (!pow2_width(score_dim))
     return fail(DA_ERR_UNSUPPORTED, "attention backward: score_dim %lld not in {64,128,256,512}", (long long)score_dim);
   if (!pow2_width(value_dim))
@@ -312,6 +315,7 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
   a.RP = static_cast<int>(score_dim);
   a.D = static_cast<int>(value_dim);
   a.causal = (flags & DA_ATTN_CAUSAL) != 0;
+  a.out_f32 = (flags & DA_ATTN_OUT_F32) != 0;
   a.qk_dtype = qk_dtype;
   a.v_dtype = v_dtype;
   da::launch_routed_attention_backward(a, workspace, reinterpret_cast<hipStream_t>(stream));

@@ -32,6 +32,7 @@ enum : int {
   kAttnCausal = 1,
   kAttnScalesAreLog = 2,
   kAttnMix = 4,   // weighted sum over maps into one output; else one output per map
+  kAttnOutF32 = 8,   // outputs in fp32 (else in the value dtype)
 };
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
@@ -86,7 +87,7 @@ struct AttentionBwdArgs {
   const void* q;         // [B*S][T][RP] routed queries, qk_dtype
   const void* k;         // [B*S][Tk][RP] routed keys
   const void* v;         // [B][Tk][D] values, v_dtype
-  const void* out;       // [B*S][T][D] forward output, v_dtype
+  const void* out;       // [B*S][T][D] forward output, v_dtype (fp32 with out_f32)
   const void* dout;      // [B*S][T][D] output gradient, v_dtype
   const float* gamma;    // [S] score scales
   float* dq;             // [B*S][T][RP]
@@ -96,6 +97,7 @@ struct AttentionBwdArgs {
   int B, S, T, RP, D;
   int Tk;                // keys per sequence (== T when causal)
   bool causal;
+  bool out_f32;          // out holds fp32 values
   int qk_dtype, v_dtype;
 };
 // Byte offsets of the backward's workspace pieces (256-byte aligned).

@@ -28,6 +28,7 @@ DA_ROUTE_DIRECT_SILU = 64
 DA_ATTN_CAUSAL = 1
 DA_ATTN_SCALES_ARE_LOG = 2
 DA_ATTN_MIX = 4
+DA_ATTN_OUT_F32 = 8
 
 DA_SDA_NORMALIZE_INPUT = 1
 DA_SDA_NORMALIZE_OUTPUT = 2

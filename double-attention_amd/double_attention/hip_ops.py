@@ -240,18 +240,20 @@ def _route_forward(
     normalize_input: bool,
     normalize_output: bool,
     variant: RouteVariant = RouteVariant(),
+    out_dtype: torch.dtype | None = None,
 ) -> Tensor:
     routing_dim = x.shape[-1]
+    out_dtype = x.dtype if out_dtype is None else out_dtype
     if routing_dim != layout.key_t.shape[1]:
         raise ValueError("input width does not match the dictionary routing_dim")
     if routing_dim not in SUPPORTED_WIDTHS:
         raise NotImplementedError(f"HIP route supports routing_dim in {SUPPORTED_WIDTHS}, got {routing_dim}")
     rows_view = x.reshape(-1, routing_dim)
     if rows_view.shape[0] == 0:
-        return torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        return torch.empty(x.shape, dtype=out_dtype, device=x.device)
     if rows_view.stride(-1) != 1 or rows_view.stride(0) % 8 or rows_view.data_ptr() % 16:
         rows_view = _aligned(rows_view)
-    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
     flags = (
         (_lib.DA_ROUTE_NORMALIZE_INPUT if normalize_input else 0)
         | (_lib.DA_ROUTE_NORMALIZE_OUTPUT if normalize_output else 0)
@@ -288,7 +290,7 @@ def _route_forward(
             float(variant.logit_scale(routing_dim)),
             out.data_ptr(),
             routing_dim,
-            _half_code(x.dtype),
+            _half_code(out_dtype),
             _stream(x.device),
         ),
         "dictionary_route_hip",
@@ -505,6 +507,59 @@ def _route_backward_rows(
     )
 
 
+def route_gradients(
+    x: Tensor,
+    dictionary_key: Tensor,
+    dictionary_value: Tensor,
+    beta: Tensor | float,
+    eps: float,
+    normalize_input: bool,
+    normalize_output: bool,
+    variant: RouteVariant,
+    grad: Tensor,
+    needs: tuple[bool, bool, bool, bool] = (True, True, True, True),
+) -> tuple[Tensor | None, Tensor | None, Tensor | None, Tensor | None]:
+    """(dx, dDk, dDv, dbeta) of the route for ``d loss / d out = grad``.
+
+    The attention backward kernels take the plain softmax route up to
+    256-wide rows; the row kernel with library GEMMs takes every width and
+    variant up to 4096 atoms; beyond that autograd recomputes the torch route.
+    ``needs`` marks the wanted gradients (dbeta only for a tensor beta).
+    """
+
+    native = None
+    if _route_backward_supported(x, dictionary_key, variant):
+        native = _route_backward(x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad)
+    elif _route_backward_rows_supported(x, dictionary_key):
+        native = _route_backward_rows(
+            x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, variant
+        )
+    if native is not None:
+        dx, ddk, ddv, dbeta = native
+        beta_grad = dbeta.reshape(beta.shape).to(beta.dtype) if isinstance(beta, Tensor) and needs[3] else None
+        return (dx if needs[0] else None, ddk if needs[1] else None, ddv if needs[2] else None, beta_grad)
+    with torch.enable_grad():
+        inputs = [t.detach().requires_grad_(need) for t, need in zip((x, dictionary_key, dictionary_value), needs)]
+        beta_in = beta.detach().requires_grad_(needs[3]) if isinstance(beta, Tensor) else beta
+        out = dictionary_route_reference(
+            inputs[0], inputs[1], inputs[2], beta_in, eps,
+            activation="silu" if variant.silu_logits else "identity",
+            assignment="silu" if variant.direct_silu else "softmax",
+            silu_gain=variant.silu_gain,
+            standardize_logits=variant.standardize_logits,
+            standardized_logit_scale=variant.standardized_logit_scale,
+            normalize_input=normalize_input, normalize_output=normalize_output,
+        )
+        wrt = [t for t in inputs if t.requires_grad]
+        if isinstance(beta_in, Tensor) and beta_in.requires_grad:
+            wrt.append(beta_in)
+        grads = torch.autograd.grad(out, wrt, grad, allow_unused=True) if wrt else ()
+    it = iter(grads)
+    result = [next(it) if t.requires_grad else None for t in inputs]
+    beta_grad = next(it) if isinstance(beta_in, Tensor) and beta_in.requires_grad else None
+    return (*result, beta_grad)
+
+
 class _RouteFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, variant):  # type: ignore[override]
@@ -522,42 +577,8 @@ class _RouteFunction(torch.autograd.Function):
         saved = ctx.saved_tensors
         x, dk, dv = saved[:3]
         beta = saved[3] if ctx.beta_is_tensor else ctx.beta
-        native = None
-        if _route_backward_supported(x, dk, ctx.variant):
-            native = _route_backward(x, dk, dv, beta, ctx.eps, *ctx.flags, grad)
-        elif _route_backward_rows_supported(x, dk):
-            native = _route_backward_rows(x, dk, dv, beta, ctx.eps, *ctx.flags, grad, ctx.variant)
-        if native is not None:
-            dx, ddk, ddv, dbeta = native
-            return (
-                dx if ctx.needs_input_grad[0] else None,
-                ddk if ctx.needs_input_grad[1] else None,
-                ddv if ctx.needs_input_grad[2] else None,
-                dbeta.reshape(beta.shape).to(beta.dtype) if ctx.beta_is_tensor and ctx.needs_input_grad[3] else None,
-                None, None, None, None,
-            )
-        # More atoms than the row kernel holds: recompute through the torch route.
-        with torch.enable_grad():
-            inputs = [t.detach().requires_grad_(t.requires_grad) for t in (x, dk, dv)]
-            beta_in = beta.detach().requires_grad_(beta.requires_grad) if ctx.beta_is_tensor else beta
-            v = ctx.variant
-            out = dictionary_route_reference(
-                inputs[0], inputs[1], inputs[2], beta_in, ctx.eps,
-                activation="silu" if v.silu_logits else "identity",
-                assignment="silu" if v.direct_silu else "softmax",
-                silu_gain=v.silu_gain,
-                standardize_logits=v.standardize_logits,
-                standardized_logit_scale=v.standardized_logit_scale,
-                normalize_input=ctx.flags[0], normalize_output=ctx.flags[1],
-            )
-            wrt = [t for t in inputs if t.requires_grad]
-            if ctx.beta_is_tensor and beta_in.requires_grad:
-                wrt.append(beta_in)
-            grads = torch.autograd.grad(out, wrt, grad) if wrt else ()
-        it = iter(grads)
-        result = [next(it) if t.requires_grad else None for t in inputs]
-        beta_grad = next(it) if ctx.beta_is_tensor and beta_in.requires_grad else None
-        return (*result, beta_grad, None, None, None, None)
+        grads = route_gradients(x, dk, dv, beta, ctx.eps, *ctx.flags, ctx.variant, grad, tuple(ctx.needs_input_grad[:4]))
+        return (*grads, None, None, None, None)
 
 
 def dictionary_route_hip(
@@ -627,10 +648,18 @@ def value_transposed(value: Tensor, width: int | None = None) -> Tensor:
 
 
 def _attention_forward(
-    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, causal: bool, score_bound: float = 0.0
+    query: Tensor, key: Tensor, value: Tensor | None, scales: Tensor, causal: bool, score_bound: float = 0.0,
+    vt: Tensor | None = None, out_dtype: torch.dtype | None = None,
 ) -> Tensor:
+    """Per-map outputs ``[B, S, T, D]``; the values come as rows ``value``
+    ``[B, T, D]`` or already as the projection's V^T tiles ``vt`` (D a
+    supported width).  ``out_dtype`` torch.float32 keeps the outputs in fp32
+    (else the value dtype)."""
+
     batch, maps, length, score_dim = query.shape
-    model_dim = value.shape[-1]
+    model_dim = value.shape[-1] if vt is None else vt.shape[2]
+    value_dtype = value.dtype if vt is None else vt.dtype
+    device = query.device
     score_width = _next_width(score_dim)
     value_width = _next_width(model_dim)
     q = query.detach()
@@ -641,13 +670,17 @@ def _attention_forward(
         k = torch.nn.functional.pad(k, pad)
     q = _aligned(q)
     k = _aligned(k)
-    vt = value_transposed(value, value_width)
-    out = torch.empty(batch, maps, length, value_width, dtype=value.dtype, device=value.device)
+    if vt is None:
+        vt = value_transposed(value, value_width)
+    elif value_width != model_dim:
+        raise ValueError("V^T tiles need a supported value width")
+    out_f32 = out_dtype == torch.float32
+    out = torch.empty(batch, maps, length, value_width, dtype=torch.float32 if out_f32 else value_dtype, device=device)
     scales_c = scales.detach().contiguous()
     lib = _lib.get()
-    flags = _lib.DA_ATTN_CAUSAL if causal else 0
+    flags = (_lib.DA_ATTN_CAUSAL if causal else 0) | (_lib.DA_ATTN_OUT_F32 if out_f32 else 0)
     ws_bytes = lib.da_attention_workspace_bytes(batch, maps, length, score_width, value_width, flags)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=value.device) if ws_bytes > 0 else None
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
     _lib.check(
         lib.da_routed_attention(
             q.data_ptr(), k.data_ptr(),
@@ -656,10 +689,10 @@ def _attention_forward(
             batch, maps, length, value_width,
             scales_c.data_ptr(), dtype_code(scales_c.dtype), 1.0, None, _lib.DA_F32,
             flags, float(score_bound),
-            _half_code(q.dtype), _half_code(value.dtype),
+            _half_code(q.dtype), _half_code(value_dtype),
             out.data_ptr(), out.stride(0), out.stride(2), out.stride(1),
             _ptr(workspace), ws_bytes,
-            _stream(value.device),
+            _stream(device),
         ),
         "routed_attention_hip",
     )
@@ -697,7 +730,9 @@ def _attention_backward(
     q = _padded_rows(query.detach(), score_width)
     k = _padded_rows(key.detach(), score_width)
     v = _padded_rows(value.detach(), value_width)
-    o = _padded_rows(out.detach(), value_width)
+    # fp32 forward outputs stay fp32 (the kernel's rowsum(dO . O) reads them so).
+    out_f32 = out.dtype == torch.float32
+    o = _padded_rows(out.detach() if out_f32 else out.detach().to(value.dtype), value_width)
     go = _padded_rows(grad.detach().to(value.dtype), value_width)
     gamma = scales.detach().float().contiguous()
     lib = _lib.get()
@@ -711,7 +746,8 @@ def _attention_backward(
         lib.da_routed_attention_backward(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), go.data_ptr(), gamma.data_ptr(),
             batch, maps, length, length, score_width, value_width,
-            _lib.DA_ATTN_CAUSAL if causal else 0, _half_code(q.dtype), _half_code(value.dtype),
+            (_lib.DA_ATTN_CAUSAL if causal else 0) | (_lib.DA_ATTN_OUT_F32 if out_f32 else 0),
+            _half_code(q.dtype), _half_code(value.dtype),
             workspace.data_ptr(), ws_bytes, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(),
             _stream(device),
         ),
@@ -731,6 +767,26 @@ def _native_backward_supported(query: Tensor, value: Tensor) -> bool:
     return score_dim <= BACKWARD_SCORE_WIDTHS[-1] and batch * maps <= 65535 and value.shape[-1] <= SUPPORTED_WIDTHS[-1]
 
 
+def attention_gradients(
+    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, out: Tensor, grad: Tensor, causal: bool,
+    needs: tuple[bool, bool, bool, bool] = (True, True, True, True),
+) -> tuple[Tensor | None, Tensor | None, Tensor | None, Tensor | None]:
+    """(dq, dk, dv, dscales) of the outer attention whose output was ``out``:
+    the native backward kernels, or autograd of the fp32-softmax reference
+    for score widths above 512."""
+
+    if _native_backward_supported(query, value) and query.numel() and value.numel():
+        grads = _attention_backward(query, key, value, scales, out, grad, causal)
+        return tuple(g if need else None for g, need in zip(grads, needs))  # type: ignore[return-value]
+    with torch.enable_grad():
+        inputs = [t.detach().requires_grad_(need) for t, need in zip((query, key, value, scales), needs)]
+        ref = routed_attention_reference(*inputs, causal)
+        wrt = [t for t in inputs if t.requires_grad]
+        grads = torch.autograd.grad(ref, wrt, grad) if wrt else ()
+    it = iter(grads)
+    return tuple(next(it) if t.requires_grad else None for t in inputs)  # type: ignore[return-value]
+
+
 class _AttentionFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, query, key, value, scales, causal):  # type: ignore[override]
@@ -742,18 +798,8 @@ class _AttentionFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad):  # type: ignore[override]
         query, key, value, scales, out = ctx.saved_tensors
-        needs = ctx.needs_input_grad[:4]
-        if _native_backward_supported(query, value) and query.numel() and value.numel():
-            grads = _attention_backward(query, key, value, scales, out, grad, ctx.causal)
-            return (*[g if need else None for g, need in zip(grads, needs)], None)
-        # Score widths above 512: recompute through the fp32-softmax reference.
-        with torch.enable_grad():
-            inputs = [t.detach().requires_grad_(need) for t, need in zip((query, key, value, scales), needs)]
-            ref = routed_attention_reference(*inputs, ctx.causal)
-            wrt = [t for t in inputs if t.requires_grad]
-            grads = torch.autograd.grad(ref, wrt, grad) if wrt else ()
-        it = iter(grads)
-        return (*[next(it) if t.requires_grad else None for t in inputs], None)
+        grads = attention_gradients(query, key, value, scales, out, grad, ctx.causal, tuple(ctx.needs_input_grad[:4]))
+        return (*grads, None)
 
 
 def routed_attention_hip(

@@ -400,10 +400,18 @@ class SharedDictionaryAttention(nn.Module):
 
 
 class _HipModuleFunction(torch.autograd.Function):
-    """HIP forward with a backward that recomputes the PyTorch composition.
+    """HIP forward and native backward of one ``SharedDictionaryAttention`` call.
 
     Inputs are ``x``, the normalized dictionary (or the raw bank parameters)
     and every module parameter, so autograd routes gradients to all of them.
+    The forward runs the library's stages one launch each (Q/K/V projection,
+    route, per-map attention, map combine, output projection) and keeps what
+    the backward needs: the pre-route rows, the routed rows, the per-map
+    attention outputs, the combined maps and the V^T tiles.  The backward
+    then runs no forward again: the output projection's GEMMs, the map
+    combine's backward, the native attention backward, the score-map
+    assembly's backward, the native route backward and the projection GEMMs
+    (reference modules.py:190-291 and its autograd).
     """
 
     @staticmethod
@@ -430,31 +438,162 @@ class _HipModuleFunction(torch.autograd.Function):
     def forward(ctx, module, dtype, x, dictionary_key, dictionary_value, *params):  # type: ignore[override]
         from . import hip_ops
 
+        cfg = module.config
+        batch, length, model_dim = x.shape
+        branches, maps, routing_dim = cfg.qk_branches, cfg.outer_maps, cfg.routing_dim
+
+        def cast(t: Tensor) -> Tensor:
+            return hip_ops._aligned(t.detach().to(dtype))
+
+        xc = cast(x)
+        qk, vt = hip_ops.qkv_projection_hip(
+            xc, cast(module.query.weight), cast(module.key.weight), cast(module.value.weight), module.value.bias
+        )
+        key_dtype = hip_ops.route_key_dtype(cfg.normalize_routing_input, dtype)
+        layout = hip_ops.route_layout(dictionary_key, dictionary_value, key_dtype)
+        variant = hip_ops.RouteVariant.of_config(cfg)
+        beta = module.beta.detach()
+        # Q and K rows route together, as [B, T, 2, H, R] rows; fp16 out (the
+        # attention's operand type for bounded rows).
+        routed = hip_ops._route_forward(
+            qk.view(-1, routing_dim), layout, beta, cfg.eps, cfg.normalize_routing_input,
+            cfg.normalize_routing_output, variant, out_dtype=torch.float16,
+        )
+        score_query, score_key = _HipModuleFunction._score_maps(routed, batch, length, branches, maps, routing_dim)
+        scales = score_scale_from_log(module.log_score_scales.detach()).float()
+        group = branches // maps if branches > maps else 1
+        bound = 1.01 * group if cfg.normalize_routing_output else 0.0
+        # fp32 per-map outputs: the combine sums them before one rounding (as
+        # the fused forward's in-kernel mix), and the backward's rowsum(dO . O)
+        # and map-mix gradient read them unrounded.
+        map_output = hip_ops._attention_forward(
+            score_query, score_key, None, scales, cfg.causal, bound, vt=vt, out_dtype=torch.float32
+        )
+        factors = None
+        if cfg.map_combine == "weighted_sum":
+            if module.map_mix_logits is None:
+                mixed = map_output[:, 0].to(dtype)
+            else:
+                # The weights rounded to the map dtype, the sum in fp32 (as _combine).
+                factors = torch.softmax(module.map_mix_logits.detach(), dim=0).to(dtype).float()
+                mixed = (map_output.float() * factors[None, :, None, None]).sum(1).to(dtype)
+        else:
+            mixed = map_output.permute(0, 2, 1, 3).reshape(batch, length, maps * model_dim).to(dtype)
+        mixed = hip_ops._aligned(mixed)
+        output_weight = cast(module.output.weight) if isinstance(module.output, nn.Linear) else None
+        out = mixed if output_weight is None else hip_ops.linear_hip(mixed, output_weight)
         ctx.module = module
         ctx.dtype = dtype
-        ctx.autocast = x.is_cuda and torch.is_autocast_enabled("cuda")
-        ctx.save_for_backward(x, dictionary_key, dictionary_value, *params)
-        key_dtype = hip_ops.route_key_dtype(module.config.normalize_routing_input, dtype)
-        layout = hip_ops.route_layout(dictionary_key, dictionary_value, key_dtype)
-        return hip_ops.shared_dictionary_attention_hip(module, x, layout, dtype).output
+        ctx.param_names = [name for name, _ in module.named_parameters()]
+        ctx.x_dtype = x.dtype
+        ctx.save_for_backward(xc, qk, routed, map_output, mixed, vt, scales, beta, dictionary_key, dictionary_value,
+                              factors if factors is not None else torch.empty(0), *params)
+        return out
+
+    @staticmethod
+    def _score_maps(routed: Tensor, batch: int, length: int, branches: int, maps: int, routing_dim: int):
+        rows = routed.view(batch, length, 2, branches, routing_dim)
+        return assemble_score_maps(rows[:, :, 0].transpose(1, 2), rows[:, :, 1].transpose(1, 2), maps)
 
     @staticmethod
     def backward(ctx, grad):  # type: ignore[override]
+        from . import hip_ops
+        from .hip_ops import _mm_f32
+
         module = ctx.module
-        saved = ctx.saved_tensors
-        x, dk, dv = saved[:3]
-        params = list(module.parameters())
-        with torch.enable_grad(), torch.autocast("cuda", dtype=ctx.dtype, enabled=ctx.autocast):
-            xs = x.detach().requires_grad_(x.requires_grad)
-            dks = dk.detach().requires_grad_(dk.requires_grad)
-            dvs = dv.detach().requires_grad_(dv.requires_grad)
-            out = module._torch_forward(xs, dks, dvs, False, attention="hip")
-            wrt = [t for t in (xs, dks, dvs) if t.requires_grad] + [p for p in params if p.requires_grad]
-            grads = torch.autograd.grad(out, wrt, grad.to(out.dtype), allow_unused=True) if wrt else ()
-        it = iter(grads)
-        head = [next(it) if t.requires_grad else None for t in (xs, dks, dvs)]
-        tail = [next(it) if p.requires_grad else None for p in params]
-        return (None, None, *head, *tail)
+        cfg = module.config
+        dtype = ctx.dtype
+        xc, qk, routed, map_output, mixed, vt, scales, beta, dk, dv, factors, *params = ctx.saved_tensors
+        named = dict(zip(ctx.param_names, params))
+        batch, length, model_dim = xc.shape
+        branches, maps, routing_dim = cfg.qk_branches, cfg.outer_maps, cfg.routing_dim
+        width = branches * routing_dim
+        tokens = batch * length
+        grads: dict[str, Tensor] = {}
+
+        def wants(name: str) -> bool:
+            return name in named and named[name].requires_grad
+
+        # Output projection.
+        g = grad.reshape(tokens, -1).to(dtype)
+        mixed2d = mixed.reshape(tokens, -1)
+        if isinstance(module.output, nn.Linear):
+            d_mixed = torch.mm(g, named["output.weight"].detach().to(dtype))
+            if wants("output.weight"):
+                grads["output.weight"] = _mm_f32(g.t(), mixed2d)
+        else:
+            d_mixed = g
+        # Map combine.
+        if cfg.map_combine == "weighted_sum":
+            if module.map_mix_logits is None:
+                d_maps = d_mixed.view(batch, 1, length, model_dim)
+            else:
+                d32 = d_mixed.float().view(batch, 1, length, model_dim)
+                if wants("map_mix_logits"):
+                    # fp32 throughout: the per-map sums dY . O_s are large and
+                    # nearly equal, and the softmax backward differences them.
+                    per_map = (map_output.float() * d32).sum(dim=(0, 2, 3))
+                    alpha = torch.softmax(module.map_mix_logits.detach().float(), dim=0)
+                    grads["map_mix_logits"] = alpha * (per_map - (alpha * per_map).sum())
+                d_maps = (d32 * factors[None, :, None, None]).to(dtype)
+        else:
+            d_maps = d_mixed.view(batch, length, maps, model_dim).transpose(1, 2)
+        # Outer attention.
+        score_query, score_key = _HipModuleFunction._score_maps(routed, batch, length, branches, maps, routing_dim)
+        padded = vt.shape[1] * 32
+        value_rows = vt.transpose(2, 3).reshape(batch, padded, model_dim)[:, :length]
+        d_sq, d_sk, d_value, d_scales = hip_ops.attention_gradients(
+            score_query, score_key, value_rows, scales, map_output, d_maps, cfg.causal
+        )
+        if wants("log_score_scales"):
+            log_scales = named["log_score_scales"].detach()
+            inside = (log_scales >= math.log(0.25)) & (log_scales <= math.log(1024.0))
+            grads["log_score_scales"] = d_scales.float() * scales * inside
+        # Score-map assembly (views, grouping or repetition of the branches).
+        if branches == maps:
+            d_rq, d_rk = d_sq, d_sk
+        else:
+            with torch.enable_grad():
+                rows = routed.view(batch, length, 2, branches, routing_dim)
+                rq = rows[:, :, 0].transpose(1, 2).detach().requires_grad_()
+                rk = rows[:, :, 1].transpose(1, 2).detach().requires_grad_()
+                sq, sk = assemble_score_maps(rq, rk, maps)
+                d_rq, d_rk = torch.autograd.grad((sq, sk), (rq, rk), (d_sq.to(sq.dtype), d_sk.to(sk.dtype)))
+        d_routed = torch.stack((d_rq.transpose(1, 2), d_rk.transpose(1, 2)), dim=2).reshape(-1, routing_dim)
+        # Route.
+        variant = hip_ops.RouteVariant.of_config(cfg)
+        d_rows, d_key, d_val, d_beta = hip_ops.route_gradients(
+            qk.view(-1, routing_dim), dk, dv, beta, cfg.eps, cfg.normalize_routing_input,
+            cfg.normalize_routing_output, variant, d_routed,
+            (True, ctx.needs_input_grad[3], ctx.needs_input_grad[4], wants("log_beta")),
+        )
+        if wants("log_beta") and d_beta is not None:
+            log_beta = named["log_beta"].detach()
+            inside = (log_beta >= math.log(0.05)) & (log_beta <= math.log(64.0))
+            grads["log_beta"] = d_beta.float() * beta.float() * inside
+        # Q/K/V projections.
+        x2d = xc.reshape(tokens, model_dim)
+        d_qk = d_rows.reshape(tokens, 2 * width).to(dtype)
+        d_v = d_value.reshape(tokens, model_dim).to(dtype)
+        dx = None
+        if ctx.needs_input_grad[2]:
+            dx = torch.mm(d_v, named["value.weight"].detach().to(dtype))
+            dx.addmm_(d_qk[:, :width], named["query.weight"].detach().to(dtype))
+            dx.addmm_(d_qk[:, width:], named["key.weight"].detach().to(dtype))
+            dx = dx.view(batch, length, model_dim).to(ctx.x_dtype)
+        if wants("query.weight"):
+            grads["query.weight"] = _mm_f32(d_qk[:, :width].t(), x2d)
+        if wants("key.weight"):
+            grads["key.weight"] = _mm_f32(d_qk[:, width:].t(), x2d)
+        if wants("value.weight"):
+            grads["value.weight"] = _mm_f32(d_v.t(), x2d)
+        if wants("value.bias"):
+            grads["value.bias"] = d_v.float().sum(0)
+        tail = [
+            grads[name].to(named[name].dtype).reshape(named[name].shape) if name in grads else None
+            for name in ctx.param_names
+        ]
+        return (None, None, dx, d_key, d_val, *tail)
 
 
 def _hip_attention_backward_fits(score_query: Tensor, value: Tensor) -> bool:

@@ -75,6 +75,7 @@ typedef struct ihipStream_t* da_stream_t; /* hipStream_t; NULL = default stream 
 #define DA_ATTN_CAUSAL 1
 #define DA_ATTN_SCALES_ARE_LOG 2    /* scales are log_score_scales: exp(clamp(., ln .25, ln 1024)) */
 #define DA_ATTN_MIX 4               /* alpha-weighted sum of the maps into one output */
+#define DA_ATTN_OUT_F32 8           /* out holds fp32 values (forward: written so; backward: read so) */
 
 /* da_shared_dictionary_attention_forward flags */
 #define DA_SDA_NORMALIZE_INPUT 1
@@ -183,8 +184,8 @@ int da_dictionary_route_backward_rows(const float* logits, const float* grad_wei
  *     the probability type skip the online-softmax rescaling (bf16 V only).
  * maps <= 64.  score_dim and value_dim must be 64, 128, 256 or 512.  Element types:
  *   (qk_dtype, v_dtype) in {(F16, BF16), (F16, F16), (BF16, BF16)}; the output
- *   has v_dtype.  V^T padding tokens (length .. padded length - 1) must hold
- *   finite values.
+ *   has v_dtype, or fp32 with DA_ATTN_OUT_F32 (strides then count floats).
+ *   V^T padding tokens (length .. padded length - 1) must hold finite values.
  */
 int da_routed_attention(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
                         int64_t map_stride, int64_t map_repeat, int64_t score_dim,
@@ -213,7 +214,9 @@ int64_t da_attention_workspace_bytes(int64_t batch, int64_t maps, int64_t length
  *                for causal; other lengths serve cross attention such as the
  *                dictionary route, where the atoms are the keys and values)
  *   value:       [batch, key_length, value_dim], v_dtype
- *   out:         [batch*maps, length, value_dim], v_dtype (the forward output)
+ *   out:         [batch*maps, length, value_dim], v_dtype (the forward output),
+ *                or fp32 with DA_ATTN_OUT_F32 (rowsum(dO . O) then sees no
+ *                16-bit rounding of O)
  *   grad_out:    [batch*maps, length, value_dim], v_dtype
  *   scales:      [maps] fp32 score scales (already exponentiated)
  *   workspace:   >= da_attention_backward_workspace_bytes(...) bytes,
@@ -223,7 +226,7 @@ int64_t da_attention_workspace_bytes(int64_t batch, int64_t maps, int64_t length
  *   grad_value:  [batch, key_length, value_dim] fp32 (summed over the maps)
  *   grad_scales: [maps] fp32
  *   score_dim and value_dim in {64, 128, 256, 512}; flags:
- *   DA_ATTN_CAUSAL only.  The gradients are zeroed and then accumulated with
+ *   DA_ATTN_CAUSAL and DA_ATTN_OUT_F32.  The gradients are zeroed and then accumulated with
  *   fp32 atomics, so their last bits vary between runs.
  */
 int64_t da_attention_backward_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t key_length,

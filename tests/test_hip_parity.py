@@ -385,6 +385,35 @@ def test_routed_attention_backward(case, dtypes) -> None:
             assert_parity(grad, exp, rel, max(2e-2 * scale, 1e-6), f"{label} d{name}")
 
 
+@pytest.mark.parametrize("case", [(2, 3, 77, 64, 128, True), (1, 2, 200, 256, 512, True), (2, 1, 130, 512, 512, False)],
+                         ids=lambda c: "b{}s{}t{}r{}d{}{}".format(*c[:5], "c" if c[5] else ""))
+def test_attention_fp32_outputs(case) -> None:
+    # DA_ATTN_OUT_F32: the forward writes its per-map outputs in fp32 (the
+    # module's training forward) and the backward reads them so; both against
+    # the fp32 oracle, the outputs at the bf16 bar and within one bf16 rounding
+    # of the bf16 outputs, the gradients at the attention backward's bar.
+    device = _device()
+    batch, maps, length, score_dim, value_dim, causal = case
+    q = unit_rows((batch, maps, length, score_dim), torch.float16, device, 30)
+    k = unit_rows((batch, maps, length, score_dim), torch.float16, device, 31)
+    g = torch.Generator().manual_seed(32)
+    v = torch.randn(batch, length, value_dim, generator=g).to(device, torch.bfloat16)
+    s = torch.linspace(4.0, 16.0, maps, device=device)
+    w = torch.randn(batch, maps, length, value_dim, generator=g).to(device, torch.bfloat16)
+    out32 = da.hip_ops._attention_forward(q, k, v, s, causal, out_dtype=torch.float32)
+    out16 = da.hip_ops._attention_forward(q, k, v, s, causal)
+    assert out32.dtype == torch.float32 and out16.dtype == torch.bfloat16
+    expected = oracle.routed_attention(np32(q), np32(k), np32(v), np32(s), causal)
+    assert_parity(out32, expected, label=f"attention fp32 out {case}")
+    torch.testing.assert_close(out32.to(torch.bfloat16), out16, rtol=0, atol=0)
+    grads = da.hip_ops._attention_backward(q, k, v, s, out32, w, causal)
+    exp_grads = oracle.routed_attention_backward(np32(q), np32(k), np32(v), np32(s), np32(w), causal)
+    for name, grad, exp in zip("qkvs", grads, exp_grads):
+        scale = float(np.abs(exp).max())
+        rel = 3e-2 if name == "s" else 1e-2
+        assert_parity(grad, exp, rel, max(2e-2 * scale, 1e-6), f"attention backward fp32 out {case} d{name}")
+
+
 # ---------------------------------------------------------------- whole module
 
 
@@ -673,59 +702,90 @@ def test_hip_backward_matches_torch_path() -> None:
         torch.testing.assert_close(p.grad, p_ref.grad, atol=1e-3, rtol=5e-2, msg=name)
 
 
-def test_module_backward_runs_native_attention_backward(monkeypatch) -> None:
-    # The module's backward recomputes the projections through torch; the
-    # route and the outer attention take the native backward kernels.  Each
-    # gradient of the bf16 HIP module is held to max(3e-2, 2x) the relative
-    # error of the same module on the bf16 torch path, both against fp32.
-    # The score-scale gradient sums dS (q . k) over rows whose dS sums to
-    # zero, so in bf16 it is mostly rounding on either path (rel ~0.9).
+MODULE_BACKWARD_CASES = [
+    # (preset, overrides, tokens): widths 256 and 512, the route variants,
+    # grouped / repeated / one-per-branch score maps, and the concat combine.
+    ("a1", {}, 70),
+    ("a1-r512-d1536", {}, 70),
+    ("a1-silu", {}, 40),
+    ("a1-silu-logitnorm", {}, 40),
+    ("a1-no-softmax-g4", {}, 40),
+    ("a1-no-qnorm", {}, 40),
+    ("qk2-s2", {}, 40),
+    ("qk4-s4", {}, 40),
+    ("qk2-s1", {}, 40),
+    ("a1", {"outer_maps": 2}, 40),
+    ("qk2-s2", {"map_combine": "concat"}, 40),
+]
+
+
+@pytest.mark.parametrize(("preset", "overrides", "tokens"), MODULE_BACKWARD_CASES,
+                         ids=lambda v: v if isinstance(v, str) else "-".join(f"{k}={v[k]}" for k in v) if isinstance(v, dict) else str(v))
+def test_module_backward_runs_native_kernels(monkeypatch, preset, overrides, tokens) -> None:
+    # The module's backward runs no forward again: the output projection and
+    # the map combine, then the native attention and route backwards, then
+    # the projection GEMMs.  Each gradient's relative error against fp32, as a
+    # root mean square over three seeds, is held to max(3e-2, 2x) that of the
+    # same module on the bf16 torch path.  Over eight seeds because the
+    # scalar gradients (score scales, beta, map mix) sum terms that cancel:
+    # the score-scale gradient sums dS (q . k) over rows whose dS sums to
+    # zero, so one seed's error on either path is mostly the luck of its 16-bit
+    # roundings of V, dO and the routed rows (measured on a1: 0.1 to 0.9
+    # absolute on values of 1 to 6, on both paths).
     device = _device()
-    torch.manual_seed(6)
-    config = da.experiment_config("a1", backend="hip")
-    module = da.SharedDictionaryAttention(config).to(device, torch.bfloat16)
-    torch_bf16 = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(device, torch.bfloat16)
-    torch_bf16.load_state_dict(module.state_dict())
-    reference = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(device, torch.float32)
-    reference.load_state_dict({k: v.float() for k, v in module.state_dict().items()})
+    config = da.experiment_config(preset, backend="hip", **overrides)
     calls = []
-    original = da.hip_ops._attention_backward
+    for fn in ("_attention_backward", "_route_backward", "_route_backward_rows", "_route_forward"):
+        original = getattr(da.hip_ops, fn)
 
-    def counted(*args):
-        calls.append(args[0].shape)
-        return original(*args)
+        def counted(*args, _original=original, _name=fn, **kwargs):
+            calls.append(_name)
+            return _original(*args, **kwargs)
 
-    monkeypatch.setattr(da.hip_ops, "_attention_backward", counted)
-    route_calls = []
-    original_route = da.hip_ops._route_backward
-
-    def counted_route(*args):
-        route_calls.append(args[0].shape)
-        return original_route(*args)
-
-    monkeypatch.setattr(da.hip_ops, "_route_backward", counted_route)
-    g = torch.Generator().manual_seed(7)
-    x = torch.randn(2, 70, 512, generator=g).to(device, torch.bfloat16)
-    w = torch.randn(2, 70, 512, generator=g).to(device)
-    grads = []
-    for m, dtype in ((module, torch.bfloat16), (torch_bf16, torch.bfloat16), (reference, torch.float32)):
-        xi = x.detach().to(dtype).clone().requires_grad_()
-        (m(xi).float() * w).sum().backward()
-        grads.append([xi.grad] + [p.grad for p in m.parameters()])
-    assert len(calls) == 1 and len(route_calls) == 1
-    names = ["x"] + [n for n, _ in module.named_parameters()]
+        monkeypatch.setattr(da.hip_ops, fn, counted)
 
     def rel(a, b):
         return float((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-30))
 
-    for name, hip_g, t16_g, ref_g in zip(names, *grads):
-        if ref_g is None:   # a parameter the torch path leaves unused
-            assert hip_g is None or not torch.count_nonzero(hip_g), name
-            continue
-        assert hip_g is not None and torch.isfinite(hip_g).all(), name
-        err, bound = rel(hip_g, ref_g), max(3e-2, 2 * rel(t16_g, ref_g))
-        print(f"[parity] module d{name}: hip {err:.3e}, torch bf16 {rel(t16_g, ref_g):.3e}", flush=True)
-        assert err <= bound, f"d{name}: rel {err:.3e} > {bound:.3e}"
+    seeds = tuple(range(6, 86, 10))
+    squares: dict[str, list[float]] = {}
+    for seed in seeds:
+        torch.manual_seed(seed)
+        module = da.SharedDictionaryAttention(config).to(device, torch.bfloat16)
+        torch_bf16 = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(device, torch.bfloat16)
+        torch_bf16.load_state_dict(module.state_dict())
+        reference = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(device, torch.float32)
+        reference.load_state_dict({k: v.float() for k, v in module.state_dict().items()})
+        g = torch.Generator().manual_seed(seed + 1)
+        x = torch.randn(2, tokens, 512, generator=g).to(device, torch.bfloat16)
+        w = torch.randn(2, tokens, 512, generator=g).to(device)
+        grads = []
+        calls.clear()
+        for m, dtype in ((module, torch.bfloat16), (torch_bf16, torch.bfloat16), (reference, torch.float32)):
+            xi = x.detach().to(dtype).clone().requires_grad_()
+            (m(xi).float() * w).sum().backward()
+            grads.append([xi.grad] + [p.grad for p in m.parameters()])
+        # One attention backward and one native route backward; the only
+        # route forwards are the module forward's and the route backward's r.
+        assert calls.count("_attention_backward") == 1, calls
+        assert calls.count("_route_backward") + calls.count("_route_backward_rows") == 1, calls
+        assert calls.count("_route_forward") == 2, calls
+        names = ["x"] + [n for n, _ in module.named_parameters()]
+        for name, hip_g, t16_g, ref_g in zip(names, *grads):
+            if ref_g is None:   # a parameter the torch path leaves unused
+                assert hip_g is None or not torch.count_nonzero(hip_g), name
+                continue
+            assert hip_g is not None and torch.isfinite(hip_g).all(), name
+            assert hip_g.dtype == t16_g.dtype, name
+            acc = squares.setdefault(name, [0.0, 0.0])
+            acc[0] += rel(hip_g, ref_g) ** 2
+            acc[1] += rel(t16_g, ref_g) ** 2
+    for name, (hip_sq, t16_sq) in squares.items():
+        err, t16 = math.sqrt(hip_sq / len(seeds)), math.sqrt(t16_sq / len(seeds))
+        bound = max(3e-2, 2 * t16)
+        print(f"[parity] module {preset} {overrides} d{name}: hip {err:.3e}, torch bf16 {t16:.3e} (rms over seeds)",
+              flush=True)
+        assert err <= bound, f"d{name}: rms rel {err:.3e} > {bound:.3e}"
 
 
 def test_module_and_ops_accept_misaligned_views() -> None:
