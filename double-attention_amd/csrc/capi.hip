@@ -115,7 +115,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 14; }
+int da_abi_version(void) { return 15; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -157,8 +157,9 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
 }
 
 int da_dictionary_route_backward_rows(const float* logits, const float* grad_weights, int64_t rows,
-                                      int64_t atoms, int64_t ld_in, const void* beta, int beta_dtype,
-                                      float beta_value, int flags, float silu_gain, float logit_scale, float eps,
+                                      int64_t atoms, int64_t causal_period, int64_t ld_in, const void* beta,
+                                      int beta_dtype, float beta_value, int64_t beta_count, int64_t beta_period,
+                                      int flags, float silu_gain, float logit_scale, float eps,
                                       void* grad_logits, void* weights, int64_t ld_out, int out_dtype,
                                       float* dbeta_rows, da_stream_t stream) {
   constexpr int kBwdRowsFlags = DA_ROUTE_BETA_IS_LOG | DA_ROUTE_SILU_LOGITS | DA_ROUTE_STANDARDIZE | DA_ROUTE_DIRECT_SILU;
@@ -174,12 +175,16 @@ int da_dictionary_route_backward_rows(const float* logits, const float* grad_wei
     return fail(DA_ERR_UNSUPPORTED, "route backward rows: at most %d atoms (got %lld)", da::kRouteBwdRowsMaxAtoms,
                 (long long)atoms);
   if (ld_in < atoms || ld_out < atoms) return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: row pitches < atoms");
+  if (causal_period < 0) return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: causal_period must be >= 0");
+  if (beta_count < 1 || beta_count > 64 || (beta_count > 1 && (beta_period < 1 || !beta)))
+    return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: beta_count in [1, 64] with a positive beta_period");
   if (rows == 0) return ok();
   if (!logits || !grad_weights || !grad_logits || !weights)
     return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: null pointer");
   if (beta && !any_dtype(beta_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: bad beta dtype");
   if ((rows + 3) / 4 > 0x7fffffffLL) return fail(DA_ERR_UNSUPPORTED, "route backward rows: too many rows");
-  da::RouteBwdRowsArgs a{logits, grad_weights, rows, static_cast<int>(atoms), ld_in, beta, beta_dtype, beta_value,
+  da::RouteBwdRowsArgs a{logits, grad_weights, rows, static_cast<int>(atoms), causal_period, ld_in, beta, beta_dtype,
+                         beta_value, static_cast<int>(beta_count), beta_count > 1 ? beta_period : 1,
                          flags, silu_gain, logit_scale, eps, grad_logits, weights, ld_out, out_dtype, dbeta_rows};
   da::launch_route_backward_rows(a, reinterpret_cast<hipStream_t>(stream));
   return check_launch("route backward rows");

@@ -143,10 +143,13 @@ struct RouteBwdRowsArgs {
   const float* grad_weights;  // [rows, ld_in] <dr, Dv_j>
   int64_t rows;
   int atoms;                  // M <= kRouteBwdRowsMaxAtoms
+  int64_t causal_period;      // 0, or row r keeps columns j <= r % causal_period
   int64_t ld_in;
   const void* beta_ptr;
   int beta_dtype;
   float beta_value;
+  int beta_count;             // entries of beta_ptr: row r takes (r / beta_period) % beta_count
+  int64_t beta_period;
   int flags;                  // kRouteBetaIsLog and the variant bits
   float silu_gain, logit_scale, eps;
   void* grad_logits;          // [rows, ld_out] out_dtype
@@ -157,6 +160,7 @@ struct RouteBwdRowsArgs {
 };
 constexpr int kRouteBwdRowsMaxAtoms = 4096;
 void launch_route_backward_rows(const RouteBwdRowsArgs& a, hipStream_t stream);
+
 // LayerNorm over the last dimension (dim a multiple of 8, at most 4096).
 void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight, const void* bias, int param_dtype,
                        float eps, int dtype, void* out, hipStream_t stream);

@@ -19,7 +19,9 @@
 //   SiLU activation: dl = da0 2 SiLU'(l),  SiLU'(x) = sig(x) (1 + x (1 - sig(x)))
 // One wave per row, the row's atoms strided over the lanes and held in VGPRs
 // (NPL per lane, M <= 64 NPL), so every reduction is a wave reduction and the
-// two inputs are read once, coalesced.
+// two inputs are read once, coalesced.  The outer attention's backward uses
+// the same kernel for its softmax (scores as logits, dP as dW, gamma as beta,
+// a causal row length).
 #include "da_common.h"
 #include "da_launch.h"
 #include "da_tile.h"
@@ -43,15 +45,19 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
   const int lane = lane_id();
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + uniform_wave();
   if (row >= a.rows) return;   // whole waves
-  const int M = a.atoms;
+  // With causal_period P, row r (token r % P of its sequence) keeps columns
+  // j <= r % P; the others get zero weight and gradient.
+  const int M = a.causal_period ? min(a.atoms, static_cast<int>(row % a.causal_period) + 1) : a.atoms;
   const float* lrow = a.logits + row * a.ld_in;
   const float* grow = a.grad_weights + row * a.ld_in;
   const bool silu_logits = a.flags & kRouteSiluLogits;
   const bool standardize = a.flags & kRouteStandardize;
   const bool direct = a.flags & kRouteDirectSilu;
 
+  // beta of this row: one value, or entry (row / beta_period) % beta_count.
+  const int64_t beta_index = a.beta_count > 1 ? (row / a.beta_period) % a.beta_count : 0;
   const ScalarHalves beta_bits = fetch_scalar(a.beta_ptr ? a.beta_ptr : static_cast<const void*>(a.logits),
-                                              a.beta_ptr ? a.beta_dtype : kF32, 0);
+                                              a.beta_ptr ? a.beta_dtype : kF32, a.beta_ptr ? beta_index : 0);
   float l[NPL], g[NPL];
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
@@ -150,9 +156,9 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
     const int j = lane + 64 * i;
-    if (j < M) {
-      dl_row[j] = static_cast<TO>(g[i]);
-      w_row[j] = static_cast<TO>(w[i]);
+    if (j < a.atoms) {
+      dl_row[j] = static_cast<TO>(j < M ? g[i] : 0.f);
+      w_row[j] = static_cast<TO>(j < M ? w[i] : 0.f);
     }
   }
   if (a.dbeta_rows && lane == 0) a.dbeta_rows[row] = direct ? 0.f : dbeta;

@@ -47,7 +47,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 NOALLOC_SCRATCH_BYTES = 128 << 20
 
 _vp = ctypes.c_void_p
@@ -115,8 +115,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_dictionary_route_backward_rows": (
         _i32,
         [
-            _vp, _vp, _i64, _i64, _i64,  # logits, grad_weights, rows, atoms, input pitch
-            _vp, _i32, _f32, _i32,  # beta, beta dtype, beta value, flags
+            _vp, _vp, _i64, _i64, _i64, _i64,  # logits, grad_weights, rows, atoms, causal period, input pitch
+            _vp, _i32, _f32, _i64, _i64, _i32,  # beta, beta dtype, beta value, beta count, beta period, flags
             _f32, _f32, _f32,  # silu gain, logit scale, eps
             _vp, _vp, _i64, _i32, _vp, _vp,  # grad_logits, weights, output pitch, out dtype, dbeta rows, stream
         ],

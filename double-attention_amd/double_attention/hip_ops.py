@@ -18,10 +18,12 @@ handed to the library as a raw pointer; kernels run on
 ``torch.cuda.current_stream()``.  Nothing here falls back to another
 implementation: an unsupported shape or variant raises.
 
-Autograd: the kernels are forward-only.  When gradients are required the
-forward still runs on the HIP path and the backward recomputes the
-PyTorch reference composition (``ops.py``) on the same device, the pattern
-the reference itself used before it had native backward kernels.
+Autograd: the route and the outer attention have native backwards
+(``route_gradients``, ``attention_gradients``): the attention backward
+kernels, or library GEMMs around the row kernel of the assignment's
+backward.  Shapes neither covers (more than 4096 atoms, a row kernel width
+it lacks) recompute the PyTorch reference composition (``ops.py``) on the
+same device under autograd.
 """
 
 from __future__ import annotations
@@ -326,6 +328,7 @@ def _route_backward(
     normalize_input: bool,
     normalize_output: bool,
     grad: Tensor,
+    r: Tensor | None = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients of the softmax route (``ops.py:16-62``) on the attention backward kernels.
 
@@ -344,16 +347,23 @@ def _route_backward(
     device = x.device
     rows = x.detach().reshape(-1, routing_dim).float()
     n = rows.shape[0]
+    # The forward kernel's operands: unit rows rounded once to fp16 with fp16
+    # keys; raw 16-bit rows in their own dtype with keys in that dtype (the
+    # backward kernels recompute P from the same values the forward used).
     if normalize_input:
         x_norm = rows.norm(dim=1, keepdim=True)
         u = rows / x_norm.clamp_min(eps)
+        qk_type = torch.float16
     else:
         u = rows
-    u16 = _aligned(u.to(torch.float16))
-    # r without the output norm, from the fp16 rows on fp16 keys.
-    layout16 = route_layout(dictionary_key.detach(), dictionary_value.detach(), torch.float16)
+        qk_type = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
+    u16 = _aligned(u.to(qk_type))
     beta_t = beta.detach().float().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
-    r = _route_forward(u16, layout16, beta_t, eps, False, False, RouteVariant()).float()
+    # r from those rows and keys: the forward's own r, else one route launch.
+    if r is None:
+        layout16 = route_layout(dictionary_key.detach(), dictionary_value.detach(), qk_type)
+        r = _route_forward(u16, layout16, beta_t, eps, False, False, RouteVariant())
+    r = r.reshape(-1, routing_dim).float()
     g = grad.detach().reshape(-1, routing_dim).float()
     if normalize_output:
         r_norm = r.norm(dim=1, keepdim=True)
@@ -361,7 +371,7 @@ def _route_backward(
         dr = torch.where(r_norm > eps, (g - z * (z * g).sum(1, keepdim=True)) / r_norm.clamp_min(eps), g / eps)
     else:
         dr = g
-    keys = _aligned(dictionary_key.detach().t().to(torch.float16))
+    keys = _aligned(dictionary_key.detach().t().to(qk_type))
     # Values, r and dr in fp16 for fp16 inputs (8x finer than bf16: with the
     # output norm, rowsum(dr . r) is analytically zero and its rounding noise
     # reaches every atom's gradient), bf16 for bf16 inputs.
@@ -379,7 +389,7 @@ def _route_backward(
     _lib.check(
         lib.da_routed_attention_backward(
             u16.data_ptr(), keys.data_ptr(), values.data_ptr(), out.data_ptr(), go.data_ptr(), beta_t.data_ptr(),
-            1, 1, n, atoms, routing_dim, routing_dim, 0, _lib.DA_F16, _half_code(v_type),
+            1, 1, n, atoms, routing_dim, routing_dim, 0, _half_code(qk_type), _half_code(v_type),
             workspace.data_ptr(), ws_bytes, du.data_ptr(), dkt.data_ptr(), dvt.data_ptr(), dbeta.data_ptr(),
             _stream(device),
         ),
@@ -427,6 +437,7 @@ def _route_backward_rows(
     normalize_output: bool,
     grad: Tensor,
     variant: RouteVariant,
+    r: Tensor | None = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients of the route (``ops.py:16-62``) for every variant and width.
 
@@ -436,9 +447,10 @@ def _route_backward_rows(
     turns them into the gradient at the logits and the assignment weights,
     and three GEMMs give dN_in(x), dDk and dDv.  The logits use the forward
     kernel's operands (unit rows rounded once to fp16 with fp16 keys; raw rows
-    in their own dtype); r, the reconstruction before the output norm, comes
-    from one route launch.  Returns gradients in the dtypes of ``x`` and the
-    dictionary tensors, and d beta as a 1-element fp32 tensor.
+    in their own dtype); r, the reconstruction before the output norm, is the
+    forward's (``r``) or comes from one route launch.  Returns gradients in
+    the dtypes of ``x`` and the dictionary tensors, and d beta as a 1-element
+    fp32 tensor.
     """
 
     routing_dim = x.shape[-1]
@@ -455,9 +467,11 @@ def _route_backward_rows(
         u = rows
         key_type = x.dtype
         u_h = _aligned(x.detach().reshape(-1, routing_dim))
-    layout = route_layout(dictionary_key.detach(), dictionary_value.detach(), key_type)
     beta_t = beta.detach().float().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
-    r = _route_forward(u_h, layout, beta_t, eps, False, False, variant).float()
+    if r is None:
+        layout = route_layout(dictionary_key.detach(), dictionary_value.detach(), key_type)
+        r = _route_forward(u_h, layout, beta_t, eps, False, False, variant)
+    r = r.reshape(-1, routing_dim).float()
     g = grad.detach().reshape(-1, routing_dim).float()
     if normalize_output:
         r_norm = r.norm(dim=1, keepdim=True)
@@ -466,32 +480,31 @@ def _route_backward_rows(
     else:
         dr = g
     # 16-bit operands of the GEMMs: fp16 for fp16 inputs, bf16 for bf16 ones.
+    # dW = dr Dv takes dr as a 16-bit head and its rounding residual ([n, 2R]
+    # against [Dv; Dv]): the softmax backward differences dW_j - sum_k w_k dW_k,
+    # so one 16-bit rounding of dr would reach every atom's gradient.
     v_type = torch.float16 if x.dtype == torch.float16 else torch.bfloat16
     keys_h = dictionary_key.detach().to(key_type)
     logits = _mm_f32(u_h, keys_h)
     dr_v = dr.to(v_type)
     values_v = dictionary_value.detach().to(v_type)
-    # dW = dr Dv with dr split into two 16-bit terms (head + rounding
-    # residual): the softmax backward differences dW_j - sum_k w_k dW_k, so
-    # one 16-bit rounding of dr would reach every atom's gradient.
-    grad_weights = _mm_f32(dr_v, values_v)
-    grad_weights += _mm_f32((dr - dr_v.float()).to(v_type), values_v)
+    grad_weights = _mm_f32(torch.cat((dr_v, (dr - dr_v.float()).to(v_type)), dim=1), torch.cat((values_v, values_v)))
     grad_logits = torch.empty(n, atoms, dtype=v_type, device=device)
     weights = torch.empty(n, atoms, dtype=v_type, device=device)
     dbeta_rows = torch.empty(n, dtype=torch.float32, device=device)
     lib = _lib.get()
     _lib.check(
         lib.da_dictionary_route_backward_rows(
-            logits.data_ptr(), grad_weights.data_ptr(), n, atoms, atoms,
-            beta_t.data_ptr(), _lib.DA_F32, 0.0, variant.flags(),
+            logits.data_ptr(), grad_weights.data_ptr(), n, atoms, 0, atoms,
+            beta_t.data_ptr(), _lib.DA_F32, 0.0, 1, 1, variant.flags(),
             float(variant.silu_gain), float(variant.logit_scale(routing_dim)), float(eps),
             grad_logits.data_ptr(), weights.data_ptr(), atoms, _half_code(v_type), dbeta_rows.data_ptr(),
             _stream(device),
         ),
         "dictionary_route_hip backward rows",
     )
-    keys_v = dictionary_key.detach().to(v_type)
-    du = _mm_f32(grad_logits, keys_v.t())
+    keys_vt = dictionary_key.detach().to(v_type).t().contiguous()
+    du = _mm_f32(grad_logits, keys_vt)
     d_key = _mm_f32(u.to(v_type).t(), grad_logits)
     d_value = _mm_f32(dr_v.t(), weights)
     dbeta = dbeta_rows.sum().reshape(1)
@@ -518,21 +531,26 @@ def route_gradients(
     variant: RouteVariant,
     grad: Tensor,
     needs: tuple[bool, bool, bool, bool] = (True, True, True, True),
+    r: Tensor | None = None,
 ) -> tuple[Tensor | None, Tensor | None, Tensor | None, Tensor | None]:
     """(dx, dDk, dDv, dbeta) of the route for ``d loss / d out = grad``.
 
     The attention backward kernels take the plain softmax route up to
     256-wide rows; the row kernel with library GEMMs takes every width and
     variant up to 4096 atoms; beyond that autograd recomputes the torch route.
-    ``needs`` marks the wanted gradients (dbeta only for a tensor beta).
+    ``needs`` marks the wanted gradients (dbeta only for a tensor beta); ``r``
+    is the forward's reconstruction before the output norm, when the caller
+    kept it (else one route launch forms it again).
     """
 
     native = None
     if _route_backward_supported(x, dictionary_key, variant):
-        native = _route_backward(x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad)
+        native = _route_backward(
+            x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, r
+        )
     elif _route_backward_rows_supported(x, dictionary_key):
         native = _route_backward_rows(
-            x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, variant
+            x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, variant, r
         )
     if native is not None:
         dx, ddk, ddv, dbeta = native
@@ -767,14 +785,88 @@ def _native_backward_supported(query: Tensor, value: Tensor) -> bool:
     return score_dim <= BACKWARD_SCORE_WIDTHS[-1] and batch * maps <= 65535 and value.shape[-1] <= SUPPORTED_WIDTHS[-1]
 
 
+# 512-wide scores whose score matrices fit (B*S*T*T fp32 <= 512 MiB, T <= the
+# row kernel's 4096 columns) take the dense backward: there the flash
+# backward splits each key tile over two workgroups and forms S and dP twice.
+DENSE_BACKWARD_MIN_SCORE_DIM = 512
+DENSE_BACKWARD_MAX_SCORES = 1 << 27
+
+
+def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
+    batch, maps, length, score_dim = query.shape
+    return (
+        score_dim >= DENSE_BACKWARD_MIN_SCORE_DIM
+        and score_dim <= BACKWARD_SCORE_WIDTHS[-1]
+        and value.shape[-1] <= SUPPORTED_WIDTHS[-1]
+        and 1 <= length <= ROUTE_BACKWARD_ROWS_MAX_ATOMS
+        and batch * maps * length * length <= DENSE_BACKWARD_MAX_SCORES
+        and maps <= 64
+    )
+
+
+def _attention_backward_dense(
+    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, grad: Tensor, causal: bool
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Outer-attention gradients with the score matrices materialized.
+
+    Library GEMMs form S = q k^T and dP = dO V^T (fp32 results) per
+    (sequence, map); ``da_dictionary_route_backward_rows`` turns each row into
+    P and gamma P (dP - sum P dP) (the gradient at q . k) with the causal row
+    length and the map's gamma, plus the row's term of d gamma; GEMMs then
+    give dq = dS k, dk = dS^T q and dV = sum over maps of P^T dO.  The row
+    sum uses P and dP themselves, no saved output.
+    """
+
+    batch, maps, length, score_dim = query.shape
+    model_dim = value.shape[-1]
+    rows = batch * maps
+    device = value.device
+    v_type = value.dtype if value.dtype in (torch.float16, torch.bfloat16) else torch.bfloat16
+    q = query.detach().reshape(rows, length, score_dim).contiguous()
+    k = key.detach().reshape(rows, length, score_dim).contiguous()
+    # Right operands of the products are contiguous (no transposed views).
+    scores = torch.bmm(q, k.transpose(1, 2).contiguous(), out_dtype=torch.float32)
+    go = grad.detach().reshape(rows, length, model_dim).to(v_type).contiguous()
+    vt = value.detach().to(v_type).transpose(1, 2).contiguous()
+    if maps > 1:
+        vt = vt.unsqueeze(1).expand(batch, maps, model_dim, length).reshape(rows, model_dim, length)
+    grad_p = torch.bmm(go, vt, out_dtype=torch.float32)
+    grad_s = torch.empty(rows, length, length, dtype=v_type, device=device)
+    probs = torch.empty_like(grad_s)
+    dgamma_rows = torch.empty(rows * length, dtype=torch.float32, device=device)
+    gamma = scales.detach().float().contiguous()
+    lib = _lib.get()
+    _lib.check(
+        lib.da_dictionary_route_backward_rows(
+            scores.data_ptr(), grad_p.data_ptr(), rows * length, length, length if causal else 0, length,
+            gamma.data_ptr(), _lib.DA_F32, 0.0, maps, length, 0, 1.0, 1.0, 0.0,
+            grad_s.data_ptr(), probs.data_ptr(), length, _half_code(v_type), dgamma_rows.data_ptr(),
+            _stream(device),
+        ),
+        "routed_attention_hip dense backward",
+    )
+    del scores, grad_p
+    dq = torch.bmm(grad_s, k.to(v_type), out_dtype=torch.float32)
+    dk = torch.bmm(grad_s.transpose(1, 2), q.to(v_type), out_dtype=torch.float32)
+    dv = torch.bmm(probs.transpose(1, 2), go, out_dtype=torch.float32)
+    dv = dv.view(batch, maps, length, model_dim).sum(1)
+    dgamma = dgamma_rows.view(batch, maps, length).sum(dim=(0, 2))
+    shape = (batch, maps, length, score_dim)
+    return dq.view(shape).to(query.dtype), dk.view(shape).to(key.dtype), dv.to(value.dtype), dgamma.to(scales.dtype)
+
+
 def attention_gradients(
     query: Tensor, key: Tensor, value: Tensor, scales: Tensor, out: Tensor, grad: Tensor, causal: bool,
     needs: tuple[bool, bool, bool, bool] = (True, True, True, True),
 ) -> tuple[Tensor | None, Tensor | None, Tensor | None, Tensor | None]:
     """(dq, dk, dv, dscales) of the outer attention whose output was ``out``:
-    the native backward kernels, or autograd of the fp32-softmax reference
-    for score widths above 512."""
+    the dense backward for 512-wide scores whose matrices fit, the flash
+    backward kernels otherwise, or autograd of the fp32-softmax reference for
+    score widths above 512."""
 
+    if query.numel() and value.numel() and _dense_backward_fits(query, value):
+        grads = _attention_backward_dense(query, key, value, scales, grad, causal)
+        return tuple(g if need else None for g, need in zip(grads, needs))  # type: ignore[return-value]
     if _native_backward_supported(query, value) and query.numel() and value.numel():
         grads = _attention_backward(query, key, value, scales, out, grad, causal)
         return tuple(g if need else None for g, need in zip(grads, needs))  # type: ignore[return-value]

@@ -453,12 +453,18 @@ class _HipModuleFunction(torch.autograd.Function):
         layout = hip_ops.route_layout(dictionary_key, dictionary_value, key_dtype)
         variant = hip_ops.RouteVariant.of_config(cfg)
         beta = module.beta.detach()
-        # Q and K rows route together, as [B, T, 2, H, R] rows; fp16 out (the
-        # attention's operand type for bounded rows).
-        routed = hip_ops._route_forward(
-            qk.view(-1, routing_dim), layout, beta, cfg.eps, cfg.normalize_routing_input,
-            cfg.normalize_routing_output, variant, out_dtype=torch.float16,
+        # Q and K rows route together, as [B, T, 2, H, R] rows, fp16 out (the
+        # attention's operand type for bounded rows).  The route stops before
+        # its output norm: the backward needs that reconstruction r, and the
+        # norm is one row normalization here.
+        recon = hip_ops._route_forward(
+            qk.view(-1, routing_dim), layout, beta, cfg.eps, cfg.normalize_routing_input, False, variant,
+            out_dtype=torch.float16,
         )
+        if cfg.normalize_routing_output:
+            routed = F.normalize(recon.float(), dim=-1, eps=cfg.eps).to(torch.float16)
+        else:
+            routed = recon
         score_query, score_key = _HipModuleFunction._score_maps(routed, batch, length, branches, maps, routing_dim)
         scales = score_scale_from_log(module.log_score_scales.detach()).float()
         group = branches // maps if branches > maps else 1
@@ -486,8 +492,8 @@ class _HipModuleFunction(torch.autograd.Function):
         ctx.dtype = dtype
         ctx.param_names = [name for name, _ in module.named_parameters()]
         ctx.x_dtype = x.dtype
-        ctx.save_for_backward(xc, qk, routed, map_output, mixed, vt, scales, beta, dictionary_key, dictionary_value,
-                              factors if factors is not None else torch.empty(0), *params)
+        ctx.save_for_backward(xc, qk, recon, routed, map_output, mixed, vt, scales, beta, dictionary_key,
+                              dictionary_value, factors if factors is not None else torch.empty(0), *params)
         return out
 
     @staticmethod
@@ -503,7 +509,7 @@ class _HipModuleFunction(torch.autograd.Function):
         module = ctx.module
         cfg = module.config
         dtype = ctx.dtype
-        xc, qk, routed, map_output, mixed, vt, scales, beta, dk, dv, factors, *params = ctx.saved_tensors
+        xc, qk, recon, routed, map_output, mixed, vt, scales, beta, dk, dv, factors, *params = ctx.saved_tensors
         named = dict(zip(ctx.param_names, params))
         batch, length, model_dim = xc.shape
         branches, maps, routing_dim = cfg.qk_branches, cfg.outer_maps, cfg.routing_dim
@@ -565,7 +571,7 @@ class _HipModuleFunction(torch.autograd.Function):
         d_rows, d_key, d_val, d_beta = hip_ops.route_gradients(
             qk.view(-1, routing_dim), dk, dv, beta, cfg.eps, cfg.normalize_routing_input,
             cfg.normalize_routing_output, variant, d_routed,
-            (True, ctx.needs_input_grad[3], ctx.needs_input_grad[4], wants("log_beta")),
+            (True, ctx.needs_input_grad[3], ctx.needs_input_grad[4], wants("log_beta")), recon,
         )
         if wants("log_beta") and d_beta is not None:
             log_beta = named["log_beta"].detach()

@@ -153,13 +153,19 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  * Writes, per row, the gradient at the raw logits (grad_logits) and the
  * assignment weights (weights), rows x atoms with pitch ld_out in out_dtype
  * (DA_F16 or DA_BF16), and the row's share of d beta to dbeta_rows[row]
- * (fp32; 0 for DA_ROUTE_DIRECT_SILU; may be NULL).  atoms <= 4096.  The GEMMs
+ * (fp32; 0 for DA_ROUTE_DIRECT_SILU; may be NULL).  atoms <= 4096.
+ * causal_period > 0 limits row r to columns j <= r % causal_period (zeros
+ * written past them), and beta may hold beta_count (<= 64) values, row r
+ * taking entry (r / beta_period) % beta_count: the outer attention's softmax
+ * backward, with scores as logits, dP = dO V^T as grad_weights and the maps'
+ * gammas as beta (rows ordered batch, map, token).  The GEMMs
  * around it (logits, grad_weights, then dN_in(x) = grad_logits Dk^T,
  * dDk = N_in(x)^T grad_logits, dDv = dr^T weights) are plain library GEMMs.
  */
 int da_dictionary_route_backward_rows(const float* logits, const float* grad_weights, int64_t rows,
-                                      int64_t atoms, int64_t ld_in, const void* beta, int beta_dtype,
-                                      float beta_value, int flags, float silu_gain, float logit_scale, float eps,
+                                      int64_t atoms, int64_t causal_period, int64_t ld_in, const void* beta,
+                                      int beta_dtype, float beta_value, int64_t beta_count, int64_t beta_period,
+                                      int flags, float silu_gain, float logit_scale, float eps,
                                       void* grad_logits, void* weights, int64_t ld_out, int out_dtype,
                                       float* dbeta_rows, da_stream_t stream);
 

@@ -213,8 +213,9 @@ def test_route_backward_rows_rejects_bad_arguments() -> None:
     buf = ctypes.c_void_p(16)   # never dereferenced
 
     def call(**kw):
-        args = dict(logits=buf, grad_weights=buf, rows=10, atoms=100, ld_in=100, beta=None, beta_dtype=lib.DA_F32,
-                    beta_value=1.0, flags=0, silu_gain=1.0, logit_scale=1.0, eps=1e-6, grad_logits=buf, weights=buf,
+        args = dict(logits=buf, grad_weights=buf, rows=10, atoms=100, causal_period=0, ld_in=100, beta=None,
+                    beta_dtype=lib.DA_F32,
+                    beta_value=1.0, beta_count=1, beta_period=1, flags=0, silu_gain=1.0, logit_scale=1.0, eps=1e-6, grad_logits=buf, weights=buf,
                     ld_out=100, out_dtype=lib.DA_BF16, dbeta_rows=None, stream=None)
         args.update(kw)
         return h.da_dictionary_route_backward_rows(*args.values())
@@ -226,6 +227,9 @@ def test_route_backward_rows_rejects_bad_arguments() -> None:
     assert call(flags=lib.DA_ROUTE_DIRECT_SILU, silu_gain=0.0) == -1
     assert call(flags=lib.DA_ROUTE_STANDARDIZE, logit_scale=-1.0) == -1
     assert call(logits=None) == -1
-    assert b"atoms" in h.da_last_error() or b"null" in h.da_last_error()
+    assert b"null" in h.da_last_error()
+    assert call(causal_period=-1) == -1
+    assert call(beta_count=3, beta_period=0) == -1
+    assert b"beta_count" in h.da_last_error()
     assert call(rows=0, logits=None) == 0               # nothing to do
 

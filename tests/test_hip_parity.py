@@ -350,6 +350,10 @@ BACKWARD_CASES = [
     (1, 2, 1, 64, 64, True),
     (2, 2, 150, 512, 512, True),
     (1, 1, 70, 400, 128, False),
+    # 512-wide scores take the dense backward (library GEMMs around the row kernel).
+    (1, 3, 100, 512, 256, True),
+    (2, 1, 64, 512, 128, False),
+    (1, 1, 1, 512, 64, True),
 ]
 
 
@@ -577,12 +581,13 @@ def test_lm_c4_qk2_s2_tied(dtype) -> None:
 def test_lm_training_gradients(monkeypatch) -> None:
     # One training step of a two-layer tied LM (the C4 preset) with the HIP
     # backend: the attention layers' route and outer attention run the native
-    # backward kernels; every gradient's relative error against fp32, as a root
-    # mean square over three seeds, is held to max(3e-2, 2x) that of the same
-    # LM on the bf16 torch path.  One seed is not enough: the map-mix logits'
+    # backward kernels; every gradient's relative error against fp32, pooled
+    # over eight seeds (all seeds' error norm over their gradient norm), is
+    # held to max(3e-2, 2x) that of the same LM on the bf16 torch path.  One seed is not enough: the map-mix logits'
     # gradient a_s (g_s - sum a g) differences two per-map sums g_s that agree
     # to ~0.5%, so a 4e-4 error in g_s is a ~10% error in the gradient, and the
-    # bf16 torch path's error there ranges over 4%..80% from seed to seed.
+    # bf16 torch path's error there ranges over 4%..80% from seed to seed; the
+    # score-scale gradients are sums that cancel in the same way.
     device = _device()
     config = da.experiment_config("qk2-s2", untied_dictionary=False, backend="hip")
     kwargs = dict(dictionary_group_size=2, feedforward_dim=1536)
@@ -599,7 +604,7 @@ def test_lm_training_gradients(monkeypatch) -> None:
     def rel(a, b):
         return float((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-30))
 
-    seeds = (3, 5, 7)
+    seeds = tuple(range(3, 19, 2))
     squares: dict[str, list[float]] = {}
     for seed in seeds:
         torch.manual_seed(seed)
@@ -624,19 +629,20 @@ def test_lm_training_gradients(monkeypatch) -> None:
             if p_ref.grad is None:
                 continue
             assert p_hip.grad is not None and torch.isfinite(p_hip.grad).all(), name
-            acc = squares.setdefault(name, [0.0, 0.0])
-            acc[0] += rel(p_hip.grad, p_ref.grad) ** 2
-            acc[1] += rel(p_t16.grad, p_ref.grad) ** 2
+            acc = squares.setdefault(name, [0.0, 0.0, 0.0])
+            acc[0] += float((p_hip.grad.float() - p_ref.grad.float()).square().sum())
+            acc[1] += float((p_t16.grad.float() - p_ref.grad.float()).square().sum())
+            acc[2] += float(p_ref.grad.float().square().sum())
     results = []
-    for name, (hip_sq, t16_sq) in squares.items():
-        err = math.sqrt(hip_sq / len(seeds))
-        bound = max(3e-2, 2 * math.sqrt(t16_sq / len(seeds)))
+    for name, (hip_sq, t16_sq, ref_sq) in squares.items():
+        err = math.sqrt(hip_sq / max(ref_sq, 1e-60))
+        bound = max(3e-2, 2 * math.sqrt(t16_sq / max(ref_sq, 1e-60)))
         results.append((err / bound, name, err, bound))
     results.sort(reverse=True)
     for ratio, name, err, bound in results[:4]:
-        print(f"[parity] lm training d{name}: rms rel {err:.3e}, bound {bound:.3e} (ratio {ratio:.2f})", flush=True)
+        print(f"[parity] lm training d{name}: pooled rel {err:.3e}, bound {bound:.3e} (ratio {ratio:.2f})", flush=True)
     for ratio, name, err, bound in results:
-        assert err <= bound, f"d{name}: rms rel {err:.3e} > {bound:.3e}"
+        assert err <= bound, f"d{name}: pooled rel {err:.3e} > {bound:.3e}"
 
 
 @pytest.mark.parametrize("preset", ["a1-d1536-qffn", "a1-r512-d1536-qffn"])
@@ -735,7 +741,8 @@ def test_module_backward_runs_native_kernels(monkeypatch, preset, overrides, tok
     device = _device()
     config = da.experiment_config(preset, backend="hip", **overrides)
     calls = []
-    for fn in ("_attention_backward", "_route_backward", "_route_backward_rows", "_route_forward"):
+    for fn in ("_attention_backward", "_attention_backward_dense", "_route_backward", "_route_backward_rows",
+               "_route_forward"):
         original = getattr(da.hip_ops, fn)
 
         def counted(*args, _original=original, _name=fn, **kwargs):
@@ -766,10 +773,10 @@ def test_module_backward_runs_native_kernels(monkeypatch, preset, overrides, tok
             (m(xi).float() * w).sum().backward()
             grads.append([xi.grad] + [p.grad for p in m.parameters()])
         # One attention backward and one native route backward; the only
-        # route forwards are the module forward's and the route backward's r.
-        assert calls.count("_attention_backward") == 1, calls
+        # route launch is the module forward's (the backward reuses its r).
+        assert calls.count("_attention_backward") + calls.count("_attention_backward_dense") == 1, calls
         assert calls.count("_route_backward") + calls.count("_route_backward_rows") == 1, calls
-        assert calls.count("_route_forward") == 2, calls
+        assert calls.count("_route_forward") == 1, calls
         names = ["x"] + [n for n, _ in module.named_parameters()]
         for name, hip_g, t16_g, ref_g in zip(names, *grads):
             if ref_g is None:   # a parameter the torch path leaves unused
@@ -777,15 +784,19 @@ def test_module_backward_runs_native_kernels(monkeypatch, preset, overrides, tok
                 continue
             assert hip_g is not None and torch.isfinite(hip_g).all(), name
             assert hip_g.dtype == t16_g.dtype, name
-            acc = squares.setdefault(name, [0.0, 0.0])
-            acc[0] += rel(hip_g, ref_g) ** 2
-            acc[1] += rel(t16_g, ref_g) ** 2
-    for name, (hip_sq, t16_sq) in squares.items():
-        err, t16 = math.sqrt(hip_sq / len(seeds)), math.sqrt(t16_sq / len(seeds))
+            acc = squares.setdefault(name, [0.0, 0.0, 0.0])
+            acc[0] += float((hip_g.float() - ref_g.float()).square().sum())
+            acc[1] += float((t16_g.float() - ref_g.float()).square().sum())
+            acc[2] += float(ref_g.float().square().sum())
+    for name, (hip_sq, t16_sq, ref_sq) in squares.items():
+        # Pooled over the seeds: the error norm of all seeds' gradients over
+        # their norm, so a seed whose gradient nearly cancels to zero does not
+        # dominate.
+        err, t16 = math.sqrt(hip_sq / max(ref_sq, 1e-60)), math.sqrt(t16_sq / max(ref_sq, 1e-60))
         bound = max(3e-2, 2 * t16)
-        print(f"[parity] module {preset} {overrides} d{name}: hip {err:.3e}, torch bf16 {t16:.3e} (rms over seeds)",
+        print(f"[parity] module {preset} {overrides} d{name}: hip {err:.3e}, torch bf16 {t16:.3e} (pooled over seeds)",
               flush=True)
-        assert err <= bound, f"d{name}: rms rel {err:.3e} > {bound:.3e}"
+        assert err <= bound, f"d{name}: pooled rel {err:.3e} > {bound:.3e}"
 
 
 def test_module_and_ops_accept_misaligned_views() -> None:
