@@ -115,7 +115,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 15; }
+int da_abi_version(void) { return 16; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -138,6 +138,24 @@ int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_
                                   static_cast<int>(atoms), eps, key_t, key_dtype, value, value_rows,
                                   reinterpret_cast<hipStream_t>(stream));
   return check_launch("normalize");
+}
+
+int da_dictionary_normalize_backward(const void* raw_key, const void* raw_value, int raw_dtype,
+                                     int64_t routing_dim, int64_t atoms, float eps, const float* grad_key,
+                                     const float* grad_value, void* d_raw_key, void* d_raw_value,
+                                     da_stream_t stream) {
+  if (!any_dtype(raw_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: bad dtype");
+  if (routing_dim < 1 || routing_dim > (1 << 16))
+    return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: routing_dim %lld out of range", (long long)routing_dim);
+  if (atoms < 1 || atoms > (1 << 24)) return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: bad atom count");
+  if (!(eps >= 0.f)) return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: eps must be >= 0");
+  if (!raw_key || !grad_key || !d_raw_key) return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: null pointer");
+  if (!raw_value && d_raw_value)
+    return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: d_raw_value given for a tied bank");
+  const da::NormBwdArgs a{raw_key, raw_value, raw_dtype, static_cast<int>(routing_dim), atoms, eps,
+                          grad_key, grad_value, d_raw_key, d_raw_value};
+  da::launch_dictionary_normalize_backward(a, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("normalize backward");
 }
 
 int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_t x_row_stride,

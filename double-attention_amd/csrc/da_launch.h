@@ -136,6 +136,16 @@ void launch_dictionary_normalize(const void* raw_key, const void* raw_value, int
                                  int M, float eps, void* key_t, int key_dtype, void* value,
                                  void* value_rows, hipStream_t stream);
 void launch_dictionary_route(const RouteArgs& a, hipStream_t stream);
+// Backward of the column normalization (dict_norm.hip).  Banks [R, M]
+// row-major of one dtype; gradients fp32 [R, M]; raw_value NULL = tied bank
+// (the key gradient plus grad_value, when given, flows into d_key).
+struct NormBwdArgs {
+  const void* raw_key; const void* raw_value; int dtype;
+  int R; int64_t M; float eps;
+  const float* grad_key; const float* grad_value;
+  void* d_key; void* d_value;
+};
+void launch_dictionary_normalize_backward(const NormBwdArgs& a, hipStream_t stream);
 
 // Row-wise backward of the route's assignment (route_bwd.hip).
 struct RouteBwdRowsArgs {

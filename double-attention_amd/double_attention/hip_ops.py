@@ -167,6 +167,55 @@ def dictionary_normalize_hip(
     return _tag(key_t[:atoms].t(), value_rows[:, :atoms], layout)
 
 
+def dictionary_normalize_backward_hip(
+    raw_key: Tensor,
+    raw_value: Tensor | None,
+    grad_key: Tensor | None,
+    grad_value: Tensor | None,
+    eps: float = 1e-6,
+) -> tuple[Tensor, Tensor | None]:
+    """Gradients at the raw bank of ``SharedDictionaryBank.normalized``
+    (``modules.py:45-48`` under autograd) in one launch.
+
+    ``grad_key`` / ``grad_value`` are the gradients at the normalized key and
+    value atoms (``[R, M]``; None = zero); a tied bank (``raw_value`` None)
+    takes both into its key atoms.  Returns ``(d_raw_key, d_raw_value)`` in
+    the raw dtype (``d_raw_value`` None for a tied bank).
+    """
+
+    if raw_key.ndim != 2:
+        raise ValueError("raw_key must be [routing_dim, atoms]")
+    if raw_value is not None and raw_value.shape != raw_key.shape:
+        raise ValueError("raw_value must match raw_key")
+    _require_cuda(raw_key)
+    routing_dim, atoms = raw_key.shape
+    device = raw_key.device
+    if grad_key is None:
+        grad_key = torch.zeros(routing_dim, atoms, dtype=torch.float32, device=device)
+
+    def as_grad(g: Tensor | None) -> Tensor | None:
+        if g is None:
+            return None
+        if g.shape != raw_key.shape:
+            raise ValueError("bank gradients must be [routing_dim, atoms]")
+        return g.detach().to(torch.float32).contiguous()
+
+    key_c = raw_key.detach().contiguous()
+    value_c = None if raw_value is None else raw_value.detach().to(key_c.dtype).contiguous()
+    gk, gv = as_grad(grad_key), as_grad(grad_value)
+    d_key = torch.empty_like(key_c)
+    d_value = None if value_c is None else torch.empty_like(value_c)
+    lib = _lib.get()
+    _lib.check(
+        lib.da_dictionary_normalize_backward(
+            key_c.data_ptr(), _ptr(value_c), dtype_code(key_c.dtype), routing_dim, atoms, float(eps),
+            gk.data_ptr(), _ptr(gv), d_key.data_ptr(), _ptr(d_value), _stream(device),
+        ),
+        "dictionary_normalize_hip backward",
+    )
+    return d_key, d_value
+
+
 def _untile_value(value: Tensor) -> Tensor:
     """``[Mp / 32, R, 32]`` value tiles -> ``[R, Mp]``."""
 
@@ -302,10 +351,9 @@ def _route_forward(
 
 
 # Routing widths whose route backward runs on the attention backward kernels.
-# Up to 256 it takes about the time of the torch recompute and keeps fp32
+# Up to 256 they take about the time of the GEMM path and keep fp32
 # accumulation throughout; at 512-wide rows the two-workgroup split recomputes
-# S and dP per half and the torch path's dense GEMMs are faster (C3: 3.1
-# against 2.2 ms per module step), so 512 stays on the torch recompute.
+# S and dP per half, and the GEMM path around the row kernel is faster.
 ROUTE_BACKWARD_WIDTHS = (64, 128, 256)
 
 
@@ -319,6 +367,32 @@ def _route_backward_supported(x: Tensor, dictionary_key: Tensor, variant: RouteV
     )
 
 
+def _row_norm(rows: Tensor) -> Tensor:
+    """Per-row L2 norms ``[n, 1]`` in fp32 (one pass over 16-bit or fp32 rows)."""
+
+    return torch.linalg.vector_norm(rows, dim=1, keepdim=True, dtype=torch.float32)
+
+
+def _scaled_rows(rows: Tensor, factor: Tensor, dtype: torch.dtype) -> Tensor:
+    """``rows * factor`` ([n, R] by [n, 1]) computed in fp32, rounded once to ``dtype``."""
+
+    return torch.mul(rows, factor, out=torch.empty(rows.shape, dtype=dtype, device=rows.device))
+
+
+def _normalize_backward(v: Tensor, norm: Tensor, h: Tensor, eps: float, dtype: torch.dtype) -> Tensor:
+    """The backward of N(v) = v / max(|v|, eps) (``F.normalize``) at gradient h.
+
+    (h - n <n, h>) / |v| with n = v / |v| where |v| > eps, h / eps elsewhere;
+    written as h i - v (<v, h> i^3 [|v| > eps]) with i = 1 / max(|v|, eps), in
+    fp32 and rounded once to ``dtype``.  ``norm`` is |v| as ``[n, 1]`` fp32.
+    """
+
+    inv = norm.clamp_min(eps).reciprocal()
+    coef = (v * h).sum(1, keepdim=True) * torch.where(norm > eps, inv.pow(3), 0.0)
+    out = torch.empty(h.shape, dtype=dtype, device=h.device)
+    return torch.addcmul(h * inv, v, coef, value=-1.0, out=out)
+
+
 def _route_backward(
     x: Tensor,
     dictionary_key: Tensor,
@@ -329,56 +403,53 @@ def _route_backward(
     normalize_output: bool,
     grad: Tensor,
     r: Tensor | None = None,
+    bank_grad_dtype: torch.dtype | None = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients of the softmax route (``ops.py:16-62``) on the attention backward kernels.
 
     The route is one attention per row: the (normalized) row u is the query,
     the key atoms the keys, the value atoms the values, beta the score scale
     and r = softmax(beta u Dk) Dv^T the output, then z = r / max(|r|, eps).
-    The host forms u, r (one route launch without the output norm) and the
-    output-norm backward dr; ``da_routed_attention_backward`` with the atoms
-    as a key sequence of their own returns du, dDk, dDv and dbeta; the
-    input-norm backward gives dx.  Returns fp32-accumulated gradients in the
-    dtypes of ``x`` and the dictionary tensors.
+    The host forms u, r (the forward's, or one route launch without the
+    output norm) and the output-norm backward dr; ``da_routed_attention_backward``
+    with the atoms as a key sequence of their own returns du, dDk, dDv and
+    dbeta; the input-norm backward gives dx.  Returns fp32-accumulated
+    gradients in the dtypes of ``x`` and the dictionary tensors (or
+    ``bank_grad_dtype`` for the two bank gradients).
     """
 
     routing_dim = x.shape[-1]
     atoms = dictionary_key.shape[1]
     device = x.device
-    rows = x.detach().reshape(-1, routing_dim).float()
+    rows = _aligned(x.detach().reshape(-1, routing_dim))
     n = rows.shape[0]
     # The forward kernel's operands: unit rows rounded once to fp16 with fp16
     # keys; raw 16-bit rows in their own dtype with keys in that dtype (the
     # backward kernels recompute P from the same values the forward used).
     if normalize_input:
-        x_norm = rows.norm(dim=1, keepdim=True)
-        u = rows / x_norm.clamp_min(eps)
+        x_norm = _row_norm(rows)
         qk_type = torch.float16
+        u16 = _scaled_rows(rows, x_norm.clamp_min(eps).reciprocal(), qk_type)
     else:
-        u = rows
         qk_type = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
-    u16 = _aligned(u.to(qk_type))
+        u16 = _aligned(rows.to(qk_type))
     beta_t = beta.detach().float().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
-    # r from those rows and keys: the forward's own r, else one route launch.
     if r is None:
         layout16 = route_layout(dictionary_key.detach(), dictionary_value.detach(), qk_type)
         r = _route_forward(u16, layout16, beta_t, eps, False, False, RouteVariant())
-    r = r.reshape(-1, routing_dim).float()
-    g = grad.detach().reshape(-1, routing_dim).float()
-    if normalize_output:
-        r_norm = r.norm(dim=1, keepdim=True)
-        z = r / r_norm.clamp_min(eps)
-        dr = torch.where(r_norm > eps, (g - z * (z * g).sum(1, keepdim=True)) / r_norm.clamp_min(eps), g / eps)
-    else:
-        dr = g
-    keys = _aligned(dictionary_key.detach().t().to(qk_type))
+    r = r.reshape(-1, routing_dim)
+    g = grad.detach().reshape(-1, routing_dim)
     # Values, r and dr in fp16 for fp16 inputs (8x finer than bf16: with the
     # output norm, rowsum(dr . r) is analytically zero and its rounding noise
     # reaches every atom's gradient), bf16 for bf16 inputs.
     v_type = torch.float16 if x.dtype == torch.float16 else torch.bfloat16
+    if normalize_output:
+        go = _normalize_backward(r, _row_norm(r), g, eps, v_type)
+    else:
+        go = _aligned(g.to(v_type))
+    keys = _aligned(dictionary_key.detach().t().to(qk_type))
     values = _aligned(dictionary_value.detach().t().to(v_type))
     out = _aligned(r.to(v_type))
-    go = _aligned(dr.to(v_type))
     lib = _lib.get()
     ws_bytes = lib.da_attention_backward_workspace_bytes(1, 1, n, atoms, routing_dim, routing_dim)
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
@@ -395,20 +466,28 @@ def _route_backward(
         ),
         "dictionary_route_hip backward",
     )
-    if normalize_input:
-        dx = torch.where(x_norm > eps, (du - u * (u * du).sum(1, keepdim=True)) / x_norm.clamp_min(eps), du / eps)
-    else:
-        dx = du
+    dx = _normalize_backward(rows, x_norm, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
     return (
-        dx.reshape(x.shape).to(x.dtype),
-        dkt.t().to(dictionary_key.dtype),
-        dvt.t().to(dictionary_value.dtype),
+        dx.reshape(x.shape),
+        dkt.t().to(bank_grad_dtype or dictionary_key.dtype),
+        dvt.t().to(bank_grad_dtype or dictionary_value.dtype),
         dbeta,
     )
 
 
 # The row kernel holds a row's atoms in VGPRs (at most 4096).
 ROUTE_BACKWARD_ROWS_MAX_ATOMS = 4096
+
+
+def route_backward_is_native(routing_dim: int, atoms: int, dtype: torch.dtype, variant: RouteVariant) -> bool:
+    """Whether ``route_gradients`` takes rows of this width and dtype (on a
+    ROCm device) and a bank of this size on a native path."""
+
+    if dtype not in (torch.float16, torch.bfloat16) or atoms < 1:
+        return False
+    if variant.flags() == 0 and routing_dim in ROUTE_BACKWARD_WIDTHS:
+        return True
+    return routing_dim in SUPPORTED_WIDTHS and atoms <= ROUTE_BACKWARD_ROWS_MAX_ATOMS
 
 
 def _route_backward_rows_supported(x: Tensor, dictionary_key: Tensor) -> bool:
@@ -427,6 +506,42 @@ def _mm_f32(a: Tensor, b: Tensor) -> Tensor:
     return torch.mm(a, b, out_dtype=torch.float32)
 
 
+# Split-K for the weight-gradient products: chunks of at least this many
+# rows of K, at most this many chunks.
+SPLIT_K_MIN_CHUNK = 1024
+SPLIT_K_MAX = 8
+
+
+def _mm_tn_f32(a: Tensor, b: Tensor) -> Tensor:
+    """``a^T b`` for row-major ``a [K, M]`` and ``b [K, N]`` (16-bit, unit
+    column stride), fp32 result.
+
+    The weight gradients have a long K (tokens or rows) over a small output:
+    one library GEMM runs a few dozen output tiles on 256 CUs.  K is cut into
+    s chunks whose partial products run as one batched GEMM (fp32 partials,
+    summed): up to 2.3x faster at [16384 x 512]^T [16384 x 1536].
+    """
+
+    k, m = a.shape
+    n = b.shape[1]
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    if b.stride(1) != 1:
+        b = b.contiguous()
+    tiles = -(-m // 128) * -(-n // 128)
+    s = 1
+    while s < SPLIT_K_MAX and k % (2 * s) == 0 and k // (2 * s) >= SPLIT_K_MIN_CHUNK and tiles * s < 512:
+        s *= 2
+    if s == 1:
+        return _mm_f32(a.t(), b)
+    chunk = k // s
+    # Left operand: the transposed chunks of a (column-major views); right
+    # operand: row-major chunks of b.
+    a3 = a.as_strided((s, m, chunk), (chunk * a.stride(0), 1, a.stride(0)))
+    b3 = b.as_strided((s, chunk, n), (chunk * b.stride(0), b.stride(0), 1))
+    return torch.bmm(a3, b3, out_dtype=torch.float32).sum(0)
+
+
 def _route_backward_rows(
     x: Tensor,
     dictionary_key: Tensor,
@@ -438,6 +553,7 @@ def _route_backward_rows(
     grad: Tensor,
     variant: RouteVariant,
     r: Tensor | None = None,
+    bank_grad_dtype: torch.dtype | None = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients of the route (``ops.py:16-62``) for every variant and width.
 
@@ -449,46 +565,45 @@ def _route_backward_rows(
     kernel's operands (unit rows rounded once to fp16 with fp16 keys; raw rows
     in their own dtype); r, the reconstruction before the output norm, is the
     forward's (``r``) or comes from one route launch.  Returns gradients in
-    the dtypes of ``x`` and the dictionary tensors, and d beta as a 1-element
-    fp32 tensor.
+    the dtypes of ``x`` and the dictionary tensors (or ``bank_grad_dtype`` for
+    the two bank gradients), and d beta as a 1-element fp32 tensor.
     """
 
     routing_dim = x.shape[-1]
     atoms = dictionary_key.shape[1]
     device = x.device
-    rows = x.detach().reshape(-1, routing_dim).float()
+    rows = _aligned(x.detach().reshape(-1, routing_dim))
     n = rows.shape[0]
+    # 16-bit operands of the GEMMs: fp16 for fp16 inputs, bf16 for bf16 ones.
+    v_type = torch.float16 if x.dtype == torch.float16 else torch.bfloat16
     if normalize_input:
-        x_norm = rows.norm(dim=1, keepdim=True)
-        u = rows / x_norm.clamp_min(eps)
+        x_norm = _row_norm(rows)
+        inv_x = x_norm.clamp_min(eps).reciprocal()
         key_type = torch.float16
-        u_h = _aligned(u.to(key_type))
+        u_h = _scaled_rows(rows, inv_x, key_type)
+        u_v = u_h if v_type == key_type else _scaled_rows(rows, inv_x, v_type)
     else:
-        u = rows
         key_type = x.dtype
-        u_h = _aligned(x.detach().reshape(-1, routing_dim))
+        u_h = u_v = rows
     beta_t = beta.detach().float().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
     if r is None:
         layout = route_layout(dictionary_key.detach(), dictionary_value.detach(), key_type)
         r = _route_forward(u_h, layout, beta_t, eps, False, False, variant)
-    r = r.reshape(-1, routing_dim).float()
-    g = grad.detach().reshape(-1, routing_dim).float()
-    if normalize_output:
-        r_norm = r.norm(dim=1, keepdim=True)
-        z = r / r_norm.clamp_min(eps)
-        dr = torch.where(r_norm > eps, (g - z * (z * g).sum(1, keepdim=True)) / r_norm.clamp_min(eps), g / eps)
-    else:
-        dr = g
-    # 16-bit operands of the GEMMs: fp16 for fp16 inputs, bf16 for bf16 ones.
+    r = r.reshape(-1, routing_dim)
+    g = grad.detach().reshape(-1, routing_dim)
     # dW = dr Dv takes dr as a 16-bit head and its rounding residual ([n, 2R]
     # against [Dv; Dv]): the softmax backward differences dW_j - sum_k w_k dW_k,
     # so one 16-bit rounding of dr would reach every atom's gradient.
-    v_type = torch.float16 if x.dtype == torch.float16 else torch.bfloat16
+    dr = _normalize_backward(r, _row_norm(r), g, eps, torch.float32) if normalize_output else g.float()
+    dr2 = torch.empty(n, 2 * routing_dim, dtype=v_type, device=device)
+    dr_v = dr2[:, :routing_dim]
+    dr_v.copy_(dr)
+    torch.sub(dr, dr_v, out=dr2[:, routing_dim:])
+    del dr
     keys_h = dictionary_key.detach().to(key_type)
     logits = _mm_f32(u_h, keys_h)
-    dr_v = dr.to(v_type)
     values_v = dictionary_value.detach().to(v_type)
-    grad_weights = _mm_f32(torch.cat((dr_v, (dr - dr_v.float()).to(v_type)), dim=1), torch.cat((values_v, values_v)))
+    grad_weights = _mm_f32(dr2, torch.cat((values_v, values_v)))
     grad_logits = torch.empty(n, atoms, dtype=v_type, device=device)
     weights = torch.empty(n, atoms, dtype=v_type, device=device)
     dbeta_rows = torch.empty(n, dtype=torch.float32, device=device)
@@ -503,19 +618,17 @@ def _route_backward_rows(
         ),
         "dictionary_route_hip backward rows",
     )
+    del logits, grad_weights
     keys_vt = dictionary_key.detach().to(v_type).t().contiguous()
     du = _mm_f32(grad_logits, keys_vt)
-    d_key = _mm_f32(u.to(v_type).t(), grad_logits)
-    d_value = _mm_f32(dr_v.t(), weights)
+    d_key = _mm_tn_f32(u_v, grad_logits)
+    d_value = _mm_tn_f32(dr_v, weights)
     dbeta = dbeta_rows.sum().reshape(1)
-    if normalize_input:
-        dx = torch.where(x_norm > eps, (du - u * (u * du).sum(1, keepdim=True)) / x_norm.clamp_min(eps), du / eps)
-    else:
-        dx = du
+    dx = _normalize_backward(rows, x_norm, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
     return (
-        dx.reshape(x.shape).to(x.dtype),
-        d_key.to(dictionary_key.dtype),
-        d_value.to(dictionary_value.dtype),
+        dx.reshape(x.shape),
+        d_key.to(bank_grad_dtype or dictionary_key.dtype),
+        d_value.to(bank_grad_dtype or dictionary_value.dtype),
         dbeta,
     )
 
@@ -532,6 +645,7 @@ def route_gradients(
     grad: Tensor,
     needs: tuple[bool, bool, bool, bool] = (True, True, True, True),
     r: Tensor | None = None,
+    bank_grad_dtype: torch.dtype | None = None,
 ) -> tuple[Tensor | None, Tensor | None, Tensor | None, Tensor | None]:
     """(dx, dDk, dDv, dbeta) of the route for ``d loss / d out = grad``.
 
@@ -540,17 +654,20 @@ def route_gradients(
     variant up to 4096 atoms; beyond that autograd recomputes the torch route.
     ``needs`` marks the wanted gradients (dbeta only for a tensor beta); ``r``
     is the forward's reconstruction before the output norm, when the caller
-    kept it (else one route launch forms it again).
+    kept it (else one route launch forms it again); ``bank_grad_dtype``
+    overrides the dtype of the two bank gradients (the native paths only).
     """
 
     native = None
     if _route_backward_supported(x, dictionary_key, variant):
         native = _route_backward(
-            x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, r
+            x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, r,
+            bank_grad_dtype,
         )
     elif _route_backward_rows_supported(x, dictionary_key):
         native = _route_backward_rows(
-            x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, variant, r
+            x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, variant, r,
+            bank_grad_dtype,
         )
     if native is not None:
         dx, ddk, ddv, dbeta = native

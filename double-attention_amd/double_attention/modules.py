@@ -402,8 +402,12 @@ class SharedDictionaryAttention(nn.Module):
 class _HipModuleFunction(torch.autograd.Function):
     """HIP forward and native backward of one ``SharedDictionaryAttention`` call.
 
-    Inputs are ``x``, the normalized dictionary (or the raw bank parameters)
+    Inputs are ``x``, the normalized dictionary or the raw bank parameters,
     and every module parameter, so autograd routes gradients to all of them.
+    With the raw bank (a module's own bank whose route backward is native)
+    the forward normalizes it in one launch straight into the route layouts,
+    and the backward returns the gradients at the raw atoms through
+    ``da_dictionary_normalize_backward``.
     The forward runs the library's stages one launch each (Q/K/V projection,
     route, per-map attention, map combine, output projection) and keeps what
     the backward needs: the pre-route rows, the routed rows, the per-map
@@ -416,27 +420,53 @@ class _HipModuleFunction(torch.autograd.Function):
 
     @staticmethod
     def run(module, x, bank, normalized_dictionary, dtype, return_aux):
+        from . import hip_ops
+
+        cfg = module.config
         params = [p for p in module.parameters()]
-        if normalized_dictionary is None:
-            dictionary = bank.normalized(module.config.eps)
+        raw_bank = (
+            normalized_dictionary is None
+            and x.is_cuda
+            and hip_ops.route_backward_is_native(
+                cfg.routing_dim, bank.dictionary_size, dtype, hip_ops.RouteVariant.of_config(cfg)
+            )
+        )
+        if raw_bank:
+            dictionary = (bank.raw_key, bank.raw_value)
+        elif normalized_dictionary is None:
+            dictionary = bank.normalized(cfg.eps)
             if dictionary[0] is dictionary[1]:
                 dictionary = (dictionary[0], dictionary[0].view_as(dictionary[0]))
         else:
             dictionary = normalized_dictionary
-        out = _HipModuleFunction.apply(module, dtype, x, dictionary[0], dictionary[1], *params)
+        out = _HipModuleFunction.apply(module, (dtype, raw_bank), x, dictionary[0], dictionary[1], *params)
         if not return_aux:
             return out
         with torch.no_grad():
-            from . import hip_ops
-
-            key_dtype = hip_ops.route_key_dtype(module.config.normalize_routing_input, dtype)
-            layout = hip_ops.route_layout(dictionary[0], dictionary[1], key_dtype)
-            routed = hip_ops.shared_dictionary_attention_hip(module, x, layout, dtype).routed
-        return out, module._hip_aux(routed, dtype)
+            key_dtype = hip_ops.route_key_dtype(cfg.normalize_routing_input, dtype)
+            if raw_bank:
+                layout = hip_ops.own_bank_layout(bank, key_dtype)
+                result = hip_ops.shared_dictionary_attention_hip(
+                    module, x, layout, dtype, raw_bank=(bank.raw_key, bank.raw_value)
+                )
+            else:
+                layout = hip_ops.route_layout(dictionary[0], dictionary[1], key_dtype)
+                result = hip_ops.shared_dictionary_attention_hip(module, x, layout, dtype)
+        return out, module._hip_aux(result.routed, dtype)
 
     @staticmethod
-    def forward(ctx, module, dtype, x, dictionary_key, dictionary_value, *params):  # type: ignore[override]
+    def forward(ctx, module, spec, x, dictionary_key, dictionary_value, *params):  # type: ignore[override]
         from . import hip_ops
+
+        dtype, raw_bank = spec
+        ctx.raw_bank = raw_bank
+        raw_key = raw_value = None
+        if raw_bank:
+            raw_key, raw_value = dictionary_key, dictionary_value
+            dictionary_key, dictionary_value = hip_ops.dictionary_normalize_hip(
+                raw_key, raw_value, module.config.eps,
+                hip_ops.route_key_dtype(module.config.normalize_routing_input, dtype),
+            )
 
         cfg = module.config
         batch, length, model_dim = x.shape
@@ -462,7 +492,8 @@ class _HipModuleFunction(torch.autograd.Function):
             out_dtype=torch.float16,
         )
         if cfg.normalize_routing_output:
-            routed = F.normalize(recon.float(), dim=-1, eps=cfg.eps).to(torch.float16)
+            # F.normalize in fp32, one rounding to fp16.
+            routed = hip_ops._scaled_rows(recon, hip_ops._row_norm(recon).clamp_min(cfg.eps).reciprocal(), torch.float16)
         else:
             routed = recon
         score_query, score_key = _HipModuleFunction._score_maps(routed, batch, length, branches, maps, routing_dim)
@@ -493,7 +524,8 @@ class _HipModuleFunction(torch.autograd.Function):
         ctx.param_names = [name for name, _ in module.named_parameters()]
         ctx.x_dtype = x.dtype
         ctx.save_for_backward(xc, qk, recon, routed, map_output, mixed, vt, scales, beta, dictionary_key,
-                              dictionary_value, factors if factors is not None else torch.empty(0), *params)
+                              dictionary_value, factors if factors is not None else torch.empty(0), raw_key,
+                              raw_value, *params)
         return out
 
     @staticmethod
@@ -504,12 +536,13 @@ class _HipModuleFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad):  # type: ignore[override]
         from . import hip_ops
-        from .hip_ops import _mm_f32
+        from .hip_ops import _mm_tn_f32
 
         module = ctx.module
         cfg = module.config
         dtype = ctx.dtype
-        xc, qk, recon, routed, map_output, mixed, vt, scales, beta, dk, dv, factors, *params = ctx.saved_tensors
+        (xc, qk, recon, routed, map_output, mixed, vt, scales, beta, dk, dv, factors, raw_key, raw_value,
+         *params) = ctx.saved_tensors
         named = dict(zip(ctx.param_names, params))
         batch, length, model_dim = xc.shape
         branches, maps, routing_dim = cfg.qk_branches, cfg.outer_maps, cfg.routing_dim
@@ -526,7 +559,7 @@ class _HipModuleFunction(torch.autograd.Function):
         if isinstance(module.output, nn.Linear):
             d_mixed = torch.mm(g, named["output.weight"].detach().to(dtype))
             if wants("output.weight"):
-                grads["output.weight"] = _mm_f32(g.t(), mixed2d)
+                grads["output.weight"] = _mm_tn_f32(g, mixed2d)
         else:
             d_mixed = g
         # Map combine.
@@ -568,11 +601,22 @@ class _HipModuleFunction(torch.autograd.Function):
         d_routed = torch.stack((d_rq.transpose(1, 2), d_rk.transpose(1, 2)), dim=2).reshape(-1, routing_dim)
         # Route.
         variant = hip_ops.RouteVariant.of_config(cfg)
+        # With the raw bank the gradients at the normalized atoms stay fp32
+        # for the normalization's backward; a tied bank's key atoms take both.
+        need_key, need_value = ctx.needs_input_grad[3], ctx.needs_input_grad[4]
+        if ctx.raw_bank and raw_value is None:
+            need_value = need_key
         d_rows, d_key, d_val, d_beta = hip_ops.route_gradients(
             qk.view(-1, routing_dim), dk, dv, beta, cfg.eps, cfg.normalize_routing_input,
-            cfg.normalize_routing_output, variant, d_routed,
-            (True, ctx.needs_input_grad[3], ctx.needs_input_grad[4], wants("log_beta")), recon,
+            cfg.normalize_routing_output, variant, d_routed, (True, need_key, need_value, wants("log_beta")), recon,
+            torch.float32 if ctx.raw_bank else None,
         )
+        if ctx.raw_bank and (need_key or need_value):
+            d_key, d_val = hip_ops.dictionary_normalize_backward_hip(raw_key, raw_value, d_key, d_val, cfg.eps)
+            if not ctx.needs_input_grad[3]:
+                d_key = None
+            if not ctx.needs_input_grad[4]:
+                d_val = None
         if wants("log_beta") and d_beta is not None:
             log_beta = named["log_beta"].detach()
             inside = (log_beta >= math.log(0.05)) & (log_beta <= math.log(64.0))
@@ -587,12 +631,15 @@ class _HipModuleFunction(torch.autograd.Function):
             dx.addmm_(d_qk[:, :width], named["query.weight"].detach().to(dtype))
             dx.addmm_(d_qk[:, width:], named["key.weight"].detach().to(dtype))
             dx = dx.view(batch, length, model_dim).to(ctx.x_dtype)
-        if wants("query.weight"):
-            grads["query.weight"] = _mm_f32(d_qk[:, :width].t(), x2d)
-        if wants("key.weight"):
-            grads["key.weight"] = _mm_f32(d_qk[:, width:].t(), x2d)
+        if wants("query.weight") and wants("key.weight"):
+            d_wqk = _mm_tn_f32(d_qk, x2d)
+            grads["query.weight"], grads["key.weight"] = d_wqk[:width], d_wqk[width:]
+        elif wants("query.weight"):
+            grads["query.weight"] = _mm_tn_f32(d_qk[:, :width], x2d)
+        elif wants("key.weight"):
+            grads["key.weight"] = _mm_tn_f32(d_qk[:, width:], x2d)
         if wants("value.weight"):
-            grads["value.weight"] = _mm_f32(d_v.t(), x2d)
+            grads["value.weight"] = _mm_tn_f32(d_v, x2d)
         if wants("value.bias"):
             grads["value.bias"] = d_v.float().sum(0)
         tail = [

@@ -17,6 +17,8 @@
  * Reference interfaces replaced (paths relative to the reference repository
  * Ahnd6474/double-attention):
  *   da_dictionary_normalize   SharedDictionaryBank.normalized        src/double_attention/modules.py:45-48
+ *   da_dictionary_normalize_backward
+ *                             autograd of SharedDictionaryBank.normalized  src/double_attention/modules.py:45-48
  *   da_dictionary_route       dictionary_route_triton / _reference   src/double_attention/triton_kernels.py:1984-2019, ops.py:16-62
  *   da_dictionary_route_backward_rows
  *                             _row_scaled_softmax_backward_kernel    src/double_attention/triton_kernels.py:589-671, 1480
@@ -116,6 +118,25 @@ int64_t da_padded_length(int64_t length);
 int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_dtype,
                             int64_t routing_dim, int64_t atoms, float eps, void* key_t,
                             int key_dtype, void* value, void* value_rows, da_stream_t stream);
+
+/*
+ * Backward of da_dictionary_normalize (F.normalize(raw, dim=0) under autograd,
+ * modules.py:45-48): gradients at the raw bank from gradients at the
+ * normalized atoms.
+ *   raw_key, raw_value: [routing_dim, atoms] row-major, raw_dtype (raw_value
+ *           NULL = tied bank)
+ *   grad_key, grad_value: [routing_dim, atoms] fp32, the gradients at the
+ *           normalized key and value atoms (grad_value may be NULL: zero).
+ *           For a tied bank both flow into the key atoms.
+ *   d_raw_key, d_raw_value: out, [routing_dim, atoms] raw_dtype (d_raw_value
+ *           NULL = not wanted; must be NULL for a tied bank)
+ * Atom j with raw column v and gradient h gets (h - n <n, h>) / |v| with
+ * n = v / |v| where |v| > eps, and h / eps elsewhere.
+ */
+int da_dictionary_normalize_backward(const void* raw_key, const void* raw_value, int raw_dtype,
+                                     int64_t routing_dim, int64_t atoms, float eps, const float* grad_key,
+                                     const float* grad_value, void* d_raw_key, void* d_raw_value,
+                                     da_stream_t stream);
 
 /*
  * Fused dictionary route (ops.py:16-62), for any number of rows:

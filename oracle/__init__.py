@@ -12,6 +12,10 @@ Functions and what pins them (each check is in ``tests/test_oracle.py``):
 
 * ``l2_normalize``            closed form; zero vector stays zero; unit norms.
 * ``bank_normalized``         unit column norms; tied bank returns one array.
+* ``bank_normalized_backward``
+                              central finite differences in fp64 of both
+                              banks, tied and untied, with a column below eps
+                              (the closed form h / eps there).
 * ``dictionary_route``        zero input -> normalized mean atom; huge beta ->
                               the argmax atom; one-atom bank; input-scale
                               invariance; atom-permutation invariance; scalar
@@ -39,6 +43,7 @@ Functions and what pins them (each check is in ``tests/test_oracle.py``):
 from .sda import (
     assemble_score_maps,
     bank_normalized,
+    bank_normalized_backward,
     beta_from_log,
     dictionary_route,
     dictionary_route_backward,
@@ -55,6 +60,7 @@ from .sda import (
 __all__ = [
     "assemble_score_maps",
     "bank_normalized",
+    "bank_normalized_backward",
     "beta_from_log",
     "dictionary_route",
     "dictionary_route_backward",

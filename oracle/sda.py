@@ -61,6 +61,17 @@ def bank_normalized(raw_key: np.ndarray, raw_value: np.ndarray | None, eps: floa
     return key, value
 
 
+def bank_normalized_backward(raw_key: np.ndarray, raw_value: np.ndarray | None, grad_key: np.ndarray,
+                             grad_value: np.ndarray, eps: float = 1e-6):
+    """Gradients at the raw bank of ``bank_normalized`` (modules.py:45-48 under
+    autograd): each column through ``v / max(|v|, eps)``; a tied bank's key
+    atoms collect both gradients.  Returns ``(d_raw_key, d_raw_value or None)``."""
+
+    if raw_value is None:
+        return _normalize_backward(raw_key.T, (grad_key + grad_value).T, eps).T, None
+    return _normalize_backward(raw_key.T, grad_key.T, eps).T, _normalize_backward(raw_value.T, grad_value.T, eps).T
+
+
 def dictionary_route(
     x: np.ndarray,
     dictionary_key: np.ndarray,

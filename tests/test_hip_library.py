@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 19
+    assert len(names) == 20
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -233,3 +233,23 @@ def test_route_backward_rows_rejects_bad_arguments() -> None:
     assert b"beta_count" in h.da_last_error()
     assert call(rows=0, logits=None) == 0               # nothing to do
 
+
+
+def test_normalize_backward_rejects_bad_arguments() -> None:
+    h = lib.get()
+    buf = ctypes.c_void_p(16)   # never dereferenced
+
+    def call(**kw):
+        args = dict(raw_key=buf, raw_value=buf, raw_dtype=lib.DA_F32, routing_dim=64, atoms=100, eps=1e-6,
+                    grad_key=buf, grad_value=buf, d_raw_key=buf, d_raw_value=buf, stream=None)
+        args.update(kw)
+        return h.da_dictionary_normalize_backward(*args.values())
+
+    assert call(raw_dtype=7) == -1
+    assert call(routing_dim=0) == -1
+    assert call(atoms=0) == -1
+    assert call(eps=-1.0) == -1
+    assert call(grad_key=None) == -1
+    assert b"null" in h.da_last_error()
+    assert call(raw_value=None) == -1                   # d_raw_value for a tied bank
+    assert b"tied" in h.da_last_error()

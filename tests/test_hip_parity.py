@@ -89,6 +89,43 @@ def test_dictionary_normalize(key_dtype, raw_dtype, routing_dim, atoms, tied) ->
     assert torch.count_nonzero(da.hip_ops._untile_value(layout.value)[:, atoms:]) == 0
 
 
+@pytest.mark.parametrize("raw_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize(("routing_dim", "atoms", "tied"), [(64, 100, False), (256, 512, True), (512, 1536, False),
+                                                            (512, 1536, True), (96, 1, False)])
+def test_dictionary_normalize_backward(raw_dtype, routing_dim, atoms, tied) -> None:
+    # Gradients at the raw bank (F.normalize(dim=0) under autograd) against
+    # the oracle in fp64 on the same rounded inputs; column 0 is zero (the
+    # h / eps branch), the others span three orders of magnitude in norm.
+    device = _device()
+    eps = 1e-6
+    g = torch.Generator().manual_seed(7 * routing_dim + atoms)
+    scale = torch.logspace(-1.5, 1.5, atoms)
+    raw_key = (torch.randn(routing_dim, atoms, generator=g) * scale)
+    raw_key[:, 0] = 0.0
+    raw_key = raw_key.to(device, raw_dtype)
+    raw_value = None if tied else (torch.randn(routing_dim, atoms, generator=g) * scale).to(device, raw_dtype)
+    grad_key = torch.randn(routing_dim, atoms, generator=g).to(device)
+    grad_value = torch.randn(routing_dim, atoms, generator=g).to(device)
+    d_key, d_value = da.hip_ops.dictionary_normalize_backward_hip(raw_key, raw_value, grad_key, grad_value, eps)
+    torch.cuda.synchronize()
+    assert d_key.dtype == raw_dtype and (d_value is None) == tied
+    rk = np32(raw_key).astype(np.float64)
+    rv = None if tied else np32(raw_value).astype(np.float64)
+    ek, ev = oracle.bank_normalized_backward(rk, rv, np32(grad_key).astype(np.float64),
+                                             np32(grad_value).astype(np.float64), eps)
+    # The eps column: the plain gradient over eps (~1e6), checked relatively.
+    total = (grad_key + grad_value) if tied else grad_key
+    assert torch.allclose(d_key[:, 0].float(), total[:, 0] / eps, rtol=8e-3, atol=0.0)
+    if atoms > 1:
+        # The rest per column relative to that column's scale (1 / |v|).
+        for actual, expected, raw in ((d_key, ek, rk), (d_value, ev, rv)):
+            if actual is None:
+                continue
+            col = np.maximum(np.linalg.norm(raw, axis=0), eps)[1:]
+            assert_parity(actual[:, 1:] * torch.as_tensor(col, device=device, dtype=torch.float32),
+                          expected[:, 1:] * col, 5e-3, 4e-2, "bank backward")
+
+
 # ---------------------------------------------------------------- GEMMs
 
 

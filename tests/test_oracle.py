@@ -167,6 +167,44 @@ def test_route_brute_force_loop() -> None:
         np.testing.assert_allclose(z[i], [v / n for v in rec], rtol=1e-12)
 
 
+@pytest.mark.parametrize("tied", [False, True])
+def test_bank_normalized_backward_matches_finite_differences(tied: bool) -> None:
+    # Gradients at the raw bank through the column normalization, against
+    # central differences of bank_normalized in fp64; one column is scaled
+    # below eps (the h / eps branch) and one is large.
+    rng = np.random.default_rng(21)
+    r, m, eps = 5, 6, 1e-3
+    raw_key = rng.standard_normal((r, m))
+    raw_key[:, 2] *= 1e-5
+    raw_key[:, 4] *= 30.0
+    raw_value = None if tied else rng.standard_normal((r, m))
+    wk, wv = rng.standard_normal((r, m)), rng.standard_normal((r, m))
+    d_key, d_value = oracle.bank_normalized_backward(raw_key, raw_value, wk, wv, eps)
+    assert (d_value is None) == tied
+
+    def loss(k_, v_):
+        key, value = oracle.bank_normalized(k_, v_, eps)
+        return float((key * wk).sum() + (value * wv).sum())
+
+    h = 1e-7
+    for which, arr, grad in ((0, raw_key, d_key), (1, raw_value, d_value)):
+        if arr is None:
+            continue
+        numeric = np.zeros_like(arr)
+        for pos in np.ndindex(arr.shape):
+            plus, minus = arr.copy(), arr.copy()
+            plus[pos] += h
+            minus[pos] -= h
+            args_p, args_m = [raw_key, raw_value], [raw_key, raw_value]
+            args_p[which], args_m[which] = plus, minus
+            numeric[pos] = (loss(*args_p) - loss(*args_m)) / (2 * h)
+        np.testing.assert_allclose(grad, numeric, rtol=1e-5, atol=1e-6)
+    # The small column is in the h / eps branch: its gradient is the plain
+    # scaled one, no projection.
+    total = wk + wv if tied else wk
+    np.testing.assert_allclose(d_key[:, 2], total[:, 2] / eps, rtol=1e-12)
+
+
 @pytest.mark.parametrize(("normalize_input", "normalize_output"), [(True, True), (False, True), (True, False)])
 def test_route_backward_matches_finite_differences(normalize_input: bool, normalize_output: bool) -> None:
     rng = np.random.default_rng(11)
