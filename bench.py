@@ -74,7 +74,8 @@ def parse_args() -> argparse.Namespace:
         "--kernels-only",
         action="store_true",
         help="run only the per-kernel timing loops (each kernel 5 + --kernel-reps launches, in a fixed order) "
-        "and the --copy-mib calibration copies: the child run that --collect-counters profiles",
+        "and the --copy-mib calibration copies: the child run that --collect-counters profiles; with "
+        "--backward, only --steps HIP training steps (module, and for c4 the LM), for a kernel trace",
     )
     p.add_argument(
         "--collect-counters",
@@ -338,7 +339,9 @@ def backward_bench(args: argparse.Namespace) -> None:
     out = hip_ops._attention_forward(q, k, v, scales, causal)
 
     def native():
-        return hip_ops._attention_backward(q, k, v, scales, out, grad, causal)
+        # The dispatcher the module backward uses: the dense path for
+        # 512-wide scores whose matrices fit, the key-tile kernels otherwise.
+        return hip_ops.attention_gradients(q, k, v, scales, out, grad, causal)
 
     def recompute():
         with torch.enable_grad():
@@ -376,6 +379,24 @@ def backward_bench(args: argparse.Namespace) -> None:
             m(x).backward(grad_x)
         return run
 
+    if args.kernels_only:
+        # Only the HIP training step (and for C4 the HIP LM step), for a
+        # kernel trace of what one step launches: args.steps reps, no timing.
+        step = train_step(hip_module)
+        for _ in range(args.steps):
+            step()
+        if args.workload == "c4":
+            kwargs = dict(dictionary_group_size=LM_LAYERS, feedforward_dim=LM_FEEDFORWARD)
+            lm = da.DoubleAttentionLM(LM_VOCAB, length, config, LM_LAYERS, **kwargs).to(device, torch.bfloat16)
+            ids = torch.randint(0, LM_VOCAB, (batch, length), generator=g).to(device)
+            targets = torch.randint(0, LM_VOCAB, (batch, length), generator=g).to(device)
+            for _ in range(args.steps):
+                for param in lm.parameters():
+                    param.grad = None
+                lm(ids, targets)[1].backward()
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": args.workload, "training_steps": args.steps}), flush=True)
+        return
     module_ms = {name: round(timed(train_step(m), max(1, min(args.steps, 20))), 4)
                  for name, m in (("hip", hip_module), ("torch_bf16", torch_module))}
     del hip_module, torch_module
@@ -425,6 +446,7 @@ def backward_bench(args: argparse.Namespace) -> None:
         "speedup_vs_recompute": None if ref_ms is None else round(ref_ms / ms, 2),
         "module_fwd_bwd_ms": module_ms,
         "lm_fwd_bwd_ms": lm_ms,
+        "attention_backward_path": "dense" if hip_ops._dense_backward_fits(q, v) else "key-tile kernels",
         "dtype": "fp16 q/k, bf16 v",
         "config": {"workload": description, "batch": batch, "maps": S, "length": length, "score_dim": rp,
                    "value_dim": d, "causal": causal},

@@ -384,7 +384,8 @@ def _normalize_backward(v: Tensor, norm: Tensor, h: Tensor, eps: float, dtype: t
 
     (h - n <n, h>) / |v| with n = v / |v| where |v| > eps, h / eps elsewhere;
     written as h i - v (<v, h> i^3 [|v| > eps]) with i = 1 / max(|v|, eps), in
-    fp32 and rounded once to ``dtype``.  ``norm`` is |v| as ``[n, 1]`` fp32.
+    fp32 and rounded once to ``dtype``.  ``norm`` is |v| as ``[n, 1]`` fp32;
+    ``h`` is fp32 (so every product of <v, h> is an fp32 product).
     """
 
     inv = norm.clamp_min(eps).reciprocal()
@@ -438,7 +439,8 @@ def _route_backward(
         layout16 = route_layout(dictionary_key.detach(), dictionary_value.detach(), qk_type)
         r = _route_forward(u16, layout16, beta_t, eps, False, False, RouteVariant())
     r = r.reshape(-1, routing_dim)
-    g = grad.detach().reshape(-1, routing_dim)
+    # fp32 gradient rows: the output norm's backward takes <r, g> of fp32 products.
+    g = grad.detach().reshape(-1, routing_dim).float()
     # Values, r and dr in fp16 for fp16 inputs (8x finer than bf16: with the
     # output norm, rowsum(dr . r) is analytically zero and its rounding noise
     # reaches every atom's gradient), bf16 for bf16 inputs.
@@ -590,11 +592,12 @@ def _route_backward_rows(
         layout = route_layout(dictionary_key.detach(), dictionary_value.detach(), key_type)
         r = _route_forward(u_h, layout, beta_t, eps, False, False, variant)
     r = r.reshape(-1, routing_dim)
-    g = grad.detach().reshape(-1, routing_dim)
+    # fp32 gradient rows: the output norm's backward takes <r, g> of fp32 products.
+    g = grad.detach().reshape(-1, routing_dim).float()
     # dW = dr Dv takes dr as a 16-bit head and its rounding residual ([n, 2R]
     # against [Dv; Dv]): the softmax backward differences dW_j - sum_k w_k dW_k,
     # so one 16-bit rounding of dr would reach every atom's gradient.
-    dr = _normalize_backward(r, _row_norm(r), g, eps, torch.float32) if normalize_output else g.float()
+    dr = _normalize_backward(r, _row_norm(r), g, eps, torch.float32) if normalize_output else g
     dr2 = torch.empty(n, 2 * routing_dim, dtype=v_type, device=device)
     dr_v = dr2[:, :routing_dim]
     dr_v.copy_(dr)
