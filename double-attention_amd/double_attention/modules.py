@@ -103,8 +103,39 @@ def _compute_dtype(x: Tensor, weight: Tensor) -> torch.dtype:
     return weight.dtype if x.dtype == weight.dtype else torch.promote_types(x.dtype, weight.dtype)
 
 
+def _hip_covers(config: DoubleAttentionConfig) -> bool:
+    """Whether the HIP kernels cover this configuration (``backend="auto"``
+    takes the torch path for one they do not; ``"hip"`` raises instead)."""
+
+    from . import hip_ops
+
+    try:
+        hip_ops.check_module_supported(config)
+    except NotImplementedError:
+        return False
+    return True
+
+
 class SharedDictionaryAttention(nn.Module):
-    """Routing/content-decoupled attention (``modules.py:68-291``)."""
+    """Routing/content-decoupled attention (``modules.py:68-291``).
+
+    ``config.backend`` picks the implementation: ``"torch"`` (the PyTorch
+    composition, any shape), ``"hip"`` (the gfx950 kernels; raises
+    ``NotImplementedError`` for a configuration they do not cover) or
+    ``"auto"`` (the kernels when they cover the call, else torch).  Limits of
+    the kernels (``hip_ops.check_module_supported``):
+
+    * ``model_dim`` and ``routing_dim`` in {64, 128, 256, 512} (every preset);
+      a grouped score width ``(qk_branches // outer_maps) * routing_dim`` of at
+      most 512; at most 64 outer maps;
+    * ``dictionary_activation`` "identity" or "silu", ``dictionary_assignment``
+      "softmax" or "silu"; any number of atoms and rows in the forward;
+    * 16-bit compute (bf16 or fp16 inputs, or autocast) on a ROCm device.
+
+    Training on ``"hip"`` runs the native backward for every covered forward;
+    a bank of more than 4096 atoms takes the route's gradients from autograd
+    of the torch route, and score widths above 512 the outer attention's.
+    """
 
     def __init__(
         self,
@@ -329,6 +360,8 @@ class SharedDictionaryAttention(nn.Module):
         dtype = _compute_dtype(x, self.query.weight)
         if resolve_backend(cfg.backend, (_Spec(x.is_cuda, dtype),)) != "hip":  # type: ignore[arg-type]
             return None
+        if cfg.backend == "auto" and not _hip_covers(cfg):
+            return None
         if torch.is_grad_enabled() and (
             x.requires_grad
             or any(p.requires_grad for p in self.parameters())
@@ -389,7 +422,7 @@ class SharedDictionaryAttention(nn.Module):
         if cfg.backend != "torch":
             dtype = _compute_dtype(x, self.query.weight)
             spec = _Spec(x.is_cuda, dtype)
-            if resolve_backend(cfg.backend, (spec,)) == "hip":  # type: ignore[arg-type]
+            if resolve_backend(cfg.backend, (spec,)) == "hip" and (cfg.backend == "hip" or _hip_covers(cfg)):  # type: ignore[arg-type]
                 return self._hip_forward(x, active, normalized_dictionary, dtype, return_aux)
 
         if normalized_dictionary is None:
@@ -705,7 +738,8 @@ class DoubleAttentionBlock(nn.Module):
         LayerNorms run as the library's LayerNorm kernel; the residual adds
         ride in the epilogues of the attention's output projection and of the
         FFN's second linear; the FFN's GELU rides in its first linear.  The
-        Q-dictionary FFN keeps its PyTorch expansion.
+        Q-dictionary FFN expands on the library's GEMM against the normalized
+        key atoms.
         """
 
         from . import hip_ops
@@ -726,10 +760,34 @@ class DoubleAttentionBlock(nn.Module):
         norm2 = self.feedforward_norm
         normalized_x = hip_ops.layer_norm_hip(x, norm2.weight, norm2.bias, norm2.eps)
         if attention.config.q_dictionary_feedforward:
-            return self._q_dictionary_feedforward(x, normalized_x, bank, normalized_dictionary)
+            return self._q_dictionary_feedforward_hip(x, normalized_x, bank, normalized_dictionary, dtype)
         first, second = self.feedforward[0], self.feedforward[2]
         expanded = hip_ops.linear_hip(normalized_x, first.weight, first.bias, activation="gelu")
         return hip_ops.linear_hip(expanded, second.weight, second.bias, residual=x)
+
+    def _q_dictionary_feedforward_hip(
+        self,
+        x: Tensor,
+        normalized_x: Tensor,
+        bank: SharedDictionaryBank,
+        normalized_dictionary: tuple[Tensor, Tensor] | None,
+        dtype: torch.dtype,
+    ) -> Tensor:
+        """The Q-dictionary FFN (``modules.py:546``) on the library's GEMM: the
+        query projection, the expansion against the normalized key atoms with
+        GELU in its epilogue, then the second linear with the residual add."""
+
+        from . import hip_ops
+
+        if normalized_dictionary is None:
+            dictionary_key, _ = bank.normalized(self.attention.config.eps)
+        else:
+            dictionary_key, _ = normalized_dictionary
+        query = hip_ops.linear_hip(normalized_x, self.attention.query.weight.to(dtype))
+        atoms_by_dim = hip_ops._aligned(dictionary_key.detach().t().to(dtype))   # [atoms, R]
+        hidden = hip_ops.linear_hip(query, atoms_by_dim, activation="gelu")
+        second = self.feedforward[2]
+        return hip_ops.linear_hip(hidden, second.weight.to(dtype), second.bias, residual=x)
 
     def _q_dictionary_feedforward(
         self,

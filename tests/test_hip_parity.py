@@ -863,6 +863,20 @@ def test_unsupported_width_raises_on_gpu() -> None:
         module(torch.randn(1, 8, 512, device=device, dtype=torch.bfloat16))
 
 
+def test_auto_backend_takes_torch_for_uncovered_width() -> None:
+    # backend="auto" on a width the kernels do not cover runs the torch path
+    # (same output as backend="torch"); backend="hip" raises (above).
+    device = _device()
+    torch.manual_seed(4)
+    config = da.experiment_config("a1", routing_dim=96, backend="auto")
+    module = da.SharedDictionaryAttention(config).to(device, torch.bfloat16)
+    reference = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(device, torch.bfloat16)
+    reference.load_state_dict(module.state_dict())
+    x = torch.randn(1, 8, 512, device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        torch.testing.assert_close(module(x), reference(x), rtol=0, atol=0)
+
+
 # ---------------------------------------------------------------- route backward
 
 
