@@ -42,6 +42,15 @@ __device__ __forceinline__ void wait_vmem_at_most() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// Workgroup barrier for hand-offs through LDS: this wave's LDS accesses are
+// complete (lgkmcnt(0)), then s_barrier.  Unlike __syncthreads, whose fence
+// also waits for every vector memory operation (vmcnt(0)), it leaves
+// global->LDS loads in flight, so a ring of stage buffers keeps its later
+// stages loading across the barrier; the caller first waits for the stage it
+// reads with wait_vmem_at_most.  The "memory" clobber keeps the compiler from
+// moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // A wave-uniform pointer moved to SGPRs, so that an address built from it
 // takes the scalar-base + 32-bit lane-offset form.
 template <typename T>

@@ -107,8 +107,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   typedef typename Cfg::TileP TileP;
   constexpr int STAGE = Cfg::STAGE;            // P tile, then Q tile
   constexpr int NA = Cfg::NA;
+  // Stage buffers: three for 64-row tiles (two workgroups still share a
+  // CU), two for 128-row tiles.
+  constexpr int NST = BI == 64 ? 3 : 2;
   static_assert(2 * STAGE >= kNormLdsBytes, "a normalization workgroup reuses the stage buffers");
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds[NST * STAGE];
   char* const lds0 = lds;
   char* const lds1 = lds + STAGE;
 
@@ -207,17 +210,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   const int bfrag[2] = {TileP::BYTES + GemmTileQ::base(wj * 64 + c, g, 0),
                         TileP::BYTES + GemmTileQ::base(wj * 64 + c, g, 1)};
 
-  // Two stage buffers: step st reads stage st and issues stage st + 1 into
-  // the other buffer.  Every fragment of the stage is read first (LDS latency
-  // is paid once, and the reads precede the next stage's DMA in program
-  // order: the compiler keeps any LDS read behind a DMA that writes LDS),
-  // then the next stage is issued, then the MFMAs run.  A final half stage
-  // (K % 64 == 32) takes one 32-deep step.  (A third stage, or a deeper ring
-  // at one workgroup per CU, ran slower at every projection and FFN shape
-  // measured: two co-resident workgroups hide more latency.)
+  // A ring of NST stage buffers: step st reads stage st (buffer st % NST) and
+  // issues stage st + NST - 1 into the buffer stage st - 1 used, so a stage
+  // has NST - 1 steps to land.  The step waits for its own stage only (the
+  // later one stays in flight across the barrier), reads every fragment of
+  // it (LDS latency paid once), issues the next stage, then runs the MFMAs.
+  // A final half stage (K % 64 == 32) takes one 32-deep step.
   auto step = [&](int st, char* cur, char* nxt) {
-    wait_vmem();
-    __syncthreads();
+    if (NST == 3 && st + 1 < n_stages) {
+      wait_vmem_at_most<Cfg::PER_WAVE>();   // stage st + 1 may stay in flight
+    } else {
+      wait_vmem();
+    }
+    lds_barrier();
     const bool full = K - st * kBK >= kBK;
     v8 af[2][NA], bf[2][4];
 #pragma unroll
@@ -228,7 +233,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
 #pragma unroll
       for (int b = 0; b < 4; ++b) bf[kk][b] = lds_v8<T>(cur + bfrag[kk] + b * GemmTileQ::ROW_BLOCK);
     }
-    if (st + 1 < n_stages) issue(nxt, (st + 1) * kBK);
+    if (st + NST - 1 < n_stages) issue(nxt, (st + NST - 1) * kBK);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       if (kk == 1 && !full) break;
@@ -239,13 +244,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
     }
   };
 
-  issue(lds0, 0);
-  int st = 0;
-  for (; st + 1 < n_stages; st += 2) {
-    step(st, lds0, lds1);
-    step(st + 1, lds1, lds0);
+  if constexpr (NST == 2) {
+    issue(lds0, 0);
+    int st = 0;
+    for (; st + 1 < n_stages; st += 2) {
+      step(st, lds0, lds1);
+      step(st + 1, lds1, lds0);
+    }
+    if (st < n_stages) step(st, lds0, lds1);
+  } else {
+    char* const lds2 = lds + 2 * STAGE;
+    issue(lds0, 0);
+    if (n_stages > 1) issue(lds1, kBK);
+    int st = 0;
+    for (; st + 2 < n_stages; st += 3) {
+      step(st, lds0, lds2);
+      step(st + 1, lds1, lds0);
+      step(st + 2, lds2, lds1);
+    }
+    if (st < n_stages) step(st, lds0, lds2);
+    if (st + 1 < n_stages) step(st + 1, lds1, lds0);
   }
-  if (st < n_stages) step(st, lds0, lds1);
 
   // Epilogue.  Lane (c, g) holds D[i0 + wi*BI/2 + a*16 + 4g + r][j0 + wj*64 + b*16 + c],
   // r = 0..3: four consecutive i of one j.  Both output layouts run along i
