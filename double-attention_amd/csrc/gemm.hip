@@ -115,18 +115,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   char* const lds0 = lds;
   char* const lds1 = lds + STAGE;
 
-  // The normalization's workgroups follow the GEMM tiles: they take the
-  // CU slots that the first finished tiles free, instead of pushing tiles
-  // into a second round.
-  const int w = static_cast<int>(blockIdx.x);
-  if (w >= prm.gemm_blocks) {
-    normalize_block(prm.norm, w - prm.gemm_blocks, lds);
+  // The normalization's workgroups come first: they start with the first
+  // round of tiles instead of after it.
+  const int n_norm = norm_blocks(prm.norm);
+  if (static_cast<int>(blockIdx.x) < n_norm) {
+    normalize_block(prm.norm, static_cast<int>(blockIdx.x), lds);
     return;
   }
-  // XCD-aware order: workgroup w runs on XCD w % kXcds (round-robin
-  // dispatch), so each XCD takes one contiguous range of tiles.  Inside a
-  // segment consecutive tiles share their block of the larger operand, which
-  // the XCD's L2 then fetches once.
+  const int w = static_cast<int>(blockIdx.x) - n_norm;
+  // XCD-aware order: workgroup w runs on XCD (w + n_norm) % kXcds
+  // (round-robin dispatch), so the workgroups of one residue of w take one
+  // contiguous range of tiles.  Inside a segment consecutive tiles share their
+  // block of the larger operand, which the XCD's L2 then fetches once.
   const int xcd = w % kXcds;
   const int per = prm.gemm_blocks / kXcds, rem = prm.gemm_blocks % kXcds;
   int tile = xcd * per + min(xcd, rem) + w / kXcds;
