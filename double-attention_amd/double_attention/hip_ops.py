@@ -57,7 +57,16 @@ def _half_code(dtype: torch.dtype) -> int:
     return _DTYPE_CODES[dtype]
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> int:
+    """The device's current stream as a raw ``hipStream_t`` (the one
+    ``torch.cuda.current_stream(device)`` wraps, without building the wrapper
+    object: this runs once per kernel call)."""
+
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -1103,11 +1112,11 @@ def layer_norm_hip(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: f
     code = _half_code(x.dtype)
     dim = x.shape[-1]
     xc = _aligned(x)
-    params = [_aligned(t.detach()) for t in (weight, bias) if t is not None]
-    if len({t.dtype for t in params}) > 1:
+    w = None if weight is None else _aligned(weight.detach())
+    b = None if bias is None else _aligned(bias.detach())
+    params = [t for t in (w, b) if t is not None]
+    if len(params) == 2 and w.dtype != b.dtype:
         raise ValueError("LayerNorm weight and bias must share a dtype")
-    w = None if weight is None else params[0]
-    b = None if bias is None else params[-1]
     out = torch.empty_like(xc)
     lib = _lib.get()
     _lib.check(
@@ -1192,31 +1201,23 @@ def own_bank_layout(bank, key_dtype: torch.dtype) -> RouteDictionary:
     return RouteDictionary(key_t, value, atoms, True)
 
 
-def shared_dictionary_attention_hip(
-    module,
-    x: Tensor,
-    layout: RouteDictionary,
-    dtype: torch.dtype,
-    raw_bank: tuple[Tensor, Tensor | None] | None = None,
-    residual: Tensor | None = None,
-    no_alloc: bool = False,
-) -> HipForwardResult:
-    """One ``SharedDictionaryAttention`` forward through the fused C entry point.
+def _module_operands(module, dtype: torch.dtype):
+    """The operands of ``module`` that ``shared_dictionary_attention_hip``
+    passes: the Q/K/V/output weights in the compute dtype, the value bias and
+    log beta in the scalars' dtype, the log score scales and the map-mix
+    logits, and that dtype.  Kept on the module while the parameters are the
+    same tensors at the same version (a forward then casts nothing)."""
 
-    With ``raw_bank`` (the bank's raw key / value atoms) the call first
-    normalizes them into ``layout`` (from ``own_bank_layout``), inside its
-    projection launch.  ``residual`` ([B, T, d] of the output dtype) is added
-    to the output projection's rounded result (the block's ``x + ...``).
-    ``no_alloc`` runs the allocation-free entry point, whose workspace is the
-    library's per-GPU scratch array: no workspace tensor is allocated, and
-    ``routed`` is None (the scratch belongs to the next call).
-    """
-
-    config = module.config
-    batch, length, model_dim = x.shape
-    code = _half_code(dtype)
-    if layout.key_t.dtype != route_key_dtype(config.normalize_routing_input, dtype):
-        raise ValueError("route dictionary key dtype does not match the configuration")
+    output = module.output.weight if isinstance(module.output, torch.nn.Linear) else None
+    params = (module.query.weight, module.key.weight, module.value.weight, output, module.value.bias,
+              module.log_beta, module.log_score_scales, module.map_mix_logits)
+    try:
+        key = (dtype, tuple(None if p is None else (p.data_ptr(), p._version) for p in params))
+    except RuntimeError:   # inference tensors keep no version counter
+        key = None
+    cached = module.__dict__.get("_hip_operands")
+    if key is not None and cached is not None and cached[0] == key:
+        return cached[1]
 
     def cast(t: Tensor | None) -> Tensor | None:
         if t is None:
@@ -1226,19 +1227,54 @@ def shared_dictionary_attention_hip(
             t = t.to(dtype)
         return _aligned(t)
 
-    xc = cast(x)
-    wq = cast(module.query.weight)
-    wk = cast(module.key.weight)
-    wv = cast(module.value.weight)
-    wo = cast(module.output.weight) if isinstance(module.output, torch.nn.Linear) else None
     # Scalars and the value bias share one dtype code.
     scalar_dtype = module.log_score_scales.dtype
     bv = module.value.bias
     bv = None if bv is None else bv.detach().to(scalar_dtype).contiguous()
-    log_beta = module.log_beta.detach().to(scalar_dtype).contiguous()
-    log_scales = module.log_score_scales.detach().contiguous()
     mix = module.map_mix_logits
-    mix = None if mix is None else mix.detach().to(scalar_dtype).contiguous()
+    operands = (
+        cast(module.query.weight), cast(module.key.weight), cast(module.value.weight), cast(output), bv,
+        module.log_beta.detach().to(scalar_dtype).contiguous(), module.log_score_scales.detach().contiguous(),
+        None if mix is None else mix.detach().to(scalar_dtype).contiguous(), scalar_dtype,
+    )
+    if key is not None:
+        module.__dict__["_hip_operands"] = (key, operands)
+    return operands
+
+
+def shared_dictionary_attention_hip(
+    module,
+    x: Tensor,
+    layout: RouteDictionary,
+    dtype: torch.dtype,
+    raw_bank: tuple[Tensor, Tensor | None] | None = None,
+    residual: Tensor | None = None,
+    no_alloc: bool = False,
+    want_routed: bool = True,
+) -> HipForwardResult:
+    """One ``SharedDictionaryAttention`` forward through the fused C entry point.
+
+    With ``raw_bank`` (the bank's raw key / value atoms) the call first
+    normalizes them into ``layout`` (from ``own_bank_layout``), inside its
+    projection launch.  ``residual`` ([B, T, d] of the output dtype) is added
+    to the output projection's rounded result (the block's ``x + ...``).
+    ``no_alloc`` runs the allocation-free entry point, whose workspace is the
+    library's per-GPU scratch array: no workspace tensor is allocated, and
+    ``routed`` is None (the scratch belongs to the next call), as it is
+    with ``want_routed`` False.
+    """
+
+    config = module.config
+    batch, length, model_dim = x.shape
+    code = _half_code(dtype)
+    if layout.key_t.dtype != route_key_dtype(config.normalize_routing_input, dtype):
+        raise ValueError("route dictionary key dtype does not match the configuration")
+
+    xc = x.detach()
+    if xc.dtype != dtype:
+        xc = xc.to(dtype)
+    xc = _aligned(xc)
+    wq, wk, wv, wo, bv, log_beta, log_scales, mix, scalar_dtype = _module_operands(module, dtype)
 
     concat = config.map_combine == "concat"
     width = config.total_qk_width
@@ -1282,6 +1318,8 @@ def shared_dictionary_attention_hip(
                    "shared_dictionary_attention_hip (no_alloc)")
         return HipForwardResult(out, None)
     _lib.check(lib.da_shared_dictionary_attention_forward(args, _stream(x.device)), "shared_dictionary_attention_hip")
+    if not want_routed:
+        return HipForwardResult(out, None)
     routed_bytes = batch * length * 2 * width * 2
     routed = workspace[:routed_bytes].view(torch.float16).view(
         batch, length, 2, config.qk_branches, config.routing_dim

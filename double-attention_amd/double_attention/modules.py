@@ -335,8 +335,10 @@ class SharedDictionaryAttention(nn.Module):
         normalized_dictionary: tuple[Tensor, Tensor] | None,
         dtype: torch.dtype,
         residual: Tensor | None = None,
+        want_routed: bool = True,
     ):
-        """The fused forward (no autograd); ``residual`` is added to its output."""
+        """The fused forward (no autograd); ``residual`` is added to its output.
+        ``want_routed`` False skips the routed-rows view (only the output is used)."""
 
         from . import hip_ops
 
@@ -345,10 +347,12 @@ class SharedDictionaryAttention(nn.Module):
             # The forward normalizes its own bank inside its projection launch.
             layout = hip_ops.own_bank_layout(bank, key_dtype)
             return hip_ops.shared_dictionary_attention_hip(
-                self, x, layout, dtype, raw_bank=(bank.raw_key, bank.raw_value), residual=residual
+                self, x, layout, dtype, raw_bank=(bank.raw_key, bank.raw_value), residual=residual,
+                want_routed=want_routed,
             )
         layout = hip_ops.route_layout(*normalized_dictionary, key_dtype)
-        return hip_ops.shared_dictionary_attention_hip(self, x, layout, dtype, residual=residual)
+        return hip_ops.shared_dictionary_attention_hip(self, x, layout, dtype, residual=residual,
+                                                       want_routed=want_routed)
 
     def _hip_inference_dtype(self, x: Tensor, bank: SharedDictionaryBank) -> torch.dtype | None:
         """The compute dtype when a forward of ``x`` would run the HIP kernels
@@ -756,7 +760,7 @@ class DoubleAttentionBlock(nn.Module):
         x = x.contiguous()
         norm1 = self.attention_norm
         hidden = hip_ops.layer_norm_hip(x, norm1.weight, norm1.bias, norm1.eps)
-        x = attention._hip_call(hidden, bank, normalized_dictionary, dtype, residual=x).output
+        x = attention._hip_call(hidden, bank, normalized_dictionary, dtype, residual=x, want_routed=False).output
         norm2 = self.feedforward_norm
         normalized_x = hip_ops.layer_norm_hip(x, norm2.weight, norm2.bias, norm2.eps)
         if attention.config.q_dictionary_feedforward:
