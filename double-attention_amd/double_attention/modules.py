@@ -207,27 +207,8 @@ class SharedDictionaryAttention(nn.Module):
         query, key = fused.split(self.config.total_qk_width, dim=-1)
         return self._reshape_branches(query, batch, length), self._reshape_branches(key, batch, length)
 
-    def _hip_route_backward_fits(self, rows: Tensor, atoms: int) -> bool:
-        """Whether a native route backward (either path) takes these rows and atoms."""
-
-        from . import hip_ops
-
-        variant = hip_ops.RouteVariant.of_config(self.config)
-        keys = torch.empty(rows.shape[-1], atoms, device="meta")
-        return hip_ops._route_backward_supported(rows, keys, variant) or hip_ops._route_backward_rows_supported(rows, keys)
-
-    def _route(self, x: Tensor, dictionary_key: Tensor, dictionary_value: Tensor, backend: str) -> Tensor:
+    def _route(self, x: Tensor, dictionary_key: Tensor, dictionary_value: Tensor) -> Tensor:
         cfg = self.config
-        if backend == "hip":
-            from .hip_ops import dictionary_route_hip
-
-            return dictionary_route_hip(
-                x, dictionary_key, dictionary_value, self.beta, cfg.eps,
-                cfg.dictionary_activation == "silu", cfg.dictionary_assignment == "silu",
-                cfg.dictionary_silu_gain, cfg.standardize_dictionary_logits,
-                cfg.standardized_logit_scale, cfg.normalize_routing_input,
-                cfg.normalize_routing_output,
-            )
         return dictionary_route_reference(
             x, dictionary_key, dictionary_value, self.beta, cfg.eps,
             cfg.dictionary_activation, cfg.dictionary_assignment, cfg.dictionary_silu_gain,
@@ -235,20 +216,12 @@ class SharedDictionaryAttention(nn.Module):
             cfg.normalize_routing_input, cfg.normalize_routing_output,
         )
 
-    def _combine(self, x: Tensor, map_output: Tensor, fp32_weight_grad: bool = False) -> tuple[Tensor, Tensor]:
+    def _combine(self, x: Tensor, map_output: Tensor) -> tuple[Tensor, Tensor]:
         if self.config.map_combine == "weighted_sum":
             if self.map_mix_logits is None:
                 return self.output(map_output[:, 0]), x.new_ones(1)
             weights = torch.softmax(self.map_mix_logits, dim=0).to(map_output.dtype)
             factors = weights.float()
-            if fp32_weight_grad:
-                # Same forward value (the weights rounded to the map dtype),
-                # but the gradient reaches the logits in fp32: the per-map
-                # gradients sum dY.O_s are large and nearly equal, and their
-                # softmax backward takes differences that a 16-bit rounding
-                # of each would swamp.
-                exact = torch.softmax(self.map_mix_logits.float(), dim=0)
-                factors = exact + (factors - exact).detach()
             # The weighted map sum in fp32, rounded once (as einsum's fp32
             # accumulation does), without einsum's internal transposed bmm.
             combined = (map_output.float() * factors[None, :, None, None]).sum(1).to(map_output.dtype)
@@ -262,7 +235,6 @@ class SharedDictionaryAttention(nn.Module):
         dictionary_key: Tensor,
         dictionary_value: Tensor,
         return_aux: bool,
-        attention: str = "torch",
     ) -> Tensor | tuple[Tensor, DoubleAttentionAux]:
         query, key = self._project_query_key(x)
         dense_value = self.value(x)
@@ -273,24 +245,12 @@ class SharedDictionaryAttention(nn.Module):
             dictionary_value = dictionary_value.to(query.dtype)
         # Q and K tokens route together, as one batch of rows (modules.py:236-241).
         pair = torch.cat((query, key), dim=2)
-        # The HIP backward's recompute routes on the library's kernel when the
-        # native route backward covers this configuration.
-        route_backend = (
-            "hip" if attention == "hip" and self._hip_route_backward_fits(pair, dictionary_key.shape[1]) else "torch"
-        )
-        routed = self._route(pair, dictionary_key, dictionary_value, route_backend)
+        routed = self._route(pair, dictionary_key, dictionary_value)
         routed_query, routed_key = routed.split(x.shape[1], dim=2)
         score_query, score_key = assemble_score_maps(routed_query, routed_key, self.config.outer_maps)
         scales = score_scale_from_log(self.log_score_scales)
-        if attention == "hip" and _hip_attention_backward_fits(score_query, dense_value):
-            # The HIP backward's recompute: the outer attention on the library's
-            # forward kernel, so its autograd runs the native backward kernels.
-            from . import hip_ops
-
-            map_output = hip_ops.routed_attention_hip(score_query, score_key, dense_value, scales, self.config.causal)
-        else:
-            map_output = routed_attention_reference(score_query, score_key, dense_value, scales, self.config.causal)
-        output, weights = self._combine(x, map_output, fp32_weight_grad=attention == "hip")
+        map_output = routed_attention_reference(score_query, score_key, dense_value, scales, self.config.causal)
+        output, weights = self._combine(x, map_output)
         if not return_aux:
             return output
         return output, DoubleAttentionAux(
@@ -684,21 +644,6 @@ class _HipModuleFunction(torch.autograd.Function):
             for name in ctx.param_names
         ]
         return (None, None, dx, d_key, d_val, *tail)
-
-
-def _hip_attention_backward_fits(score_query: Tensor, value: Tensor) -> bool:
-    """Whether the native attention backward takes these score-map operands."""
-
-    from . import hip_ops
-
-    halves = (torch.float16, torch.bfloat16)
-    return (
-        score_query.is_cuda
-        and score_query.dtype in halves
-        and value.dtype in halves
-        and (score_query.dtype == value.dtype or score_query.dtype == torch.float16)
-        and hip_ops._native_backward_supported(score_query, value)
-    )
 
 
 class DoubleAttentionBlock(nn.Module):

@@ -129,6 +129,25 @@ def test_dictionary_normalize_backward(raw_dtype, routing_dim, atoms, tied) -> N
 # ---------------------------------------------------------------- GEMMs
 
 
+@pytest.mark.parametrize(("k", "m", "n", "ld"), [(300, 64, 96, 64), (16384, 512, 1536, 512), (8192, 256, 512, 768)])
+def test_weight_gradient_product(k, m, n, ld) -> None:
+    # a^T b for the weight gradients (split over K into batched fp32 partials
+    # when K is long and the output small; a with a row pitch above its width
+    # as the module passes column slices) against fp64.
+    device = _device()
+    g = torch.Generator().manual_seed(k + m)
+    a_full = torch.randn(k, ld, generator=g).to(device, torch.bfloat16)
+    a = a_full[:, :m]
+    b = torch.randn(k, n, generator=g).to(device, torch.bfloat16)
+    got = da.hip_ops._mm_tn_f32(a, b)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32 and got.shape == (m, n)
+    expected = np32(a).astype(np.float64).T @ np32(b).astype(np.float64)
+    rel = np.linalg.norm(np32(got) - expected) / np.linalg.norm(expected)
+    print(f"[parity] a^T b {k}x{m}x{n} rel_l2={rel:.2e}", flush=True)
+    assert rel <= 1e-5   # fp32 accumulation of exact 16-bit products
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize(("rows", "k", "n", "bias"), [(33, 64, 96, False), (300, 512, 512, True), (4096, 512, 512, False)])
 def test_linear(dtype, rows, k, n, bias) -> None:

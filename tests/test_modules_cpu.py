@@ -255,3 +255,56 @@ def test_backward_dispatch_rules() -> None:
     # The row-kernel path takes every width and variant up to 4096 atoms, on the GPU only.
     assert not hip_ops._route_backward_rows_supported(meta, key)
     assert hip_ops.ROUTE_BACKWARD_ROWS_MAX_ATOMS == 4096
+    # route_backward_is_native: the module's choice of the raw-bank path.
+    assert hip_ops.route_backward_is_native(256, 512, torch.bfloat16, standard)
+    assert hip_ops.route_backward_is_native(512, 1536, torch.float16, silu)
+    assert hip_ops.route_backward_is_native(128, 4096, torch.bfloat16, silu)
+    assert not hip_ops.route_backward_is_native(512, 4097, torch.bfloat16, standard)
+    assert not hip_ops.route_backward_is_native(256, 512, torch.float32, standard)
+    assert not hip_ops.route_backward_is_native(96, 512, torch.bfloat16, silu)
+
+
+@pytest.mark.parametrize("shape", [(7, 5), (3, 64)])
+def test_normalize_backward_matches_autograd(shape) -> None:
+    # The closed form the route backward uses for F.normalize's backward
+    # (rows, with one row below eps) against torch autograd in fp64.
+    from double_attention import hip_ops
+
+    g = torch.Generator().manual_seed(5)
+    v = torch.randn(*shape, generator=g, dtype=torch.float64)
+    v[1] *= 1e-9
+    h = torch.randn(*shape, generator=g, dtype=torch.float64)
+    eps = 1e-6
+    vv = v.clone().requires_grad_()
+    (torch.nn.functional.normalize(vv, dim=1, eps=eps) * h).sum().backward()
+    norm = torch.linalg.vector_norm(v, dim=1, keepdim=True)
+    got = hip_ops._normalize_backward(v, norm, h, eps, torch.float64)
+    torch.testing.assert_close(got, vv.grad, rtol=1e-10, atol=1e-12)
+
+
+def test_auto_backend_picks_torch_for_uncovered_configs() -> None:
+    # backend="auto" keeps a configuration the kernels do not cover on torch;
+    # "hip" raises for it instead (host logic: no GPU needed).
+    assert modules._hip_covers(da.experiment_config("a1"))
+    assert not modules._hip_covers(da.experiment_config("a1", routing_dim=96))
+    assert not modules._hip_covers(da.experiment_config("a1", model_dim=384))
+
+
+def test_module_operands_follow_parameter_updates() -> None:
+    # The cast operands of the fused forward are reused while the parameters
+    # are unchanged and rebuilt after an in-place update (version counter) or
+    # a new tensor (data pointer).
+    from double_attention import hip_ops
+
+    module = da.SharedDictionaryAttention(da.experiment_config("a1"))
+    first = hip_ops._module_operands(module, torch.bfloat16)
+    assert hip_ops._module_operands(module, torch.bfloat16) is first
+    with torch.no_grad():
+        module.query.weight.mul_(2.0)
+    second = hip_ops._module_operands(module, torch.bfloat16)
+    assert second is not first
+    torch.testing.assert_close(second[0], module.query.weight.detach().to(torch.bfloat16))
+    module.key.weight = torch.nn.Parameter(torch.zeros_like(module.key.weight))
+    third = hip_ops._module_operands(module, torch.bfloat16)
+    assert third is not second and torch.count_nonzero(third[1]) == 0
+    assert hip_ops._module_operands(module, torch.float16)[0].dtype == torch.float16
