@@ -778,6 +778,9 @@ MODULE_BACKWARD_CASES = [
     ("qk2-s1", {}, 40),
     ("a1", {"outer_maps": 2}, 40),
     ("qk2-s2", {"map_combine": "concat"}, 40),
+    # Tied banks: the key atoms' raw gradient collects both roles.
+    ("a1", {"untied_dictionary": False}, 40),
+    ("a1-r512-d1536", {"untied_dictionary": False}, 40),
 ]
 
 
