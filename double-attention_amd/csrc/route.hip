@@ -344,7 +344,10 @@ __global__ __launch_bounds__(kRouteWaves * 64, R >= 512 || SUB == 2 ? 1 : 2) voi
       const float lmax = fmaxf(fmaxf(fmaxf(st_prev[0][0], st_prev[0][1]), fmaxf(st_prev[0][2], st_prev[0][3])),
                                fmaxf(fmaxf(st_prev[1][0], st_prev[1][1]), fmaxf(st_prev[1][2], st_prev[1][3])));
       lazy_rescale<RB>(lmax, scale, m_run, l_part, acc);
-      m_use = -m_run;
+      // A sub-stream whose tiles so far are all padding (with at most 32
+      // atoms, the odd one's only tile) keeps the reference at -inf: its
+      // weights are exp2(-inf) = 0 and the merge gives it factor 0.
+      m_use = m_run == -INFINITY ? 0.f : -m_run;
     }
 
     wait_vmem();

@@ -245,6 +245,8 @@ def test_route_flags_odd_rows(dtype, normalize_input, normalize_output) -> None:
     (256, 100, 77, 4.0),            # atom count that is not a tile multiple
     (512, 2855, 333, 5.0),
     (128, 300, 500, 12.0),          # beta past the fixed-reference range: online rescaling
+    (64, 30, 50, -4.0),             # the last 32-atom tile is all padding; negative beta
+    (256, 1000, 3000, 4.0),
 ])
 def test_route_shapes(dtype, normalized_bank, routing_dim, atoms, rows, beta) -> None:
     # normalized_bank: the bank comes from dictionary_normalize_hip, whose unit
