@@ -115,7 +115,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 16; }
+int da_abi_version(void) { return 17; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -156,6 +156,55 @@ int da_dictionary_normalize_backward(const void* raw_key, const void* raw_value,
                           grad_key, grad_value, d_raw_key, d_raw_value};
   da::launch_dictionary_normalize_backward(a, reinterpret_cast<hipStream_t>(stream));
   return check_launch("normalize backward");
+}
+
+namespace {
+
+int validate_row_norm(const char* what, const void* x, int x_dtype, int64_t rows, int64_t width, int64_t ld_x,
+                      float eps, const void* grad, int grad_dtype, int64_t ld_grad, bool backward, const void* out,
+                      int out_dtype, int64_t ld_out) {
+  if (!any_dtype(x_dtype) || !any_dtype(out_dtype) || (backward && !any_dtype(grad_dtype)))
+    return fail(DA_ERR_INVALID_ARGUMENT, "%s: bad dtype", what);
+  if (rows < 0 || rows > 0x7fffffffLL * 4) return fail(DA_ERR_INVALID_ARGUMENT, "%s: bad row count", what);
+  if (width < 4 || width > (1 << 20) || width % 4)
+    return fail(DA_ERR_UNSUPPORTED, "%s: width %lld must be a positive multiple of 4", what, (long long)width);
+  if (!(eps >= 0.f)) return fail(DA_ERR_INVALID_ARGUMENT, "%s: eps must be >= 0", what);
+  if (!x || !out || (backward && !grad)) return fail(DA_ERR_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (ld_x < width || ld_out < width || (backward && ld_grad < width) || ld_x % 4 || ld_out % 4 ||
+      (backward && ld_grad % 4))
+    return fail(DA_ERR_ALIGNMENT, "%s: row pitches must be >= width and multiples of 4", what);
+  const auto elem = [](int d) { return d == DA_F32 ? 4 : 2; };
+  if (reinterpret_cast<uintptr_t>(x) % (4 * elem(x_dtype)) || reinterpret_cast<uintptr_t>(out) % (4 * elem(out_dtype)) ||
+      (backward && reinterpret_cast<uintptr_t>(grad) % (4 * elem(grad_dtype))))
+    return fail(DA_ERR_ALIGNMENT, "%s: tensors must be aligned to 4 elements", what);
+  return 0;
+}
+
+}  // namespace
+
+int da_row_normalize(const void* x, int x_dtype, int64_t rows, int64_t width, int64_t ld_x, float eps, void* out,
+                     int out_dtype, int64_t ld_out, da_stream_t stream) {
+  int rc = validate_row_norm("row normalize", x, x_dtype, rows, width, ld_x, eps, nullptr, DA_F32, 0, false, out,
+                             out_dtype, ld_out);
+  if (rc) return rc;
+  if (rows == 0) return ok();
+  const da::RowNormArgs a{x, x_dtype, ld_x, rows, static_cast<int>(width), eps, nullptr, DA_F32, 0, out, out_dtype,
+                          ld_out};
+  da::launch_row_normalize(a, false, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("row normalize");
+}
+
+int da_row_normalize_backward(const void* x, int x_dtype, int64_t rows, int64_t width, int64_t ld_x, float eps,
+                              const void* grad, int grad_dtype, int64_t ld_grad, void* grad_x, int out_dtype,
+                              int64_t ld_out, da_stream_t stream) {
+  int rc = validate_row_norm("row normalize backward", x, x_dtype, rows, width, ld_x, eps, grad, grad_dtype, ld_grad,
+                             true, grad_x, out_dtype, ld_out);
+  if (rc) return rc;
+  if (rows == 0) return ok();
+  const da::RowNormArgs a{x, x_dtype, ld_x, rows, static_cast<int>(width), eps, grad, grad_dtype, ld_grad, grad_x,
+                          out_dtype, ld_out};
+  da::launch_row_normalize(a, true, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("row normalize backward");
 }
 
 int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_t x_row_stride,

@@ -147,6 +147,17 @@ struct NormBwdArgs {
 };
 void launch_dictionary_normalize_backward(const NormBwdArgs& a, hipStream_t stream);
 
+// Row L2 normalization and its backward (row_norm.hip).  R % 4 == 0; row
+// pitches multiples of 4 elements; x, grad and out aligned to 4 elements.
+// Arithmetic in fp32 whatever the element types.
+struct RowNormArgs {
+  const void* x; int x_dtype; int64_t ld_x;
+  int64_t rows; int R; float eps;
+  const void* grad; int grad_dtype; int64_t ld_grad;   // backward only: dL/dy
+  void* out; int out_dtype; int64_t ld_out;
+};
+void launch_row_normalize(const RowNormArgs& a, bool backward, hipStream_t stream);
+
 // Row-wise backward of the route's assignment (route_bwd.hip).
 struct RouteBwdRowsArgs {
   const float* logits;        // [rows, ld_in] raw logits <u, Dk_j>

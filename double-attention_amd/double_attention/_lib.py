@@ -47,7 +47,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 NOALLOC_SCRATCH_BYTES = 128 << 20
 
 _vp = ctypes.c_void_p
@@ -103,6 +103,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_padded_length": (_i64, [_i64]),
     "da_dictionary_normalize": (_i32, [_vp, _vp, _i32, _i64, _i64, _f32, _vp, _i32, _vp, _vp, _vp]),
     "da_dictionary_normalize_backward": (_i32, [_vp, _vp, _i32, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp]),
+    "da_row_normalize": (_i32, [_vp, _i32, _i64, _i64, _i64, _f32, _vp, _i32, _i64, _vp]),
+    "da_row_normalize_backward": (_i32, [_vp, _i32, _i64, _i64, _i64, _f32, _vp, _i32, _i64, _vp, _i32, _i64, _vp]),
     "da_dictionary_route": (
         _i32,
         [

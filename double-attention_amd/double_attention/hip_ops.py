@@ -376,31 +376,45 @@ def _route_backward_supported(x: Tensor, dictionary_key: Tensor, variant: RouteV
     )
 
 
-def _row_norm(rows: Tensor) -> Tensor:
-    """Per-row L2 norms ``[n, 1]`` in fp32 (one pass over 16-bit or fp32 rows)."""
+def _row_normalize(rows: Tensor, eps: float, dtype: torch.dtype) -> Tensor:
+    """``F.normalize(rows, dim=-1, eps)`` of ``[n, R]`` rows (``ops.py:39, 62``):
+    fp32 arithmetic, one rounding to ``dtype`` (``da_row_normalize``)."""
 
-    return torch.linalg.vector_norm(rows, dim=1, keepdim=True, dtype=torch.float32)
+    rows = _aligned(rows)
+    n, width = rows.shape
+    out = torch.empty(n, width, dtype=dtype, device=rows.device)
+    lib = _lib.get()
+    _lib.check(
+        lib.da_row_normalize(
+            rows.data_ptr(), dtype_code(rows.dtype), n, width, width, float(eps), out.data_ptr(), dtype_code(dtype),
+            width, _stream(rows.device),
+        ),
+        "row normalize",
+    )
+    return out
 
 
-def _scaled_rows(rows: Tensor, factor: Tensor, dtype: torch.dtype) -> Tensor:
-    """``rows * factor`` ([n, R] by [n, 1]) computed in fp32, rounded once to ``dtype``."""
-
-    return torch.mul(rows, factor, out=torch.empty(rows.shape, dtype=dtype, device=rows.device))
-
-
-def _normalize_backward(v: Tensor, norm: Tensor, h: Tensor, eps: float, dtype: torch.dtype) -> Tensor:
+def _normalize_backward(v: Tensor, h: Tensor, eps: float, dtype: torch.dtype) -> Tensor:
     """The backward of N(v) = v / max(|v|, eps) (``F.normalize``) at gradient h.
 
-    (h - n <n, h>) / |v| with n = v / |v| where |v| > eps, h / eps elsewhere;
-    written as h i - v (<v, h> i^3 [|v| > eps]) with i = 1 / max(|v|, eps), in
-    fp32 and rounded once to ``dtype``.  ``norm`` is |v| as ``[n, 1]`` fp32;
-    ``h`` is fp32 (so every product of <v, h> is an fp32 product).
+    (h - n <n, h>) / |v| with n = v / |v| where |v| > eps, h / eps elsewhere,
+    for ``[n, R]`` rows v and h: one pass of ``da_row_normalize_backward``,
+    fp32 arithmetic, one rounding to ``dtype``.
     """
 
-    inv = norm.clamp_min(eps).reciprocal()
-    coef = (v * h).sum(1, keepdim=True) * torch.where(norm > eps, inv.pow(3), 0.0)
-    out = torch.empty(h.shape, dtype=dtype, device=h.device)
-    return torch.addcmul(h * inv, v, coef, value=-1.0, out=out)
+    v = _aligned(v)
+    h = _aligned(h)
+    n, width = v.shape
+    out = torch.empty(n, width, dtype=dtype, device=v.device)
+    lib = _lib.get()
+    _lib.check(
+        lib.da_row_normalize_backward(
+            v.data_ptr(), dtype_code(v.dtype), n, width, width, float(eps), h.data_ptr(), dtype_code(h.dtype), width,
+            out.data_ptr(), dtype_code(dtype), width, _stream(v.device),
+        ),
+        "row normalize backward",
+    )
+    return out
 
 
 def _route_backward(
@@ -437,9 +451,8 @@ def _route_backward(
     # keys; raw 16-bit rows in their own dtype with keys in that dtype (the
     # backward kernels recompute P from the same values the forward used).
     if normalize_input:
-        x_norm = _row_norm(rows)
         qk_type = torch.float16
-        u16 = _scaled_rows(rows, x_norm.clamp_min(eps).reciprocal(), qk_type)
+        u16 = _row_normalize(rows, eps, qk_type)
     else:
         qk_type = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
         u16 = _aligned(rows.to(qk_type))
@@ -448,14 +461,13 @@ def _route_backward(
         layout16 = route_layout(dictionary_key.detach(), dictionary_value.detach(), qk_type)
         r = _route_forward(u16, layout16, beta_t, eps, False, False, RouteVariant())
     r = r.reshape(-1, routing_dim)
-    # fp32 gradient rows: the output norm's backward takes <r, g> of fp32 products.
-    g = grad.detach().reshape(-1, routing_dim).float()
+    g = grad.detach().reshape(-1, routing_dim)
     # Values, r and dr in fp16 for fp16 inputs (8x finer than bf16: with the
     # output norm, rowsum(dr . r) is analytically zero and its rounding noise
     # reaches every atom's gradient), bf16 for bf16 inputs.
     v_type = torch.float16 if x.dtype == torch.float16 else torch.bfloat16
     if normalize_output:
-        go = _normalize_backward(r, _row_norm(r), g, eps, v_type)
+        go = _normalize_backward(r, g, eps, v_type)
     else:
         go = _aligned(g.to(v_type))
     keys = _aligned(dictionary_key.detach().t().to(qk_type))
@@ -477,7 +489,7 @@ def _route_backward(
         ),
         "dictionary_route_hip backward",
     )
-    dx = _normalize_backward(rows, x_norm, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
+    dx = _normalize_backward(rows, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
     return (
         dx.reshape(x.shape),
         dkt.t().to(bank_grad_dtype or dictionary_key.dtype),
@@ -588,11 +600,9 @@ def _route_backward_rows(
     # 16-bit operands of the GEMMs: fp16 for fp16 inputs, bf16 for bf16 ones.
     v_type = torch.float16 if x.dtype == torch.float16 else torch.bfloat16
     if normalize_input:
-        x_norm = _row_norm(rows)
-        inv_x = x_norm.clamp_min(eps).reciprocal()
         key_type = torch.float16
-        u_h = _scaled_rows(rows, inv_x, key_type)
-        u_v = u_h if v_type == key_type else _scaled_rows(rows, inv_x, v_type)
+        u_h = _row_normalize(rows, eps, key_type)
+        u_v = u_h if v_type == key_type else _row_normalize(rows, eps, v_type)
     else:
         key_type = x.dtype
         u_h = u_v = rows
@@ -601,12 +611,11 @@ def _route_backward_rows(
         layout = route_layout(dictionary_key.detach(), dictionary_value.detach(), key_type)
         r = _route_forward(u_h, layout, beta_t, eps, False, False, variant)
     r = r.reshape(-1, routing_dim)
-    # fp32 gradient rows: the output norm's backward takes <r, g> of fp32 products.
-    g = grad.detach().reshape(-1, routing_dim).float()
+    g = grad.detach().reshape(-1, routing_dim)
     # dW = dr Dv takes dr as a 16-bit head and its rounding residual ([n, 2R]
     # against [Dv; Dv]): the softmax backward differences dW_j - sum_k w_k dW_k,
     # so one 16-bit rounding of dr would reach every atom's gradient.
-    dr = _normalize_backward(r, _row_norm(r), g, eps, torch.float32) if normalize_output else g
+    dr = _normalize_backward(r, g, eps, torch.float32) if normalize_output else g.float()
     dr2 = torch.empty(n, 2 * routing_dim, dtype=v_type, device=device)
     dr_v = dr2[:, :routing_dim]
     dr_v.copy_(dr)
@@ -636,7 +645,7 @@ def _route_backward_rows(
     d_key = _mm_tn_f32(u_v, grad_logits)
     d_value = _mm_tn_f32(dr_v, weights)
     dbeta = dbeta_rows.sum().reshape(1)
-    dx = _normalize_backward(rows, x_norm, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
+    dx = _normalize_backward(rows, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
     return (
         dx.reshape(x.shape),
         d_key.to(bank_grad_dtype or dictionary_key.dtype),

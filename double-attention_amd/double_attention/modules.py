@@ -490,7 +490,7 @@ class _HipModuleFunction(torch.autograd.Function):
         )
         if cfg.normalize_routing_output:
             # F.normalize in fp32, one rounding to fp16.
-            routed = hip_ops._scaled_rows(recon, hip_ops._row_norm(recon).clamp_min(cfg.eps).reciprocal(), torch.float16)
+            routed = hip_ops._row_normalize(recon, cfg.eps, torch.float16)
         else:
             routed = recon
         score_query, score_key = _HipModuleFunction._score_maps(routed, batch, length, branches, maps, routing_dim)

@@ -19,6 +19,8 @@
  *   da_dictionary_normalize   SharedDictionaryBank.normalized        src/double_attention/modules.py:45-48
  *   da_dictionary_normalize_backward
  *                             autograd of SharedDictionaryBank.normalized  src/double_attention/modules.py:45-48
+ *   da_row_normalize          F.normalize of the route's rows        src/double_attention/ops.py:39, 62; triton_kernels.py:1286-1308
+ *   da_row_normalize_backward _row_l2_normalize_backward             src/double_attention/triton_kernels.py:553-586, 1410-1440
  *   da_dictionary_route       dictionary_route_triton / _reference   src/double_attention/triton_kernels.py:1984-2019, ops.py:16-62
  *   da_dictionary_route_backward_rows
  *                             _row_scaled_softmax_backward_kernel    src/double_attention/triton_kernels.py:589-671, 1480
@@ -137,6 +139,30 @@ int da_dictionary_normalize_backward(const void* raw_key, const void* raw_value,
                                      int64_t routing_dim, int64_t atoms, float eps, const float* grad_key,
                                      const float* grad_value, void* d_raw_key, void* d_raw_value,
                                      da_stream_t stream);
+
+/*
+ * Row L2 normalization, F.normalize(x, dim=-1, eps) (ops.py:39, :62; the
+ * reference's Triton _row_l2_normalize, triton_kernels.py:30-45, 1286-1308):
+ *   out[i, :] = x[i, :] / max(|x[i, :]|, eps), computed in fp32 and rounded
+ *   once to out_dtype.
+ *   x: [rows, width] with row pitch ld_x, x_dtype; out: [rows, width], pitch
+ *   ld_out, out_dtype.  width, ld_x and ld_out multiples of 4; x and out
+ *   aligned to 4 elements.
+ */
+int da_row_normalize(const void* x, int x_dtype, int64_t rows, int64_t width, int64_t ld_x, float eps, void* out,
+                     int out_dtype, int64_t ld_out, da_stream_t stream);
+
+/*
+ * Backward of da_row_normalize (autograd of F.normalize; the reference's
+ * _row_l2_normalize_backward, triton_kernels.py:553-586, 1410-1440): from x
+ * and grad = dL/dout (grad_dtype, pitch ld_grad), grad_x = (grad - y <y,
+ * grad>) / |x| with y = x / |x| where |x| > eps, grad / eps elsewhere; fp32
+ * arithmetic, rounded once to out_dtype.  Same layout rules as
+ * da_row_normalize, grad included.
+ */
+int da_row_normalize_backward(const void* x, int x_dtype, int64_t rows, int64_t width, int64_t ld_x, float eps,
+                              const void* grad, int grad_dtype, int64_t ld_grad, void* grad_x, int out_dtype,
+                              int64_t ld_out, da_stream_t stream);
 
 /*
  * Fused dictionary route (ops.py:16-62), for any number of rows:

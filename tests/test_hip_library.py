@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 20
+    assert len(names) == 22
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -253,3 +253,31 @@ def test_normalize_backward_rejects_bad_arguments() -> None:
     assert b"null" in h.da_last_error()
     assert call(raw_value=None) == -1                   # d_raw_value for a tied bank
     assert b"tied" in h.da_last_error()
+
+
+def test_row_normalize_rejects_bad_arguments() -> None:
+    h = lib.get()
+    buf = ctypes.c_void_p(1 << 20)   # never dereferenced
+
+    def fwd(**kw):
+        args = dict(x=buf, x_dtype=lib.DA_BF16, rows=10, width=256, ld_x=256, eps=1e-6, out=buf,
+                    out_dtype=lib.DA_F16, ld_out=256, stream=None)
+        args.update(kw)
+        return h.da_row_normalize(*args.values())
+
+    def bwd(**kw):
+        args = dict(x=buf, x_dtype=lib.DA_F16, rows=10, width=256, ld_x=256, eps=1e-6, grad=buf,
+                    grad_dtype=lib.DA_F32, ld_grad=256, grad_x=buf, out_dtype=lib.DA_BF16, ld_out=256, stream=None)
+        args.update(kw)
+        return h.da_row_normalize_backward(*args.values())
+
+    assert fwd(x_dtype=7) == -1 and bwd(grad_dtype=7) == -1
+    assert fwd(width=6) == -2 and b"multiple of 4" in h.da_last_error()
+    assert fwd(eps=-1.0) == -1
+    assert fwd(x=None) == -1 and bwd(grad=None) == -1
+    assert b"null" in h.da_last_error()
+    assert fwd(ld_x=128) == -3 and bwd(ld_grad=258) == -3
+    assert fwd(x=ctypes.c_void_p((1 << 20) + 2)) == -3                     # 4 bf16 elements are 8 bytes
+    assert bwd(grad=ctypes.c_void_p((1 << 20) + 8)) == -3 and b"aligned" in h.da_last_error()
+    assert fwd(rows=0, x=None) == -1                                      # null checked before the empty case
+    assert fwd(rows=0) == 0 and bwd(rows=0) == 0                          # nothing to do

@@ -126,6 +126,61 @@ def test_dictionary_normalize_backward(raw_dtype, routing_dim, atoms, tied) -> N
                           expected[:, 1:] * col, 5e-3, 4e-2, "bank backward")
 
 
+ROW_NORM_CASES = [
+    # (rows, width, x dtype, grad dtype, out dtype, row pitch)
+    (1000, 256, torch.float16, torch.float32, torch.bfloat16, 256),
+    (333, 64, torch.bfloat16, torch.bfloat16, torch.float32, 64),
+    (77, 512, torch.float32, torch.float16, torch.float16, 520),
+    (5, 4, torch.bfloat16, torch.float32, torch.float32, 4),
+]
+
+
+@pytest.mark.parametrize("case", ROW_NORM_CASES, ids=lambda c: f"n{c[0]}w{c[1]}ld{c[5]}")
+def test_row_normalize_and_backward(case) -> None:
+    # Rows (one of them zero: the eps branch) spanning three orders of
+    # magnitude in norm; the forward against x / max(|x|, eps) in fp64, the
+    # backward against the oracle's column-normalization backward applied to
+    # the transposed rows, both on the same rounded inputs.
+    rows, width, x_dtype, g_dtype, out_dtype, ld = case
+    device = _device()
+    eps = 1e-6
+    gen = torch.Generator().manual_seed(rows + width)
+    x = torch.randn(rows, ld, generator=gen) * torch.logspace(-1.5, 1.5, rows)[:, None]
+    x[min(1, rows - 1)] = 0.0
+    x = x.to(device, x_dtype)
+    h = torch.randn(rows, ld, generator=gen).to(device, g_dtype)
+    lib = da._lib.get()
+    out = torch.empty(rows, ld, dtype=out_dtype, device=device)
+    code = da.hip_ops.dtype_code
+    stream = da.hip_ops._stream(device)
+    da._lib.check(lib.da_row_normalize(x.data_ptr(), code(x_dtype), rows, width, ld, eps, out.data_ptr(),
+                                       code(out_dtype), ld, stream), "row normalize")
+    dx = torch.empty(rows, ld, dtype=out_dtype, device=device)
+    da._lib.check(lib.da_row_normalize_backward(x.data_ptr(), code(x_dtype), rows, width, ld, eps, h.data_ptr(),
+                                                code(g_dtype), ld, dx.data_ptr(), code(out_dtype), ld, stream),
+                  "row normalize backward")
+    torch.cuda.synchronize()
+    xv = np32(x[:, :width]).astype(np.float64)
+    hv = np32(h[:, :width]).astype(np.float64)
+    expected = xv / np.maximum(np.linalg.norm(xv, axis=1, keepdims=True), eps)
+    assert_parity(out[:, :width], expected, label="row normalize")
+    ek, _ = oracle.bank_normalized_backward(xv.T, None, hv.T, np.zeros_like(hv.T), eps)
+    norms = np.maximum(np.linalg.norm(xv, axis=1), eps)
+    zero = min(1, rows - 1)
+    # The zero row is the plain gradient over eps (about 1e6: inf in fp16,
+    # as the rounding of that value is); the others relative to 1 / |x|.
+    torch.testing.assert_close(dx[zero, :width].float(), (h[zero, :width].float() / eps).to(out_dtype).float(),
+                               rtol=8e-3, atol=0.0)
+    keep = np.arange(rows) != zero
+    scale = torch.as_tensor(norms[keep], device=device, dtype=torch.float32)[:, None]
+    assert_parity(dx[keep][:, :width].float() * scale, ek.T[keep] * norms[keep, None], label="row normalize backward")
+    # The wrappers the route backward uses: contiguous rows, same kernels.
+    if ld == width:
+        wrapped = da.hip_ops._normalize_backward(x, h, eps, out_dtype)
+        assert torch.equal(wrapped, dx)
+        assert torch.equal(da.hip_ops._row_normalize(x, eps, out_dtype), out)
+
+
 # ---------------------------------------------------------------- GEMMs
 
 

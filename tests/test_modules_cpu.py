@@ -264,24 +264,6 @@ def test_backward_dispatch_rules() -> None:
     assert not hip_ops.route_backward_is_native(96, 512, torch.bfloat16, silu)
 
 
-@pytest.mark.parametrize("shape", [(7, 5), (3, 64)])
-def test_normalize_backward_matches_autograd(shape) -> None:
-    # The closed form the route backward uses for F.normalize's backward
-    # (rows, with one row below eps) against torch autograd in fp64.
-    from double_attention import hip_ops
-
-    g = torch.Generator().manual_seed(5)
-    v = torch.randn(*shape, generator=g, dtype=torch.float64)
-    v[1] *= 1e-9
-    h = torch.randn(*shape, generator=g, dtype=torch.float64)
-    eps = 1e-6
-    vv = v.clone().requires_grad_()
-    (torch.nn.functional.normalize(vv, dim=1, eps=eps) * h).sum().backward()
-    norm = torch.linalg.vector_norm(v, dim=1, keepdim=True)
-    got = hip_ops._normalize_backward(v, norm, h, eps, torch.float64)
-    torch.testing.assert_close(got, vv.grad, rtol=1e-10, atol=1e-12)
-
-
 def test_auto_backend_picks_torch_for_uncovered_configs() -> None:
     # backend="auto" keeps a configuration the kernels do not cover on torch;
     # "hip" raises for it instead (host logic: no GPU needed).
