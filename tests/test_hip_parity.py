@@ -408,6 +408,10 @@ def test_route_variants(dtype, variant, normalize_input, normalize_output, routi
     (1, 2, 300, 512, 128, (10.0, 13.0)),  # 512-wide scores: four-wave workgroups
     (1, 1, 2000, 64, 128, (12.0,)),       # long key ranges: stream split and merge, ragged tail
     (1, 1, 1000, 512, 128, (14.0,)),      # stream split with four-wave workgroups, ragged tail
+    # One map, 256- and 512-wide values: two sub-streams over even and odd key tiles.
+    (8, 1, 512, 256, 512, (16.0,)),       # C1's attention
+    (2, 1, 300, 128, 256, (12.0,)),       # ragged tail
+    (3, 1, 77, 64, 512, (64.0,)),         # scaled bound past the fixed range: online rescaling
 ])
 def test_routed_attention(dtype, causal, score_bound, batch, maps, length, score_dim, value_dim, scales) -> None:
     # Rows are unit vectors, so 1.01 bounds every score: bf16 maps whose scaled
