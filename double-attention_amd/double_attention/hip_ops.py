@@ -709,7 +709,7 @@ def route_gradients(
         wrt = [t for t in inputs if t.requires_grad]
         if isinstance(beta_in, Tensor) and beta_in.requires_grad:
             wrt.append(beta_in)
-        grads = torch.autograd.grad(out, wrt, grad, allow_unused=True) if wrt else ()
+        grads = torch.autograd.grad(out, wrt, grad.to(out.dtype), allow_unused=True) if wrt else ()
     it = iter(grads)
     result = [next(it) if t.requires_grad else None for t in inputs]
     beta_grad = next(it) if isinstance(beta_in, Tensor) and beta_in.requires_grad else None
@@ -867,7 +867,8 @@ def _padded_rows(t: Tensor, width: int) -> Tensor:
 
 
 def _attention_backward(
-    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, out: Tensor, grad: Tensor, causal: bool
+    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, out: Tensor, grad: Tensor, causal: bool,
+    qk_grad_dtype: torch.dtype | None = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients of ``routed_attention_reference`` on the library's backward kernels.
 
@@ -911,8 +912,8 @@ def _attention_backward(
     )
     shape = (batch, maps, length, score_width)
     return (
-        dq.view(shape)[..., :score_dim].to(query.dtype),
-        dk.view(shape)[..., :score_dim].to(key.dtype),
+        dq.view(shape)[..., :score_dim].to(qk_grad_dtype or query.dtype),
+        dk.view(shape)[..., :score_dim].to(qk_grad_dtype or key.dtype),
         dv[..., :model_dim].to(value.dtype),
         dg.to(scales.dtype),
     )
@@ -943,7 +944,8 @@ def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
 
 
 def _attention_backward_dense(
-    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, grad: Tensor, causal: bool
+    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, grad: Tensor, causal: bool,
+    qk_grad_dtype: torch.dtype | None = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Outer-attention gradients with the score matrices materialized.
 
@@ -990,23 +992,25 @@ def _attention_backward_dense(
     dv = dv.view(batch, maps, length, model_dim).sum(1)
     dgamma = dgamma_rows.view(batch, maps, length).sum(dim=(0, 2))
     shape = (batch, maps, length, score_dim)
-    return dq.view(shape).to(query.dtype), dk.view(shape).to(key.dtype), dv.to(value.dtype), dgamma.to(scales.dtype)
+    return (dq.view(shape).to(qk_grad_dtype or query.dtype), dk.view(shape).to(qk_grad_dtype or key.dtype),
+            dv.to(value.dtype), dgamma.to(scales.dtype))
 
 
 def attention_gradients(
     query: Tensor, key: Tensor, value: Tensor, scales: Tensor, out: Tensor, grad: Tensor, causal: bool,
-    needs: tuple[bool, bool, bool, bool] = (True, True, True, True),
+    needs: tuple[bool, bool, bool, bool] = (True, True, True, True), qk_grad_dtype: torch.dtype | None = None,
 ) -> tuple[Tensor | None, Tensor | None, Tensor | None, Tensor | None]:
     """(dq, dk, dv, dscales) of the outer attention whose output was ``out``:
     the dense backward for 512-wide scores whose matrices fit, the flash
     backward kernels otherwise, or autograd of the fp32-softmax reference for
-    score widths above 512."""
+    score widths above 512.  ``qk_grad_dtype`` (e.g. fp32) keeps dq and dk in
+    that dtype on the native paths instead of rounding them to the inputs'."""
 
     if query.numel() and value.numel() and _dense_backward_fits(query, value):
-        grads = _attention_backward_dense(query, key, value, scales, grad, causal)
+        grads = _attention_backward_dense(query, key, value, scales, grad, causal, qk_grad_dtype)
         return tuple(g if need else None for g, need in zip(grads, needs))  # type: ignore[return-value]
     if _native_backward_supported(query, value) and query.numel() and value.numel():
-        grads = _attention_backward(query, key, value, scales, out, grad, causal)
+        grads = _attention_backward(query, key, value, scales, out, grad, causal, qk_grad_dtype)
         return tuple(g if need else None for g, need in zip(grads, needs))  # type: ignore[return-value]
     with torch.enable_grad():
         inputs = [t.detach().requires_grad_(need) for t, need in zip((query, key, value, scales), needs)]

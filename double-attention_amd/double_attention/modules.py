@@ -578,12 +578,15 @@ class _HipModuleFunction(torch.autograd.Function):
         score_query, score_key = _HipModuleFunction._score_maps(routed, batch, length, branches, maps, routing_dim)
         padded = vt.shape[1] * 32
         value_rows = vt.transpose(2, 3).reshape(batch, padded, model_dim)[:, :length]
+        # dq and dk stay fp32 (no rounding, no cast): the route backward takes
+        # fp32 gradient rows.
         d_sq, d_sk, d_value, d_scales = hip_ops.attention_gradients(
-            score_query, score_key, value_rows, scales, map_output, d_maps, cfg.causal
+            score_query, score_key, value_rows, scales, map_output, d_maps, cfg.causal, qk_grad_dtype=torch.float32
         )
         if wants("log_score_scales"):
+            # The clamp passes the gradient only inside its window.
             log_scales = named["log_score_scales"].detach()
-            inside = (log_scales >= math.log(0.25)) & (log_scales <= math.log(1024.0))
+            inside = log_scales.clamp(math.log(0.25), math.log(1024.0)) == log_scales
             grads["log_score_scales"] = d_scales.float() * scales * inside
         # Score-map assembly (views, grouping or repetition of the branches).
         if branches == maps:
@@ -616,7 +619,7 @@ class _HipModuleFunction(torch.autograd.Function):
                 d_val = None
         if wants("log_beta") and d_beta is not None:
             log_beta = named["log_beta"].detach()
-            inside = (log_beta >= math.log(0.05)) & (log_beta <= math.log(64.0))
+            inside = log_beta.clamp(math.log(0.05), math.log(64.0)) == log_beta
             grads["log_beta"] = d_beta.float() * beta.float() * inside
         # Q/K/V projections.
         x2d = xc.reshape(tokens, model_dim)
