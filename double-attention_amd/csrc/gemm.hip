@@ -29,6 +29,24 @@
 
 namespace da {
 
+// erf for the GELU epilogue: Abramowitz & Stegun, Handbook of Mathematical
+// Functions, formula 7.1.26, erf(x) = 1 - (a1 t + ... + a5 t^5) e^(-x^2) with
+// t = 1 / (1 + p x) for x >= 0 (odd extension), absolute error <= 1.5e-7, far
+// below one rounding of the 16-bit outputs.  Branch-free: a reciprocal, an
+// exponential and five FMAs, where the library erff takes several times the
+// VALU work (the epilogue of a 4096 x 1536 GEMM runs it 6.3 million times).
+__device__ __forceinline__ float erf_fast(float x) {
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, ax, 1.f));
+  float poly = __builtin_fmaf(t, 1.061405429f, -1.453152027f);
+  poly = __builtin_fmaf(t, poly, 1.421413741f);
+  poly = __builtin_fmaf(t, poly, -0.284496736f);
+  poly = __builtin_fmaf(t, poly, 0.254829592f);
+  poly *= t;
+  const float y = 1.f - poly * __builtin_amdgcn_exp2f(-ax * ax * kLog2e);
+  return copysignf(y, x);
+}
+
 constexpr int kBJ = 128;
 constexpr int kBK = 64;
 typedef XorTile<kBJ, kBK / 8, false> GemmTileQ;         // Q operand tile: 128 rows x 64 k
@@ -294,7 +312,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float v = acc[a][b][r] + bias_i[a][r] + bj;
-        if constexpr ((EPI & kGemmActGelu) != 0) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+        if constexpr ((EPI & kGemmActGelu) != 0) v = 0.5f * v * (1.f + erf_fast(v * 0.70710678118654752f));
         o[r] = static_cast<T>(v);
       }
       *reinterpret_cast<typename Elem<T>::v4*>(stage_w + (b * 16 + c) * ROWB + (a * 16 + 4 * g) * 2) = o;
