@@ -8,11 +8,14 @@
 // or every O_s written to its own slot (per-map mode, used by the concat
 // combine and by the operator-level API).
 //
-// A workgroup of NW waves (2 or 4) owns 32*NW query rows of one sequence and
-// a slice of DS value features; every wave owns 32 queries (two 16-column MFMA
-// blocks) and the whole slice, so no score tile is formed twice inside a
-// workgroup.  The value width is split over workgroups (DS <= 128) to keep a
-// wave's accumulators small enough for two waves per SIMD.  A wave walks the
+// A workgroup of NW waves (2 or 4) owns 32*NW/SUB query rows of one sequence
+// (SUB sub-streams share the same queries, below) and a slice of DS value
+// features; every wave owns 32 queries (two 16-column MFMA blocks) and the
+// whole slice, so no score tile is formed twice inside a sub-stream.  The
+// value width is split over workgroups (DS <= 128), which bounds a wave's O^T
+// accumulators and multiplies the workgroups of small grids; the variants the
+// module uses still hold more than 256 registers per lane (query, key and
+// score fragments beside the accumulators), one wave per SIMD.  A wave walks the
 // (map, 32-key tile) sequence up to the causal bound in the transposed domain:
 //   S^T[key, q] = sum_r K[key, r] Q^T[r, q]      (A = key rows from LDS, B = queries in VGPRs)
 //   O^T[d, q]  += sum_key V^T[d, key] P^T[key, q] (A = V^T from LDS, B = P in VGPRs)

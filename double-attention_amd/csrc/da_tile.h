@@ -1,11 +1,12 @@
-// LDS tile staging for gfx950: direct global->LDS DMA into padded tiles.
+// LDS tile staging for gfx950: direct global->LDS DMA into padded tiles
+// (PaddedTile, below) or XOR-swizzled tiles without padding (XorTile).
 //
 // Tiles are staged with global_load_lds_dwordx4: every lane names its own
 // 16-byte global chunk and a wave writes 64 consecutive 16-byte LDS slots
 // (slot = M0 base + 16 * lane).  Data never passes through VGPRs, so the next
 // tile's loads run while the current tile is being multiplied.
 //
-// A tile is ROWS rows of NCK 16-byte chunks.  In LDS each row occupies
+// A PaddedTile is ROWS rows of NCK 16-byte chunks.  In LDS each row occupies
 // NCK + 1 slots (one pad slot), so the 16 lanes of a ds_read_b128 that read
 // 16 consecutive rows at one chunk position hit 16 distinct bank groups, and
 // a lane's address for chunk k of row r is base + 16 * (r * (NCK + 1) + k):
@@ -92,34 +93,6 @@ struct PaddedTile {
 
   // Byte offset of (physical row, chunk).
   static __device__ __forceinline__ constexpr int offset(int prow, int ck) { return (prow * PITCH + ck) * 16; }
-};
-
-// A tile of ROWS rows of four 16-byte chunks with no pad slots: chunk c of
-// row r sits at slot 4r + (c ^ ((r >> 2) & 3)).  Sixteen lanes that read
-// sixteen consecutive rows at one chunk position cover 4 rows x 4 distinct
-// chunk slots of each 256-byte bank row, so they hit distinct bank groups,
-// and the DMA moves no padding.  For rows 16 apart the XOR term is equal, so
-// offset(r + 16 m, c) = offset(r, c) + 1024 m: fragment reads stay a per-lane
-// base plus an immediate offset.
-template <int ROWS>
-struct SwizzledTile4 {
-  static_assert(ROWS % 16 == 0, "whole wave loads");
-  static constexpr int NCK = 4;
-  static constexpr int SLOTS = ROWS * NCK;
-  static constexpr int LOADS = SLOTS / 64;
-  static constexpr int BYTES = LOADS * 1024;
-
-  // What slot `slot` holds (every slot is real).
-  static __device__ __forceinline__ bool slot_chunk(int slot, int& row, int& ck) {
-    row = slot >> 2;
-    ck = (slot & 3) ^ ((row >> 2) & 3);
-    return true;
-  }
-
-  // Byte offset of (row, chunk).
-  static __device__ __forceinline__ constexpr int offset(int row, int ck) {
-    return (row * NCK + (ck ^ ((row >> 2) & 3))) * 16;
-  }
 };
 
 // Chunk permutation of an XOR-swizzled tile row (NCK chunks of 16 bytes).

@@ -15,9 +15,12 @@
 //           attention kernel streams one contiguous tile at a time.  Rows i
 //           run over B * Tp "virtual" tokens (t < Tp, the padded length);
 //           tokens past T reuse the last real row, so the padding is finite.
-// Tiles: 128 x 128 per workgroup, 64-wide K stages double-buffered in
-// XOR-swizzled LDS tiles (da_tile.h, conflict-free MFMA operand reads) and filled by global->LDS DMA; each of the four waves
-// owns a 64 x 64 quadrant (4 x 4 MFMA 16x16x32 blocks).
+// Tiles: 128 x 128 per workgroup when the launch has at least 512 of them
+// (two per CU), else 64 x 128 (twice the workgroups).  64-deep K stages sit
+// in XOR-swizzled LDS tiles (da_tile.h, conflict-free MFMA operand reads)
+// filled by global->LDS DMA, in a ring of two buffers (128-row tiles) or
+// three (64-row tiles); each of the four waves owns a (BI/2) x 64 block
+// (BI/32 x 4 MFMA 16x16x32 blocks).
 //
 // A launch may also carry a dictionary normalization (dict_norm.h): its
 // workgroups precede the GEMM tiles, so the module forward normalizes its bank

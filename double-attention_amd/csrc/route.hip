@@ -15,11 +15,14 @@
 // first MFMA is directly the B operand of the second:
 //   S^T[j, c] = sum_r Dk^T[j, r] U^T[r, c]      (A = key atoms from LDS, B = rows in VGPRs)
 //   O^T[r, c] += sum_j Dv[r, j] P^T[j, c]       (A = value atoms from LDS, B = P in VGPRs)
-// A workgroup of four waves shares each dictionary tile, double-buffered in
+// The waves of a workgroup (or of each of its two sub-streams, below) share
+// each dictionary tile, double-buffered in
 // XOR-swizzled LDS tiles (da_tile.h) and filled by global->LDS DMA while the previous
-// tile is multiplied.  Each wave owns QW rows (QW/16 MFMA column blocks), so
-// every dictionary fragment read from LDS feeds QW/16 MFMAs.  The input scale
-// beta/||x|| is applied before the single rounding of the unit row.
+// tile is multiplied.  Each wave owns 16 rows (one MFMA column block), so
+// every dictionary fragment read from LDS feeds one MFMA and each wave reads
+// the whole of every stage tile of its stream (SUB, below) from LDS.  The
+// input scale beta/||x|| is applied before the single rounding of the unit
+// row.
 //
 // Element types: TX = input rows, TK = key atoms and the normalized input (fp16
 // when the input is L2-normalized, since |u_i| <= 1; else TX), value atoms and
