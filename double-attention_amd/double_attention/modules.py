@@ -879,8 +879,11 @@ class DoubleAttentionLM(nn.Module):
             raise ValueError(
                 f"sequence length {length} exceeds configured maximum {self.max_sequence_length}"
             )
-        positions = torch.arange(length, device=token_ids.device)
-        hidden = self.token_embedding(token_ids) + self.position_embedding(positions)[None]
+        # Positions 0 .. length-1 of the plain position table are its first
+        # `length` rows (reference modules.py:452-453 gathers them with an
+        # arange): the same values and gradients without an index tensor or
+        # a gather launch.
+        hidden = self.token_embedding(token_ids) + self.position_embedding.weight[:length][None]
         logits = self.lm_head(self._final_norm(self.stack(hidden)))
         loss = None
         if targets is not None:

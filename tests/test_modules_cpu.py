@@ -73,6 +73,37 @@ def test_lm_default_init_and_logits_match_reference(name: str) -> None:
     _assert_scaled(logits, g["logits"])
 
 
+def test_lm_position_rows_match_an_embedding_lookup() -> None:
+    """The LM reads positions 0..T-1 as the first T rows of its position
+    table; the reference gathers them with an arange (modules.py:452-453).
+    Logits, loss and every gradient agree bit for bit."""
+
+    torch.manual_seed(3)
+    model = da.DoubleAttentionLM(
+        vocab_size=64, max_sequence_length=24,
+        config=da.experiment_config("a1", model_dim=64, routing_dim=32, dictionary_size=48, backend="torch"),
+        num_layers=1, feedforward_dim=96,
+    )
+    ids = torch.randint(0, 64, (2, 17))
+    targets = torch.randint(0, 64, (2, 17))
+    twin = copy.deepcopy(model)
+    logits, loss = model(ids, targets)
+    loss.backward()
+
+    def lookup_forward(self, token_ids, targets=None):
+        positions = torch.arange(token_ids.shape[1])
+        hidden = self.token_embedding(token_ids) + self.position_embedding(positions)[None]
+        out = self.lm_head(self._final_norm(self.stack(hidden)))
+        return out, torch.nn.functional.cross_entropy(out.flatten(0, 1), targets.flatten())
+
+    ref_logits, ref_loss = lookup_forward(twin, ids, targets)
+    ref_loss.backward()
+    assert torch.equal(logits, ref_logits) and torch.equal(loss, ref_loss)
+    for (name, p), (_, q) in zip(model.named_parameters(), twin.named_parameters()):
+        assert torch.equal(p.grad, q.grad), name
+    assert model.position_embedding.weight.grad[17:].abs().max() == 0
+
+
 # Parameter counts recorded in the reference's run reports for the 6-layer,
 # d=512, vocab 2048, sequence 64 models (runs/tied/RESULTS.md:11,
 # runs/screen/RESULTS.md:13, runs/a1_multicorpus_8k/python_docs/
