@@ -900,6 +900,259 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   }
 }
 
+// Short sequences (T <= 64): one workgroup per (sequence, map group, value
+// slice) loads all of its keys and its V^T slice once -- no key-tile loop,
+// no stage ring, no online softmax -- and each wave computes the scores of
+// its 32 queries against at most two key tiles, the exact row softmax
+// (maximum and sum over the row in registers) and P V.  Wave w takes map
+// slot w / 2 of the group and query block w % 2; with the map mix the waves
+// of slot 1 hand alpha_s O_s to those of slot 0 through LDS.  The kernel's
+// code is a fraction of the general one's: with two steps per sequence the
+// general kernel's first pass through its loop is most of its time.
+template <typename TQ, typename TV, int RP, int DS, int NMAP>
+__global__ __launch_bounds__(128 * NMAP, 1) void attention_short_kernel(AttnParams p) {
+  static_assert(NMAP == 1 || NMAP == 2, "one or two map slots");
+  typedef XorTile<kKeyTile, RP / 8, true> KT;   // keys (blocked rows)
+  typedef XorTile<DS, 4, false> VT;             // V^T rows: DS features x 32 tokens
+  typedef typename Elem<TQ>::v8 q8;
+  constexpr int NW = 2 * NMAP;
+  constexpr int KS = RP / 32;
+  constexpr int NB = DS / 16;
+  constexpr int KBYTES = 2 * KT::BYTES;          // one map slot's two key tiles
+  constexpr int VOFF = NMAP * KBYTES;            // the two V^T tiles follow the keys
+  constexpr int LOADS = NMAP * 2 * KT::LOADS + 2 * VT::LOADS;   // wave loads of the workgroup
+  static_assert(LOADS % NW == 0, "every wave issues the same number of loads");
+  // The map hand-over (after every wave has read its tiles) reuses the LDS.
+  constexpr int XBYTES = NMAP == 2 ? 2 * 2 * NB * 256 * 4 : 0;
+  constexpr int LDS_BYTES = VOFF + 2 * VT::BYTES > XBYTES ? VOFF + 2 * VT::BYTES : XBYTES;
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+
+  const int lane = lane_id();
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int wave = uniform_wave();
+  const int mslot = wave >> 1;
+  const int qb = wave & 1;
+  const bool causal = p.flags & kAttnCausal;
+  const bool mix = p.flags & kAttnMix;
+  // Workgroups of one sequence are consecutive in the logical order and so
+  // share an XCD (dispatch deals workgroups to the XCDs round-robin).
+  const int n_wg = static_cast<int>(gridDim.x);
+  const int wg = static_cast<int>(blockIdx.x);
+  const int xcd = wg % kXcds, per_xcd = n_wg / kXcds, rem_xcd = n_wg % kXcds;
+  const int logical = xcd * per_xcd + min(xcd, rem_xcd) + wg / kXcds;
+  const int n_mg = (p.S + NMAP - 1) / NMAP;
+  const int b = logical / (n_mg * p.n_slices);
+  const int mg = (logical / p.n_slices) % n_mg;
+  const int slice = logical % p.n_slices;
+  const int ds0 = slice * DS;
+  auto map_of = [&](int ms) { return min(mg * NMAP + ms, p.S - 1); };
+  const int s = map_of(mslot);
+  const bool real_map = mg * NMAP + mslot < p.S;   // a missing slot repeats the last map and stores nothing
+
+  // Per-map scalars, lane i holding map min(i, S-1), issued first.
+  const int map_lane = min(lane, p.S - 1);
+  const ScalarHalves scale_raw = fetch_scalar(p.scales, p.scales_dtype, map_lane);
+  const bool mix_logits = mix && p.mix_logits != nullptr;
+  const ScalarHalves mix_raw = fetch_scalar(mix_logits ? p.mix_logits : p.scales,
+                                            mix_logits ? p.mix_dtype : p.scales_dtype, map_lane);
+
+  // Query fragments of this wave's map and block (rows past T repeat row
+  // T-1; their outputs are never stored).
+  const TQ* qbase = static_cast<const TQ*>(p.q) + b * p.qk_stride_b + (s / p.map_repeat) * p.map_stride;
+  q8 qf[2][KS];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int tq = min(32 * qb + 16 * cb + c, p.T - 1);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qf[cb][kk] = load8(qbase + static_cast<int64_t>(tq) * p.qk_stride_t + kk * 32 + 8 * g);
+  }
+  // The workgroup's keys (both tiles of every map slot; rows past T read
+  // row T-1) and V^T tiles, by global->LDS DMA, spread over the waves.
+  const int kstride = static_cast<int>(p.qk_stride_t) * static_cast<int>(sizeof(TQ));
+  const char* vbase =
+      reinterpret_cast<const char*>(static_cast<const TV*>(p.vt) + b * p.vt_stride_b + 32 * ds0);
+#pragma unroll
+  for (int i = 0; i < LOADS / NW; ++i) {
+    const int j = i * NW + wave;
+    int row, ck;
+    if (j < NMAP * 2 * KT::LOADS) {
+      const int ms = j / (2 * KT::LOADS);
+      const int kt = (j / KT::LOADS) % 2;
+      const int jj = j % KT::LOADS;
+      KT::slot_chunk(jj * 64 + lane, row, ck);
+      const int key = min(kt * kKeyTile + row, p.T - 1);
+      const char* kb = reinterpret_cast<const char*>(static_cast<const TQ*>(p.k) + b * p.qk_stride_b +
+                                                     (map_of(ms) / p.map_repeat) * p.map_stride);
+      dma16(uniform_ptr(kb) + static_cast<uint32_t>(key * kstride + ck * 16),
+            lds + ms * KBYTES + kt * KT::BYTES + jj * 1024);
+    } else {
+      const int v = j - NMAP * 2 * KT::LOADS;
+      const int kt = v / VT::LOADS;
+      const int jj = v % VT::LOADS;
+      VT::slot_chunk(jj * 64 + lane, row, ck);
+      dma16(uniform_ptr(vbase + static_cast<int64_t>(kt) * kKeyTile * p.D * sizeof(TV)) +
+                static_cast<uint32_t>((row * kKeyTile + ck * 8) * sizeof(TV)),
+            lds + VOFF + kt * VT::BYTES + jj * 1024);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmem();
+
+  auto lane_value = [](float v, int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i)); };
+  float gamma = lane_value(scalar_value(scale_raw, p.scales_dtype), s);
+  if (p.flags & kAttnScalesAreLog) gamma = expf(fminf(fmaxf(gamma, kLogScaleMin), kLogScaleMax));
+  gamma *= p.scale_mult;
+  float weight = 1.f;
+  if (mix) {
+    if (!mix_logits) {
+      weight = 1.f / static_cast<float>(p.S);
+    } else {
+      const float logit = scalar_value(mix_raw, p.mix_dtype);
+      float mx = -INFINITY;
+      for (int i = 0; i < p.S; ++i) mx = fmaxf(mx, lane_value(logit, i));
+      float den = 0.f;
+      for (int i = 0; i < p.S; ++i) den += expf(lane_value(logit, i) - mx);
+      weight = expf(lane_value(logit, s) - mx) / den;
+    }
+  }
+  // A negative scale folds into the queries (exact), so row maxima of raw
+  // scores are maxima of scaled ones.
+  if (gamma < 0.f) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) qf[cb][kk] = -qf[cb][kk];
+  }
+  const float sc = fabsf(gamma) * kLog2e;
+  __syncthreads();
+
+  // Scores: lane (c, g) of block (kt, cb, kb) holds key 32kt + 8g + 4kb + e
+  // for query 32qb + 16cb + c.  Query block qb sees key tiles 0 .. qb when
+  // causal; tile 1 exists when T > 32.
+  const char* kl = lds + mslot * KBYTES;
+  int kfrag[KS < 4 ? KS : 4];
+#pragma unroll
+  for (int k = 0; k < (KS < 4 ? KS : 4); ++k) kfrag[k] = KT::base(c, g, k);
+  const int n_kt = p.T > kKeyTile && (!causal || qb == 1) ? 2 : 1;
+  f32x4 st[2][2][2];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) st[kt][cb][0] = st[kt][cb][1] = zero4();
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    if (kt < n_kt) {
+      const char* tile = kl + kt * KT::BYTES;
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const q8 k0 = lds_v8<TQ>(tile + kfrag[kk & 3] + 256 * (kk >> 2));
+        const q8 k1 = lds_v8<TQ>(tile + kfrag[kk & 3] + 256 * (kk >> 2) + KT::ROW_BLOCK);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          st[kt][cb][0] = Elem<TQ>::mma(k0, qf[cb][kk], st[kt][cb][0]);
+          st[kt][cb][1] = Elem<TQ>::mma(k1, qf[cb][kk], st[kt][cb][1]);
+        }
+      }
+    }
+  }
+  // Exact row softmax: the row maximum over the valid keys, exponentials
+  // against it, the row sum; masked keys get probability zero.
+  auto valid = [&](int kt, int cb, int kb, int e) {
+    const int key = kt * kKeyTile + 8 * g + 4 * kb + e;
+    const int tq = 32 * qb + 16 * cb + c;
+    return kt < n_kt && key < p.T && (!causal || key <= tq);
+  };
+  typename Elem<TV>::v8 pb[2][2];
+  float inv_l[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (valid(kt, cb, kb, e)) m = fmaxf(m, st[kt][cb][kb][e]);
+    m = group_max(m) * sc;
+    float l = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pr = valid(kt, cb, kb, e) ? __builtin_amdgcn_exp2f(__builtin_fmaf(st[kt][cb][kb][e], sc, -m)) : 0.f;
+          st[kt][cb][kb][e] = pr;
+          l += pr;
+        }
+    inv_l[cb] = 1.f / group_sum(l);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) pb[kt][cb] = pack_blocked<TV>(st[kt][cb][0], st[kt][cb][1]);
+  }
+  // O^T += V^T P^T over the key tiles.
+  const char* vl = lds + VOFF + VT::offset(c, g);
+  f32x4 acc[2][NB];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int db = 0; db < NB; ++db) acc[cb][db] = zero4();
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    if (kt < n_kt) {
+#pragma unroll
+      for (int db = 0; db < NB; ++db) {
+        const typename Elem<TV>::v8 vf = lds_v8<TV>(vl + kt * VT::BYTES + db * 1024);
+        acc[0][db] = Elem<TV>::mma(vf, pb[kt][0], acc[0][db]);
+        acc[1][db] = Elem<TV>::mma(vf, pb[kt][1], acc[1][db]);
+      }
+    }
+  }
+  if (NMAP == 2 && mix) {
+    // Slot 1 hands weight * O (normalized) to slot 0 of the same query block.
+    __syncthreads();
+    float* xch = reinterpret_cast<float*>(lds) + qb * (2 * NB * 256);
+    if (mslot == 1) {
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int db = 0; db < NB; ++db)
+          *reinterpret_cast<f32x4*>(xch + ((cb * NB + db) * 64 + lane) * 4) =
+              real_map ? acc[cb][db] * (weight * inv_l[cb]) : zero4();
+    }
+    __syncthreads();
+    if (mslot == 1) return;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int tq = 32 * qb + 16 * cb + c;
+      f32x4 o[NB];
+#pragma unroll
+      for (int db = 0; db < NB; ++db)
+        o[db] = acc[cb][db] * (weight * inv_l[cb]) + *reinterpret_cast<const f32x4*>(xch + ((cb * NB + db) * 64 + lane) * 4);
+      if (tq < p.T) store_rows<TV, DS>(p, b, 0, tq, g, ds0, o, 1.f);
+    }
+    return;
+  }
+  if (!real_map) return;
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int tq = 32 * qb + 16 * cb + c;
+    if (tq < p.T) store_rows<TV, DS>(p, b, mix ? 0 : s, tq, g, ds0, acc[cb], weight * inv_l[cb]);
+  }
+}
+
+template <typename TQ, typename TV, int RP, int DS>
+static void launch_attn_short(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
+  p.n_slices = a.D / DS;
+  if (a.S == 1) {
+    hipLaunchKernelGGL((attention_short_kernel<TQ, TV, RP, DS, 1>), dim3(a.B * p.n_slices), dim3(128), 0, s, p);
+  } else {
+    const int n_mg = (a.S + 1) / 2;
+    hipLaunchKernelGGL((attention_short_kernel<TQ, TV, RP, DS, 2>), dim3(a.B * p.n_slices * n_mg), dim3(256), 0, s, p);
+  }
+}
+
 template <typename TQ, typename TV, int RP, int DS, bool MULTI, int NW>
 static void launch_attn_4(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
   constexpr int QT = NW * kAttnQW;
@@ -1052,10 +1305,30 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
   return plan;
 }
 
+template <typename TQ, typename TV, int RP>
+static void launch_attn_short_d(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
+  if (a.D >= 128) launch_attn_short<TQ, TV, RP, 128>(a, p, s);
+  else launch_attn_short<TQ, TV, RP, 64>(a, p, s);
+}
+
+template <typename TQ, typename TV>
+static void launch_attn_short_r(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
+  switch (a.RP) {
+    case 64: launch_attn_short_d<TQ, TV, 64>(a, p, s); break;
+    case 128: launch_attn_short_d<TQ, TV, 128>(a, p, s); break;
+    default: launch_attn_short_d<TQ, TV, 256>(a, p, s); break;
+  }
+}
+
+// The short-sequence kernel takes sequences of at most two key tiles with
+// scores up to 256 wide; with the map mix, at most two maps (one workgroup
+// holds every map of its sequence).
+static bool attention_short_fits(const AttentionArgs& a) {
+  return a.T <= 2 * kKeyTile && a.RP <= 256 && (a.S <= 2 || !(a.flags & kAttnMix));
+}
+
 void launch_routed_attention(const AttentionArgs& a, void* partials, hipStream_t stream) {
   if (a.T == 0 || a.B == 0) return;
-  const AttnPlan plan = plan_attention(a.B, a.S, a.T, a.D, a.RP, (a.flags & kAttnMix) && a.S > 1,
-                                       a.flags & kAttnCausal, partials != nullptr);
   AttnParams p;
   p.part = static_cast<float*>(partials);
   p.q = a.q;
@@ -1080,6 +1353,17 @@ void launch_routed_attention(const AttentionArgs& a, void* partials, hipStream_t
   p.out_stride_b = a.out_stride_b;
   p.out_stride_t = a.out_stride_t;
   p.out_stride_s = a.out_stride_s;
+  if (attention_short_fits(a)) {
+    p.n_qt = 1;
+    p.stream_len = 0;
+    p.n_seg = 0;
+    if (a.qk_dtype == kF16 && a.v_dtype == kBF16) launch_attn_short_r<_Float16, __bf16>(a, p, stream);
+    else if (a.qk_dtype == kF16) launch_attn_short_r<_Float16, _Float16>(a, p, stream);
+    else launch_attn_short_r<__bf16, __bf16>(a, p, stream);
+    return;
+  }
+  const AttnPlan plan = plan_attention(a.B, a.S, a.T, a.D, a.RP, (a.flags & kAttnMix) && a.S > 1,
+                                       a.flags & kAttnCausal, partials != nullptr);
   if (a.qk_dtype == kF16 && a.v_dtype == kBF16) launch_attn_0<_Float16, __bf16>(a, plan, p, stream);
   else if (a.qk_dtype == kF16) launch_attn_0<_Float16, _Float16>(a, plan, p, stream);
   else launch_attn_0<__bf16, __bf16>(a, plan, p, stream);

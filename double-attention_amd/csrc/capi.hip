@@ -283,6 +283,9 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
     return fail(DA_ERR_INVALID_ARGUMENT, "attention: score_bound must be finite and >= 0");
   if (flags & ~(DA_ATTN_CAUSAL | DA_ATTN_SCALES_ARE_LOG | DA_ATTN_MIX | DA_ATTN_OUT_F32))
     return fail(DA_ERR_INVALID_ARGUMENT, "attention: unknown flag bits 0x%x", flags);
+  // fp32 outputs are written as 16-byte vectors of four floats.
+  if ((flags & DA_ATTN_OUT_F32) && !aligned(out, 16))
+    return fail(DA_ERR_ALIGNMENT, "attention: fp32 out (DA_ATTN_OUT_F32) must be 16-byte aligned");
   const int64_t need = da_attention_workspace_bytes(batch, maps, length, score_dim, value_dim, flags);
   if (workspace && need > 0) {
     if (!aligned(workspace, 256)) return fail(DA_ERR_ALIGNMENT, "attention: workspace must be 256-byte aligned");
@@ -653,18 +656,33 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_of_current_device(void** out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+// The scratch of the device that `stream` launches on (the current device
+// for the null stream): each GPU holds its own copy of the array, at its own
+// address, which hipGetSymbolAddress returns with that device current.
+int scratch_of_stream_device(hipStream_t stream, void** out) {
+  int current = -1;
+  hipError_t e = hipGetDevice(&current);
   if (e != hipSuccess) return fail(DA_ERR_LAUNCH, "noalloc forward: hipGetDevice: %s", hipGetErrorString(e));
+  int dev = current;
+  if (stream) {
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) return fail(DA_ERR_LAUNCH, "noalloc forward: hipStreamGetDevice: %s", hipGetErrorString(e));
+  }
   if (dev < 0 || dev >= kMaxDevices) return fail(DA_ERR_UNSUPPORTED, "noalloc forward: device %d out of range", dev);
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (!g_scratch_ptr[dev]) {
+    if (dev != current) {
+      e = hipSetDevice(dev);
+      if (e != hipSuccess) return fail(DA_ERR_LAUNCH, "noalloc forward: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    }
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    const hipError_t restore = dev != current ? hipSetDevice(current) : hipSuccess;
     if (e != hipSuccess || !ptr)
       return fail(DA_ERR_LAUNCH, "noalloc forward: hipGetSymbolAddress(scratch) on device %d: %s", dev,
                   hipGetErrorString(e));
+    if (restore != hipSuccess)
+      return fail(DA_ERR_LAUNCH, "noalloc forward: hipSetDevice(%d): %s", current, hipGetErrorString(restore));
     g_scratch_ptr[dev] = ptr;
   }
   *out = g_scratch_ptr[dev];
@@ -686,7 +704,7 @@ extern "C" int da_shared_dictionary_attention_forward_noalloc(const da_sda_forwa
                 "(use da_shared_dictionary_attention_forward with a workspace)",
                 (long long)need, (long long)DA_NOALLOC_SCRATCH_BYTES);
   void* ptr = nullptr;
-  const int rc = scratch_of_current_device(&ptr);
+  const int rc = scratch_of_stream_device(reinterpret_cast<hipStream_t>(stream), &ptr);
   if (rc) return rc;
   // Nothing in the workspace needs to start at zero: every byte a kernel
   // reads was written earlier in the same call.

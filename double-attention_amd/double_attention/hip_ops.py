@@ -954,7 +954,9 @@ def _attention_backward_dense(
     P and gamma P (dP - sum P dP) (the gradient at q . k) with the causal row
     length and the map's gamma, plus the row's term of d gamma; GEMMs then
     give dq = dS k, dk = dS^T q and dV = sum over maps of P^T dO.  The row
-    sum uses P and dP themselves, no saved output.
+    sum uses P and dP themselves, no saved output.  dS and P are stored in
+    the value dtype (16-bit) between the row kernel and the GEMMs, which
+    accumulate in fp32.
     """
 
     batch, maps, length, score_dim = query.shape
@@ -1004,7 +1006,10 @@ def attention_gradients(
     the dense backward for 512-wide scores whose matrices fit, the flash
     backward kernels otherwise, or autograd of the fp32-softmax reference for
     score widths above 512.  ``qk_grad_dtype`` (e.g. fp32) keeps dq and dk in
-    that dtype on the native paths instead of rounding them to the inputs'."""
+    that dtype on the native paths instead of rounding them to the inputs'.
+    On the dense path the row kernel writes dS (the gradient at q . k) and P
+    in the value dtype, so there dq and dk are fp32 sums of 16-bit dS
+    entries, not products of an unrounded dS."""
 
     if query.numel() and value.numel() and _dense_backward_fits(query, value):
         grads = _attention_backward_dense(query, key, value, scales, grad, causal, qk_grad_dtype)
@@ -1327,8 +1332,11 @@ def shared_dictionary_attention_hip(
         args.raw_value = _ptr(raw_value)
         args.raw_dtype = dtype_code(raw_key.dtype)
     if no_alloc:
-        _lib.check(lib.da_shared_dictionary_attention_forward_noalloc(args, _stream(x.device)),
-                   "shared_dictionary_attention_hip (no_alloc)")
+        # The library picks the scratch array of the stream's device; x's
+        # device is also made current for the call.
+        with torch.cuda.device(x.device):
+            _lib.check(lib.da_shared_dictionary_attention_forward_noalloc(args, _stream(x.device)),
+                       "shared_dictionary_attention_hip (no_alloc)")
         return HipForwardResult(out, None)
     _lib.check(lib.da_shared_dictionary_attention_forward(args, _stream(x.device)), "shared_dictionary_attention_hip")
     if not want_routed:

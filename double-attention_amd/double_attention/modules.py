@@ -592,12 +592,15 @@ class _HipModuleFunction(torch.autograd.Function):
         if branches == maps:
             d_rq, d_rk = d_sq, d_sk
         else:
+            # The assembly is linear (scales, concatenation, repetition): its
+            # backward runs on fp32 copies of the rows, so the fp32 dq/dk reach
+            # the route backward unrounded.
             with torch.enable_grad():
                 rows = routed.view(batch, length, 2, branches, routing_dim)
-                rq = rows[:, :, 0].transpose(1, 2).detach().requires_grad_()
-                rk = rows[:, :, 1].transpose(1, 2).detach().requires_grad_()
+                rq = rows[:, :, 0].transpose(1, 2).detach().float().requires_grad_()
+                rk = rows[:, :, 1].transpose(1, 2).detach().float().requires_grad_()
                 sq, sk = assemble_score_maps(rq, rk, maps)
-                d_rq, d_rk = torch.autograd.grad((sq, sk), (rq, rk), (d_sq.to(sq.dtype), d_sk.to(sk.dtype)))
+                d_rq, d_rk = torch.autograd.grad((sq, sk), (rq, rk), (d_sq.float(), d_sk.float()))
         d_routed = torch.stack((d_rq.transpose(1, 2), d_rk.transpose(1, 2)), dim=2).reshape(-1, routing_dim)
         # Route.
         variant = hip_ops.RouteVariant.of_config(cfg)

@@ -237,7 +237,8 @@ int da_dictionary_route_backward_rows(const float* logits, const float* grad_wei
  *     the probability type skip the online-softmax rescaling (bf16 V only).
  * maps <= 64.  score_dim and value_dim must be 64, 128, 256 or 512.  Element types:
  *   (qk_dtype, v_dtype) in {(F16, BF16), (F16, F16), (BF16, BF16)}; the output
- *   has v_dtype, or fp32 with DA_ATTN_OUT_F32 (strides then count floats).
+ *   has v_dtype, or fp32 with DA_ATTN_OUT_F32 (strides then count floats, and
+ *   out must be 16-byte aligned).
  *   V^T padding tokens (length .. padded length - 1) must hold finite values.
  */
 int da_routed_attention(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
@@ -399,7 +400,9 @@ int da_shared_dictionary_attention_forward(const da_sda_forward_args* args, da_s
  * that forbid hipMalloc).  args->workspace and args->workspace_bytes are
  * ignored; the workspace is a library-owned device array of
  * DA_NOALLOC_SCRATCH_BYTES per GPU (each GPU the library runs on holds it
- * until the process ends), found once per device on its first call there.
+ * until the process ends), found once per device on its first call there;
+ * the call uses the array of the device `stream` launches on (the current
+ * device for the null stream).
  * Problems whose da_sda_workspace_bytes exceed it fail with DA_ERR_WORKSPACE.
  * The call itself allocates nothing.  Every call on one GPU shares that GPU's
  * array, which keeps the last call's contents: calls that overlap on one GPU

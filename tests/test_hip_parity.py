@@ -412,6 +412,11 @@ def test_route_variants(dtype, variant, normalize_input, normalize_output, routi
     (8, 1, 512, 256, 512, (16.0,)),       # C1's attention
     (2, 1, 300, 128, 256, (12.0,)),       # ragged tail
     (3, 1, 77, 64, 512, (64.0,)),         # scaled bound past the fixed range: online rescaling
+    # At most 64 tokens: the short-sequence kernel (every key tile loaded once).
+    (4, 2, 33, 256, 512, (16.0, 11.0)),
+    (3, 3, 50, 128, 256, (9.0, 13.0, 20.0)),   # three maps: two map groups
+    (2, 1, 64, 256, 512, (120.0,)),           # large scale: exact row maxima
+    (5, 2, 20, 64, 64, (-8.0, 16.0)),         # negative scale folded into the queries
 ])
 def test_routed_attention(dtype, causal, score_bound, batch, maps, length, score_dim, value_dim, scales) -> None:
     # Rows are unit vectors, so 1.01 bounds every score: bf16 maps whose scaled
@@ -917,6 +922,68 @@ def test_module_backward_runs_native_kernels(monkeypatch, preset, overrides, tok
         print(f"[parity] module {preset} {overrides} d{name}: hip {err:.3e}, torch bf16 {t16:.3e} (pooled over seeds)",
               flush=True)
         assert err <= bound, f"d{name}: pooled rel {err:.3e} > {bound:.3e}"
+
+
+@pytest.mark.parametrize("log_beta", [math.log(4.0), math.log(0.01), math.log(100.0)], ids=["inside", "below", "above"])
+def test_module_learnable_beta_gradient(monkeypatch, log_beta) -> None:
+    # A learnable beta (modules.py: log_beta is a Parameter) takes its gradient
+    # from the native route backward's d(beta) times beta, inside the clamp
+    # window [ln 0.05, ln 64] only (reference modules.py:107-110, 130-132).
+    # Against a central difference of the float64 oracle's loss in log_beta
+    # (step 1e-4), pooled over four seeds: the HIP gradient's relative error is
+    # held to max(5e-2, 2x) that of the bf16 torch path.  Outside the window
+    # both paths give exactly zero.
+    device = _device()
+    config = da.experiment_config("a1", backend="hip", learnable_beta=True)
+    calls = []
+    original = da.hip_ops._route_backward
+
+    def counted(*args, **kwargs):
+        calls.append(1)
+        return original(*args, **kwargs)
+
+    monkeypatch.setattr(da.hip_ops, "_route_backward", counted)
+    inside = math.log(0.05) < log_beta < math.log(64.0)
+    sq = [0.0, 0.0, 0.0]
+    for seed in (3, 13, 23, 33):
+        torch.manual_seed(seed)
+        module = da.SharedDictionaryAttention(config).to(device, torch.bfloat16)
+        with torch.no_grad():
+            module.log_beta.fill_(log_beta)
+        assert isinstance(module.log_beta, torch.nn.Parameter)
+        torch_bf16 = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(device, torch.bfloat16)
+        torch_bf16.load_state_dict(module.state_dict())
+        g = torch.Generator().manual_seed(seed + 1)
+        x = torch.randn(2, 40, 512, generator=g).to(device, torch.bfloat16)
+        w = torch.randn(2, 40, 512, generator=g)
+        got = []
+        calls.clear()
+        for m in (module, torch_bf16):
+            m.zero_grad()
+            (m(x).float() * w.to(device)).sum().backward()
+            got.append(float(m.log_beta.grad))
+        assert calls == [1], calls
+        if not inside:
+            assert got == [0.0, 0.0], got
+            continue
+        params = {k: v.double().cpu().numpy() for k, v in module.state_dict().items()}
+        xd, wd = x.double().cpu().numpy(), w.double().numpy()
+
+        def loss(lb: float) -> float:
+            p = dict(params)
+            p["log_beta"] = np.asarray(lb, dtype=np.float64)
+            return float((oracle.shared_dictionary_attention(p, config, xd) * wd).sum())
+
+        h = 1e-4
+        expected = (loss(log_beta + h) - loss(log_beta - h)) / (2 * h)
+        print(f"[parity] learnable beta seed {seed}: hip {got[0]:.5f}, torch bf16 {got[1]:.5f}, "
+              f"fp64 central difference {expected:.5f}", flush=True)
+        sq[0] += (got[0] - expected) ** 2
+        sq[1] += (got[1] - expected) ** 2
+        sq[2] += expected ** 2
+    if inside:
+        err, t16 = math.sqrt(sq[0] / sq[2]), math.sqrt(sq[1] / sq[2])
+        assert err <= max(5e-2, 2 * t16), (err, t16)
 
 
 def test_module_and_ops_accept_misaligned_views() -> None:

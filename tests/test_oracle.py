@@ -78,6 +78,15 @@ def test_golden_check_detects_planted_mistakes() -> None:
     noncausal = dict(g.config, causal=False)
     out = oracle.shared_dictionary_attention(params, noncausal, g["x"])
     assert np.abs(out - g["out"]).max() / np.abs(g["out"]).max() > 100 * GOLDEN_SCALED_TOL
+    # A dropped term (the value bias), a sign (of the value bias) and a
+    # transposed operand (query and key projections swapped, which transposes
+    # every score matrix before the causal mask).
+    dropped = dict(params, **{"value.bias": np.zeros_like(params["value.bias"])})
+    flipped = dict(params, **{"value.bias": -params["value.bias"]})
+    swapped = dict(params, **{"query.weight": params["key.weight"], "key.weight": params["query.weight"]})
+    for wrong in (dropped, flipped, swapped):
+        out = oracle.shared_dictionary_attention(wrong, g.config, g["x"])
+        assert np.abs(out - g["out"]).max() / np.abs(g["out"]).max() > 100 * GOLDEN_SCALED_TOL
 
 
 # ---------------------------------------------------------------- normalization
