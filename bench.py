@@ -78,6 +78,13 @@ def parse_args() -> argparse.Namespace:
         "--backward, only --steps HIP training steps (module, and for c4 the LM), for a kernel trace",
     )
     p.add_argument(
+        "--compare-library",
+        action="store_true",
+        help="instead of the benchmark: the projection and FFN GEMMs of C1-C5 on the library's MFMA GEMM against "
+        "torch (hipBLASLt), both replayed from HIP graphs, and the C1-C5 forwards on backend='hip' against "
+        "backend='torch' in bf16 on the same GPU (one JSON line; not the headline metric)",
+    )
+    p.add_argument(
         "--collect-counters",
         action="store_true",
         help="profile a --kernels-only child run of the workload under rocprofv3 --pmc (MFMA, LDS and HBM "
@@ -453,10 +460,140 @@ def backward_bench(args: argparse.Namespace) -> None:
     }), flush=True)
 
 
+def compare_library() -> None:
+    """GEMMs at the C1-C5 shapes: the library's hand GEMM (with its fused
+    epilogues: V^T layout and bias for the Q/K/V projection, GELU, residual)
+    against torch's GEMM (hipBLASLt) with the same epilogue as separate ops
+    and without it; every launch replayed 20 at a time from a HIP graph, so
+    host work is not timed.  Then the C1-C5 forwards (C4: the six-layer LM)
+    on backend="hip" against backend="torch" in bf16 on the same GPU, eager,
+    HIP events over 30 forwards (best of three), the reference's own forward
+    comparison (Triton against its PyTorch path)."""
+
+    import torch
+    import torch.nn.functional as F
+
+    import double_attention as da
+    from double_attention import hip_ops
+
+    dev = torch.device("cuda:0")
+
+    def graph_us(fn, calls=20, replays=20):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(calls):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(replays):
+                graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) * 1e3 / (replays * calls))
+        return round(best, 2)
+
+    def eager_us(fn, reps=30):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) * 1e3 / reps)
+        return round(best, 2)
+
+    gen = torch.Generator().manual_seed(0)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=gen) * scale).to(dev, torch.bfloat16)
+
+    gemms = []
+    for name, (batch, length, width) in {"c1": (8, 512, 256), "c2": (8, 1024, 512), "c3": (4, 2048, 512),
+                                         "c4": (64, 64, 512), "c5": (1, 8192, 256)}.items():
+        x = rnd(batch, length, 512)
+        wq, wk, wv = (rnd(n, 512, scale=512 ** -0.5) for n in (width, width, 512))
+        bv = rnd(512)
+        wcat = torch.cat([wq, wk, wv])
+        bcat = torch.cat([torch.zeros(2 * width, dtype=bv.dtype, device=dev), bv])
+        gemms.append({
+            "gemm": f"{name} Q/K/V projection {batch * length}x512 -> {2 * width}+512",
+            "hip_us": graph_us(lambda: hip_ops.qkv_projection_hip(x, wq, wk, wv, bv)),
+            "torch_us": graph_us(lambda: F.linear(x, wcat, bcat)),
+            "gflop": round(2 * batch * length * 512 * (2 * width + 512) / 1e9, 3),
+        })
+    for name, (n, k, o, act, res) in {
+        "c1 output projection": (4096, 512, 512, None, False),
+        "c2/c3/c5 output projection": (8192, 512, 512, None, False),
+        "c4 output projection + residual": (4096, 512, 512, None, True),
+        "c4 FFN up + bias + GELU": (4096, 512, 1536, "gelu", False),
+        "c4 FFN down + bias + residual": (4096, 1536, 512, None, True),
+    }.items():
+        x = rnd(n, k)
+        w = rnd(o, k, scale=k ** -0.5)
+        bias = rnd(o) if (act or res) else None
+        r = rnd(n, o) if res else None
+        if act == "gelu":
+            unfused = lambda: F.gelu(F.linear(x, w, bias))  # noqa: E731
+        elif res:
+            unfused = lambda: r + F.linear(x, w, bias)  # noqa: E731
+        else:
+            unfused = lambda: F.linear(x, w)  # noqa: E731
+        gemms.append({
+            "gemm": f"{name} {n}x{k} -> {o}",
+            "hip_us": graph_us(lambda: hip_ops.linear_hip(x, w, bias, activation=act, residual=r)),
+            "torch_us": graph_us(unfused),
+            "torch_gemm_only_us": graph_us(lambda: F.linear(x, w, bias)),
+            "gflop": round(2 * n * k * o / 1e9, 3),
+        })
+    forwards = []
+    for name in ("c1", "c2", "c3", "c5", "c4"):
+        preset, batch, length, overrides, _ = WORKLOADS[name]
+        config = da.experiment_config(preset, backend="hip", **overrides)
+        torch.manual_seed(0)
+        if name == "c4":
+            hip = da.DoubleAttentionLM(LM_VOCAB, length, config, LM_LAYERS, dictionary_group_size=LM_LAYERS,
+                                       feedforward_dim=LM_FEEDFORWARD).to(dev, torch.bfloat16).eval()
+            ref = da.DoubleAttentionLM(LM_VOCAB, length, config.with_updates(backend="torch"), LM_LAYERS,
+                                       dictionary_group_size=LM_LAYERS,
+                                       feedforward_dim=LM_FEEDFORWARD).to(dev, torch.bfloat16).eval()
+            inp = torch.randint(0, LM_VOCAB, (batch, length), generator=torch.Generator().manual_seed(1)).to(dev)
+        else:
+            hip = da.SharedDictionaryAttention(config).to(dev, torch.bfloat16).eval()
+            ref = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(dev, torch.bfloat16).eval()
+            inp = torch.randn(batch, length, config.model_dim, generator=torch.Generator().manual_seed(1)).to(
+                dev, torch.bfloat16)
+        ref.load_state_dict(hip.state_dict())
+        with torch.inference_mode():
+            t_hip, t_ref = eager_us(lambda: hip(inp)), eager_us(lambda: ref(inp))
+        forwards.append({"workload": name, "hip_us": t_hip, "torch_bf16_us": t_ref,
+                         "speedup": round(t_ref / t_hip, 2)})
+        del hip, ref
+    print(json.dumps({"compare_library": {"gemms": gemms, "forwards": forwards}}), flush=True)
+
+
 def main() -> None:
     args = parse_args()
     if args.collect_counters:
         collect_counters(args)
+        return
+    if args.compare_library and args.gpus == 1:
+        compare_library()
         return
     if args.backward and args.gpus == 1:
         backward_bench(args)

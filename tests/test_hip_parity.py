@@ -793,6 +793,46 @@ def test_lm_q_dictionary_feedforward(preset) -> None:
                   label=f"lm {preset}")
 
 
+@pytest.mark.parametrize(("preset", "overrides", "shape"), [
+    ("a1", {}, (8, 512, 512)),
+    ("a1", {"untied_dictionary": False}, (8, 512, 512)),     # tied: one bank, both layouts
+    ("qk4-s4", {}, (2, 256, 512)),                           # 128-wide atoms
+    ("a1-r512-d1536", {}, (4, 2048, 512)),                   # 512-wide atoms, 1536 of them
+    ("a1", {"dictionary_size": 300}, (2, 200, 512)),          # padding atoms
+    ("a1", {}, (1, 5, 512)),                                 # few GEMM tiles
+])
+def test_projection_launch_normalizes_the_bank(preset, overrides, shape) -> None:
+    # A module that owns its bank normalizes it inside the projection launch
+    # (workgroups of their own ahead of the GEMM tiles), straight into the
+    # route layouts: key atoms [Mp, R] and 32-atom value tiles, zero past M,
+    # within one 16-bit rounding of the oracle.
+    device = _device()
+    torch.manual_seed(9)
+    config = da.experiment_config(preset, backend="hip", **overrides)
+    module = da.SharedDictionaryAttention(config).to(device, torch.bfloat16).eval()
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(10)).to(device, torch.bfloat16)
+    bank = module.bank
+    key_dtype = da.hip_ops.route_key_dtype(config.normalize_routing_input, torch.bfloat16)
+    layout = da.hip_ops.own_bank_layout(bank, key_dtype)
+    layout.key_t.fill_(float("nan"))
+    layout.value.fill_(float("nan"))
+    with torch.inference_mode():
+        da.hip_ops.shared_dictionary_attention_hip(module, x, layout, torch.bfloat16,
+                                                   raw_bank=(bank.raw_key, bank.raw_value))
+    torch.cuda.synchronize()
+    raw_value = None if bank.raw_value is None else np32(bank.raw_value)
+    key, value = oracle.bank_normalized(np32(bank.raw_key), raw_value, config.eps)
+    atoms = key.shape[1]
+    got_key = np32(layout.key_t)
+    got_value = np32(da.hip_ops._untile_value(layout.value))
+    assert np.isfinite(got_key).all() and np.isfinite(got_value).all()
+    np.testing.assert_array_equal(got_key[atoms:], 0.0)
+    np.testing.assert_array_equal(got_value[:, atoms:], 0.0)
+    ulp = 2.0 ** -8 if key_dtype == torch.bfloat16 else 2.0 ** -11
+    np.testing.assert_allclose(got_key[:atoms].T, key, rtol=ulp, atol=1e-6)
+    np.testing.assert_allclose(got_value[:, :atoms], value, rtol=2.0 ** -11, atol=1e-6)
+
+
 def test_stack_normalizes_each_bank_once_on_hip(monkeypatch) -> None:
     device = _device()
     config = da.experiment_config("a1", backend="hip")
