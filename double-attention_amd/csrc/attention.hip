@@ -565,12 +565,15 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 
     // Fragment reads come before the stage loads in program order where the
     // registers allow: the loads write LDS, so the compiler keeps every later
-    // LDS read behind them.  Up to eight key steps and eight V^T blocks are
-    // read up front; 512-wide scores read their keys in groups of four steps,
-    // each two steps ahead of its first use, and their V^T blocks after the
+    // LDS read behind them.  Key fragments are read two chunk steps at a
+    // time, two steps ahead of their MFMAs, so few reads are waited for at
+    // once (against reading up to eight steps up front, the attention kernel
+    // at C1/C2/C3/C5 went about 16.3/71/76.2/100 -> 15.7/69.5/74.2/98.8 us);
+    // up to eight V^T blocks are read up front, after the scores for 512-wide
     // scores.  The loads are spread over the second half of the score MFMAs.
-    constexpr int KG = KS <= 8 ? KS : 4;
+    constexpr int KG = KS < 2 ? KS : 2;
     constexpr int KLEAD = 2;
+    constexpr int KIN = KS < (KG > KLEAD ? KG : KLEAD) ? KS : (KG > KLEAD ? KG : KLEAD);   // steps read up front
     constexpr int VA = KS <= 8 ? (NB < 8 ? NB : 8) : 0;
     const char* kf = cur;
     const char* vf = cur + vfrag;
@@ -581,7 +584,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       kfr[kk][1] = key_frag(kf, kk, 1);
     };
 #pragma unroll
-    for (int kk = 0; kk < KG; ++kk) read_keys(kk);
+    for (int kk = 0; kk < KIN; ++kk) read_keys(kk);
 #pragma unroll
     for (int db = 0; db < VA; ++db) vfr[db] = lds_v8<TV>(vf + db * 1024);
 
@@ -590,7 +593,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     for (int cb = 0; cb < 2; ++cb) st_new[cb][0] = st_new[cb][1] = zero4();
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      if (KG < KS && kk + KLEAD >= KG && kk + KLEAD < KS && (kk + KLEAD) % KG == 0) {
+      if (KIN < KS && kk + KLEAD >= KIN && kk + KLEAD < KS && (kk + KLEAD) % KG == 0) {
 #pragma unroll
         for (int k2 = kk + KLEAD; k2 < kk + KLEAD + KG; ++k2) read_keys(k2);
       }
