@@ -154,7 +154,8 @@ COPY_MIB = 256        # calibration copy of the counter runs
 
 
 def _kernel_label(name: str) -> str:
-    for key, label in (("route_kernel", "route"), ("attention_kernel", "attention"), ("merge", "attention_merge"),
+    for key, label in (("route_kernel", "route"), ("attention_kernel", "attention"), ("attention_short_kernel", "attention"),
+                       ("merge", "attention_merge"),
                        ("dict_normalize", "dict_normalize"), ("gemm_kernel", "gemm"), ("copyBuffer", "copy")):
         if key in name:
             return label

@@ -59,10 +59,12 @@ struct AttnParams {
   // query tile, every map.
   int stream_len;
   int n_seg;           // workgroups per (sequence, slice) in the stream split
-  // Per workgroup of the stream split, slots of QT*(DS+2) floats: two unit
-  // pieces ([QT][DS] normalized outputs, [QT] reference m, [QT] sums l) and,
-  // with the map mix, two partial mixes ([QT][DS]).
-  float* part;
+  // Per workgroup of the stream split, slots of attn_slot_bytes(QT, DS, es)
+  // bytes: two unit pieces ([QT][DS] normalized outputs, es bytes each, then
+  // [QT] reference m and [QT] sums l in fp32) and, with the map mix, two
+  // partial mixes ([QT][DS] outputs).  es is 2 (the value dtype; the outputs
+  // are bounded by max |V|) unless the call asks for fp32 outputs (4).
+  char* part;
   const void* scales;
   int scales_dtype;
   float scale_mult;
@@ -73,6 +75,32 @@ struct AttnParams {
   void* out;
   int64_t out_stride_b, out_stride_t, out_stride_s;
 };
+
+// Piece element bytes of a call, and the bytes of one slot.
+__host__ __device__ inline int attn_piece_bytes(int flags) { return (flags & kAttnOutF32) ? 4 : 2; }
+__host__ __device__ inline int64_t attn_slot_bytes(int QT, int DS, int es) {
+  return static_cast<int64_t>(QT) * DS * es + 8 * static_cast<int64_t>(QT);
+}
+
+// Store four normalized outputs of a piece (or a partial mix) at element
+// offset `at`, in fp32 or in the value dtype.
+template <typename TV, int es>
+__device__ __forceinline__ void store_piece4(char* slot, int at, f32x4 v) {
+  if constexpr (es == 4) {
+    *reinterpret_cast<f32x4*>(slot + 4 * at) = v;
+  } else {
+    typename Elem<TV>::v4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = static_cast<TV>(v[i]);
+    *reinterpret_cast<typename Elem<TV>::v4*>(slot + 2 * at) = o;
+  }
+}
+template <typename TV, int es>
+__device__ __forceinline__ f32x4 load_piece4(const char* slot, int at) {
+  if constexpr (es == 4) return *reinterpret_cast<const f32x4*>(slot + 4 * at);
+  const typename Elem<TV>::v4 v = *reinterpret_cast<const typename Elem<TV>::v4*>(slot + 2 * at);
+  return f32x4{static_cast<float>(v[0]), static_cast<float>(v[1]), static_cast<float>(v[2]), static_cast<float>(v[3])};
+}
 
 __device__ __forceinline__ float map_weight(const AttnParams& p, int s) {
   if (!(p.flags & kAttnMix)) return 1.f;
@@ -190,7 +218,7 @@ struct AttnTile {
 // masked tiles); at the end the odd sub-stream hands its accumulators over
 // LDS to the even one, which merges and stores.  A small grid so keeps every
 // SIMD of a CU busy, and long map mixes finish in half the steps.
-template <typename TQ, typename TV, int RP, int DS, int NW, int NST, bool MULTI, int SUB>
+template <typename TQ, typename TV, int RP, int DS, int NW, int NST, bool MULTI, int SUB, int PIECE = 2>
 __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
   static_assert(NST == 2 || NST == 3, "two or three stage buffers");
   static_assert(SUB == 1 || SUB == 2, "one or two sub-streams");
@@ -644,9 +672,12 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     cur_off = cur_off + SBYTES == NST * SBYTES ? 0 : cur_off + SBYTES;
   };
 
-  // Slots of this workgroup's partial results (stream split).
-  constexpr int ITEM = QT * (DS + 2);
-  float* slots = p.part + static_cast<int64_t>(gx * p.n_seg + gy) * (MULTI ? 4 : 2) * ITEM;
+  // Slots of this workgroup's partial results (stream split); PIECE is
+  // attn_piece_bytes(p.flags), a template argument so that only the piece
+  // store of the call's type is compiled into the loop.
+  constexpr int es = PIECE;
+  const int64_t slot_bytes = attn_slot_bytes(QT, DS, es);
+  char* slots = p.part + static_cast<int64_t>(gx * p.n_seg + gy) * (MULTI ? 4 : 2) * slot_bytes;
   // The fixed reference keeps every probability within the range of the
   // operand type: bf16 holds 2^-120 .. 1 exactly in exponent; fp16 does not.
   auto fixed_for = [&](float scale) {
@@ -675,11 +706,13 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     if (keep) break;
     const float wmap = weight_of(s);
     // A piece of a unit's key range (stream split) stores its normalized
-    // outputs, reference and row sums in fp32 for the merge kernel: slot 0 if
-    // it is the run's first unit, else slot 1.  A whole unit goes to its
-    // output slot, or with the map mix into the query tile's mix.
+    // outputs (16-bit, or fp32 for fp32 outputs), reference and row sum
+    // (fp32) for the merge kernel: slot 0 if it is the run's first unit, else
+    // slot 1.  A whole unit goes to its output slot, or with the map mix
+    // into the query tile's mix.
     const bool partial = stream && (kt_start > 0 || n_here < n_unit);
-    float* piece = slots + (unit == unit_first ? 0 : 1) * ITEM;
+    char* piece = slots + (unit == unit_first ? 0 : 1) * slot_bytes;
+    float* piece_stats = reinterpret_cast<float*>(piece + static_cast<int64_t>(QT) * DS * es);
     const int q0 = qt * QT;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
@@ -689,11 +722,10 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       const int tq = q0 + ql;
       if (partial) {
 #pragma unroll
-        for (int db = 0; db < NB; ++db)
-          *reinterpret_cast<f32x4*>(piece + ql * DS + db * 16 + 4 * g) = acc[cb][db] * w;
+        for (int db = 0; db < NB; ++db) store_piece4<TV, es>(piece, ql * DS + db * 16 + 4 * g, acc[cb][db] * w);
         if (g == 0) {
-          piece[QT * DS + ql] = fixed ? p.score_bound * sc : m_run[cb];
-          piece[QT * DS + QT + ql] = l;
+          piece_stats[ql] = fixed ? p.score_bound * sc : m_run[cb];
+          piece_stats[QT + ql] = l;
         }
       } else if constexpr (MULTI) {
 #pragma unroll
@@ -712,7 +744,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
       // query tile) or 1 for the merge kernel.
       if (!more || unit_qt(unit + 1) != qt) {
         const bool whole = qt_from_start && s == p.S - 1 && !partial;
-        float* mix = slots + (2 + (qt == unit_qt(unit_first) ? 0 : 1)) * ITEM;
+        char* mix = slots + (2 + (qt == unit_qt(unit_first) ? 0 : 1)) * slot_bytes;
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
           const int ql = wave * kAttnQW + cb * 16 + c;
@@ -720,7 +752,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
             if (q0 + ql < p.T) store_rows<TV, DS>(p, b, 0, q0 + ql, g, ds0, yacc[cb], 1.f);
           } else {
 #pragma unroll
-            for (int db = 0; db < NB; ++db) *reinterpret_cast<f32x4*>(mix + ql * DS + db * 16 + 4 * g) = yacc[cb][db];
+            for (int db = 0; db < NB; ++db) store_piece4<TV, es>(mix, ql * DS + db * 16 + 4 * g, yacc[cb][db]);
           }
 #pragma unroll
           for (int i = 0; i < NB; ++i) yacc[cb][i] = zero4();
@@ -815,7 +847,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 // (slot rule as for pieces, offset by two slots).  Each wave takes one query
 // row, its lanes covering consecutive features, so every partial row is read
 // by one coalesced sweep.
-template <typename TV, int DS, int QT, bool MULTI>
+template <typename TV, int DS, int QT, bool MULTI, int PIECE>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   const int qt = static_cast<int>(blockIdx.y);
   const int64_t L = p.stream_len;
@@ -826,11 +858,12 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   if (y0 == y1) return;   // written directly by its workgroup
   const int b = static_cast<int>(blockIdx.x) / p.n_slices;
   const int ds0 = (static_cast<int>(blockIdx.x) - b * p.n_slices) * DS;
-  constexpr int ITEM = QT * (DS + 2);
+  constexpr int es = PIECE;
+  const int64_t slot_bytes = attn_slot_bytes(QT, DS, es);
   constexpr int NSLOT = MULTI ? 4 : 2;
-  auto slot = [&](int y, int64_t start, int k) {
+  auto slot = [&](int y, int64_t start, int k) -> const char* {
     const int first = (y == static_cast<int>(start / L) && start != (start / L) * L) ? 1 : 0;
-    return p.part + ((static_cast<int64_t>(blockIdx.x) * p.n_seg + y) * NSLOT + k + first) * ITEM;
+    return p.part + ((static_cast<int64_t>(blockIdx.x) * p.n_seg + y) * NSLOT + k + first) * slot_bytes;
   };
   const int lane = lane_id();
   // blockIdx.z picks four query rows of the tile, one per wave.
@@ -843,11 +876,11 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   for (int k = 0; k < NV; ++k) out[k] = zero4();
   if constexpr (MULTI) {
     for (int y = y0; y <= y1; ++y) {
-      const float* mix = slot(y, A, 2);
+      const char* mix = slot(y, A, 2);
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         const int d4 = (k * 64 + lane) * 4;
-        if (d4 < DS) out[k] += *reinterpret_cast<const f32x4*>(mix + ql * DS + d4);
+        if (d4 < DS) out[k] += load_piece4<TV, es>(mix, ql * DS + d4);
       }
     }
   }
@@ -864,14 +897,15 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) o[k] = zero4();
     for (int y = ya; y <= yb; ++y) {
-      const float* pc = slot(y, start, 0);
-      const float m = pc[QT * DS + ql];
-      const float l = pc[QT * DS + QT + ql];
+      const char* pc = slot(y, start, 0);
+      const float* stats = reinterpret_cast<const float*>(pc + static_cast<int64_t>(QT) * DS * es);
+      const float m = stats[ql];
+      const float l = stats[QT + ql];
       f32x4 v[NV];
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         const int d4 = min((k * 64 + lane) * 4, DS - 4);
-        v[k] = *reinterpret_cast<const f32x4*>(pc + ql * DS + d4);
+        v[k] = load_piece4<TV, es>(pc, ql * DS + d4);
       }
       if (m == -INFINITY) continue;   // a piece with every key masked
       const float Mn = fmaxf(M, m);
@@ -1159,12 +1193,24 @@ static void launch_attn_short(const AttentionArgs& a, AttnParams& p, hipStream_t
 template <typename TQ, typename TV, int RP, int DS, bool MULTI, int NW>
 static void launch_attn_4(const AttentionArgs& a, const AttnPlan& plan, AttnParams& p, hipStream_t s) {
   constexpr int QT = NW * kAttnQW;
-  const int gy = plan.stream_len > 0 ? plan.n_seg : plan.n_qt;
-  hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, NW, kAttnStages, MULTI, 1>), dim3(a.B * p.n_slices, gy),
-                     dim3(NW * 64), 0, s, p);
-  if (plan.stream_len > 0)
-    hipLaunchKernelGGL((attention_merge_kernel<TV, DS, QT, MULTI>), dim3(a.B * p.n_slices, plan.n_qt, QT / 4),
-                       dim3(256), 0, s, p);
+  if (plan.stream_len == 0) {
+    hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, NW, kAttnStages, MULTI, 1>), dim3(a.B * p.n_slices, plan.n_qt),
+                       dim3(NW * 64), 0, s, p);
+    return;
+  }
+  // The stream split: pieces in the value dtype, or in fp32 when the call
+  // asks for fp32 outputs.  plan_attention gives it four-wave workgroups
+  // only (every key and V^T tile it stages serves 128 queries).
+  if constexpr (NW == 4) {
+    const dim3 grid(a.B * p.n_slices, plan.n_seg), merge(a.B * p.n_slices, plan.n_qt, QT / 4);
+    if (attn_piece_bytes(a.flags) == 4) {
+      hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, NW, kAttnStages, MULTI, 1, 4>), grid, dim3(NW * 64), 0, s, p);
+      hipLaunchKernelGGL((attention_merge_kernel<TV, DS, QT, MULTI, 4>), merge, dim3(256), 0, s, p);
+    } else {
+      hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, NW, kAttnStages, MULTI, 1, 2>), grid, dim3(NW * 64), 0, s, p);
+      hipLaunchKernelGGL((attention_merge_kernel<TV, DS, QT, MULTI, 2>), merge, dim3(256), 0, s, p);
+    }
+  }
 }
 
 template <typename TQ, typename TV, int RP, int DS, bool MULTI>
@@ -1233,7 +1279,7 @@ constexpr int64_t kCUs = 256;
 constexpr int64_t kLdsBytes = 160 * 1024;
 
 AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, bool multi, bool causal,
-                        bool allow_split) {
+                        bool allow_split, int piece_bytes) {
   AttnPlan plan{};
   const int64_t nw = RP == 512 ? 4 : 2;
   const int64_t qtile = nw * kAttnQW;
@@ -1304,7 +1350,9 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
     plan.n_seg = static_cast<int>((all4 + share4 - 1) / share4);
     part_qtile = q4;
   }
-  plan.part_bytes = plan.stream_len > 0 ? B * slices * plan.n_seg * (multi ? 4 : 2) * part_qtile * (ds + 2) * 4 : 0;
+  plan.part_bytes = plan.stream_len > 0 ? B * slices * plan.n_seg * (multi ? 4 : 2) *
+                                              attn_slot_bytes(static_cast<int>(part_qtile), static_cast<int>(ds), piece_bytes)
+                                        : 0;
   return plan;
 }
 
@@ -1333,7 +1381,7 @@ static bool attention_short_fits(const AttentionArgs& a) {
 void launch_routed_attention(const AttentionArgs& a, void* partials, hipStream_t stream) {
   if (a.T == 0 || a.B == 0) return;
   AttnParams p;
-  p.part = static_cast<float*>(partials);
+  p.part = static_cast<char*>(partials);
   p.q = a.q;
   p.k = a.k;
   p.qk_stride_b = a.qk_stride_b;
@@ -1366,7 +1414,7 @@ void launch_routed_attention(const AttentionArgs& a, void* partials, hipStream_t
     return;
   }
   const AttnPlan plan = plan_attention(a.B, a.S, a.T, a.D, a.RP, (a.flags & kAttnMix) && a.S > 1,
-                                       a.flags & kAttnCausal, partials != nullptr);
+                                       a.flags & kAttnCausal, partials != nullptr, attn_piece_bytes(a.flags));
   if (a.qk_dtype == kF16 && a.v_dtype == kBF16) launch_attn_0<_Float16, __bf16>(a, plan, p, stream);
   else if (a.qk_dtype == kF16) launch_attn_0<_Float16, _Float16>(a, plan, p, stream);
   else launch_attn_0<__bf16, __bf16>(a, plan, p, stream);

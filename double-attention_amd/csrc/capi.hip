@@ -261,7 +261,8 @@ int64_t da_attention_workspace_bytes(int64_t batch, int64_t maps, int64_t length
                                      int64_t value_dim, int flags) {
   if (batch < 1 || maps < 1 || length < 1 || value_dim < 1) return 0;
   const bool multi = (flags & DA_ATTN_MIX) && maps > 1;
-  return align_up(da::plan_attention(batch, maps, length, value_dim, score_dim, multi, flags & DA_ATTN_CAUSAL, true)
+  return align_up(da::plan_attention(batch, maps, length, value_dim, score_dim, multi, flags & DA_ATTN_CAUSAL, true,
+                                     (flags & DA_ATTN_OUT_F32) ? 4 : 2)
                       .part_bytes);
 }
 
@@ -492,8 +493,8 @@ int64_t da_sda_workspace_offset(int64_t batch, int64_t length, int64_t model_dim
 static int64_t attention_partial_bytes(int64_t batch, int64_t length, int64_t model_dim, int64_t qk_width,
                                        int64_t outer_maps) {
   if (outer_maps != 1) return 0;
-  const da::AttnPlan causal = da::plan_attention(batch, 1, length, model_dim, qk_width, false, true, true);
-  const da::AttnPlan full = da::plan_attention(batch, 1, length, model_dim, qk_width, false, false, true);
+  const da::AttnPlan causal = da::plan_attention(batch, 1, length, model_dim, qk_width, false, true, true, 2);
+  const da::AttnPlan full = da::plan_attention(batch, 1, length, model_dim, qk_width, false, false, true, 2);
   return align_up(std::max(causal.part_bytes, full.part_bytes));
 }
 

@@ -187,7 +187,8 @@ void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight,
                        float eps, int dtype, void* out, hipStream_t stream);
 // Launch shape of the attention for a problem: value slice width, waves per
 // query tile, sub-streams, query tiles, the stream split of long key ranges (run length, 0
-// = none; runs per sequence and slice) and the bytes of partials it needs.
+// = none; runs per sequence and slice) and the bytes of partials it needs
+// with piece outputs of piece_bytes (2: 16-bit, 4: fp32 for fp32 outputs).
 struct AttnPlan {
   int ds;
   int nw;
@@ -198,7 +199,7 @@ struct AttnPlan {
   int64_t part_bytes;
 };
 AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, bool multi, bool causal,
-                        bool allow_split);
+                        bool allow_split, int piece_bytes);
 // `partials`: plan.part_bytes of device scratch (plan with allow_split), or
 // nullptr to run without key-range splitting.
 void launch_routed_attention(const AttentionArgs& a, void* partials, hipStream_t stream);
