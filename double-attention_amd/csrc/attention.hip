@@ -598,7 +598,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
     // once (against reading up to eight steps up front, the attention kernel
     // at C1/C2/C3/C5 went about 16.3/71/76.2/100 -> 15.7/69.5/74.2/98.8 us);
     // up to eight V^T blocks are read up front, after the scores for 512-wide
-    // scores.  The loads are spread over the second half of the score MFMAs.
+    // scores.  The next stage's loads are spread over the score MFMAs.
     constexpr int KG = KS < 2 ? KS : 2;
     constexpr int KLEAD = 2;
     constexpr int KIN = KS < (KG > KLEAD ? KG : KLEAD) ? KS : (KG > KLEAD ? KG : KLEAD);   // steps read up front
@@ -625,7 +625,11 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 #pragma unroll
         for (int k2 = kk + KLEAD; k2 < kk + KLEAD + KG; ++k2) read_keys(k2);
       }
-      constexpr int D0 = KS / 2;
+      // The next stage's loads start at chunk step D0: over the whole score
+      // loop for 256-wide scores, over its second half otherwise (measured:
+      // from step 0 the C1 and C5 attention ran 15.7 -> 15.4 and 99.8 -> 95.7
+      // us, C2 and C3 (128- and 512-wide scores) about 0.8 us slower).
+      constexpr int D0 = KS == 8 ? 0 : KS / 2;
 #pragma unroll
       for (int n = 0; n < NL; ++n)
         if (kk >= D0 && D0 + n * (KS - D0) / NL == kk) issue_one(nxt, src, n);
