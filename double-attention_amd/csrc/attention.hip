@@ -848,9 +848,10 @@ __global__ __launch_bounds__(NW * 64, 1) void attention_kernel(AttnParams p) {
 // slot 1 of ya when the unit does not open ya's run, else in slot 0.  With
 // the map mix the output is sum_s alpha_s O_s over the split units plus the
 // partial mixes of the whole units, one per workgroup ya .. yb of the tile
-// (slot rule as for pieces, offset by two slots).  Each wave takes one query
-// row, its lanes covering consecutive features, so every partial row is read
-// by one coalesced sweep.
+// (slot rule as for pieces, offset by two slots).  A workgroup takes 32 query
+// rows of the tile, each wave eight of them; the lanes cover consecutive
+// features, so a partial row is one coalesced sweep, and the loads of a
+// piece's eight rows are issued together.
 template <typename TV, int DS, int QT, bool MULTI, int PIECE>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
   const int qt = static_cast<int>(blockIdx.y);
@@ -870,22 +871,27 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
     return p.part + ((static_cast<int64_t>(blockIdx.x) * p.n_seg + y) * NSLOT + k + first) * slot_bytes;
   };
   const int lane = lane_id();
-  // blockIdx.z picks four query rows of the tile, one per wave.
-  const int ql = static_cast<int>(blockIdx.z) * 4 + (static_cast<int>(threadIdx.x) >> 6);
-  const int tq = qt * QT + ql;
-  if (tq >= p.T) return;
+  constexpr int RW = 8;                             // query rows per wave
+  static_assert(QT % 32 == 0, "32 rows per workgroup");
+  // blockIdx.z picks 32 rows of the tile; rows past T are merged (their
+  // pieces lie inside the slots) but not stored.
+  const int q_base = static_cast<int>(blockIdx.z) * 32 + (static_cast<int>(threadIdx.x) >> 6) * RW;
   constexpr int NV = DS / 256 > 0 ? DS / 256 : 1;   // 4-feature vectors per lane
-  f32x4 out[NV];
+  f32x4 out[RW][NV];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) out[k] = zero4();
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int k = 0; k < NV; ++k) out[r][k] = zero4();
   if constexpr (MULTI) {
     for (int y = y0; y <= y1; ++y) {
       const char* mix = slot(y, A, 2);
 #pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        const int d4 = (k * 64 + lane) * 4;
-        if (d4 < DS) out[k] += load_piece4<TV, es>(mix, ql * DS + d4);
-      }
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+          const int d4 = (k * 64 + lane) * 4;
+          if (d4 < DS) out[r][k] += load_piece4<TV, es>(mix, (q_base + r) * DS + d4);
+        }
     }
   }
   for (int s = 0; s < p.S; ++s) {
@@ -893,49 +899,69 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p) {
     const int ya = static_cast<int>(start / L);
     const int yb = static_cast<int>((start + n - 1) / L);
     if (ya == yb) continue;   // whole in one run: stored or in that run's mix
-    // One pass with a running maximum: each piece's loads (reference, row
-    // sum, values) are issued together and do not wait on the previous
-    // piece's arithmetic.
-    float M = -INFINITY, den = 0.f;
-    f32x4 o[NV];
+    // One pass with a running maximum per row: a piece's loads (references,
+    // row sums, values of all eight rows) are issued together.
+    float M[RW], den[RW];
+    f32x4 o[RW][NV];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) o[k] = zero4();
+    for (int r = 0; r < RW; ++r) {
+      M[r] = -INFINITY;
+      den[r] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) o[r][k] = zero4();
+    }
     for (int y = ya; y <= yb; ++y) {
       const char* pc = slot(y, start, 0);
       const float* stats = reinterpret_cast<const float*>(pc + static_cast<int64_t>(QT) * DS * es);
-      const float m = stats[ql];
-      const float l = stats[QT + ql];
-      f32x4 v[NV];
+      float m[RW], l[RW];
+      f32x4 v[RW][NV];
 #pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        const int d4 = min((k * 64 + lane) * 4, DS - 4);
-        v[k] = load_piece4<TV, es>(pc, ql * DS + d4);
+      for (int r = 0; r < RW; ++r) {
+        m[r] = stats[q_base + r];
+        l[r] = stats[QT + q_base + r];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+          const int d4 = min((k * 64 + lane) * 4, DS - 4);
+          v[r][k] = load_piece4<TV, es>(pc, (q_base + r) * DS + d4);
+        }
       }
-      if (m == -INFINITY) continue;   // a piece with every key masked
-      const float Mn = fmaxf(M, m);
-      const float f_old = M == -INFINITY ? 0.f : exp2f(M - Mn);
-      const float wl = exp2f(m - Mn) * l;
-      den = den * f_old + wl;
 #pragma unroll
-      for (int k = 0; k < NV; ++k) o[k] = o[k] * f_old + v[k] * wl;
-      M = Mn;
+      for (int r = 0; r < RW; ++r) {
+        if (m[r] == -INFINITY) continue;   // a piece with every key masked
+        const float Mn = fmaxf(M[r], m[r]);
+        const float f_old = M[r] == -INFINITY ? 0.f : exp2f(M[r] - Mn);
+        const float wl = exp2f(m[r] - Mn) * l[r];
+        den[r] = den[r] * f_old + wl;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) o[r][k] = o[r][k] * f_old + v[r][k] * wl;
+        M[r] = Mn;
+      }
     }
-    const float w = (MULTI ? map_weight(p, s) : 1.f) * (den > 0.f ? 1.f / den : 0.f);
+    const float wmap = MULTI ? map_weight(p, s) : 1.f;
 #pragma unroll
-    for (int k = 0; k < NV; ++k) out[k] += o[k] * w;
+    for (int r = 0; r < RW; ++r) {
+      const float w = wmap * (den[r] > 0.f ? 1.f / den[r] : 0.f);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) out[r][k] += o[r][k] * w;
+    }
   }
-  const int64_t at = b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t + ds0;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int d4 = (k * 64 + lane) * 4;
-    if (d4 < DS) {
-      if (p.flags & kAttnOutF32) {
-        *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + at + d4) = out[k];
-      } else {
-        typename Elem<TV>::v4 v;
+  for (int r = 0; r < RW; ++r) {
+    const int tq = qt * QT + q_base + r;
+    if (tq >= p.T) continue;
+    const int64_t at = b * p.out_stride_b + static_cast<int64_t>(tq) * p.out_stride_t + ds0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(out[k][i]);
-        *reinterpret_cast<typename Elem<TV>::v4*>(static_cast<TV*>(p.out) + at + d4) = v;
+    for (int k = 0; k < NV; ++k) {
+      const int d4 = (k * 64 + lane) * 4;
+      if (d4 < DS) {
+        if (p.flags & kAttnOutF32) {
+          *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + at + d4) = out[r][k];
+        } else {
+          typename Elem<TV>::v4 v;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = static_cast<TV>(out[r][k][i]);
+          *reinterpret_cast<typename Elem<TV>::v4*>(static_cast<TV*>(p.out) + at + d4) = v;
+        }
       }
     }
   }
@@ -1206,7 +1232,7 @@ static void launch_attn_4(const AttentionArgs& a, const AttnPlan& plan, AttnPara
   // asks for fp32 outputs.  plan_attention gives it four-wave workgroups
   // only (every key and V^T tile it stages serves 128 queries).
   if constexpr (NW == 4) {
-    const dim3 grid(a.B * p.n_slices, plan.n_seg), merge(a.B * p.n_slices, plan.n_qt, QT / 4);
+    const dim3 grid(a.B * p.n_slices, plan.n_seg), merge(a.B * p.n_slices, plan.n_qt, QT / 32);
     if (attn_piece_bytes(a.flags) == 4) {
       hipLaunchKernelGGL((attention_kernel<TQ, TV, RP, DS, NW, kAttnStages, MULTI, 1, 4>), grid, dim3(NW * 64), 0, s, p);
       hipLaunchKernelGGL((attention_merge_kernel<TV, DS, QT, MULTI, 4>), merge, dim3(256), 0, s, p);
