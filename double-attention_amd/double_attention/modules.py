@@ -283,7 +283,7 @@ class SharedDictionaryAttention(nn.Module):
         )
         if needs_grad:
             return _HipModuleFunction.run(self, x, bank, normalized_dictionary, dtype, return_aux)
-        result = self._hip_call(x, bank, normalized_dictionary, dtype)
+        result = self._hip_call(x, bank, normalized_dictionary, dtype, want_routed=return_aux)
         if not return_aux:
             return result.output
         return result.output, self._hip_aux(result.routed, dtype)
