@@ -1318,9 +1318,16 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
   // Value slice: as wide as possible (one score tile serves more value columns
   // and the softmax is shared by more MFMAs) while the grid keeps at least 256
   // workgroups.  The register budget caps it at 256 features, and at 128 with
-  // the map mix (a second accumulator set) or 512-wide scores.
+  // the map mix (a second accumulator set) or 512-wide scores; a slice width
+  // (256, 128 or 64) divides D, which is a multiple of 64.
   const int64_t tiles = B * plan.n_qt;
-  int64_t ds = std::min<int64_t>(D, (multi || RP == 512) ? 128 : 256);
+  const int64_t cap = (multi || RP == 512) ? 128 : 256;
+  int64_t ds = 64;
+  for (int64_t w = 256; w > 64; w /= 2)
+    if (w <= cap && D % w == 0) {
+      ds = w;
+      break;
+    }
   while (ds > 128 && tiles * (D / ds) < 256) ds /= 2;
   plan.ds = static_cast<int>(ds);
   const int64_t slices = D / ds;
@@ -1388,7 +1395,7 @@ AttnPlan plan_attention(int64_t B, int64_t S, int64_t T, int64_t D, int64_t RP, 
 
 template <typename TQ, typename TV, int RP>
 static void launch_attn_short_d(const AttentionArgs& a, AttnParams& p, hipStream_t s) {
-  if (a.D >= 128) launch_attn_short<TQ, TV, RP, 128>(a, p, s);
+  if (a.D % 128 == 0) launch_attn_short<TQ, TV, RP, 128>(a, p, s);
   else launch_attn_short<TQ, TV, RP, 64>(a, p, s);
 }
 

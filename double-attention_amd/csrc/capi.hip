@@ -31,6 +31,9 @@ int fail(int code, const char* fmt, ...) {
 
 bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 bool pow2_width(int64_t v) { return v == 64 || v == 128 || v == 256 || v == 512; }
+// The attention forward takes value (model) widths that are multiples of 64:
+// its value slices are 64, 128 or 256 features wide.
+constexpr int64_t kMaxValueDim = 4096;
 bool half_dtype(int d) { return d == DA_F16 || d == DA_BF16; }
 bool any_dtype(int d) { return d == DA_F32 || d == DA_F16 || d == DA_BF16; }
 
@@ -93,7 +96,9 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
   if (!types_ok)
     return fail(DA_ERR_UNSUPPORTED, "attention: (qk_dtype, v_dtype) must be (F16,BF16), (F16,F16) or (BF16,BF16)");
   if (!pow2_width(RP)) return fail(DA_ERR_UNSUPPORTED, "attention: score_dim %lld not in {64,128,256,512}", (long long)RP);
-  if (!pow2_width(D)) return fail(DA_ERR_UNSUPPORTED, "attention: value_dim %lld not in {64,128,256,512}", (long long)D);
+  if (D < 64 || D > kMaxValueDim || D % 64)
+    return fail(DA_ERR_UNSUPPORTED, "attention: value_dim %lld must be a multiple of 64 in [64, %lld]", (long long)D,
+                (long long)kMaxValueDim);
   if (B < 0 || T < 0 || S < 1 || rep < 1 || B > 65535 || T > (1LL << 30))
     return fail(DA_ERR_INVALID_ARGUMENT, "attention: bad batch/maps/length/map_repeat");
   if (S > 64) return fail(DA_ERR_UNSUPPORTED, "attention: at most 64 maps (got %lld)", (long long)S);

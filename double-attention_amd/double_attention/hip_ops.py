@@ -40,6 +40,10 @@ from .ops import dictionary_route_reference, routed_attention_reference
 
 _DTYPE_CODES = {torch.float32: _lib.DA_F32, torch.float16: _lib.DA_F16, torch.bfloat16: _lib.DA_BF16}
 SUPPORTED_WIDTHS = (64, 128, 256, 512)
+# The attention forward's value (model) widths: multiples of 64 up to 4096
+# (its value slices are 64, 128 or 256 features wide).
+VALUE_WIDTH_STEP = 64
+MAX_VALUE_WIDTH = 4096
 ATOM_PAD = 64
 TOKEN_PAD = 64
 
@@ -790,6 +794,16 @@ def _next_width(width: int) -> int:
     raise NotImplementedError(f"HIP attention supports widths up to {SUPPORTED_WIDTHS[-1]}, got {width}")
 
 
+def _value_width(width: int) -> int:
+    """The attention forward's value width for ``width`` features: the next
+    multiple of 64 (the tail is zero-padded), at most 4096."""
+
+    padded = _round_up(max(width, 1), VALUE_WIDTH_STEP)
+    if padded > MAX_VALUE_WIDTH:
+        raise NotImplementedError(f"HIP attention supports value widths up to {MAX_VALUE_WIDTH}, got {width}")
+    return padded
+
+
 def value_transposed(value: Tensor, width: int | None = None) -> Tensor:
     """``[B, T, D]`` -> zero-padded V^T in 32-token tiles ``[B, Tp/32, width, 32]``."""
 
@@ -808,16 +822,16 @@ def _attention_forward(
     vt: Tensor | None = None, out_dtype: torch.dtype | None = None,
 ) -> Tensor:
     """Per-map outputs ``[B, S, T, D]``; the values come as rows ``value``
-    ``[B, T, D]`` or already as the projection's V^T tiles ``vt`` (D a
-    supported width).  ``out_dtype`` torch.float32 keeps the outputs in fp32
-    (else the value dtype)."""
+    ``[B, T, D]`` (zero-padded to a multiple of 64 features) or already as the
+    projection's V^T tiles ``vt`` (D a multiple of 64).  ``out_dtype``
+    torch.float32 keeps the outputs in fp32 (else the value dtype)."""
 
     batch, maps, length, score_dim = query.shape
     model_dim = value.shape[-1] if vt is None else vt.shape[2]
     value_dtype = value.dtype if vt is None else vt.dtype
     device = query.device
     score_width = _next_width(score_dim)
-    value_width = _next_width(model_dim)
+    value_width = _value_width(model_dim)
     q = query.detach()
     k = key.detach()
     if score_width != score_dim:
@@ -829,7 +843,7 @@ def _attention_forward(
     if vt is None:
         vt = value_transposed(value, value_width)
     elif value_width != model_dim:
-        raise ValueError("V^T tiles need a supported value width")
+        raise ValueError(f"V^T tiles need a value width that is a multiple of {VALUE_WIDTH_STEP}")
     out_f32 = out_dtype == torch.float32
     out = torch.empty(batch, maps, length, value_width, dtype=torch.float32 if out_f32 else value_dtype, device=device)
     scales_c = scales.detach().contiguous()
@@ -881,7 +895,7 @@ def _attention_backward(
     batch, maps, length, score_dim = query.shape
     model_dim = value.shape[-1]
     score_width = _next_width(score_dim)
-    value_width = _next_width(model_dim)
+    value_width = _next_width(model_dim)   # the backward kernels take 64 .. 512
     rows = batch * maps
     device = value.device
     q = _padded_rows(query.detach(), score_width)
@@ -1202,8 +1216,10 @@ def check_module_supported(config) -> None:
     group = config.qk_branches // config.outer_maps if config.qk_branches > config.outer_maps else 1
     if group * config.routing_dim not in SUPPORTED_WIDTHS:
         raise NotImplementedError("backend='hip' supports grouped score widths up to 512")
-    if config.model_dim not in SUPPORTED_WIDTHS:
-        raise NotImplementedError(f"backend='hip' supports model_dim in {SUPPORTED_WIDTHS}")
+    if config.model_dim % VALUE_WIDTH_STEP or not VALUE_WIDTH_STEP <= config.model_dim <= MAX_VALUE_WIDTH:
+        raise NotImplementedError(
+            f"backend='hip' supports model_dim a multiple of {VALUE_WIDTH_STEP} in [{VALUE_WIDTH_STEP}, {MAX_VALUE_WIDTH}]"
+        )
     if config.outer_maps > 64:
         raise NotImplementedError("backend='hip' supports at most 64 outer maps")
 

@@ -235,7 +235,8 @@ int da_dictionary_route_backward_rows(const float* logits, const float* grad_wei
  *   score_bound: 0, or an upper bound on |q . k| over all raw query/key rows
  *     (1 for L2-normalized rows).  With a bound, maps whose scaled bound fits
  *     the probability type skip the online-softmax rescaling (bf16 V only).
- * maps <= 64.  score_dim and value_dim must be 64, 128, 256 or 512.  Element types:
+ * maps <= 64.  score_dim must be 64, 128, 256 or 512; value_dim a multiple of
+ * 64 in [64, 4096].  Element types:
  *   (qk_dtype, v_dtype) in {(F16, BF16), (F16, F16), (BF16, BF16)}; the output
  *   has v_dtype, or fp32 with DA_ATTN_OUT_F32 (strides then count floats, and
  *   out must be 16-byte aligned).
@@ -338,7 +339,9 @@ int da_linear_ex(const void* x, int64_t rows, int64_t in_features, const void* w
 int da_layer_norm(const void* x, int64_t rows, int64_t dim, const void* weight, const void* bias, int param_dtype,
                   float eps, int dtype, void* out, da_stream_t stream);
 
-/* Whole SharedDictionaryAttention forward (modules.py:190-291). */
+/* Whole SharedDictionaryAttention forward (modules.py:190-291): model_dim a
+ * multiple of 64 in [64, 4096], routing_dim (and the grouped score width) in
+ * {64, 128, 256, 512}. */
 typedef struct da_sda_forward_args {
   const void* x;            /* [batch, length, model_dim] */
   int64_t batch, length, model_dim;

@@ -417,6 +417,12 @@ def test_route_variants(dtype, variant, normalize_input, normalize_output, routi
     (3, 3, 50, 128, 256, (9.0, 13.0, 20.0)),   # three maps: two map groups
     (2, 1, 64, 256, 512, (120.0,)),           # large scale: exact row maxima
     (5, 2, 20, 64, 64, (-8.0, 16.0)),         # negative scale folded into the queries
+    # Value widths outside {64, ..., 512}: 64-feature slices where 128 does not
+    # divide the width, a zero-padded tail, wider than 512.
+    (2, 2, 40, 128, 192, (12.0, 14.0)),       # short kernel, 64-feature slices
+    (1, 1, 1500, 128, 320, (13.0,)),          # stream split, 64-feature slices
+    (2, 1, 300, 256, 768, (15.0,)),           # 256-feature slices
+    (1, 2, 129, 64, 1000, (10.0, 12.0)),      # padded to 1024
 ])
 def test_routed_attention(dtype, causal, score_bound, batch, maps, length, score_dim, value_dim, scales) -> None:
     # Rows are unit vectors, so 1.01 bounds every score: bf16 maps whose scaled
@@ -630,6 +636,19 @@ def test_module_variants_odd_shapes(preset, overrides) -> None:
     run_module_case(preset, (1, 1, 512), seed=4, relative_to_torch=relative, **overrides)
 
 
+@pytest.mark.parametrize(("preset", "overrides", "shape"), [
+    ("a1", {"model_dim": 192}, (2, 33, 192)),     # 64-feature value slices
+    ("a1", {"model_dim": 192}, (1, 700, 192)),
+    ("a1", {"model_dim": 768}, (2, 300, 768)),    # 256-feature slices, three per sequence
+    ("qk2-s2", {"model_dim": 384}, (2, 100, 384)),   # map mix: 128-feature slices
+    ("a1", {"model_dim": 1024}, (1, 2000, 1024)),    # stream split
+    ("qk2-s2", {"model_dim": 320, "map_combine": "concat"}, (2, 60, 320)),
+])
+def test_module_model_widths(preset, overrides, shape) -> None:
+    # model_dim need not be a power of two: any multiple of 64 up to 4096.
+    run_module_case(preset, shape, seed=9, **overrides)
+
+
 @pytest.mark.parametrize("preset", [
     "a1-silu", "a1-silu-logitnorm", "a1-silu-logitnorm-t1", "a1-no-softmax", "a1-no-softmax-g4",
 ])
@@ -698,6 +717,31 @@ def test_lm_c4_qk2_s2_tied(dtype) -> None:
     print(f"[parity] lm c4 {dtype} torch path rel_l2={torch_rel:.3e} max_abs={torch_max:.3e}", flush=True)
     assert_parity(logits, expected, rel_l2=max(5e-3, 1.1 * torch_rel), max_abs=max(2e-2, 1.1 * torch_max),
                   label=f"lm c4 {dtype}")
+
+
+def test_lm_model_width_192() -> None:
+    # A two-layer LM whose model width is not a power of two: LayerNorm,
+    # the fused attention (64-feature value slices) and the FFN GEMMs (576).
+    device = _device()
+    config = da.experiment_config("qk2-s2", model_dim=192, backend="hip")
+    torch.manual_seed(2)
+    model = da.DoubleAttentionLM(512, 128, config, 2, dictionary_group_size=2, feedforward_dim=576)
+    model = model.to(device=device, dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, 512, (4, 80), generator=torch.Generator().manual_seed(3))
+    with torch.inference_mode():
+        logits, _ = model(ids.to(device))
+        torch_model = da.DoubleAttentionLM(
+            512, 128, config.with_updates(backend="torch"), 2, dictionary_group_size=2, feedforward_dim=576
+        ).to(device=device, dtype=torch.bfloat16).eval()
+        torch_model.load_state_dict(model.state_dict())
+        torch_logits, _ = torch_model(ids.to(device))
+    expected = oracle.double_attention_lm(oracle_params(model), config, ids.numpy(), 2, 2, dtype=np.float32)
+    e = expected.astype(np.float64)
+    torch_rel = np.linalg.norm(np32(torch_logits) - e) / np.linalg.norm(e)
+    torch_max = np.abs(np32(torch_logits) - e).max()
+    print(f"[parity] lm d192 torch path rel_l2={torch_rel:.3e} max_abs={torch_max:.3e}", flush=True)
+    assert_parity(logits, expected, rel_l2=max(5e-3, 1.1 * torch_rel), max_abs=max(2e-2, 1.1 * torch_max),
+                  label="lm d192")
 
 
 def test_lm_training_gradients(monkeypatch) -> None:
@@ -887,6 +931,11 @@ MODULE_BACKWARD_CASES = [
     # Tied banks: the key atoms' raw gradient collects both roles.
     ("a1", {"untied_dictionary": False}, 40),
     ("a1-r512-d1536", {"untied_dictionary": False}, 40),
+    # model_dim 192: the attention backward pads the values to 256 features;
+    # 768: wider than its kernels, so that one stage runs autograd of the
+    # fp32 torch composition.
+    ("a1", {"model_dim": 192}, 40),
+    ("a1", {"model_dim": 768}, 40),
 ]
 
 
@@ -929,17 +978,19 @@ def test_module_backward_runs_native_kernels(monkeypatch, preset, overrides, tok
         reference = da.SharedDictionaryAttention(config.with_updates(backend="torch")).to(device, torch.float32)
         reference.load_state_dict({k: v.float() for k, v in module.state_dict().items()})
         g = torch.Generator().manual_seed(seed + 1)
-        x = torch.randn(2, tokens, 512, generator=g).to(device, torch.bfloat16)
-        w = torch.randn(2, tokens, 512, generator=g).to(device)
+        x = torch.randn(2, tokens, config.model_dim, generator=g).to(device, torch.bfloat16)
+        w = torch.randn(2, tokens, config.model_dim, generator=g).to(device)
         grads = []
         calls.clear()
         for m, dtype in ((module, torch.bfloat16), (torch_bf16, torch.bfloat16), (reference, torch.float32)):
             xi = x.detach().to(dtype).clone().requires_grad_()
             (m(xi).float() * w).sum().backward()
             grads.append([xi.grad] + [p.grad for p in m.parameters()])
-        # One attention backward and one native route backward; the only
-        # route launch is the module forward's (the backward reuses its r).
-        assert calls.count("_attention_backward") + calls.count("_attention_backward_dense") == 1, calls
+        # One attention backward (native up to 512 value features) and one
+        # native route backward; the only route launch is the module
+        # forward's (the backward reuses its r).
+        native_attention = 1 if config.model_dim <= 512 else 0
+        assert calls.count("_attention_backward") + calls.count("_attention_backward_dense") == native_attention, calls
         assert calls.count("_route_backward") + calls.count("_route_backward_rows") == 1, calls
         assert calls.count("_route_forward") == 1, calls
         names = ["x"] + [n for n, _ in module.named_parameters()]

@@ -248,8 +248,13 @@ def test_hip_supports_every_preset_and_rejects_other_widths() -> None:
         check_module_supported(da.experiment_config(name))
     with pytest.raises(NotImplementedError):
         check_module_supported(da.experiment_config("a1", routing_dim=96))
-    with pytest.raises(NotImplementedError):
-        check_module_supported(da.experiment_config("a1", model_dim=384))
+    # model_dim: any multiple of 64 up to 4096 (the attention's value slices
+    # are 64, 128 or 256 features wide).
+    for model_dim in (64, 192, 384, 768, 1024, 4096):
+        check_module_supported(da.experiment_config("a1", model_dim=model_dim))
+    for model_dim in (100, 32, 4160):
+        with pytest.raises(NotImplementedError):
+            check_module_supported(da.experiment_config("a1", model_dim=model_dim))
 
 
 def test_route_variant_flags_follow_the_config() -> None:
@@ -300,7 +305,8 @@ def test_auto_backend_picks_torch_for_uncovered_configs() -> None:
     # "hip" raises for it instead (host logic: no GPU needed).
     assert modules._hip_covers(da.experiment_config("a1"))
     assert not modules._hip_covers(da.experiment_config("a1", routing_dim=96))
-    assert not modules._hip_covers(da.experiment_config("a1", model_dim=384))
+    assert not modules._hip_covers(da.experiment_config("a1", model_dim=100))
+    assert modules._hip_covers(da.experiment_config("a1", model_dim=384))
 
 
 def test_module_operands_follow_parameter_updates() -> None:
