@@ -179,7 +179,9 @@ struct RouteBwdRowsArgs {
   int out_dtype;
   float* dbeta_rows;          // [rows] or nullptr
 };
-constexpr int kRouteBwdRowsMaxAtoms = 4096;
+// Rows of up to 4096 columns are held in registers; longer rows take a
+// multi-pass kernel over the row.
+constexpr int kRouteBwdRowsMaxAtoms = 1 << 24;
 void launch_route_backward_rows(const RouteBwdRowsArgs& a, hipStream_t stream);
 
 // LayerNorm over the last dimension (dim a multiple of 8, at most 4096).

@@ -18,8 +18,9 @@
 //            da0 = isd (dc - mean dc - c mean(dc c))
 //   SiLU activation: dl = da0 2 SiLU'(l),  SiLU'(x) = sig(x) (1 + x (1 - sig(x)))
 // One wave per row, the row's atoms strided over the lanes and held in VGPRs
-// (NPL per lane, M <= 64 NPL), so every reduction is a wave reduction and the
-// two inputs are read once, coalesced.  The outer attention's backward uses
+// (NPL per lane, M <= 64 NPL <= 4096), so every reduction is a wave reduction
+// and the two inputs are read once, coalesced; longer rows take the
+// multi-pass kernel below.  The outer attention's backward uses
 // the same kernel for its softmax (scores as logits, dP as dW, gamma as beta,
 // a causal row length).
 #include "da_common.h"
@@ -164,10 +165,185 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
   if (a.dbeta_rows && lane == 0) a.dbeta_rows[row] = direct ? 0.f : dbeta;
 }
 
+// Rows longer than the register-held kernel's 4096 columns: the same algebra
+// in passes over the row, each re-reading the fp32 inputs (written just
+// before by the GEMMs) 1024 columns at a time and forming the forward values
+// again: the standardization's mean, then its variance; the softmax's
+// maximum, normalizer and sum_j w_j dW_j in one pass with a running maximum
+// per lane; then d beta and the standardization's backward sums; then the
+// outputs.  One wave per row, as above.
+template <typename TO>
+__global__ __launch_bounds__(256) void route_backward_long_rows_kernel(RouteBwdRowsArgs a) {
+  constexpr int CH = 16;        // columns per lane in one chunk
+  constexpr int CW = 64 * CH;   // columns per chunk
+  const int lane = lane_id();
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + uniform_wave();
+  if (row >= a.rows) return;   // whole waves
+  const int M = a.causal_period ? min(a.atoms, static_cast<int>(row % a.causal_period) + 1) : a.atoms;
+  const float* lrow = a.logits + row * a.ld_in;
+  const float* grow = a.grad_weights + row * a.ld_in;
+  const bool silu_logits = a.flags & kRouteSiluLogits;
+  const bool standardize = a.flags & kRouteStandardize;
+  const bool direct = a.flags & kRouteDirectSilu;
+  const int64_t beta_index = a.beta_count > 1 ? (row / a.beta_period) % a.beta_count : 0;
+  const ScalarHalves beta_bits = fetch_scalar(a.beta_ptr ? a.beta_ptr : static_cast<const void*>(a.logits),
+                                              a.beta_ptr ? a.beta_dtype : kF32, a.beta_ptr ? beta_index : 0);
+  const float beta_raw = a.beta_ptr ? scalar_value(beta_bits, a.beta_dtype) : a.beta_value;
+  const float beta = (a.flags & kRouteBetaIsLog) ? expf(fminf(fmaxf(beta_raw, kLogBetaMin), kLogBetaMax)) : beta_raw;
+  const float inv_m = 1.f / static_cast<float>(M);
+  auto act = [&](float x) { return silu_logits ? 2.f * x * sigmoidf(x) : x; };
+
+  // Standardization statistics (two passes: the mean, then the spread).
+  float mean = 0.f, isd = 1.f;
+  if (standardize) {
+    float s1 = 0.f;
+    for (int j0 = 0; j0 < M; j0 += CW) {
+      float v[CH];
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int j = j0 + lane + 64 * i;
+        v[i] = j < M ? act(lrow[j]) : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < CH; ++i) s1 += v[i];
+    }
+    mean = wave_sum64(s1) * inv_m;
+    float s2 = 0.f;
+    for (int j0 = 0; j0 < M; j0 += CW) {
+      float v[CH];
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int j = j0 + lane + 64 * i;
+        v[i] = j < M ? act(lrow[j]) - mean : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < CH; ++i) s2 += v[i] * v[i];
+    }
+    isd = rsqrtf(wave_sum64(s2) * inv_m + a.eps);
+  }
+  const float s = standardize ? a.logit_scale : 1.f;
+  auto cval = [&](float x) { return standardize ? (act(x) - mean) * isd : act(x); };
+
+  // Softmax statistics: maximum, normalizer and sum_j w_j dW_j (running
+  // maximum per lane, merged over the wave at the end).
+  float mx = 0.f, inv_z = 0.f, d = 0.f;
+  if (!direct) {
+    float m_l = -INFINITY, z_l = 0.f, dn_l = 0.f;
+    for (int j0 = 0; j0 < M; j0 += CW) {
+      float x[CH], gv[CH];
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int j = j0 + lane + 64 * i;
+        x[i] = j < M ? beta * (cval(lrow[j]) * s) : -INFINITY;
+        gv[i] = j < M ? grow[j] : 0.f;
+      }
+      float cm = m_l;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) cm = fmaxf(cm, x[i]);
+      if (cm > m_l) {
+        const float f = m_l == -INFINITY ? 0.f : __expf(m_l - cm);
+        z_l *= f;
+        dn_l *= f;
+        m_l = cm;
+      }
+      if (m_l != -INFINITY) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          const float e = x[i] == -INFINITY ? 0.f : __expf(x[i] - m_l);
+          z_l += e;
+          dn_l += e * gv[i];
+        }
+      }
+    }
+    mx = wave_max64(m_l);
+    const float f = m_l == -INFINITY ? 0.f : __expf(m_l - mx);
+    inv_z = 1.f / wave_sum64(z_l * f);
+    d = wave_sum64(dn_l * f) * inv_z;
+  }
+
+  // Per column: the weight and the gradient at the assignment logits (times
+  // s), and the column's d beta term.
+  auto column = [&](float lj, float gj, float& wj, float& cj, float& db) {
+    cj = cval(lj);
+    if (direct) {
+      const float x = a.silu_gain * (cj * s);
+      const float sg = sigmoidf(x);
+      wj = (2.f / a.silu_gain) * x * sg;
+      db = 0.f;
+      return gj * 2.f * sg * (1.f + x * (1.f - sg)) * s;
+    }
+    wj = __expf(beta * (cj * s) - mx) * inv_z;
+    const float dsc = wj * (gj - d);
+    db = dsc * (cj * s);
+    return beta * dsc * s;
+  };
+
+  // d beta and the standardization's backward sums.
+  float dbeta = 0.f, m1 = 0.f, m2 = 0.f;
+  if (!direct || standardize) {
+    for (int j0 = 0; j0 < M; j0 += CW) {
+      float lv[CH], gv[CH];
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int j = j0 + lane + 64 * i;
+        lv[i] = j < M ? lrow[j] : 0.f;
+        gv[i] = j < M ? grow[j] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        if (j0 + lane + 64 * i < M) {
+          float wj, cj, db;
+          const float gs = column(lv[i], gv[i], wj, cj, db);
+          dbeta += db;
+          m1 += gs;
+          m2 += gs * cj;
+        }
+      }
+    }
+    dbeta = wave_sum64(dbeta);
+    m1 = wave_sum64(m1) * inv_m;
+    m2 = wave_sum64(m2) * inv_m;
+  }
+
+  // Outputs.
+  TO* dl_row = static_cast<TO*>(a.grad_logits) + row * a.ld_out;
+  TO* w_row = static_cast<TO*>(a.weights) + row * a.ld_out;
+  for (int j0 = 0; j0 < a.atoms; j0 += CW) {
+    float lv[CH], gv[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int j = j0 + lane + 64 * i;
+      lv[i] = j < M ? lrow[j] : 0.f;
+      gv[i] = j < M ? grow[j] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int j = j0 + lane + 64 * i;
+      if (j < a.atoms) {
+        float wj = 0.f, gj = 0.f;
+        if (j < M) {
+          float cj, db;
+          gj = column(lv[i], gv[i], wj, cj, db);
+          if (standardize) gj = isd * (gj - m1 - cj * m2);
+          if (silu_logits) {
+            const float sg = sigmoidf(lv[i]);
+            gj *= 2.f * sg * (1.f + lv[i] * (1.f - sg));
+          }
+        }
+        dl_row[j] = static_cast<TO>(gj);
+        w_row[j] = static_cast<TO>(wj);
+      }
+    }
+  }
+  if (a.dbeta_rows && lane == 0) a.dbeta_rows[row] = direct ? 0.f : dbeta;
+}
+
 template <typename TO>
 static void launch_route_bwd_rows_t(const RouteBwdRowsArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
-  if (a.atoms <= 512) {
+  if (a.atoms > 4096) {
+    hipLaunchKernelGGL((route_backward_long_rows_kernel<TO>), grid, dim3(256), 0, s, a);
+  } else if (a.atoms <= 512) {
     hipLaunchKernelGGL((route_backward_rows_kernel<TO, 8>), grid, dim3(256), 0, s, a);
   } else if (a.atoms <= 1024) {
     hipLaunchKernelGGL((route_backward_rows_kernel<TO, 16>), grid, dim3(256), 0, s, a);

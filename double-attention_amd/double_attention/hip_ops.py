@@ -502,8 +502,9 @@ def _route_backward(
     )
 
 
-# The row kernel holds a row's atoms in VGPRs (at most 4096).
-ROUTE_BACKWARD_ROWS_MAX_ATOMS = 4096
+# The row kernel holds rows of up to 4096 atoms in VGPRs and takes longer
+# rows in passes over the row; the bound is the C ABI's.
+ROUTE_BACKWARD_ROWS_MAX_ATOMS = 1 << 24
 
 
 def route_backward_is_native(routing_dim: int, atoms: int, dtype: torch.dtype, variant: RouteVariant) -> bool:
@@ -939,10 +940,12 @@ def _native_backward_supported(query: Tensor, value: Tensor) -> bool:
 
 
 # 512-wide scores whose score matrices fit (B*S*T*T fp32 <= 512 MiB, T <= the
-# row kernel's 4096 columns) take the dense backward: there the flash
-# backward splits each key tile over two workgroups and forms S and dP twice.
+# 4096 columns the row kernel holds in registers) take the dense backward:
+# there the flash backward splits each key tile over two workgroups and forms
+# S and dP twice.
 DENSE_BACKWARD_MIN_SCORE_DIM = 512
 DENSE_BACKWARD_MAX_SCORES = 1 << 27
+DENSE_BACKWARD_MAX_LENGTH = 4096
 
 
 def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
@@ -951,7 +954,7 @@ def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
         score_dim >= DENSE_BACKWARD_MIN_SCORE_DIM
         and score_dim <= BACKWARD_SCORE_WIDTHS[-1]
         and value.shape[-1] <= SUPPORTED_WIDTHS[-1]
-        and 1 <= length <= ROUTE_BACKWARD_ROWS_MAX_ATOMS
+        and 1 <= length <= DENSE_BACKWARD_MAX_LENGTH
         and batch * maps * length * length <= DENSE_BACKWARD_MAX_SCORES
         and maps <= 64
     )

@@ -220,7 +220,8 @@ def test_route_backward_rows_rejects_bad_arguments() -> None:
         args.update(kw)
         return h.da_dictionary_route_backward_rows(*args.values())
 
-    assert call(atoms=5000) == -2                       # more atoms than the row kernel holds
+    big = (1 << 24) + 1
+    assert call(atoms=big, ld_in=big, ld_out=big) == -2    # more atoms than the row kernels take
     assert call(flags=lib.DA_ROUTE_NORMALIZE_INPUT) == -1   # not a flag of this entry point
     assert call(out_dtype=lib.DA_F32) == -1
     assert call(ld_in=50) == -1

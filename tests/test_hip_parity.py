@@ -936,6 +936,9 @@ MODULE_BACKWARD_CASES = [
     # fp32 torch composition.
     ("a1", {"model_dim": 192}, 40),
     ("a1", {"model_dim": 768}, 40),
+    # A bank of 5000 atoms with SiLU logits: the route backward's multi-pass
+    # row kernel.
+    ("a1-silu", {"dictionary_size": 5000}, 40),
 ]
 
 
@@ -1190,6 +1193,11 @@ ROUTE_ROWS_CASES = [
     (150, 256, 700, False, False, dict(direct_silu=True, silu_gain=3.0)),
     (120, 128, 512, True, True, dict(silu_logits=True, standardize_logits=True)),
     (120, 256, 512, True, True, dict(silu_logits=True, standardize_logits=True, direct_silu=True, silu_gain=2.0)),
+    # Banks above 4096 atoms: the multi-pass row kernel.
+    (80, 256, 5000, True, True, {}),
+    (70, 128, 9000, True, True, dict(silu_logits=True, standardize_logits=True)),
+    (60, 512, 6000, False, True, dict(direct_silu=True, silu_gain=2.0)),
+    (60, 128, 4500, True, False, dict(standardize_logits=True, direct_silu=True)),
 ]
 
 

@@ -288,14 +288,16 @@ def test_backward_dispatch_rules() -> None:
     assert hip_ops.ROUTE_BACKWARD_WIDTHS == (64, 128, 256)
     assert 512 in hip_ops.BACKWARD_SCORE_WIDTHS
     assert silu.flags() != 0 and standard.flags() == 0
-    # The row-kernel path takes every width and variant up to 4096 atoms, on the GPU only.
+    # The row-kernel path takes every width, variant and bank size, on the GPU only.
     assert not hip_ops._route_backward_rows_supported(meta, key)
-    assert hip_ops.ROUTE_BACKWARD_ROWS_MAX_ATOMS == 4096
+    assert hip_ops.ROUTE_BACKWARD_ROWS_MAX_ATOMS == 1 << 24
+    assert hip_ops.DENSE_BACKWARD_MAX_LENGTH == 4096
     # route_backward_is_native: the module's choice of the raw-bank path.
     assert hip_ops.route_backward_is_native(256, 512, torch.bfloat16, standard)
     assert hip_ops.route_backward_is_native(512, 1536, torch.float16, silu)
     assert hip_ops.route_backward_is_native(128, 4096, torch.bfloat16, silu)
-    assert not hip_ops.route_backward_is_native(512, 4097, torch.bfloat16, standard)
+    assert hip_ops.route_backward_is_native(512, 4097, torch.bfloat16, standard)
+    assert hip_ops.route_backward_is_native(256, 20000, torch.float16, silu)
     assert not hip_ops.route_backward_is_native(256, 512, torch.float32, standard)
     assert not hip_ops.route_backward_is_native(96, 512, torch.bfloat16, silu)
 
