@@ -939,25 +939,27 @@ def _native_backward_supported(query: Tensor, value: Tensor) -> bool:
     return score_dim <= BACKWARD_SCORE_WIDTHS[-1] and batch * maps <= 65535 and value.shape[-1] <= SUPPORTED_WIDTHS[-1]
 
 
-# 512-wide scores whose score matrices fit (B*S*T*T fp32 <= 512 MiB, T <= the
-# 4096 columns the row kernel holds in registers) take the dense backward:
-# there the flash backward splits each key tile over two workgroups and forms
-# S and dP twice.
+# The dense backward (library GEMMs around the row kernel, the score matrices
+# materialized: 12 bytes per score) against the key-tile kernels, measured at
+# outer-attention shapes (ms, causal, fp16 q/k, bf16 v): T 8192 R 256: 1.177
+# flash / 0.884 dense; T 4096: 0.376 / 0.265; 4 x 2048: 0.333 / 0.274; 4 x 2048
+# at 512-wide scores: 0.523 / 0.305 (there the flash backward splits each key
+# tile over two workgroups and forms S and dP twice); 8 x 512: 0.126 / 0.243;
+# 8 sequences x 4 maps x 1024 at R 128: 0.397 / 0.399.  So the dense path takes
+# sequences of at least 2048 tokens, 512-wide scores, and value widths past the
+# key-tile kernels' 512, whenever B*S*T*T <= 2^27.
 DENSE_BACKWARD_MIN_SCORE_DIM = 512
+DENSE_BACKWARD_MIN_LENGTH = 2048
 DENSE_BACKWARD_MAX_SCORES = 1 << 27
-DENSE_BACKWARD_MAX_LENGTH = 4096
 
 
 def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
     batch, maps, length, score_dim = query.shape
-    return (
-        score_dim >= DENSE_BACKWARD_MIN_SCORE_DIM
-        and score_dim <= BACKWARD_SCORE_WIDTHS[-1]
-        and value.shape[-1] <= SUPPORTED_WIDTHS[-1]
-        and 1 <= length <= DENSE_BACKWARD_MAX_LENGTH
-        and batch * maps * length * length <= DENSE_BACKWARD_MAX_SCORES
-        and maps <= 64
-    )
+    if not (score_dim <= BACKWARD_SCORE_WIDTHS[-1] and length >= 1 and maps <= 64
+            and batch * maps * length * length <= DENSE_BACKWARD_MAX_SCORES):
+        return False
+    return (score_dim >= DENSE_BACKWARD_MIN_SCORE_DIM or length >= DENSE_BACKWARD_MIN_LENGTH
+            or value.shape[-1] > SUPPORTED_WIDTHS[-1])
 
 
 def _attention_backward_dense(
@@ -1020,9 +1022,10 @@ def attention_gradients(
     needs: tuple[bool, bool, bool, bool] = (True, True, True, True), qk_grad_dtype: torch.dtype | None = None,
 ) -> tuple[Tensor | None, Tensor | None, Tensor | None, Tensor | None]:
     """(dq, dk, dv, dscales) of the outer attention whose output was ``out``:
-    the dense backward for 512-wide scores whose matrices fit, the flash
-    backward kernels otherwise, or autograd of the fp32-softmax reference for
-    score widths above 512.  ``qk_grad_dtype`` (e.g. fp32) keeps dq and dk in
+    the dense backward for long sequences, 512-wide scores and values wider
+    than 512 whose score matrices fit, the flash backward kernels otherwise,
+    or autograd of the fp32-softmax reference for score widths above 512 (or
+    wide values whose matrices do not fit).  ``qk_grad_dtype`` (e.g. fp32) keeps dq and dk in
     that dtype on the native paths instead of rounding them to the inputs'.
     On the dense path the row kernel writes dS (the gradient at q . k) and P
     in the value dtype, so there dq and dk are fp32 sums of 16-bit dS

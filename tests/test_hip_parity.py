@@ -482,6 +482,11 @@ BACKWARD_CASES = [
     (1, 3, 100, 512, 256, True),
     (2, 1, 64, 512, 128, False),
     (1, 1, 1, 512, 64, True),
+    # So do sequences of 2048 tokens or more (rows past 4096 keys: the row
+    # kernel's passes over the row) and values wider than 512.
+    (1, 1, 4500, 256, 128, True),
+    (1, 2, 2100, 128, 64, False),
+    (2, 1, 40, 128, 768, True),
 ]
 
 
@@ -932,8 +937,7 @@ MODULE_BACKWARD_CASES = [
     ("a1", {"untied_dictionary": False}, 40),
     ("a1-r512-d1536", {"untied_dictionary": False}, 40),
     # model_dim 192: the attention backward pads the values to 256 features;
-    # 768: wider than its kernels, so that one stage runs autograd of the
-    # fp32 torch composition.
+    # 768: wider than the key-tile kernels, so the dense backward.
     ("a1", {"model_dim": 192}, 40),
     ("a1", {"model_dim": 768}, 40),
     # A bank of 5000 atoms with SiLU logits: the route backward's multi-pass
@@ -989,11 +993,9 @@ def test_module_backward_runs_native_kernels(monkeypatch, preset, overrides, tok
             xi = x.detach().to(dtype).clone().requires_grad_()
             (m(xi).float() * w).sum().backward()
             grads.append([xi.grad] + [p.grad for p in m.parameters()])
-        # One attention backward (native up to 512 value features) and one
-        # native route backward; the only route launch is the module
-        # forward's (the backward reuses its r).
-        native_attention = 1 if config.model_dim <= 512 else 0
-        assert calls.count("_attention_backward") + calls.count("_attention_backward_dense") == native_attention, calls
+        # One attention backward and one native route backward; the only
+        # route launch is the module forward's (the backward reuses its r).
+        assert calls.count("_attention_backward") + calls.count("_attention_backward_dense") == 1, calls
         assert calls.count("_route_backward") + calls.count("_route_backward_rows") == 1, calls
         assert calls.count("_route_forward") == 1, calls
         names = ["x"] + [n for n, _ in module.named_parameters()]

@@ -291,7 +291,12 @@ def test_backward_dispatch_rules() -> None:
     # The row-kernel path takes every width, variant and bank size, on the GPU only.
     assert not hip_ops._route_backward_rows_supported(meta, key)
     assert hip_ops.ROUTE_BACKWARD_ROWS_MAX_ATOMS == 1 << 24
-    assert hip_ops.DENSE_BACKWARD_MAX_LENGTH == 4096
+    # The dense attention backward: long sequences, 512-wide scores, wide values.
+    assert hip_ops.DENSE_BACKWARD_MIN_LENGTH == 2048
+    assert hip_ops._dense_backward_fits(torch.empty(1, 1, 8192, 256, device="meta"), torch.empty(1, 8192, 512, device="meta"))
+    assert not hip_ops._dense_backward_fits(torch.empty(8, 1, 512, 256, device="meta"), torch.empty(8, 512, 512, device="meta"))
+    assert hip_ops._dense_backward_fits(torch.empty(2, 1, 40, 256, device="meta"), torch.empty(2, 40, 768, device="meta"))
+    assert not hip_ops._dense_backward_fits(torch.empty(1, 1, 20000, 256, device="meta"), torch.empty(1, 20000, 512, device="meta"))
     # route_backward_is_native: the module's choice of the raw-bank path.
     assert hip_ops.route_backward_is_native(256, 512, torch.bfloat16, standard)
     assert hip_ops.route_backward_is_native(512, 1536, torch.float16, silu)
