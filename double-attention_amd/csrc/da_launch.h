@@ -179,8 +179,8 @@ struct RouteBwdRowsArgs {
   int out_dtype;
   float* dbeta_rows;          // [rows] or nullptr
 };
-// Rows of up to 4096 columns are held in registers; longer rows take a
-// multi-pass kernel over the row.
+// Rows of up to 16384 columns are held in registers (one wave up to 4096,
+// a workgroup's four waves above); longer rows take a multi-pass kernel.
 constexpr int kRouteBwdRowsMaxAtoms = 1 << 24;
 void launch_route_backward_rows(const RouteBwdRowsArgs& a, hipStream_t stream);
 

@@ -19,8 +19,9 @@
 //   SiLU activation: dl = da0 2 SiLU'(l),  SiLU'(x) = sig(x) (1 + x (1 - sig(x)))
 // One wave per row, the row's atoms strided over the lanes and held in VGPRs
 // (NPL per lane, M <= 64 NPL <= 4096), so every reduction is a wave reduction
-// and the two inputs are read once, coalesced; longer rows take the
-// multi-pass kernel below.  The outer attention's backward uses
+// and the two inputs are read once, coalesced; rows of up to 16384 atoms are
+// shared by a workgroup's four waves (their sums meet in LDS), and longer rows
+// take the multi-pass kernel below.  The outer attention's backward uses
 // the same kernel for its softmax (scores as logits, dP as dW, gamma as beta,
 // a causal row length).
 #include "da_common.h"
@@ -41,11 +42,34 @@ __device__ __forceinline__ float wave_max64(float v) {
 }
 __device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
 
-template <typename TO, int NPL>
+// WPR waves per row: with WPR = 1 a workgroup's four waves take four rows;
+// with WPR = 4 its waves share one row (column j at wave j / 64 % 4), and the
+// row sums meet in LDS.
+template <typename TO, int NPL, int WPR>
 __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsArgs a) {
+  static_assert(WPR == 1 || WPR == 4, "one wave per row, or the workgroup's four");
+  constexpr int STRIDE = 64 * WPR;   // columns between a lane's consecutive elements
+  __shared__ float red[2][WPR];
   const int lane = lane_id();
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + uniform_wave();
-  if (row >= a.rows) return;   // whole waves
+  const int wave = uniform_wave();
+  const int64_t row = WPR == 1 ? static_cast<int64_t>(blockIdx.x) * 4 + wave : static_cast<int64_t>(blockIdx.x);
+  if (row >= a.rows) return;   // whole waves (WPR 1), or the whole workgroup
+  const int col0 = (WPR == 1 ? 0 : wave * 64) + lane;
+  // Sum or maximum over the row: the wave's lanes, then (WPR 4) the four
+  // waves through one of two LDS slots in turn, so one barrier per call.
+  int slot = 0;
+  auto row_reduce = [&](float v, bool is_max) {
+    v = is_max ? wave_max64(v) : wave_sum64(v);
+    if constexpr (WPR > 1) {
+      if (lane == 0) red[slot][wave] = v;
+      __syncthreads();
+      v = red[slot][0];
+#pragma unroll
+      for (int i = 1; i < WPR; ++i) v = is_max ? fmaxf(v, red[slot][i]) : v + red[slot][i];
+      slot ^= 1;
+    }
+    return v;
+  };
   // With causal_period P, row r (token r % P of its sequence) keeps columns
   // j <= r % P; the others get zero weight and gradient.
   const int M = a.causal_period ? min(a.atoms, static_cast<int>(row % a.causal_period) + 1) : a.atoms;
@@ -62,7 +86,7 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
   float l[NPL], g[NPL];
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
-    const int j = lane + 64 * i;
+    const int j = col0 + STRIDE * i;
     l[i] = j < M ? lrow[j] : 0.f;
     g[i] = j < M ? grow[j] : 0.f;
   }
@@ -79,15 +103,15 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
   if (standardize) {
     float s1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) s1 += lane + 64 * i < M ? c[i] : 0.f;
-    const float mean = wave_sum64(s1) * inv_m;
+    for (int i = 0; i < NPL; ++i) s1 += col0 + STRIDE * i < M ? c[i] : 0.f;
+    const float mean = row_reduce(s1, false) * inv_m;
     float s2 = 0.f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-      c[i] = lane + 64 * i < M ? c[i] - mean : 0.f;
+      c[i] = col0 + STRIDE * i < M ? c[i] - mean : 0.f;
       s2 += c[i] * c[i];
     }
-    isd = rsqrtf(wave_sum64(s2) * inv_m + a.eps);
+    isd = rsqrtf(row_reduce(s2, false) * inv_m + a.eps);
 #pragma unroll
     for (int i = 0; i < NPL; ++i) c[i] *= isd;
   }
@@ -107,29 +131,29 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NPL; ++i)
-      if (lane + 64 * i < M) mx = fmaxf(mx, beta * (c[i] * s));
-    mx = wave_max64(mx);
+      if (col0 + STRIDE * i < M) mx = fmaxf(mx, beta * (c[i] * s));
+    mx = row_reduce(mx, true);
     float z = 0.f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-      w[i] = lane + 64 * i < M ? __expf(beta * (c[i] * s) - mx) : 0.f;
+      w[i] = col0 + STRIDE * i < M ? __expf(beta * (c[i] * s) - mx) : 0.f;
       z += w[i];
     }
-    const float inv_z = 1.f / wave_sum64(z);
+    const float inv_z = 1.f / row_reduce(z, false);
     float d = 0.f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       w[i] *= inv_z;
       d += w[i] * g[i];
     }
-    d = wave_sum64(d);
+    d = row_reduce(d, false);
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       const float dsc = w[i] * (g[i] - d);   // gradient at beta a_j
       dbeta += dsc * (c[i] * s);
       g[i] = beta * dsc;
     }
-    dbeta = wave_sum64(dbeta);
+    dbeta = row_reduce(dbeta, false);
   }
   if (standardize) {
     float m1 = 0.f, m2 = 0.f;
@@ -139,8 +163,8 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
       m1 += g[i];
       m2 += g[i] * c[i];
     }
-    m1 = wave_sum64(m1) * inv_m;
-    m2 = wave_sum64(m2) * inv_m;
+    m1 = row_reduce(m1, false) * inv_m;
+    m2 = row_reduce(m2, false) * inv_m;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) g[i] = isd * (g[i] - m1 - c[i] * m2);
   }
@@ -156,16 +180,16 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
   TO* w_row = static_cast<TO*>(a.weights) + row * a.ld_out;
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
-    const int j = lane + 64 * i;
+    const int j = col0 + STRIDE * i;
     if (j < a.atoms) {
       dl_row[j] = static_cast<TO>(j < M ? g[i] : 0.f);
       w_row[j] = static_cast<TO>(j < M ? w[i] : 0.f);
     }
   }
-  if (a.dbeta_rows && lane == 0) a.dbeta_rows[row] = direct ? 0.f : dbeta;
+  if (a.dbeta_rows && lane == 0 && (WPR == 1 || wave == 0)) a.dbeta_rows[row] = direct ? 0.f : dbeta;
 }
 
-// Rows longer than the register-held kernel's 4096 columns: the same algebra
+// Rows longer than the register-held kernels' 16384 columns: the same algebra
 // in passes over the row, each re-reading the fp32 inputs (written just
 // before by the GEMMs) 1024 columns at a time and forming the forward values
 // again: the standardization's mean, then its variance; the softmax's
@@ -341,16 +365,23 @@ __global__ __launch_bounds__(256) void route_backward_long_rows_kernel(RouteBwdR
 template <typename TO>
 static void launch_route_bwd_rows_t(const RouteBwdRowsArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
-  if (a.atoms > 4096) {
+  // Up to 4096 columns one wave holds a row; up to 16384 the workgroup's four
+  // waves share it (32 or 64 columns per lane); longer rows take passes.
+  const dim3 per_row(static_cast<unsigned>(a.rows));
+  if (a.atoms > 16384) {
     hipLaunchKernelGGL((route_backward_long_rows_kernel<TO>), grid, dim3(256), 0, s, a);
+  } else if (a.atoms > 8192) {
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 64, 4>), per_row, dim3(256), 0, s, a);
+  } else if (a.atoms > 4096) {
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 32, 4>), per_row, dim3(256), 0, s, a);
   } else if (a.atoms <= 512) {
-    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 8>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 8, 1>), grid, dim3(256), 0, s, a);
   } else if (a.atoms <= 1024) {
-    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 16>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 16, 1>), grid, dim3(256), 0, s, a);
   } else if (a.atoms <= 2048) {
-    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 32>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 32, 1>), grid, dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 64>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((route_backward_rows_kernel<TO, 64, 1>), grid, dim3(256), 0, s, a);
   }
 }
 

@@ -201,7 +201,7 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  * assignment weights (weights), rows x atoms with pitch ld_out in out_dtype
  * (DA_F16 or DA_BF16), and the row's share of d beta to dbeta_rows[row]
  * (fp32; 0 for DA_ROUTE_DIRECT_SILU; may be NULL).  atoms <= 2^24 (rows of
- * up to 4096 atoms are held in registers, longer rows are passed over several
+ * up to 16384 atoms are held in registers, longer rows are passed over several
  * times).
  * causal_period > 0 limits row r to columns j <= r % causal_period (zeros
  * written past them), and beta may hold beta_count (<= 64) values, row r

@@ -1195,11 +1195,14 @@ ROUTE_ROWS_CASES = [
     (150, 256, 700, False, False, dict(direct_silu=True, silu_gain=3.0)),
     (120, 128, 512, True, True, dict(silu_logits=True, standardize_logits=True)),
     (120, 256, 512, True, True, dict(silu_logits=True, standardize_logits=True, direct_silu=True, silu_gain=2.0)),
-    # Banks above 4096 atoms: the multi-pass row kernel.
+    # Banks above 4096 atoms: rows shared by a workgroup's four waves (up to
+    # 16384 atoms), then the multi-pass row kernel.
     (80, 256, 5000, True, True, {}),
     (70, 128, 9000, True, True, dict(silu_logits=True, standardize_logits=True)),
     (60, 512, 6000, False, True, dict(direct_silu=True, silu_gain=2.0)),
     (60, 128, 4500, True, False, dict(standardize_logits=True, direct_silu=True)),
+    (40, 256, 20000, True, True, {}),
+    (40, 128, 17000, True, True, dict(silu_logits=True, standardize_logits=True)),
 ]
 
 
