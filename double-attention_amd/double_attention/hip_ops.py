@@ -366,8 +366,12 @@ def _route_forward(
 # Routing widths whose route backward runs on the attention backward kernels.
 # Up to 256 they take about the time of the GEMM path and keep fp32
 # accumulation throughout; at 512-wide rows the two-workgroup split recomputes
-# S and dP per half, and the GEMM path around the row kernel is faster.
+# S and dP per half, and the GEMM path around the row kernel is faster.  So
+# is it for banks above 1024 atoms (ms, plain softmax, both norms, against the
+# attention kernels: 16384 rows R 256 M 1536: 0.447 / 0.595; at M 512 the
+# attention kernels take 0.19-0.28 against 0.28-0.29 for 8192-32768 rows).
 ROUTE_BACKWARD_WIDTHS = (64, 128, 256)
+ROUTE_BACKWARD_MAX_ATOMS = 1024
 
 
 def _route_backward_supported(x: Tensor, dictionary_key: Tensor, variant: RouteVariant) -> bool:
@@ -376,7 +380,7 @@ def _route_backward_supported(x: Tensor, dictionary_key: Tensor, variant: RouteV
         and x.is_cuda
         and x.dtype in (torch.float16, torch.bfloat16)
         and x.shape[-1] in ROUTE_BACKWARD_WIDTHS
-        and dictionary_key.shape[1] >= 1
+        and 1 <= dictionary_key.shape[1] <= ROUTE_BACKWARD_MAX_ATOMS
     )
 
 
@@ -676,8 +680,8 @@ def route_gradients(
     """(dx, dDk, dDv, dbeta) of the route for ``d loss / d out = grad``.
 
     The attention backward kernels take the plain softmax route up to
-    256-wide rows; the row kernel with library GEMMs takes every width and
-    variant up to 4096 atoms; beyond that autograd recomputes the torch route.
+    256-wide rows and 1024 atoms; the row kernel with library GEMMs takes
+    every other width, variant and bank size.
     ``needs`` marks the wanted gradients (dbeta only for a tensor beta); ``r``
     is the forward's reconstruction before the output norm, when the caller
     kept it (else one route launch forms it again); ``bank_grad_dtype``

@@ -125,16 +125,18 @@ class SharedDictionaryAttention(nn.Module):
     ``"auto"`` (the kernels when they cover the call, else torch).  Limits of
     the kernels (``hip_ops.check_module_supported``):
 
-    * ``model_dim`` and ``routing_dim`` in {64, 128, 256, 512} (every preset);
-      a grouped score width ``(qk_branches // outer_maps) * routing_dim`` of at
-      most 512; at most 64 outer maps;
+    * ``routing_dim`` in {64, 128, 256, 512}, ``model_dim`` a multiple of 64
+      from 64 to 4096 (every preset); a grouped score width
+      ``(qk_branches // outer_maps) * routing_dim`` of at most 512; at most 64
+      outer maps;
     * ``dictionary_activation`` "identity" or "silu", ``dictionary_assignment``
-      "softmax" or "silu"; any number of atoms and rows in the forward;
+      "softmax" or "silu"; any number of atoms and rows;
     * 16-bit compute (bf16 or fp16 inputs, or autocast) on a ROCm device.
 
-    Training on ``"hip"`` runs the native backward for every covered forward;
-    a bank of more than 4096 atoms takes the route's gradients from autograd
-    of the torch route, and score widths above 512 the outer attention's.
+    Training on ``"hip"`` runs the native backward for every covered forward
+    (any bank size); only model widths above 512 whose score matrices do not
+    fit the dense attention backward take the outer attention's gradients
+    from autograd of the torch composition.
     """
 
     def __init__(
@@ -644,7 +646,7 @@ class _HipModuleFunction(torch.autograd.Function):
         if wants("value.weight"):
             grads["value.weight"] = _mm_tn_f32(d_v, x2d)
         if wants("value.bias"):
-            grads["value.bias"] = d_v.float().sum(0)
+            grads["value.bias"] = d_v.sum(0, dtype=torch.float32)   # fp32 accumulation, no fp32 copy
         tail = [
             grads[name].to(named[name].dtype).reshape(named[name].shape) if name in grads else None
             for name in ctx.param_names
