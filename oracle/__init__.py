@@ -33,6 +33,13 @@ Functions and what pins them (each check is in ``tests/test_oracle.py``):
                               zero output gradient -> zero gradients.
 * ``assemble_score_maps``     RMS-sum identity q'.k' = sum_g q_g.k_g / sqrt(g);
                               repeat layout; shapes.
+* ``assemble_score_maps_backward`` / ``shared_dictionary_attention_backward``
+                              central finite differences in fp64 of x and of
+                              every module parameter (log beta included) for
+                              ten layouts: untied and tied banks, the map mix,
+                              grouped and repeated branches, concat, no output
+                              projection or bias, non-causal, the route
+                              variants.
 * ``shared_dictionary_attention`` / ``double_attention_lm``
                               golden vectors written by the reference's own
                               PyTorch path (``tests/golden/make_golden.py``)
@@ -42,6 +49,7 @@ Functions and what pins them (each check is in ``tests/test_oracle.py``):
 
 from .sda import (
     assemble_score_maps,
+    assemble_score_maps_backward,
     bank_normalized,
     bank_normalized_backward,
     beta_from_log,
@@ -55,10 +63,12 @@ from .sda import (
     routed_attention_backward,
     score_scale_from_log,
     shared_dictionary_attention,
+    shared_dictionary_attention_backward,
 )
 
 __all__ = [
     "assemble_score_maps",
+    "assemble_score_maps_backward",
     "bank_normalized",
     "bank_normalized_backward",
     "beta_from_log",
@@ -72,4 +82,5 @@ __all__ = [
     "routed_attention_backward",
     "score_scale_from_log",
     "shared_dictionary_attention",
+    "shared_dictionary_attention_backward",
 ]

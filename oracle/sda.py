@@ -357,6 +357,157 @@ def shared_dictionary_attention(
     return out
 
 
+def assemble_score_maps_backward(grad_query: np.ndarray, grad_key: np.ndarray, branches: int):
+    """Gradients at the routed branches of :func:`assemble_score_maps` (its
+    three layouts are linear: identity, scaled concatenation of a group, repeat)."""
+
+    outer_maps = grad_query.shape[1]
+    if branches == outer_maps:
+        return grad_query, grad_key
+    if branches > outer_maps:
+        group = branches // outer_maps
+        factor = group ** -0.25
+
+        def ungrouped(g: np.ndarray) -> np.ndarray:
+            b, _, length, gw = g.shape
+            width = gw // group
+            parts = g.reshape(b, outer_maps, length, group, width).transpose(0, 1, 3, 2, 4)
+            return parts.reshape(b, branches, length, width) * factor
+
+        return ungrouped(grad_query), ungrouped(grad_key)
+    repeats = outer_maps // branches
+
+    def summed(g: np.ndarray) -> np.ndarray:
+        b, _, length, width = g.shape
+        return g.reshape(b, branches, repeats, length, width).sum(axis=2)
+
+    return summed(grad_query), summed(grad_key)
+
+
+def shared_dictionary_attention_backward(
+    params: Mapping[str, np.ndarray],
+    cfg: Any,
+    x: np.ndarray,
+    grad_out: np.ndarray,
+    prefix: str = "",
+) -> dict[str, np.ndarray]:
+    """Gradients of :func:`shared_dictionary_attention` (modules.py:190-291
+    under autograd) for ``d loss / d out = grad_out``, the module's own bank.
+
+    The chain of the forward's stages, each through a backward pinned on its
+    own: the output projection, the map combine (the mix softmax's backward
+    ``alpha (da - sum alpha da)``, or the concat split),
+    :func:`routed_attention_backward` (with the score scale's clamp),
+    :func:`assemble_score_maps_backward`, :func:`dictionary_route_backward`
+    over the Q and K rows together (with beta's clamp),
+    :func:`bank_normalized_backward`, then the Q, K and V projections.
+    Returns ``{"x": dx, <state-dict name>: gradient}`` for every parameter
+    (and for ``log_beta`` whether or not it is a parameter).
+    """
+
+    dt = x.dtype
+
+    def p(name: str) -> np.ndarray | None:
+        v = params.get(prefix + name)
+        return None if v is None else np.asarray(v, dtype=dt)
+
+    batch, length, model_dim = x.shape
+    branches = _cfg(cfg, "qk_branches")
+    routing = _cfg(cfg, "routing_dim")
+    maps = _cfg(cfg, "outer_maps")
+    eps = _cfg(cfg, "eps")
+    causal = _cfg(cfg, "causal")
+    grads: dict[str, np.ndarray] = {}
+
+    # Forward again, keeping the intermediates.
+    def project(weight: np.ndarray) -> np.ndarray:
+        return (x @ weight.T).reshape(batch, length, branches, routing).transpose(0, 2, 1, 3)
+
+    query, key = project(p("query.weight")), project(p("key.weight"))
+    value = x @ p("value.weight").T
+    if p("value.bias") is not None:
+        value = value + p("value.bias")
+    raw_key, raw_value = p("bank.raw_key"), p("bank.raw_value")
+    dk, dv = bank_normalized(raw_key, raw_value, eps)
+    log_beta = p("log_beta")
+    beta = float(beta_from_log(log_beta))
+    route_kw = dict(
+        activation=_cfg(cfg, "dictionary_activation"), assignment=_cfg(cfg, "dictionary_assignment"),
+        silu_gain=_cfg(cfg, "dictionary_silu_gain"), standardize_logits=_cfg(cfg, "standardize_dictionary_logits"),
+        standardized_logit_scale=_cfg(cfg, "standardized_logit_scale"),
+        normalize_input=_cfg(cfg, "normalize_routing_input"), normalize_output=_cfg(cfg, "normalize_routing_output"),
+    )
+    rows = np.concatenate([query, key], axis=2)
+    pair = dictionary_route(
+        rows, dk, dv, beta, eps, route_kw["activation"], route_kw["assignment"], route_kw["silu_gain"],
+        route_kw["standardize_logits"], route_kw["standardized_logit_scale"], route_kw["normalize_input"],
+        route_kw["normalize_output"],
+    )
+    score_query, score_key = assemble_score_maps(pair[:, :, :length], pair[:, :, length:], maps)
+    log_scales = p("log_score_scales")
+    scales = score_scale_from_log(log_scales)
+    map_output = routed_attention(score_query, score_key, value, scales, causal)
+    combine = _cfg(cfg, "map_combine")
+    alpha = None
+    if combine == "weighted_sum":
+        combined = map_output[:, 0] if maps == 1 else np.einsum("s,bstd->btd", _softmax(p("map_mix_logits"), 0),
+                                                               map_output)
+        if maps > 1:
+            alpha = _softmax(p("map_mix_logits"), 0)
+    else:
+        combined = map_output.transpose(0, 2, 1, 3).reshape(batch, length, -1)
+
+    # Output projection.
+    g = np.asarray(grad_out, dtype=dt)
+    w_out = p("output.weight")
+    if w_out is not None:
+        grads["output.weight"] = g.reshape(-1, g.shape[-1]).T @ combined.reshape(-1, combined.shape[-1])
+        d_combined = g @ w_out
+    else:
+        d_combined = g
+    # Map combine.
+    if combine == "weighted_sum":
+        if maps == 1:
+            d_maps = d_combined[:, None]
+        else:
+            d_maps = alpha[None, :, None, None] * d_combined[:, None]
+            d_alpha = np.einsum("btd,bstd->s", d_combined, map_output)
+            grads["map_mix_logits"] = alpha * (d_alpha - np.sum(alpha * d_alpha))
+    else:
+        d_maps = d_combined.reshape(batch, length, maps, model_dim).transpose(0, 2, 1, 3)
+    # Outer attention and its score scales (clamp: the gradient passes inside).
+    d_sq, d_sk, d_value, d_scales = routed_attention_backward(score_query, score_key, value, scales, d_maps, causal)
+    inside = (log_scales >= LOG_SCALE_MIN) & (log_scales <= LOG_SCALE_MAX)
+    grads["log_score_scales"] = d_scales * scales * inside
+    # Score maps, then the route of the Q and K rows together.
+    d_rq, d_rk = assemble_score_maps_backward(d_sq, d_sk, branches)
+    d_rows, d_dk, d_dv, d_beta = dictionary_route_backward(
+        rows, dk, dv, beta, np.concatenate([d_rq, d_rk], axis=2), eps, **route_kw
+    )
+    inside_beta = LOG_BETA_MIN <= float(log_beta) <= LOG_BETA_MAX
+    grads["log_beta"] = np.asarray(d_beta * beta * inside_beta, dtype=dt)
+    d_raw_key, d_raw_value = bank_normalized_backward(raw_key, raw_value, d_dk, d_dv, eps)
+    grads["bank.raw_key"] = d_raw_key
+    if d_raw_value is not None:
+        grads["bank.raw_value"] = d_raw_value
+    # Projections.
+    x2 = x.reshape(-1, model_dim)
+
+    def unproject(d: np.ndarray) -> np.ndarray:
+        return d.transpose(0, 2, 1, 3).reshape(-1, branches * routing)
+
+    d_q, d_k = unproject(d_rows[:, :, :length]), unproject(d_rows[:, :, length:])
+    d_v = d_value.reshape(-1, model_dim)
+    grads["query.weight"] = d_q.T @ x2
+    grads["key.weight"] = d_k.T @ x2
+    grads["value.weight"] = d_v.T @ x2
+    if p("value.bias") is not None:
+        grads["value.bias"] = d_v.sum(axis=0)
+    dx = d_q @ p("query.weight") + d_k @ p("key.weight") + d_v @ p("value.weight")
+    grads["x"] = dx.reshape(x.shape)
+    return grads
+
+
 def layer_norm(x: np.ndarray, weight: np.ndarray, bias: np.ndarray, eps: float = 1e-5) -> np.ndarray:
     """``nn.LayerNorm`` over the last axis (biased variance)."""
 

@@ -413,6 +413,81 @@ def test_assemble_repeat_layout() -> None:
         np.testing.assert_array_equal(sk[:, s], q[:, s // 2] + 1)
 
 
+def _module_case(rng, branches=1, maps=1, tied=False, bias=True, output=True, combine="weighted_sum", **route):
+    """A tiny module (model width 8, routing width 4, 6 atoms) as a state dict
+    and its config, with every parameter drawn away from the clamps' edges."""
+
+    d, r, m = 8, 4, 6
+    cfg = dict(qk_branches=branches, routing_dim=r, outer_maps=maps, eps=1e-6, causal=route.pop("causal", True),
+               dictionary_activation="identity", dictionary_assignment="softmax", dictionary_silu_gain=1.0,
+               standardize_dictionary_logits=False, standardized_logit_scale=None, normalize_routing_input=True,
+               normalize_routing_output=True, map_combine=combine)
+    cfg.update(route)
+    params = {
+        "query.weight": rng.standard_normal((branches * r, d)) * 0.5,
+        "key.weight": rng.standard_normal((branches * r, d)) * 0.5,
+        "value.weight": rng.standard_normal((d, d)) * 0.5,
+        "bank.raw_key": rng.standard_normal((r, m)),
+        "log_score_scales": np.log(np.array([2.0, 3.5, 1.2, 2.7][:maps])),
+        "log_beta": np.array(math.log(3.0)),
+    }
+    if bias:
+        params["value.bias"] = rng.standard_normal(d) * 0.1
+    if not tied:
+        params["bank.raw_value"] = rng.standard_normal((r, m))
+    if combine == "weighted_sum" and maps > 1:
+        params["map_mix_logits"] = rng.standard_normal(maps) * 0.5
+    if output:
+        params["output.weight"] = rng.standard_normal((d, d * (maps if combine == "concat" else 1))) * 0.5
+    return params, cfg
+
+
+MODULE_BACKWARD_LAYOUTS = [
+    dict(),
+    dict(tied=True),
+    dict(branches=2, maps=2),
+    dict(branches=2, maps=1),
+    dict(branches=1, maps=2),
+    dict(branches=2, maps=2, combine="concat"),
+    dict(bias=False, output=False),
+    dict(causal=False),
+    dict(dictionary_activation="silu", standardize_dictionary_logits=True, normalize_routing_input=False),
+    dict(dictionary_assignment="silu", dictionary_silu_gain=2.0, standardized_logit_scale=0.7,
+         standardize_dictionary_logits=True),
+]
+
+
+@pytest.mark.parametrize("layout", MODULE_BACKWARD_LAYOUTS, ids=lambda c: "-".join(f"{k}={v}" for k, v in c.items()) or "a1")
+def test_module_backward_matches_finite_differences(layout) -> None:
+    # Loss = sum(W * out); central differences in fp64 of every element of x
+    # and of every parameter (log beta included) pin the composed module
+    # backward: the map combine, the score-map layouts, the clamps, the route
+    # variants, the bank normalization and the projections.
+    rng = np.random.default_rng(11)
+    params, cfg = _module_case(rng, **dict(layout))
+    x = rng.standard_normal((2, 5, 8))
+    w = rng.standard_normal((2, 5, 8))
+    grads = oracle.shared_dictionary_attention_backward(params, cfg, x, w)
+
+    def loss(ps, x_):
+        return float((oracle.shared_dictionary_attention(ps, cfg, x_) * w).sum())
+
+    h = 1e-6
+    targets = [("x", x)] + [(name, v) for name, v in params.items()]
+    for name, arr in targets:
+        numeric = np.zeros(np.shape(arr))
+        for pos in np.ndindex(numeric.shape):
+            def shifted(delta):
+                a = np.array(arr, dtype=np.float64, copy=True)
+                a[pos] += delta
+                if name == "x":
+                    return loss(params, a)
+                return loss({**params, name: a}, x)
+            numeric[pos] = (shifted(h) - shifted(-h)) / (2 * h)
+        scale = max(float(np.abs(numeric).max()), 1e-12)
+        np.testing.assert_allclose(grads[name], numeric, rtol=1e-5, atol=1e-6 * scale, err_msg=name)
+
+
 def test_temperature_clamps() -> None:
     np.testing.assert_allclose(oracle.score_scale_from_log(np.array([-10.0, math.log(16.0), 20.0])), [0.25, 16.0, 1024.0])
     np.testing.assert_allclose(oracle.beta_from_log(np.array([-10.0, math.log(4.0), 20.0])), [0.05, 4.0, 64.0])
