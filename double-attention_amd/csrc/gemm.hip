@@ -16,11 +16,12 @@
 //           run over B * Tp "virtual" tokens (t < Tp, the padded length);
 //           tokens past T reuse the last real row, so the padding is finite.
 // Tiles: 128 x 128 per workgroup when the launch has at least 512 of them
-// (two per CU), else 64 x 128 (twice the workgroups).  64-deep K stages sit
+// (two per CU), else 96 x 128 where that fills one round of 512 workgroups
+// and 64 x 128 would not, else 64 x 128 (twice the workgroups).  64-deep K stages sit
 // in XOR-swizzled LDS tiles (da_tile.h, conflict-free MFMA operand reads)
-// filled by global->LDS DMA, in a ring of two buffers (128-row tiles) or
-// three (64-row tiles); each of the four waves owns a (BI/2) x 64 block
-// (BI/32 x 4 MFMA 16x16x32 blocks).
+// filled by global->LDS DMA, in a ring of two buffers (128- and 96-row
+// tiles) or three (64-row tiles); each of the four waves owns a (BI/2) x 64
+// block (BI/32 x 4 MFMA 16x16x32 blocks).
 //
 // A launch may also carry a dictionary normalization (dict_norm.h): its
 // workgroups precede the GEMM tiles, so the module forward normalizes its bank
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   constexpr int STAGE = Cfg::STAGE;            // P tile, then Q tile
   constexpr int NA = Cfg::NA;
   // Stage buffers: three for 64-row tiles (two workgroups still share a
-  // CU), two for 128-row tiles.
+  // CU), two for 96- and 128-row tiles.
   constexpr int NST = BI == 64 ? 3 : 2;
   static_assert(2 * STAGE >= kNormLdsBytes, "a normalization workgroup reuses the stage buffers");
   __shared__ __attribute__((aligned(1024))) char lds[NST * STAGE];
@@ -324,10 +325,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams prm) {
   // Same-wave LDS round trip: the stores above complete before the loads below.
   T* out = static_cast<T*>(sg.out);
   constexpr int CHUNKS = WI / 8;             // 16-byte chunks per staged row
-  constexpr int ROWS_PER_PASS = 64 / CHUNKS;
+  constexpr int ROWS_PER_PASS = 64 / CHUNKS;   // 16, 10 or 8 rows (WI 32, 48, 64)
+  constexpr int PASSES = (64 + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
 #pragma unroll
-  for (int pass = 0; pass < 64 / ROWS_PER_PASS; ++pass) {
+  for (int pass = 0; pass < PASSES; ++pass) {
     const int jr = pass * ROWS_PER_PASS + lane / CHUNKS;   // staged row (j)
+    // With 48-row blocks a pass covers 60 lanes' chunks and the last pass
+    // 4 rows; other lanes have no chunk.
+    if (lane >= ROWS_PER_PASS * CHUNKS || jr >= 64) continue;
     const int ic = (lane % CHUNKS) * 8;                     // first i of the chunk
     const int64_t j = j0 + wj * 64 + jr;
     const int64_t i = i0 + wi * WI + ic;
@@ -415,8 +420,12 @@ static void launch_gemm_k(const GemmParams& prm, int total, int nb, hipStream_t 
 }
 
 // 128-row tiles when the grid holds two workgroups per CU, else 64-row tiles
-// (twice the workgroups, so two share every CU and hide each other's waits).
+// (twice the workgroups, so two share every CU and hide each other's waits),
+// or 96-row tiles where 64-row ones would need a second, partial round of
+// the 512 workgroup slots and 96-row ones fill at least three quarters of
+// one (e.g. 4096 x 512 -> 1536: 768 tiles of 64 rows, 512 of 96).
 // `norm` (or nullptr) adds a dictionary normalization's workgroups.
+constexpr int kGemmSlots = 512;   // two workgroups per CU
 void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t stream, const NormJob* norm) {
   GemmParams prm;
   const int tiles128 = setup_gemm<128>(segs, nseg, prm);
@@ -424,14 +433,23 @@ void launch_gemm(const GemmSegment* segs, int nseg, int dtype, hipStream_t strea
   const int nb = norm_blocks(prm.norm);
   if (tiles128 + nb == 0) return;
   const bool f16 = dtype == kF16;
-  if (tiles128 >= 512) {
+  if (tiles128 >= kGemmSlots) {
     prm.gemm_blocks = tiles128;
     f16 ? launch_gemm_k<_Float16, 128>(prm, tiles128, nb, stream) : launch_gemm_k<__bf16, 128>(prm, tiles128, nb, stream);
     return;
   }
-  const int total = setup_gemm<64>(segs, nseg, prm);
-  prm.gemm_blocks = total;
-  f16 ? launch_gemm_k<_Float16, 64>(prm, total, nb, stream) : launch_gemm_k<__bf16, 64>(prm, total, nb, stream);
+  const int tiles96 = setup_gemm<96>(segs, nseg, prm);
+  const int tiles64 = setup_gemm<64>(segs, nseg, prm);
+  // (Plain linears only: the Q/K/V launch's V^T segment keeps 64-row tiles.)
+  const bool plain = nseg == 1 && segs[0].mode == 0;
+  if (plain && tiles64 + nb > kGemmSlots && tiles96 + nb <= kGemmSlots && 4 * (tiles96 + nb) >= 3 * kGemmSlots) {
+    setup_gemm<96>(segs, nseg, prm);
+    prm.gemm_blocks = tiles96;
+    f16 ? launch_gemm_k<_Float16, 96>(prm, tiles96, nb, stream) : launch_gemm_k<__bf16, 96>(prm, tiles96, nb, stream);
+    return;
+  }
+  prm.gemm_blocks = tiles64;
+  f16 ? launch_gemm_k<_Float16, 64>(prm, tiles64, nb, stream) : launch_gemm_k<__bf16, 64>(prm, tiles64, nb, stream);
 }
 
 }  // namespace da

@@ -217,7 +217,8 @@ def test_linear(dtype, rows, k, n, bias) -> None:
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize(("rows", "k", "n"), [(33, 512, 1536), (4096, 512, 1536), (4096, 1536, 512), (100, 64, 68)])
+@pytest.mark.parametrize(("rows", "k", "n"), [(33, 512, 1536), (4096, 512, 1536), (4096, 1536, 512), (100, 64, 68),
+                                             (4000, 512, 1400)])   # 96-row tiles, partial in both directions
 def test_linear_gelu_and_residual(dtype, rows, k, n) -> None:
     # The block's FFN: GELU(x W1^T + b1), then h + (. W2^T + b2), against fp32.
     device = _device()
