@@ -24,6 +24,8 @@
 // rows.  Only dQ = dS K needs dS with the query as the row, through LDS.
 // dQ accumulates over key tiles and dK, dV over query runs (and dV over the
 // maps) with fp32 atomics.
+#include <type_traits>
+
 #include "da_common.h"
 #include "da_launch.h"
 #include "da_tile.h"
@@ -36,25 +38,43 @@ constexpr int kQTile = 32;    // queries per step (and tokens per transposed til
 constexpr int kKTile = 64;    // keys per workgroup (16 per wave)
 
 struct BwdParams {
-  const void* q;        // [BS][T][RP] routed queries (score dtype)
-  const void* k;        // [BS][Tk][RP] routed keys
-  const void* v;        // [B][Tk][D] values
-  const void* out;      // [BS][T][D] forward output
+  // Query row t of (sequence b, map s) at q + b q_sb + (s / rep) q_ms + t q_st
+  // (elements, score dtype), key rows alike; grad_query and grad_key (fp32)
+  // use the same strides.  Contiguous [BS][T][RP] rows are q_sb = S T RP,
+  // q_ms = T RP, q_st = RP, rep = 1.
+  const void* q;
+  const void* k;
+  const void* v;        // [B] x v_sb: [Tk][D] value rows (or the prep's copy in vrows)
+  const void* out;      // [BS][T][D] forward output, out_dtype
   const void* dout;     // [BS][T][D] output gradient
   void* qt;             // [BS][Tp/32][RP][32] Q^T tiles (workspace)
   void* kt;             // [BS][Tkp/32][RP][32] K^T tiles
   void* doutt;          // [BS][Tp/32][D][32] dO^T tiles
   float* lse2;          // [BS][T]
   float* dvec;          // [BS][T] rowsum(dO . O)
-  const float* gamma;   // [S] score scales
-  float* dq;            // [BS][T][RP]
-  float* dk;            // [BS][Tk][RP]
+  const void* scales;   // [S] score scales (or their logs), scales_dtype
+  float* dq;
+  float* dk;
   float* dv;            // [B][Tk][D]
-  float* dgamma;        // [S]
+  float* dgamma;        // [S] d loss / d scales[s] (of the logs with scales_log)
+  int64_t q_sb, q_st, q_ms;
+  int64_t k_sb, k_st, k_ms;
+  int rep;
+  int64_t v_sb;         // elements between sequences' value rows
+  // Values given as V^T tiles [B] x vt_sb: [Tkp/32][D][32] (16-bit, vt_dtype):
+  // the prep kernel writes them as rows [B][Tkp][D] (TV) into vrows.
+  const void* vt;
+  int64_t vt_sb;
+  int vt_dtype;
+  void* vrows;
+  int scales_dtype;
+  int scales_log;       // gamma = exp(clamp(scales[s], log_lo, log_hi))
+  float log_lo, log_hi;
+  float scale_mult;     // every gamma times this
   int S, T, Tp, RP, D;
   int Tk, Tkp;          // keys (== T when causal) and their padded count
   int causal;
-  int out_f32;          // out holds fp32 values
+  int out_dtype;        // kF32, kF16 or kBF16
   int qchunk;           // query tiles per workgroup of the main kernel
   int n_chunks;         // query runs per key tile
 };
@@ -65,16 +85,44 @@ __host__ __device__ constexpr int row_pitch(int width) { return width * 2 + 16; 
 constexpr int kTPitch = 80;
 constexpr int kDsPitch = kKTile * 2 + 16;
 
-// Rows [t0, t0+32) of a [len][W] tensor, transposed into a [W][32] tile at
-// `dst` (zero for tokens >= len).  Uses `lds` (32 * row_pitch(W) bytes).
+// First query / key row of sequence x map bs (elements).
+__device__ __forceinline__ int64_t q_rows0(const BwdParams& p, int bs) {
+  const int b = bs / p.S, s = bs - b * p.S;
+  return b * p.q_sb + (s / p.rep) * p.q_ms;
+}
+__device__ __forceinline__ int64_t k_rows0(const BwdParams& p, int bs) {
+  const int b = bs / p.S, s = bs - b * p.S;
+  return b * p.k_sb + (s / p.rep) * p.k_ms;
+}
+
+// The score scale of map s as the kernels apply it: scales[s] (or the
+// clamped exponential of the log) times scale_mult.
+__device__ __forceinline__ float bwd_gamma(const BwdParams& p, int s) {
+  float v = load_scalar(p.scales, p.scales_dtype, s);
+  if (p.scales_log) v = expf(fminf(fmaxf(v, p.log_lo), p.log_hi));
+  return v * p.scale_mult;
+}
+
+// Factor from sum dS (q . k) (the gradient at the applied scale) to the
+// gradient at scales[s]: scale_mult, or for a log, the applied scale where the
+// clamp passes the gradient (log_lo <= scales[s] <= log_hi) and 0 elsewhere.
+__device__ __forceinline__ float bwd_dscale_factor(const BwdParams& p, int s) {
+  const float v = load_scalar(p.scales, p.scales_dtype, s);
+  if (!p.scales_log) return p.scale_mult;
+  return v >= p.log_lo && v <= p.log_hi ? expf(v) * p.scale_mult : 0.f;
+}
+
+// Rows [t0, t0+32) of a [len][W] tensor whose rows are `ld` elements apart,
+// transposed into a [W][32] tile at `dst` (zero for tokens >= len).  Uses
+// `lds` (32 * row_pitch(W) bytes).
 template <typename T, int W>
-__device__ __forceinline__ void transpose_tile(const T* src, int t0, int len, T* dst, char* lds) {
+__device__ __forceinline__ void transpose_tile(const T* src, int64_t ld, int t0, int len, T* dst, char* lds) {
   constexpr int P = row_pitch(W);
   const int tid = static_cast<int>(threadIdx.x);
   __syncthreads();   // the previous user of `lds` is done
   for (int ch = tid; ch < kQTile * W / 8; ch += 256) {
     const int r = ch / (W / 8), c8 = (ch % (W / 8)) * 8;
-    u32x4 v = load16B(src + static_cast<int64_t>(min(t0 + r, len - 1)) * W + c8);
+    u32x4 v = load16B(src + static_cast<int64_t>(min(t0 + r, len - 1)) * ld + c8);
     if (t0 + r >= len) v = u32x4{0u, 0u, 0u, 0u};
     store16B(lds + r * P + c8 * 2, v);
   }
@@ -88,6 +136,36 @@ __device__ __forceinline__ void transpose_tile(const T* src, int t0, int len, T*
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = static_cast<uint32_t>(e[2 * j]) | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
     store16B(dst + f * kQTile + t8, v);
+  }
+}
+
+// Tokens [32 tile, 32 tile + 32) of a V^T tile [D][32] (16-bit of dtype
+// src_dtype) written as rows [32][D] of TV at `dst` (the tile's first row).
+// Uses `lds` (32 * row_pitch(D) bytes).
+template <typename TV, int D>
+__device__ __forceinline__ void vt_tile_to_rows(const uint16_t* src, int src_dtype, TV* dst, char* lds) {
+  constexpr int P = row_pitch(D);
+  const int tid = static_cast<int>(threadIdx.x);
+  const bool same = src_dtype == (std::is_same<TV, __bf16>::value ? kBF16 : kF16);
+  __syncthreads();   // the previous user of `lds` is done
+  for (int ch = tid; ch < D * 4; ch += 256) {
+    const int f = ch / 4, t8 = (ch % 4) * 8;
+    const u32x4 v = load16B(src + f * kQTile + t8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint16_t e = static_cast<uint16_t>(v[j / 2] >> (16 * (j % 2)));
+      if (!same) {
+        const float x = src_dtype == kBF16 ? __uint_as_float(static_cast<uint32_t>(e) << 16)
+                                           : static_cast<float>(__builtin_bit_cast(_Float16, e));
+        e = __builtin_bit_cast(uint16_t, static_cast<TV>(x));
+      }
+      *reinterpret_cast<uint16_t*>(lds + (t8 + j) * P + f * 2) = e;
+    }
+  }
+  __syncthreads();
+  for (int ch = tid; ch < kQTile * D / 8; ch += 256) {
+    const int r = ch / (D / 8), c8 = (ch % (D / 8)) * 8;
+    store16B(dst + static_cast<int64_t>(r) * D + c8, load16B(lds + r * P + c8 * 2));
   }
 }
 
@@ -105,20 +183,24 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
   const int tile = static_cast<int>(blockIdx.x);
   const int t0 = tile * kQTile;
   const int64_t tiles = p.Tp / kQTile, ktiles = p.Tkp / kQTile;
-  const int64_t rows = static_cast<int64_t>(bs) * p.T, krows = static_cast<int64_t>(bs) * p.Tk;
+  const int64_t rows = static_cast<int64_t>(bs) * p.T;
+  const int64_t q0 = q_rows0(p, bs), k0 = k_rows0(p, bs);
 
   // Tile conditions are uniform over the workgroup (transpose_tile syncs).
   if (tile < tiles)
-    transpose_tile<TQ, RP>(static_cast<const TQ*>(p.q) + rows * RP, t0, p.T,
+    transpose_tile<TQ, RP>(static_cast<const TQ*>(p.q) + q0, p.q_st, t0, p.T,
                            static_cast<TQ*>(p.qt) + (bs * tiles + tile) * RP * kQTile, lds);
   if (tile < ktiles)
-    transpose_tile<TQ, RP>(static_cast<const TQ*>(p.k) + krows * RP, t0, p.Tk,
+    transpose_tile<TQ, RP>(static_cast<const TQ*>(p.k) + k0, p.k_st, t0, p.Tk,
                            static_cast<TQ*>(p.kt) + (bs * ktiles + tile) * RP * kQTile, lds);
   if (tile < tiles)
-    transpose_tile<TV, D>(static_cast<const TV*>(p.dout) + rows * D, t0, p.T,
+    transpose_tile<TV, D>(static_cast<const TV*>(p.dout) + rows * D, D, t0, p.T,
                           static_cast<TV*>(p.doutt) + (bs * tiles + tile) * D * kQTile, lds);
+  if (p.vt != nullptr && s == 0 && tile < ktiles)
+    vt_tile_to_rows<TV, D>(static_cast<const uint16_t*>(p.vt) + b * p.vt_sb + static_cast<int64_t>(tile) * D * kQTile,
+                           p.vt_dtype, static_cast<TV*>(p.vrows) + (static_cast<int64_t>(b) * p.Tkp + t0) * D, lds);
 
-  // rowsum(dO . O): wave w takes rows w, w+4, ...  O in fp32 (out_f32) keeps
+  // rowsum(dO . O): wave w takes rows w, w+4, ...  O in fp32 (out_dtype) keeps
   // this sum free of O's 16-bit rounding, which would otherwise reach every
   // dS = P (dP - rowsum) of the row (and the scale gradient's sum over them).
   const TV* dob = static_cast<const TV*>(p.dout) + rows * D;
@@ -129,7 +211,7 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
     for (int d = lane * 8; d < D; d += 512) {
       const typename Elem<TV>::v8 x = load8(dob + static_cast<int64_t>(t) * D + d);
       float y[8];
-      if (p.out_f32) {
+      if (p.out_dtype == kF32) {
         const float* of = static_cast<const float*>(p.out) + (rows + t) * D + d;
         const f32x4 y0 = *reinterpret_cast<const f32x4*>(of);
         const f32x4 y1 = *reinterpret_cast<const f32x4*>(of + 4);
@@ -139,9 +221,13 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
           y[4 + j] = y1[j];
         }
       } else {
-        const typename Elem<TV>::v8 yh = load8(static_cast<const TV*>(p.out) + (rows + t) * D + d);
+        const u32x4 yh = load16B(static_cast<const uint16_t*>(p.out) + (rows + t) * D + d);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = static_cast<float>(yh[j]);
+        for (int j = 0; j < 8; ++j) {
+          const uint16_t e = static_cast<uint16_t>(yh[j / 2] >> (16 * (j % 2)));
+          y[j] = p.out_dtype == kBF16 ? __uint_as_float(static_cast<uint32_t>(e) << 16)
+                                      : static_cast<float>(__builtin_bit_cast(_Float16, e));
+        }
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc += static_cast<float>(x[j]) * y[j];
@@ -153,8 +239,14 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
   // Zero the accumulated gradients of this tile's query and key rows.
   const f32x4 z = zero4();
   const int q_rows = max(0, min(kQTile, p.T - t0)), k_rows = max(0, min(kQTile, p.Tk - t0));
-  for (int i = tid; i < q_rows * RP / 4; i += 256) reinterpret_cast<f32x4*>(p.dq + (rows + t0) * RP)[i] = z;
-  for (int i = tid; i < k_rows * RP / 4; i += 256) reinterpret_cast<f32x4*>(p.dk + (krows + t0) * RP)[i] = z;
+  for (int i = tid; i < q_rows * RP / 4; i += 256) {
+    const int r = i / (RP / 4), c4 = i - r * (RP / 4);
+    reinterpret_cast<f32x4*>(p.dq + q0 + (t0 + r) * p.q_st)[c4] = z;
+  }
+  for (int i = tid; i < k_rows * RP / 4; i += 256) {
+    const int r = i / (RP / 4), c4 = i - r * (RP / 4);
+    reinterpret_cast<f32x4*>(p.dk + k0 + (t0 + r) * p.k_st)[c4] = z;
+  }
   if (s == 0)
     for (int i = tid; i < k_rows * D / 4; i += 256)
       reinterpret_cast<f32x4*>(p.dv + (static_cast<int64_t>(b) * p.Tk + t0) * D)[i] = z;
@@ -171,22 +263,22 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
   const int wave = uniform_wave();
   const int bs = static_cast<int>(blockIdx.y);
   const int q0 = static_cast<int>(blockIdx.x) * kQTile;
-  const float sc = p.gamma[bs % p.S] * kLog2e;
-  const TQ* qb = static_cast<const TQ*>(p.q) + static_cast<int64_t>(bs) * p.T * RP;
-  const TQ* kbase = static_cast<const TQ*>(p.k) + static_cast<int64_t>(bs) * p.Tk * RP;
+  const float sc = bwd_gamma(p, bs % p.S) * kLog2e;
+  const TQ* qb = static_cast<const TQ*>(p.q) + q_rows0(p, bs);
+  const TQ* kbase = static_cast<const TQ*>(p.k) + k_rows0(p, bs);
   q8 qf[2][KS];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk)
-      qf[cb][kk] = load8(qb + static_cast<int64_t>(min(q0 + cb * 16 + c, p.T - 1)) * RP + kk * 32 + 8 * g);
+      qf[cb][kk] = load8(qb + static_cast<int64_t>(min(q0 + cb * 16 + c, p.T - 1)) * p.q_st + kk * 32 + 8 * g);
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
   const int k_end = p.causal ? min(q0 + kQTile, p.Tk) : p.Tk;
   for (int k0 = wave * kQTile; k0 < k_end; k0 += 4 * kQTile) {
     f32x4 st[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const TQ* krow = kbase + static_cast<int64_t>(min(k0 + kb * 16 + c, p.Tk - 1)) * RP + 8 * g;
+      const TQ* krow = kbase + static_cast<int64_t>(min(k0 + kb * 16 + c, p.Tk - 1)) * p.k_st + 8 * g;
       q8 kf[KS];
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) kf[kk] = load8(krow + kk * 32);
@@ -303,14 +395,15 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   const int qt_begin = (p.causal ? k0 / kQTile : 0) + chunk * p.qchunk;
   if (qt_begin >= n_qt) return;   // whole workgroup, before any barrier
   const int qt_end = min(n_qt, qt_begin + p.qchunk);
-  const float gamma = p.gamma[s];
+  const float gamma = bwd_gamma(p, s);
   const float sc = gamma * kLog2e;
   const int64_t tiles = p.Tp / kQTile;
-  const TQ* qb = static_cast<const TQ*>(p.q) + static_cast<int64_t>(bs) * p.T * RP;
-  const TQ* kbase = static_cast<const TQ*>(p.k) + static_cast<int64_t>(bs) * p.Tk * RP;
+  const int64_t qrows0 = q_rows0(p, bs), krows0 = k_rows0(p, bs);
+  const TQ* qb = static_cast<const TQ*>(p.q) + qrows0;
+  const TQ* kbase = static_cast<const TQ*>(p.k) + krows0;
   const TQ* qtb = static_cast<const TQ*>(p.qt) + bs * tiles * RP * kQTile;
   const TQ* ktb = static_cast<const TQ*>(p.kt) + bs * static_cast<int64_t>(p.Tkp / kQTile) * RP * kQTile;
-  const TV* vb = static_cast<const TV*>(p.v) + static_cast<int64_t>(b) * p.Tk * D;
+  const TV* vb = static_cast<const TV*>(p.v) + static_cast<int64_t>(b) * p.v_sb;
   const TV* dob = static_cast<const TV*>(p.dout) + static_cast<int64_t>(bs) * p.T * D;
   const TV* dotb = static_cast<const TV*>(p.doutt) + bs * tiles * D * kQTile;
 
@@ -320,7 +413,7 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   const int krow = min(kw + c, p.Tk - 1);
   q8 kf[KS];
 #pragma unroll
-  for (int kk = 0; kk < KS; ++kk) kf[kk] = load8(kbase + static_cast<int64_t>(krow) * RP + kk * 32 + 8 * g);
+  for (int kk = 0; kk < KS; ++kk) kf[kk] = load8(kbase + static_cast<int64_t>(krow) * p.k_st + kk * 32 + 8 * g);
   v8 vf[DC];
 #pragma unroll
   for (int j = 0; j < DC; ++j) vf[j] = load8(vb + static_cast<int64_t>(krow) * D + j * 32 + 8 * g);
@@ -352,7 +445,7 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
     for (int L = wave; L < QRows::LOADS; L += 4) {
       int r, ck;
       QRows::slot_chunk(L * 64 + lane, r, ck);
-      dma16(qb + static_cast<int64_t>(min(q0 + r, p.T - 1)) * RP + ck * 8, lds + OFF_Q + L * 1024);
+      dma16(qb + static_cast<int64_t>(min(q0 + r, p.T - 1)) * p.q_st + ck * 8, lds + OFF_Q + L * 1024);
     }
     for (int L = wave; L < QCols::LOADS; L += 4) {
       int r, ck;
@@ -491,7 +584,7 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int q = q0 + cb * 16 + 4 * g + i;
-          if (q < p.T) unsafeAtomicAdd(p.dq + (static_cast<int64_t>(bs) * p.T + q) * RP + r, acc[i] * gamma);
+          if (q < p.T) unsafeAtomicAdd(p.dq + qrows0 + q * p.q_st + r, acc[i] * gamma);
         }
       }
     }
@@ -505,13 +598,13 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
     if (kr >= p.Tk) continue;
 #pragma unroll
     for (int j = 0; j < NK; ++j)
-      unsafeAtomicAdd(p.dk + (static_cast<int64_t>(bs) * p.Tk + kr) * RP + r_base + j * 16 + c, dk_acc[j][i] * gamma);
+      unsafeAtomicAdd(p.dk + krows0 + kr * p.k_st + r_base + j * 16 + c, dk_acc[j][i] * gamma);
 #pragma unroll
     for (int j = 0; j < NV; ++j)
       unsafeAtomicAdd(p.dv + (static_cast<int64_t>(b) * p.Tk + kr) * D + d_base + j * 16 + c, dv_acc[j][i]);
   }
   dgamma = wave_sum(dgamma);
-  if (lane == 0 && half == 0) unsafeAtomicAdd(p.dgamma + s, dgamma);
+  if (lane == 0 && half == 0) unsafeAtomicAdd(p.dgamma + s, dgamma * bwd_dscale_factor(p, s));
 }
 
 namespace {
@@ -573,27 +666,32 @@ static void launch_bwd_t(const BwdParams& p, int B, hipStream_t stream) {
   }
 }
 
-AttentionBwdLayout attention_bwd_layout(int64_t BS, int64_t T, int64_t Tk, int64_t RP, int64_t D) {
+AttentionBwdLayout attention_bwd_layout(int64_t B, int64_t S, int64_t T, int64_t Tk, int64_t RP, int64_t D) {
   auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
-  const int64_t Tp = round_up(T, kKeyPad), Tkp = round_up(Tk, kKeyPad);
+  const int64_t BS = B * S, Tp = round_up(T, kKeyPad), Tkp = round_up(Tk, kKeyPad);
   AttentionBwdLayout l;
   l.qt = 0;
   l.kt = l.qt + up(BS * Tp * RP * 2);
   l.doutt = l.kt + up(BS * Tkp * RP * 2);
   l.lse2 = l.doutt + up(BS * Tp * D * 2);
   l.dvec = l.lse2 + up(BS * T * 4);
-  l.bytes = l.dvec + up(BS * T * 4);
+  l.vrows = l.dvec + up(BS * T * 4);
+  l.bytes = l.vrows + up(B * Tkp * D * 2);
   return l;
 }
 
 void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace, hipStream_t stream) {
-  const AttentionBwdLayout l = attention_bwd_layout(static_cast<int64_t>(a.B) * a.S, a.T, a.Tk, a.RP, a.D);
+  const AttentionBwdLayout l = attention_bwd_layout(a.B, a.S, a.T, a.Tk, a.RP, a.D);
   char* ws = static_cast<char*>(workspace);
-  BwdParams p{a.q, a.k, a.v, a.out, a.dout, ws + l.qt, ws + l.kt, ws + l.doutt,
-              reinterpret_cast<float*>(ws + l.lse2), reinterpret_cast<float*>(ws + l.dvec), a.gamma,
+  const int64_t Tkp = round_up(a.Tk, kKeyPad);
+  BwdParams p{a.q, a.k, a.vt ? static_cast<const void*>(ws + l.vrows) : a.v, a.out, a.dout, ws + l.qt, ws + l.kt, ws + l.doutt,
+              reinterpret_cast<float*>(ws + l.lse2), reinterpret_cast<float*>(ws + l.dvec), a.scales,
               a.dq, a.dk, a.dv, a.dgamma,
+              a.q_stride_b, a.q_stride_t, a.q_map_stride, a.k_stride_b, a.k_stride_t, a.k_map_stride,
+              a.map_repeat, a.vt ? Tkp * a.D : static_cast<int64_t>(a.Tk) * a.D, a.vt, a.vt_stride_b, a.vt_dtype,
+              ws + l.vrows, a.scales_dtype, a.scales_log ? 1 : 0, a.log_lo, a.log_hi, a.scale_mult,
               a.S, a.T, static_cast<int>(round_up(a.T, kKeyPad)), a.RP, a.D,
-              a.Tk, static_cast<int>(round_up(a.Tk, kKeyPad)), a.causal ? 1 : 0, a.out_f32 ? 1 : 0, 1, 1};
+              a.Tk, static_cast<int>(Tkp), a.causal ? 1 : 0, a.out_dtype, 1, 1};
   if (a.qk_dtype == kF16) {
     if (a.v_dtype == kBF16) launch_bwd_t<_Float16, __bf16>(p, a.B, stream);
     else launch_bwd_t<_Float16, _Float16>(p, a.B, stream);

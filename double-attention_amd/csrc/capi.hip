@@ -120,7 +120,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 17; }
+int da_abi_version(void) { return 18; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -147,8 +147,8 @@ int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_
 
 int da_dictionary_normalize_backward(const void* raw_key, const void* raw_value, int raw_dtype,
                                      int64_t routing_dim, int64_t atoms, float eps, const float* grad_key,
-                                     const float* grad_value, void* d_raw_key, void* d_raw_value,
-                                     da_stream_t stream) {
+                                     const float* grad_value, int64_t grad_ld_r, int64_t grad_ld_j,
+                                     void* d_raw_key, void* d_raw_value, da_stream_t stream) {
   if (!any_dtype(raw_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: bad dtype");
   if (routing_dim < 1 || routing_dim > (1 << 16))
     return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: routing_dim %lld out of range", (long long)routing_dim);
@@ -157,8 +157,15 @@ int da_dictionary_normalize_backward(const void* raw_key, const void* raw_value,
   if (!raw_key || !grad_key || !d_raw_key) return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: null pointer");
   if (!raw_value && d_raw_value)
     return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: d_raw_value given for a tied bank");
+  // Each atom's coordinates must be distinct elements: one stride 1 and the
+  // other covering the first's range.
+  const bool coord_major = grad_ld_j == 1 && grad_ld_r >= atoms;
+  const bool atom_major = grad_ld_r == 1 && grad_ld_j >= routing_dim;
+  if (!coord_major && !atom_major)
+    return fail(DA_ERR_INVALID_ARGUMENT, "normalize backward: gradient strides (%lld, %lld) must be (>= atoms, 1) or "
+                "(1, >= routing_dim)", (long long)grad_ld_r, (long long)grad_ld_j);
   const da::NormBwdArgs a{raw_key, raw_value, raw_dtype, static_cast<int>(routing_dim), atoms, eps,
-                          grad_key, grad_value, d_raw_key, d_raw_value};
+                          grad_key, grad_value, grad_ld_r, grad_ld_j, d_raw_key, d_raw_value};
   da::launch_dictionary_normalize_backward(a, reinterpret_cast<hipStream_t>(stream));
   return check_launch("normalize backward");
 }
@@ -334,7 +341,106 @@ int da_routed_attention(const void* query, const void* key, int64_t stride_b, in
 int64_t da_attention_backward_workspace_bytes(int64_t batch, int64_t maps, int64_t length, int64_t key_length,
                                               int64_t score_dim, int64_t value_dim) {
   if (batch < 1 || maps < 1 || length < 1 || key_length < 1 || score_dim < 1 || value_dim < 1) return 0;
-  return da::attention_bwd_layout(batch * maps, length, key_length, score_dim, value_dim).bytes;
+  return da::attention_bwd_layout(batch, maps, length, key_length, score_dim, value_dim).bytes;
+}
+
+int da_routed_attention_backward_ex(const da_attention_backward_args* args, da_stream_t stream) {
+  if (!args) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: null args");
+  const da_attention_backward_args& x = *args;
+  const int qk_dtype = x.qk_dtype, v_dtype = x.v_dtype, flags = x.flags;
+  const bool types_ok = (qk_dtype == DA_F16 && (v_dtype == DA_BF16 || v_dtype == DA_F16)) ||
+                        (qk_dtype == DA_BF16 && v_dtype == DA_BF16);
+  if (!types_ok)
+    return fail(DA_ERR_UNSUPPORTED,
+                "attention backward: (qk_dtype, v_dtype) must be (F16,BF16), (F16,F16) or (BF16,BF16)");
+  if (flags & ~(DA_ATTN_CAUSAL | DA_ATTN_SCALES_ARE_LOG))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: unknown flag bits 0x%x", flags);
+  if (!any_dtype(x.out_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: bad out dtype");
+  if (!x.value && !(half_dtype(x.value_t_dtype) && x.value_t_stride_b >= 0 && x.value_t_stride_b % 8 == 0))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: V^T tiles need a 16-bit dtype and a stride_b multiple of 8");
+  if (!pow2_width(x.score_dim))
+    return fail(DA_ERR_UNSUPPORTED, "attention backward: score_dim %lld not in {64,128,256,512}", (long long)x.score_dim);
+  if (!pow2_width(x.value_dim))
+    return fail(DA_ERR_UNSUPPORTED, "attention backward: value_dim %lld not in {64,128,256,512}", (long long)x.value_dim);
+  const int64_t batch = x.batch, maps = x.maps, length = x.length, key_length = x.key_length;
+  if (batch < 0 || length < 0 || key_length < 0 || maps < 1 || maps > 64 || batch * maps > 65535 ||
+      length > (1LL << 24) || key_length > (1LL << 24))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: bad batch/maps/length/key_length");
+  if (x.map_repeat < 1 || maps % x.map_repeat)
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: maps must be a multiple of map_repeat >= 1");
+  if ((flags & DA_ATTN_CAUSAL) && key_length != length)
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: a causal mask needs key_length == length");
+  if (!any_dtype(x.scales_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: bad scales dtype");
+  if (!(x.scale_mult > 0.f) || std::isinf(x.scale_mult))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: scale_mult must be finite and > 0");
+  if ((flags & DA_ATTN_SCALES_ARE_LOG) &&
+      !(x.log_min <= x.log_max && std::isfinite(x.log_min) && std::isfinite(x.log_max)))
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: log_min <= log_max must be finite");
+  const int64_t qs[] = {x.query_stride_b, x.query_stride_t, x.query_map_stride,
+                        x.key_stride_b, x.key_stride_t, x.key_map_stride};
+  for (int64_t st : qs)
+    if (st < 0 || st % 8) return fail(DA_ERR_ALIGNMENT, "attention backward: strides must be multiples of 8");
+  if (x.query_stride_t < x.score_dim || x.key_stride_t < x.score_dim)
+    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: stride_t must be >= score_dim");
+  if (batch == 0 || length == 0) return ok();
+  if (key_length == 0) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: queries need at least one key");
+  const void* values = x.value ? x.value : x.value_t;
+  const void* ptrs[] = {x.query, x.key, values, x.out, x.grad_out, x.scales, x.workspace, x.grad_query,
+                        x.grad_key, x.grad_value, x.grad_scales};
+  for (const void* ptr : ptrs)
+    if (!ptr) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: null pointer");
+  const void* halves[] = {x.query, x.key, values, x.out, x.grad_out};
+  for (const void* ptr : halves)
+    if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: half-precision tensors must be 16-byte aligned");
+  const void* f32[] = {x.grad_query, x.grad_key, x.grad_value};
+  for (const void* ptr : f32)
+    if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: gradients must be 16-byte aligned");
+  if (!aligned(x.scales, x.scales_dtype == DA_F32 ? 4 : 2) || !aligned(x.grad_scales, 4))
+    return fail(DA_ERR_ALIGNMENT, "attention backward: scales must be aligned to their element size");
+  if (!aligned(x.workspace, 256)) return fail(DA_ERR_ALIGNMENT, "attention backward: workspace must be 256-byte aligned");
+  const int64_t need =
+      da_attention_backward_workspace_bytes(batch, maps, length, key_length, x.score_dim, x.value_dim);
+  if (x.workspace_bytes < need)
+    return fail(DA_ERR_WORKSPACE, "attention backward: workspace of %lld bytes < %lld required",
+                (long long)x.workspace_bytes, (long long)need);
+  da::AttentionBwdArgs a;
+  a.q = x.query;
+  a.k = x.key;
+  a.q_stride_b = x.query_stride_b;
+  a.q_stride_t = x.query_stride_t;
+  a.q_map_stride = x.query_map_stride;
+  a.k_stride_b = x.key_stride_b;
+  a.k_stride_t = x.key_stride_t;
+  a.k_map_stride = x.key_map_stride;
+  a.map_repeat = static_cast<int>(x.map_repeat);
+  a.v = x.value;
+  a.vt = x.value ? nullptr : x.value_t;
+  a.vt_stride_b = x.value_t_stride_b;
+  a.vt_dtype = x.value_t_dtype;
+  a.out = x.out;
+  a.out_dtype = x.out_dtype;
+  a.dout = x.grad_out;
+  a.scales = x.scales;
+  a.scales_dtype = x.scales_dtype;
+  a.scales_log = (flags & DA_ATTN_SCALES_ARE_LOG) != 0;
+  a.log_lo = x.log_min;
+  a.log_hi = x.log_max;
+  a.scale_mult = x.scale_mult;
+  a.dq = x.grad_query;
+  a.dk = x.grad_key;
+  a.dv = x.grad_value;
+  a.dgamma = x.grad_scales;
+  a.B = static_cast<int>(batch);
+  a.S = static_cast<int>(maps);
+  a.T = static_cast<int>(length);
+  a.Tk = static_cast<int>(key_length);
+  a.RP = static_cast<int>(x.score_dim);
+  a.D = static_cast<int>(x.value_dim);
+  a.causal = (flags & DA_ATTN_CAUSAL) != 0;
+  a.qk_dtype = qk_dtype;
+  a.v_dtype = v_dtype;
+  da::launch_routed_attention_backward(a, x.workspace, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("attention backward");
 }
 
 int da_routed_attention_backward(const void* query, const void* key, const void* value, const void* out,
@@ -343,64 +449,42 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
                                  int flags, int qk_dtype, int v_dtype, void* workspace, int64_t workspace_bytes,
                                  float* grad_query, float* grad_key, float* grad_value, float* grad_scales,
                                  da_stream_t stream) {
-  const bool types_ok = (qk_dtype == DA_F16 && (v_dtype == DA_BF16 || v_dtype == DA_F16)) ||
-                        (qk_dtype == DA_BF16 && v_dtype == DA_BF16);
-  if (!types_ok)
-    return fail(DA_ERR_UNSUPPORTED,
-                "attention backward: (qk_dtype, v_dtype) must be (F16,BF16), (F16,F16) or (BF16,BF16)");
+  // Contiguous [batch*maps, length, score_dim] rows, value rows and fp32 scales.
   if (flags & ~(DA_ATTN_CAUSAL | DA_ATTN_OUT_F32))
     return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: unknown flag bits 0x%x", flags);
-  if (!pow2_width(score_dim))
-    return fail(DA_ERR_UNSUPPORTED, "attention backward: score_dim %lld not in {64,128,256,512}", (long long)score_dim);
-  if (!pow2_width(value_dim))
-    return fail(DA_ERR_UNSUPPORTED, "attention backward: value_dim %lld not in {64,128,256,512}", (long long)value_dim);
-  if (batch < 0 || length < 0 || key_length < 0 || maps < 1 || maps > 64 || batch * maps > 65535 ||
-      length > (1LL << 24) || key_length > (1LL << 24))
-    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: bad batch/maps/length/key_length");
-  if ((flags & DA_ATTN_CAUSAL) && key_length != length)
-    return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: a causal mask needs key_length == length");
-  if (batch == 0 || length == 0) return ok();
-  if (key_length == 0) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: queries need at least one key");
-  const void* ptrs[] = {query, key, value, out, grad_out, scales, workspace, grad_query, grad_key, grad_value,
-                        grad_scales};
-  for (const void* ptr : ptrs)
-    if (!ptr) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: null pointer");
-  const void* halves[] = {query, key, value, out, grad_out};
-  for (const void* ptr : halves)
-    if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: half-precision tensors must be 16-byte aligned");
-  const void* f32[] = {grad_query, grad_key, grad_value};
-  for (const void* ptr : f32)
-    if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: gradients must be 16-byte aligned");
-  if (!aligned(scales, 4) || !aligned(grad_scales, 4))
-    return fail(DA_ERR_ALIGNMENT, "attention backward: scales must be 4-byte aligned");
-  if (!aligned(workspace, 256)) return fail(DA_ERR_ALIGNMENT, "attention backward: workspace must be 256-byte aligned");
-  const int64_t need = da_attention_backward_workspace_bytes(batch, maps, length, key_length, score_dim, value_dim);
-  if (workspace_bytes < need)
-    return fail(DA_ERR_WORKSPACE, "attention backward: workspace of %lld bytes < %lld required",
-                (long long)workspace_bytes, (long long)need);
-  da::AttentionBwdArgs a;
-  a.q = query;
-  a.k = key;
-  a.v = value;
-  a.out = out;
-  a.dout = grad_out;
-  a.gamma = scales;
-  a.dq = grad_query;
-  a.dk = grad_key;
-  a.dv = grad_value;
-  a.dgamma = grad_scales;
-  a.B = static_cast<int>(batch);
-  a.S = static_cast<int>(maps);
-  a.T = static_cast<int>(length);
-  a.Tk = static_cast<int>(key_length);
-  a.RP = static_cast<int>(score_dim);
-  a.D = static_cast<int>(value_dim);
-  a.causal = (flags & DA_ATTN_CAUSAL) != 0;
-  a.out_f32 = (flags & DA_ATTN_OUT_F32) != 0;
-  a.qk_dtype = qk_dtype;
-  a.v_dtype = v_dtype;
-  da::launch_routed_attention_backward(a, workspace, reinterpret_cast<hipStream_t>(stream));
-  return check_launch("attention backward");
+  da_attention_backward_args x{};
+  x.query = query;
+  x.query_stride_t = score_dim;
+  x.query_map_stride = length * score_dim;
+  x.query_stride_b = maps * length * score_dim;
+  x.key = key;
+  x.key_stride_t = score_dim;
+  x.key_map_stride = key_length * score_dim;
+  x.key_stride_b = maps * key_length * score_dim;
+  x.map_repeat = 1;
+  x.value = value;
+  x.out = out;
+  x.out_dtype = (flags & DA_ATTN_OUT_F32) ? DA_F32 : v_dtype;
+  x.grad_out = grad_out;
+  x.scales = scales;
+  x.scales_dtype = DA_F32;
+  x.scale_mult = 1.f;
+  x.batch = batch;
+  x.maps = maps;
+  x.length = length;
+  x.key_length = key_length;
+  x.score_dim = score_dim;
+  x.value_dim = value_dim;
+  x.flags = flags & DA_ATTN_CAUSAL;
+  x.qk_dtype = qk_dtype;
+  x.v_dtype = v_dtype;
+  x.workspace = workspace;
+  x.workspace_bytes = workspace_bytes;
+  x.grad_query = grad_query;
+  x.grad_key = grad_key;
+  x.grad_value = grad_value;
+  x.grad_scales = grad_scales;
+  return da_routed_attention_backward_ex(&x, stream);
 }
 
 static int validate_gemm_common(const char* what, const void* x, int64_t rows, int64_t K, int dtype) {

@@ -84,27 +84,40 @@ struct AttentionArgs {
 
 // Backward of the outer attention, per score map (see attention_bwd.hip).
 struct AttentionBwdArgs {
-  const void* q;         // [B*S][T][RP] routed queries, qk_dtype
-  const void* k;         // [B*S][Tk][RP] routed keys
-  const void* v;         // [B][Tk][D] values, v_dtype
-  const void* out;       // [B*S][T][D] forward output, v_dtype (fp32 with out_f32)
+  // Query row t of (sequence b, map s) at q + b*q_stride_b +
+  // (s / map_repeat)*q_map_stride + t*q_stride_t (elements, qk_dtype), key
+  // rows alike; dq and dk (fp32) use the same strides.
+  const void* q;
+  const void* k;
+  int64_t q_stride_b, q_stride_t, q_map_stride;
+  int64_t k_stride_b, k_stride_t, k_map_stride;
+  int map_repeat;
+  const void* v;         // [B][Tk][D] values, v_dtype; or, with vt set, the V^T tiles
+  const void* vt;        // [B] x vt_stride_b: [Tkp/32][D][32], 16-bit of vt_dtype
+  int64_t vt_stride_b;
+  int vt_dtype;
+  const void* out;       // [B*S][T][D] forward output, out_dtype
   const void* dout;      // [B*S][T][D] output gradient, v_dtype
-  const float* gamma;    // [S] score scales
-  float* dq;             // [B*S][T][RP]
-  float* dk;             // [B*S][Tk][RP]
+  const void* scales;    // [S] score scales, scales_dtype
+  int scales_dtype;
+  bool scales_log;       // scales hold logs: gamma = exp(clamp(., log_lo, log_hi))
+  float log_lo, log_hi;
+  float scale_mult;      // every gamma times this
+  float* dq;
+  float* dk;
   float* dv;             // [B][Tk][D]
-  float* dgamma;         // [S]
+  float* dgamma;         // [S] gradient at scales[s] (at the log with scales_log)
   int B, S, T, RP, D;
   int Tk;                // keys per sequence (== T when causal)
   bool causal;
-  bool out_f32;          // out holds fp32 values
+  int out_dtype;         // kF32, kF16 or kBF16
   int qk_dtype, v_dtype;
 };
 // Byte offsets of the backward's workspace pieces (256-byte aligned).
 struct AttentionBwdLayout {
-  int64_t qt, kt, doutt, lse2, dvec, bytes;
+  int64_t qt, kt, doutt, lse2, dvec, vrows, bytes;
 };
-AttentionBwdLayout attention_bwd_layout(int64_t BS, int64_t T, int64_t Tk, int64_t RP, int64_t D);
+AttentionBwdLayout attention_bwd_layout(int64_t B, int64_t S, int64_t T, int64_t Tk, int64_t RP, int64_t D);
 void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace, hipStream_t stream);
 
 struct GemmSegment {
@@ -143,6 +156,7 @@ struct NormBwdArgs {
   const void* raw_key; const void* raw_value; int dtype;
   int R; int64_t M; float eps;
   const float* grad_key; const float* grad_value;
+  int64_t g_ld_r, g_ld_j;   // gradient element (r, j) at r * g_ld_r + j * g_ld_j
   void* d_key; void* d_value;
 };
 void launch_dictionary_normalize_backward(const NormBwdArgs& a, hipStream_t stream);

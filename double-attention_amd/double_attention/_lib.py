@@ -47,7 +47,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 17
+ABI_VERSION = 18
 NOALLOC_SCRATCH_BYTES = 128 << 20
 
 _vp = ctypes.c_void_p
@@ -95,6 +95,49 @@ class SdaForwardArgs(ctypes.Structure):
     ]
 
 
+class AttentionBackwardArgs(ctypes.Structure):
+    """Mirror of ``da_attention_backward_args``."""
+
+    _fields_ = [
+        ("query", _vp),
+        ("query_stride_b", _i64),
+        ("query_stride_t", _i64),
+        ("query_map_stride", _i64),
+        ("key", _vp),
+        ("key_stride_b", _i64),
+        ("key_stride_t", _i64),
+        ("key_map_stride", _i64),
+        ("map_repeat", _i64),
+        ("value", _vp),
+        ("value_t", _vp),
+        ("value_t_stride_b", _i64),
+        ("value_t_dtype", _i32),
+        ("out", _vp),
+        ("out_dtype", _i32),
+        ("grad_out", _vp),
+        ("scales", _vp),
+        ("scales_dtype", _i32),
+        ("scale_mult", _f32),
+        ("log_min", _f32),
+        ("log_max", _f32),
+        ("batch", _i64),
+        ("maps", _i64),
+        ("length", _i64),
+        ("key_length", _i64),
+        ("score_dim", _i64),
+        ("value_dim", _i64),
+        ("flags", _i32),
+        ("qk_dtype", _i32),
+        ("v_dtype", _i32),
+        ("workspace", _vp),
+        ("workspace_bytes", _i64),
+        ("grad_query", _vp),
+        ("grad_key", _vp),
+        ("grad_value", _vp),
+        ("grad_scales", _vp),
+    ]
+
+
 # name -> (restype, argtypes); every function declared in the public header.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_abi_version": (_i32, []),
@@ -102,7 +145,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_padded_atoms": (_i64, [_i64]),
     "da_padded_length": (_i64, [_i64]),
     "da_dictionary_normalize": (_i32, [_vp, _vp, _i32, _i64, _i64, _f32, _vp, _i32, _vp, _vp, _vp]),
-    "da_dictionary_normalize_backward": (_i32, [_vp, _vp, _i32, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp]),
+    "da_dictionary_normalize_backward": (
+        _i32, [_vp, _vp, _i32, _i64, _i64, _f32, _vp, _vp, _i64, _i64, _vp, _vp, _vp]
+    ),
     "da_row_normalize": (_i32, [_vp, _i32, _i64, _i64, _i64, _f32, _vp, _i32, _i64, _vp]),
     "da_row_normalize_backward": (_i32, [_vp, _i32, _i64, _i64, _i64, _f32, _vp, _i32, _i64, _vp, _i32, _i64, _vp]),
     "da_dictionary_route": (
@@ -150,6 +195,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _i64,
          _vp, _vp, _vp, _vp, _vp],
     ),
+    "da_routed_attention_backward_ex": (_i32, [ctypes.POINTER(AttentionBackwardArgs), _vp]),
     "da_sda_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),
     "da_sda_workspace_offset": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "da_shared_dictionary_attention_forward": (_i32, [ctypes.POINTER(SdaForwardArgs), _vp]),

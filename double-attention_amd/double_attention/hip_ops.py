@@ -28,6 +28,7 @@ same device under autograd.
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 from typing import NamedTuple
@@ -46,6 +47,11 @@ VALUE_WIDTH_STEP = 64
 MAX_VALUE_WIDTH = 4096
 ATOM_PAD = 64
 TOKEN_PAD = 64
+# Clamp windows of the learned logs: beta = exp(clamp(log_beta, ln 0.05,
+# ln 64)) (reference modules.py:130-132) and the outer-map temperatures
+# exp(clamp(log_scale, ln 1/4, ln 1024)) (ops.py:160-161).
+LOG_BETA_RANGE = (math.log(0.05), math.log(64.0))
+LOG_SCALE_RANGE = (math.log(0.25), math.log(1024.0))
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -211,18 +217,25 @@ def dictionary_normalize_backward_hip(
             return None
         if g.shape != raw_key.shape:
             raise ValueError("bank gradients must be [routing_dim, atoms]")
-        return g.detach().to(torch.float32).contiguous()
+        g = g.detach().to(torch.float32)
+        # [R, M] rows, or the transposed view of atom-major [M, R] rows (the
+        # route backward's), are read in place.
+        if g.stride() not in ((atoms, 1), (1, routing_dim)) or g.data_ptr() % 4:
+            g = g.contiguous()
+        return g
 
     key_c = raw_key.detach().contiguous()
     value_c = None if raw_value is None else raw_value.detach().to(key_c.dtype).contiguous()
     gk, gv = as_grad(grad_key), as_grad(grad_value)
+    if gv is not None and gv.stride() != gk.stride():
+        gk, gv = gk.contiguous(), gv.contiguous()
     d_key = torch.empty_like(key_c)
     d_value = None if value_c is None else torch.empty_like(value_c)
     lib = _lib.get()
     _lib.check(
         lib.da_dictionary_normalize_backward(
             key_c.data_ptr(), _ptr(value_c), dtype_code(key_c.dtype), routing_dim, atoms, float(eps),
-            gk.data_ptr(), _ptr(gv), d_key.data_ptr(), _ptr(d_value), _stream(device),
+            gk.data_ptr(), _ptr(gv), gk.stride(0), gk.stride(1), d_key.data_ptr(), _ptr(d_value), _stream(device),
         ),
         "dictionary_normalize_hip backward",
     )
@@ -305,7 +318,11 @@ def _route_forward(
     normalize_output: bool,
     variant: RouteVariant = RouteVariant(),
     out_dtype: torch.dtype | None = None,
+    beta_is_log: bool = False,
 ) -> Tensor:
+    """Route launch; ``beta_is_log``: ``beta`` is a log-beta tensor and the
+    kernel applies exp(clamp(., ln 0.05, ln 64))."""
+
     routing_dim = x.shape[-1]
     out_dtype = x.dtype if out_dtype is None else out_dtype
     if routing_dim != layout.key_t.shape[1]:
@@ -324,6 +341,10 @@ def _route_forward(
         | (_lib.DA_ROUTE_UNIT_KEYS if layout.unit else 0)
         | variant.flags()
     )
+    if beta_is_log:
+        if not isinstance(beta, Tensor):
+            raise ValueError("a log beta must be a tensor")
+        flags |= _lib.DA_ROUTE_BETA_IS_LOG
     if isinstance(beta, Tensor):
         if beta.numel() != 1:
             raise ValueError("beta must be a scalar")
@@ -425,6 +446,73 @@ def _normalize_backward(v: Tensor, h: Tensor, eps: float, dtype: torch.dtype) ->
     return out
 
 
+def _attention_backward_ex(
+    query: tuple[int, int, int, int],
+    key: tuple[int, int, int, int],
+    map_repeat: int,
+    value: Tensor | tuple[Tensor, int, torch.dtype],
+    out: Tensor,
+    grad_out: Tensor,
+    scales: Tensor,
+    scale_mult: float,
+    log_range: tuple[float, float] | None,
+    shape: tuple[int, int, int, int, int, int],
+    causal: bool,
+    qk_dtype: torch.dtype,
+    grad_query: int,
+    grad_key: int,
+    grad_value: Tensor,
+    grad_scales: Tensor,
+    what: str,
+) -> None:
+    """One ``da_routed_attention_backward_ex`` call.
+
+    ``query`` / ``key`` are (data pointer, stride_b, stride_t, map_stride) in
+    elements; ``grad_query`` / ``grad_key`` point at fp32 buffers with the
+    same strides.  ``value`` is the value rows, or (V^T tiles, their
+    per-sequence stride, the dtype the kernels take them in).  ``shape`` is
+    (batch, maps, length, key_length, score_dim, value_dim).  ``log_range``
+    set: ``scales`` holds logs clamped to it, and ``grad_scales`` receives the
+    gradient at the logs.
+    """
+
+    batch, maps, length, key_length, score_dim, value_dim = shape
+    lib = _lib.get()
+    ws_bytes = lib.da_attention_backward_workspace_bytes(batch, maps, length, key_length, score_dim, value_dim)
+    device = out.device
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    args = _lib.AttentionBackwardArgs()
+    args.query, args.query_stride_b, args.query_stride_t, args.query_map_stride = query
+    args.key, args.key_stride_b, args.key_stride_t, args.key_map_stride = key
+    args.map_repeat = map_repeat
+    if isinstance(value, Tensor):
+        args.value = value.data_ptr()
+        v_dtype = value.dtype
+    else:
+        tiles, args.value_t_stride_b, v_dtype = value
+        args.value_t = tiles.data_ptr()
+        args.value_t_dtype = _half_code(tiles.dtype)
+    args.out = out.data_ptr()
+    args.out_dtype = dtype_code(out.dtype)
+    args.grad_out = grad_out.data_ptr()
+    args.scales = scales.data_ptr()
+    args.scales_dtype = dtype_code(scales.dtype)
+    args.scale_mult = scale_mult
+    args.log_min, args.log_max = log_range if log_range is not None else (0.0, 0.0)
+    args.batch, args.maps, args.length, args.key_length = batch, maps, length, key_length
+    args.score_dim, args.value_dim = score_dim, value_dim
+    args.flags = (_lib.DA_ATTN_CAUSAL if causal else 0) | (_lib.DA_ATTN_SCALES_ARE_LOG if log_range is not None else 0)
+    args.qk_dtype = _half_code(qk_dtype)
+    args.v_dtype = _half_code(v_dtype)
+    args.workspace = workspace.data_ptr()
+    args.workspace_bytes = ws_bytes
+    args.grad_query = grad_query
+    args.grad_key = grad_key
+    args.grad_value = grad_value.data_ptr()
+    args.grad_scales = grad_scales.data_ptr()
+    _lib.check(lib.da_routed_attention_backward_ex(ctypes.byref(args), _stream(device)), what)
+
+
 def _route_backward(
     x: Tensor,
     dictionary_key: Tensor,
@@ -436,6 +524,7 @@ def _route_backward(
     grad: Tensor,
     r: Tensor | None = None,
     bank_grad_dtype: torch.dtype | None = None,
+    beta_is_log: bool = False,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients of the softmax route (``ops.py:16-62``) on the attention backward kernels.
 
@@ -443,11 +532,12 @@ def _route_backward(
     the key atoms the keys, the value atoms the values, beta the score scale
     and r = softmax(beta u Dk) Dv^T the output, then z = r / max(|r|, eps).
     The host forms u, r (the forward's, or one route launch without the
-    output norm) and the output-norm backward dr; ``da_routed_attention_backward``
+    output norm) and the output-norm backward dr; ``da_routed_attention_backward_ex``
     with the atoms as a key sequence of their own returns du, dDk, dDv and
     dbeta; the input-norm backward gives dx.  Returns fp32-accumulated
     gradients in the dtypes of ``x`` and the dictionary tensors (or
-    ``bank_grad_dtype`` for the two bank gradients).
+    ``bank_grad_dtype`` for the two bank gradients).  ``beta_is_log``: ``beta``
+    is log-beta, clamped in the kernels, and the last gradient is at the log.
     """
 
     routing_dim = x.shape[-1]
@@ -464,10 +554,10 @@ def _route_backward(
     else:
         qk_type = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
         u16 = _aligned(rows.to(qk_type))
-    beta_t = beta.detach().float().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
+    beta_t = beta.detach().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
     if r is None:
         layout16 = route_layout(dictionary_key.detach(), dictionary_value.detach(), qk_type)
-        r = _route_forward(u16, layout16, beta_t, eps, False, False, RouteVariant())
+        r = _route_forward(u16, layout16, beta_t, eps, False, False, RouteVariant(), beta_is_log=beta_is_log)
     r = r.reshape(-1, routing_dim)
     g = grad.detach().reshape(-1, routing_dim)
     # Values, r and dr in fp16 for fp16 inputs (8x finer than bf16: with the
@@ -479,23 +569,24 @@ def _route_backward(
     else:
         go = _aligned(g.to(v_type))
     keys = _aligned(dictionary_key.detach().t().to(qk_type))
-    values = _aligned(dictionary_value.detach().t().to(v_type))
-    out = _aligned(r.to(v_type))
-    lib = _lib.get()
-    ws_bytes = lib.da_attention_backward_workspace_bytes(1, 1, n, atoms, routing_dim, routing_dim)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    # The values as the route layout's 32-atom tiles when the bank carries
+    # them (the prep kernel turns them into v_type rows), else as rows; r in
+    # its own dtype (it only enters rowsum(dr . r)).
+    layout = getattr(dictionary_key, "_da_route_layout", None)
+    if layout is not None and getattr(dictionary_value, "_da_route_layout", None) is layout and layout.atoms == atoms:
+        values: Tensor | tuple[Tensor, int, torch.dtype] = (layout.value, 0, v_type)
+    else:
+        values = _aligned(dictionary_value.detach().t().to(v_type))
+    out = _aligned(r)
     du = torch.empty(n, routing_dim, dtype=torch.float32, device=device)
     dkt = torch.empty(atoms, routing_dim, dtype=torch.float32, device=device)
     dvt = torch.empty(atoms, routing_dim, dtype=torch.float32, device=device)
     dbeta = torch.empty(1, dtype=torch.float32, device=device)
-    _lib.check(
-        lib.da_routed_attention_backward(
-            u16.data_ptr(), keys.data_ptr(), values.data_ptr(), out.data_ptr(), go.data_ptr(), beta_t.data_ptr(),
-            1, 1, n, atoms, routing_dim, routing_dim, 0, _half_code(qk_type), _half_code(v_type),
-            workspace.data_ptr(), ws_bytes, du.data_ptr(), dkt.data_ptr(), dvt.data_ptr(), dbeta.data_ptr(),
-            _stream(device),
-        ),
-        "dictionary_route_hip backward",
+    _attention_backward_ex(
+        (u16.data_ptr(), n * routing_dim, routing_dim, 0), (keys.data_ptr(), atoms * routing_dim, routing_dim, 0), 1,
+        values, out, go, beta_t, 1.0, LOG_BETA_RANGE if beta_is_log else None,
+        (1, 1, n, atoms, routing_dim, routing_dim), False, qk_type,
+        du.data_ptr(), dkt.data_ptr(), dvt, dbeta, "dictionary_route_hip backward",
     )
     dx = _normalize_backward(rows, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
     return (
@@ -544,14 +635,16 @@ SPLIT_K_MIN_CHUNK = 1024
 SPLIT_K_MAX = 8
 
 
-def _mm_tn_f32(a: Tensor, b: Tensor) -> Tensor:
+def _mm_tn_f32(a: Tensor, b: Tensor, out_dtype: torch.dtype = torch.float32) -> Tensor:
     """``a^T b`` for row-major ``a [K, M]`` and ``b [K, N]`` (16-bit, unit
-    column stride), fp32 result.
+    column stride), accumulated in fp32 and rounded once to ``out_dtype``.
 
     The weight gradients have a long K (tokens or rows) over a small output:
     one library GEMM runs a few dozen output tiles on 256 CUs.  K is cut into
     s chunks whose partial products run as one batched GEMM (fp32 partials,
-    summed): up to 2.3x faster at [16384 x 512]^T [16384 x 1536].
+    summed in fp32, then rounded; a reduction into a 16-bit output would
+    round the partials first): up to 2.3x faster at [16384 x 512]^T
+    [16384 x 1536].
     """
 
     k, m = a.shape
@@ -565,13 +658,31 @@ def _mm_tn_f32(a: Tensor, b: Tensor) -> Tensor:
     while s < SPLIT_K_MAX and k % (2 * s) == 0 and k // (2 * s) >= SPLIT_K_MIN_CHUNK and tiles * s < 512:
         s *= 2
     if s == 1:
-        return _mm_f32(a.t(), b)
+        # The library accumulates in fp32 and rounds once to its output dtype.
+        return _mm_f32(a.t(), b) if out_dtype == torch.float32 else torch.mm(a.t(), b).to(out_dtype)
     chunk = k // s
     # Left operand: the transposed chunks of a (column-major views); right
     # operand: row-major chunks of b.
     a3 = a.as_strided((s, m, chunk), (chunk * a.stride(0), 1, a.stride(0)))
     b3 = b.as_strided((s, chunk, n), (chunk * b.stride(0), b.stride(0), 1))
-    return torch.bmm(a3, b3, out_dtype=torch.float32).sum(0)
+    return torch.bmm(a3, b3, out_dtype=torch.float32).sum(0).to(out_dtype)
+
+
+_ONES: dict[tuple[torch.device, int, torch.dtype], Tensor] = {}
+
+
+def column_sums(x: Tensor, out_dtype: torch.dtype) -> Tensor:
+    """Column sums of a 16-bit ``[K, N]`` matrix (a bias gradient): one
+    library product with a ones row, fp32 accumulation, one rounding to
+    ``out_dtype``."""
+
+    key = (x.device, x.shape[0], x.dtype)
+    ones = _ONES.get(key)
+    if ones is None:
+        ones = _ONES[key] = torch.ones(1, x.shape[0], dtype=x.dtype, device=x.device)
+    if out_dtype == torch.float32:
+        return _mm_f32(ones, x).view(-1)
+    return torch.mm(ones, x).view(-1).to(out_dtype)
 
 
 def _route_backward_rows(
@@ -586,6 +697,7 @@ def _route_backward_rows(
     variant: RouteVariant,
     r: Tensor | None = None,
     bank_grad_dtype: torch.dtype | None = None,
+    beta_is_log: bool = False,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients of the route (``ops.py:16-62``) for every variant and width.
 
@@ -598,7 +710,8 @@ def _route_backward_rows(
     in their own dtype); r, the reconstruction before the output norm, is the
     forward's (``r``) or comes from one route launch.  Returns gradients in
     the dtypes of ``x`` and the dictionary tensors (or ``bank_grad_dtype`` for
-    the two bank gradients), and d beta as a 1-element fp32 tensor.
+    the two bank gradients), and d beta as a 1-element fp32 tensor (at the
+    log with ``beta_is_log``: ``beta`` is then log-beta, clamped in the kernels).
     """
 
     routing_dim = x.shape[-1]
@@ -615,10 +728,10 @@ def _route_backward_rows(
     else:
         key_type = x.dtype
         u_h = u_v = rows
-    beta_t = beta.detach().float().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
+    beta_t = beta.detach().reshape(1) if isinstance(beta, Tensor) else torch.full((1,), float(beta), device=device)
     if r is None:
         layout = route_layout(dictionary_key.detach(), dictionary_value.detach(), key_type)
-        r = _route_forward(u_h, layout, beta_t, eps, False, False, variant)
+        r = _route_forward(u_h, layout, beta_t, eps, False, False, variant, beta_is_log=beta_is_log)
     r = r.reshape(-1, routing_dim)
     g = grad.detach().reshape(-1, routing_dim)
     # dW = dr Dv takes dr as a 16-bit head and its rounding residual ([n, 2R]
@@ -641,7 +754,8 @@ def _route_backward_rows(
     _lib.check(
         lib.da_dictionary_route_backward_rows(
             logits.data_ptr(), grad_weights.data_ptr(), n, atoms, 0, atoms,
-            beta_t.data_ptr(), _lib.DA_F32, 0.0, 1, 1, variant.flags(),
+            beta_t.data_ptr(), dtype_code(beta_t.dtype), 0.0, 1, 1,
+            variant.flags() | (_lib.DA_ROUTE_BETA_IS_LOG if beta_is_log else 0),
             float(variant.silu_gain), float(variant.logit_scale(routing_dim)), float(eps),
             grad_logits.data_ptr(), weights.data_ptr(), atoms, _half_code(v_type), dbeta_rows.data_ptr(),
             _stream(device),
@@ -654,6 +768,11 @@ def _route_backward_rows(
     d_key = _mm_tn_f32(u_v, grad_logits)
     d_value = _mm_tn_f32(dr_v, weights)
     dbeta = dbeta_rows.sum().reshape(1)
+    if beta_is_log:
+        # d/d log_beta: beta where the clamp passes the gradient.
+        log_beta = beta_t.float()
+        lo, hi = LOG_BETA_RANGE
+        dbeta = dbeta * log_beta.exp() * ((log_beta >= lo) & (log_beta <= hi))
     dx = _normalize_backward(rows, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
     return (
         dx.reshape(x.shape),
@@ -676,6 +795,7 @@ def route_gradients(
     needs: tuple[bool, bool, bool, bool] = (True, True, True, True),
     r: Tensor | None = None,
     bank_grad_dtype: torch.dtype | None = None,
+    beta_is_log: bool = False,
 ) -> tuple[Tensor | None, Tensor | None, Tensor | None, Tensor | None]:
     """(dx, dDk, dDv, dbeta) of the route for ``d loss / d out = grad``.
 
@@ -686,18 +806,20 @@ def route_gradients(
     is the forward's reconstruction before the output norm, when the caller
     kept it (else one route launch forms it again); ``bank_grad_dtype``
     overrides the dtype of the two bank gradients (the native paths only).
+    ``beta_is_log``: ``beta`` is the log-beta tensor (the route uses
+    exp(clamp(., ln 0.05, ln 64))) and the last gradient is at the log.
     """
 
     native = None
     if _route_backward_supported(x, dictionary_key, variant):
         native = _route_backward(
             x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, r,
-            bank_grad_dtype,
+            bank_grad_dtype, beta_is_log,
         )
     elif _route_backward_rows_supported(x, dictionary_key):
         native = _route_backward_rows(
             x, dictionary_key, dictionary_value, beta, eps, normalize_input, normalize_output, grad, variant, r,
-            bank_grad_dtype,
+            bank_grad_dtype, beta_is_log,
         )
     if native is not None:
         dx, ddk, ddv, dbeta = native
@@ -706,8 +828,9 @@ def route_gradients(
     with torch.enable_grad():
         inputs = [t.detach().requires_grad_(need) for t, need in zip((x, dictionary_key, dictionary_value), needs)]
         beta_in = beta.detach().requires_grad_(needs[3]) if isinstance(beta, Tensor) else beta
+        beta_used = beta_in.clamp(*LOG_BETA_RANGE).exp() if beta_is_log else beta_in
         out = dictionary_route_reference(
-            inputs[0], inputs[1], inputs[2], beta_in, eps,
+            inputs[0], inputs[1], inputs[2], beta_used, eps,
             activation="silu" if variant.silu_logits else "identity",
             assignment="silu" if variant.direct_silu else "softmax",
             silu_gain=variant.silu_gain,
@@ -874,6 +997,61 @@ def _attention_forward(
     return out if value_width == model_dim else out[..., :model_dim]
 
 
+def routed_score_layout(branches: int, maps: int, routing_dim: int) -> tuple[int, int, int, float]:
+    """(score width, map stride, map repeat, scale multiplier) of the score maps
+    read as views of routed ``[B, T, 2, branches, routing_dim]`` rows: the
+    assembly of ``assemble_score_maps`` (``ops.py:96-139``) without copies.
+    Grouped branches (``branches > maps``) form one map of ``group`` adjacent
+    branches with the scores multiplied by ``group^-1/2`` (the ``group^-1/4``
+    factor on both operands); repeated branches (``maps > branches``) serve
+    ``maps / branches`` maps each."""
+
+    if branches > maps:
+        group = branches // maps
+        return group * routing_dim, group * routing_dim, 1, group ** -0.5
+    return routing_dim, routing_dim, maps // branches, 1.0
+
+
+def _attention_forward_rows(
+    routed: Tensor, branches: int, maps: int, vt: Tensor, log_scales: Tensor, causal: bool, score_bound: float,
+) -> Tensor:
+    """Per-map fp32 outputs ``[B, S, T, D]`` of the outer attention
+    (``modules.py:242-263`` without the combine), reading the score maps as
+    views of the routed ``[B, T, 2, H, R]`` rows (``routed_score_layout``)
+    and the temperatures as the kernel's exp(clamp(log_scales, ln 1/4,
+    ln 1024)); values come as the projection's V^T tiles ``vt``."""
+
+    batch, length, _, _, routing_dim = routed.shape
+    if routed.stride(-1) != 1 or not routed.is_contiguous() or routed.data_ptr() % 16:
+        raise ValueError("routed rows must be contiguous and 16-byte aligned")
+    width = branches * routing_dim
+    score_dim, map_stride, repeat, mult = routed_score_layout(branches, maps, routing_dim)
+    model_dim = vt.shape[2]
+    device = routed.device
+    out = torch.empty(batch, maps, length, model_dim, dtype=torch.float32, device=device)
+    scales = log_scales.detach().contiguous()
+    flags = (_lib.DA_ATTN_CAUSAL if causal else 0) | _lib.DA_ATTN_OUT_F32 | _lib.DA_ATTN_SCALES_ARE_LOG
+    lib = _lib.get()
+    ws_bytes = lib.da_attention_workspace_bytes(batch, maps, length, score_dim, model_dim, flags)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
+    _lib.check(
+        lib.da_routed_attention(
+            routed.data_ptr(), routed.data_ptr() + width * routed.element_size(),
+            length * 2 * width, 2 * width, map_stride, repeat, score_dim,
+            vt.data_ptr(), vt.stride(0),
+            batch, maps, length, model_dim,
+            scales.data_ptr(), dtype_code(scales.dtype), float(mult), None, _lib.DA_F32,
+            flags, float(score_bound),
+            _half_code(routed.dtype), _half_code(vt.dtype),
+            out.data_ptr(), out.stride(0), out.stride(2), out.stride(1),
+            _ptr(workspace), ws_bytes,
+            _stream(device),
+        ),
+        "routed_attention_hip",
+    )
+    return out
+
+
 BACKWARD_SCORE_WIDTHS = (64, 128, 256, 512)
 
 
@@ -938,6 +1116,66 @@ def _attention_backward(
     )
 
 
+def rows_backward_supported(
+    batch: int, length: int, branches: int, maps: int, routing_dim: int, model_dim: int
+) -> bool:
+    """Whether ``attention_gradients_rows`` takes this module shape: the
+    key-tile kernels' score and value widths, and not the dense path."""
+
+    score_dim = routed_score_layout(branches, maps, routing_dim)[0]
+    if score_dim not in BACKWARD_SCORE_WIDTHS or model_dim not in SUPPORTED_WIDTHS:
+        return False
+    if batch * maps > 65535 or length < 1:
+        return False
+    return not _dense_fits(batch, maps, length, score_dim, model_dim)
+
+
+def attention_gradients_rows(
+    routed: Tensor, branches: int, maps: int, vt: Tensor, log_scales: Tensor, out: Tensor, grad: Tensor,
+    causal: bool,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Outer-attention gradients at the routed rows (the backward of
+    ``_attention_forward_rows``) on the key-tile kernels, for shapes
+    ``rows_backward_supported`` accepts.
+
+    ``routed`` ``[B, T, 2, H, R]`` (16-bit), ``vt`` the forward's V^T tiles
+    ``[B, Tp/32, D, 32]`` (read as they are: the prep kernel turns them into
+    value rows), ``out`` the fp32 per-map outputs ``[B, S, T, D]`` and
+    ``grad`` their gradient.  Returns ``(d_routed, d_value, d_log_scales)``,
+    all fp32:
+    ``d_routed`` has the routed rows' shape (the score-map assembly's
+    backward, maps sharing rows summed), ``d_log_scales`` the gradient at
+    ``log_scales`` through the kernels' clamp.
+    """
+
+    batch, length, _, _, routing_dim = routed.shape
+    model_dim = vt.shape[2]
+    if vt.shape[0] != batch or vt.shape[1] * 32 < length or vt.shape[3] != 32 or not vt.is_contiguous():
+        raise ValueError("vt must be contiguous [B, Tp/32, D, 32] V^T tiles covering the sequence")
+    if vt.shape[1] * 32 != _round_up(length, TOKEN_PAD):
+        raise ValueError(f"vt must hold the sequence padded to a multiple of {TOKEN_PAD} tokens")
+    width = branches * routing_dim
+    score_dim, map_stride, repeat, mult = routed_score_layout(branches, maps, routing_dim)
+    device = routed.device
+    v_type = vt.dtype
+    v = (vt, vt.stride(0), v_type)
+    o = _aligned(out.detach())
+    go = _aligned(grad.detach().to(v_type))
+    scales = log_scales.detach().contiguous()
+    d_routed = torch.empty(batch, length, 2, branches, routing_dim, dtype=torch.float32, device=device)
+    d_value = torch.empty(batch, length, model_dim, dtype=torch.float32, device=device)
+    d_scales = torch.empty(maps, dtype=torch.float32, device=device)
+    row = (length * 2 * width, 2 * width, map_stride)
+    q_ptr, k_off = routed.data_ptr(), width * routed.element_size()
+    dq_ptr, dk_off = d_routed.data_ptr(), width * 4
+    _attention_backward_ex(
+        (q_ptr, *row), (q_ptr + k_off, *row), repeat, v, o, go, scales, float(mult), LOG_SCALE_RANGE,
+        (batch, maps, length, length, score_dim, model_dim), causal, routed.dtype,
+        dq_ptr, dq_ptr + dk_off, d_value, d_scales, "routed_attention_hip backward",
+    )
+    return d_routed, d_value, d_scales
+
+
 def _native_backward_supported(query: Tensor, value: Tensor) -> bool:
     batch, maps, _, score_dim = query.shape
     return score_dim <= BACKWARD_SCORE_WIDTHS[-1] and batch * maps <= 65535 and value.shape[-1] <= SUPPORTED_WIDTHS[-1]
@@ -957,13 +1195,17 @@ DENSE_BACKWARD_MIN_LENGTH = 2048
 DENSE_BACKWARD_MAX_SCORES = 1 << 27
 
 
-def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
-    batch, maps, length, score_dim = query.shape
+def _dense_fits(batch: int, maps: int, length: int, score_dim: int, model_dim: int) -> bool:
     if not (score_dim <= BACKWARD_SCORE_WIDTHS[-1] and length >= 1 and maps <= 64
             and batch * maps * length * length <= DENSE_BACKWARD_MAX_SCORES):
         return False
     return (score_dim >= DENSE_BACKWARD_MIN_SCORE_DIM or length >= DENSE_BACKWARD_MIN_LENGTH
-            or value.shape[-1] > SUPPORTED_WIDTHS[-1])
+            or model_dim > SUPPORTED_WIDTHS[-1])
+
+
+def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
+    batch, maps, length, score_dim = query.shape
+    return _dense_fits(batch, maps, length, score_dim, value.shape[-1])
 
 
 def _attention_backward_dense(

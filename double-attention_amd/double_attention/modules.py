@@ -481,29 +481,31 @@ class _HipModuleFunction(torch.autograd.Function):
         key_dtype = hip_ops.route_key_dtype(cfg.normalize_routing_input, dtype)
         layout = hip_ops.route_layout(dictionary_key, dictionary_value, key_dtype)
         variant = hip_ops.RouteVariant.of_config(cfg)
-        beta = module.beta.detach()
+        # beta and the score scales are formed from their logs in the kernels
+        # (the clamped exponentials of modules.py:130-132 and ops.py:160-161).
+        log_beta = module.log_beta.detach()
         # Q and K rows route together, as [B, T, 2, H, R] rows, fp16 out (the
         # attention's operand type for bounded rows).  The route stops before
         # its output norm: the backward needs that reconstruction r, and the
         # norm is one row normalization here.
         recon = hip_ops._route_forward(
-            qk.view(-1, routing_dim), layout, beta, cfg.eps, cfg.normalize_routing_input, False, variant,
-            out_dtype=torch.float16,
+            qk.view(-1, routing_dim), layout, log_beta, cfg.eps, cfg.normalize_routing_input, False, variant,
+            out_dtype=torch.float16, beta_is_log=True,
         )
         if cfg.normalize_routing_output:
             # F.normalize in fp32, one rounding to fp16.
             routed = hip_ops._row_normalize(recon, cfg.eps, torch.float16)
         else:
             routed = recon
-        score_query, score_key = _HipModuleFunction._score_maps(routed, batch, length, branches, maps, routing_dim)
-        scales = score_scale_from_log(module.log_score_scales.detach()).float()
         group = branches // maps if branches > maps else 1
         bound = 1.01 * group if cfg.normalize_routing_output else 0.0
         # fp32 per-map outputs: the combine sums them before one rounding (as
         # the fused forward's in-kernel mix), and the backward's rowsum(dO . O)
-        # and map-mix gradient read them unrounded.
-        map_output = hip_ops._attention_forward(
-            score_query, score_key, None, scales, cfg.causal, bound, vt=vt, out_dtype=torch.float32
+        # and map-mix gradient read them unrounded.  The score maps are views
+        # of the routed rows (no assembled copies).
+        map_output = hip_ops._attention_forward_rows(
+            routed.view(batch, length, 2, branches, routing_dim), branches, maps, vt, module.log_score_scales,
+            cfg.causal, bound,
         )
         factors = None
         if cfg.map_combine == "weighted_sum":
@@ -522,7 +524,7 @@ class _HipModuleFunction(torch.autograd.Function):
         ctx.dtype = dtype
         ctx.param_names = [name for name, _ in module.named_parameters()]
         ctx.x_dtype = x.dtype
-        ctx.save_for_backward(xc, qk, recon, routed, map_output, mixed, vt, scales, beta, dictionary_key,
+        ctx.save_for_backward(xc, qk, recon, routed, map_output, mixed, vt, log_beta, dictionary_key,
                               dictionary_value, factors if factors is not None else torch.empty(0), raw_key,
                               raw_value, *params)
         return out
@@ -540,7 +542,7 @@ class _HipModuleFunction(torch.autograd.Function):
         module = ctx.module
         cfg = module.config
         dtype = ctx.dtype
-        (xc, qk, recon, routed, map_output, mixed, vt, scales, beta, dk, dv, factors, raw_key, raw_value,
+        (xc, qk, recon, routed, map_output, mixed, vt, log_beta, dk, dv, factors, raw_key, raw_value,
          *params) = ctx.saved_tensors
         named = dict(zip(ctx.param_names, params))
         batch, length, model_dim = xc.shape
@@ -558,7 +560,7 @@ class _HipModuleFunction(torch.autograd.Function):
         if isinstance(module.output, nn.Linear):
             d_mixed = torch.mm(g, named["output.weight"].detach().to(dtype))
             if wants("output.weight"):
-                grads["output.weight"] = _mm_tn_f32(g, mixed2d)
+                grads["output.weight"] = _mm_tn_f32(g, mixed2d, named["output.weight"].dtype)
         else:
             d_mixed = g
         # Map combine.
@@ -576,34 +578,52 @@ class _HipModuleFunction(torch.autograd.Function):
                 d_maps = (d32 * factors[None, :, None, None]).to(dtype)
         else:
             d_maps = d_mixed.view(batch, length, maps, model_dim).transpose(1, 2)
-        # Outer attention.
-        score_query, score_key = _HipModuleFunction._score_maps(routed, batch, length, branches, maps, routing_dim)
-        padded = vt.shape[1] * 32
-        value_rows = vt.transpose(2, 3).reshape(batch, padded, model_dim)[:, :length]
-        # dq and dk stay fp32 (no rounding, no cast): the route backward takes
-        # fp32 gradient rows.
-        d_sq, d_sk, d_value, d_scales = hip_ops.attention_gradients(
-            score_query, score_key, value_rows, scales, map_output, d_maps, cfg.causal, qk_grad_dtype=torch.float32
-        )
-        if wants("log_score_scales"):
-            # The clamp passes the gradient only inside its window.
-            log_scales = named["log_score_scales"].detach()
-            inside = log_scales.clamp(math.log(0.25), math.log(1024.0)) == log_scales
-            grads["log_score_scales"] = d_scales.float() * scales * inside
-        # Score-map assembly (views, grouping or repetition of the branches).
-        if branches == maps:
-            d_rq, d_rk = d_sq, d_sk
+        # Outer attention.  dq and dk stay fp32 (no rounding, no cast): the
+        # route backward takes fp32 gradient rows.
+        log_scales = named["log_score_scales"]
+        if hip_ops.rows_backward_supported(batch, length, branches, maps, routing_dim, model_dim):
+            # The key-tile kernels read the score maps as views of the routed
+            # rows and write their gradients into [B, T, 2, H, R] (the
+            # assembly's backward), with the temperature clamp's backward.
+            d_rows_qk, d_value, d_log_scales = hip_ops.attention_gradients_rows(
+                routed.view(batch, length, 2, branches, routing_dim), branches, maps, vt, log_scales,
+                map_output, d_maps, cfg.causal,
+            )
+            if wants("log_score_scales"):
+                grads["log_score_scales"] = d_log_scales
+            d_routed = d_rows_qk.view(-1, routing_dim)
         else:
-            # The assembly is linear (scales, concatenation, repetition): its
-            # backward runs on fp32 copies of the rows, so the fp32 dq/dk reach
-            # the route backward unrounded.
-            with torch.enable_grad():
-                rows = routed.view(batch, length, 2, branches, routing_dim)
-                rq = rows[:, :, 0].transpose(1, 2).detach().float().requires_grad_()
-                rk = rows[:, :, 1].transpose(1, 2).detach().float().requires_grad_()
-                sq, sk = assemble_score_maps(rq, rk, maps)
-                d_rq, d_rk = torch.autograd.grad((sq, sk), (rq, rk), (d_sq.float(), d_sk.float()))
-        d_routed = torch.stack((d_rq.transpose(1, 2), d_rk.transpose(1, 2)), dim=2).reshape(-1, routing_dim)
+            padded = vt.shape[1] * 32
+            value_rows = vt.transpose(2, 3).reshape(batch, padded, model_dim)[:, :length]
+            score_query, score_key = _HipModuleFunction._score_maps(
+                routed, batch, length, branches, maps, routing_dim
+            )
+            # The temperatures as the forward kernel formed them: fp32
+            # exponentials of the clamped logs.
+            log32 = log_scales.detach().float()
+            scales = log32.clamp(*hip_ops.LOG_SCALE_RANGE).exp()
+            d_sq, d_sk, d_value, d_scales = hip_ops.attention_gradients(
+                score_query, score_key, value_rows, scales, map_output, d_maps, cfg.causal,
+                qk_grad_dtype=torch.float32,
+            )
+            if wants("log_score_scales"):
+                # The clamp passes the gradient only inside its window.
+                inside = (log32 >= hip_ops.LOG_SCALE_RANGE[0]) & (log32 <= hip_ops.LOG_SCALE_RANGE[1])
+                grads["log_score_scales"] = d_scales.float() * scales * inside
+            # Score-map assembly (views, grouping or repetition of the branches).
+            if branches == maps:
+                d_rq, d_rk = d_sq, d_sk
+            else:
+                # The assembly is linear (scales, concatenation, repetition):
+                # its backward runs on fp32 copies of the rows, so the fp32
+                # dq/dk reach the route backward unrounded.
+                with torch.enable_grad():
+                    rows = routed.view(batch, length, 2, branches, routing_dim)
+                    rq = rows[:, :, 0].transpose(1, 2).detach().float().requires_grad_()
+                    rk = rows[:, :, 1].transpose(1, 2).detach().float().requires_grad_()
+                    sq, sk = assemble_score_maps(rq, rk, maps)
+                    d_rq, d_rk = torch.autograd.grad((sq, sk), (rq, rk), (d_sq.float(), d_sk.float()))
+            d_routed = torch.stack((d_rq.transpose(1, 2), d_rk.transpose(1, 2)), dim=2).reshape(-1, routing_dim)
         # Route.
         variant = hip_ops.RouteVariant.of_config(cfg)
         # With the raw bank the gradients at the normalized atoms stay fp32
@@ -612,9 +632,9 @@ class _HipModuleFunction(torch.autograd.Function):
         if ctx.raw_bank and raw_value is None:
             need_value = need_key
         d_rows, d_key, d_val, d_beta = hip_ops.route_gradients(
-            qk.view(-1, routing_dim), dk, dv, beta, cfg.eps, cfg.normalize_routing_input,
+            qk.view(-1, routing_dim), dk, dv, log_beta, cfg.eps, cfg.normalize_routing_input,
             cfg.normalize_routing_output, variant, d_routed, (True, need_key, need_value, wants("log_beta")), recon,
-            torch.float32 if ctx.raw_bank else None,
+            torch.float32 if ctx.raw_bank else None, beta_is_log=True,
         )
         if ctx.raw_bank and (need_key or need_value):
             d_key, d_val = hip_ops.dictionary_normalize_backward_hip(raw_key, raw_value, d_key, d_val, cfg.eps)
@@ -623,9 +643,8 @@ class _HipModuleFunction(torch.autograd.Function):
             if not ctx.needs_input_grad[4]:
                 d_val = None
         if wants("log_beta") and d_beta is not None:
-            log_beta = named["log_beta"].detach()
-            inside = log_beta.clamp(math.log(0.05), math.log(64.0)) == log_beta
-            grads["log_beta"] = d_beta.float() * beta.float() * inside
+            # At the log, through the clamp (the route backward's beta_is_log).
+            grads["log_beta"] = d_beta
         # Q/K/V projections.
         x2d = xc.reshape(tokens, model_dim)
         d_qk = d_rows.reshape(tokens, 2 * width).to(dtype)
@@ -637,16 +656,17 @@ class _HipModuleFunction(torch.autograd.Function):
             dx.addmm_(d_qk[:, width:], named["key.weight"].detach().to(dtype))
             dx = dx.view(batch, length, model_dim).to(ctx.x_dtype)
         if wants("query.weight") and wants("key.weight"):
-            d_wqk = _mm_tn_f32(d_qk, x2d)
+            wq_dtype, wk_dtype = named["query.weight"].dtype, named["key.weight"].dtype
+            d_wqk = _mm_tn_f32(d_qk, x2d, wq_dtype if wq_dtype == wk_dtype else torch.float32)
             grads["query.weight"], grads["key.weight"] = d_wqk[:width], d_wqk[width:]
         elif wants("query.weight"):
-            grads["query.weight"] = _mm_tn_f32(d_qk[:, :width], x2d)
+            grads["query.weight"] = _mm_tn_f32(d_qk[:, :width], x2d, named["query.weight"].dtype)
         elif wants("key.weight"):
-            grads["key.weight"] = _mm_tn_f32(d_qk[:, width:], x2d)
+            grads["key.weight"] = _mm_tn_f32(d_qk[:, width:], x2d, named["key.weight"].dtype)
         if wants("value.weight"):
-            grads["value.weight"] = _mm_tn_f32(d_v, x2d)
+            grads["value.weight"] = _mm_tn_f32(d_v, x2d, named["value.weight"].dtype)
         if wants("value.bias"):
-            grads["value.bias"] = d_v.sum(0, dtype=torch.float32)   # fp32 accumulation, no fp32 copy
+            grads["value.bias"] = hip_ops.column_sums(d_v, named["value.bias"].dtype)
         tail = [
             grads[name].to(named[name].dtype).reshape(named[name].shape) if name in grads else None
             for name in ctx.param_names

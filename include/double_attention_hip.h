@@ -27,8 +27,10 @@
  *                             + direct-SiLU backward branch          src/double_attention/triton_kernels.py:1940-1948
  *   da_routed_attention       routed_attention_triton / _reference   src/double_attention/triton_kernels.py:2290-2305, ops.py:65-93
  *                             + map combine                          src/double_attention/modules.py:265-272
- *   da_routed_attention_backward, da_attention_backward_workspace_bytes
+ *   da_routed_attention_backward, da_routed_attention_backward_ex, da_attention_backward_workspace_bytes
  *                             backward of routed_attention_triton    src/double_attention/triton_kernels.py:2093-2263, 2290-2305
+ *                             (_ex: on the score maps as views of the routed rows, with the
+ *                             temperature clamp's backward,          src/double_attention/modules.py:242-263, ops.py:160-161)
  *   da_qkv_projection         _project_query_key + self.value        src/double_attention/modules.py:143-157, 212
  *   da_linear                 self.output                            src/double_attention/modules.py:117-121, 272
  *   da_linear_ex              DoubleAttentionBlock.feedforward       src/double_attention/modules.py:318-330, 343-346
@@ -127,9 +129,12 @@ int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_
  * normalized atoms.
  *   raw_key, raw_value: [routing_dim, atoms] row-major, raw_dtype (raw_value
  *           NULL = tied bank)
- *   grad_key, grad_value: [routing_dim, atoms] fp32, the gradients at the
- *           normalized key and value atoms (grad_value may be NULL: zero).
- *           For a tied bank both flow into the key atoms.
+ *   grad_key, grad_value: fp32 gradients at the normalized key and value
+ *           atoms, coordinate r of atom j at [r * grad_ld_r + j * grad_ld_j]
+ *           (grad_ld_r = atoms, grad_ld_j = 1 for [routing_dim, atoms] rows;
+ *           grad_ld_r = 1, grad_ld_j = routing_dim for the atom-major
+ *           [atoms, routing_dim] gradients of the route backward); grad_value
+ *           may be NULL (zero).  For a tied bank both flow into the key atoms.
  *   d_raw_key, d_raw_value: out, [routing_dim, atoms] raw_dtype (d_raw_value
  *           NULL = not wanted; must be NULL for a tied bank)
  * Atom j with raw column v and gradient h gets (h - n <n, h>) / |v| with
@@ -137,8 +142,8 @@ int da_dictionary_normalize(const void* raw_key, const void* raw_value, int raw_
  */
 int da_dictionary_normalize_backward(const void* raw_key, const void* raw_value, int raw_dtype,
                                      int64_t routing_dim, int64_t atoms, float eps, const float* grad_key,
-                                     const float* grad_value, void* d_raw_key, void* d_raw_value,
-                                     da_stream_t stream);
+                                     const float* grad_value, int64_t grad_ld_r, int64_t grad_ld_j,
+                                     void* d_raw_key, void* d_raw_value, da_stream_t stream);
 
 /*
  * Row L2 normalization, F.normalize(x, dim=-1, eps) (ops.py:39, :62; the
@@ -294,6 +299,64 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
                                  int flags, int qk_dtype, int v_dtype, void* workspace, int64_t workspace_bytes,
                                  float* grad_query, float* grad_key, float* grad_value, float* grad_scales,
                                  da_stream_t stream);
+
+/*
+ * da_routed_attention_backward on strided query and key rows, with score
+ * scales in any dtype or as logs.  Query row t of (sequence b, map s) starts
+ * at query + b*query_stride_b + (s / map_repeat)*query_map_stride +
+ * t*query_stride_t elements (key rows alike), so the score maps can be views
+ * of the module's routed [batch, length, 2, branches, routing_dim] rows
+ * (modules.py:242-247 reads them through assemble_score_maps): map_repeat
+ * maps sharing one branch (outer_maps > qk_branches), or query_map_stride =
+ * score_dim with score_dim = group * routing_dim for grouped branches
+ * (qk_branches > outer_maps, with scale_mult = group^-1/2 in place of the
+ * group^-1/4 factor on both operands).  grad_query and grad_key are fp32 with
+ * the strides of query and key (every map's rows are zeroed, then
+ * accumulated: maps sharing rows add up); they must not overlap each other.
+ * Strides are multiples of 8, stride_t >= score_dim, and maps a multiple of
+ * map_repeat.
+ * The applied scale of map s is scales[s] * scale_mult, or with
+ * DA_ATTN_SCALES_ARE_LOG exp(clamp(scales[s], log_min, log_max)) *
+ * scale_mult; grad_scales[s] is the gradient at scales[s], which for logs
+ * is zero outside [log_min, log_max] (the clamp's backward).
+ * The values come as rows (value, v_dtype) or, with value NULL, as the
+ * forward's V^T tiles (value_t: sequence b at value_t + b*value_t_stride_b
+ * elements, [padded key_length / 32][value_dim][32], 16-bit of
+ * value_t_dtype, converted to v_dtype; padding tokens finite, as
+ * da_routed_attention requires).  out has out_dtype (DA_F32, DA_F16 or
+ * DA_BF16) whatever v_dtype is.  flags: DA_ATTN_CAUSAL and
+ * DA_ATTN_SCALES_ARE_LOG.  Everything else is as for
+ * da_routed_attention_backward (whose workspace size serves both).
+ */
+typedef struct da_attention_backward_args {
+  const void* query;
+  int64_t query_stride_b, query_stride_t, query_map_stride;
+  const void* key;
+  int64_t key_stride_b, key_stride_t, key_map_stride;
+  int64_t map_repeat;
+  const void* value;        /* [batch, key_length, value_dim], or NULL: value_t */
+  const void* value_t;
+  int64_t value_t_stride_b;
+  int value_t_dtype;
+  const void* out;          /* [batch*maps, length, value_dim], out_dtype */
+  int out_dtype;
+  const void* grad_out;     /* [batch*maps, length, value_dim] */
+  const void* scales;       /* [maps], scales_dtype */
+  int scales_dtype;
+  float scale_mult;
+  float log_min, log_max;   /* with DA_ATTN_SCALES_ARE_LOG */
+  int64_t batch, maps, length, key_length, score_dim, value_dim;
+  int flags;                /* DA_ATTN_CAUSAL, DA_ATTN_SCALES_ARE_LOG */
+  int qk_dtype, v_dtype;
+  void* workspace;
+  int64_t workspace_bytes;
+  float* grad_query;
+  float* grad_key;
+  float* grad_value;        /* [batch, key_length, value_dim] */
+  float* grad_scales;       /* [maps] */
+} da_attention_backward_args;
+
+int da_routed_attention_backward_ex(const da_attention_backward_args* args, da_stream_t stream);
 
 /*
  * Q/K and V projections in one launch (modules.py:143-157 and 212):

@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 22
+    assert len(names) == 23
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -156,12 +156,13 @@ def test_attention_backward_rejects_bad_arguments() -> None:
     h = lib.get()
     f = _fake()
     need = h.da_attention_backward_workspace_bytes(2, 3, 100, 100, 128, 256)
-    # Q^T, K^T and dO^T tiles over 128 padded tokens, then two fp32 rows
-    # (6 * 100 * 4 = 2400 bytes, rounded up to 2560).
-    assert need == 2 * (6 * 128 * 128 * 2) + 6 * 128 * 256 * 2 + 2 * 2560
+    # Q^T, K^T and dO^T tiles over 128 padded tokens, two fp32 rows (6 * 100 * 4
+    # = 2400 bytes, rounded up to 2560), then value rows [2, 128, 256] for
+    # V^T tiles (da_routed_attention_backward_ex).
+    assert need == 2 * (6 * 128 * 128 * 2) + 6 * 128 * 256 * 2 + 2 * 2560 + 2 * 128 * 256 * 2
     # Cross attention: K^T tiles follow the key count (300 -> 320 padded).
     cross = h.da_attention_backward_workspace_bytes(2, 3, 100, 300, 128, 256)
-    assert cross == 6 * 128 * 128 * 2 + 6 * 320 * 128 * 2 + 6 * 128 * 256 * 2 + 2 * 2560
+    assert cross == 6 * 128 * 128 * 2 + 6 * 320 * 128 * 2 + 6 * 128 * 256 * 2 + 2 * 2560 + 2 * 320 * 256 * 2
     good = [f, f, f, f, f, f, 2, 3, 100, 100, 128, 256, lib.DA_ATTN_CAUSAL, lib.DA_BF16, lib.DA_BF16,
             f, need, f, f, f, f, None]
     cases = [
@@ -189,6 +190,65 @@ def test_attention_backward_rejects_bad_arguments() -> None:
     no_keys[9] = 0
     no_keys[12] = 0
     assert h.da_routed_attention_backward(*no_keys) == -1
+    # Log scales only through da_routed_attention_backward_ex.
+    logs = list(good)
+    logs[12] = lib.DA_ATTN_SCALES_ARE_LOG
+    assert h.da_routed_attention_backward(*logs) == -1
+    assert "flag bits" in h.da_last_error().decode()
+
+
+def test_strided_attention_backward_rejects_bad_arguments() -> None:
+    # da_routed_attention_backward_ex: the module layout [B, T, 2, H, R] of
+    # C1's shape, then one bad field at a time.
+    h = lib.get()
+    f = _fake()
+    need = h.da_attention_backward_workspace_bytes(8, 1, 512, 512, 256, 512)
+    assert h.da_routed_attention_backward_ex(None, None) == -1
+    assert "null args" in h.da_last_error().decode()
+
+    def args(**changes):
+        a = lib.AttentionBackwardArgs()
+        a.query, a.query_stride_b, a.query_stride_t, a.query_map_stride = f, 512 * 512, 512, 256
+        a.key, a.key_stride_b, a.key_stride_t, a.key_map_stride = f + 512, 512 * 512, 512, 256
+        a.map_repeat = 1
+        a.value = a.out = a.grad_out = a.scales = f
+        a.out_dtype = lib.DA_F32
+        a.scales_dtype, a.scale_mult = lib.DA_BF16, 1.0
+        a.log_min, a.log_max = -1.3862944, 6.9314718
+        a.batch, a.maps, a.length, a.key_length, a.score_dim, a.value_dim = 8, 1, 512, 512, 256, 512
+        a.flags = lib.DA_ATTN_CAUSAL | lib.DA_ATTN_SCALES_ARE_LOG
+        a.qk_dtype, a.v_dtype = lib.DA_F16, lib.DA_BF16
+        a.workspace, a.workspace_bytes = f, need
+        a.grad_query, a.grad_key, a.grad_value, a.grad_scales = f, f + 1024, f, f
+        for name, value in changes.items():
+            setattr(a, name, value)
+        return a
+
+    cases = [
+        (dict(map_repeat=0), -1, "map_repeat"),
+        (dict(maps=3, map_repeat=2), -1, "map_repeat"),
+        (dict(query_stride_t=260), -3, "multiples of 8"),
+        (dict(key_map_stride=-8), -3, "multiples of 8"),
+        (dict(query_stride_t=128), -1, "stride_t must be >= score_dim"),
+        (dict(scales_dtype=7), -1, "scales dtype"),
+        (dict(scale_mult=0.0), -1, "scale_mult"),
+        (dict(log_min=2.0, log_max=1.0), -1, "log_min <= log_max"),
+        (dict(flags=lib.DA_ATTN_MIX), -1, "flag bits"),
+        (dict(flags=lib.DA_ATTN_OUT_F32), -1, "flag bits"),   # out_dtype says it
+        (dict(out_dtype=5), -1, "bad out dtype"),
+        (dict(value=None, value_t=f, value_t_dtype=lib.DA_F32), -1, "V^T tiles"),
+        (dict(value=None, value_t=f, value_t_dtype=lib.DA_F16, value_t_stride_b=12), -1, "V^T tiles"),
+        (dict(value=None, value_t=None, value_t_dtype=lib.DA_F16), -1, "null pointer"),
+        (dict(grad_key=f + 1028), -3, "gradients"),
+        (dict(scales=f + 1, scales_dtype=lib.DA_BF16), -3, "element size"),
+        (dict(workspace_bytes=need - 1), -5, "workspace of"),
+    ]
+    for changes, code, pattern in cases:
+        a = args(**changes)
+        assert h.da_routed_attention_backward_ex(ctypes.byref(a), None) == code, (changes, h.da_last_error())
+        assert pattern in h.da_last_error().decode(), h.da_last_error()
+    empty = args(batch=0)
+    assert h.da_routed_attention_backward_ex(ctypes.byref(empty), None) == 0
 
 
 def test_noalloc_forward_rejects_oversized_problems_on_the_host() -> None:
@@ -242,7 +302,8 @@ def test_normalize_backward_rejects_bad_arguments() -> None:
 
     def call(**kw):
         args = dict(raw_key=buf, raw_value=buf, raw_dtype=lib.DA_F32, routing_dim=64, atoms=100, eps=1e-6,
-                    grad_key=buf, grad_value=buf, d_raw_key=buf, d_raw_value=buf, stream=None)
+                    grad_key=buf, grad_value=buf, grad_ld_r=100, grad_ld_j=1, d_raw_key=buf, d_raw_value=buf,
+                    stream=None)
         args.update(kw)
         return h.da_dictionary_normalize_backward(*args.values())
 
@@ -254,6 +315,11 @@ def test_normalize_backward_rejects_bad_arguments() -> None:
     assert b"null" in h.da_last_error()
     assert call(raw_value=None) == -1                   # d_raw_value for a tied bank
     assert b"tied" in h.da_last_error()
+    # Gradient strides: coordinate-major (>= atoms, 1) or atom-major (1, >= routing_dim).
+    assert call(grad_ld_r=99) == -1
+    assert b"gradient strides" in h.da_last_error()
+    assert call(grad_ld_r=1, grad_ld_j=63) == -1
+    assert call(grad_ld_r=2, grad_ld_j=64) == -1
 
 
 def test_row_normalize_rejects_bad_arguments() -> None:

@@ -124,6 +124,12 @@ def test_dictionary_normalize_backward(raw_dtype, routing_dim, atoms, tied) -> N
             col = np.maximum(np.linalg.norm(raw, axis=0), eps)[1:]
             assert_parity(actual[:, 1:] * torch.as_tensor(col, device=device, dtype=torch.float32),
                           expected[:, 1:] * col, 5e-3, 4e-2, "bank backward")
+    # The same gradients handed over atom-major (transposed views of [M, R]
+    # rows, as the route backward produces them) give the same bits.
+    gk_t, gv_t = grad_key.t().contiguous().t(), grad_value.t().contiguous().t()
+    assert atoms == 1 or gk_t.stride() == (1, routing_dim)
+    d_key_t, d_value_t = da.hip_ops.dictionary_normalize_backward_hip(raw_key, raw_value, gk_t, gv_t, eps)
+    assert torch.equal(d_key_t, d_key) and (tied or torch.equal(d_value_t, d_value))
 
 
 ROW_NORM_CASES = [
@@ -552,6 +558,88 @@ def test_attention_fp32_outputs(case) -> None:
         assert_parity(grad, exp, rel, max(2e-2 * scale, 1e-6), f"attention backward fp32 out {case} d{name}")
 
 
+# (batch, length, branches, maps, routing_dim, model_dim, causal): identity
+# maps, grouped branches (one map of two or four adjacent branches, scores
+# times group^-1/2) and repeated branches, read as views of the routed rows.
+ROWS_LAYOUTS = [
+    (2, 200, 1, 1, 256, 512, True),
+    (2, 130, 2, 1, 128, 256, True),
+    (1, 96, 4, 2, 64, 128, False),
+    (2, 70, 1, 2, 128, 64, True),
+    (1, 150, 2, 4, 64, 512, True),
+    (2, 64, 4, 4, 128, 256, True),
+]
+
+
+@pytest.mark.parametrize("layout", ROWS_LAYOUTS, ids=lambda c: "b{}t{}h{}s{}r{}d{}{}".format(*c[:6], "c" if c[6] else ""))
+def test_attention_on_routed_rows(layout) -> None:
+    # The training path's outer attention: the score maps are strided views
+    # of [B, T, 2, H, R] routed rows, the temperatures clamped exponentials of
+    # bf16 logs (some maps below ln 1/4 or above ln 1024, where the clamp
+    # passes no gradient).  Forward and gradients (routed rows, values, logs)
+    # against the oracle's assembly, attention and their backwards.
+    device = _device()
+    batch, length, branches, maps, routing_dim, model_dim, causal = layout
+    routed = unit_rows((batch, length, 2, branches, routing_dim), torch.float16, device, 60)
+    g = torch.Generator().manual_seed(61)
+    value = torch.randn(batch, length, model_dim, generator=g).to(device, torch.bfloat16)
+    logs = [math.log(4.0) + 0.5 * i for i in range(maps)]
+    if maps > 1:
+        logs[-1] = 7.5          # above ln 1024
+    if maps > 2:
+        logs[0] = -2.0          # below ln 1/4
+    log_scales = torch.tensor(logs, dtype=torch.bfloat16, device=device)
+    grad = torch.randn(batch, maps, length, model_dim, generator=g).to(device, torch.bfloat16)
+    vt = da.hip_ops.value_transposed(value)
+    group = branches // maps if branches > maps else 1
+    out = da.hip_ops._attention_forward_rows(routed, branches, maps, vt, log_scales, causal, 1.01 * group)
+
+    rows = np32(routed).astype(np.float64)
+    rq, rk = rows[:, :, 0].transpose(0, 2, 1, 3), rows[:, :, 1].transpose(0, 2, 1, 3)
+    sq, sk = oracle.assemble_score_maps(rq, rk, maps)
+    log64 = np32(log_scales).astype(np.float64)
+    lo, hi = math.log(0.25), math.log(1024.0)
+    gamma = np.exp(np.clip(log64, lo, hi))
+    v64 = np32(value).astype(np.float64)
+    label = "routed-rows attention {}".format(layout)
+    expected_out = oracle.routed_attention(sq, sk, v64, gamma, causal)
+    assert_parity(out, expected_out, label=label + " out")
+
+    d_routed, d_value, d_logs = da.hip_ops.attention_gradients_rows(
+        routed, branches, maps, vt, log_scales, out, grad, causal
+    )
+    dq, dk, dv, dgamma = oracle.routed_attention_backward(sq, sk, v64, gamma, np32(grad).astype(np.float64), causal)
+    drq, drk = oracle.assemble_score_maps_backward(dq, dk, branches)
+    expected_rows = np.stack((drq.transpose(0, 2, 1, 3), drk.transpose(0, 2, 1, 3)), axis=2)
+    inside = (log64 >= lo) & (log64 <= hi)
+    expected_logs = dgamma * gamma * inside
+    for name, got, exp in (("rows", d_routed, expected_rows), ("value", d_value, dv)):
+        scale = float(np.abs(exp).max())
+        assert_parity(got, exp, 1e-2, max(2e-2 * scale, 1e-6), f"{label} d{name}")
+    assert d_logs.shape == (maps,)
+    got_logs = np32(d_logs)
+    # Outside the clamp window the gradient is exactly zero.
+    assert (got_logs[~inside] == 0).all(), got_logs
+    # The scale gradient sums dS (q.k) over every score, terms that cancel
+    # (each row of dS sums to zero).  The kernels take D_i = rowsum(dO . O)
+    # from the forward's fp32 output, whose bf16 probabilities leave about
+    # 2e-3 relative error in D_i (2.1e-3 measured at the first map of
+    # b2t70h1s2r128d64c, where the result then reads -0.2298 for -0.2084,
+    # exactly what D from that output gives in fp64).  That error reaches the
+    # sum through gamma sum_i D_i E_P[q.k]_i without cancelling, so the bar
+    # allows 3e-3 of that sum beside a 3e-2 relative error.
+    scores = np.matmul(sq, np.swapaxes(sk, -1, -2))
+    logits = scores * gamma[None, :, None, None]
+    if causal:
+        logits = np.where(np.triu(np.ones((length, length), bool), 1), -np.inf, logits)
+    probs = np.exp(logits - logits.max(-1, keepdims=True))
+    probs /= probs.sum(-1, keepdims=True)
+    d_rows = (np32(grad).astype(np.float64) * expected_out).sum(-1)
+    cond = gamma * (np.abs(d_rows) * np.abs((probs * scores).sum(-1))).sum(axis=(0, 2))
+    bound = 3e-2 * np.abs(expected_logs) + 3e-3 * cond + 1e-6
+    assert (np.abs(got_logs - expected_logs) <= bound).all(), (label, got_logs, expected_logs, bound)
+
+
 # ---------------------------------------------------------------- whole module
 
 
@@ -764,12 +852,12 @@ def test_lm_training_gradients(monkeypatch) -> None:
     config = da.experiment_config("qk2-s2", untied_dictionary=False, backend="hip")
     kwargs = dict(dictionary_group_size=2, feedforward_dim=1536)
     calls = []
-    for fn in ("_attention_backward", "_route_backward"):
+    for fn in ("_attention_backward", "attention_gradients_rows", "_route_backward"):
         original = getattr(da.hip_ops, fn)
 
-        def counted(*args, _original=original, _name=fn):
+        def counted(*args, _original=original, _name=fn, **kwargs):
             calls.append(_name)
-            return _original(*args)
+            return _original(*args, **kwargs)
 
         monkeypatch.setattr(da.hip_ops, fn, counted)
 
@@ -794,7 +882,9 @@ def test_lm_training_gradients(monkeypatch) -> None:
         for m in models:
             _, loss = m(ids, targets)
             loss.float().backward()
-        assert calls.count("_attention_backward") == 2 and calls.count("_route_backward") == 2
+        # Two layers: their outer attentions on the routed rows, their routes
+        # on the attention backward kernels.
+        assert calls.count("attention_gradients_rows") == 2 and calls.count("_route_backward") == 2, calls
         for (name, p_hip), p_t16, p_ref in zip(
             models[0].named_parameters(), models[1].parameters(), models[2].parameters()
         ):
@@ -964,8 +1054,8 @@ def test_module_backward_runs_native_kernels(monkeypatch, preset, overrides, tok
     device = _device()
     config = da.experiment_config(preset, backend="hip", **overrides)
     calls = []
-    for fn in ("_attention_backward", "_attention_backward_dense", "_route_backward", "_route_backward_rows",
-               "_route_forward"):
+    for fn in ("_attention_backward", "_attention_backward_dense", "attention_gradients_rows", "_route_backward",
+               "_route_backward_rows", "_route_forward"):
         original = getattr(da.hip_ops, fn)
 
         def counted(*args, _original=original, _name=fn, **kwargs):
@@ -1000,7 +1090,8 @@ def test_module_backward_runs_native_kernels(monkeypatch, preset, overrides, tok
             torch.from_numpy(np.asarray(ref[n])) if n in ref else None for n, _ in module.named_parameters()])
         # One attention backward and one native route backward; the only
         # route launch is the module forward's (the backward reuses its r).
-        assert calls.count("_attention_backward") + calls.count("_attention_backward_dense") == 1, calls
+        outer = ("_attention_backward", "_attention_backward_dense", "attention_gradients_rows")
+        assert sum(calls.count(name) for name in outer) == 1, calls
         assert calls.count("_route_backward") + calls.count("_route_backward_rows") == 1, calls
         assert calls.count("_route_forward") == 1, calls
         names = ["x"] + [n for n, _ in module.named_parameters()]
