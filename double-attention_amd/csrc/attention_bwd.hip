@@ -56,6 +56,8 @@ struct BwdParams {
   float* dq;
   float* dk;
   float* dv;            // [B][Tk][D]
+  float* dv_sum;        // [D] column sums of dv over every sequence and key, or nullptr
+  int v_dtype;          // kF16 or kBF16: the element type of dout
   float* dgamma;        // [S] d loss / d scales[s] (of the logs with scales_log)
   int64_t q_sb, q_st, q_ms;
   int64_t k_sb, k_st, k_ms;
@@ -251,6 +253,8 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
     for (int i = tid; i < k_rows * D / 4; i += 256)
       reinterpret_cast<f32x4*>(p.dv + (static_cast<int64_t>(b) * p.Tk + t0) * D)[i] = z;
   if (bs == 0 && tile == 0 && tid < p.S) p.dgamma[tid] = 0.f;
+  if (p.dv_sum && bs == 0 && tile == 0)
+    for (int i = tid; i < D; i += 256) p.dv_sum[i] = 0.f;
 }
 
 template <typename TQ, int RP>
@@ -264,6 +268,22 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
   const int bs = static_cast<int>(blockIdx.y);
   const int q0 = static_cast<int>(blockIdx.x) * kQTile;
   const float sc = bwd_gamma(p, bs % p.S) * kLog2e;
+  // Summed over the keys, dV = P^T dO gives the column sums of dO over the
+  // queries (every row of P sums to one).  With dv_sum set this workgroup
+  // adds those of its 32 rows of dO: one column pair per thread (D <= 512),
+  // each row a coalesced pass.  The loads are issued here and summed after
+  // the key loop, and the adds to the D shared addresses come at the end,
+  // when the workgroups of a causal staircase finish at different times.
+  // Rows past the sequence re-read its last row and are dropped.
+  const int tid0 = static_cast<int>(threadIdx.x);
+  const bool col_sums = p.dv_sum != nullptr && tid0 < p.D / 2;
+  const int last_row = min(kQTile, p.T - q0) - 1;
+  uint32_t dorow[kQTile];
+  if (col_sums) {
+    const uint32_t* rows = static_cast<const uint32_t*>(p.dout) + (static_cast<int64_t>(bs) * p.T + q0) * (p.D / 2);
+#pragma unroll
+    for (int r = 0; r < kQTile; ++r) dorow[r] = rows[static_cast<int64_t>(min(r, last_row)) * (p.D / 2) + tid0];
+  }
   const TQ* qb = static_cast<const TQ*>(p.q) + q_rows0(p, bs);
   const TQ* kbase = static_cast<const TQ*>(p.k) + k_rows0(p, bs);
   q8 qf[2][KS];
@@ -333,6 +353,22 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
       if (part[w][0][tid] != -INFINITY) ll += part[w][1][tid] * exp2f(part[w][0][tid] - mm);
     const int q = q0 + tid;
     if (q < p.T) p.lse2[static_cast<int64_t>(bs) * p.T + q] = mm + log2f(ll);
+  }
+  if (col_sums) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int r = 0; r < kQTile; ++r) {
+      const uint32_t x = r <= last_row ? dorow[r] : 0u;
+      if (p.v_dtype == kBF16) {
+        s0 += __uint_as_float(x << 16);
+        s1 += __uint_as_float(x & 0xffff0000u);
+      } else {
+        s0 += static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x)));
+        s1 += static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x >> 16)));
+      }
+    }
+    unsafeAtomicAdd(p.dv_sum + 2 * tid0, s0);
+    unsafeAtomicAdd(p.dv_sum + 2 * tid0 + 1, s1);
   }
 }
 
@@ -686,7 +722,7 @@ void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace
   const int64_t Tkp = round_up(a.Tk, kKeyPad);
   BwdParams p{a.q, a.k, a.vt ? static_cast<const void*>(ws + l.vrows) : a.v, a.out, a.dout, ws + l.qt, ws + l.kt, ws + l.doutt,
               reinterpret_cast<float*>(ws + l.lse2), reinterpret_cast<float*>(ws + l.dvec), a.scales,
-              a.dq, a.dk, a.dv, a.dgamma,
+              a.dq, a.dk, a.dv, a.dv_sum, a.v_dtype, a.dgamma,
               a.q_stride_b, a.q_stride_t, a.q_map_stride, a.k_stride_b, a.k_stride_t, a.k_map_stride,
               a.map_repeat, a.vt ? Tkp * a.D : static_cast<int64_t>(a.Tk) * a.D, a.vt, a.vt_stride_b, a.vt_dtype,
               ws + l.vrows, a.scales_dtype, a.scales_log ? 1 : 0, a.log_lo, a.log_hi, a.scale_mult,

@@ -395,7 +395,8 @@ int da_routed_attention_backward_ex(const da_attention_backward_args* args, da_s
   const void* f32[] = {x.grad_query, x.grad_key, x.grad_value};
   for (const void* ptr : f32)
     if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: gradients must be 16-byte aligned");
-  if (!aligned(x.scales, x.scales_dtype == DA_F32 ? 4 : 2) || !aligned(x.grad_scales, 4))
+  if (!aligned(x.scales, x.scales_dtype == DA_F32 ? 4 : 2) || !aligned(x.grad_scales, 4) ||
+      !aligned(x.grad_value_sum, 4))
     return fail(DA_ERR_ALIGNMENT, "attention backward: scales must be aligned to their element size");
   if (!aligned(x.workspace, 256)) return fail(DA_ERR_ALIGNMENT, "attention backward: workspace must be 256-byte aligned");
   const int64_t need =
@@ -429,6 +430,7 @@ int da_routed_attention_backward_ex(const da_attention_backward_args* args, da_s
   a.dq = x.grad_query;
   a.dk = x.grad_key;
   a.dv = x.grad_value;
+  a.dv_sum = x.grad_value_sum;
   a.dgamma = x.grad_scales;
   a.B = static_cast<int>(batch);
   a.S = static_cast<int>(maps);

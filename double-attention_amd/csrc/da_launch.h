@@ -106,6 +106,7 @@ struct AttentionBwdArgs {
   float* dq;
   float* dk;
   float* dv;             // [B][Tk][D]
+  float* dv_sum;         // [D] column sums of dv, or nullptr
   float* dgamma;         // [S] gradient at scales[s] (at the log with scales_log)
   int B, S, T, RP, D;
   int Tk;                // keys per sequence (== T when causal)

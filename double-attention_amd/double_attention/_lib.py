@@ -135,6 +135,7 @@ class AttentionBackwardArgs(ctypes.Structure):
         ("grad_key", _vp),
         ("grad_value", _vp),
         ("grad_scales", _vp),
+        ("grad_value_sum", _vp),
     ]
 
 

@@ -464,6 +464,7 @@ def _attention_backward_ex(
     grad_value: Tensor,
     grad_scales: Tensor,
     what: str,
+    grad_value_sum: Tensor | None = None,
 ) -> None:
     """One ``da_routed_attention_backward_ex`` call.
 
@@ -510,6 +511,7 @@ def _attention_backward_ex(
     args.grad_key = grad_key
     args.grad_value = grad_value.data_ptr()
     args.grad_scales = grad_scales.data_ptr()
+    args.grad_value_sum = _ptr(grad_value_sum)
     _lib.check(lib.da_routed_attention_backward_ex(ctypes.byref(args), _stream(device)), what)
 
 
@@ -1133,7 +1135,7 @@ def rows_backward_supported(
 def attention_gradients_rows(
     routed: Tensor, branches: int, maps: int, vt: Tensor, log_scales: Tensor, out: Tensor, grad: Tensor,
     causal: bool,
-) -> tuple[Tensor, Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Outer-attention gradients at the routed rows (the backward of
     ``_attention_forward_rows``) on the key-tile kernels, for shapes
     ``rows_backward_supported`` accepts.
@@ -1141,8 +1143,9 @@ def attention_gradients_rows(
     ``routed`` ``[B, T, 2, H, R]`` (16-bit), ``vt`` the forward's V^T tiles
     ``[B, Tp/32, D, 32]`` (read as they are: the prep kernel turns them into
     value rows), ``out`` the fp32 per-map outputs ``[B, S, T, D]`` and
-    ``grad`` their gradient.  Returns ``(d_routed, d_value, d_log_scales)``,
-    all fp32:
+    ``grad`` their gradient.  Returns ``(d_routed, d_value, d_log_scales,
+    d_value_sums)``, all fp32 (the last the column sums of ``d_value``, the
+    gradient of the value projection's bias):
     ``d_routed`` has the routed rows' shape (the score-map assembly's
     backward, maps sharing rows summed), ``d_log_scales`` the gradient at
     ``log_scales`` through the kernels' clamp.
@@ -1165,15 +1168,16 @@ def attention_gradients_rows(
     d_routed = torch.empty(batch, length, 2, branches, routing_dim, dtype=torch.float32, device=device)
     d_value = torch.empty(batch, length, model_dim, dtype=torch.float32, device=device)
     d_scales = torch.empty(maps, dtype=torch.float32, device=device)
+    d_sums = torch.empty(model_dim, dtype=torch.float32, device=device)
     row = (length * 2 * width, 2 * width, map_stride)
     q_ptr, k_off = routed.data_ptr(), width * routed.element_size()
     dq_ptr, dk_off = d_routed.data_ptr(), width * 4
     _attention_backward_ex(
         (q_ptr, *row), (q_ptr + k_off, *row), repeat, v, o, go, scales, float(mult), LOG_SCALE_RANGE,
         (batch, maps, length, length, score_dim, model_dim), causal, routed.dtype,
-        dq_ptr, dq_ptr + dk_off, d_value, d_scales, "routed_attention_hip backward",
+        dq_ptr, dq_ptr + dk_off, d_value, d_scales, "routed_attention_hip backward", d_sums,
     )
-    return d_routed, d_value, d_scales
+    return d_routed, d_value, d_scales, d_sums
 
 
 def _native_backward_supported(query: Tensor, value: Tensor) -> bool:

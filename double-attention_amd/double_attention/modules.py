@@ -581,11 +581,12 @@ class _HipModuleFunction(torch.autograd.Function):
         # Outer attention.  dq and dk stay fp32 (no rounding, no cast): the
         # route backward takes fp32 gradient rows.
         log_scales = named["log_score_scales"]
+        d_value_sums = None
         if hip_ops.rows_backward_supported(batch, length, branches, maps, routing_dim, model_dim):
             # The key-tile kernels read the score maps as views of the routed
             # rows and write their gradients into [B, T, 2, H, R] (the
             # assembly's backward), with the temperature clamp's backward.
-            d_rows_qk, d_value, d_log_scales = hip_ops.attention_gradients_rows(
+            d_rows_qk, d_value, d_log_scales, d_value_sums = hip_ops.attention_gradients_rows(
                 routed.view(batch, length, 2, branches, routing_dim), branches, maps, vt, log_scales,
                 map_output, d_maps, cfg.causal,
             )
@@ -666,7 +667,10 @@ class _HipModuleFunction(torch.autograd.Function):
         if wants("value.weight"):
             grads["value.weight"] = _mm_tn_f32(d_v, x2d, named["value.weight"].dtype)
         if wants("value.bias"):
-            grads["value.bias"] = hip_ops.column_sums(d_v, named["value.bias"].dtype)
+            grads["value.bias"] = (
+                d_value_sums.to(named["value.bias"].dtype) if d_value_sums is not None
+                else hip_ops.column_sums(d_v, named["value.bias"].dtype)
+            )
         tail = [
             grads[name].to(named[name].dtype).reshape(named[name].shape) if name in grads else None
             for name in ctx.param_names

@@ -324,7 +324,9 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
  * elements, [padded key_length / 32][value_dim][32], 16-bit of
  * value_t_dtype, converted to v_dtype; padding tokens finite, as
  * da_routed_attention requires).  out has out_dtype (DA_F32, DA_F16 or
- * DA_BF16) whatever v_dtype is.  flags: DA_ATTN_CAUSAL and
+ * DA_BF16) whatever v_dtype is.  grad_value_sum (optional, [value_dim]
+ * fp32) receives the column sums of grad_value over every sequence and key:
+ * the gradient of a bias added to the values.  flags: DA_ATTN_CAUSAL and
  * DA_ATTN_SCALES_ARE_LOG.  Everything else is as for
  * da_routed_attention_backward (whose workspace size serves both).
  */
@@ -354,6 +356,7 @@ typedef struct da_attention_backward_args {
   float* grad_key;
   float* grad_value;        /* [batch, key_length, value_dim] */
   float* grad_scales;       /* [maps] */
+  float* grad_value_sum;    /* [value_dim] or NULL */
 } da_attention_backward_args;
 
 int da_routed_attention_backward_ex(const da_attention_backward_args* args, da_stream_t stream);

@@ -605,10 +605,13 @@ def test_attention_on_routed_rows(layout) -> None:
     expected_out = oracle.routed_attention(sq, sk, v64, gamma, causal)
     assert_parity(out, expected_out, label=label + " out")
 
-    d_routed, d_value, d_logs = da.hip_ops.attention_gradients_rows(
+    d_routed, d_value, d_logs, d_sums = da.hip_ops.attention_gradients_rows(
         routed, branches, maps, vt, log_scales, out, grad, causal
     )
     dq, dk, dv, dgamma = oracle.routed_attention_backward(sq, sk, v64, gamma, np32(grad).astype(np.float64), causal)
+    # The value bias's gradient: column sums of dV over every sequence and key.
+    sums = dv.sum(axis=(0, 1))
+    assert_parity(d_sums, sums, 1e-2, max(2e-2 * float(np.abs(sums).max()), 1e-6), label + " dvalue column sums")
     drq, drk = oracle.assemble_score_maps_backward(dq, dk, branches)
     expected_rows = np.stack((drq.transpose(0, 2, 1, 3), drk.transpose(0, 2, 1, 3)), axis=2)
     inside = (log64 >= lo) & (log64 <= hi)
