@@ -568,14 +568,16 @@ class _HipModuleFunction(torch.autograd.Function):
             if module.map_mix_logits is None:
                 d_maps = d_mixed.view(batch, 1, length, model_dim)
             else:
-                d32 = d_mixed.float().view(batch, 1, length, model_dim)
                 if wants("map_mix_logits"):
                     # fp32 throughout: the per-map sums dY . O_s are large and
-                    # nearly equal, and the softmax backward differences them.
-                    per_map = (map_output.float() * d32).sum(dim=(0, 2, 3))
+                    # nearly equal, and the softmax backward differences them
+                    # (dY enters the fp32 product as its exact fp32 value).
+                    per_map = (map_output * d_mixed.view(batch, 1, length, model_dim)).sum(dim=(0, 2, 3))
                     alpha = torch.softmax(module.map_mix_logits.detach().float(), dim=0)
                     grads["map_mix_logits"] = alpha * (per_map - (alpha * per_map).sum())
-                d_maps = (d32 * factors[None, :, None, None]).to(dtype)
+                # bf16 x bf16 products are exact in the fp32 the op computes
+                # in, so this rounds alpha_s dY once, as the fp32 product would.
+                d_maps = d_mixed.view(batch, 1, length, model_dim) * factors.to(dtype).view(1, maps, 1, 1)
         else:
             d_maps = d_mixed.view(batch, length, maps, model_dim).transpose(1, 2)
         # Outer attention.  dq and dk stay fp32 (no rounding, no cast): the
