@@ -57,6 +57,11 @@ struct BwdParams {
   float* dk;
   float* dv;            // [B][Tk][D]
   float* dv_sum;        // [D] column sums of dv over every sequence and key, or nullptr
+  // With ds_out set the main kernel writes gamma dS (score dtype, rounded
+  // once) as rows [BS][T] of ds_ld elements, keys 0 .. Tkp-1, instead of
+  // forming dQ = gamma dS K with atomics (dq is then not touched).
+  void* ds_out;
+  int64_t ds_ld;
   int v_dtype;          // kF16 or kBF16: the element type of dout
   float* dgamma;        // [S] d loss / d scales[s] (of the logs with scales_log)
   int64_t q_sb, q_st, q_ms;
@@ -240,7 +245,7 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
 
   // Zero the accumulated gradients of this tile's query and key rows.
   const f32x4 z = zero4();
-  const int q_rows = max(0, min(kQTile, p.T - t0)), k_rows = max(0, min(kQTile, p.Tk - t0));
+  const int q_rows = p.ds_out ? 0 : max(0, min(kQTile, p.T - t0)), k_rows = max(0, min(kQTile, p.Tk - t0));
   for (int i = tid; i < q_rows * RP / 4; i += 256) {
     const int r = i / (RP / 4), c4 = i - r * (RP / 4);
     reinterpret_cast<f32x4*>(p.dq + q0 + (t0 + r) * p.q_st)[c4] = z;
@@ -560,6 +565,10 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
         dgamma += ds * sv[cb][i];
         pa[cb * 4 + i] = static_cast<TV>(pr);
         dsa[cb * 4 + i] = static_cast<TQ>(ds);
+        // gamma dS for ds_out, rounded once (the LDS tile is free: every
+        // wave passed this step's first barrier after reading it last).
+        if (p.ds_out)
+          *reinterpret_cast<TQ*>(lds + OFF_DS + ql * kDsPitch + (wave * 16 + c) * 2) = static_cast<TQ>(ds * gamma);
       }
     // dV += P^T dO and dK += dS^T Q; B rows read the same query order.  The
     // B operands go in groups of eight: eight LDS reads, then eight MFMAs,
@@ -594,12 +603,22 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
       __builtin_amdgcn_sched_group_barrier(0x100, 2 * GK, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, GK, 0);
     }
-    // dS with the query as the row, for dQ.
+    // dS with the query as the row, for dQ (ds_out: written above).
+    if (!p.ds_out) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      *reinterpret_cast<TQ*>(lds + OFF_DS + ((e >> 2) * 16 + 4 * g + (e & 3)) * kDsPitch + (wave * 16 + c) * 2) = dsa[e];
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<TQ*>(lds + OFF_DS + ((e >> 2) * 16 + 4 * g + (e & 3)) * kDsPitch + (wave * 16 + c) * 2) = dsa[e];
+    }
     __syncthreads();   // dS of all four waves is in LDS; the staged tiles are free
     if (qt + 1 < qt_end) issue(qt + 1);
+    if (p.ds_out) {
+      // 32 query rows x 64 keys: one 16-byte chunk per thread, eight per row.
+      const int row = tid >> 3, ch = tid & 7;
+      if (q0 + row < p.T)
+        store16B(static_cast<TQ*>(p.ds_out) + (static_cast<int64_t>(bs) * p.T + q0 + row) * p.ds_ld + k0 + ch * 8,
+                 *reinterpret_cast<const u32x4*>(lds + OFF_DS + row * kDsPitch + ch * 16));
+      continue;
+    }
 
     // dQ = dS K over the 64 keys, this wave's 16-column blocks.
     q8 dsf[2][2];
@@ -722,7 +741,7 @@ void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace
   const int64_t Tkp = round_up(a.Tk, kKeyPad);
   BwdParams p{a.q, a.k, a.vt ? static_cast<const void*>(ws + l.vrows) : a.v, a.out, a.dout, ws + l.qt, ws + l.kt, ws + l.doutt,
               reinterpret_cast<float*>(ws + l.lse2), reinterpret_cast<float*>(ws + l.dvec), a.scales,
-              a.dq, a.dk, a.dv, a.dv_sum, a.v_dtype, a.dgamma,
+              a.dq, a.dk, a.dv, a.dv_sum, a.ds_out, a.ds_ld, a.v_dtype, a.dgamma,
               a.q_stride_b, a.q_stride_t, a.q_map_stride, a.k_stride_b, a.k_stride_t, a.k_map_stride,
               a.map_repeat, a.vt ? Tkp * a.D : static_cast<int64_t>(a.Tk) * a.D, a.vt, a.vt_stride_b, a.vt_dtype,
               ws + l.vrows, a.scales_dtype, a.scales_log ? 1 : 0, a.log_lo, a.log_hi, a.scale_mult,

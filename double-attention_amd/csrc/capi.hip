@@ -384,15 +384,21 @@ int da_routed_attention_backward_ex(const da_attention_backward_args* args, da_s
     return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: stride_t must be >= score_dim");
   if (batch == 0 || length == 0) return ok();
   if (key_length == 0) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: queries need at least one key");
+  if (x.grad_scores && (x.grad_scores_ld < da::round_up(key_length, da::kKeyPad) || x.grad_scores_ld % 8 ||
+                        !aligned(x.grad_scores, 16)))
+    return fail(DA_ERR_ALIGNMENT, "attention backward: grad_scores needs a 16-byte aligned buffer and a row pitch "
+                "that is a multiple of 8 of at least the padded key count");
   const void* values = x.value ? x.value : x.value_t;
-  const void* ptrs[] = {x.query, x.key, values, x.out, x.grad_out, x.scales, x.workspace, x.grad_query,
+  // grad_scores replaces grad_query.
+  const void* dq = x.grad_scores ? x.grad_scores : static_cast<const void*>(x.grad_query);
+  const void* ptrs[] = {x.query, x.key, values, x.out, x.grad_out, x.scales, x.workspace, dq,
                         x.grad_key, x.grad_value, x.grad_scales};
   for (const void* ptr : ptrs)
     if (!ptr) return fail(DA_ERR_INVALID_ARGUMENT, "attention backward: null pointer");
   const void* halves[] = {x.query, x.key, values, x.out, x.grad_out};
   for (const void* ptr : halves)
     if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: half-precision tensors must be 16-byte aligned");
-  const void* f32[] = {x.grad_query, x.grad_key, x.grad_value};
+  const void* f32[] = {dq, x.grad_key, x.grad_value};
   for (const void* ptr : f32)
     if (!aligned(ptr, 16)) return fail(DA_ERR_ALIGNMENT, "attention backward: gradients must be 16-byte aligned");
   if (!aligned(x.scales, x.scales_dtype == DA_F32 ? 4 : 2) || !aligned(x.grad_scales, 4) ||
@@ -431,6 +437,8 @@ int da_routed_attention_backward_ex(const da_attention_backward_args* args, da_s
   a.dk = x.grad_key;
   a.dv = x.grad_value;
   a.dv_sum = x.grad_value_sum;
+  a.ds_out = x.grad_scores;
+  a.ds_ld = x.grad_scores_ld;
   a.dgamma = x.grad_scales;
   a.B = static_cast<int>(batch);
   a.S = static_cast<int>(maps);

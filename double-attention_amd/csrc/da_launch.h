@@ -107,6 +107,8 @@ struct AttentionBwdArgs {
   float* dk;
   float* dv;             // [B][Tk][D]
   float* dv_sum;         // [D] column sums of dv, or nullptr
+  void* ds_out;          // gamma dS rows [B*S*T][ds_ld] (qk_dtype) instead of dq, or nullptr
+  int64_t ds_ld;
   float* dgamma;         // [S] gradient at scales[s] (at the log with scales_log)
   int B, S, T, RP, D;
   int Tk;                // keys per sequence (== T when causal)

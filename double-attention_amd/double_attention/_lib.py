@@ -136,6 +136,8 @@ class AttentionBackwardArgs(ctypes.Structure):
         ("grad_value", _vp),
         ("grad_scales", _vp),
         ("grad_value_sum", _vp),
+        ("grad_scores", _vp),
+        ("grad_scores_ld", _i64),
     ]
 
 

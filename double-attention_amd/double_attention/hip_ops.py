@@ -465,6 +465,7 @@ def _attention_backward_ex(
     grad_scales: Tensor,
     what: str,
     grad_value_sum: Tensor | None = None,
+    grad_scores: Tensor | None = None,
 ) -> None:
     """One ``da_routed_attention_backward_ex`` call.
 
@@ -474,7 +475,8 @@ def _attention_backward_ex(
     per-sequence stride, the dtype the kernels take them in).  ``shape`` is
     (batch, maps, length, key_length, score_dim, value_dim).  ``log_range``
     set: ``scales`` holds logs clamped to it, and ``grad_scales`` receives the
-    gradient at the logs.
+    gradient at the logs.  ``grad_scores`` (a 2-D view of rows, score dtype):
+    the kernels write scale * dS there instead of the query gradient.
     """
 
     batch, maps, length, key_length, score_dim, value_dim = shape
@@ -512,6 +514,9 @@ def _attention_backward_ex(
     args.grad_value = grad_value.data_ptr()
     args.grad_scales = grad_scales.data_ptr()
     args.grad_value_sum = _ptr(grad_value_sum)
+    if grad_scores is not None:
+        args.grad_scores = grad_scores.data_ptr()
+        args.grad_scores_ld = grad_scores.stride(0)
     _lib.check(lib.da_routed_attention_backward_ex(ctypes.byref(args), _stream(device)), what)
 
 
@@ -580,16 +585,20 @@ def _route_backward(
     else:
         values = _aligned(dictionary_value.detach().t().to(v_type))
     out = _aligned(r)
-    du = torch.empty(n, routing_dim, dtype=torch.float32, device=device)
     dkt = torch.empty(atoms, routing_dim, dtype=torch.float32, device=device)
     dvt = torch.empty(atoms, routing_dim, dtype=torch.float32, device=device)
     dbeta = torch.empty(1, dtype=torch.float32, device=device)
+    # Every row meets every atom: the kernels write beta dS (the gradient at
+    # the logits, rounded once) and one GEMM forms du = beta dS Dk, instead
+    # of one fp32 atomic add per row element and 64-atom tile.
+    scores = torch.empty(n, _round_up(atoms, ATOM_PAD), dtype=qk_type, device=device)
     _attention_backward_ex(
         (u16.data_ptr(), n * routing_dim, routing_dim, 0), (keys.data_ptr(), atoms * routing_dim, routing_dim, 0), 1,
         values, out, go, beta_t, 1.0, LOG_BETA_RANGE if beta_is_log else None,
         (1, 1, n, atoms, routing_dim, routing_dim), False, qk_type,
-        du.data_ptr(), dkt.data_ptr(), dvt, dbeta, "dictionary_route_hip backward",
+        0, dkt.data_ptr(), dvt, dbeta, "dictionary_route_hip backward", grad_scores=scores,
     )
+    du = _mm_f32(scores[:, :atoms], keys)
     dx = _normalize_backward(rows, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
     return (
         dx.reshape(x.shape),

@@ -326,7 +326,13 @@ int da_routed_attention_backward(const void* query, const void* key, const void*
  * da_routed_attention requires).  out has out_dtype (DA_F32, DA_F16 or
  * DA_BF16) whatever v_dtype is.  grad_value_sum (optional, [value_dim]
  * fp32) receives the column sums of grad_value over every sequence and key:
- * the gradient of a bias added to the values.  flags: DA_ATTN_CAUSAL and
+ * the gradient of a bias added to the values.  With grad_scores set
+ * (qk_dtype, rows of grad_scores_ld >= key_length padded to a multiple of 64,
+ * 16-byte aligned) the gradient at the scaled scores, scale * dS, is written
+ * there as [batch*maps*length] rows (padding keys zero) instead of
+ * grad_query = scale * dS K, which is then not touched (may be NULL): a
+ * caller with few keys per query (the dictionary route) forms it with one
+ * GEMM instead of one atomic add per key tile.  flags: DA_ATTN_CAUSAL and
  * DA_ATTN_SCALES_ARE_LOG.  Everything else is as for
  * da_routed_attention_backward (whose workspace size serves both).
  */
@@ -357,6 +363,8 @@ typedef struct da_attention_backward_args {
   float* grad_value;        /* [batch, key_length, value_dim] */
   float* grad_scales;       /* [maps] */
   float* grad_value_sum;    /* [value_dim] or NULL */
+  void* grad_scores;        /* [batch*maps*length, grad_scores_ld], qk_dtype, or NULL */
+  int64_t grad_scores_ld;
 } da_attention_backward_args;
 
 int da_routed_attention_backward_ex(const da_attention_backward_args* args, da_stream_t stream);

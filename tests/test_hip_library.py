@@ -239,6 +239,11 @@ def test_strided_attention_backward_rejects_bad_arguments() -> None:
         (dict(value=None, value_t=f, value_t_dtype=lib.DA_F32), -1, "V^T tiles"),
         (dict(value=None, value_t=f, value_t_dtype=lib.DA_F16, value_t_stride_b=12), -1, "V^T tiles"),
         (dict(value=None, value_t=None, value_t_dtype=lib.DA_F16), -1, "null pointer"),
+        # Rows of scale * dS instead of the query gradient: padded key count, 16 bytes.
+        (dict(grad_scores=f, grad_scores_ld=504), -3, "grad_scores"),
+        (dict(grad_scores=f, grad_scores_ld=516), -3, "grad_scores"),
+        (dict(grad_scores=f + 8, grad_scores_ld=512), -3, "grad_scores"),
+        (dict(grad_scores=f, grad_scores_ld=512, grad_key=f + 1028), -3, "gradients"),
         (dict(grad_key=f + 1028), -3, "gradients"),
         (dict(scales=f + 1, scales_dtype=lib.DA_BF16), -3, "element size"),
         (dict(workspace_bytes=need - 1), -5, "workspace of"),
