@@ -124,10 +124,32 @@ class RouteDictionary(NamedTuple):
     unit: bool = False   # key atoms have L2 norm <= 1 (a normalized bank)
 
 
+def _version_of(t: Tensor) -> int | None:
+    # Inference tensors keep no version counter.
+    return None if t.is_inference() else t._version
+
+
 def _tag(key: Tensor, value: Tensor, layout: RouteDictionary) -> tuple[Tensor, Tensor]:
-    key._da_route_layout = layout  # type: ignore[attr-defined]
-    value._da_route_layout = layout  # type: ignore[attr-defined]
+    """Attach ``layout`` to the ``[R, M]`` pair it was built from, with the
+    pair's version counters: an in-place change of either (an optimizer
+    step) makes the layout stale, and ``_tagged_layout`` then ignores it."""
+
+    versions = (_version_of(key), _version_of(value))
+    for t in (key, value):
+        t._da_route_layout = layout  # type: ignore[attr-defined]
+        t._da_route_versions = versions  # type: ignore[attr-defined]
     return key, value
+
+
+def _tagged_layout(key: Tensor, value: Tensor) -> RouteDictionary | None:
+    """The route layout attached to this key/value pair, if still current."""
+
+    layout = getattr(key, "_da_route_layout", None)
+    if layout is None or getattr(value, "_da_route_layout", None) is not layout:
+        return None
+    if getattr(key, "_da_route_versions", None) != (_version_of(key), _version_of(value)):
+        return None
+    return layout
 
 
 def route_key_dtype(normalize_input: bool, dtype: torch.dtype) -> torch.dtype:
@@ -249,14 +271,15 @@ def _untile_value(value: Tensor) -> Tensor:
 
 
 def route_layout(dictionary_key: Tensor, dictionary_value: Tensor, key_dtype: torch.dtype) -> RouteDictionary:
-    """Route layouts for a normalized ``[R, M]`` key/value pair (copy-free when tagged)."""
+    """Route layouts for a normalized ``[R, M]`` key/value pair.
 
-    layout = getattr(dictionary_key, "_da_route_layout", None)
-    if (
-        layout is not None
-        and getattr(dictionary_value, "_da_route_layout", None) is layout
-        and layout.key_t.dtype == key_dtype
-    ):
+    Copy-free when the pair carries current layouts (a bank normalized into
+    them, or a pair laid out before and unchanged since): the blocks of a
+    stack that share one normalized bank lay it out once per forward.
+    """
+
+    layout = _tagged_layout(dictionary_key, dictionary_value)
+    if layout is not None and layout.key_t.dtype == key_dtype:
         return layout
     if dictionary_key.ndim != 2 or dictionary_value.shape != dictionary_key.shape:
         raise ValueError("dictionary key and value must both be [routing_dim, atoms]")
@@ -267,7 +290,13 @@ def route_layout(dictionary_key: Tensor, dictionary_value: Tensor, key_dtype: to
     key_t[:atoms].copy_(dictionary_key.detach().t())
     value[:, :atoms].copy_(dictionary_value.detach())
     tiles = value.view(routing_dim, padded // 32, 32).permute(1, 0, 2).contiguous()
-    return RouteDictionary(key_t, tiles, atoms)
+    layout = RouteDictionary(key_t, tiles, atoms)
+    # Parameters are left untagged (writes through .data, which the version
+    # counter does not see, would leave their layout stale), and so are
+    # inference tensors, which keep no version counter.
+    if not any((t.is_leaf and t.requires_grad) or t.is_inference() for t in (dictionary_key, dictionary_value)):
+        _tag(dictionary_key, dictionary_value, layout)
+    return layout
 
 
 # --------------------------------------------------------------------------
@@ -579,8 +608,8 @@ def _route_backward(
     # The values as the route layout's 32-atom tiles when the bank carries
     # them (the prep kernel turns them into v_type rows), else as rows; r in
     # its own dtype (it only enters rowsum(dr . r)).
-    layout = getattr(dictionary_key, "_da_route_layout", None)
-    if layout is not None and getattr(dictionary_value, "_da_route_layout", None) is layout and layout.atoms == atoms:
+    layout = _tagged_layout(dictionary_key, dictionary_value)
+    if layout is not None and layout.atoms == atoms:
         values: Tensor | tuple[Tensor, int, torch.dtype] = (layout.value, 0, v_type)
     else:
         values = _aligned(dictionary_value.detach().t().to(v_type))
@@ -907,7 +936,7 @@ def dictionary_route_hip(
         raise ValueError("standardized_logit_scale must be positive when provided")
     _require_cuda(input, dictionary_key, dictionary_value)
     _half_code(input.dtype)
-    tagged = getattr(dictionary_key, "_da_route_layout", None) is not None
+    tagged = _tagged_layout(dictionary_key, dictionary_value) is not None
     if not tagged and (dictionary_key.dtype != input.dtype or dictionary_value.dtype != input.dtype):
         raise ValueError("input and dictionaries must have one matching dtype")
     needs_grad = torch.is_grad_enabled() and any(

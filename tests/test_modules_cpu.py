@@ -334,3 +334,31 @@ def test_module_operands_follow_parameter_updates() -> None:
     third = hip_ops._module_operands(module, torch.bfloat16)
     assert third is not second and torch.count_nonzero(third[1]) == 0
     assert hip_ops._module_operands(module, torch.float16)[0].dtype == torch.float16
+
+
+def test_route_layout_is_reused_while_the_bank_is_unchanged() -> None:
+    # The blocks of a stack share one normalized bank: the first lays it out,
+    # the others reuse that layout; an in-place change (version bump) makes it
+    # stale, and parameters are never tagged (writes through .data bypass the
+    # version counter).  The layout itself holds the atom-major keys and the
+    # 32-atom value tiles of the same numbers.
+    from double_attention import hip_ops
+
+    g = torch.Generator().manual_seed(0)
+    key = torch.randn(64, 40, generator=g)
+    value = torch.randn(64, 40, generator=g)
+    first = hip_ops.route_layout(key, value, torch.float16)
+    assert hip_ops.route_layout(key, value, torch.float16) is first
+    assert torch.equal(first.key_t[:40].float(), key.t().half().float())
+    assert torch.count_nonzero(first.key_t[40:]) == 0 and first.key_t.shape == (64, 64)
+    assert torch.equal(hip_ops._untile_value(first.value)[:, :40].float(), value.half().float())
+    # Another key dtype lays it out again.
+    assert hip_ops.route_layout(key, value, torch.bfloat16) is not first
+    again = hip_ops.route_layout(key, value, torch.float16)
+    value.mul_(2.0)
+    fresh = hip_ops.route_layout(key, value, torch.float16)
+    assert fresh is not again
+    assert torch.equal(hip_ops._untile_value(fresh.value)[:, :40].float(), value.half().float())
+    param = torch.nn.Parameter(torch.randn(64, 40, generator=g))
+    a = hip_ops.route_layout(param, param, torch.float16)
+    assert hip_ops.route_layout(param, param, torch.float16) is not a
