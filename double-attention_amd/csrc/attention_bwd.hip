@@ -666,22 +666,28 @@ namespace {
 
 // Query tiles per main-kernel workgroup: the longest run (at most 16 tiles
 // for causal attention, 32 without a mask) that still gives at least 256
-// non-empty workgroups (one per CU).  Every workgroup ends with 64 x (RP + D)
-// atomic adds of its dK and dV rows, so shorter runs than that cost more in
-// atomics than they gain in balance.  Measured: the route backward at 16384
-// rows x 1024 atoms 333 us with runs of at most 16 tiles, 304 us with 32, and
-// 32768 rows x 128-wide rows 307 / 288 (64-tile runs leave 32768 rows on 256
-// workgroups: 347 us); the causal C2 outer attention 0.403 / 0.416 ms.
+// non-empty workgroups without a mask, 128 with one.  Every workgroup ends
+// with 64 x (RP + D) atomic adds of its dK and dV rows, so shorter runs than
+// that cost more in atomics than they gain in balance.  Measured: the route
+// backward at 16384 rows x 1024 atoms 333 us with runs of at most 16 tiles,
+// 304 us with 32, and 32768 rows x 128-wide rows 307 / 288 (64-tile runs
+// leave 32768 rows on 256 workgroups: 347 us); the causal C2 outer attention
+// 0.403 / 0.416 ms with runs of 16 / 32.  For causal key ranges the 256
+// workgroups left C1 (8 x 512 tokens) with runs of two query tiles: 122 us,
+// against 95 us with the 160 workgroups of four-tile runs (C4 92 / 74 us;
+// 96 workgroups at C1: 149 us); without a mask 128 workgroups were slower
+// at 8192 rows x 512 atoms (182 / 171 us).
 int pick_qchunk(int B_S, int T, int Tk, bool causal) {
   const int n_qt = (T + kQTile - 1) / kQTile;
   const int n_kt = (Tk + kKTile - 1) / kKTile;
+  const int64_t min_wgs = causal ? 128 : 256;
   for (int qc = causal ? 16 : 32; qc > 1; qc /= 2) {
     int64_t wgs = 0;
     for (int kt = 0; kt < n_kt; ++kt) {
       const int steps = causal ? n_qt - kt * (kKTile / kQTile) : n_qt;
       wgs += (steps + qc - 1) / qc;
     }
-    if (wgs * B_S >= 256) return qc;
+    if (wgs * B_S >= min_wgs) return qc;
   }
   return 1;
 }
