@@ -619,15 +619,21 @@ def _route_backward(
     dbeta = torch.empty(1, dtype=torch.float32, device=device)
     # Every row meets every atom: the kernels write beta dS (the gradient at
     # the logits, rounded once) and one GEMM forms du = beta dS Dk, instead
-    # of one fp32 atomic add per row element and 64-atom tile.
-    scores = torch.empty(n, _round_up(atoms, ATOM_PAD), dtype=qk_type, device=device)
+    # of one fp32 atomic add per row element and 64-atom tile -- while the
+    # [rows, atoms] score gradients stay within ROUTE_SCORES_MAX_BYTES.
+    padded = _round_up(atoms, ATOM_PAD)
+    use_scores = n * padded * 2 <= ROUTE_SCORES_MAX_BYTES
+    scores = torch.empty(n, padded, dtype=qk_type, device=device) if use_scores else None
+    du = None if use_scores else torch.empty(n, routing_dim, dtype=torch.float32, device=device)
     _attention_backward_ex(
         (u16.data_ptr(), n * routing_dim, routing_dim, 0), (keys.data_ptr(), atoms * routing_dim, routing_dim, 0), 1,
         values, out, go, beta_t, 1.0, LOG_BETA_RANGE if beta_is_log else None,
         (1, 1, n, atoms, routing_dim, routing_dim), False, qk_type,
-        0, dkt.data_ptr(), dvt, dbeta, "dictionary_route_hip backward", grad_scores=scores,
+        0 if use_scores else du.data_ptr(), dkt.data_ptr(), dvt, dbeta, "dictionary_route_hip backward",
+        grad_scores=scores,
     )
-    du = _mm_f32(scores[:, :atoms], keys)
+    if use_scores:
+        du = _mm_f32(scores[:, :atoms], keys)
     dx = _normalize_backward(rows, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
     return (
         dx.reshape(x.shape),
@@ -635,6 +641,11 @@ def _route_backward(
         dvt.t().to(bank_grad_dtype or dictionary_value.dtype),
         dbeta,
     )
+
+
+# Largest [rows, atoms] buffer of score gradients the route backward uses in
+# place of the query-gradient atomics (beyond it, the atomics).
+ROUTE_SCORES_MAX_BYTES = 512 << 20
 
 
 # The row kernel holds rows of up to 4096 atoms in VGPRs and takes longer

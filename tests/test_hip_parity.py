@@ -1285,6 +1285,32 @@ def test_route_backward(case, dtype) -> None:
     assert abs(db - expected[3]) <= rel_beta * max(abs(expected[3]), 1e-3) + 1e-3, (db, expected[3])
 
 
+@pytest.mark.parametrize("case", [(300, 128, 512, True, True), (257, 256, 1000, True, False)],
+                         ids=lambda c: "n{}r{}m{}".format(*c[:3]))
+def test_route_backward_without_score_rows(case, monkeypatch) -> None:
+    # Past ROUTE_SCORES_MAX_BYTES the route backward's du comes from the
+    # kernels' query-gradient atomics instead of the beta dS rows and a GEMM:
+    # the same gradients, within the two paths' roundings, and the oracle's.
+    device = _device()
+    rows, routing_dim, atoms, normalize_input, normalize_output = case
+    g = torch.Generator().manual_seed(rows + atoms)
+    x = torch.randn(rows, routing_dim, generator=g).to(device, torch.bfloat16)
+    dk = unit_columns(routing_dim, atoms, torch.bfloat16, device, rows)
+    dv = unit_columns(routing_dim, atoms, torch.bfloat16, device, rows + 1)
+    beta = torch.tensor(6.0, device=device)
+    w = torch.randn(rows, routing_dim, generator=g).to(device, torch.bfloat16)
+    args = (x, dk, dv, beta, 1e-6, normalize_input, normalize_output, w)
+    with_rows = da.hip_ops._route_backward(*args)
+    monkeypatch.setattr(da.hip_ops, "ROUTE_SCORES_MAX_BYTES", 0)
+    atomics = da.hip_ops._route_backward(*args)
+    expected = oracle.dictionary_route_backward(np32(x), np32(dk), np32(dv), 6.0, np32(w), 1e-6,
+                                                normalize_input, normalize_output)
+    for name, a, b, exp in zip(("x", "dk", "dv"), with_rows[:3], atomics[:3], expected[:3]):
+        scale = float(np.abs(exp).max())
+        assert_parity(b, exp, 1e-2, 3e-2 * scale, f"route backward atomics {case} d{name}")
+        assert_parity(a, np32(b), 1e-2, 3e-2 * scale, f"route backward rows vs atomics {case} d{name}")
+
+
 ROUTE_ROWS_CASES = [
     # (rows, routing_dim, atoms, normalize_input, normalize_output, variant kwargs)
     (300, 512, 1536, True, True, {}),
