@@ -119,69 +119,32 @@ __device__ __forceinline__ float bwd_dscale_factor(const BwdParams& p, int s) {
   return v >= p.log_lo && v <= p.log_hi ? expf(v) * p.scale_mult : 0.f;
 }
 
-// Rows [t0, t0+32) of a [len][W] tensor whose rows are `ld` elements apart,
-// transposed into a [W][32] tile at `dst` (zero for tokens >= len).  Uses
-// `lds` (32 * row_pitch(W) bytes).
-template <typename T, int W>
-__device__ __forceinline__ void transpose_tile(const T* src, int64_t ld, int t0, int len, T* dst, char* lds) {
-  constexpr int P = row_pitch(W);
-  const int tid = static_cast<int>(threadIdx.x);
-  __syncthreads();   // the previous user of `lds` is done
-  for (int ch = tid; ch < kQTile * W / 8; ch += 256) {
-    const int r = ch / (W / 8), c8 = (ch % (W / 8)) * 8;
-    u32x4 v = load16B(src + static_cast<int64_t>(min(t0 + r, len - 1)) * ld + c8);
-    if (t0 + r >= len) v = u32x4{0u, 0u, 0u, 0u};
-    store16B(lds + r * P + c8 * 2, v);
-  }
-  __syncthreads();
-  for (int ch = tid; ch < W * 4; ch += 256) {
-    const int f = ch / 4, t8 = (ch % 4) * 8;
-    uint16_t e[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) e[j] = *reinterpret_cast<const uint16_t*>(lds + (t8 + j) * P + f * 2);
-    u32x4 v;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = static_cast<uint32_t>(e[2 * j]) | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
-    store16B(dst + f * kQTile + t8, v);
-  }
-}
-
-// Tokens [32 tile, 32 tile + 32) of a V^T tile [D][32] (16-bit of dtype
-// src_dtype) written as rows [32][D] of TV at `dst` (the tile's first row).
-// Uses `lds` (32 * row_pitch(D) bytes).
-template <typename TV, int D>
-__device__ __forceinline__ void vt_tile_to_rows(const uint16_t* src, int src_dtype, TV* dst, char* lds) {
-  constexpr int P = row_pitch(D);
-  const int tid = static_cast<int>(threadIdx.x);
-  const bool same = src_dtype == (std::is_same<TV, __bf16>::value ? kBF16 : kF16);
-  __syncthreads();   // the previous user of `lds` is done
-  for (int ch = tid; ch < D * 4; ch += 256) {
-    const int f = ch / 4, t8 = (ch % 4) * 8;
-    const u32x4 v = load16B(src + f * kQTile + t8);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      uint16_t e = static_cast<uint16_t>(v[j / 2] >> (16 * (j % 2)));
-      if (!same) {
-        const float x = src_dtype == kBF16 ? __uint_as_float(static_cast<uint32_t>(e) << 16)
-                                           : static_cast<float>(__builtin_bit_cast(_Float16, e));
-        e = __builtin_bit_cast(uint16_t, static_cast<TV>(x));
-      }
-      *reinterpret_cast<uint16_t*>(lds + (t8 + j) * P + f * 2) = e;
-    }
-  }
-  __syncthreads();
-  for (int ch = tid; ch < kQTile * D / 8; ch += 256) {
-    const int r = ch / (D / 8), c8 = (ch % (D / 8)) * 8;
-    store16B(dst + static_cast<int64_t>(r) * D + c8, load16B(lds + r * P + c8 * 2));
-  }
-}
-
 }  // namespace
+
+// Eight 16-bit elements of dtype `dt` (kF16 or kBF16) as floats.
+__device__ __forceinline__ void halves_to_float(u32x4 v, int dt, float (&y)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint16_t e = static_cast<uint16_t>(v[j / 2] >> (16 * (j % 2)));
+    y[j] = dt == kBF16 ? __uint_as_float(static_cast<uint32_t>(e) << 16)
+                       : static_cast<float>(__builtin_bit_cast(_Float16, e));
+  }
+}
 
 template <typename TQ, typename TV, int RP, int D>
 __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
-  constexpr int WMAX = RP > D ? RP : D;
-  __shared__ __attribute__((aligned(16))) char lds[kQTile * row_pitch(WMAX)];
+  // One workgroup per (sequence x map, 32-token tile): the tile's Q, K and
+  // dO rows become the Q^T, K^T and dO^T tiles, the V^T tile (values given
+  // as tiles) becomes value rows, and the rows' rowsum(dO . O).  Every global
+  // load of the workgroup is issued first (one memory round trip); the Q, K
+  // and dO rows meet in LDS behind one barrier, and the V tile reuses the dO
+  // region afterwards (LDS 32 x (2 row_pitch(RP) + row_pitch(D)) bytes).
+  constexpr int PQ = row_pitch(RP), PD = row_pitch(D);
+  constexpr int NQ = kQTile * RP / 8 / 256;   // 16-byte chunks per thread of a Q or K tile
+  constexpr int ND = kQTile * D / 8 / 256;    // of a dO tile, and of a V^T tile (D rows x 4 chunks)
+  static_assert(NQ >= 1 && ND >= 1 && kQTile * RP / 8 % 256 == 0 && kQTile * D / 8 % 256 == 0, "whole chunks per thread");
+  constexpr int OFF_K = kQTile * PQ, OFF_D = 2 * kQTile * PQ;
+  __shared__ __attribute__((aligned(16))) char lds[OFF_D + kQTile * PD];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
   const int wave = uniform_wave();
@@ -192,55 +155,132 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
   const int64_t tiles = p.Tp / kQTile, ktiles = p.Tkp / kQTile;
   const int64_t rows = static_cast<int64_t>(bs) * p.T;
   const int64_t q0 = q_rows0(p, bs), k0 = k_rows0(p, bs);
+  const bool has_q = tile < tiles, has_k = tile < ktiles;   // uniform
+  const bool has_v = p.vt != nullptr && s == 0 && has_k;
 
-  // Tile conditions are uniform over the workgroup (transpose_tile syncs).
-  if (tile < tiles)
-    transpose_tile<TQ, RP>(static_cast<const TQ*>(p.q) + q0, p.q_st, t0, p.T,
-                           static_cast<TQ*>(p.qt) + (bs * tiles + tile) * RP * kQTile, lds);
-  if (tile < ktiles)
-    transpose_tile<TQ, RP>(static_cast<const TQ*>(p.k) + k0, p.k_st, t0, p.Tk,
-                           static_cast<TQ*>(p.kt) + (bs * ktiles + tile) * RP * kQTile, lds);
-  if (tile < tiles)
-    transpose_tile<TV, D>(static_cast<const TV*>(p.dout) + rows * D, D, t0, p.T,
-                          static_cast<TV*>(p.doutt) + (bs * tiles + tile) * D * kQTile, lds);
-  if (p.vt != nullptr && s == 0 && tile < ktiles)
-    vt_tile_to_rows<TV, D>(static_cast<const uint16_t*>(p.vt) + b * p.vt_sb + static_cast<int64_t>(tile) * D * kQTile,
-                           p.vt_dtype, static_cast<TV*>(p.vrows) + (static_cast<int64_t>(b) * p.Tkp + t0) * D, lds);
-
-  // rowsum(dO . O): wave w takes rows w, w+4, ...  O in fp32 (out_dtype) keeps
-  // this sum free of O's 16-bit rounding, which would otherwise reach every
-  // dS = P (dP - rowsum) of the row (and the scale gradient's sum over them).
-  const TV* dob = static_cast<const TV*>(p.dout) + rows * D;
-  for (int r = wave; r < kQTile; r += 4) {
-    const int t = t0 + r;
-    if (t >= p.T) break;
-    float acc = 0.f;
-    for (int d = lane * 8; d < D; d += 512) {
-      const typename Elem<TV>::v8 x = load8(dob + static_cast<int64_t>(t) * D + d);
-      float y[8];
-      if (p.out_dtype == kF32) {
-        const float* of = static_cast<const float*>(p.out) + (rows + t) * D + d;
-        const f32x4 y0 = *reinterpret_cast<const f32x4*>(of);
-        const f32x4 y1 = *reinterpret_cast<const f32x4*>(of + 4);
+  // 1. Loads.  Rows clamp into their tensors (a tile past the queries or keys
+  // re-reads the last row and stores nothing), so the Q, K and dO loads need
+  // no branch; O is loaded as two 16-byte halves of a chunk whatever its
+  // dtype (a 16-bit chunk reads its 16 bytes twice).
+  const TQ* qsrc = static_cast<const TQ*>(p.q) + q0;
+  const TQ* ksrc = static_cast<const TQ*>(p.k) + k0;
+  const TV* dsrc = static_cast<const TV*>(p.dout) + rows * D;
+  u32x4 qv[NQ], kv[NQ], dv8[ND], vv[ND];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          y[j] = y0[j];
-          y[4 + j] = y1[j];
+  for (int i = 0; i < NQ; ++i) {
+    const int ch = tid + 256 * i, r = ch / (RP / 8), c8 = (ch % (RP / 8)) * 8;
+    qv[i] = load16B(qsrc + static_cast<int64_t>(min(t0 + r, p.T - 1)) * p.q_st + c8);
+    kv[i] = load16B(ksrc + static_cast<int64_t>(min(t0 + r, p.Tk - 1)) * p.k_st + c8);
+  }
+#pragma unroll
+  for (int i = 0; i < ND; ++i) {
+    const int ch = tid + 256 * i, r = ch / (D / 8), c8 = (ch % (D / 8)) * 8;
+    dv8[i] = load16B(dsrc + static_cast<int64_t>(min(t0 + r, p.T - 1)) * D + c8);
+  }
+  // rowsum(dO . O): wave w takes rows w, w + 4, ..., lane l chunk l of the
+  // row (D / 8 <= 64 chunks).
+  constexpr int OC = D / 8;
+  const int es = p.out_dtype == kF32 ? 4 : 2;
+  const char* obase = static_cast<const char*>(p.out);
+  u32x4 oa[kQTile / 4], ob[kQTile / 4];
+#pragma unroll
+  for (int j = 0; j < kQTile / 4; ++j) {
+    const int t = min(t0 + wave + 4 * j, p.T - 1);
+    const char* at = obase + ((rows + t) * D + min(lane, OC - 1) * 8) * es;
+    oa[j] = load16B(at);
+    ob[j] = load16B(at + (es == 4 ? 16 : 0));
+  }
+  if (has_v) {
+    const uint16_t* vsrc = static_cast<const uint16_t*>(p.vt) + b * p.vt_sb + static_cast<int64_t>(tile) * D * kQTile;
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const int ch = tid + 256 * i, f = ch / 4, t8 = (ch % 4) * 8;
+      vv[i] = load16B(vsrc + f * kQTile + t8);
+    }
+  }
+
+  // 2. The rows into LDS (zero past the sequence).
+  const u32x4 zv = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int ch = tid + 256 * i, r = ch / (RP / 8), c8 = (ch % (RP / 8)) * 8;
+    store16B(lds + r * PQ + c8 * 2, t0 + r < p.T ? qv[i] : zv);
+    store16B(lds + OFF_K + r * PQ + c8 * 2, t0 + r < p.Tk ? kv[i] : zv);
+  }
+#pragma unroll
+  for (int i = 0; i < ND; ++i) {
+    const int ch = tid + 256 * i, r = ch / (D / 8), c8 = (ch % (D / 8)) * 8;
+    store16B(lds + OFF_D + r * PD + c8 * 2, t0 + r < p.T ? dv8[i] : zv);
+  }
+  __syncthreads();
+
+  // 3. Transposed tiles: feature f of tokens t8 .. t8+7 as one 16-byte chunk.
+  auto transposed = [&](int off, int pitch, int width, void* dst) {
+    for (int ch = tid; ch < width * 4; ch += 256) {
+      const int f = ch / 4, t8 = (ch % 4) * 8;
+      u32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = *reinterpret_cast<const uint16_t*>(lds + off + (t8 + 2 * j) * pitch + f * 2);
+        const uint32_t hi = *reinterpret_cast<const uint16_t*>(lds + off + (t8 + 2 * j + 1) * pitch + f * 2);
+        v[j] = lo | (hi << 16);
+      }
+      store16B(static_cast<uint16_t*>(dst) + f * kQTile + t8, v);
+    }
+  };
+  if (has_q) transposed(0, PQ, RP, static_cast<TQ*>(p.qt) + (bs * tiles + tile) * RP * kQTile);
+  if (has_k) transposed(OFF_K, PQ, RP, static_cast<TQ*>(p.kt) + (bs * ktiles + tile) * RP * kQTile);
+  if (has_q) transposed(OFF_D, PD, D, static_cast<TV*>(p.doutt) + (bs * tiles + tile) * D * kQTile);
+
+  // 4. rowsum(dO . O), O in fp32 (out_dtype) keeping this sum free of O's
+  // 16-bit rounding, which would otherwise reach every dS = P (dP - rowsum)
+  // of the row (and the scale gradient's sum over them).
+#pragma unroll
+  for (int j = 0; j < kQTile / 4; ++j) {
+    const int r = wave + 4 * j, t = t0 + r;
+    if (t >= p.T) break;   // uniform over the wave
+    float acc = 0.f;
+    if (lane < OC) {
+      float x[8], y[8];
+      halves_to_float(load16B(lds + OFF_D + r * PD + lane * 16), std::is_same<TV, __bf16>::value ? kBF16 : kF16, x);
+      if (es == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y[e] = __uint_as_float(oa[j][e]);
+          y[4 + e] = __uint_as_float(ob[j][e]);
         }
       } else {
-        const u32x4 yh = load16B(static_cast<const uint16_t*>(p.out) + (rows + t) * D + d);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const uint16_t e = static_cast<uint16_t>(yh[j / 2] >> (16 * (j % 2)));
-          y[j] = p.out_dtype == kBF16 ? __uint_as_float(static_cast<uint32_t>(e) << 16)
-                                      : static_cast<float>(__builtin_bit_cast(_Float16, e));
-        }
+        halves_to_float(oa[j], p.out_dtype, y);
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc += static_cast<float>(x[j]) * y[j];
+      for (int e = 0; e < 8; ++e) acc += x[e] * y[e];
     }
     acc = wave_sum(acc);
     if (lane == 0) p.dvec[rows + t] = acc;
+  }
+
+  // 5. The V^T tile transposed into value rows of TV, through the dO region.
+  if (has_v) {
+    __syncthreads();   // the dO^T stores and the sums are done with the region
+    const bool same = p.vt_dtype == (std::is_same<TV, __bf16>::value ? kBF16 : kF16);
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const int ch = tid + 256 * i, f = ch / 4, t8 = (ch % 4) * 8;
+      float y[8];
+      halves_to_float(vv[i], p.vt_dtype, y);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint16_t e = same ? static_cast<uint16_t>(vv[i][j / 2] >> (16 * (j % 2)))
+                                : __builtin_bit_cast(uint16_t, static_cast<TV>(y[j]));
+        *reinterpret_cast<uint16_t*>(lds + OFF_D + (t8 + j) * PD + f * 2) = e;
+      }
+    }
+    __syncthreads();
+    TV* vdst = static_cast<TV*>(p.vrows) + (static_cast<int64_t>(b) * p.Tkp + t0) * D;
+    for (int ch = tid; ch < kQTile * D / 8; ch += 256) {
+      const int r = ch / (D / 8), c8 = (ch % (D / 8)) * 8;
+      store16B(vdst + static_cast<int64_t>(r) * D + c8, load16B(lds + OFF_D + r * PD + c8 * 2));
+    }
   }
 
   // Zero the accumulated gradients of this tile's query and key rows.
