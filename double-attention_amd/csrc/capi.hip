@@ -120,7 +120,9 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 
 extern "C" {
 
-int da_abi_version(void) { return 18; }
+static_assert(DA_OUT_SPLIT == da::kOutSplit, "split-output flag");
+
+int da_abi_version(void) { return 19; }
 
 const char* da_last_error(void) { return g_error.c_str(); }
 
@@ -175,6 +177,15 @@ namespace {
 int validate_row_norm(const char* what, const void* x, int x_dtype, int64_t rows, int64_t width, int64_t ld_x,
                       float eps, const void* grad, int grad_dtype, int64_t ld_grad, bool backward, const void* out,
                       int out_dtype, int64_t ld_out) {
+  // DA_OUT_SPLIT (backward only, 16-bit outputs): head and residual side by
+  // side, so the output row spans 2 x width.
+  const bool split = backward && (out_dtype & DA_OUT_SPLIT);
+  if (split) {
+    out_dtype &= ~DA_OUT_SPLIT;
+    if (out_dtype != DA_F16 && out_dtype != DA_BF16)
+      return fail(DA_ERR_INVALID_ARGUMENT, "%s: DA_OUT_SPLIT needs a 16-bit output", what);
+    if (ld_out < 2 * width) return fail(DA_ERR_ALIGNMENT, "%s: DA_OUT_SPLIT needs ld_out >= 2 width", what);
+  }
   if (!any_dtype(x_dtype) || !any_dtype(out_dtype) || (backward && !any_dtype(grad_dtype)))
     return fail(DA_ERR_INVALID_ARGUMENT, "%s: bad dtype", what);
   if (rows < 0 || rows > 0x7fffffffLL * 4) return fail(DA_ERR_INVALID_ARGUMENT, "%s: bad row count", what);

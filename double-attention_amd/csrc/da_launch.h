@@ -167,6 +167,9 @@ void launch_dictionary_normalize_backward(const NormBwdArgs& a, hipStream_t stre
 // Row L2 normalization and its backward (row_norm.hip).  R % 4 == 0; row
 // pitches multiples of 4 elements; x, grad and out aligned to 4 elements.
 // Arithmetic in fp32 whatever the element types.
+// Row-normalize backward output: a 16-bit dtype or'd with kOutSplit writes
+// the rounded gradient and its rounding residual side by side.
+constexpr int kOutSplit = 0x100;
 struct RowNormArgs {
   const void* x; int x_dtype; int64_t ld_x;
   int64_t rows; int R; float eps;

@@ -42,6 +42,13 @@ __device__ __forceinline__ float wave_max64(float v) {
 }
 __device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
 
+// With DA_ROUTE_BETA_IS_LOG the row's d beta term is written at log beta:
+// times beta where the clamp passes the gradient, zero outside its window.
+__device__ __forceinline__ float dbeta_at(int flags, float dbeta, float beta_raw, float beta) {
+  if (!(flags & kRouteBetaIsLog)) return dbeta;
+  return beta_raw >= kLogBetaMin && beta_raw <= kLogBetaMax ? dbeta * beta : 0.f;
+}
+
 // WPR waves per row: with WPR = 1 a workgroup's four waves take four rows;
 // with WPR = 4 its waves share one row (column j at wave j / 64 % 4), and the
 // row sums meet in LDS.
@@ -186,7 +193,7 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
       w_row[j] = static_cast<TO>(j < M ? w[i] : 0.f);
     }
   }
-  if (a.dbeta_rows && lane == 0 && (WPR == 1 || wave == 0)) a.dbeta_rows[row] = direct ? 0.f : dbeta;
+  if (a.dbeta_rows && lane == 0 && (WPR == 1 || wave == 0)) a.dbeta_rows[row] = direct ? 0.f : dbeta_at(a.flags, dbeta, beta_raw, beta);
 }
 
 // Rows longer than the register-held kernels' 16384 columns: the same algebra
@@ -359,7 +366,7 @@ __global__ __launch_bounds__(256) void route_backward_long_rows_kernel(RouteBwdR
       }
     }
   }
-  if (a.dbeta_rows && lane == 0) a.dbeta_rows[row] = direct ? 0.f : dbeta;
+  if (a.dbeta_rows && lane == 0) a.dbeta_rows[row] = direct ? 0.f : dbeta_at(a.flags, dbeta, beta_raw, beta);
 }
 
 template <typename TO>

@@ -80,7 +80,9 @@ __global__ __launch_bounds__(64 * kRowWaves) void row_normalize_kernel(RowNormAr
   }
 }
 
-template <typename TX, typename TG, typename TO>
+// SPLIT: the 16-bit result at columns [0, R) and its rounding residual
+// (the fp32 value minus the rounded one, rounded) at [R, 2R) of the row.
+template <typename TX, typename TG, typename TO, bool SPLIT>
 __global__ __launch_bounds__(64 * kRowWaves) void row_normalize_backward_kernel(RowNormArgs a) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowWaves + (threadIdx.x >> 6);
   if (row >= a.rows) return;
@@ -110,6 +112,11 @@ __global__ __launch_bounds__(64 * kRowWaves) void row_normalize_backward_kernel(
 #pragma unroll
     for (int e = 0; e < 4; ++e) f[e] = g[e] * inv - f[e] * coef;
     store4(dx + c, f);
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) f[e] -= static_cast<float>(static_cast<TO>(f[e]));
+      store4(dx + a.R + c, f);
+    }
   }
 }
 
@@ -122,9 +129,14 @@ void launch_fwd(const RowNormArgs& a, dim3 grid, hipStream_t s) {
 
 template <typename TX, typename TG>
 void launch_bwd_g(const RowNormArgs& a, dim3 grid, hipStream_t s) {
-  if (a.out_dtype == kF32) hipLaunchKernelGGL((row_normalize_backward_kernel<TX, TG, float>), grid, dim3(64 * kRowWaves), 0, s, a);
-  else if (a.out_dtype == kF16) hipLaunchKernelGGL((row_normalize_backward_kernel<TX, TG, _Float16>), grid, dim3(64 * kRowWaves), 0, s, a);
-  else hipLaunchKernelGGL((row_normalize_backward_kernel<TX, TG, __bf16>), grid, dim3(64 * kRowWaves), 0, s, a);
+  const dim3 block(64 * kRowWaves);
+  const bool split = a.out_dtype & kOutSplit;
+  const int dt = a.out_dtype & ~kOutSplit;
+  if (dt == kF32) hipLaunchKernelGGL((row_normalize_backward_kernel<TX, TG, float, false>), grid, block, 0, s, a);
+  else if (dt == kF16 && split) hipLaunchKernelGGL((row_normalize_backward_kernel<TX, TG, _Float16, true>), grid, block, 0, s, a);
+  else if (dt == kF16) hipLaunchKernelGGL((row_normalize_backward_kernel<TX, TG, _Float16, false>), grid, block, 0, s, a);
+  else if (split) hipLaunchKernelGGL((row_normalize_backward_kernel<TX, TG, __bf16, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((row_normalize_backward_kernel<TX, TG, __bf16, false>), grid, block, 0, s, a);
 }
 
 template <typename TX>

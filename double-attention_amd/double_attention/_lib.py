@@ -16,6 +16,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libdouble_attention_hip.so"
 
 DA_F32, DA_F16, DA_BF16 = 0, 1, 2
+DA_OUT_SPLIT = 0x100
 
 DA_ROUTE_NORMALIZE_INPUT = 1
 DA_ROUTE_NORMALIZE_OUTPUT = 2
@@ -47,7 +48,7 @@ ERROR_NAMES = {
     -5: "workspace too small",
 }
 
-ABI_VERSION = 18
+ABI_VERSION = 19
 NOALLOC_SCRATCH_BYTES = 128 << 20
 
 _vp = ctypes.c_void_p

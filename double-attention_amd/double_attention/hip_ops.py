@@ -452,23 +452,26 @@ def _row_normalize(rows: Tensor, eps: float, dtype: torch.dtype) -> Tensor:
     return out
 
 
-def _normalize_backward(v: Tensor, h: Tensor, eps: float, dtype: torch.dtype) -> Tensor:
+def _normalize_backward(v: Tensor, h: Tensor, eps: float, dtype: torch.dtype, split: bool = False) -> Tensor:
     """The backward of N(v) = v / max(|v|, eps) (``F.normalize``) at gradient h.
 
     (h - n <n, h>) / |v| with n = v / |v| where |v| > eps, h / eps elsewhere,
     for ``[n, R]`` rows v and h: one pass of ``da_row_normalize_backward``,
-    fp32 arithmetic, one rounding to ``dtype``.
+    fp32 arithmetic, one rounding to ``dtype``.  With ``split`` (16-bit
+    ``dtype``) the result is ``[n, 2R]``: the rounded gradient, then its
+    rounding residual (rounded), side by side.
     """
 
     v = _aligned(v)
     h = _aligned(h)
     n, width = v.shape
-    out = torch.empty(n, width, dtype=dtype, device=v.device)
+    cols = 2 * width if split else width
+    out = torch.empty(n, cols, dtype=dtype, device=v.device)
     lib = _lib.get()
     _lib.check(
         lib.da_row_normalize_backward(
             v.data_ptr(), dtype_code(v.dtype), n, width, width, float(eps), h.data_ptr(), dtype_code(h.dtype), width,
-            out.data_ptr(), dtype_code(dtype), width, _stream(v.device),
+            out.data_ptr(), dtype_code(dtype) | (_lib.DA_OUT_SPLIT if split else 0), cols, _stream(v.device),
         ),
         "row normalize backward",
     )
@@ -788,16 +791,26 @@ def _route_backward_rows(
     # dW = dr Dv takes dr as a 16-bit head and its rounding residual ([n, 2R]
     # against [Dv; Dv]): the softmax backward differences dW_j - sum_k w_k dW_k,
     # so one 16-bit rounding of dr would reach every atom's gradient.
-    dr = _normalize_backward(r, g, eps, torch.float32) if normalize_output else g.float()
-    dr2 = torch.empty(n, 2 * routing_dim, dtype=v_type, device=device)
-    dr_v = dr2[:, :routing_dim]
-    dr_v.copy_(dr)
-    torch.sub(dr, dr_v, out=dr2[:, routing_dim:])
-    del dr
+    # The row-norm backward writes the pair in one pass; a 16-bit gradient of
+    # the value dtype is its own head (no residual).
     keys_h = dictionary_key.detach().to(key_type)
     logits = _mm_f32(u_h, keys_h)
     values_v = dictionary_value.detach().to(v_type)
-    grad_weights = _mm_f32(dr2, torch.cat((values_v, values_v)))
+    if normalize_output:
+        dr2 = _normalize_backward(r, g, eps, v_type, split=True)
+        dr_v = dr2[:, :routing_dim]
+        grad_weights = _mm_f32(dr2, torch.cat((values_v, values_v)))
+    elif g.dtype == v_type:
+        dr_v = _aligned(g)
+        grad_weights = _mm_f32(dr_v, values_v)
+    else:
+        dr = g.float()
+        dr2 = torch.empty(n, 2 * routing_dim, dtype=v_type, device=device)
+        dr_v = dr2[:, :routing_dim]
+        dr_v.copy_(dr)
+        torch.sub(dr, dr_v, out=dr2[:, routing_dim:])
+        del dr
+        grad_weights = _mm_f32(dr2, torch.cat((values_v, values_v)))
     grad_logits = torch.empty(n, atoms, dtype=v_type, device=device)
     weights = torch.empty(n, atoms, dtype=v_type, device=device)
     dbeta_rows = torch.empty(n, dtype=torch.float32, device=device)
@@ -818,12 +831,9 @@ def _route_backward_rows(
     du = _mm_f32(grad_logits, keys_vt)
     d_key = _mm_tn_f32(u_v, grad_logits)
     d_value = _mm_tn_f32(dr_v, weights)
+    # With beta_is_log the row kernel writes the terms at log beta (times
+    # beta inside the clamp's window, zero outside).
     dbeta = dbeta_rows.sum().reshape(1)
-    if beta_is_log:
-        # d/d log_beta: beta where the clamp passes the gradient.
-        log_beta = beta_t.float()
-        lo, hi = LOG_BETA_RANGE
-        dbeta = dbeta * log_beta.exp() * ((log_beta >= lo) & (log_beta <= hi))
     dx = _normalize_backward(rows, du, eps, x.dtype) if normalize_input else du.to(x.dtype)
     return (
         dx.reshape(x.shape),
@@ -1262,8 +1272,8 @@ def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
 
 
 def _attention_backward_dense(
-    query: Tensor, key: Tensor, value: Tensor, scales: Tensor, grad: Tensor, causal: bool,
-    qk_grad_dtype: torch.dtype | None = None,
+    query: Tensor, key: Tensor, value: Tensor | None, scales: Tensor, grad: Tensor, causal: bool,
+    qk_grad_dtype: torch.dtype | None = None, value_t: Tensor | None = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Outer-attention gradients with the score matrices materialized.
 
@@ -1275,19 +1285,40 @@ def _attention_backward_dense(
     sum uses P and dP themselves, no saved output.  dS and P are stored in
     the value dtype (16-bit) between the row kernel and the GEMMs, which
     accumulate in fp32.
+
+    ``query`` and ``key`` may be strided views (rows of unit stride: the
+    score maps of the routed rows); the values come as rows ``value``
+    ``[B, T, D]`` or, with ``value`` None, as the forward's V^T tiles
+    ``value_t`` ``[B, Tp/32, D, 32]``, laid out as V^T by one copy.
     """
 
     batch, maps, length, score_dim = query.shape
-    model_dim = value.shape[-1]
     rows = batch * maps
-    device = value.device
-    v_type = value.dtype if value.dtype in (torch.float16, torch.bfloat16) else torch.bfloat16
-    q = query.detach().reshape(rows, length, score_dim).contiguous()
-    k = key.detach().reshape(rows, length, score_dim).contiguous()
+    device = query.device
+    if value is None:
+        if value_t is None:
+            raise ValueError("value or value_t is required")
+        model_dim, in_type = value_t.shape[2], value_t.dtype
+    else:
+        model_dim, in_type = value.shape[-1], value.dtype
+    v_type = in_type if in_type in (torch.float16, torch.bfloat16) else torch.bfloat16
+
+    def rows_of(t: Tensor) -> Tensor:
+        # [rows, T, R] without a copy where the rows already have unit stride.
+        t = t.detach().reshape(rows, length, score_dim)
+        return t if t.stride(2) == 1 and t.stride(1) >= score_dim else t.contiguous()
+
+    q, k = rows_of(query), rows_of(key)
     # Right operands of the products are contiguous (no transposed views).
     scores = torch.bmm(q, k.transpose(1, 2).contiguous(), out_dtype=torch.float32)
     go = grad.detach().reshape(rows, length, model_dim).to(v_type).contiguous()
-    vt = value.detach().to(v_type).transpose(1, 2).contiguous()
+    if value is None:
+        padded = value_t.shape[1] * 32
+        vt = value_t.detach().to(v_type).permute(0, 2, 1, 3).reshape(batch, model_dim, padded)
+        if padded != length:
+            vt = vt[:, :, :length].contiguous()
+    else:
+        vt = value.detach().to(v_type).transpose(1, 2).contiguous()
     if maps > 1:
         vt = vt.unsqueeze(1).expand(batch, maps, model_dim, length).reshape(rows, model_dim, length)
     grad_p = torch.bmm(go, vt, out_dtype=torch.float32)
@@ -1309,11 +1340,11 @@ def _attention_backward_dense(
     dq = torch.bmm(grad_s, k.to(v_type), out_dtype=torch.float32)
     dk = torch.bmm(grad_s.transpose(1, 2), q.to(v_type), out_dtype=torch.float32)
     dv = torch.bmm(probs.transpose(1, 2), go, out_dtype=torch.float32)
-    dv = dv.view(batch, maps, length, model_dim).sum(1)
+    dv = dv.view(batch, length, model_dim) if maps == 1 else dv.view(batch, maps, length, model_dim).sum(1)
     dgamma = dgamma_rows.view(batch, maps, length).sum(dim=(0, 2))
     shape = (batch, maps, length, score_dim)
     return (dq.view(shape).to(qk_grad_dtype or query.dtype), dk.view(shape).to(qk_grad_dtype or key.dtype),
-            dv.to(value.dtype), dgamma.to(scales.dtype))
+            dv.to(in_type), dgamma.to(scales.dtype))
 
 
 def attention_gradients(

@@ -596,8 +596,6 @@ class _HipModuleFunction(torch.autograd.Function):
                 grads["log_score_scales"] = d_log_scales
             d_routed = d_rows_qk.view(-1, routing_dim)
         else:
-            padded = vt.shape[1] * 32
-            value_rows = vt.transpose(2, 3).reshape(batch, padded, model_dim)[:, :length]
             score_query, score_key = _HipModuleFunction._score_maps(
                 routed, batch, length, branches, maps, routing_dim
             )
@@ -605,10 +603,18 @@ class _HipModuleFunction(torch.autograd.Function):
             # exponentials of the clamped logs.
             log32 = log_scales.detach().float()
             scales = log32.clamp(*hip_ops.LOG_SCALE_RANGE).exp()
-            d_sq, d_sk, d_value, d_scales = hip_ops.attention_gradients(
-                score_query, score_key, value_rows, scales, map_output, d_maps, cfg.causal,
-                qk_grad_dtype=torch.float32,
-            )
+            if hip_ops._dense_fits(batch, maps, length, score_query.shape[-1], model_dim):
+                # The dense backward lays the V^T tiles out as V^T itself.
+                d_sq, d_sk, d_value, d_scales = hip_ops._attention_backward_dense(
+                    score_query, score_key, None, scales, d_maps, cfg.causal, torch.float32, value_t=vt,
+                )
+            else:
+                padded = vt.shape[1] * 32
+                value_rows = vt.transpose(2, 3).reshape(batch, padded, model_dim)[:, :length]
+                d_sq, d_sk, d_value, d_scales = hip_ops.attention_gradients(
+                    score_query, score_key, value_rows, scales, map_output, d_maps, cfg.causal,
+                    qk_grad_dtype=torch.float32,
+                )
             if wants("log_score_scales"):
                 # The clamp passes the gradient only inside its window.
                 inside = (log32 >= hip_ops.LOG_SCALE_RANGE[0]) & (log32 <= hip_ops.LOG_SCALE_RANGE[1])

@@ -55,6 +55,7 @@ typedef struct ihipStream_t* da_stream_t; /* hipStream_t; NULL = default stream 
 #define DA_F32 0
 #define DA_F16 1
 #define DA_BF16 2
+#define DA_OUT_SPLIT 0x100 /* or'd into a 16-bit out_dtype: see da_row_normalize_backward */
 
 /* error codes */
 #define DA_OK 0
@@ -94,7 +95,7 @@ typedef struct ihipStream_t* da_stream_t; /* hipStream_t; NULL = default stream 
                                        normalizes the bank itself); never set it for a bank whose
                                        atoms were not normalized. */
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature or semantics change). */
 int da_abi_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -163,7 +164,12 @@ int da_row_normalize(const void* x, int x_dtype, int64_t rows, int64_t width, in
  * and grad = dL/dout (grad_dtype, pitch ld_grad), grad_x = (grad - y <y,
  * grad>) / |x| with y = x / |x| where |x| > eps, grad / eps elsewhere; fp32
  * arithmetic, rounded once to out_dtype.  Same layout rules as
- * da_row_normalize, grad included.
+ * da_row_normalize, grad included.  out_dtype DA_F16 or DA_BF16 or'd with
+ * DA_OUT_SPLIT writes each row's 16-bit result at columns [0, width) and its
+ * rounding residual (the fp32 value minus the rounded one, rounded) at
+ * [width, 2 width), with ld_out >= 2 width: a 16-bit operand pair that carries
+ * the gradient to about 16 significant bits through a GEMM with fp32
+ * accumulation.
  */
 int da_row_normalize_backward(const void* x, int x_dtype, int64_t rows, int64_t width, int64_t ld_x, float eps,
                               const void* grad, int grad_dtype, int64_t ld_grad, void* grad_x, int out_dtype,
@@ -205,7 +211,9 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  * Writes, per row, the gradient at the raw logits (grad_logits) and the
  * assignment weights (weights), rows x atoms with pitch ld_out in out_dtype
  * (DA_F16 or DA_BF16), and the row's share of d beta to dbeta_rows[row]
- * (fp32; 0 for DA_ROUTE_DIRECT_SILU; may be NULL).  atoms <= 2^24 (rows of
+ * (fp32; 0 for DA_ROUTE_DIRECT_SILU; may be NULL); with DA_ROUTE_BETA_IS_LOG
+ * the share of d log_beta (beta times the share inside the clamp's window
+ * [ln .05, ln 64], zero outside it).  atoms <= 2^24 (rows of
  * up to 16384 atoms are held in registers, longer rows are passed over several
  * times).
  * causal_period > 0 limits row r to columns j <= r % causal_period (zeros
