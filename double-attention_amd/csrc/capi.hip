@@ -121,6 +121,7 @@ int validate_attention(const void* q, const void* k, int64_t sb, int64_t st, int
 extern "C" {
 
 static_assert(DA_OUT_SPLIT == da::kOutSplit, "split-output flag");
+static_assert(DA_ROUTE_BETA_IS_LOG_SCALE == da::kRouteBetaIsLogScale, "route flag");
 
 int da_abi_version(void) { return 19; }
 
@@ -252,9 +253,12 @@ int da_dictionary_route_backward_rows(const float* logits, const float* grad_wei
                                       int flags, float silu_gain, float logit_scale, float eps,
                                       void* grad_logits, void* weights, int64_t ld_out, int out_dtype,
                                       float* dbeta_rows, da_stream_t stream) {
-  constexpr int kBwdRowsFlags = DA_ROUTE_BETA_IS_LOG | DA_ROUTE_SILU_LOGITS | DA_ROUTE_STANDARDIZE | DA_ROUTE_DIRECT_SILU;
+  constexpr int kBwdRowsFlags = DA_ROUTE_BETA_IS_LOG | DA_ROUTE_BETA_IS_LOG_SCALE | DA_ROUTE_SILU_LOGITS |
+                                DA_ROUTE_STANDARDIZE | DA_ROUTE_DIRECT_SILU;
   if (flags & ~kBwdRowsFlags)
     return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: unknown flag bits 0x%x", flags);
+  if ((flags & DA_ROUTE_BETA_IS_LOG) && (flags & DA_ROUTE_BETA_IS_LOG_SCALE))
+    return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: DA_ROUTE_BETA_IS_LOG and _LOG_SCALE exclude each other");
   if ((flags & DA_ROUTE_DIRECT_SILU) && !(silu_gain > 0.f && std::isfinite(silu_gain)))
     return fail(DA_ERR_INVALID_ARGUMENT, "route backward rows: silu_gain must be positive and finite");
   if ((flags & DA_ROUTE_STANDARDIZE) && !(logit_scale > 0.f && std::isfinite(logit_scale)))

@@ -25,6 +25,9 @@ enum : int {
   kRouteSiluLogits = 16,    // logits -> 2 SiLU(logits)                        (ops.py:41-44)
   kRouteStandardize = 32,   // logits -> (logits - mean) / std * logit_scale   (ops.py:47-55)
   kRouteDirectSilu = 64,    // weights = (2/g) SiLU(g logits), no softmax      (ops.py:58-59)
+  kRouteBetaIsLogScale = 128,   // row backward only: beta holds log gamma, the
+                                // outer attention's temperature (clamp window
+                                // kLogScaleMin .. kLogScaleMax)
 };
 
 // Attention flags.

@@ -42,11 +42,32 @@ __device__ __forceinline__ float wave_max64(float v) {
 }
 __device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
 
-// With DA_ROUTE_BETA_IS_LOG the row's d beta term is written at log beta:
-// times beta where the clamp passes the gradient, zero outside its window.
+// The scale of the assignment from the beta argument: beta itself, or
+// exp(clamp(.)) of a log with kRouteBetaIsLog (log beta, window ln .05 ..
+// ln 64) or kRouteBetaIsLogScale (log gamma, window ln .25 .. ln 1024).
+__device__ __forceinline__ bool beta_log_window(int flags, float& lo, float& hi) {
+  if (flags & kRouteBetaIsLog) {
+    lo = kLogBetaMin;
+    hi = kLogBetaMax;
+    return true;
+  }
+  if (flags & kRouteBetaIsLogScale) {
+    lo = kLogScaleMin;
+    hi = kLogScaleMax;
+    return true;
+  }
+  return false;
+}
+__device__ __forceinline__ float beta_from(int flags, float beta_raw) {
+  float lo, hi;
+  return beta_log_window(flags, lo, hi) ? expf(fminf(fmaxf(beta_raw, lo), hi)) : beta_raw;
+}
+// With a log argument the row's d beta term is written at the log: times
+// beta where the clamp passes the gradient, zero outside its window.
 __device__ __forceinline__ float dbeta_at(int flags, float dbeta, float beta_raw, float beta) {
-  if (!(flags & kRouteBetaIsLog)) return dbeta;
-  return beta_raw >= kLogBetaMin && beta_raw <= kLogBetaMax ? dbeta * beta : 0.f;
+  float lo, hi;
+  if (!beta_log_window(flags, lo, hi)) return dbeta;
+  return beta_raw >= lo && beta_raw <= hi ? dbeta * beta : 0.f;
 }
 
 // WPR waves per row: with WPR = 1 a workgroup's four waves take four rows;
@@ -98,7 +119,7 @@ __global__ __launch_bounds__(256) void route_backward_rows_kernel(RouteBwdRowsAr
     g[i] = j < M ? grow[j] : 0.f;
   }
   const float beta_raw = a.beta_ptr ? scalar_value(beta_bits, a.beta_dtype) : a.beta_value;
-  const float beta = (a.flags & kRouteBetaIsLog) ? expf(fminf(fmaxf(beta_raw, kLogBetaMin), kLogBetaMax)) : beta_raw;
+  const float beta = beta_from(a.flags, beta_raw);
   const float inv_m = 1.f / static_cast<float>(M);
 
   // Activation, then standardization: c holds the standardized value
@@ -220,7 +241,7 @@ __global__ __launch_bounds__(256) void route_backward_long_rows_kernel(RouteBwdR
   const ScalarHalves beta_bits = fetch_scalar(a.beta_ptr ? a.beta_ptr : static_cast<const void*>(a.logits),
                                               a.beta_ptr ? a.beta_dtype : kF32, a.beta_ptr ? beta_index : 0);
   const float beta_raw = a.beta_ptr ? scalar_value(beta_bits, a.beta_dtype) : a.beta_value;
-  const float beta = (a.flags & kRouteBetaIsLog) ? expf(fminf(fmaxf(beta_raw, kLogBetaMin), kLogBetaMax)) : beta_raw;
+  const float beta = beta_from(a.flags, beta_raw);
   const float inv_m = 1.f / static_cast<float>(M);
   auto act = [&](float x) { return silu_logits ? 2.f * x * sigmoidf(x) : x; };
 

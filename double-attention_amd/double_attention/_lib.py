@@ -25,6 +25,7 @@ DA_ROUTE_UNIT_KEYS = 8
 DA_ROUTE_SILU_LOGITS = 16
 DA_ROUTE_STANDARDIZE = 32
 DA_ROUTE_DIRECT_SILU = 64
+DA_ROUTE_BETA_IS_LOG_SCALE = 128
 
 DA_ATTN_CAUSAL = 1
 DA_ATTN_SCALES_ARE_LOG = 2

@@ -1273,7 +1273,7 @@ def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
 
 def _attention_backward_dense(
     query: Tensor, key: Tensor, value: Tensor | None, scales: Tensor, grad: Tensor, causal: bool,
-    qk_grad_dtype: torch.dtype | None = None, value_t: Tensor | None = None,
+    qk_grad_dtype: torch.dtype | None = None, value_t: Tensor | None = None, scales_are_log: bool = False,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Outer-attention gradients with the score matrices materialized.
 
@@ -1289,7 +1289,10 @@ def _attention_backward_dense(
     ``query`` and ``key`` may be strided views (rows of unit stride: the
     score maps of the routed rows); the values come as rows ``value``
     ``[B, T, D]`` or, with ``value`` None, as the forward's V^T tiles
-    ``value_t`` ``[B, Tp/32, D, 32]``, laid out as V^T by one copy.
+    ``value_t`` ``[B, Tp/32, D, 32]``, laid out as V^T by one copy.  With
+    ``scales_are_log`` the scales are log gammas: the row kernel clamps and
+    exponentiates them (the temperature window ``LOG_SCALE_RANGE``) and the
+    scale gradient comes back at the logs (zero outside the window).
     """
 
     batch, maps, length, score_dim = query.shape
@@ -1325,12 +1328,13 @@ def _attention_backward_dense(
     grad_s = torch.empty(rows, length, length, dtype=v_type, device=device)
     probs = torch.empty_like(grad_s)
     dgamma_rows = torch.empty(rows * length, dtype=torch.float32, device=device)
-    gamma = scales.detach().float().contiguous()
+    gamma = scales.detach().contiguous() if scales_are_log else scales.detach().float().contiguous()
     lib = _lib.get()
     _lib.check(
         lib.da_dictionary_route_backward_rows(
             scores.data_ptr(), grad_p.data_ptr(), rows * length, length, length if causal else 0, length,
-            gamma.data_ptr(), _lib.DA_F32, 0.0, maps, length, 0, 1.0, 1.0, 0.0,
+            gamma.data_ptr(), dtype_code(gamma.dtype), 0.0, maps, length,
+            _lib.DA_ROUTE_BETA_IS_LOG_SCALE if scales_are_log else 0, 1.0, 1.0, 0.0,
             grad_s.data_ptr(), probs.data_ptr(), length, _half_code(v_type), dgamma_rows.data_ptr(),
             _stream(device),
         ),

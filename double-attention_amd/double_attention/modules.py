@@ -599,26 +599,30 @@ class _HipModuleFunction(torch.autograd.Function):
             score_query, score_key = _HipModuleFunction._score_maps(
                 routed, batch, length, branches, maps, routing_dim
             )
-            # The temperatures as the forward kernel formed them: fp32
-            # exponentials of the clamped logs.
-            log32 = log_scales.detach().float()
-            scales = log32.clamp(*hip_ops.LOG_SCALE_RANGE).exp()
             if hip_ops._dense_fits(batch, maps, length, score_query.shape[-1], model_dim):
-                # The dense backward lays the V^T tiles out as V^T itself.
-                d_sq, d_sk, d_value, d_scales = hip_ops._attention_backward_dense(
-                    score_query, score_key, None, scales, d_maps, cfg.causal, torch.float32, value_t=vt,
+                # The dense backward lays the V^T tiles out as V^T itself, and
+                # its row kernel takes the log temperatures with their clamp
+                # (the scale gradient comes back at the logs).
+                d_sq, d_sk, d_value, d_log_scales = hip_ops._attention_backward_dense(
+                    score_query, score_key, None, log_scales.detach(), d_maps, cfg.causal, torch.float32,
+                    value_t=vt, scales_are_log=True,
                 )
             else:
+                # The temperatures as the forward kernel formed them: fp32
+                # exponentials of the clamped logs.
+                log32 = log_scales.detach().float()
+                scales = log32.clamp(*hip_ops.LOG_SCALE_RANGE).exp()
                 padded = vt.shape[1] * 32
                 value_rows = vt.transpose(2, 3).reshape(batch, padded, model_dim)[:, :length]
                 d_sq, d_sk, d_value, d_scales = hip_ops.attention_gradients(
                     score_query, score_key, value_rows, scales, map_output, d_maps, cfg.causal,
                     qk_grad_dtype=torch.float32,
                 )
-            if wants("log_score_scales"):
                 # The clamp passes the gradient only inside its window.
                 inside = (log32 >= hip_ops.LOG_SCALE_RANGE[0]) & (log32 <= hip_ops.LOG_SCALE_RANGE[1])
-                grads["log_score_scales"] = d_scales.float() * scales * inside
+                d_log_scales = d_scales.float() * scales * inside
+            if wants("log_score_scales"):
+                grads["log_score_scales"] = d_log_scales
             # Score-map assembly (views, grouping or repetition of the branches).
             if branches == maps:
                 d_rq, d_rk = d_sq, d_sk

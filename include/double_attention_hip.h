@@ -77,6 +77,9 @@ typedef struct ihipStream_t* da_stream_t; /* hipStream_t; NULL = default stream 
                                        atoms (standardize_logits, ops.py:47-55): two passes */
 #define DA_ROUTE_DIRECT_SILU 64     /* weights = (2/silu_gain) SiLU(silu_gain logits) instead of
                                        softmax(beta logits) (assignment "silu", ops.py:56-59) */
+#define DA_ROUTE_BETA_IS_LOG_SCALE 128 /* da_dictionary_route_backward_rows only: *beta holds
+                                       log_score_scales, exp(clamp(., ln .25, ln 1024)) (the
+                                       outer attention's temperatures, ops.py:160-161) */
 
 /* da_routed_attention flags */
 #define DA_ATTN_CAUSAL 1
@@ -212,8 +215,8 @@ int da_dictionary_route(const void* x, int64_t rows, int64_t routing_dim, int64_
  * assignment weights (weights), rows x atoms with pitch ld_out in out_dtype
  * (DA_F16 or DA_BF16), and the row's share of d beta to dbeta_rows[row]
  * (fp32; 0 for DA_ROUTE_DIRECT_SILU; may be NULL); with DA_ROUTE_BETA_IS_LOG
- * the share of d log_beta (beta times the share inside the clamp's window
- * [ln .05, ln 64], zero outside it).  atoms <= 2^24 (rows of
+ * or DA_ROUTE_BETA_IS_LOG_SCALE the share of the gradient at the log (beta
+ * times the share inside the clamp's window, zero outside it).  atoms <= 2^24 (rows of
  * up to 16384 atoms are held in registers, longer rows are passed over several
  * times).
  * causal_period > 0 limits row r to columns j <= r % causal_period (zeros

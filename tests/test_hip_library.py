@@ -62,7 +62,7 @@ def _fake(addr: int = 1 << 20) -> int:
         ({"x": 0}, -1, "null pointer"),
         ({"x": (1 << 20) + 2}, -3, "16-byte aligned"),
         ({"atoms": 0}, -1, "rows/atoms"),
-        ({"flags": 3 | 128}, -1, "unknown flag bits"),
+        ({"flags": 3 | lib.DA_ROUTE_BETA_IS_LOG_SCALE}, -1, "unknown flag bits"),   # row backward only
         ({"flags": 3 | lib.DA_ROUTE_DIRECT_SILU, "silu_gain": 0.0}, -1, "silu_gain"),
         ({"flags": 3 | lib.DA_ROUTE_STANDARDIZE, "logit_scale": float("inf")}, -1, "logit_scale"),
     ],
@@ -298,6 +298,9 @@ def test_route_backward_rows_rejects_bad_arguments() -> None:
     assert call(beta_count=3, beta_period=0) == -1
     assert b"beta_count" in h.da_last_error()
     assert call(rows=0, logits=None) == 0               # nothing to do
+    both = lib.DA_ROUTE_BETA_IS_LOG | lib.DA_ROUTE_BETA_IS_LOG_SCALE
+    assert call(flags=both) == -1 and b"exclude each other" in h.da_last_error()
+    assert call(rows=0, flags=lib.DA_ROUTE_BETA_IS_LOG_SCALE) == 0
 
 
 
@@ -353,3 +356,9 @@ def test_row_normalize_rejects_bad_arguments() -> None:
     assert bwd(grad=ctypes.c_void_p((1 << 20) + 8)) == -3 and b"aligned" in h.da_last_error()
     assert fwd(rows=0, x=None) == -1                                      # null checked before the empty case
     assert fwd(rows=0) == 0 and bwd(rows=0) == 0                          # nothing to do
+    # DA_OUT_SPLIT: backward only, 16-bit outputs, two widths per output row.
+    split = lib.DA_BF16 | lib.DA_OUT_SPLIT
+    assert bwd(out_dtype=lib.DA_F32 | lib.DA_OUT_SPLIT) == -1 and b"16-bit" in h.da_last_error()
+    assert bwd(out_dtype=split) == -3 and b"2 width" in h.da_last_error()
+    assert bwd(out_dtype=split, ld_out=512, rows=0) == 0
+    assert fwd(out_dtype=split) == -1                                     # not a forward dtype

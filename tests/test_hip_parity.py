@@ -185,6 +185,24 @@ def test_row_normalize_and_backward(case) -> None:
         wrapped = da.hip_ops._normalize_backward(x, h, eps, out_dtype)
         assert torch.equal(wrapped, dx)
         assert torch.equal(da.hip_ops._row_normalize(x, eps, out_dtype), out)
+    # DA_OUT_SPLIT: the 16-bit result (bit-identical) beside its rounding
+    # residual; head + residual carries the fp32 result to about twice the
+    # 16-bit precision (the zero row's 1e6 / eps overflows fp16 and is left
+    # out).
+    if ld == width and out_dtype != torch.float32:
+        pair = da.hip_ops._normalize_backward(x, h, eps, out_dtype, split=True)
+        assert pair.shape == (rows, 2 * width)
+        assert torch.equal(pair[:, :width], dx)
+        exact = da.hip_ops._normalize_backward(x, h, eps, torch.float32)
+        both = pair[:, :width].float() + pair[:, width:].float()
+        head_err = (dx.float() - exact)[keep].abs().max()
+        pair_err = (both - exact)[keep].abs()
+        # Significant bits of the 16-bit type; fp16 residuals below 2^-14
+        # are subnormal (absolute spacing 2^-24).
+        bits, floor = (11, 2.0 ** -25) if out_dtype == torch.float16 else (8, 0.0)
+        assert torch.isfinite(pair_err).all()
+        assert float((pair_err - exact[keep].abs() * 2.0 ** (-2 * bits)).max()) <= floor + 1e-30
+        assert float(pair_err.max()) <= float(head_err) * 2.0 ** (-bits + 2)
 
 
 # ---------------------------------------------------------------- GEMMs
@@ -527,6 +545,37 @@ def test_routed_attention_backward(case, dtypes) -> None:
             assert_parity(grad, exp, 3 * rel, max(6e-2 * scale, 1e-6), f"{label} d{name}")
         else:
             assert_parity(grad, exp, rel, max(2e-2 * scale, 1e-6), f"{label} d{name}")
+
+
+def test_dense_attention_backward_log_scales() -> None:
+    # The dense backward with log temperatures (the module's path): the row
+    # kernel clamps and exponentiates them (ln .25 .. ln 1024) and returns the
+    # scale gradient at the logs, the plain-gamma call's gradient times gamma
+    # inside the window and zero outside; the other gradients as with gamma.
+    # The value tiles come in the forward's V^T tile layout.
+    device = _device()
+    batch, maps, length, score_dim, value_dim = 2, 3, 100, 512, 256
+    q = unit_rows((batch, maps, length, score_dim), torch.float16, device, 30)
+    k = unit_rows((batch, maps, length, score_dim), torch.float16, device, 31)
+    g = torch.Generator().manual_seed(32)
+    v = torch.randn(batch, length, value_dim, generator=g).to(device, torch.bfloat16)
+    w = torch.randn(batch, maps, length, value_dim, generator=g).to(device, torch.bfloat16)
+    logs = torch.tensor([math.log(8.0), 7.5, -2.0], device=device)   # inside, above, below
+    lo, hi = da.hip_ops.LOG_SCALE_RANGE
+    gamma = logs.clamp(lo, hi).exp()
+    padded = (length + 31) // 32 * 32
+    vt = torch.zeros(batch, padded, value_dim, device=device, dtype=torch.bfloat16)
+    vt[:, :length] = v
+    vt = vt.view(batch, padded // 32, 32, value_dim).transpose(2, 3).contiguous()
+    plain = da.hip_ops._attention_backward_dense(q, k, v, gamma, w, True, torch.float32)
+    at_log = da.hip_ops._attention_backward_dense(q, k, None, logs, w, True, torch.float32, value_t=vt,
+                                                  scales_are_log=True)
+    for a, b in zip(plain[:3], at_log[:3]):
+        torch.testing.assert_close(b.float(), a.float(), rtol=1e-2, atol=1e-4 * float(a.abs().max()))
+    inside = (logs >= lo) & (logs <= hi)
+    expected = plain[3].float() * gamma * inside
+    assert not bool(inside[1]) and not bool(inside[2]) and bool(inside[0])
+    torch.testing.assert_close(at_log[3].float(), expected, rtol=1e-3, atol=1e-6)
 
 
 @pytest.mark.parametrize("case", [(2, 3, 77, 64, 128, True), (1, 2, 200, 256, 512, True), (2, 1, 130, 512, 512, False)],
@@ -1333,6 +1382,34 @@ ROUTE_ROWS_CASES = [
     (40, 256, 20000, True, True, {}),
     (40, 128, 17000, True, True, dict(silu_logits=True, standardize_logits=True)),
 ]
+
+
+@pytest.mark.parametrize("log_beta", [math.log(6.0), 4.5, -3.5], ids=["inside", "above", "below"])
+def test_route_backward_rows_log_beta(log_beta) -> None:
+    # With beta_is_log the row kernel forms beta = exp(clamp(log beta,
+    # ln .05, ln 64)) itself and writes the d beta terms at log beta: the
+    # plain-beta call's d beta times beta inside the clamp's window, zero
+    # outside (where the clamp passes no gradient), and the same row
+    # gradients.
+    device = _device()
+    rows, routing_dim, atoms = 200, 512, 700
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(rows, routing_dim, generator=g).to(device, torch.bfloat16)
+    dk = unit_columns(routing_dim, atoms, torch.bfloat16, device, 3)
+    dv = unit_columns(routing_dim, atoms, torch.bfloat16, device, 4)
+    w = torch.randn(rows, routing_dim, generator=g).to(device, torch.bfloat16)
+    variant = da.hip_ops.RouteVariant(False, False, 1.0, False, None)
+    lo, hi = da.hip_ops.LOG_BETA_RANGE
+    beta = math.exp(min(max(log_beta, lo), hi))
+    plain = da.hip_ops._route_backward_rows(
+        x, dk, dv, torch.tensor(beta, device=device), 1e-6, True, True, w, variant)
+    at_log = da.hip_ops._route_backward_rows(
+        x, dk, dv, torch.tensor(log_beta, device=device), 1e-6, True, True, w, variant, beta_is_log=True)
+    for a, b in zip(plain[:3], at_log[:3]):
+        torch.testing.assert_close(b.float(), a.float(), rtol=2e-2, atol=1e-5)
+    expected = float(plain[3]) * beta if lo <= log_beta <= hi else 0.0
+    assert abs(float(at_log[3]) - expected) <= 1e-3 * abs(float(plain[3]) * beta) + 1e-6, (
+        float(at_log[3]), expected)
 
 
 def _rows_case_id(c) -> str:
