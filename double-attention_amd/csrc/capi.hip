@@ -592,6 +592,50 @@ int da_layer_norm(const void* x, int64_t rows, int64_t dim, const void* weight, 
   return check_launch("layer_norm");
 }
 
+namespace {
+
+int validate_map_combine(const char* what, const float* maps, int64_t batch, int64_t n_maps, int64_t length,
+                         int64_t width, const float* weights, int dtype) {
+  if (!half_dtype(dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "%s: dtype must be DA_F16 or DA_BF16", what);
+  if (batch < 0 || length < 0 || n_maps < 1 || n_maps > da::kMapCombineMaxMaps)
+    return fail(DA_ERR_UNSUPPORTED, "%s: maps must be in [1, %d] and sizes >= 0", what, da::kMapCombineMaxMaps);
+  if (width < 8 || width % 8 || width > (1 << 20))
+    return fail(DA_ERR_UNSUPPORTED, "%s: width must be a positive multiple of 8", what);
+  if (!maps || !weights) return fail(DA_ERR_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (!aligned(maps, 16)) return fail(DA_ERR_ALIGNMENT, "%s: the map outputs must be 16-byte aligned", what);
+  return 0;
+}
+
+}  // namespace
+
+int da_map_combine(const float* maps, int64_t batch, int64_t n_maps, int64_t length, int64_t width,
+                   const float* weights, void* out, int out_dtype, da_stream_t stream) {
+  int rc = validate_map_combine("map combine", maps, batch, n_maps, length, width, weights, out_dtype);
+  if (rc) return rc;
+  if (batch * length == 0) return ok();
+  if (!out) return fail(DA_ERR_INVALID_ARGUMENT, "map combine: null pointer");
+  if (!aligned(out, 16)) return fail(DA_ERR_ALIGNMENT, "map combine: out must be 16-byte aligned");
+  const da::MapCombineArgs a{maps, weights, batch * length, length, static_cast<int>(n_maps), static_cast<int>(width),
+                             out_dtype, out, nullptr, nullptr, nullptr};
+  da::launch_map_combine(a, false, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("map combine");
+}
+
+int da_map_combine_backward(const float* maps, int64_t batch, int64_t n_maps, int64_t length, int64_t width,
+                            const float* weights, const void* grad, int grad_dtype, void* grad_maps,
+                            float* weight_sums, da_stream_t stream) {
+  int rc = validate_map_combine("map combine backward", maps, batch, n_maps, length, width, weights, grad_dtype);
+  if (rc) return rc;
+  if (batch * length == 0) return ok();
+  if (!grad || !grad_maps || !weight_sums) return fail(DA_ERR_INVALID_ARGUMENT, "map combine backward: null pointer");
+  if (!aligned(grad, 16) || !aligned(grad_maps, 16))
+    return fail(DA_ERR_ALIGNMENT, "map combine backward: grad and grad_maps must be 16-byte aligned");
+  const da::MapCombineArgs a{maps, weights, batch * length, length, static_cast<int>(n_maps), static_cast<int>(width),
+                             grad_dtype, nullptr, grad, grad_maps, weight_sums};
+  da::launch_map_combine(a, true, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("map combine backward");
+}
+
 int64_t da_sda_workspace_offset(int64_t batch, int64_t length, int64_t model_dim, int64_t qk_width,
                                 int which) {
   const int64_t tokens = batch * length;

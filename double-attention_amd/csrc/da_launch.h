@@ -207,6 +207,24 @@ struct RouteBwdRowsArgs {
 constexpr int kRouteBwdRowsMaxAtoms = 1 << 24;
 void launch_route_backward_rows(const RouteBwdRowsArgs& a, hipStream_t stream);
 
+// Map combine of the training path (map_combine.hip): out = sum_s w_s O_s
+// over per-map fp32 outputs O [B, S, T, D]; backward grad_maps = w_s dY (dtype)
+// and weight_sums[s] += <O_s, dY> (fp32 atomics; zeroed by the caller).
+struct MapCombineArgs {
+  const float* maps;      // [B, S, T, D] fp32
+  const float* weights;   // [S] fp32
+  int64_t rows;           // B * T
+  int64_t T;
+  int S, D;               // S <= 8, D a multiple of 8
+  int dtype;              // kF16 or kBF16: out, or grad and grad_maps
+  void* out;              // [B, T, D] (forward)
+  const void* grad;       // [B, T, D] (backward)
+  void* grad_maps;        // [B, S, T, D] (backward)
+  float* weight_sums;     // [S] (backward)
+};
+constexpr int kMapCombineMaxMaps = 8;
+void launch_map_combine(const MapCombineArgs& a, bool backward, hipStream_t stream);
+
 // LayerNorm over the last dimension (dim a multiple of 8, at most 4096).
 void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight, const void* bias, int param_dtype,
                        float eps, int dtype, void* out, hipStream_t stream);

@@ -1502,6 +1502,56 @@ def layer_norm_hip(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: f
     return out
 
 
+MAP_COMBINE_MAX_MAPS = 8
+
+
+def map_combine_supported(map_output: Tensor) -> bool:
+    """Whether ``map_combine`` / ``map_combine_backward`` take these per-map
+    outputs (fp32 ``[B, S, T, D]``, S <= 8, D a multiple of 8)."""
+
+    return (map_output.is_cuda and map_output.dtype == torch.float32 and map_output.dim() == 4
+            and 1 <= map_output.shape[1] <= MAP_COMBINE_MAX_MAPS and map_output.shape[3] % 8 == 0)
+
+
+def map_combine(map_output: Tensor, weights: Tensor, dtype: torch.dtype) -> Tensor:
+    """``einsum("s,bstd->btd", weights, map_output)`` (``modules.py:265-272``)
+    over fp32 per-map outputs ``[B, S, T, D]``: fp32 sum, one rounding to
+    ``dtype`` (``da_map_combine``)."""
+
+    batch, maps, length, width = map_output.shape
+    o = _aligned(map_output)
+    w = weights.detach().float().contiguous()
+    out = torch.empty(batch, length, width, dtype=dtype, device=o.device)
+    lib = _lib.get()
+    _lib.check(
+        lib.da_map_combine(o.data_ptr(), batch, maps, length, width, w.data_ptr(), out.data_ptr(),
+                           _half_code(dtype), _stream(o.device)),
+        "map combine",
+    )
+    return out
+
+
+def map_combine_backward(map_output: Tensor, weights: Tensor, grad: Tensor) -> tuple[Tensor, Tensor]:
+    """The backward of ``map_combine`` at ``grad`` ``[B, T, D]`` (16-bit):
+    ``(grad_maps, weight_grad)`` with grad_maps[b, s] = weights[s] grad[b]
+    rounded to grad's dtype and weight_grad[s] = <map_output[:, s], grad>
+    (fp32), in one pass (``da_map_combine_backward``)."""
+
+    batch, maps, length, width = map_output.shape
+    o = _aligned(map_output)
+    g = _aligned(grad)
+    w = weights.detach().float().contiguous()
+    grad_maps = torch.empty(batch, maps, length, width, dtype=g.dtype, device=o.device)
+    sums = torch.zeros(maps, dtype=torch.float32, device=o.device)
+    lib = _lib.get()
+    _lib.check(
+        lib.da_map_combine_backward(o.data_ptr(), batch, maps, length, width, w.data_ptr(), g.data_ptr(),
+                                    _half_code(g.dtype), grad_maps.data_ptr(), sums.data_ptr(), _stream(o.device)),
+        "map combine backward",
+    )
+    return grad_maps, sums
+
+
 def qkv_projection_hip(
     x: Tensor, query_weight: Tensor, key_weight: Tensor, value_weight: Tensor, value_bias: Tensor | None
 ) -> tuple[Tensor, Tensor]:

@@ -514,7 +514,10 @@ class _HipModuleFunction(torch.autograd.Function):
             else:
                 # The weights rounded to the map dtype, the sum in fp32 (as _combine).
                 factors = torch.softmax(module.map_mix_logits.detach(), dim=0).to(dtype).float()
-                mixed = (map_output.float() * factors[None, :, None, None]).sum(1).to(dtype)
+                if hip_ops.map_combine_supported(map_output):
+                    mixed = hip_ops.map_combine(map_output, factors, dtype)
+                else:
+                    mixed = (map_output.float() * factors[None, :, None, None]).sum(1).to(dtype)
         else:
             mixed = map_output.permute(0, 2, 1, 3).reshape(batch, length, maps * model_dim).to(dtype)
         mixed = hip_ops._aligned(mixed)
@@ -568,16 +571,21 @@ class _HipModuleFunction(torch.autograd.Function):
             if module.map_mix_logits is None:
                 d_maps = d_mixed.view(batch, 1, length, model_dim)
             else:
-                if wants("map_mix_logits"):
-                    # fp32 throughout: the per-map sums dY . O_s are large and
-                    # nearly equal, and the softmax backward differences them
-                    # (dY enters the fp32 product as its exact fp32 value).
+                # The per-map sums dY . O_s in fp32 throughout: they are large
+                # and nearly equal, and the softmax backward differences them
+                # (dY enters the fp32 product as its exact fp32 value).
+                # alpha_s dY is rounded once (bf16 x bf16 products are exact
+                # in fp32).  One pass over the map outputs when the kernel
+                # takes them.
+                if hip_ops.map_combine_supported(map_output):
+                    d_maps, per_map = hip_ops.map_combine_backward(
+                        map_output, factors, d_mixed.view(batch, length, model_dim))
+                else:
                     per_map = (map_output * d_mixed.view(batch, 1, length, model_dim)).sum(dim=(0, 2, 3))
+                    d_maps = d_mixed.view(batch, 1, length, model_dim) * factors.to(dtype).view(1, maps, 1, 1)
+                if wants("map_mix_logits"):
                     alpha = torch.softmax(module.map_mix_logits.detach().float(), dim=0)
                     grads["map_mix_logits"] = alpha * (per_map - (alpha * per_map).sum())
-                # bf16 x bf16 products are exact in the fp32 the op computes
-                # in, so this rounds alpha_s dY once, as the fp32 product would.
-                d_maps = d_mixed.view(batch, 1, length, model_dim) * factors.to(dtype).view(1, maps, 1, 1)
         else:
             d_maps = d_mixed.view(batch, length, maps, model_dim).transpose(1, 2)
         # Outer attention.  dq and dk stay fp32 (no rounding, no cast): the

@@ -37,6 +37,9 @@
  *                             + the block's residual adds
  *   da_layer_norm             attention_norm / feedforward_norm /    src/double_attention/modules.py:311, 313, 440
  *                             final_norm (nn.LayerNorm)
+ *   da_map_combine, da_map_combine_backward
+ *                             map_combine "weighted_sum" (einsum      src/double_attention/modules.py:265-272
+ *                             over the per-map outputs) and its backward
  *   da_shared_dictionary_attention_forward
  *                             SharedDictionaryAttention.forward      src/double_attention/modules.py:190-291
  */
@@ -425,6 +428,25 @@ int da_linear_ex(const void* x, int64_t rows, int64_t in_features, const void* w
  */
 int da_layer_norm(const void* x, int64_t rows, int64_t dim, const void* weight, const void* bias, int param_dtype,
                   float eps, int dtype, void* out, da_stream_t stream);
+
+/*
+ * The weighted map combine (modules.py:265-272: einsum("s,bstd->btd", w,
+ * map_output)) over fp32 per-map outputs, as the training path keeps them:
+ *   maps: [batch, n_maps, length, width] fp32, contiguous, 16-byte aligned
+ *   weights: [n_maps] fp32 (device), n_maps in [1, 8]; width a multiple of 8
+ *   out[b, t, :] = sum_s weights[s] maps[b, s, t, :], fp32 sum rounded once to
+ *   out_dtype (DA_F16 or DA_BF16), [batch, length, width], 16-byte aligned.
+ * Its backward at grad = dL/dout ([batch, length, width], grad_dtype):
+ *   grad_maps[b, s, t, :] = weights[s] grad[b, t, :] rounded to grad_dtype
+ *   ([batch, n_maps, length, width]), and weight_sums[s] += sum over b, t and
+ *   the features of maps[b, s, t, :] grad[b, t, :] (fp32 atomic adds: the
+ *   caller zeroes weight_sums; the gradient at the weights themselves).
+ */
+int da_map_combine(const float* maps, int64_t batch, int64_t n_maps, int64_t length, int64_t width,
+                   const float* weights, void* out, int out_dtype, da_stream_t stream);
+int da_map_combine_backward(const float* maps, int64_t batch, int64_t n_maps, int64_t length, int64_t width,
+                            const float* weights, const void* grad, int grad_dtype, void* grad_maps,
+                            float* weight_sums, da_stream_t stream);
 
 /* Whole SharedDictionaryAttention forward (modules.py:190-291): model_dim a
  * multiple of 64 in [64, 4096], routing_dim (and the grouped score width) in

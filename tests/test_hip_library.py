@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 23
+    assert len(names) == 25
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -362,3 +362,29 @@ def test_row_normalize_rejects_bad_arguments() -> None:
     assert bwd(out_dtype=split) == -3 and b"2 width" in h.da_last_error()
     assert bwd(out_dtype=split, ld_out=512, rows=0) == 0
     assert fwd(out_dtype=split) == -1                                     # not a forward dtype
+
+
+def test_map_combine_rejects_bad_arguments() -> None:
+    h = lib.get()
+    buf = ctypes.c_void_p(1 << 20)   # never dereferenced
+
+    def fwd(**kw):
+        args = dict(maps=buf, batch=2, n_maps=4, length=10, width=64, weights=buf, out=buf, out_dtype=lib.DA_BF16,
+                    stream=None)
+        args.update(kw)
+        return h.da_map_combine(*args.values())
+
+    def bwd(**kw):
+        args = dict(maps=buf, batch=2, n_maps=4, length=10, width=64, weights=buf, grad=buf, grad_dtype=lib.DA_BF16,
+                    grad_maps=buf, weight_sums=buf, stream=None)
+        args.update(kw)
+        return h.da_map_combine_backward(*args.values())
+
+    assert fwd(out_dtype=lib.DA_F32) == -1 and bwd(grad_dtype=7) == -1
+    assert fwd(n_maps=0) == -2 and fwd(n_maps=9) == -2 and b"maps must be in [1, 8]" in h.da_last_error()
+    assert bwd(width=12) == -2 and b"multiple of 8" in h.da_last_error()
+    assert fwd(maps=None) == -1 and bwd(weights=None) == -1 and b"null" in h.da_last_error()
+    assert fwd(out=None) == -1 and bwd(weight_sums=None) == -1
+    assert fwd(maps=ctypes.c_void_p((1 << 20) + 8)) == -3
+    assert bwd(grad_maps=ctypes.c_void_p((1 << 20) + 4)) == -3 and b"aligned" in h.da_last_error()
+    assert fwd(batch=0, out=None) == 0 and bwd(length=0, grad=None) == 0   # nothing to do

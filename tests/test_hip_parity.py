@@ -205,6 +205,30 @@ def test_row_normalize_and_backward(case) -> None:
         assert float(pair_err.max()) <= float(head_err) * 2.0 ** (-bits + 2)
 
 
+@pytest.mark.parametrize(("batch", "maps", "length", "width", "dtype"),
+                         [(8, 4, 1024, 512, torch.bfloat16), (3, 2, 77, 192, torch.float16), (1, 8, 5, 8, torch.bfloat16),
+                          (2, 1, 33, 64, torch.bfloat16)])
+def test_map_combine(batch, maps, length, width, dtype) -> None:
+    # The weighted map combine (einsum("s,bstd->btd", w, O)) against fp64 on
+    # the same fp32 inputs, within one rounding of the output; its backward:
+    # w_s dY bit-identical to the 16-bit product torch forms, and the per-map
+    # sums <O_s, dY> against fp64.
+    device = _device()
+    g = torch.Generator().manual_seed(batch * 100 + maps)
+    o = torch.randn(batch, maps, length, width, generator=g).to(device)
+    w = torch.softmax(torch.randn(maps, generator=g), 0).to(dtype).float().to(device)
+    out = da.hip_ops.map_combine(o, w, dtype)
+    exact = torch.einsum("s,bstd->btd", w.double().cpu(), o.double().cpu())
+    assert out.dtype == dtype and out.shape == (batch, length, width)
+    ulp = 2.0 ** (-8 if dtype == torch.bfloat16 else -11)
+    assert float(((out.double().cpu() - exact).abs() - ulp * exact.abs()).max()) <= 1e-6
+    dy = torch.randn(batch, length, width, generator=g).to(device, dtype)
+    d_maps, sums = da.hip_ops.map_combine_backward(o, w, dy)
+    assert torch.equal(d_maps, dy.view(batch, 1, length, width) * w.to(dtype).view(1, maps, 1, 1))
+    expected = (o.double() * dy.double().view(batch, 1, length, width)).sum(dim=(0, 2, 3))
+    torch.testing.assert_close(sums.double(), expected, rtol=1e-5, atol=1e-3)
+
+
 # ---------------------------------------------------------------- GEMMs
 
 
