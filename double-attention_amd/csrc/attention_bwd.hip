@@ -345,19 +345,25 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
   const int k_end = p.causal ? min(q0 + kQTile, p.Tk) : p.Tk;
   for (int k0 = wave * kQTile; k0 < k_end; k0 += 4 * kQTile) {
     f32x4 st[2][2];
+    // Both key blocks' fragments are loaded before the first MFMA (one
+    // memory round trip per tile; the scheduling barrier keeps the second
+    // block's loads ahead of the first block's products).
+    q8 kf[2][KS];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const TQ* krow = kbase + static_cast<int64_t>(min(k0 + kb * 16 + c, p.Tk - 1)) * p.k_st + 8 * g;
-      q8 kf[KS];
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) kf[kk] = load8(krow + kk * 32);
+      for (int kk = 0; kk < KS; ++kk) kf[kb][kk] = load8(krow + kk * 32);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
         st[kb][cb] = zero4();
 #pragma unroll
-        for (int kk = 0; kk < KS; ++kk) st[kb][cb] = Elem<TQ>::mma(kf[kk], qf[cb][kk], st[kb][cb]);
+        for (int kk = 0; kk < KS; ++kk) st[kb][cb] = Elem<TQ>::mma(kf[kb][kk], qf[cb][kk], st[kb][cb]);
       }
-    }
     // Lane (c, g) holds keys k0 + 16kb + 4g + i of query q0 + 16cb + c.
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
