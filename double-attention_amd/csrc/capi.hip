@@ -636,6 +636,18 @@ int da_map_combine_backward(const float* maps, int64_t batch, int64_t n_maps, in
   return check_launch("map combine backward");
 }
 
+int da_sum_partials(const float* partials, int64_t count, int64_t n, void* out, int out_dtype, da_stream_t stream) {
+  if (!half_dtype(out_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "sum partials: out_dtype must be DA_F16 or DA_BF16");
+  if (count < 1 || count > 1024 || n < 0 || n % 8)
+    return fail(DA_ERR_UNSUPPORTED, "sum partials: count must be in [1, 1024] and n a multiple of 8");
+  if (n == 0) return ok();
+  if (!partials || !out) return fail(DA_ERR_INVALID_ARGUMENT, "sum partials: null pointer");
+  if (!aligned(partials, 16) || !aligned(out, 16))
+    return fail(DA_ERR_ALIGNMENT, "sum partials: partials and out must be 16-byte aligned");
+  da::launch_sum_partials(partials, static_cast<int>(count), n, out, out_dtype, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("sum partials");
+}
+
 int64_t da_sda_workspace_offset(int64_t batch, int64_t length, int64_t model_dim, int64_t qk_width,
                                 int which) {
   const int64_t tokens = batch * length;

@@ -224,6 +224,8 @@ struct MapCombineArgs {
 };
 constexpr int kMapCombineMaxMaps = 8;
 void launch_map_combine(const MapCombineArgs& a, bool backward, hipStream_t stream);
+// out[i] = sum_c partials[c * n + i] rounded once to out_dtype (kF16 / kBF16); n % 8 == 0.
+void launch_sum_partials(const float* partials, int count, int64_t n, void* out, int out_dtype, hipStream_t stream);
 
 // LayerNorm over the last dimension (dim a multiple of 8, at most 4096).
 void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight, const void* bias, int param_dtype,

@@ -1,4 +1,5 @@
-// Map combine of the training path and its backward: the weighted sum over
+// Map combine of the training path and its backward, and the sum of split-K
+// partial products.  The map combine is the weighted sum over
 // the outer maps (the reference's map_combine "weighted_sum",
 // src/double_attention/modules.py:265-272, combined = einsum("s,bstd->btd",
 // softmax(map_mix_logits), map_output)) over per-map outputs the attention
@@ -12,6 +13,8 @@
 // every map's loads issued before they are used, in a grid-stride loop over
 // the tokens' chunks; the backward's per-map sums meet per workgroup in LDS
 // and leave as one atomic add per workgroup and map.
+// The partial sum adds the fp32 partial products of a split-K GEMM (the
+// training path's weight gradients) and rounds the sum once to 16 bits.
 #include "da_common.h"
 #include "da_launch.h"
 
@@ -146,7 +149,58 @@ void launch_t(const MapCombineArgs& a, bool backward, hipStream_t stream) {
   }
 }
 
+// out[i] = sum_c partials[c n + i] (fp32, in order c = 0, 1, ...), rounded once
+// to TO: eight elements per thread; with C > 0 partials known at compile time
+// every partial's loads are issued together, C = 0 loops over `count`.
+template <typename TO, int C>
+__global__ __launch_bounds__(kMixThreads) void sum_partials_kernel(const float* partials, int count, int64_t n,
+                                                                   TO* out) {
+  const int64_t n8 = n / 8;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kMixThreads + threadIdx.x; i < n8;
+       i += static_cast<int64_t>(gridDim.x) * kMixThreads) {
+    float acc[8];
+    if constexpr (C > 0) {
+      float x[C][8];
+#pragma unroll
+      for (int c = 0; c < C; ++c) load_f32x8(partials + static_cast<int64_t>(c) * n + 8 * i, x[c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        acc[e] = x[0][e];
+#pragma unroll
+        for (int c = 1; c < C; ++c) acc[e] += x[c][e];
+      }
+    } else {
+      float x[8];
+      load_f32x8(partials + 8 * i, acc);
+      for (int c = 1; c < count; ++c) {
+        load_f32x8(partials + static_cast<int64_t>(c) * n + 8 * i, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += x[e];
+      }
+    }
+    store8f(out + 8 * i, acc);
+  }
+}
+
+template <typename TO>
+void launch_sum_partials_t(const float* partials, int count, int64_t n, TO* out, hipStream_t stream) {
+  const dim3 grid(mix_grid(n / 8)), block(kMixThreads);
+  switch (count) {
+    case 1: hipLaunchKernelGGL((sum_partials_kernel<TO, 1>), grid, block, 0, stream, partials, count, n, out); break;
+    case 2: hipLaunchKernelGGL((sum_partials_kernel<TO, 2>), grid, block, 0, stream, partials, count, n, out); break;
+    case 4: hipLaunchKernelGGL((sum_partials_kernel<TO, 4>), grid, block, 0, stream, partials, count, n, out); break;
+    case 8: hipLaunchKernelGGL((sum_partials_kernel<TO, 8>), grid, block, 0, stream, partials, count, n, out); break;
+    default: hipLaunchKernelGGL((sum_partials_kernel<TO, 0>), grid, block, 0, stream, partials, count, n, out); break;
+  }
+}
+
 }  // namespace
+
+void launch_sum_partials(const float* partials, int count, int64_t n, void* out, int out_dtype, hipStream_t stream) {
+  if (n == 0) return;
+  if (out_dtype == kF16) launch_sum_partials_t(partials, count, n, static_cast<_Float16*>(out), stream);
+  else launch_sum_partials_t(partials, count, n, static_cast<__bf16*>(out), stream);
+}
 
 void launch_map_combine(const MapCombineArgs& a, bool backward, hipStream_t stream) {
   if (a.rows == 0) return;

@@ -712,14 +712,25 @@ def _mm_tn_f32(a: Tensor, b: Tensor, out_dtype: torch.dtype = torch.float32) -> 
     while s < SPLIT_K_MAX and k % (2 * s) == 0 and k // (2 * s) >= SPLIT_K_MIN_CHUNK and tiles * s < 512:
         s *= 2
     if s == 1:
-        # The library accumulates in fp32 and rounds once to its output dtype.
-        return _mm_f32(a.t(), b) if out_dtype == torch.float32 else torch.mm(a.t(), b).to(out_dtype)
+        # The library accumulates in fp32 and rounds once to its output dtype
+        # (the operands' dtype; another 16-bit dtype is rounded from fp32).
+        return torch.mm(a.t(), b) if out_dtype == a.dtype else _mm_f32(a.t(), b).to(out_dtype)
     chunk = k // s
     # Left operand: the transposed chunks of a (column-major views); right
     # operand: row-major chunks of b.
     a3 = a.as_strided((s, m, chunk), (chunk * a.stride(0), 1, a.stride(0)))
     b3 = b.as_strided((s, chunk, n), (chunk * b.stride(0), b.stride(0), 1))
-    return torch.bmm(a3, b3, out_dtype=torch.float32).sum(0).to(out_dtype)
+    partials = torch.bmm(a3, b3, out_dtype=torch.float32)
+    if out_dtype in (torch.float16, torch.bfloat16) and (m * n) % 8 == 0 and partials.is_cuda:
+        # The fp32 sum and the one rounding in one launch.
+        out = torch.empty(m, n, dtype=out_dtype, device=partials.device)
+        _lib.check(
+            _lib.get().da_sum_partials(partials.data_ptr(), s, m * n, out.data_ptr(), _half_code(out_dtype),
+                                       _stream(partials.device)),
+            "sum partials",
+        )
+        return out
+    return partials.sum(0).to(out_dtype)
 
 
 _ONES: dict[tuple[torch.device, int, torch.dtype], Tensor] = {}

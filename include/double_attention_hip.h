@@ -37,6 +37,7 @@
  *                             + the block's residual adds
  *   da_layer_norm             attention_norm / feedforward_norm /    src/double_attention/modules.py:311, 313, 440
  *                             final_norm (nn.LayerNorm)
+ *   da_sum_partials           (split-K weight gradients of the training path; no reference counterpart)
  *   da_map_combine, da_map_combine_backward
  *                             map_combine "weighted_sum" (einsum      src/double_attention/modules.py:265-272
  *                             over the per-map outputs) and its backward
@@ -444,6 +445,15 @@ int da_layer_norm(const void* x, int64_t rows, int64_t dim, const void* weight, 
  */
 int da_map_combine(const float* maps, int64_t batch, int64_t n_maps, int64_t length, int64_t width,
                    const float* weights, void* out, int out_dtype, da_stream_t stream);
+
+/*
+ * out[i] = sum over c < count of partials[c * n + i], summed in fp32 in order
+ * and rounded once to out_dtype (DA_F16 or DA_BF16): the split-K partial
+ * products of the training path's weight gradients (no counterpart in the
+ * reference, whose autograd forms them in one GEMM).  n a multiple of 8,
+ * count in [1, 1024], pointers 16-byte aligned.
+ */
+int da_sum_partials(const float* partials, int64_t count, int64_t n, void* out, int out_dtype, da_stream_t stream);
 int da_map_combine_backward(const float* maps, int64_t batch, int64_t n_maps, int64_t length, int64_t width,
                             const float* weights, const void* grad, int grad_dtype, void* grad_maps,
                             float* weight_sums, da_stream_t stream);

@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 25
+    assert len(names) == 26
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -388,3 +388,20 @@ def test_map_combine_rejects_bad_arguments() -> None:
     assert fwd(maps=ctypes.c_void_p((1 << 20) + 8)) == -3
     assert bwd(grad_maps=ctypes.c_void_p((1 << 20) + 4)) == -3 and b"aligned" in h.da_last_error()
     assert fwd(batch=0, out=None) == 0 and bwd(length=0, grad=None) == 0   # nothing to do
+
+
+def test_sum_partials_rejects_bad_arguments() -> None:
+    h = lib.get()
+    buf = ctypes.c_void_p(1 << 20)   # never dereferenced
+
+    def call(**kw):
+        args = dict(partials=buf, count=4, n=1024, out=buf, out_dtype=lib.DA_BF16, stream=None)
+        args.update(kw)
+        return h.da_sum_partials(*args.values())
+
+    assert call(out_dtype=lib.DA_F32) == -1
+    assert call(count=0) == -2 and call(count=1025) == -2 and call(n=12) == -2
+    assert b"multiple of 8" in h.da_last_error()
+    assert call(out=None) == -1 and b"null" in h.da_last_error()
+    assert call(partials=ctypes.c_void_p((1 << 20) + 4)) == -3
+    assert call(n=0, out=None) == 0

@@ -249,6 +249,35 @@ def test_weight_gradient_product(k, m, n, ld) -> None:
     rel = np.linalg.norm(np32(got) - expected) / np.linalg.norm(expected)
     print(f"[parity] a^T b {k}x{m}x{n} rel_l2={rel:.2e}", flush=True)
     assert rel <= 1e-5   # fp32 accumulation of exact 16-bit products
+    # Rounded once to 16 bits (the split-K partials summed in fp32 first, by
+    # da_sum_partials): the fp32 result's rounding, up to its last fp32 bits.
+    for dtype in DTYPES:
+        rounded = da.hip_ops._mm_tn_f32(a, b, dtype)
+        assert rounded.dtype == dtype
+        # Half a 16-bit ulp of v is at most 2^-8 |v| (bf16) or 2^-11 |v| (fp16);
+        # the two fp32 sums (partials summed in another order) differ by a few
+        # fp32 ulps of the largest entries, which reach small, cancelled ones.
+        half_ulp = 2.0 ** (-8 if dtype == torch.bfloat16 else -11)
+        diff = (rounded.float() - got).abs() - half_ulp * got.abs()
+        assert float(diff.max()) <= 2.0 ** -20 * float(got.abs().max()), dtype
+
+
+def test_sum_partials() -> None:
+    # da_sum_partials against fp64 sums of the partials, for every partial
+    # count it specializes (1, 2, 4, 8) and the generic loop (3, 16).
+    device = _device()
+    lib = da._lib.get()
+    for count in (1, 2, 3, 4, 8, 16):
+        for dtype in DTYPES:
+            g = torch.Generator().manual_seed(count)
+            parts = torch.randn(count, 1000 * 8, generator=g).to(device)
+            out = torch.empty(1000 * 8, dtype=dtype, device=device)
+            da._lib.check(lib.da_sum_partials(parts.data_ptr(), count, parts.shape[1], out.data_ptr(),
+                                              da.hip_ops._half_code(dtype), da.hip_ops._stream(device)),
+                          "sum partials")
+            exact = parts.double().sum(0)
+            ulp = 2.0 ** (-8 if dtype == torch.bfloat16 else -11)
+            assert float(((out.double() - exact).abs() - ulp * exact.abs() - 1e-6).max()) <= 0, (count, dtype)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
