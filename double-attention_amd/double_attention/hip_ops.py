@@ -745,9 +745,9 @@ def column_sums(x: Tensor, out_dtype: torch.dtype) -> Tensor:
     ones = _ONES.get(key)
     if ones is None:
         ones = _ONES[key] = torch.ones(1, x.shape[0], dtype=x.dtype, device=x.device)
-    if out_dtype == torch.float32:
-        return _mm_f32(ones, x).view(-1)
-    return torch.mm(ones, x).view(-1).to(out_dtype)
+    if out_dtype == x.dtype:
+        return torch.mm(ones, x).view(-1)
+    return _mm_f32(ones, x).view(-1).to(out_dtype)
 
 
 def _route_backward_rows(

@@ -698,6 +698,53 @@ class _HipModuleFunction(torch.autograd.Function):
         return (None, None, dx, d_key, d_val, *tail)
 
 
+class _HipFeedForwardFunction(torch.autograd.Function):
+    """``x + W2 GELU(W1 h + b1) + b2`` (the block's feed-forward and its
+    residual add, reference ``modules.py:318-330, 343-346``) on the library's
+    GEMM, with a native backward.
+
+    Forward: z = W1 h + b1 (one GEMM, bias in its epilogue), u = GELU(z)
+    (exact, ``nn.GELU()``), y = W2 u + b2 + x (one GEMM, bias and residual in
+    its epilogue); z and u are kept.  Backward: dU = dY W2, dZ = dU GELU'(z),
+    dH = dZ W1, the weight gradients as split-K library products rounded once
+    and the bias gradients as column sums (library GEMVs), where torch's
+    autograd would reduce the 16-bit gradients over the rows.
+    """
+
+    @staticmethod
+    def forward(ctx, x, h, w1, b1, w2, b2):  # type: ignore[override]
+        from . import hip_ops
+
+        dtype = x.dtype
+        cast = lambda t: t if t is None or t.dtype == dtype else t.to(dtype)  # noqa: E731
+        z = hip_ops.linear_hip(h, cast(w1.detach()), b1.detach() if b1 is not None else None)
+        u = F.gelu(z)
+        y = hip_ops.linear_hip(u, cast(w2.detach()), b2.detach() if b2 is not None else None, residual=x.detach())
+        ctx.save_for_backward(h, z, u, w1, w2)
+        ctx.has_bias = (b1 is not None, b2 is not None)
+        ctx.bias_dtypes = (b1.dtype if b1 is not None else None, b2.dtype if b2 is not None else None)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad):  # type: ignore[override]
+        from . import hip_ops
+
+        h, z, u, w1, w2 = ctx.saved_tensors
+        dtype = z.dtype
+        rows = z.numel() // z.shape[-1]
+        dy = grad.reshape(rows, -1).to(dtype)
+        h2, z2, u2 = h.reshape(rows, -1), z.reshape(rows, -1), u.reshape(rows, -1)
+        du = torch.mm(dy, w2.detach().to(dtype))
+        d_w2 = hip_ops._mm_tn_f32(dy, u2, w2.dtype) if ctx.needs_input_grad[4] else None
+        d_b2 = hip_ops.column_sums(dy, ctx.bias_dtypes[1]) if ctx.has_bias[1] and ctx.needs_input_grad[5] else None
+        dz = torch.ops.aten.gelu_backward(du, z2)
+        d_w1 = hip_ops._mm_tn_f32(dz, h2, w1.dtype) if ctx.needs_input_grad[2] else None
+        d_b1 = hip_ops.column_sums(dz, ctx.bias_dtypes[0]) if ctx.has_bias[0] and ctx.needs_input_grad[3] else None
+        dh = torch.mm(dz, w1.detach().to(dtype)).view(h.shape) if ctx.needs_input_grad[1] else None
+        dx = grad if ctx.needs_input_grad[0] else None
+        return dx, dh, d_w1, d_b1, d_w2, d_b2
+
+
 class DoubleAttentionBlock(nn.Module):
     """Pre-norm transformer block around ``SharedDictionaryAttention`` (``modules.py:294-356``)."""
 
@@ -822,8 +869,35 @@ class DoubleAttentionBlock(nn.Module):
         )
         normalized_x = self.feedforward_norm(x)
         if not self.attention.config.q_dictionary_feedforward:
+            if self._hip_feedforward_applies(x, normalized_x):
+                first, second = self.feedforward[0], self.feedforward[2]
+                return _HipFeedForwardFunction.apply(x, normalized_x, first.weight, first.bias, second.weight,
+                                                     second.bias)
             return x + self.feedforward(normalized_x)
         return self._q_dictionary_feedforward(x, normalized_x, bank, normalized_dictionary)
+
+    def _hip_feedforward_applies(self, x: Tensor, normalized_x: Tensor) -> bool:
+        """Whether the feed-forward runs as ``_HipFeedForwardFunction``: the
+        attention's backend resolves to HIP for this input, the activations
+        are 16-bit with the parameters in their dtype or fp32, and no dropout
+        is active (eval, or p = 0)."""
+
+        cfg = self.attention.config
+        first, second = self.feedforward[0], self.feedforward[2]
+        if cfg.backend == "torch" or not isinstance(first, nn.Linear) or not isinstance(second, nn.Linear):
+            return False
+        if self.training and self.feedforward[3].p > 0:
+            return False
+        dtype = x.dtype
+        if dtype not in (torch.float16, torch.bfloat16) or normalized_x.dtype != dtype or not x.is_cuda:
+            return False
+        if torch.is_autocast_enabled("cuda"):
+            return False
+        if any(p.dtype not in (dtype, torch.float32) for p in (first.weight, second.weight)):
+            return False
+        if first.in_features % 32 or second.in_features % 32 or first.out_features % 4 or second.out_features % 4:
+            return False
+        return resolve_backend(cfg.backend, (_Spec(True, dtype),)) == "hip"  # type: ignore[arg-type]
 
 
 class DoubleAttentionStack(nn.Module):

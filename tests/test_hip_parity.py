@@ -17,6 +17,7 @@ import math
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 import double_attention as da
 import oracle
@@ -260,6 +261,46 @@ def test_weight_gradient_product(k, m, n, ld) -> None:
         half_ulp = 2.0 ** (-8 if dtype == torch.bfloat16 else -11)
         diff = (rounded.float() - got).abs() - half_ulp * got.abs()
         assert float(diff.max()) <= 2.0 ** -20 * float(got.abs().max()), dtype
+
+
+def test_feedforward_function() -> None:
+    # The block's feed-forward with its residual add on the library's GEMM
+    # and its native backward (modules._HipFeedForwardFunction) against fp32
+    # autograd of the same block, beside the bf16 torch path: every gradient
+    # (x, the normalized input, both weights and biases) within
+    # max(2e-2, 2x) the bf16 torch path's relative error.
+    device = _device()
+    torch.manual_seed(3)
+    config = da.experiment_config("qk2-s2", backend="hip")
+    block = da.DoubleAttentionBlock(config).to(device, torch.bfloat16)
+    ff = block.feedforward
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(4, 64, config.model_dim, generator=g).to(device, torch.bfloat16)
+    h = torch.randn(4, 64, config.model_dim, generator=g).to(device, torch.bfloat16)
+    w = torch.randn(4, 64, config.model_dim, generator=g).to(device)
+    params = [ff[0].weight, ff[0].bias, ff[2].weight, ff[2].bias]
+
+    def grads(fn, dtype):
+        xi = x.detach().to(dtype).requires_grad_()
+        hi = h.detach().to(dtype).requires_grad_()
+        ps = [p.detach().to(dtype).requires_grad_() for p in params]
+        y = fn(xi, hi, ps)
+        (y.float() * w).sum().backward()
+        return [y.detach().float()] + [t.grad.float() for t in (xi, hi, *ps)]
+
+    def torch_ff(xi, hi, ps):
+        return xi + F.linear(F.gelu(F.linear(hi, ps[0], ps[1])), ps[2], ps[3])
+
+    hip = grads(lambda xi, hi, ps: da.modules._HipFeedForwardFunction.apply(xi, hi, *ps), torch.bfloat16)
+    ref = grads(torch_ff, torch.float32)
+    t16 = grads(torch_ff, torch.bfloat16)
+    for name, a, b, c in zip(("y", "x", "h", "w1", "b1", "w2", "b2"), hip, t16, ref):
+        rel = float((a - c).norm() / c.norm())
+        rel16 = float((b - c).norm() / c.norm())
+        print(f"[parity] feed-forward d{name}: hip {rel:.2e} torch bf16 {rel16:.2e}", flush=True)
+        assert rel <= max(2e-2, 2 * rel16), name
+    # The block routes its training-path feed-forward through the function.
+    assert block._hip_feedforward_applies(x, h)
 
 
 def test_sum_partials() -> None:
