@@ -648,6 +648,22 @@ int da_sum_partials(const float* partials, int64_t count, int64_t n, void* out, 
   return check_launch("sum partials");
 }
 
+int da_layer_norm_backward(const void* x, const void* grad, int64_t rows, int64_t dim, const void* weight,
+                           int param_dtype, float eps, int dtype, void* grad_x, float* grad_params, da_stream_t stream) {
+  if (!half_dtype(dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "layer_norm backward: dtype must be DA_F16 or DA_BF16");
+  if (weight && !any_dtype(param_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "layer_norm backward: bad parameter dtype");
+  if (rows < 0 || dim < 8 || dim % 8 || dim > 4096)
+    return fail(DA_ERR_UNSUPPORTED, "layer_norm backward: dim must be a multiple of 8 in [8, 4096]");
+  if (rows == 0) return ok();
+  if (!x || !grad || !grad_x || !grad_params) return fail(DA_ERR_INVALID_ARGUMENT, "layer_norm backward: null pointer");
+  if (!aligned(x, 16) || !aligned(grad, 16) || !aligned(grad_x, 16) || !aligned(weight, 16))
+    return fail(DA_ERR_ALIGNMENT, "layer_norm backward: x, grad, grad_x and weight must be 16-byte aligned");
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(DA_ERR_INVALID_ARGUMENT, "layer_norm backward: bad eps");
+  da::launch_layer_norm_backward(x, grad, rows, static_cast<int>(dim), weight, param_dtype, eps, dtype, grad_x,
+                                 grad_params, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("layer_norm backward");
+}
+
 int64_t da_sda_workspace_offset(int64_t batch, int64_t length, int64_t model_dim, int64_t qk_width,
                                 int which) {
   const int64_t tokens = batch * length;

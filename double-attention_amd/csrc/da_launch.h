@@ -230,6 +230,10 @@ void launch_sum_partials(const float* partials, int count, int64_t n, void* out,
 // LayerNorm over the last dimension (dim a multiple of 8, at most 4096).
 void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight, const void* bias, int param_dtype,
                        float eps, int dtype, void* out, hipStream_t stream);
+// Its backward: dx (dtype) and the fp32 parameter gradients added into
+// dparams [2 * dim] (weight then bias; zeroed by the caller).
+void launch_layer_norm_backward(const void* x, const void* dy, int64_t rows, int dim, const void* weight,
+                                int param_dtype, float eps, int dtype, void* dx, float* dparams, hipStream_t stream);
 // Launch shape of the attention for a problem: value slice width, waves per
 // query tile, sub-streams, query tiles, the stream split of long key ranges (run length, 0
 // = none; runs per sequence and slice) and the bytes of partials it needs

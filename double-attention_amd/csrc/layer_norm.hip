@@ -87,6 +87,115 @@ __global__ __launch_bounds__(64 * kLnRowsPerBlock) void layer_norm_kernel(const 
   }
 }
 
+// Backward of the LayerNorm above at dy = dL/dy, the statistics formed again
+// from x (fp32, two passes as the forward forms them):
+//   xh = (x - mean) rstd,  g = dy w,
+//   dx = rstd (g - mean(g) - xh mean(g xh))                 (one rounding)
+//   dw += sum over rows of dy xh,  db += sum over rows of dy (fp32)
+// A wave takes rows wave, wave + W, ... (W = waves in the grid), each row
+// held in registers, the next row's loads issued before this row's sums.
+// The row sums take two rounds of wave reductions, two independent sums
+// each: (sum x, sum g), then (sum (x - mean)^2, sum g (x - mean)).  The
+// parameter gradients stay in the lanes' registers over the wave's rows,
+// meet across the workgroup's waves in LDS and leave as one fp32 atomic add
+// per workgroup and column (the caller zeroes them).
+template <typename T, int CH>
+__global__ __launch_bounds__(64 * kLnRowsPerBlock) void layer_norm_backward_kernel(
+    const T* x, const T* dy, int64_t rows, int dim, const void* weight, int pdt, float eps, T* dx, float* dparams) {
+  extern __shared__ float part[];   // [2][dim]: weight, then bias gradients
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int nch = dim / 8;
+  const float inv_dim = 1.f / static_cast<float>(dim);
+  float w[CH][8], gw[CH][8], gb[CH][8];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    load_params8(weight, pdt, static_cast<int64_t>(min(lane + 64 * k, nch - 1)) * 8, w[k], 1.f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gw[k][e] = gb[k][e] = 0.f;
+  }
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kLnRowsPerBlock;
+  typename Elem<T>::v8 rx[CH], rg[CH];
+  auto load_row = [&](int64_t row) {
+    const int64_t r = min(row, rows - 1);
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int64_t c = static_cast<int64_t>(min(lane + 64 * k, nch - 1)) * 8;
+      rx[k] = load8(x + r * dim + c);
+      rg[k] = load8(dy + r * dim + c);
+    }
+  };
+  int64_t row = static_cast<int64_t>(blockIdx.x) * kLnRowsPerBlock + wave;
+  if (row < rows) load_row(row);
+  for (; row < rows; row += step) {
+    float v[CH][8], g[CH][8];
+    float sx = 0.f, sg = 0.f;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const bool valid = lane + 64 * k < nch;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[k][e] = valid ? static_cast<float>(rx[k][e]) : 0.f;
+        const float d = valid ? static_cast<float>(rg[k][e]) : 0.f;
+        gb[k][e] += d;
+        g[k][e] = d;
+        sg += d * w[k][e];
+        sx += v[k][e];
+      }
+    }
+    load_row(row + step);   // the next row (clamped past the last) while this one is reduced
+    __builtin_amdgcn_sched_barrier(0);
+    const float mean = wave_sum(sx) * inv_dim;
+    const float a = wave_sum(sg) * inv_dim;
+    float sq = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const bool valid = lane + 64 * k < nch;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = valid ? v[k][e] - mean : 0.f;
+        v[k][e] = d;
+        sq += d * d;
+        sgx += g[k][e] * w[k][e] * d;
+      }
+    }
+    const float rstd = 1.f / sqrtf(wave_sum(sq) * inv_dim + eps);
+    const float bq = wave_sum(sgx) * inv_dim * rstd;   // mean(g xh)
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int ci = lane + 64 * k;
+      typename Elem<T>::v8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xh = v[k][e] * rstd;
+        gw[k][e] += g[k][e] * xh;
+        o[e] = static_cast<T>(rstd * (g[k][e] * w[k][e] - a - xh * bq));
+      }
+      if (ci < nch) store16B(dx + row * dim + ci * 8, __builtin_bit_cast(u32x4, o));
+    }
+  }
+  // Parameter gradients: the workgroup's waves add theirs into one LDS copy
+  // in turn, then one atomic add per workgroup and column.
+  for (int q = 0; q < kLnRowsPerBlock; ++q) {
+    if (wave == q) {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        const int ci = lane + 64 * k;
+        if (ci >= nch) break;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float* pw = part + ci * 8 + e;
+          float* pb = part + dim + ci * 8 + e;
+          *pw = q == 0 ? gw[k][e] : *pw + gw[k][e];
+          *pb = q == 0 ? gb[k][e] : *pb + gb[k][e];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  for (int i = static_cast<int>(threadIdx.x); i < 2 * dim; i += 64 * kLnRowsPerBlock) unsafeAtomicAdd(dparams + i, part[i]);
+}
+
 template <typename T>
 static void launch_ln_t(const void* x, int64_t rows, int dim, const void* w, const void* b, int pdt, float eps,
                         void* out, hipStream_t s) {
@@ -99,6 +208,36 @@ static void launch_ln_t(const void* x, int64_t rows, int dim, const void* w, con
   else if (nch <= 128) hipLaunchKernelGGL((layer_norm_kernel<T, 2>), grid, block, 0, s, xt, rows, dim, w, b, pdt, eps, ot);
   else if (nch <= 256) hipLaunchKernelGGL((layer_norm_kernel<T, 4>), grid, block, 0, s, xt, rows, dim, w, b, pdt, eps, ot);
   else hipLaunchKernelGGL((layer_norm_kernel<T, 8>), grid, block, 0, s, xt, rows, dim, w, b, pdt, eps, ot);
+}
+
+template <typename T>
+static void launch_ln_bwd_t(const void* x, const void* dy, int64_t rows, int dim, const void* w, int pdt, float eps,
+                            void* dx, float* dparams, hipStream_t s) {
+  // One workgroup per CU, each wave then looping over its rows (more
+  // workgroups add atomic adds per column faster than they add speed).
+  const int64_t blocks = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+  const dim3 grid(static_cast<unsigned>(blocks < 256 ? blocks : 256));
+  const dim3 block(64 * kLnRowsPerBlock);
+  const size_t lds = 2 * static_cast<size_t>(dim) * sizeof(float);   // <= 32 KiB
+  const int nch = dim / 8;
+  const T* xt = static_cast<const T*>(x);
+  const T* gt = static_cast<const T*>(dy);
+  T* ot = static_cast<T*>(dx);
+  if (nch <= 64)
+    hipLaunchKernelGGL((layer_norm_backward_kernel<T, 1>), grid, block, lds, s, xt, gt, rows, dim, w, pdt, eps, ot, dparams);
+  else if (nch <= 128)
+    hipLaunchKernelGGL((layer_norm_backward_kernel<T, 2>), grid, block, lds, s, xt, gt, rows, dim, w, pdt, eps, ot, dparams);
+  else if (nch <= 256)
+    hipLaunchKernelGGL((layer_norm_backward_kernel<T, 4>), grid, block, lds, s, xt, gt, rows, dim, w, pdt, eps, ot, dparams);
+  else
+    hipLaunchKernelGGL((layer_norm_backward_kernel<T, 8>), grid, block, lds, s, xt, gt, rows, dim, w, pdt, eps, ot, dparams);
+}
+
+void launch_layer_norm_backward(const void* x, const void* dy, int64_t rows, int dim, const void* weight,
+                                int param_dtype, float eps, int dtype, void* dx, float* dparams, hipStream_t stream) {
+  if (rows == 0) return;
+  if (dtype == kF16) launch_ln_bwd_t<_Float16>(x, dy, rows, dim, weight, param_dtype, eps, dx, dparams, stream);
+  else launch_ln_bwd_t<__bf16>(x, dy, rows, dim, weight, param_dtype, eps, dx, dparams, stream);
 }
 
 void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight, const void* bias, int param_dtype,

@@ -194,6 +194,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_linear": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _vp, _vp]),
     "da_linear_ex": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "da_layer_norm": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _f32, _i32, _vp, _vp]),
+    "da_layer_norm_backward": (_i32, [_vp, _vp, _i64, _i64, _vp, _i32, _f32, _i32, _vp, _vp, _vp]),
     "da_map_combine": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _vp]),
     "da_sum_partials": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
     "da_map_combine_backward": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _vp]),

@@ -1513,6 +1513,33 @@ def layer_norm_hip(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: f
     return out
 
 
+def layer_norm_backward_hip(
+    x: Tensor, grad: Tensor, weight: Tensor | None, eps: float = 1e-5
+) -> tuple[Tensor, Tensor, Tensor]:
+    """The backward of ``layer_norm_hip`` (autograd of ``nn.LayerNorm``) at
+    ``grad``: ``(dx, d_weight, d_bias)``, dx in x's dtype, the parameter
+    gradients fp32 sums over the rows (``da_layer_norm_backward``; the
+    statistics are formed again from x)."""
+
+    _require_cuda(x)
+    dim = x.shape[-1]
+    xc = _aligned(x.detach())
+    g = _aligned(grad.detach().to(x.dtype))
+    w = None if weight is None else _aligned(weight.detach())
+    dx = torch.empty_like(xc)
+    dparams = torch.zeros(2, dim, dtype=torch.float32, device=x.device)
+    lib = _lib.get()
+    _lib.check(
+        lib.da_layer_norm_backward(
+            xc.data_ptr(), g.data_ptr(), xc.numel() // dim if dim else 0, dim, _ptr(w),
+            dtype_code(w.dtype) if w is not None else _lib.DA_F32, float(eps), _half_code(x.dtype), dx.data_ptr(),
+            dparams.data_ptr(), _stream(x.device),
+        ),
+        "layer_norm_hip backward",
+    )
+    return dx.view(x.shape), dparams[0], dparams[1]
+
+
 MAP_COMBINE_MAX_MAPS = 8
 
 

@@ -698,6 +698,59 @@ class _HipModuleFunction(torch.autograd.Function):
         return (None, None, dx, d_key, d_val, *tail)
 
 
+class _HipLayerNormFunction(torch.autograd.Function):
+    """``nn.LayerNorm`` over the last dimension (the blocks' and the LM's
+    norms, reference ``modules.py:311, 313, 440``) on the library's LayerNorm
+    kernel, with its native backward (``da_layer_norm_backward``: dx and the
+    parameter gradients in one pass over x and dY)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps):  # type: ignore[override]
+        from . import hip_ops
+
+        ctx.save_for_backward(x, weight)
+        ctx.eps = eps
+        ctx.param_dtypes = (weight.dtype if weight is not None else None, bias.dtype if bias is not None else None)
+        return hip_ops.layer_norm_hip(x, weight, bias, eps)
+
+    @staticmethod
+    def backward(ctx, grad):  # type: ignore[override]
+        from . import hip_ops
+
+        x, weight = ctx.saved_tensors
+        dx, d_weight, d_bias = hip_ops.layer_norm_backward_hip(x, grad, weight, ctx.eps)
+        wd, bd = ctx.param_dtypes
+        return (dx if ctx.needs_input_grad[0] else None,
+                d_weight.to(wd) if wd is not None and ctx.needs_input_grad[1] else None,
+                d_bias.to(bd) if bd is not None and ctx.needs_input_grad[2] else None, None)
+
+
+def _hip_layer_norm_applies(norm: nn.Module, x: Tensor, backend: str) -> bool:
+    """Whether ``norm`` (an ``nn.LayerNorm``) runs as ``_HipLayerNormFunction``
+    on x: a 16-bit CUDA input whose backend resolves to HIP, one normalized
+    dimension (a multiple of 8 up to 4096), weight and bias both present or
+    both absent in one dtype."""
+
+    if backend == "torch" or not isinstance(norm, nn.LayerNorm) or len(norm.normalized_shape) != 1:
+        return False
+    if x.dtype not in (torch.float16, torch.bfloat16) or not x.is_cuda or torch.is_autocast_enabled("cuda"):
+        return False
+    dim = norm.normalized_shape[0]
+    if dim % 8 or dim > 4096 or x.shape[-1] != dim:
+        return False
+    if (norm.weight is None) != (norm.bias is None):
+        return False
+    if norm.weight is not None and norm.weight.dtype != norm.bias.dtype:
+        return False
+    return resolve_backend(backend, (_Spec(True, x.dtype),)) == "hip"  # type: ignore[arg-type]
+
+
+def _layer_norm(norm: nn.LayerNorm, x: Tensor, backend: str) -> Tensor:
+    if _hip_layer_norm_applies(norm, x, backend):
+        return _HipLayerNormFunction.apply(x, norm.weight, norm.bias, norm.eps)
+    return norm(x)
+
+
 class _HipFeedForwardFunction(torch.autograd.Function):
     """``x + W2 GELU(W1 h + b1) + b2`` (the block's feed-forward and its
     residual add, reference ``modules.py:318-330, 343-346``) on the library's
@@ -864,10 +917,11 @@ class DoubleAttentionBlock(nn.Module):
         fused = self._hip_block(x, bank, normalized_dictionary)
         if fused is not None:
             return fused
+        backend = self.attention.config.backend
         x = x + self.attention(
-            self.attention_norm(x), bank=bank, normalized_dictionary=normalized_dictionary
+            _layer_norm(self.attention_norm, x, backend), bank=bank, normalized_dictionary=normalized_dictionary
         )
-        normalized_x = self.feedforward_norm(x)
+        normalized_x = _layer_norm(self.feedforward_norm, x, backend)
         if not self.attention.config.q_dictionary_feedforward:
             if self._hip_feedforward_applies(x, normalized_x):
                 first, second = self.feedforward[0], self.feedforward[2]
@@ -985,14 +1039,15 @@ class DoubleAttentionLM(nn.Module):
         self.lm_head.weight = self.token_embedding.weight
 
     def _final_norm(self, hidden: Tensor) -> Tensor:
-        # On the HIP path (inference) the final LayerNorm is the library's kernel.
+        # On the HIP path the final LayerNorm is the library's kernel (with
+        # its native backward when training).
         attention = self.stack.blocks[0].attention
         needs_grad = torch.is_grad_enabled() and any(p.requires_grad for p in self.final_norm.parameters())
         if not needs_grad and attention._hip_inference_dtype(hidden, self.stack.banks[0]) == hidden.dtype:
             from . import hip_ops
 
             return hip_ops.layer_norm_hip(hidden, self.final_norm.weight, self.final_norm.bias, self.final_norm.eps)
-        return self.final_norm(hidden)
+        return _layer_norm(self.final_norm, hidden, attention.config.backend)
 
     def forward(self, token_ids: Tensor, targets: Tensor | None = None) -> tuple[Tensor, Tensor | None]:
         if token_ids.ndim != 2:

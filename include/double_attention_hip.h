@@ -35,8 +35,9 @@
  *   da_linear                 self.output                            src/double_attention/modules.py:117-121, 272
  *   da_linear_ex              DoubleAttentionBlock.feedforward       src/double_attention/modules.py:318-330, 343-346
  *                             + the block's residual adds
- *   da_layer_norm             attention_norm / feedforward_norm /    src/double_attention/modules.py:311, 313, 440
- *                             final_norm (nn.LayerNorm)
+ *   da_layer_norm, da_layer_norm_backward
+ *                             attention_norm / feedforward_norm /    src/double_attention/modules.py:311, 313, 440
+ *                             final_norm (nn.LayerNorm) and its autograd backward
  *   da_sum_partials           (split-K weight gradients of the training path; no reference counterpart)
  *   da_map_combine, da_map_combine_backward
  *                             map_combine "weighted_sum" (einsum      src/double_attention/modules.py:265-272
@@ -429,6 +430,19 @@ int da_linear_ex(const void* x, int64_t rows, int64_t in_features, const void* w
  */
 int da_layer_norm(const void* x, int64_t rows, int64_t dim, const void* weight, const void* bias, int param_dtype,
                   float eps, int dtype, void* out, da_stream_t stream);
+
+/*
+ * Backward of da_layer_norm (autograd of nn.LayerNorm) at grad = dL/dout
+ * ([rows, dim] of dtype): the statistics are formed again from x in fp32;
+ * grad_x = rstd (g - mean(g) - xh mean(g xh)) with xh = (x - mean) rstd and
+ * g = grad weight (weight of param_dtype, or NULL for 1), rounded once to
+ * dtype; grad_params[0, dim) += sum over rows of grad xh (the weight's
+ * gradient) and grad_params[dim, 2 dim) += sum over rows of grad (the
+ * bias's), fp32 atomic adds (the caller zeroes grad_params).  Same layout
+ * rules as da_layer_norm.
+ */
+int da_layer_norm_backward(const void* x, const void* grad, int64_t rows, int64_t dim, const void* weight,
+                           int param_dtype, float eps, int dtype, void* grad_x, float* grad_params, da_stream_t stream);
 
 /*
  * The weighted map combine (modules.py:265-272: einsum("s,bstd->btd", w,

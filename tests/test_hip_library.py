@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 26
+    assert len(names) == 27
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -405,3 +405,21 @@ def test_sum_partials_rejects_bad_arguments() -> None:
     assert call(out=None) == -1 and b"null" in h.da_last_error()
     assert call(partials=ctypes.c_void_p((1 << 20) + 4)) == -3
     assert call(n=0, out=None) == 0
+
+
+def test_layer_norm_backward_rejects_bad_arguments() -> None:
+    h = lib.get()
+    buf = ctypes.c_void_p(1 << 20)   # never dereferenced
+
+    def call(**kw):
+        args = dict(x=buf, grad=buf, rows=10, dim=512, weight=buf, param_dtype=lib.DA_BF16, eps=1e-5,
+                    dtype=lib.DA_BF16, grad_x=buf, grad_params=buf, stream=None)
+        args.update(kw)
+        return h.da_layer_norm_backward(*args.values())
+
+    assert call(dtype=lib.DA_F32) == -1 and call(param_dtype=9) == -1
+    assert call(dim=12) == -2 and call(dim=8192) == -2 and b"multiple of 8" in h.da_last_error()
+    assert call(grad_params=None) == -1 and b"null" in h.da_last_error()
+    assert call(grad=ctypes.c_void_p((1 << 20) + 8)) == -3
+    assert call(eps=-1.0) == -1
+    assert call(rows=0, x=None) == 0

@@ -263,6 +263,42 @@ def test_weight_gradient_product(k, m, n, ld) -> None:
         assert float(diff.max()) <= 2.0 ** -20 * float(got.abs().max()), dtype
 
 
+@pytest.mark.parametrize(("rows", "dim", "dtype", "param_dtype"), [(4096, 512, torch.bfloat16, torch.bfloat16),
+                                                                    (77, 192, torch.float16, torch.float32),
+                                                                    (3, 4096, torch.bfloat16, torch.float32)])
+def test_layer_norm_function(rows, dim, dtype, param_dtype) -> None:
+    # nn.LayerNorm on the library's kernels with the native backward
+    # (modules._HipLayerNormFunction) against fp32 autograd on the same
+    # rounded inputs, beside the 16-bit torch path: every output and gradient
+    # within max(2e-2, 2x) the torch path's relative error (the incoming
+    # gradient is 16-bit on both, which bounds the parameter gradients too).
+    device = _device()
+    g = torch.Generator().manual_seed(rows + dim)
+    norm = torch.nn.LayerNorm(dim).to(device, param_dtype)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(dim, generator=g))
+        norm.bias.copy_(0.1 * torch.randn(dim, generator=g))
+    x = (torch.randn(rows, dim, generator=g) * 3 + 1).to(device, dtype)
+    w = torch.randn(rows, dim, generator=g).to(device)
+
+    def run(fn, xdtype, pdtype):
+        xi = x.detach().to(xdtype).requires_grad_()
+        wi = norm.weight.detach().to(pdtype).requires_grad_()
+        bi = norm.bias.detach().to(pdtype).requires_grad_()
+        y = fn(xi, wi, bi)
+        (y.float() * w).sum().backward()
+        return [y.detach().float(), xi.grad.float(), wi.grad.float(), bi.grad.float()]
+
+    hip = run(lambda xi, wi, bi: da.modules._HipLayerNormFunction.apply(xi, wi, bi, norm.eps), dtype, param_dtype)
+    ref = run(lambda xi, wi, bi: F.layer_norm(xi, (dim,), wi, bi, norm.eps), torch.float32, torch.float32)
+    t16 = run(lambda xi, wi, bi: F.layer_norm(xi, (dim,), wi.to(dtype), bi.to(dtype), norm.eps), dtype, param_dtype)
+    for name, a, b, c in zip(("y", "x", "w", "b"), hip, t16, ref):
+        rel = float((a - c).norm() / c.norm())
+        rel16 = float((b - c).norm() / c.norm())
+        print(f"[parity] layer norm {rows}x{dim} d{name}: hip {rel:.2e} torch 16-bit {rel16:.2e}", flush=True)
+        assert rel <= max(2e-2, 2 * rel16), name
+
+
 def test_feedforward_function() -> None:
     # The block's feed-forward with its residual add on the library's GEMM
     # and its native backward (modules._HipFeedForwardFunction) against fp32
