@@ -607,11 +607,15 @@ def _route_backward(
         go = _normalize_backward(r, g, eps, v_type)
     else:
         go = _aligned(g.to(v_type))
-    keys = _aligned(dictionary_key.detach().t().to(qk_type))
-    # The values as the route layout's 32-atom tiles when the bank carries
-    # them (the prep kernel turns them into v_type rows), else as rows; r in
-    # its own dtype (it only enters rowsum(dr . r)).
+    # The keys as the route layout's atom-major rows and the values as its
+    # 32-atom tiles when the bank carries them (the prep kernel turns the
+    # tiles into v_type rows), else laid out here; r in its own dtype (it only
+    # enters rowsum(dr . r)).
     layout = _tagged_layout(dictionary_key, dictionary_value)
+    if layout is not None and layout.atoms == atoms and layout.key_t.dtype == qk_type:
+        keys = layout.key_t[:atoms]
+    else:
+        keys = _aligned(dictionary_key.detach().t().to(qk_type))
     if layout is not None and layout.atoms == atoms:
         values: Tensor | tuple[Tensor, int, torch.dtype] = (layout.value, 0, v_type)
     else:
@@ -1514,12 +1518,12 @@ def layer_norm_hip(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: f
 
 
 def layer_norm_backward_hip(
-    x: Tensor, grad: Tensor, weight: Tensor | None, eps: float = 1e-5
+    x: Tensor, grad: Tensor, weight: Tensor | None, eps: float = 1e-5, params_dtype: torch.dtype = torch.float32
 ) -> tuple[Tensor, Tensor, Tensor]:
     """The backward of ``layer_norm_hip`` (autograd of ``nn.LayerNorm``) at
     ``grad``: ``(dx, d_weight, d_bias)``, dx in x's dtype, the parameter
     gradients fp32 sums over the rows (``da_layer_norm_backward``; the
-    statistics are formed again from x)."""
+    statistics are formed again from x), rounded once to ``params_dtype``."""
 
     _require_cuda(x)
     dim = x.shape[-1]
@@ -1537,6 +1541,8 @@ def layer_norm_backward_hip(
         ),
         "layer_norm_hip backward",
     )
+    if params_dtype != torch.float32:
+        dparams = dparams.to(params_dtype)
     return dx.view(x.shape), dparams[0], dparams[1]
 
 

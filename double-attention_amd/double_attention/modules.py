@@ -718,8 +718,10 @@ class _HipLayerNormFunction(torch.autograd.Function):
         from . import hip_ops
 
         x, weight = ctx.saved_tensors
-        dx, d_weight, d_bias = hip_ops.layer_norm_backward_hip(x, grad, weight, ctx.eps)
         wd, bd = ctx.param_dtypes
+        # One cast for both parameter gradients when they share a dtype.
+        dx, d_weight, d_bias = hip_ops.layer_norm_backward_hip(
+            x, grad, weight, ctx.eps, params_dtype=wd if wd is not None and wd == bd else torch.float32)
         return (dx if ctx.needs_input_grad[0] else None,
                 d_weight.to(wd) if wd is not None and ctx.needs_input_grad[1] else None,
                 d_bias.to(bd) if bd is not None and ctx.needs_input_grad[2] else None, None)
