@@ -1051,6 +1051,17 @@ def test_lm_training_gradients(monkeypatch) -> None:
     def rel(a, b):
         return float((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-30))
 
+    # The blocks' LayerNorms and feed-forwards train on the library's kernels
+    # too (counted on the HIP model's step only).
+    for cls in (da.modules._HipLayerNormFunction, da.modules._HipFeedForwardFunction):
+        original_apply = cls.apply
+
+        def counted_apply(*args, _original=original_apply, _name=cls.__name__):
+            calls.append(_name)
+            return _original(*args)
+
+        monkeypatch.setattr(cls, "apply", counted_apply)
+
     seeds = tuple(range(3, 19, 2))
     squares: dict[str, list[float]] = {}
     for seed in seeds:
@@ -1072,6 +1083,8 @@ def test_lm_training_gradients(monkeypatch) -> None:
         # Two layers: their outer attentions on the routed rows, their routes
         # on the attention backward kernels.
         assert calls.count("attention_gradients_rows") == 2 and calls.count("_route_backward") == 2, calls
+        # Two norms per block and the final norm; one feed-forward per block.
+        assert calls.count("_HipLayerNormFunction") == 5 and calls.count("_HipFeedForwardFunction") == 2, calls
         for (name, p_hip), p_t16, p_ref in zip(
             models[0].named_parameters(), models[1].parameters(), models[2].parameters()
         ):
