@@ -58,6 +58,7 @@ struct BwdParams {
   float* dk;
   float* dv;            // [B][Tk][D]
   float* dv_sum;        // [D] column sums of dv over every sequence and key, or nullptr
+  float* dv_copies;     // [kDvCopies][D] workspace: the LSE pass's partial column sums
   // With ds_out set the main kernel writes gamma dS (score dtype, rounded
   // once) as rows [BS][T] of ds_ld elements, keys 0 .. Tkp-1, instead of
   // forming dQ = gamma dS K with atomics (dq is then not touched).
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(256) void attention_bwd_prep_kernel(BwdParams p) {
       reinterpret_cast<f32x4*>(p.dv + (static_cast<int64_t>(b) * p.Tk + t0) * D)[i] = z;
   if (bs == 0 && tile == 0 && tid < p.S) p.dgamma[tid] = 0.f;
   if (p.dv_sum && bs == 0 && tile == 0)
-    for (int i = tid; i < D; i += 256) p.dv_sum[i] = 0.f;
+    for (int i = tid; i < kDvCopies * D; i += 256) p.dv_copies[i] = 0.f;
 }
 
 template <typename TQ, int RP>
@@ -422,8 +423,12 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
         s1 += static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x >> 16)));
       }
     }
-    unsafeAtomicAdd(p.dv_sum + 2 * tid0, s0);
-    unsafeAtomicAdd(p.dv_sum + 2 * tid0 + 1, s1);
+    // Workgroups spread their adds over kDvCopies copies of the sums (one
+    // address per copy takes 1 / kDvCopies of the adds); the main kernel
+    // adds the copies up.
+    float* copy = p.dv_copies + static_cast<int64_t>((blockIdx.x + blockIdx.y) % kDvCopies) * p.D;
+    unsafeAtomicAdd(copy + 2 * tid0, s0);
+    unsafeAtomicAdd(copy + 2 * tid0 + 1, s1);
   }
 }
 
@@ -465,6 +470,15 @@ __global__ __launch_bounds__(256, 1) void attention_bwd_kernel(BwdParams p) {
   const int c = lane & 15, g = lane >> 4;
   const int wave = uniform_wave();
   const int tid = static_cast<int>(threadIdx.x);
+  // The value bias's gradient: the LSE pass's copies of the column sums of
+  // dO, added up by one workgroup (before any return).
+  if (p.dv_sum && blockIdx.x == 0 && blockIdx.y == 0)
+    for (int i = tid; i < D; i += 256) {
+      float t = 0.f;
+#pragma unroll
+      for (int k = 0; k < kDvCopies; ++k) t += p.dv_copies[k * D + i];
+      p.dv_sum[i] = t;
+    }
   // Workgroups go round-robin over the XCDs; each XCD takes a contiguous run
   // of the logical order (sequence, query run, key tile), so the workgroups
   // that run together on one XCD stage nearly the same query tiles from its L2.
@@ -791,7 +805,8 @@ AttentionBwdLayout attention_bwd_layout(int64_t B, int64_t S, int64_t T, int64_t
   l.lse2 = l.doutt + up(BS * Tp * D * 2);
   l.dvec = l.lse2 + up(BS * T * 4);
   l.vrows = l.dvec + up(BS * T * 4);
-  l.bytes = l.vrows + up(B * Tkp * D * 2);
+  l.dv_copies = l.vrows + up(B * Tkp * D * 2);
+  l.bytes = l.dv_copies + up(kDvCopies * D * 4);
   return l;
 }
 
@@ -801,7 +816,7 @@ void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace
   const int64_t Tkp = round_up(a.Tk, kKeyPad);
   BwdParams p{a.q, a.k, a.vt ? static_cast<const void*>(ws + l.vrows) : a.v, a.out, a.dout, ws + l.qt, ws + l.kt, ws + l.doutt,
               reinterpret_cast<float*>(ws + l.lse2), reinterpret_cast<float*>(ws + l.dvec), a.scales,
-              a.dq, a.dk, a.dv, a.dv_sum, a.ds_out, a.ds_ld, a.v_dtype, a.dgamma,
+              a.dq, a.dk, a.dv, a.dv_sum, reinterpret_cast<float*>(ws + l.dv_copies), a.ds_out, a.ds_ld, a.v_dtype, a.dgamma,
               a.q_stride_b, a.q_stride_t, a.q_map_stride, a.k_stride_b, a.k_stride_t, a.k_map_stride,
               a.map_repeat, a.vt ? Tkp * a.D : static_cast<int64_t>(a.Tk) * a.D, a.vt, a.vt_stride_b, a.vt_dtype,
               ws + l.vrows, a.scales_dtype, a.scales_log ? 1 : 0, a.log_lo, a.log_hi, a.scale_mult,

@@ -121,8 +121,11 @@ struct AttentionBwdArgs {
 };
 // Byte offsets of the backward's workspace pieces (256-byte aligned).
 struct AttentionBwdLayout {
-  int64_t qt, kt, doutt, lse2, dvec, vrows, bytes;
+  int64_t qt, kt, doutt, lse2, dvec, vrows, dv_copies, bytes;
 };
+// Copies of the value bias's gradient the LSE pass's workgroups spread
+// their atomic adds over.
+constexpr int kDvCopies = 8;
 AttentionBwdLayout attention_bwd_layout(int64_t B, int64_t S, int64_t T, int64_t Tk, int64_t RP, int64_t D);
 void launch_routed_attention_backward(const AttentionBwdArgs& a, void* workspace, hipStream_t stream);
 

@@ -157,12 +157,14 @@ def test_attention_backward_rejects_bad_arguments() -> None:
     f = _fake()
     need = h.da_attention_backward_workspace_bytes(2, 3, 100, 100, 128, 256)
     # Q^T, K^T and dO^T tiles over 128 padded tokens, two fp32 rows (6 * 100 * 4
-    # = 2400 bytes, rounded up to 2560), then value rows [2, 128, 256] for
-    # V^T tiles (da_routed_attention_backward_ex).
-    assert need == 2 * (6 * 128 * 128 * 2) + 6 * 128 * 256 * 2 + 2 * 2560 + 2 * 128 * 256 * 2
+    # = 2400 bytes, rounded up to 2560), value rows [2, 128, 256] for V^T
+    # tiles (da_routed_attention_backward_ex), then eight fp32 copies of the
+    # value bias's gradient [8, 256].
+    assert need == 2 * (6 * 128 * 128 * 2) + 6 * 128 * 256 * 2 + 2 * 2560 + 2 * 128 * 256 * 2 + 8 * 256 * 4
     # Cross attention: K^T tiles follow the key count (300 -> 320 padded).
     cross = h.da_attention_backward_workspace_bytes(2, 3, 100, 300, 128, 256)
-    assert cross == 6 * 128 * 128 * 2 + 6 * 320 * 128 * 2 + 6 * 128 * 256 * 2 + 2 * 2560 + 2 * 320 * 256 * 2
+    assert cross == (6 * 128 * 128 * 2 + 6 * 320 * 128 * 2 + 6 * 128 * 256 * 2 + 2 * 2560 + 2 * 320 * 256 * 2
+                     + 8 * 256 * 4)
     good = [f, f, f, f, f, f, 2, 3, 100, 100, 128, 256, lib.DA_ATTN_CAUSAL, lib.DA_BF16, lib.DA_BF16,
             f, need, f, f, f, f, None]
     cases = [
