@@ -234,7 +234,9 @@ void launch_sum_partials(const float* partials, int count, int64_t n, void* out,
 void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight, const void* bias, int param_dtype,
                        float eps, int dtype, void* out, hipStream_t stream);
 // Its backward: dx (dtype) and the fp32 parameter gradients added into
-// dparams [2 * dim] (weight then bias; zeroed by the caller).
+// dparams [kLnParamCopies][2 * dim] (weight then bias; zeroed by the caller,
+// the gradients are the sums over the copies).
+constexpr int kLnParamCopies = 8;
 void launch_layer_norm_backward(const void* x, const void* dy, int64_t rows, int dim, const void* weight,
                                 int param_dtype, float eps, int dtype, void* dx, float* dparams, hipStream_t stream);
 // Launch shape of the attention for a problem: value slice width, waves per

@@ -98,7 +98,8 @@ __global__ __launch_bounds__(64 * kLnRowsPerBlock) void layer_norm_kernel(const 
 // each: (sum x, sum g), then (sum (x - mean)^2, sum g (x - mean)).  The
 // parameter gradients stay in the lanes' registers over the wave's rows,
 // meet across the workgroup's waves in LDS and leave as one fp32 atomic add
-// per workgroup and column (the caller zeroes them).
+// per workgroup and column into one of kLnParamCopies copies (the caller
+// zeroes them and adds the copies up).
 template <typename T, int CH>
 __global__ __launch_bounds__(64 * kLnRowsPerBlock) void layer_norm_backward_kernel(
     const T* x, const T* dy, int64_t rows, int dim, const void* weight, int pdt, float eps, T* dx, float* dparams) {
@@ -193,7 +194,10 @@ __global__ __launch_bounds__(64 * kLnRowsPerBlock) void layer_norm_backward_kern
     }
     __syncthreads();
   }
-  for (int i = static_cast<int>(threadIdx.x); i < 2 * dim; i += 64 * kLnRowsPerBlock) unsafeAtomicAdd(dparams + i, part[i]);
+  // Copy blockIdx % kLnParamCopies of the sums: each address takes
+  // 1 / kLnParamCopies of the workgroups' adds.
+  float* copy = dparams + static_cast<int64_t>(blockIdx.x % kLnParamCopies) * 2 * dim;
+  for (int i = static_cast<int>(threadIdx.x); i < 2 * dim; i += 64 * kLnRowsPerBlock) unsafeAtomicAdd(copy + i, part[i]);
 }
 
 template <typename T>

@@ -15,6 +15,8 @@
 // and leave as one atomic add per workgroup and map.
 // The partial sum adds the fp32 partial products of a split-K GEMM (the
 // training path's weight gradients) and rounds the sum once to 16 bits.
+#include <algorithm>
+
 #include "da_common.h"
 #include "da_launch.h"
 
@@ -130,7 +132,9 @@ unsigned mix_grid(int64_t n) {
 
 template <typename T, int S>
 void launch_s(const MapCombineArgs& a, bool backward, hipStream_t stream) {
-  const unsigned grid = mix_grid(a.rows * (a.D / 8));
+  // The backward's S per-map sums take one atomic add per workgroup each:
+  // 256 workgroups (a few chunks per thread) keep those adds few.
+  const unsigned grid = backward ? std::min(mix_grid(a.rows * (a.D / 8)), 256u) : mix_grid(a.rows * (a.D / 8));
   if (backward) hipLaunchKernelGGL((map_combine_backward_kernel<T, S>), dim3(grid), dim3(kMixThreads), 0, stream, a);
   else hipLaunchKernelGGL((map_combine_kernel<T, S>), dim3(grid), dim3(kMixThreads), 0, stream, a);
 }

@@ -1517,6 +1517,11 @@ def layer_norm_hip(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: f
     return out
 
 
+# Copies of the LayerNorm backward's parameter gradients its workgroups
+# spread their atomic adds over (da_layer_norm_backward).
+LAYER_NORM_PARAM_COPIES = 8
+
+
 def layer_norm_backward_hip(
     x: Tensor, grad: Tensor, weight: Tensor | None, eps: float = 1e-5, params_dtype: torch.dtype = torch.float32
 ) -> tuple[Tensor, Tensor, Tensor]:
@@ -1531,7 +1536,7 @@ def layer_norm_backward_hip(
     g = _aligned(grad.detach().to(x.dtype))
     w = None if weight is None else _aligned(weight.detach())
     dx = torch.empty_like(xc)
-    dparams = torch.zeros(2, dim, dtype=torch.float32, device=x.device)
+    dparams = torch.zeros(LAYER_NORM_PARAM_COPIES, 2, dim, dtype=torch.float32, device=x.device)
     lib = _lib.get()
     _lib.check(
         lib.da_layer_norm_backward(
@@ -1541,9 +1546,17 @@ def layer_norm_backward_hip(
         ),
         "layer_norm_hip backward",
     )
-    if params_dtype != torch.float32:
-        dparams = dparams.to(params_dtype)
-    return dx.view(x.shape), dparams[0], dparams[1]
+    if params_dtype in (torch.float16, torch.bfloat16) and dim % 4 == 0:
+        # The copies added up and rounded once, in one launch.
+        out = torch.empty(2, dim, dtype=params_dtype, device=x.device)
+        _lib.check(
+            lib.da_sum_partials(dparams.data_ptr(), LAYER_NORM_PARAM_COPIES, 2 * dim, out.data_ptr(),
+                                _half_code(params_dtype), _stream(x.device)),
+            "layer_norm_hip backward sums",
+        )
+        return dx.view(x.shape), out[0], out[1]
+    summed = dparams.sum(0).to(params_dtype)
+    return dx.view(x.shape), summed[0], summed[1]
 
 
 MAP_COMBINE_MAX_MAPS = 8

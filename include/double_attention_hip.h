@@ -436,10 +436,12 @@ int da_layer_norm(const void* x, int64_t rows, int64_t dim, const void* weight, 
  * ([rows, dim] of dtype): the statistics are formed again from x in fp32;
  * grad_x = rstd (g - mean(g) - xh mean(g xh)) with xh = (x - mean) rstd and
  * g = grad weight (weight of param_dtype, or NULL for 1), rounded once to
- * dtype; grad_params[0, dim) += sum over rows of grad xh (the weight's
- * gradient) and grad_params[dim, 2 dim) += sum over rows of grad (the
- * bias's), fp32 atomic adds (the caller zeroes grad_params).  Same layout
- * rules as da_layer_norm.
+ * dtype.  grad_params is [8][2 dim] fp32, zeroed by the caller: the rows'
+ * sums of grad xh (the weight's gradient) and of grad (the bias's) are added
+ * into its eight copies (fp32 atomic adds spread over the copies), and the
+ * gradients are the sums over the copies: weight columns [0, dim), bias
+ * columns [dim, 2 dim) of each copy (da_sum_partials adds them and rounds to
+ * 16 bits in one launch).  Same layout rules as da_layer_norm.
  */
 int da_layer_norm_backward(const void* x, const void* grad, int64_t rows, int64_t dim, const void* weight,
                            int param_dtype, float eps, int dtype, void* grad_x, float* grad_params, da_stream_t stream);
