@@ -322,9 +322,10 @@ __global__ __launch_bounds__(256) void attention_lse_kernel(BwdParams p) {
   // queries (every row of P sums to one).  With dv_sum set this workgroup
   // adds those of its 32 rows of dO: one column pair per thread (D <= 512),
   // each row a coalesced pass.  The loads are issued here and summed after
-  // the key loop, and the adds to the D shared addresses come at the end,
-  // when the workgroups of a causal staircase finish at different times.
-  // Rows past the sequence re-read its last row and are dropped.
+  // the key loop, and the adds (into one of kDvCopies copies of the D sums)
+  // come at the end, when the workgroups of a causal staircase finish at
+  // different times.  Rows past the sequence re-read its last row and are
+  // dropped.
   const int tid0 = static_cast<int>(threadIdx.x);
   const bool col_sums = p.dv_sum != nullptr && tid0 < p.D / 2;
   const int last_row = min(kQTile, p.T - q0) - 1;
