@@ -636,6 +636,30 @@ int da_map_combine_backward(const float* maps, int64_t batch, int64_t n_maps, in
   return check_launch("map combine backward");
 }
 
+int da_dense_attention_operands(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
+                                int64_t map_stride, int64_t map_repeat, int qk_dtype, int64_t batch, int64_t maps,
+                                int64_t length, int64_t score_dim, void* key_t, void* query_out, void* key_out,
+                                int out_dtype, da_stream_t stream) {
+  if (!half_dtype(qk_dtype) || !half_dtype(out_dtype))
+    return fail(DA_ERR_INVALID_ARGUMENT, "dense operands: dtypes must be DA_F16 or DA_BF16");
+  if (batch < 0 || maps < 1 || maps > 65535 || length < 0 || batch * maps > 65535 || map_repeat < 1)
+    return fail(DA_ERR_INVALID_ARGUMENT, "dense operands: bad batch, maps, length or map_repeat");
+  if (score_dim < 64 || score_dim % 64 || score_dim > 4096)
+    return fail(DA_ERR_UNSUPPORTED, "dense operands: score_dim must be a multiple of 64 up to 4096");
+  if (batch == 0 || length == 0) return ok();
+  if (!query || !key || !key_t || !query_out || !key_out)
+    return fail(DA_ERR_INVALID_ARGUMENT, "dense operands: null pointer");
+  if (stride_b % 8 || stride_t % 8 || map_stride % 8 || stride_t < score_dim || !aligned(query, 16) ||
+      !aligned(key, 16) || !aligned(key_t, 16) || !aligned(query_out, 16) || !aligned(key_out, 16))
+    return fail(DA_ERR_ALIGNMENT, "dense operands: strides must be multiples of 8 (stride_t >= score_dim), "
+                "pointers 16-byte aligned");
+  const da::DenseOperandArgs a{query, key, stride_b, stride_t, map_stride, static_cast<int>(map_repeat), qk_dtype,
+                               static_cast<int>(batch), static_cast<int>(maps), static_cast<int>(length),
+                               static_cast<int>(score_dim), key_t, query_out, key_out, out_dtype};
+  da::launch_dense_operands(a, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("dense operands");
+}
+
 int da_sum_partials(const float* partials, int64_t count, int64_t n, void* out, int out_dtype, da_stream_t stream) {
   if (!half_dtype(out_dtype)) return fail(DA_ERR_INVALID_ARGUMENT, "sum partials: out_dtype must be DA_F16 or DA_BF16");
   if (count < 1 || count > 1024 || n < 0 || n % 8)

@@ -230,6 +230,24 @@ void launch_map_combine(const MapCombineArgs& a, bool backward, hipStream_t stre
 // out[i] = sum_c partials[c * n + i] rounded once to out_dtype (kF16 / kBF16); n % 8 == 0.
 void launch_sum_partials(const float* partials, int count, int64_t n, void* out, int out_dtype, hipStream_t stream);
 
+// Operands of the dense attention backward (dense_operands.hip): from the
+// score maps (row (b, s, t) at q/k + b*stride_b + (s/map_repeat)*map_stride +
+// t*stride_t, R elements) K^T [B*S, R, T] in qk_dtype and q, k [B*S, T, R] in
+// out_dtype.  R a multiple of 64.
+struct DenseOperandArgs {
+  const void* q;
+  const void* k;
+  int64_t stride_b, stride_t, map_stride;
+  int map_repeat;
+  int qk_dtype;
+  int B, S, T, R;
+  void* key_t;
+  void* q_out;
+  void* k_out;
+  int out_dtype;
+};
+void launch_dense_operands(const DenseOperandArgs& a, hipStream_t stream);
+
 // LayerNorm over the last dimension (dim a multiple of 8, at most 4096).
 void launch_layer_norm(const void* x, int64_t rows, int dim, const void* weight, const void* bias, int param_dtype,
                        float eps, int dtype, void* out, hipStream_t stream);

@@ -197,6 +197,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "da_layer_norm_backward": (_i32, [_vp, _vp, _i64, _i64, _vp, _i32, _f32, _i32, _vp, _vp, _vp]),
     "da_map_combine": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _vp]),
     "da_sum_partials": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
+    "da_dense_attention_operands": (
+        _i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp]),
     "da_map_combine_backward": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _vp, _vp]),
     "da_attention_backward_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "da_routed_attention_backward": (

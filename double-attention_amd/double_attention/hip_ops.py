@@ -1286,6 +1286,34 @@ def _dense_backward_fits(query: Tensor, value: Tensor) -> bool:
     return _dense_fits(batch, maps, length, score_dim, value.shape[-1])
 
 
+def _dense_operands(query: Tensor, key: Tensor, v_type: torch.dtype) -> tuple[Tensor, Tensor, Tensor] | None:
+    """``(K^T, q, k)`` of the dense backward from the score maps ``query`` and
+    ``key`` ``[B, S, T, R]`` (16-bit, rows of unit stride, the same layout):
+    ``da_dense_attention_operands``, or None where the kernel does not take
+    them."""
+
+    batch, maps, length, score_dim = query.shape
+    if (not query.is_cuda or query.dtype not in (torch.float16, torch.bfloat16) or key.dtype != query.dtype
+            or key.shape != query.shape or key.stride() != query.stride() or query.stride(3) != 1
+            or score_dim % 64 or score_dim > 4096 or batch * maps > 65535 or length == 0):
+        return None
+    sb, ms, st = query.stride(0), query.stride(1), query.stride(2)
+    if sb % 8 or ms % 8 or st % 8 or st < score_dim or query.data_ptr() % 16 or key.data_ptr() % 16:
+        return None
+    rows = batch * maps
+    k_t = torch.empty(rows, score_dim, length, dtype=query.dtype, device=query.device)
+    q_v = torch.empty(rows, length, score_dim, dtype=v_type, device=query.device)
+    k_v = torch.empty_like(q_v)
+    _lib.check(
+        _lib.get().da_dense_attention_operands(
+            query.data_ptr(), key.data_ptr(), sb, st, ms, 1, _half_code(query.dtype), batch, maps, length, score_dim,
+            k_t.data_ptr(), q_v.data_ptr(), k_v.data_ptr(), _half_code(v_type), _stream(query.device),
+        ),
+        "dense attention operands",
+    )
+    return k_t, q_v, k_v
+
+
 def _attention_backward_dense(
     query: Tensor, key: Tensor, value: Tensor | None, scales: Tensor, grad: Tensor, causal: bool,
     qk_grad_dtype: torch.dtype | None = None, value_t: Tensor | None = None, scales_are_log: bool = False,
@@ -1327,8 +1355,15 @@ def _attention_backward_dense(
         return t if t.stride(2) == 1 and t.stride(1) >= score_dim else t.contiguous()
 
     q, k = rows_of(query), rows_of(key)
-    # Right operands of the products are contiguous (no transposed views).
-    scores = torch.bmm(q, k.transpose(1, 2).contiguous(), out_dtype=torch.float32)
+    # Right operands of the products are contiguous (no transposed views):
+    # K^T for S = q k^T, and q, k in the value dtype for dk and dq, written in
+    # one pass over the score maps where the kernel takes their layout.
+    operands = _dense_operands(query, key, v_type)
+    if operands is not None:
+        k_t, q_v, k_v = operands
+    else:
+        k_t, q_v, k_v = k.transpose(1, 2).contiguous(), None, None
+    scores = torch.bmm(q, k_t, out_dtype=torch.float32)
     go = grad.detach().reshape(rows, length, model_dim).to(v_type).contiguous()
     if value is None:
         padded = value_t.shape[1] * 32
@@ -1356,8 +1391,8 @@ def _attention_backward_dense(
         "routed_attention_hip dense backward",
     )
     del scores, grad_p
-    dq = torch.bmm(grad_s, k.to(v_type), out_dtype=torch.float32)
-    dk = torch.bmm(grad_s.transpose(1, 2), q.to(v_type), out_dtype=torch.float32)
+    dq = torch.bmm(grad_s, k_v if k_v is not None else k.to(v_type), out_dtype=torch.float32)
+    dk = torch.bmm(grad_s.transpose(1, 2), q_v if q_v is not None else q.to(v_type), out_dtype=torch.float32)
     dv = torch.bmm(probs.transpose(1, 2), go, out_dtype=torch.float32)
     dv = dv.view(batch, length, model_dim) if maps == 1 else dv.view(batch, maps, length, model_dim).sum(1)
     dgamma = dgamma_rows.view(batch, maps, length).sum(dim=(0, 2))

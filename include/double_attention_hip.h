@@ -39,6 +39,8 @@
  *                             attention_norm / feedforward_norm /    src/double_attention/modules.py:311, 313, 440
  *                             final_norm (nn.LayerNorm) and its autograd backward
  *   da_sum_partials           (split-K weight gradients of the training path; no reference counterpart)
+ *   da_dense_attention_operands
+ *                             operands of the dense attention backward src/double_attention/triton_kernels.py:2093-2263
  *   da_map_combine, da_map_combine_backward
  *                             map_combine "weighted_sum" (einsum      src/double_attention/modules.py:265-272
  *                             over the per-map outputs) and its backward
@@ -461,6 +463,23 @@ int da_layer_norm_backward(const void* x, const void* grad, int64_t rows, int64_
  */
 int da_map_combine(const float* maps, int64_t batch, int64_t n_maps, int64_t length, int64_t width,
                    const float* weights, void* out, int out_dtype, da_stream_t stream);
+
+/*
+ * Operands of the dense outer-attention backward (library GEMMs around
+ * da_dictionary_route_backward_rows for long sequences and wide scores; the
+ * products of the reference's attention backward, triton_kernels.py:2093-2263)
+ * in one pass over the score maps.  Row (b, s, t) of query and key starts at
+ *   base + b*stride_b + (s / map_repeat)*map_stride + t*stride_t
+ * and holds score_dim elements of qk_dtype (strides in elements, multiples of
+ * 8).  Writes key_t [batch*maps, score_dim, length] (K^T, qk_dtype) and
+ * query_out, key_out [batch*maps, length, score_dim] (out_dtype): the right
+ * operands of S = q k^T, dk = dS^T q and dq = dS k.  score_dim a multiple of
+ * 64 up to 4096, batch*maps <= 65535, pointers 16-byte aligned.
+ */
+int da_dense_attention_operands(const void* query, const void* key, int64_t stride_b, int64_t stride_t,
+                                int64_t map_stride, int64_t map_repeat, int qk_dtype, int64_t batch, int64_t maps,
+                                int64_t length, int64_t score_dim, void* key_t, void* query_out, void* key_out,
+                                int out_dtype, da_stream_t stream);
 
 /*
  * out[i] = sum over c < count of partials[c * n + i], summed in fp32 in order

@@ -22,7 +22,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol() -> None:
     handle = lib.get()
     names = declared_functions()
-    assert len(names) == 27
+    assert len(names) == 28
     for name in names:
         assert hasattr(handle, name), name
         assert name in lib.SIGNATURES, f"{name} has no ctypes signature"
@@ -425,3 +425,23 @@ def test_layer_norm_backward_rejects_bad_arguments() -> None:
     assert call(grad=ctypes.c_void_p((1 << 20) + 8)) == -3
     assert call(eps=-1.0) == -1
     assert call(rows=0, x=None) == 0
+
+
+def test_dense_attention_operands_rejects_bad_arguments() -> None:
+    h = lib.get()
+    buf = ctypes.c_void_p(1 << 20)   # never dereferenced
+
+    def call(**kw):
+        args = dict(query=buf, key=buf, stride_b=100 * 1024, stride_t=1024, map_stride=256, map_repeat=1,
+                    qk_dtype=lib.DA_F16, batch=2, maps=2, length=100, score_dim=256, key_t=buf, query_out=buf,
+                    key_out=buf, out_dtype=lib.DA_BF16, stream=None)
+        args.update(kw)
+        return h.da_dense_attention_operands(*args.values())
+
+    assert call(qk_dtype=lib.DA_F32) == -1 and call(out_dtype=9) == -1
+    assert call(score_dim=96) == -2 and b"multiple of 64" in h.da_last_error()
+    assert call(map_repeat=0) == -1 and call(batch=300, maps=300) == -1
+    assert call(key_t=None) == -1 and b"null" in h.da_last_error()
+    assert call(stride_t=128) == -3 and call(map_stride=4) == -3
+    assert call(key=ctypes.c_void_p((1 << 20) + 8)) == -3
+    assert call(length=0, query=None) == 0

@@ -677,6 +677,28 @@ def test_routed_attention_backward(case, dtypes) -> None:
             assert_parity(grad, exp, rel, max(2e-2 * scale, 1e-6), f"{label} d{name}")
 
 
+@pytest.mark.parametrize(("batch", "maps", "length", "score_dim", "heads"),
+                         [(2, 1, 2100, 512, 1), (1, 2, 100, 256, 2), (2, 2, 77, 128, 1)])
+def test_dense_attention_operands(batch, maps, length, score_dim, heads) -> None:
+    # K^T and the value-dtype q, k of the dense backward from strided score
+    # maps (the routed rows [B, T, 2, H, R] with maps over the heads, or one
+    # map repeated by a zero stride), bit-identical to the torch copies; a
+    # ragged length exercises the element stores of K^T.
+    device = _device()
+    g = torch.Generator().manual_seed(length)
+    routed = torch.randn(batch, length, 2, heads, score_dim, generator=g).to(device, torch.float16)
+    q = routed[:, :, 0].transpose(1, 2)
+    k = routed[:, :, 1].transpose(1, 2)
+    if heads < maps:
+        q, k = q.expand(batch, maps, length, score_dim), k.expand(batch, maps, length, score_dim)
+    got = da.hip_ops._dense_operands(q, k, torch.bfloat16)
+    assert got is not None
+    rows = batch * maps
+    assert torch.equal(got[0], k.reshape(rows, length, score_dim).transpose(1, 2))
+    assert torch.equal(got[1], q.reshape(rows, length, score_dim).to(torch.bfloat16))
+    assert torch.equal(got[2], k.reshape(rows, length, score_dim).to(torch.bfloat16))
+
+
 def test_dense_attention_backward_log_scales() -> None:
     # The dense backward with log temperatures (the module's path): the row
     # kernel clamps and exponentiates them (ln .25 .. ln 1024) and returns the
